@@ -1,0 +1,192 @@
+/*
+ * ortmi_kernels.h - C ABI of the MI355X (gfx950) kernel library
+ * (libortmi_kernels.so).
+ *
+ * This library is the compute backend of the MI355X execution provider. It takes
+ * the place that mlx-c / MLX hold in the reference EP: the reference's op
+ * translators (rust/src/ops/quant.rs, rust/src/ops/attention.rs,
+ * rust/src/ops/norm.rs) bind mlx-c functions through bindgen
+ * (rust/build.rs:76-87) and hand them MLX arrays; the MI355X EP's op layer calls
+ * these entry points instead, with plain device pointers and sizes.
+ *
+ * Conventions (all entry points):
+ *  - Tensor pointers are device pointers (hipMalloc'd or from the EP's
+ *    allocator); scalar sizes are host values; `stream` is a hipStream_t (NULL =
+ *    the null stream). Work is enqueued asynchronously on `stream`.
+ *  - `dtype` is the ONNX TensorProto element type of the float tensors:
+ *    ORTMI_F32 (1), ORTMI_F16 (10) or ORTMI_BF16 (16).
+ *  - Return 0 on success, otherwise an ORTMI_E_* code; ortmi_last_error()
+ *    returns the calling thread's last message. Errors are detected on the host
+ *    before any launch, so a failed call enqueues nothing.
+ *  - Workspace, where an entry point needs one, is caller-owned device memory;
+ *    the matching *_workspace_size() gives its size. The library itself never
+ *    allocates device memory.
+ */
+#ifndef ORTMI_KERNELS_H
+#define ORTMI_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    ORTMI_F32 = 1,
+    ORTMI_F16 = 10,
+    ORTMI_BF16 = 16,
+};
+
+enum {
+    ORTMI_OK = 0,
+    ORTMI_E_INVALID = 1,     /* bad argument / unsupported form */
+    ORTMI_E_HIP = 2,         /* HIP runtime error */
+    ORTMI_E_WORKSPACE = 3,   /* workspace too small */
+};
+
+#define ORTMI_ABI_VERSION 1
+
+int ortmi_abi_version(void);
+const char* ortmi_last_error(void);
+
+/*
+ * MatMulNBits (com.microsoft): Y[M,N] = A[M,K] . dequant(B)^T with
+ * dequant(B)[n,k] = (q[n,k] - zp[n,k/bs]) * scales[n,k/bs].
+ * B: uint8 [N, ceil(K/bs), bs*bits/8] (ORT layout, low nibble first);
+ * scales: dtype [N*ceil(K/bs)]; zero_points: NULL (symmetric, zp = 2^(bits-1)),
+ * or uint8 packed [N*ceil(ceil(K/bs)/2)] for bits=4, [N*ceil(K/bs)] for bits=8.
+ * bits in {4, 8}; block_size in {16, 32, 64, 128}; A, scales and Y share dtype.
+ * Replaces: the mlx_quantized_matmul call (rust/src/ops/quant.rs:570-601) reached
+ * from matmulnbits_op (quant.rs:986-1130), plus the repack/bias preparation it
+ * needs (quant.rs:637-984), which this library does not need: it reads ORT's
+ * layout directly.
+ */
+int ortmi_matmul_nbits(const void* A, const uint8_t* B, const void* scales,
+                       const uint8_t* zero_points, void* Y, int64_t M, int64_t N, int64_t K,
+                       int64_t bits, int64_t block_size, int32_t dtype, void* stream);
+
+/*
+ * GroupQueryAttention (com.microsoft), decode and prefill, with in-op RoPE.
+ * query [B,S,H*hd] (or packed [B,S,(H+2*KV)*hd] when key == value == NULL),
+ * key/value [B,S,KV*hd]; past_key/past_value [B,KV,past_cap,hd].
+ * valid_past = total_sequence_length - S (one value for the batch); the
+ * shared-buffer contract applies when past_cap > valid_past: present_* are
+ * [B,KV,past_cap,hd] (they may alias past_*, then only the S new rows are
+ * written); otherwise the growing contract: present_* are [B,KV,past_cap+S,hd].
+ * cos_cache/sin_cache [max_pos, rotary_half] (NULL when do_rotary = 0), in dtype.
+ * output [B,S,H*hd]. scale = 0 means 1/sqrt(hd).
+ * Replaces: group_query_attention_op (rust/src/ops/attention.rs:556-952): the
+ * two mlx_fast_rope calls (attention.rs:671-708), the KV concat /
+ * slice_update (attention.rs:881-908) and mlx_fast_scaled_dot_product_attention
+ * (attention.rs:111-135, 264-285).
+ */
+size_t ortmi_group_query_attention_workspace_size(int64_t batch, int64_t seq_len,
+                                                  int64_t num_heads, int64_t head_size,
+                                                  int64_t total_kv);
+int ortmi_group_query_attention(const void* query, const void* key, const void* value,
+                                const void* past_key, const void* past_value,
+                                int64_t past_cap, int32_t total_sequence_length,
+                                const void* cos_cache, const void* sin_cache,
+                                int64_t rotary_half, int64_t max_pos,
+                                void* output, void* present_key, void* present_value,
+                                int64_t batch, int64_t seq_len, int64_t num_heads,
+                                int64_t kv_num_heads, int64_t head_size, float scale,
+                                int32_t rotary_interleaved, int32_t dtype, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/*
+ * PagedAttention (com.microsoft), mixed prefill + decode over a block-paged KV
+ * cache. query [T,H*hd], key [T,KV*hd], value [T,KV*vhd] (value == NULL and
+ * value_cache == NULL selects the LATENT layout: values are the first vhd dims
+ * of the keys); key_cache [num_blocks, block_size, KV, hd], value_cache
+ * [num_blocks, block_size, KV, vhd], updated in place. cum_seqlens [batch+1],
+ * past_seqlens [batch], block_table [batch, max_blocks] and slot_mapping [T]
+ * (optional, slot < 0 skips the write) are int32 device tensors: nothing is read
+ * back to the host. max_context is a host upper bound on past + new tokens of
+ * every sequence (max_blocks * block_size always is one); keys beyond it are not
+ * attended. cos/sin caches are [rotary_max_pos, rotary_half]. head_sink [H],
+ * q_norm_weight/k_norm_weight [hd] optional. output [T,H*vhd]. Malformed control
+ * tensors (block ids or positions out of range) never cause out-of-bounds
+ * accesses: such keys are masked and such writes skipped.
+ * Replaces: paged_attention_op (rust/src/ops/attention.rs:2495-2744), which
+ * syncs the control tensors to the host and loops over sequences with MLX
+ * take/scatter/concat and fp32 SDPA.
+ */
+size_t ortmi_paged_attention_workspace_size(int64_t num_tokens, int64_t batch,
+                                            int64_t num_heads, int64_t kv_num_heads,
+                                            int64_t head_size, int64_t v_head_size,
+                                            int64_t max_context);
+int ortmi_paged_attention(const void* query, const void* key, const void* value,
+                          void* key_cache, void* value_cache, int64_t num_blocks,
+                          int64_t block_size, const int32_t* cum_seqlens,
+                          const int32_t* past_seqlens, const int32_t* block_table,
+                          int64_t batch, int64_t max_blocks, int64_t num_tokens,
+                          int64_t max_context, const void* cos_cache, const void* sin_cache,
+                          int64_t rotary_half, int64_t rotary_max_pos,
+                          int32_t rotary_interleaved, int64_t rotary_offset, const int32_t* slot_mapping,
+                          const void* head_sink, const void* q_norm_weight,
+                          const void* k_norm_weight, float qk_norm_eps, void* output,
+                          int64_t num_heads, int64_t kv_num_heads, int64_t head_size,
+                          int64_t v_head_size, float scale, int32_t dtype, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
+ * RotaryEmbedding (com.microsoft / ai.onnx), standalone.
+ * x: rank-3 [B,S,NH*hd] (is_bnsd = 0) or rank-4 [B,NH,S,hd] (is_bnsd = 1).
+ * Position forms (rust/src/ops/attention.rs:1288-1315, 1337-1400):
+ *   position_ids == NULL: cos/sin are per-token [B*S, half] rows;
+ *   pos_is_offset = 1: position_ids is int64 [1], token (b,s) uses row offset+s;
+ *   otherwise position_ids is int64 [B,S].
+ * cos/sin are [max_pos, rotary_half]. Rotates dims [0, 2*rotary_half) of each
+ * head; the rest pass through.
+ * Replaces: rotary_embedding_op (attention.rs:1317-1411) / mlx_fast_rope.
+ */
+int ortmi_rotary_embedding(const void* x, const int64_t* position_ids, int32_t pos_is_offset,
+                           const void* cos_cache, const void* sin_cache, int64_t max_pos, void* y,
+                           int64_t batch, int64_t seq_len, int64_t num_heads,
+                           int64_t head_size, int64_t rotary_half, int32_t is_bnsd,
+                           int32_t interleaved, int32_t dtype, void* stream);
+
+/*
+ * SimplifiedLayerNormalization / SkipSimplifiedLayerNormalization
+ * (com.microsoft) and RMSNormalization: r = x (+ skip) (+ bias);
+ * y = r / sqrt(mean(r^2) + eps) * gamma over the last axis of length D.
+ * skip, bias and residual_out are optional (NULL).
+ * Replaces: mlx_fast_rms_norm via simplified_layer_norm_op / skip_rms_norm_op /
+ * rms_norm_op (rust/src/ops/norm.rs:164-248).
+ */
+int ortmi_rms_norm(const void* x, const void* skip, const void* bias, const void* gamma,
+                   void* y, void* residual_out, int64_t rows, int64_t D, float eps,
+                   int32_t dtype, void* stream);
+
+/*
+ * Decoder glue claimed with the hot path so the whole int4 decoder graph runs on
+ * the device (rust/src/ops/elementwise.rs:928-980, rust/src/ops/shape.rs:2453).
+ *  - ortmi_gather_rows: Gather along axis 0 of a [V, D] table by int64 ids
+ *    (negative ids count from the end, out of range is reported via the
+ *    returned status only when checked on the host by the caller).
+ *  - ortmi_swiglu: out = (g * sigmoid(g)) * u, each op rounded to dtype as the
+ *    Sigmoid/Mul/Mul graph does.
+ *  - ortmi_binary: elementwise Add (op 0) / Mul (op 1) / Sub (op 2) of
+ *    same-shape tensors.
+ *  - ortmi_sigmoid: elementwise Sigmoid.
+ *  - ortmi_argmax_rows: int64 index of the max of each row (first on ties).
+ *  - ortmi_cast: f32 <-> f16 <-> bf16.
+ */
+int ortmi_gather_rows(const void* table, const int64_t* ids, void* out, int64_t num_ids,
+                      int64_t vocab, int64_t D, int32_t dtype, void* stream);
+int ortmi_swiglu(const void* gate, const void* up, void* out, int64_t n, int32_t dtype,
+                 void* stream);
+int ortmi_binary(int32_t op, const void* a, const void* b, void* out, int64_t n,
+                 int32_t dtype, void* stream);
+int ortmi_sigmoid(const void* x, void* out, int64_t n, int32_t dtype, void* stream);
+int ortmi_argmax_rows(const void* x, int64_t* out, int64_t rows, int64_t cols, int32_t dtype,
+                      void* stream);
+int ortmi_cast(const void* x, int32_t src_dtype, void* y, int32_t dst_dtype, int64_t n,
+               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

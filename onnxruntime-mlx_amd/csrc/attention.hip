@@ -1,0 +1,1170 @@
+// GroupQueryAttention, PagedAttention and RotaryEmbedding for gfx950.
+//
+// Kernels:
+//  * gqa_prep / paged_prep - per new token: optional QK RMS-norm, RoPE on Q and K
+//    (fp32 math, one rounding to the op dtype), new K/V written to their cache
+//    rows (dense present buffer or paged slot); rotated Q (and, paged, rotated K)
+//    staged in the workspace.
+//  * gqa_decode - S == 1 over a dense [B,KV,T,hd] cache. One workgroup per
+//    (batch, kv head, key split); it reads each K/V row once for all H/KV query
+//    heads of the group (16 lanes x 16 bytes per 128-dim row, a wave covers 4
+//    contiguous rows per load), and in the growing contract writes the same rows
+//    to `present` from the registers it already holds, so the past->present copy
+//    costs no extra read. Partial softmax states are merged by attn_merge.
+//  * attn_tile - VALU flash-attention tile for everything else (GQA prefill and
+//    PagedAttention): Q rows of one sequence and one kv-head group against
+//    64-key tiles staged in LDS, online softmax in fp32. Paged keys are fetched
+//    through the block table on the device; no control tensor is read back to
+//    the host.
+//  * attn_merge - log-sum-exp merge of split-K partials.
+#include <type_traits>
+
+#include "common.h"
+
+namespace ortmi {
+
+// ------------------------------------------------------------------ RoPE --
+
+// Rotate dims [off, off + 2*half) of a head vector held in `v` (fp32), in place.
+// Non-interleaved pairs (i, i+half) and interleaved pairs (2i, 2i+1) follow
+// rust/src/ops/attention.rs:1234-1282.
+template <typename T>
+__device__ __forceinline__ void rope_pair_index(int i, int half, int interleaved, int& ia,
+                                                int& ib) {
+    if (interleaved) {
+        ia = 2 * i;
+        ib = 2 * i + 1;
+    } else {
+        ia = i;
+        ib = i + half;
+    }
+}
+
+// Block-cooperative: thread t handles pair t (and t + blockDim.x ...).
+template <typename T>
+__device__ void rope_head_lds(float* v, const T* cos_row, const T* sin_row, int half,
+                              int interleaved, int off) {
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        int ia, ib;
+        rope_pair_index<T>(i, half, interleaved, ia, ib);
+        const float c = to_f32(cos_row[i]), s = to_f32(sin_row[i]);
+        const float a = v[off + ia], b = v[off + ib];
+        v[off + ia] = a * c - b * s;
+        v[off + ib] = b * c + a * s;
+    }
+}
+
+// RMS-normalise a head vector in LDS (block reduction), scale by w.
+template <typename T>
+__device__ void rms_head_lds(float* v, int hd, const T* w, float eps, float* red) {
+    float ss = 0.f;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) ss += v[d] * v[d];
+    ss = wave_sum(ss);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < (int)(blockDim.x + 63) / 64; ++i) tot += red[i];
+    const float inv = 1.0f / sqrtf(tot / hd + eps);
+    __syncthreads();
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) v[d] = round_to<T>(v[d] * inv * to_f32(w[d]));
+    __syncthreads();
+}
+
+// -------------------------------------------------------------- GQA prep --
+
+// One workgroup (64 threads) per (token, head) with heads 0..H-1 = query,
+// H..H+KV-1 = key. Rotated Q goes to qrot [B*S, H, hd]; rotated K and raw V go
+// to present rows valid_past + s.
+template <typename T>
+__global__ __launch_bounds__(64) void gqa_prep_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ cos_c, const T* __restrict__ sin_c, int half, int interleaved,
+    T* __restrict__ qrot, T* __restrict__ pk, T* __restrict__ pv, int B, int S, int H, int KV,
+    int hd, int64_t pcap, int vp, int64_t q_stride, int64_t kv_stride) {
+    extern __shared__ float sv[];
+    const int tok = blockIdx.x;  // b*S + s
+    const int head = blockIdx.y;
+    const int b = tok / S, s = tok % S;
+    const int pos = vp + s;
+    const bool is_q = head < H;
+    const T* src = is_q ? q + (int64_t)tok * q_stride + (int64_t)head * hd
+                        : k + (int64_t)tok * kv_stride + (int64_t)(head - H) * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) sv[d] = to_f32(src[d]);
+    __syncthreads();
+    if (cos_c) rope_head_lds<T>(sv, cos_c + (int64_t)pos * half, sin_c + (int64_t)pos * half, half,
+                                interleaved, 0);
+    __syncthreads();
+    if (is_q) {
+        T* dst = qrot + ((int64_t)tok * H + head) * hd;
+        for (int d = threadIdx.x; d < hd; d += blockDim.x) dst[d] = from_f32<T>(sv[d]);
+    } else {
+        const int kvh = head - H;
+        const int64_t row = (((int64_t)b * KV + kvh) * pcap + pos) * hd;
+        const T* vs = v + (int64_t)tok * kv_stride + (int64_t)kvh * hd;
+        for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+            pk[row + d] = from_f32<T>(sv[d]);
+            pv[row + d] = vs[d];
+        }
+    }
+}
+
+// Plain copy of `rows` rows of hd elements from [B,KV,src_cap,hd] to
+// [B,KV,dst_cap,hd] (rows < copy_rows), 16-byte vectors.
+__global__ __launch_bounds__(256) void kv_copy_kernel(const uint4* __restrict__ src,
+                                                      uint4* __restrict__ dst, int64_t src_cap,
+                                                      int64_t dst_cap, int64_t copy_rows,
+                                                      int vec_per_row, int64_t total_vec) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total_vec; i += stride) {
+        const int64_t per_head = copy_rows * vec_per_row;
+        const int64_t bh = i / per_head;
+        const int64_t rem = i % per_head;
+        dst[bh * dst_cap * vec_per_row + rem] = src[bh * src_cap * vec_per_row + rem];
+    }
+}
+
+// ---------------------------------------------------------- GQA decode --
+
+// Partial state layout (floats): [row][split][vhd + 2] with o (unnormalised),
+// then m (running max) and l (sum of exp).
+template <typename T, int HD, int G>
+__global__ __launch_bounds__(256) void gqa_decode_kernel(
+    const T* __restrict__ qrot, const T* __restrict__ kread, const T* __restrict__ vread,
+    T* __restrict__ kwrite, T* __restrict__ vwrite, int64_t read_cap, int64_t write_cap,
+    int copy_rows, int nkeys, int chunk, int nsplit, int KV, float scale,
+    float* __restrict__ part) {
+    constexpr int LPR = HD / 8;          // lanes per K/V row (16 bytes each)
+    constexpr int RPW = 64 / LPR;        // rows per wave per step
+    constexpr int RPS = 4 * RPW;         // rows per workgroup step
+    __shared__ float s_p[G][1024];
+    __shared__ float s_red[4][G][HD];
+    __shared__ float s_ml[G][2];
+
+    const int bk = blockIdx.x;  // b*KV + kvh
+    const int split = blockIdx.y;
+    const int b = bk / KV, kvh = bk % KV;
+    const int j0 = split * chunk;
+    const int j1 = min(nkeys, j0 + chunk);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = lane / LPR;      // row within the wave step
+    const int dl = (lane % LPR) * 8; // first dim of this lane
+
+    // Query fragment for the G heads of this kv group.
+    float qf[G][8];
+    const int H = KV * G;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const T* qp = qrot + ((int64_t)b * H + kvh * G + g) * HD + dl;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[g][i] = to_f32(qp[i]) * scale;
+    }
+
+    const T* kbase = kread + (int64_t)bk * read_cap * HD;
+    const T* vbase = vread + (int64_t)bk * read_cap * HD;
+    T* kw = kwrite ? kwrite + (int64_t)bk * write_cap * HD : nullptr;
+    T* vw = vwrite ? vwrite + (int64_t)bk * write_cap * HD : nullptr;
+
+    // Scores: rows j0 + step*RPS + wave*RPW + sub, U steps of loads in flight.
+    // Rows at or beyond copy_rows (the new rows of the growing contract) are read
+    // from `present`, the rest from the read buffer.
+    constexpr int U = 4;
+    for (int base = j0; base < j1; base += RPS * U) {
+        uint4 kv4[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = base + u * RPS + wave * RPW + sub;
+            kv4[u] = make_uint4(0, 0, 0, 0);
+            if (j < j1) {
+                const T* src = (kw && j >= copy_rows) ? kw + (int64_t)j * HD + dl
+                                                      : kbase + (int64_t)j * HD + dl;
+                kv4[u] = *reinterpret_cast<const uint4*>(src);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = base + u * RPS + wave * RPW + sub;
+            if (kw && j < copy_rows && j < j1)
+                *reinterpret_cast<uint4*>(kw + (int64_t)j * HD + dl) = kv4[u];
+            const T* kvals = reinterpret_cast<const T*>(&kv4[u]);
+            float kf[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kf[i] = to_f32(kvals[i]);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float d = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
+                d = group_sum<LPR>(d);
+                if (j < j1 && (lane % LPR) == 0) s_p[g][j - j0] = d;
+            }
+        }
+    }
+    __syncthreads();
+    // Softmax statistics per head (one wave per head, G <= 4 handled by looping).
+    const int n = j1 - j0;
+    for (int g = wave; g < G; g += 4) {
+        float m = -INFINITY;
+        for (int i = lane; i < n; i += 64) m = fmaxf(m, s_p[g][i]);
+        m = wave_max(m);
+        float l = 0.f;
+        for (int i = lane; i < n; i += 64) {
+            const float e = __expf(s_p[g][i] - m);
+            s_p[g][i] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            s_ml[g][0] = m;
+            s_ml[g][1] = l;
+        }
+    }
+    __syncthreads();
+    // P.V
+    float o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
+    for (int base = j0; base < j1; base += RPS * U) {
+        uint4 vv4[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = base + u * RPS + wave * RPW + sub;
+            vv4[u] = make_uint4(0, 0, 0, 0);
+            if (j < j1) {
+                const T* src = (vw && j >= copy_rows) ? vw + (int64_t)j * HD + dl
+                                                      : vbase + (int64_t)j * HD + dl;
+                vv4[u] = *reinterpret_cast<const uint4*>(src);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = base + u * RPS + wave * RPW + sub;
+            if (j >= j1) continue;
+            if (vw && j < copy_rows) *reinterpret_cast<uint4*>(vw + (int64_t)j * HD + dl) = vv4[u];
+            const T* vvals = reinterpret_cast<const T*>(&vv4[u]);
+            float vf[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vf[i] = to_f32(vvals[i]);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float p = s_p[g][j - j0];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i]);
+            }
+        }
+    }
+    // Reduce the RPW rows of a wave (lanes with equal lane % LPR), then the 4 waves.
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float x = o[g][i];
+#pragma unroll
+            for (int off = LPR; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
+            o[g][i] = x;
+        }
+    if (sub == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s_red[wave][g][dl + i] = o[g][i];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * HD; idx += 256) {
+        const int g = idx / HD, d = idx % HD;
+        const float acc = s_red[0][g][d] + s_red[1][g][d] + s_red[2][g][d] + s_red[3][g][d];
+        const int64_t row = (int64_t)b * H + kvh * G + g;
+        float* dst = part + (row * nsplit + split) * (HD + 2);
+        dst[d] = acc;
+        if (d == 0) {
+            dst[HD] = s_ml[g][0];
+            dst[HD + 1] = s_ml[g][1];
+        }
+    }
+}
+
+// Merge split partials: out[row][d] = sum_i o_i e^{m_i-M} / sum_i l_i e^{m_i-M}.
+// Output row r goes to out + (r / H) * out_tok_stride + (r % H) * vhd.
+template <typename T>
+__global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict__ part,
+                                                         T* __restrict__ out, int nsplit,
+                                                         const int* __restrict__ nsplit_row,
+                                                         int vhd, int H,
+                                                         int64_t out_tok_stride,
+                                                         const int* __restrict__ row_map) {
+    const int r = blockIdx.x;
+    int orow = r;
+    if (row_map) {
+        orow = row_map[r];
+        if (orow < 0) return;
+    }
+    const int ns = nsplit_row ? nsplit_row[r] : nsplit;
+    const float* p = part + (int64_t)r * nsplit * (vhd + 2);
+    float M = -INFINITY;
+    for (int i = 0; i < ns; ++i) M = fmaxf(M, p[i * (vhd + 2) + vhd]);
+    float L = 0.f;
+    for (int i = 0; i < ns; ++i) {
+        const float m = p[i * (vhd + 2) + vhd];
+        if (m != -INFINITY) L += p[i * (vhd + 2) + vhd + 1] * __expf(m - M);
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    T* o = out + (int64_t)(orow / H) * out_tok_stride + (int64_t)(orow % H) * vhd;
+    for (int d = threadIdx.x; d < vhd; d += blockDim.x) {
+        float acc = 0.f;
+        for (int i = 0; i < ns; ++i) {
+            const float m = p[i * (vhd + 2) + vhd];
+            if (m != -INFINITY) acc += p[i * (vhd + 2) + d] * __expf(m - M);
+        }
+        o[d] = from_f32<T>(acc * inv);
+    }
+}
+
+// ------------------------------------------------------------ attn_tile --
+
+// Key/value source for one (sequence, kv head).
+struct DenseKV {
+    // [B, KV, cap, hd]
+    const void* k;
+    const void* v;
+    int64_t cap;
+    int KV;
+};
+struct PagedKV {
+    const void* kcache;  // [nblk, blk, KV, hd]
+    const void* vcache;  // [nblk, blk, KV, vhd] or null (latent)
+    const void* knew;    // rotated new keys [T, KV, hd]
+    const void* vnew;    // raw new values [T, KV*vhd] or null (latent)
+    const int32_t* bt;
+    int64_t nblk;
+    int blk, maxb, KV;
+};
+
+struct TileDesc {
+    int seq;        // sequence index
+    int tok0;       // first token (packed row) of the tile
+    int ntok;       // tokens in the tile
+    int qpos0;      // absolute position of the first query token
+    int past;       // keys [0, past) come from the cache
+    int nkeys;      // total keys (past + new tokens of the sequence)
+    int tok_seq0;   // first packed token of the sequence (paged)
+};
+
+constexpr int kTileRows = 64;   // max query rows per workgroup
+constexpr int kKeyTile = 64;
+
+template <typename T, int HD, int VHD, bool PAGED>
+__device__ __forceinline__ const T* key_ptr(const DenseKV& d, const PagedKV& p, const TileDesc& t,
+                                            int b, int kvh, int j, bool value) {
+    if constexpr (!PAGED) {
+        const T* base = static_cast<const T*>(value ? d.v : d.k);
+        return base + (((int64_t)b * d.KV + kvh) * d.cap + j) * (value ? VHD : HD);
+    } else {
+        if (j >= t.past) {
+            const int tok = t.tok_seq0 + (j - t.past);
+            if (value && p.vnew)
+                return static_cast<const T*>(p.vnew) + ((int64_t)tok * p.KV + kvh) * VHD;
+            return static_cast<const T*>(p.knew) + ((int64_t)tok * p.KV + kvh) * HD;
+        }
+        const int lb = j / p.blk;
+        const int phys = (j >= 0 && lb < p.maxb) ? p.bt[(int64_t)t.seq * p.maxb + lb] : -1;
+        if (phys < 0 || phys >= p.nblk) return nullptr;
+        const int64_t slot = (int64_t)phys * p.blk + (j % p.blk);
+        if (value && p.vcache)
+            return static_cast<const T*>(p.vcache) + (slot * p.KV + kvh) * VHD;
+        return static_cast<const T*>(p.kcache) + (slot * p.KV + kvh) * HD;
+    }
+}
+
+// One workgroup: `rows` = ntok * G query rows (row r -> token r / G, head r % G
+// of the group) against keys [k0, k1) of one (sequence, kv head). When
+// `part` is null the normalised output is written; otherwise the partial state.
+template <typename T, int HD, int VHD, bool PAGED>
+__device__ void attn_tile_body(const TileDesc& t, int kvh, int G, int H, const T* __restrict__ qrot,
+                               const DenseKV& dk, const PagedKV& pk, float scale,
+                               const float* __restrict__ sink, int k0, int k1,
+                               T* __restrict__ out, int64_t out_tok_stride,
+                               float* __restrict__ part, int nsplit, int split) {
+    __shared__ float sQ[kTileRows][HD + 1];
+    __shared__ T sK[kKeyTile][HD + 8];
+    __shared__ T sV[kKeyTile][VHD + 8];
+    __shared__ float sS[kTileRows][kKeyTile + 1];
+    __shared__ float sM[kTileRows], sL[kTileRows], sAlpha[kTileRows];
+    __shared__ int sOk[kKeyTile];
+
+    const int tid = threadIdx.x;
+    const int rows = t.ntok * G;
+    for (int idx = tid; idx < kTileRows * HD; idx += 256) {
+        const int r = idx / HD, d = idx % HD;
+        float v = 0.f;
+        if (r < rows) {
+            const int tok = t.tok0 + r / G, h = kvh * G + r % G;
+            v = to_f32(qrot[((int64_t)tok * H + h) * HD + d]) * scale;
+        }
+        sQ[r][d] = v;
+    }
+    if (tid < kTileRows) {
+        sM[tid] = -INFINITY;
+        sL[tid] = 0.f;
+    }
+    // Thread -> (row, 16-key slice) for scores; (row, VHD/4 dims) for P.V.
+    const int r_s = tid / 4, c_s = (tid % 4) * 16;
+    constexpr int DV = VHD / 4;
+    const int d_o = (tid % 4) * DV;
+    float o[DV];
+#pragma unroll
+    for (int i = 0; i < DV; ++i) o[i] = 0.f;
+    const bool row_live = r_s < rows;
+    const int qpos = t.qpos0 + r_s / G;
+    __syncthreads();
+
+    for (int kb = k0; kb < k1; kb += kKeyTile) {
+        const int nk = min(kKeyTile, k1 - kb);
+        // Stage K/V tile (16-byte vectors).
+        constexpr int KV_VEC = HD / 8, VV_VEC = VHD / 8;
+        for (int idx = tid; idx < kKeyTile * KV_VEC; idx += 256) {
+            const int r = idx / KV_VEC, c = (idx % KV_VEC) * 8;
+            uint4 val = make_uint4(0, 0, 0, 0);
+            const T* p = r < nk ? key_ptr<T, HD, VHD, PAGED>(dk, pk, t, t.seq, kvh, kb + r, false)
+                                : nullptr;
+            if (p) val = *reinterpret_cast<const uint4*>(p + c);
+            *reinterpret_cast<uint4*>(&sK[r][c]) = val;
+            if (c == 0) sOk[r] = p != nullptr;
+        }
+        for (int idx = tid; idx < kKeyTile * VV_VEC; idx += 256) {
+            const int r = idx / VV_VEC, c = (idx % VV_VEC) * 8;
+            uint4 val = make_uint4(0, 0, 0, 0);
+            if (r < nk) {
+                const T* p = key_ptr<T, HD, VHD, PAGED>(dk, pk, t, t.seq, kvh, kb + r, true);
+                if (p) val = *reinterpret_cast<const uint4*>(p + c);
+            }
+            *reinterpret_cast<uint4*>(&sV[r][c]) = val;
+        }
+        __syncthreads();
+        // Scores.
+        float tmax = -INFINITY;
+        if (row_live) {
+            for (int c = 0; c < 16; ++c) {
+                const int jj = c_s + c, j = kb + jj;
+                float sc = -INFINITY;
+                const bool ok = jj < nk && j <= qpos && sOk[jj];
+                if (ok) {
+                    float acc = 0.f;
+#pragma unroll 16
+                    for (int d = 0; d < HD; ++d) acc = fmaf(sQ[r_s][d], to_f32(sK[jj][d]), acc);
+                    sc = acc;
+                }
+                sS[r_s][jj] = sc;
+                tmax = fmaxf(tmax, sc);
+            }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
+        __syncthreads();
+        if (row_live) {
+            const float m_old = sM[r_s];
+            const float m_new = fmaxf(m_old, tmax);
+            float lsum = 0.f;
+            for (int c = 0; c < 16; ++c) {
+                const int jj = c_s + c;
+                const float e = (m_new == -INFINITY) ? 0.f : __expf(sS[r_s][jj] - m_new);
+                sS[r_s][jj] = e;
+                lsum += e;
+            }
+            lsum += __shfl_xor(lsum, 1, 64);
+            lsum += __shfl_xor(lsum, 2, 64);
+            const float alpha = (m_old == -INFINITY) ? 0.f : __expf(m_old - m_new);
+            if ((tid % 4) == 0) {
+                sL[r_s] = sL[r_s] * alpha + lsum;
+                sM[r_s] = m_new;
+                sAlpha[r_s] = alpha;
+            }
+        }
+        __syncthreads();
+        if (row_live) {
+            const float alpha = sAlpha[r_s];
+#pragma unroll
+            for (int i = 0; i < DV; ++i) o[i] *= alpha;
+            for (int jj = 0; jj < nk; ++jj) {
+                const float p = sS[r_s][jj];
+#pragma unroll
+                for (int i = 0; i < DV; ++i) o[i] = fmaf(p, to_f32(sV[jj][d_o + i]), o[i]);
+            }
+        }
+        __syncthreads();
+    }
+    if (!row_live) return;
+    const int tok = t.tok0 + r_s / G, h = kvh * G + r_s % G;
+    float m = sM[r_s], l = sL[r_s];
+    if (part) {
+        // Partial row index: (tile-local row) handled by caller via `part` offset.
+        float* dst = part + ((int64_t)r_s * nsplit + split) * (VHD + 2);
+#pragma unroll
+        for (int i = 0; i < DV; ++i) dst[d_o + i] = o[i];
+        if ((tid % 4) == 0) {
+            dst[VHD] = m;
+            dst[VHD + 1] = l;
+        }
+        return;
+    }
+    if (sink) {
+        const float sv = sink[h];
+        const float mm = fmaxf(m, sv);
+        const float a = (m == -INFINITY) ? 0.f : __expf(m - mm);
+        l = l * a + __expf(sv - mm);
+#pragma unroll
+        for (int i = 0; i < DV; ++i) o[i] *= a;
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    T* dst = out + (int64_t)tok * out_tok_stride + (int64_t)h * VHD + d_o;
+#pragma unroll
+    for (int i = 0; i < DV; ++i) dst[i] = from_f32<T>(o[i] * inv);
+}
+
+// GQA prefill / S > 1: grid (B * tiles_per_seq, KV). Keys from `present`.
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void gqa_tile_kernel(const T* __restrict__ qrot, DenseKV dk,
+                                                       int S, int QT, int tiles_per_seq, int G,
+                                                       int H, int vp, float scale,
+                                                       T* __restrict__ out) {
+    const int b = blockIdx.x / tiles_per_seq;
+    const int tile = blockIdx.x % tiles_per_seq;
+    const int kvh = blockIdx.y;
+    TileDesc t;
+    t.seq = b;
+    const int s0 = tile * QT;
+    t.ntok = min(QT, S - s0);
+    t.tok0 = b * S + s0;
+    t.qpos0 = vp + s0;
+    t.past = vp;
+    t.nkeys = vp + S;
+    t.tok_seq0 = b * S;
+    PagedKV none{};
+    const int k1 = min(t.nkeys, t.qpos0 + t.ntok);  // causal bound of the tile
+    attn_tile_body<T, HD, HD, false>(t, kvh, G, H, qrot, dk, none, scale, nullptr, 0, k1, out,
+                                     (int64_t)H * HD, nullptr, 1, 0);
+}
+
+// ------------------------------------------------------- PagedAttention --
+
+// Tile map built on the device: for each sequence, ceil(nq/QT) tiles of QT
+// tokens. tiles[i] = {seq, first token, ntok}; tiles[max_tiles] = count.
+__global__ void paged_tilemap_kernel(const int32_t* __restrict__ cum, int batch, int QT,
+                                     int max_tiles, int4* __restrict__ tiles,
+                                     int* __restrict__ count) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    int n = 0;
+    for (int b = 0; b < batch; ++b) {
+        const int s0 = cum[b], s1 = cum[b + 1];
+        for (int t = s0; t < s1 && n < max_tiles; t += QT) {
+            tiles[n] = make_int4(b, t, min(QT, s1 - t), 0);
+            ++n;
+        }
+    }
+    *count = n;
+}
+
+// One workgroup (64 threads) per (token, head slot); slots 0..H-1 are query
+// heads, H..H+KV-1 key heads. Q/K: optional RMS norm, RoPE; rotated Q ->
+// qrot, rotated K -> knew, K/V -> cache slot.
+template <typename T>
+__global__ __launch_bounds__(64) void paged_prep_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    T* __restrict__ kcache, T* __restrict__ vcache, int64_t nblk, int blk,
+    const int32_t* __restrict__ cum, const int32_t* __restrict__ past,
+    const int32_t* __restrict__ bt, int batch, int maxb, const T* __restrict__ cos_c,
+    const T* __restrict__ sin_c, int half, int interleaved, int rot_off,
+    const int32_t* __restrict__ slot_mapping, const T* __restrict__ qw,
+    const T* __restrict__ kw, float eps, int H, int KV, int hd, int vhd,
+    T* __restrict__ qrot, T* __restrict__ knew, int64_t max_pos) {
+    extern __shared__ float sv[];
+    __shared__ float red[4];
+    const int tok = blockIdx.x, head = blockIdx.y;
+    // Sequence of this token: last b with cum[b] <= tok.
+    int lo = 0, hi = batch;  // invariant: cum[lo] <= tok < cum[hi]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (cum[mid] <= tok) lo = mid;
+        else hi = mid;
+    }
+    const int b = lo;
+    const int pos = past[b] + (tok - cum[b]);
+    const bool is_q = head < H;
+    const T* src = is_q ? q + ((int64_t)tok * H + head) * hd
+                        : k + ((int64_t)tok * KV + (head - H)) * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) sv[d] = to_f32(src[d]);
+    __syncthreads();
+    const T* nw = is_q ? qw : kw;
+    if (nw) rms_head_lds<T>(sv, hd, nw, eps, red);
+    if (cos_c) {
+        // A position outside the cache violates the op contract; clamp the row so
+        // the read stays inside the cos/sin tensors.
+        const int64_t prow = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+        rope_head_lds<T>(sv, cos_c + prow * half, sin_c + prow * half, half, interleaved, rot_off);
+        __syncthreads();
+        for (int d = threadIdx.x; d < hd; d += blockDim.x) sv[d] = round_to<T>(sv[d]);
+    }
+    __syncthreads();
+    if (is_q) {
+        T* dst = qrot + ((int64_t)tok * H + head) * hd;
+        for (int d = threadIdx.x; d < hd; d += blockDim.x) dst[d] = from_f32<T>(sv[d]);
+        return;
+    }
+    const int kvh = head - H;
+    T* kn = knew + ((int64_t)tok * KV + kvh) * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) kn[d] = from_f32<T>(sv[d]);
+    int64_t slot;
+    if (slot_mapping) {
+        slot = slot_mapping[tok];
+    } else {
+        const int lb = pos / blk;
+        const int phys = (pos >= 0 && lb < maxb) ? bt[(int64_t)b * maxb + lb] : -1;
+        slot = phys < 0 ? -1 : (int64_t)phys * blk + pos % blk;
+    }
+    if (slot < 0 || slot >= nblk * blk) return;
+    T* kc = kcache + (slot * KV + kvh) * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) kc[d] = from_f32<T>(sv[d]);
+    if (vcache) {
+        const T* vs = v + ((int64_t)tok * KV + kvh) * vhd;
+        T* vc = vcache + (slot * KV + kvh) * vhd;
+        for (int d = threadIdx.x; d < vhd; d += blockDim.x) vc[d] = vs[d];
+    }
+}
+
+// grid (max_tiles, KV, nsplit). Multi-token tiles are not split (split 0 takes
+// all keys); single-token tiles split keys into `chunk`-sized ranges and write
+// partials (merged by attn_merge).
+template <typename T, int HD, int VHD>
+__global__ __launch_bounds__(256) void paged_tile_kernel(
+    const int4* __restrict__ tiles, const int* __restrict__ tile_count,
+    const int32_t* __restrict__ cum, const int32_t* __restrict__ past_lens, PagedKV pk,
+    const T* __restrict__ qrot, int G, int H, float scale, const float* __restrict__ sink,
+    int chunk, int nsplit, T* __restrict__ out, float* __restrict__ part,
+    int* __restrict__ nsplit_row, int* __restrict__ row_map) {
+    const int ti = blockIdx.x, kvh = blockIdx.y, split = blockIdx.z;
+    if (ti >= *tile_count) return;
+    const int4 td = tiles[ti];
+    TileDesc t;
+    t.seq = td.x;
+    t.tok0 = td.y;
+    t.ntok = td.z;
+    t.tok_seq0 = cum[t.seq];
+    t.past = past_lens[t.seq];
+    t.qpos0 = t.past + (t.tok0 - t.tok_seq0);
+    t.nkeys = t.past + (cum[t.seq + 1] - t.tok_seq0);
+    const int kend = min(t.nkeys, t.qpos0 + t.ntok);
+    DenseKV none{};
+    if (t.ntok > 1 || nsplit == 1) {
+        if (split != 0) return;
+        attn_tile_body<T, HD, VHD, true>(t, kvh, G, H, qrot, none, pk, scale, sink, 0, kend, out,
+                                         (int64_t)H * VHD, nullptr, 1, 0);
+        return;
+    }
+    // Single token: split keys.
+    const int ns = min(nsplit, max(1, (kend + chunk - 1) / chunk));
+    const int64_t prow = ((int64_t)ti * pk.KV + kvh) * G;  // partial row base
+    if (split == 0 && threadIdx.x < G) {
+        nsplit_row[prow + threadIdx.x] = ns;
+        row_map[prow + threadIdx.x] = t.tok0 * H + kvh * G + threadIdx.x;
+    }
+    if (split >= ns) return;
+    const int k0 = split * chunk;
+    const int k1 = split == ns - 1 ? kend : min(kend, k0 + chunk);
+    attn_tile_body<T, HD, VHD, true>(t, kvh, G, H, qrot, none, pk, scale, sink, k0, k1, out,
+                                     (int64_t)H * VHD, part + prow * nsplit * (VHD + 2), nsplit,
+                                     split);
+}
+
+// Merge for paged single-token tiles, with the optional head sink folded in.
+template <typename T>
+__global__ __launch_bounds__(128) void paged_merge_kernel(const float* __restrict__ part,
+                                                          T* __restrict__ out, int nsplit,
+                                                          const int* __restrict__ nsplit_row,
+                                                          const int* __restrict__ row_map,
+                                                          int vhd, int H,
+                                                          const float* __restrict__ sink,
+                                                          const int4* __restrict__ tiles,
+                                                          const int* __restrict__ tile_count,
+                                                          int KV, int G) {
+    const int r = blockIdx.x;
+    const int ti = r / (KV * G);
+    if (ti >= *tile_count) return;
+    if (tiles[ti].z != 1) return;
+    const int orow = row_map[r];
+    if (orow < 0) return;
+    const int ns = nsplit_row[r];
+    const float* p = part + (int64_t)r * nsplit * (vhd + 2);
+    float M = -INFINITY;
+    for (int i = 0; i < ns; ++i) M = fmaxf(M, p[i * (vhd + 2) + vhd]);
+    const int h = orow % H;
+    if (sink) M = fmaxf(M, sink[h]);
+    float L = 0.f;
+    for (int i = 0; i < ns; ++i) {
+        const float m = p[i * (vhd + 2) + vhd];
+        if (m != -INFINITY) L += p[i * (vhd + 2) + vhd + 1] * __expf(m - M);
+    }
+    if (sink) L += __expf(sink[h] - M);
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    T* o = out + (int64_t)(orow / H) * ((int64_t)H * vhd) + (int64_t)h * vhd;
+    for (int d = threadIdx.x; d < vhd; d += blockDim.x) {
+        float acc = 0.f;
+        for (int i = 0; i < ns; ++i) {
+            const float m = p[i * (vhd + 2) + vhd];
+            if (m != -INFINITY) acc += p[i * (vhd + 2) + d] * __expf(m - M);
+        }
+        o[d] = from_f32<T>(acc * inv);
+    }
+}
+
+__global__ void fill_i32_kernel(int* __restrict__ p, int v, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void sink_to_f32_kernel(const void* src, int dtype, float* dst, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    if (dtype == ORTMI_F32) dst[i] = static_cast<const float*>(src)[i];
+    else if (dtype == ORTMI_F16) dst[i] = (float)static_cast<const half_t*>(src)[i];
+    else dst[i] = to_f32(static_cast<const uint16_t*>(src)[i]);
+}
+
+// ------------------------------------------------------ RotaryEmbedding --
+
+template <typename T>
+__global__ __launch_bounds__(256) void rotary_kernel(const T* __restrict__ x,
+                                                     const int64_t* __restrict__ pos,
+                                                     int pos_is_offset,
+                                                     const T* __restrict__ cos_c,
+                                                     const T* __restrict__ sin_c,
+                                                     T* __restrict__ y, int B, int S, int NH,
+                                                     int hd, int half, int bnsd,
+                                                     int interleaved, int64_t total_pairs,
+                                                     int64_t max_pos) {
+    // One thread per (b, s, n, pair) plus pass-through of dims >= 2*half.
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int rot = 2 * half;
+    const int per_head = half + (hd - rot);
+    if (i >= total_pairs) return;
+    const int64_t hidx = i / per_head;  // (b, s, n) flattened as b, s, n
+    const int e = (int)(i % per_head);
+    const int n = (int)(hidx % NH);
+    const int64_t bs = hidx / NH;
+    const int s = (int)(bs % S), b = (int)(bs / S);
+    const int64_t base = bnsd ? (((int64_t)b * NH + n) * S + s) * hd
+                              : ((int64_t)b * S + s) * (int64_t)NH * hd + (int64_t)n * hd;
+    if (e >= half) {
+        const int d = rot + (e - half);
+        y[base + d] = x[base + d];
+        return;
+    }
+    int64_t row;
+    if (!pos) row = (int64_t)b * S + s;
+    else if (pos_is_offset) row = pos[0] + s;
+    else row = pos[(int64_t)b * S + s];
+    // Out-of-range positions violate the op contract; clamp so reads stay in bounds.
+    row = row < 0 ? 0 : (row >= max_pos ? max_pos - 1 : row);
+    int ia, ib;
+    rope_pair_index<T>(e, half, interleaved, ia, ib);
+    const float c = to_f32(cos_c[row * half + e]), sn = to_f32(sin_c[row * half + e]);
+    const float a = to_f32(x[base + ia]), bb = to_f32(x[base + ib]);
+    y[base + ia] = from_f32<T>(a * c - bb * sn);
+    y[base + ib] = from_f32<T>(bb * c + a * sn);
+}
+
+// ------------------------------------------------------------- helpers --
+
+static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static int gqa_nsplit(int64_t BKV, int64_t nkeys, int& chunk) {
+    // Aim for >= 2048 workgroups; chunk a multiple of 64 keys, at most 1024.
+    int64_t want = (2048 + BKV - 1) / BKV;
+    int64_t c = (nkeys + want - 1) / want;
+    c = ((c + 63) / 64) * 64;
+    if (c < 64) c = 64;
+    if (c > 1024) c = 1024;
+    chunk = (int)c;
+    return (int)((nkeys + c - 1) / c);
+}
+
+}  // namespace ortmi
+
+using namespace ortmi;
+
+// ---------------------------------------------------------------- GQA API --
+
+extern "C" size_t ortmi_group_query_attention_workspace_size(int64_t batch, int64_t seq_len,
+                                                             int64_t num_heads, int64_t head_size,
+                                                             int64_t total_kv) {
+    // qrot (fp32-sized upper bound) + decode partials.
+    size_t q = align_up((size_t)batch * seq_len * num_heads * head_size * 4);
+    // Chunks are at least 64 keys, so ceil(total_kv / 64) bounds the split count.
+    const int64_t nkv = total_kv > 0 ? total_kv : 1;
+    const int64_t ns = (nkv + 63) / 64;
+    size_t part = align_up((size_t)batch * num_heads * (size_t)ns * (head_size + 2) * 4);
+    return q + part;
+}
+
+template <typename T, int HD>
+static int run_gqa(const void* query, const void* key, const void* value, const void* past_key,
+                   const void* past_value, int64_t cap, int total, const void* cos_c,
+                   const void* sin_c, int half, void* output, void* pk, void* pv, int B, int S,
+                   int H, int KV, float scale, int interleaved, void* ws, size_t ws_bytes,
+                   hipStream_t st) {
+    const int hd = HD;
+    int vp = total - S;
+    bool shared;
+    if (vp < 0 || vp > cap) {
+        shared = false;
+        vp = (int)cap;
+    } else {
+        shared = cap > vp;
+    }
+    const int64_t pcap = shared ? cap : cap + S;
+    const bool packed = key == nullptr;
+    const int64_t q_stride = packed ? (int64_t)(H + 2 * KV) * hd : (int64_t)H * hd;
+    const int64_t kv_stride = packed ? q_stride : (int64_t)KV * hd;
+    const T* q = static_cast<const T*>(query);
+    const T* k = packed ? q + (int64_t)H * hd : static_cast<const T*>(key);
+    const T* v = packed ? q + (int64_t)(H + KV) * hd : static_cast<const T*>(value);
+    const int nkeys = vp + S;
+    const int G = H / KV;
+    const float sc = scale != 0.f ? scale : 1.0f / sqrtf((float)hd);
+
+    size_t need = ortmi_group_query_attention_workspace_size(B, S, H, hd, nkeys);
+    if (!ws || ws_bytes < need)
+        return fail(ORTMI_E_WORKSPACE, "GroupQueryAttention: workspace too small");
+    T* qrot = static_cast<T*>(ws);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(ws) +
+                                           align_up((size_t)B * S * H * hd * 4));
+
+    // Past rows that must reach `present` when it is a different buffer.
+    const bool aliased = (pk == past_key) && (pv == past_value);
+    const bool fuse_copy = !shared && !aliased && S == 1;
+    if (!aliased && !fuse_copy) {
+        // Shared contract into a separate present buffer copies every cap row;
+        // growing prefill copies the cap past rows.
+        const int64_t rows = cap;
+        if (rows > 0) {
+            const int vec_per_row = hd * (int)sizeof(T) / 16;
+            const int64_t total_vec = (int64_t)B * KV * rows * vec_per_row;
+            int grid = (int)std::min<int64_t>((total_vec + 255) / 256, 65536);
+            hipLaunchKernelGGL(kv_copy_kernel, dim3(grid), dim3(256), 0, st,
+                               static_cast<const uint4*>(past_key), static_cast<uint4*>(pk), cap,
+                               pcap, rows, vec_per_row, total_vec);
+            hipLaunchKernelGGL(kv_copy_kernel, dim3(grid), dim3(256), 0, st,
+                               static_cast<const uint4*>(past_value), static_cast<uint4*>(pv),
+                               cap, pcap, rows, vec_per_row, total_vec);
+            if (int rc = check_launch("gqa kv copy")) return rc;
+        }
+    }
+    hipLaunchKernelGGL((gqa_prep_kernel<T>), dim3(B * S, H + KV), dim3(64), hd * sizeof(float), st,
+                       q, k, v, static_cast<const T*>(cos_c), static_cast<const T*>(sin_c), half,
+                       interleaved, qrot, static_cast<T*>(pk), static_cast<T*>(pv), B, S, H, KV,
+                       hd, pcap, vp, q_stride, kv_stride);
+    if (int rc = check_launch("gqa_prep")) return rc;
+
+    if (S == 1 && (G == 1 || G == 2 || G == 4 || G == 8)) {
+        int chunk = 0;
+        const int ns = gqa_nsplit((int64_t)B * KV, nkeys, chunk);
+        // Keys [0, vp) are read from past (fused copy) or present; key vp from present.
+        const T* kread = static_cast<const T*>(fuse_copy ? past_key : pk);
+        const T* vread = static_cast<const T*>(fuse_copy ? past_value : pv);
+        const int64_t read_cap = fuse_copy ? cap : pcap;
+        // In the fused-copy (growing) contract the new row lives in present only:
+        // the kernel reads rows < vp from past and row vp from present. Handle that
+        // by reading from past for rows < vp and present for the last row.
+        dim3 grid(B * KV, ns);
+        auto launch = [&](auto gtag) {
+            constexpr int GG = decltype(gtag)::value;
+            if (fuse_copy) {
+                // Rows [0, vp): read past, write present. Row vp: attended from present.
+                hipLaunchKernelGGL((gqa_decode_kernel<T, HD, GG>), grid, dim3(256), 0, st, qrot,
+                                   kread, vread, static_cast<T*>(pk), static_cast<T*>(pv),
+                                   read_cap, pcap, vp, nkeys, chunk, ns, KV, sc, part);
+            } else {
+                hipLaunchKernelGGL((gqa_decode_kernel<T, HD, GG>), grid, dim3(256), 0, st, qrot,
+                                   kread, vread, (T*)nullptr, (T*)nullptr, read_cap, pcap, 0,
+                                   nkeys, chunk, ns, KV, sc, part);
+            }
+        };
+        if (G == 1) launch(std::integral_constant<int, 1>());
+        if (G == 2) launch(std::integral_constant<int, 2>());
+        if (G == 4) launch(std::integral_constant<int, 4>());
+        if (G == 8) launch(std::integral_constant<int, 8>());
+        if (int rc = check_launch("gqa_decode")) return rc;
+        hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(B * H), dim3(128), 0, st, part,
+                           static_cast<T*>(output), ns, (const int*)nullptr, hd, H,
+                           (int64_t)H * hd, (const int*)nullptr);
+        return check_launch("gqa_merge");
+    }
+    const int QT = std::max(1, kTileRows / G);
+    const int tiles = (S + QT - 1) / QT;
+    DenseKV dk{pk, pv, pcap, KV};
+    hipLaunchKernelGGL((gqa_tile_kernel<T, HD>), dim3(B * tiles, KV), dim3(256), 0, st, qrot, dk,
+                       S, QT, tiles, G, H, vp, sc, static_cast<T*>(output));
+    return check_launch("gqa_tile");
+}
+
+extern "C" int ortmi_group_query_attention(
+    const void* query, const void* key, const void* value, const void* past_key,
+    const void* past_value, int64_t past_cap, int32_t total_sequence_length, const void* cos_cache,
+    const void* sin_cache, int64_t rotary_half, int64_t max_pos, void* output, void* present_key,
+    void* present_value, int64_t batch, int64_t seq_len, int64_t num_heads, int64_t kv_num_heads,
+    int64_t head_size, float scale, int32_t rotary_interleaved, int32_t dtype, void* workspace,
+    size_t workspace_bytes, void* stream) {
+    // Claim/op contract of rust/src/ops/attention.rs:1527-1738 and 556-952.
+    ORTMI_REQUIRE(num_heads > 0 && kv_num_heads > 0 && num_heads % kv_num_heads == 0,
+                  "GroupQueryAttention: num_heads must be a positive multiple of kv_num_heads");
+    ORTMI_REQUIRE(head_size == 64 || head_size == 128,
+                  "GroupQueryAttention: head_size must be 64 or 128");
+    ORTMI_REQUIRE(batch > 0 && seq_len > 0 && past_cap >= 0, "GroupQueryAttention: bad shape");
+    ORTMI_REQUIRE(query && output && present_key && present_value,
+                  "GroupQueryAttention: null tensor");
+    ORTMI_REQUIRE((key == nullptr) == (value == nullptr),
+                  "GroupQueryAttention: key and value must both be given or both be packed");
+    ORTMI_REQUIRE(past_cap == 0 || (past_key && past_value), "GroupQueryAttention: null past");
+    ORTMI_REQUIRE(kv_num_heads <= 4096 && num_heads / kv_num_heads <= 64,
+                  "GroupQueryAttention: too many heads per group");
+    const bool rotary = cos_cache != nullptr;
+    ORTMI_REQUIRE(rotary == (sin_cache != nullptr),
+                  "GroupQueryAttention: cos_cache and sin_cache must both be given");
+    int vp = total_sequence_length - (int)seq_len;
+    if (vp < 0 || vp > past_cap) vp = (int)past_cap;
+    if (rotary) {
+        ORTMI_REQUIRE(rotary_half > 0 && 2 * rotary_half <= head_size,
+                      "GroupQueryAttention: rotary dim exceeds head_size");
+        ORTMI_REQUIRE(vp + seq_len <= max_pos,
+                      "GroupQueryAttention: position exceeds the cos/sin cache");
+    }
+    if (past_cap > 0 && (past_key == present_key) != (past_value == present_value))
+        return fail(ORTMI_E_INVALID, "GroupQueryAttention: present_key/value alias mismatch");
+    const bool shared_c = (total_sequence_length - seq_len >= 0) &&
+                          (total_sequence_length - seq_len <= past_cap) &&
+                          past_cap > total_sequence_length - seq_len;
+    if (!shared_c && past_cap > 0)
+        ORTMI_REQUIRE(past_key != present_key,
+                      "GroupQueryAttention: growing contract cannot write in place");
+    if (shared_c)
+        ORTMI_REQUIRE(total_sequence_length <= past_cap,
+                      "GroupQueryAttention: total_sequence_length exceeds the KV buffer capacity");
+    hipStream_t st = as_stream(stream);
+    const int B = (int)batch, S = (int)seq_len, H = (int)num_heads, KV = (int)kv_num_heads;
+    const int half = (int)rotary_half;
+#define ORTMI_GQA(T, HD)                                                                          \
+    return run_gqa<T, HD>(query, key, value, past_key, past_value, past_cap,                      \
+                          total_sequence_length, cos_cache, sin_cache, half, output, present_key, \
+                          present_value, B, S, H, KV, scale, rotary_interleaved, workspace,       \
+                          workspace_bytes, st)
+    if (dtype == ORTMI_F16) {
+        if (head_size == 64) ORTMI_GQA(half_t, 64);
+        ORTMI_GQA(half_t, 128);
+    }
+    if (dtype == ORTMI_BF16) {
+        if (head_size == 64) ORTMI_GQA(uint16_t, 64);
+        ORTMI_GQA(uint16_t, 128);
+    }
+#undef ORTMI_GQA
+    return fail(ORTMI_E_INVALID, "GroupQueryAttention: dtype must be fp16 or bf16");
+}
+
+// ------------------------------------------------------- PagedAttention API --
+
+static int paged_max_tiles(int64_t T, int64_t batch, int QT) {
+    return (int)((T + QT - 1) / QT + batch);
+}
+static int paged_qt(int G) { return std::max(1, kTileRows / G); }
+static int paged_nsplit(int64_t max_context, int& chunk) {
+    chunk = 512;
+    return (int)std::max<int64_t>(1, (max_context + chunk - 1) / chunk);
+}
+
+extern "C" size_t ortmi_paged_attention_workspace_size(int64_t num_tokens, int64_t batch,
+                                                       int64_t num_heads, int64_t kv_num_heads,
+                                                       int64_t head_size, int64_t v_head_size,
+                                                       int64_t max_context) {
+    const int64_t vhd = v_head_size > 0 ? v_head_size : head_size;
+    const int G = (int)(num_heads / (kv_num_heads > 0 ? kv_num_heads : 1));
+    const int QT = paged_qt(G > 0 ? G : 1);
+    const int mt = paged_max_tiles(num_tokens, batch, QT);
+    int chunk;
+    const int ns = paged_nsplit(max_context, chunk);
+    const int64_t prow = (int64_t)mt * num_heads;  // tiles * KV * G
+    size_t sz = 0;
+    sz += align_up((size_t)num_tokens * num_heads * head_size * 4);      // qrot
+    sz += align_up((size_t)num_tokens * kv_num_heads * head_size * 4);   // knew
+    sz += align_up((size_t)(mt + 1) * 16);                               // tiles + count
+    sz += align_up((size_t)prow * 4 * 2);                                // nsplit_row, row_map
+    sz += align_up((size_t)prow * ns * (vhd + 2) * 4);                   // partials
+    sz += align_up((size_t)num_heads * 4);                               // sink fp32
+    return sz;
+}
+
+template <typename T, int HD, int VHD>
+static int run_paged(const void* query, const void* key, const void* value, void* kcache,
+                     void* vcache, int64_t nblk, int blk, const int32_t* cum, const int32_t* past,
+                     const int32_t* bt, int batch, int maxb, int64_t T_, int64_t max_context,
+                     const void* cos_c, const void* sin_c, int half, int64_t max_pos,
+                     int interleaved, int rot_off, const int32_t* slot_mapping, const void* sink, int sink_dtype,
+                     const void* qw, const void* kw, float eps, void* output, int H, int KV,
+                     float scale, void* ws, size_t ws_bytes, hipStream_t st) {
+    const int G = H / KV;
+    const int QT = paged_qt(G);
+    const int mt = paged_max_tiles(T_, batch, QT);
+    int chunk;
+    const int ns = paged_nsplit(max_context, chunk);
+    const size_t need =
+        ortmi_paged_attention_workspace_size(T_, batch, H, KV, HD, VHD, max_context);
+    if (!ws || ws_bytes < need) return fail(ORTMI_E_WORKSPACE, "PagedAttention: workspace too small");
+    char* p = static_cast<char*>(ws);
+    T* qrot = reinterpret_cast<T*>(p);
+    p += align_up((size_t)T_ * H * HD * 4);
+    T* knew = reinterpret_cast<T*>(p);
+    p += align_up((size_t)T_ * KV * HD * 4);
+    int4* tiles = reinterpret_cast<int4*>(p);
+    int* count = reinterpret_cast<int*>(tiles + mt);
+    p += align_up((size_t)(mt + 1) * 16);
+    const int64_t prow = (int64_t)mt * H;
+    int* nsplit_row = reinterpret_cast<int*>(p);
+    int* row_map = nsplit_row + prow;
+    p += align_up((size_t)prow * 8);
+    float* part = reinterpret_cast<float*>(p);
+    p += align_up((size_t)prow * ns * (VHD + 2) * 4);
+    float* sink32 = reinterpret_cast<float*>(p);
+    const float sc = scale != 0.f ? scale : 1.0f / sqrtf((float)HD);
+
+    if (T_ > 0) {
+        hipLaunchKernelGGL((paged_prep_kernel<T>), dim3((unsigned)T_, H + KV), dim3(64),
+                           HD * sizeof(float), st, static_cast<const T*>(query),
+                           static_cast<const T*>(key), static_cast<const T*>(value),
+                           static_cast<T*>(kcache), static_cast<T*>(vcache), nblk, blk, cum, past,
+                           bt, batch, maxb, static_cast<const T*>(cos_c),
+                           static_cast<const T*>(sin_c), half, interleaved, rot_off, slot_mapping,
+                           static_cast<const T*>(qw), static_cast<const T*>(kw), eps, H, KV, HD,
+                           VHD, qrot, knew, max_pos);
+        if (int rc = check_launch("paged_prep")) return rc;
+    }
+    hipLaunchKernelGGL(paged_tilemap_kernel, dim3(1), dim3(64), 0, st, cum, batch, QT, mt, tiles,
+                       count);
+    if (sink) {
+        hipLaunchKernelGGL(sink_to_f32_kernel, dim3((H + 63) / 64), dim3(64), 0, st, sink,
+                           sink_dtype, sink32, H);
+    }
+    if (int rc = check_launch("paged_tilemap")) return rc;
+    if (T_ == 0) return ORTMI_OK;
+    // Invalidate partial rows so the merge skips rows not owned by a 1-token tile.
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((prow + 255) / 256)), dim3(256), 0, st,
+                       row_map, -1, prow);
+    PagedKV pk{kcache, vcache, knew, value, bt, nblk, blk, maxb, KV};
+    if (!vcache) pk.vnew = nullptr;
+    hipLaunchKernelGGL((paged_tile_kernel<T, HD, VHD>), dim3(mt, KV, ns), dim3(256), 0, st, tiles,
+                       count, cum, past, pk, qrot, G, H, sc, sink ? sink32 : nullptr, chunk, ns,
+                       static_cast<T*>(output), part, nsplit_row, row_map);
+    if (int rc = check_launch("paged_tile")) return rc;
+    if (ns > 1) {
+        hipLaunchKernelGGL((paged_merge_kernel<T>), dim3((unsigned)prow), dim3(128), 0, st, part,
+                           static_cast<T*>(output), ns, nsplit_row, row_map, VHD, H,
+                           sink ? sink32 : nullptr, tiles, count, KV, G);
+        return check_launch("paged_merge");
+    }
+    return ORTMI_OK;
+}
+
+extern "C" int ortmi_paged_attention(
+    const void* query, const void* key, const void* value, void* key_cache, void* value_cache,
+    int64_t num_blocks, int64_t block_size, const int32_t* cum_seqlens,
+    const int32_t* past_seqlens, const int32_t* block_table, int64_t batch, int64_t max_blocks,
+    int64_t num_tokens, int64_t max_context, const void* cos_cache, const void* sin_cache,
+    int64_t rotary_half, int64_t rotary_max_pos, int32_t rotary_interleaved,
+    int64_t rotary_offset,
+    const int32_t* slot_mapping, const void* head_sink, const void* q_norm_weight,
+    const void* k_norm_weight, float qk_norm_eps, void* output, int64_t num_heads,
+    int64_t kv_num_heads, int64_t head_size, int64_t v_head_size, float scale, int32_t dtype,
+    void* workspace, size_t workspace_bytes, void* stream) {
+    // Claim/op contract of rust/src/ops/attention.rs:2746-2977 and 2495-2744.
+    ORTMI_REQUIRE(num_heads > 0 && kv_num_heads > 0 && num_heads % kv_num_heads == 0,
+                  "PagedAttention: bad num_heads/kv_num_heads");
+    const int64_t vhd = v_head_size > 0 ? v_head_size : head_size;
+    const bool latent = value_cache == nullptr;
+    ORTMI_REQUIRE(latent == (value == nullptr),
+                  "PagedAttention: value and value_cache must both be given (or both absent for LATENT)");
+    ORTMI_REQUIRE(head_size == 64 || head_size == 128, "PagedAttention: head_size must be 64 or 128");
+    ORTMI_REQUIRE(vhd == head_size || (latent && (vhd == 64 || vhd == 128) && vhd <= head_size),
+                  "PagedAttention: unsupported v_head_size");
+    ORTMI_REQUIRE(batch > 0 && block_size > 0 && num_blocks > 0 && max_blocks > 0,
+                  "PagedAttention: bad cache or batch shape");
+    ORTMI_REQUIRE(num_tokens >= 0 && num_tokens < (1LL << 31), "PagedAttention: bad token count");
+    ORTMI_REQUIRE(max_context > 0, "PagedAttention: max_context must be positive");
+    ORTMI_REQUIRE(cum_seqlens && past_seqlens && block_table && key_cache && output,
+                  "PagedAttention: null tensor");
+    ORTMI_REQUIRE(num_tokens == 0 || (query && key), "PagedAttention: null query/key");
+    ORTMI_REQUIRE((cos_cache != nullptr) == (sin_cache != nullptr),
+                  "PagedAttention: cos_cache and sin_cache must both be given");
+    ORTMI_REQUIRE(!cos_cache || (rotary_half > 0 && rotary_offset >= 0 &&
+                                 rotary_offset + 2 * rotary_half <= head_size),
+                  "PagedAttention: rotary dims exceed head_size");
+    ORTMI_REQUIRE(!cos_cache || rotary_max_pos > 0, "PagedAttention: empty cos/sin cache");
+    ORTMI_REQUIRE((q_norm_weight != nullptr) == (k_norm_weight != nullptr),
+                  "PagedAttention: q/k norm weights must both be given");
+    ORTMI_REQUIRE(num_heads / kv_num_heads <= 64, "PagedAttention: too many heads per group");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_PA(T, HD, VHD)                                                                     \
+    return run_paged<T, HD, VHD>(query, key, value, key_cache, value_cache, num_blocks,          \
+                                 (int)block_size, cum_seqlens, past_seqlens, block_table,        \
+                                 (int)batch, (int)max_blocks, num_tokens, max_context,           \
+                                 cos_cache, sin_cache, (int)rotary_half, rotary_max_pos,         \
+                                 rotary_interleaved,                                             \
+                                 (int)rotary_offset, slot_mapping, head_sink, dtype,             \
+                                 q_norm_weight, k_norm_weight, qk_norm_eps, output,              \
+                                 (int)num_heads, (int)kv_num_heads, scale, workspace,            \
+                                 workspace_bytes, st)
+    if (dtype == ORTMI_F16) {
+        if (head_size == 64) ORTMI_PA(half_t, 64, 64);
+        if (vhd == 64) ORTMI_PA(half_t, 128, 64);
+        ORTMI_PA(half_t, 128, 128);
+    }
+    if (dtype == ORTMI_BF16) {
+        if (head_size == 64) ORTMI_PA(uint16_t, 64, 64);
+        if (vhd == 64) ORTMI_PA(uint16_t, 128, 64);
+        ORTMI_PA(uint16_t, 128, 128);
+    }
+#undef ORTMI_PA
+    return fail(ORTMI_E_INVALID, "PagedAttention: dtype must be fp16 or bf16");
+}
+
+// ------------------------------------------------------- RotaryEmbedding --
+
+extern "C" int ortmi_rotary_embedding(const void* x, const int64_t* position_ids,
+                                      int32_t pos_is_offset, const void* cos_cache,
+                                      const void* sin_cache, int64_t max_pos, void* y,
+                                      int64_t batch,
+                                      int64_t seq_len, int64_t num_heads, int64_t head_size,
+                                      int64_t rotary_half, int32_t is_bnsd, int32_t interleaved,
+                                      int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(x && y && cos_cache && sin_cache, "RotaryEmbedding: null tensor");
+    ORTMI_REQUIRE(batch >= 0 && seq_len >= 0 && num_heads > 0 && head_size > 0,
+                  "RotaryEmbedding: bad shape");
+    ORTMI_REQUIRE(rotary_half > 0 && 2 * rotary_half <= head_size,
+                  "RotaryEmbedding: rotary dim exceeds head_size");
+    ORTMI_REQUIRE(max_pos > 0, "RotaryEmbedding: empty cos/sin cache");
+    ORTMI_REQUIRE(position_ids || max_pos >= batch * seq_len,
+                  "RotaryEmbedding: per-token cos/sin must have batch*seq_len rows");
+    const int64_t per_head = rotary_half + (head_size - 2 * rotary_half);
+    const int64_t total = batch * seq_len * num_heads * per_head;
+    if (total == 0) return ORTMI_OK;
+    const int grid = (int)((total + 255) / 256);
+    hipStream_t st = as_stream(stream);
+#define ORTMI_ROPE(T)                                                                             \
+    hipLaunchKernelGGL((rotary_kernel<T>), dim3(grid), dim3(256), 0, st, static_cast<const T*>(x), \
+                       position_ids, pos_is_offset, static_cast<const T*>(cos_cache),            \
+                       static_cast<const T*>(sin_cache), static_cast<T*>(y), (int)batch,         \
+                       (int)seq_len, (int)num_heads, (int)head_size, (int)rotary_half, is_bnsd,  \
+                       interleaved, total, max_pos);                                             \
+    return check_launch("rotary")
+    if (dtype == ORTMI_F32) { ORTMI_ROPE(float); }
+    if (dtype == ORTMI_F16) { ORTMI_ROPE(half_t); }
+    if (dtype == ORTMI_BF16) { ORTMI_ROPE(uint16_t); }
+#undef ORTMI_ROPE
+    return fail(ORTMI_E_INVALID, "RotaryEmbedding: unsupported dtype");
+}

@@ -1,0 +1,257 @@
+// (Skip)SimplifiedLayerNormalization and the elementwise/gather glue of the int4
+// decoder graph, for gfx950.
+#include "common.h"
+
+namespace ortmi {
+
+// One workgroup per row. r = x (+ skip) (+ bias), rounded to T when a sum was
+// formed (the reference adds in the op dtype, rust/src/ops/norm.rs:237-238);
+// y = r * rsqrt(mean(r^2) + eps) * gamma with one rounding (norm.rs:239).
+template <typename T>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const T* __restrict__ x,
+                                                       const T* __restrict__ skip,
+                                                       const T* __restrict__ bias,
+                                                       const T* __restrict__ gamma,
+                                                       T* __restrict__ y, T* __restrict__ res,
+                                                       int64_t D, float eps) {
+    extern __shared__ float sr[];  // D floats
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const T* xr = x + row * D;
+    const T* sk = skip ? skip + row * D : nullptr;
+    const bool summed = skip || bias;
+    float ss = 0.f;
+    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
+        float v = to_f32(xr[d]);
+        if (sk) v += to_f32(sk[d]);
+        if (bias) v += to_f32(bias[d]);
+        if (summed) v = round_to<T>(v);
+        sr[d] = v;
+        ss += v * v;
+        if (res) res[row * D + d] = from_f32<T>(v);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / sqrtf(tot / (float)D + eps);
+    for (int64_t d = threadIdx.x; d < D; d += blockDim.x)
+        y[row * D + d] = from_f32<T>(sr[d] * inv * to_f32(gamma[d]));
+}
+
+template <typename T>
+__global__ void gather_rows_kernel(const T* __restrict__ table, const int64_t* __restrict__ ids,
+                                   T* __restrict__ out, int64_t V, int64_t D) {
+    const int64_t r = blockIdx.x;
+    int64_t id = ids[r];
+    if (id < 0) id += V;
+    const bool ok = id >= 0 && id < V;
+    for (int64_t d = threadIdx.x; d < D; d += blockDim.x)
+        out[r * D + d] = ok ? table[id * D + d] : from_f32<T>(0.f);
+}
+
+// Sigmoid -> Mul(g, sig) -> Mul(., u), each result rounded to T.
+template <typename T>
+__global__ void swiglu_kernel(const T* __restrict__ g, const T* __restrict__ u, T* __restrict__ o,
+                              int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float gv = to_f32(g[i]);
+    const float sig = round_to<T>(1.0f / (1.0f + __expf(-gv)));
+    const float t = round_to<T>(gv * sig);
+    o[i] = from_f32<T>(t * to_f32(u[i]));
+}
+
+template <typename T>
+__global__ void binary_kernel(int op, const T* __restrict__ a, const T* __restrict__ b,
+                              T* __restrict__ o, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float x = to_f32(a[i]), y = to_f32(b[i]);
+    const float r = op == 0 ? x + y : (op == 1 ? x * y : x - y);
+    o[i] = from_f32<T>(r);
+}
+
+template <typename T>
+__global__ void sigmoid_kernel(const T* __restrict__ x, T* __restrict__ o, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    o[i] = from_f32<T>(1.0f / (1.0f + __expf(-to_f32(x[i]))));
+}
+
+// First index of the maximum of each row; NaNs are skipped.
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ x,
+                                                          int64_t* __restrict__ out,
+                                                          int64_t cols) {
+    __shared__ float sv[256];
+    __shared__ int64_t si[256];
+    const int64_t row = blockIdx.x;
+    const T* xr = x + row * cols;
+    float best = -INFINITY;
+    int64_t bi = -1;
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+        const float v = to_f32(xr[c]);
+        if (v > best || (bi < 0 && v == best)) {
+            best = v;
+            bi = c;
+        }
+    }
+    sv[threadIdx.x] = best;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            const float ov = sv[threadIdx.x + s];
+            const int64_t oi = si[threadIdx.x + s];
+            const float mv = sv[threadIdx.x];
+            const int64_t mi = si[threadIdx.x];
+            const bool take = oi >= 0 && (mi < 0 || ov > mv || (ov == mv && oi < mi));
+            if (take) {
+                sv[threadIdx.x] = ov;
+                si[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[row] = si[0] < 0 ? 0 : si[0];
+}
+
+template <typename S, typename D>
+__global__ void cast_kernel(const S* __restrict__ x, D* __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = from_f32<D>(to_f32(x[i]));
+}
+
+static unsigned blocks_for(int64_t n, int t = 256) { return (unsigned)((n + t - 1) / t); }
+
+}  // namespace ortmi
+
+using namespace ortmi;
+
+#define ORTMI_DISPATCH_FLOAT(dtype, MACRO)                                      \
+    switch (dtype) {                                                            \
+        case ORTMI_F32: MACRO(float);                                           \
+        case ORTMI_F16: MACRO(half_t);                                          \
+        case ORTMI_BF16: MACRO(uint16_t);                                       \
+        default: return fail(ORTMI_E_INVALID, "unsupported dtype");             \
+    }
+
+extern "C" int ortmi_rms_norm(const void* x, const void* skip, const void* bias,
+                              const void* gamma, void* y, void* residual_out, int64_t rows,
+                              int64_t D, float eps, int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(rows >= 0 && D > 0, "SimplifiedLayerNormalization: bad shape");
+    ORTMI_REQUIRE(D <= 16384, "SimplifiedLayerNormalization: normalized axis too long");
+    if (rows == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(x && gamma && y, "SimplifiedLayerNormalization: null tensor");
+    ORTMI_REQUIRE(rows < (1LL << 31), "SimplifiedLayerNormalization: too many rows");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_RMS(T)                                                                          \
+    hipLaunchKernelGGL((rms_norm_kernel<T>), dim3((unsigned)rows), dim3(256), D * sizeof(float), \
+                       st, static_cast<const T*>(x), static_cast<const T*>(skip),             \
+                       static_cast<const T*>(bias), static_cast<const T*>(gamma),             \
+                       static_cast<T*>(y), static_cast<T*>(residual_out), D, eps);            \
+    return check_launch("rms_norm")
+    ORTMI_DISPATCH_FLOAT(dtype, ORTMI_RMS)
+#undef ORTMI_RMS
+}
+
+extern "C" int ortmi_gather_rows(const void* table, const int64_t* ids, void* out,
+                                 int64_t num_ids, int64_t vocab, int64_t D, int32_t dtype,
+                                 void* stream) {
+    ORTMI_REQUIRE(num_ids >= 0 && vocab > 0 && D > 0, "Gather: bad shape");
+    if (num_ids == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(table && ids && out, "Gather: null tensor");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_GATHER(T)                                                                     \
+    hipLaunchKernelGGL((gather_rows_kernel<T>), dim3((unsigned)num_ids), dim3(256), 0, st,  \
+                       static_cast<const T*>(table), ids, static_cast<T*>(out), vocab, D); \
+    return check_launch("gather_rows")
+    ORTMI_DISPATCH_FLOAT(dtype, ORTMI_GATHER)
+#undef ORTMI_GATHER
+}
+
+extern "C" int ortmi_swiglu(const void* gate, const void* up, void* out, int64_t n,
+                            int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(n >= 0, "SwiGLU: bad size");
+    if (n == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(gate && up && out, "SwiGLU: null tensor");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_SWIGLU(T)                                                                      \
+    hipLaunchKernelGGL((swiglu_kernel<T>), dim3(blocks_for(n)), dim3(256), 0, st,            \
+                       static_cast<const T*>(gate), static_cast<const T*>(up),               \
+                       static_cast<T*>(out), n);                                             \
+    return check_launch("swiglu")
+    ORTMI_DISPATCH_FLOAT(dtype, ORTMI_SWIGLU)
+#undef ORTMI_SWIGLU
+}
+
+extern "C" int ortmi_binary(int32_t op, const void* a, const void* b, void* out, int64_t n,
+                            int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(op >= 0 && op <= 2, "binary: op must be 0 (Add), 1 (Mul) or 2 (Sub)");
+    ORTMI_REQUIRE(n >= 0, "binary: bad size");
+    if (n == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(a && b && out, "binary: null tensor");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_BIN(T)                                                                          \
+    hipLaunchKernelGGL((binary_kernel<T>), dim3(blocks_for(n)), dim3(256), 0, st, (int)op,   \
+                       static_cast<const T*>(a), static_cast<const T*>(b),                   \
+                       static_cast<T*>(out), n);                                             \
+    return check_launch("binary")
+    ORTMI_DISPATCH_FLOAT(dtype, ORTMI_BIN)
+#undef ORTMI_BIN
+}
+
+extern "C" int ortmi_sigmoid(const void* x, void* out, int64_t n, int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(n >= 0, "Sigmoid: bad size");
+    if (n == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(x && out, "Sigmoid: null tensor");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_SIG(T)                                                                           \
+    hipLaunchKernelGGL((sigmoid_kernel<T>), dim3(blocks_for(n)), dim3(256), 0, st,             \
+                       static_cast<const T*>(x), static_cast<T*>(out), n);                     \
+    return check_launch("sigmoid")
+    ORTMI_DISPATCH_FLOAT(dtype, ORTMI_SIG)
+#undef ORTMI_SIG
+}
+
+extern "C" int ortmi_argmax_rows(const void* x, int64_t* out, int64_t rows, int64_t cols,
+                                 int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(rows >= 0 && cols > 0, "ArgMax: bad shape");
+    if (rows == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(x && out, "ArgMax: null tensor");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_ARGMAX(T)                                                                        \
+    hipLaunchKernelGGL((argmax_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0, st,        \
+                       static_cast<const T*>(x), out, cols);                                   \
+    return check_launch("argmax_rows")
+    ORTMI_DISPATCH_FLOAT(dtype, ORTMI_ARGMAX)
+#undef ORTMI_ARGMAX
+}
+
+extern "C" int ortmi_cast(const void* x, int32_t src_dtype, void* y, int32_t dst_dtype, int64_t n,
+                          void* stream) {
+    ORTMI_REQUIRE(n >= 0, "Cast: bad size");
+    if (n == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(x && y, "Cast: null tensor");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_CAST2(S, D)                                                                    \
+    hipLaunchKernelGGL((cast_kernel<S, D>), dim3(blocks_for(n)), dim3(256), 0, st,           \
+                       static_cast<const S*>(x), static_cast<D*>(y), n);                     \
+    return check_launch("cast")
+#define ORTMI_CAST_FROM(S)                                                                   \
+    switch (dst_dtype) {                                                                     \
+        case ORTMI_F32: ORTMI_CAST2(S, float);                                               \
+        case ORTMI_F16: ORTMI_CAST2(S, half_t);                                              \
+        case ORTMI_BF16: ORTMI_CAST2(S, uint16_t);                                           \
+        default: return fail(ORTMI_E_INVALID, "Cast: unsupported destination dtype");       \
+    }
+    switch (src_dtype) {
+        case ORTMI_F32: ORTMI_CAST_FROM(float)
+        case ORTMI_F16: ORTMI_CAST_FROM(half_t)
+        case ORTMI_BF16: ORTMI_CAST_FROM(uint16_t)
+        default: return fail(ORTMI_E_INVALID, "Cast: unsupported source dtype");
+    }
+#undef ORTMI_CAST_FROM
+#undef ORTMI_CAST2
+}

@@ -1,0 +1,247 @@
+"""Python face of the CPU oracle (oracle.c), plus numpy helpers.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, always as the checker (or the timed CPU baseline), never by the
+shipped library.
+
+All float inputs are taken as numpy arrays of any float dtype; fp16 inputs are
+widened exactly to fp32 before the C code sees them. Results are fp64/fp32 arrays
+that the caller rounds to the op dtype.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build() -> str:
+    """Compile liboracle.so with the committed Makefile (gcc + OpenMP)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_flt = ctypes.c_float
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    L.orc_f16_to_f32_n.argtypes = [_u16p, _f32p, _i64]
+    L.orc_f32_to_f16_n.argtypes = [_f32p, _u16p, _i64]
+    L.orc_mnb_dequant.argtypes = [_u8p, _f32p, _u8p, _i64, _i64, _int, _int, _f32p]
+    L.orc_mnb_matmul.argtypes = [_f32p, _u8p, _f32p, _u8p, _i64, _i64, _i64, _int, _int,
+                                 _f64p, _int]
+    L.orc_rotary.argtypes = [_f32p, _f32p, _int, _int, _int, _int, _i64, _i64, _i64, _i64p,
+                             _f32p, _f32p, _int, _int, _int, _int]
+    L.orc_rotary.restype = None
+    L.orc_gqa_contract.argtypes = [_int, _int, _i64, _i32p, _i64p]
+    L.orc_gqa.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _int, _f32p, _f32p, _int,
+                          _int, _int, _int, _int, _int, _int, _flt, _int, _f32p, _f32p, _f32p]
+    L.orc_paged_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _int, _i32p,
+                                      _i32p, _i32p, _int, _int, _f32p, _f32p, _int, _int, _int,
+                                      _i32p, _f32p, _f32p, _f32p, _flt, _int, _int, _int, _int,
+                                      _flt, _int, _f32p]
+    L.orc_rms_norm.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _flt, _int, _f32p,
+                               _f32p]
+    L.orc_rms_norm.restype = None
+
+
+def _p(a, t):
+    if a is None:
+        return None
+    return a.ctypes.data_as(t)
+
+
+def _f32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ------------------------------------------------------------------ fp16 ----
+def f16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().orc_f16_to_f32_n(_p(bits, _u16p), _p(out, _f32p), bits.size)
+    return out
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_n(_p(x, _f32p), _p(out, _u16p), x.size)
+    return out
+
+
+# ------------------------------------------------------------ MatMulNBits ----
+def pack_nibbles(vals: np.ndarray) -> np.ndarray:
+    """Pack 4-bit values along the last axis, low nibble first.
+
+    Restates the packing the reference's tests feed MatMulNBits
+    (tests/ops/test_matmulnbits_asym.py:23-27)."""
+    vals = np.asarray(vals, dtype=np.uint8)
+    return (vals[..., 0::2] | (vals[..., 1::2] << 4)).astype(np.uint8)
+
+
+def pack_zero_points(zp: np.ndarray, bits: int) -> np.ndarray:
+    """[N, nb] zero points -> the ORT input layout (tests/ops/test_matmulnbits_asym.py:48-58):
+    4-bit values are padded to an even count per row and packed, 8-bit ones kept."""
+    zp = np.asarray(zp, dtype=np.uint8)
+    if bits == 8:
+        return zp.reshape(-1).copy()
+    if zp.shape[1] % 2:
+        zp = np.concatenate([zp, np.zeros((zp.shape[0], 1), np.uint8)], axis=1)
+    return pack_nibbles(zp).reshape(-1)
+
+
+def mnb_dequant(B, scales, zp, N, K, bits=4, block=32) -> np.ndarray:
+    B = np.ascontiguousarray(B, dtype=np.uint8)
+    s = _f32(scales)
+    z = None if zp is None else np.ascontiguousarray(zp, dtype=np.uint8)
+    W = np.empty((N, K), np.float32)
+    rc = lib().orc_mnb_dequant(_p(B, _u8p), _p(s, _f32p), _p(z, _u8p), N, K, bits, block,
+                               _p(W, _f32p))
+    if rc:
+        raise ValueError("oracle: unsupported MatMulNBits form")
+    return W
+
+
+def mnb_matmul(A, B, scales, zp, N, K, bits=4, block=32, nthreads=0) -> np.ndarray:
+    A2 = _f32(A).reshape(-1, K)
+    B = np.ascontiguousarray(B, dtype=np.uint8)
+    s = _f32(scales)
+    z = None if zp is None else np.ascontiguousarray(zp, dtype=np.uint8)
+    Y = np.empty((A2.shape[0], N), np.float64)
+    rc = lib().orc_mnb_matmul(_p(A2, _f32p), _p(B, _u8p), _p(s, _f32p), _p(z, _u8p),
+                              A2.shape[0], N, K, bits, block, _p(Y, _f64p), nthreads)
+    if rc:
+        raise ValueError("oracle: unsupported MatMulNBits form")
+    return Y.reshape(tuple(np.shape(A)[:-1]) + (N,))
+
+
+# ------------------------------------------------------------------ RoPE ----
+def rotary(x, rows, cos, sin, interleaved=False, offset=0, round16=False, layout="bsnd",
+           num_heads=None):
+    """Rotary embedding. x is [B,S,NH*hd] (layout 'bsnd' with num_heads given) or
+    [B,NH,S,hd] (layout 'bnsd'); rows[b,s] is the cos/sin cache row of token (b,s)."""
+    x = _f32(x)
+    cos, sin = _f32(cos), _f32(sin)
+    half = cos.shape[-1]
+    if layout == "bnsd":
+        B, NH, S, hd = x.shape
+        sb, ss, sn = NH * S * hd, hd, S * hd
+    else:
+        B, S, hidden = x.shape
+        NH = num_heads
+        hd = hidden // NH
+        sb, ss, sn = S * hidden, hidden, hd
+    rows = np.ascontiguousarray(np.broadcast_to(np.asarray(rows, np.int64), (B, S)))
+    y = np.empty_like(x)
+    lib().orc_rotary(_p(x, _f32p), _p(y, _f32p), B, S, NH, hd, sb, ss, sn, _p(rows, _i64p),
+                     _p(cos, _f32p), _p(sin, _f32p), half, int(interleaved), offset,
+                     int(round16))
+    return y
+
+
+# ------------------------------------------------------------------- GQA ----
+def gqa_contract(total_seq_len: int, S: int, cap: int):
+    vp = ctypes.c_int32(0)
+    pcap = ctypes.c_int64(0)
+    shared = lib().orc_gqa_contract(total_seq_len, S, cap, ctypes.byref(vp), ctypes.byref(pcap))
+    return bool(shared), vp.value, pcap.value
+
+
+def gqa(q, k, v, past_k, past_v, total_seq_len, num_heads, kv_heads, cos=None, sin=None,
+        interleaved=False, scale=0.0, round16=False):
+    """GroupQueryAttention; returns (out [B,S,H*hd] f32, present_k, present_v, shared)."""
+    q = _f32(q)
+    B, S, _ = q.shape
+    past_k, past_v = _f32(past_k), _f32(past_v)
+    _, KV, cap, hd = past_k.shape
+    k, v = _f32(k), _f32(v)
+    shared, vp, pcap = gqa_contract(total_seq_len, S, cap)
+    out = np.zeros((B, S, num_heads * hd), np.float32)
+    pk = np.zeros((B, KV, pcap, hd), np.float32)
+    pv = np.zeros((B, KV, pcap, hd), np.float32)
+    cos, sin = _f32(cos), _f32(sin)
+    half = 0 if cos is None else cos.shape[-1]
+    rc = lib().orc_gqa(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p), _p(past_k, _f32p),
+                       _p(past_v, _f32p), cap, total_seq_len, _p(cos, _f32p), _p(sin, _f32p),
+                       half, int(interleaved), B, S, num_heads, KV, hd, scale, int(round16),
+                       _p(out, _f32p), _p(pk, _f32p), _p(pv, _f32p))
+    if rc < 0:
+        raise ValueError("oracle: bad GroupQueryAttention arguments")
+    return out, pk, pv, shared
+
+
+# -------------------------------------------------------- PagedAttention ----
+def paged_attention(q, k, v, kcache, vcache, cum, past, block_table, num_heads, kv_heads,
+                    cos=None, sin=None, interleaved=False, rotary_offset=0, slot_mapping=None,
+                    head_sink=None, q_norm=None, k_norm=None, qk_eps=1e-6, v_head_size=0,
+                    scale=0.0, round16=False):
+    """PagedAttention; returns (out [T,H*vhd] f32, kcache', vcache'). v/vcache None = LATENT."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    kc = _f32(kcache).copy()
+    vc = None if vcache is None else _f32(vcache).copy()
+    nblk, blk, KV, hd = kc.shape
+    vhd = v_head_size or hd
+    cum = np.ascontiguousarray(cum, np.int32)
+    past = np.ascontiguousarray(past, np.int32)
+    bt = np.ascontiguousarray(block_table, np.int32)
+    batch = cum.shape[0] - 1
+    maxb = bt.shape[1] if bt.ndim == 2 else 0
+    T = int(cum[-1])
+    out = np.zeros((T, num_heads * vhd), np.float32)
+    cos, sin = _f32(cos), _f32(sin)
+    half = 0 if cos is None else cos.shape[-1]
+    sm = None if slot_mapping is None else np.ascontiguousarray(slot_mapping, np.int32)
+    rc = lib().orc_paged_attention(
+        _p(q, _f32p), _p(k, _f32p), _p(v, _f32p), _p(kc, _f32p), _p(vc, _f32p), nblk, blk,
+        _p(cum, _i32p), _p(past, _i32p), _p(bt, _i32p), batch, maxb, _p(cos, _f32p),
+        _p(sin, _f32p), half, int(interleaved), rotary_offset, _p(sm, _i32p),
+        _p(_f32(head_sink), _f32p), _p(_f32(q_norm), _f32p), _p(_f32(k_norm), _f32p), qk_eps,
+        num_heads, KV, hd, vhd, scale, int(round16), _p(out, _f32p))
+    if rc:
+        raise ValueError("oracle: bad PagedAttention arguments")
+    return out, kc, vc
+
+
+# --------------------------------------------------------------- RMS norm ----
+def rms_norm(x, gamma, eps, skip=None, bias=None, round16=False):
+    """(Skip)SimplifiedLayerNormalization; returns (y f32, residual f32)."""
+    x = _f32(x)
+    D = x.shape[-1]
+    rows = x.size // D
+    y = np.empty_like(x)
+    r = np.empty_like(x)
+    lib().orc_rms_norm(_p(x, _f32p), _p(_f32(skip), _f32p), _p(_f32(bias), _f32p),
+                       _p(_f32(gamma), _f32p), rows, D, eps, int(round16), _p(y, _f32p),
+                       _p(r, _f32p))
+    return y, r
+
+
+def round_f16(x) -> np.ndarray:
+    """Round to fp16 (RNE) and widen back to fp32."""
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)

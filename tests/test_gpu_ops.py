@@ -1,0 +1,464 @@
+"""GPU parity: every hot-path kernel, called through the C ABI, against the oracle.
+
+Tolerances (stated per test):
+  * int4/int8 unpack, block and zero-point indexing, KV-cache row copies and
+    paged slot writes: bit-exact.
+  * fp32 outputs: max abs diff <= 6e-5 (plus the fp32-accumulation term for long
+    reductions where noted).
+  * fp16 outputs: |got - exact| <= 1e-3 + 1 fp16 ULP of the exact value (the
+    output is itself rounded to fp16, so a correctly rounded result is within half
+    an ULP; at |y| >= 2 one ULP exceeds 1e-3). The MFMA prefill GEMM also rounds
+    each dequantised weight to fp16 (fp16((q - zp) * s)); its rigorous bound
+    2^-11 * sum_k |a_k * w_nk| is added for that path and reported.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import refs
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(x, dtype=None):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(x))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy() if t.is_floating_point() else t.cpu().numpy()
+
+
+def ulp16(x):
+    x = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.maximum(x, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def assert_f16_close(got, exact, extra=0.0, what=""):
+    got = np.asarray(got, np.float64)
+    exact = np.asarray(exact, np.float64)
+    tol = 1e-3 + ulp16(exact) + extra
+    bad = np.abs(got - exact) > tol
+    assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} beyond tolerance; max diff "
+                           f"{np.abs(got - exact).max():.3e}, max ulp "
+                           f"{refs.max_ulp_f16(got, exact):.2f}")
+
+
+# ------------------------------------------------------------------ MatMulNBits --
+
+def _mnb_inputs(rng, M, N, K, block, bits=4, asym=True, zp_all8=False, dtype=np.float32):
+    nb = (K + block - 1) // block
+    q = rng.integers(0, 1 << bits, size=(N, nb, block), dtype=np.uint8)
+    import oracle
+
+    B = oracle.pack_nibbles(q) if bits == 4 else q
+    s = (np.abs(rng.standard_normal(N * nb) * 0.02) + 1e-4).astype(dtype)
+    zp = None
+    if zp_all8:
+        zp = np.full(N * ((nb + 1) // 2), 0x88, np.uint8)
+    elif asym:
+        zp = oracle.pack_zero_points(rng.integers(0, 1 << bits, size=(N, nb), dtype=np.uint8), bits)
+    A = rng.standard_normal((M, K)).astype(dtype)
+    return A, B, s, zp
+
+
+@pytest.mark.parametrize("K,block", [(256, 32), (1176, 32), (256, 64), (512, 128), (8960, 32),
+                                     (1536, 32)])
+@pytest.mark.parametrize("asym", [False, True])
+def test_mnb_gemv_fp32(ortmi, oracle, K, block, asym):
+    import torch
+
+    rng = np.random.default_rng(K + block + asym)
+    N = 200
+    A, B, s, zp = _mnb_inputs(rng, 1, N, K, block, asym=asym)
+    Y = ortmi.matmul_nbits(dev(A), dev(B), dev(s), None if zp is None else dev(zp), K=K, N=N,
+                           block_size=block)
+    ref = oracle.mnb_matmul(A, B, s, zp, N, K, 4, block)
+    got = host(Y)
+    # fp32: 6e-5 plus fp32 accumulation over K terms (bounded by K * eps32 * sum|a*w|).
+    W = refs.dequant_ref(B, s, zp, N, K, 4, block)
+    acc_bound = K * 2.0 ** -24 * (np.abs(A.astype(np.float64)) @ np.abs(W).T)
+    assert np.all(np.abs(got - ref) <= 6e-5 + acc_bound), np.abs(got - ref).max()
+    assert Y.dtype == torch.float32
+
+
+def test_mnb_gemv_config1_shape(ortmi, oracle):
+    """K=4096, N=11008, fp32, block 32, zero points all 8 (the single-node config)."""
+    rng = np.random.default_rng(2024)
+    K, N = 4096, 11008
+    A, B, s, zp = _mnb_inputs(rng, 1, N, K, 32, zp_all8=True)
+    got = host(ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N))
+    ref = oracle.mnb_matmul(A, B, s, zp, N, K, 4, 32)
+    diff = np.abs(got - ref).max()
+    assert diff <= 6e-5, diff
+
+
+@pytest.mark.parametrize("K,block", [(1536, 32), (8960, 32), (4096, 64)])
+def test_mnb_gemv_fp16(ortmi, oracle, K, block):
+    import torch
+
+    rng = np.random.default_rng(K * 3 + block)
+    N = 300
+    A, B, s, zp = _mnb_inputs(rng, 1, N, K, block, dtype=np.float16)
+    Y = ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N, block_size=block)
+    assert Y.dtype == torch.float16
+    ref = oracle.mnb_matmul(A, B, s, zp, N, K, 4, block)
+    assert_f16_close(host(Y), ref, what="gemv fp16")
+
+
+@pytest.mark.parametrize("M", [2, 8, 64, 130])
+@pytest.mark.parametrize("K,N,block", [(256, 192, 32), (512, 256, 64), (384, 160, 128),
+                                       (1176, 64, 32)])
+def test_mnb_gemm_fp16(ortmi, oracle, M, K, N, block):
+    rng = np.random.default_rng(M * 11 + K + N + block)
+    A, B, s, zp = _mnb_inputs(rng, M, N, K, block, dtype=np.float16)
+    got = host(ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N, block_size=block))
+    ref = oracle.mnb_matmul(A, B, s, zp, N, K, 4, block)
+    W = refs.dequant_ref(B, s, zp, N, K, 4, block)
+    bound = 2.0 ** -11 * (np.abs(A.astype(np.float64)) @ np.abs(W).T)
+    assert_f16_close(got, ref, extra=bound, what="gemm fp16")
+    # Structure check with the weight rounding modelled: exact to output rounding.
+    W16 = W.astype(np.float16).astype(np.float64)
+    ref16 = A.astype(np.float64) @ W16.T
+    assert_f16_close(got, ref16, what="gemm fp16 (fp16 weights)")
+
+
+def test_mnb_gemm_config2_shape(ortmi, oracle):
+    """M=512, K=4096, N=4096 fp16, block 32, zero points U{0..15} (the prefill config)."""
+    rng = np.random.default_rng(4096)
+    M, K, N = 512, 4096, 4096
+    A, B, s, zp = _mnb_inputs(rng, M, N, K, 32, dtype=np.float16)
+    got = host(ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N))
+    rows = np.arange(0, M, 37)  # oracle on a sample of rows keeps the CPU side short
+    ref = oracle.mnb_matmul(A[rows], B, s, zp, N, K, 4, 32)
+    W = refs.dequant_ref(B, s, zp, N, K, 4, 32)
+    bound = 2.0 ** -11 * (np.abs(A[rows].astype(np.float64)) @ np.abs(W).T)
+    assert_f16_close(got[rows], ref, extra=bound, what="gemm config2")
+
+
+@pytest.mark.parametrize("M,bits,block", [(1, 8, 32), (3, 8, 64), (1, 4, 16), (5, 4, 16)])
+def test_mnb_generic_forms_fp32(ortmi, oracle, M, bits, block):
+    rng = np.random.default_rng(M + bits + block)
+    K, N = 3 * block + 5, 70
+    A, B, s, zp = _mnb_inputs(rng, M, N, K, block, bits=bits)
+    got = host(ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N, bits=bits,
+                                  block_size=block))
+    ref = oracle.mnb_matmul(A, B, s, zp, N, K, bits, block)
+    assert np.abs(got - ref).max() <= 6e-5
+
+
+def test_mnb_dequant_indexing_bit_exact(ortmi, oracle):
+    """One-hot activations read single dequantised columns: (q - zp) * s must be
+    exact in fp32 for every code, block and zero-point nibble."""
+    rng = np.random.default_rng(5)
+    N, K, block = 64, 256, 32
+    _, B, s, zp = _mnb_inputs(rng, 1, N, K, block)
+    W = oracle.mnb_dequant(B, s, zp, N, K, 4, block)
+    Bd, sd, zd = dev(B), dev(s), dev(zp)
+    for k in (0, 1, 30, 31, 32, 33, 127, 128, 255):
+        e = np.zeros((1, K), np.float32)
+        e[0, k] = 1
+        got = host(ortmi.matmul_nbits(dev(e), Bd, sd, zd, K=K, N=N))
+        np.testing.assert_array_equal(got[0], W[:, k])
+
+
+# ------------------------------------------------------------ GroupQueryAttention --
+
+def _gqa_inputs(rng, B, S, H, KV, hd, cap, rope=True, base=10000.0, max_pos=8192):
+    q = rng.standard_normal((B, S, H * hd)).astype(np.float16)
+    k = rng.standard_normal((B, S, KV * hd)).astype(np.float16)
+    v = rng.standard_normal((B, S, KV * hd)).astype(np.float16)
+    pk = rng.standard_normal((B, KV, cap, hd)).astype(np.float16)
+    pv = rng.standard_normal((B, KV, cap, hd)).astype(np.float16)
+    cos = sin = None
+    if rope:
+        c, s_ = refs.rotary_caches(max_pos, hd, base)
+        cos, sin = c.astype(np.float16), s_.astype(np.float16)
+    return q, k, v, pk, pv, cos, sin
+
+
+def _run_gqa(ortmi, oracle, B, S, H, KV, hd, cap, past, rope=True, interleaved=False,
+             inplace=False, seed=0, base=10000.0):
+    import torch
+
+    rng = np.random.default_rng(seed)
+    q, k, v, pk, pv, cos, sin = _gqa_inputs(rng, B, S, H, KV, hd, cap, rope, base)
+    total = past + S
+    dq, dk, dv, dpk, dpv = dev(q), dev(k), dev(v), dev(pk), dev(pv)
+    kw = {}
+    if inplace:
+        kw = dict(present_key=dpk, present_value=dpv)
+    out, prk, prv = ortmi.group_query_attention(
+        dq, dk, dv, dpk, dpv, dev(np.full(B, total - 1, np.int32)), total,
+        None if cos is None else dev(cos), None if sin is None else dev(sin), num_heads=H,
+        kv_num_heads=KV, do_rotary=int(rope), rotary_interleaved=int(interleaved), **kw)
+    ro, rk, rv, shared = oracle.gqa(q, k, v, pk, pv, total, H, KV, cos=cos, sin=sin,
+                                    interleaved=interleaved, round16=True)
+    assert_f16_close(host(out), ro, what="gqa output")
+    got_k, got_v = host(prk), host(prv)
+    vp = past if (0 <= past <= cap) else cap
+    # Rows other than the new ones are bit-exact copies; new V rows are copies of
+    # the input; new K rows are RoPE outputs rounded once (<= 1 fp16 ULP).
+    old = np.ones(got_k.shape[2], bool)
+    old[vp:vp + S] = False
+    np.testing.assert_array_equal(got_k[:, :, old], rk[:, :, old].astype(np.float16).astype(np.float32))
+    np.testing.assert_array_equal(got_v, rv.astype(np.float16).astype(np.float32))
+    dk_new = np.abs(got_k[:, :, vp:vp + S] - rk[:, :, vp:vp + S])
+    assert (dk_new <= ulp16(rk[:, :, vp:vp + S])).all()
+    assert prk.dtype == torch.float16
+    return shared
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_gqa_decode_growing(ortmi, oracle, interleaved):
+    assert not _run_gqa(ortmi, oracle, B=2, S=1, H=8, KV=2, hd=128, cap=300, past=300,
+                        interleaved=interleaved, seed=1)
+
+
+def test_gqa_decode_shared_inplace(ortmi, oracle):
+    assert _run_gqa(ortmi, oracle, B=2, S=1, H=12, KV=2, hd=128, cap=512, past=200, inplace=True,
+                    seed=2, base=1e6)
+
+
+def test_gqa_decode_shared_separate_present(ortmi, oracle):
+    assert _run_gqa(ortmi, oracle, B=3, S=1, H=4, KV=4, hd=64, cap=100, past=37, seed=3)
+
+
+def test_gqa_decode_config3_shape(ortmi, oracle):
+    """B=8, H=32, KV=8, hd=128, past 4096, growing contract (the decode config)."""
+    assert not _run_gqa(ortmi, oracle, B=8, S=1, H=32, KV=8, hd=128, cap=4096, past=4096, seed=4)
+
+
+@pytest.mark.parametrize("S,past,cap", [(16, 0, 0), (5, 7, 7), (33, 10, 64)])
+def test_gqa_prefill(ortmi, oracle, S, past, cap):
+    _run_gqa(ortmi, oracle, B=2, S=S, H=8, KV=2, hd=128, cap=cap, past=past, seed=S + past)
+
+
+def test_gqa_prefill_decoder_shape(ortmi, oracle):
+    """Prompt of 128 tokens into an empty shared buffer, 12 query / 2 kv heads, base 1e6."""
+    _run_gqa(ortmi, oracle, B=1, S=128, H=12, KV=2, hd=128, cap=256, past=0, inplace=True,
+             seed=9, base=1e6)
+
+
+def test_gqa_no_rotary(ortmi, oracle):
+    _run_gqa(ortmi, oracle, B=1, S=1, H=8, KV=8, hd=64, cap=40, past=40, rope=False, seed=12)
+
+
+# ------------------------------------------------------------------ PagedAttention --
+
+def _run_paged(ortmi, oracle, H, KV, d, nb, blk, batch, seed, rope=False, interleaved=0,
+               new_max=4, slot_mapping=None, head_sink=None, qk_norm=False):
+    rng = np.random.default_rng(seed)
+    maxb = nb // batch
+    cap = maxb * blk
+    new_lens = rng.integers(1, min(new_max, cap) + 1, size=batch).astype(np.int32)
+    past = np.array([rng.integers(0, cap - nl + 1) for nl in new_lens], np.int32)
+    cum = np.concatenate([[0], np.cumsum(new_lens)]).astype(np.int32)
+    nt = int(cum[-1])
+    q = (rng.standard_normal((nt, H * d)) * 0.3).astype(np.float16)
+    k = (rng.standard_normal((nt, KV * d)) * 0.3).astype(np.float16)
+    v = (rng.standard_normal((nt, KV * d)) * 0.3).astype(np.float16)
+    kc = (rng.standard_normal((nb, blk, KV, d)) * 0.3).astype(np.float16)
+    vc = (rng.standard_normal((nb, blk, KV, d)) * 0.3).astype(np.float16)
+    bt = rng.permutation(nb).astype(np.int32).reshape(batch, maxb)
+    cos = sin = None
+    if rope:
+        c, s_ = refs.rotary_caches(cap, d)
+        cos, sin = c.astype(np.float16), s_.astype(np.float16)
+    qw = kw = None
+    if qk_norm:
+        qw = np.linspace(0.75, 1.25, d).astype(np.float16)
+        kw = np.linspace(1.25, 0.75, d).astype(np.float16)
+    sm = None if slot_mapping is None else slot_mapping(cum, past, bt, blk)
+    dkc, dvc = dev(kc), dev(vc)
+    out = ortmi.paged_attention(
+        dev(q), dev(k), dev(v), dkc, dvc, dev(cum), dev(past), dev(bt),
+        None if cos is None else dev(cos), None if sin is None else dev(sin),
+        None if sm is None else dev(sm), None if head_sink is None else dev(head_sink),
+        None if qw is None else dev(qw), None if kw is None else dev(kw), num_heads=H,
+        kv_num_heads=KV, do_rotary=int(rope), rotary_interleaved=interleaved,
+        qk_norm_epsilon=1e-5)
+    ro, rkc, rvc = oracle.paged_attention(q, k, v, kc, vc, cum, past, bt, H, KV, cos=cos, sin=sin,
+                                          interleaved=interleaved, slot_mapping=sm,
+                                          head_sink=head_sink, q_norm=qw, k_norm=kw,
+                                          qk_eps=1e-5, round16=True)
+    assert_f16_close(host(out), ro, what="paged output")
+    gk, gv = host(dkc), host(dvc)
+    np.testing.assert_array_equal(gv, rvc)  # slot writes of V are bit-exact copies
+    # K slots: untouched rows bit-exact, written rows within 1 ULP (rounded RoPE/norm).
+    assert (np.abs(gk - rkc) <= ulp16(rkc)).all()
+    return out
+
+
+@pytest.mark.parametrize("H,KV", [(4, 2), (4, 4), (8, 2), (2, 1)])
+@pytest.mark.parametrize("batch", [1, 3])
+def test_paged_core(ortmi, oracle, H, KV, batch):
+    _run_paged(ortmi, oracle, H, KV, 64, nb=8 * batch, blk=4, batch=batch, seed=H * 10 + KV + batch)
+
+
+@pytest.mark.parametrize("blk", [2, 16])
+def test_paged_multiblock_long(ortmi, oracle, blk):
+    # Long pasts force the split-K path for single-token sequences.
+    _run_paged(ortmi, oracle, 8, 2, 128, nb=96 * 2, blk=blk, batch=2, seed=blk + 7, new_max=1)
+
+
+@pytest.mark.parametrize("interleaved", [0, 1])
+def test_paged_rotary(ortmi, oracle, interleaved):
+    _run_paged(ortmi, oracle, 4, 2, 64, nb=16, blk=4, batch=2, seed=31 + interleaved, rope=True,
+               interleaved=interleaved)
+
+
+def test_paged_optional_inputs(ortmi, oracle):
+    def slots(cum, past, bt, blk):
+        nt = int(cum[-1])
+        s = np.full(nt, -1, np.int32)
+        for b in range(len(cum) - 1):
+            for i in range(cum[b], cum[b + 1]):
+                p = past[b] + (i - cum[b])
+                s[i] = bt[b, p // blk] * blk + p % blk
+        s[0] = -1
+        return s
+    sink = np.array([-0.5, 0.25, 1.0, -1.0], np.float16)
+    _run_paged(ortmi, oracle, 4, 2, 64, nb=8, blk=4, batch=2, seed=129, slot_mapping=slots,
+               head_sink=sink, qk_norm=True)
+
+
+def test_paged_mixed_batch_reduced(ortmi, oracle):
+    """Mixed prefill + decode: 2 sequences prefill 40-token chunks, 6 decode one token,
+    block 16, 32/8 heads, hd 128 (a reduced form of the mixed-batch config)."""
+    rng = np.random.default_rng(55)
+    H, KV, d, blk = 32, 8, 128, 16
+    ctx = rng.integers(64, 700, size=8)
+    new = np.array([40, 40, 1, 1, 1, 1, 1, 1])
+    past = (ctx - new).astype(np.int32)
+    nblocks = [int((c + blk - 1) // blk) for c in ctx]
+    nb = sum(nblocks)
+    maxb = max(nblocks)
+    perm = rng.permutation(nb).astype(np.int32)
+    bt = np.zeros((8, maxb), np.int32)
+    o = 0
+    for b, n in enumerate(nblocks):
+        bt[b, :n] = perm[o:o + n]
+        o += n
+    cum = np.concatenate([[0], np.cumsum(new)]).astype(np.int32)
+    nt = int(cum[-1])
+    q = rng.standard_normal((nt, H * d)).astype(np.float16)
+    k = rng.standard_normal((nt, KV * d)).astype(np.float16)
+    v = rng.standard_normal((nt, KV * d)).astype(np.float16)
+    kc = rng.standard_normal((nb, blk, KV, d)).astype(np.float16)
+    vc = rng.standard_normal((nb, blk, KV, d)).astype(np.float16)
+    dkc, dvc = dev(kc), dev(vc)
+    out = ortmi.paged_attention(dev(q), dev(k), dev(v), dkc, dvc, dev(cum), dev(past), dev(bt),
+                                num_heads=H, kv_num_heads=KV)
+    ro, rkc, rvc = oracle.paged_attention(q, k, v, kc, vc, cum, past, bt, H, KV, round16=True)
+    assert_f16_close(host(out), ro, what="paged mixed")
+    np.testing.assert_array_equal(host(dkc), rkc)
+    np.testing.assert_array_equal(host(dvc), rvc)
+
+
+# ---------------------------------------------------------------- RotaryEmbedding --
+
+@pytest.mark.parametrize("form", ["bsnd_ids", "bsnd_offset", "bnsd_ids", "per_token"])
+@pytest.mark.parametrize("interleaved", [0, 1])
+def test_rotary_embedding(ortmi, oracle, form, interleaved):
+    import torch
+
+    rng = np.random.default_rng(hash(form) % 1000 + interleaved)
+    B, S, NH, hd = 2, 7, 4, 64
+    c, s_ = refs.rotary_caches(64, hd)
+    cos, sin = c.astype(np.float16), s_.astype(np.float16)
+    x = rng.standard_normal((B, S, NH * hd)).astype(np.float16)
+    if form == "bsnd_offset":
+        pos = np.array([5], np.int64)
+        rows = np.broadcast_to(5 + np.arange(S), (B, S))
+    elif form == "per_token":
+        pos = None
+        rows = np.arange(B * S).reshape(B, S)
+        cos = cos[:B * S].reshape(B, S, hd // 2)
+        sin = sin[:B * S].reshape(B, S, hd // 2)
+    else:
+        pos = rng.integers(0, 64, size=(B, S)).astype(np.int64)
+        rows = pos
+    xin = x
+    if form == "bnsd_ids":
+        xin = x.reshape(B, S, NH, hd).transpose(0, 2, 1, 3).copy()
+    y = ortmi.rotary_embedding(dev(xin), None if pos is None else dev(pos), dev(cos), dev(sin),
+                               interleaved=interleaved, num_heads=NH)
+    ref = oracle.rotary(x, rows, cos.reshape(-1, hd // 2), sin.reshape(-1, hd // 2),
+                        interleaved=bool(interleaved), num_heads=NH, round16=True)
+    got = host(y)
+    if form == "bnsd_ids":
+        got = got.transpose(0, 2, 1, 3).reshape(B, S, NH * hd)
+    assert (np.abs(got - ref) <= ulp16(ref)).all()
+    assert y.dtype == torch.float16
+
+
+# ------------------------------------------------------------ (Skip)SimplifiedLN --
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+@pytest.mark.parametrize("skip", [False, True])
+def test_rms_norm(ortmi, oracle, dtype, skip):
+    rng = np.random.default_rng(int(skip) + (dtype == np.float16))
+    x = rng.standard_normal((9, 1536)).astype(dtype)
+    sk = rng.standard_normal((9, 1536)).astype(dtype)
+    g = rng.standard_normal(1536).astype(dtype)
+    r16 = dtype == np.float16
+    if skip:
+        y, r = ortmi.skip_simplified_layer_norm(dev(x), dev(sk), dev(g), epsilon=1e-6)
+        ry, rr = oracle.rms_norm(x, g, 1e-6, skip=sk, round16=r16)
+        np.testing.assert_array_equal(host(r), rr)  # residual: one rounding of x + skip
+    else:
+        y = ortmi.simplified_layer_norm(dev(x), dev(g), epsilon=1e-5)
+        ry, _ = oracle.rms_norm(x, g, 1e-5, round16=r16)
+    if r16:
+        assert_f16_close(host(y), ry, what="rms fp16")
+    else:
+        assert np.abs(host(y) - ry).max() <= 6e-5
+
+
+# ------------------------------------------------------------------------- glue --
+
+def test_glue_kernels(ortmi):
+    import ctypes
+
+    import torch
+
+    lib = ortmi.load_kernels()
+    rng = np.random.default_rng(77)
+    g = rng.standard_normal(5000).astype(np.float16)
+    u = rng.standard_normal(5000).astype(np.float16)
+    dg, du = dev(g), dev(u)
+    out = torch.empty_like(dg)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ortmi.check(lib.ortmi_swiglu(ctypes.c_void_p(dg.data_ptr()), ctypes.c_void_p(du.data_ptr()),
+                                 ctypes.c_void_p(out.data_ptr()), 5000, 10, st))
+    g32 = g.astype(np.float32)
+    sig = (1.0 / (1.0 + np.exp(-g32.astype(np.float64)))).astype(np.float16).astype(np.float32)
+    t = (g32 * sig).astype(np.float16).astype(np.float32)
+    ref = (t * u.astype(np.float32)).astype(np.float16).astype(np.float32)
+    assert (np.abs(host(out) - ref) <= ulp16(ref)).all()
+    # argmax: first index on ties
+    x = rng.standard_normal((3, 151936)).astype(np.float16)
+    x[1, 17] = x[1, 99] = 100.0
+    idx = torch.empty(3, dtype=torch.int64, device="cuda")
+    dx = dev(x)
+    ortmi.check(lib.ortmi_argmax_rows(ctypes.c_void_p(dx.data_ptr()), ctypes.c_void_p(idx.data_ptr()),
+                                      3, 151936, 10, st))
+    np.testing.assert_array_equal(host(idx), np.argmax(x.astype(np.float32), axis=1))
+    # gather rows with a negative id
+    table = rng.standard_normal((100, 64)).astype(np.float16)
+    ids = np.array([3, -1, 50], np.int64)
+    dt_, di = dev(table), dev(ids)
+    o = torch.empty((3, 64), dtype=torch.float16, device="cuda")
+    ortmi.check(lib.ortmi_gather_rows(ctypes.c_void_p(dt_.data_ptr()), ctypes.c_void_p(di.data_ptr()),
+                                      ctypes.c_void_p(o.data_ptr()), 3, 100, 64, 10, st))
+    np.testing.assert_array_equal(host(o), table[[3, 99, 50]].astype(np.float32))

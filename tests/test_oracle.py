@@ -1,0 +1,354 @@
+"""Pin the C oracle (oracle/oracle.c) before it is trusted as the parity target.
+
+Each check is chosen so that a plausible mistake in the oracle (nibble order, zero
+point column, block index, sign of the rotation, GQA head mapping, causal offset,
+cache slot arithmetic) fails it: closed forms, known-answer data from the
+reference's own tests, and independent numpy restatements of the reference
+tests' numpy references (tests/refs.py). CPU only.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import refs
+
+# --------------------------------------------------------------------- fp16 ---
+
+
+def test_f16_conversions_match_ieee(oracle):
+    bits = np.arange(65536, dtype=np.uint16)
+    f = oracle.f16_bits_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    same = (f.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(f) & np.isnan(ref))
+    assert same.all()
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(200_000) * np.exp(rng.uniform(-25, 12, 200_000))).astype(np.float32)
+    edge = np.array([65504, 65519.99, 65520, 2.0**-24, 2.0**-25, 3 * 2.0**-26, -0.0, np.inf],
+                    np.float32)
+    x = np.concatenate([x, edge])
+    with np.errstate(over="ignore"):
+        assert (oracle.f32_to_f16_bits(x) == x.astype(np.float16).view(np.uint16)).all()
+
+
+# -------------------------------------------------------------- MatMulNBits ---
+
+
+def _gbq_fixture():
+    """Known-answer data of tests/ops/_models.py:558-580: two rows of 32 codes,
+    code k of row r = (k + r) & 15, packed low nibble first, block 16, scales
+    [[0.5, 1], [2, 4]], symmetric (zero point 8)."""
+    qdata = np.empty((2, 16), np.uint8)
+    for row in range(2):
+        vals = (np.arange(32, dtype=np.uint8) + row) & 0x0F
+        qdata[row] = vals[0::2] | (vals[1::2] << 4)
+    scales = np.array([[0.5, 1.0], [2.0, 4.0]], np.float32)
+    return qdata, scales
+
+
+def test_mnb_dequant_known_answer(oracle):
+    qdata, scales = _gbq_fixture()
+    W = oracle.mnb_dequant(qdata, scales, None, N=2, K=32, bits=4, block=16)
+    # Closed form of the fixture, written out by hand: w[r,k] = (((k+r)&15) - 8) * s[r, k//16].
+    expected = np.array([[(((k + r) & 15) - 8) * scales[r, k // 16] for k in range(32)]
+                         for r in range(2)], np.float32)
+    np.testing.assert_array_equal(W, expected)
+    # The GatherBlockQuantized op of that test gathers rows [1, -2] -> [1, 0].
+    np.testing.assert_array_equal(W[[1, 0]], expected[[1, 0]])
+    # A nibble-order mistake would not pass: swapping nibbles changes the table.
+    swapped = ((qdata & 0x0F) << 4) | (qdata >> 4)
+    assert not np.array_equal(oracle.mnb_dequant(swapped, scales, None, 2, 32, 4, 16), expected)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("block", [16, 32, 64, 128])
+@pytest.mark.parametrize("asym", [False, True])
+def test_mnb_dequant_matches_numpy_unpack(oracle, bits, block, asym):
+    rng = np.random.default_rng(bits * 1000 + block + asym)
+    N, K = 5, block * 3 - (7 if block > 16 else 0)  # includes a partial final block
+    nb = (K + block - 1) // block
+    q = rng.integers(0, 1 << bits, size=(N, nb, block), dtype=np.uint8)
+    B = oracle.pack_nibbles(q) if bits == 4 else q
+    s = (rng.standard_normal(N * nb) * 0.05).astype(np.float32)
+    zp = None
+    if asym:
+        zp = oracle.pack_zero_points(rng.integers(0, 1 << bits, size=(N, nb), dtype=np.uint8), bits)
+    W = oracle.mnb_dequant(B, s, zp, N, K, bits, block)
+    np.testing.assert_array_equal(W, refs.dequant_ref(B, s, zp, N, K, bits, block).astype(np.float32))
+
+
+def test_mnb_special_cases(oracle):
+    rng = np.random.default_rng(7)
+    N, K, bs = 6, 96, 32
+    nb = K // bs
+    q = rng.integers(0, 16, size=(N, nb, bs), dtype=np.uint8)
+    B = oracle.pack_nibbles(q)
+    s = np.abs(rng.standard_normal(N * nb)).astype(np.float32) + 0.1
+    # All-8 zero points are the symmetric form (config-1 zero points are all 0x88).
+    zp8 = np.full(N * ((nb + 1) // 2), 0x88, np.uint8)
+    A = rng.standard_normal((3, K)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.mnb_matmul(A, B, s, zp8, N, K),
+                                  oracle.mnb_matmul(A, B, s, None, N, K))
+    # Codes equal to their zero point dequantise to exactly zero.
+    zq = oracle.pack_zero_points(q[:, :, 0], 4)
+    q_eq = np.repeat(q[:, :, :1], bs, axis=2)
+    assert not oracle.mnb_matmul(A, oracle.pack_nibbles(q_eq), s, zq, N, K).any()
+    # A one-hot activation row selects one dequantised column.
+    W = refs.dequant_ref(B, s, None, N, K, 4, bs)
+    for k in (0, 31, 32, 95):
+        e = np.zeros((1, K), np.float32)
+        e[0, k] = 1
+        np.testing.assert_array_equal(oracle.mnb_matmul(e, B, s, None, N, K)[0], W[:, k])
+
+
+@pytest.mark.parametrize("M", [1, 8])
+@pytest.mark.parametrize("K,block", [(128, 32), (1176, 32), (192, 64), (384, 128), (48, 16)])
+def test_mnb_matmul_matches_fp64_gemm(oracle, M, K, block):
+    rng = np.random.default_rng(M * 7 + K)
+    N = 33
+    nb = (K + block - 1) // block
+    B = oracle.pack_nibbles(rng.integers(0, 16, size=(N, nb, block), dtype=np.uint8))
+    s = (rng.standard_normal(N * nb) * 0.05).astype(np.float32)
+    zp = oracle.pack_zero_points(rng.integers(0, 16, size=(N, nb), dtype=np.uint8), 4)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    Y = oracle.mnb_matmul(A, B, s, zp, N, K, 4, block)
+    ref = A.astype(np.float64) @ refs.dequant_ref(B, s, zp, N, K, 4, block).T
+    np.testing.assert_allclose(Y, ref, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------- RoPE ---
+
+
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rotary_closed_forms(oracle, interleaved):
+    rng = np.random.default_rng(3)
+    B, S, NH, hd = 2, 5, 3, 16
+    cos, sin = refs.rotary_caches(64, hd)
+    x = rng.standard_normal((B, S, NH * hd)).astype(np.float32)
+    rows = np.arange(S)[None, :] + np.array([[0], [7]])
+    y = oracle.rotary(x, rows, cos, sin, interleaved=interleaved, num_heads=NH)
+    # Position 0 is the identity (cos 1, sin 0).
+    np.testing.assert_allclose(y[0, 0], x[0, 0], rtol=0, atol=1e-7)
+    # Each rotated pair keeps its norm.
+    xr = x.reshape(B, S, NH, hd).astype(np.float64)
+    yr = y.reshape(B, S, NH, hd).astype(np.float64)
+    if interleaved:
+        nx = xr[..., 0::2] ** 2 + xr[..., 1::2] ** 2
+        ny = yr[..., 0::2] ** 2 + yr[..., 1::2] ** 2
+    else:
+        nx = xr[..., :8] ** 2 + xr[..., 8:] ** 2
+        ny = yr[..., :8] ** 2 + yr[..., 8:] ** 2
+    np.testing.assert_allclose(ny, nx, rtol=1e-5)
+    # Against the numpy restatement (sign of the rotation, pair layout).
+    for b in range(B):
+        ref = refs.apply_rope(xr[b], cos, sin, rows[b], interleaved)
+        np.testing.assert_allclose(yr[b], ref, rtol=1e-5, atol=1e-6)
+    # Rotation by p1 then p2 equals rotation by p1 + p2 (exact caches).
+    y1 = oracle.rotary(x, np.full((B, S), 3), cos, sin, interleaved=interleaved, num_heads=NH)
+    y2 = oracle.rotary(y1, np.full((B, S), 4), cos, sin, interleaved=interleaved, num_heads=NH)
+    y7 = oracle.rotary(x, np.full((B, S), 7), cos, sin, interleaved=interleaved, num_heads=NH)
+    np.testing.assert_allclose(y2, y7, rtol=1e-5, atol=1e-5)
+
+
+def test_rotary_partial_dims_pass_through(oracle):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((1, 3, 2 * 32)).astype(np.float32)
+    cos, sin = refs.rotary_caches(16, 16)  # rotary dim 16 of head 32
+    y = oracle.rotary(x, np.arange(3)[None], cos, sin, num_heads=2)
+    np.testing.assert_array_equal(y.reshape(1, 3, 2, 32)[..., 16:], x.reshape(1, 3, 2, 32)[..., 16:])
+
+
+# ----------------------------------------------------------------------- GQA ---
+
+
+@pytest.mark.parametrize("S,past,cap", [(1, 12, 12), (1, 12, 20), (5, 0, 0), (4, 6, 16), (3, 8, 8)])
+@pytest.mark.parametrize("rope", [False, True])
+def test_gqa_matches_numpy(oracle, S, past, cap, rope):
+    rng = np.random.default_rng(S * 100 + past * 10 + cap + rope)
+    B, H, KV, hd = 2, 8, 2, 16
+    q = rng.standard_normal((B, S, H * hd)).astype(np.float32)
+    k = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    v = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    pk = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    pv = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    total = past + S
+    cos = sin = None
+    if rope:
+        cos, sin = refs.rotary_caches(64, hd)
+    out, pres_k, pres_v, shared = oracle.gqa(q, k, v, pk, pv, total, H, KV, cos=cos, sin=sin)
+    ro, rk, rv = refs.gqa_ref(q, k, v, pk, pv, total, H, KV, cos=cos, sin=sin)
+    assert shared == (cap > past)
+    np.testing.assert_allclose(out, ro, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(pres_k, rk, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(pres_v, rv, rtol=0, atol=0)
+
+
+def test_gqa_packed_equals_separate(oracle):
+    rng = np.random.default_rng(5)
+    B, S, H, KV, hd, cap = 1, 3, 4, 2, 8, 5
+    q = rng.standard_normal((B, S, H * hd)).astype(np.float32)
+    k = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    v = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    pk = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    pv = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    a = oracle.gqa(q, k, v, pk, pv, cap + S, H, KV)
+    packed = np.concatenate([q, k, v], axis=-1)
+    b = oracle.gqa(packed, None, None, pk, pv, cap + S, H, KV)
+    np.testing.assert_array_equal(a[0], b[0])
+
+
+def test_gqa_single_key_returns_value(oracle):
+    # With no past and S = 1 the only key is the new one: softmax = 1, out = V.
+    rng = np.random.default_rng(6)
+    B, H, KV, hd = 1, 4, 1, 8
+    q = rng.standard_normal((B, 1, H * hd)).astype(np.float32)
+    k = rng.standard_normal((B, 1, KV * hd)).astype(np.float32)
+    v = rng.standard_normal((B, 1, KV * hd)).astype(np.float32)
+    empty = np.zeros((B, KV, 0, hd), np.float32)
+    out, *_ = oracle.gqa(q, k, v, empty, empty, 1, H, KV)
+    np.testing.assert_allclose(out.reshape(H, hd), np.tile(v.reshape(1, hd), (H, 1)), rtol=1e-6)
+
+
+def test_gqa_head_mapping_sensitivity(oracle):
+    # Query head h must read kv head h // (H/KV); an h % KV mapping would differ.
+    rng = np.random.default_rng(8)
+    B, S, H, KV, hd, cap = 1, 1, 4, 2, 8, 6
+    q = rng.standard_normal((B, S, H * hd)).astype(np.float32)
+    k = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    v = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    pk = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    pv = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    out, *_ = oracle.gqa(q, k, v, pk, pv, cap + 1, H, KV)
+    ref, *_ = refs.gqa_ref(q, k, v, pk, pv, cap + 1, H, KV)
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+    swapped_kv = pk[:, ::-1].copy(), pv[:, ::-1].copy()
+    other, *_ = oracle.gqa(q, k[..., ::-1].copy(), v, *swapped_kv, cap + 1, H, KV)
+    assert not np.allclose(other, out)
+
+
+# ------------------------------------------------------------ PagedAttention ---
+
+
+def _paged_case(rng, H, KV, d, nb, blk, batch, new_max=4):
+    maxb = nb // batch
+    cap = maxb * blk
+    new_lens = rng.integers(1, min(new_max, cap) + 1, size=batch).astype(np.int32)
+    past = np.array([rng.integers(0, cap - nl + 1) for nl in new_lens], np.int32)
+    cum = np.concatenate([[0], np.cumsum(new_lens)]).astype(np.int32)
+    nt = int(cum[-1])
+    q = (rng.standard_normal((nt, H * d)) * 0.3).astype(np.float32)
+    k = (rng.standard_normal((nt, KV * d)) * 0.3).astype(np.float32)
+    v = (rng.standard_normal((nt, KV * d)) * 0.3).astype(np.float32)
+    kc = (rng.standard_normal((nb, blk, KV, d)) * 0.3).astype(np.float32)
+    vc = (rng.standard_normal((nb, blk, KV, d)) * 0.3).astype(np.float32)
+    bt = rng.permutation(nb).astype(np.int32).reshape(batch, maxb)
+    return q, k, v, kc, vc, cum, past, bt
+
+
+@pytest.mark.parametrize("H,KV", [(4, 2), (4, 4), (8, 2), (2, 1)])
+@pytest.mark.parametrize("rope,interleaved", [(False, 0), (True, 0), (True, 1)])
+def test_paged_matches_numpy(oracle, H, KV, rope, interleaved):
+    rng = np.random.default_rng(H * 10 + KV + rope * 3 + interleaved)
+    d, blk, batch = 16, 4, 3
+    q, k, v, kc, vc, cum, past, bt = _paged_case(rng, H, KV, d, 8 * batch, blk, batch)
+    cos = sin = None
+    if rope:
+        cos, sin = refs.rotary_caches(8 * blk, d)
+    out, okc, ovc = oracle.paged_attention(q, k, v, kc, vc, cum, past, bt, H, KV, cos=cos, sin=sin,
+                                           interleaved=interleaved)
+    ref, rkc, rvc = refs.paged_ref(q, k, v, kc, vc, cum, past, bt, H, KV, d, cos=cos, sin=sin,
+                                   interleaved=interleaved)
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(okc, rkc, rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(ovc, rvc)
+
+
+def test_paged_optional_inputs(oracle):
+    # slot_mapping (with a skipped slot), head_sink and QK-norm together
+    # (tests/ops/test_paged_attention.py:290-457 form).
+    rng = np.random.default_rng(129)
+    h, kv, d, nb, blk = 4, 2, 8, 4, 4
+    q = rng.standard_normal((3, h * d)).astype(np.float32)
+    k = rng.standard_normal((3, kv * d)).astype(np.float32)
+    v = rng.standard_normal((3, kv * d)).astype(np.float32)
+    kc = rng.standard_normal((nb, blk, kv, d)).astype(np.float32)
+    vc = rng.standard_normal((nb, blk, kv, d)).astype(np.float32)
+    cum = np.array([0, 3], np.int32)
+    past = np.array([3], np.int32)
+    bt = np.array([[2, 0, 1, 3]], np.int32)
+    slots = np.array([3, -1, 9], np.int32)
+    sink = np.array([-0.5, 0.25, 1.0, -1.0], np.float32)
+    qw = np.linspace(0.75, 1.25, d).astype(np.float32)
+    kw = np.linspace(1.25, 0.75, d).astype(np.float32)
+    out, okc, ovc = oracle.paged_attention(q, k, v, kc, vc, cum, past, bt, h, kv,
+                                           slot_mapping=slots, head_sink=sink, q_norm=qw,
+                                           k_norm=kw, qk_eps=1e-5)
+    ref, rkc, rvc = refs.paged_ref(q, k, v, kc, vc, cum, past, bt, h, kv, d, slot_mapping=slots,
+                                   head_sink=sink, q_norm=qw, k_norm=kw, norm_eps=1e-5)
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(okc, rkc, rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(ovc, rvc)
+
+
+def test_paged_latent_layout_and_offset(oracle):
+    rng = np.random.default_rng(291)
+    h, kv, d, vd, nb, blk = 2, 1, 16, 8, 3, 4
+    q = (rng.standard_normal((2, h * d)) * 0.2).astype(np.float32)
+    k = (rng.standard_normal((2, d)) * 0.2).astype(np.float32)
+    kc = (rng.standard_normal((nb, blk, kv, d)) * 0.2).astype(np.float32)
+    cum, past, bt = np.array([0, 2], np.int32), np.array([3], np.int32), np.array([[1, 0, 2]], np.int32)
+    cos, sin = refs.rotary_caches(nb * blk, 8)
+    out, okc, _ = oracle.paged_attention(q, k, None, kc, None, cum, past, bt, h, kv, cos=cos,
+                                         sin=sin, rotary_offset=8, v_head_size=vd, scale=0.2)
+    ref, rkc, _ = refs.paged_ref(q, k, None, kc, None, cum, past, bt, h, kv, d, cos=cos, sin=sin,
+                                 rotary_offset=8, vd=vd, scale=0.2)
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(okc, rkc, rtol=1e-6, atol=1e-6)
+
+
+def test_paged_equals_dense_gqa_and_is_permutation_invariant(oracle):
+    # Identity block table over a contiguous cache is dense GQA; relabelling the
+    # physical blocks (and the table) must not change the output.
+    rng = np.random.default_rng(11)
+    H, KV, d, blk, past, nq = 4, 2, 16, 4, 9, 3
+    nblk = 4
+    q = rng.standard_normal((nq, H * d)).astype(np.float32)
+    k = rng.standard_normal((nq, KV * d)).astype(np.float32)
+    v = rng.standard_normal((nq, KV * d)).astype(np.float32)
+    kc = rng.standard_normal((nblk, blk, KV, d)).astype(np.float32)
+    vc = rng.standard_normal((nblk, blk, KV, d)).astype(np.float32)
+    cum, pastv = np.array([0, nq], np.int32), np.array([past], np.int32)
+    ident = np.arange(nblk, dtype=np.int32)[None]
+    out, *_ = oracle.paged_attention(q, k, v, kc, vc, cum, pastv, ident, H, KV)
+    dense_pk = kc.reshape(nblk * blk, KV, d)[:past].transpose(1, 0, 2)[None]
+    dense_pv = vc.reshape(nblk * blk, KV, d)[:past].transpose(1, 0, 2)[None]
+    g, *_ = oracle.gqa(q[None], k[None], v[None], dense_pk.copy(), dense_pv.copy(), past + nq, H, KV)
+    np.testing.assert_allclose(out, g[0], rtol=1e-5, atol=1e-6)
+    perm = rng.permutation(nblk)
+    inv = np.argsort(perm)
+    kc2, vc2 = kc[perm], vc[perm]  # physical block i now holds old block perm[i]
+    table2 = inv[ident].astype(np.int32)
+    out2, *_ = oracle.paged_attention(q, k, v, kc2, vc2, cum, pastv, table2, H, KV)
+    np.testing.assert_allclose(out2, out, rtol=1e-6, atol=1e-7)
+
+
+# ------------------------------------------------------------------ RMS norm ---
+
+
+def test_rms_norm_closed_form_and_numpy(oracle):
+    D = 64
+    gamma = np.linspace(0.5, 1.5, D).astype(np.float32)
+    x = np.full((2, D), 3.0, np.float32)
+    y, _ = oracle.rms_norm(x, gamma, 1e-6)
+    np.testing.assert_allclose(y, np.broadcast_to(3.0 / np.sqrt(9.0 + 1e-6) * gamma, (2, D)),
+                               rtol=1e-6)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((5, D)).astype(np.float32)
+    skip = rng.standard_normal((5, D)).astype(np.float32)
+    y, r = oracle.rms_norm(x, gamma, 1e-6, skip=skip)
+    np.testing.assert_allclose(r, x + skip, rtol=1e-6)
+    np.testing.assert_allclose(y, refs.rms_norm_ref(x + skip, gamma), rtol=1e-5, atol=1e-6)
+    # fp16 residual rounding: the norm is taken of the rounded residual.
+    y16, r16 = oracle.rms_norm(x, gamma, 1e-6, skip=skip, round16=True)
+    np.testing.assert_array_equal(r16, (x + skip).astype(np.float16).astype(np.float32))
+    np.testing.assert_allclose(y16, refs.rms_norm_ref(r16, gamma), rtol=1e-5, atol=1e-6)
