@@ -1,0 +1,372 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X execution provider's hot path on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|gemv|gemm|gqa|paged|copy]
+
+Primary line: int4 MatMulNBits decode GEMV (K=4096, N=11008, block 32, fp32
+activations) as achieved HBM GB/s. A step is one MatMulNBits call; consecutive
+steps rotate over >= 512 MB of distinct weight copies so every call streams its
+weights from HBM, not from the 256 MB Infinity Cache. Launches are captured in a
+HIP graph and replayed, and the per-launch duration is taken from HIP events
+recorded on the stream the kernels run on.
+
+Secondary measurements (same JSON line, "secondary"): the MFMA prefill GEMM
+(M=512, K=N=4096, fp16), the GQA decode step (B=8, H=32/8, hd=128, 4K context,
+growing KV contract) and the PagedAttention mixed batch.
+
+cpu_baseline: the oracle's C restatement of MatMulNBits (OpenMP over the host
+cores) timed on a bounded sample of the same GEMV on this machine's CPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "onnxruntime-mlx_amd")
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP16_DENSE_TFLOPS = 2500.0     # MI355X dense fp16 MFMA
+MALL_BYTES = 256 << 20         # Infinity Cache
+
+METRIC = "int4 MatMulNBits GB/s (% HBM peak); int4 decoder decode tokens/sec, 1 GPU"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def load_pkg():
+    if "ortmi" in sys.modules:
+        return sys.modules["ortmi"]
+    spec = importlib.util.spec_from_file_location(
+        "ortmi", os.path.join(PKG_DIR, "__init__.py"), submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["ortmi"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def timed_graph(torch, launch_batch, batch_len, steps, warmup):
+    """Capture `launch_batch()` (batch_len launches) in a HIP graph, replay it to
+    cover warmup + steps launches; return (gpu ms per launch, wall ms per launch)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launch_batch()  # eager warm-up outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch_batch()
+    reps_w = max(1, warmup // batch_len)
+    reps = max(1, steps // batch_len)
+    for _ in range(reps_w):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    n = reps * batch_len
+    return e0.elapsed_time(e1) / n, (t1 - t0) * 1e3 / n, n
+
+
+def timed_eager(torch, launch_one, steps, warmup):
+    for i in range(warmup):
+        launch_one(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        launch_one(i)
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return e0.elapsed_time(e1) / steps, (t1 - t0) * 1e3 / steps, steps
+
+
+# ------------------------------------------------------------------- workloads --
+
+def bench_gemv(torch, ortmi, steps, warmup):
+    import ctypes
+
+    from ortmi import workloads  # noqa: F401  (loaded as a submodule)
+
+    wl = sys.modules["ortmi.workloads"]
+    K, N = 4096, 11008
+    A, B, s, zp = wl.mnb_gemv_config()
+    bytes_per_call = B.nbytes + s.nbytes + zp.nbytes + A.nbytes + N * 4
+    copies = max(2, -(-(2 * MALL_BYTES) // bytes_per_call))
+    dA = torch.from_numpy(A).cuda()
+    dB0, ds0, dz0 = (torch.from_numpy(x).cuda() for x in (B, s, zp))
+    bufs = [(dB0, ds0, dz0)] + [(dB0.clone(), ds0.clone(), dz0.clone()) for _ in range(copies - 1)]
+    Y = torch.empty((1, N), dtype=torch.float32, device="cuda")
+    lib = ortmi.load_kernels()
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    args = [(ptr(dA), ptr(b), ptr(sc), ptr(z), ptr(Y)) for b, sc, z in bufs]
+
+    def launch_batch():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for a, b, sc, z, y in args:
+            rc = lib.ortmi_matmul_nbits(a, b, sc, z, y, 1, N, K, 4, 32, 1, st)
+            if rc:
+                raise RuntimeError(lib.ortmi_last_error().decode())
+
+    gpu_ms, wall_ms, n = timed_graph(torch, launch_batch, len(args), steps, warmup)
+    gbs = bytes_per_call / (gpu_ms * 1e-3) / 1e9
+    return dict(kernel="mnb_gemv4_kernel<float,32,2,4>", bytes_per_call=bytes_per_call,
+                copies=copies, gpu_ms=gpu_ms, wall_ms=wall_ms, launches=n, gbs=gbs,
+                inputs=(A, B, s, zp))
+
+
+def bench_gemm(torch, ortmi, steps, warmup):
+    import ctypes
+
+    wl = sys.modules["ortmi.workloads"]
+    M, K, N = 512, 4096, 4096
+    A, B, s, zp = wl.mnb_gemm_config()
+    dA, dB, ds, dz = (torch.from_numpy(x).cuda() for x in (A, B, s, zp))
+    Y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    lib = ortmi.load_kernels()
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    a = (ptr(dA), ptr(dB), ptr(ds), ptr(dz), ptr(Y))
+
+    def launch_batch():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for _ in range(10):
+            rc = lib.ortmi_matmul_nbits(*a, M, N, K, 4, 32, 10, st)
+            if rc:
+                raise RuntimeError(lib.ortmi_last_error().decode())
+
+    gpu_ms, wall_ms, n = timed_graph(torch, launch_batch, 10, max(10, steps // 10),
+                                     max(10, warmup // 10))
+    flops = 2.0 * M * N * K
+    tflops = flops / (gpu_ms * 1e-3) / 1e12
+    return dict(kernel="mnb_gemm4_kernel", flops_per_call=flops, gpu_ms=gpu_ms, wall_ms=wall_ms,
+                launches=n, tflops=tflops, mfma_frac=tflops / FP16_DENSE_TFLOPS)
+
+
+def bench_gqa(torch, ortmi, steps, warmup):
+    import ctypes
+
+    wl = sys.modules["ortmi.workloads"]
+    cfg = wl.gqa_decode_config()
+    B, H, KV, hd, past = 8, 32, 8, 128, 4096
+    kv_bytes = cfg["pk"].nbytes + cfg["pv"].nbytes
+    copies = max(2, -(-(2 * MALL_BYTES) // (2 * kv_bytes)))
+    dq, dk, dv = (torch.from_numpy(cfg[x]).cuda() for x in ("q", "k", "v"))
+    dcos, dsin = torch.from_numpy(cfg["cos"]).cuda(), torch.from_numpy(cfg["sin"]).cuda()
+    pk0, pv0 = torch.from_numpy(cfg["pk"]).cuda(), torch.from_numpy(cfg["pv"]).cuda()
+    pasts = [(pk0, pv0)] + [(pk0.clone(), pv0.clone()) for _ in range(copies - 1)]
+    presents = [(torch.empty((B, KV, past + 1, hd), dtype=torch.float16, device="cuda"),
+                 torch.empty((B, KV, past + 1, hd), dtype=torch.float16, device="cuda"))
+                for _ in range(copies)]
+    out = torch.empty((B, 1, H * hd), dtype=torch.float16, device="cuda")
+    lib = ortmi.load_kernels()
+    ws_bytes = lib.ortmi_group_query_attention_workspace_size(B, 1, H, hd, past + 1)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    total = past + 1
+
+    def launch_batch():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for (pk, pv), (prk, prv) in zip(pasts, presents):
+            rc = lib.ortmi_group_query_attention(
+                ptr(dq), ptr(dk), ptr(dv), ptr(pk), ptr(pv), past, total, ptr(dcos), ptr(dsin),
+                hd // 2, 8192, ptr(out), ptr(prk), ptr(prv), B, 1, H, KV, hd, 0.0, 0, 10, ptr(ws),
+                ws_bytes, st)
+            if rc:
+                raise RuntimeError(lib.ortmi_last_error().decode())
+
+    gpu_ms, wall_ms, n = timed_graph(torch, launch_batch, copies, max(copies, steps // 20),
+                                     max(copies, warmup // 20))
+    read = kv_bytes
+    write = 2 * B * KV * (past + 1) * hd * 2
+    small = (B * H * hd * 2) * 2 + (B * KV * hd * 2) * 2
+    total_bytes = read + write + small
+    return dict(kernels="gqa_prep + gqa_decode + attn_merge", contract="growing",
+                bytes_per_call=total_bytes, copies=copies, gpu_ms=gpu_ms, wall_ms=wall_ms,
+                launches=n, gbs=total_bytes / (gpu_ms * 1e-3) / 1e9)
+
+
+def bench_paged(torch, ortmi, steps, warmup):
+    wl = sys.modules["ortmi.workloads"]
+    cfg = wl.paged_mixed_config()
+    d = {k: torch.from_numpy(cfg[k]).cuda() for k in ("q", "k", "v", "kc", "vc", "cum", "past", "bt")}
+    H, KV = cfg["H"], cfg["KV"]
+
+    def launch_one(_i):
+        ortmi.paged_attention(d["q"], d["k"], d["v"], d["kc"], d["vc"], d["cum"], d["past"],
+                              d["bt"], num_heads=H, kv_num_heads=KV)
+
+    reps = max(3, steps // 200)
+    gpu_ms, wall_ms, n = timed_eager(torch, launch_one, reps, max(1, warmup // 200))
+    nbytes, flops = wl.paged_work(cfg)
+    return dict(kernels="paged_prep + paged_tilemap + paged_tile + paged_merge",
+                bytes_per_call=nbytes, flops_per_call=flops, gpu_ms=gpu_ms, wall_ms=wall_ms,
+                launches=n, gbs=nbytes / (gpu_ms * 1e-3) / 1e9,
+                tflops=flops / (gpu_ms * 1e-3) / 1e12, tokens=int(cfg["new"].sum()),
+                total_context=int(cfg["ctx"].sum()))
+
+
+def bench_copy(torch, steps, warmup):
+    """Plain device copy of a known size, for calibrating rocprofv3 byte counters."""
+    n = 512 << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+
+    def one(_i):
+        b.copy_(a)
+
+    gpu_ms, wall_ms, k = timed_eager(torch, one, max(5, steps // 100), 2)
+    return dict(bytes_read=n, bytes_written=n, gpu_ms=gpu_ms, gbs=2 * n / (gpu_ms * 1e-3) / 1e9)
+
+
+def cpu_baseline_gemv(inputs, budget_s=12.0):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle
+
+    A, B, s, zp = inputs
+    K, N = A.shape[1], B.shape[0]
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    times = []
+    t_start = time.perf_counter()
+    while (len(times) < 3 or time.perf_counter() - t_start < budget_s) and len(times) < 200:
+        t0 = time.perf_counter()
+        oracle.mnb_matmul(A, B, s, zp, N, K, 4, 32, nthreads=threads)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    nbytes = B.nbytes + s.nbytes + zp.nbytes + A.nbytes + N * 4
+    return dict(value=nbytes / med / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"{len(times)} full K=4096 N=11008 int4 GEMV calls of the oracle's C "
+                       f"restatement (fp64 accumulation, OpenMP {threads} threads); median "
+                       f"{med * 1e3:.2f} ms per call")
+
+
+# ------------------------------------------------------------------------ main --
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "gemv", "gemm", "gqa", "paged", "copy"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the sharding "
+              "design is described in DESIGN.md); run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    ortmi = load_pkg()
+    import importlib
+
+    importlib.import_module("ortmi.workloads")
+    dev = torch.cuda.get_device_properties(0)
+    log(f"device: {dev.name} CUs={dev.multi_processor_count}")
+
+    wl = args.workload
+    if wl == "copy":
+        r = bench_copy(torch, args.steps, args.warmup)
+        log(json.dumps(r))
+        return 0
+    secondary = {}
+    gemv = None
+    if wl in ("all", "gemv"):
+        gemv = bench_gemv(torch, ortmi, args.steps, args.warmup)
+        log(f"gemv: {gemv['gbs']:.1f} GB/s ({gemv['gpu_ms'] * 1e3:.2f} us/call)")
+    if wl in ("all", "gemm"):
+        r = bench_gemm(torch, ortmi, args.steps, args.warmup)
+        secondary["mnb_gemm_prefill"] = {
+            "config": "M=512 K=4096 N=4096 bits=4 block=32 fp16, zero points U{0..15}",
+            "tflops": round(r["tflops"], 2), "us_per_call": round(r["gpu_ms"] * 1e3, 2),
+            "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2),
+                         "peak": FP16_DENSE_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(r["mfma_frac"], 4)}}
+        log(f"gemm: {r['tflops']:.1f} TFLOP/s ({r['gpu_ms'] * 1e3:.2f} us/call)")
+    if wl in ("all", "gqa"):
+        r = bench_gqa(torch, ortmi, args.steps, args.warmup)
+        secondary["gqa_decode"] = {
+            "config": "B=8 H=32 KV=8 hd=128 past=4096 fp16 rotary, growing contract",
+            "gbs": round(r["gbs"], 1), "us_per_call": round(r["gpu_ms"] * 1e3, 2),
+            "bytes_per_call": r["bytes_per_call"],
+            "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}}
+        log(f"gqa: {r['gbs']:.1f} GB/s ({r['gpu_ms'] * 1e3:.2f} us/call)")
+    if wl in ("all", "paged"):
+        r = bench_paged(torch, ortmi, args.steps, args.warmup)
+        secondary["paged_attention_mixed"] = {
+            "config": "32 seqs ctx U[256,8192], 4 prefill x 256 + 28 decode, block 16, "
+                      "H=32 KV=8 hd=128 fp16",
+            "gbs": round(r["gbs"], 1), "tflops": round(r["tflops"], 2),
+            "us_per_call": round(r["gpu_ms"] * 1e3, 2),
+            "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}}
+        log(f"paged: {r['gbs']:.1f} GB/s {r['tflops']:.1f} TFLOP/s ({r['gpu_ms'] * 1e3:.1f} us)")
+
+    if gemv is None:
+        print(json.dumps({"workload": wl, "secondary": secondary}))
+        return 0
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_gemv(gemv["inputs"])
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": round(gemv["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": gemv["launches"],
+        "warmup": args.warmup,
+        "ms_per_step": round(gemv["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "MatMulNBits decode GEMV: M=1 K=4096 N=11008 bits=4 block=32, fp32 "
+                        "activations/scales, zero points all 8",
+            "weights_rotated_over_bytes": gemv["bytes_per_call"] * gemv["copies"],
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gemv["gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gemv["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": gemv["kernel"],
+            "us_per_launch": round(gemv["gpu_ms"] * 1e3, 3),
+            "bytes_per_launch": gemv["bytes_per_call"],
+        },
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
