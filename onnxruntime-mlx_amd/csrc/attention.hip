@@ -126,167 +126,249 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(const uint4* __restrict__ 
 
 // ---------------------------------------------------------- GQA decode --
 
+// Rotate the 8 dims [dl, dl+8) held by this lane (head vector spread over LPR
+// lanes, 8 dims each). Non-interleaved pairs (i, i+half) live `half/8` lanes apart
+// and are exchanged with a shuffle; interleaved pairs sit inside the lane.
+template <typename T, int LPR>
+__device__ __forceinline__ void rope_lane8(float (&x)[8], int dl, const T* __restrict__ c,
+                                           const T* __restrict__ s, int half, int interleaved) {
+    if (interleaved) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            const int p = (dl + i) / 2;
+            if (dl + i + 1 < 2 * half) {
+                const float cs = to_f32(c[p]), sn = to_f32(s[p]);
+                const float a = x[i], b = x[i + 1];
+                x[i] = a * cs - b * sn;
+                x[i + 1] = b * cs + a * sn;
+            }
+        }
+        return;
+    }
+    const int off = half / 8;  // lane distance between partners
+    const int lane = threadIdx.x & 63;
+    float partner[8];
+    const bool lowhalf = dl < half;
+    const int src = lowhalf ? lane + off : lane - off;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) partner[i] = __shfl(x[i], src, 64);
+    if (dl < 2 * half) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int p = lowhalf ? dl + i : dl + i - half;
+            const float cs = to_f32(c[p]), sn = to_f32(s[p]);
+            x[i] = lowhalf ? x[i] * cs - partner[i] * sn : x[i] * cs + partner[i] * sn;
+        }
+    }
+}
+
 // Partial state layout (floats): [row][split][vhd + 2] with o (unnormalised),
 // then m (running max) and l (sum of exp).
+//
+// One workgroup per (batch, kv head, key split). RoPE of the G query heads (and,
+// in the split holding key vp, of the new key) is applied in registers; the new
+// K/V row is written to `present` and then read back like every other row. Each
+// lane group of LPR lanes walks rows with an online softmax over blocks of U
+// rows; K and V of a block are loaded together. In the growing contract rows
+// below vp are copied from past to present out of the registers already loaded.
 template <typename T, int HD, int G>
 __global__ __launch_bounds__(256) void gqa_decode_kernel(
-    const T* __restrict__ qrot, const T* __restrict__ kread, const T* __restrict__ vread,
-    T* __restrict__ kwrite, T* __restrict__ vwrite, int64_t read_cap, int64_t write_cap,
-    int copy_rows, int nkeys, int chunk, int nsplit, int KV, float scale,
-    float* __restrict__ part) {
-    constexpr int LPR = HD / 8;          // lanes per K/V row (16 bytes each)
+    const T* __restrict__ q, const T* __restrict__ knew, const T* __restrict__ vnew,
+    int64_t q_stride, int64_t kv_stride, const T* __restrict__ cos_c, const T* __restrict__ sin_c,
+    int half, int interleaved, const T* __restrict__ kpast, const T* __restrict__ vpast,
+    T* __restrict__ kpres, T* __restrict__ vpres, int64_t past_cap, int64_t pres_cap,
+    int copy_past, int vp, int chunk, int nsplit, int KV, float scale, float* __restrict__ part,
+    T* __restrict__ out) {
+    constexpr int LPR = HD / 8;          // lanes per row (16 bytes each)
     constexpr int RPW = 64 / LPR;        // rows per wave per step
     constexpr int RPS = 4 * RPW;         // rows per workgroup step
-    __shared__ float s_p[G][1024];
-    __shared__ float s_red[4][G][HD];
-    __shared__ float s_ml[G][2];
+    constexpr int U = 4;                 // steps per online-softmax block
+    __shared__ float s_o[4][G][HD];
+    __shared__ float s_m[4][RPW][G], s_l[4][RPW][G];
 
     const int bk = blockIdx.x;  // b*KV + kvh
     const int split = blockIdx.y;
     const int b = bk / KV, kvh = bk % KV;
+    const int H = KV * G;
+    const int nkeys = vp + 1;
     const int j0 = split * chunk;
     const int j1 = min(nkeys, j0 + chunk);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int sub = lane / LPR;      // row within the wave step
-    const int dl = (lane % LPR) * 8; // first dim of this lane
+    const int sub = lane / LPR;
+    const int dl = (lane % LPR) * 8;
+    const T* cr = cos_c ? cos_c + (int64_t)vp * half : nullptr;
+    const T* sr = sin_c ? sin_c + (int64_t)vp * half : nullptr;
 
-    // Query fragment for the G heads of this kv group.
+    // Query fragments (rotated, rounded to T as the reference materialises them).
     float qf[G][8];
-    const int H = KV * G;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const T* qp = qrot + ((int64_t)b * H + kvh * G + g) * HD + dl;
+        const T* qp = q + (int64_t)b * q_stride + (int64_t)(kvh * G + g) * HD + dl;
+        const uint4 raw = *reinterpret_cast<const uint4*>(qp);
+        const T* rv = reinterpret_cast<const T*>(&raw);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qf[g][i] = to_f32(qp[i]) * scale;
+        for (int i = 0; i < 8; ++i) qf[g][i] = to_f32(rv[i]);
+        if (cr) rope_lane8<T, LPR>(qf[g], dl, cr, sr, half, interleaved);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[g][i] = round_to<T>(qf[g][i]) * scale;
     }
-
-    const T* kbase = kread + (int64_t)bk * read_cap * HD;
-    const T* vbase = vread + (int64_t)bk * read_cap * HD;
-    T* kw = kwrite ? kwrite + (int64_t)bk * write_cap * HD : nullptr;
-    T* vw = vwrite ? vwrite + (int64_t)bk * write_cap * HD : nullptr;
-
-    // Scores: rows j0 + step*RPS + wave*RPW + sub, U steps of loads in flight.
-    // Rows at or beyond copy_rows (the new rows of the growing contract) are read
-    // from `present`, the rest from the read buffer.
-    constexpr int U = 4;
-    for (int base = j0; base < j1; base += RPS * U) {
-        uint4 kv4[U];
+    T* kw = kpres + (int64_t)bk * pres_cap * HD;
+    T* vw = vpres + (int64_t)bk * pres_cap * HD;
+    // The split holding key vp writes the new row (rotated K, raw V) to present.
+    if (vp >= j0 && vp < j1) {
+        if (wave == 0) {
+            const T* kp = knew + (int64_t)b * kv_stride + (int64_t)kvh * HD + dl;
+            const uint4 raw = *reinterpret_cast<const uint4*>(kp);
+            const T* rv = reinterpret_cast<const T*>(&raw);
+            float kx[8];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int j = base + u * RPS + wave * RPW + sub;
-            kv4[u] = make_uint4(0, 0, 0, 0);
-            if (j < j1) {
-                const T* src = (kw && j >= copy_rows) ? kw + (int64_t)j * HD + dl
-                                                      : kbase + (int64_t)j * HD + dl;
-                kv4[u] = *reinterpret_cast<const uint4*>(src);
+            for (int i = 0; i < 8; ++i) kx[i] = to_f32(rv[i]);
+            if (cr) rope_lane8<T, LPR>(kx, dl, cr, sr, half, interleaved);
+            T outk[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) outk[i] = from_f32<T>(kx[i]);
+            if (sub == 0) {
+                *reinterpret_cast<uint4*>(kw + (int64_t)vp * HD + dl) =
+                    *reinterpret_cast<uint4*>(outk);
+                *reinterpret_cast<uint4*>(vw + (int64_t)vp * HD + dl) = *reinterpret_cast<const uint4*>(
+                    vnew + (int64_t)b * kv_stride + (int64_t)kvh * HD + dl);
             }
         }
+        __syncthreads();
+    }
+    const T* kbase = (copy_past ? kpast + (int64_t)bk * past_cap * HD : kw);
+    const T* vbase = (copy_past ? vpast + (int64_t)bk * past_cap * HD : vw);
+
+    float m[G], l[G], o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
+    }
+    for (int base = j0; base < j1; base += RPS * U) {
+        uint4 kr[U], vr[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = base + u * RPS + wave * RPW + sub;
-            if (kw && j < copy_rows && j < j1)
-                *reinterpret_cast<uint4*>(kw + (int64_t)j * HD + dl) = kv4[u];
-            const T* kvals = reinterpret_cast<const T*>(&kv4[u]);
+            kr[u] = make_uint4(0, 0, 0, 0);
+            vr[u] = make_uint4(0, 0, 0, 0);
+            if (j < j1) {
+                const bool fresh = j >= vp;  // the new row lives in present
+                const T* ks = (fresh ? kw : kbase) + (int64_t)j * HD + dl;
+                const T* vs = (fresh ? vw : vbase) + (int64_t)j * HD + dl;
+                kr[u] = *reinterpret_cast<const uint4*>(ks);
+                vr[u] = *reinterpret_cast<const uint4*>(vs);
+            }
+        }
+        float sc[U][G];
+        float bmax[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) bmax[g] = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = base + u * RPS + wave * RPW + sub;
+            if (copy_past && j < vp && j < j1) {
+                *reinterpret_cast<uint4*>(kw + (int64_t)j * HD + dl) = kr[u];
+                *reinterpret_cast<uint4*>(vw + (int64_t)j * HD + dl) = vr[u];
+            }
+            const T* kv = reinterpret_cast<const T*>(&kr[u]);
             float kf[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) kf[i] = to_f32(kvals[i]);
+            for (int i = 0; i < 8; ++i) kf[i] = to_f32(kv[i]);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float d = 0.f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
                 d = group_sum<LPR>(d);
-                if (j < j1 && (lane % LPR) == 0) s_p[g][j - j0] = d;
-            }
-        }
-    }
-    __syncthreads();
-    // Softmax statistics per head (one wave per head, G <= 4 handled by looping).
-    const int n = j1 - j0;
-    for (int g = wave; g < G; g += 4) {
-        float m = -INFINITY;
-        for (int i = lane; i < n; i += 64) m = fmaxf(m, s_p[g][i]);
-        m = wave_max(m);
-        float l = 0.f;
-        for (int i = lane; i < n; i += 64) {
-            const float e = __expf(s_p[g][i] - m);
-            s_p[g][i] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (lane == 0) {
-            s_ml[g][0] = m;
-            s_ml[g][1] = l;
-        }
-    }
-    __syncthreads();
-    // P.V
-    float o[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
-    for (int base = j0; base < j1; base += RPS * U) {
-        uint4 vv4[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int j = base + u * RPS + wave * RPW + sub;
-            vv4[u] = make_uint4(0, 0, 0, 0);
-            if (j < j1) {
-                const T* src = (vw && j >= copy_rows) ? vw + (int64_t)j * HD + dl
-                                                      : vbase + (int64_t)j * HD + dl;
-                vv4[u] = *reinterpret_cast<const uint4*>(src);
+                sc[u][g] = j < j1 ? d : -INFINITY;
+                bmax[g] = fmaxf(bmax[g], sc[u][g]);
             }
         }
 #pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mn = fmaxf(m[g], bmax[g]);
+            if (mn == -INFINITY) continue;
+            const float alpha = __expf(m[g] - mn);  // m = -inf gives 0
+            l[g] *= alpha;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[g][i] *= alpha;
+            m[g] = mn;
+        }
+#pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int j = base + u * RPS + wave * RPW + sub;
-            if (j >= j1) continue;
-            if (vw && j < copy_rows) *reinterpret_cast<uint4*>(vw + (int64_t)j * HD + dl) = vv4[u];
-            const T* vvals = reinterpret_cast<const T*>(&vv4[u]);
+            const T* vv = reinterpret_cast<const T*>(&vr[u]);
             float vf[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) vf[i] = to_f32(vvals[i]);
+            for (int i = 0; i < 8; ++i) vf[i] = to_f32(vv[i]);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float p = s_p[g][j - j0];
+                const float p = sc[u][g] == -INFINITY ? 0.f : __expf(sc[u][g] - m[g]);
+                l[g] += p;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i]);
             }
         }
     }
-    // Reduce the RPW rows of a wave (lanes with equal lane % LPR), then the 4 waves.
+    // Merge the RPW lane groups of each wave and the 4 waves through LDS.
+    if ((lane % LPR) == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g) {
+            s_m[wave][sub][g] = m[g];
+            s_l[wave][sub][g] = l[g];
+        }
+    }
+    __syncthreads();
+    float M[G], L[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float mm = -INFINITY;
+        for (int w = 0; w < 4; ++w)
+            for (int r = 0; r < RPW; ++r) mm = fmaxf(mm, s_m[w][r][g]);
+        float ll = 0.f;
+        for (int w = 0; w < 4; ++w)
+            for (int r = 0; r < RPW; ++r)
+                if (s_m[w][r][g] != -INFINITY) ll += s_l[w][r][g] * __expf(s_m[w][r][g] - mm);
+        M[g] = mm;
+        L[g] = ll;
+        const float f = m[g] == -INFINITY ? 0.f : __expf(m[g] - mm);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            float x = o[g][i];
+            float x = o[g][i] * f;
 #pragma unroll
             for (int off = LPR; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
             o[g][i] = x;
         }
+    }
     if (sub == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s_red[wave][g][dl + i] = o[g][i];
+            for (int i = 0; i < 8; ++i) s_o[wave][g][dl + i] = o[g][i];
     }
     __syncthreads();
     for (int idx = tid; idx < G * HD; idx += 256) {
         const int g = idx / HD, d = idx % HD;
-        const float acc = s_red[0][g][d] + s_red[1][g][d] + s_red[2][g][d] + s_red[3][g][d];
+        const float acc = s_o[0][g][d] + s_o[1][g][d] + s_o[2][g][d] + s_o[3][g][d];
         const int64_t row = (int64_t)b * H + kvh * G + g;
+        if (nsplit == 1) {
+            out[row * HD + d] = from_f32<T>(L[g] > 0.f ? acc / L[g] : 0.f);
+            continue;
+        }
         float* dst = part + (row * nsplit + split) * (HD + 2);
         dst[d] = acc;
         if (d == 0) {
-            dst[HD] = s_ml[g][0];
-            dst[HD + 1] = s_ml[g][1];
+            dst[HD] = M[g];
+            dst[HD + 1] = L[g];
         }
     }
 }
 
 // Merge split partials: out[row][d] = sum_i o_i e^{m_i-M} / sum_i l_i e^{m_i-M}.
-// Output row r goes to out + (r / H) * out_tok_stride + (r % H) * vhd.
+// One workgroup per row: split weights are computed once into LDS, then each
+// thread sums its output dims over the splits with independent loads.
 template <typename T>
 __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict__ part,
                                                          T* __restrict__ out, int nsplit,
@@ -294,29 +376,40 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict
                                                          int vhd, int H,
                                                          int64_t out_tok_stride,
                                                          const int* __restrict__ row_map) {
+    __shared__ float s_w[1024];
+    __shared__ float s_red[2];
     const int r = blockIdx.x;
     int orow = r;
     if (row_map) {
         orow = row_map[r];
         if (orow < 0) return;
     }
-    const int ns = nsplit_row ? nsplit_row[r] : nsplit;
+    const int ns = min(1024, nsplit_row ? nsplit_row[r] : nsplit);
     const float* p = part + (int64_t)r * nsplit * (vhd + 2);
-    float M = -INFINITY;
-    for (int i = 0; i < ns; ++i) M = fmaxf(M, p[i * (vhd + 2) + vhd]);
-    float L = 0.f;
-    for (int i = 0; i < ns; ++i) {
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < ns; i += blockDim.x) mx = fmaxf(mx, p[i * (vhd + 2) + vhd]);
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    const float M = fmaxf(s_red[0], s_red[1]);
+    __syncthreads();
+    float lsum = 0.f;
+    for (int i = threadIdx.x; i < ns; i += blockDim.x) {
         const float m = p[i * (vhd + 2) + vhd];
-        if (m != -INFINITY) L += p[i * (vhd + 2) + vhd + 1] * __expf(m - M);
+        const float w = m == -INFINITY ? 0.f : __expf(m - M);
+        s_w[i] = w;
+        lsum += w * p[i * (vhd + 2) + vhd + 1];
     }
+    lsum = wave_sum(lsum);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = lsum;
+    __syncthreads();
+    const float L = s_red[0] + s_red[1];
     const float inv = L > 0.f ? 1.0f / L : 0.f;
     T* o = out + (int64_t)(orow / H) * out_tok_stride + (int64_t)(orow % H) * vhd;
     for (int d = threadIdx.x; d < vhd; d += blockDim.x) {
         float acc = 0.f;
-        for (int i = 0; i < ns; ++i) {
-            const float m = p[i * (vhd + 2) + vhd];
-            if (m != -INFINITY) acc += p[i * (vhd + 2) + d] * __expf(m - M);
-        }
+#pragma unroll 8
+        for (int i = 0; i < ns; ++i) acc = fmaf(p[i * (vhd + 2) + d], s_w[i], acc);
         o[d] = from_f32<T>(acc * inv);
     }
 }
@@ -784,6 +877,9 @@ static int gqa_nsplit(int64_t BKV, int64_t nkeys, int& chunk) {
     c = ((c + 63) / 64) * 64;
     if (c < 64) c = 64;
     if (c > 1024) c = 1024;
+    // The merge kernel weighs at most 1024 splits.
+    const int64_t cmin = ((nkeys + 1023) / 1024 + 63) / 64 * 64;
+    if (c < cmin) c = cmin;
     chunk = (int)c;
     return (int)((nkeys + c - 1) / c);
 }
@@ -839,66 +935,59 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
     float* part = reinterpret_cast<float*>(static_cast<char*>(ws) +
                                            align_up((size_t)B * S * H * hd * 4));
 
-    // Past rows that must reach `present` when it is a different buffer.
+    const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool decode_fast = S == 1 && (G == 1 || G == 2 || G == 4 || G == 8) &&
+                             (!cos_c || interleaved || half % 8 == 0) && a16(q) && a16(k) &&
+                             a16(v) && a16(pk) && a16(pv) && (cap == 0 || (a16(past_key) &&
+                             a16(past_value)));
+    // Past rows that must reach `present` when it is a different buffer: the fused
+    // decode kernel copies them itself in the growing contract; otherwise a copy
+    // kernel runs first (shared contract into a separate present copies all cap
+    // rows; growing prefill copies the cap past rows).
     const bool aliased = (pk == past_key) && (pv == past_value);
-    const bool fuse_copy = !shared && !aliased && S == 1;
-    if (!aliased && !fuse_copy) {
-        // Shared contract into a separate present buffer copies every cap row;
-        // growing prefill copies the cap past rows.
-        const int64_t rows = cap;
-        if (rows > 0) {
-            const int vec_per_row = hd * (int)sizeof(T) / 16;
-            const int64_t total_vec = (int64_t)B * KV * rows * vec_per_row;
-            int grid = (int)std::min<int64_t>((total_vec + 255) / 256, 65536);
-            hipLaunchKernelGGL(kv_copy_kernel, dim3(grid), dim3(256), 0, st,
-                               static_cast<const uint4*>(past_key), static_cast<uint4*>(pk), cap,
-                               pcap, rows, vec_per_row, total_vec);
-            hipLaunchKernelGGL(kv_copy_kernel, dim3(grid), dim3(256), 0, st,
-                               static_cast<const uint4*>(past_value), static_cast<uint4*>(pv),
-                               cap, pcap, rows, vec_per_row, total_vec);
-            if (int rc = check_launch("gqa kv copy")) return rc;
-        }
+    const bool fused_copy = decode_fast && !shared && !aliased;
+    if (!aliased && !fused_copy && cap > 0) {
+        const int vec_per_row = hd * (int)sizeof(T) / 16;
+        const int64_t total_vec = (int64_t)B * KV * cap * vec_per_row;
+        int grid = (int)std::min<int64_t>((total_vec + 255) / 256, 65536);
+        hipLaunchKernelGGL(kv_copy_kernel, dim3(grid), dim3(256), 0, st,
+                           static_cast<const uint4*>(past_key), static_cast<uint4*>(pk), cap,
+                           pcap, cap, vec_per_row, total_vec);
+        hipLaunchKernelGGL(kv_copy_kernel, dim3(grid), dim3(256), 0, st,
+                           static_cast<const uint4*>(past_value), static_cast<uint4*>(pv), cap,
+                           pcap, cap, vec_per_row, total_vec);
+        if (int rc = check_launch("gqa kv copy")) return rc;
     }
-    hipLaunchKernelGGL((gqa_prep_kernel<T>), dim3(B * S, H + KV), dim3(64), hd * sizeof(float), st,
-                       q, k, v, static_cast<const T*>(cos_c), static_cast<const T*>(sin_c), half,
-                       interleaved, qrot, static_cast<T*>(pk), static_cast<T*>(pv), B, S, H, KV,
-                       hd, pcap, vp, q_stride, kv_stride);
-    if (int rc = check_launch("gqa_prep")) return rc;
-
-    if (S == 1 && (G == 1 || G == 2 || G == 4 || G == 8)) {
+    if (decode_fast) {
         int chunk = 0;
         const int ns = gqa_nsplit((int64_t)B * KV, nkeys, chunk);
-        // Keys [0, vp) are read from past (fused copy) or present; key vp from present.
-        const T* kread = static_cast<const T*>(fuse_copy ? past_key : pk);
-        const T* vread = static_cast<const T*>(fuse_copy ? past_value : pv);
-        const int64_t read_cap = fuse_copy ? cap : pcap;
-        // In the fused-copy (growing) contract the new row lives in present only:
-        // the kernel reads rows < vp from past and row vp from present. Handle that
-        // by reading from past for rows < vp and present for the last row.
         dim3 grid(B * KV, ns);
         auto launch = [&](auto gtag) {
             constexpr int GG = decltype(gtag)::value;
-            if (fuse_copy) {
-                // Rows [0, vp): read past, write present. Row vp: attended from present.
-                hipLaunchKernelGGL((gqa_decode_kernel<T, HD, GG>), grid, dim3(256), 0, st, qrot,
-                                   kread, vread, static_cast<T*>(pk), static_cast<T*>(pv),
-                                   read_cap, pcap, vp, nkeys, chunk, ns, KV, sc, part);
-            } else {
-                hipLaunchKernelGGL((gqa_decode_kernel<T, HD, GG>), grid, dim3(256), 0, st, qrot,
-                                   kread, vread, (T*)nullptr, (T*)nullptr, read_cap, pcap, 0,
-                                   nkeys, chunk, ns, KV, sc, part);
-            }
+            hipLaunchKernelGGL((gqa_decode_kernel<T, HD, GG>), grid, dim3(256), 0, st, q, k, v,
+                               q_stride, kv_stride, static_cast<const T*>(cos_c),
+                               static_cast<const T*>(sin_c), half, interleaved,
+                               static_cast<const T*>(past_key), static_cast<const T*>(past_value),
+                               static_cast<T*>(pk), static_cast<T*>(pv), cap, pcap,
+                               fused_copy ? 1 : 0, vp, chunk, ns, KV, sc, part,
+                               static_cast<T*>(output));
         };
         if (G == 1) launch(std::integral_constant<int, 1>());
         if (G == 2) launch(std::integral_constant<int, 2>());
         if (G == 4) launch(std::integral_constant<int, 4>());
         if (G == 8) launch(std::integral_constant<int, 8>());
         if (int rc = check_launch("gqa_decode")) return rc;
+        if (ns == 1) return ORTMI_OK;
         hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(B * H), dim3(128), 0, st, part,
                            static_cast<T*>(output), ns, (const int*)nullptr, hd, H,
                            (int64_t)H * hd, (const int*)nullptr);
         return check_launch("gqa_merge");
     }
+    hipLaunchKernelGGL((gqa_prep_kernel<T>), dim3(B * S, H + KV), dim3(64), hd * sizeof(float), st,
+                       q, k, v, static_cast<const T*>(cos_c), static_cast<const T*>(sin_c), half,
+                       interleaved, qrot, static_cast<T*>(pk), static_cast<T*>(pv), B, S, H, KV,
+                       hd, pcap, vp, q_stride, kv_stride);
+    if (int rc = check_launch("gqa_prep")) return rc;
     const int QT = std::max(1, kTileRows / G);
     const int tiles = (S + QT - 1) / QT;
     DenseKV dk{pk, pv, pcap, KV};

@@ -48,6 +48,55 @@ __device__ __forceinline__ float dot32_codes(const float* a, uint4 w) {
     return d0 + d1;
 }
 
+// Activations live in LDS as fp32 in 16-byte units; unit i of 32-float chunk c
+// is stored at unit 8c + (i ^ (c & 7)), so the 8 lanes of one LDS read phase
+// (consecutive c, equal i) hit 8 different bank groups.
+__device__ __forceinline__ int swz_unit(int q) { return (q & ~7) | ((q & 7) ^ ((q >> 3) & 7)); }
+
+// Stage A[0, K) (zero-padded to Kp) into swizzled fp32 LDS: every thread issues
+// all of its 16-byte loads before its first LDS store.
+template <typename T>
+__device__ __forceinline__ void stage_activations(const T* __restrict__ A, float4* sA, int K,
+                                                  int Kp) {
+    constexpr int EPL = 16 / sizeof(T);  // elements per 16-byte load
+    constexpr int U = 4;
+    const int nvec = Kp / EPL;
+    const bool vec_ok = (K % EPL) == 0 && (reinterpret_cast<uintptr_t>(A) % 16) == 0;
+    for (int base = threadIdx.x; base < nvec; base += 256 * U) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int vi = base + u * 256;
+            const int k0 = vi * EPL;
+            if (vi < nvec && vec_ok && k0 + EPL <= K) {
+                v[u] = *reinterpret_cast<const uint4*>(A + k0);
+            } else {
+                T t[EPL];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e)
+                    t[e] = (vi < nvec && k0 + e < K) ? A[k0 + e] : from_f32<T>(0.f);
+                v[u] = *reinterpret_cast<const uint4*>(t);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int vi = base + u * 256;
+            if (vi >= nvec) continue;
+            const T* t = reinterpret_cast<const T*>(&v[u]);
+#pragma unroll
+            for (int e = 0; e < EPL; e += 4) {
+                const int q = (vi * EPL + e) / 4;  // fp32 16-byte unit
+                sA[swz_unit(q)] = make_float4(to_f32(t[e]), to_f32(t[e + 1]), to_f32(t[e + 2]),
+                                              to_f32(t[e + 3]));
+            }
+        }
+    }
+}
+
+// One wave per R consecutive rows of B (a strided loop covers N beyond
+// grid*4*R). Lane l owns the 32-code chunks c = l + 64j (j < BPL) of every row and
+// keeps their activations in VGPRs. All R*BPL 16-byte weight loads of a row group
+// are in flight before the activations are staged.
 template <typename T, int BS, int BPL, int R>
 __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ B,
@@ -55,19 +104,17 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ Z,
                                                         T* __restrict__ Y, int N, int K,
                                                         int nb) {
-    extern __shared__ float sA[];
+    extern __shared__ float4 sA[];
     const int Kp = nb * BS;
     const int C = Kp / 32;  // 32-code chunks per row
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int waves_total = gridDim.x * 4;
-    const int gw = blockIdx.x * 4 + wave;
+    const int stride = gridDim.x * 4 * R;
     const size_t row_bytes = (size_t)Kp / 2;
     const int zp_cols = (nb + 1) / 2;
 
-    // Issue the first row group's weight loads before staging A so the HBM
-    // latency overlaps the activation staging.
     uint4 w[R][BPL];
+    float sc[R][BPL], zc[R][BPL];
     auto load_group = [&](int n0) {
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -78,15 +125,20 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                     const u32x4_t v = __builtin_nontemporal_load(
                         reinterpret_cast<const u32x4_t*>(B + (size_t)n * row_bytes) + c);
                     w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
+                    const int blk = (32 * c) / BS;
+                    sc[r][j] = to_f32(S[(size_t)n * nb + blk]);
+                    zc[r][j] = Z ? (float)nibble(Z[(size_t)n * zp_cols + blk / 2], blk & 1) : 8.f;
                 } else {
                     w[r][j] = make_uint4(0, 0, 0, 0);
+                    sc[r][j] = 0.f;
+                    zc[r][j] = 0.f;
                 }
             }
     };
-    int n0 = gw * R;
+    int n0 = (blockIdx.x * 4 + wave) * R;
     if (n0 < N) load_group(n0);
 
-    for (int k = threadIdx.x; k < Kp; k += 256) sA[k] = k < K ? to_f32(A[k]) : 0.f;
+    stage_activations<T>(A, sA, K, Kp);
     __syncthreads();
 
     float a[BPL][32];
@@ -96,35 +148,30 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
         const int c = lane + 64 * j;
         float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            a[j][i] = c < C ? sA[32 * c + i] : 0.f;
-            s += a[j][i];
+        for (int i = 0; i < 8; ++i) {
+            const float4 v = c < C ? sA[swz_unit(8 * c + i)] : make_float4(0.f, 0.f, 0.f, 0.f);
+            a[j][4 * i + 0] = v.x;
+            a[j][4 * i + 1] = v.y;
+            a[j][4 * i + 2] = v.z;
+            a[j][4 * i + 3] = v.w;
+            s += (v.x + v.y) + (v.z + v.w);
         }
         asum[j] = s;
     }
 
-    for (; n0 < N; n0 += waves_total * R) {
+    for (; n0 < N; n0 += stride) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int n = n0 + r;
             float total = 0.f;
 #pragma unroll
             for (int j = 0; j < BPL; ++j) {
-                const int c = lane + 64 * j;
-                if (n < N && c < C) {
-                    const int blk = (32 * c) / BS;
-                    const float s = to_f32(S[(size_t)n * nb + blk]);
-                    const float z = Z ? (float)nibble(Z[(size_t)n * zp_cols + blk / 2], blk & 1)
-                                      : 8.f;
-                    const float d = dot32_codes(a[j], w[r][j]);
-                    total = fmaf(s, d - z * asum[j], total);
-                }
+                const float d = dot32_codes(a[j], w[r][j]);
+                total = fmaf(sc[r][j], d - zc[r][j] * asum[j], total);
             }
             acc[r] = total;
         }
-        const int next = n0 + waves_total * R;
-        if (next < N) load_group(next);
+        if (n0 + stride < N) load_group(n0 + stride);
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
         if (lane < R) {
@@ -137,18 +184,48 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     }
 }
 
-template <typename T, int BS, int BPL>
-static int launch_gemv4_bpl(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
-                            int N, int K, int nb, hipStream_t st) {
-    constexpr int R = BPL == 1 ? 8 : (BPL == 2 ? 4 : 2);
+template <typename T, int BS, int BPL, int R>
+static int launch_gemv4_r(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y, int N,
+                          int K, int nb, int grid, hipStream_t st) {
     const int Kp = nb * BS;
-    const int groups = (N + R - 1) / R;
-    int grid = (groups + 3) / 4;
-    const int cap = device_cu_count() * 4;
-    if (grid > cap) grid = cap;
     hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, BPL, R>), dim3(grid), dim3(256),
                        (size_t)Kp * sizeof(float), st, A, B, S, Z, Y, N, K, nb);
     return check_launch("mnb_gemv4");
+}
+
+// Rows per wave: aim for about two workgroups of 4 waves per CU, each wave
+// owning R consecutive rows (R from a small set; large N loops).
+template <typename T, int BS, int BPL>
+static int launch_gemv4_bpl(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
+                            int N, int K, int nb, hipStream_t st) {
+    const int target_waves = device_cu_count() * 8;
+    const int want = (N + target_waves - 1) / target_waves;
+    constexpr int RMAX = BPL <= 2 ? 8 : (BPL <= 4 ? 2 : 1);
+    int R = want <= 1 ? 1 : want <= 2 ? 2 : want <= 4 ? 4 : want <= 6 ? 6 : 8;
+    if (R > RMAX) R = RMAX;
+    const long groups = ((long)N + R - 1) / R;
+    long grid = (groups + 3) / 4;
+    if (grid > 2L * device_cu_count()) grid = 2L * device_cu_count();
+    switch (R) {
+        case 1: return launch_gemv4_r<T, BS, BPL, 1>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
+        case 2:
+            if constexpr (RMAX >= 2)
+                return launch_gemv4_r<T, BS, BPL, 2>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
+            break;
+        case 4:
+            if constexpr (RMAX >= 4)
+                return launch_gemv4_r<T, BS, BPL, 4>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
+            break;
+        case 6:
+            if constexpr (RMAX >= 6)
+                return launch_gemv4_r<T, BS, BPL, 6>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
+            break;
+        default:
+            if constexpr (RMAX >= 8)
+                return launch_gemv4_r<T, BS, BPL, 8>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
+            break;
+    }
+    return -1;
 }
 
 template <typename T, int BS>
@@ -163,17 +240,49 @@ static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t*
         case 4: return launch_gemv4_bpl<T, BS, 4>(A, B, S, Z, Y, N, K, nb, st);
         case 5: return launch_gemv4_bpl<T, BS, 5>(A, B, S, Z, Y, N, K, nb, st);
         case 6: return launch_gemv4_bpl<T, BS, 6>(A, B, S, Z, Y, N, K, nb, st);
-        case 7: return launch_gemv4_bpl<T, BS, 7>(A, B, S, Z, Y, N, K, nb, st);
-        case 8: return launch_gemv4_bpl<T, BS, 8>(A, B, S, Z, Y, N, K, nb, st);
-        default: return -1;  // caller falls back
+        default: return -1;  // K > 12288: the caller falls back
     }
 }
 
 // ------------------------------------------------------------- GEMM (MFMA) --
 
-// LDS rows are 32 halfs of data padded to 40 (80 bytes): 8 consecutive lanes
-// reading 16 bytes at row stride 80 hit 8 disjoint 16-byte bank groups.
-constexpr int kLdsRow = 40;
+// k-steps of 64 codes. LDS rows hold 64 halfs padded to 72 (144 bytes): 16-byte
+// reads of 8 consecutive rows fall in 8 different bank groups (144/16 = 9 = 1 mod 8).
+constexpr int kBK = 64;
+constexpr int kLdsRow = 72;
+
+// Dequantise one 32-bit word (codes k0..k7 of a chunk) to four fp16 pairs
+// (k0,k4) (k1,k5) (k2,k6) (k3,k7): (w >> 4j) & 0x000F000F | 0x6400 6400 is the
+// pair (1024 + q) exactly; subtracting (1024 + zp) is exact, and the multiply by
+// the scale rounds once, giving fp16((q - zp) * s).
+__device__ __forceinline__ uint4 dequant_word_pairs(uint32_t w, half2_t zoff, half2_t s2) {
+    uint32_t r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t m = ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+        half2_t h = __builtin_bit_cast(half2_t, m);
+        h = (h - zoff) * s2;
+        r[j] = __builtin_bit_cast(uint32_t, h);
+    }
+    return make_uint4(r[0], r[1], r[2], r[3]);
+}
+
+// Reorder 8 activations [a0..a7] to the pair order [a0,a4,a1,a5,a2,a6,a3,a7] used by
+// the dequantised weights (an identical permutation of k on both MFMA operands).
+__device__ __forceinline__ uint4 permute_act8(uint4 v) {
+    return make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u),
+                      __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                      __builtin_amdgcn_perm(v.w, v.y, 0x05040100u),
+                      __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+}
+
+template <int BM, int BN, int BS>
+struct GemmStage {
+    static constexpr int A_VEC = BM * kBK / 8 / 256;  // 16-byte activation vectors per thread
+    uint4 a[A_VEC];
+    uint4 b;        // 32 codes (one 32-code chunk of one weight row)
+    float s, z;     // scale and zero point of that chunk's block
+};
 
 template <int BM, int BN, int BS>
 __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict__ A,
@@ -183,98 +292,78 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
                                                         half_t* __restrict__ Y, int M, int N,
                                                         int K, int nb, int tiles_m,
                                                         int tiles_n) {
-    // Wave layout 2 x 2; each wave owns a (BM/2) x (BN/2) block of 32x32 MFMA tiles.
+    static_assert(BN * 2 == 256, "one 32-code weight chunk per thread per k-step");
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TM = WM / 32, TN = WN / 32;
+    using Stage = GemmStage<BM, BN, BS>;
+    constexpr int A_VEC = Stage::A_VEC;
     __shared__ half_t sA[2][BM * kLdsRow];
     __shared__ half_t sB[2][BN * kLdsRow];
 
-    // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs, so
-    // remap so that each XCD receives a contiguous range of tiles (tiles that
-    // share activation rows then share that XCD's L2).
+    // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; give each
+    // XCD a contiguous range of tiles (m fastest) so tiles sharing weight columns
+    // share that XCD's L2.
     const int nwg = gridDim.x;
-    const int bid = blockIdx.x;
-    int tile = bid;
-    if (nwg % 8 == 0) tile = (bid % 8) * (nwg / 8) + bid / 8;
-    const int tm = tile % tiles_m;
-    const int tn = tile / tiles_m;
+    int tile = blockIdx.x;
+    if (nwg % 8 == 0) tile = (blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8;
+    const int tm = tile % tiles_m, tn = tile / tiles_m;
     const int m0 = tm * BM, n0 = tn * BN;
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave & 1) * WM, wn = (wave >> 1) * WN;
     const int Kp = nb * BS;
-    const int ksteps = Kp / 32;
+    const int ksteps = (Kp + kBK - 1) / kBK;
+    const int chunks = Kp / 32;
     const size_t row_bytes = (size_t)Kp / 2;
     const int zp_cols = (nb + 1) / 2;
+    const bool kvec = (K % 8) == 0;
 
-    // Global->register staging assignments.
-    // A: BM x 32 halfs = BM*64 bytes; 16 bytes per thread per pass.
-    constexpr int A_PASSES = (BM * 4) / 256;
-    // B: BN rows x 16 bytes of codes; two threads per row, 8 bytes each.
-    constexpr int B_PASSES = (BN * 2) / 256;
-    uint4 ra[A_PASSES];
-    uint2 rb[B_PASSES];
-    float rs[B_PASSES], rz[B_PASSES];
-
-    auto gload = [&](int ks) {
-        const int k0 = ks * 32;
+    auto gload = [&](Stage& st, int ks) {
+        const int k0 = ks * kBK;
 #pragma unroll
-        for (int p = 0; p < A_PASSES; ++p) {
+        for (int p = 0; p < A_VEC; ++p) {
             const int idx = tid + p * 256;
-            const int r = idx >> 2, c = (idx & 3) * 8;
+            const int r = idx >> 3, c = (idx & 7) * 8;
             const int m = m0 + r, k = k0 + c;
-            if (m < M && k + 8 <= K) {
-                ra[p] = *reinterpret_cast<const uint4*>(A + (size_t)m * K + k);
-            } else if (m < M && k < K) {
-                half_t t[8];
-                for (int i = 0; i < 8; ++i) t[i] = (k + i < K) ? A[(size_t)m * K + k + i] : (half_t)0;
-                ra[p] = *reinterpret_cast<uint4*>(t);
+            if (m < M && kvec && k + 8 <= K) {
+                st.a[p] = *reinterpret_cast<const uint4*>(A + (size_t)m * K + k);
             } else {
-                ra[p] = make_uint4(0, 0, 0, 0);
+                half_t t[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    t[i] = (m < M && k + i < K) ? A[(size_t)m * K + k + i] : (half_t)0;
+                st.a[p] = *reinterpret_cast<const uint4*>(t);
             }
         }
-#pragma unroll
-        for (int p = 0; p < B_PASSES; ++p) {
-            const int idx = tid + p * 256;
-            const int r = idx >> 1, h = idx & 1;
-            const int n = n0 + r;
-            if (n < N) {
-                rb[p] = *reinterpret_cast<const uint2*>(B + (size_t)n * row_bytes + ks * 16 + h * 8);
-                const int blk = k0 / BS;
-                rs[p] = (float)S[(size_t)n * nb + blk];
-                rz[p] = Z ? (float)nibble(Z[(size_t)n * zp_cols + blk / 2], blk & 1) : 8.f;
-            } else {
-                rb[p] = make_uint2(0, 0);
-                rs[p] = 0.f;
-                rz[p] = 0.f;
-            }
+        const int r = tid >> 1;
+        const int chunk = 2 * ks + (tid & 1);
+        const int n = n0 + r;
+        if (n < N && chunk < chunks) {
+            st.b = *reinterpret_cast<const uint4*>(B + (size_t)n * row_bytes + (size_t)chunk * 16);
+            const int blk = (chunk * 32) / BS;
+            st.s = (float)S[(size_t)n * nb + blk];
+            st.z = Z ? (float)nibble(Z[(size_t)n * zp_cols + blk / 2], blk & 1) : 8.f;
+        } else {
+            st.b = make_uint4(0, 0, 0, 0);
+            st.s = 0.f;
+            st.z = 0.f;
         }
     };
-    auto sstore = [&](int buf) {
+    auto sstore = [&](const Stage& st, int buf) {
 #pragma unroll
-        for (int p = 0; p < A_PASSES; ++p) {
+        for (int p = 0; p < A_VEC; ++p) {
             const int idx = tid + p * 256;
-            const int r = idx >> 2, c = (idx & 3) * 8;
-            *reinterpret_cast<uint4*>(&sA[buf][r * kLdsRow + c]) = ra[p];
+            const int r = idx >> 3, c = (idx & 7) * 8;
+            *reinterpret_cast<uint4*>(&sA[buf][r * kLdsRow + c]) = permute_act8(st.a[p]);
         }
-#pragma unroll
-        for (int p = 0; p < B_PASSES; ++p) {
-            const int idx = tid + p * 256;
-            const int r = idx >> 1, h = idx & 1;
-            const uint32_t wds[2] = {rb[p].x, rb[p].y};
-            half_t out[16];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float q = (float)((wds[i] >> (4 * j)) & 0xfu);
-                    out[i * 8 + j] = (half_t)((q - rz[p]) * rs[p]);
-                }
-            uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 16]);
-            dst[0] = reinterpret_cast<uint4*>(out)[0];
-            dst[1] = reinterpret_cast<uint4*>(out)[1];
-        }
+        const int r = tid >> 1, h = tid & 1;
+        const half2_t zoff = {(half_t)(1024.f + st.z), (half_t)(1024.f + st.z)};
+        const half2_t s2 = {(half_t)st.s, (half_t)st.s};
+        uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32]);
+        dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
+        dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
+        dst[2] = dequant_word_pairs(st.b.z, zoff, s2);
+        dst[3] = dequant_word_pairs(st.b.w, zoff, s2);
     };
 
     float16_t acc[TM][TN];
@@ -285,15 +374,10 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    gload(0);
-    sstore(0);
-    __syncthreads();
     const int lrow = lane & 31, lk = (lane >> 5) * 8;
-    for (int ks = 0; ks < ksteps; ++ks) {
-        const int buf = ks & 1;
-        if (ks + 1 < ksteps) gload(ks + 1);
+    auto compute = [&](int buf) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < kBK / 16; ++kk) {
             half8_t af[TM], bf[TN];
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -310,7 +394,26 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0,
                                                                        0, 0);
         }
-        if (ks + 1 < ksteps) sstore(buf ^ 1);
+    };
+
+    // Pipeline: loads for step s are issued two steps ahead (register sets r0/r1
+    // alternate), stored to the LDS buffer of step s at the end of step s-1.
+    Stage r0, r1;
+    gload(r0, 0);
+    if (ksteps > 1) gload(r1, 1);
+    sstore(r0, 0);
+    __syncthreads();
+    for (int ks = 0; ks < ksteps; ks += 2) {
+        // even step ks: LDS buf 0 holds it; r1 holds step ks+1.
+        if (ks + 2 < ksteps) gload(r0, ks + 2);
+        compute(0);
+        if (ks + 1 < ksteps) sstore(r1, 1);
+        __syncthreads();
+        if (ks + 1 >= ksteps) break;
+        // odd step ks+1: LDS buf 1; r0 holds step ks+2.
+        if (ks + 3 < ksteps) gload(r1, ks + 3);
+        compute(1);
+        if (ks + 2 < ksteps) sstore(r0, 0);
         __syncthreads();
     }
 
@@ -430,7 +533,7 @@ static int run_mnb(const void* A, const uint8_t* B, const void* S, const uint8_t
     T* y = static_cast<T*>(Y);
     const bool aligned = (reinterpret_cast<uintptr_t>(B) % 16) == 0;
     const bool fast_form = bits == 4 && (bs == 32 || bs == 64 || bs == 128) && aligned;
-    if (fast_form && M == 1 && (size_t)nb * bs * sizeof(float) <= 64 * 1024) {
+    if (fast_form && M == 1 && (size_t)nb * bs <= 12288) {
         int rc = -1;
         if (bs == 32) rc = launch_gemv4<T, 32>(a, B, s, Z, y, N, K, nb, st);
         if (bs == 64) rc = launch_gemv4<T, 64>(a, B, s, Z, y, N, K, nb, st);
