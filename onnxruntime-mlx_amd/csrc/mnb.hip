@@ -9,10 +9,11 @@
 // Kernels:
 //  * mnb_gemv4  - decode (M == 1), bits 4, bs in {32, 64, 128}. HBM-bound: each
 //    lane owns fixed 32-code chunks of K and keeps the matching activations in
-//    VGPRs (staged once per workgroup through LDS), then streams rows of B with
-//    128-bit loads (a wave reads 1 KiB contiguous per instruction). Zero points
-//    are folded as s*(sum(a*q) - zp*sum(a)), so the inner loop is one
-//    byte-convert + one FMA per code.
+//    VGPRs as three int8 limbs per value (staged once per workgroup through LDS),
+//    then streams rows of B with 128-bit loads (a wave reads 1 KiB contiguous per
+//    instruction). Codes are dotted with the limbs by v_dot4 (exact integer
+//    sums), so a code costs ~1.4 VALU ops instead of a convert and an FMA. Zero
+//    points are folded as s*(sum(a*q) - zp*sum(a)).
 //  * mnb_gemm4  - prefill (M > 1, fp16), bits 4, bs in {32, 64, 128}. MFMA
 //    v_mfma_f32_32x32x16_f16: the weight tile is dequantised to fp16 in LDS
 //    (fp16((q - zp) * s), one rounding) and the activation tile is staged in LDS;
@@ -25,27 +26,71 @@ namespace ortmi {
 
 // -------------------------------------------------------------- GEMV (M=1) --
 
-// Dot product of 32 activations with the 32 4-bit codes of one 16-byte chunk.
-// Code i of the chunk is nibble (i & 1) of byte i/2, i.e. bits [4i, 4i+4) of the
-// little-endian 128-bit word.
-__device__ __forceinline__ float dot32_codes(const float* a, uint4 w) {
+// One 32-code chunk of activations in integer form: a_i ~= sc * (l0_i + l1_i/254 +
+// l2_i/254^2) with int8 limbs, packed to match the code bytes of a 16-byte weight
+// chunk: word w of the weights holds codes 8w..8w+7; (w & 0x0F0F0F0F) has codes
+// 8w+{0,2,4,6} in its bytes and ((w >> 4) & 0x0F0F0F0F) codes 8w+{1,3,5,7}.
+// The reconstruction error is at most 0.5 * sc / 254^2 ~ 2^-24 * max|a|, the same
+// order as fp32 rounding of the activations, and the integer dots are exact.
+struct ActChunk {
+    int lo[3][4], hi[3][4];  // [limb][word]
+    float sc;                // chunk scale (max|a| / 127)
+    float asum;              // sum of the activations (for the zero-point term)
+};
+
+__device__ __forceinline__ void make_act_chunk(const float (&a)[32], ActChunk& q) {
+    float amax = 0.f, s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        amax = fmaxf(amax, fabsf(a[i]));
+        s += a[i];
+    }
+    q.asum = s;
+    q.sc = amax * (1.0f / 127.0f);
+    const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+    int8_t l[3][32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const float x = a[i] * inv;  // |x| <= 127
+        const float l0 = rintf(x);
+        const float r1 = (x - l0) * 254.0f;  // |r1| <= 127
+        const float l1 = rintf(r1);
+        const float l2 = rintf((r1 - l1) * 254.0f);
+        l[0][i] = (int8_t)l0;
+        l[1][i] = (int8_t)l1;
+        l[2][i] = (int8_t)l2;
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int b = 8 * w;
+            q.lo[j][w] = (int)((uint32_t)(uint8_t)l[j][b + 0] | ((uint32_t)(uint8_t)l[j][b + 2] << 8) |
+                               ((uint32_t)(uint8_t)l[j][b + 4] << 16) |
+                               ((uint32_t)(uint8_t)l[j][b + 6] << 24));
+            q.hi[j][w] = (int)((uint32_t)(uint8_t)l[j][b + 1] | ((uint32_t)(uint8_t)l[j][b + 3] << 8) |
+                               ((uint32_t)(uint8_t)l[j][b + 5] << 16) |
+                               ((uint32_t)(uint8_t)l[j][b + 7] << 24));
+        }
+}
+
+// sum_i a_i * q_i for the 32 codes of one 16-byte weight chunk.
+__device__ __forceinline__ float dot32_act(const ActChunk& a, uint4 w) {
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-    float d0 = 0.f, d1 = 0.f;
+    int d0 = 0, d1 = 0, d2 = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t lo = words[i] & 0x0F0F0F0Fu;         // codes 8i+0,2,4,6
-        const uint32_t hi = (words[i] >> 4) & 0x0F0F0F0Fu;  // codes 8i+1,3,5,7
-        const float* ai = a + 8 * i;
-        d0 = fmaf(ai[0], (float)(lo & 0xffu), d0);
-        d1 = fmaf(ai[1], (float)(hi & 0xffu), d1);
-        d0 = fmaf(ai[2], (float)((lo >> 8) & 0xffu), d0);
-        d1 = fmaf(ai[3], (float)((hi >> 8) & 0xffu), d1);
-        d0 = fmaf(ai[4], (float)((lo >> 16) & 0xffu), d0);
-        d1 = fmaf(ai[5], (float)((hi >> 16) & 0xffu), d1);
-        d0 = fmaf(ai[6], (float)(lo >> 24), d0);
-        d1 = fmaf(ai[7], (float)(hi >> 24), d1);
+        const int lo = (int)(words[i] & 0x0F0F0F0Fu);
+        const int hi = (int)((words[i] >> 4) & 0x0F0F0F0Fu);
+        d0 = __builtin_amdgcn_sdot4(a.lo[0][i], lo, d0, false);
+        d1 = __builtin_amdgcn_sdot4(a.lo[1][i], lo, d1, false);
+        d2 = __builtin_amdgcn_sdot4(a.lo[2][i], lo, d2, false);
+        d0 = __builtin_amdgcn_sdot4(a.hi[0][i], hi, d0, false);
+        d1 = __builtin_amdgcn_sdot4(a.hi[1][i], hi, d1, false);
+        d2 = __builtin_amdgcn_sdot4(a.hi[2][i], hi, d2, false);
     }
-    return d0 + d1;
+    const float t = fmaf((float)d2, 1.0f / 64516.0f, fmaf((float)d1, 1.0f / 254.0f, (float)d0));
+    return a.sc * t;
 }
 
 // Activations live in LDS as fp32 in 16-byte units; unit i of 32-float chunk c
@@ -93,10 +138,16 @@ __device__ __forceinline__ void stage_activations(const T* __restrict__ A, float
     }
 }
 
-// One wave per R consecutive rows of B (a strided loop covers N beyond
-// grid*4*R). Lane l owns the 32-code chunks c = l + 64j (j < BPL) of every row and
-// keeps their activations in VGPRs. All R*BPL 16-byte weight loads of a row group
-// are in flight before the activations are staged.
+template <int R, int BPL>
+struct GemvGroup {
+    uint4 w[R][BPL];
+    float s[R][BPL], z[R][BPL];
+};
+
+// Rows are taken in groups of R consecutive rows; group g goes to wave
+// g mod (total waves). Lane l owns the 32-code chunks c = l + 64j (j < BPL) of
+// every row; its activations are converted once to integer limbs. The weight
+// loads of the next group are in flight while the current group is reduced.
 template <typename T, int BS, int BPL, int R>
 __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ B,
@@ -105,75 +156,75 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         T* __restrict__ Y, int N, int K,
                                                         int nb) {
     extern __shared__ float4 sA[];
+    using Group = GemvGroup<R, BPL>;
     const int Kp = nb * BS;
     const int C = Kp / 32;  // 32-code chunks per row
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int stride = gridDim.x * 4 * R;
+    const int waves_total = gridDim.x * 4;
+    const int ngroups = (N + R - 1) / R;
     const size_t row_bytes = (size_t)Kp / 2;
     const int zp_cols = (nb + 1) / 2;
 
-    uint4 w[R][BPL];
-    float sc[R][BPL], zc[R][BPL];
-    auto load_group = [&](int n0) {
+    auto load_group = [&](Group& g, int gi) {
+        const int n0 = gi * R;
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int j = 0; j < BPL; ++j) {
                 const int n = n0 + r, c = lane + 64 * j;
-                if (n < N && c < C) {
+                if (gi < ngroups && n < N && c < C) {
                     const u32x4_t v = __builtin_nontemporal_load(
                         reinterpret_cast<const u32x4_t*>(B + (size_t)n * row_bytes) + c);
-                    w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
+                    g.w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
                     const int blk = (32 * c) / BS;
-                    sc[r][j] = to_f32(S[(size_t)n * nb + blk]);
-                    zc[r][j] = Z ? (float)nibble(Z[(size_t)n * zp_cols + blk / 2], blk & 1) : 8.f;
+                    g.s[r][j] = to_f32(S[(size_t)n * nb + blk]);
+                    g.z[r][j] = Z ? (float)nibble(Z[(size_t)n * zp_cols + blk / 2], blk & 1) : 8.f;
                 } else {
-                    w[r][j] = make_uint4(0, 0, 0, 0);
-                    sc[r][j] = 0.f;
-                    zc[r][j] = 0.f;
+                    g.w[r][j] = make_uint4(0, 0, 0, 0);
+                    g.s[r][j] = 0.f;
+                    g.z[r][j] = 0.f;
                 }
             }
     };
-    int n0 = (blockIdx.x * 4 + wave) * R;
-    if (n0 < N) load_group(n0);
+
+    const int g0 = blockIdx.x * 4 + wave;
+    Group ga, gb;
+    load_group(ga, g0);
 
     stage_activations<T>(A, sA, K, Kp);
     __syncthreads();
-
-    float a[BPL][32];
-    float asum[BPL];
+    ActChunk act[BPL];
 #pragma unroll
     for (int j = 0; j < BPL; ++j) {
         const int c = lane + 64 * j;
-        float s = 0.f;
+        float a[32];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float4 v = c < C ? sA[swz_unit(8 * c + i)] : make_float4(0.f, 0.f, 0.f, 0.f);
-            a[j][4 * i + 0] = v.x;
-            a[j][4 * i + 1] = v.y;
-            a[j][4 * i + 2] = v.z;
-            a[j][4 * i + 3] = v.w;
-            s += (v.x + v.y) + (v.z + v.w);
+            a[4 * i + 0] = v.x;
+            a[4 * i + 1] = v.y;
+            a[4 * i + 2] = v.z;
+            a[4 * i + 3] = v.w;
         }
-        asum[j] = s;
+        make_act_chunk(a, act[j]);
     }
 
-    for (; n0 < N; n0 += stride) {
+    auto reduce_store = [&](const Group& g, int gi) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             float total = 0.f;
 #pragma unroll
             for (int j = 0; j < BPL; ++j) {
-                const float d = dot32_codes(a[j], w[r][j]);
-                total = fmaf(sc[r][j], d - zc[r][j] * asum[j], total);
+                const float d = dot32_act(act[j], g.w[r][j]);
+                total = fmaf(g.s[r][j], d - g.z[r][j] * act[j].asum, total);
             }
             acc[r] = total;
         }
-        if (n0 + stride < N) load_group(n0 + stride);
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+        const int n0 = gi * R;
         if (lane < R) {
             float v = acc[0];
 #pragma unroll
@@ -181,51 +232,31 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                 if (lane == r) v = acc[r];
             if (n0 + lane < N) Y[n0 + lane] = from_f32<T>(v);
         }
+    };
+
+    for (int gi = g0; gi < ngroups; gi += 2 * waves_total) {
+        const int g1 = gi + waves_total;
+        if (g1 < ngroups) load_group(gb, g1);
+        reduce_store(ga, gi);
+        if (g1 >= ngroups) break;
+        const int g2 = g1 + waves_total;
+        if (g2 < ngroups) load_group(ga, g2);
+        reduce_store(gb, g1);
     }
 }
 
 template <typename T, int BS, int BPL, int R>
 static int launch_gemv4_r(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y, int N,
-                          int K, int nb, int grid, hipStream_t st) {
+                          int K, int nb, hipStream_t st) {
     const int Kp = nb * BS;
-    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, BPL, R>), dim3(grid), dim3(256),
-                       (size_t)Kp * sizeof(float), st, A, B, S, Z, Y, N, K, nb);
-    return check_launch("mnb_gemv4");
-}
-
-// Rows per wave: aim for about two workgroups of 4 waves per CU, each wave
-// owning R consecutive rows (R from a small set; large N loops).
-template <typename T, int BS, int BPL>
-static int launch_gemv4_bpl(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
-                            int N, int K, int nb, hipStream_t st) {
-    const int target_waves = device_cu_count() * 8;
-    const int want = (N + target_waves - 1) / target_waves;
-    constexpr int RMAX = BPL <= 2 ? 8 : (BPL <= 4 ? 2 : 1);
-    int R = want <= 1 ? 1 : want <= 2 ? 2 : want <= 4 ? 4 : want <= 6 ? 6 : 8;
-    if (R > RMAX) R = RMAX;
     const long groups = ((long)N + R - 1) / R;
+    // Two workgroups of 4 waves per CU; each wave walks its groups with one group of
+    // weight loads in flight ahead of the one being reduced.
     long grid = (groups + 3) / 4;
     if (grid > 2L * device_cu_count()) grid = 2L * device_cu_count();
-    switch (R) {
-        case 1: return launch_gemv4_r<T, BS, BPL, 1>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
-        case 2:
-            if constexpr (RMAX >= 2)
-                return launch_gemv4_r<T, BS, BPL, 2>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
-            break;
-        case 4:
-            if constexpr (RMAX >= 4)
-                return launch_gemv4_r<T, BS, BPL, 4>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
-            break;
-        case 6:
-            if constexpr (RMAX >= 6)
-                return launch_gemv4_r<T, BS, BPL, 6>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
-            break;
-        default:
-            if constexpr (RMAX >= 8)
-                return launch_gemv4_r<T, BS, BPL, 8>(A, B, S, Z, Y, N, K, nb, (int)grid, st);
-            break;
-    }
-    return -1;
+    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, BPL, R>), dim3((unsigned)grid), dim3(256),
+                       (size_t)Kp * sizeof(float), st, A, B, S, Z, Y, N, K, nb);
+    return check_launch("mnb_gemv4");
 }
 
 template <typename T, int BS>
@@ -234,13 +265,12 @@ static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t*
     const int C = nb * BS / 32;
     const int bpl = (C + 63) / 64;
     switch (bpl) {
-        case 1: return launch_gemv4_bpl<T, BS, 1>(A, B, S, Z, Y, N, K, nb, st);
-        case 2: return launch_gemv4_bpl<T, BS, 2>(A, B, S, Z, Y, N, K, nb, st);
-        case 3: return launch_gemv4_bpl<T, BS, 3>(A, B, S, Z, Y, N, K, nb, st);
-        case 4: return launch_gemv4_bpl<T, BS, 4>(A, B, S, Z, Y, N, K, nb, st);
-        case 5: return launch_gemv4_bpl<T, BS, 5>(A, B, S, Z, Y, N, K, nb, st);
-        case 6: return launch_gemv4_bpl<T, BS, 6>(A, B, S, Z, Y, N, K, nb, st);
-        default: return -1;  // K > 12288: the caller falls back
+        case 1: return launch_gemv4_r<T, BS, 1, 4>(A, B, S, Z, Y, N, K, nb, st);
+        case 2: return launch_gemv4_r<T, BS, 2, 2>(A, B, S, Z, Y, N, K, nb, st);
+        case 3: return launch_gemv4_r<T, BS, 3, 1>(A, B, S, Z, Y, N, K, nb, st);
+        case 4: return launch_gemv4_r<T, BS, 4, 1>(A, B, S, Z, Y, N, K, nb, st);
+        case 5: return launch_gemv4_r<T, BS, 5, 1>(A, B, S, Z, Y, N, K, nb, st);
+        default: return -1;  // K > 10240: the caller falls back
     }
 }
 
@@ -533,7 +563,7 @@ static int run_mnb(const void* A, const uint8_t* B, const void* S, const uint8_t
     T* y = static_cast<T*>(Y);
     const bool aligned = (reinterpret_cast<uintptr_t>(B) % 16) == 0;
     const bool fast_form = bits == 4 && (bs == 32 || bs == 64 || bs == 128) && aligned;
-    if (fast_form && M == 1 && (size_t)nb * bs <= 12288) {
+    if (fast_form && M == 1 && (size_t)nb * bs <= 10240) {
         int rc = -1;
         if (bs == 32) rc = launch_gemv4<T, 32>(a, B, s, Z, y, N, K, nb, st);
         if (bs == 64) rc = launch_gemv4<T, 64>(a, B, s, Z, y, N, K, nb, st);
