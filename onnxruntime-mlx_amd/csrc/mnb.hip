@@ -30,8 +30,10 @@ namespace ortmi {
 // l2_i/254^2) with int8 limbs, packed to match the code bytes of a 16-byte weight
 // chunk: word w of the weights holds codes 8w..8w+7; (w & 0x0F0F0F0F) has codes
 // 8w+{0,2,4,6} in its bytes and ((w >> 4) & 0x0F0F0F0F) codes 8w+{1,3,5,7}.
-// The reconstruction error is at most 0.5 * sc / 254^2 ~ 2^-24 * max|a|, the same
-// order as fp32 rounding of the activations, and the integer dots are exact.
+// With a power-of-two sc <= max|a|/64 the reconstruction error is at most
+// 0.5 * sc / 254^2 < 2^-23 * max|a|, the order of fp32 rounding of the
+// activations; the integer dots are exact, and a chunk whose values are exact
+// multiples of sc (one-hot rows, small integers) is reproduced exactly.
 struct ActChunk {
     int lo[3][4], hi[3][4];  // [limb][word]
     float sc;                // chunk scale (max|a| / 127)
@@ -46,8 +48,14 @@ __device__ __forceinline__ void make_act_chunk(const float (&a)[32], ActChunk& q
         s += a[i];
     }
     q.asum = s;
-    q.sc = amax * (1.0f / 127.0f);
-    const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+    // Power-of-two chunk scale, so that a -> a/sc -> sc*(...) scales exactly: with
+    // amax = m * 2^e (m in [0.5, 1)), sc = 2^(e-7) puts max|a|/sc in [64, 128);
+    // the top of the binade (m * 128 > 127) takes sc = 2^(e-6) instead.
+    int e = 0;
+    const float m = frexpf(amax, &e);
+    const int sh = (m * 128.0f > 127.0f) ? e - 6 : e - 7;
+    q.sc = amax > 0.f ? ldexpf(1.0f, sh) : 0.f;
+    const float inv = amax > 0.f ? ldexpf(1.0f, -sh) : 0.f;
     int8_t l[3][32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
