@@ -8,12 +8,11 @@
 //
 // Kernels:
 //  * mnb_gemv4  - decode (M == 1), bits 4, bs in {32, 64, 128}. HBM-bound: each
-//    lane owns fixed 32-code chunks of K and keeps the matching activations in
-//    VGPRs as three int8 limbs per value (staged once per workgroup through LDS),
-//    then streams rows of B with 128-bit loads (a wave reads 1 KiB contiguous per
-//    instruction). Codes are dotted with the limbs by v_dot4 (exact integer
-//    sums), so a code costs ~1.4 VALU ops instead of a convert and an FMA. Zero
-//    points are folded as s*(sum(a*q) - zp*sum(a)).
+//    lane owns a contiguous run of 32-code chunks of K and keeps the matching
+//    activations in VGPRs (staged once per workgroup through LDS), then streams
+//    rows of B with 128-bit loads. Zero points are folded as
+//    s*(sum(a*q) - zp*sum(a)), so the inner loop is one byte-convert and one FMA
+//    per code.
 //  * mnb_gemm4  - prefill (M > 1, fp16), bits 4, bs in {32, 64, 128}. MFMA
 //    v_mfma_f32_32x32x16_f16: the weight tile is dequantised to fp16 in LDS
 //    (fp16((q - zp) * s), one rounding) and the activation tile is staged in LDS;
@@ -26,137 +25,51 @@ namespace ortmi {
 
 // -------------------------------------------------------------- GEMV (M=1) --
 
-// One 32-code chunk of activations in integer form: a_i ~= sc * (l0_i + l1_i/254 +
-// l2_i/254^2) with int8 limbs, packed to match the code bytes of a 16-byte weight
-// chunk: word w of the weights holds codes 8w..8w+7; (w & 0x0F0F0F0F) has codes
-// 8w+{0,2,4,6} in its bytes and ((w >> 4) & 0x0F0F0F0F) codes 8w+{1,3,5,7}.
-// With a power-of-two sc <= max|a|/64 the reconstruction error is at most
-// 0.5 * sc / 254^2 < 2^-23 * max|a|, the order of fp32 rounding of the
-// activations; the integer dots are exact, and a chunk whose values are exact
-// multiples of sc (one-hot rows, small integers) is reproduced exactly.
-struct ActChunk {
-    int lo[3][4], hi[3][4];  // [limb][word]
-    float sc;                // chunk scale (max|a| / 127)
-    float asum;              // sum of the activations (for the zero-point term)
-};
-
-__device__ __forceinline__ void make_act_chunk(const float (&a)[32], ActChunk& q) {
-    float amax = 0.f, s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        amax = fmaxf(amax, fabsf(a[i]));
-        s += a[i];
-    }
-    q.asum = s;
-    // Power-of-two chunk scale, so that a -> a/sc -> sc*(...) scales exactly: with
-    // amax = m * 2^e (m in [0.5, 1)), sc = 2^(e-7) puts max|a|/sc in [64, 128);
-    // the top of the binade (m * 128 > 127) takes sc = 2^(e-6) instead.
-    int e = 0;
-    const float m = frexpf(amax, &e);
-    const int sh = (m * 128.0f > 127.0f) ? e - 6 : e - 7;
-    q.sc = amax > 0.f ? ldexpf(1.0f, sh) : 0.f;
-    const float inv = amax > 0.f ? ldexpf(1.0f, -sh) : 0.f;
-    int8_t l[3][32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const float x = a[i] * inv;  // |x| <= 127
-        const float l0 = rintf(x);
-        const float r1 = (x - l0) * 254.0f;  // |r1| <= 127
-        const float l1 = rintf(r1);
-        const float l2 = rintf((r1 - l1) * 254.0f);
-        l[0][i] = (int8_t)l0;
-        l[1][i] = (int8_t)l1;
-        l[2][i] = (int8_t)l2;
-    }
-#pragma unroll
-    for (int j = 0; j < 3; ++j)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const int b = 8 * w;
-            q.lo[j][w] = (int)((uint32_t)(uint8_t)l[j][b + 0] | ((uint32_t)(uint8_t)l[j][b + 2] << 8) |
-                               ((uint32_t)(uint8_t)l[j][b + 4] << 16) |
-                               ((uint32_t)(uint8_t)l[j][b + 6] << 24));
-            q.hi[j][w] = (int)((uint32_t)(uint8_t)l[j][b + 1] | ((uint32_t)(uint8_t)l[j][b + 3] << 8) |
-                               ((uint32_t)(uint8_t)l[j][b + 5] << 16) |
-                               ((uint32_t)(uint8_t)l[j][b + 7] << 24));
-        }
-}
-
-// sum_i a_i * q_i for the 32 codes of one 16-byte weight chunk.
-__device__ __forceinline__ float dot32_act(const ActChunk& a, uint4 w) {
+// Dot product of 32 activations with the 32 4-bit codes of one 16-byte chunk.
+// Code i of the chunk is nibble (i & 1) of byte i/2, i.e. bits [4i, 4i+4) of the
+// little-endian 128-bit word.
+__device__ __forceinline__ float dot32_codes(const float* a, uint4 w) {
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-    int d0 = 0, d1 = 0, d2 = 0;
+    float d0 = 0.f, d1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int lo = (int)(words[i] & 0x0F0F0F0Fu);
-        const int hi = (int)((words[i] >> 4) & 0x0F0F0F0Fu);
-        d0 = __builtin_amdgcn_sdot4(a.lo[0][i], lo, d0, false);
-        d1 = __builtin_amdgcn_sdot4(a.lo[1][i], lo, d1, false);
-        d2 = __builtin_amdgcn_sdot4(a.lo[2][i], lo, d2, false);
-        d0 = __builtin_amdgcn_sdot4(a.hi[0][i], hi, d0, false);
-        d1 = __builtin_amdgcn_sdot4(a.hi[1][i], hi, d1, false);
-        d2 = __builtin_amdgcn_sdot4(a.hi[2][i], hi, d2, false);
+        const uint32_t lo = words[i] & 0x0F0F0F0Fu;         // codes 8i+0,2,4,6
+        const uint32_t hi = (words[i] >> 4) & 0x0F0F0F0Fu;  // codes 8i+1,3,5,7
+        const float* ai = a + 8 * i;
+        d0 = fmaf(ai[0], (float)(lo & 0xffu), d0);
+        d1 = fmaf(ai[1], (float)(hi & 0xffu), d1);
+        d0 = fmaf(ai[2], (float)((lo >> 8) & 0xffu), d0);
+        d1 = fmaf(ai[3], (float)((hi >> 8) & 0xffu), d1);
+        d0 = fmaf(ai[4], (float)((lo >> 16) & 0xffu), d0);
+        d1 = fmaf(ai[5], (float)((hi >> 16) & 0xffu), d1);
+        d0 = fmaf(ai[6], (float)(lo >> 24), d0);
+        d1 = fmaf(ai[7], (float)(hi >> 24), d1);
     }
-    const float t = fmaf((float)d2, 1.0f / 64516.0f, fmaf((float)d1, 1.0f / 254.0f, (float)d0));
-    return a.sc * t;
+    return d0 + d1;
 }
 
-// Activations live in LDS as fp32 in 16-byte units; unit i of 32-float chunk c
-// is stored at unit 8c + (i ^ (c & 7)), so the 8 lanes of one LDS read phase
-// (consecutive c, equal i) hit 8 different bank groups.
-__device__ __forceinline__ int swz_unit(int q) { return (q & ~7) | ((q & 7) ^ ((q >> 3) & 7)); }
-
-// Stage A[0, K) (zero-padded to Kp) into swizzled fp32 LDS: every thread issues
-// all of its 16-byte loads before its first LDS store.
-template <typename T>
-__device__ __forceinline__ void stage_activations(const T* __restrict__ A, float4* sA, int K,
-                                                  int Kp) {
-    constexpr int EPL = 16 / sizeof(T);  // elements per 16-byte load
-    constexpr int U = 4;
-    const int nvec = Kp / EPL;
-    const bool vec_ok = (K % EPL) == 0 && (reinterpret_cast<uintptr_t>(A) % 16) == 0;
-    for (int base = threadIdx.x; base < nvec; base += 256 * U) {
-        uint4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int vi = base + u * 256;
-            const int k0 = vi * EPL;
-            if (vi < nvec && vec_ok && k0 + EPL <= K) {
-                v[u] = *reinterpret_cast<const uint4*>(A + k0);
-            } else {
-                T t[EPL];
-#pragma unroll
-                for (int e = 0; e < EPL; ++e)
-                    t[e] = (vi < nvec && k0 + e < K) ? A[k0 + e] : from_f32<T>(0.f);
-                v[u] = *reinterpret_cast<const uint4*>(t);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int vi = base + u * 256;
-            if (vi >= nvec) continue;
-            const T* t = reinterpret_cast<const T*>(&v[u]);
-#pragma unroll
-            for (int e = 0; e < EPL; e += 4) {
-                const int q = (vi * EPL + e) / 4;  // fp32 16-byte unit
-                sA[swz_unit(q)] = make_float4(to_f32(t[e]), to_f32(t[e + 1]), to_f32(t[e + 2]),
-                                              to_f32(t[e + 3]));
-            }
-        }
-    }
+// Activations live in LDS as fp32 in 16-byte units. Lane l reads the 8*CPL
+// consecutive units of its chunks; unit u of lane l is stored at
+// u ^ ((u / (8*CPL)) & 7), so the 8 lanes of one read phase hit 8 bank groups.
+template <int CPL>
+__device__ __forceinline__ int act_unit(int u) {
+    return u ^ ((u / (8 * CPL)) & 7);
 }
 
-template <int R, int BPL>
+template <int R, int CPL>
 struct GemvGroup {
-    uint4 w[R][BPL];
-    float s[R][BPL], z[R][BPL];
+    uint4 w[R][CPL];
+    float s[R][CPL], z[R][CPL];
 };
 
-// Rows are taken in groups of R consecutive rows; group g goes to wave
-// g mod (total waves). Lane l owns the 32-code chunks c = l + 64j (j < BPL) of
-// every row; its activations are converted once to integer limbs. The weight
-// loads of the next group are in flight while the current group is reduced.
-template <typename T, int BS, int BPL, int R>
+// Lane l owns the CPL consecutive 32-code chunks [l*CPL, (l+1)*CPL) of every row,
+// so a row costs one 16*CPL-byte weight run, CPL adjacent scales and one or two
+// zero-point bytes per lane. The activation loads are issued first, then the
+// weight loads of the wave's first row group; the activations go through LDS
+// (one copy per workgroup) into VGPRs while the weights are in flight. Row groups
+// of R rows are dealt to waves round-robin; the next group's loads are issued
+// before the current group is reduced.
+template <typename T, int BS, int CPL, int R>
 __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ B,
                                                         const T* __restrict__ S,
@@ -164,7 +77,7 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         T* __restrict__ Y, int N, int K,
                                                         int nb) {
     extern __shared__ float4 sA[];
-    using Group = GemvGroup<R, BPL>;
+    using Group = GemvGroup<R, CPL>;
     const int Kp = nb * BS;
     const int C = Kp / 32;  // 32-code chunks per row
     const int lane = threadIdx.x & 63;
@@ -173,49 +86,102 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     const int ngroups = (N + R - 1) / R;
     const size_t row_bytes = (size_t)Kp / 2;
     const int zp_cols = (nb + 1) / 2;
+    const int c0 = lane * CPL;
 
+    // 1. activation loads (16 bytes each), all in flight before anything else.
+    constexpr int EPL = 16 / sizeof(T);
+    constexpr int AV = 8;  // up to 8 vectors per thread: Kp <= 2048 * EPL
+    const int nvec = Kp / EPL;
+    const bool vec_ok = (K % EPL) == 0 && (reinterpret_cast<uintptr_t>(A) % 16) == 0;
+    uint4 av[AV];
+#pragma unroll
+    for (int u = 0; u < AV; ++u) {
+        const int vi = threadIdx.x + u * 256;
+        const int k0 = vi * EPL;
+        if (vi < nvec && vec_ok && k0 + EPL <= K) {
+            av[u] = *reinterpret_cast<const uint4*>(A + k0);
+        } else {
+            T t[EPL];
+#pragma unroll
+            for (int e = 0; e < EPL; ++e)
+                t[e] = (vi < nvec && k0 + e < K) ? A[k0 + e] : from_f32<T>(0.f);
+            av[u] = *reinterpret_cast<const uint4*>(t);
+        }
+    }
+
+    // 2. weights of the first row group.
     auto load_group = [&](Group& g, int gi) {
         const int n0 = gi * R;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+        for (int r = 0; r < R; ++r) {
+            const int n = n0 + r;
+            const bool row_ok = gi < ngroups && n < N;
+            const uint8_t* brow = B + (size_t)n * row_bytes;
+            // Zero-point bytes covering this lane's blocks (at most 3 for CPL <= 5).
+            const int blk0 = (32 * c0) / BS;
+            uint8_t zb[3] = {0x88, 0x88, 0x88};
+            if (row_ok && Z && c0 < C) {
+                const int clast = min(c0 + CPL - 1, C - 1);
+                const int last_byte = ((32 * clast) / BS) / 2;
 #pragma unroll
-            for (int j = 0; j < BPL; ++j) {
-                const int n = n0 + r, c = lane + 64 * j;
-                if (gi < ngroups && n < N && c < C) {
+                for (int t = 0; t < 3; ++t)
+                    if (blk0 / 2 + t <= last_byte) zb[t] = Z[(size_t)n * zp_cols + blk0 / 2 + t];
+            }
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = c0 + j;
+                if (row_ok && c < C) {
                     const u32x4_t v = __builtin_nontemporal_load(
-                        reinterpret_cast<const u32x4_t*>(B + (size_t)n * row_bytes) + c);
+                        reinterpret_cast<const u32x4_t*>(brow) + c);
                     g.w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
                     const int blk = (32 * c) / BS;
                     g.s[r][j] = to_f32(S[(size_t)n * nb + blk]);
-                    g.z[r][j] = Z ? (float)nibble(Z[(size_t)n * zp_cols + blk / 2], blk & 1) : 8.f;
+                    const int d = blk / 2 - blk0 / 2;
+                    const uint8_t zbyte = d == 0 ? zb[0] : (d == 1 ? zb[1] : zb[2]);
+                    g.z[r][j] = Z ? (float)nibble(zbyte, blk & 1) : 8.f;
                 } else {
                     g.w[r][j] = make_uint4(0, 0, 0, 0);
                     g.s[r][j] = 0.f;
                     g.z[r][j] = 0.f;
                 }
             }
+        }
     };
-
     const int g0 = blockIdx.x * 4 + wave;
     Group ga, gb;
     load_group(ga, g0);
 
-    stage_activations<T>(A, sA, K, Kp);
-    __syncthreads();
-    ActChunk act[BPL];
+    // 3. activations -> LDS (swizzled fp32 units) -> VGPRs.
 #pragma unroll
-    for (int j = 0; j < BPL; ++j) {
-        const int c = lane + 64 * j;
-        float a[32];
+    for (int u = 0; u < AV; ++u) {
+        const int vi = threadIdx.x + u * 256;
+        if (vi >= nvec) continue;
+        const T* t = reinterpret_cast<const T*>(&av[u]);
+#pragma unroll
+        for (int e = 0; e < EPL; e += 4) {
+            const int q = (vi * EPL + e) / 4;
+            sA[act_unit<CPL>(q)] = make_float4(to_f32(t[e]), to_f32(t[e + 1]), to_f32(t[e + 2]),
+                                               to_f32(t[e + 3]));
+        }
+    }
+    __syncthreads();
+    float a[CPL][32];
+    float asum[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int c = c0 + j;
+        float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float4 v = c < C ? sA[swz_unit(8 * c + i)] : make_float4(0.f, 0.f, 0.f, 0.f);
-            a[4 * i + 0] = v.x;
-            a[4 * i + 1] = v.y;
-            a[4 * i + 2] = v.z;
-            a[4 * i + 3] = v.w;
+            const float4 v =
+                c < C ? sA[act_unit<CPL>(8 * c + i)] : make_float4(0.f, 0.f, 0.f, 0.f);
+            a[j][4 * i + 0] = v.x;
+            a[j][4 * i + 1] = v.y;
+            a[j][4 * i + 2] = v.z;
+            a[j][4 * i + 3] = v.w;
+            s += (v.x + v.y) + (v.z + v.w);
         }
-        make_act_chunk(a, act[j]);
+        asum[j] = s;
     }
 
     auto reduce_store = [&](const Group& g, int gi) {
@@ -224,9 +190,9 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
         for (int r = 0; r < R; ++r) {
             float total = 0.f;
 #pragma unroll
-            for (int j = 0; j < BPL; ++j) {
-                const float d = dot32_act(act[j], g.w[r][j]);
-                total = fmaf(g.s[r][j], d - g.z[r][j] * act[j].asum, total);
+            for (int j = 0; j < CPL; ++j) {
+                const float d = dot32_codes(a[j], g.w[r][j]);
+                total = fmaf(g.s[r][j], d - g.z[r][j] * asum[j], total);
             }
             acc[r] = total;
         }
@@ -253,31 +219,46 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     }
 }
 
-template <typename T, int BS, int BPL, int R>
+template <typename T, int BS, int CPL, int R>
 static int launch_gemv4_r(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y, int N,
                           int K, int nb, hipStream_t st) {
     const int Kp = nb * BS;
     const long groups = ((long)N + R - 1) / R;
-    // Two workgroups of 4 waves per CU; each wave walks its groups with one group of
-    // weight loads in flight ahead of the one being reduced.
+    // One row group per wave while that gives at most 8 workgroups per CU; larger
+    // N loops with the next group's loads in flight.
     long grid = (groups + 3) / 4;
-    if (grid > 2L * device_cu_count()) grid = 2L * device_cu_count();
-    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, BPL, R>), dim3((unsigned)grid), dim3(256),
+    if (grid > 8L * device_cu_count()) grid = 8L * device_cu_count();
+    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R>), dim3((unsigned)grid), dim3(256),
                        (size_t)Kp * sizeof(float), st, A, B, S, Z, Y, N, K, nb);
     return check_launch("mnb_gemv4");
+}
+
+// Rows per group: the smallest R in {1, 2, 4} that still leaves >= 4 workgroups
+// per CU, so small N spreads over the whole GPU and large N amortises staging.
+template <typename T, int BS, int CPL>
+static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
+                            int N, int K, int nb, hipStream_t st) {
+    const long per_r4 = ((long)N + 3) / 4 / 4;  // workgroups at R = 4
+    const long want = 4L * device_cu_count();
+    if (CPL <= 2 && per_r4 >= want)
+        return launch_gemv4_r<T, BS, CPL, CPL <= 2 ? 4 : 1>(A, B, S, Z, Y, N, K, nb, st);
+    if (CPL <= 3 && per_r4 * 2 >= want)
+        return launch_gemv4_r<T, BS, CPL, CPL <= 3 ? 2 : 1>(A, B, S, Z, Y, N, K, nb, st);
+    return launch_gemv4_r<T, BS, CPL, 1>(A, B, S, Z, Y, N, K, nb, st);
 }
 
 template <typename T, int BS>
 static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y, int N,
                         int K, int nb, hipStream_t st) {
     const int C = nb * BS / 32;
-    const int bpl = (C + 63) / 64;
-    switch (bpl) {
-        case 1: return launch_gemv4_r<T, BS, 1, 4>(A, B, S, Z, Y, N, K, nb, st);
-        case 2: return launch_gemv4_r<T, BS, 2, 2>(A, B, S, Z, Y, N, K, nb, st);
-        case 3: return launch_gemv4_r<T, BS, 3, 1>(A, B, S, Z, Y, N, K, nb, st);
-        case 4: return launch_gemv4_r<T, BS, 4, 1>(A, B, S, Z, Y, N, K, nb, st);
-        case 5: return launch_gemv4_r<T, BS, 5, 1>(A, B, S, Z, Y, N, K, nb, st);
+    const int cpl = (C + 63) / 64;
+    if ((long)nb * BS > 2048L * (16 / (long)sizeof(T))) return -1;  // activation staging bound
+    switch (cpl) {
+        case 1: return launch_gemv4_cpl<T, BS, 1>(A, B, S, Z, Y, N, K, nb, st);
+        case 2: return launch_gemv4_cpl<T, BS, 2>(A, B, S, Z, Y, N, K, nb, st);
+        case 3: return launch_gemv4_cpl<T, BS, 3>(A, B, S, Z, Y, N, K, nb, st);
+        case 4: return launch_gemv4_cpl<T, BS, 4>(A, B, S, Z, Y, N, K, nb, st);
+        case 5: return launch_gemv4_cpl<T, BS, 5>(A, B, S, Z, Y, N, K, nb, st);
         default: return -1;  // K > 10240: the caller falls back
     }
 }
