@@ -23,7 +23,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
 KERNEL_SOURCES = ["runtime.hip", "mnb.hip", "attention.hip", "norm.hip"]
-EP_SOURCES = ["ep/ep_abi.cpp", "ep/plan.cpp", "ep/ops.cpp"]
+EP_SOURCES = ["ep/ep.cpp", "ep/graph.cpp", "ep/plan.cpp"]
 
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -47,7 +47,8 @@ def _run(cmd: list[str]) -> None:
 def _compile(src: str) -> str:
     os.makedirs(OBJ, exist_ok=True)
     obj = os.path.join(OBJ, src.replace("/", "_") + ".o")
-    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    extra = ["-fvisibility=hidden"] if src.startswith("ep/") else []
+    _run([HIPCC, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj
 
 
@@ -79,11 +80,23 @@ def build_ep(jobs: int = 4) -> str | None:
     return out
 
 
+def build_harness() -> str:
+    """The in-repo harness host that drives a plugin EP through the ORT plugin ABI."""
+    obj = _compile("host/harness.cpp")
+    out = os.path.join(LIB, "libortmi_harness.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, obj, "-ldl",
+          "-Wl,-soname,libortmi_harness.so"])
+    os.replace(tmp, out)
+    return out
+
+
 def build_all(jobs: int = 4) -> list[str]:
     outs = [build_kernels(jobs)]
     ep = build_ep(jobs)
     if ep:
         outs.append(ep)
+    outs.append(build_harness())
     return outs
 
 

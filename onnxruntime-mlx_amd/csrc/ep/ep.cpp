@@ -1,0 +1,386 @@
+// C-ABI surface of the MI355X plugin execution provider: CreateEpFactories /
+// ReleaseEpFactory and the OrtEpFactory / OrtEp / OrtNodeComputeInfo vtables.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <set>
+
+#include "../../../include/ortmi_kernels.h"
+#include "ep_internal.h"
+
+#define ORTMI_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace ortmi_ep {
+
+using namespace ort_abi;
+
+namespace {
+
+constexpr uint32_t kVendorIdAmd = 0x1002;
+constexpr const char* kDefaultName = "MI355XExecutionProvider";
+constexpr const char* kVersion = "0.29.0";
+
+// Nothing may unwind across the ABI (rust/src/lib.rs:37-71): every entry runs
+// its body under this guard and turns exceptions into an OrtStatus.
+template <typename F>
+OrtStatus* guard(const OrtApi* a, const char* what, F&& body) {
+    try {
+        body();
+        return nullptr;
+    } catch (const EpError& e) {
+        std::string m = std::string("MI355X EP ") + what + ": " + e.what();
+        return a ? api::CreateStatus(a)(e.code, m.c_str()) : nullptr;
+    } catch (const std::exception& e) {
+        std::string m = std::string("MI355X EP ") + what + ": " + e.what();
+        return a ? api::CreateStatus(a)(ORT_EP_FAIL, m.c_str()) : nullptr;
+    } catch (...) {
+        std::string m = std::string("MI355X EP ") + what + ": unknown failure";
+        return a ? api::CreateStatus(a)(ORT_EP_FAIL, m.c_str()) : nullptr;
+    }
+}
+
+bool env_flag(const char* name) {
+    const char* v = std::getenv(name);
+    return v && *v && std::strcmp(v, "0") != 0;
+}
+
+// ------------------------------------------------------------- allocator --
+struct DeviceAllocator {
+    OrtAllocator base;  // first member: an OrtAllocator* is a DeviceAllocator*
+    const OrtMemoryInfo* info;
+    int device;
+};
+
+void* alloc_fn(OrtAllocator* self, size_t size) {
+    auto* d = reinterpret_cast<DeviceAllocator*>(self);
+    void* p = nullptr;
+    if (hipSetDevice(d->device) != hipSuccess) return nullptr;
+    if (hipMalloc(&p, size ? size : 1) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
+void free_fn(OrtAllocator*, void* p) {
+    if (p) (void)hipFree(p);
+}
+const OrtMemoryInfo* info_fn(const OrtAllocator* self) {
+    return reinterpret_cast<const DeviceAllocator*>(self)->info;
+}
+void* reserve_fn(OrtAllocator* self, size_t size) { return alloc_fn(self, size); }
+void* alloc_on_stream_fn(OrtAllocator* self, size_t size, OrtSyncStreamImpl*) {
+    return alloc_fn(self, size);
+}
+
+// --------------------------------------------------------- data transfer --
+struct DataTransfer {
+    OrtDataTransferImpl base;
+    const OrtApi* api;
+};
+
+void dt_release(OrtDataTransferImpl* self) { delete reinterpret_cast<DataTransfer*>(self); }
+bool dt_can_copy(const OrtDataTransferImpl*, const OrtMemoryDevice*, const OrtMemoryDevice*) {
+    return true;  // unified addressing: hipMemcpyDefault handles every direction
+}
+OrtStatus* dt_copy(OrtDataTransferImpl* self, const OrtValue** src, OrtValue** dst,
+                   OrtSyncStreamImpl**, size_t n) {
+    const OrtApi* a = reinterpret_cast<DataTransfer*>(self)->api;
+    return guard(a, "CopyTensors", [&] {
+        for (size_t i = 0; i < n; ++i) {
+            OrtTensorTypeAndShapeInfo* info = nullptr;
+            check_ort(a, api::GetTensorTypeAndShape(a)(src[i], &info), "GetTensorTypeAndShape");
+            size_t count = 0;
+            ONNXTensorElementDataType et = ONNX_TENSOR_ELEMENT_DATA_TYPE_UNDEFINED;
+            OrtStatus* s1 = api::GetTensorShapeElementCount(a)(info, &count);
+            OrtStatus* s2 = s1 ? nullptr : api::GetTensorElementType(a)(info, &et);
+            api::ReleaseTensorTypeAndShapeInfo(a)(info);
+            check_ort(a, s1, "GetTensorShapeElementCount");
+            check_ort(a, s2, "GetTensorElementType");
+            const void* s = nullptr;
+            void* d = nullptr;
+            check_ort(a, api::GetTensorData(a)(src[i], &s), "GetTensorData");
+            check_ort(a, api::GetTensorMutableData(a)(dst[i], &d), "GetTensorMutableData");
+            const size_t bytes = count * dtype_size(et);
+            if (bytes) check_hip(hipMemcpy(d, s, bytes, hipMemcpyDefault), "hipMemcpy");
+        }
+    });
+}
+
+// -------------------------------------------------------- compute info --
+struct ComputeInfo {
+    OrtNodeComputeInfo base;
+    const OrtApi* api;
+    std::unique_ptr<Plan> plan;
+    std::string name;
+};
+
+OrtStatus* ci_create_state(OrtNodeComputeInfo* self, OrtNodeComputeContext*, void** state) {
+    // The plan is the state (rust/src/ep.rs:1918-1927).
+    *state = self;
+    return nullptr;
+}
+OrtStatus* ci_compute(OrtNodeComputeInfo* self, void* state, OrtKernelContext* ctx) {
+    auto* ci = reinterpret_cast<ComputeInfo*>(state ? state : self);
+    return guard(ci->api, "Compute", [&] { ci->plan->compute(ci->api, ctx); });
+}
+void ci_release_state(OrtNodeComputeInfo*, void*) {}
+
+// --------------------------------------------------------------------- EP --
+struct Factory;
+
+struct Ep {
+    OrtEp base;
+    Factory* factory;
+    const OrtApi* api;
+    const OrtEpApi* ep_api;
+    std::string name;
+    int device = 0;
+};
+
+struct Factory {
+    OrtEpFactory base;
+    const OrtApi* api;
+    const OrtEpApi* ep_api;
+    std::string name, vendor, version;
+};
+
+const char* ep_get_name(const OrtEp* self) { return reinterpret_cast<const Ep*>(self)->name.c_str(); }
+
+OrtStatus* ep_get_capability(OrtEp* self, const OrtGraph* graph, OrtEpGraphSupportInfo* support) {
+    Ep* ep = reinterpret_cast<Ep*>(self);
+    return guard(ep->api, "GetCapability", [&] {
+        GraphIR g = read_graph(ep->api, graph);
+        std::vector<bool> claimed(g.nodes.size(), false);
+        const bool debug = env_flag("ORTMI_EP_CLAIM_DEBUG");
+        for (size_t i = 0; i < g.nodes.size(); ++i) {
+            std::string why = claim_reason(g.nodes[i], g);
+            claimed[i] = why.empty();
+            if (debug && !why.empty())
+                std::fprintf(stderr, "[mi355x-ep] decline %s (%s): %s\n", g.nodes[i].name.c_str(),
+                             g.nodes[i].op.c_str(), why.c_str());
+        }
+        for (const auto& cl : build_clusters(g, claimed)) {
+            std::vector<const OrtNode*> nodes;
+            for (size_t i : cl) nodes.push_back(g.nodes[i].handle);
+            OrtNodeFusionOptions opts{ORT_API_VERSION, true};
+            check_ort(ep->api,
+                      ep_api::EpGraphSupportInfo_AddNodesToFuse(ep->ep_api)(support, nodes.data(),
+                                                                            nodes.size(), &opts),
+                      "EpGraphSupportInfo_AddNodesToFuse");
+        }
+    });
+}
+
+OrtStatus* ep_compile(OrtEp* self, const OrtGraph** graphs, const OrtNode** fused_nodes,
+                      size_t count, OrtNodeComputeInfo** infos, OrtNode** ep_context_nodes) {
+    Ep* ep = reinterpret_cast<Ep*>(self);
+    (void)ep_context_nodes;  // no EPContext serialisation (rust/src/ep.rs:957)
+    for (size_t i = 0; i < count; ++i) infos[i] = nullptr;
+    return guard(ep->api, "Compile", [&] {
+        for (size_t i = 0; i < count; ++i) {
+            const OrtApi* a = ep->api;
+            GraphIR sub = read_graph(a, graphs[i]);
+            // Kernel-context order = the fused node's input / output order.
+            auto names = [&](auto count_fn, auto get_fn) {
+                size_t n = 0;
+                check_ort(a, count_fn(a)(fused_nodes[i], &n), "fused node io");
+                std::vector<const OrtValueInfo*> vis(n);
+                if (n) check_ort(a, get_fn(a)(fused_nodes[i], vis.data(), n), "fused node io");
+                std::vector<std::string> out;
+                for (auto* vi : vis) {
+                    const char* nm = nullptr;
+                    if (vi) check_ort(a, api::GetValueInfoName(a)(vi, &nm), "GetValueInfoName");
+                    out.push_back(nm ? nm : "");
+                }
+                return out;
+            };
+            auto ins = names(api::Node_GetNumInputs, api::Node_GetInputs);
+            auto outs = names(api::Node_GetNumOutputs, api::Node_GetOutputs);
+            auto ci = new ComputeInfo();
+            ci->base.ort_version_supported = ORT_API_VERSION;
+            ci->base.CreateState = ci_create_state;
+            ci->base.Compute = ci_compute;
+            ci->base.ReleaseState = ci_release_state;
+            ci->api = a;
+            try {
+                ci->plan = std::make_unique<Plan>(std::move(sub), ins, outs, ep->device);
+            } catch (...) {
+                delete ci;
+                for (size_t j = 0; j < i; ++j) {
+                    delete reinterpret_cast<ComputeInfo*>(infos[j]);
+                    infos[j] = nullptr;
+                }
+                throw;
+            }
+            infos[i] = &ci->base;
+        }
+    });
+}
+
+void ep_release_infos(OrtEp*, OrtNodeComputeInfo** infos, size_t n) {
+    for (size_t i = 0; i < n; ++i) delete reinterpret_cast<ComputeInfo*>(infos[i]);
+}
+
+const OrtMemoryDevice* ep_default_memory_device(const OrtEp*) {
+    return nullptr;  // CPU memory, as the reference (rust/src/ep.rs:104-113); inputs
+                     // already in HBM are used in place, host ones are staged.
+}
+
+// ---------------------------------------------------------------- factory --
+Factory* F(const OrtEpFactory* p) { return reinterpret_cast<Factory*>(const_cast<OrtEpFactory*>(p)); }
+
+const char* f_name(const OrtEpFactory* p) { return F(p)->name.c_str(); }
+const char* f_vendor(const OrtEpFactory* p) { return F(p)->vendor.c_str(); }
+uint32_t f_vendor_id(const OrtEpFactory*) { return kVendorIdAmd; }
+const char* f_version(const OrtEpFactory* p) { return F(p)->version.c_str(); }
+bool f_stream_aware(const OrtEpFactory*) { return false; }
+
+OrtStatus* f_supported_devices(OrtEpFactory* p, const OrtHardwareDevice* const* devices,
+                               size_t num_devices, OrtEpDevice** ep_devices, size_t max_ep_devices,
+                               size_t* num_ep_devices) {
+    Factory* f = F(p);
+    return guard(f->api, "GetSupportedDevices", [&] {
+        *num_ep_devices = 0;
+        int hip_devices = 0;
+        if (hipGetDeviceCount(&hip_devices) != hipSuccess) {
+            (void)hipGetLastError();
+            hip_devices = 0;
+        }
+        if (hip_devices <= 0 || max_ep_devices < 1) return;  // nothing to offer
+        // First GPU hardware device (rust/src/factory.rs:116-164).
+        const OrtHardwareDevice* gpu = nullptr;
+        for (size_t i = 0; i < num_devices && !gpu; ++i)
+            if (api::HardwareDevice_Type(f->api)(devices[i]) == OrtHardwareDeviceType_GPU)
+                gpu = devices[i];
+        if (!gpu) return;
+        OrtEpDevice* d = nullptr;
+        check_ort(f->api, ep_api::CreateEpDevice(f->ep_api)(p, gpu, nullptr, nullptr, &d),
+                  "CreateEpDevice");
+        ep_devices[0] = d;
+        *num_ep_devices = 1;
+    });
+}
+
+OrtStatus* f_create_ep(OrtEpFactory* p, const OrtHardwareDevice* const*,
+                       const OrtKeyValuePairs* const*, size_t num_devices,
+                       const OrtSessionOptions*, const OrtLogger*, OrtEp** out) {
+    Factory* f = F(p);
+    *out = nullptr;
+    return guard(f->api, "CreateEp", [&] {
+        if (num_devices != 1)
+            fail("MI355XExecutionProvider expects exactly one device", ORT_INVALID_ARGUMENT);
+        auto* ep = new Ep();
+        std::memset(&ep->base, 0, sizeof(ep->base));
+        ep->base.ort_version_supported = ORT_API_VERSION;
+        ep->base.GetName = ep_get_name;
+        ep->base.GetCapability = ep_get_capability;
+        ep->base.Compile = ep_compile;
+        ep->base.ReleaseNodeComputeInfos = ep_release_infos;
+        ep->base.GetDefaultMemoryDevice = ep_default_memory_device;
+        ep->factory = f;
+        ep->api = f->api;
+        ep->ep_api = f->ep_api;
+        ep->name = f->name;
+        ep->device = 0;
+        *out = &ep->base;
+    });
+}
+
+void f_release_ep(OrtEpFactory*, OrtEp* ep) { delete reinterpret_cast<Ep*>(ep); }
+
+OrtStatus* f_create_allocator(OrtEpFactory* p, const OrtMemoryInfo* info, const OrtKeyValuePairs*,
+                              OrtAllocator** out) {
+    Factory* f = F(p);
+    return guard(f->api, "CreateAllocator", [&] {
+        auto* a = new DeviceAllocator();
+        std::memset(&a->base, 0, sizeof(a->base));
+        a->base.version = ORT_API_VERSION;
+        a->base.Alloc = alloc_fn;
+        a->base.Free = free_fn;
+        a->base.Info = info_fn;
+        a->base.Reserve = reserve_fn;
+        a->base.AllocOnStream = alloc_on_stream_fn;
+        a->info = info;
+        a->device = 0;
+        *out = &a->base;
+    });
+}
+void f_release_allocator(OrtEpFactory*, OrtAllocator* a) {
+    delete reinterpret_cast<DeviceAllocator*>(a);
+}
+OrtStatus* f_create_data_transfer(OrtEpFactory* p, OrtDataTransferImpl** out) {
+    Factory* f = F(p);
+    return guard(f->api, "CreateDataTransfer", [&] {
+        auto* t = new DataTransfer();
+        t->base.ort_version_supported = ORT_API_VERSION;
+        t->base.Release = dt_release;
+        t->base.CanCopy = dt_can_copy;
+        t->base.CopyTensors = dt_copy;
+        t->api = f->api;
+        *out = &t->base;
+    });
+}
+OrtStatus* f_create_stream(OrtEpFactory*, const OrtMemoryDevice*, const OrtKeyValuePairs*,
+                           OrtSyncStreamImpl** out) {
+    *out = nullptr;  // not stream aware
+    return nullptr;
+}
+
+}  // namespace
+}  // namespace ortmi_ep
+
+using namespace ortmi_ep;
+
+// Entry point resolved by ORT through dlsym (rust/src/lib.rs:90-155).
+ORTMI_EXPORT OrtStatus* CreateEpFactories(const char* registration_name,
+                                          const OrtApiBase* ort_api_base,
+                                          const OrtLogger* default_logger,
+                                          OrtEpFactory** factories, size_t max_factories,
+                                          size_t* num_factories) {
+    (void)default_logger;
+    if (num_factories) *num_factories = 0;
+    // Without an API base no status can be created: report zero factories.
+    if (!ort_api_base || !ort_api_base->GetApi) return nullptr;
+    const OrtApi* a = ort_api_base->GetApi(ORT_API_VERSION);
+    if (!a) {
+        const OrtApi* legacy = ort_api_base->GetApi(1);
+        if (!legacy) return nullptr;
+        return api::CreateStatus(legacy)(
+            ORT_INVALID_ARGUMENT, "MI355XExecutionProvider requires ONNX Runtime with ORT_API_VERSION >= 29");
+    }
+    return guard(a, "CreateEpFactories", [&] {
+        if (!factories || !num_factories) fail("null output arguments", ORT_INVALID_ARGUMENT);
+        *num_factories = 0;
+        if (max_factories < 1)
+            fail("MI355XExecutionProvider needs room for one OrtEpFactory", ORT_INVALID_ARGUMENT);
+        auto* f = new Factory();
+        std::memset(&f->base, 0, sizeof(f->base));
+        f->api = a;
+        f->ep_api = api::GetEpApi(a)();
+        f->name = (registration_name && *registration_name) ? registration_name : kDefaultName;
+        f->vendor = "AMD";
+        f->version = kVersion;
+        OrtEpFactory& b = f->base;
+        b.ort_version_supported = ORT_API_VERSION;
+        b.GetName = f_name;
+        b.GetVendor = f_vendor;
+        b.GetVendorId = f_vendor_id;
+        b.GetVersion = f_version;
+        b.GetSupportedDevices = f_supported_devices;
+        b.CreateEp = f_create_ep;
+        b.ReleaseEp = f_release_ep;
+        b.CreateAllocator = f_create_allocator;
+        b.ReleaseAllocator = f_release_allocator;
+        b.CreateDataTransfer = f_create_data_transfer;
+        b.IsStreamAware = f_stream_aware;
+        b.CreateSyncStreamForDevice = f_create_stream;
+        factories[0] = &f->base;
+        *num_factories = 1;
+    });
+}
+
+// rust/src/lib.rs:161-167
+ORTMI_EXPORT OrtStatus* ReleaseEpFactory(OrtEpFactory* factory) {
+    delete reinterpret_cast<Factory*>(factory);
+    return nullptr;
+}

@@ -1,0 +1,157 @@
+// Internal declarations of the MI355X plugin execution provider.
+//
+// Layering (reference counterparts in parentheses):
+//   ep.cpp     C-ABI entry points, factory / EP / node-compute-info vtables,
+//              hipMalloc allocator and data transfer (rust/src/lib.rs,
+//              rust/src/factory.rs, rust/src/ep.rs:48-113, 1878-2171)
+//   graph.cpp  reading an OrtGraph into an owned IR, claim predicates and
+//              convex clustering (rust/src/registry.rs, rust/src/ep.rs:119-895)
+//   plan.cpp   per-fused-node plan: initializers copied to HBM once, topological
+//              op list, shape inference and kernel launches at Compute
+//              (rust/src/ep.rs:928-1298, rust/src/engine.rs)
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../../include/ort_plugin_ep_abi.h"
+
+namespace ortmi_ep {
+
+// ------------------------------------------------------------------ errors --
+struct EpError : std::runtime_error {
+    OrtErrorCode code;
+    EpError(OrtErrorCode c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+[[noreturn]] inline void fail(const std::string& msg, OrtErrorCode c = ORT_EP_FAIL) {
+    throw EpError(c, msg);
+}
+// Throw on a non-null OrtStatus returned by the host, releasing it first.
+void check_ort(const OrtApi* api, OrtStatus* st, const char* what);
+void check_hip(hipError_t e, const char* what);
+void check_kernel(int rc, const char* what);
+
+// ---------------------------------------------------------------------- IR --
+struct Attr {
+    OrtOpAttrType type = ORT_OP_ATTR_UNDEFINED;
+    int64_t i = 0;
+    float f = 0.f;
+    std::string s;
+    std::vector<int64_t> ints;
+    std::vector<float> floats;
+};
+
+struct ValueDesc {
+    std::string name;
+    int dtype = 0;                 // ONNXTensorElementDataType
+    std::vector<int64_t> dims;     // -1 for symbolic
+    bool has_shape = false;
+    bool is_initializer = false;
+    std::vector<uint8_t> data;     // initializer bytes (copied at read time)
+};
+
+struct NodeDesc {
+    size_t id = 0;
+    std::string name, op, domain;
+    int since_version = 0;
+    std::vector<std::string> inputs;   // "" = absent optional input
+    std::vector<std::string> outputs;  // "" = absent optional output
+    std::map<std::string, Attr> attrs;
+    const OrtNode* handle = nullptr;   // valid during GetCapability / Compile only
+
+    int64_t attr_int(const char* k, int64_t dflt) const {
+        auto it = attrs.find(k);
+        return it == attrs.end() ? dflt : it->second.i;
+    }
+    float attr_float(const char* k, float dflt) const {
+        auto it = attrs.find(k);
+        return it == attrs.end() ? dflt : it->second.f;
+    }
+    std::string attr_str(const char* k, const std::string& dflt) const {
+        auto it = attrs.find(k);
+        return it == attrs.end() ? dflt : it->second.s;
+    }
+    bool has_input(size_t i) const { return i < inputs.size() && !inputs[i].empty(); }
+};
+
+struct GraphIR {
+    std::vector<NodeDesc> nodes;                 // graph order
+    std::map<std::string, ValueDesc> values;     // every named value seen
+    std::vector<std::string> inputs, outputs;    // graph inputs / outputs
+};
+
+// Read a whole OrtGraph (nodes, value infos, initializer bytes, attributes).
+GraphIR read_graph(const OrtApi* api, const OrtGraph* graph);
+
+// ------------------------------------------------------------- op registry --
+// Claim predicate: returns "" when the node is supported, else the reason.
+using ClaimFn = std::string (*)(const NodeDesc&, const GraphIR&);
+ClaimFn find_claim(const std::string& domain, const std::string& op);
+std::string claim_reason(const NodeDesc& n, const GraphIR& g);  // "" = claimed
+
+// Partition the claimed nodes into convex, acyclic clusters (each becomes one
+// fused node). Returns node indices (into g.nodes) per cluster, topologically
+// ordered inside each cluster.
+std::vector<std::vector<size_t>> build_clusters(const GraphIR& g, const std::vector<bool>& claimed);
+
+// ------------------------------------------------------------------- plan --
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    ~DeviceBuffer();
+};
+
+// Compiled form of one fused node.
+class Plan {
+   public:
+    Plan(GraphIR sub, std::vector<std::string> inputs, std::vector<std::string> outputs,
+         int device);
+    ~Plan();
+    // Run with the fused node's kernel context.
+    void compute(const OrtApi* api, OrtKernelContext* ctx);
+    const std::vector<std::string>& input_names() const { return inputs_; }
+    const std::vector<std::string>& output_names() const { return outputs_; }
+
+   private:
+    struct Tensor {
+        void* ptr = nullptr;
+        int dtype = 0;
+        std::vector<int64_t> dims;
+        int64_t numel() const {
+            int64_t n = 1;
+            for (auto d : dims) n *= d;
+            return n;
+        }
+    };
+    void* arena_alloc(size_t bytes);
+    Tensor& out_tensor(const std::string& name, int dtype, const std::vector<int64_t>& dims,
+                       const OrtApi* api, OrtKernelContext* ctx);
+    void run_node(const NodeDesc& n, const OrtApi* api, OrtKernelContext* ctx);
+    int32_t host_i32(const std::string& name);
+
+    GraphIR sub_;
+    std::vector<std::string> inputs_, outputs_;
+    std::map<std::string, int> output_index_;
+    std::map<std::string, std::unique_ptr<DeviceBuffer>> constants_;  // initializers in HBM
+    std::map<std::string, Tensor> env_;                               // values of this run
+    std::map<std::string, int32_t> host_scalars_;
+    int device_ = 0;
+    hipStream_t stream_ = nullptr;
+    // Bump arena for intermediates, reset per Compute and grown on demand.
+    std::vector<std::unique_ptr<DeviceBuffer>> arena_;
+    size_t arena_off_ = 0;
+    size_t arena_need_ = 0;
+    std::unique_ptr<DeviceBuffer> workspace_;
+    std::mutex mu_;  // one Compute at a time per fused node (rust/src/ep.rs:1884-1889)
+};
+
+size_t dtype_size(int dtype);
+
+}  // namespace ortmi_ep

@@ -1,0 +1,499 @@
+// Per-fused-node plan of the MI355X EP: constants in HBM, one HIP stream, shape
+// inference and kernel launches at Compute.
+#include <cstdlib>
+#include <cstring>
+
+#include "../../../include/ortmi_kernels.h"
+#include "ep_internal.h"
+
+namespace ortmi_ep {
+
+using namespace ort_abi;
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) fail(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void check_kernel(int rc, const char* what) {
+    if (rc != 0) fail(std::string(what) + ": " + ortmi_last_error());
+}
+
+DeviceBuffer::~DeviceBuffer() {
+    if (ptr) (void)hipFree(ptr);
+}
+
+static std::unique_ptr<DeviceBuffer> device_alloc(size_t bytes) {
+    auto b = std::make_unique<DeviceBuffer>();
+    b->bytes = bytes;
+    if (bytes) check_hip(hipMalloc(&b->ptr, bytes), "hipMalloc");
+    return b;
+}
+
+// True when `p` is device memory this process can hand to a kernel.
+static bool is_device_ptr(const void* p) {
+    if (!p) return true;
+    hipPointerAttribute_t attr;
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+// SiLU-gated MLP: Sigmoid(g) -> Mul(g, sig) -> Mul(., u) becomes one SwiGLU node
+// when the two intermediates feed nothing else and are not fused-node outputs.
+static void fuse_swiglu(GraphIR& g, const std::vector<std::string>& outputs) {
+    std::map<std::string, int> uses;
+    for (const auto& n : g.nodes)
+        for (const auto& in : n.inputs)
+            if (!in.empty()) uses[in]++;
+    for (const auto& o : outputs) uses[o] += 1000;  // fused outputs stay materialised
+    auto other = [](const NodeDesc& m, const std::string& x) -> std::string {
+        if (m.inputs.size() != 2) return "";
+        if (m.inputs[0] == x) return m.inputs[1];
+        if (m.inputs[1] == x) return m.inputs[0];
+        return "";
+    };
+    std::vector<bool> dead(g.nodes.size(), false);
+    for (size_t i = 0; i < g.nodes.size(); ++i) {
+        const NodeDesc& sg = g.nodes[i];
+        if (sg.op != "Sigmoid" || sg.domain != "" || sg.outputs.empty()) continue;
+        const std::string x = sg.inputs[0], s = sg.outputs[0];
+        if (uses[s] != 1) continue;
+        for (size_t j = 0; j < g.nodes.size(); ++j) {
+            NodeDesc& m1 = g.nodes[j];
+            if (dead[j] || m1.op != "Mul" || other(m1, s) != x || m1.outputs.empty()) continue;
+            const std::string t = m1.outputs[0];
+            if (uses[t] != 1) break;
+            for (size_t k = 0; k < g.nodes.size(); ++k) {
+                NodeDesc& m2 = g.nodes[k];
+                if (dead[k] || m2.op != "Mul") continue;
+                const std::string u = other(m2, t);
+                if (u.empty() || u == t) continue;
+                const auto vx = g.values.find(x), vu = g.values.find(u);
+                if (vx == g.values.end() || vu == g.values.end() ||
+                    vx->second.dims != vu->second.dims)
+                    break;
+                m2.op = "SwiGLU";
+                m2.inputs = {x, u};
+                dead[i] = dead[j] = true;
+                break;
+            }
+            break;
+        }
+    }
+    std::vector<NodeDesc> kept;
+    for (size_t i = 0; i < g.nodes.size(); ++i)
+        if (!dead[i]) kept.push_back(std::move(g.nodes[i]));
+    g.nodes = std::move(kept);
+}
+
+Plan::Plan(GraphIR sub, std::vector<std::string> inputs, std::vector<std::string> outputs,
+           int device)
+    : sub_(std::move(sub)), inputs_(std::move(inputs)), outputs_(std::move(outputs)),
+      device_(device) {
+    fuse_swiglu(sub_, outputs_);
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    check_hip(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
+    for (size_t i = 0; i < outputs_.size(); ++i)
+        if (!outputs_[i].empty()) output_index_[outputs_[i]] = (int)i;
+    // Constant initializers are copied to HBM once (the reference keeps a plan-owned
+    // constant cache, rust/src/engine.rs:409-411).
+    for (auto& kv : sub_.values) {
+        ValueDesc& v = kv.second;
+        if (!v.is_initializer) continue;
+        auto buf = device_alloc(v.data.size());
+        if (!v.data.empty())
+            check_hip(hipMemcpy(buf->ptr, v.data.data(), v.data.size(), hipMemcpyHostToDevice),
+                      "upload initializer");
+        constants_[kv.first] = std::move(buf);
+        std::vector<uint8_t>().swap(v.data);
+    }
+}
+
+Plan::~Plan() {
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void* Plan::arena_alloc(size_t bytes) {
+    bytes = (bytes + 255) & ~(size_t)255;
+    // Chunks are kept across runs; offsets restart at every Compute.
+    size_t off = arena_off_;
+    size_t base = 0;
+    for (auto& ch : arena_) {
+        if (off < base + ch->bytes) {
+            size_t local = off - base;
+            if (local + bytes <= ch->bytes) {
+                arena_off_ = off + bytes;
+                return static_cast<char*>(ch->ptr) + local;
+            }
+            off = base + ch->bytes;  // skip the chunk's tail
+        }
+        base += ch->bytes;
+    }
+    size_t grow = std::max(bytes, (size_t)64 << 20);
+    arena_.push_back(device_alloc(grow));
+    arena_off_ = base + bytes;
+    return arena_.back()->ptr;
+}
+
+int32_t Plan::host_i32(const std::string& name) {
+    auto hs = host_scalars_.find(name);
+    if (hs != host_scalars_.end()) return hs->second;
+    auto it = env_.find(name);
+    if (it == env_.end()) fail("missing scalar input " + name);
+    int32_t v = 0;
+    if (is_device_ptr(it->second.ptr)) {
+        check_hip(hipMemcpyAsync(&v, it->second.ptr, 4, hipMemcpyDeviceToHost, stream_), "read scalar");
+        check_hip(hipStreamSynchronize(stream_), "read scalar");
+    } else {
+        std::memcpy(&v, it->second.ptr, 4);
+    }
+    host_scalars_[name] = v;
+    return v;
+}
+
+namespace {
+struct Staged {
+    void* host;
+    void* dev;
+    size_t bytes;
+};
+thread_local std::vector<Staged>* g_out_staging = nullptr;
+}  // namespace
+
+Plan::Tensor& Plan::out_tensor(const std::string& name, int dtype,
+                               const std::vector<int64_t>& dims, const OrtApi* a,
+                               OrtKernelContext* ctx) {
+    Tensor t;
+    t.dtype = dtype;
+    t.dims = dims;
+    const size_t bytes = (size_t)std::max<int64_t>(t.numel(), 0) * dtype_size(dtype);
+    auto oi = output_index_.find(name);
+    if (oi != output_index_.end()) {
+        OrtValue* ov = nullptr;
+        check_ort(a, api::KernelContext_GetOutput(a)(ctx, (size_t)oi->second, dims.data(),
+                                                     dims.size(), &ov),
+                  "KernelContext_GetOutput");
+        void* p = nullptr;
+        check_ort(a, api::GetTensorMutableData(a)(ov, &p), "GetTensorMutableData");
+        if (bytes && !is_device_ptr(p)) {
+            void* d = arena_alloc(bytes);
+            g_out_staging->push_back({p, d, bytes});
+            p = d;
+        }
+        t.ptr = p;
+    } else {
+        t.ptr = bytes ? arena_alloc(bytes) : nullptr;
+    }
+    env_[name] = t;
+    return env_[name];
+}
+
+void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
+    std::lock_guard<std::mutex> lock(mu_);
+    check_hip(hipSetDevice(device_), "hipSetDevice");
+    env_.clear();
+    host_scalars_.clear();
+    arena_off_ = 0;
+    std::vector<Staged> out_staging;
+    g_out_staging = &out_staging;
+    for (size_t i = 0; i < inputs_.size(); ++i) {
+        if (inputs_[i].empty()) continue;
+        const OrtValue* v = nullptr;
+        check_ort(a, api::KernelContext_GetInput(a)(ctx, i, &v), "KernelContext_GetInput");
+        if (!v) continue;
+        OrtTensorTypeAndShapeInfo* info = nullptr;
+        check_ort(a, api::GetTensorTypeAndShape(a)(v, &info), "GetTensorTypeAndShape");
+        ONNXTensorElementDataType et = ONNX_TENSOR_ELEMENT_DATA_TYPE_UNDEFINED;
+        size_t nd = 0;
+        OrtStatus* s1 = api::GetTensorElementType(a)(info, &et);
+        OrtStatus* s2 = s1 ? nullptr : api::GetDimensionsCount(a)(info, &nd);
+        Tensor t;
+        t.dtype = et;
+        t.dims.resize(nd);
+        OrtStatus* s3 = (s1 || s2 || !nd) ? nullptr : api::GetDimensions(a)(info, t.dims.data(), nd);
+        api::ReleaseTensorTypeAndShapeInfo(a)(info);
+        check_ort(a, s1, "GetTensorElementType");
+        check_ort(a, s2, "GetDimensionsCount");
+        check_ort(a, s3, "GetDimensions");
+        const void* p = nullptr;
+        check_ort(a, api::GetTensorData(a)(v, &p), "GetTensorData");
+        const size_t bytes = (size_t)std::max<int64_t>(t.numel(), 0) * dtype_size(et);
+        if (bytes && !is_device_ptr(p)) {
+            // Host-memory input: stage it into HBM (the boundary copy that a GPU
+            // memory device would make unnecessary).
+            void* d = arena_alloc(bytes);
+            check_hip(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, stream_), "stage input");
+            host_scalars_.erase(inputs_[i]);
+            t.ptr = d;
+            // keep the host copy for scalar reads without a device round trip
+            if (bytes == 4) {
+                int32_t hv;
+                std::memcpy(&hv, p, 4);
+                host_scalars_[inputs_[i]] = hv;
+            }
+        } else {
+            t.ptr = const_cast<void*>(p);
+        }
+        env_[inputs_[i]] = t;
+    }
+    for (auto& kv : constants_) {
+        const ValueDesc& v = sub_.values.at(kv.first);
+        Tensor t;
+        t.ptr = kv.second->ptr;
+        t.dtype = v.dtype;
+        t.dims = v.dims;
+        env_[kv.first] = t;
+    }
+    for (const NodeDesc& n : sub_.nodes) run_node(n, a, ctx);
+    for (const Staged& s : out_staging)
+        check_hip(hipMemcpyAsync(s.host, s.dev, s.bytes, hipMemcpyDeviceToHost, stream_),
+                  "stage output");
+    check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+    g_out_staging = nullptr;
+}
+
+// ------------------------------------------------------------ op dispatch --
+
+static int32_t kdt(int onnx_dtype) {
+    switch (onnx_dtype) {
+        case ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT: return ORTMI_F32;
+        case ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16: return ORTMI_F16;
+        case ONNX_TENSOR_ELEMENT_DATA_TYPE_BFLOAT16: return ORTMI_BF16;
+        default: fail("unsupported element type", ORT_INVALID_ARGUMENT);
+    }
+}
+
+void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
+    auto in = [&](size_t i) -> Tensor* {
+        if (!n.has_input(i)) return nullptr;
+        auto it = env_.find(n.inputs[i]);
+        if (it == env_.end()) fail(n.op + ": input " + n.inputs[i] + " is not available");
+        return &it->second;
+    };
+    auto need = [&](size_t i) -> Tensor& {
+        Tensor* t = in(i);
+        if (!t) fail(n.op + ": missing input " + std::to_string(i), ORT_INVALID_ARGUMENT);
+        return *t;
+    };
+    auto outname = [&](size_t i) -> std::string {
+        return i < n.outputs.size() ? n.outputs[i] : std::string();
+    };
+    void* st = stream_;
+    const std::string& op = n.op;
+
+    if (op == "MatMulNBits") {
+        Tensor& A = need(0);
+        Tensor& B = need(1);
+        Tensor& S = need(2);
+        Tensor* Z = in(3);
+        const int64_t K = n.attr_int("K", 0), N = n.attr_int("N", 0);
+        if (A.dims.empty() || A.dims.back() != K) fail("MatMulNBits: A's last dim != K", ORT_INVALID_ARGUMENT);
+        std::vector<int64_t> od = A.dims;
+        od.back() = N;
+        const int dtype = A.dtype;
+        const int64_t M = A.numel() / K;
+        void *ap = A.ptr, *bp = B.ptr, *sp = S.ptr, *zp = Z ? Z->ptr : nullptr;
+        Tensor& Y = out_tensor(outname(0), dtype, od, a, ctx);
+        check_kernel(ortmi_matmul_nbits(ap, (const uint8_t*)bp, sp, (const uint8_t*)zp, Y.ptr, M,
+                                        N, K, n.attr_int("bits", 4), n.attr_int("block_size", 32),
+                                        kdt(dtype), st),
+                     "MatMulNBits");
+        return;
+    }
+    if (op == "GroupQueryAttention") {
+        Tensor q = need(0);
+        Tensor* kp = in(1);
+        Tensor* vp = in(2);
+        Tensor* pk = in(3);
+        Tensor* pv = in(4);
+        const int32_t total = host_i32(n.inputs[6]);
+        const int64_t H = n.attr_int("num_heads", 0), KV = n.attr_int("kv_num_heads", 0);
+        const int64_t B = q.dims[0], S = q.dims[1];
+        const bool packed = kp == nullptr;
+        const int64_t hd = packed ? q.dims[2] / (H + 2 * KV) : q.dims[2] / H;
+        const int64_t cap = pk ? pk->dims[2] : 0;
+        int64_t vpast = total - S;
+        bool shared;
+        if (vpast < 0 || vpast > cap) {
+            shared = false;
+            vpast = cap;
+        } else {
+            shared = cap > vpast;
+        }
+        const int64_t pcap = shared ? cap : cap + S;
+        const bool rotary = n.attr_int("do_rotary", 0) != 0;
+        Tensor* cs = rotary ? in(7) : nullptr;
+        Tensor* sn = rotary ? in(8) : nullptr;
+        void* kptr = kp ? kp->ptr : nullptr;
+        void* vptr = vp ? vp->ptr : nullptr;
+        void* pkp = pk ? pk->ptr : nullptr;
+        void* pvp = pv ? pv->ptr : nullptr;
+        void* csp = cs ? cs->ptr : nullptr;
+        void* snp = sn ? sn->ptr : nullptr;
+        const int64_t half = cs ? cs->dims[1] : 0, max_pos = cs ? cs->dims[0] : 0;
+        Tensor& O = out_tensor(outname(0), q.dtype, {B, S, H * hd}, a, ctx);
+        void* optr = O.ptr;
+        void *prk, *prv;
+        if (!outname(1).empty()) prk = out_tensor(outname(1), q.dtype, {B, KV, pcap, hd}, a, ctx).ptr;
+        else prk = arena_alloc((size_t)(B * KV * pcap * hd) * dtype_size(q.dtype));
+        if (!outname(2).empty()) prv = out_tensor(outname(2), q.dtype, {B, KV, pcap, hd}, a, ctx).ptr;
+        else prv = arena_alloc((size_t)(B * KV * pcap * hd) * dtype_size(q.dtype));
+        const size_t wsb = ortmi_group_query_attention_workspace_size(B, S, H, hd, vpast + S);
+        if (!workspace_ || workspace_->bytes < wsb) workspace_ = device_alloc(wsb);
+        check_kernel(ortmi_group_query_attention(
+                         q.ptr, kptr, vptr, pkp, pvp, cap, total, csp, snp, half, max_pos, optr, prk,
+                         prv, B, S, H, KV, hd, n.attr_float("scale", 0.f),
+                         (int32_t)n.attr_int("rotary_interleaved", 0), kdt(q.dtype),
+                         workspace_->ptr, workspace_->bytes, st),
+                     "GroupQueryAttention");
+        return;
+    }
+    if (op == "PagedAttention") {
+        Tensor q = need(0);
+        Tensor k = need(1);
+        Tensor* v = in(2);
+        Tensor kc = need(3);
+        Tensor* vc = in(4);
+        Tensor cum = need(5), past = need(6), bt = need(7);
+        const bool latent = n.attr_str("kv_cache_layout", "SEPARATE") == "LATENT";
+        const bool rotary = n.attr_int("do_rotary", 0) != 0;
+        Tensor* cs = rotary ? in(8) : nullptr;
+        Tensor* sn = rotary ? in(9) : nullptr;
+        Tensor* sm = in(10);
+        Tensor* sink = in(11);
+        Tensor* qw = in(12);
+        Tensor* kw = in(13);
+        const int64_t H = n.attr_int("num_heads", 0), KV = n.attr_int("kv_num_heads", 0);
+        const int64_t T = q.dims[0], nblk = kc.dims[0], blk = kc.dims[1], hd = kc.dims[3];
+        const int64_t vhd = n.attr_int("v_head_size", 0) ? n.attr_int("v_head_size", 0) : hd;
+        const int64_t batch = cum.dims[0] - 1, maxb = bt.dims.size() == 2 ? bt.dims[1] : 0;
+        const int64_t max_ctx = maxb * blk;
+        Tensor& O = out_tensor(outname(0), q.dtype, {T, H * vhd}, a, ctx);
+        const size_t wsb = ortmi_paged_attention_workspace_size(T, batch, H, KV, hd, vhd, max_ctx);
+        if (!workspace_ || workspace_->bytes < wsb) workspace_ = device_alloc(wsb);
+        check_kernel(ortmi_paged_attention(
+                         q.ptr, k.ptr, latent ? nullptr : (v ? v->ptr : nullptr), kc.ptr,
+                         latent ? nullptr : (vc ? vc->ptr : nullptr), nblk, blk,
+                         (const int32_t*)cum.ptr, (const int32_t*)past.ptr, (const int32_t*)bt.ptr,
+                         batch, maxb, T, max_ctx, cs ? cs->ptr : nullptr, sn ? sn->ptr : nullptr,
+                         cs ? cs->dims[1] : 0, cs ? cs->dims[0] : 0,
+                         (int32_t)n.attr_int("rotary_interleaved", 0), n.attr_int("rotary_offset", 0),
+                         sm ? (const int32_t*)sm->ptr : nullptr, sink ? sink->ptr : nullptr,
+                         qw ? qw->ptr : nullptr, kw ? kw->ptr : nullptr,
+                         n.attr_float("qk_norm_epsilon", 1e-6f), O.ptr, H, KV, hd, vhd,
+                         n.attr_float("scale", 0.f), kdt(q.dtype), workspace_->ptr,
+                         workspace_->bytes, st),
+                     "PagedAttention");
+        // Updated caches: written in place (rust/src/engine.rs:823-847); outputs 1/2,
+        // when requested, receive the same contents.
+        const Tensor* caches[2] = {&kc, vc};
+        for (int i = 0; i < 2; ++i) {
+            if (outname(1 + i).empty() || !caches[i]) continue;
+            Tensor& oc = out_tensor(outname(1 + i), caches[i]->dtype, caches[i]->dims, a, ctx);
+            if (oc.ptr != caches[i]->ptr)
+                check_hip(hipMemcpyAsync(oc.ptr, caches[i]->ptr,
+                                         (size_t)caches[i]->numel() * dtype_size(caches[i]->dtype),
+                                         hipMemcpyDeviceToDevice, stream_),
+                          "cache output");
+        }
+        return;
+    }
+    if (op == "RotaryEmbedding") {
+        const bool ms = n.domain == "com.microsoft";
+        Tensor x = need(0);
+        Tensor* pos = ms ? in(1) : in(3);
+        Tensor cs = need(ms ? 2 : 1), sn = need(ms ? 3 : 2);
+        const bool bnsd = x.dims.size() == 4;
+        int64_t B, S, NH, hd;
+        if (bnsd) {
+            B = x.dims[0];
+            NH = x.dims[1];
+            S = x.dims[2];
+            hd = x.dims[3];
+        } else {
+            B = x.dims[0];
+            S = x.dims[1];
+            const int64_t nh_attr = n.attr_int("num_heads", 0);
+            hd = nh_attr > 0 ? x.dims[2] / nh_attr : 2 * cs.dims.back();
+            NH = x.dims[2] / hd;
+        }
+        int64_t half = cs.dims.back();
+        const int64_t rdim = n.attr_int("rotary_embedding_dim", 0);
+        if (rdim > 0 && rdim / 2 != half) fail("RotaryEmbedding: partial rotary cache layout", ORT_NOT_IMPLEMENTED);
+        const int64_t rows = cs.numel() / half;
+        Tensor& Y = out_tensor(outname(0), x.dtype, x.dims, a, ctx);
+        check_kernel(ortmi_rotary_embedding(x.ptr, pos ? (const int64_t*)pos->ptr : nullptr,
+                                            pos && pos->numel() == 1 ? 1 : 0, cs.ptr, sn.ptr, rows,
+                                            Y.ptr, B, S, NH, hd, half, bnsd ? 1 : 0,
+                                            (int32_t)n.attr_int("interleaved", 0), kdt(x.dtype), st),
+                     "RotaryEmbedding");
+        return;
+    }
+    if (op == "SimplifiedLayerNormalization" || op == "RMSNormalization" ||
+        op == "SkipSimplifiedLayerNormalization") {
+        const bool skip = op == "SkipSimplifiedLayerNormalization";
+        Tensor x = need(0);
+        Tensor* sk = skip ? &need(1) : nullptr;
+        Tensor& g = need(skip ? 2 : 1);
+        Tensor* bias = skip ? in(3) : nullptr;
+        const int64_t D = x.dims.back();
+        const float eps = n.attr_float("epsilon", skip ? 1e-6f : 1e-5f);
+        void* skp = sk ? sk->ptr : nullptr;
+        void* gp = g.ptr;
+        void* bp = bias ? bias->ptr : nullptr;
+        Tensor& Y = out_tensor(outname(0), x.dtype, x.dims, a, ctx);
+        void* yp = Y.ptr;
+        void* rp = nullptr;
+        if (skip && n.outputs.size() >= 2 && !n.outputs.back().empty())
+            rp = out_tensor(n.outputs.back(), x.dtype, x.dims, a, ctx).ptr;
+        check_kernel(ortmi_rms_norm(x.ptr, skp, bp, gp, yp, rp, x.numel() / D, D, eps,
+                                    kdt(x.dtype), st),
+                     op.c_str());
+        return;
+    }
+    if (op == "Add" || op == "Mul" || op == "Sub") {
+        Tensor x = need(0), y = need(1);
+        if (x.dims != y.dims) fail(op + ": runtime shapes differ", ORT_INVALID_ARGUMENT);
+        Tensor& O = out_tensor(outname(0), x.dtype, x.dims, a, ctx);
+        check_kernel(ortmi_binary(op == "Add" ? 0 : (op == "Mul" ? 1 : 2), x.ptr, y.ptr, O.ptr,
+                                  x.numel(), kdt(x.dtype), st),
+                     op.c_str());
+        return;
+    }
+    if (op == "Sigmoid") {
+        Tensor x = need(0);
+        Tensor& O = out_tensor(outname(0), x.dtype, x.dims, a, ctx);
+        check_kernel(ortmi_sigmoid(x.ptr, O.ptr, x.numel(), kdt(x.dtype), st), "Sigmoid");
+        return;
+    }
+    if (op == "SwiGLU") {  // fused Sigmoid -> Mul -> Mul (fuse_swiglu)
+        Tensor g = need(0), u = need(1);
+        if (g.dims != u.dims) fail("SwiGLU: gate and up shapes differ", ORT_INVALID_ARGUMENT);
+        Tensor& O = out_tensor(outname(0), g.dtype, g.dims, a, ctx);
+        check_kernel(ortmi_swiglu(g.ptr, u.ptr, O.ptr, g.numel(), kdt(g.dtype), st), "SwiGLU");
+        return;
+    }
+    if (op == "Cast") {
+        Tensor x = need(0);
+        const int to = (int)n.attr_int("to", 0);
+        Tensor& O = out_tensor(outname(0), to, x.dims, a, ctx);
+        check_kernel(ortmi_cast(x.ptr, kdt(x.dtype), O.ptr, kdt(to), x.numel(), st), "Cast");
+        return;
+    }
+    if (op == "Gather") {
+        Tensor tab = need(0), ids = need(1);
+        std::vector<int64_t> od = ids.dims;
+        od.push_back(tab.dims[1]);
+        Tensor& O = out_tensor(outname(0), tab.dtype, od, a, ctx);
+        check_kernel(ortmi_gather_rows(tab.ptr, (const int64_t*)ids.ptr, O.ptr, ids.numel(),
+                                       tab.dims[0], tab.dims[1], kdt(tab.dtype), st),
+                     "Gather");
+        return;
+    }
+    fail("no executor for " + op, ORT_NOT_IMPLEMENTED);
+}
+
+}  // namespace ortmi_ep

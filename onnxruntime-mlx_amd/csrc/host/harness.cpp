@@ -1,0 +1,711 @@
+// In-process harness host for plugin execution providers.
+//
+// ONNX Runtime itself is not available to this project, so this file plays its
+// part on the plugin ABI: it implements the OrtApi / OrtEpApi slots listed in
+// include/ort_plugin_ep_abi.h over an in-memory graph, loads an EP library with
+// dlopen, and drives CreateEpFactories -> GetSupportedDevices -> CreateEp ->
+// GetCapability -> Compile -> CreateState/Compute the way ORT's plugin loader
+// does (the reference's call sequence: rust/src/lib.rs:90-155,
+// rust/src/factory.rs:116-213, rust/src/ep.rs:119-357, 928-1211, 1931-2134).
+// Graphs must be claimed completely: there is no CPU execution provider here.
+// Every tensor the harness hands to Compute lives in HBM (hipMalloc).
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <set>
+#include <string>
+#include <type_traits>
+#include <vector>
+
+#include "../../../include/ort_plugin_ep_abi.h"
+
+// ----------------------------------------------------------- host objects --
+struct OrtStatus {
+    OrtErrorCode code;
+    std::string msg;
+};
+struct OrtHardwareDevice {
+    OrtHardwareDeviceType type;
+};
+struct OrtEpDevice {
+    OrtEpFactory* factory;
+    const OrtHardwareDevice* device;
+};
+// Type/shape info; the same object serves as OrtTypeInfo and as the tensor info.
+struct OrtTensorTypeAndShapeInfo {
+    int dtype = 0;
+    std::vector<int64_t> dims;
+};
+struct OrtTypeInfo : OrtTensorTypeAndShapeInfo {};
+struct OrtValue {
+    OrtTensorTypeAndShapeInfo info;
+    void* data = nullptr;       // device pointer (or host for initializers)
+    std::vector<uint8_t> host;  // initializer storage
+};
+struct OrtValueInfo {
+    std::string name;
+    OrtTypeInfo type;
+    bool is_initializer = false;
+    OrtValue init;  // initializer value (host memory)
+    const OrtNode* producer = nullptr;
+    size_t producer_output = 0;
+};
+struct OrtOpAttr {
+    std::string name;
+    OrtOpAttrType type = ORT_OP_ATTR_UNDEFINED;
+    int64_t i = 0;
+    float f = 0.f;
+    std::string s;
+    std::vector<int64_t> ints;
+    std::vector<float> floats;
+};
+struct OrtNode {
+    size_t id = 0;
+    std::string name, op, domain;
+    int since = 1;
+    std::vector<OrtValueInfo*> inputs, outputs;
+    std::vector<std::unique_ptr<OrtOpAttr>> attrs;
+};
+struct OrtGraph {
+    std::vector<OrtNode*> nodes;
+    std::vector<OrtValueInfo*> inputs, outputs, initializers;
+};
+struct OrtEpGraphSupportInfo {
+    std::vector<std::vector<const OrtNode*>> groups;
+};
+struct OrtKernelContext {
+    std::vector<OrtValue*> inputs;
+    std::vector<std::string> output_names;
+    struct Session* session;
+    std::vector<OrtValue*> outputs;
+};
+struct OrtNodeComputeContext {
+    std::string name;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+OrtStatus* mk(OrtErrorCode c, const std::string& m) { return new OrtStatus{c, m}; }
+
+// ------------------------------------------------------------ OrtApi impl --
+OrtStatus* h_CreateStatus(OrtErrorCode code, const char* msg) { return mk(code, msg ? msg : ""); }
+OrtErrorCode h_GetErrorCode(const OrtStatus* s) { return s ? s->code : ORT_OK; }
+const char* h_GetErrorMessage(const OrtStatus* s) { return s ? s->msg.c_str() : ""; }
+void h_ReleaseStatus(OrtStatus* s) { delete s; }
+OrtStatus* h_GetTensorMutableData(OrtValue* v, void** out) {
+    *out = v->data;
+    return nullptr;
+}
+OrtStatus* h_GetTensorData(const OrtValue* v, const void** out) {
+    *out = v->data;
+    return nullptr;
+}
+OrtStatus* h_CastTypeInfoToTensorInfo(const OrtTypeInfo* t, const OrtTensorTypeAndShapeInfo** out) {
+    *out = t;
+    return nullptr;
+}
+OrtStatus* h_GetOnnxTypeFromTypeInfo(const OrtTypeInfo*, ONNXType* out) {
+    *out = ONNX_TYPE_TENSOR;
+    return nullptr;
+}
+OrtStatus* h_GetTensorElementType(const OrtTensorTypeAndShapeInfo* t, ONNXTensorElementDataType* out) {
+    *out = (ONNXTensorElementDataType)t->dtype;
+    return nullptr;
+}
+OrtStatus* h_GetDimensionsCount(const OrtTensorTypeAndShapeInfo* t, size_t* out) {
+    *out = t->dims.size();
+    return nullptr;
+}
+OrtStatus* h_GetDimensions(const OrtTensorTypeAndShapeInfo* t, int64_t* dims, size_t len) {
+    for (size_t i = 0; i < len && i < t->dims.size(); ++i) dims[i] = t->dims[i];
+    return nullptr;
+}
+OrtStatus* h_GetTensorShapeElementCount(const OrtTensorTypeAndShapeInfo* t, size_t* out) {
+    size_t n = 1;
+    for (auto d : t->dims) n *= (size_t)(d < 0 ? 0 : d);
+    *out = n;
+    return nullptr;
+}
+OrtStatus* h_GetTensorTypeAndShape(const OrtValue* v, OrtTensorTypeAndShapeInfo** out) {
+    *out = new OrtTensorTypeAndShapeInfo(v->info);
+    return nullptr;
+}
+void h_ReleaseTensorTypeAndShapeInfo(OrtTensorTypeAndShapeInfo* t) { delete t; }
+OrtStatus* h_KernelContext_GetInputCount(const OrtKernelContext* c, size_t* out) {
+    *out = c->inputs.size();
+    return nullptr;
+}
+OrtStatus* h_KernelContext_GetOutputCount(const OrtKernelContext* c, size_t* out) {
+    *out = c->output_names.size();
+    return nullptr;
+}
+OrtStatus* h_KernelContext_GetInput(const OrtKernelContext* c, size_t i, const OrtValue** out) {
+    if (i >= c->inputs.size()) return mk(ORT_INVALID_ARGUMENT, "input index out of range");
+    *out = c->inputs[i];
+    return nullptr;
+}
+OrtStatus* h_KernelContext_GetOutput(OrtKernelContext* c, size_t i, const int64_t* dims,
+                                     size_t n, OrtValue** out);  // defined after Session
+const OrtEpApi* h_GetEpApi();
+OrtHardwareDeviceType h_HardwareDevice_Type(const OrtHardwareDevice* d) { return d->type; }
+OrtStatus* h_GetValueInfoName(const OrtValueInfo* v, const char** name) {
+    *name = v->name.c_str();
+    return nullptr;
+}
+OrtStatus* h_GetValueInfoTypeInfo(const OrtValueInfo* v, const OrtTypeInfo** t) {
+    *t = &v->type;
+    return nullptr;
+}
+OrtStatus* h_ValueInfo_GetValueProducer(const OrtValueInfo* v, const OrtNode** p, size_t* idx) {
+    *p = v->producer;
+    if (idx) *idx = v->producer_output;
+    return nullptr;
+}
+OrtStatus* h_ValueInfo_GetInitializerValue(const OrtValueInfo* v, const OrtValue** out) {
+    *out = v->is_initializer ? &v->init : nullptr;
+    return nullptr;
+}
+OrtStatus* h_ValueInfo_IsConstantInitializer(const OrtValueInfo* v, bool* out) {
+    *out = v->is_initializer;
+    return nullptr;
+}
+#define LIST_FNS(NAME, FIELD, T)                                                      \
+    OrtStatus* h_Graph_GetNum##NAME(const OrtGraph* g, size_t* out) {                 \
+        *out = g->FIELD.size();                                                       \
+        return nullptr;                                                               \
+    }                                                                                 \
+    OrtStatus* h_Graph_Get##NAME(const OrtGraph* g, const T** out, size_t num) {      \
+        for (size_t i = 0; i < num && i < g->FIELD.size(); ++i) out[i] = g->FIELD[i]; \
+        return nullptr;                                                               \
+    }
+LIST_FNS(Inputs, inputs, OrtValueInfo)
+LIST_FNS(Outputs, outputs, OrtValueInfo)
+LIST_FNS(Initializers, initializers, OrtValueInfo)
+LIST_FNS(Nodes, nodes, OrtNode)
+#undef LIST_FNS
+OrtStatus* h_Node_GetId(const OrtNode* n, size_t* id) {
+    *id = n->id;
+    return nullptr;
+}
+OrtStatus* h_Node_GetName(const OrtNode* n, const char** s) {
+    *s = n->name.c_str();
+    return nullptr;
+}
+OrtStatus* h_Node_GetOperatorType(const OrtNode* n, const char** s) {
+    *s = n->op.c_str();
+    return nullptr;
+}
+OrtStatus* h_Node_GetDomain(const OrtNode* n, const char** s) {
+    *s = n->domain.c_str();
+    return nullptr;
+}
+OrtStatus* h_Node_GetSinceVersion(const OrtNode* n, int* v) {
+    *v = n->since;
+    return nullptr;
+}
+OrtStatus* h_Node_GetNumInputs(const OrtNode* n, size_t* out) {
+    *out = n->inputs.size();
+    return nullptr;
+}
+OrtStatus* h_Node_GetInputs(const OrtNode* n, const OrtValueInfo** out, size_t num) {
+    for (size_t i = 0; i < num && i < n->inputs.size(); ++i) out[i] = n->inputs[i];
+    return nullptr;
+}
+OrtStatus* h_Node_GetNumOutputs(const OrtNode* n, size_t* out) {
+    *out = n->outputs.size();
+    return nullptr;
+}
+OrtStatus* h_Node_GetOutputs(const OrtNode* n, const OrtValueInfo** out, size_t num) {
+    for (size_t i = 0; i < num && i < n->outputs.size(); ++i) out[i] = n->outputs[i];
+    return nullptr;
+}
+OrtStatus* h_Node_GetNumAttributes(const OrtNode* n, size_t* out) {
+    *out = n->attrs.size();
+    return nullptr;
+}
+OrtStatus* h_Node_GetAttributes(const OrtNode* n, const OrtOpAttr** out, size_t num) {
+    for (size_t i = 0; i < num && i < n->attrs.size(); ++i) out[i] = n->attrs[i].get();
+    return nullptr;
+}
+OrtStatus* h_Node_GetAttributeByName(const OrtNode* n, const char* name, const OrtOpAttr** out) {
+    *out = nullptr;
+    for (auto& a : n->attrs)
+        if (a->name == name) {
+            *out = a.get();
+            return nullptr;
+        }
+    return mk(ORT_NOT_FOUND, std::string("attribute not found: ") + name);
+}
+OrtStatus* h_OpAttr_GetType(const OrtOpAttr* a, OrtOpAttrType* t) {
+    *t = a->type;
+    return nullptr;
+}
+OrtStatus* h_OpAttr_GetName(const OrtOpAttr* a, const char** s) {
+    *s = a->name.c_str();
+    return nullptr;
+}
+OrtStatus* h_ReadOpAttr(const OrtOpAttr* a, OrtOpAttrType t, void* data, size_t len, size_t* out) {
+    if (t != a->type) return mk(ORT_INVALID_ARGUMENT, "attribute type mismatch");
+    const void* src = nullptr;
+    size_t need = 0;
+    switch (t) {
+        case ORT_OP_ATTR_INT: src = &a->i; need = 8; break;
+        case ORT_OP_ATTR_FLOAT: src = &a->f; need = 4; break;
+        case ORT_OP_ATTR_STRING: src = a->s.data(); need = a->s.size(); break;
+        case ORT_OP_ATTR_INTS: src = a->ints.data(); need = a->ints.size() * 8; break;
+        case ORT_OP_ATTR_FLOATS: src = a->floats.data(); need = a->floats.size() * 4; break;
+        default: return mk(ORT_NOT_IMPLEMENTED, "attribute type");
+    }
+    *out = need;
+    if (len < need) return mk(ORT_INVALID_ARGUMENT, "buffer too small");
+    if (need) std::memcpy(data, src, need);
+    return nullptr;
+}
+
+// ---------------------------------------------------------- OrtEpApi impl --
+OrtStatus* h_CreateEpDevice(OrtEpFactory* f, const OrtHardwareDevice* d, const OrtKeyValuePairs*,
+                            const OrtKeyValuePairs*, OrtEpDevice** out) {
+    *out = new OrtEpDevice{f, d};
+    return nullptr;
+}
+void h_ReleaseEpDevice(OrtEpDevice* d) { delete d; }
+OrtStatus* h_EpGraphSupportInfo_AddNodesToFuse(OrtEpGraphSupportInfo* info,
+                                               const OrtNode* const* nodes, size_t n,
+                                               const OrtNodeFusionOptions* opts) {
+    if (!opts || opts->ort_version_supported < 1) return mk(ORT_INVALID_ARGUMENT, "bad fusion options");
+    info->groups.emplace_back(nodes, nodes + n);
+    return nullptr;
+}
+OrtStatus* h_EpGraphSupportInfo_AddSingleNode(OrtEpGraphSupportInfo* info, const OrtNode* node) {
+    info->groups.push_back({node});
+    return nullptr;
+}
+const char* h_NodeComputeContext_NodeName(const OrtNodeComputeContext* c) { return c->name.c_str(); }
+
+// Function tables built from the shared slot lists.
+void* g_api[ORTMI_ORT_API_TABLE_SIZE];
+void* g_ep_api[ORTMI_ORT_EP_API_TABLE_SIZE];
+
+#define CHECK_SIG(slot, name, ret, params) \
+    static_assert(std::is_same<decltype(&h_##name), ort_abi::api::name##_fn>::value, #name);
+#define CHECK_EP_SIG(slot, name, ret, params) \
+    static_assert(std::is_same<decltype(&h_##name), ort_abi::ep_api::name##_fn>::value, #name);
+
+const OrtEpApi* h_GetEpApi() { return reinterpret_cast<const OrtEpApi*>(g_ep_api); }
+
+const OrtApi* get_api(uint32_t version) {
+    static bool init = false;
+    if (!init) {
+#define FILL(slot, name, ret, params) g_api[slot] = reinterpret_cast<void*>(&h_##name);
+#define FILL_EP(slot, name, ret, params) g_ep_api[slot] = reinterpret_cast<void*>(&h_##name);
+        ORTMI_ORT_API_SLOTS(FILL)
+        ORTMI_ORT_EP_API_SLOTS(FILL_EP)
+#undef FILL
+#undef FILL_EP
+        init = true;
+    }
+    return version <= ORT_API_VERSION ? reinterpret_cast<const OrtApi*>(g_api) : nullptr;
+}
+const char* get_version_string() { return "1.29.0-harness"; }
+OrtApiBase g_api_base{get_api, get_version_string};
+
+}  // namespace
+
+ORTMI_ORT_API_SLOTS(CHECK_SIG)
+ORTMI_ORT_EP_API_SLOTS(CHECK_EP_SIG)
+
+// ------------------------------------------------------------------ graph --
+struct HxGraph {
+    OrtGraph g;
+    std::map<std::string, std::unique_ptr<OrtValueInfo>> values;
+    std::vector<std::unique_ptr<OrtNode>> nodes;
+    OrtValueInfo* value(const std::string& name) {
+        auto it = values.find(name);
+        if (it != values.end()) return it->second.get();
+        auto v = std::make_unique<OrtValueInfo>();
+        v->name = name;
+        OrtValueInfo* p = v.get();
+        values[name] = std::move(v);
+        return p;
+    }
+};
+
+// ---------------------------------------------------------------- session --
+struct Partition {
+    OrtGraph sub;
+    OrtNode fused;
+    OrtNodeComputeInfo* info = nullptr;
+    void* state = nullptr;
+};
+
+struct DevBuf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct Session {
+    HxGraph* graph = nullptr;
+    void* lib = nullptr;
+    ReleaseEpFactoryFn release_factory = nullptr;
+    OrtEpFactory* factory = nullptr;
+    OrtEpDevice* ep_device = nullptr;
+    OrtEp* ep = nullptr;
+    OrtHardwareDevice gpu{OrtHardwareDeviceType_GPU}, cpu{OrtHardwareDeviceType_CPU};
+    std::vector<std::unique_ptr<Partition>> parts;
+    std::vector<std::unique_ptr<OrtValueInfo>> extra_vis;
+    std::set<const OrtNode*> claimed;
+    std::map<std::string, std::unique_ptr<OrtValue>> env;      // values of the current run
+    std::map<std::string, DevBuf> owned;                        // harness-allocated outputs
+    std::map<std::string, void*> bound;                         // caller-bound output buffers
+    std::vector<std::unique_ptr<OrtNodeComputeContext>> ctxs;
+    ~Session();
+};
+
+static size_t esize(int dt) {
+    switch (dt) {
+        case 1: case 6: case 12: return 4;
+        case 10: case 16: case 4: case 5: return 2;
+        case 7: case 11: case 13: return 8;
+        default: return 1;
+    }
+}
+
+namespace {
+OrtStatus* h_KernelContext_GetOutput(OrtKernelContext* c, size_t i, const int64_t* dims, size_t n,
+                                     OrtValue** out) {
+    if (i >= c->output_names.size()) return mk(ORT_INVALID_ARGUMENT, "output index out of range");
+    Session* s = c->session;
+    const std::string& name = c->output_names[i];
+    auto v = std::make_unique<OrtValue>();
+    v->info.dims.assign(dims, dims + n);
+    auto vi = s->graph->values.find(name);
+    v->info.dtype = vi != s->graph->values.end() ? vi->second->type.dtype : 0;
+    size_t bytes = esize(v->info.dtype);
+    for (size_t k = 0; k < n; ++k) bytes *= (size_t)(dims[k] < 0 ? 0 : dims[k]);
+    auto b = s->bound.find(name);
+    if (b != s->bound.end()) {
+        v->data = b->second;
+    } else {
+        DevBuf& buf = s->owned[name];
+        if (buf.bytes < bytes) {
+            if (buf.ptr) (void)hipFree(buf.ptr);
+            buf.ptr = nullptr;
+            if (hipMalloc(&buf.ptr, bytes ? bytes : 1) != hipSuccess)
+                return mk(ORT_FAIL, "harness: hipMalloc failed for output " + name);
+            buf.bytes = bytes;
+        }
+        v->data = buf.ptr;
+    }
+    *out = v.get();
+    s->env[name] = std::move(v);
+    return nullptr;
+}
+}  // namespace
+
+Session::~Session() {
+    for (auto& p : parts)
+        if (p->info && p->info->ReleaseState) p->info->ReleaseState(p->info, p->state);
+    if (ep && !parts.empty()) {
+        std::vector<OrtNodeComputeInfo*> infos;
+        for (auto& p : parts) infos.push_back(p->info);
+        ep->ReleaseNodeComputeInfos(ep, infos.data(), infos.size());
+    }
+    if (ep) factory->ReleaseEp(factory, ep);
+    if (ep_device) h_ReleaseEpDevice(ep_device);
+    if (factory && release_factory) release_factory(factory);
+    for (auto& kv : owned)
+        if (kv.second.ptr) (void)hipFree(kv.second.ptr);
+    if (lib) dlclose(lib);
+}
+
+static bool take(OrtStatus* st, const char* what) {
+    if (!st) return true;
+    g_err = std::string(what) + ": " + st->msg;
+    delete st;
+    return false;
+}
+
+extern "C" {
+
+const char* hx_last_error() { return g_err.c_str(); }
+const OrtApiBase* hx_api_base() { return &g_api_base; }
+
+HxGraph* hx_graph_new() { return new HxGraph(); }
+void hx_graph_free(HxGraph* g) { delete g; }
+
+int hx_graph_add_value(HxGraph* g, const char* name, int dtype, int rank, const int64_t* dims) {
+    OrtValueInfo* v = g->value(name);
+    v->type.dtype = dtype;
+    v->type.dims.assign(dims, dims + rank);
+    return 0;
+}
+
+int hx_graph_add_initializer(HxGraph* g, const char* name, int dtype, int rank,
+                             const int64_t* dims, const void* data, size_t nbytes) {
+    OrtValueInfo* v = g->value(name);
+    v->type.dtype = dtype;
+    v->type.dims.assign(dims, dims + rank);
+    v->is_initializer = true;
+    v->init.info = v->type;
+    v->init.host.assign((const uint8_t*)data, (const uint8_t*)data + nbytes);
+    v->init.data = v->init.host.data();
+    g->g.initializers.push_back(v);
+    return 0;
+}
+
+int hx_graph_add_node(HxGraph* g, const char* op, const char* domain, const char* name, int since,
+                      int n_in, const char** inputs, int n_out, const char** outputs) {
+    auto n = std::make_unique<OrtNode>();
+    n->id = g->nodes.size();
+    n->op = op;
+    n->domain = domain ? domain : "";
+    n->name = name ? name : "";
+    n->since = since;
+    for (int i = 0; i < n_in; ++i)
+        n->inputs.push_back(inputs[i] && *inputs[i] ? g->value(inputs[i]) : nullptr);
+    for (int i = 0; i < n_out; ++i) {
+        OrtValueInfo* v = outputs[i] && *outputs[i] ? g->value(outputs[i]) : nullptr;
+        if (v) {
+            v->producer = n.get();
+            v->producer_output = i;
+        }
+        n->outputs.push_back(v);
+    }
+    g->g.nodes.push_back(n.get());
+    g->nodes.push_back(std::move(n));
+    return (int)g->nodes.size() - 1;
+}
+
+static OrtOpAttr* new_attr(HxGraph* g, int node, const char* name, OrtOpAttrType t) {
+    auto a = std::make_unique<OrtOpAttr>();
+    a->name = name;
+    a->type = t;
+    OrtOpAttr* p = a.get();
+    g->nodes[node]->attrs.push_back(std::move(a));
+    return p;
+}
+int hx_node_attr_int(HxGraph* g, int node, const char* name, int64_t v) {
+    new_attr(g, node, name, ORT_OP_ATTR_INT)->i = v;
+    return 0;
+}
+int hx_node_attr_float(HxGraph* g, int node, const char* name, float v) {
+    new_attr(g, node, name, ORT_OP_ATTR_FLOAT)->f = v;
+    return 0;
+}
+int hx_node_attr_string(HxGraph* g, int node, const char* name, const char* v) {
+    new_attr(g, node, name, ORT_OP_ATTR_STRING)->s = v;
+    return 0;
+}
+int hx_node_attr_ints(HxGraph* g, int node, const char* name, int n, const int64_t* v) {
+    new_attr(g, node, name, ORT_OP_ATTR_INTS)->ints.assign(v, v + n);
+    return 0;
+}
+
+int hx_graph_set_io(HxGraph* g, int n_in, const char** ins, int n_out, const char** outs) {
+    g->g.inputs.clear();
+    g->g.outputs.clear();
+    for (int i = 0; i < n_in; ++i) g->g.inputs.push_back(g->value(ins[i]));
+    for (int i = 0; i < n_out; ++i) g->g.outputs.push_back(g->value(outs[i]));
+    return 0;
+}
+
+// Load the EP, run device selection, CreateEp and GetCapability. With
+// compile = 0 the session stops after GetCapability (no GPU work at all).
+// force_device = 1 creates the EP on the GPU hardware device even when the EP
+// offered none (no GPU visible): only GetCapability runs then, for CPU tests of
+// the claim and partition logic.
+Session* hx_session_new(HxGraph* g, const char* ep_path, const char* registration_name,
+                        int compile, int force_device) {
+    auto s = std::make_unique<Session>();
+    s->graph = g;
+    s->lib = dlopen(ep_path, RTLD_NOW | RTLD_LOCAL);
+    if (!s->lib) {
+        g_err = std::string("dlopen: ") + dlerror();
+        return nullptr;
+    }
+    auto create = (CreateEpFactoriesFn)dlsym(s->lib, "CreateEpFactories");
+    s->release_factory = (ReleaseEpFactoryFn)dlsym(s->lib, "ReleaseEpFactory");
+    if (!create || !s->release_factory) {
+        g_err = "EP library lacks CreateEpFactories / ReleaseEpFactory";
+        return nullptr;
+    }
+    OrtEpFactory* facs[4] = {};
+    size_t nf = 0;
+    if (!take(create(registration_name, &g_api_base, nullptr, facs, 4, &nf), "CreateEpFactories"))
+        return nullptr;
+    if (nf < 1) {
+        g_err = "no factory";
+        return nullptr;
+    }
+    s->factory = facs[0];
+    const OrtHardwareDevice* hw[2] = {&s->cpu, &s->gpu};
+    OrtEpDevice* devs[2] = {};
+    size_t nd = 0;
+    if (!take(s->factory->GetSupportedDevices(s->factory, hw, 2, devs, 2, &nd), "GetSupportedDevices"))
+        return nullptr;
+    const OrtHardwareDevice* sel[1] = {&s->gpu};
+    if (nd >= 1) {
+        s->ep_device = devs[0];
+        sel[0] = s->ep_device->device;
+    } else if (!force_device || compile) {
+        g_err = "EP offered no device (is a GPU visible?)";
+        return nullptr;
+    }
+    if (!take(s->factory->CreateEp(s->factory, sel, nullptr, 1, nullptr, nullptr, &s->ep), "CreateEp"))
+        return nullptr;
+    OrtEpGraphSupportInfo support;
+    if (!take(s->ep->GetCapability(s->ep, &g->g, &support), "GetCapability")) return nullptr;
+    for (auto& grp : support.groups) {
+        auto p = std::make_unique<Partition>();
+        std::set<const OrtNode*> in_group(grp.begin(), grp.end());
+        for (const OrtNode* n : grp) s->claimed.insert(n);
+        std::set<std::string> produced, consumed_outside;
+        for (auto& n : g->nodes)
+            if (!in_group.count(n.get()))
+                for (auto* v : n->inputs)
+                    if (v) consumed_outside.insert(v->name);
+        for (auto* v : g->g.outputs) consumed_outside.insert(v->name);
+        std::vector<std::string> ins, outs;
+        std::set<std::string> seen_in;
+        for (const OrtNode* n : grp) {
+            p->sub.nodes.push_back(const_cast<OrtNode*>(n));
+            for (auto* v : n->outputs)
+                if (v) produced.insert(v->name);
+        }
+        std::set<std::string> seen_init;
+        for (const OrtNode* n : grp) {
+            for (auto* v : n->inputs) {
+                if (!v || produced.count(v->name)) continue;
+                if (v->is_initializer) {  // constants are dropped from the fused inputs
+                    if (seen_init.insert(v->name).second) p->sub.initializers.push_back(v);
+                    continue;
+                }
+                if (seen_in.insert(v->name).second) {
+                    ins.push_back(v->name);
+                    p->fused.inputs.push_back(v);
+                    p->sub.inputs.push_back(v);
+                }
+            }
+            for (auto* v : n->outputs)
+                if (v && consumed_outside.count(v->name)) {
+                    outs.push_back(v->name);
+                    p->fused.outputs.push_back(v);
+                    p->sub.outputs.push_back(v);
+                }
+        }
+        p->fused.name = "MI355X_fused_" + std::to_string(s->parts.size());
+        p->fused.op = p->fused.name;
+        p->fused.domain = "";
+        s->parts.push_back(std::move(p));
+    }
+    if (!compile) return s.release();
+    for (auto& n : g->nodes)
+        if (!s->claimed.count(n.get())) {
+            g_err = "node " + n->name + " (" + n->op + ") was not claimed and the harness has no "
+                    "CPU execution provider";
+            return nullptr;
+        }
+    std::vector<const OrtGraph*> graphs;
+    std::vector<const OrtNode*> fused;
+    for (auto& p : s->parts) {
+        graphs.push_back(&p->sub);
+        fused.push_back(&p->fused);
+    }
+    std::vector<OrtNodeComputeInfo*> infos(s->parts.size(), nullptr);
+    std::vector<OrtNode*> ctx_nodes(s->parts.size(), nullptr);
+    if (!take(s->ep->Compile(s->ep, graphs.data(), fused.data(), graphs.size(), infos.data(),
+                             ctx_nodes.data()),
+              "Compile"))
+        return nullptr;
+    for (size_t i = 0; i < s->parts.size(); ++i) {
+        s->parts[i]->info = infos[i];
+        auto ctx = std::make_unique<OrtNodeComputeContext>();
+        ctx->name = s->parts[i]->fused.name;
+        if (!take(infos[i]->CreateState(infos[i], ctx.get(), &s->parts[i]->state), "CreateState"))
+            return nullptr;
+        s->ctxs.push_back(std::move(ctx));
+    }
+    return s.release();
+}
+
+void hx_session_free(Session* s) { delete s; }
+
+int hx_session_num_partitions(Session* s) { return (int)s->parts.size(); }
+int hx_session_partition_size(Session* s, int i) { return (int)s->parts[i]->sub.nodes.size(); }
+int hx_session_partition_node(Session* s, int i, int j) { return (int)s->parts[i]->sub.nodes[j]->id; }
+int hx_session_node_claimed(Session* s, int node) {
+    return s->claimed.count(s->graph->nodes[node].get()) ? 1 : 0;
+}
+
+// Bind a caller-owned device buffer as the storage of a graph value produced by
+// the EP (an IOBinding analogue; binding a present-KV output to the past-KV input
+// buffer gives the shared-buffer contract).
+int hx_session_bind_output(Session* s, const char* name, void* ptr) {
+    if (ptr) s->bound[name] = ptr;
+    else s->bound.erase(name);
+    return 0;
+}
+
+int hx_session_set_input(Session* s, const char* name, void* ptr, int dtype, int rank,
+                         const int64_t* dims) {
+    auto v = std::make_unique<OrtValue>();
+    v->data = ptr;
+    v->info.dtype = dtype;
+    v->info.dims.assign(dims, dims + rank);
+    s->env[name] = std::move(v);
+    return 0;
+}
+
+int hx_session_run(Session* s) {
+    // Run partitions in dependency order: a partition is ready once every fused
+    // input is available (a graph input or an output of a finished partition).
+    // Values produced by partitions are dropped first, so a partition never runs on
+    // a previous run's outputs.
+    for (auto& p : s->parts)
+        for (auto* v : p->fused.outputs) s->env.erase(v->name);
+    std::vector<bool> done(s->parts.size(), false);
+    for (size_t round = 0; round < s->parts.size(); ++round) {
+        bool progressed = false;
+        for (size_t pi = 0; pi < s->parts.size(); ++pi) {
+            if (done[pi]) continue;
+            auto& p = s->parts[pi];
+            bool ready = true;
+            for (auto* v : p->fused.inputs)
+                if (!s->env.count(v->name)) ready = false;
+            if (!ready) continue;
+            OrtKernelContext ctx;
+            ctx.session = s;
+            for (auto* v : p->fused.inputs) ctx.inputs.push_back(s->env[v->name].get());
+            for (auto* v : p->fused.outputs) ctx.output_names.push_back(v->name);
+            if (!take(p->info->Compute(p->info, p->state, &ctx), "Compute")) return 1;
+            done[pi] = progressed = true;
+        }
+        if (!progressed) break;
+    }
+    for (size_t pi = 0; pi < s->parts.size(); ++pi)
+        if (!done[pi]) {
+            g_err = "partition " + std::to_string(pi) + " never became ready (missing input)";
+            return 1;
+        }
+    return 0;
+}
+
+int hx_session_get_output(Session* s, const char* name, void** ptr, int* rank, int64_t* dims) {
+    auto it = s->env.find(name);
+    if (it == s->env.end()) {
+        g_err = std::string("no value ") + name;
+        return 1;
+    }
+    *ptr = it->second->data;
+    *rank = (int)it->second->info.dims.size();
+    for (int i = 0; i < *rank && i < 8; ++i) dims[i] = it->second->info.dims[i];
+    return 0;
+}
+
+}  // extern "C"

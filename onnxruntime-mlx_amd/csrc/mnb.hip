@@ -219,32 +219,18 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     }
 }
 
-template <typename T, int BS, int CPL, int R>
-static int launch_gemv4_r(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y, int N,
-                          int K, int nb, hipStream_t st) {
-    const int Kp = nb * BS;
-    const long groups = ((long)N + R - 1) / R;
-    // One row group per wave while that gives at most 8 workgroups per CU; larger
-    // N loops with the next group's loads in flight.
-    long grid = (groups + 3) / 4;
-    if (grid > 8L * device_cu_count()) grid = 8L * device_cu_count();
-    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R>), dim3((unsigned)grid), dim3(256),
-                       (size_t)Kp * sizeof(float), st, A, B, S, Z, Y, N, K, nb);
-    return check_launch("mnb_gemv4");
-}
-
-// Rows per group: the smallest R in {1, 2, 4} that still leaves >= 4 workgroups
-// per CU, so small N spreads over the whole GPU and large N amortises staging.
 template <typename T, int BS, int CPL>
 static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
                             int N, int K, int nb, hipStream_t st) {
-    const long per_r4 = ((long)N + 3) / 4 / 4;  // workgroups at R = 4
-    const long want = 4L * device_cu_count();
-    if (CPL <= 2 && per_r4 >= want)
-        return launch_gemv4_r<T, BS, CPL, CPL <= 2 ? 4 : 1>(A, B, S, Z, Y, N, K, nb, st);
-    if (CPL <= 3 && per_r4 * 2 >= want)
-        return launch_gemv4_r<T, BS, CPL, CPL <= 3 ? 2 : 1>(A, B, S, Z, Y, N, K, nb, st);
-    return launch_gemv4_r<T, BS, CPL, 1>(A, B, S, Z, Y, N, K, nb, st);
+    // One row per group; at most 4 workgroups per CU, each wave walking its rows
+    // with the next row's loads in flight (measured best on MI355X for the
+    // K=4096 x N=11008 shape against 1-4 rows per group and 1-8 workgroups/CU).
+    const int Kp = nb * BS;
+    long grid = ((long)N + 3) / 4;
+    if (grid > 4L * device_cu_count()) grid = 4L * device_cu_count();
+    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, 1>), dim3((unsigned)grid), dim3(256),
+                       (size_t)Kp * sizeof(float), st, A, B, S, Z, Y, N, K, nb);
+    return check_launch("mnb_gemv4");
 }
 
 template <typename T, int BS>

@@ -1,0 +1,248 @@
+"""Int4 Llama-style decoder expressed as an ONNX contrib-op graph, run through the EP.
+
+The graph mirrors what ONNX Runtime GenAI exports for a q4f16 decoder (the op
+histogram the reference records for Qwen2.5-0.5B decode,
+examples/traces/qwen2.5-0.5b-decode.json): an embedding Gather, per layer
+(Skip)SimplifiedLayerNormalization, seven MatMulNBits, GroupQueryAttention with
+in-op rotary, and a Sigmoid/Mul/Mul SwiGLU, then a final norm and the lm_head
+MatMulNBits. Weights are random (seeded); every linear layer is 4-bit, block 32,
+symmetric, with fp16 scales |N(0, 0.02)|.
+
+The KV cache is device resident with a fixed capacity: each layer's present
+output is bound to its past input buffer, so GroupQueryAttention writes the new
+rows in place (the shared-buffer contract, rust/src/ops/attention.rs:893-902).
+Greedy decoding takes the argmax on the device and feeds it back as the next
+input id, so a decode step reads nothing back to the host but total_sequence_length.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import time
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import check, load_kernels
+from . import harness as hx
+
+
+@dataclass
+class DecoderConfig:
+    layers: int = 28
+    hidden: int = 1536
+    heads: int = 12
+    kv_heads: int = 2
+    head_dim: int = 128
+    inter: int = 8960
+    vocab: int = 151936
+    rope_base: float = 1e6
+    eps: float = 1e-6
+    block: int = 32
+    max_pos: int = 4096
+
+    def linear_shapes(self):
+        """(name, N, K) of every MatMulNBits in one layer."""
+        H, KV, hd, D, I = self.heads, self.kv_heads, self.head_dim, self.hidden, self.inter
+        return [("q", H * hd, D), ("k", KV * hd, D), ("v", KV * hd, D), ("o", D, H * hd),
+                ("gate", I, D), ("up", I, D), ("down", D, I)]
+
+    def weight_bytes(self) -> int:
+        """int4 codes + fp16 scales of all linear layers (the per-token weight stream)."""
+        total = 0
+        for _, N, K in self.linear_shapes():
+            total += N * K // 2 + N * (K // self.block) * 2
+        total *= self.layers
+        total += self.vocab * self.hidden // 2 + self.vocab * (self.hidden // self.block) * 2
+        return total
+
+
+def _quant_linear(rng, N, K, block):
+    nb = K // block
+    B = rng.integers(0, 256, size=(N, nb, block // 2), dtype=np.uint8)
+    s = np.abs(rng.standard_normal(N * nb) * 0.02).astype(np.float16)
+    return B, s
+
+
+def make_weights(cfg: DecoderConfig, seed: int = 4):
+    rng = np.random.default_rng(seed)
+    w = {"embed": rng.standard_normal((cfg.vocab, cfg.hidden)).astype(np.float16)}
+    for layer in range(cfg.layers):
+        for name, N, K in cfg.linear_shapes():
+            B, s = _quant_linear(rng, N, K, cfg.block)
+            w[f"l{layer}.{name}.B"] = B
+            w[f"l{layer}.{name}.s"] = s
+        w[f"l{layer}.ln1"] = np.ones(cfg.hidden, np.float16)
+        w[f"l{layer}.ln2"] = np.ones(cfg.hidden, np.float16)
+    w["final_ln"] = np.ones(cfg.hidden, np.float16)
+    B, s = _quant_linear(rng, cfg.vocab, cfg.hidden, cfg.block)
+    w["lm_head.B"], w["lm_head.s"] = B, s
+    half = cfg.head_dim // 2
+    inv = 1.0 / (cfg.rope_base ** (np.arange(half, dtype=np.float64) / half))
+    ang = np.arange(cfg.max_pos, dtype=np.float64)[:, None] * inv[None, :]
+    w["cos"] = np.cos(ang).astype(np.float16)
+    w["sin"] = np.sin(ang).astype(np.float16)
+    return w
+
+
+def build_graph(cfg: DecoderConfig, w, cap: int) -> hx.Graph:
+    """Decoder graph with symbolic sequence length S and KV capacity `cap`."""
+    g = hx.Graph()
+    F16, I32, I64 = hx.FLOAT16, hx.INT32, hx.INT64
+    D, H, KV, hd = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
+    S = -1
+    g.value("input_ids", I64, [1, S])
+    g.value("seqlens_k", I32, [1])
+    g.value("total_sequence_length", I32, [1])
+    g.value("logits", F16, [1, S, cfg.vocab])
+    g.initializer("embed", w["embed"])
+    g.initializer("cos_cache", w["cos"])
+    g.initializer("sin_cache", w["sin"])
+    inputs = ["input_ids", "seqlens_k", "total_sequence_length"]
+    outputs = ["logits"]
+
+    def linear(x, name, wkey, N, K, out):
+        g.initializer(f"{wkey}.B", w[f"{wkey}.B"])
+        g.initializer(f"{wkey}.s", w[f"{wkey}.s"])
+        g.value(out, F16, [1, S, N])
+        g.node("MatMulNBits", [x, f"{wkey}.B", f"{wkey}.s"], [out], domain="com.microsoft",
+               name=name, K=K, N=N, bits=4, block_size=cfg.block)
+
+    g.value("h0", F16, [1, S, D])
+    g.node("Gather", ["embed", "input_ids"], ["h0"], name="embed_gather", axis=0)
+    prev_out, residual = None, "h0"
+    for layer in range(cfg.layers):
+        p = f"l{layer}"
+        g.initializer(f"{p}.ln1", w[f"{p}.ln1"])
+        g.initializer(f"{p}.ln2", w[f"{p}.ln2"])
+        g.value(f"{p}.x", F16, [1, S, D])
+        if layer == 0:
+            g.node("SimplifiedLayerNormalization", ["h0", f"{p}.ln1"], [f"{p}.x"],
+                   name=f"{p}.ln1", epsilon=cfg.eps, axis=-1)
+        else:
+            g.value(f"{p}.res1", F16, [1, S, D])
+            g.node("SkipSimplifiedLayerNormalization", [prev_out, residual, f"{p}.ln1"],
+                   [f"{p}.x", "", "", f"{p}.res1"], domain="com.microsoft", name=f"{p}.ln1",
+                   epsilon=cfg.eps)
+            residual = f"{p}.res1"
+        for name, N, K in cfg.linear_shapes()[:3]:
+            linear(f"{p}.x", f"{p}.{name}_proj", f"{p}.{name}", N, K, f"{p}.{name}")
+        for kv in ("key", "value"):
+            g.value(f"past_key_values.{layer}.{kv}", F16, [1, KV, cap, hd])
+            g.value(f"present.{layer}.{kv}", F16, [1, KV, cap, hd])
+            inputs.append(f"past_key_values.{layer}.{kv}")
+            outputs.append(f"present.{layer}.{kv}")
+        g.value(f"{p}.attn", F16, [1, S, H * hd])
+        g.node("GroupQueryAttention",
+               [f"{p}.q", f"{p}.k", f"{p}.v", f"past_key_values.{layer}.key",
+                f"past_key_values.{layer}.value", "seqlens_k", "total_sequence_length",
+                "cos_cache", "sin_cache"],
+               [f"{p}.attn", f"present.{layer}.key", f"present.{layer}.value"],
+               domain="com.microsoft", name=f"{p}.gqa", num_heads=H, kv_num_heads=KV,
+               do_rotary=1, rotary_interleaved=0, scale=0.0)
+        linear(f"{p}.attn", f"{p}.o_proj", f"{p}.o", D, H * hd, f"{p}.o")
+        g.value(f"{p}.x2", F16, [1, S, D])
+        g.value(f"{p}.res2", F16, [1, S, D])
+        g.node("SkipSimplifiedLayerNormalization", [f"{p}.o", residual, f"{p}.ln2"],
+               [f"{p}.x2", "", "", f"{p}.res2"], domain="com.microsoft", name=f"{p}.ln2",
+               epsilon=cfg.eps)
+        residual = f"{p}.res2"
+        linear(f"{p}.x2", f"{p}.gate_proj", f"{p}.gate", cfg.inter, D, f"{p}.gate")
+        linear(f"{p}.x2", f"{p}.up_proj", f"{p}.up", cfg.inter, D, f"{p}.up")
+        for v in ("sig", "silu", "act"):
+            g.value(f"{p}.{v}", F16, [1, S, cfg.inter])
+        g.node("Sigmoid", [f"{p}.gate"], [f"{p}.sig"], name=f"{p}.sigmoid")
+        g.node("Mul", [f"{p}.gate", f"{p}.sig"], [f"{p}.silu"], name=f"{p}.silu")
+        g.node("Mul", [f"{p}.silu", f"{p}.up"], [f"{p}.act"], name=f"{p}.gated")
+        linear(f"{p}.act", f"{p}.down_proj", f"{p}.down", D, cfg.inter, f"{p}.down")
+        prev_out = f"{p}.down"
+    g.initializer("final_ln", w["final_ln"])
+    g.value("xf", F16, [1, S, D])
+    g.value("resf", F16, [1, S, D])
+    g.node("SkipSimplifiedLayerNormalization", [prev_out, residual, "final_ln"],
+           ["xf", "", "", "resf"], domain="com.microsoft", name="final_ln", epsilon=cfg.eps)
+    g.initializer("lm_head.B", w["lm_head.B"])
+    g.initializer("lm_head.s", w["lm_head.s"])
+    g.node("MatMulNBits", ["xf", "lm_head.B", "lm_head.s"], ["logits"], domain="com.microsoft",
+           name="lm_head", K=D, N=cfg.vocab, bits=4, block_size=cfg.block)
+    g.io(inputs, outputs)
+    return g
+
+
+class DecoderRunner:
+    """Greedy generation through the EP with a device-resident KV cache."""
+
+    def __init__(self, cfg: DecoderConfig, weights, cap: int, max_prompt: int):
+        import torch
+
+        self.torch = torch
+        self.cfg = cfg
+        self.cap = cap
+        self.graph = build_graph(cfg, weights, cap)
+        self.session = hx.Session(self.graph)
+        dev = "cuda"
+        self.kv = []
+        for layer in range(cfg.layers):
+            k = torch.zeros((1, cfg.kv_heads, cap, cfg.head_dim), dtype=torch.float16, device=dev)
+            v = torch.zeros_like(k)
+            self.kv.append((k, v))
+            self.session.bind_output(f"present.{layer}.key", k)
+            self.session.bind_output(f"present.{layer}.value", v)
+        self.logits = torch.empty((1, max_prompt, cfg.vocab), dtype=torch.float16, device=dev)
+        self.ids = torch.zeros((1, max_prompt), dtype=torch.int64, device=dev)
+        self.next_id = torch.zeros((1, 1), dtype=torch.int64, device=dev)
+        self.seqlens = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.total = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.length = 0
+        self.lib = load_kernels()
+
+    def _run(self, ids, S):
+        torch = self.torch
+        self.total.fill_(self.length + S)
+        self.seqlens.fill_(self.length + S - 1)
+        logits = self.logits[:, :S] if S > 1 else self.logits[:, :1]
+        logits = logits if logits.is_contiguous() else None
+        feeds = {"input_ids": (ids, hx.INT64), "seqlens_k": (self.seqlens, hx.INT32),
+                 "total_sequence_length": (self.total, hx.INT32)}
+        for layer, (k, v) in enumerate(self.kv):
+            feeds[f"past_key_values.{layer}.key"] = (k, hx.FLOAT16)
+            feeds[f"past_key_values.{layer}.value"] = (v, hx.FLOAT16)
+        self.session.bind_output("logits", self.logits)
+        self.session.run(feeds)
+        self.length += S
+        del torch, logits
+
+    def argmax_last(self, S):
+        st = ctypes.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+        last = self.logits[0, S - 1]
+        check(self.lib.ortmi_argmax_rows(ctypes.c_void_p(last.data_ptr()),
+                                         ctypes.c_void_p(self.next_id.data_ptr()), 1,
+                                         self.cfg.vocab, 10, st))
+
+    def prefill(self, prompt: np.ndarray):
+        S = prompt.shape[-1]
+        self.ids[0, :S].copy_(self.torch.from_numpy(prompt.reshape(-1)))
+        self._run(self.ids[:, :S].contiguous(), S)
+        self.argmax_last(S)
+
+    def decode_step(self):
+        self._run(self.next_id, 1)
+        self.argmax_last(1)
+
+    def generate(self, prompt: np.ndarray, steps: int):
+        """Returns (tokens, ttft_s, per-step seconds)."""
+        torch = self.torch
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        self.prefill(prompt)
+        torch.cuda.synchronize()
+        ttft = time.perf_counter() - t0
+        tokens = [int(self.next_id.item())]
+        times = []
+        for _ in range(steps - 1):
+            t1 = time.perf_counter()
+            self.decode_step()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t1)
+            tokens.append(int(self.next_id.item()))
+        return tokens, ttft, times

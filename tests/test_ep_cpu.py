@@ -1,0 +1,257 @@
+"""Plugin-EP boundary on the CPU: library loading, CreateEpFactories, GetCapability.
+
+The harness host loads libonnxruntime_mi355x_ep.so exactly as ONNX Runtime's
+plugin loader would (dlopen, CreateEpFactories, GetSupportedDevices, CreateEp,
+GetCapability). Without a GPU the factory offers no device, so these sessions
+are created with force_device and stop after GetCapability: they check which
+nodes the EP claims and how it groups them into fused nodes (the reference's
+claim tests, rust/src/ep.rs:119-895 and its #[cfg(test)] partition cases).
+"""
+
+import ctypes
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import load_package
+
+pkg = load_package()
+from importlib import import_module  # noqa: E402
+
+hx = import_module(pkg.__name__ + ".harness")
+dec = import_module(pkg.__name__ + ".decoder")
+
+F16, I32, I64, U8, F32 = hx.FLOAT16, hx.INT32, hx.INT64, hx.UINT8, hx.FLOAT
+
+
+def session(g):
+    return hx.Session(g, compile=False, force_device=True)
+
+
+def mnb_node(g, x, out, N, K, name, bits=4, block=32, zp=False, dtype=F16):
+    nb = K // block
+    blob = block * bits // 8
+    g.initializer(f"{name}.B", np.zeros((N, nb, blob), np.uint8))
+    g.initializer(f"{name}.s", np.ones(N * nb, np.float16 if dtype == F16 else np.float32))
+    ins = [x, f"{name}.B", f"{name}.s"]
+    if zp:
+        g.initializer(f"{name}.zp", np.zeros(N * ((nb * bits + 7) // 8), np.uint8))
+        ins.append(f"{name}.zp")
+    g.value(out, dtype, [1, -1, N])
+    return g.node("MatMulNBits", ins, [out], domain="com.microsoft", name=name, K=K, N=N,
+                  bits=bits, block_size=block)
+
+
+def test_ep_exports_only_plugin_entry_points():
+    out = subprocess.run(["nm", "-D", "--defined-only", pkg.EP_LIB], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert exported == {"CreateEpFactories", "ReleaseEpFactory"}
+
+
+def test_create_ep_factories_contract():
+    L = ctypes.CDLL(pkg.EP_LIB)
+    create = L.CreateEpFactories
+    create.restype = ctypes.c_void_p
+    create.argtypes = [ctypes.c_char_p, ctypes.c_void_p, ctypes.c_void_p,
+                       ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t,
+                       ctypes.POINTER(ctypes.c_size_t)]
+    release = L.ReleaseEpFactory
+    release.restype = ctypes.c_void_p
+    release.argtypes = [ctypes.c_void_p]
+    h = hx.lib()
+    h.hx_api_base.restype = ctypes.c_void_p
+    base = h.hx_api_base()
+    facs = (ctypes.c_void_p * 2)()
+    n = ctypes.c_size_t(99)
+    # No room for a factory: an error status, zero factories.
+    st = create(b"MI355XExecutionProvider", base, None, facs, 0, ctypes.byref(n))
+    assert st and n.value == 0
+    # Normal registration: exactly one factory, released through ReleaseEpFactory.
+    st = create(b"MI355XExecutionProvider", base, None, facs, 2, ctypes.byref(n))
+    assert not st and n.value == 1 and facs[0]
+    assert not release(facs[0])
+    # A null API base yields no factory rather than a crash.
+    n.value = 99
+    assert not create(b"x", None, None, facs, 2, ctypes.byref(n)) and n.value == 0
+
+
+def test_no_device_offered_without_gpu_blocks_compile():
+    g = hx.Graph()
+    g.value("x", F16, [1, 1, 64])
+    mnb_node(g, "x", "y", 32, 64, "mm")
+    g.io(["x"], ["y"])
+    try:
+        import torch
+        has_gpu = torch.cuda.is_available()
+    except Exception:
+        has_gpu = False
+    if has_gpu:
+        pytest.skip("a GPU is visible")
+    with pytest.raises(RuntimeError, match="offered no device"):
+        hx.Session(g, compile=True)
+
+
+def test_single_matmulnbits_is_one_partition():
+    g = hx.Graph()
+    g.value("x", F16, [1, -1, 64])
+    mnb_node(g, "x", "y", 32, 64, "mm")
+    g.io(["x"], ["y"])
+    s = session(g)
+    assert s.partitions() == [[0]]
+
+
+@pytest.mark.parametrize("kw,claimed", [
+    (dict(bits=4, block=32), True),
+    (dict(bits=8, block=64), True),
+    (dict(bits=4, block=16, zp=True), True),
+    (dict(bits=4, block=128, dtype=F32), True),
+    (dict(bits=3, block=32), False),     # quant.rs:1697-1703 rejects other widths
+    (dict(bits=4, block=256), False),
+])
+def test_matmulnbits_claim_predicate(kw, claimed):
+    g = hx.Graph()
+    dtype = kw.get("dtype", F16)
+    g.value("x", dtype, [1, 1, 256])
+    mnb_node(g, "x", "y", 16, 256, "mm", **kw)
+    g.io(["x"], ["y"])
+    assert session(g).claimed(0) is claimed
+
+
+def test_matmulnbits_bias_input_declined():
+    g = hx.Graph()
+    g.value("x", F16, [1, 1, 64])
+    g.initializer("B", np.zeros((8, 2, 16), np.uint8))
+    g.initializer("s", np.ones(16, np.float16))
+    g.initializer("bias", np.ones(8, np.float16))
+    g.value("y", F16, [1, 1, 8])
+    g.node("MatMulNBits", ["x", "B", "s", "", "", "bias"], ["y"], domain="com.microsoft",
+           K=64, N=8, bits=4, block_size=32)
+    g.io(["x"], ["y"])
+    assert not session(g).claimed(0)
+
+
+def gqa_graph(hd=64, extra=None, inputs_extra=()):
+    g = hx.Graph()
+    H, KV, cap = 4, 2, 32
+    g.value("q", F16, [1, 1, H * hd])
+    g.value("k", F16, [1, 1, KV * hd])
+    g.value("v", F16, [1, 1, KV * hd])
+    g.value("pk", F16, [1, KV, cap, hd])
+    g.value("pv", F16, [1, KV, cap, hd])
+    g.value("sl", I32, [1])
+    g.value("tot", I32, [1])
+    g.initializer("cos", np.ones((64, hd // 2), np.float16))
+    g.initializer("sin", np.zeros((64, hd // 2), np.float16))
+    for name, dt, dims in inputs_extra:
+        g.value(name, dt, dims)
+    g.value("o", F16, [1, 1, H * hd])
+    g.value("ok", F16, [1, KV, cap, hd])
+    g.value("ov", F16, [1, KV, cap, hd])
+    ins = ["q", "k", "v", "pk", "pv", "sl", "tot", "cos", "sin"] + [n for n, _, _ in inputs_extra]
+    attrs = dict(num_heads=H, kv_num_heads=KV, do_rotary=1)
+    attrs.update(extra or {})
+    g.node("GroupQueryAttention", ins, ["o", "ok", "ov"], domain="com.microsoft", **attrs)
+    g.io([n for n in ins if n not in ("cos", "sin")], ["o", "ok", "ov"])
+    return g
+
+
+@pytest.mark.parametrize("hd,extra,ins,claimed", [
+    (128, None, (), True),
+    (64, None, (), True),
+    (96, None, (), False),                                  # head size without a kernel
+    (128, dict(softcap=30.0), (), False),
+    (128, dict(local_window_size=128), (), False),
+    (128, dict(kv_num_heads=3), (), False),                 # 4 % 3 != 0
+    (128, None, (("pos", I64, [1, 1]),), False),            # position_ids
+])
+def test_gqa_claim_predicate(hd, extra, ins, claimed):
+    assert session(gqa_graph(hd, extra, ins)).claimed(0) is claimed
+
+
+def test_unsupported_node_splits_partitions():
+    # mm0 -> Softmax (no kernel) -> mm1: two fused nodes around the declined op.
+    g = hx.Graph()
+    g.value("x", F16, [1, 1, 64])
+    mnb_node(g, "x", "a", 64, 64, "mm0")
+    g.value("b", F16, [1, 1, 64])
+    g.node("Softmax", ["a"], ["b"], axis=-1)
+    mnb_node(g, "b", "y", 32, 64, "mm1")
+    g.io(["x"], ["y"])
+    s = session(g)
+    assert not s.claimed(1)
+    assert sorted(s.partitions()) == [[0], [2]]
+
+
+def test_clusters_stay_convex():
+    # a = mm0(x); b = Softmax(a) [declined]; y = Add(a, c) with c = mm1(b).
+    # mm0 and the Add cannot share a fused node: the path mm0 -> Softmax -> mm1 -> Add
+    # leaves the cluster and re-enters it, which would make the fused graph cyclic.
+    g = hx.Graph()
+    g.value("x", F16, [1, 1, 64])
+    mnb_node(g, "x", "a", 64, 64, "mm0")
+    g.value("b", F16, [1, 1, 64])
+    g.node("Softmax", ["a"], ["b"], axis=-1)
+    mnb_node(g, "b", "c", 64, 64, "mm1")
+    g.value("y", F16, [1, 1, 64])
+    g.node("Add", ["a", "c"], ["y"])
+    g.io(["x"], ["y"])
+    s = session(g)
+    parts = s.partitions()
+    assert not s.claimed(1)
+    where = {n: i for i, p in enumerate(parts) for n in p}
+    assert where[0] != where[3]
+    # every claimed node is in exactly one partition
+    assert sorted(n for p in parts for n in p) == [0, 2, 3]
+
+
+def test_independent_branches_fuse_together():
+    g = hx.Graph()
+    g.value("x", F16, [1, 1, 64])
+    mnb_node(g, "x", "a", 64, 64, "mm0")
+    mnb_node(g, "x", "b", 64, 64, "mm1")
+    g.value("y", F16, [1, 1, 64])
+    g.node("Add", ["a", "b"], ["y"])
+    g.io(["x"], ["y"])
+    assert [sorted(p) for p in session(g).partitions()] == [[0, 1, 2]]
+
+
+def test_broadcasting_add_declined():
+    g = hx.Graph()
+    g.value("a", F16, [1, 4, 64])
+    g.value("b", F16, [1, 1, 64])
+    g.value("y", F16, [1, 4, 64])
+    g.node("Add", ["a", "b"], ["y"])
+    g.io(["a", "b"], ["y"])
+    assert not session(g).claimed(0)
+
+
+def test_norm_claims():
+    g = hx.Graph()
+    g.value("x", F16, [1, -1, 1536])
+    g.value("r", F16, [1, -1, 1536])
+    g.initializer("w", np.ones(1536, np.float16))
+    for v in ("y0", "y1", "res", "y2", "mean"):
+        g.value(v, F16, [1, -1, 1536])
+    g.node("SimplifiedLayerNormalization", ["x", "w"], ["y0"], epsilon=1e-6, axis=-1)
+    g.node("SkipSimplifiedLayerNormalization", ["x", "r", "w"], ["y1", "", "", "res"],
+           domain="com.microsoft", epsilon=1e-6)
+    g.node("SkipSimplifiedLayerNormalization", ["x", "r", "w"], ["y2", "mean"],
+           domain="com.microsoft", epsilon=1e-6)
+    g.io(["x", "r"], ["y0", "y1", "res", "y2", "mean"])
+    s = session(g)
+    assert s.claimed(0) and s.claimed(1) and not s.claimed(2)
+
+
+def test_decoder_graph_fully_claimed_as_one_fused_node():
+    cfg = dec.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, inter=512,
+                            vocab=1000, max_pos=256)
+    w = dec.make_weights(cfg, seed=0)
+    g = dec.build_graph(cfg, w, cap=64)
+    s = session(g)
+    parts = s.partitions()
+    assert len(parts) == 1
+    assert len(parts[0]) == g.n_nodes
+    # the ops of one layer: 2 norms, 7 MatMulNBits, GQA, Sigmoid + 2 Mul
+    assert g.n_nodes == 1 + cfg.layers * 13 + 2
