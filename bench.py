@@ -235,6 +235,38 @@ def bench_copy(torch, steps, warmup):
     return dict(bytes_read=n, bytes_written=n, gpu_ms=gpu_ms, gbs=2 * n / (gpu_ms * 1e-3) / 1e9)
 
 
+def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
+    """Int4 decoder through the EP: prompt prefill, then greedy decode steps.
+
+    A decode step is one EP Compute over the whole graph for one token (host
+    total_sequence_length in, argmax on the device), timed on the wall clock with
+    the device synchronised at both ends, as a serving loop sees it."""
+    import importlib
+
+    import numpy as np
+
+    dec = importlib.import_module("ortmi.decoder")
+    cfg = dec.DecoderConfig()
+    w = dec.make_weights(cfg, seed=4)
+    cap = prompt_len + gen
+    runner = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=prompt_len)
+    del w
+    prompt = np.random.default_rng(44).integers(0, cfg.vocab, size=prompt_len)
+    runner.generate(prompt[:16], steps=4)  # warm-up: allocations and first launches
+    tokens, ttft, times = runner.generate(prompt, steps=gen)
+    dec_s = float(np.sum(times))
+    tok_s = len(times) / dec_s
+    wbytes = cfg.weight_bytes()
+    # KV read per token at the mean decode context, K and V, all layers.
+    mean_ctx = prompt_len + gen / 2
+    kv = cfg.layers * 2 * cfg.kv_heads * cfg.head_dim * 2 * mean_ctx
+    per_tok = wbytes + kv
+    return dict(tok_s=tok_s, ms_per_token=dec_s / len(times) * 1e3, ttft_ms=ttft * 1e3,
+                prefill_tok_s=prompt_len / ttft, bytes_per_token=int(per_tok),
+                gbs=per_tok * tok_s / 1e9, tokens=tokens[:8], n_decode=len(times),
+                p50_ms=float(np.median(times)) * 1e3)
+
+
 def cpu_baseline_gemv(inputs, budget_s=12.0):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
@@ -265,7 +297,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "gemv", "gemm", "gqa", "paged", "copy"])
+                    choices=["all", "gemv", "gemm", "gqa", "paged", "decoder", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -323,6 +355,21 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}}
         log(f"paged: {r['gbs']:.1f} GB/s {r['tflops']:.1f} TFLOP/s ({r['gpu_ms'] * 1e3:.1f} us)")
+
+    if wl in ("all", "decoder"):
+        r = bench_decoder(torch, ortmi)
+        secondary["int4_decoder"] = {
+            "config": "28 layers, hidden 1536, 12/2 heads, hd 128, SwiGLU 8960, vocab 151936, "
+                      "int4 block 32; 512-token prompt then 128 greedy tokens, batch 1",
+            "decode_tok_s": round(r["tok_s"], 1), "ms_per_token": round(r["ms_per_token"], 3),
+            "p50_ms_per_token": round(r["p50_ms"], 3), "prefill_ms": round(r["ttft_ms"], 2),
+            "prefill_tok_s": round(r["prefill_tok_s"], 1),
+            "bytes_per_token": r["bytes_per_token"],
+            "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)},
+            "first_tokens": r["tokens"]}
+        log(f"decoder: {r['tok_s']:.1f} tok/s ({r['ms_per_token']:.3f} ms/token, p50 "
+            f"{r['p50_ms']:.3f}), prefill {r['ttft_ms']:.1f} ms")
 
     if gemv is None:
         print(json.dumps({"workload": wl, "secondary": secondary}))

@@ -936,7 +936,7 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
                                            align_up((size_t)B * S * H * hd * 4));
 
     const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-    const bool decode_fast = S == 1 && (G == 1 || G == 2 || G == 4 || G == 8) &&
+    const bool decode_fast = S == 1 && G >= 1 && G <= 8 &&
                              (!cos_c || interleaved || half % 8 == 0) && a16(q) && a16(k) &&
                              a16(v) && a16(pk) && a16(pv) && (cap == 0 || (a16(past_key) &&
                              a16(past_value)));
@@ -972,10 +972,16 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
                                fused_copy ? 1 : 0, vp, chunk, ns, KV, sc, part,
                                static_cast<T*>(output));
         };
-        if (G == 1) launch(std::integral_constant<int, 1>());
-        if (G == 2) launch(std::integral_constant<int, 2>());
-        if (G == 4) launch(std::integral_constant<int, 4>());
-        if (G == 8) launch(std::integral_constant<int, 8>());
+        switch (G) {  // query heads per KV head of common decoders (e.g. 6 and 7 in Qwen2.5)
+            case 1: launch(std::integral_constant<int, 1>()); break;
+            case 2: launch(std::integral_constant<int, 2>()); break;
+            case 3: launch(std::integral_constant<int, 3>()); break;
+            case 4: launch(std::integral_constant<int, 4>()); break;
+            case 5: launch(std::integral_constant<int, 5>()); break;
+            case 6: launch(std::integral_constant<int, 6>()); break;
+            case 7: launch(std::integral_constant<int, 7>()); break;
+            default: launch(std::integral_constant<int, 8>()); break;
+        }
         if (int rc = check_launch("gqa_decode")) return rc;
         if (ns == 1) return ORTMI_OK;
         hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(B * H), dim3(128), 0, st, part,

@@ -245,3 +245,59 @@ def rms_norm(x, gamma, eps, skip=None, bias=None, round16=False):
 def round_f16(x) -> np.ndarray:
     """Round to fp16 (RNE) and widen back to fp32."""
     return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+# ------------------------------------------------------- int4 decoder -------
+def decoder_forward(w, cfg, ids, past_k, past_v, total):
+    """One forward of the int4 Llama-style decoder graph, op by op in fp16.
+
+    The graph is the ONNX Runtime GenAI q4f16 decoder (op histogram in
+    examples/traces/qwen2.5-0.5b-decode.json): Gather -> per layer
+    (Skip)SimplifiedLayerNormalization, MatMulNBits q/k/v, GroupQueryAttention
+    with rotary on a shared KV buffer, MatMulNBits o, SkipSimplifiedLayerNorm,
+    gate/up MatMulNBits, Sigmoid/Mul/Mul, down MatMulNBits -> final
+    SkipSimplifiedLayerNorm -> lm_head MatMulNBits. Every op output is rounded
+    to fp16, as the fp16 graph stores it.
+
+    w: weight dict (int4 codes [N, K/32, 16], fp16 scales, embed, norms, cos/sin);
+    cfg: an object with layers, hidden, heads, kv_heads, head_dim, inter, vocab,
+    eps, block; ids: int array [S]; past_k/past_v: per-layer f32 [1, KV, cap, hd]
+    arrays, updated in place; total: total sequence length after this call.
+    Returns fp16-rounded logits [S, vocab] as f32.
+    """
+    r16 = round_f16
+    S = len(ids)
+    D, H, KV, hd = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
+
+    def mm(x, key, N, K):
+        return r16(mnb_matmul(x, w[key + ".B"], w[key + ".s"], None, N, K, 4, cfg.block))
+
+    h = w["embed"][np.asarray(ids)].astype(np.float32).reshape(1, S, D)
+    cos, sin = w["cos"], w["sin"]
+    down, residual = None, h
+    for layer in range(cfg.layers):
+        p = f"l{layer}"
+        if layer == 0:
+            x, _ = rms_norm(h, w[p + ".ln1"], cfg.eps, round16=True)
+        else:
+            x, residual = rms_norm(down, w[p + ".ln1"], cfg.eps, skip=residual, round16=True)
+        x = r16(x)
+        q = mm(x, p + ".q", H * hd, D)
+        k = mm(x, p + ".k", KV * hd, D)
+        v = mm(x, p + ".v", KV * hd, D)
+        out, pk, pv, shared = gqa(q, k, v, past_k[layer], past_v[layer], total, H, KV, cos, sin,
+                                  round16=True)
+        assert shared, "the decoder runs the shared-buffer KV contract"
+        past_k[layer][...] = pk
+        past_v[layer][...] = pv
+        o = mm(r16(out), p + ".o", D, H * hd)
+        x2, residual = rms_norm(o, w[p + ".ln2"], cfg.eps, skip=residual, round16=True)
+        x2 = r16(x2)
+        gate = mm(x2, p + ".gate", cfg.inter, D)
+        up = mm(x2, p + ".up", cfg.inter, D)
+        sig = r16(1.0 / (1.0 + np.exp(-gate.astype(np.float64))))
+        act = r16(r16(gate * sig) * up)
+        down = mm(act, p + ".down", D, cfg.inter)
+    xf, _ = rms_norm(down, w["final_ln"], cfg.eps, skip=residual, round16=True)
+    logits = mm(r16(xf), "lm_head", cfg.vocab, D)
+    return logits.reshape(S, cfg.vocab)

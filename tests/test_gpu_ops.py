@@ -229,6 +229,13 @@ def test_gqa_decode_shared_inplace(ortmi, oracle):
                     seed=2, base=1e6)
 
 
+@pytest.mark.parametrize("H,KV,hd", [(14, 2, 64), (6, 2, 128), (5, 1, 128), (24, 3, 128)])
+def test_gqa_decode_group_sizes(ortmi, oracle, H, KV, hd):
+    """Every query-heads-per-KV-head ratio 1..8 has a decode kernel (G = 7, 3, 5, 8 here)."""
+    assert _run_gqa(ortmi, oracle, B=2, S=1, H=H, KV=KV, hd=hd, cap=700, past=650, inplace=True,
+                    seed=H * 10 + KV, base=1e6)
+
+
 def test_gqa_decode_shared_separate_present(ortmi, oracle):
     assert _run_gqa(ortmi, oracle, B=3, S=1, H=4, KV=4, hd=64, cap=100, past=37, seed=3)
 
