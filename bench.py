@@ -267,6 +267,20 @@ def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
                 p50_ms=float(np.median(times)) * 1e3)
 
 
+def measured_traffic(profile: str):
+    """HBM bytes per launch from the committed counter summary (two rocprofv3 --pmc
+    passes, FETCH_SIZE and WRITE_SIZE, scaled by a copy of known size), or None."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", profile)
+    try:
+        with open(path) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def cpu_baseline_gemv(inputs, budget_s=12.0):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
@@ -403,7 +417,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gemv["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("mnb_gemv_k4096_n11008_f32.md"),
             "kernel": gemv["kernel"],
             "us_per_launch": round(gemv["gpu_ms"] * 1e3, 3),
             "bytes_per_launch": gemv["bytes_per_call"],

@@ -96,6 +96,30 @@ int ortmi_group_query_attention(const void* query, const void* key, const void* 
                                 size_t workspace_bytes, void* stream);
 
 /*
+ * One-token GroupQueryAttention decode step over a fixed-capacity shared KV
+ * buffer, in a form that can be captured into a HIP graph and replayed across
+ * steps: total_sequence_length is read from device memory by the kernels, and
+ * the launch shape depends only on kv_cap. kv_key/kv_value [B,KV,kv_cap,hd] are
+ * both past and present (the new row is written at total-1, in place). Results
+ * equal ortmi_group_query_attention's for seq_len = 1 under the shared-buffer
+ * contract. The caller guarantees 1 <= total <= kv_cap (and total <= max_pos
+ * with rotary); the kernels clamp the row index into the buffers regardless.
+ * Workspace: ortmi_group_query_attention_workspace_size(B, 1, H, hd, kv_cap).
+ * Returns ORTMI_E_INVALID for forms without a capturable kernel (more than 8
+ * query heads per KV head, unaligned tensors, rotary half not a multiple of 8).
+ * Replaces: the compiled-decode fast path (rust/src/engine.rs:417, 1720-1736),
+ * where a shapeless mlx_compile trace reads valid_past from a tensor so one
+ * compiled closure serves every decode step.
+ */
+int ortmi_group_query_attention_decode_capturable(
+    const void* query, const void* key, const void* value, void* kv_key, void* kv_value,
+    int64_t kv_cap, const int32_t* total_sequence_length_device, const void* cos_cache,
+    const void* sin_cache, int64_t rotary_half, int64_t max_pos, void* output, int64_t batch,
+    int64_t num_heads, int64_t kv_num_heads, int64_t head_size, float scale,
+    int32_t rotary_interleaved, int32_t dtype, void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/*
  * PagedAttention (com.microsoft), mixed prefill + decode over a block-paged KV
  * cache. query [T,H*hd], key [T,KV*hd], value [T,KV*vhd] (value == NULL and
  * value_cache == NULL selects the LATENT layout: values are the first vhd dims

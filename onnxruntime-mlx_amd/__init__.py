@@ -63,6 +63,9 @@ SIGNATURES = {
     "ortmi_group_query_attention": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
         _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
+    "ortmi_group_query_attention_decode_capturable": (ctypes.c_int, [
+        _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
+        _f32, _i32, _i32, _vp, _sz, _vp]),
     "ortmi_paged_attention_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "ortmi_paged_attention": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp,
@@ -96,6 +99,7 @@ def check(rc: int) -> None:
 from . import ops  # noqa: E402  (ops needs the loader above)
 from .ops import (  # noqa: E402,F401
     group_query_attention,
+    group_query_attention_decode_capturable,
     matmul_nbits,
     paged_attention,
     rotary_embedding,

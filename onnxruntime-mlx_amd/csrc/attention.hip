@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     int half, int interleaved, const T* __restrict__ kpast, const T* __restrict__ vpast,
     T* __restrict__ kpres, T* __restrict__ vpres, int64_t past_cap, int64_t pres_cap,
     int copy_past, int vp, int chunk, int nsplit, int KV, float scale, float* __restrict__ part,
-    T* __restrict__ out) {
+    T* __restrict__ out, const int* __restrict__ total_dev, int vp_max) {
     constexpr int LPR = HD / 8;          // lanes per row (16 bytes each)
     constexpr int RPW = 64 / LPR;        // rows per wave per step
     constexpr int RPS = 4 * RPW;         // rows per workgroup step
@@ -186,6 +186,9 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     __shared__ float s_o[4][G][HD];
     __shared__ float s_m[4][RPW][G], s_l[4][RPW][G];
 
+    // Capturable form: the past length comes from device memory (one token, so
+    // vp = total - 1), clamped to the rows the buffers and the cos/sin cache hold.
+    if (total_dev) vp = min(max(total_dev[0] - 1, 0), vp_max);
     const int bk = blockIdx.x;  // b*KV + kvh
     const int split = blockIdx.y;
     const int b = bk / KV, kvh = bk % KV;
@@ -970,7 +973,7 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
                                static_cast<const T*>(past_key), static_cast<const T*>(past_value),
                                static_cast<T*>(pk), static_cast<T*>(pv), cap, pcap,
                                fused_copy ? 1 : 0, vp, chunk, ns, KV, sc, part,
-                               static_cast<T*>(output));
+                               static_cast<T*>(output), (const int*)nullptr, 0);
         };
         switch (G) {  // query heads per KV head of common decoders (e.g. 6 and 7 in Qwen2.5)
             case 1: launch(std::integral_constant<int, 1>()); break;
@@ -1061,6 +1064,104 @@ extern "C" int ortmi_group_query_attention(
         ORTMI_GQA(uint16_t, 128);
     }
 #undef ORTMI_GQA
+    return fail(ORTMI_E_INVALID, "GroupQueryAttention: dtype must be fp16 or bf16");
+}
+
+// Capturable one-token decode step over a fixed-capacity shared KV buffer.
+template <typename T, int HD>
+static int run_gqa_decode_capturable(const void* query, const void* key, const void* value,
+                                     void* kv_key, void* kv_value, int64_t cap,
+                                     const int32_t* total_dev, const void* cos_c,
+                                     const void* sin_c, int half, int64_t max_pos, void* output,
+                                     int B, int H, int KV, float scale, int interleaved, void* ws,
+                                     size_t ws_bytes, hipStream_t st) {
+    const int G = H / KV;
+    const bool packed = key == nullptr;
+    const int64_t q_stride = packed ? (int64_t)(H + 2 * KV) * HD : (int64_t)H * HD;
+    const int64_t kv_stride = packed ? q_stride : (int64_t)KV * HD;
+    const T* q = static_cast<const T*>(query);
+    const T* k = packed ? q + (int64_t)H * HD : static_cast<const T*>(key);
+    const T* v = packed ? q + (int64_t)(H + KV) * HD : static_cast<const T*>(value);
+    const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (G < 1 || G > 8 || (cos_c && !interleaved && half % 8 != 0) || !a16(q) || !a16(k) ||
+        !a16(v) || !a16(kv_key) || !a16(kv_value))
+        return fail(ORTMI_E_INVALID, "GroupQueryAttention: form has no capturable decode kernel");
+    if (ws_bytes < ortmi_group_query_attention_workspace_size(B, 1, H, HD, cap) || !ws)
+        return fail(ORTMI_E_WORKSPACE, "GroupQueryAttention: workspace too small");
+    float* part = reinterpret_cast<float*>(static_cast<char*>(ws) +
+                                           align_up((size_t)B * H * HD * 4));
+    // Splits are sized for a full buffer; splits past the live keys contribute
+    // empty partials (max -inf, sum 0) that the merge weighs by zero.
+    int chunk = 0;
+    const int ns = gqa_nsplit((int64_t)B * KV, cap, chunk);
+    const float sc = scale != 0.f ? scale : 1.0f / sqrtf((float)HD);
+    const int vp_max = (int)std::min<int64_t>(cap, cos_c ? max_pos : cap) - 1;
+    dim3 grid(B * KV, ns);
+    auto launch = [&](auto gtag) {
+        constexpr int GG = decltype(gtag)::value;
+        hipLaunchKernelGGL((gqa_decode_kernel<T, HD, GG>), grid, dim3(256), 0, st, q, k, v,
+                           q_stride, kv_stride, static_cast<const T*>(cos_c),
+                           static_cast<const T*>(sin_c), half, interleaved,
+                           static_cast<const T*>(kv_key), static_cast<const T*>(kv_value),
+                           static_cast<T*>(kv_key), static_cast<T*>(kv_value), cap, cap, 0, 0,
+                           chunk, ns, KV, sc, part, static_cast<T*>(output), total_dev, vp_max);
+    };
+    switch (G) {
+        case 1: launch(std::integral_constant<int, 1>()); break;
+        case 2: launch(std::integral_constant<int, 2>()); break;
+        case 3: launch(std::integral_constant<int, 3>()); break;
+        case 4: launch(std::integral_constant<int, 4>()); break;
+        case 5: launch(std::integral_constant<int, 5>()); break;
+        case 6: launch(std::integral_constant<int, 6>()); break;
+        case 7: launch(std::integral_constant<int, 7>()); break;
+        default: launch(std::integral_constant<int, 8>()); break;
+    }
+    if (int rc = check_launch("gqa_decode")) return rc;
+    if (ns == 1) return ORTMI_OK;
+    hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(B * H), dim3(128), 0, st, part,
+                       static_cast<T*>(output), ns, (const int*)nullptr, HD, H, (int64_t)H * HD,
+                       (const int*)nullptr);
+    return check_launch("gqa_merge");
+}
+
+extern "C" int ortmi_group_query_attention_decode_capturable(
+    const void* query, const void* key, const void* value, void* kv_key, void* kv_value,
+    int64_t kv_cap, const int32_t* total_sequence_length_device, const void* cos_cache,
+    const void* sin_cache, int64_t rotary_half, int64_t max_pos, void* output, int64_t batch,
+    int64_t num_heads, int64_t kv_num_heads, int64_t head_size, float scale,
+    int32_t rotary_interleaved, int32_t dtype, void* workspace, size_t workspace_bytes,
+    void* stream) {
+    ORTMI_REQUIRE(num_heads > 0 && kv_num_heads > 0 && num_heads % kv_num_heads == 0,
+                  "GroupQueryAttention: num_heads must be a positive multiple of kv_num_heads");
+    ORTMI_REQUIRE(head_size == 64 || head_size == 128,
+                  "GroupQueryAttention: head_size must be 64 or 128");
+    ORTMI_REQUIRE(batch > 0 && kv_cap > 0, "GroupQueryAttention: bad shape");
+    ORTMI_REQUIRE(query && output && kv_key && kv_value && total_sequence_length_device,
+                  "GroupQueryAttention: null tensor");
+    ORTMI_REQUIRE((key == nullptr) == (value == nullptr),
+                  "GroupQueryAttention: key and value must both be given or both be packed");
+    const bool rotary = cos_cache != nullptr;
+    ORTMI_REQUIRE(rotary == (sin_cache != nullptr),
+                  "GroupQueryAttention: cos_cache and sin_cache must both be given");
+    if (rotary)
+        ORTMI_REQUIRE(rotary_half > 0 && 2 * rotary_half <= head_size && max_pos > 0,
+                      "GroupQueryAttention: rotary dim exceeds head_size");
+    hipStream_t st = as_stream(stream);
+    const int B = (int)batch, H = (int)num_heads, KV = (int)kv_num_heads;
+#define ORTMI_GQA_CAP(T, HD)                                                                   \
+    return run_gqa_decode_capturable<T, HD>(query, key, value, kv_key, kv_value, kv_cap,       \
+                                            total_sequence_length_device, cos_cache, sin_cache, \
+                                            (int)rotary_half, max_pos, output, B, H, KV, scale, \
+                                            rotary_interleaved, workspace, workspace_bytes, st)
+    if (dtype == ORTMI_F16) {
+        if (head_size == 64) ORTMI_GQA_CAP(half_t, 64);
+        ORTMI_GQA_CAP(half_t, 128);
+    }
+    if (dtype == ORTMI_BF16) {
+        if (head_size == 64) ORTMI_GQA_CAP(uint16_t, 64);
+        ORTMI_GQA_CAP(uint16_t, 128);
+    }
+#undef ORTMI_GQA_CAP
     return fail(ORTMI_E_INVALID, "GroupQueryAttention: dtype must be fp16 or bf16");
 }
 

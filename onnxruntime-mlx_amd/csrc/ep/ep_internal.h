@@ -130,11 +130,36 @@ class Plan {
             return n;
         }
     };
+    // Launch signature of one input: its device address (null for host inputs,
+    // which are staged into a fixed buffer), element type and shape.
+    struct InputSig {
+        const void* ptr = nullptr;
+        int dtype = 0;
+        std::vector<int64_t> dims;
+        bool operator==(const InputSig& o) const {
+            return ptr == o.ptr && dtype == o.dtype && dims == o.dims;
+        }
+    };
+    // A host scalar a captured graph depends on: 1 <= value <= hi.
+    struct Guard {
+        std::string name;
+        int64_t hi = 0;
+    };
+    struct OutputRec {
+        size_t index = 0;
+        std::vector<int64_t> dims;
+        void* ptr = nullptr;
+    };
+
     void* arena_alloc(size_t bytes);
+    void* workspace(size_t bytes);
     Tensor& out_tensor(const std::string& name, int dtype, const std::vector<int64_t>& dims,
                        const OrtApi* api, OrtKernelContext* ctx);
     void run_node(const NodeDesc& n, const OrtApi* api, OrtKernelContext* ctx);
     int32_t host_i32(const std::string& name);
+    bool guards_hold(const std::vector<Guard>& guards) const;
+    bool replay(const OrtApi* api, OrtKernelContext* ctx);
+    bool capture(const OrtApi* api, OrtKernelContext* ctx, const std::vector<InputSig>& sig);
 
     GraphIR sub_;
     std::vector<std::string> inputs_, outputs_;
@@ -149,7 +174,28 @@ class Plan {
     size_t arena_off_ = 0;
     size_t arena_need_ = 0;
     std::unique_ptr<DeviceBuffer> workspace_;
+    std::vector<std::unique_ptr<DeviceBuffer>> stage_;   // per input: host-input staging
+    std::vector<std::pair<const void*, bool>> devptr_;   // per input: last pointer, is device
     std::mutex mu_;  // one Compute at a time per fused node (rust/src/ep.rs:1884-1889)
+
+    // HIP-graph replay of a whole Compute. A run whose every launch is graph-safe
+    // (no host round trip, no host-memory output, decode attention reading the
+    // sequence length from device memory) marks its signature capturable; the
+    // next run with the same signature is captured, later ones replay the graph.
+    // Any device (re)allocation bumps mem_epoch_ and retires the graph.
+    bool graphs_enabled_ = true;
+    bool capturable_ = false;      // the current run so far is graph-safe
+    bool capturing_ = false;
+    uint64_t mem_epoch_ = 0;
+    std::vector<Guard> guards_;
+    std::vector<OutputRec> outs_;
+    std::vector<InputSig> last_sig_;
+    bool last_capturable_ = false;
+    hipGraphExec_t graph_exec_ = nullptr;
+    std::vector<InputSig> graph_sig_;
+    std::vector<Guard> graph_guards_;
+    std::vector<OutputRec> graph_outs_;
+    uint64_t graph_epoch_ = 0;
 };
 
 size_t dtype_size(int dtype);

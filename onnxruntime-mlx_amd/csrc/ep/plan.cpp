@@ -94,6 +94,7 @@ Plan::Plan(GraphIR sub, std::vector<std::string> inputs, std::vector<std::string
     : sub_(std::move(sub)), inputs_(std::move(inputs)), outputs_(std::move(outputs)),
       device_(device) {
     fuse_swiglu(sub_, outputs_);
+    if (const char* g = std::getenv("ORTMI_EP_GRAPH")) graphs_enabled_ = std::strcmp(g, "0") != 0;
     check_hip(hipSetDevice(device_), "hipSetDevice");
     check_hip(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
     for (size_t i = 0; i < outputs_.size(); ++i)
@@ -113,7 +114,18 @@ Plan::Plan(GraphIR sub, std::vector<std::string> inputs, std::vector<std::string
 }
 
 Plan::~Plan() {
+    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
     if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void* Plan::workspace(size_t bytes) {
+    if (!workspace_ || workspace_->bytes < bytes) {
+        if (capturing_) fail("workspace growth during graph capture");
+        workspace_.reset();
+        workspace_ = device_alloc(bytes);
+        ++mem_epoch_;
+    }
+    return workspace_->ptr;
 }
 
 void* Plan::arena_alloc(size_t bytes) {
@@ -132,8 +144,10 @@ void* Plan::arena_alloc(size_t bytes) {
         }
         base += ch->bytes;
     }
+    if (capturing_) fail("arena growth during graph capture");
     size_t grow = std::max(bytes, (size_t)64 << 20);
     arena_.push_back(device_alloc(grow));
+    ++mem_epoch_;
     arena_off_ = base + bytes;
     return arena_.back()->ptr;
 }
@@ -145,6 +159,8 @@ int32_t Plan::host_i32(const std::string& name) {
     if (it == env_.end()) fail("missing scalar input " + name);
     int32_t v = 0;
     if (is_device_ptr(it->second.ptr)) {
+        if (capturing_) fail("host read of a device scalar during graph capture");
+        capturable_ = false;
         check_hip(hipMemcpyAsync(&v, it->second.ptr, 4, hipMemcpyDeviceToHost, stream_), "read scalar");
         check_hip(hipStreamSynchronize(stream_), "read scalar");
     } else {
@@ -178,7 +194,10 @@ Plan::Tensor& Plan::out_tensor(const std::string& name, int dtype,
                   "KernelContext_GetOutput");
         void* p = nullptr;
         check_ort(a, api::GetTensorMutableData(a)(ov, &p), "GetTensorMutableData");
+        outs_.push_back({(size_t)oi->second, dims, p});
         if (bytes && !is_device_ptr(p)) {
+            if (capturing_) fail("host-memory output during graph capture");
+            capturable_ = false;
             void* d = arena_alloc(bytes);
             g_out_staging->push_back({p, d, bytes});
             p = d;
@@ -191,6 +210,68 @@ Plan::Tensor& Plan::out_tensor(const std::string& name, int dtype,
     return env_[name];
 }
 
+bool Plan::guards_hold(const std::vector<Guard>& guards) const {
+    for (const Guard& g : guards) {
+        auto it = host_scalars_.find(g.name);
+        if (it == host_scalars_.end() || it->second < 1 || it->second > g.hi) return false;
+    }
+    return true;
+}
+
+// Replay the captured graph when every output lands where it did at capture.
+bool Plan::replay(const OrtApi* a, OrtKernelContext* ctx) {
+    for (const OutputRec& o : graph_outs_) {
+        OrtValue* ov = nullptr;
+        check_ort(a, api::KernelContext_GetOutput(a)(ctx, o.index, o.dims.data(), o.dims.size(), &ov),
+                  "KernelContext_GetOutput");
+        void* p = nullptr;
+        check_ort(a, api::GetTensorMutableData(a)(ov, &p), "GetTensorMutableData");
+        if (p != o.ptr) return false;
+    }
+    check_hip(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+    return true;
+}
+
+// Capture this run's launches into a graph and launch it. Returns false, with
+// nothing enqueued, when some launch turns out not to be graph-safe.
+bool Plan::capture(const OrtApi* a, OrtKernelContext* ctx, const std::vector<InputSig>& sig) {
+    const auto saved_env = env_;
+    const size_t saved_off = arena_off_;
+    capturing_ = true;
+    capturable_ = true;
+    guards_.clear();
+    outs_.clear();
+    hipGraph_t graph = nullptr;
+    bool ok = hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal) == hipSuccess;
+    if (ok) {
+        try {
+            for (const NodeDesc& n : sub_.nodes) run_node(n, a, ctx);
+        } catch (const std::exception&) {
+            ok = false;
+        }
+        ok = hipStreamEndCapture(stream_, &graph) == hipSuccess && ok && capturable_;
+    }
+    capturing_ = false;
+    hipGraphExec_t exec = nullptr;
+    if (ok) ok = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) == hipSuccess;
+    if (graph) (void)hipGraphDestroy(graph);
+    if (!ok) {
+        (void)hipGetLastError();
+        env_ = saved_env;
+        arena_off_ = saved_off;
+        last_capturable_ = false;
+        return false;
+    }
+    if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+    graph_exec_ = exec;
+    graph_sig_ = sig;
+    graph_guards_ = guards_;
+    graph_outs_ = outs_;
+    graph_epoch_ = mem_epoch_;
+    check_hip(hipGraphLaunch(graph_exec_, stream_), "hipGraphLaunch");
+    return true;
+}
+
 void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
     std::lock_guard<std::mutex> lock(mu_);
     check_hip(hipSetDevice(device_), "hipSetDevice");
@@ -199,6 +280,9 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
     arena_off_ = 0;
     std::vector<Staged> out_staging;
     g_out_staging = &out_staging;
+    if (stage_.size() < inputs_.size()) stage_.resize(inputs_.size());
+    if (devptr_.size() < inputs_.size()) devptr_.resize(inputs_.size(), {nullptr, false});
+    std::vector<InputSig> sig(inputs_.size());
     for (size_t i = 0; i < inputs_.size(); ++i) {
         if (inputs_[i].empty()) continue;
         const OrtValue* v = nullptr;
@@ -221,21 +305,30 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
         const void* p = nullptr;
         check_ort(a, api::GetTensorData(a)(v, &p), "GetTensorData");
         const size_t bytes = (size_t)std::max<int64_t>(t.numel(), 0) * dtype_size(et);
-        if (bytes && !is_device_ptr(p)) {
-            // Host-memory input: stage it into HBM (the boundary copy that a GPU
-            // memory device would make unnecessary).
-            void* d = arena_alloc(bytes);
-            check_hip(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, stream_), "stage input");
-            host_scalars_.erase(inputs_[i]);
-            t.ptr = d;
+        if (devptr_[i].first != p || !p) devptr_[i] = {p, is_device_ptr(p)};
+        sig[i].dtype = et;
+        sig[i].dims = t.dims;
+        if (bytes && !devptr_[i].second) {
+            // Host-memory input: staged into a buffer of its own (a fixed address,
+            // so graphs can read it), e.g. total_sequence_length, which ONNX
+            // Runtime keeps in CPU memory.
+            auto& buf = stage_[i];
+            if (!buf || buf->bytes < bytes) {
+                buf = device_alloc(std::max<size_t>(bytes, 256));
+                ++mem_epoch_;
+            }
+            check_hip(hipMemcpyAsync(buf->ptr, p, bytes, hipMemcpyHostToDevice, stream_),
+                      "stage input");
+            t.ptr = buf->ptr;
             // keep the host copy for scalar reads without a device round trip
-            if (bytes == 4) {
+            if (bytes == 4 && (et == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT32)) {
                 int32_t hv;
                 std::memcpy(&hv, p, 4);
                 host_scalars_[inputs_[i]] = hv;
             }
         } else {
             t.ptr = const_cast<void*>(p);
+            sig[i].ptr = p;
         }
         env_[inputs_[i]] = t;
     }
@@ -247,12 +340,33 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
         t.dims = v.dims;
         env_[kv.first] = t;
     }
+    if (graphs_enabled_) {
+        if (graph_exec_ && graph_epoch_ != mem_epoch_) {
+            (void)hipGraphExecDestroy(graph_exec_);
+            graph_exec_ = nullptr;
+        }
+        bool done = false;
+        if (graph_exec_ && sig == graph_sig_ && guards_hold(graph_guards_))
+            done = replay(a, ctx);
+        else if (last_capturable_ && sig == last_sig_ && guards_hold(guards_))
+            done = capture(a, ctx, sig);
+        if (done) {
+            check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+            g_out_staging = nullptr;
+            return;
+        }
+    }
+    capturable_ = true;
+    guards_.clear();
+    outs_.clear();
     for (const NodeDesc& n : sub_.nodes) run_node(n, a, ctx);
     for (const Staged& s : out_staging)
         check_hip(hipMemcpyAsync(s.host, s.dev, s.bytes, hipMemcpyDeviceToHost, stream_),
                   "stage output");
     check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
     g_out_staging = nullptr;
+    last_sig_ = std::move(sig);
+    last_capturable_ = capturable_ && out_staging.empty();
 }
 
 // ------------------------------------------------------------ op dispatch --
@@ -341,17 +455,38 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         else prk = arena_alloc((size_t)(B * KV * pcap * hd) * dtype_size(q.dtype));
         if (!outname(2).empty()) prv = out_tensor(outname(2), q.dtype, {B, KV, pcap, hd}, a, ctx).ptr;
         else prv = arena_alloc((size_t)(B * KV * pcap * hd) * dtype_size(q.dtype));
+        const float scale = n.attr_float("scale", 0.f);
+        const int32_t inter = (int32_t)n.attr_int("rotary_interleaved", 0);
+        // One-token decode into a shared buffer written in place: the capturable
+        // kernels read total_sequence_length from device memory, so the step can
+        // be replayed from a graph. Eager runs take the same kernels, so replayed
+        // and eager steps give identical results.
+        if (S == 1 && shared && pk && pv && prk == pkp && prv == pvp &&
+            host_scalars_.count(n.inputs[6]) && (!cs || total <= max_pos)) {
+            const size_t wsb = ortmi_group_query_attention_workspace_size(B, 1, H, hd, cap);
+            void* ws = workspace(wsb);
+            const int rc = ortmi_group_query_attention_decode_capturable(
+                q.ptr, kptr, vptr, prk, prv, cap, (const int32_t*)env_.at(n.inputs[6]).ptr, csp,
+                snp, half, max_pos, optr, B, H, KV, hd, scale, inter, kdt(q.dtype), ws, wsb, st);
+            if (rc == ORTMI_OK) {
+                guards_.push_back({n.inputs[6], cs ? std::min<int64_t>(cap, max_pos) : cap});
+                return;
+            }
+            if (rc != ORTMI_E_INVALID) check_kernel(rc, "GroupQueryAttention");
+        }
+        if (capturing_) fail("GroupQueryAttention form is not capturable");
+        capturable_ = false;
         const size_t wsb = ortmi_group_query_attention_workspace_size(B, S, H, hd, vpast + S);
-        if (!workspace_ || workspace_->bytes < wsb) workspace_ = device_alloc(wsb);
-        check_kernel(ortmi_group_query_attention(
-                         q.ptr, kptr, vptr, pkp, pvp, cap, total, csp, snp, half, max_pos, optr, prk,
-                         prv, B, S, H, KV, hd, n.attr_float("scale", 0.f),
-                         (int32_t)n.attr_int("rotary_interleaved", 0), kdt(q.dtype),
-                         workspace_->ptr, workspace_->bytes, st),
+        void* ws = workspace(wsb);
+        check_kernel(ortmi_group_query_attention(q.ptr, kptr, vptr, pkp, pvp, cap, total, csp, snp,
+                                                 half, max_pos, optr, prk, prv, B, S, H, KV, hd,
+                                                 scale, inter, kdt(q.dtype), ws, wsb, st),
                      "GroupQueryAttention");
         return;
     }
     if (op == "PagedAttention") {
+        if (capturing_) fail("PagedAttention is not captured");
+        capturable_ = false;
         Tensor q = need(0);
         Tensor k = need(1);
         Tensor* v = in(2);
@@ -373,7 +508,7 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         const int64_t max_ctx = maxb * blk;
         Tensor& O = out_tensor(outname(0), q.dtype, {T, H * vhd}, a, ctx);
         const size_t wsb = ortmi_paged_attention_workspace_size(T, batch, H, KV, hd, vhd, max_ctx);
-        if (!workspace_ || workspace_->bytes < wsb) workspace_ = device_alloc(wsb);
+        workspace(wsb);
         check_kernel(ortmi_paged_attention(
                          q.ptr, k.ptr, latent ? nullptr : (v ? v->ptr : nullptr), kc.ptr,
                          latent ? nullptr : (vc ? vc->ptr : nullptr), nblk, blk,

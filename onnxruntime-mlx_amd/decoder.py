@@ -212,9 +212,16 @@ class DecoderRunner:
         self.ids = torch.zeros((1, max_prompt), dtype=torch.int64, device=dev)
         self.next_id = torch.zeros((1, 1), dtype=torch.int64, device=dev)
         self.seqlens = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.total = torch.zeros(1, dtype=torch.int32)  # host memory
+        # total_sequence_length lives in (pinned) host memory, as ONNX Runtime keeps it.
+        self.total = torch.zeros(1, dtype=torch.int32, pin_memory=True)
         self.length = 0
         self.lib = load_kernels()
+        # Inputs that keep their buffers for the whole generation are bound once.
+        self.session.set_input("seqlens_k", self.seqlens, hx.INT32)
+        self.session.set_input("total_sequence_length", self.total, hx.INT32)
+        for layer, (k, v) in enumerate(self.kv):
+            self.session.set_input(f"past_key_values.{layer}.key", k, hx.FLOAT16)
+            self.session.set_input(f"past_key_values.{layer}.value", v, hx.FLOAT16)
 
     def reset(self):
         self.length = 0
@@ -223,16 +230,11 @@ class DecoderRunner:
         """Forward S new tokens (device int64 [1, S]); logits land in self.logits[:, :S]."""
         if self.length + S > self.cap:
             raise ValueError(f"KV capacity {self.cap} exceeded")
-        self.total[0] = self.length + S
         self.seqlens.fill_(self.length + S - 1)
-        feeds = {"input_ids": (ids, hx.INT64), "seqlens_k": (self.seqlens, hx.INT32),
-                 "total_sequence_length": (self.total, hx.INT32)}
-        for layer, (k, v) in enumerate(self.kv):
-            feeds[f"past_key_values.{layer}.key"] = (k, hx.FLOAT16)
-            feeds[f"past_key_values.{layer}.value"] = (v, hx.FLOAT16)
         # The EP is not stream aware: like ONNX Runtime, hand it inputs that are ready.
         self.torch.cuda.current_stream().synchronize()
-        self.session.run(feeds)
+        self.total[0] = self.length + S
+        self.session.run({"input_ids": (ids, hx.INT64)})
         self.length += S
 
     def argmax_last(self, S: int):

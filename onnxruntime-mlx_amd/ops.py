@@ -131,6 +131,39 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
     return out, present_key, present_value
 
 
+def group_query_attention_decode_capturable(query, key, value, kv_key, kv_value,
+                                            total_sequence_length_device, cos_cache=None,
+                                            sin_cache=None, *, num_heads, kv_num_heads,
+                                            scale=0.0, rotary_interleaved=0, workspace=None,
+                                            stream=None):
+    """One-token GroupQueryAttention step, shared KV buffer updated in place, with
+    total_sequence_length read from a device int32 tensor (graph-capturable: the
+    launches depend only on the buffer capacity). Returns the output [B, 1, H*hd].
+
+    Equal to group_query_attention(..., present_key=kv_key, present_value=kv_value)
+    for S = 1 under the shared-buffer contract; the caller keeps
+    1 <= total <= capacity. Pass a preallocated `workspace` (uint8 device tensor)
+    when capturing, so no allocation happens inside the capture."""
+    B, S, hidden = query.shape
+    if S != 1:
+        raise ValueError("capturable GroupQueryAttention decodes one token")
+    hd = hidden // num_heads
+    cap = kv_key.shape[2]
+    out = torch.empty((B, 1, num_heads * hd), dtype=query.dtype, device=query.device)
+    lib = load_kernels()
+    ws_bytes = lib.ortmi_group_query_attention_workspace_size(B, 1, num_heads, hd, cap)
+    ws = workspace if workspace is not None else _workspace(ws_bytes, query.device)
+    half = cos_cache.shape[1] if cos_cache is not None else 0
+    max_pos = cos_cache.shape[0] if cos_cache is not None else 0
+    check(lib.ortmi_group_query_attention_decode_capturable(
+        _p(query), _p(key), _p(value), _p(kv_key), _p(kv_value), cap,
+        _p(total_sequence_length_device), _p(cos_cache) if cos_cache is not None else None,
+        _p(sin_cache) if sin_cache is not None else None, half, max_pos, _p(out), B, num_heads,
+        kv_num_heads, hd, float(scale), int(rotary_interleaved), _dt(query), _p(ws), ws.numel(),
+        _stream(stream)))
+    return out
+
+
 # --------------------------------------------------------------- PagedAttention
 def paged_attention(query, key, value, key_cache, value_cache, cumulative_sequence_length,
                     past_seqlens, block_table, cos_cache=None, sin_cache=None, slot_mapping=None,

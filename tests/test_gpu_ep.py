@@ -241,3 +241,28 @@ def test_ep_decoder_prefill_matches_incremental_decode(ortmi, dec):
     tok = int(runner.next_id.item())
     if tok != tokens[-1]:  # prefill (MFMA GEMM) and decode (GEMV) may split a near tie
         assert float(pre[tok] - pre[tokens[-1]]) <= 2 * err
+
+
+def test_ep_decode_graph_replay_matches_eager(ortmi, dec, monkeypatch):
+    """Decode steps replayed from the EP's captured HIP graph equal eager steps bit
+    for bit (same kernels), across a fresh prefill between generations."""
+    cfg = _small_cfg(dec, 128)
+    w = dec.make_weights(cfg, seed=21)
+    prompt = np.random.default_rng(22).integers(0, cfg.vocab, size=20)
+
+    def run(graphs):
+        monkeypatch.setenv("ORTMI_EP_GRAPH", "1" if graphs else "0")
+        r = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
+        seen = []
+        for rep in range(2):
+            r.reset()
+            r.prefill(prompt[: 20 - 4 * rep])
+            seen.append(host(r.logits[0, :1]))
+            for _ in range(8):
+                r.decode_step()
+                seen.append(host(r.logits[0, :1]))
+        return np.stack(seen)
+
+    eager = run(False)
+    graphed = run(True)
+    np.testing.assert_array_equal(graphed, eager)

@@ -236,6 +236,56 @@ def test_gqa_decode_group_sizes(ortmi, oracle, H, KV, hd):
                     seed=H * 10 + KV, base=1e6)
 
 
+@pytest.mark.parametrize("H,KV,hd", [(12, 2, 128), (32, 8, 128), (8, 8, 64)])
+def test_gqa_decode_capturable(ortmi, oracle, H, KV, hd):
+    """Device-resident total_sequence_length: equal to the oracle, and a HIP graph
+    captured at one length and replayed at others equals eager calls bit for bit."""
+    import torch
+
+    rng = np.random.default_rng(H + KV + hd)
+    B, cap, past = 2, 300, 140
+    q, k, v, pk, pv, cos, sin = _gqa_inputs(rng, B, 1, H, KV, hd, cap, True, 1e6)
+    dcos, dsin = dev(cos), dev(sin)
+    tot = torch.tensor([past + 1], dtype=torch.int32, device="cuda")
+    dpk, dpv = dev(pk), dev(pv)
+    out = ortmi.group_query_attention_decode_capturable(
+        dev(q), dev(k), dev(v), dpk, dpv, tot, dcos, dsin, num_heads=H, kv_num_heads=KV)
+    ro, rk, rv, shared = oracle.gqa(q, k, v, pk, pv, past + 1, H, KV, cos=cos, sin=sin,
+                                    round16=True)
+    assert shared
+    assert_f16_close(host(out), ro, what="capturable gqa")
+    np.testing.assert_array_equal(host(dpv), rv.astype(np.float16).astype(np.float32))
+    old = np.ones(cap, bool)
+    old[past] = False
+    np.testing.assert_array_equal(host(dpk)[:, :, old], pk.astype(np.float32)[:, :, old])
+
+    # Graph captured at total = 61, replayed at 62..64 with eager work in between.
+    sq, sk, sv = dev(q), dev(k), dev(v)
+    kg, vg = dev(pk), dev(pv)
+    ke, ve = dev(pk), dev(pv)
+    ws = torch.empty(ortmi.load_kernels().ortmi_group_query_attention_workspace_size(
+        B, 1, H, hd, cap), dtype=torch.uint8, device="cuda")
+    tg = torch.tensor([61], dtype=torch.int32, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout = ortmi.group_query_attention_decode_capturable(
+            sq, sk, sv, kg, vg, tg, dcos, dsin, num_heads=H, kv_num_heads=KV, workspace=ws)
+    for t in (62, 63, 64):
+        step = rng.standard_normal((3, B, 1, max(H, KV) * hd)).astype(np.float16)
+        sq.copy_(dev(step[0][..., :H * hd]))
+        sk.copy_(dev(step[1][..., :KV * hd]))
+        sv.copy_(dev(step[2][..., :KV * hd]))
+        tg.fill_(t)
+        graph.replay()
+        torch.cuda.synchronize()
+        te = torch.tensor([t], dtype=torch.int32, device="cuda")
+        eout = ortmi.group_query_attention_decode_capturable(
+            sq, sk, sv, ke, ve, te, dcos, dsin, num_heads=H, kv_num_heads=KV)
+        torch.cuda.synchronize()
+        assert torch.equal(gout, eout), f"replay at total={t} differs from eager"
+        assert torch.equal(kg, ke) and torch.equal(vg, ve)
+
+
 def test_gqa_decode_shared_separate_present(ortmi, oracle):
     assert _run_gqa(ortmi, oracle, B=3, S=1, H=4, KV=4, hd=64, cap=100, past=37, seed=3)
 

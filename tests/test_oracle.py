@@ -9,6 +9,9 @@ tests' numpy references (tests/refs.py). CPU only.
 
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import pytest
 import refs
@@ -35,29 +38,25 @@ def test_f16_conversions_match_ieee(oracle):
 
 
 def _gbq_fixture():
-    """Known-answer data of tests/ops/_models.py:558-580: two rows of 32 codes,
-    code k of row r = (k + r) & 15, packed low nibble first, block 16, scales
-    [[0.5, 1], [2, 4]], symmetric (zero point 8)."""
-    qdata = np.empty((2, 16), np.uint8)
-    for row in range(2):
-        vals = (np.arange(32, dtype=np.uint8) + row) & 0x0F
-        qdata[row] = vals[0::2] | (vals[1::2] << 4)
-    scales = np.array([[0.5, 1.0], [2.0, 4.0]], np.float32)
-    return qdata, scales
+    """Known-answer case of tests/ops/_models.py:558-580 as committed in
+    tests/golden/gbq_kat.json (packed bytes, scales, indices and the expected
+    gathered rows written from the definition of the codes)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "gbq_kat.json")
+    with open(path) as f:
+        kat = json.load(f)
+    return (np.array(kat["data_uint8"], np.uint8), np.array(kat["scales_f32"], np.float32),
+            np.array(kat["indices_int64"], np.int64), np.array(kat["expected_f32"], np.float32))
 
 
 def test_mnb_dequant_known_answer(oracle):
-    qdata, scales = _gbq_fixture()
+    qdata, scales, indices, expected = _gbq_fixture()
     W = oracle.mnb_dequant(qdata, scales, None, N=2, K=32, bits=4, block=16)
-    # Closed form of the fixture, written out by hand: w[r,k] = (((k+r)&15) - 8) * s[r, k//16].
-    expected = np.array([[(((k + r) & 15) - 8) * scales[r, k // 16] for k in range(32)]
-                         for r in range(2)], np.float32)
-    np.testing.assert_array_equal(W, expected)
-    # The GatherBlockQuantized op of that test gathers rows [1, -2] -> [1, 0].
-    np.testing.assert_array_equal(W[[1, 0]], expected[[1, 0]])
+    # GatherBlockQuantized gathers rows [1, -2] -> [1, 0] of the dequantised table.
+    np.testing.assert_array_equal(W[indices % 2], expected)
     # A nibble-order mistake would not pass: swapping nibbles changes the table.
     swapped = ((qdata & 0x0F) << 4) | (qdata >> 4)
-    assert not np.array_equal(oracle.mnb_dequant(swapped, scales, None, 2, 32, 4, 16), expected)
+    assert not np.array_equal(oracle.mnb_dequant(swapped, scales, None, 2, 32, 4, 16)[indices % 2],
+                              expected)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
