@@ -67,6 +67,32 @@ int ortmi_matmul_nbits(const void* A, const uint8_t* B, const void* scales,
                        int64_t bits, int64_t block_size, int32_t dtype, void* stream);
 
 /*
+ * MatMulNBits decode step (M = 1, 4-bit, block 32/64/128, fp16/bf16) with its
+ * graph neighbours fused in; flags select what is fused:
+ *  - ORTMI_FUSE_RMS_NORM: the activation row is first normalised,
+ *    a = (x [+ skip]) / sqrt(mean((x [+ skip])^2) + epsilon) * gamma, each
+ *    result rounded to dtype as the unfused ops store it; skip is optional, and
+ *    residual (optional, needs skip) receives x + skip ([K]).
+ *    Replaces: mlx_fast_rms_norm of (Skip)SimplifiedLayerNormalization
+ *    (rust/src/ops/norm.rs:164-248) feeding quantized_matmul (quant.rs:570-601).
+ *  - ORTMI_FUSE_SWIGLU_PAIRS: B holds N rows interleaved gate/up (row 2i = gate
+ *    row i, row 2i+1 = up row i, scales and zero points likewise) and
+ *    Y[i] = (g * sigmoid(g)) * u for i < N/2, each op rounded to dtype.
+ *    Replaces: the two gate/up quantized_matmul calls and the
+ *    Sigmoid/Mul/Mul translation (rust/src/ops/elementwise.rs:928-980).
+ * x, skip, gamma, residual: [K]; Y: [N] (or [N/2] with SwiGLU pairs).
+ */
+enum {
+    ORTMI_FUSE_RMS_NORM = 1,
+    ORTMI_FUSE_SWIGLU_PAIRS = 2,
+};
+int ortmi_matmul_nbits_decode_fused(const void* x, const void* skip, const void* gamma,
+                                    float epsilon, void* residual, const uint8_t* B,
+                                    const void* scales, const uint8_t* zero_points, void* Y,
+                                    int64_t N, int64_t K, int64_t block_size, int32_t flags,
+                                    int32_t dtype, void* stream);
+
+/*
  * GroupQueryAttention (com.microsoft), decode and prefill, with in-op RoPE.
  * query [B,S,H*hd] (or packed [B,S,(H+2*KV)*hd] when key == value == NULL),
  * key/value [B,S,KV*hd]; past_key/past_value [B,KV,past_cap,hd].
@@ -192,21 +218,31 @@ int ortmi_rms_norm(const void* x, const void* skip, const void* bias, const void
  *    returned status only when checked on the host by the caller).
  *  - ortmi_swiglu: out = (g * sigmoid(g)) * u, each op rounded to dtype as the
  *    Sigmoid/Mul/Mul graph does.
+ *  - ortmi_swiglu_pairs: the same over interleaved gate/up columns, y [rows, 2P]
+ *    (column 2i gate, 2i+1 up) -> out [rows, P]; the prefill side of the
+ *    SwiGLU-pairs fusion of ortmi_matmul_nbits_decode_fused.
  *  - ortmi_binary: elementwise Add (op 0) / Mul (op 1) / Sub (op 2) of
  *    same-shape tensors.
  *  - ortmi_sigmoid: elementwise Sigmoid.
- *  - ortmi_argmax_rows: int64 index of the max of each row (first on ties).
+ *  - ortmi_argmax_rows: int64 index of the max of each row (first on ties; NaN
+ *    never wins). With a workspace of ortmi_argmax_rows_workspace_size bytes,
+ *    long rows are reduced by many workgroups in two passes; with workspace =
+ *    NULL one workgroup scans each row. Greedy decoding takes it over the last
+ *    logits row (the reference's callers do this on the host after Compute).
  *  - ortmi_cast: f32 <-> f16 <-> bf16.
  */
 int ortmi_gather_rows(const void* table, const int64_t* ids, void* out, int64_t num_ids,
                       int64_t vocab, int64_t D, int32_t dtype, void* stream);
 int ortmi_swiglu(const void* gate, const void* up, void* out, int64_t n, int32_t dtype,
                  void* stream);
+int ortmi_swiglu_pairs(const void* y, void* out, int64_t rows, int64_t pairs, int32_t dtype,
+                       void* stream);
 int ortmi_binary(int32_t op, const void* a, const void* b, void* out, int64_t n,
                  int32_t dtype, void* stream);
 int ortmi_sigmoid(const void* x, void* out, int64_t n, int32_t dtype, void* stream);
+size_t ortmi_argmax_rows_workspace_size(int64_t rows, int64_t cols);
 int ortmi_argmax_rows(const void* x, int64_t* out, int64_t rows, int64_t cols, int32_t dtype,
-                      void* stream);
+                      void* workspace, size_t workspace_bytes, void* stream);
 int ortmi_cast(const void* x, int32_t src_dtype, void* y, int32_t dst_dtype, int64_t n,
                void* stream);
 

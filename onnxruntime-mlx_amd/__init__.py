@@ -59,6 +59,8 @@ SIGNATURES = {
     "ortmi_last_error": (ctypes.c_char_p, []),
     "ortmi_matmul_nbits": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                           _i32, _vp]),
+    "ortmi_matmul_nbits_decode_fused": (ctypes.c_int, [
+        _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
     "ortmi_group_query_attention_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "ortmi_group_query_attention": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
@@ -76,9 +78,11 @@ SIGNATURES = {
     "ortmi_rms_norm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "ortmi_gather_rows": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
     "ortmi_swiglu": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _vp]),
+    "ortmi_swiglu_pairs": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp]),
     "ortmi_binary": (ctypes.c_int, [_i32, _vp, _vp, _vp, _i64, _i32, _vp]),
     "ortmi_sigmoid": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp]),
-    "ortmi_argmax_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp]),
+    "ortmi_argmax_rows_workspace_size": (_sz, [_i64, _i64]),
+    "ortmi_argmax_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp, _sz, _vp]),
     "ortmi_cast": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _vp]),
 }
 

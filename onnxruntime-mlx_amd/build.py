@@ -23,7 +23,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
 KERNEL_SOURCES = ["runtime.hip", "mnb.hip", "attention.hip", "norm.hip"]
-EP_SOURCES = ["ep/ep.cpp", "ep/graph.cpp", "ep/plan.cpp"]
+EP_SOURCES = ["ep/ep.cpp", "ep/graph.cpp", "ep/fuse.cpp", "ep/plan.cpp"]
 
 HIP_FLAGS = [
     "--offload-arch=gfx950",

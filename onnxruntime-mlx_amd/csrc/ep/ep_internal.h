@@ -101,6 +101,10 @@ std::string claim_reason(const NodeDesc& n, const GraphIR& g);  // "" = claimed
 // ordered inside each cluster.
 std::vector<std::vector<size_t>> build_clusters(const GraphIR& g, const std::vector<bool>& claimed);
 
+// Compile-time rewrites of a fused node's subgraph (SwiGLU, and with
+// decode_fusions the QKV / gate-up merges and norm prologues).
+void fuse_subgraph(GraphIR& g, const std::vector<std::string>& outputs, bool decode_fusions);
+
 // ------------------------------------------------------------------- plan --
 struct DeviceBuffer {
     void* ptr = nullptr;

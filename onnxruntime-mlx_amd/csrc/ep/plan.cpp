@@ -41,59 +41,12 @@ static bool is_device_ptr(const void* p) {
     return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
 
-// SiLU-gated MLP: Sigmoid(g) -> Mul(g, sig) -> Mul(., u) becomes one SwiGLU node
-// when the two intermediates feed nothing else and are not fused-node outputs.
-static void fuse_swiglu(GraphIR& g, const std::vector<std::string>& outputs) {
-    std::map<std::string, int> uses;
-    for (const auto& n : g.nodes)
-        for (const auto& in : n.inputs)
-            if (!in.empty()) uses[in]++;
-    for (const auto& o : outputs) uses[o] += 1000;  // fused outputs stay materialised
-    auto other = [](const NodeDesc& m, const std::string& x) -> std::string {
-        if (m.inputs.size() != 2) return "";
-        if (m.inputs[0] == x) return m.inputs[1];
-        if (m.inputs[1] == x) return m.inputs[0];
-        return "";
-    };
-    std::vector<bool> dead(g.nodes.size(), false);
-    for (size_t i = 0; i < g.nodes.size(); ++i) {
-        const NodeDesc& sg = g.nodes[i];
-        if (sg.op != "Sigmoid" || sg.domain != "" || sg.outputs.empty()) continue;
-        const std::string x = sg.inputs[0], s = sg.outputs[0];
-        if (uses[s] != 1) continue;
-        for (size_t j = 0; j < g.nodes.size(); ++j) {
-            NodeDesc& m1 = g.nodes[j];
-            if (dead[j] || m1.op != "Mul" || other(m1, s) != x || m1.outputs.empty()) continue;
-            const std::string t = m1.outputs[0];
-            if (uses[t] != 1) break;
-            for (size_t k = 0; k < g.nodes.size(); ++k) {
-                NodeDesc& m2 = g.nodes[k];
-                if (dead[k] || m2.op != "Mul") continue;
-                const std::string u = other(m2, t);
-                if (u.empty() || u == t) continue;
-                const auto vx = g.values.find(x), vu = g.values.find(u);
-                if (vx == g.values.end() || vu == g.values.end() ||
-                    vx->second.dims != vu->second.dims)
-                    break;
-                m2.op = "SwiGLU";
-                m2.inputs = {x, u};
-                dead[i] = dead[j] = true;
-                break;
-            }
-            break;
-        }
-    }
-    std::vector<NodeDesc> kept;
-    for (size_t i = 0; i < g.nodes.size(); ++i)
-        if (!dead[i]) kept.push_back(std::move(g.nodes[i]));
-    g.nodes = std::move(kept);
-}
-
 Plan::Plan(GraphIR sub, std::vector<std::string> inputs, std::vector<std::string> outputs,
            int device)
     : sub_(std::move(sub)), inputs_(std::move(inputs)), outputs_(std::move(outputs)),
       device_(device) {
-    fuse_swiglu(sub_, outputs_);
+    const char* fz = std::getenv("ORTMI_EP_FUSE");
+    fuse_subgraph(sub_, outputs_, !(fz && std::strcmp(fz, "0") == 0));
     if (const char* g = std::getenv("ORTMI_EP_GRAPH")) graphs_enabled_ = std::strcmp(g, "0") != 0;
     check_hip(hipSetDevice(device_), "hipSetDevice");
     check_hip(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
@@ -398,23 +351,59 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
     void* st = stream_;
     const std::string& op = n.op;
 
-    if (op == "MatMulNBits") {
-        Tensor& A = need(0);
-        Tensor& B = need(1);
-        Tensor& S = need(2);
+    if (op == "MatMulNBits" || op == "MatMulNBitsSwiGLU") {
+        // Plain MatMulNBits, or one merged by the decode rewrites: an optional
+        // (Skip)SimplifiedLayerNorm prologue (inputs 6 skip, 7 gamma; output 1 the
+        // residual sum) and/or SwiGLU over interleaved gate/up rows.
+        const bool pair = op == "MatMulNBitsSwiGLU";
+        const bool norm = n.attr_int("__norm", 0) != 0;
+        Tensor X = need(0);
+        Tensor B = need(1);
+        Tensor S = need(2);
         Tensor* Z = in(3);
+        Tensor* skip = norm ? in(6) : nullptr;
+        Tensor* gamma = norm ? &need(7) : nullptr;
+        const float eps = n.attr_float("__norm_eps", 1e-6f);
         const int64_t K = n.attr_int("K", 0), N = n.attr_int("N", 0);
-        if (A.dims.empty() || A.dims.back() != K) fail("MatMulNBits: A's last dim != K", ORT_INVALID_ARGUMENT);
-        std::vector<int64_t> od = A.dims;
-        od.back() = N;
-        const int dtype = A.dtype;
-        const int64_t M = A.numel() / K;
-        void *ap = A.ptr, *bp = B.ptr, *sp = S.ptr, *zp = Z ? Z->ptr : nullptr;
+        const int64_t bits = n.attr_int("bits", 4), bs = n.attr_int("block_size", 32);
+        if (X.dims.empty() || X.dims.back() != K) fail(op + ": A's last dim != K", ORT_INVALID_ARGUMENT);
+        if (skip && skip->dims != X.dims) fail(op + ": skip shape differs", ORT_INVALID_ARGUMENT);
+        const int dtype = X.dtype;
+        const int64_t M = X.numel() / K;
+        std::vector<int64_t> od = X.dims;
+        od.back() = pair ? N / 2 : N;
+        const std::string res_name = norm && n.outputs.size() > 1 ? n.outputs[1] : std::string();
+        void* zp = Z ? Z->ptr : nullptr;
+        if (M == 1 && bits == 4 && (norm || pair) &&
+            (dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16 ||
+             dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_BFLOAT16)) {
+            Tensor& Y = out_tensor(outname(0), dtype, od, a, ctx);
+            void* yp = Y.ptr;
+            void* rp = res_name.empty() ? nullptr : out_tensor(res_name, dtype, X.dims, a, ctx).ptr;
+            const int rc = ortmi_matmul_nbits_decode_fused(
+                X.ptr, skip ? skip->ptr : nullptr, gamma ? gamma->ptr : nullptr, eps, rp,
+                (const uint8_t*)B.ptr, S.ptr, (const uint8_t*)zp, yp, N, K, bs,
+                (norm ? ORTMI_FUSE_RMS_NORM : 0) | (pair ? ORTMI_FUSE_SWIGLU_PAIRS : 0), kdt(dtype),
+                st);
+            if (rc == ORTMI_OK) return;
+            if (rc != ORTMI_E_INVALID) check_kernel(rc, op.c_str());
+        }
+        // Unfused: norm into a temporary, the matmul, then SwiGLU over the pairs.
+        void* ap = X.ptr;
+        if (norm) {
+            ap = arena_alloc((size_t)X.numel() * dtype_size(dtype));
+            void* rp = res_name.empty() ? nullptr : out_tensor(res_name, dtype, X.dims, a, ctx).ptr;
+            check_kernel(ortmi_rms_norm(X.ptr, skip ? skip->ptr : nullptr, nullptr, gamma->ptr, ap,
+                                        rp, M, K, eps, kdt(dtype), st),
+                         "SimplifiedLayerNormalization");
+        }
         Tensor& Y = out_tensor(outname(0), dtype, od, a, ctx);
-        check_kernel(ortmi_matmul_nbits(ap, (const uint8_t*)bp, sp, (const uint8_t*)zp, Y.ptr, M,
-                                        N, K, n.attr_int("bits", 4), n.attr_int("block_size", 32),
-                                        kdt(dtype), st),
+        void* yp = pair ? arena_alloc((size_t)(M * N) * dtype_size(dtype)) : Y.ptr;
+        check_kernel(ortmi_matmul_nbits(ap, (const uint8_t*)B.ptr, S.ptr, (const uint8_t*)zp, yp,
+                                        M, N, K, bits, bs, kdt(dtype), st),
                      "MatMulNBits");
+        if (pair)
+            check_kernel(ortmi_swiglu_pairs(yp, Y.ptr, M, N / 2, kdt(dtype), st), "SwiGLU");
         return;
     }
     if (op == "GroupQueryAttention") {

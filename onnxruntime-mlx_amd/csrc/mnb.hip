@@ -69,14 +69,32 @@ struct GemvGroup {
 // (one copy per workgroup) into VGPRs while the weights are in flight. Row groups
 // of R rows are dealt to waves round-robin; the next group's loads are issued
 // before the current group is reduced.
-template <typename T, int BS, int CPL, int R>
+// Optional fusions of the decoder's neighbours into the GEMV (decode only):
+//  * prologue: the activation row is (Skip)SimplifiedLayerNorm(x [+ skip]) * gamma,
+//    computed by every workgroup from x (K elements) before staging; workgroup 0
+//    also writes the residual x + skip. Rounding as the unfused ops: the sum is
+//    rounded to T, the normalised value once more.
+//  * SwiGLU pairs: rows come interleaved (gate row i, up row i), a wave takes both
+//    rows of a pair and writes Y[i] = (g * sigmoid(g)) * u, each op rounded to T as
+//    the Sigmoid/Mul/Mul graph stores it.
+template <typename T>
+struct GemvPrologue {
+    const T* skip;
+    const T* gamma;
+    T* residual;
+    float eps;
+};
+
+template <typename T, int BS, int CPL, int R, bool PRO = false, bool PAIR = false>
 __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ B,
                                                         const T* __restrict__ S,
                                                         const uint8_t* __restrict__ Z,
                                                         T* __restrict__ Y, int N, int K,
-                                                        int nb) {
+                                                        int nb, GemvPrologue<T> pro) {
+    static_assert(!PAIR || R == 2, "SwiGLU pairs take two rows per group");
     extern __shared__ float4 sA[];
+    __shared__ float s_red[4];
     using Group = GemvGroup<R, CPL>;
     const int Kp = nb * BS;
     const int C = Kp / 32;  // 32-code chunks per row
@@ -90,22 +108,29 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
 
     // 1. activation loads (16 bytes each), all in flight before anything else.
     constexpr int EPL = 16 / sizeof(T);
-    constexpr int AV = 8;  // up to 8 vectors per thread: Kp <= 2048 * EPL
+    // Kp <= 64 lanes * CPL * 32 codes, so 256 threads need ceil(8 * CPL / EPL) vectors each.
+    constexpr int AV = (8 * CPL + EPL - 1) / EPL;
     const int nvec = Kp / EPL;
     const bool vec_ok = (K % EPL) == 0 && (reinterpret_cast<uintptr_t>(A) % 16) == 0;
     uint4 av[AV];
-#pragma unroll
-    for (int u = 0; u < AV; ++u) {
+    auto load_vec = [&](const T* src, int u) -> uint4 {
         const int vi = threadIdx.x + u * 256;
         const int k0 = vi * EPL;
-        if (vi < nvec && vec_ok && k0 + EPL <= K) {
-            av[u] = *reinterpret_cast<const uint4*>(A + k0);
-        } else {
-            T t[EPL];
+        if (vi < nvec && vec_ok && k0 + EPL <= K) return *reinterpret_cast<const uint4*>(src + k0);
+        T t[EPL];
 #pragma unroll
-            for (int e = 0; e < EPL; ++e)
-                t[e] = (vi < nvec && k0 + e < K) ? A[k0 + e] : from_f32<T>(0.f);
-            av[u] = *reinterpret_cast<const uint4*>(t);
+        for (int e = 0; e < EPL; ++e)
+            t[e] = (vi < nvec && k0 + e < K) ? src[k0 + e] : from_f32<T>(0.f);
+        return *reinterpret_cast<const uint4*>(t);
+    };
+#pragma unroll
+    for (int u = 0; u < AV; ++u) av[u] = load_vec(A, u);
+    uint4 skv[PRO ? AV : 1], gmv[PRO ? AV : 1];
+    if constexpr (PRO) {
+#pragma unroll
+        for (int u = 0; u < AV; ++u) {
+            skv[u] = pro.skip ? load_vec(pro.skip, u) : make_uint4(0, 0, 0, 0);
+            gmv[u] = load_vec(pro.gamma, u);
         }
     }
 
@@ -151,17 +176,55 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     Group ga, gb;
     load_group(ga, g0);
 
-    // 3. activations -> LDS (swizzled fp32 units) -> VGPRs.
+    // 3. activations (normalised first when fused) -> LDS (swizzled fp32 units) -> VGPRs.
+    float scale_all = 1.f;
+    if constexpr (PRO) {
+        float ss = 0.f;
+#pragma unroll
+        for (int u = 0; u < AV; ++u) {
+            const int vi = threadIdx.x + u * 256;
+            if (vi >= nvec) continue;
+            T* t = reinterpret_cast<T*>(&av[u]);
+            const T* k = reinterpret_cast<const T*>(&skv[u]);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                float v = to_f32(t[e]);
+                if (pro.skip) v = round_to<T>(v + to_f32(k[e]));
+                t[e] = from_f32<T>(v);
+                ss += v * v;
+            }
+            if (pro.residual && blockIdx.x == 0) {
+                const int k0 = vi * EPL;
+                if (vec_ok && k0 + EPL <= K) {
+                    *reinterpret_cast<uint4*>(pro.residual + k0) = av[u];
+                } else {
+                    for (int e = 0; e < EPL; ++e)
+                        if (k0 + e < K) pro.residual[k0 + e] = t[e];
+                }
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) s_red[wave] = ss;
+        __syncthreads();
+        scale_all = 1.0f / sqrtf((s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)K + pro.eps);
+    }
 #pragma unroll
     for (int u = 0; u < AV; ++u) {
         const int vi = threadIdx.x + u * 256;
         if (vi >= nvec) continue;
         const T* t = reinterpret_cast<const T*>(&av[u]);
+        float f[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) f[e] = to_f32(t[e]);
+        if constexpr (PRO) {
+            const T* gm = reinterpret_cast<const T*>(&gmv[u]);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) f[e] = round_to<T>(f[e] * scale_all * to_f32(gm[e]));
+        }
 #pragma unroll
         for (int e = 0; e < EPL; e += 4) {
             const int q = (vi * EPL + e) / 4;
-            sA[act_unit<CPL>(q)] = make_float4(to_f32(t[e]), to_f32(t[e + 1]), to_f32(t[e + 2]),
-                                               to_f32(t[e + 3]));
+            sA[act_unit<CPL>(q)] = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
         }
     }
     __syncthreads();
@@ -199,6 +262,14 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
         const int n0 = gi * R;
+        if constexpr (PAIR) {
+            if (lane == 0 && n0 + 1 < N) {
+                const float g = round_to<T>(acc[0]), up = round_to<T>(acc[1]);
+                const float sig = round_to<T>(1.0f / (1.0f + __expf(-g)));
+                Y[gi] = from_f32<T>(round_to<T>(g * sig) * up);
+            }
+            return;
+        }
         if (lane < R) {
             float v = acc[0];
 #pragma unroll
@@ -219,32 +290,36 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     }
 }
 
-template <typename T, int BS, int CPL>
+template <typename T, int BS, int CPL, bool PRO, bool PAIR>
 static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
-                            int N, int K, int nb, hipStream_t st) {
-    // One row per group; at most 4 workgroups per CU, each wave walking its rows
-    // with the next row's loads in flight (measured best on MI355X for the
-    // K=4096 x N=11008 shape against 1-4 rows per group and 1-8 workgroups/CU).
+                            int N, int K, int nb, const GemvPrologue<T>& pro, hipStream_t st) {
+    // One row (or one gate/up pair) per group; at most 4 workgroups per CU, each
+    // wave walking its groups with the next group's loads in flight (measured best
+    // on MI355X for the K=4096 x N=11008 shape against 1-4 rows per group and 1-8
+    // workgroups/CU).
+    constexpr int R = PAIR ? 2 : 1;
     const int Kp = nb * BS;
-    long grid = ((long)N + 3) / 4;
+    const long groups = ((long)N + R - 1) / R;
+    long grid = (groups + 3) / 4;
     if (grid > 4L * device_cu_count()) grid = 4L * device_cu_count();
-    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, 1>), dim3((unsigned)grid), dim3(256),
-                       (size_t)Kp * sizeof(float), st, A, B, S, Z, Y, N, K, nb);
+    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, PRO, PAIR>), dim3((unsigned)grid),
+                       dim3(256), (size_t)Kp * sizeof(float), st, A, B, S, Z, Y, N, K, nb, pro);
     return check_launch("mnb_gemv4");
 }
 
-template <typename T, int BS>
+template <typename T, int BS, bool PRO = false, bool PAIR = false>
 static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y, int N,
-                        int K, int nb, hipStream_t st) {
+                        int K, int nb, hipStream_t st,
+                        const GemvPrologue<T>& pro = GemvPrologue<T>{nullptr, nullptr, nullptr, 0.f}) {
     const int C = nb * BS / 32;
     const int cpl = (C + 63) / 64;
     if ((long)nb * BS > 2048L * (16 / (long)sizeof(T))) return -1;  // activation staging bound
     switch (cpl) {
-        case 1: return launch_gemv4_cpl<T, BS, 1>(A, B, S, Z, Y, N, K, nb, st);
-        case 2: return launch_gemv4_cpl<T, BS, 2>(A, B, S, Z, Y, N, K, nb, st);
-        case 3: return launch_gemv4_cpl<T, BS, 3>(A, B, S, Z, Y, N, K, nb, st);
-        case 4: return launch_gemv4_cpl<T, BS, 4>(A, B, S, Z, Y, N, K, nb, st);
-        case 5: return launch_gemv4_cpl<T, BS, 5>(A, B, S, Z, Y, N, K, nb, st);
+        case 1: return launch_gemv4_cpl<T, BS, 1, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
+        case 2: return launch_gemv4_cpl<T, BS, 2, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
+        case 3: return launch_gemv4_cpl<T, BS, 3, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
+        case 4: return launch_gemv4_cpl<T, BS, 4, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
+        case 5: return launch_gemv4_cpl<T, BS, 5, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
         default: return -1;  // K > 10240: the caller falls back
     }
 }
@@ -559,6 +634,74 @@ static int run_mnb(const void* A, const uint8_t* B, const void* S, const uint8_t
 }  // namespace ortmi
 
 using namespace ortmi;
+
+namespace ortmi {
+template <typename T, bool PRO, bool PAIR>
+static int run_fused_gemv(const void* x, const void* skip, const void* gamma, float eps,
+                          void* residual, const uint8_t* B, const void* S, const uint8_t* Z,
+                          void* Y, int N, int K, int bs, hipStream_t st) {
+    const int nb = (K + bs - 1) / bs;
+    GemvPrologue<T> pro{static_cast<const T*>(skip), static_cast<const T*>(gamma),
+                        static_cast<T*>(residual), eps};
+    const T* a = static_cast<const T*>(x);
+    const T* s = static_cast<const T*>(S);
+    T* y = static_cast<T*>(Y);
+    if (bs == 32) return launch_gemv4<T, 32, PRO, PAIR>(a, B, s, Z, y, N, K, nb, st, pro);
+    if (bs == 64) return launch_gemv4<T, 64, PRO, PAIR>(a, B, s, Z, y, N, K, nb, st, pro);
+    return launch_gemv4<T, 128, PRO, PAIR>(a, B, s, Z, y, N, K, nb, st, pro);
+}
+
+template <typename T>
+static int dispatch_fused_gemv(const void* x, const void* skip, const void* gamma, float eps,
+                               void* residual, const uint8_t* B, const void* S,
+                               const uint8_t* Z, void* Y, int N, int K, int bs, bool norm,
+                               bool pair, hipStream_t st) {
+    if (norm && pair)
+        return run_fused_gemv<T, true, true>(x, skip, gamma, eps, residual, B, S, Z, Y, N, K, bs, st);
+    if (norm)
+        return run_fused_gemv<T, true, false>(x, skip, gamma, eps, residual, B, S, Z, Y, N, K, bs, st);
+    if (pair)
+        return run_fused_gemv<T, false, true>(x, skip, gamma, eps, residual, B, S, Z, Y, N, K, bs, st);
+    return run_fused_gemv<T, false, false>(x, skip, gamma, eps, residual, B, S, Z, Y, N, K, bs, st);
+}
+}  // namespace ortmi
+
+extern "C" int ortmi_matmul_nbits_decode_fused(const void* x, const void* skip, const void* gamma,
+                                               float epsilon, void* residual, const uint8_t* B,
+                                               const void* scales, const uint8_t* zero_points,
+                                               void* Y, int64_t N, int64_t K, int64_t block_size,
+                                               int32_t flags, int32_t dtype, void* stream) {
+    const bool norm = (flags & ORTMI_FUSE_RMS_NORM) != 0;
+    const bool pair = (flags & ORTMI_FUSE_SWIGLU_PAIRS) != 0;
+    ORTMI_REQUIRE((flags & ~(ORTMI_FUSE_RMS_NORM | ORTMI_FUSE_SWIGLU_PAIRS)) == 0,
+                  "MatMulNBits fused: unknown flags");
+    ORTMI_REQUIRE(block_size == 32 || block_size == 64 || block_size == 128,
+                  "MatMulNBits fused: block_size must be 32, 64 or 128");
+    ORTMI_REQUIRE(N > 0 && K > 0 && N < (1LL << 31), "MatMulNBits fused: bad shape");
+    ORTMI_REQUIRE(!pair || N % 2 == 0, "MatMulNBits fused: SwiGLU pairs need an even N");
+    ORTMI_REQUIRE(x && B && scales && Y, "MatMulNBits fused: null tensor");
+    ORTMI_REQUIRE(!norm || gamma, "MatMulNBits fused: the norm needs gamma");
+    ORTMI_REQUIRE(!residual || (norm && skip), "MatMulNBits fused: residual needs the skip norm");
+    ORTMI_REQUIRE((reinterpret_cast<uintptr_t>(B) & 15) == 0,
+                  "MatMulNBits fused: B must be 16-byte aligned");
+    const int64_t nb = (K + block_size - 1) / block_size;
+    const int64_t limit = 2048LL * (dtype == ORTMI_F32 ? 4 : 8);
+    ORTMI_REQUIRE(nb * block_size <= std::min<int64_t>(limit, 10240),
+                  "MatMulNBits fused: K too large for the decode kernel");
+    hipStream_t st = as_stream(stream);
+    switch (dtype) {
+        case ORTMI_F16:
+            return dispatch_fused_gemv<half_t>(x, skip, gamma, epsilon, residual, B, scales,
+                                               zero_points, Y, (int)N, (int)K, (int)block_size,
+                                               norm, pair, st);
+        case ORTMI_BF16:
+            return dispatch_fused_gemv<uint16_t>(x, skip, gamma, epsilon, residual, B, scales,
+                                                 zero_points, Y, (int)N, (int)K, (int)block_size,
+                                                 norm, pair, st);
+        default:
+            return fail(ORTMI_E_INVALID, "MatMulNBits fused: fp16 or bf16 activations only");
+    }
+}
 
 extern "C" int ortmi_matmul_nbits(const void* A, const uint8_t* B, const void* scales,
                                   const uint8_t* zero_points, void* Y, int64_t M, int64_t N,

@@ -62,6 +62,20 @@ __global__ void swiglu_kernel(const T* __restrict__ g, const T* __restrict__ u, 
     o[i] = from_f32<T>(t * to_f32(u[i]));
 }
 
+// SwiGLU over interleaved gate/up columns: y is [rows, 2P] with column 2i the
+// gate and 2i+1 the up projection of output i; out is [rows, P].
+template <typename T>
+__global__ void swiglu_pairs_kernel(const T* __restrict__ y, T* __restrict__ o, int64_t pairs,
+                                    int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t row = i / pairs, p = i % pairs;
+    const T* yr = y + row * 2 * pairs + 2 * p;
+    const float gv = to_f32(yr[0]);
+    const float sig = round_to<T>(1.0f / (1.0f + __expf(-gv)));
+    o[i] = from_f32<T>(round_to<T>(gv * sig) * to_f32(yr[1]));
+}
+
 template <typename T>
 __global__ void binary_kernel(int op, const T* __restrict__ a, const T* __restrict__ b,
                               T* __restrict__ o, int64_t n) {
@@ -115,6 +129,88 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ 
         __syncthreads();
     }
     if (threadIdx.x == 0) out[row] = si[0] < 0 ? 0 : si[0];
+}
+
+// Block-wide argmax of (value, index) pairs held one per thread; the lowest index
+// wins ties. Returns the winner in thread 0.
+__device__ __forceinline__ void argmax_block(float& best, int64_t& bi, float* sv, int64_t* si) {
+    sv[threadIdx.x] = best;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            const float ov = sv[threadIdx.x + s];
+            const int64_t oi = si[threadIdx.x + s];
+            const float mv = sv[threadIdx.x];
+            const int64_t mi = si[threadIdx.x];
+            if (oi >= 0 && (mi < 0 || ov > mv || (ov == mv && oi < mi))) {
+                sv[threadIdx.x] = ov;
+                si[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    best = sv[0];
+    bi = si[0];
+}
+
+// Two-pass argmax for long rows: `parts` workgroups per row each reduce a
+// contiguous slice to one (value, index) partial, then one workgroup per row
+// reduces the partials.
+struct ArgPartial {
+    float v;
+    int32_t pad;
+    int64_t i;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const T* __restrict__ x,
+                                                             ArgPartial* __restrict__ part,
+                                                             int64_t cols, int parts,
+                                                             int64_t slice) {
+    __shared__ float sv[256];
+    __shared__ int64_t si[256];
+    const int64_t row = blockIdx.y;
+    const int p = blockIdx.x;
+    const T* xr = x + row * cols;
+    const int64_t c0 = (int64_t)p * slice;
+    const int64_t c1 = min(cols, c0 + slice);
+    float best = -INFINITY;
+    int64_t bi = -1;
+    for (int64_t c = c0 + threadIdx.x; c < c1; c += blockDim.x) {
+        const float v = to_f32(xr[c]);
+        if (v > best || (bi < 0 && v == best)) {
+            best = v;
+            bi = c;
+        }
+    }
+    argmax_block(best, bi, sv, si);
+    if (threadIdx.x == 0) part[row * parts + p] = ArgPartial{best, 0, bi};
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const ArgPartial* __restrict__ part,
+                                                           int64_t* __restrict__ out,
+                                                           int parts) {
+    __shared__ float sv[256];
+    __shared__ int64_t si[256];
+    const int64_t row = blockIdx.x;
+    float best = -INFINITY;
+    int64_t bi = -1;
+    for (int p = threadIdx.x; p < parts; p += blockDim.x) {
+        const ArgPartial a = part[row * parts + p];
+        if (a.i >= 0 && (bi < 0 || a.v > best || (a.v == best && a.i < bi))) {
+            best = a.v;
+            bi = a.i;
+        }
+    }
+    argmax_block(best, bi, sv, si);
+    if (threadIdx.x == 0) out[row] = bi < 0 ? 0 : bi;
+}
+
+static int argmax_parts(int64_t cols) {
+    // About 2048 columns per workgroup, at most 256 partials per row.
+    int64_t p = (cols + 2047) / 2048;
+    return (int)std::min<int64_t>(std::max<int64_t>(p, 1), 256);
 }
 
 template <typename S, typename D>
@@ -186,6 +282,21 @@ extern "C" int ortmi_swiglu(const void* gate, const void* up, void* out, int64_t
 #undef ORTMI_SWIGLU
 }
 
+extern "C" int ortmi_swiglu_pairs(const void* y, void* out, int64_t rows, int64_t pairs,
+                                  int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(rows >= 0 && pairs >= 0, "SwiGLU pairs: bad shape");
+    const int64_t n = rows * pairs;
+    if (n == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(y && out, "SwiGLU pairs: null tensor");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_SWIGLU_PAIRS(T)                                                                \
+    hipLaunchKernelGGL((swiglu_pairs_kernel<T>), dim3(blocks_for(n)), dim3(256), 0, st,      \
+                       static_cast<const T*>(y), static_cast<T*>(out), pairs, n);            \
+    return check_launch("swiglu_pairs")
+    ORTMI_DISPATCH_FLOAT(dtype, ORTMI_SWIGLU_PAIRS)
+#undef ORTMI_SWIGLU_PAIRS
+}
+
 extern "C" int ortmi_binary(int32_t op, const void* a, const void* b, void* out, int64_t n,
                             int32_t dtype, void* stream) {
     ORTMI_REQUIRE(op >= 0 && op <= 2, "binary: op must be 0 (Add), 1 (Mul) or 2 (Sub)");
@@ -215,15 +326,35 @@ extern "C" int ortmi_sigmoid(const void* x, void* out, int64_t n, int32_t dtype,
 #undef ORTMI_SIG
 }
 
+extern "C" size_t ortmi_argmax_rows_workspace_size(int64_t rows, int64_t cols) {
+    if (rows <= 0 || cols <= 0) return 0;
+    return (size_t)rows * (size_t)argmax_parts(cols) * sizeof(ArgPartial);
+}
+
 extern "C" int ortmi_argmax_rows(const void* x, int64_t* out, int64_t rows, int64_t cols,
-                                 int32_t dtype, void* stream) {
+                                 int32_t dtype, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
     ORTMI_REQUIRE(rows >= 0 && cols > 0, "ArgMax: bad shape");
     if (rows == 0) return ORTMI_OK;
     ORTMI_REQUIRE(x && out, "ArgMax: null tensor");
+    ORTMI_REQUIRE(rows <= 65535, "ArgMax: too many rows");
     hipStream_t st = as_stream(stream);
-#define ORTMI_ARGMAX(T)                                                                        \
-    hipLaunchKernelGGL((argmax_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0, st,        \
-                       static_cast<const T*>(x), out, cols);                                   \
+    const int parts = argmax_parts(cols);
+    const bool split = parts > 1 && workspace &&
+                       workspace_bytes >= ortmi_argmax_rows_workspace_size(rows, cols);
+    const int64_t slice = (cols + parts - 1) / parts;
+#define ORTMI_ARGMAX(T)                                                                         \
+    if (split) {                                                                                \
+        hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3((unsigned)parts, (unsigned)rows),   \
+                           dim3(256), 0, st, static_cast<const T*>(x),                          \
+                           static_cast<ArgPartial*>(workspace), cols, parts, slice);            \
+        if (int rc = check_launch("argmax_partial")) return rc;                                 \
+        hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)rows), dim3(256), 0, st,         \
+                           static_cast<const ArgPartial*>(workspace), out, parts);              \
+        return check_launch("argmax_final");                                                    \
+    }                                                                                           \
+    hipLaunchKernelGGL((argmax_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0, st,         \
+                       static_cast<const T*>(x), out, cols);                                    \
     return check_launch("argmax_rows")
     ORTMI_DISPATCH_FLOAT(dtype, ORTMI_ARGMAX)
 #undef ORTMI_ARGMAX

@@ -216,6 +216,9 @@ class DecoderRunner:
         self.total = torch.zeros(1, dtype=torch.int32, pin_memory=True)
         self.length = 0
         self.lib = load_kernels()
+        self.argmax_ws = torch.empty(
+            max(1, self.lib.ortmi_argmax_rows_workspace_size(1, cfg.vocab)), dtype=torch.uint8,
+            device=dev)
         # Inputs that keep their buffers for the whole generation are bound once.
         self.session.set_input("seqlens_k", self.seqlens, hx.INT32)
         self.session.set_input("total_sequence_length", self.total, hx.INT32)
@@ -242,7 +245,9 @@ class DecoderRunner:
         last = self.logits[0, S - 1]
         check(self.lib.ortmi_argmax_rows(ctypes.c_void_p(last.data_ptr()),
                                          ctypes.c_void_p(self.next_id.data_ptr()), 1,
-                                         self.cfg.vocab, 10, st))
+                                         self.cfg.vocab, 10,
+                                         ctypes.c_void_p(self.argmax_ws.data_ptr()),
+                                         self.argmax_ws.numel(), st))
 
     def prefill(self, prompt: np.ndarray):
         S = int(prompt.shape[-1])

@@ -266,3 +266,29 @@ def test_ep_decode_graph_replay_matches_eager(ortmi, dec, monkeypatch):
     eager = run(False)
     graphed = run(True)
     np.testing.assert_array_equal(graphed, eager)
+
+
+def test_ep_decoder_fusions_match_unfused(ortmi, dec, monkeypatch):
+    """The decode rewrites (QKV and gate/up merges, norm prologues, SwiGLU
+    epilogue) against the same graph run op by op: logits within the fp16
+    tolerance carried through two layers, the same greedy tokens."""
+    cfg = _small_cfg(dec, 128)
+    w = dec.make_weights(cfg, seed=31)
+    prompt = np.random.default_rng(32).integers(0, cfg.vocab, size=12)
+
+    def run(fuse):
+        monkeypatch.setenv("ORTMI_EP_FUSE", "1" if fuse else "0")
+        r = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
+        r.prefill(prompt)
+        logits, toks = [host(r.logits[0, :12])], [int(r.next_id.item())]
+        for _ in range(6):
+            r.decode_step()
+            logits.append(host(r.logits[0, :1]))
+            toks.append(int(r.next_id.item()))
+        return logits, toks
+
+    fl, ft = run(True)
+    ul, ut = run(False)
+    for a, b in zip(fl, ul):
+        assert np.abs(a - b).max() <= 0.02 * max(1.0, np.abs(b).max())
+    assert ft == ut

@@ -71,6 +71,56 @@ def _mnb_inputs(rng, M, N, K, block, bits=4, asym=True, zp_all8=False, dtype=np.
     return A, B, s, zp
 
 
+@pytest.mark.parametrize("K,N,block,skip,pair", [
+    (1536, 2048, 32, False, False), (1536, 1536, 32, True, False), (1536, 17920, 32, True, True),
+    (8960, 1536, 32, True, False), (4096, 512, 128, True, True), (1000, 64, 64, False, True)])
+def test_mnb_decode_fused(ortmi, oracle, K, N, block, skip, pair):
+    """Norm prologue and SwiGLU-pair epilogue of the decode GEMV against the unfused
+    ops of the oracle (norm rounded to fp16, matmul in fp64, SwiGLU op by op)."""
+    import ctypes
+
+    import torch
+
+    rng = np.random.default_rng(K + N + block)
+    A, B, s, zp = _mnb_inputs(rng, 1, N, K, block, asym=N % 3 == 0, dtype=np.float16)
+    x = A[0]
+    sk = rng.standard_normal(K).astype(np.float16) if skip else None
+    gamma = (1 + 0.2 * rng.standard_normal(K)).astype(np.float16)
+    y, r = oracle.rms_norm(x, gamma, 1e-6, skip=sk, round16=True)
+    a16 = oracle.round_f16(y)
+    exact = oracle.mnb_matmul(a16, B, s, zp, N, K, 4, block)
+    lib = ortmi.load_kernels()
+    dx, dB, ds = dev(x), dev(B), dev(s)
+    dz = dev(zp) if zp is not None else None
+    dsk = dev(sk) if skip else None
+    res = torch.empty(K, dtype=torch.float16, device="cuda") if skip else None
+    out = torch.empty(N // 2 if pair else N, dtype=torch.float16, device="cuda")
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    flags = 1 | (2 if pair else 0)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ortmi.check(lib.ortmi_matmul_nbits_decode_fused(
+        p(dx), p(dsk), p(dev(gamma)), 1e-6, p(res), p(dB), p(ds), p(dz), p(out), N, K, block,
+        flags, 10, st))
+    got = host(out)
+    if skip:
+        np.testing.assert_array_equal(host(res), r)
+    W = oracle.mnb_dequant(B, s, zp, N, K, 4, block)
+    # The normalised activations may differ from the oracle's by one fp16 rounding.
+    extra = np.abs(W) @ (np.abs(a16) * 2.0 ** -10)
+    if not pair:
+        assert_f16_close(got, exact, extra=extra, what="fused norm GEMV")
+        return
+    g, u = oracle.round_f16(exact[0::2]), oracle.round_f16(exact[1::2])
+    sig = oracle.round_f16(1.0 / (1.0 + np.exp(-g.astype(np.float64))))
+    ref = oracle.round_f16(oracle.round_f16(g * sig) * u)
+    # g and u each carry the GEMV tolerance; propagate it through silu(g) * u.
+    eg = 1e-3 + ulp16(g) + extra[0::2]
+    eu = 1e-3 + ulp16(u) + extra[1::2]
+    dsilu = np.abs(sig * (1 + g * (1 - sig)))
+    bound = eg * dsilu * np.abs(u) + eu * np.abs(g * sig) + eg * eu * 1.2 + 2 * ulp16(ref)
+    assert (np.abs(got - ref) <= 1e-3 + bound).all(), np.abs(got - ref).max()
+
+
 @pytest.mark.parametrize("K,block", [(256, 32), (1176, 32), (256, 64), (512, 128), (8960, 32),
                                      (1536, 32)])
 @pytest.mark.parametrize("asym", [False, True])
@@ -284,6 +334,24 @@ def test_gqa_decode_capturable(ortmi, oracle, H, KV, hd):
         torch.cuda.synchronize()
         assert torch.equal(gout, eout), f"replay at total={t} differs from eager"
         assert torch.equal(kg, ke) and torch.equal(vg, ve)
+
+
+@pytest.mark.parametrize("S,past,cap", [(1, 40, 64), (9, 10, 64)])
+def test_gqa_packed_qkv(ortmi, oracle, S, past, cap):
+    """Packed [B, S, (H + 2 KV) hd] input (key = value = None) equals separate Q/K/V."""
+    rng = np.random.default_rng(S * 7 + past)
+    B, H, KV, hd = 2, 12, 2, 128
+    q, k, v, pk, pv, cos, sin = _gqa_inputs(rng, B, S, H, KV, hd, cap, True, 1e6)
+    packed = np.concatenate([q, k, v], axis=-1)
+    total = past + S
+    dpk, dpv = dev(pk), dev(pv)
+    out, _, _ = ortmi.group_query_attention(
+        dev(packed), None, None, dpk, dpv, dev(np.full(B, total - 1, np.int32)), total,
+        dev(cos), dev(sin), num_heads=H, kv_num_heads=KV, do_rotary=1, present_key=dpk,
+        present_value=dpv)
+    ro, rk, rv, _ = oracle.gqa(q, k, v, pk, pv, total, H, KV, cos=cos, sin=sin, round16=True)
+    assert_f16_close(host(out), ro, what="packed gqa")
+    np.testing.assert_array_equal(host(dpv), rv.astype(np.float16).astype(np.float32))
 
 
 def test_gqa_decode_shared_separate_present(ortmi, oracle):
@@ -503,14 +571,20 @@ def test_glue_kernels(ortmi):
     t = (g32 * sig).astype(np.float16).astype(np.float32)
     ref = (t * u.astype(np.float32)).astype(np.float16).astype(np.float32)
     assert (np.abs(host(out) - ref) <= ulp16(ref)).all()
-    # argmax: first index on ties
+    # argmax: first index on ties, one-pass and two-pass (the tie straddles partials)
     x = rng.standard_normal((3, 151936)).astype(np.float16)
     x[1, 17] = x[1, 99] = 100.0
+    x[2, 4000] = x[2, 151935] = 100.0
     idx = torch.empty(3, dtype=torch.int64, device="cuda")
     dx = dev(x)
-    ortmi.check(lib.ortmi_argmax_rows(ctypes.c_void_p(dx.data_ptr()), ctypes.c_void_p(idx.data_ptr()),
-                                      3, 151936, 10, st))
-    np.testing.assert_array_equal(host(idx), np.argmax(x.astype(np.float32), axis=1))
+    wsz = lib.ortmi_argmax_rows_workspace_size(3, 151936)
+    ws = torch.empty(wsz, dtype=torch.uint8, device="cuda")
+    for w, wb in ((None, 0), (ctypes.c_void_p(ws.data_ptr()), wsz)):
+        idx.fill_(-5)
+        ortmi.check(lib.ortmi_argmax_rows(ctypes.c_void_p(dx.data_ptr()),
+                                          ctypes.c_void_p(idx.data_ptr()), 3, 151936, 10, w, wb,
+                                          st))
+        np.testing.assert_array_equal(host(idx), np.argmax(x.astype(np.float32), axis=1))
     # gather rows with a negative id
     table = rng.standard_normal((100, 64)).astype(np.float16)
     ids = np.array([3, -1, 50], np.int64)
