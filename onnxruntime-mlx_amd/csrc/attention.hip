@@ -150,8 +150,14 @@ __device__ __forceinline__ void rope_lane8(float (&x)[8], int dl, const T* __res
     float partner[8];
     const bool lowhalf = dl < half;
     const int src = lowhalf ? lane + off : lane - off;
+    if (LPR == 16 && off == 8) {
+        // Full rotary over 128 dims: the partner is lane ^ 8 inside a 16-lane row.
 #pragma unroll
-    for (int i = 0; i < 8; ++i) partner[i] = __shfl(x[i], src, 64);
+        for (int i = 0; i < 8; ++i) partner[i] = dpp_mov<0x128>(x[i]);  // row_ror:8
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) partner[i] = __shfl(x[i], src, 64);
+    }
     if (dl < 2 * half) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -165,12 +171,21 @@ __device__ __forceinline__ void rope_lane8(float (&x)[8], int dl, const T* __res
 // Partial state layout (floats): [row][split][vhd + 2] with o (unnormalised),
 // then m (running max) and l (sum of exp).
 //
-// One workgroup per (batch, kv head, key split). RoPE of the G query heads (and,
-// in the split holding key vp, of the new key) is applied in registers; the new
-// K/V row is written to `present` and then read back like every other row. Each
-// lane group of LPR lanes walks rows with an online softmax over blocks of U
-// rows; K and V of a block are loaded together. In the growing contract rows
-// below vp are copied from past to present out of the registers already loaded.
+// One workgroup per (batch, kv head, key split). Built for latency, since a
+// decode step at short context is a handful of dependent memory round trips:
+//  * every load that does not depend on the past length is issued first (the
+//    query rows, the new K/V row, and the first block of cached rows, fetched
+//    speculatively: rows past the live keys are in bounds and masked later);
+//  * RoPE of the G query heads and of the new key runs in registers once the
+//    cos/sin row of position vp has arrived;
+//  * the new key/value row is written to `present` but never read back: the
+//    split holding position vp uses the rotated row from registers, so no wave
+//    waits for that store;
+//  * blocks of U*RPS rows are software-pipelined (the next block's K and V loads
+//    are in flight while the current block is scored).
+// Each lane group of LPR lanes owns one row per step; scores use a blocked
+// online softmax. In the growing contract rows below vp are copied from past to
+// present out of the registers already loaded.
 template <typename T, int HD, int G>
 __global__ __launch_bounds__(256) void gqa_decode_kernel(
     const T* __restrict__ q, const T* __restrict__ knew, const T* __restrict__ vnew,
@@ -178,69 +193,100 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     int half, int interleaved, const T* __restrict__ kpast, const T* __restrict__ vpast,
     T* __restrict__ kpres, T* __restrict__ vpres, int64_t past_cap, int64_t pres_cap,
     int copy_past, int vp, int chunk, int nsplit, int KV, float scale, float* __restrict__ part,
-    T* __restrict__ out, const int* __restrict__ total_dev, int vp_max) {
+    T* __restrict__ out, const int* __restrict__ total_dev, int vp_max, int gsplit) {
     constexpr int LPR = HD / 8;          // lanes per row (16 bytes each)
     constexpr int RPW = 64 / LPR;        // rows per wave per step
     constexpr int RPS = 4 * RPW;         // rows per workgroup step
-    constexpr int U = 4;                 // steps per online-softmax block
+    constexpr int U = G <= 4 ? 4 : 2;    // steps per online-softmax block (registers)
+    constexpr int BLK = RPS * U;         // rows per block
     __shared__ float s_o[4][G][HD];
-    __shared__ float s_m[4][RPW][G], s_l[4][RPW][G];
+    __shared__ float s_m[4][G], s_l[4][G];
 
-    // Capturable form: the past length comes from device memory (one token, so
-    // vp = total - 1), clamped to the rows the buffers and the cos/sin cache hold.
-    if (total_dev) vp = min(max(total_dev[0] - 1, 0), vp_max);
-    const int bk = blockIdx.x;  // b*KV + kvh
+    // blockIdx.x = (b*KV + kvh) * gsplit + head group: the G*gsplit query heads of
+    // a KV head may be spread over gsplit workgroups that read the same rows.
+    const int bk = blockIdx.x / gsplit;
+    const int hgrp = blockIdx.x % gsplit;
     const int split = blockIdx.y;
     const int b = bk / KV, kvh = bk % KV;
-    const int H = KV * G;
-    const int nkeys = vp + 1;
+    const int GT = G * gsplit;  // query heads per KV head
+    const int H = KV * GT;
+    const int h0 = kvh * GT + hgrp * G;  // first query head of this workgroup
     const int j0 = split * chunk;
-    const int j1 = min(nkeys, j0 + chunk);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = lane / LPR;
     const int dl = (lane % LPR) * 8;
+    T* kw = kpres + (int64_t)bk * pres_cap * HD;
+    T* vw = vpres + (int64_t)bk * pres_cap * HD;
+    const T* kbase = copy_past ? kpast + (int64_t)bk * past_cap * HD : kw;
+    const T* vbase = copy_past ? vpast + (int64_t)bk * past_cap * HD : vw;
+    const int64_t src_rows = copy_past ? past_cap : pres_cap;
+
+    // 1. Loads independent of the past length.
+    int tv = 0;
+    if (total_dev) tv = total_dev[0];
+    uint4 qraw[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        qraw[g] = *reinterpret_cast<const uint4*>(q + (int64_t)b * q_stride +
+                                                  (int64_t)(h0 + g) * HD + dl);
+    const uint4 kraw = *reinterpret_cast<const uint4*>(knew + (int64_t)b * kv_stride +
+                                                       (int64_t)kvh * HD + dl);
+    const uint4 vraw = *reinterpret_cast<const uint4*>(vnew + (int64_t)b * kv_stride +
+                                                       (int64_t)kvh * HD + dl);
+    uint4 kr[U], vr[U];
+    auto load_block = [&](uint4 (&kk)[U], uint4 (&vv)[U], int base) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = base + u * RPS + wave * RPW + sub;
+            if (j < src_rows && j < j0 + chunk) {
+                kk[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)j * HD + dl);
+                vv[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)j * HD + dl);
+            } else {
+                kk[u] = make_uint4(0, 0, 0, 0);
+                vv[u] = make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    load_block(kr, vr, j0);
+
+    // 2. Past length, then RoPE of the queries and of the new key.
+    if (total_dev) vp = min(max(tv - 1, 0), vp_max);
+    const int nkeys = vp + 1;
+    const int j1 = min(nkeys, j0 + chunk);
     const T* cr = cos_c ? cos_c + (int64_t)vp * half : nullptr;
     const T* sr = sin_c ? sin_c + (int64_t)vp * half : nullptr;
-
-    // Query fragments (rotated, rounded to T as the reference materialises them).
     float qf[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const T* qp = q + (int64_t)b * q_stride + (int64_t)(kvh * G + g) * HD + dl;
-        const uint4 raw = *reinterpret_cast<const uint4*>(qp);
-        const T* rv = reinterpret_cast<const T*>(&raw);
+        const T* rv = reinterpret_cast<const T*>(&qraw[g]);
 #pragma unroll
         for (int i = 0; i < 8; ++i) qf[g][i] = to_f32(rv[i]);
         if (cr) rope_lane8<T, LPR>(qf[g], dl, cr, sr, half, interleaved);
 #pragma unroll
         for (int i = 0; i < 8; ++i) qf[g][i] = round_to<T>(qf[g][i]) * scale;
     }
-    T* kw = kpres + (int64_t)bk * pres_cap * HD;
-    T* vw = vpres + (int64_t)bk * pres_cap * HD;
-    // The split holding key vp writes the new row (rotated K, raw V) to present.
-    if (vp >= j0 && vp < j1) {
-        if (wave == 0) {
-            const T* kp = knew + (int64_t)b * kv_stride + (int64_t)kvh * HD + dl;
-            const uint4 raw = *reinterpret_cast<const uint4*>(kp);
-            const T* rv = reinterpret_cast<const T*>(&raw);
-            float kx[8];
+    const bool own_new = vp >= j0 && vp < j1;
+    float knf[8], vnf[8];
+    {
+        const T* rk = reinterpret_cast<const T*>(&kraw);
+        const T* rvv = reinterpret_cast<const T*>(&vraw);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) kx[i] = to_f32(rv[i]);
-            if (cr) rope_lane8<T, LPR>(kx, dl, cr, sr, half, interleaved);
-            T outk[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) outk[i] = from_f32<T>(kx[i]);
-            if (sub == 0) {
-                *reinterpret_cast<uint4*>(kw + (int64_t)vp * HD + dl) =
-                    *reinterpret_cast<uint4*>(outk);
-                *reinterpret_cast<uint4*>(vw + (int64_t)vp * HD + dl) = *reinterpret_cast<const uint4*>(
-                    vnew + (int64_t)b * kv_stride + (int64_t)kvh * HD + dl);
-            }
+        for (int i = 0; i < 8; ++i) {
+            knf[i] = to_f32(rk[i]);
+            vnf[i] = to_f32(rvv[i]);
         }
-        __syncthreads();
+        if (cr) rope_lane8<T, LPR>(knf, dl, cr, sr, half, interleaved);
+        T outk[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            outk[i] = from_f32<T>(knf[i]);
+            knf[i] = to_f32(outk[i]);  // the stored (rounded) key is what gets attended
+        }
+        if (own_new && hgrp == 0 && wave == 0 && sub == 0) {
+            *reinterpret_cast<uint4*>(kw + (int64_t)vp * HD + dl) = *reinterpret_cast<uint4*>(outk);
+            *reinterpret_cast<uint4*>(vw + (int64_t)vp * HD + dl) = vraw;
+        }
     }
-    const T* kbase = (copy_past ? kpast + (int64_t)bk * past_cap * HD : kw);
-    const T* vbase = (copy_past ? vpast + (int64_t)bk * past_cap * HD : vw);
 
     float m[G], l[G], o[G][8];
 #pragma unroll
@@ -250,21 +296,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
     }
-    for (int base = j0; base < j1; base += RPS * U) {
-        uint4 kr[U], vr[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int j = base + u * RPS + wave * RPW + sub;
-            kr[u] = make_uint4(0, 0, 0, 0);
-            vr[u] = make_uint4(0, 0, 0, 0);
-            if (j < j1) {
-                const bool fresh = j >= vp;  // the new row lives in present
-                const T* ks = (fresh ? kw : kbase) + (int64_t)j * HD + dl;
-                const T* vs = (fresh ? vw : vbase) + (int64_t)j * HD + dl;
-                kr[u] = *reinterpret_cast<const uint4*>(ks);
-                vr[u] = *reinterpret_cast<const uint4*>(vs);
-            }
-        }
+    auto process = [&](const uint4 (&kk)[U], const uint4 (&vv)[U], int base) {
         float sc[U][G];
         float bmax[G];
 #pragma unroll
@@ -272,14 +304,15 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = base + u * RPS + wave * RPW + sub;
-            if (copy_past && j < vp && j < j1) {
-                *reinterpret_cast<uint4*>(kw + (int64_t)j * HD + dl) = kr[u];
-                *reinterpret_cast<uint4*>(vw + (int64_t)j * HD + dl) = vr[u];
+            if (copy_past && hgrp == 0 && j < vp && j < j1) {
+                *reinterpret_cast<uint4*>(kw + (int64_t)j * HD + dl) = kk[u];
+                *reinterpret_cast<uint4*>(vw + (int64_t)j * HD + dl) = vv[u];
             }
-            const T* kv = reinterpret_cast<const T*>(&kr[u]);
+            const T* kv = reinterpret_cast<const T*>(&kk[u]);
+            const bool fresh = j == vp;
             float kf[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) kf[i] = to_f32(kv[i]);
+            for (int i = 0; i < 8; ++i) kf[i] = fresh ? knf[i] : to_f32(kv[i]);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float d = 0.f;
@@ -302,10 +335,11 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const T* vv = reinterpret_cast<const T*>(&vr[u]);
+            const int j = base + u * RPS + wave * RPW + sub;
+            const T* vv8 = reinterpret_cast<const T*>(&vv[u]);
             float vf[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) vf[i] = to_f32(vv[i]);
+            for (int i = 0; i < 8; ++i) vf[i] = j == vp ? vnf[i] : to_f32(vv8[i]);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const float p = sc[u][g] == -INFINITY ? 0.f : __expf(sc[u][g] - m[g]);
@@ -314,35 +348,42 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
                 for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i]);
             }
         }
+    };
+    // 3. Blocks, software-pipelined.
+    for (int base = j0; base < j1; base += 2 * BLK) {
+        uint4 kn[U], vn[U];
+        const bool more = base + BLK < j1;
+        if (more) load_block(kn, vn, base + BLK);
+        process(kr, vr, base);
+        if (!more) break;
+        if (base + 2 * BLK < j1) load_block(kr, vr, base + 2 * BLK);
+        process(kn, vn, base + BLK);
     }
-    // Merge the RPW lane groups of each wave and the 4 waves through LDS.
-    if ((lane % LPR) == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            s_m[wave][sub][g] = m[g];
-            s_l[wave][sub][g] = l[g];
-        }
-    }
-    __syncthreads();
-    float M[G], L[G];
+    // Merge the RPW lane groups of each wave with cross-lane sums, then the 4
+    // waves through LDS.
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        float mm = -INFINITY;
-        for (int w = 0; w < 4; ++w)
-            for (int r = 0; r < RPW; ++r) mm = fmaxf(mm, s_m[w][r][g]);
-        float ll = 0.f;
-        for (int w = 0; w < 4; ++w)
-            for (int r = 0; r < RPW; ++r)
-                if (s_m[w][r][g] != -INFINITY) ll += s_l[w][r][g] * __expf(s_m[w][r][g] - mm);
-        M[g] = mm;
-        L[g] = ll;
-        const float f = m[g] == -INFINITY ? 0.f : __expf(m[g] - mm);
+        float mw = m[g];
+        {
+            if constexpr (LPR == 8) mw = fmaxf(mw, dpp_mov<0x128>(mw));
+            if constexpr (LPR <= 16) {
+                const LanePair p = swap16(mw);
+                mw = fmaxf(p.a, p.b);
+            }
+            const LanePair p = swap32(mw);
+            mw = fmaxf(p.a, p.b);
+        }
+        const float f = m[g] == -INFINITY ? 0.f : __expf(m[g] - mw);
+        l[g] = across_groups_sum<LPR>(l[g] * f);
+        m[g] = mw;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float x = o[g][i] * f;
+        for (int i = 0; i < 8; ++i) o[g][i] = across_groups_sum<LPR>(o[g][i] * f);
+    }
+    if (lane == 0) {
 #pragma unroll
-            for (int off = LPR; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
-            o[g][i] = x;
+        for (int g = 0; g < G; ++g) {
+            s_m[wave][g] = m[g];
+            s_l[wave][g] = l[g];
         }
     }
     if (sub == 0) {
@@ -354,17 +395,25 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     __syncthreads();
     for (int idx = tid; idx < G * HD; idx += 256) {
         const int g = idx / HD, d = idx % HD;
-        const float acc = s_o[0][g][d] + s_o[1][g][d] + s_o[2][g][d] + s_o[3][g][d];
-        const int64_t row = (int64_t)b * H + kvh * G + g;
+        const float m0 = s_m[0][g], m1 = s_m[1][g], m2 = s_m[2][g], m3 = s_m[3][g];
+        const float M = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+        const float w0 = m0 == -INFINITY ? 0.f : __expf(m0 - M);
+        const float w1 = m1 == -INFINITY ? 0.f : __expf(m1 - M);
+        const float w2 = m2 == -INFINITY ? 0.f : __expf(m2 - M);
+        const float w3 = m3 == -INFINITY ? 0.f : __expf(m3 - M);
+        const float L = s_l[0][g] * w0 + s_l[1][g] * w1 + s_l[2][g] * w2 + s_l[3][g] * w3;
+        const float acc = s_o[0][g][d] * w0 + s_o[1][g][d] * w1 + s_o[2][g][d] * w2 +
+                          s_o[3][g][d] * w3;
+        const int64_t row = (int64_t)b * H + h0 + g;
         if (nsplit == 1) {
-            out[row * HD + d] = from_f32<T>(L[g] > 0.f ? acc / L[g] : 0.f);
+            out[row * HD + d] = from_f32<T>(L > 0.f ? acc / L : 0.f);
             continue;
         }
         float* dst = part + (row * nsplit + split) * (HD + 2);
         dst[d] = acc;
         if (d == 0) {
-            dst[HD] = M[g];
-            dst[HD + 1] = L[g];
+            dst[HD] = M;
+            dst[HD + 1] = L;
         }
     }
 }
@@ -555,8 +604,7 @@ __device__ void attn_tile_body(const TileDesc& t, int kvh, int G, int H, const T
                 tmax = fmaxf(tmax, sc);
             }
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
+        tmax = group_max<4>(tmax);
         __syncthreads();
         if (row_live) {
             const float m_old = sM[r_s];
@@ -568,8 +616,7 @@ __device__ void attn_tile_body(const TileDesc& t, int kvh, int G, int H, const T
                 sS[r_s][jj] = e;
                 lsum += e;
             }
-            lsum += __shfl_xor(lsum, 1, 64);
-            lsum += __shfl_xor(lsum, 2, 64);
+            lsum = group_sum<4>(lsum);  // the 4 lanes of a row share row_live
             const float alpha = (m_old == -INFINITY) ? 0.f : __expf(m_old - m_new);
             if ((tid % 4) == 0) {
                 sL[r_s] = sL[r_s] * alpha + lsum;
@@ -905,6 +952,43 @@ extern "C" size_t ortmi_group_query_attention_workspace_size(int64_t batch, int6
     return q + part;
 }
 
+// Launch of the one-token decode kernel for G query heads per KV head. When the
+// (batch x KV head x key split) grid is small, the G heads are spread over
+// workgroups (each reading the same cached rows) so that fewer heads sit on one
+// workgroup's critical path: a decode step at short context is bound by the
+// instructions of one workgroup, not by bandwidth.
+template <typename T, int HD>
+static int launch_gqa_decode(int G, int B, int KV, int ns, int chunk, const T* q, const T* k,
+                             const T* v, int64_t q_stride, int64_t kv_stride, const T* cos_c,
+                             const T* sin_c, int half, int interleaved, const T* kpast,
+                             const T* vpast, T* kpres, T* vpres, int64_t past_cap,
+                             int64_t pres_cap, int copy_past, int vp, float sc, float* part,
+                             T* out, const int* total_dev, int vp_max, hipStream_t st) {
+    // One head per workgroup measured best at 20 workgroups (6 heads per KV head,
+    // 640-row buffer): 7.3 us with the merge against 8.5 / 9.7 / 12.8 us for 2 / 3 / 6.
+    const int per = (int64_t)B * KV * ns < 2L * device_cu_count() ? 1 : G;
+    const int gsplit = G / per;
+    dim3 grid((unsigned)(B * KV * gsplit), (unsigned)ns);
+    auto launch = [&](auto gtag) {
+        constexpr int GG = decltype(gtag)::value;
+        hipLaunchKernelGGL((gqa_decode_kernel<T, HD, GG>), grid, dim3(256), 0, st, q, k, v,
+                           q_stride, kv_stride, cos_c, sin_c, half, interleaved, kpast, vpast,
+                           kpres, vpres, past_cap, pres_cap, copy_past, vp, chunk, ns, KV, sc,
+                           part, out, total_dev, vp_max, gsplit);
+    };
+    switch (per) {  // query heads per workgroup
+        case 1: launch(std::integral_constant<int, 1>()); break;
+        case 2: launch(std::integral_constant<int, 2>()); break;
+        case 3: launch(std::integral_constant<int, 3>()); break;
+        case 4: launch(std::integral_constant<int, 4>()); break;
+        case 5: launch(std::integral_constant<int, 5>()); break;
+        case 6: launch(std::integral_constant<int, 6>()); break;
+        case 7: launch(std::integral_constant<int, 7>()); break;
+        default: launch(std::integral_constant<int, 8>()); break;
+    }
+    return check_launch("gqa_decode");
+}
+
 template <typename T, int HD>
 static int run_gqa(const void* query, const void* key, const void* value, const void* past_key,
                    const void* past_value, int64_t cap, int total, const void* cos_c,
@@ -964,28 +1048,12 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
     if (decode_fast) {
         int chunk = 0;
         const int ns = gqa_nsplit((int64_t)B * KV, nkeys, chunk);
-        dim3 grid(B * KV, ns);
-        auto launch = [&](auto gtag) {
-            constexpr int GG = decltype(gtag)::value;
-            hipLaunchKernelGGL((gqa_decode_kernel<T, HD, GG>), grid, dim3(256), 0, st, q, k, v,
-                               q_stride, kv_stride, static_cast<const T*>(cos_c),
-                               static_cast<const T*>(sin_c), half, interleaved,
-                               static_cast<const T*>(past_key), static_cast<const T*>(past_value),
-                               static_cast<T*>(pk), static_cast<T*>(pv), cap, pcap,
-                               fused_copy ? 1 : 0, vp, chunk, ns, KV, sc, part,
-                               static_cast<T*>(output), (const int*)nullptr, 0);
-        };
-        switch (G) {  // query heads per KV head of common decoders (e.g. 6 and 7 in Qwen2.5)
-            case 1: launch(std::integral_constant<int, 1>()); break;
-            case 2: launch(std::integral_constant<int, 2>()); break;
-            case 3: launch(std::integral_constant<int, 3>()); break;
-            case 4: launch(std::integral_constant<int, 4>()); break;
-            case 5: launch(std::integral_constant<int, 5>()); break;
-            case 6: launch(std::integral_constant<int, 6>()); break;
-            case 7: launch(std::integral_constant<int, 7>()); break;
-            default: launch(std::integral_constant<int, 8>()); break;
-        }
-        if (int rc = check_launch("gqa_decode")) return rc;
+        if (int rc = launch_gqa_decode<T, HD>(
+                G, B, KV, ns, chunk, q, k, v, q_stride, kv_stride, static_cast<const T*>(cos_c),
+                static_cast<const T*>(sin_c), half, interleaved, static_cast<const T*>(past_key),
+                static_cast<const T*>(past_value), static_cast<T*>(pk), static_cast<T*>(pv), cap,
+                pcap, fused_copy ? 1 : 0, vp, sc, part, static_cast<T*>(output), nullptr, 0, st))
+            return rc;
         if (ns == 1) return ORTMI_OK;
         hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(B * H), dim3(128), 0, st, part,
                            static_cast<T*>(output), ns, (const int*)nullptr, hd, H,
@@ -1096,27 +1164,12 @@ static int run_gqa_decode_capturable(const void* query, const void* key, const v
     const int ns = gqa_nsplit((int64_t)B * KV, cap, chunk);
     const float sc = scale != 0.f ? scale : 1.0f / sqrtf((float)HD);
     const int vp_max = (int)std::min<int64_t>(cap, cos_c ? max_pos : cap) - 1;
-    dim3 grid(B * KV, ns);
-    auto launch = [&](auto gtag) {
-        constexpr int GG = decltype(gtag)::value;
-        hipLaunchKernelGGL((gqa_decode_kernel<T, HD, GG>), grid, dim3(256), 0, st, q, k, v,
-                           q_stride, kv_stride, static_cast<const T*>(cos_c),
-                           static_cast<const T*>(sin_c), half, interleaved,
-                           static_cast<const T*>(kv_key), static_cast<const T*>(kv_value),
-                           static_cast<T*>(kv_key), static_cast<T*>(kv_value), cap, cap, 0, 0,
-                           chunk, ns, KV, sc, part, static_cast<T*>(output), total_dev, vp_max);
-    };
-    switch (G) {
-        case 1: launch(std::integral_constant<int, 1>()); break;
-        case 2: launch(std::integral_constant<int, 2>()); break;
-        case 3: launch(std::integral_constant<int, 3>()); break;
-        case 4: launch(std::integral_constant<int, 4>()); break;
-        case 5: launch(std::integral_constant<int, 5>()); break;
-        case 6: launch(std::integral_constant<int, 6>()); break;
-        case 7: launch(std::integral_constant<int, 7>()); break;
-        default: launch(std::integral_constant<int, 8>()); break;
-    }
-    if (int rc = check_launch("gqa_decode")) return rc;
+    if (int rc = launch_gqa_decode<T, HD>(
+            G, B, KV, ns, chunk, q, k, v, q_stride, kv_stride, static_cast<const T*>(cos_c),
+            static_cast<const T*>(sin_c), half, interleaved, static_cast<const T*>(kv_key),
+            static_cast<const T*>(kv_value), static_cast<T*>(kv_key), static_cast<T*>(kv_value),
+            cap, cap, 0, 0, sc, part, static_cast<T*>(output), total_dev, vp_max, st))
+        return rc;
     if (ns == 1) return ORTMI_OK;
     hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(B * H), dim3(128), 0, st, part,
                        static_cast<T*>(output), ns, (const int*)nullptr, HD, H, (int64_t)H * HD,

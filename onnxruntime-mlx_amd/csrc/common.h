@@ -46,23 +46,80 @@ template <typename T>
 __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
 
 // ------------------------------------------------------------ reductions --
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// Cross-lane reductions without the LDS permute path: inside a 16-lane row the
+// partner values come from DPP moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror), which after the two quad steps pair every lane
+// with a lane holding the other part of its group; across rows the gfx950
+// v_permlane16_swap / v_permlane32_swap exchange the halves of 32 / 64 lanes.
+// Every lane of a group ends with the same value (the combining operations are
+// commutative). All lanes of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+struct LanePair {
+    float a, b;
+};
+__device__ __forceinline__ LanePair swap16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v),
+                                                    __builtin_bit_cast(unsigned, v), false, false);
+    return {__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1])};
 }
+__device__ __forceinline__ LanePair swap32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
+                                                    __builtin_bit_cast(unsigned, v), false, false);
+    return {__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1])};
+}
+
 // Sum over aligned groups of `W` lanes (W a power of two <= 64).
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if constexpr (W >= 2) v += dpp_mov<0xB1>(v);
+    if constexpr (W >= 4) v += dpp_mov<0x4E>(v);
+    if constexpr (W >= 8) v += dpp_mov<0x141>(v);
+    if constexpr (W >= 16) v += dpp_mov<0x140>(v);
+    if constexpr (W >= 32) {
+        const LanePair p = swap16(v);
+        v = p.a + p.b;
+    }
+    if constexpr (W >= 64) {
+        const LanePair p = swap32(v);
+        v = p.a + p.b;
+    }
     return v;
 }
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (W >= 2) v = fmaxf(v, dpp_mov<0xB1>(v));
+    if constexpr (W >= 4) v = fmaxf(v, dpp_mov<0x4E>(v));
+    if constexpr (W >= 8) v = fmaxf(v, dpp_mov<0x141>(v));
+    if constexpr (W >= 16) v = fmaxf(v, dpp_mov<0x140>(v));
+    if constexpr (W >= 32) {
+        const LanePair p = swap16(v);
+        v = fmaxf(p.a, p.b);
+    }
+    if constexpr (W >= 64) {
+        const LanePair p = swap32(v);
+        v = fmaxf(p.a, p.b);
+    }
+    return v;
+}
+// Sum over the lanes that share (lane % LPR), i.e. across the 64 / LPR aligned
+// groups of LPR lanes (LPR in {8, 16, 32}).
+template <int LPR>
+__device__ __forceinline__ float across_groups_sum(float v) {
+    static_assert(LPR == 8 || LPR == 16 || LPR == 32, "group width");
+    if constexpr (LPR == 8) v += dpp_mov<0x128>(v);  // row_ror:8 = lane ^ 8 in a row
+    if constexpr (LPR <= 16) {
+        const LanePair p = swap16(v);
+        v = p.a + p.b;
+    }
+    const LanePair p = swap32(v);
+    return p.a + p.b;
+}
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
 __device__ __forceinline__ int nibble(uint8_t byte, int hi) { return hi ? (byte >> 4) : (byte & 0x0f); }
 
