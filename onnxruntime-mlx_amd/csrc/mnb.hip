@@ -56,10 +56,27 @@ __device__ __forceinline__ int act_unit(int u) {
     return u ^ ((u / (8 * CPL)) & 7);
 }
 
-template <int R, int CPL>
+// Zero-point bytes that cover the blocks of one lane's CPL chunks, worst case
+// over the 64 lanes (4-bit zero points: two blocks per byte).
+constexpr int zp_window(int BS, int CPL) {
+    int most = 1;
+    for (int l = 0; l < 64; ++l) {
+        const int c0 = l * CPL;
+        const int b0 = (32 * c0) / BS / 2, b1 = (32 * (c0 + CPL - 1)) / BS / 2;
+        if (b1 - b0 + 1 > most) most = b1 - b0 + 1;
+    }
+    return most;
+}
+
+// One group of R rows as loaded: weights, scales and zero-point bytes are kept
+// raw and converted only when the group is reduced, so no instruction consumes a
+// prefetched value before its row is needed (a conversion at load time would
+// make the compiler wait for the prefetch there).
+template <typename T, int R, int CPL, int ZB>
 struct GemvGroup {
     uint4 w[R][CPL];
-    float s[R][CPL], z[R][CPL];
+    T s[R][CPL];
+    uint8_t z[R][ZB];
 };
 
 // Lane l owns the CPL consecutive 32-code chunks [l*CPL, (l+1)*CPL) of every row,
@@ -95,7 +112,8 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     static_assert(!PAIR || R == 2, "SwiGLU pairs take two rows per group");
     extern __shared__ float4 sA[];
     __shared__ float s_red[4];
-    using Group = GemvGroup<R, CPL>;
+    constexpr int ZB = zp_window(BS, CPL);
+    using Group = GemvGroup<T, R, CPL, ZB>;
     const int Kp = nb * BS;
     const int C = Kp / 32;  // 32-code chunks per row
     const int lane = threadIdx.x & 63;
@@ -134,41 +152,27 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
         }
     }
 
-    // 2. weights of the first row group.
+    // 2. weights of the first row group. Loads never branch: a group index past
+    // the end is clamped to the last group and a chunk past the row end to the
+    // last chunk (in bounds; such lanes hold zero activations, so they add
+    // nothing), which keeps every wait on a prefetch exact.
+    const int blk0 = (32 * min(c0, C - 1)) / BS;
     auto load_group = [&](Group& g, int gi) {
-        const int n0 = gi * R;
+        const int gc = min(gi, ngroups - 1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int n = n0 + r;
-            const bool row_ok = gi < ngroups && n < N;
+            const int n = min(gc * R + r, N - 1);
             const uint8_t* brow = B + (size_t)n * row_bytes;
-            // Zero-point bytes covering this lane's blocks (at most 3 for CPL <= 5).
-            const int blk0 = (32 * c0) / BS;
-            uint8_t zb[3] = {0x88, 0x88, 0x88};
-            if (row_ok && Z && c0 < C) {
-                const int clast = min(c0 + CPL - 1, C - 1);
-                const int last_byte = ((32 * clast) / BS) / 2;
 #pragma unroll
-                for (int t = 0; t < 3; ++t)
-                    if (blk0 / 2 + t <= last_byte) zb[t] = Z[(size_t)n * zp_cols + blk0 / 2 + t];
-            }
+            for (int t = 0; t < ZB; ++t)
+                g.z[r][t] = Z ? Z[(size_t)n * zp_cols + min(blk0 / 2 + t, zp_cols - 1)] : 0x88;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
-                const int c = c0 + j;
-                if (row_ok && c < C) {
-                    const u32x4_t v = __builtin_nontemporal_load(
-                        reinterpret_cast<const u32x4_t*>(brow) + c);
-                    g.w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
-                    const int blk = (32 * c) / BS;
-                    g.s[r][j] = to_f32(S[(size_t)n * nb + blk]);
-                    const int d = blk / 2 - blk0 / 2;
-                    const uint8_t zbyte = d == 0 ? zb[0] : (d == 1 ? zb[1] : zb[2]);
-                    g.z[r][j] = Z ? (float)nibble(zbyte, blk & 1) : 8.f;
-                } else {
-                    g.w[r][j] = make_uint4(0, 0, 0, 0);
-                    g.s[r][j] = 0.f;
-                    g.z[r][j] = 0.f;
-                }
+                const int c = min(c0 + j, C - 1);
+                const u32x4_t v =
+                    __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(brow) + c);
+                g.w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
+                g.s[r][j] = S[(size_t)n * nb + (32 * c) / BS];
             }
         }
     };
@@ -248,44 +252,50 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     }
 
     auto reduce_store = [&](const Group& g, int gi) {
+        const int gc = min(gi, ngroups - 1);
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             float total = 0.f;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
-                const float d = dot32_codes(a[j], g.w[r][j]);
-                total = fmaf(g.s[r][j], d - g.z[r][j] * asum[j], total);
+                const int blk = (32 * min(c0 + j, C - 1)) / BS;
+                const int d = blk / 2 - blk0 / 2;
+                uint8_t zbyte = g.z[r][0];
+#pragma unroll
+                for (int t = 1; t < ZB; ++t)
+                    if (d == t) zbyte = g.z[r][t];
+                const float zf = (float)nibble(zbyte, blk & 1);
+                const float d32 = dot32_codes(a[j], g.w[r][j]);
+                total = fmaf(to_f32(g.s[r][j]), d32 - zf * asum[j], total);
             }
             acc[r] = total;
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-        const int n0 = gi * R;
+        // Every lane holds the sums and every lane stores (same-address writes of a
+        // wave coalesce). A clamped group past the end recomputed the last group,
+        // so it writes that group's values again: no branch around the store.
         if constexpr (PAIR) {
-            if (lane == 0 && n0 + 1 < N) {
-                const float g = round_to<T>(acc[0]), up = round_to<T>(acc[1]);
-                const float sig = round_to<T>(1.0f / (1.0f + __expf(-g)));
-                Y[gi] = from_f32<T>(round_to<T>(g * sig) * up);
-            }
+            const float gv = round_to<T>(acc[0]), up = round_to<T>(acc[1]);
+            const float sig = round_to<T>(1.0f / (1.0f + __expf(-gv)));
+            Y[gc] = from_f32<T>(round_to<T>(gv * sig) * up);
             return;
         }
-        if (lane < R) {
-            float v = acc[0];
+        const int r = lane % R;
+        float v = acc[0];
 #pragma unroll
-            for (int r = 1; r < R; ++r)
-                if (lane == r) v = acc[r];
-            if (n0 + lane < N) Y[n0 + lane] = from_f32<T>(v);
-        }
+        for (int i = 1; i < R; ++i)
+            if (r == i) v = acc[i];
+        Y[min(gc * R + r, N - 1)] = from_f32<T>(v);
     };
 
     for (int gi = g0; gi < ngroups; gi += 2 * waves_total) {
         const int g1 = gi + waves_total;
-        if (g1 < ngroups) load_group(gb, g1);
+        load_group(gb, g1);
         reduce_store(ga, gi);
         if (g1 >= ngroups) break;
-        const int g2 = g1 + waves_total;
-        if (g2 < ngroups) load_group(ga, g2);
+        load_group(ga, g1 + waves_total);
         reduce_store(gb, g1);
     }
 }
