@@ -641,8 +641,8 @@ __device__ void attn_tile_body(const TileDesc& t, int kvh, int G, int H, const T
     const int tok = t.tok0 + r_s / G, h = kvh * G + r_s % G;
     float m = sM[r_s], l = sL[r_s];
     if (part) {
-        // Partial row index: (tile-local row) handled by caller via `part` offset.
-        float* dst = part + ((int64_t)r_s * nsplit + split) * (VHD + 2);
+        // Partial rows are token-major: row tok * H + h.
+        float* dst = part + (((int64_t)tok * H + h) * nsplit + split) * (VHD + 2);
 #pragma unroll
         for (int i = 0; i < DV; ++i) dst[d_o + i] = o[i];
         if ((tid % 4) == 0) {
@@ -665,6 +665,281 @@ __device__ void attn_tile_body(const TileDesc& t, int kvh, int G, int H, const T
     for (int i = 0; i < DV; ++i) dst[i] = from_f32<T>(o[i] * inv);
 }
 
+// The attention tile on the matrix cores (fp16), 128 query rows per workgroup,
+// computed transposed so that everything a query needs stays in its lanes:
+//   S^T = K Q^T     (v_mfma_f32_32x32x16_f16; A = 32 keys x 16 dims from LDS,
+//                    B = 16 dims x 32 queries, held in registers for the whole tile)
+//   O^T += V^T P^T  (A = 32 head dims x 16 keys from transposed V in LDS,
+//                    B = 16 keys x 32 queries = this lane's own probabilities)
+// In the accumulator layout a lane holds one query (column lane % 32) and 16 keys
+// (or 16 head dims) of it, and the two lanes lane, lane ^ 32 share a query. So the
+// online softmax is register arithmetic plus one permlane32 swap per reduction,
+// and P never goes through LDS: the k-order of the P V product is permuted to the
+// keys a lane already holds (keys {4h..4h+3, 8+4h..8+4h+3} of each 16 for lane half
+// h), and V^T is read in that same order. fp32 accumulation; P is rounded to
+// fp16 once and the softmax denominator sums the same rounded values.
+// Wave w owns queries 32w..32w+31 of the tile. Key blocks of 64 go global ->
+// registers -> LDS, the next block's loads in flight while the current one is used.
+constexpr int kMfmaRows = 128;
+
+template <int HD, int VHD, bool PAGED>
+__device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
+                               const half_t* __restrict__ qrot, const DenseKV& dk,
+                               const PagedKV& pk, float scale, const float* __restrict__ sink,
+                               int k0, int k1, half_t* __restrict__ out, int64_t out_tok_stride,
+                               float* __restrict__ part, int nsplit, int split) {
+    static_assert(kKeyTile == 64 && HD % 16 == 0 && VHD % 32 == 0, "tile shape");
+    constexpr int KP = HD + 8, VP = kKeyTile + 8;
+    constexpr int DT = VHD / 32;          // head-dim tiles of O^T
+    __shared__ half_t sK[kKeyTile * KP];
+    __shared__ half_t sVt[VHD * VP];
+    __shared__ unsigned long long sOk;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lrow = lane & 31, hh = lane >> 5, lk = hh * 8;
+    const int rows = t.ntok * G;
+    const int q = wave * 32 + lrow;                // this lane's query row in the tile
+    const bool qlive = q < rows;
+    const int qpos = t.qpos0 + (qlive ? q / G : 0);
+    // Earliest position among the wave's queries: keys up to it are causally
+    // visible to every query of the wave.
+    const int qpos_wave = t.qpos0 + (wave * 32) / G;
+    // Scores are kept in the log2 domain (exp2 is the hardware exponential).
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float sc2 = scale * kLog2e;
+    // Q^T operand: 8 consecutive head dims per k-step of this lane's query.
+    half8_t qb[HD / 16];
+    {
+        const half_t* qr = qlive ? qrot + ((int64_t)(t.tok0 + q / G) * H + kvh * G + q % G) * HD
+                                 : nullptr;
+#pragma unroll
+        for (int s2 = 0; s2 < HD / 16; ++s2) {
+            half8_t v;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = (half_t)0.f;
+            if (qr) v = *reinterpret_cast<const half8_t*>(qr + s2 * 16 + lk);
+            qb[s2] = v;
+        }
+    }
+    float m = -INFINITY, l = 0.f;
+    float16_t oT[DT];
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oT[d][e] = 0.f;
+
+    constexpr int KPT = kKeyTile * (HD / 8) / 256, VPT = kKeyTile * (VHD / 8) / 256;
+    static_assert(KPT >= 1 && VPT >= 1, "block staging");
+    uint4 kreg[KPT], vreg[VPT];
+    int kok = 0;
+    auto fetch = [&](int kb) {
+        const int nk = min(kKeyTile, k1 - kb);
+        kok = 0;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int idx = tid + 256 * i, r = idx % kKeyTile, c = (idx / kKeyTile) * 8;
+            const half_t* p =
+                r < nk ? key_ptr<half_t, HD, VHD, PAGED>(dk, pk, t, t.seq, kvh, kb + r, false)
+                       : nullptr;
+            kreg[i] = p ? *reinterpret_cast<const uint4*>(p + c) : make_uint4(0, 0, 0, 0);
+            kok |= (p != nullptr) << i;
+        }
+        // V: a thread takes VPT consecutive keys of one 8-dim chunk, so the
+        // transposed store writes VPT keys of a head dim at once.
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int r = VPT * (tid % (kKeyTile / VPT)) + i, c = (tid / (kKeyTile / VPT)) * 8;
+            const half_t* p =
+                r < nk ? key_ptr<half_t, HD, VHD, PAGED>(dk, pk, t, t.seq, kvh, kb + r, true)
+                       : nullptr;
+            vreg[i] = p ? *reinterpret_cast<const uint4*>(p + c) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int idx = tid + 256 * i, r = idx % kKeyTile, c = (idx / kKeyTile) * 8;
+            *reinterpret_cast<uint4*>(&sK[r * KP + c]) = kreg[i];
+        }
+        // Threads 0..63 hold the first vector (c = 0) of keys 0..63: one ballot.
+        const unsigned long long ok = __ballot(kok & 1);
+        if (tid == 0) sOk = ok;
+        {
+            const int r0 = VPT * (tid % (kKeyTile / VPT)), c = (tid / (kKeyTile / VPT)) * 8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                half_t col[VPT];
+#pragma unroll
+                for (int i = 0; i < VPT; ++i) col[i] = reinterpret_cast<const half_t*>(&vreg[i])[e];
+                if constexpr (VPT == 4)
+                    *reinterpret_cast<uint2*>(&sVt[(c + e) * VP + r0]) =
+                        *reinterpret_cast<const uint2*>(col);
+                else if constexpr (VPT == 2)
+                    *reinterpret_cast<uint32_t*>(&sVt[(c + e) * VP + r0]) =
+                        *reinterpret_cast<const uint32_t*>(col);
+                else
+#pragma unroll
+                    for (int i = 0; i < VPT; ++i) sVt[(c + e) * VP + r0 + i] = col[i];
+            }
+        }
+    };
+    if (k0 < k1) fetch(k0);
+    for (int kb = k0; kb < k1; kb += kKeyTile) {
+        commit();
+        __syncthreads();
+        if (kb + kKeyTile < k1) fetch(kb + kKeyTile);
+        const unsigned long long okm = sOk;
+        // S^T for the two 32-key tiles.
+        float16_t st[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) st[kt][e] = 0.f;
+#pragma unroll
+            for (int s2 = 0; s2 < HD / 16; ++s2) {
+                const half8_t a =
+                    *reinterpret_cast<const half8_t*>(&sK[(kt * 32 + lrow) * KP + s2 * 16 + lk]);
+                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[s2], st[kt], 0, 0, 0);
+            }
+        }
+        // Mask (only blocks that are not fully visible), scale, block max.
+        const bool full = kb + kKeyTile <= k1 && okm == ~0ull && kb + kKeyTile - 1 <= qpos_wave;
+        float bmax = -INFINITY;
+        if (full) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    st[kt][e] *= sc2;
+                    bmax = fmaxf(bmax, st[kt][e]);
+                }
+        } else {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int kk = kt * 32 + 8 * (e / 4) + 4 * hh + (e & 3);
+                    const int j = kb + kk;
+                    const bool ok = j < k1 && j <= qpos && ((okm >> kk) & 1ull);
+                    const float x = ok ? st[kt][e] * sc2 : -INFINITY;
+                    st[kt][e] = x;
+                    bmax = fmaxf(bmax, x);
+                }
+        }
+        {
+            const LanePair pr = swap32(bmax);
+            bmax = fmaxf(pr.a, pr.b);
+        }
+        const float m_new = fmaxf(m, bmax);
+        const float alpha = (m == -INFINITY) ? 0.f : exp2f(m - m_new);
+        half8_t pb[4];  // P^T operands: k-step kk uses e in [8 (kk % 2), 8 (kk % 2) + 8) of tile kk / 2
+        float lsum = 0.f;
+        const float mref = m_new == -INFINITY ? 0.f : m_new;  // exp2(-inf - 0) = 0
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const half_t ph = (half_t)exp2f(st[kt][e] - mref);
+                pb[kt * 2 + e / 8][e % 8] = ph;
+                lsum += (float)ph;
+            }
+        {
+            const LanePair pr = swap32(lsum);
+            lsum = pr.a + pr.b;
+        }
+        l = l * alpha + lsum;
+        m = m_new;
+        // Rescale O only when some query's running max moved.
+        if (__any(alpha != 1.f)) {
+#pragma unroll
+            for (int d = 0; d < DT; ++d)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oT[d][e] *= alpha;
+        }
+        // O^T += V^T P^T over the 4 k-steps of 16 keys.
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int kbase = (kk / 2) * 32 + (kk % 2) * 16 + 4 * hh;
+#pragma unroll
+            for (int d = 0; d < DT; ++d) {
+                const half_t* vr = &sVt[(d * 32 + lrow) * VP + kbase];
+                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
+                half8_t a;
+                const half_t* lo_h = reinterpret_cast<const half_t*>(&lo);
+                const half_t* hi_h = reinterpret_cast<const half_t*>(&hi);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    a[i] = lo_h[i];
+                    a[4 + i] = hi_h[i];
+                }
+                oT[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kk], oT[d], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // the next block overwrites sK, sVt and sOk
+    }
+    if (!qlive) return;
+    m = m == -INFINITY ? m : m / kLog2e;  // back to the natural-log domain of the merge
+    const int tok = t.tok0 + q / G, h = kvh * G + q % G;
+    if (part) {
+        float* dst = part + (((int64_t)tok * H + h) * nsplit + split) * (VHD + 2);
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) dst[d * 32 + 8 * (e / 4) + 4 * hh + (e & 3)] = oT[d][e];
+        if (hh == 0) {
+            dst[VHD] = m;
+            dst[VHD + 1] = l;
+        }
+        return;
+    }
+    float a = 1.f;
+    if (sink) {
+        const float sv2 = sink[h];
+        const float mm = fmaxf(m, sv2);
+        a = (m == -INFINITY) ? 0.f : __expf(m - mm);
+        l = l * a + __expf(sv2 - mm);
+    }
+    const float inv = l > 0.f ? a / l : 0.f;
+    half_t* dst = out + (int64_t)tok * out_tok_stride + (int64_t)h * VHD;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            half_t v4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v4[i] = (half_t)(oT[d][4 * e4 + i] * inv);
+            *reinterpret_cast<uint2*>(dst + d * 32 + 8 * e4 + 4 * hh) =
+                *reinterpret_cast<const uint2*>(v4);
+        }
+}
+
+// Tile body for a dtype: the matrix-core tile for fp16, the VALU tile otherwise.
+// Query rows per workgroup of the tile body used for dtype T.
+template <typename T, int VHD>
+constexpr int tile_rows() {
+    return std::is_same<T, half_t>::value && VHD % 32 == 0 ? kMfmaRows : kTileRows;
+}
+template <typename T>
+static int tile_rows_for(int vhd) {
+    return std::is_same<T, half_t>::value && vhd % 32 == 0 ? kMfmaRows : kTileRows;
+}
+
+template <typename T, int HD, int VHD, bool PAGED>
+__device__ __forceinline__ void attn_tile(const TileDesc& t, int kvh, int G, int H,
+                                          const T* __restrict__ qrot, const DenseKV& dk,
+                                          const PagedKV& pk, float scale,
+                                          const float* __restrict__ sink, int k0, int k1,
+                                          T* __restrict__ out, int64_t out_tok_stride,
+                                          float* __restrict__ part, int nsplit, int split) {
+    if constexpr (tile_rows<T, VHD>() == kMfmaRows)
+        attn_mfma_body<HD, VHD, PAGED>(t, kvh, G, H, qrot, dk, pk, scale, sink, k0, k1, out,
+                                        out_tok_stride, part, nsplit, split);
+    else
+        attn_tile_body<T, HD, VHD, PAGED>(t, kvh, G, H, qrot, dk, pk, scale, sink, k0, k1, out,
+                                          out_tok_stride, part, nsplit, split);
+}
+
 // GQA prefill / S > 1: grid (B * tiles_per_seq, KV). Keys from `present`.
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void gqa_tile_kernel(const T* __restrict__ qrot, DenseKV dk,
@@ -685,8 +960,8 @@ __global__ __launch_bounds__(256) void gqa_tile_kernel(const T* __restrict__ qro
     t.tok_seq0 = b * S;
     PagedKV none{};
     const int k1 = min(t.nkeys, t.qpos0 + t.ntok);  // causal bound of the tile
-    attn_tile_body<T, HD, HD, false>(t, kvh, G, H, qrot, dk, none, scale, nullptr, 0, k1, out,
-                                     (int64_t)H * HD, nullptr, 1, 0);
+    attn_tile<T, HD, HD, false>(t, kvh, G, H, qrot, dk, none, scale, nullptr, 0, k1, out,
+                                (int64_t)H * HD, nullptr, 1, 0);
 }
 
 // ------------------------------------------------------- PagedAttention --
@@ -775,16 +1050,17 @@ __global__ __launch_bounds__(64) void paged_prep_kernel(
     }
 }
 
-// grid (max_tiles, KV, nsplit). Multi-token tiles are not split (split 0 takes
-// all keys); single-token tiles split keys into `chunk`-sized ranges and write
-// partials (merged by attn_merge).
+// grid (max_tiles, KV, nsplit). A tile's causal key range [0, kend) is split
+// into `chunk`-key ranges; with one range the tile writes its rows directly,
+// otherwise each split writes partial rows (token-major, row tok * H + h) and
+// split 0 records the split count of its rows for paged_merge (0 = direct).
 template <typename T, int HD, int VHD>
 __global__ __launch_bounds__(256) void paged_tile_kernel(
     const int4* __restrict__ tiles, const int* __restrict__ tile_count,
     const int32_t* __restrict__ cum, const int32_t* __restrict__ past_lens, PagedKV pk,
     const T* __restrict__ qrot, int G, int H, float scale, const float* __restrict__ sink,
     int chunk, int nsplit, T* __restrict__ out, float* __restrict__ part,
-    int* __restrict__ nsplit_row, int* __restrict__ row_map) {
+    int* __restrict__ nsplit_row) {
     const int ti = blockIdx.x, kvh = blockIdx.y, split = blockIdx.z;
     if (ti >= *tile_count) return;
     const int4 td = tiles[ti];
@@ -798,49 +1074,39 @@ __global__ __launch_bounds__(256) void paged_tile_kernel(
     t.nkeys = t.past + (cum[t.seq + 1] - t.tok_seq0);
     const int kend = min(t.nkeys, t.qpos0 + t.ntok);
     DenseKV none{};
-    if (t.ntok > 1 || nsplit == 1) {
-        if (split != 0) return;
-        attn_tile_body<T, HD, VHD, true>(t, kvh, G, H, qrot, none, pk, scale, sink, 0, kend, out,
-                                         (int64_t)H * VHD, nullptr, 1, 0);
-        return;
-    }
-    // Single token: split keys.
     const int ns = min(nsplit, max(1, (kend + chunk - 1) / chunk));
-    const int64_t prow = ((int64_t)ti * pk.KV + kvh) * G;  // partial row base
-    if (split == 0 && threadIdx.x < G) {
-        nsplit_row[prow + threadIdx.x] = ns;
-        row_map[prow + threadIdx.x] = t.tok0 * H + kvh * G + threadIdx.x;
+    if (split == 0) {
+        for (int r = threadIdx.x; r < t.ntok * G; r += blockDim.x)
+            nsplit_row[(int64_t)(t.tok0 + r / G) * H + kvh * G + r % G] = ns > 1 ? ns : 0;
     }
     if (split >= ns) return;
+    if (ns == 1) {
+        attn_tile<T, HD, VHD, true>(t, kvh, G, H, qrot, none, pk, scale, sink, 0, kend, out,
+                                    (int64_t)H * VHD, nullptr, 1, 0);
+        return;
+    }
     const int k0 = split * chunk;
     const int k1 = split == ns - 1 ? kend : min(kend, k0 + chunk);
-    attn_tile_body<T, HD, VHD, true>(t, kvh, G, H, qrot, none, pk, scale, sink, k0, k1, out,
-                                     (int64_t)H * VHD, part + prow * nsplit * (VHD + 2), nsplit,
-                                     split);
+    attn_tile<T, HD, VHD, true>(t, kvh, G, H, qrot, none, pk, scale, sink, k0, k1, out,
+                                (int64_t)H * VHD, part, nsplit, split);
 }
 
-// Merge for paged single-token tiles, with the optional head sink folded in.
+// Merge of split rows, one workgroup per (token, head) row, with the optional
+// head sink folded in. Rows with a split count of 0 were written directly.
 template <typename T>
 __global__ __launch_bounds__(128) void paged_merge_kernel(const float* __restrict__ part,
                                                           T* __restrict__ out, int nsplit,
                                                           const int* __restrict__ nsplit_row,
-                                                          const int* __restrict__ row_map,
                                                           int vhd, int H,
-                                                          const float* __restrict__ sink,
-                                                          const int4* __restrict__ tiles,
-                                                          const int* __restrict__ tile_count,
-                                                          int KV, int G) {
-    const int r = blockIdx.x;
-    const int ti = r / (KV * G);
-    if (ti >= *tile_count) return;
-    if (tiles[ti].z != 1) return;
-    const int orow = row_map[r];
-    if (orow < 0) return;
-    const int ns = nsplit_row[r];
-    const float* p = part + (int64_t)r * nsplit * (vhd + 2);
+                                                          const float* __restrict__ sink) {
+    const int64_t tok = blockIdx.x;
+    const int h = blockIdx.y;
+    const int64_t r = tok * H + h;
+    const int ns = min(nsplit, nsplit_row[r]);
+    if (ns <= 0) return;
+    const float* p = part + r * nsplit * (vhd + 2);
     float M = -INFINITY;
     for (int i = 0; i < ns; ++i) M = fmaxf(M, p[i * (vhd + 2) + vhd]);
-    const int h = orow % H;
     if (sink) M = fmaxf(M, sink[h]);
     float L = 0.f;
     for (int i = 0; i < ns; ++i) {
@@ -849,7 +1115,7 @@ __global__ __launch_bounds__(128) void paged_merge_kernel(const float* __restric
     }
     if (sink) L += __expf(sink[h] - M);
     const float inv = L > 0.f ? 1.0f / L : 0.f;
-    T* o = out + (int64_t)(orow / H) * ((int64_t)H * vhd) + (int64_t)h * vhd;
+    T* o = out + tok * ((int64_t)H * vhd) + (int64_t)h * vhd;
     for (int d = threadIdx.x; d < vhd; d += blockDim.x) {
         float acc = 0.f;
         for (int i = 0; i < ns; ++i) {
@@ -1065,7 +1331,7 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
                        interleaved, qrot, static_cast<T*>(pk), static_cast<T*>(pv), B, S, H, KV,
                        hd, pcap, vp, q_stride, kv_stride);
     if (int rc = check_launch("gqa_prep")) return rc;
-    const int QT = std::max(1, kTileRows / G);
+    const int QT = std::max(1, tile_rows_for<T>(HD) / G);
     const int tiles = (S + QT - 1) / QT;
     DenseKV dk{pk, pv, pcap, KV};
     hipLaunchKernelGGL((gqa_tile_kernel<T, HD>), dim3(B * tiles, KV), dim3(256), 0, st, qrot, dk,
@@ -1224,9 +1490,11 @@ static int paged_max_tiles(int64_t T, int64_t batch, int QT) {
     return (int)((T + QT - 1) / QT + batch);
 }
 static int paged_qt(int G) { return std::max(1, kTileRows / G); }
+// Keys per split: at least 512, and at most 8 splits per row (bounds the partials).
 static int paged_nsplit(int64_t max_context, int& chunk) {
-    chunk = 512;
-    return (int)std::max<int64_t>(1, (max_context + chunk - 1) / chunk);
+    const int64_t c = std::max<int64_t>(512, ((max_context + 7) / 8 + 63) / 64 * 64);
+    chunk = (int)c;
+    return (int)std::max<int64_t>(1, (max_context + c - 1) / c);
 }
 
 extern "C" size_t ortmi_paged_attention_workspace_size(int64_t num_tokens, int64_t batch,
@@ -1239,12 +1507,12 @@ extern "C" size_t ortmi_paged_attention_workspace_size(int64_t num_tokens, int64
     const int mt = paged_max_tiles(num_tokens, batch, QT);
     int chunk;
     const int ns = paged_nsplit(max_context, chunk);
-    const int64_t prow = (int64_t)mt * num_heads;  // tiles * KV * G
+    const int64_t prow = num_tokens * num_heads;  // partial rows, token-major
     size_t sz = 0;
     sz += align_up((size_t)num_tokens * num_heads * head_size * 4);      // qrot
     sz += align_up((size_t)num_tokens * kv_num_heads * head_size * 4);   // knew
     sz += align_up((size_t)(mt + 1) * 16);                               // tiles + count
-    sz += align_up((size_t)prow * 4 * 2);                                // nsplit_row, row_map
+    sz += align_up((size_t)prow * 4);                                    // nsplit_row
     sz += align_up((size_t)prow * ns * (vhd + 2) * 4);                   // partials
     sz += align_up((size_t)num_heads * 4);                               // sink fp32
     return sz;
@@ -1259,7 +1527,9 @@ static int run_paged(const void* query, const void* key, const void* value, void
                      const void* qw, const void* kw, float eps, void* output, int H, int KV,
                      float scale, void* ws, size_t ws_bytes, hipStream_t st) {
     const int G = H / KV;
-    const int QT = paged_qt(G);
+    // Tiles of the kernel used for T (the workspace is sized for the smaller tile,
+    // which gives more tiles, so it bounds this layout too).
+    const int QT = std::max(1, tile_rows_for<T>(VHD) / G);
     const int mt = paged_max_tiles(T_, batch, QT);
     int chunk;
     const int ns = paged_nsplit(max_context, chunk);
@@ -1274,10 +1544,9 @@ static int run_paged(const void* query, const void* key, const void* value, void
     int4* tiles = reinterpret_cast<int4*>(p);
     int* count = reinterpret_cast<int*>(tiles + mt);
     p += align_up((size_t)(mt + 1) * 16);
-    const int64_t prow = (int64_t)mt * H;
+    const int64_t prow = T_ * H;
     int* nsplit_row = reinterpret_cast<int*>(p);
-    int* row_map = nsplit_row + prow;
-    p += align_up((size_t)prow * 8);
+    p += align_up((size_t)prow * 4);
     float* part = reinterpret_cast<float*>(p);
     p += align_up((size_t)prow * ns * (VHD + 2) * 4);
     float* sink32 = reinterpret_cast<float*>(p);
@@ -1302,19 +1571,19 @@ static int run_paged(const void* query, const void* key, const void* value, void
     }
     if (int rc = check_launch("paged_tilemap")) return rc;
     if (T_ == 0) return ORTMI_OK;
-    // Invalidate partial rows so the merge skips rows not owned by a 1-token tile.
+    // Rows that no tile owns (a malformed cum) keep a split count of 0.
     hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((prow + 255) / 256)), dim3(256), 0, st,
-                       row_map, -1, prow);
+                       nsplit_row, 0, prow);
     PagedKV pk{kcache, vcache, knew, value, bt, nblk, blk, maxb, KV};
     if (!vcache) pk.vnew = nullptr;
     hipLaunchKernelGGL((paged_tile_kernel<T, HD, VHD>), dim3(mt, KV, ns), dim3(256), 0, st, tiles,
                        count, cum, past, pk, qrot, G, H, sc, sink ? sink32 : nullptr, chunk, ns,
-                       static_cast<T*>(output), part, nsplit_row, row_map);
+                       static_cast<T*>(output), part, nsplit_row);
     if (int rc = check_launch("paged_tile")) return rc;
     if (ns > 1) {
-        hipLaunchKernelGGL((paged_merge_kernel<T>), dim3((unsigned)prow), dim3(128), 0, st, part,
-                           static_cast<T*>(output), ns, nsplit_row, row_map, VHD, H,
-                           sink ? sink32 : nullptr, tiles, count, KV, G);
+        hipLaunchKernelGGL((paged_merge_kernel<T>), dim3((unsigned)T_, (unsigned)H), dim3(128), 0, st, part,
+                           static_cast<T*>(output), ns, nsplit_row, VHD, H,
+                           sink ? sink32 : nullptr);
         return check_launch("paged_merge");
     }
     return ORTMI_OK;

@@ -102,7 +102,8 @@ struct GemvPrologue {
     float eps;
 };
 
-template <typename T, int BS, int CPL, int R, bool PRO = false, bool PAIR = false>
+template <typename T, int BS, int CPL, int R, bool PRO = false, bool PAIR = false,
+          bool SV = false>
 __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ B,
                                                         const T* __restrict__ S,
@@ -172,7 +173,18 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                 const u32x4_t v =
                     __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(brow) + c);
                 g.w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
-                g.s[r][j] = S[(size_t)n * nb + (32 * c) / BS];
+                if constexpr (!SV) g.s[r][j] = S[(size_t)n * nb + (32 * c) / BS];
+            }
+            if constexpr (SV) {
+                // Block 32 and an even CPL: the lane's scales are CPL/2 aligned pairs.
+                struct alignas(2 * sizeof(T)) Pair { T a, b; };
+#pragma unroll
+                for (int j = 0; j < CPL; j += 2) {
+                    const int c = min(c0 + j, C - 2);
+                    const Pair p = *reinterpret_cast<const Pair*>(S + (size_t)n * nb + c);
+                    g.s[r][j] = p.a;
+                    g.s[r][j + 1] = p.b;
+                }
             }
         }
     };
@@ -303,6 +315,21 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
 template <typename T, int BS, int CPL, bool PRO, bool PAIR>
 static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
                             int N, int K, int nb, const GemvPrologue<T>& pro, hipStream_t st) {
+    if constexpr (BS == 32 && CPL % 2 == 0) {
+        // Scale pairs as one load when every lane's pair is aligned.
+        const bool sv = nb % 2 == 0 && (reinterpret_cast<uintptr_t>(S) % (2 * sizeof(T))) == 0 &&
+                        nb >= 2;
+        if (sv) {
+            constexpr int R = PAIR ? 2 : 1;
+            const long groups = ((long)N + R - 1) / R;
+            long grid = (groups + 3) / 4;
+            if (grid > 4L * device_cu_count()) grid = 4L * device_cu_count();
+            hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, PRO, PAIR, true>),
+                               dim3((unsigned)grid), dim3(256), (size_t)nb * BS * sizeof(float),
+                               st, A, B, S, Z, Y, N, K, nb, pro);
+            return check_launch("mnb_gemv4");
+        }
+    }
     // One row (or one gate/up pair) per group; at most 4 workgroups per CU, each
     // wave walking its groups with the next group's loads in flight (measured best
     // on MI355X for the K=4096 x N=11008 shape against 1-4 rows per group and 1-8
