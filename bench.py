@@ -127,7 +127,7 @@ def bench_gemv(torch, ortmi, steps, warmup):
 
     gpu_ms, wall_ms, n = timed_graph(torch, launch_batch, len(args), steps, warmup)
     gbs = bytes_per_call / (gpu_ms * 1e-3) / 1e9
-    return dict(kernel="mnb_gemv4_kernel<float, 32, 2, 1, false, false>", bytes_per_call=bytes_per_call,
+    return dict(kernel="mnb_gemv4_kernel<float, 32, 2, 1, 2, false, false, true, false, true>", bytes_per_call=bytes_per_call,
                 copies=copies, gpu_ms=gpu_ms, wall_ms=wall_ms, launches=n, gbs=gbs,
                 inputs=(A, B, s, zp))
 

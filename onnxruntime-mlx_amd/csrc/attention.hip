@@ -168,21 +168,63 @@ __device__ __forceinline__ void rope_lane8(float (&x)[8], int dl, const T* __res
     }
 }
 
-// Partial state layout (floats): [row][split][vhd + 2] with o (unnormalised),
-// then m (running max) and l (sum of exp).
-//
-// One workgroup per (batch, kv head, key split). Built for latency, since a
-// decode step at short context is a handful of dependent memory round trips:
-//  * every load that does not depend on the past length is issued first (the
-//    query rows, the new K/V row, and the first block of cached rows, fetched
-//    speculatively: rows past the live keys are in bounds and masked later);
-//  * RoPE of the G query heads and of the new key runs in registers once the
-//    cos/sin row of position vp has arrived;
-//  * the new key/value row is written to `present` but never read back: the
-//    split holding position vp uses the rotated row from registers, so no wave
-//    waits for that store;
-//  * blocks of U*RPS rows are software-pipelined (the next block's K and V loads
-//    are in flight while the current block is scored).
+// End of a decode workgroup (NW waves, lane groups of LPR lanes each holding an
+// online-softmax state (m, l, o[8] over dims dl..dl+7) for G heads): merges the
+// groups of each wave with cross-lane reductions, then the NW waves through LDS,
+// and calls emit(g, d, M, L, acc) once per (head, dim) with the merged state.
+template <int HD, int G, int LPR, int NW, typename Emit>
+__device__ __forceinline__ void decode_merge(float (&m)[G], float (&l)[G], float (&o)[G][8],
+                                             float (&s_m)[NW][G], float (&s_l)[NW][G],
+                                             float (&s_o)[NW][G][HD], Emit emit) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int dl = (lane % LPR) * 8;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float mw = m[g];
+        if constexpr (LPR == 8) mw = fmaxf(mw, dpp_mov<0x128>(mw));
+        if constexpr (LPR <= 16) {
+            const LanePair p = swap16(mw);
+            mw = fmaxf(p.a, p.b);
+        }
+        const LanePair p = swap32(mw);
+        mw = fmaxf(p.a, p.b);
+        const float f = m[g] == -INFINITY ? 0.f : __expf(m[g] - mw);
+        l[g] = across_groups_sum<LPR>(l[g] * f);
+        m[g] = mw;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[g][i] = across_groups_sum<LPR>(o[g][i] * f);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            s_m[wave][g] = m[g];
+            s_l[wave][g] = l[g];
+        }
+    }
+    if (lane < LPR) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s_o[wave][g][dl + i] = o[g][i];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * HD; idx += 64 * NW) {
+        const int g = idx / HD, d = idx % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][g]);
+        float L = 0.f, acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float mw = s_m[w][g];
+            const float f = mw == -INFINITY ? 0.f : __expf(mw - M);
+            L += s_l[w][g] * f;
+            acc += s_o[w][g][d] * f;
+        }
+        emit(g, d, M, L, acc);
+    }
+}
+
 // Each lane group of LPR lanes owns one row per step; scores use a blocked
 // online softmax. In the growing contract rows below vp are copied from past to
 // present out of the registers already loaded.
@@ -196,11 +238,12 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     T* __restrict__ out, const int* __restrict__ total_dev, int vp_max, int gsplit) {
     constexpr int LPR = HD / 8;          // lanes per row (16 bytes each)
     constexpr int RPW = 64 / LPR;        // rows per wave per step
-    constexpr int RPS = 4 * RPW;         // rows per workgroup step
+    constexpr int NW = 4;                // waves
+    constexpr int RPS = NW * RPW;        // rows per workgroup step
     constexpr int U = G <= 4 ? 4 : 2;    // steps per online-softmax block (registers)
     constexpr int BLK = RPS * U;         // rows per block
-    __shared__ float s_o[4][G][HD];
-    __shared__ float s_m[4][G], s_l[4][G];
+    __shared__ float s_o[NW][G][HD];
+    __shared__ float s_m[NW][G], s_l[NW][G];
 
     // blockIdx.x = (b*KV + kvh) * gsplit + head group: the G*gsplit query heads of
     // a KV head may be spread over gsplit workgroups that read the same rows.
@@ -359,55 +402,11 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
         if (base + 2 * BLK < j1) load_block(kr, vr, base + 2 * BLK);
         process(kn, vn, base + BLK);
     }
-    // Merge the RPW lane groups of each wave with cross-lane sums, then the 4
-    // waves through LDS.
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float mw = m[g];
-        {
-            if constexpr (LPR == 8) mw = fmaxf(mw, dpp_mov<0x128>(mw));
-            if constexpr (LPR <= 16) {
-                const LanePair p = swap16(mw);
-                mw = fmaxf(p.a, p.b);
-            }
-            const LanePair p = swap32(mw);
-            mw = fmaxf(p.a, p.b);
-        }
-        const float f = m[g] == -INFINITY ? 0.f : __expf(m[g] - mw);
-        l[g] = across_groups_sum<LPR>(l[g] * f);
-        m[g] = mw;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[g][i] = across_groups_sum<LPR>(o[g][i] * f);
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            s_m[wave][g] = m[g];
-            s_l[wave][g] = l[g];
-        }
-    }
-    if (sub == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) s_o[wave][g][dl + i] = o[g][i];
-    }
-    __syncthreads();
-    for (int idx = tid; idx < G * HD; idx += 256) {
-        const int g = idx / HD, d = idx % HD;
-        const float m0 = s_m[0][g], m1 = s_m[1][g], m2 = s_m[2][g], m3 = s_m[3][g];
-        const float M = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
-        const float w0 = m0 == -INFINITY ? 0.f : __expf(m0 - M);
-        const float w1 = m1 == -INFINITY ? 0.f : __expf(m1 - M);
-        const float w2 = m2 == -INFINITY ? 0.f : __expf(m2 - M);
-        const float w3 = m3 == -INFINITY ? 0.f : __expf(m3 - M);
-        const float L = s_l[0][g] * w0 + s_l[1][g] * w1 + s_l[2][g] * w2 + s_l[3][g] * w3;
-        const float acc = s_o[0][g][d] * w0 + s_o[1][g][d] * w1 + s_o[2][g][d] * w2 +
-                          s_o[3][g][d] * w3;
+    decode_merge<HD, G, LPR, NW>(m, l, o, s_m, s_l, s_o, [&](int g, int d, float M, float L, float acc) {
         const int64_t row = (int64_t)b * H + h0 + g;
         if (nsplit == 1) {
             out[row * HD + d] = from_f32<T>(L > 0.f ? acc / L : 0.f);
-            continue;
+            return;
         }
         float* dst = part + (row * nsplit + split) * (HD + 2);
         dst[d] = acc;
@@ -415,7 +414,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
             dst[HD] = M;
             dst[HD + 1] = L;
         }
-    }
+    });
 }
 
 // Merge split partials: out[row][d] = sum_i o_i e^{m_i-M} / sum_i l_i e^{m_i-M}.
@@ -1060,10 +1059,11 @@ __global__ __launch_bounds__(256) void paged_tile_kernel(
     const int32_t* __restrict__ cum, const int32_t* __restrict__ past_lens, PagedKV pk,
     const T* __restrict__ qrot, int G, int H, float scale, const float* __restrict__ sink,
     int chunk, int nsplit, T* __restrict__ out, float* __restrict__ part,
-    int* __restrict__ nsplit_row) {
+    int* __restrict__ nsplit_row, int skip_single) {
     const int ti = blockIdx.x, kvh = blockIdx.y, split = blockIdx.z;
     if (ti >= *tile_count) return;
     const int4 td = tiles[ti];
+    if (skip_single && td.z == 1) return;  // paged_decode_kernel's
     TileDesc t;
     t.seq = td.x;
     t.tok0 = td.y;
@@ -1089,6 +1089,198 @@ __global__ __launch_bounds__(256) void paged_tile_kernel(
     const int k1 = split == ns - 1 ? kend : min(kend, k0 + chunk);
     attn_tile<T, HD, VHD, true>(t, kvh, G, H, qrot, none, pk, scale, sink, k0, k1, out,
                                 (int64_t)H * VHD, part, nsplit, split);
+}
+
+// Single-token tiles (every decoding sequence, and the last token of a prefill
+// whose length leaves one over) on the vector units, the way the dense decode
+// kernel does them: the G query heads of one kv head against keys [k0, k1) of the
+// sequence, one 16-byte slice of a key/value row per lane, rows spread over lane
+// groups, a blocked online softmax and loads one block ahead. Cache rows are
+// found through the block table, whose slice for the keys in hand is staged in
+// LDS first; rows from `past` on are the sequence's own new (rotated) keys and
+// values. A row whose block-table entry is out of range is masked, as in the tile
+// kernel. grid (max_tiles, KV, nsplit), same splits and outputs as
+// paged_tile_kernel, which leaves these tiles to this kernel.
+template <typename T, int HD, int G>
+__global__ __launch_bounds__(256) void paged_decode_kernel(
+    const int4* __restrict__ tiles, const int* __restrict__ tile_count,
+    const int32_t* __restrict__ cum, const int32_t* __restrict__ past_lens, PagedKV pk,
+    int blk_shift, const T* __restrict__ qrot, int H, float scale,
+    const float* __restrict__ sink, int chunk, int nsplit, T* __restrict__ out,
+    float* __restrict__ part, int* __restrict__ nsplit_row) {
+    constexpr int LPR = HD / 8;        // lanes per row (16 bytes each)
+    constexpr int RPW = 64 / LPR;      // rows per wave per step
+    constexpr int RPS = 4 * RPW;       // rows per workgroup step
+    constexpr int U = G <= 4 ? 4 : 2;  // steps per online-softmax block
+    constexpr int BLK = RPS * U;       // rows per block
+    constexpr int kBt = 256;           // block-table entries staged at a time
+    __shared__ int s_bt[kBt];
+    __shared__ float s_o[4][G][HD];
+    __shared__ float s_m[4][G], s_l[4][G];
+
+    const int ti = blockIdx.x, kvh = blockIdx.y, split = blockIdx.z;
+    if (ti >= *tile_count) return;
+    const int4 td = tiles[ti];
+    if (td.z != 1) return;
+    const int seq = td.x, tok = td.y;
+    const int tok_seq0 = cum[seq];
+    const int past = past_lens[seq];
+    const int kend = past + (tok - tok_seq0) + 1;  // causal: keys up to the token itself
+    const int ns = min(nsplit, max(1, (kend + chunk - 1) / chunk));
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = lane / LPR;
+    const int dl = (lane % LPR) * 8;
+    const int KV = pk.KV;
+    if (split == 0 && tid < G) nsplit_row[(int64_t)tok * H + kvh * G + tid] = ns > 1 ? ns : 0;
+    if (split >= ns) return;
+    const int k0 = split * chunk;
+    const int k1 = split == ns - 1 ? kend : min(kend, k0 + chunk);
+
+    const T* kc = static_cast<const T*>(pk.kcache) + (int64_t)kvh * HD + dl;
+    const T* vc = static_cast<const T*>(pk.vcache) + (int64_t)kvh * HD + dl;
+    // New rows: row past + i is token tok_seq0 + i.
+    const int64_t new0 = (int64_t)tok_seq0 - past;
+    const T* kn = static_cast<const T*>(pk.knew) + (int64_t)kvh * HD + dl;
+    const T* vn = static_cast<const T*>(pk.vnew) + (int64_t)kvh * HD + dl;
+    const int64_t rs = (int64_t)KV * HD;  // row stride of caches and new rows
+    const int bmask = (1 << blk_shift) - 1;
+
+    float qf[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(
+            qrot + ((int64_t)tok * H + kvh * G + g) * HD + dl);
+        const T* rv = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qf[g][i] = to_f32(rv[i]) * scale;
+    }
+    float m[G], l[G], o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
+    }
+
+    // Windows [w0, w1) of keys whose block-table slice fits s_bt: (kBt - 1) blocks
+    // of keys touch at most kBt blocks whatever the alignment of w0.
+    const int W = (kBt - 1) << blk_shift;
+    for (int w0 = k0; w0 < k1; w0 += W) {
+        const int w1 = min(k1, w0 + W);
+        const int lb0 = w0 >> blk_shift;
+        const int cend = min(w1, past);  // cache rows are [w0, cend)
+        const int nlb = cend > w0 ? ((cend - 1) >> blk_shift) - lb0 + 1 : 0;
+        if (w0 != k0) __syncthreads();  // the previous window is done with s_bt
+        for (int i = tid; i < nlb; i += 256) {
+            const int lb = lb0 + i;
+            s_bt[i] = lb < pk.maxb ? pk.bt[(int64_t)seq * pk.maxb + lb] : -1;
+        }
+        __syncthreads();
+
+        // Rows beyond w1 load row w1 - 1 again (masked); a row with a bad
+        // block-table entry loads row 0 of block 0 (masked, value zeroed).
+        uint4 kr[U], vr[U];
+        unsigned okr = 0;
+        auto load_block = [&](uint4 (&kk)[U], uint4 (&vv)[U], unsigned& ok, int base) {
+            ok = 0;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int j = min(base + u * RPS + wave * RPW + sub, w1 - 1);
+                const bool cached = j < past;
+                const int phys = s_bt[cached ? (j >> blk_shift) - lb0 : 0];
+                const bool good = !cached || (phys >= 0 && phys < pk.nblk);
+                const int64_t slot = good ? (int64_t)phys * (bmask + 1) + (j & bmask) : 0;
+                const T* kp = cached ? kc + slot * rs : kn + (new0 + j) * rs;
+                const T* vp = cached ? vc + slot * rs : vn + (new0 + j) * rs;
+                kk[u] = *reinterpret_cast<const uint4*>(kp);
+                vv[u] = *reinterpret_cast<const uint4*>(vp);
+                ok |= (unsigned)good << u;
+            }
+        };
+        auto process = [&](const uint4 (&kk)[U], const uint4 (&vv)[U], unsigned ok, int base) {
+            float sc[U][G];
+            float bmax[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) bmax[g] = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int j = base + u * RPS + wave * RPW + sub;
+                const bool live = j < w1 && ((ok >> u) & 1u);
+                const T* kv = reinterpret_cast<const T*>(&kk[u]);
+                float kf[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) kf[i] = to_f32(kv[i]);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    float d = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
+                    d = group_sum<LPR>(d);
+                    sc[u][g] = live ? d : -INFINITY;
+                    bmax[g] = fmaxf(bmax[g], sc[u][g]);
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float mn = fmaxf(m[g], bmax[g]);
+                if (mn == -INFINITY) continue;
+                const float alpha = __expf(m[g] - mn);  // m = -inf gives 0
+                l[g] *= alpha;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[g][i] *= alpha;
+                m[g] = mn;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool good = (ok >> u) & 1u;
+                const T* vv8 = reinterpret_cast<const T*>(&vv[u]);
+                float vf[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) vf[i] = good ? to_f32(vv8[i]) : 0.f;
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float p = sc[u][g] == -INFINITY ? 0.f : __expf(sc[u][g] - m[g]);
+                    l[g] += p;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i]);
+                }
+            }
+        };
+        load_block(kr, vr, okr, w0);
+        for (int base = w0; base < w1; base += 2 * BLK) {
+            uint4 kn2[U], vn2[U];
+            unsigned okn = 0;
+            const bool more = base + BLK < w1;
+            if (more) load_block(kn2, vn2, okn, base + BLK);
+            process(kr, vr, okr, base);
+            if (!more) break;
+            if (base + 2 * BLK < w1) load_block(kr, vr, okr, base + 2 * BLK);
+            process(kn2, vn2, okn, base + BLK);
+        }
+    }
+
+    decode_merge<HD, G, LPR, 4>(m, l, o, s_m, s_l, s_o, [&](int g, int d, float M, float L, float acc) {
+        const int h = kvh * G + g;
+        const int64_t row = (int64_t)tok * H + h;
+        if (ns > 1) {
+            float* dst = part + (row * nsplit + split) * (HD + 2);
+            dst[d] = acc;
+            if (d == 0) {
+                dst[HD] = M;
+                dst[HD + 1] = L;
+            }
+            return;
+        }
+        if (sink) {
+            const float sv = sink[h];
+            const float mm = fmaxf(M, sv);
+            const float a = M == -INFINITY ? 0.f : __expf(M - mm);
+            L = L * a + __expf(sv - mm);
+            acc *= a;
+        }
+        out[row * HD + d] = from_f32<T>(L > 0.f ? acc / L : 0.f);
+    });
 }
 
 // Merge of split rows, one workgroup per (token, head) row, with the optional
@@ -1576,9 +1768,33 @@ static int run_paged(const void* query, const void* key, const void* value, void
                        nsplit_row, 0, prow);
     PagedKV pk{kcache, vcache, knew, value, bt, nblk, blk, maxb, KV};
     if (!vcache) pk.vnew = nullptr;
+    // Single-token tiles go to the vector-unit decode kernel when the block size is a
+    // power of two and values have the key's head size.
+    int blk_shift = 0;
+    while ((1 << blk_shift) < blk && blk_shift < 30) ++blk_shift;
+    bool dec = false;
+    if constexpr (VHD == HD) {
+        dec = vcache && value && (1 << blk_shift) == blk && blk_shift <= 12;
+        auto launch = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3(mt, KV, ns), dim3(256), 0, st, tiles, count, cum, past,
+                               pk, blk_shift, qrot, H, sc, sink ? sink32 : nullptr, chunk, ns,
+                               static_cast<T*>(output), part, nsplit_row);
+        };
+        if (dec) {
+            switch (G) {
+                case 1: launch(paged_decode_kernel<T, HD, 1>); break;
+                case 2: launch(paged_decode_kernel<T, HD, 2>); break;
+                case 4: launch(paged_decode_kernel<T, HD, 4>); break;
+                case 8: launch(paged_decode_kernel<T, HD, 8>); break;
+                default: dec = false;
+            }
+            if (dec)
+                if (int rc = check_launch("paged_decode")) return rc;
+        }
+    }
     hipLaunchKernelGGL((paged_tile_kernel<T, HD, VHD>), dim3(mt, KV, ns), dim3(256), 0, st, tiles,
                        count, cum, past, pk, qrot, G, H, sc, sink ? sink32 : nullptr, chunk, ns,
-                       static_cast<T*>(output), part, nsplit_row);
+                       static_cast<T*>(output), part, nsplit_row, dec ? 1 : 0);
     if (int rc = check_launch("paged_tile")) return rc;
     if (ns > 1) {
         hipLaunchKernelGGL((paged_merge_kernel<T>), dim3((unsigned)T_, (unsigned)H), dim3(128), 0, st, part,

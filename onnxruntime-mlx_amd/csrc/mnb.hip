@@ -10,9 +10,11 @@
 //  * mnb_gemv4  - decode (M == 1), bits 4, bs in {32, 64, 128}. HBM-bound: each
 //    lane owns a contiguous run of 32-code chunks of K and keeps the matching
 //    activations in VGPRs (staged once per workgroup through LDS), then streams
-//    rows of B with 128-bit loads. Zero points are folded as
-//    s*(sum(a*q) - zp*sum(a)), so the inner loop is one byte-convert and one FMA
-//    per code.
+//    rows of B with 128-bit range-checked buffer loads, a ring of row groups in
+//    flight per wave. fp32/bf16 activations: zero points folded as
+//    s*(sum(a*q) - zp*sum(a)), one byte-convert and one FMA per code. fp16
+//    activations: codes become exact fp16 (q - zp) pairs and v_dot2_f32_f16
+//    takes two codes per instruction.
 //  * mnb_gemm4  - prefill (M > 1, fp16), bits 4, bs in {32, 64, 128}. MFMA
 //    v_mfma_f32_32x32x16_f16: the weight tile is dequantised to fp16 in LDS
 //    (fp16((q - zp) * s), one rounding) and the activation tile is staged in LDS;
@@ -48,6 +50,15 @@ __device__ __forceinline__ float dot32_codes(const float* a, uint4 w) {
     return d0 + d1;
 }
 
+// Reorder 8 activations [a0..a7] to the pair order [a0,a4,a1,a5,a2,a6,a3,a7] used by
+// the dequantised weights (an identical permutation of k on both MFMA operands).
+__device__ __forceinline__ uint4 permute_act8(uint4 v) {
+    return make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u),
+                      __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                      __builtin_amdgcn_perm(v.w, v.y, 0x05040100u),
+                      __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+}
+
 // Activations live in LDS as fp32 in 16-byte units. Lane l reads the 8*CPL
 // consecutive units of its chunks; unit u of lane l is stored at
 // u ^ ((u / (8*CPL)) & 7), so the 8 lanes of one read phase hit 8 bank groups.
@@ -79,13 +90,37 @@ struct GemvGroup {
     uint8_t z[R][ZB];
 };
 
+// fp16 activations as pairs: sum over the 32 codes of one chunk of a * (q - zp).
+// `av` holds the chunk's activations in pair order (a_j, a_j+4) for each 8-code
+// word, the order dequant_word_pairs gives the codes in; (1024 + q) - (1024 + zp)
+// is exact in fp16, v_dot2_f32_f16 multiplies exactly and accumulates in fp32.
+__device__ __forceinline__ float dot32_pairs(const uint4 (&av)[4], uint4 w, half2_t zoff) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t aw[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t m = ((words[i] >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+            const half2_t q = __builtin_bit_cast(half2_t, m) - zoff;
+            const half2_t a = __builtin_bit_cast(half2_t, aw[j]);
+            if (j & 1) d1 = __builtin_amdgcn_fdot2(a, q, d1, false);
+            else d0 = __builtin_amdgcn_fdot2(a, q, d0, false);
+        }
+    }
+    return d0 + d1;
+}
+
 // Lane l owns the CPL consecutive 32-code chunks [l*CPL, (l+1)*CPL) of every row,
 // so a row costs one 16*CPL-byte weight run, CPL adjacent scales and one or two
 // zero-point bytes per lane. The activation loads are issued first, then the
-// weight loads of the wave's first row group; the activations go through LDS
+// weight loads of the wave's first D row groups; the activations go through LDS
 // (one copy per workgroup) into VGPRs while the weights are in flight. Row groups
-// of R rows are dealt to waves round-robin; the next group's loads are issued
-// before the current group is reduced.
+// of R rows are dealt to waves round-robin; a ring of D groups keeps the next
+// D - 1 groups' loads in flight while one group is reduced.
+// Activations in VGPRs: fp32 (32 per chunk) for fp32/bf16, fp16 pairs (16 VGPRs
+// per chunk, v_dot2 products) for fp16 (H2).
 // Optional fusions of the decoder's neighbours into the GEMV (decode only):
 //  * prologue: the activation row is (Skip)SimplifiedLayerNorm(x [+ skip]) * gamma,
 //    computed by every workgroup from x (K elements) before staging; workgroup 0
@@ -102,8 +137,35 @@ struct GemvPrologue {
     float eps;
 };
 
-template <typename T, int BS, int CPL, int R, bool PRO = false, bool PAIR = false,
-          bool SV = false>
+// Buffer resource word 3 for raw (untyped) buffer loads on gfx9-family GPUs.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of a buffer load that marks it non-temporal.
+constexpr int kCachePolicyNT = 2;
+
+// One scale, or an aligned pair of scales, through a buffer load.
+template <typename T>
+__device__ __forceinline__ T load_scale(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    } else {
+        return __builtin_bit_cast(T, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+    }
+}
+template <typename T>
+__device__ __forceinline__ void load_scale_pair(__amdgpu_buffer_rsrc_t r, uint32_t off, T& a, T& b) {
+    if constexpr (sizeof(T) == 4) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+        a = __builtin_bit_cast(T, (uint32_t)v[0]);
+        b = __builtin_bit_cast(T, (uint32_t)v[1]);
+    } else {
+        const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+        a = __builtin_bit_cast(T, (uint16_t)(v & 0xffffu));
+        b = __builtin_bit_cast(T, (uint16_t)(v >> 16));
+    }
+}
+
+template <typename T, int BS, int CPL, int R, int D, bool PRO = false, bool PAIR = false,
+          bool SV = false, bool H2 = std::is_same<T, half_t>::value, bool NT = true>
 __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ B,
                                                         const T* __restrict__ S,
@@ -111,6 +173,8 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         T* __restrict__ Y, int N, int K,
                                                         int nb, GemvPrologue<T> pro) {
     static_assert(!PAIR || R == 2, "SwiGLU pairs take two rows per group");
+    static_assert(!H2 || std::is_same<T, half_t>::value, "fp16 pairs need fp16 activations");
+    static_assert(D >= 1, "ring depth");
     extern __shared__ float4 sA[];
     __shared__ float s_red[4];
     constexpr int ZB = zp_window(BS, CPL);
@@ -153,46 +217,67 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
         }
     }
 
-    // 2. weights of the first row group. Loads never branch: a group index past
-    // the end is clamped to the last group and a chunk past the row end to the
-    // last chunk (in bounds; such lanes hold zero activations, so they add
-    // nothing), which keeps every wait on a prefetch exact.
+    // 2. weights of the first D row groups, issued after the activation loads (a
+    // wait on a load also waits on every load issued before it). Loads never
+    // branch, which keeps every wait on a prefetch exact: they are buffer loads,
+    // and a group past the end, or a chunk past the row end, gets an offset past
+    // the buffer's range, which returns zeros without a memory access (a zero chunk
+    // meets zero activations, a missing group is never reduced). The last group's
+    // second row, when N is odd, repeats row N - 1 (in bounds).
+    const int g0 = blockIdx.x * 4 + wave;
     const int blk0 = (32 * min(c0, C - 1)) / BS;
+    const uint32_t b_end = (uint32_t)((size_t)N * row_bytes);
+    const uint32_t s_end = (uint32_t)((size_t)N * nb * sizeof(T));
+    const uint32_t z_end = (uint32_t)((size_t)N * zp_cols);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(B), 0, (int)b_end, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(S), 0, (int)s_end, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(Z ? Z : B), 0, Z ? (int)z_end : 0, kBufferWord3);
     auto load_group = [&](Group& g, int gi) {
-        const int gc = min(gi, ngroups - 1);
+        const bool live = gi < ngroups;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int n = min(gc * R + r, N - 1);
-            const uint8_t* brow = B + (size_t)n * row_bytes;
+            const int n = min(gi * R + r, N - 1);
+            const uint32_t zoff = live ? (uint32_t)(n * zp_cols) : z_end;
 #pragma unroll
             for (int t = 0; t < ZB; ++t)
-                g.z[r][t] = Z ? Z[(size_t)n * zp_cols + min(blk0 / 2 + t, zp_cols - 1)] : 0x88;
+                g.z[r][t] = Z ? (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(
+                                    rz, zoff + (uint32_t)min(blk0 / 2 + t, zp_cols - 1), 0, 0)
+                              : (uint8_t)0x88;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
-                const int c = min(c0 + j, C - 1);
+                const int c = c0 + j;
+                const bool ok = live && c < C;
+                const uint32_t boff = ok ? (uint32_t)((size_t)n * row_bytes) + 16u * c : b_end;
+                // Streamed once: optionally non-temporal (cache policy nt).
                 const u32x4_t v =
-                    __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(brow) + c);
+                    __builtin_amdgcn_raw_buffer_load_b128(rb, boff, 0, NT ? kCachePolicyNT : 0);
                 g.w[r][j] = make_uint4(v.x, v.y, v.z, v.w);
-                if constexpr (!SV) g.s[r][j] = S[(size_t)n * nb + (32 * c) / BS];
+                if constexpr (!SV) {
+                    const uint32_t soff =
+                        ok ? (uint32_t)(((size_t)n * nb + (32 * c) / BS) * sizeof(T)) : s_end;
+                    g.s[r][j] = load_scale<T>(rs, soff);
+                }
             }
             if constexpr (SV) {
                 // Block 32 and an even CPL: the lane's scales are CPL/2 aligned pairs.
-                struct alignas(2 * sizeof(T)) Pair { T a, b; };
 #pragma unroll
                 for (int j = 0; j < CPL; j += 2) {
-                    const int c = min(c0 + j, C - 2);
-                    const Pair p = *reinterpret_cast<const Pair*>(S + (size_t)n * nb + c);
-                    g.s[r][j] = p.a;
-                    g.s[r][j + 1] = p.b;
+                    const int c = c0 + j;
+                    const uint32_t soff =
+                        live && c < C ? (uint32_t)(((size_t)n * nb + c) * sizeof(T)) : s_end;
+                    load_scale_pair(rs, soff, g.s[r][j], g.s[r][j + 1]);
                 }
             }
         }
     };
-    const int g0 = blockIdx.x * 4 + wave;
-    Group ga, gb;
-    load_group(ga, g0);
+    Group g[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_group(g[d], g0 + d * waves_total);
 
-    // 3. activations (normalised first when fused) -> LDS (swizzled fp32 units) -> VGPRs.
+    // 3. activations (normalised first when fused) -> LDS -> VGPRs.
     float scale_all = 1.f;
     if constexpr (PRO) {
         float ss = 0.f;
@@ -228,43 +313,62 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     for (int u = 0; u < AV; ++u) {
         const int vi = threadIdx.x + u * 256;
         if (vi >= nvec) continue;
-        const T* t = reinterpret_cast<const T*>(&av[u]);
-        float f[EPL];
+        T* t = reinterpret_cast<T*>(&av[u]);
+        if constexpr (H2) {
+            // 8 halfs = one 8-code word: one 16-byte unit in pair order.
+            if constexpr (PRO) {
+                const T* gm = reinterpret_cast<const T*>(&gmv[u]);
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) f[e] = to_f32(t[e]);
-        if constexpr (PRO) {
-            const T* gm = reinterpret_cast<const T*>(&gmv[u]);
+                for (int e = 0; e < EPL; ++e)
+                    t[e] = from_f32<T>(to_f32(t[e]) * scale_all * to_f32(gm[e]));
+            }
+            reinterpret_cast<uint4*>(sA)[vi] = permute_act8(av[u]);
+        } else {
+            float f[EPL];
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) f[e] = round_to<T>(f[e] * scale_all * to_f32(gm[e]));
-        }
+            for (int e = 0; e < EPL; ++e) f[e] = to_f32(t[e]);
+            if constexpr (PRO) {
+                const T* gm = reinterpret_cast<const T*>(&gmv[u]);
 #pragma unroll
-        for (int e = 0; e < EPL; e += 4) {
-            const int q = (vi * EPL + e) / 4;
-            sA[act_unit<CPL>(q)] = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
+                for (int e = 0; e < EPL; ++e) f[e] = round_to<T>(f[e] * scale_all * to_f32(gm[e]));
+            }
+#pragma unroll
+            for (int e = 0; e < EPL; e += 4) {
+                const int q = (vi * EPL + e) / 4;
+                sA[act_unit<CPL>(q)] = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
+            }
         }
     }
     __syncthreads();
-    float a[CPL][32];
-    float asum[CPL];
+    // fp32 form: a[j][*] and asum[j]; fp16 pairs: ah[j][*] (the other form is unused).
+    float a[H2 ? 1 : CPL][32];
+    float asum[H2 ? 1 : CPL];
+    uint4 ah[H2 ? CPL : 1][4];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int c = c0 + j;
-        float s = 0.f;
+        if constexpr (H2) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 v =
-                c < C ? sA[act_unit<CPL>(8 * c + i)] : make_float4(0.f, 0.f, 0.f, 0.f);
-            a[j][4 * i + 0] = v.x;
-            a[j][4 * i + 1] = v.y;
-            a[j][4 * i + 2] = v.z;
-            a[j][4 * i + 3] = v.w;
-            s += (v.x + v.y) + (v.z + v.w);
+            for (int i = 0; i < 4; ++i)
+                ah[j][i] = c < C ? reinterpret_cast<const uint4*>(sA)[4 * c + i]
+                                 : make_uint4(0, 0, 0, 0);
+        } else {
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 v =
+                    c < C ? sA[act_unit<CPL>(8 * c + i)] : make_float4(0.f, 0.f, 0.f, 0.f);
+                a[j][4 * i + 0] = v.x;
+                a[j][4 * i + 1] = v.y;
+                a[j][4 * i + 2] = v.z;
+                a[j][4 * i + 3] = v.w;
+                s += (v.x + v.y) + (v.z + v.w);
+            }
+            asum[j] = s;
         }
-        asum[j] = s;
     }
 
-    auto reduce_store = [&](const Group& g, int gi) {
-        const int gc = min(gi, ngroups - 1);
+    auto reduce_store = [&](const Group& gr, int gi) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -273,25 +377,30 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
             for (int j = 0; j < CPL; ++j) {
                 const int blk = (32 * min(c0 + j, C - 1)) / BS;
                 const int d = blk / 2 - blk0 / 2;
-                uint8_t zbyte = g.z[r][0];
+                uint8_t zbyte = gr.z[r][0];
 #pragma unroll
                 for (int t = 1; t < ZB; ++t)
-                    if (d == t) zbyte = g.z[r][t];
-                const float zf = (float)nibble(zbyte, blk & 1);
-                const float d32 = dot32_codes(a[j], g.w[r][j]);
-                total = fmaf(to_f32(g.s[r][j]), d32 - zf * asum[j], total);
+                    if (d == t) zbyte = gr.z[r][t];
+                const int zq = nibble(zbyte, blk & 1);
+                if constexpr (H2) {
+                    const half_t zo = (half_t)(1024 + zq);
+                    const half2_t zoff = {zo, zo};
+                    total = fmaf(to_f32(gr.s[r][j]), dot32_pairs(ah[j], gr.w[r][j], zoff), total);
+                } else {
+                    const float d32 = dot32_codes(a[j], gr.w[r][j]);
+                    total = fmaf(to_f32(gr.s[r][j]), d32 - (float)zq * asum[j], total);
+                }
             }
             acc[r] = total;
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
         // Every lane holds the sums and every lane stores (same-address writes of a
-        // wave coalesce). A clamped group past the end recomputed the last group,
-        // so it writes that group's values again: no branch around the store.
+        // wave coalesce).
         if constexpr (PAIR) {
             const float gv = round_to<T>(acc[0]), up = round_to<T>(acc[1]);
             const float sig = round_to<T>(1.0f / (1.0f + __expf(-gv)));
-            Y[gc] = from_f32<T>(round_to<T>(gv * sig) * up);
+            Y[gi] = from_f32<T>(round_to<T>(gv * sig) * up);
             return;
         }
         const int r = lane % R;
@@ -299,49 +408,73 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
 #pragma unroll
         for (int i = 1; i < R; ++i)
             if (r == i) v = acc[i];
-        Y[min(gc * R + r, N - 1)] = from_f32<T>(v);
+        Y[min(gi * R + r, N - 1)] = from_f32<T>(v);
     };
 
-    for (int gi = g0; gi < ngroups; gi += 2 * waves_total) {
-        const int g1 = gi + waves_total;
-        load_group(gb, g1);
-        reduce_store(ga, gi);
-        if (g1 >= ngroups) break;
-        load_group(ga, g1 + waves_total);
-        reduce_store(gb, g1);
+    for (int gi = g0; gi < ngroups; gi += D * waves_total) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int idx = gi + d * waves_total;
+            if (idx >= ngroups) return;
+            reduce_store(g[d], idx);
+            load_group(g[d], idx + D * waves_total);
+        }
     }
 }
 
+// Launch of one kernel instance: `grid` workgroups of 4 waves.
+template <typename T, int BS, int CPL, int R, int D, bool PRO, bool PAIR, bool SV, bool H2,
+          bool NT = true>
+static int launch_gemv4_inst(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
+                             int N, int K, int nb, const GemvPrologue<T>& pro, long grid,
+                             hipStream_t st) {
+    const size_t lds = (size_t)nb * BS * (H2 ? sizeof(half_t) : sizeof(float));
+    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, D, PRO, PAIR, SV, H2, NT>),
+                       dim3((unsigned)grid), dim3(256), lds, st, A, B, S, Z, Y, N, K, nb, pro);
+    return check_launch("mnb_gemv4");
+}
+
+// Grid, ring depth and cache policy per shape, from sweeps on MI355X with the
+// weights streamed from HBM (the decoder's N x K = 2048 x 1536, 1536 x 1536,
+// 17920 x 1536 in pairs, 1536 x 8960 and 151936 x 1536 in fp16, and 11008 x 4096
+// in fp32). Groups per wave: 1 while the groups fit about 10 waves per CU, 2 for
+// K > 4096 fp16 (activations fill the VGPRs), about 2.7 (4 workgroups per CU) for
+// fp32 K = 4096, 3 up to about 80 groups per CU, 16 beyond. A ring of 2, of 1 when
+// the activations fill the VGPRs, of 4 for the long walks. Weights non-temporal
+// except for those two cases, which measured faster with cached loads.
 template <typename T, int BS, int CPL, bool PRO, bool PAIR>
 static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
                             int N, int K, int nb, const GemvPrologue<T>& pro, hipStream_t st) {
-    if constexpr (BS == 32 && CPL % 2 == 0) {
-        // Scale pairs as one load when every lane's pair is aligned.
-        const bool sv = nb % 2 == 0 && (reinterpret_cast<uintptr_t>(S) % (2 * sizeof(T))) == 0 &&
-                        nb >= 2;
-        if (sv) {
-            constexpr int R = PAIR ? 2 : 1;
-            const long groups = ((long)N + R - 1) / R;
-            long grid = (groups + 3) / 4;
-            if (grid > 4L * device_cu_count()) grid = 4L * device_cu_count();
-            hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, PRO, PAIR, true>),
-                               dim3((unsigned)grid), dim3(256), (size_t)nb * BS * sizeof(float),
-                               st, A, B, S, Z, Y, N, K, nb, pro);
-            return check_launch("mnb_gemv4");
-        }
-    }
-    // One row (or one gate/up pair) per group; at most 4 workgroups per CU, each
-    // wave walking its groups with the next group's loads in flight (measured best
-    // on MI355X for the K=4096 x N=11008 shape against 1-4 rows per group and 1-8
-    // workgroups/CU).
     constexpr int R = PAIR ? 2 : 1;
-    const int Kp = nb * BS;
+    constexpr bool H2 = std::is_same<T, half_t>::value;
     const long groups = ((long)N + R - 1) / R;
-    long grid = (groups + 3) / 4;
-    if (grid > 4L * device_cu_count()) grid = 4L * device_cu_count();
-    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, PRO, PAIR>), dim3((unsigned)grid),
-                       dim3(256), (size_t)Kp * sizeof(float), st, A, B, S, Z, Y, N, K, nb, pro);
-    return check_launch("mnb_gemv4");
+    const long cus = device_cu_count();
+    const bool longwalk = groups > 80 * cus;
+    long grid;
+    if (longwalk) grid = (groups + 63) / 64;
+    else if (CPL >= 3) grid = (groups + 7) / 8;
+    else if (groups <= 10 * cus) grid = (groups + 3) / 4;
+    else if (CPL >= 2) grid = std::min((groups + 3) / 4, 4 * cus);
+    else grid = (groups + 11) / 12;
+    bool sv = false;
+    if constexpr (BS == 32 && CPL % 2 == 0)  // scale pairs as one load when every lane's pair is aligned
+        sv = nb % 2 == 0 && (reinterpret_cast<uintptr_t>(S) % (2 * sizeof(T))) == 0 && nb >= 2;
+    constexpr bool kSV = BS == 32 && CPL % 2 == 0;
+#define ORTMI_GEMV_INST(DV, SVV, NTV)                                                              \
+    return launch_gemv4_inst<T, BS, CPL, R, DV, PRO, PAIR, SVV, H2, NTV>(A, B, S, Z, Y, N, K, nb, \
+                                                                        pro, grid, st)
+    if constexpr (CPL >= 3) {
+        if (sv) ORTMI_GEMV_INST(1, kSV, false);
+        ORTMI_GEMV_INST(1, false, false);
+    } else {
+        if (longwalk) {
+            if (sv) ORTMI_GEMV_INST(4, kSV, false);
+            ORTMI_GEMV_INST(4, false, false);
+        }
+        if (sv) ORTMI_GEMV_INST(2, kSV, true);
+        ORTMI_GEMV_INST(2, false, true);
+    }
+#undef ORTMI_GEMV_INST
 }
 
 template <typename T, int BS, bool PRO = false, bool PAIR = false>
@@ -351,6 +484,7 @@ static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t*
     const int C = nb * BS / 32;
     const int cpl = (C + 63) / 64;
     if ((long)nb * BS > 2048L * (16 / (long)sizeof(T))) return -1;  // activation staging bound
+    if ((size_t)N * nb * BS / 2 > 0xFFFFFF00ull) return -1;  // buffer offsets are 32-bit
     switch (cpl) {
         case 1: return launch_gemv4_cpl<T, BS, 1, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
         case 2: return launch_gemv4_cpl<T, BS, 2, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
@@ -384,14 +518,6 @@ __device__ __forceinline__ uint4 dequant_word_pairs(uint32_t w, half2_t zoff, ha
     return make_uint4(r[0], r[1], r[2], r[3]);
 }
 
-// Reorder 8 activations [a0..a7] to the pair order [a0,a4,a1,a5,a2,a6,a3,a7] used by
-// the dequantised weights (an identical permutation of k on both MFMA operands).
-__device__ __forceinline__ uint4 permute_act8(uint4 v) {
-    return make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u),
-                      __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
-                      __builtin_amdgcn_perm(v.w, v.y, 0x05040100u),
-                      __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
-}
 
 template <int BM, int BN, int BS>
 struct GemmStage {
