@@ -93,6 +93,21 @@ int ortmi_matmul_nbits_decode_fused(const void* x, const void* skip, const void*
                                     int32_t dtype, void* stream);
 
 /*
+ * MatMulNBits decode step (M = 1) whose activation row is the output of the
+ * one-token GroupQueryAttention still held as split partials (written by
+ * ortmi_group_query_attention_decode_partials): partials [K / head_size heads]
+ * [splits][head_size + 2] fp32 (o[head_size], max, sum), merged per head as
+ * a = (sum_i e^(m_i - M) o_i) / (sum_i e^(m_i - M) l_i), M = max_i m_i, rounded
+ * to dtype, then the GEMV. K = heads * head_size (batch 1). fp16/bf16 only.
+ * Replaces: the GQA output write (rust/src/ops/attention.rs:910-920) and the
+ * o_proj quantized_matmul (rust/src/ops/quant.rs:570-601) reading it back.
+ */
+int ortmi_matmul_nbits_decode_merge(const float* partials, int64_t splits, int64_t head_size,
+                                    const uint8_t* B, const void* scales,
+                                    const uint8_t* zero_points, void* Y, int64_t N, int64_t K,
+                                    int64_t block_size, int32_t dtype, void* stream);
+
+/*
  * GroupQueryAttention (com.microsoft), decode and prefill, with in-op RoPE.
  * query [B,S,H*hd] (or packed [B,S,(H+2*KV)*hd] when key == value == NULL),
  * key/value [B,S,KV*hd]; past_key/past_value [B,KV,past_cap,hd].
@@ -144,6 +159,29 @@ int ortmi_group_query_attention_decode_capturable(
     int64_t num_heads, int64_t kv_num_heads, int64_t head_size, float scale,
     int32_t rotary_interleaved, int32_t dtype, void* workspace, size_t workspace_bytes,
     void* stream);
+
+/*
+ * The one-token step of ortmi_group_query_attention_decode_capturable, leaving
+ * the attention output as split partials for ortmi_matmul_nbits_decode_merge
+ * (the o_proj consumer) instead of merging them: partials [batch * num_heads]
+ * [splits][head_size + 2] fp32 (16-byte aligned), splits =
+ * ortmi_group_query_attention_decode_splits(batch, num_heads, kv_num_heads,
+ * head_size, kv_cap), chosen so that the partials of all heads stay within what
+ * the merging GEMV stages (8192 floats); 0 (and ORTMI_E_INVALID from the step,
+ * before any write) when even one split per head does not fit. No workspace.
+ * The KV append is the same.
+ * Replaces: as ortmi_group_query_attention_decode_capturable, minus the output
+ * write (rust/src/ops/attention.rs:910-920), which the consumer folds in.
+ */
+int64_t ortmi_group_query_attention_decode_splits(int64_t batch, int64_t num_heads,
+                                                  int64_t kv_num_heads, int64_t head_size,
+                                                  int64_t kv_cap);
+int ortmi_group_query_attention_decode_partials(
+    const void* query, const void* key, const void* value, void* kv_key, void* kv_value,
+    int64_t kv_cap, const int32_t* total_sequence_length_device, const void* cos_cache,
+    const void* sin_cache, int64_t rotary_half, int64_t max_pos, float* partials, int64_t batch,
+    int64_t num_heads, int64_t kv_num_heads, int64_t head_size, float scale,
+    int32_t rotary_interleaved, int32_t dtype, void* stream);
 
 /*
  * PagedAttention (com.microsoft), mixed prefill + decode over a block-paged KV

@@ -61,6 +61,8 @@ SIGNATURES = {
                                           _i32, _vp]),
     "ortmi_matmul_nbits_decode_fused": (ctypes.c_int, [
         _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
+    "ortmi_matmul_nbits_decode_merge": (ctypes.c_int, [
+        _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
     "ortmi_group_query_attention_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "ortmi_group_query_attention": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
@@ -68,6 +70,10 @@ SIGNATURES = {
     "ortmi_group_query_attention_decode_capturable": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
         _f32, _i32, _i32, _vp, _sz, _vp]),
+    "ortmi_group_query_attention_decode_splits": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "ortmi_group_query_attention_decode_partials": (ctypes.c_int, [
+        _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
+        _f32, _i32, _i32, _vp]),
     "ortmi_paged_attention_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "ortmi_paged_attention": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp,

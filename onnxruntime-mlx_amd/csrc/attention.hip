@@ -402,9 +402,10 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
         if (base + 2 * BLK < j1) load_block(kr, vr, base + 2 * BLK);
         process(kn, vn, base + BLK);
     }
+    // out == null: split partials only (even for one split), merged by the consumer.
     decode_merge<HD, G, LPR, NW>(m, l, o, s_m, s_l, s_o, [&](int g, int d, float M, float L, float acc) {
         const int64_t row = (int64_t)b * H + h0 + g;
-        if (nsplit == 1) {
+        if (nsplit == 1 && out) {
             out[row * HD + d] = from_f32<T>(L > 0.f ? acc / L : 0.f);
             return;
         }
@@ -1392,6 +1393,22 @@ static int gqa_nsplit(int64_t BKV, int64_t nkeys, int& chunk) {
     return (int)((nkeys + c - 1) / c);
 }
 
+// Splits of a one-token step whose partials go to the o_proj GEMV: the GQA rule,
+// with longer chunks when the partials of all heads would exceed what the GEMV
+// stages (0 when even one split does not fit).
+static int gqa_partials_nsplit(int64_t B, int64_t H, int64_t KV, int64_t hd, int64_t cap,
+                               int& chunk) {
+    const int64_t per_split = B * H * (hd + 2);
+    const int64_t max_ns = kDecodeMergeMaxFloats / per_split;
+    if (max_ns < 1) return 0;
+    const int ns = gqa_nsplit(B * KV, cap, chunk);
+    if (ns <= max_ns) return ns;
+    int64_t c = (cap + max_ns - 1) / max_ns;
+    c = (c + 63) / 64 * 64;
+    chunk = (int)c;
+    return (int)((cap + c - 1) / c);
+}
+
 }  // namespace ortmi
 
 using namespace ortmi;
@@ -1600,7 +1617,7 @@ static int run_gqa_decode_capturable(const void* query, const void* key, const v
                                      const int32_t* total_dev, const void* cos_c,
                                      const void* sin_c, int half, int64_t max_pos, void* output,
                                      int B, int H, int KV, float scale, int interleaved, void* ws,
-                                     size_t ws_bytes, hipStream_t st) {
+                                     size_t ws_bytes, float* partials_out, hipStream_t st) {
     const int G = H / KV;
     const bool packed = key == nullptr;
     const int64_t q_stride = packed ? (int64_t)(H + 2 * KV) * HD : (int64_t)H * HD;
@@ -1612,33 +1629,38 @@ static int run_gqa_decode_capturable(const void* query, const void* key, const v
     if (G < 1 || G > 8 || (cos_c && !interleaved && half % 8 != 0) || !a16(q) || !a16(k) ||
         !a16(v) || !a16(kv_key) || !a16(kv_value))
         return fail(ORTMI_E_INVALID, "GroupQueryAttention: form has no capturable decode kernel");
-    if (ws_bytes < ortmi_group_query_attention_workspace_size(B, 1, H, HD, cap) || !ws)
-        return fail(ORTMI_E_WORKSPACE, "GroupQueryAttention: workspace too small");
-    float* part = reinterpret_cast<float*>(static_cast<char*>(ws) +
-                                           align_up((size_t)B * H * HD * 4));
+    float* part = partials_out;
+    if (!part) {
+        if (ws_bytes < ortmi_group_query_attention_workspace_size(B, 1, H, HD, cap) || !ws)
+            return fail(ORTMI_E_WORKSPACE, "GroupQueryAttention: workspace too small");
+        part = reinterpret_cast<float*>(static_cast<char*>(ws) + align_up((size_t)B * H * HD * 4));
+    }
     // Splits are sized for a full buffer; splits past the live keys contribute
     // empty partials (max -inf, sum 0) that the merge weighs by zero.
     int chunk = 0;
-    const int ns = gqa_nsplit((int64_t)B * KV, cap, chunk);
+    const int ns = partials_out ? gqa_partials_nsplit(B, H, KV, HD, cap, chunk)
+                                : gqa_nsplit((int64_t)B * KV, cap, chunk);
+    if (ns < 1) return fail(ORTMI_E_INVALID, "GroupQueryAttention: too many heads for partials");
     const float sc = scale != 0.f ? scale : 1.0f / sqrtf((float)HD);
     const int vp_max = (int)std::min<int64_t>(cap, cos_c ? max_pos : cap) - 1;
     if (int rc = launch_gqa_decode<T, HD>(
             G, B, KV, ns, chunk, q, k, v, q_stride, kv_stride, static_cast<const T*>(cos_c),
             static_cast<const T*>(sin_c), half, interleaved, static_cast<const T*>(kv_key),
             static_cast<const T*>(kv_value), static_cast<T*>(kv_key), static_cast<T*>(kv_value),
-            cap, cap, 0, 0, sc, part, static_cast<T*>(output), total_dev, vp_max, st))
+            cap, cap, 0, 0, sc, part, partials_out ? nullptr : static_cast<T*>(output), total_dev,
+            vp_max, st))
         return rc;
-    if (ns == 1) return ORTMI_OK;
+    if (ns == 1 || partials_out) return ORTMI_OK;
     hipLaunchKernelGGL((attn_merge_kernel<T>), dim3(B * H), dim3(128), 0, st, part,
                        static_cast<T*>(output), ns, (const int*)nullptr, HD, H, (int64_t)H * HD,
                        (const int*)nullptr);
     return check_launch("gqa_merge");
 }
 
-extern "C" int ortmi_group_query_attention_decode_capturable(
+static int gqa_decode_capturable_entry(
     const void* query, const void* key, const void* value, void* kv_key, void* kv_value,
-    int64_t kv_cap, const int32_t* total_sequence_length_device, const void* cos_cache,
-    const void* sin_cache, int64_t rotary_half, int64_t max_pos, void* output, int64_t batch,
+    int64_t kv_cap, const int32_t* total_dev, const void* cos_cache, const void* sin_cache,
+    int64_t rotary_half, int64_t max_pos, void* output, float* partials, int64_t batch,
     int64_t num_heads, int64_t kv_num_heads, int64_t head_size, float scale,
     int32_t rotary_interleaved, int32_t dtype, void* workspace, size_t workspace_bytes,
     void* stream) {
@@ -1647,7 +1669,7 @@ extern "C" int ortmi_group_query_attention_decode_capturable(
     ORTMI_REQUIRE(head_size == 64 || head_size == 128,
                   "GroupQueryAttention: head_size must be 64 or 128");
     ORTMI_REQUIRE(batch > 0 && kv_cap > 0, "GroupQueryAttention: bad shape");
-    ORTMI_REQUIRE(query && output && kv_key && kv_value && total_sequence_length_device,
+    ORTMI_REQUIRE(query && (output || partials) && kv_key && kv_value && total_dev,
                   "GroupQueryAttention: null tensor");
     ORTMI_REQUIRE((key == nullptr) == (value == nullptr),
                   "GroupQueryAttention: key and value must both be given or both be packed");
@@ -1661,9 +1683,9 @@ extern "C" int ortmi_group_query_attention_decode_capturable(
     const int B = (int)batch, H = (int)num_heads, KV = (int)kv_num_heads;
 #define ORTMI_GQA_CAP(T, HD)                                                                   \
     return run_gqa_decode_capturable<T, HD>(query, key, value, kv_key, kv_value, kv_cap,       \
-                                            total_sequence_length_device, cos_cache, sin_cache, \
-                                            (int)rotary_half, max_pos, output, B, H, KV, scale, \
-                                            rotary_interleaved, workspace, workspace_bytes, st)
+                                            total_dev, cos_cache, sin_cache, (int)rotary_half, \
+                                            max_pos, output, B, H, KV, scale, rotary_interleaved, \
+                                            workspace, workspace_bytes, partials, st)
     if (dtype == ORTMI_F16) {
         if (head_size == 64) ORTMI_GQA_CAP(half_t, 64);
         ORTMI_GQA_CAP(half_t, 128);
@@ -1674,6 +1696,44 @@ extern "C" int ortmi_group_query_attention_decode_capturable(
     }
 #undef ORTMI_GQA_CAP
     return fail(ORTMI_E_INVALID, "GroupQueryAttention: dtype must be fp16 or bf16");
+}
+
+extern "C" int ortmi_group_query_attention_decode_capturable(
+    const void* query, const void* key, const void* value, void* kv_key, void* kv_value,
+    int64_t kv_cap, const int32_t* total_sequence_length_device, const void* cos_cache,
+    const void* sin_cache, int64_t rotary_half, int64_t max_pos, void* output, int64_t batch,
+    int64_t num_heads, int64_t kv_num_heads, int64_t head_size, float scale,
+    int32_t rotary_interleaved, int32_t dtype, void* workspace, size_t workspace_bytes,
+    void* stream) {
+    ORTMI_REQUIRE(output, "GroupQueryAttention: null output");
+    return gqa_decode_capturable_entry(query, key, value, kv_key, kv_value, kv_cap,
+                                       total_sequence_length_device, cos_cache, sin_cache,
+                                       rotary_half, max_pos, output, nullptr, batch, num_heads,
+                                       kv_num_heads, head_size, scale, rotary_interleaved, dtype,
+                                       workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t ortmi_group_query_attention_decode_splits(int64_t batch, int64_t num_heads,
+                                                             int64_t kv_num_heads,
+                                                             int64_t head_size, int64_t kv_cap) {
+    if (batch <= 0 || num_heads <= 0 || kv_num_heads <= 0 || head_size <= 0 || kv_cap <= 0)
+        return 0;
+    int chunk = 0;
+    return gqa_partials_nsplit(batch, num_heads, kv_num_heads, head_size, kv_cap, chunk);
+}
+
+extern "C" int ortmi_group_query_attention_decode_partials(
+    const void* query, const void* key, const void* value, void* kv_key, void* kv_value,
+    int64_t kv_cap, const int32_t* total_sequence_length_device, const void* cos_cache,
+    const void* sin_cache, int64_t rotary_half, int64_t max_pos, float* partials, int64_t batch,
+    int64_t num_heads, int64_t kv_num_heads, int64_t head_size, float scale,
+    int32_t rotary_interleaved, int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(partials, "GroupQueryAttention: null partials");
+    return gqa_decode_capturable_entry(query, key, value, kv_key, kv_value, kv_cap,
+                                       total_sequence_length_device, cos_cache, sin_cache,
+                                       rotary_half, max_pos, nullptr, partials, batch, num_heads,
+                                       kv_num_heads, head_size, scale, rotary_interleaved, dtype,
+                                       nullptr, 0, stream);
 }
 
 // ------------------------------------------------------- PagedAttention API --

@@ -19,6 +19,10 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
+// Largest split-partial array a one-token attention hands to the o_proj GEMV
+// (fp32 floats, all heads): the GEMV's workgroups stage it in LDS (32 KB).
+constexpr int kDecodeMergeMaxFloats = 8192;
+
 // ---------------------------------------------------------------- dtype IO --
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(half_t x) { return (float)x; }

@@ -128,6 +128,10 @@ class Plan {
         void* ptr = nullptr;
         int dtype = 0;
         std::vector<int64_t> dims;
+        // splits > 0: the value is a one-token attention output still held as fp32
+        // split partials [heads][splits][head + 2] (see the attention-merge rewrite).
+        int64_t splits = 0;
+        int64_t head = 0;
         int64_t numel() const {
             int64_t n = 1;
             for (auto d : dims) n *= d;

@@ -15,6 +15,10 @@
 //                                                   => the norm runs as that
 //     node's prologue (attributes __norm / __norm_eps, skip and gamma as inputs
 //     6 and 7, the residual sum as output 1)
+//  5. GroupQueryAttention whose output feeds one plain MatMulNBits and nothing
+//     else                                          => at one-token decode steps
+//     the attention leaves its split partials and the MatMulNBits merges them in
+//     its prologue (attributes __partials / __merge); other steps run unfused
 #include <algorithm>
 #include <map>
 #include <set>
@@ -322,6 +326,32 @@ void fuse_norm_prologue(GraphIR& g, const std::vector<std::string>& outputs) {
     drop_dead(g, dead);
 }
 
+void mark_attention_merge(GraphIR& g, const std::vector<std::string>& outputs) {
+    auto uses = count_uses(g, outputs);
+    for (auto& n : g.nodes) {
+        if (n.op != "GroupQueryAttention" || n.outputs.empty() || n.outputs[0].empty()) continue;
+        const std::string& y = n.outputs[0];
+        if (uses[y] != 1) continue;
+        const int64_t H = n.attr_int("num_heads", 0);
+        for (auto& c : g.nodes) {
+            if (c.op != "MatMulNBits" || c.inputs.empty() || c.inputs[0] != y) continue;
+            if (!plain_mnb(c, g) || c.attr_int("__norm", 0)) continue;
+            const int64_t K = c.attr_int("K", 0), bs = c.attr_int("block_size", 32);
+            const int sdt = constant(g, c.inputs[2])->dtype;
+            const bool half_scales = sdt == ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16 ||
+                                     sdt == ONNX_TENSOR_ELEMENT_DATA_TYPE_BFLOAT16;
+            const int64_t hd = H > 0 && K % H == 0 ? K / H : 0;
+            // The merge GEMV's form: 4-bit, block 32-128, K within its staging,
+            // fp16/bf16, head size 64 or 128.
+            if (!half_scales || (bs != 32 && bs != 64 && bs != 128) || K > 10240 ||
+                (hd != 64 && hd != 128))
+                continue;
+            n.attrs["__partials"] = int_attr(1);
+            c.attrs["__merge"] = int_attr(1);
+        }
+    }
+}
+
 // Stable topological order (a merged node may now produce a value that an
 // earlier node in the old order reads).
 void topo_sort(GraphIR& g) {
@@ -368,6 +398,7 @@ void fuse_subgraph(GraphIR& g, const std::vector<std::string>& outputs, bool dec
         fuse_qkv(g, outputs);
         fuse_gate_up(g, outputs);
         fuse_norm_prologue(g, outputs);
+        mark_attention_merge(g, outputs);
         drop_unused_constants(g);
     }
     topo_sort(g);

@@ -374,6 +374,17 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         od.back() = pair ? N / 2 : N;
         const std::string res_name = norm && n.outputs.size() > 1 ? n.outputs[1] : std::string();
         void* zp = Z ? Z->ptr : nullptr;
+        if (X.splits > 0) {
+            // The attention before this node left its one-token output as split
+            // partials (attention-merge rewrite): merge them in the GEMV prologue.
+            if (M != 1 || norm || pair) fail(op + ": split partials need a plain decode GEMV");
+            Tensor& Y = out_tensor(outname(0), dtype, od, a, ctx);
+            check_kernel(ortmi_matmul_nbits_decode_merge(
+                             (const float*)X.ptr, X.splits, X.head, (const uint8_t*)B.ptr, S.ptr,
+                             (const uint8_t*)zp, Y.ptr, N, K, bs, kdt(dtype), st),
+                         op.c_str());
+            return;
+        }
         if (M == 1 && bits == 4 && (norm || pair) &&
             (dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16 ||
              dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_BFLOAT16)) {
@@ -452,11 +463,30 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         // and eager steps give identical results.
         if (S == 1 && shared && pk && pv && prk == pkp && prv == pvp &&
             host_scalars_.count(n.inputs[6]) && (!cs || total <= max_pos)) {
+            const int32_t* tdev = (const int32_t*)env_.at(n.inputs[6]).ptr;
+            if (B == 1 && n.attr_int("__partials", 0) &&
+                ortmi_group_query_attention_decode_splits(B, H, KV, hd, cap) > 0) {
+                // Output left as split partials for the o_proj GEMV to merge.
+                const int64_t ns = ortmi_group_query_attention_decode_splits(B, H, KV, hd, cap);
+                float* part = (float*)arena_alloc((size_t)(B * H * ns * (hd + 2)) * sizeof(float));
+                const int rc = ortmi_group_query_attention_decode_partials(
+                    q.ptr, kptr, vptr, prk, prv, cap, tdev, csp, snp, half, max_pos, part, B, H,
+                    KV, hd, scale, inter, kdt(q.dtype), st);
+                if (rc == ORTMI_OK) {
+                    Tensor& o = env_[outname(0)];
+                    o.ptr = part;
+                    o.splits = ns;
+                    o.head = hd;
+                    guards_.push_back({n.inputs[6], cs ? std::min<int64_t>(cap, max_pos) : cap});
+                    return;
+                }
+                if (rc != ORTMI_E_INVALID) check_kernel(rc, "GroupQueryAttention");
+            }
             const size_t wsb = ortmi_group_query_attention_workspace_size(B, 1, H, hd, cap);
             void* ws = workspace(wsb);
             const int rc = ortmi_group_query_attention_decode_capturable(
-                q.ptr, kptr, vptr, prk, prv, cap, (const int32_t*)env_.at(n.inputs[6]).ptr, csp,
-                snp, half, max_pos, optr, B, H, KV, hd, scale, inter, kdt(q.dtype), ws, wsb, st);
+                q.ptr, kptr, vptr, prk, prv, cap, tdev, csp, snp, half, max_pos, optr, B, H, KV,
+                hd, scale, inter, kdt(q.dtype), ws, wsb, st);
             if (rc == ORTMI_OK) {
                 guards_.push_back({n.inputs[6], cs ? std::min<int64_t>(cap, max_pos) : cap});
                 return;

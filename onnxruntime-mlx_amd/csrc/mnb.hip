@@ -129,12 +129,18 @@ __device__ __forceinline__ float dot32_pairs(const uint4 (&av)[4], uint4 w, half
 //  * SwiGLU pairs: rows come interleaved (gate row i, up row i), a wave takes both
 //    rows of a pair and writes Y[i] = (g * sigmoid(g)) * u, each op rounded to T as
 //    the Sigmoid/Mul/Mul graph stores it.
+//  * split merge (MRG): the activation row is attention output still held as
+//    split partials [heads][splits][hd + 2] (o, max, sum) by the one-token decode;
+//    each workgroup merges them as the merge kernel would, rounding to T.
 template <typename T>
 struct GemvPrologue {
     const T* skip;
     const T* gamma;
     T* residual;
     float eps;
+    const float* part = nullptr;
+    int splits = 0;
+    int hd = 0;
 };
 
 // Buffer resource word 3 for raw (untyped) buffer loads on gfx9-family GPUs.
@@ -164,8 +170,24 @@ __device__ __forceinline__ void load_scale_pair(__amdgpu_buffer_rsrc_t r, uint32
     }
 }
 
+// Split-merge prologue bounds: partial floats per workgroup (one batch of
+// float4 loads, kMergeVec per thread).
+constexpr int kMergeVec = kDecodeMergeMaxFloats / (256 * 4);
+
+// LDS bytes of the staged activation row (fp16 pairs or fp32 units).
+template <typename T, bool H2>
+constexpr size_t gemv_stage_bytes(int Kp) {
+    return (size_t)Kp * (H2 ? sizeof(half_t) : sizeof(float));
+}
+// LDS bytes of the split-merge prologue: partials, split weights, 1/L per head.
+static inline size_t gemv_merge_bytes(int K, int hd, int splits) {
+    const size_t nh = (size_t)K / hd, nparts = nh * splits * (hd + 2);
+    return (((nparts + 3) & ~(size_t)3) + nh * splits + nh) * sizeof(float);
+}
+
 template <typename T, int BS, int CPL, int R, int D, bool PRO = false, bool PAIR = false,
-          bool SV = false, bool H2 = std::is_same<T, half_t>::value, bool NT = true>
+          bool SV = false, bool H2 = std::is_same<T, half_t>::value, bool NT = true,
+          bool MRG = false>
 __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ B,
                                                         const T* __restrict__ S,
@@ -206,8 +228,23 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
             t[e] = (vi < nvec && k0 + e < K) ? src[k0 + e] : from_f32<T>(0.f);
         return *reinterpret_cast<const uint4*>(t);
     };
+    // Split merge: the whole partial array in one batch of loads (at most
+    // kMergeVec float4 per thread; the launcher checks the size).
+    float4 pbuf[MRG ? kMergeVec : 1];
+    float ptail = 0.f;
+    if constexpr (MRG) {
+        const int nparts = (K / pro.hd) * pro.splits * (pro.hd + 2);
 #pragma unroll
-    for (int u = 0; u < AV; ++u) av[u] = load_vec(A, u);
+        for (int u = 0; u < kMergeVec; ++u) {
+            const int idx = threadIdx.x + 256 * u;
+            pbuf[u] = idx < nparts / 4 ? reinterpret_cast<const float4*>(pro.part)[idx]
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (threadIdx.x < (nparts & 3)) ptail = pro.part[(nparts & ~3) + threadIdx.x];
+    } else {
+#pragma unroll
+        for (int u = 0; u < AV; ++u) av[u] = load_vec(A, u);
+    }
     uint4 skv[PRO ? AV : 1], gmv[PRO ? AV : 1];
     if constexpr (PRO) {
 #pragma unroll
@@ -276,6 +313,62 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     Group g[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) load_group(g[d], g0 + d * waves_total);
+
+    if constexpr (MRG) {
+        // Partials -> LDS (after the staging area), then per head h the split
+        // weights e^(m_i - M) and 1 / sum_i w_i l_i, then activation k = h*hd + d
+        // as (sum_i w_i o_i[d]) / L, rounded to T as the merge kernel stores it.
+        const int nh = K / pro.hd, ns = pro.splits, stride = pro.hd + 2;
+        const int nparts = nh * ns * stride;
+        float* sP = reinterpret_cast<float*>(reinterpret_cast<char*>(sA) + gemv_stage_bytes<T, H2>(Kp));
+        float* sW = sP + ((nparts + 3) & ~3);
+        float* sInv = sW + nh * ns;
+#pragma unroll
+        for (int u = 0; u < kMergeVec; ++u) {
+            const int idx = threadIdx.x + 256 * u;
+            if (idx < nparts / 4) reinterpret_cast<float4*>(sP)[idx] = pbuf[u];
+        }
+        if (threadIdx.x < (nparts & 3)) sP[(nparts & ~3) + threadIdx.x] = ptail;
+        __syncthreads();
+        for (int h = threadIdx.x; h < nh; h += 256) {
+            const float* ph = sP + h * ns * stride;
+            float M = -INFINITY;
+            for (int i = 0; i < ns; ++i) M = fmaxf(M, ph[i * stride + pro.hd]);
+            float L = 0.f;
+            for (int i = 0; i < ns; ++i) {
+                const float mi = ph[i * stride + pro.hd];
+                const float w = mi == -INFINITY ? 0.f : __expf(mi - M);
+                sW[h * ns + i] = w;
+                L += w * ph[i * stride + pro.hd + 1];
+            }
+            sInv[h] = L > 0.f ? 1.0f / L : 0.f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < AV; ++u) {
+            const int vi = threadIdx.x + u * 256;
+            const int k0 = vi * EPL;
+            T t[EPL];
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) t[e] = from_f32<T>(0.f);
+            if (vi < nvec && k0 < K) {
+                const int h = k0 / pro.hd, d0 = k0 % pro.hd;
+                const float* ph = sP + h * ns * stride + d0;
+                const float* wh = sW + h * ns;
+                float acc[EPL];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+                for (int i = 0; i < ns; ++i) {
+                    const float w = wh[i];
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) acc[e] = fmaf(ph[i * stride + e], w, acc[e]);
+                }
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) t[e] = from_f32<T>(acc[e] * sInv[h]);
+            }
+            av[u] = *reinterpret_cast<const uint4*>(t);
+        }
+    }
 
     // 3. activations (normalised first when fused) -> LDS -> VGPRs.
     float scale_all = 1.f;
@@ -424,12 +517,13 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
 
 // Launch of one kernel instance: `grid` workgroups of 4 waves.
 template <typename T, int BS, int CPL, int R, int D, bool PRO, bool PAIR, bool SV, bool H2,
-          bool NT = true>
+          bool NT = true, bool MRG = false>
 static int launch_gemv4_inst(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
                              int N, int K, int nb, const GemvPrologue<T>& pro, long grid,
                              hipStream_t st) {
-    const size_t lds = (size_t)nb * BS * (H2 ? sizeof(half_t) : sizeof(float));
-    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, D, PRO, PAIR, SV, H2, NT>),
+    size_t lds = gemv_stage_bytes<T, H2>(nb * BS);
+    if constexpr (MRG) lds += gemv_merge_bytes(K, pro.hd, pro.splits);
+    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, D, PRO, PAIR, SV, H2, NT, MRG>),
                        dim3((unsigned)grid), dim3(256), lds, st, A, B, S, Z, Y, N, K, nb, pro);
     return check_launch("mnb_gemv4");
 }
@@ -442,7 +536,7 @@ static int launch_gemv4_inst(const T* A, const uint8_t* B, const T* S, const uin
 // fp32 K = 4096, 3 up to about 80 groups per CU, 16 beyond. A ring of 2, of 1 when
 // the activations fill the VGPRs, of 4 for the long walks. Weights non-temporal
 // except for those two cases, which measured faster with cached loads.
-template <typename T, int BS, int CPL, bool PRO, bool PAIR>
+template <typename T, int BS, int CPL, bool PRO, bool PAIR, bool MRG>
 static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
                             int N, int K, int nb, const GemvPrologue<T>& pro, hipStream_t st) {
     constexpr int R = PAIR ? 2 : 1;
@@ -461,8 +555,8 @@ static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint
         sv = nb % 2 == 0 && (reinterpret_cast<uintptr_t>(S) % (2 * sizeof(T))) == 0 && nb >= 2;
     constexpr bool kSV = BS == 32 && CPL % 2 == 0;
 #define ORTMI_GEMV_INST(DV, SVV, NTV)                                                              \
-    return launch_gemv4_inst<T, BS, CPL, R, DV, PRO, PAIR, SVV, H2, NTV>(A, B, S, Z, Y, N, K, nb, \
-                                                                        pro, grid, st)
+    return launch_gemv4_inst<T, BS, CPL, R, DV, PRO, PAIR, SVV, H2, NTV, MRG>(A, B, S, Z, Y, N, K, \
+                                                                             nb, pro, grid, st)
     if constexpr (CPL >= 3) {
         if (sv) ORTMI_GEMV_INST(1, kSV, false);
         ORTMI_GEMV_INST(1, false, false);
@@ -477,7 +571,7 @@ static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint
 #undef ORTMI_GEMV_INST
 }
 
-template <typename T, int BS, bool PRO = false, bool PAIR = false>
+template <typename T, int BS, bool PRO = false, bool PAIR = false, bool MRG = false>
 static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y, int N,
                         int K, int nb, hipStream_t st,
                         const GemvPrologue<T>& pro = GemvPrologue<T>{nullptr, nullptr, nullptr, 0.f}) {
@@ -486,11 +580,11 @@ static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t*
     if ((long)nb * BS > 2048L * (16 / (long)sizeof(T))) return -1;  // activation staging bound
     if ((size_t)N * nb * BS / 2 > 0xFFFFFF00ull) return -1;  // buffer offsets are 32-bit
     switch (cpl) {
-        case 1: return launch_gemv4_cpl<T, BS, 1, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
-        case 2: return launch_gemv4_cpl<T, BS, 2, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
-        case 3: return launch_gemv4_cpl<T, BS, 3, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
-        case 4: return launch_gemv4_cpl<T, BS, 4, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
-        case 5: return launch_gemv4_cpl<T, BS, 5, PRO, PAIR>(A, B, S, Z, Y, N, K, nb, pro, st);
+        case 1: return launch_gemv4_cpl<T, BS, 1, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
+        case 2: return launch_gemv4_cpl<T, BS, 2, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
+        case 3: return launch_gemv4_cpl<T, BS, 3, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
+        case 4: return launch_gemv4_cpl<T, BS, 4, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
+        case 5: return launch_gemv4_cpl<T, BS, 5, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
         default: return -1;  // K > 10240: the caller falls back
     }
 }
@@ -864,6 +958,57 @@ extern "C" int ortmi_matmul_nbits_decode_fused(const void* x, const void* skip, 
         default:
             return fail(ORTMI_E_INVALID, "MatMulNBits fused: fp16 or bf16 activations only");
     }
+}
+
+namespace ortmi {
+template <typename T>
+static int run_merge_gemv(const float* part, int splits, int hd, const uint8_t* B, const void* S,
+                          const uint8_t* Z, void* Y, int N, int K, int bs, hipStream_t st) {
+    const int nb = (K + bs - 1) / bs;
+    GemvPrologue<T> pro{nullptr, nullptr, nullptr, 0.f, part, splits, hd};
+    const T* s = static_cast<const T*>(S);
+    T* y = static_cast<T*>(Y);
+    if (bs == 32) return launch_gemv4<T, 32, false, false, true>(nullptr, B, s, Z, y, N, K, nb, st, pro);
+    if (bs == 64) return launch_gemv4<T, 64, false, false, true>(nullptr, B, s, Z, y, N, K, nb, st, pro);
+    return launch_gemv4<T, 128, false, false, true>(nullptr, B, s, Z, y, N, K, nb, st, pro);
+}
+}  // namespace ortmi
+
+extern "C" int ortmi_matmul_nbits_decode_merge(const float* partials, int64_t splits,
+                                               int64_t head_size, const uint8_t* B,
+                                               const void* scales, const uint8_t* zero_points,
+                                               void* Y, int64_t N, int64_t K, int64_t block_size,
+                                               int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(partials && B && scales && Y, "MatMulNBits merge: null tensor");
+    ORTMI_REQUIRE(splits >= 1 && splits <= 4096, "MatMulNBits merge: bad split count");
+    ORTMI_REQUIRE(head_size == 64 || head_size == 128,
+                  "MatMulNBits merge: head_size must be 64 or 128");
+    ORTMI_REQUIRE(K > 0 && K % head_size == 0 && N > 0 && N < (1LL << 31),
+                  "MatMulNBits merge: K must be a whole number of heads");
+    ORTMI_REQUIRE(block_size == 32 || block_size == 64 || block_size == 128,
+                  "MatMulNBits merge: block_size must be 32, 64 or 128");
+    ORTMI_REQUIRE((reinterpret_cast<uintptr_t>(B) & 15) == 0,
+                  "MatMulNBits merge: B must be 16-byte aligned");
+    const int64_t nb = (K + block_size - 1) / block_size;
+    ORTMI_REQUIRE(nb * block_size <= 10240, "MatMulNBits merge: K too large for the decode kernel");
+    ORTMI_REQUIRE((reinterpret_cast<uintptr_t>(partials) & 15) == 0,
+                  "MatMulNBits merge: partials must be 16-byte aligned");
+    const size_t stage = (size_t)nb * block_size * (dtype == ORTMI_F16 ? 2 : 4);
+    if ((K / head_size) * splits * (head_size + 2) > kDecodeMergeMaxFloats ||
+        gemv_merge_bytes((int)K, (int)head_size, (int)splits) + stage > 65536)
+        return fail(ORTMI_E_INVALID, "MatMulNBits merge: too many split partials for one workgroup");
+    hipStream_t st = as_stream(stream);
+    int rc = -1;
+    if (dtype == ORTMI_F16)
+        rc = run_merge_gemv<half_t>(partials, (int)splits, (int)head_size, B, scales, zero_points,
+                                    Y, (int)N, (int)K, (int)block_size, st);
+    else if (dtype == ORTMI_BF16)
+        rc = run_merge_gemv<uint16_t>(partials, (int)splits, (int)head_size, B, scales,
+                                      zero_points, Y, (int)N, (int)K, (int)block_size, st);
+    else
+        return fail(ORTMI_E_INVALID, "MatMulNBits merge: fp16 or bf16 activations only");
+    if (rc < 0) return fail(ORTMI_E_INVALID, "MatMulNBits merge: shape has no decode kernel");
+    return rc;
 }
 
 extern "C" int ortmi_matmul_nbits(const void* A, const uint8_t* B, const void* scales,

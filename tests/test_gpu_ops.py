@@ -336,6 +336,50 @@ def test_gqa_decode_capturable(ortmi, oracle, H, KV, hd):
         assert torch.equal(kg, ke) and torch.equal(vg, ve)
 
 
+@pytest.mark.parametrize("H,KV,hd,past", [(12, 2, 128, 140), (8, 8, 64, 5), (16, 4, 128, 299)])
+def test_gqa_partials_merge_gemv(ortmi, oracle, H, KV, hd, past):
+    """One-token attention left as split partials and merged in the o_proj GEMV's
+    prologue equals the capturable attention followed by the plain GEMV (same KV
+    append, bit for bit; outputs within the GEMV tolerance plus one fp16 rounding
+    of each activation)."""
+    import ctypes
+
+    import torch
+
+    rng = np.random.default_rng(H * 3 + hd + past)
+    B, cap = 1, 300
+    q, k, v, pk, pv, cos, sin = _gqa_inputs(rng, B, 1, H, KV, hd, cap, True, 1e6)
+    dq, dk, dv, dcos, dsin = dev(q), dev(k), dev(v), dev(cos), dev(sin)
+    tot = torch.tensor([past + 1], dtype=torch.int32, device="cuda")
+    ka, va, kb, vb = dev(pk), dev(pv), dev(pk), dev(pv)
+    ref = ortmi.group_query_attention_decode_capturable(
+        dq, dk, dv, ka, va, tot, dcos, dsin, num_heads=H, kv_num_heads=KV)
+    K, N, block = H * hd, 1536, 32
+    _, W, s_, zp = _mnb_inputs(rng, 1, N, K, block, asym=True, dtype=np.float16)
+    dW, ds, dz = dev(W), dev(s_), dev(zp)
+    y_ref = ortmi.matmul_nbits(ref.reshape(1, K), dW, ds, dz, K=K, N=N, bits=4, block_size=block)
+    lib = ortmi.load_kernels()
+    ns = lib.ortmi_group_query_attention_decode_splits(B, H, KV, hd, cap)
+    assert ns >= 1
+    part = torch.empty(B * H * ns * (hd + 2), dtype=torch.float32, device="cuda")
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ortmi.check(lib.ortmi_group_query_attention_decode_partials(
+        p(dq), p(dk), p(dv), p(kb), p(vb), cap, p(tot), p(dcos), p(dsin), cos.shape[1],
+        cos.shape[0], p(part), B, H, KV, hd, 0.0, 0, 10, st))
+    y = torch.empty(N, dtype=torch.float16, device="cuda")
+    ortmi.check(lib.ortmi_matmul_nbits_decode_merge(
+        p(part), ns, hd, p(dW), p(ds), p(dz), p(y), N, K, block, 10, st))
+    torch.cuda.synchronize()
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+    a = host(ref).reshape(K)
+    Wd = oracle.mnb_dequant(W, s_, zp, N, K, 4, block)
+    exact = oracle.mnb_matmul(oracle.round_f16(a), W, s_, zp, N, K, 4, block)
+    extra = np.abs(Wd) @ (np.abs(a) * 2.0 ** -10)
+    assert_f16_close(host(y), exact, extra=extra, what="merged o_proj GEMV")
+    assert_f16_close(host(y_ref).reshape(N), exact, extra=extra, what="unfused o_proj GEMV")
+
+
 @pytest.mark.parametrize("S,past,cap", [(1, 40, 64), (9, 10, 64)])
 def test_gqa_packed_qkv(ortmi, oracle, S, past, cap):
     """Packed [B, S, (H + 2 KV) hd] input (key = value = None) equals separate Q/K/V."""
