@@ -279,10 +279,12 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
             const int n = min(gi * R + r, N - 1);
             const uint32_t zoff = live ? (uint32_t)(n * zp_cols) : z_end;
 #pragma unroll
-            for (int t = 0; t < ZB; ++t)
-                g.z[r][t] = Z ? (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(
-                                    rz, zoff + (uint32_t)min(blk0 / 2 + t, zp_cols - 1), 0, 0)
-                              : (uint8_t)0x88;
+            for (int t = 0; t < ZB; ++t) {
+                // Loaded either way (no records without Z): no load behind a branch.
+                const uint8_t zb = (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(
+                    rz, zoff + (uint32_t)min(blk0 / 2 + t, zp_cols - 1), 0, 0);
+                g.z[r][t] = Z ? zb : (uint8_t)0x88;
+            }
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const int c = c0 + j;
@@ -613,12 +615,16 @@ __device__ __forceinline__ uint4 dequant_word_pairs(uint32_t w, half2_t zoff, ha
 }
 
 
+// One k-step's loads, kept raw until they are stored to LDS (a conversion at load
+// time would make the compiler wait for this load, and so for every earlier one).
 template <int BM, int BN, int BS>
 struct GemmStage {
     static constexpr int A_VEC = BM * kBK / 8 / 256;  // 16-byte activation vectors per thread
     uint4 a[A_VEC];
-    uint4 b;        // 32 codes (one 32-code chunk of one weight row)
-    float s, z;     // scale and zero point of that chunk's block
+    uint4 b;         // 32 codes (one 32-code chunk of one weight row)
+    uint16_t s;      // fp16 bits of that chunk's block scale
+    uint8_t z;       // zero-point byte of the block pair
+    uint8_t zhi;     // 1: the block's zero point is the byte's high nibble
 };
 
 template <int BM, int BN, int BS>
@@ -653,7 +659,22 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
     const int chunks = Kp / 32;
     const size_t row_bytes = (size_t)Kp / 2;
     const int zp_cols = (nb + 1) / 2;
-    const bool kvec = (K % 8) == 0;
+    // Raw buffer loads with range checks: a row past M or N, or a chunk past the
+    // row, reads zeros without touching memory, so no load sits behind a branch
+    // and the two-step prefetch is never drained by a conservative wait. (A's
+    // rows are whole 16-byte vectors: the caller guarantees K % 8 == 0.)
+    const uint32_t a_end = (uint32_t)((size_t)M * K * sizeof(half_t));
+    const uint32_t b_end = (uint32_t)((size_t)N * row_bytes);
+    const uint32_t s_end = (uint32_t)((size_t)N * nb * sizeof(half_t));
+    const uint32_t z_end = Z ? (uint32_t)((size_t)N * zp_cols) : 0u;
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(A), 0, (int)a_end, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(B), 0, (int)b_end, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(S), 0, (int)s_end, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(Z ? Z : B), 0, (int)z_end, kBufferWord3);
 
     auto gload = [&](Stage& st, int ks) {
         const int k0 = ks * kBK;
@@ -662,29 +683,24 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
             const int idx = tid + p * 256;
             const int r = idx >> 3, c = (idx & 7) * 8;
             const int m = m0 + r, k = k0 + c;
-            if (m < M && kvec && k + 8 <= K) {
-                st.a[p] = *reinterpret_cast<const uint4*>(A + (size_t)m * K + k);
-            } else {
-                half_t t[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    t[i] = (m < M && k + i < K) ? A[(size_t)m * K + k + i] : (half_t)0;
-                st.a[p] = *reinterpret_cast<const uint4*>(t);
-            }
+            const uint32_t off =
+                (m < M && k < K) ? (uint32_t)(((size_t)m * K + k) * sizeof(half_t)) : a_end;
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+            st.a[p] = make_uint4(v.x, v.y, v.z, v.w);
         }
         const int r = tid >> 1;
         const int chunk = 2 * ks + (tid & 1);
         const int n = n0 + r;
-        if (n < N && chunk < chunks) {
-            st.b = *reinterpret_cast<const uint4*>(B + (size_t)n * row_bytes + (size_t)chunk * 16);
-            const int blk = (chunk * 32) / BS;
-            st.s = (float)S[(size_t)n * nb + blk];
-            st.z = Z ? (float)nibble(Z[(size_t)n * zp_cols + blk / 2], blk & 1) : 8.f;
-        } else {
-            st.b = make_uint4(0, 0, 0, 0);
-            st.s = 0.f;
-            st.z = 0.f;
-        }
+        const bool ok = n < N && chunk < chunks;
+        const int blk = (chunk * 32) / BS;
+        const uint32_t boff = ok ? (uint32_t)((size_t)n * row_bytes + (size_t)chunk * 16) : b_end;
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, boff, 0, 0);
+        st.b = make_uint4(v.x, v.y, v.z, v.w);
+        const uint32_t soff = ok ? (uint32_t)(((size_t)n * nb + blk) * sizeof(half_t)) : s_end;
+        st.s = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, soff, 0, 0);  // 0 out of range
+        const uint32_t zoff = ok ? (uint32_t)((size_t)n * zp_cols + blk / 2) : z_end;
+        st.z = (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(rz, zoff, 0, 0);
+        st.zhi = (uint8_t)(blk & 1);
     };
     auto sstore = [&](const Stage& st, int buf) {
 #pragma unroll
@@ -694,8 +710,10 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
             *reinterpret_cast<uint4*>(&sA[buf][r * kLdsRow + c]) = permute_act8(st.a[p]);
         }
         const int r = tid >> 1, h = tid & 1;
-        const half2_t zoff = {(half_t)(1024.f + st.z), (half_t)(1024.f + st.z)};
-        const half2_t s2 = {(half_t)st.s, (half_t)st.s};
+        const float zf = Z ? (float)nibble(st.z, st.zhi) : 8.f;
+        const half_t sh = __builtin_bit_cast(half_t, st.s);
+        const half2_t zoff = {(half_t)(1024.f + zf), (half_t)(1024.f + zf)};
+        const half2_t s2 = {sh, sh};
         uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32]);
         dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
         dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
@@ -735,22 +753,24 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
 
     // Pipeline: loads for step s are issued two steps ahead (register sets r0/r1
     // alternate), stored to the LDS buffer of step s at the end of step s-1.
+    // Loads and stores past the last step are issued too (they read zeros and
+    // fill a buffer nobody reads), so the loop has no branch around a load.
     Stage r0, r1;
     gload(r0, 0);
-    if (ksteps > 1) gload(r1, 1);
+    gload(r1, 1);
     sstore(r0, 0);
     __syncthreads();
     for (int ks = 0; ks < ksteps; ks += 2) {
         // even step ks: LDS buf 0 holds it; r1 holds step ks+1.
-        if (ks + 2 < ksteps) gload(r0, ks + 2);
+        gload(r0, ks + 2);
         compute(0);
-        if (ks + 1 < ksteps) sstore(r1, 1);
+        sstore(r1, 1);
         __syncthreads();
         if (ks + 1 >= ksteps) break;
         // odd step ks+1: LDS buf 1; r0 holds step ks+2.
-        if (ks + 3 < ksteps) gload(r1, ks + 3);
+        gload(r1, ks + 3);
         compute(1);
-        if (ks + 2 < ksteps) sstore(r0, 0);
+        sstore(r0, 0);
         __syncthreads();
     }
 
@@ -879,7 +899,9 @@ static int run_mnb(const void* A, const uint8_t* B, const void* S, const uint8_t
     }
     if constexpr (sizeof(T) == 2 && !std::is_same<T, uint16_t>::value) {
         const bool a_aligned = (reinterpret_cast<uintptr_t>(A) % 16) == 0 && K % 8 == 0;
-        if (fast_form && M > 1 && a_aligned) {
+        const bool fits32 = (size_t)M * K * 2 <= 0xFFFFFF00ull &&
+                            (size_t)N * nb * bs / 2 <= 0xFFFFFF00ull;  // 32-bit buffer offsets
+        if (fast_form && M > 1 && a_aligned && fits32) {
             if (bs == 32) return dispatch_gemm4<32>(a, B, s, Z, y, M, N, K, nb, st);
             if (bs == 64) return dispatch_gemm4<64>(a, B, s, Z, y, M, N, K, nb, st);
             if (bs == 128) return dispatch_gemm4<128>(a, B, s, Z, y, M, N, K, nb, st);
