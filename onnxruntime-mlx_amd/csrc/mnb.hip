@@ -187,7 +187,7 @@ static inline size_t gemv_merge_bytes(int K, int hd, int splits) {
 
 template <typename T, int BS, int CPL, int R, int D, bool PRO = false, bool PAIR = false,
           bool SV = false, bool H2 = std::is_same<T, half_t>::value, bool NT = true,
-          bool MRG = false>
+          bool MRG = false, int RW = 1>
 __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ B,
                                                         const T* __restrict__ S,
@@ -206,10 +206,16 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int waves_total = gridDim.x * 4;
-    const int ngroups = (N + R - 1) / R;
+    // A wave works on RW units of R rows at once, LR = 64 / RW lanes per unit
+    // (RW > 1 when a row has few chunks, so that no lane idles); a group is RW
+    // consecutive units.
+    constexpr int LR = 64 / RW;
+    const int li = lane % LR, slot = lane / LR;
+    const int nunits = (N + R - 1) / R;
+    const int ngroups = (nunits + RW - 1) / RW;
     const size_t row_bytes = (size_t)Kp / 2;
     const int zp_cols = (nb + 1) / 2;
-    const int c0 = lane * CPL;
+    const int c0 = li * CPL;
 
     // 1. activation loads (16 bytes each), all in flight before anything else.
     constexpr int EPL = 16 / sizeof(T);
@@ -272,11 +278,15 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
         __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(S), 0, (int)s_end, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(Z ? Z : B), 0, Z ? (int)z_end : 0, kBufferWord3);
+    // A unit past the end in a live group repeats the last unit (in bounds; its
+    // lanes then store the same values to the same rows).
+    auto unit_of = [&](int gi) { return min(gi * RW + slot, nunits - 1); };
     auto load_group = [&](Group& g, int gi) {
         const bool live = gi < ngroups;
+        const int unit = unit_of(gi);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int n = min(gi * R + r, N - 1);
+            const int n = min(unit * R + r, N - 1);
             const uint32_t zoff = live ? (uint32_t)(n * zp_cols) : z_end;
 #pragma unroll
             for (int t = 0; t < ZB; ++t) {
@@ -489,21 +499,22 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
             acc[r] = total;
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-        // Every lane holds the sums and every lane stores (same-address writes of a
-        // wave coalesce).
+        for (int r = 0; r < R; ++r) acc[r] = group_sum<LR>(acc[r]);
+        // Every lane of a unit holds its sums and every lane stores (same-address
+        // writes of a wave coalesce).
+        const int unit = unit_of(gi);
         if constexpr (PAIR) {
             const float gv = round_to<T>(acc[0]), up = round_to<T>(acc[1]);
             const float sig = round_to<T>(1.0f / (1.0f + __expf(-gv)));
-            Y[gi] = from_f32<T>(round_to<T>(gv * sig) * up);
+            Y[unit] = from_f32<T>(round_to<T>(gv * sig) * up);
             return;
         }
-        const int r = lane % R;
+        const int r = li % R;
         float v = acc[0];
 #pragma unroll
         for (int i = 1; i < R; ++i)
             if (r == i) v = acc[i];
-        Y[min(gi * R + r, N - 1)] = from_f32<T>(v);
+        Y[min(unit * R + r, N - 1)] = from_f32<T>(v);
     };
 
     for (int gi = g0; gi < ngroups; gi += D * waves_total) {
@@ -519,13 +530,13 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
 
 // Launch of one kernel instance: `grid` workgroups of 4 waves.
 template <typename T, int BS, int CPL, int R, int D, bool PRO, bool PAIR, bool SV, bool H2,
-          bool NT = true, bool MRG = false>
+          bool NT = true, bool MRG = false, int RW = 1>
 static int launch_gemv4_inst(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
                              int N, int K, int nb, const GemvPrologue<T>& pro, long grid,
                              hipStream_t st) {
     size_t lds = gemv_stage_bytes<T, H2>(nb * BS);
     if constexpr (MRG) lds += gemv_merge_bytes(K, pro.hd, pro.splits);
-    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, D, PRO, PAIR, SV, H2, NT, MRG>),
+    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, D, PRO, PAIR, SV, H2, NT, MRG, RW>),
                        dim3((unsigned)grid), dim3(256), lds, st, A, B, S, Z, Y, N, K, nb, pro);
     return check_launch("mnb_gemv4");
 }
@@ -581,6 +592,24 @@ static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t*
     const int cpl = (C + 63) / 64;
     if ((long)nb * BS > 2048L * (16 / (long)sizeof(T))) return -1;  // activation staging bound
     if ((size_t)N * nb * BS / 2 > 0xFFFFFF00ull) return -1;  // buffer offsets are 32-bit
+    // Long walks over short rows (lm_head: 151936 x 1536): 4 rows per wave, 16
+    // lanes x ceil(C/16) chunks each, so no lane idles on a 48-chunk row; cached
+    // loads, ring of 2, 32 groups (128 rows) per wave: 33.6 us against 39 us with
+    // a row per wave.
+    constexpr int R = PAIR ? 2 : 1;
+    const long units = ((long)N + R - 1) / R;
+    if (units > 80L * device_cu_count() && C <= 48) {
+        constexpr bool H2 = std::is_same<T, half_t>::value;
+        const long grid = ((units + 3) / 4 + 127) / 128;
+        switch ((C + 15) / 16) {
+            case 1: return launch_gemv4_inst<T, BS, 1, R, 2, PRO, PAIR, false, H2, false, MRG, 4>(
+                        A, B, S, Z, Y, N, K, nb, pro, grid, st);
+            case 2: return launch_gemv4_inst<T, BS, 2, R, 2, PRO, PAIR, false, H2, false, MRG, 4>(
+                        A, B, S, Z, Y, N, K, nb, pro, grid, st);
+            default: return launch_gemv4_inst<T, BS, 3, R, 2, PRO, PAIR, false, H2, false, MRG, 4>(
+                        A, B, S, Z, Y, N, K, nb, pro, grid, st);
+        }
+    }
     switch (cpl) {
         case 1: return launch_gemv4_cpl<T, BS, 1, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
         case 2: return launch_gemv4_cpl<T, BS, 2, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);

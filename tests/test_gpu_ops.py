@@ -73,7 +73,8 @@ def _mnb_inputs(rng, M, N, K, block, bits=4, asym=True, zp_all8=False, dtype=np.
 
 @pytest.mark.parametrize("K,N,block,skip,pair", [
     (1536, 2048, 32, False, False), (1536, 1536, 32, True, False), (1536, 17920, 32, True, True),
-    (8960, 1536, 32, True, False), (4096, 512, 128, True, True), (1000, 64, 64, False, True)])
+    (8960, 1536, 32, True, False), (4096, 512, 128, True, True), (1000, 64, 64, False, True),
+    (1536, 24576, 32, True, False), (1536, 45056, 32, False, True)])
 def test_mnb_decode_fused(ortmi, oracle, K, N, block, skip, pair):
     """Norm prologue and SwiGLU-pair epilogue of the decode GEMV against the unfused
     ops of the oracle (norm rounded to fp16, matmul in fp64, SwiGLU op by op)."""
@@ -152,12 +153,14 @@ def test_mnb_gemv_config1_shape(ortmi, oracle):
     assert diff <= 6e-5, diff
 
 
-@pytest.mark.parametrize("K,block", [(1536, 32), (8960, 32), (4096, 64)])
-def test_mnb_gemv_fp16(ortmi, oracle, K, block):
+@pytest.mark.parametrize("K,block,N", [(1536, 32, 300), (8960, 32, 300), (4096, 64, 300),
+                                       (1536, 32, 20700), (520, 32, 21001), (1000, 64, 20481)])
+def test_mnb_gemv_fp16(ortmi, oracle, K, block, N):
+    """Includes long walks over short rows (N beyond 80 rows per CU, K <= 1536),
+    which take four rows per wave, with an odd N and a partial final block."""
     import torch
 
-    rng = np.random.default_rng(K * 3 + block)
-    N = 300
+    rng = np.random.default_rng(K * 3 + block + N)
     A, B, s, zp = _mnb_inputs(rng, 1, N, K, block, dtype=np.float16)
     Y = ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N, block_size=block)
     assert Y.dtype == torch.float16
