@@ -484,6 +484,7 @@ struct PagedKV {
     const int32_t* bt;
     int64_t nblk;
     int blk, maxb, KV;
+    int blk_shift;  // log2(blk) when blk is a power of two, else -1
 };
 
 struct TileDesc {
@@ -721,38 +722,100 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
             qb[s2] = v;
         }
     }
-    float m = -INFINITY, l = 0.f;
+    float m = -INFINITY;
     float16_t oT[DT];
 #pragma unroll
     for (int d = 0; d < DT; ++d)
 #pragma unroll
         for (int e = 0; e < 16; ++e) oT[d][e] = 0.f;
+    // Running softmax sums: every element of lT holds this lane's query's sum.
+    float16_t lT;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) lT[e] = 0.f;
+    half8_t ones;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ones[i] = (half_t)1.f;
 
     constexpr int KPT = kKeyTile * (HD / 8) / 256, VPT = kKeyTile * (VHD / 8) / 256;
     static_assert(KPT >= 1 && VPT >= 1, "block staging");
     uint4 kreg[KPT], vreg[VPT];
-    int kok = 0;
+    int kok = 0, vok = 0;
+    // Paged rows: the block-table entries of keys [k0, min(k1, past)) are staged in
+    // LDS once (power-of-two block sizes), so a row costs an LDS read and a shift.
+    constexpr int kBtLds = 512;
+    __shared__ int s_bt[PAGED ? kBtLds : 1];
+    int lb0 = 0;
+    bool bt_lds = false;
+    if constexpr (PAGED) {
+        const int cend = min(k1, t.past);
+        if (cend > k0 && pk.blk_shift >= 0) {
+            lb0 = k0 >> pk.blk_shift;
+            const int n = ((cend - 1) >> pk.blk_shift) - lb0 + 1;
+            if (n <= kBtLds) {
+                bt_lds = true;
+                for (int i = tid; i < n; i += 256) {
+                    const int lb = lb0 + i;
+                    s_bt[i] = lb < pk.maxb ? pk.bt[(int64_t)t.seq * pk.maxb + lb] : -1;
+                }
+            }
+        }
+        __syncthreads();
+    }
+    // Source row of key j (k0 <= j < k1): always a valid address; `ok` is false
+    // for a row whose block-table entry is out of range (block 0 stands in).
+    auto row_src = [&](int j, bool value, bool& ok) -> const half_t* {
+        if constexpr (!PAGED) {
+            ok = true;
+            const half_t* base = static_cast<const half_t*>(value ? dk.v : dk.k);
+            return base + (((int64_t)t.seq * dk.KV + kvh) * dk.cap + j) * (value ? VHD : HD);
+        } else {
+            if (j >= t.past) {
+                ok = true;
+                const int tok = t.tok_seq0 + (j - t.past);
+                if (value && pk.vnew)
+                    return static_cast<const half_t*>(pk.vnew) + ((int64_t)tok * pk.KV + kvh) * VHD;
+                return static_cast<const half_t*>(pk.knew) + ((int64_t)tok * pk.KV + kvh) * HD;
+            }
+            int phys, within;
+            if (bt_lds) {
+                phys = s_bt[(j >> pk.blk_shift) - lb0];
+                within = j & ((1 << pk.blk_shift) - 1);
+            } else {
+                const int lb = j / pk.blk;
+                phys = lb < pk.maxb ? pk.bt[(int64_t)t.seq * pk.maxb + lb] : -1;
+                within = j - lb * pk.blk;
+            }
+            ok = phys >= 0 && phys < pk.nblk;
+            const int64_t slot = (int64_t)(ok ? phys : 0) * pk.blk + within;
+            if (value && pk.vcache)
+                return static_cast<const half_t*>(pk.vcache) + (slot * pk.KV + kvh) * VHD;
+            return static_cast<const half_t*>(pk.kcache) + (slot * pk.KV + kvh) * HD;
+        }
+    };
+    // Loads are never conditional (a branch around a load makes the compiler drain
+    // every prefetch at the join): rows past the block end load its last row again,
+    // and the validity bits mask keys (sOk) and zero values at commit.
     auto fetch = [&](int kb) {
         const int nk = min(kKeyTile, k1 - kb);
         kok = 0;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int idx = tid + 256 * i, r = idx % kKeyTile, c = (idx / kKeyTile) * 8;
-            const half_t* p =
-                r < nk ? key_ptr<half_t, HD, VHD, PAGED>(dk, pk, t, t.seq, kvh, kb + r, false)
-                       : nullptr;
-            kreg[i] = p ? *reinterpret_cast<const uint4*>(p + c) : make_uint4(0, 0, 0, 0);
-            kok |= (p != nullptr) << i;
+            bool ok;
+            const half_t* p = row_src(kb + min(r, nk - 1), false, ok);
+            kreg[i] = *reinterpret_cast<const uint4*>(p + c);
+            kok |= (int)(ok && r < nk) << i;
         }
         // V: a thread takes VPT consecutive keys of one 8-dim chunk, so the
         // transposed store writes VPT keys of a head dim at once.
+        vok = 0;
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int r = VPT * (tid % (kKeyTile / VPT)) + i, c = (tid / (kKeyTile / VPT)) * 8;
-            const half_t* p =
-                r < nk ? key_ptr<half_t, HD, VHD, PAGED>(dk, pk, t, t.seq, kvh, kb + r, true)
-                       : nullptr;
-            vreg[i] = p ? *reinterpret_cast<const uint4*>(p + c) : make_uint4(0, 0, 0, 0);
+            bool ok;
+            const half_t* p = row_src(kb + min(r, nk - 1), true, ok);
+            vreg[i] = *reinterpret_cast<const uint4*>(p + c);
+            vok |= (int)(ok && r < nk) << i;
         }
     };
     auto commit = [&]() {
@@ -766,6 +829,9 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
         if (tid == 0) sOk = ok;
         {
             const int r0 = VPT * (tid % (kKeyTile / VPT)), c = (tid / (kKeyTile / VPT)) * 8;
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
+                if (!((vok >> i) & 1)) vreg[i] = make_uint4(0, 0, 0, 0);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 half_t col[VPT];
@@ -831,31 +897,31 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
             bmax = fmaxf(pr.a, pr.b);
         }
         const float m_new = fmaxf(m, bmax);
-        const float alpha = (m == -INFINITY) ? 0.f : exp2f(m - m_new);
+        // v_exp_f32 directly: results below 2^-126 flush to zero, which the
+        // softmax weights can afford.
+        const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
         half8_t pb[4];  // P^T operands: k-step kk uses e in [8 (kk % 2), 8 (kk % 2) + 8) of tile kk / 2
-        float lsum = 0.f;
         const float mref = m_new == -INFINITY ? 0.f : m_new;  // exp2(-inf - 0) = 0
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const half_t ph = (half_t)exp2f(st[kt][e] - mref);
-                pb[kt * 2 + e / 8][e % 8] = ph;
-                lsum += (float)ph;
-            }
-        {
-            const LanePair pr = swap32(lsum);
-            lsum = pr.a + pr.b;
-        }
-        l = l * alpha + lsum;
+            for (int e = 0; e < 16; ++e)
+                pb[kt * 2 + e / 8][e % 8] = (half_t)__builtin_amdgcn_exp2f(st[kt][e] - mref);
         m = m_new;
-        // Rescale O only when some query's running max moved.
+        // Rescale O (and the running sums) only when some query's running max moved.
         if (__any(alpha != 1.f)) {
 #pragma unroll
             for (int d = 0; d < DT; ++d)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) oT[d][e] *= alpha;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) lT[e] *= alpha;
         }
+        // Row sums on the matrix cores: a row of ones times P^T sums the same fp16
+        // probabilities that weight V, for every query at once.
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            lT = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pb[kk], lT, 0, 0, 0);
         // O^T += V^T P^T over the 4 k-steps of 16 keys.
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
@@ -879,6 +945,7 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
         __syncthreads();  // the next block overwrites sK, sVt and sOk
     }
     if (!qlive) return;
+    float l = lT[0];
     m = m == -INFINITY ? m : m / kLog2e;  // back to the natural-log domain of the merge
     const int tok = t.tok0 + q / G, h = kvh * G + q % G;
     if (part) {
@@ -1826,15 +1893,16 @@ static int run_paged(const void* query, const void* key, const void* value, void
     // Rows that no tile owns (a malformed cum) keep a split count of 0.
     hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((prow + 255) / 256)), dim3(256), 0, st,
                        nsplit_row, 0, prow);
-    PagedKV pk{kcache, vcache, knew, value, bt, nblk, blk, maxb, KV};
+    int blk_shift = 0;
+    while ((1 << blk_shift) < blk && blk_shift < 30) ++blk_shift;
+    const bool pow2 = (1 << blk_shift) == blk && blk_shift <= 12;
+    PagedKV pk{kcache, vcache, knew, value, bt, nblk, blk, maxb, KV, pow2 ? blk_shift : -1};
     if (!vcache) pk.vnew = nullptr;
     // Single-token tiles go to the vector-unit decode kernel when the block size is a
     // power of two and values have the key's head size.
-    int blk_shift = 0;
-    while ((1 << blk_shift) < blk && blk_shift < 30) ++blk_shift;
     bool dec = false;
     if constexpr (VHD == HD) {
-        dec = vcache && value && (1 << blk_shift) == blk && blk_shift <= 12;
+        dec = vcache && value && pow2;
         auto launch = [&](auto kernel) {
             hipLaunchKernelGGL(kernel, dim3(mt, KV, ns), dim3(256), 0, st, tiles, count, cum, past,
                                pk, blk_shift, qrot, H, sc, sink ? sink32 : nullptr, chunk, ns,
