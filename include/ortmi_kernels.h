@@ -237,6 +237,24 @@ int ortmi_rotary_embedding(const void* x, const int64_t* position_ids, int32_t p
                            int32_t interleaved, int32_t dtype, void* stream);
 
 /*
+ * GatherBlockQuantized (com.microsoft), 4-bit, gather_axis 0, quantize_axis 1:
+ * out[i, k] = (q[row_i, k] - zp[row_i, k / block]) * scales[row_i, k / block],
+ * computed in fp32 and rounded once to dtype. data [rows, D/2] uint8 (two codes
+ * per byte, low nibble first), scales [rows, ceil(D/block)] in dtype (= the
+ * output dtype), zero_points [rows, ceil(ceil(D/block)/2)] packed int4 (low nibble
+ * = even block) or NULL (8). indices [num_indices] int32 or int64 (negative ids
+ * count from the end; ids outside [-rows, rows) give zero rows). output
+ * [num_indices, D]. block_size >= 16.
+ * Replaces: gather_block_quantized_op (rust/src/ops/quant.rs:1134-1199) and the
+ * claim checks of quant.rs:1713-1749.
+ */
+int ortmi_gather_block_quantized(const uint8_t* data, const void* scales,
+                                 const uint8_t* zero_points, const void* indices,
+                                 int32_t indices_are_int64, void* output, int64_t num_indices,
+                                 int64_t rows, int64_t D, int64_t block_size, int64_t bits,
+                                 int32_t dtype, void* stream);
+
+/*
  * SimplifiedLayerNormalization / SkipSimplifiedLayerNormalization
  * (com.microsoft) and RMSNormalization: r = x (+ skip) (+ bias);
  * y = r / sqrt(mean(r^2) + eps) * gamma over the last axis of length D.

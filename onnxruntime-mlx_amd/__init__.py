@@ -81,6 +81,8 @@ SIGNATURES = {
         _i32, _vp, _sz, _vp]),
     "ortmi_rotary_embedding": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _i64,
                                               _i64, _i64, _i64, _i32, _i32, _i32, _vp]),
+    "ortmi_gather_block_quantized": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64,
+                                                    _i64, _i64, _i64, _i32, _vp]),
     "ortmi_rms_norm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _i32, _vp]),
     "ortmi_gather_rows": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
     "ortmi_swiglu": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _vp]),
@@ -108,6 +110,7 @@ def check(rc: int) -> None:
 
 from . import ops  # noqa: E402  (ops needs the loader above)
 from .ops import (  # noqa: E402,F401
+    gather_block_quantized,
     group_query_attention,
     group_query_attention_decode_capturable,
     matmul_nbits,

@@ -421,6 +421,32 @@ std::string claim_gather(const NodeDesc& n, const GraphIR& g) {
     return "";
 }
 
+// rust/src/ops/quant.rs:1713-1749
+std::string claim_gbq(const NodeDesc& n, const GraphIR& g) {
+    REQUIRE(!n.outputs.empty() && !n.outputs[0].empty(), "requires at least one output");
+    auto* out = out_val(g, n, 0);
+    REQUIRE(out, "missing output type/shape info");
+    auto *d = val(g, n, 0), *i = val(g, n, 1), *s = val(g, n, 2);
+    REQUIRE(d && i && s, "missing tensor type/shape info on an input");
+    REQUIRE(d->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_UINT8 &&
+                (i->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT32 ||
+                 i->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64) &&
+                s->dtype == out->dtype && is_float(s->dtype),
+            "data must be uint8, indices int32/int64, and scales/output the same float dtype");
+    if (n.has_input(3)) {
+        auto* zp = val(g, n, 3);
+        REQUIRE(zp && zp->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_UINT8,
+                "zero_points must be uint8 when present");
+    }
+    REQUIRE(n.attr_int("bits", 4) == 4, "only 4-bit data is supported");
+    REQUIRE(n.attr_int("gather_axis", 0) == 0 && n.attr_int("quantize_axis", 1) == 1,
+            "only gather_axis=0 and quantize_axis=1 are supported");
+    REQUIRE(n.attr_int("block_size", 128) >= 16, "block_size must be at least 16");
+    // The kernel's table layout (the reference reads data as [V, D/2] too).
+    REQUIRE(!d->has_shape || d->dims.size() == 2, "data must be rank 2");
+    return "";
+}
+
 struct Entry {
     const char* domain;
     const char* op;
@@ -428,6 +454,7 @@ struct Entry {
 };
 const Entry kRegistry[] = {
     {"com.microsoft", "MatMulNBits", claim_matmulnbits},
+    {"com.microsoft", "GatherBlockQuantized", claim_gbq},
     {"com.microsoft", "GroupQueryAttention", claim_gqa},
     {"com.microsoft", "PagedAttention", claim_paged},
     {"com.microsoft", "RotaryEmbedding", claim_rotary},

@@ -647,6 +647,24 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
                      "Gather");
         return;
     }
+    if (op == "GatherBlockQuantized") {
+        Tensor data = need(0), ids = need(1), sc = need(2);
+        Tensor* zp = in(3);
+        if (data.dims.size() != 2) fail(op + ": data must be rank 2", ORT_INVALID_ARGUMENT);
+        const int64_t V = data.dims[0], D = data.dims[1] * 2;
+        const int64_t block = n.attr_int("block_size", 128);
+        if (sc.numel() != V * ((D + block - 1) / block))
+            fail(op + ": scales must be [V, ceil(D/block_size)]", ORT_INVALID_ARGUMENT);
+        std::vector<int64_t> od = ids.dims;
+        od.push_back(D);
+        Tensor& O = out_tensor(outname(0), sc.dtype, od, a, ctx);
+        check_kernel(ortmi_gather_block_quantized(
+                         (const uint8_t*)data.ptr, sc.ptr, zp ? (const uint8_t*)zp->ptr : nullptr,
+                         ids.ptr, ids.dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64 ? 1 : 0, O.ptr,
+                         ids.numel(), V, D, block, n.attr_int("bits", 4), kdt(sc.dtype), st),
+                     op.c_str());
+        return;
+    }
     fail("no executor for " + op, ORT_NOT_IMPLEMENTED);
 }
 

@@ -1092,3 +1092,93 @@ extern "C" int ortmi_matmul_nbits(const void* A, const uint8_t* B, const void* s
                         "MatMulNBits: activation/scales must be float (fp32/fp16/bf16)");
     }
 }
+
+// --------------------------------------------------- GatherBlockQuantized --
+
+namespace ortmi {
+
+// Rows of an int4 block-quantised table gathered by index: data [V, D/2] (two
+// codes per byte, low nibble first, the MatMulNBits row layout), scales
+// [V, ceil(D/block)], optional packed zero points [V, ceil(nblocks/2)] (low nibble
+// = even block; 8 when absent). out[i, k] = (q - zp) * scale in fp32, rounded
+// once to the output type. One thread per data byte (two codes); an index outside
+// [-V, V) yields a zero row (the host reports no error from device data).
+template <typename T, typename I>
+__global__ void gbq_kernel(const uint8_t* __restrict__ data, const T* __restrict__ scales,
+                           const uint8_t* __restrict__ zp, const I* __restrict__ idx,
+                           T* __restrict__ out, int64_t n_idx, int64_t V, int D, int block) {
+    const int bytes = D / 2;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_idx * bytes) return;
+    const int64_t i = t / bytes;
+    const int j = (int)(t % bytes);
+    int64_t row = (int64_t)idx[i];
+    if (row < 0) row += V;
+    const bool ok = row >= 0 && row < V;
+    const int nb = (D + block - 1) / block;
+    const int zcols = (nb + 1) / 2;
+    float v[2] = {0.f, 0.f};
+    if (ok) {
+        const uint8_t b = data[row * bytes + j];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = 2 * j + h;
+            const int blk = k / block;
+            const float s = to_f32(scales[row * nb + blk]);
+            const int z = zp ? nibble(zp[row * zcols + blk / 2], blk & 1) : 8;
+            v[h] = (float)(nibble(b, h) - z) * s;
+        }
+    }
+    out[i * D + 2 * j] = from_f32<T>(v[0]);
+    out[i * D + 2 * j + 1] = from_f32<T>(v[1]);
+}
+
+template <typename T>
+static int launch_gbq(const uint8_t* data, const void* scales, const uint8_t* zp,
+                      const void* idx, int idx_is_i64, void* out, int64_t n_idx, int64_t V,
+                      int64_t D, int64_t block, hipStream_t st) {
+    const int64_t threads = n_idx * (D / 2);
+    if (threads == 0) return ORTMI_OK;
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    if (idx_is_i64)
+        hipLaunchKernelGGL((gbq_kernel<T, int64_t>), dim3(grid), dim3(256), 0, st, data,
+                           static_cast<const T*>(scales), zp, static_cast<const int64_t*>(idx),
+                           static_cast<T*>(out), n_idx, V, (int)D, (int)block);
+    else
+        hipLaunchKernelGGL((gbq_kernel<T, int32_t>), dim3(grid), dim3(256), 0, st, data,
+                           static_cast<const T*>(scales), zp, static_cast<const int32_t*>(idx),
+                           static_cast<T*>(out), n_idx, V, (int)D, (int)block);
+    return check_launch("gather_block_quantized");
+}
+
+}  // namespace ortmi
+
+extern "C" int ortmi_gather_block_quantized(const uint8_t* data, const void* scales,
+                                            const uint8_t* zero_points, const void* indices,
+                                            int32_t indices_are_int64, void* output,
+                                            int64_t num_indices, int64_t rows, int64_t D,
+                                            int64_t block_size, int64_t bits, int32_t dtype,
+                                            void* stream) {
+    // Claim contract of rust/src/ops/quant.rs:1713-1749: 4-bit codes, gather axis 0,
+    // quantize axis 1, block >= 16; data/zero points uint8, scales = output dtype.
+    ORTMI_REQUIRE(bits == 4, "GatherBlockQuantized: only 4-bit data is supported");
+    ORTMI_REQUIRE(block_size >= 16, "GatherBlockQuantized: block_size must be at least 16");
+    ORTMI_REQUIRE(num_indices >= 0 && rows > 0 && D > 0 && D % 2 == 0 && D < (1LL << 30),
+                  "GatherBlockQuantized: bad shape");
+    ORTMI_REQUIRE(num_indices == 0 || (data && scales && indices && output),
+                  "GatherBlockQuantized: null tensor");
+    hipStream_t st = as_stream(stream);
+    switch (dtype) {
+        case ORTMI_F32:
+            return launch_gbq<float>(data, scales, zero_points, indices, indices_are_int64, output,
+                                     num_indices, rows, D, block_size, st);
+        case ORTMI_F16:
+            return launch_gbq<half_t>(data, scales, zero_points, indices, indices_are_int64,
+                                      output, num_indices, rows, D, block_size, st);
+        case ORTMI_BF16:
+            return launch_gbq<uint16_t>(data, scales, zero_points, indices, indices_are_int64,
+                                        output, num_indices, rows, D, block_size, st);
+        default:
+            return fail(ORTMI_E_INVALID, "GatherBlockQuantized: scales must be fp32, fp16 or bf16");
+    }
+}

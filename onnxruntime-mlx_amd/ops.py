@@ -75,6 +75,39 @@ def matmul_nbits(A, B, scales, zero_points=None, *, K, N, bits=4, block_size=32,
     return Y
 
 
+# --------------------------------------------------------- GatherBlockQuantized
+def gather_block_quantized(data, scales, indices, zero_points=None, *, block_size=128, bits=4,
+                           gather_axis=0, quantize_axis=1, out=None, stream=None):
+    """com.microsoft GatherBlockQuantized: rows of an int4 block-quantised table.
+
+    Follows gather_block_quantized_op (rust/src/ops/quant.rs:1134-1199) and its
+    claim (quant.rs:1713-1749): data uint8 [V, D/2], indices int32/int64, scales
+    [V, ceil(D/block)] in the output dtype, optional uint8 packed zero points; bits
+    4, gather_axis 0, quantize_axis 1, block_size >= 16. Output indices.shape + [D].
+    """
+    if bits != 4 or gather_axis != 0 or quantize_axis != 1 or block_size < 16:
+        raise ValueError("GatherBlockQuantized: bits 4, gather_axis 0, quantize_axis 1, "
+                         "block_size >= 16 only")
+    if data.dtype != torch.uint8 or data.dim() != 2:
+        raise TypeError("GatherBlockQuantized: data must be uint8 [V, D/2]")
+    if indices.dtype not in (torch.int32, torch.int64):
+        raise TypeError("GatherBlockQuantized: indices must be int32 or int64")
+    V, D = data.shape[0], data.shape[1] * 2
+    nb = (D + block_size - 1) // block_size
+    if scales.numel() != V * nb:
+        raise ValueError("GatherBlockQuantized: scales must be [V, ceil(D/block_size)]")
+    if zero_points is not None and (zero_points.dtype != torch.uint8 or
+                                    zero_points.numel() != V * ((nb + 1) // 2)):
+        raise ValueError("GatherBlockQuantized: zero points must be uint8 [V, ceil(nblocks/2)]")
+    n = indices.numel()
+    Y = out if out is not None else torch.empty(tuple(indices.shape) + (D,), dtype=scales.dtype,
+                                                device=data.device)
+    check(load_kernels().ortmi_gather_block_quantized(
+        _p(data), _p(scales), _p(zero_points), _p(indices), int(indices.dtype == torch.int64),
+        _p(Y), n, V, D, block_size, bits, _dt(scales), _stream(stream)))
+    return Y
+
+
 # ------------------------------------------------------------ GroupQueryAttention
 def gqa_contract(total_sequence_length: int, seq_len: int, past_cap: int):
     """(shared, valid_past, present_cap) per rust/src/ops/attention.rs:636-651."""

@@ -141,6 +141,29 @@ def mnb_matmul(A, B, scales, zp, N, K, bits=4, block=32, nthreads=0) -> np.ndarr
     return Y.reshape(tuple(np.shape(A)[:-1]) + (N,))
 
 
+def gather_block_quantized(data, scales, zp, indices, block, out_dtype=np.float32) -> np.ndarray:
+    """GatherBlockQuantized, 4-bit, gather_axis 0, quantize_axis 1
+    (rust/src/ops/quant.rs:1134-1199): rows of the dequantised table
+    (q - zp) * scale (the MatMulNBits byte layout with N = rows, K = D), indexed
+    with negative ids counting from the end; ids outside [-V, V) give zero rows.
+    (q - zp) * scale is formed in fp32 (exact for fp16/bf16 scales), then rounded
+    to out_dtype."""
+    data = np.asarray(data, np.uint8)
+    V, D = data.shape[0], data.shape[1] * 2
+    # Rows are D/2 bytes (no padding to whole blocks, unlike MatMulNBits' B): pad
+    # them to whole blocks for the dequantisation, which then ignores the padding.
+    nb = (D + block - 1) // block
+    padded = np.zeros((V, nb * block // 2), np.uint8)
+    padded[:, :D // 2] = data
+    W = mnb_dequant(padded, np.asarray(scales, np.float32).reshape(-1), zp, V, D, 4, block)
+    idx = np.asarray(indices, np.int64).reshape(-1)
+    rows = np.where(idx < 0, idx + V, idx)
+    ok = (rows >= 0) & (rows < V)
+    out = np.zeros((idx.size, D), np.float64)
+    out[ok] = W[rows[ok]]
+    return out.reshape(tuple(np.shape(indices)) + (D,)).astype(out_dtype)
+
+
 # ------------------------------------------------------------------ RoPE ----
 def rotary(x, rows, cos, sin, interleaved=False, offset=0, round16=False, layout="bsnd",
            num_heads=None):

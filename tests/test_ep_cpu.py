@@ -132,6 +132,40 @@ def test_matmulnbits_bias_input_declined():
     assert not session(g).claimed(0)
 
 
+def gbq_graph(bits=4, block=16, gather_axis=0, quantize_axis=1, sdtype=F16, odtype=F16,
+              idtype=I64, zp=False):
+    g = hx.Graph()
+    g.value("ids", idtype, [1, -1])
+    g.initializer("table", np.zeros((40, 16), np.uint8))  # V=40, D=32
+    g.initializer("scales", np.ones((40, 32 // block if block <= 32 else 1),
+                                    np.float16 if sdtype == F16 else np.float32))
+    inputs = ["table", "ids", "scales"]
+    if zp:
+        g.initializer("zp", np.full((40, 1), 0x88, np.uint8))
+        inputs.append("zp")
+    g.value("emb", odtype, [1, -1, 32])
+    g.node("GatherBlockQuantized", inputs, ["emb"], domain="com.microsoft", bits=bits,
+           block_size=block, gather_axis=gather_axis, quantize_axis=quantize_axis)
+    g.io(["ids"], ["emb"])
+    return g
+
+
+@pytest.mark.parametrize("kw,claimed", [
+    (dict(), True),
+    (dict(idtype=I32, zp=True), True),
+    (dict(block=32, sdtype=F32, odtype=F32), True),
+    (dict(bits=8), False),                 # quant.rs:1736-1739: 4-bit only
+    (dict(gather_axis=1), False),          # quant.rs:1740-1743
+    (dict(quantize_axis=0), False),
+    (dict(block=8), False),                # quant.rs:1744-1747: block >= 16
+    (dict(sdtype=F32, odtype=F16), False), # quant.rs:1723-1730: scales dtype = output dtype
+    (dict(idtype=F32), False),
+])
+def test_gather_block_quantized_claim_predicate(kw, claimed):
+    """Claim contract of gather_block_quantized_claim (rust/src/ops/quant.rs:1713-1749)."""
+    assert session(gbq_graph(**kw)).claimed(0) is claimed
+
+
 def gqa_graph(hd=64, extra=None, inputs_extra=()):
     g = hx.Graph()
     H, KV, cap = 4, 2, 32

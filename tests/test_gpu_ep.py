@@ -63,6 +63,41 @@ def test_ep_matmulnbits_node(ortmi, oracle, hx, M):
     assert_f16_close(host(y).reshape(M, N), exact, extra=extra, what="EP MatMulNBits")
 
 
+@pytest.mark.parametrize("asym", [False, True])
+def test_ep_gather_block_quantized_node(ortmi, oracle, hx, asym):
+    """An int4 embedding (GatherBlockQuantized, block 32, fp16 scales) claimed and
+    run by the EP equals the oracle bit for bit, including a negative id."""
+    import torch
+
+    rng = np.random.default_rng(77 + asym)
+    V, D, block = 1000, 256, 32
+    nb = D // block
+    q = rng.integers(0, 16, size=(V, D), dtype=np.uint8)
+    data = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    sc = (np.abs(rng.standard_normal((V, nb))) * 0.05 + 1e-3).astype(np.float16)
+    zp = oracle.pack_zero_points(rng.integers(0, 16, size=(V, nb), dtype=np.uint8), 4) if asym else None
+    g = hx.Graph()
+    g.value("ids", hx.INT64, [1, -1])
+    g.value("emb", hx.FLOAT16, [1, -1, D])
+    g.initializer("table", data)
+    g.initializer("scales", sc)
+    inputs = ["table", "ids", "scales"]
+    if asym:
+        g.initializer("zp", zp.reshape(V, -1))
+        inputs.append("zp")
+    g.node("GatherBlockQuantized", inputs, ["emb"], domain="com.microsoft", bits=4,
+           block_size=block, gather_axis=0, quantize_axis=1)
+    g.io(["ids"], ["emb"])
+    sess = hx.Session(g)
+    assert sess.partitions() == [[0]]
+    ids = np.array([[3, V - 1, -2, 0, 517]], np.int64)
+    emb = torch.empty((1, ids.shape[1], D), dtype=torch.float16, device="cuda")
+    sess.bind_output("emb", emb)
+    sess.run({"ids": (dev(ids), hx.INT64)})
+    ref = oracle.gather_block_quantized(data, sc.astype(np.float32), zp, ids, block, np.float16)
+    np.testing.assert_array_equal(host(emb), ref.astype(np.float32))
+
+
 def test_ep_output_binding_and_rerun(ortmi, oracle, hx):
     """A bound output receives the result in place; a second run with new input
     values recomputes (nothing is cached between Compute calls)."""

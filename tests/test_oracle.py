@@ -59,6 +59,23 @@ def test_mnb_dequant_known_answer(oracle):
                               expected)
 
 
+def test_gather_block_quantized_known_answer(oracle):
+    """The oracle's GatherBlockQuantized on the reference's known-answer case, bit
+    for bit, plus its index rules: a negative id counts from the end, an id out of
+    range gives a zero row, zero points 8 equal the symmetric form."""
+    qdata, scales, indices, expected = _gbq_fixture()
+    np.testing.assert_array_equal(oracle.gather_block_quantized(qdata, scales, None, indices, 16),
+                                  expected)
+    zp8 = np.full((2, 1), 0x88, np.uint8)
+    np.testing.assert_array_equal(oracle.gather_block_quantized(qdata, scales, zp8, indices, 16),
+                                  expected)
+    got = oracle.gather_block_quantized(qdata, scales, None, np.array([[0, 5], [-1, -3]]), 16)
+    assert got.shape == (2, 2, 32)
+    np.testing.assert_array_equal(got[0, 0], expected[1])  # row 0 is the KAT's second row
+    np.testing.assert_array_equal(got[1, 0], expected[0])  # -1 -> row 1
+    assert not got[0, 1].any() and not got[1, 1].any()     # 5 and -3 are out of range
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("block", [16, 32, 64, 128])
 @pytest.mark.parametrize("asym", [False, True])
