@@ -656,21 +656,29 @@ struct GemmStage {
     uint8_t zhi;     // 1: the block's zero point is the byte's high nibble
 };
 
-template <int BM, int BN, int BS>
-__global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict__ A,
-                                                        const uint8_t* __restrict__ B,
-                                                        const half_t* __restrict__ S,
-                                                        const uint8_t* __restrict__ Z,
-                                                        half_t* __restrict__ Y, int M, int N,
-                                                        int K, int nb, int tiles_m,
-                                                        int tiles_n) {
+// KS = 2 splits the k-steps of a tile between two groups of 4 waves (512 threads,
+// own LDS buffers, common barriers: both halves run the same number of steps),
+// whose accumulators are summed through LDS at the end: 2 waves per SIMD to hide
+// the load latency when the grid has only about one tile per CU.
+template <int BM, int BN, int BS, int KS = 1>
+__global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __restrict__ A,
+                                                             const uint8_t* __restrict__ B,
+                                                             const half_t* __restrict__ S,
+                                                             const uint8_t* __restrict__ Z,
+                                                             half_t* __restrict__ Y, int M,
+                                                             int N, int K, int nb, int tiles_m,
+                                                             int tiles_n) {
     static_assert(BN * 2 == 256, "one 32-code weight chunk per thread per k-step");
+    static_assert(KS == 1 || KS == 2, "k split");
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TM = WM / 32, TN = WN / 32;
     using Stage = GemmStage<BM, BN, BS>;
     constexpr int A_VEC = Stage::A_VEC;
-    __shared__ half_t sA[2][BM * kLdsRow];
-    __shared__ half_t sB[2][BN * kLdsRow];
+    __shared__ half_t sAall[KS][2][BM * kLdsRow];
+    __shared__ half_t sBall[KS][2][BN * kLdsRow];
+    const int half_id = KS == 2 ? (int)(threadIdx.x >> 8) : 0;
+    half_t (&sA)[2][BM * kLdsRow] = sAall[half_id];
+    half_t (&sB)[2][BN * kLdsRow] = sBall[half_id];
 
     // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; give each
     // XCD a contiguous range of tiles (m fastest) so tiles sharing weight columns
@@ -681,10 +689,13 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
     const int tm = tile % tiles_m, tn = tile / tiles_m;
     const int m0 = tm * BM, n0 = tn * BN;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
     const int wm = (wave & 1) * WM, wn = (wave >> 1) * WN;
     const int Kp = nb * BS;
-    const int ksteps = (Kp + kBK - 1) / kBK;
+    const int ksteps_all = (Kp + kBK - 1) / kBK;
+    // This half's k-steps: [kbase, kbase + ksteps); steps past the end read zeros.
+    const int ksteps = (ksteps_all + KS - 1) / KS;
+    const int kbase = half_id * ksteps;
     const int chunks = Kp / 32;
     const size_t row_bytes = (size_t)Kp / 2;
     const int zp_cols = (nb + 1) / 2;
@@ -705,7 +716,8 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
     const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(Z ? Z : B), 0, (int)z_end, kBufferWord3);
 
-    auto gload = [&](Stage& st, int ks) {
+    auto gload = [&](Stage& st, int ks_local) {
+        const int ks = kbase + ks_local;
         const int k0 = ks * kBK;
 #pragma unroll
         for (int p = 0; p < A_VEC; ++p) {
@@ -803,6 +815,30 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
         __syncthreads();
     }
 
+    if constexpr (KS == 2) {
+        // Half 1 hands its accumulators to half 0 through LDS (the loop ended on a
+        // barrier, so the tile buffers are free).
+        float* xch = reinterpret_cast<float*>(&sBall[0][0][0]);
+        static_assert(4 * TM * TN * 16 * 64 * sizeof(float) <= sizeof(sBall), "exchange space");
+        if (half_id == 1) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        xch[((wave * TM * TN + i * TN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+        }
+        __syncthreads();
+        if (half_id == 1) return;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    acc[i][j][e] += xch[((wave * TM * TN + i * TN + j) * 16 + e) * 64 + lane];
+    }
     // D layout of a 32x32 MFMA: lane holds column (lane & 31); accumulator e holds
     // row 8*(e/4) + 4*(lane/32) + (e%4).
 #pragma unroll
@@ -818,21 +854,24 @@ __global__ __launch_bounds__(256) void mnb_gemm4_kernel(const half_t* __restrict
         }
 }
 
-template <int BM, int BN, int BS>
+template <int BM, int BN, int BS, int KS = 1>
 static int launch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, const uint8_t* Z,
                         half_t* Y, int M, int N, int K, int nb, hipStream_t st) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    hipLaunchKernelGGL((mnb_gemm4_kernel<BM, BN, BS>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
-                       A, B, S, Z, Y, M, N, K, nb, tiles_m, tiles_n);
+    hipLaunchKernelGGL((mnb_gemm4_kernel<BM, BN, BS, KS>), dim3(tiles_m * tiles_n),
+                       dim3(256 * KS), 0, st, A, B, S, Z, Y, M, N, K, nb, tiles_m, tiles_n);
     return check_launch("mnb_gemm4");
 }
 
 template <int BS>
 static int dispatch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, const uint8_t* Z,
                           half_t* Y, int M, int N, int K, int nb, hipStream_t st) {
+    // 128x128 tiles once they fill the CUs twice over; below that, 64x128 tiles with
+    // the k-steps split over two wave groups (M=512: K=N=4096 47.9 -> 42.6 us,
+    // N=1536 K=8960 92 -> 73 us on MI355X).
     const long big = (long)((M + 127) / 128) * ((N + 127) / 128);
     if (big >= 2L * device_cu_count()) return launch_gemm4<128, 128, BS>(A, B, S, Z, Y, M, N, K, nb, st);
-    return launch_gemm4<64, 128, BS>(A, B, S, Z, Y, M, N, K, nb, st);
+    return launch_gemm4<64, 128, BS, 2>(A, B, S, Z, Y, M, N, K, nb, st);
 }
 
 // ----------------------------------------------------------------- generic --
