@@ -1447,12 +1447,14 @@ __global__ __launch_bounds__(256) void rotary_kernel(const T* __restrict__ x,
 static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 static int gqa_nsplit(int64_t BKV, int64_t nkeys, int& chunk) {
-    // Aim for >= 2048 workgroups; chunk a multiple of 64 keys, at most 1024.
-    int64_t want = (2048 + BKV - 1) / BKV;
+    // One round of two workgroups per CU (the decode kernel's occupancy): longer
+    // splits amortise the epilogue and the merge, and a second round would run
+    // with a partial tail (B=8 KV=8 ctx 4097 on MI355X: 512 workgroups 66.5 us,
+    // 1408 workgroups 73 us). Chunks are multiples of 64 keys.
+    const int64_t want = std::max<int64_t>(1, 2L * device_cu_count() / BKV);
     int64_t c = (nkeys + want - 1) / want;
     c = ((c + 63) / 64) * 64;
     if (c < 64) c = 64;
-    if (c > 1024) c = 1024;
     // The merge kernel weighs at most 1024 splits.
     const int64_t cmin = ((nkeys + 1023) / 1024 + 63) / 64 * 64;
     if (c < cmin) c = cmin;
@@ -1508,7 +1510,9 @@ static int launch_gqa_decode(int G, int B, int KV, int ns, int chunk, const T* q
                              T* out, const int* total_dev, int vp_max, hipStream_t st) {
     // One head per workgroup measured best at 20 workgroups (6 heads per KV head,
     // 640-row buffer): 7.3 us with the merge against 8.5 / 9.7 / 12.8 us for 2 / 3 / 6.
-    const int per = (int64_t)B * KV * ns < 2L * device_cu_count() ? 1 : G;
+    // Spreading multiplies the K/V reads by G, so it is only taken when even the
+    // spread grid fits one round.
+    const int per = (int64_t)B * KV * ns * G <= 2L * device_cu_count() ? 1 : G;
     const int gsplit = G / per;
     dim3 grid((unsigned)(B * KV * gsplit), (unsigned)ns);
     auto launch = [&](auto gtag) {
