@@ -594,13 +594,13 @@ static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t*
     if ((size_t)N * nb * BS / 2 > 0xFFFFFF00ull) return -1;  // buffer offsets are 32-bit
     // Long walks over short rows (lm_head: 151936 x 1536): 4 rows per wave, 16
     // lanes x ceil(C/16) chunks each, so no lane idles on a 48-chunk row; cached
-    // loads, ring of 2, 32 groups (128 rows) per wave: 33.6 us against 39 us with
+    // loads, ring of 2, 8 groups (32 rows) per wave: 33.6 us against 39 us with
     // a row per wave.
     constexpr int R = PAIR ? 2 : 1;
     const long units = ((long)N + R - 1) / R;
     if (units > 80L * device_cu_count() && C <= 48) {
         constexpr bool H2 = std::is_same<T, half_t>::value;
-        const long grid = ((units + 3) / 4 + 127) / 128;
+        const long grid = (units + 127) / 128;  // 4 waves x 32 rows per workgroup
         switch ((C + 15) / 16) {
             case 1: return launch_gemv4_inst<T, BS, 1, R, 2, PRO, PAIR, false, H2, false, MRG, 4>(
                         A, B, S, Z, Y, N, K, nb, pro, grid, st);
