@@ -1036,18 +1036,24 @@ extern "C" int ortmi_matmul_nbits_decode_fused(const void* x, const void* skip, 
     ORTMI_REQUIRE(nb * block_size <= std::min<int64_t>(limit, 10240),
                   "MatMulNBits fused: K too large for the decode kernel");
     hipStream_t st = as_stream(stream);
+    int rc;
     switch (dtype) {
         case ORTMI_F16:
-            return dispatch_fused_gemv<half_t>(x, skip, gamma, epsilon, residual, B, scales,
+            rc = dispatch_fused_gemv<half_t>(x, skip, gamma, epsilon, residual, B, scales,
+                                             zero_points, Y, (int)N, (int)K, (int)block_size, norm,
+                                             pair, st);
+            break;
+        case ORTMI_BF16:
+            rc = dispatch_fused_gemv<uint16_t>(x, skip, gamma, epsilon, residual, B, scales,
                                                zero_points, Y, (int)N, (int)K, (int)block_size,
                                                norm, pair, st);
-        case ORTMI_BF16:
-            return dispatch_fused_gemv<uint16_t>(x, skip, gamma, epsilon, residual, B, scales,
-                                                 zero_points, Y, (int)N, (int)K, (int)block_size,
-                                                 norm, pair, st);
+            break;
         default:
             return fail(ORTMI_E_INVALID, "MatMulNBits fused: fp16 or bf16 activations only");
     }
+    // The launcher declines shapes beyond its staging or 32-bit buffer range.
+    if (rc < 0) return fail(ORTMI_E_INVALID, "MatMulNBits fused: shape has no decode kernel");
+    return rc;
 }
 
 namespace ortmi {
