@@ -708,18 +708,19 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
     // Scores are kept in the log2 domain (exp2 is the hardware exponential).
     constexpr float kLog2e = 1.4426950408889634f;
     const float sc2 = scale * kLog2e;
-    // Q^T operand: 8 consecutive head dims per k-step of this lane's query.
-    half8_t qb[HD / 16];
+    // Q^T operand: the tile's query rows are staged in LDS once (zeros past the
+    // last row) and each k-step reads its 8 head dims from there, which keeps
+    // HD / 2 VGPRs free for the whole key walk.
+    __shared__ half_t sQ[kMfmaRows * KP];
     {
-        const half_t* qr = qlive ? qrot + ((int64_t)(t.tok0 + q / G) * H + kvh * G + q % G) * HD
-                                 : nullptr;
-#pragma unroll
-        for (int s2 = 0; s2 < HD / 16; ++s2) {
-            half8_t v;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = (half_t)0.f;
-            if (qr) v = *reinterpret_cast<const half8_t*>(qr + s2 * 16 + lk);
-            qb[s2] = v;
+        constexpr int CPR = HD / 8;  // 16-byte chunks per row
+        for (int i = tid; i < kMfmaRows * CPR; i += 256) {
+            const int r = i / CPR, c = i % CPR;
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (r < rows)
+                v = *reinterpret_cast<const uint4*>(
+                    qrot + ((int64_t)(t.tok0 + r / G) * H + kvh * G + r % G) * HD + c * 8);
+            *reinterpret_cast<uint4*>(&sQ[r * KP + c * 8]) = v;
         }
     }
     float m = -INFINITY;
@@ -865,7 +866,9 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
             for (int s2 = 0; s2 < HD / 16; ++s2) {
                 const half8_t a =
                     *reinterpret_cast<const half8_t*>(&sK[(kt * 32 + lrow) * KP + s2 * 16 + lk]);
-                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[s2], st[kt], 0, 0, 0);
+                const half8_t b =
+                    *reinterpret_cast<const half8_t*>(&sQ[q * KP + s2 * 16 + lk]);
+                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, st[kt], 0, 0, 0);
             }
         }
         // Mask (only blocks that are not fully visible), scale, block max.
