@@ -126,18 +126,63 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(const uint4* __restrict__ 
 
 // ---------------------------------------------------------- GQA decode --
 
+// cos/sin entries that rotate this lane's 8 dims, as raw storage bits (widened
+// where they are used). Non-interleaved dim d < 2*half uses entry d mod half;
+// an interleaved pair (2p, 2p+1) uses entry p, kept at index 2p - dl. Entries the
+// lane does not use read as zero without a memory access (offset past the row),
+// so the loads are unconditional. `half` == 0 loads nothing.
+struct RopeLane {
+    uint32_t c[8], s[8];
+};
+template <typename T>
+__device__ __forceinline__ uint32_t load_elem_bits(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (sizeof(T) == 4)
+        return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    else
+        return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+template <typename T>
+__device__ __forceinline__ float elem_from_bits(uint32_t v) {
+    if constexpr (std::is_same<T, float>::value)
+        return __uint_as_float(v);
+    else if constexpr (std::is_same<T, half_t>::value)
+        return (float)__builtin_bit_cast(half_t, (uint16_t)v);
+    else
+        return to_f32((uint16_t)v);  // bf16 bits
+}
+template <typename T>
+__device__ __forceinline__ RopeLane rope_fetch(const T* c, const T* s, int half, int dl,
+                                               int interleaved) {
+    const uint32_t bytes = (uint32_t)half * sizeof(T);
+    const __amdgpu_buffer_rsrc_t rc = buffer_rsrc(c, bytes), rs = buffer_rsrc(s, bytes);
+    RopeLane r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int d = dl + i;
+        int p = d < half ? d : d - half;
+        bool use = d < 2 * half;
+        if (interleaved) {
+            p = d / 2;
+            use = (i % 2 == 0) && d + 1 < 2 * half;
+        }
+        const uint32_t off = use ? (uint32_t)p * sizeof(T) : bytes;
+        r.c[i] = load_elem_bits<T>(rc, off);
+        r.s[i] = load_elem_bits<T>(rs, off);
+    }
+    return r;
+}
 // Rotate the 8 dims [dl, dl+8) held by this lane (head vector spread over LPR
-// lanes, 8 dims each). Non-interleaved pairs (i, i+half) live `half/8` lanes apart
-// and are exchanged with a shuffle; interleaved pairs sit inside the lane.
+// lanes, 8 dims each) with table entries from rope_fetch. Non-interleaved pairs
+// (i, i+half) live `half/8` lanes apart and are exchanged with a shuffle;
+// interleaved pairs sit inside the lane.
 template <typename T, int LPR>
-__device__ __forceinline__ void rope_lane8(float (&x)[8], int dl, const T* __restrict__ c,
-                                           const T* __restrict__ s, int half, int interleaved) {
+__device__ __forceinline__ void rope_apply(float (&x)[8], int dl, const RopeLane& r, int half,
+                                           int interleaved) {
     if (interleaved) {
 #pragma unroll
         for (int i = 0; i < 8; i += 2) {
-            const int p = (dl + i) / 2;
             if (dl + i + 1 < 2 * half) {
-                const float cs = to_f32(c[p]), sn = to_f32(s[p]);
+                const float cs = elem_from_bits<T>(r.c[i]), sn = elem_from_bits<T>(r.s[i]);
                 const float a = x[i], b = x[i + 1];
                 x[i] = a * cs - b * sn;
                 x[i + 1] = b * cs + a * sn;
@@ -145,13 +190,12 @@ __device__ __forceinline__ void rope_lane8(float (&x)[8], int dl, const T* __res
         }
         return;
     }
-    const int off = half / 8;  // lane distance between partners
+    const int off = half / 8;
     const int lane = threadIdx.x & 63;
     float partner[8];
     const bool lowhalf = dl < half;
     const int src = lowhalf ? lane + off : lane - off;
     if (LPR == 16 && off == 8) {
-        // Full rotary over 128 dims: the partner is lane ^ 8 inside a 16-lane row.
 #pragma unroll
         for (int i = 0; i < 8; ++i) partner[i] = dpp_mov<0x128>(x[i]);  // row_ror:8
     } else {
@@ -161,8 +205,7 @@ __device__ __forceinline__ void rope_lane8(float (&x)[8], int dl, const T* __res
     if (dl < 2 * half) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int p = lowhalf ? dl + i : dl + i - half;
-            const float cs = to_f32(c[p]), sn = to_f32(s[p]);
+            const float cs = elem_from_bits<T>(r.c[i]), sn = elem_from_bits<T>(r.s[i]);
             x[i] = lowhalf ? x[i] * cs - partner[i] * sn : x[i] * cs + partner[i] * sn;
         }
     }
@@ -264,7 +307,22 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     const T* vbase = copy_past ? vpast + (int64_t)bk * past_cap * HD : vw;
     const int64_t src_rows = copy_past ? past_cap : pres_cap;
 
-    // 1. Loads independent of the past length.
+    // Every global access below is unconditional (a branch around a load makes the
+    // compiler wait for every load in flight where the paths join, which would
+    // drain the block prefetch). Rows of this (b, kv) slice go through raw buffer
+    // accesses: a row outside the split, or a store that must not happen, gets an
+    // offset past the slice and touches no memory.
+    const uint32_t row_bytes = HD * sizeof(T);
+    const uint32_t src_end = (uint32_t)src_rows * row_bytes;
+    const uint32_t pres_end = (uint32_t)pres_cap * row_bytes;
+    const __amdgpu_buffer_rsrc_t rsk = buffer_rsrc(kbase, src_end);
+    const __amdgpu_buffer_rsrc_t rsv = buffer_rsrc(vbase, src_end);
+    const __amdgpu_buffer_rsrc_t rdk = buffer_rsrc(kw, pres_end);
+    const __amdgpu_buffer_rsrc_t rdv = buffer_rsrc(vw, pres_end);
+    const uint32_t lane_off = (uint32_t)(dl * sizeof(T));
+
+    // 1. Loads independent of the past length, then the first block of rows.
+    // (A scalar load: its wait does not count vector memory operations.)
     int tv = 0;
     if (total_dev) tv = total_dev[0];
     uint4 qraw[G];
@@ -276,39 +334,51 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
                                                        (int64_t)kvh * HD + dl);
     const uint4 vraw = *reinterpret_cast<const uint4*>(vnew + (int64_t)b * kv_stride +
                                                        (int64_t)kvh * HD + dl);
-    uint4 kr[U], vr[U];
-    auto load_block = [&](uint4 (&kk)[U], uint4 (&vv)[U], int base) {
+    // Rows [base, base + BLK) below `lim`; rows at or past src_rows fall outside
+    // the slice and read zeros.
+    auto load_block = [&](u32x4_t (&kk)[U], u32x4_t (&vv)[U], int base, int lim) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = base + u * RPS + wave * RPW + sub;
-            if (j < src_rows && j < j0 + chunk) {
-                kk[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)j * HD + dl);
-                vv[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)j * HD + dl);
-            } else {
-                kk[u] = make_uint4(0, 0, 0, 0);
-                vv[u] = make_uint4(0, 0, 0, 0);
-            }
+            const uint32_t off =
+                j < lim && j < src_rows ? (uint32_t)j * row_bytes + lane_off : src_end;
+            kk[u] = __builtin_amdgcn_raw_buffer_load_b128(rsk, off, 0, 0);
+            vv[u] = __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0);
         }
     };
-    load_block(kr, vr, j0);
+    // Three register sets in rotation. A set is reloaded only after another
+    // block's loads were issued behind its copy stores, so waiting for those
+    // stores (the counter retires in order) never waits for a block still ahead.
+    u32x4_t ka[U], va[U], kb[U], vb[U], kc[U], vc[U];
+    load_block(ka, va, j0, j0 + chunk);
 
-    // 2. Past length, then RoPE of the queries and of the new key.
+    // 2. Past length, the rotary table entries, the second block.
     if (total_dev) vp = min(max(tv - 1, 0), vp_max);
     const int nkeys = vp + 1;
     const int j1 = min(nkeys, j0 + chunk);
-    const T* cr = cos_c ? cos_c + (int64_t)vp * half : nullptr;
-    const T* sr = sin_c ? sin_c + (int64_t)vp * half : nullptr;
+    const bool rot = cos_c != nullptr;
+    const RopeLane rl = rope_fetch<T>(rot ? cos_c + (int64_t)vp * half : q,
+                                      rot ? sin_c + (int64_t)vp * half : q, rot ? half : 0, dl,
+                                      interleaved);
+    load_block(kb, vb, j0 + BLK, j1);
+
+    // 3. RoPE of the queries and of the new key. Scores are kept as raw dot
+    // products of the rounded query with the keys; the softmax scale (and log2 e,
+    // for the hardware exp2) is applied inside the exponent.
+    constexpr bool kDot2 = std::is_same<T, half_t>::value;
     float qf[G][8];
+    half2_t q2[G][4];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const T* rv = reinterpret_cast<const T*>(&qraw[g]);
 #pragma unroll
         for (int i = 0; i < 8; ++i) qf[g][i] = to_f32(rv[i]);
-        if (cr) rope_lane8<T, LPR>(qf[g], dl, cr, sr, half, interleaved);
+        if (rot) rope_apply<T, LPR>(qf[g], dl, rl, half, interleaved);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) qf[g][i] = round_to<T>(qf[g][i]) * scale;
+        for (int i = 0; i < 8; ++i) qf[g][i] = round_to<T>(qf[g][i]);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) q2[g][p] = half2_t{(half_t)qf[g][2 * p], (half_t)qf[g][2 * p + 1]};
     }
-    const bool own_new = vp >= j0 && vp < j1;
     float knf[8], vnf[8];
     {
         const T* rk = reinterpret_cast<const T*>(&kraw);
@@ -318,18 +388,37 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
             knf[i] = to_f32(rk[i]);
             vnf[i] = to_f32(rvv[i]);
         }
-        if (cr) rope_lane8<T, LPR>(knf, dl, cr, sr, half, interleaved);
-        T outk[8];
+        if (rot) rope_apply<T, LPR>(knf, dl, rl, half, interleaved);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            outk[i] = from_f32<T>(knf[i]);
-            knf[i] = to_f32(outk[i]);  // the stored (rounded) key is what gets attended
-        }
-        if (own_new && hgrp == 0 && wave == 0 && sub == 0) {
-            *reinterpret_cast<uint4*>(kw + (int64_t)vp * HD + dl) = *reinterpret_cast<uint4*>(outk);
-            *reinterpret_cast<uint4*>(vw + (int64_t)vp * HD + dl) = vraw;
-        }
+        for (int i = 0; i < 8; ++i)
+            knf[i] = round_to<T>(knf[i]);  // the stored (rounded) key is what gets attended
     }
+    // The new key's storage bits (stored to row vp and attended like a cache row).
+    u32x4_t knb;
+    {
+        T kt[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kt[i] = from_f32<T>(knf[i]);
+        __builtin_memcpy(&knb, kt, sizeof(knb));
+    }
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float c2 = scale * kLog2e;
+    // Partial dot product of a head's query with 8 dims of a key (this lane's).
+    auto qk = [&](int g, const u32x4_t& kv) -> float {
+        float d = 0.f;
+        if constexpr (kDot2) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t w = kv[p];  // (a bit_cast of kv[p] itself reads element 0)
+                d = __builtin_amdgcn_fdot2(q2[g][p], __builtin_bit_cast(half2_t, w), d, false);
+            }
+        } else {
+            const T* kt = reinterpret_cast<const T*>(&kv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], to_f32(kt[i]), d);
+        }
+        return d;
+    };
 
     float m[G], l[G], o[G][8];
 #pragma unroll
@@ -339,38 +428,18 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
     }
-    auto process = [&](const uint4 (&kk)[U], const uint4 (&vv)[U], int base) {
-        float sc[U][G];
-        float bmax[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) bmax[g] = -INFINITY;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int j = base + u * RPS + wave * RPW + sub;
-            if (copy_past && hgrp == 0 && j < vp && j < j1) {
-                *reinterpret_cast<uint4*>(kw + (int64_t)j * HD + dl) = kk[u];
-                *reinterpret_cast<uint4*>(vw + (int64_t)j * HD + dl) = vv[u];
-            }
-            const T* kv = reinterpret_cast<const T*>(&kk[u]);
-            const bool fresh = j == vp;
-            float kf[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) kf[i] = fresh ? knf[i] : to_f32(kv[i]);
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float d = 0.f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) d = fmaf(qf[g][i], kf[i], d);
-                d = group_sum<LPR>(d);
-                sc[u][g] = j < j1 ? d : -INFINITY;
-                bmax[g] = fmaxf(bmax[g], sc[u][g]);
-            }
-        }
+    // Online-softmax update with a block's raw scores (masked rows at -inf);
+    // `vrow(u, i)` gives the value of row u, dim i.
+    auto absorb = [&](float (&sc)[U][G], auto vrow) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float mn = fmaxf(m[g], bmax[g]);
-            if (mn == -INFINITY) continue;
-            const float alpha = __expf(m[g] - mn);  // m = -inf gives 0
+            float bmax = sc[0][g];
+#pragma unroll
+            for (int u = 1; u < U; ++u) bmax = fmaxf(bmax, sc[u][g]);
+            const float mn = fmaxf(m[g], bmax);
+            // m = -inf (nothing seen yet) gives alpha 0; mn = -inf keeps everything 0.
+            const float alpha =
+                m[g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m[g] - mn) * c2);
             l[g] *= alpha;
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[g][i] *= alpha;
@@ -378,29 +447,79 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int j = base + u * RPS + wave * RPW + sub;
-            const T* vv8 = reinterpret_cast<const T*>(&vv[u]);
             float vf[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) vf[i] = j == vp ? vnf[i] : to_f32(vv8[i]);
+            for (int i = 0; i < 8; ++i) vf[i] = vrow(u, i);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float p = sc[u][g] == -INFINITY ? 0.f : __expf(sc[u][g] - m[g]);
+                const float p = sc[u][g] == -INFINITY
+                                    ? 0.f
+                                    : __builtin_amdgcn_exp2f(fmaf(sc[u][g], c2, -m[g] * c2));
                 l[g] += p;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i]);
             }
         }
     };
-    // 3. Blocks, software-pipelined.
-    for (int base = j0; base < j1; base += 2 * BLK) {
-        uint4 kn[U], vn[U];
-        const bool more = base + BLK < j1;
-        if (more) load_block(kn, vn, base + BLK);
-        process(kr, vr, base);
-        if (!more) break;
-        if (base + 2 * BLK < j1) load_block(kr, vr, base + 2 * BLK);
-        process(kn, vn, base + BLK);
+    // Rows of the walk: [j0, jw); the new row vp (if this split owns it) is
+    // attended separately from registers.
+    const bool own_new = vp >= j0 && vp < j1;
+    const int jw = own_new ? vp : j1;
+    const bool copier = copy_past && hgrp == 0;
+    auto process = [&](const u32x4_t (&kk)[U], const u32x4_t (&vv)[U], int base) {
+        float sc[U][G];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = base + u * RPS + wave * RPW + sub;
+            // Past rows below vp are copied into the present buffer.
+            const uint32_t coff =
+                copier && j < jw ? (uint32_t)j * row_bytes + lane_off : pres_end;
+            __builtin_amdgcn_raw_buffer_store_b128(kk[u], rdk, coff, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(vv[u], rdv, coff, 0, 0);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float d = group_sum<LPR>(qk(g, kk[u]));
+                sc[u][g] = j < jw ? d : -INFINITY;
+            }
+        }
+        absorb(sc, [&](int u, int i) { return to_f32(reinterpret_cast<const T*>(&vv[u])[i]); });
+    };
+    // 4. Blocks, two ahead of the one being processed. Loads past j1 touch no memory.
+    for (int base = j0; base < jw; base += 3 * BLK) {
+        process(ka, va, base);
+        load_block(kc, vc, base + 2 * BLK, jw);
+        if (base + BLK >= jw) break;
+        process(kb, vb, base + BLK);
+        load_block(ka, va, base + 3 * BLK, jw);
+        if (base + 2 * BLK >= jw) break;
+        process(kc, vc, base + 2 * BLK);
+        load_block(kb, vb, base + 4 * BLK, jw);
+    }
+    if (own_new) {
+        // One lane group (wave 0, sub-row 0) takes the new row; the others see it
+        // masked, so it is counted once when the groups are merged.
+        float sc[U][G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float d = group_sum<LPR>(qk(g, knb));
+#pragma unroll
+            for (int u = 0; u < U; ++u) sc[u][g] = u == 0 && wave == 0 && sub == 0 ? d : -INFINITY;
+        }
+        absorb(sc, [&](int, int i) { return vnf[i]; });
+    }
+    // Back to natural-log units for the merges (scores times the scale).
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        if (m[g] != -INFINITY) m[g] *= scale;
+    // The new row (RoPE'd key, value) goes to row vp of the present buffer, from
+    // the split that owns it; it is written last so no reload waits on it.
+    {
+        const uint32_t noff = own_new && hgrp == 0 && wave == 0 && sub == 0
+                                  ? (uint32_t)vp * row_bytes + lane_off
+                                  : pres_end;
+        __builtin_amdgcn_raw_buffer_store_b128(knb, rdk, noff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{vraw.x, vraw.y, vraw.z, vraw.w}, rdv,
+                                               noff, 0, 0);
     }
     // out == null: split partials only (even for one split), merged by the consumer.
     decode_merge<HD, G, LPR, NW>(m, l, o, s_m, s_l, s_o, [&](int g, int d, float M, float L, float acc) {
@@ -419,8 +538,12 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 }
 
 // Merge split partials: out[row][d] = sum_i o_i e^{m_i-M} / sum_i l_i e^{m_i-M}.
-// One workgroup per row: split weights are computed once into LDS, then each
-// thread sums its output dims over the splits with independent loads.
+// One workgroup per row. Up to kMergeFast splits with vhd <= 128 (one dim per
+// thread), every value a thread needs is requested in one batch of loads (splits
+// past the count read zeros without an access) and merged in registers. Larger
+// cases compute the split weights once into LDS, then each thread sums its
+// output dims over the splits.
+constexpr int kMergeFast = 16;
 template <typename T>
 __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict__ part,
                                                          T* __restrict__ out, int nsplit,
@@ -438,6 +561,39 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict
     }
     const int ns = min(1024, nsplit_row ? nsplit_row[r] : nsplit);
     const float* p = part + (int64_t)r * nsplit * (vhd + 2);
+    if (ns <= kMergeFast && vhd <= 128) {
+        const uint32_t bytes = (uint32_t)(ns * (vhd + 2)) * 4u;
+        const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(p, bytes);
+        const int d = min((int)threadIdx.x, vhd - 1);
+        float mv[kMergeFast], lv[kMergeFast], ov[kMergeFast];
+#pragma unroll
+        for (int i = 0; i < kMergeFast; ++i) {
+            const uint32_t row = (uint32_t)(i * (vhd + 2)) * 4u;
+            const bool in = i < ns;
+            mv[i] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rp, in ? row + vhd * 4u : bytes, 0, 0));
+            lv[i] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rp, in ? row + vhd * 4u + 4u : bytes, 0, 0));
+            ov[i] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rp, in ? row + d * 4u : bytes, 0, 0));
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kMergeFast; ++i)
+            if (i < ns) M = fmaxf(M, mv[i]);
+        float L = 0.f, acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < kMergeFast; ++i) {
+            const float w = i < ns && mv[i] != -INFINITY ? __expf(mv[i] - M) : 0.f;
+            L = fmaf(w, lv[i], L);
+            acc = fmaf(w, ov[i], acc);
+        }
+        if ((int)threadIdx.x < vhd) {
+            T* o = out + (int64_t)(orow / H) * out_tok_stride + (int64_t)(orow % H) * vhd;
+            o[threadIdx.x] = from_f32<T>(L > 0.f ? acc / L : 0.f);
+        }
+        return;
+    }
     float mx = -INFINITY;
     for (int i = threadIdx.x; i < ns; i += blockDim.x) mx = fmaxf(mx, p[i * (vhd + 2) + vhd]);
     mx = wave_max(mx);
@@ -1517,6 +1673,11 @@ static int launch_gqa_decode(int G, int B, int KV, int ns, int chunk, const T* q
     // 640-row buffer): 7.3 us with the merge against 8.5 / 9.7 / 12.8 us for 2 / 3 / 6.
     // Spreading multiplies the K/V reads by G, so it is only taken when even the
     // spread grid fits one round.
+    // The kernel addresses one (b, kv) slice of a cache with 32-bit byte offsets.
+    const int64_t slice_rows = std::max(copy_past ? past_cap : (int64_t)0, pres_cap);
+    ORTMI_REQUIRE(slice_rows * HD * (int64_t)sizeof(T) < (int64_t)UINT32_MAX,
+                  "GroupQueryAttention decode: one (batch, kv head) slice of the KV cache "
+                  "must be under 4 GiB");
     const int per = (int64_t)B * KV * ns * G <= 2L * device_cu_count() ? 1 : G;
     const int gsplit = G / per;
     dim3 grid((unsigned)(B * KV * gsplit), (unsigned)ns);

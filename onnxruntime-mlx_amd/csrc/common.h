@@ -23,6 +23,18 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 // (fp32 floats, all heads): the GEMV's workgroups stage it in LDS (32 KB).
 constexpr int kDecodeMergeMaxFloats = 8192;
 
+// Buffer resource word 3 for raw (untyped) buffer loads and stores on gfx9-family
+// GPUs. A raw buffer access whose offset is at or past the resource's byte count
+// touches no memory: a load returns zeros and a store is dropped.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of a buffer load that marks it non-temporal.
+constexpr int kCachePolicyNT = 2;
+
+template <typename P>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const P* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<P*>(base), 0, (int)bytes, kBufferWord3);
+}
+
 // ---------------------------------------------------------------- dtype IO --
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(half_t x) { return (float)x; }
@@ -56,11 +68,14 @@ __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x
 // with a lane holding the other part of its group; across rows the gfx950
 // v_permlane16_swap / v_permlane32_swap exchange the halves of 32 / 64 lanes.
 // Every lane of a group ends with the same value (the combining operations are
-// commutative). All lanes of the wave must be active.
+// commutative). All lanes of the wave must be active. The moves are written with
+// a zero "old" value, full row/bank masks and bound_ctrl, which lets the compiler
+// fold each one into its consumer (v_add_f32_dpp, v_max_f32_dpp): one instruction
+// per step. Every pattern used here reads a lane inside the same row.
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
     return __builtin_bit_cast(
-        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 struct LanePair {
     float a, b;

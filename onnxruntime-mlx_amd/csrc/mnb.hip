@@ -143,11 +143,6 @@ struct GemvPrologue {
     int hd = 0;
 };
 
-// Buffer resource word 3 for raw (untyped) buffer loads on gfx9-family GPUs.
-constexpr int kBufferWord3 = 0x00020000;
-// Cache-policy operand of a buffer load that marks it non-temporal.
-constexpr int kCachePolicyNT = 2;
-
 // One scale, or an aligned pair of scales, through a buffer load.
 template <typename T>
 __device__ __forceinline__ T load_scale(__amdgpu_buffer_rsrc_t r, uint32_t off) {
