@@ -27,7 +27,7 @@ constexpr int kDecodeMergeMaxFloats = 8192;
 // GPUs. A raw buffer access whose offset is at or past the resource's byte count
 // touches no memory: a load returns zeros and a store is dropped.
 constexpr int kBufferWord3 = 0x00020000;
-// Cache-policy operand of a buffer load that marks it non-temporal.
+// Cache-policy operand of a buffer load or store that marks it non-temporal.
 constexpr int kCachePolicyNT = 2;
 
 template <typename P>
