@@ -1547,6 +1547,40 @@ __global__ __launch_bounds__(128) void paged_merge_kernel(const float* __restric
     const int ns = min(nsplit, nsplit_row[r]);
     if (ns <= 0) return;
     const float* p = part + r * nsplit * (vhd + 2);
+    if (ns <= kMergeFast && vhd <= 128) {
+        // Every value a thread needs in one batch of loads (splits past the count
+        // read zeros without an access), merged in registers.
+        const uint32_t bytes = (uint32_t)(ns * (vhd + 2)) * 4u;
+        const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(p, bytes);
+        const int d = min((int)threadIdx.x, vhd - 1);
+        float mv[kMergeFast], lv[kMergeFast], ov[kMergeFast];
+#pragma unroll
+        for (int i = 0; i < kMergeFast; ++i) {
+            const uint32_t row = (uint32_t)(i * (vhd + 2)) * 4u;
+            const bool in = i < ns;
+            mv[i] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rp, in ? row + vhd * 4u : bytes, 0, 0));
+            lv[i] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rp, in ? row + vhd * 4u + 4u : bytes, 0, 0));
+            ov[i] = __uint_as_float(
+                __builtin_amdgcn_raw_buffer_load_b32(rp, in ? row + d * 4u : bytes, 0, 0));
+        }
+        float M = sink ? sink[h] : -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kMergeFast; ++i)
+            if (i < ns) M = fmaxf(M, mv[i]);
+        float L = sink && M != -INFINITY ? __expf(sink[h] - M) : 0.f, acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < kMergeFast; ++i) {
+            const float w = i < ns && mv[i] != -INFINITY ? __expf(mv[i] - M) : 0.f;
+            L = fmaf(w, lv[i], L);
+            acc = fmaf(w, ov[i], acc);
+        }
+        if ((int)threadIdx.x < vhd)
+            out[tok * ((int64_t)H * vhd) + (int64_t)h * vhd + threadIdx.x] =
+                from_f32<T>(L > 0.f ? acc / L : 0.f);
+        return;
+    }
     float M = -INFINITY;
     for (int i = 0; i < ns; ++i) M = fmaxf(M, p[i * (vhd + 2) + vhd]);
     if (sink) M = fmaxf(M, sink[h]);
