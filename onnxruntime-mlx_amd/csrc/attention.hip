@@ -1289,9 +1289,16 @@ __global__ __launch_bounds__(256, 2) void paged_tile_kernel(
     const int32_t* __restrict__ cum, const int32_t* __restrict__ past_lens, PagedKV pk,
     const T* __restrict__ qrot, int G, int H, float scale, const float* __restrict__ sink,
     int chunk, int nsplit, T* __restrict__ out, float* __restrict__ part,
-    int* __restrict__ nsplit_row, int skip_single) {
-    const int ti = blockIdx.x, kvh = blockIdx.y, split = blockIdx.z;
-    if (ti >= *tile_count) return;
+    int* __restrict__ nsplit_row, int skip_single, int mt) {
+    // The tiles of one (kv head, split) group read the same K/V rows. Groups
+    // gi = kvh + KV * split are dealt round-robin to the XCDs, and an XCD runs
+    // all mt tile slots of a group back to back, so those reads meet in its L2.
+    // Dealing by gi % kXcds mixes splits on every XCD (late splits are often
+    // empty). Grid: kXcds * mt * ceil(KV * nsplit / kXcds) workgroups.
+    const int xcd = (int)blockIdx.x % kXcds, slot = (int)blockIdx.x / kXcds;
+    const int gi = xcd + kXcds * (slot / mt), ti = slot % mt;
+    const int kvh = gi % pk.KV, split = gi / pk.KV;
+    if (split >= nsplit || ti >= *tile_count) return;
     const int4 td = tiles[ti];
     if (skip_single && td.z == 1) return;  // paged_decode_kernel's
     TileDesc t;
@@ -2145,9 +2152,10 @@ static int run_paged(const void* query, const void* key, const void* value, void
                 if (int rc = check_launch("paged_decode")) return rc;
         }
     }
-    hipLaunchKernelGGL((paged_tile_kernel<T, HD, VHD>), dim3(mt, KV, ns), dim3(256), 0, st, tiles,
+    const unsigned tile_wgs = (unsigned)(kXcds * (int64_t)mt * ((KV * ns + kXcds - 1) / kXcds));
+    hipLaunchKernelGGL((paged_tile_kernel<T, HD, VHD>), dim3(tile_wgs), dim3(256), 0, st, tiles,
                        count, cum, past, pk, qrot, G, H, sc, sink ? sink32 : nullptr, chunk, ns,
-                       static_cast<T*>(output), part, nsplit_row, dec ? 1 : 0);
+                       static_cast<T*>(output), part, nsplit_row, dec ? 1 : 0, mt);
     if (int rc = check_launch("paged_tile")) return rc;
     if (ns > 1) {
         hipLaunchKernelGGL((paged_merge_kernel<T>), dim3((unsigned)T_, (unsigned)H), dim3(128), 0, st, part,

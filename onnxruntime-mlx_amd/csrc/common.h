@@ -35,6 +35,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const P* base, uin
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<P*>(base), 0, (int)bytes, kBufferWord3);
 }
 
+// MI355X dispatches the workgroups of a 1-D grid round-robin over its 8 XCDs
+// (each with its own L2): workgroup i runs on XCD i % 8 as that XCD's (i / 8)-th.
+constexpr int kXcds = 8;
+
 // ---------------------------------------------------------------- dtype IO --
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(half_t x) { return (float)x; }
