@@ -712,6 +712,9 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
         const_cast<uint8_t*>(Z ? Z : B), 0, (int)z_end, kBufferWord3);
 
     auto gload = [&](Stage& st, int ks_local) {
+        // Steps past this half's range read zeros (they may lie inside the other
+        // half's range).
+        const bool live = ks_local < ksteps;
         const int ks = kbase + ks_local;
         const int k0 = ks * kBK;
 #pragma unroll
@@ -719,15 +722,16 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
             const int idx = tid + p * 256;
             const int r = idx >> 3, c = (idx & 7) * 8;
             const int m = m0 + r, k = k0 + c;
-            const uint32_t off =
-                (m < M && k < K) ? (uint32_t)(((size_t)m * K + k) * sizeof(half_t)) : a_end;
+            const uint32_t off = (live && m < M && k < K)
+                                     ? (uint32_t)(((size_t)m * K + k) * sizeof(half_t))
+                                     : a_end;
             const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
             st.a[p] = make_uint4(v.x, v.y, v.z, v.w);
         }
         const int r = tid >> 1;
         const int chunk = 2 * ks + (tid & 1);
         const int n = n0 + r;
-        const bool ok = n < N && chunk < chunks;
+        const bool ok = live && n < N && chunk < chunks;
         const int blk = (chunk * 32) / BS;
         const uint32_t boff = ok ? (uint32_t)((size_t)n * row_bytes + (size_t)chunk * 16) : b_end;
         const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, boff, 0, 0);
@@ -790,19 +794,21 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
     // Pipeline: loads for step s are issued two steps ahead (register sets r0/r1
     // alternate), stored to the LDS buffer of step s at the end of step s-1.
     // Loads and stores past the last step are issued too (they read zeros and
-    // fill a buffer nobody reads), so the loop has no branch around a load.
+    // fill a buffer nobody reads), so the loop has no branch around a load. The
+    // loop runs an even number of steps (an odd count gets one all-zero step):
+    // a mid-body exit made the compiler copy all accumulators every iteration.
     Stage r0, r1;
     gload(r0, 0);
     gload(r1, 1);
     sstore(r0, 0);
     __syncthreads();
-    for (int ks = 0; ks < ksteps; ks += 2) {
+    const int ksteps2 = (ksteps + 1) & ~1;
+    for (int ks = 0; ks < ksteps2; ks += 2) {
         // even step ks: LDS buf 0 holds it; r1 holds step ks+1.
         gload(r0, ks + 2);
         compute(0);
         sstore(r1, 1);
         __syncthreads();
-        if (ks + 1 >= ksteps) break;
         // odd step ks+1: LDS buf 1; r0 holds step ks+2.
         gload(r1, ks + 3);
         compute(1);

@@ -669,6 +669,24 @@ def test_glue_kernels(ortmi):
                                           ctypes.c_void_p(idx.data_ptr()), 3, 151936, 10, w, wb,
                                           st))
         np.testing.assert_array_equal(host(idx), np.argmax(x.astype(np.float32), axis=1))
+    # the same rows in fp32 take the two-pass form; fp16 rows longer than one
+    # batch of the one-pass form (200000 columns), with NaNs that never win
+    for xs, dt in ((x.astype(np.float32), 1), (None, 10)):
+        if xs is None:
+            xs = rng.standard_normal((2, 200000)).astype(np.float16)
+            xs[0, 199999] = 50.0
+            xs[1, 5] = np.nan
+            xs[1, 199990] = xs[1, 196610] = 60.0
+        r = xs.shape[0]
+        wsz2 = lib.ortmi_argmax_rows_workspace_size(r, xs.shape[1])
+        ws2 = torch.empty(max(wsz2, 1), dtype=torch.uint8, device="cuda")
+        i2 = torch.full((r,), -5, dtype=torch.int64, device="cuda")
+        dxs = dev(xs)
+        ortmi.check(lib.ortmi_argmax_rows(ctypes.c_void_p(dxs.data_ptr()),
+                                          ctypes.c_void_p(i2.data_ptr()), r, xs.shape[1], dt,
+                                          ctypes.c_void_p(ws2.data_ptr()), wsz2, st))
+        expect = np.argmax(np.where(np.isnan(xs), -np.inf, xs.astype(np.float32)), axis=1)
+        np.testing.assert_array_equal(host(i2), expect)
     # gather rows with a negative id
     table = rng.standard_normal((100, 64)).astype(np.float16)
     ids = np.array([3, -1, 50], np.int64)
