@@ -202,6 +202,51 @@ def bench_gqa(torch, ortmi, steps, warmup):
                 launches=n, gbs=total_bytes / (gpu_ms * 1e-3) / 1e9)
 
 
+def bench_gqa_shared(torch, ortmi, steps, warmup):
+    """The same decode step with present bound to past (in-place contract): the
+    4096 cached rows are read, only the new row is written."""
+    import ctypes
+
+    wl = sys.modules["ortmi.workloads"]
+    cfg = wl.gqa_decode_config()
+    B, H, KV, hd, past = 8, 32, 8, 128, 4096
+    cap = past + 1
+    kv_bytes = cfg["pk"].nbytes + cfg["pv"].nbytes
+    copies = max(2, -(-(2 * MALL_BYTES) // kv_bytes))
+    dq, dk, dv = (torch.from_numpy(cfg[x]).cuda() for x in ("q", "k", "v"))
+    dcos, dsin = torch.from_numpy(cfg["cos"]).cuda(), torch.from_numpy(cfg["sin"]).cuda()
+    caches = []
+    for _ in range(copies):
+        kc = torch.empty((B, KV, cap, hd), dtype=torch.float16, device="cuda")
+        vc = torch.empty_like(kc)
+        kc[:, :, :past].copy_(torch.from_numpy(cfg["pk"]))
+        vc[:, :, :past].copy_(torch.from_numpy(cfg["pv"]))
+        caches.append((kc, vc))
+    out = torch.empty((B, 1, H * hd), dtype=torch.float16, device="cuda")
+    lib = ortmi.load_kernels()
+    ws_bytes = lib.ortmi_group_query_attention_workspace_size(B, 1, H, hd, cap)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def launch_batch():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for kc, vc in caches:
+            rc = lib.ortmi_group_query_attention(
+                ptr(dq), ptr(dk), ptr(dv), ptr(kc), ptr(vc), cap, past + 1, ptr(dcos), ptr(dsin),
+                hd // 2, 8192, ptr(out), ptr(kc), ptr(vc), B, 1, H, KV, hd, 0.0, 0, 10, ptr(ws),
+                ws_bytes, st)
+            if rc:
+                raise RuntimeError(lib.ortmi_last_error().decode())
+
+    gpu_ms, wall_ms, n = timed_graph(torch, launch_batch, copies, max(copies, steps // 20),
+                                     max(copies, warmup // 20))
+    small = (B * H * hd * 2) * 2 + (B * KV * hd * 2) * 2 * 2
+    total_bytes = kv_bytes + small
+    return dict(kernels="gqa_decode + attn_merge", contract="shared",
+                bytes_per_call=total_bytes, copies=copies, gpu_ms=gpu_ms, wall_ms=wall_ms,
+                launches=n, gbs=total_bytes / (gpu_ms * 1e-3) / 1e9)
+
+
 def bench_paged(torch, ortmi, steps, warmup):
     wl = sys.modules["ortmi.workloads"]
     cfg = wl.paged_mixed_config()
@@ -359,6 +404,14 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}}
         log(f"gqa: {r['gbs']:.1f} GB/s ({r['gpu_ms'] * 1e3:.2f} us/call)")
+        r = bench_gqa_shared(torch, ortmi, args.steps, args.warmup)
+        secondary["gqa_decode_shared"] = {
+            "config": "B=8 H=32 KV=8 hd=128 past=4096 fp16 rotary, shared (in-place) contract",
+            "gbs": round(r["gbs"], 1), "us_per_call": round(r["gpu_ms"] * 1e3, 2),
+            "bytes_per_call": r["bytes_per_call"],
+            "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}}
+        log(f"gqa shared: {r['gbs']:.1f} GB/s ({r['gpu_ms'] * 1e3:.2f} us/call)")
     if wl in ("all", "paged"):
         r = bench_paged(torch, ortmi, args.steps, args.warmup)
         secondary["paged_attention_mixed"] = {
