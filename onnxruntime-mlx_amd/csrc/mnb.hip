@@ -663,7 +663,9 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
                                                              half_t* __restrict__ Y, int M,
                                                              int N, int K, int nb, int tiles_m,
                                                              int tiles_n) {
-    static_assert(BN * 2 == 256, "one 32-code weight chunk per thread per k-step");
+    // Each k-step stages BN weight rows x 2 chunks of 32 codes: one chunk per thread
+    // (BN = 128) or half a chunk per thread (BN = 64).
+    static_assert(BN == 128 || BN == 64, "weight tile rows");
     static_assert(KS == 1 || KS == 2, "k split");
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -728,14 +730,24 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
             const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
             st.a[p] = make_uint4(v.x, v.y, v.z, v.w);
         }
-        const int r = tid >> 1;
-        const int chunk = 2 * ks + (tid & 1);
+        constexpr int TPR = 256 / BN;  // threads per weight row: 2 (one chunk) or 4 (half)
+        const int r = tid / TPR;
+        const int chunk = 2 * ks + (tid % TPR) * 2 / TPR;
         const int n = n0 + r;
         const bool ok = live && n < N && chunk < chunks;
         const int blk = (chunk * 32) / BS;
-        const uint32_t boff = ok ? (uint32_t)((size_t)n * row_bytes + (size_t)chunk * 16) : b_end;
-        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, boff, 0, 0);
-        st.b = make_uint4(v.x, v.y, v.z, v.w);
+        if constexpr (BN == 128) {
+            const uint32_t boff =
+                ok ? (uint32_t)((size_t)n * row_bytes + (size_t)chunk * 16) : b_end;
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, boff, 0, 0);
+            st.b = make_uint4(v.x, v.y, v.z, v.w);
+        } else {
+            const uint32_t boff =
+                ok ? (uint32_t)((size_t)n * row_bytes + (size_t)chunk * 16 + (tid & 1) * 8)
+                   : b_end;
+            const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rb, boff, 0, 0));
+            st.b = make_uint4(v.x, v.y, 0u, 0u);
+        }
         const uint32_t soff = ok ? (uint32_t)(((size_t)n * nb + blk) * sizeof(half_t)) : s_end;
         st.s = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, soff, 0, 0);  // 0 out of range
         const uint32_t zoff = ok ? (uint32_t)((size_t)n * zp_cols + blk / 2) : z_end;
@@ -749,16 +761,23 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
             const int r = idx >> 3, c = (idx & 7) * 8;
             *reinterpret_cast<uint4*>(&sA[buf][r * kLdsRow + c]) = permute_act8(st.a[p]);
         }
-        const int r = tid >> 1, h = tid & 1;
         const float zf = Z ? (float)nibble(st.z, st.zhi) : 8.f;
         const half_t sh = __builtin_bit_cast(half_t, st.s);
         const half2_t zoff = {(half_t)(1024.f + zf), (half_t)(1024.f + zf)};
         const half2_t s2 = {sh, sh};
-        uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32]);
-        dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
-        dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
-        dst[2] = dequant_word_pairs(st.b.z, zoff, s2);
-        dst[3] = dequant_word_pairs(st.b.w, zoff, s2);
+        if constexpr (BN == 128) {
+            const int r = tid >> 1, h = tid & 1;
+            uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32]);
+            dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
+            dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
+            dst[2] = dequant_word_pairs(st.b.z, zoff, s2);
+            dst[3] = dequant_word_pairs(st.b.w, zoff, s2);
+        } else {
+            const int r = tid >> 2, h = (tid >> 1) & 1, q = tid & 1;
+            uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32 + q * 16]);
+            dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
+            dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
+        }
     };
 
     float16_t acc[TM][TN];
@@ -867,12 +886,17 @@ static int launch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, cons
 template <int BS>
 static int dispatch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, const uint8_t* Z,
                           half_t* Y, int M, int N, int K, int nb, hipStream_t st) {
-    // 128x128 tiles once they fill the CUs twice over; below that, 64x128 tiles with
-    // the k-steps split over two wave groups (M=512: K=N=4096 47.9 -> 42.6 us,
-    // N=1536 K=8960 92 -> 73 us on MI355X).
+    // 128x128 tiles once they fill the CUs twice over; below that, the k-steps are
+    // split over two wave groups, with 64x128 tiles while those still give every
+    // CU a tile and 64x64 tiles under that (M=512 on MI355X: K=N=4096 41.6 us
+    // with 64x128; N=1536 K=8960 66.4 -> 49.7 us, N=2048 K=1536 15.1 -> 11.5 us
+    // with 64x64).
+    const int cus = device_cu_count();
     const long big = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (big >= 2L * device_cu_count()) return launch_gemm4<128, 128, BS>(A, B, S, Z, Y, M, N, K, nb, st);
-    return launch_gemm4<64, 128, BS, 2>(A, B, S, Z, Y, M, N, K, nb, st);
+    if (big >= 2L * cus) return launch_gemm4<128, 128, BS>(A, B, S, Z, Y, M, N, K, nb, st);
+    const long mid = (long)((M + 63) / 64) * ((N + 127) / 128);
+    if (mid >= cus) return launch_gemm4<64, 128, BS, 2>(A, B, S, Z, Y, M, N, K, nb, st);
+    return launch_gemm4<64, 64, BS, 2>(A, B, S, Z, Y, M, N, K, nb, st);
 }
 
 // ----------------------------------------------------------------- generic --
