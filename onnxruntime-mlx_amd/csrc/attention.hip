@@ -545,6 +545,8 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 // cases compute the split weights once into LDS, then each thread sums its
 // output dims over the splits.
 constexpr int kMergeFast = 16;
+// Most key splits of a dense prefill tile (each split writes a partial row).
+constexpr int kPrefillSplits = 4;
 template <typename T>
 __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict__ part,
                                                          T* __restrict__ out, int nsplit,
@@ -1172,10 +1174,12 @@ template <typename T, int HD>
 __global__ __launch_bounds__(256, 2) void gqa_tile_kernel(const T* __restrict__ qrot, DenseKV dk,
                                                        int S, int QT, int tiles_per_seq, int G,
                                                        int H, int vp, float scale,
-                                                       T* __restrict__ out) {
+                                                       T* __restrict__ out, int chunk, int nsplit,
+                                                       float* __restrict__ part,
+                                                       int* __restrict__ nsplit_row) {
     const int b = blockIdx.x / tiles_per_seq;
     const int tile = blockIdx.x % tiles_per_seq;
-    const int kvh = blockIdx.y;
+    const int kvh = blockIdx.y, split = blockIdx.z;
     TileDesc t;
     t.seq = b;
     const int s0 = tile * QT;
@@ -1187,8 +1191,23 @@ __global__ __launch_bounds__(256, 2) void gqa_tile_kernel(const T* __restrict__ 
     t.tok_seq0 = b * S;
     PagedKV none{};
     const int k1 = min(t.nkeys, t.qpos0 + t.ntok);  // causal bound of the tile
-    attn_tile<T, HD, HD, false>(t, kvh, G, H, qrot, dk, none, scale, nullptr, 0, k1, out,
-                                (int64_t)H * HD, nullptr, 1, 0);
+    // Key splits of `chunk` keys (the last takes the rest); rows of a tile that
+    // needs one split are written directly and marked 0 for the merge.
+    const int ns = min(nsplit, max(1, (k1 + chunk - 1) / chunk));
+    if (split == 0 && nsplit > 1) {
+        for (int r = threadIdx.x; r < t.ntok * G; r += blockDim.x)
+            nsplit_row[(int64_t)(t.tok0 + r / G) * H + kvh * G + r % G] = ns > 1 ? ns : 0;
+    }
+    if (split >= ns) return;
+    if (ns == 1) {
+        attn_tile<T, HD, HD, false>(t, kvh, G, H, qrot, dk, none, scale, nullptr, 0, k1, out,
+                                    (int64_t)H * HD, nullptr, 1, 0);
+        return;
+    }
+    const int k0 = split * chunk;
+    const int ks1 = split == ns - 1 ? k1 : min(k1, k0 + chunk);
+    attn_tile<T, HD, HD, false>(t, kvh, G, H, qrot, dk, none, scale, nullptr, k0, ks1, out,
+                                (int64_t)H * HD, part, nsplit, split);
 }
 
 // ------------------------------------------------------- PagedAttention --
@@ -1710,12 +1729,18 @@ using namespace ortmi;
 extern "C" size_t ortmi_group_query_attention_workspace_size(int64_t batch, int64_t seq_len,
                                                              int64_t num_heads, int64_t head_size,
                                                              int64_t total_kv) {
-    // qrot (fp32-sized upper bound) + decode partials.
+    // qrot (fp32-sized upper bound) + decode partials, or the prefill tiles' split
+    // partials and per-row split counts.
     size_t q = align_up((size_t)batch * seq_len * num_heads * head_size * 4);
     // Chunks are at least 64 keys, so ceil(total_kv / 64) bounds the split count.
     const int64_t nkv = total_kv > 0 ? total_kv : 1;
     const int64_t ns = (nkv + 63) / 64;
     size_t part = align_up((size_t)batch * num_heads * (size_t)ns * (head_size + 2) * 4);
+    if (seq_len > 1) {
+        const size_t rows = (size_t)batch * seq_len * num_heads;
+        part = std::max(part, align_up(rows * kPrefillSplits * (head_size + 2) * 4) +
+                                  align_up(rows * 4));
+    }
     return q + part;
 }
 
@@ -1842,9 +1867,35 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
     const int QT = std::max(1, tile_rows_for<T>(HD) / G);
     const int tiles = (S + QT - 1) / QT;
     DenseKV dk{pk, pv, pcap, KV};
-    hipLaunchKernelGGL((gqa_tile_kernel<T, HD>), dim3(B * tiles, KV), dim3(256), 0, st, qrot, dk,
-                       S, QT, tiles, G, H, vp, sc, static_cast<T*>(output));
-    return check_launch("gqa_tile");
+    // Key splits when the tiles alone leave CUs idle (a 512-token decoder prefill
+    // has 50 tiles): about two workgroups per CU, chunks of at least 128 keys, at
+    // most kPrefillSplits; the splits are merged per (token, head) row.
+    int chunk = nkeys, ns = 1;
+    {
+        const int64_t wgs = (int64_t)B * tiles * KV;
+        const int64_t want = std::min<int64_t>(
+            kPrefillSplits, (2LL * device_cu_count() + wgs - 1) / std::max<int64_t>(wgs, 1));
+        if (want > 1) {
+            chunk = (int)std::max<int64_t>(128, ((nkeys + want - 1) / want + 63) / 64 * 64);
+            ns = (nkeys + chunk - 1) / chunk;
+        }
+    }
+    float* ppart = nullptr;
+    int* prow = nullptr;
+    if (ns > 1) {
+        char* base = static_cast<char*>(ws) + align_up((size_t)B * S * H * hd * 4);
+        ppart = reinterpret_cast<float*>(base);
+        prow = reinterpret_cast<int*>(base + align_up((size_t)B * S * H * kPrefillSplits *
+                                                      (hd + 2) * 4));
+    }
+    hipLaunchKernelGGL((gqa_tile_kernel<T, HD>), dim3(B * tiles, KV, ns), dim3(256), 0, st, qrot,
+                       dk, S, QT, tiles, G, H, vp, sc, static_cast<T*>(output), chunk, ns, ppart,
+                       prow);
+    if (int rc = check_launch("gqa_tile")) return rc;
+    if (ns == 1) return ORTMI_OK;
+    hipLaunchKernelGGL((paged_merge_kernel<T>), dim3((unsigned)(B * S), (unsigned)H), dim3(128), 0,
+                       st, ppart, static_cast<T*>(output), ns, prow, hd, H, (const float*)nullptr);
+    return check_launch("gqa_tile_merge");
 }
 
 extern "C" int ortmi_group_query_attention(

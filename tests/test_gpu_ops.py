@@ -452,6 +452,14 @@ def test_gqa_prefill(ortmi, oracle, S, past, cap):
     _run_gqa(ortmi, oracle, B=2, S=S, H=8, KV=2, hd=128, cap=cap, past=past, seed=S + past)
 
 
+@pytest.mark.parametrize("S,past,cap,H", [(200, 150, 400, 8), (512, 0, 512, 12)])
+def test_gqa_prefill_key_splits(ortmi, oracle, S, past, cap, H):
+    """Prompts whose tiles are split over keys (chunks of 128 keys crossing the
+    causal diagonal of several tiles) and merged per (token, head) row."""
+    _run_gqa(ortmi, oracle, B=1 if S == 512 else 2, S=S, H=H, KV=2, hd=128, cap=cap,
+             past=past, inplace=past == 0, seed=S + 7, base=1e6)
+
+
 def test_gqa_prefill_decoder_shape(ortmi, oracle):
     """Prompt of 128 tokens into an empty shared buffer, 12 query / 2 kv heads, base 1e6."""
     _run_gqa(ortmi, oracle, B=1, S=128, H=12, KV=2, hd=128, cap=256, past=0, inplace=True,
