@@ -1467,8 +1467,11 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
                 const int64_t slot = good ? (int64_t)phys * (bmask + 1) + (j & bmask) : 0;
                 const T* kp = cached ? kc + slot * rs : kn + (new0 + j) * rs;
                 const T* vp = cached ? vc + slot * rs : vn + (new0 + j) * rs;
-                kk[u] = *reinterpret_cast<const uint4*>(kp);
-                vv[u] = *reinterpret_cast<const uint4*>(vp);
+                // Streamed once per step: non-temporal.
+                const u32x4_t kq = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(kp));
+                const u32x4_t vq = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(vp));
+                kk[u] = make_uint4(kq.x, kq.y, kq.z, kq.w);
+                vv[u] = make_uint4(vq.x, vq.y, vq.z, vq.w);
                 ok |= (unsigned)good << u;
             }
         };
