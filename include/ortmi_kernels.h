@@ -93,6 +93,22 @@ int ortmi_matmul_nbits_decode_fused(const void* x, const void* skip, const void*
                                     int32_t dtype, void* stream);
 
 /*
+ * MatMulNBits over interleaved gate/up weight rows (row 2i = gate row i, row
+ * 2i+1 = up row i; scales and zero points likewise) with SwiGLU applied in the
+ * GEMM epilogue: Y[m, i] = (g * sigmoid(g)) * u, g and u the fp16 matmul outputs,
+ * each op rounded to fp16 as the unfused ops store it. A [M, K], Y [M, N/2].
+ * fp16 only, 4-bit, block 32/64/128, A and B 16-byte aligned, K % 8 == 0;
+ * anything else returns ORTMI_E_INVALID (the caller runs ortmi_matmul_nbits and
+ * ortmi_swiglu_pairs instead).
+ * Replaces: the gate and up quantized_matmul calls (rust/src/ops/quant.rs:570-601)
+ * and the Sigmoid/Mul/Mul translation (rust/src/ops/elementwise.rs:928-980) at
+ * prompt lengths M > 1.
+ */
+int ortmi_matmul_nbits_swiglu_pairs(const void* A, const uint8_t* B, const void* scales,
+                                    const uint8_t* zero_points, void* Y, int64_t M, int64_t N,
+                                    int64_t K, int64_t block_size, int32_t dtype, void* stream);
+
+/*
  * MatMulNBits decode step (M = 1) whose activation row is the output of the
  * one-token GroupQueryAttention still held as split partials (written by
  * ortmi_group_query_attention_decode_partials): partials [K / head_size heads]

@@ -61,6 +61,8 @@ SIGNATURES = {
                                           _i32, _vp]),
     "ortmi_matmul_nbits_decode_fused": (ctypes.c_int, [
         _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
+    "ortmi_matmul_nbits_swiglu_pairs": (ctypes.c_int, [
+        _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
     "ortmi_matmul_nbits_decode_merge": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
     "ortmi_group_query_attention_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),

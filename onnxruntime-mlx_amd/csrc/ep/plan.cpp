@@ -409,6 +409,14 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
                          "SimplifiedLayerNormalization");
         }
         Tensor& Y = out_tensor(outname(0), dtype, od, a, ctx);
+        if (pair && bits == 4 && M > 1 && dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16) {
+            // Prompt steps: SwiGLU in the GEMM epilogue.
+            const int rc = ortmi_matmul_nbits_swiglu_pairs(ap, (const uint8_t*)B.ptr, S.ptr,
+                                                           (const uint8_t*)zp, Y.ptr, M, N, K, bs,
+                                                           kdt(dtype), st);
+            if (rc == ORTMI_OK) return;
+            if (rc != ORTMI_E_INVALID) check_kernel(rc, op.c_str());
+        }
         void* yp = pair ? arena_alloc((size_t)(M * N) * dtype_size(dtype)) : Y.ptr;
         check_kernel(ortmi_matmul_nbits(ap, (const uint8_t*)B.ptr, S.ptr, (const uint8_t*)zp, yp,
                                         M, N, K, bits, bs, kdt(dtype), st),

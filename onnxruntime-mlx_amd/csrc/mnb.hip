@@ -655,7 +655,7 @@ struct GemmStage {
 // own LDS buffers, common barriers: both halves run the same number of steps),
 // whose accumulators are summed through LDS at the end: 2 waves per SIMD to hide
 // the load latency when the grid has only about one tile per CU.
-template <int BM, int BN, int BS, int KS = 1>
+template <int BM, int BN, int BS, int KS = 1, bool SWI = false>
 __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __restrict__ A,
                                                              const uint8_t* __restrict__ B,
                                                              const half_t* __restrict__ S,
@@ -861,6 +861,30 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
     }
     // D layout of a 32x32 MFMA: lane holds column (lane & 31); accumulator e holds
     // row 8*(e/4) + 4*(lane/32) + (e%4).
+    if constexpr (SWI) {
+        // Interleaved gate/up columns (2i, 2i+1) sit in lanes (2l, 2l+1): the even
+        // lane takes its partner's value and writes column i of the [M, N/2] output,
+        // (g * sigmoid(g)) * u with each op rounded to fp16 as the unfused ops store.
+        const int Nh = N / 2;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = n0 + wn + j * 32 + (lane & 31);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float y = (float)(half_t)acc[i][j][e];
+                    const float partner = dpp_mov<0xB1>(y);  // quad_perm [1,0,3,2]
+                    const int m = m0 + wm + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                    if ((lane & 1) == 0 && m < M && n < N) {
+                        const float sig = (float)(half_t)(1.0f / (1.0f + __expf(-y)));
+                        Y[(size_t)m * Nh + n / 2] =
+                            (half_t)((float)(half_t)(y * sig) * partner);
+                    }
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -874,16 +898,16 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
         }
 }
 
-template <int BM, int BN, int BS, int KS = 1>
+template <int BM, int BN, int BS, int KS = 1, bool SWI = false>
 static int launch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, const uint8_t* Z,
                         half_t* Y, int M, int N, int K, int nb, hipStream_t st) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    hipLaunchKernelGGL((mnb_gemm4_kernel<BM, BN, BS, KS>), dim3(tiles_m * tiles_n),
+    hipLaunchKernelGGL((mnb_gemm4_kernel<BM, BN, BS, KS, SWI>), dim3(tiles_m * tiles_n),
                        dim3(256 * KS), 0, st, A, B, S, Z, Y, M, N, K, nb, tiles_m, tiles_n);
     return check_launch("mnb_gemm4");
 }
 
-template <int BS>
+template <int BS, bool SWI = false>
 static int dispatch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, const uint8_t* Z,
                           half_t* Y, int M, int N, int K, int nb, hipStream_t st) {
     // 128x128 tiles once they fill the CUs twice over; below that, the k-steps are
@@ -893,10 +917,10 @@ static int dispatch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, co
     // with 64x64).
     const int cus = device_cu_count();
     const long big = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (big >= 2L * cus) return launch_gemm4<128, 128, BS>(A, B, S, Z, Y, M, N, K, nb, st);
+    if (big >= 2L * cus) return launch_gemm4<128, 128, BS, 1, SWI>(A, B, S, Z, Y, M, N, K, nb, st);
     const long mid = (long)((M + 63) / 64) * ((N + 127) / 128);
-    if (mid >= cus) return launch_gemm4<64, 128, BS, 2>(A, B, S, Z, Y, M, N, K, nb, st);
-    return launch_gemm4<64, 64, BS, 2>(A, B, S, Z, Y, M, N, K, nb, st);
+    if (mid >= cus) return launch_gemm4<64, 128, BS, 2, SWI>(A, B, S, Z, Y, M, N, K, nb, st);
+    return launch_gemm4<64, 64, BS, 2, SWI>(A, B, S, Z, Y, M, N, K, nb, st);
 }
 
 // ----------------------------------------------------------------- generic --
@@ -1130,6 +1154,36 @@ extern "C" int ortmi_matmul_nbits_decode_merge(const float* partials, int64_t sp
         return fail(ORTMI_E_INVALID, "MatMulNBits merge: fp16 or bf16 activations only");
     if (rc < 0) return fail(ORTMI_E_INVALID, "MatMulNBits merge: shape has no decode kernel");
     return rc;
+}
+
+extern "C" int ortmi_matmul_nbits_swiglu_pairs(const void* A, const uint8_t* B,
+                                               const void* scales, const uint8_t* zero_points,
+                                               void* Y, int64_t M, int64_t N, int64_t K,
+                                               int64_t block_size, int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(M >= 0 && N >= 0 && K > 0 && N % 2 == 0 && M < (1LL << 31) &&
+                      N < (1LL << 31) && K < (1LL << 31),
+                  "MatMulNBits SwiGLU pairs: bad shape (N must be even)");
+    if (M == 0 || N == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(A && B && scales && Y, "MatMulNBits SwiGLU pairs: null tensor");
+    const int nb = (int)((K + block_size - 1) / block_size);
+    const bool ok = dtype == ORTMI_F16 && (block_size == 32 || block_size == 64 ||
+                                           block_size == 128) &&
+                    (reinterpret_cast<uintptr_t>(B) % 16) == 0 &&
+                    (reinterpret_cast<uintptr_t>(A) % 16) == 0 && K % 8 == 0 &&
+                    (size_t)M * K * 2 <= 0xFFFFFF00ull &&
+                    (size_t)N * nb * block_size / 2 <= 0xFFFFFF00ull;
+    if (!ok)
+        return fail(ORTMI_E_INVALID,
+                    "MatMulNBits SwiGLU pairs: needs fp16, 4-bit block 32/64/128, 16-byte "
+                    "aligned A and B, K % 8 == 0");
+    const half_t* a = static_cast<const half_t*>(A);
+    const half_t* s = static_cast<const half_t*>(scales);
+    half_t* y = static_cast<half_t*>(Y);
+    hipStream_t st = as_stream(stream);
+    const int m = (int)M, n = (int)N, k = (int)K;
+    if (block_size == 32) return dispatch_gemm4<32, true>(a, B, s, zero_points, y, m, n, k, nb, st);
+    if (block_size == 64) return dispatch_gemm4<64, true>(a, B, s, zero_points, y, m, n, k, nb, st);
+    return dispatch_gemm4<128, true>(a, B, s, zero_points, y, m, n, k, nb, st);
 }
 
 extern "C" int ortmi_matmul_nbits(const void* A, const uint8_t* B, const void* scales,

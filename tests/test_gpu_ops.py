@@ -198,6 +198,44 @@ def test_mnb_gemm_config2_shape(ortmi, oracle):
     assert_f16_close(got[rows], ref, extra=bound, what="gemm config2")
 
 
+@pytest.mark.parametrize("M,N,K,block", [(37, 400, 1536, 32), (512, 2048, 1536, 32),
+                                         (512, 17920, 1536, 32), (64, 256, 1000, 64)])
+def test_mnb_gemm_swiglu_pairs(ortmi, oracle, M, N, K, block):
+    """SwiGLU in the GEMM epilogue over interleaved gate/up rows equals the GEMM
+    followed by the SwiGLU-pairs kernel bit for bit (the same tile walk), and the
+    oracle's unfused ops (fp16 matmul outputs, SwiGLU op by op) within tolerance.
+    The shapes cover the 64x64, 64x128 and 128x128 tile forms and K % 64 != 0."""
+    import ctypes
+
+    import torch
+
+    rng = np.random.default_rng(M + N + K)
+    A, B, s, zp = _mnb_inputs(rng, M, N, K, block, dtype=np.float16)
+    dA, dB, ds, dz = dev(A), dev(B), dev(s), dev(zp)
+    lib = ortmi.load_kernels()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    y = torch.empty((M, N // 2), dtype=torch.float16, device="cuda")
+    ortmi.check(lib.ortmi_matmul_nbits_swiglu_pairs(p(dA), p(dB), p(ds), p(dz), p(y), M, N, K,
+                                                    block, 10, st))
+    full = ortmi.matmul_nbits(dA, dB, ds, dz, K=K, N=N, block_size=block)
+    y2 = torch.empty((M, N // 2), dtype=torch.float16, device="cuda")
+    ortmi.check(lib.ortmi_swiglu_pairs(p(full), p(y2), M, N // 2, 10, st))
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2), "epilogue SwiGLU differs from the unfused pair"
+    rows = np.arange(0, M, max(1, M // 16))
+    mm = oracle.mnb_matmul(A[rows], B, s, zp, N, K, 4, block)
+    g = oracle.round_f16(mm[:, 0::2])
+    u = oracle.round_f16(mm[:, 1::2])
+    sig = oracle.round_f16(1.0 / (1.0 + np.exp(-g.astype(np.float64))))
+    ref = oracle.round_f16(oracle.round_f16(g * sig) * u)
+    W = refs.dequant_ref(B, s, zp, N, K, 4, block)
+    bound = 2.0 ** -11 * (np.abs(A[rows].astype(np.float64)) @ np.abs(W).T)
+    # a 1-ulp difference in g or u moves the result by about that much times |u| or |g|
+    extra = 4.0 * (bound[:, 0::2] * np.abs(u) + bound[:, 1::2] * np.abs(g) + bound[:, 0::2])
+    assert_f16_close(host(y)[rows], ref, extra=extra, what="gemm swiglu pairs")
+
+
 @pytest.mark.parametrize("M,bits,block", [(1, 8, 32), (3, 8, 64), (1, 4, 16), (5, 4, 16)])
 def test_mnb_generic_forms_fp32(ortmi, oracle, M, bits, block):
     rng = np.random.default_rng(M + bits + block)
