@@ -7,6 +7,62 @@ namespace ortmi {
 // One workgroup per row. r = x (+ skip) (+ bias), rounded to T when a sum was
 // formed (the reference adds in the op dtype, rust/src/ops/norm.rs:237-238);
 // y = r * rsqrt(mean(r^2) + eps) * gamma with one rounding (norm.rs:239).
+// Rows of D <= 2048 2-byte values, D % 8 == 0: each thread owns one 16-byte
+// vector of x (and of skip, bias, gamma), all requested before any is used, so
+// a row costs one memory round trip. Vectors past D, and absent skip / bias, read
+// zeros without an access.
+template <typename T>
+__global__ __launch_bounds__(256) void rms_norm_vec_kernel(const T* __restrict__ x,
+                                                           const T* __restrict__ skip,
+                                                           const T* __restrict__ bias,
+                                                           const T* __restrict__ gamma,
+                                                           T* __restrict__ y, T* __restrict__ res,
+                                                           int64_t D, float eps) {
+    static_assert(sizeof(T) == 2, "2-byte elements");
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const int t = threadIdx.x;
+    const uint32_t bytes = (uint32_t)(D * 2);
+    const uint32_t off = 16u * (uint32_t)t < bytes ? 16u * (uint32_t)t : bytes;
+    const u32x4_t xv = __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(x + row * D, bytes), off, 0, 0);
+    const u32x4_t sv = __builtin_amdgcn_raw_buffer_load_b128(
+        buffer_rsrc(skip ? skip + row * D : x, skip ? bytes : 0u), off, 0, 0);
+    const u32x4_t bv = __builtin_amdgcn_raw_buffer_load_b128(
+        buffer_rsrc(bias ? bias : x, bias ? bytes : 0u), off, 0, 0);
+    const u32x4_t gv = __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(gamma, bytes), off, 0, 0);
+    const bool live = 16u * (uint32_t)t < bytes;
+    const bool summed = skip || bias;
+    const T* xe = reinterpret_cast<const T*>(&xv);
+    const T* se = reinterpret_cast<const T*>(&sv);
+    const T* be = reinterpret_cast<const T*>(&bv);
+    float v[8];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float a = to_f32(xe[i]) + to_f32(se[i]) + to_f32(be[i]);  // absent terms read 0
+        if (summed) a = round_to<T>(a);
+        v[i] = a;
+        ss += a * a;
+    }
+    if (res && live) {
+        T r[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = from_f32<T>(v[i]);
+        *reinterpret_cast<uint4*>(res + row * D + 8 * t) = *reinterpret_cast<const uint4*>(r);
+    }
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const float tot = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / sqrtf(tot / (float)D + eps);
+    if (!live) return;
+    const T* ge = reinterpret_cast<const T*>(&gv);
+    T o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(v[i] * inv * to_f32(ge[i]));
+    *reinterpret_cast<uint4*>(y + row * D + 8 * t) = *reinterpret_cast<const uint4*>(o);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void rms_norm_kernel(const T* __restrict__ x,
                                                        const T* __restrict__ skip,
@@ -307,7 +363,19 @@ extern "C" int ortmi_rms_norm(const void* x, const void* skip, const void* bias,
     ORTMI_REQUIRE(x && gamma && y, "SimplifiedLayerNormalization: null tensor");
     ORTMI_REQUIRE(rows < (1LL << 31), "SimplifiedLayerNormalization: too many rows");
     hipStream_t st = as_stream(stream);
+    const auto a16 = [](const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool vec = D % 8 == 0 && D <= 2048 && a16(x) && a16(skip) && a16(bias) && a16(gamma) &&
+                     a16(y) && a16(residual_out);
 #define ORTMI_RMS(T)                                                                          \
+    if constexpr (sizeof(T) == 2) {                                                           \
+        if (vec) {                                                                            \
+            hipLaunchKernelGGL((rms_norm_vec_kernel<T>), dim3((unsigned)rows), dim3(256), 0, st, \
+                               static_cast<const T*>(x), static_cast<const T*>(skip),         \
+                               static_cast<const T*>(bias), static_cast<const T*>(gamma),     \
+                               static_cast<T*>(y), static_cast<T*>(residual_out), D, eps);    \
+            return check_launch("rms_norm");                                                  \
+        }                                                                                     \
+    }                                                                                         \
     hipLaunchKernelGGL((rms_norm_kernel<T>), dim3((unsigned)rows), dim3(256), D * sizeof(float), \
                        st, static_cast<const T*>(x), static_cast<const T*>(skip),             \
                        static_cast<const T*>(bias), static_cast<const T*>(gamma),             \
