@@ -546,7 +546,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 // output dims over the splits.
 constexpr int kMergeFast = 16;
 // Most key splits of a dense prefill tile (each split writes a partial row).
-constexpr int kPrefillSplits = 4;
+constexpr int kPrefillSplits = 2;
 template <typename T>
 __global__ __launch_bounds__(128) void attn_merge_kernel(const float* __restrict__ part,
                                                          T* __restrict__ out, int nsplit,

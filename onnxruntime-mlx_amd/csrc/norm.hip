@@ -263,71 +263,6 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const ArgPartial* __r
     if (threadIdx.x == 0) out[row] = bi < 0 ? 0 : bi;
 }
 
-// One workgroup of 1024 threads per row of a 2-byte type: each thread requests
-// kWideVec 16-byte vectors (8 values each) before comparing any, so a 152K-column
-// row costs one memory round trip and one launch instead of two passes.
-// First index wins ties; NaN never wins.
-constexpr int kWideVec = 24;
-__device__ __forceinline__ void argmax_pick(float& best, int& bi, float ov, int oi) {
-    if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
-        best = ov;
-        bi = oi;
-    }
-}
-template <typename T>
-__global__ __launch_bounds__(1024) void argmax_wide_kernel(const T* __restrict__ x,
-                                                           int64_t* __restrict__ out,
-                                                           int64_t cols) {
-    static_assert(sizeof(T) == 2, "2-byte elements");
-    __shared__ float sv[16];
-    __shared__ int si[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const T* xr = x + (int64_t)blockIdx.x * cols;
-    const uint32_t bytes = (uint32_t)(cols * sizeof(T));
-    const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(xr, bytes);
-    const int nvec = (int)(cols / 8);
-    float best = -INFINITY;
-    int bi = -1;
-    for (int base = 0; base < nvec; base += 1024 * kWideVec) {
-        u32x4_t v[kWideVec];
-#pragma unroll
-        for (int i = 0; i < kWideVec; ++i) {
-            const int vi = base + tid + 1024 * i;
-            v[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                rx, vi < nvec ? (uint32_t)vi * 16u : bytes, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < kWideVec; ++i) {
-            const int vi = base + tid + 1024 * i;
-            if (vi >= nvec) continue;
-            const T* h = reinterpret_cast<const T*>(&v[i]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float val = to_f32(h[e]);
-                if (val > best || (bi < 0 && val == best)) {
-                    best = val;
-                    bi = vi * 8 + e;
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int w = 1; w < 64; w <<= 1) {
-        const float ov = __shfl_xor(best, w, 64);
-        const int oi = __shfl_xor(bi, w, 64);
-        argmax_pick(best, bi, ov, oi);
-    }
-    if (lane == 0) {
-        sv[wave] = best;
-        si[wave] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < 16; ++w) argmax_pick(best, bi, sv[w], si[w]);
-        out[blockIdx.x] = bi < 0 ? 0 : bi;
-    }
-}
-
 static int argmax_parts(int64_t cols) {
     // About 2048 columns per workgroup, at most 256 partials per row.
     int64_t p = (cols + 2047) / 2048;
@@ -476,17 +411,7 @@ extern "C" int ortmi_argmax_rows(const void* x, int64_t* out, int64_t rows, int6
     const bool split = parts > 1 && workspace &&
                        workspace_bytes >= ortmi_argmax_rows_workspace_size(rows, cols);
     const int64_t slice = (cols + parts - 1) / parts;
-    // Long rows of a 2-byte type, few rows: one 1024-thread workgroup per row.
-    const bool wide = dtype != ORTMI_F32 && parts > 1 && rows <= 256 && cols % 8 == 0 &&
-                      cols * 2 < (int64_t)UINT32_MAX && reinterpret_cast<uintptr_t>(x) % 16 == 0;
 #define ORTMI_ARGMAX(T)                                                                         \
-    if constexpr (sizeof(T) == 2) {                                                             \
-        if (wide) {                                                                             \
-            hipLaunchKernelGGL((argmax_wide_kernel<T>), dim3((unsigned)rows), dim3(1024), 0, st, \
-                               static_cast<const T*>(x), out, cols);                            \
-            return check_launch("argmax_wide");                                                 \
-        }                                                                                       \
-    }                                                                                           \
     if (split) {                                                                                \
         hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3((unsigned)parts, (unsigned)rows),   \
                            dim3(256), 0, st, static_cast<const T*>(x),                          \

@@ -715,8 +715,7 @@ def test_glue_kernels(ortmi):
                                           ctypes.c_void_p(idx.data_ptr()), 3, 151936, 10, w, wb,
                                           st))
         np.testing.assert_array_equal(host(idx), np.argmax(x.astype(np.float32), axis=1))
-    # the same rows in fp32 take the two-pass form; fp16 rows longer than one
-    # batch of the one-pass form (200000 columns), with NaNs that never win
+    # the same rows in fp32, and fp16 rows of 200000 columns with NaNs that never win
     for xs, dt in ((x.astype(np.float32), 1), (None, 10)):
         if xs is None:
             xs = rng.standard_normal((2, 200000)).astype(np.float16)
