@@ -840,15 +840,17 @@ __device__ void attn_tile_body(const TileDesc& t, int kvh, int G, int H, const T
 // fp16 once and the softmax denominator sums the same rounded values.
 // Wave w owns queries 32w..32w+31 of the tile. Key blocks of 64 go global ->
 // registers -> LDS, the next block's loads in flight while the current one is used.
-constexpr int kMfmaRows = 128;
 
-template <int HD, int VHD, bool PAGED>
+template <int HD, int VHD, bool PAGED, int NW = 4>
 __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
                                const half_t* __restrict__ qrot, const DenseKV& dk,
                                const PagedKV& pk, float scale, const float* __restrict__ sink,
                                int k0, int k1, half_t* __restrict__ out, int64_t out_tok_stride,
                                float* __restrict__ part, int nsplit, int split) {
     static_assert(kKeyTile == 64 && HD % 16 == 0 && VHD % 32 == 0, "tile shape");
+    static_assert(NW == 4 || NW == 8, "waves per tile");
+    constexpr int NT = 64 * NW;       // threads
+    constexpr int kRows = 32 * NW;    // query rows of the tile (32 per wave)
     constexpr int KP = HD + 8, VP = kKeyTile + 8;
     constexpr int DT = VHD / 32;          // head-dim tiles of O^T
     __shared__ half_t sK[kKeyTile * KP];
@@ -870,10 +872,10 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
     // Q^T operand: the tile's query rows are staged in LDS once (zeros past the
     // last row) and each k-step reads its 8 head dims from there, which keeps
     // HD / 2 VGPRs free for the whole key walk.
-    __shared__ half_t sQ[kMfmaRows * KP];
+    __shared__ half_t sQ[kRows * KP];
     {
         constexpr int CPR = HD / 8;  // 16-byte chunks per row
-        for (int i = tid; i < kMfmaRows * CPR; i += 256) {
+        for (int i = tid; i < kRows * CPR; i += NT) {
             const int r = i / CPR, c = i % CPR;
             uint4 v = make_uint4(0u, 0u, 0u, 0u);
             if (r < rows)
@@ -896,7 +898,7 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
 #pragma unroll
     for (int i = 0; i < 8; ++i) ones[i] = (half_t)1.f;
 
-    constexpr int KPT = kKeyTile * (HD / 8) / 256, VPT = kKeyTile * (VHD / 8) / 256;
+    constexpr int KPT = kKeyTile * (HD / 8) / NT, VPT = kKeyTile * (VHD / 8) / NT;
     static_assert(KPT >= 1 && VPT >= 1, "block staging");
     uint4 kreg[KPT], vreg[VPT];
     int kok = 0, vok = 0;
@@ -913,7 +915,7 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
             const int n = ((cend - 1) >> pk.blk_shift) - lb0 + 1;
             if (n <= kBtLds) {
                 bt_lds = true;
-                for (int i = tid; i < n; i += 256) {
+                for (int i = tid; i < n; i += NT) {
                     const int lb = lb0 + i;
                     s_bt[i] = lb < pk.maxb ? pk.bt[(int64_t)t.seq * pk.maxb + lb] : -1;
                 }
@@ -960,7 +962,7 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
         kok = 0;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-            const int idx = tid + 256 * i, r = idx % kKeyTile, c = (idx / kKeyTile) * 8;
+            const int idx = tid + NT * i, r = idx % kKeyTile, c = (idx / kKeyTile) * 8;
             bool ok;
             const half_t* p = row_src(kb + min(r, nk - 1), false, ok);
             kreg[i] = *reinterpret_cast<const uint4*>(p + c);
@@ -981,7 +983,7 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
     auto commit = [&]() {
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-            const int idx = tid + 256 * i, r = idx % kKeyTile, c = (idx / kKeyTile) * 8;
+            const int idx = tid + NT * i, r = idx % kKeyTile, c = (idx / kKeyTile) * 8;
             *reinterpret_cast<uint4*>(&sK[r * KP + c]) = kreg[i];
         }
         // Threads 0..63 hold the first vector (c = 0) of keys 0..63: one ballot.
@@ -1143,27 +1145,33 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
         }
 }
 
-// Tile body for a dtype: the matrix-core tile for fp16, the VALU tile otherwise.
-// Query rows per workgroup of the tile body used for dtype T.
+// Tile body for a dtype: the matrix-core tile for fp16 (NW waves of 32 query
+// rows), the VALU tile (kTileRows rows, 256 threads) otherwise.
 template <typename T, int VHD>
-constexpr int tile_rows() {
-    return std::is_same<T, half_t>::value && VHD % 32 == 0 ? kMfmaRows : kTileRows;
+constexpr bool mfma_tile() {
+    return std::is_same<T, half_t>::value && VHD % 32 == 0;
 }
+// Query rows per workgroup of the tile body used for dtype T.
 template <typename T>
-static int tile_rows_for(int vhd) {
-    return std::is_same<T, half_t>::value && vhd % 32 == 0 ? kMfmaRows : kTileRows;
+static int tile_rows_for(int vhd, int nw = 4) {
+    return std::is_same<T, half_t>::value && vhd % 32 == 0 ? 32 * nw : kTileRows;
+}
+// Threads of a tile workgroup.
+template <typename T, int VHD, int NW>
+constexpr int tile_threads() {
+    return mfma_tile<T, VHD>() ? 64 * NW : 256;
 }
 
-template <typename T, int HD, int VHD, bool PAGED>
+template <typename T, int HD, int VHD, bool PAGED, int NW = 4>
 __device__ __forceinline__ void attn_tile(const TileDesc& t, int kvh, int G, int H,
                                           const T* __restrict__ qrot, const DenseKV& dk,
                                           const PagedKV& pk, float scale,
                                           const float* __restrict__ sink, int k0, int k1,
                                           T* __restrict__ out, int64_t out_tok_stride,
                                           float* __restrict__ part, int nsplit, int split) {
-    if constexpr (tile_rows<T, VHD>() == kMfmaRows)
-        attn_mfma_body<HD, VHD, PAGED>(t, kvh, G, H, qrot, dk, pk, scale, sink, k0, k1, out,
-                                        out_tok_stride, part, nsplit, split);
+    if constexpr (mfma_tile<T, VHD>())
+        attn_mfma_body<HD, VHD, PAGED, NW>(t, kvh, G, H, qrot, dk, pk, scale, sink, k0, k1, out,
+                                            out_tok_stride, part, nsplit, split);
     else
         attn_tile_body<T, HD, VHD, PAGED>(t, kvh, G, H, qrot, dk, pk, scale, sink, k0, k1, out,
                                           out_tok_stride, part, nsplit, split);
@@ -1302,8 +1310,12 @@ __global__ __launch_bounds__(64) void paged_prep_kernel(
 // split 0 records the split count of its rows for paged_merge (0 = direct).
 // Two workgroups per CU (launch bound): a few VGPRs spill, but the second wave per
 // SIMD hides the K/V fetch of the first (mixed 32-sequence batch 917 -> 756 us).
+// Paged prefill tiles take 8 waves (256 query rows) on the matrix-core path: each
+// K/V block fetched serves twice the queries of a 4-wave tile.
+constexpr int kPagedTileWaves = 8;
 template <typename T, int HD, int VHD>
-__global__ __launch_bounds__(256, 2) void paged_tile_kernel(
+__global__ __launch_bounds__((tile_threads<T, VHD, kPagedTileWaves>()),
+                             (mfma_tile<T, VHD>() ? 1 : 2)) void paged_tile_kernel(
     const int4* __restrict__ tiles, const int* __restrict__ tile_count,
     const int32_t* __restrict__ cum, const int32_t* __restrict__ past_lens, PagedKV pk,
     const T* __restrict__ qrot, int G, int H, float scale, const float* __restrict__ sink,
@@ -1337,13 +1349,13 @@ __global__ __launch_bounds__(256, 2) void paged_tile_kernel(
     }
     if (split >= ns) return;
     if (ns == 1) {
-        attn_tile<T, HD, VHD, true>(t, kvh, G, H, qrot, none, pk, scale, sink, 0, kend, out,
+        attn_tile<T, HD, VHD, true, kPagedTileWaves>(t, kvh, G, H, qrot, none, pk, scale, sink, 0, kend, out,
                                     (int64_t)H * VHD, nullptr, 1, 0);
         return;
     }
     const int k0 = split * chunk;
     const int k1 = split == ns - 1 ? kend : min(kend, k0 + chunk);
-    attn_tile<T, HD, VHD, true>(t, kvh, G, H, qrot, none, pk, scale, sink, k0, k1, out,
+    attn_tile<T, HD, VHD, true, kPagedTileWaves>(t, kvh, G, H, qrot, none, pk, scale, sink, k0, k1, out,
                                 (int64_t)H * VHD, part, nsplit, split);
 }
 
@@ -2134,7 +2146,7 @@ static int run_paged(const void* query, const void* key, const void* value, void
     const int G = H / KV;
     // Tiles of the kernel used for T (the workspace is sized for the smaller tile,
     // which gives more tiles, so it bounds this layout too).
-    const int QT = std::max(1, tile_rows_for<T>(VHD) / G);
+    const int QT = std::max(1, tile_rows_for<T>(VHD, kPagedTileWaves) / G);
     const int mt = paged_max_tiles(T_, batch, QT);
     int chunk;
     const int ns = paged_nsplit(max_context, chunk);
@@ -2207,7 +2219,8 @@ static int run_paged(const void* query, const void* key, const void* value, void
         }
     }
     const unsigned tile_wgs = (unsigned)(kXcds * (int64_t)mt * ((KV * ns + kXcds - 1) / kXcds));
-    hipLaunchKernelGGL((paged_tile_kernel<T, HD, VHD>), dim3(tile_wgs), dim3(256), 0, st, tiles,
+    hipLaunchKernelGGL((paged_tile_kernel<T, HD, VHD>), dim3(tile_wgs),
+                       dim3(tile_threads<T, VHD, kPagedTileWaves>()), 0, st, tiles,
                        count, cum, past, pk, qrot, G, H, sc, sink ? sink32 : nullptr, chunk, ns,
                        static_cast<T*>(output), part, nsplit_row, dec ? 1 : 0, mt);
     if (int rc = check_launch("paged_tile")) return rc;
