@@ -1253,19 +1253,35 @@ __global__ __launch_bounds__(64) void paged_prep_kernel(
     extern __shared__ float sv[];
     __shared__ float red[4];
     const int tok = blockIdx.x, head = blockIdx.y;
-    // Sequence of this token: last b with cum[b] <= tok.
-    int lo = 0, hi = batch;  // invariant: cum[lo] <= tok < cum[hi]
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) / 2;
-        if (cum[mid] <= tok) lo = mid;
-        else hi = mid;
-    }
-    const int b = lo;
-    const int pos = past[b] + (tok - cum[b]);
     const bool is_q = head < H;
     const T* src = is_q ? q + ((int64_t)tok * H + head) * hd
                         : k + ((int64_t)tok * KV + (head - H)) * hd;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) sv[d] = to_f32(src[d]);
+    // Sequence of this token: the last b with cum[b] <= tok. Up to 64 sequences,
+    // lane l holds cum[l] and past[l] (one batch of loads, together with the
+    // head row) and a ballot counts the cum[l] <= tok for l >= 1; beyond that, a
+    // binary search.
+    const int lane = threadIdx.x;
+    int b, cb, pb;
+    if (batch <= 64) {
+        const int l = min(lane, batch - 1);
+        const int cl = cum[l], pl = past[l];
+        for (int d = lane; d < hd; d += blockDim.x) sv[d] = to_f32(src[d]);
+        b = (int)__popcll(__ballot(lane >= 1 && lane < batch && cl <= tok));
+        cb = __shfl(cl, b, 64);
+        pb = __shfl(pl, b, 64);
+    } else {
+        int lo = 0, hi = batch;  // invariant: cum[lo] <= tok < cum[hi]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) / 2;
+            if (cum[mid] <= tok) lo = mid;
+            else hi = mid;
+        }
+        b = lo;
+        cb = cum[b];
+        pb = past[b];
+        for (int d = lane; d < hd; d += blockDim.x) sv[d] = to_f32(src[d]);
+    }
+    const int pos = pb + (tok - cb);
     __syncthreads();
     const T* nw = is_q ? qw : kw;
     if (nw) rms_head_lds<T>(sv, hd, nw, eps, red);
