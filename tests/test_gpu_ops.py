@@ -587,6 +587,40 @@ def test_paged_optional_inputs(ortmi, oracle):
                head_sink=sink, qk_norm=True)
 
 
+@pytest.mark.parametrize("new_max,nbs", [(5, 8), (1, 96)])
+def test_paged_bf16(ortmi, oracle, new_max, nbs):
+    """bf16 caches and activations (the VALU tile and the bf16 decode kernel): the
+    oracle runs in fp32 on the same bf16 values; outputs within bf16 rounding, V
+    slots bit-exact, K slots within one bf16 ulp."""
+    import torch
+
+    rng = np.random.default_rng(71 + new_max)
+    H, KV, d, blk, batch = 8, 2, 128, 4, 2
+    nb = nbs * batch
+    maxb = nb // batch
+    cap = maxb * blk
+    new_lens = rng.integers(1, new_max + 1, size=batch).astype(np.int32)
+    past = np.array([rng.integers(0, cap - nl + 1) for nl in new_lens], np.int32)
+    cum = np.concatenate([[0], np.cumsum(new_lens)]).astype(np.int32)
+    nt = int(cum[-1])
+    bf = lambda a: torch.from_numpy((a * 0.3).astype(np.float32)).to(torch.bfloat16)  # noqa: E731
+    q, k, v = (bf(rng.standard_normal((nt, n * d))) for n in (H, KV, KV))
+    kc, vc = (bf(rng.standard_normal((nb, blk, KV, d))) for _ in range(2))
+    bt = rng.permutation(nb).astype(np.int32).reshape(batch, maxb)
+    dkc, dvc = kc.cuda(), vc.cuda()
+    out = ortmi.paged_attention(q.cuda(), k.cuda(), v.cuda(), dkc, dvc, dev(cum), dev(past),
+                                dev(bt), num_heads=H, kv_num_heads=KV)
+    f = lambda t: t.float().numpy()  # noqa: E731
+    ro, rkc, rvc = oracle.paged_attention(f(q), f(k), f(v), f(kc), f(vc), cum, past, bt, H, KV)
+    got = out.float().cpu().numpy()
+    assert out.dtype == torch.bfloat16
+    tol = 2e-3 + 2.0 ** -7 * np.abs(ro)
+    assert (np.abs(got - ro) <= tol).all(), f"paged bf16: max diff {np.abs(got - ro).max():.3e}"
+    np.testing.assert_array_equal(dvc.float().cpu().numpy(), rvc)
+    gk = dkc.float().cpu().numpy()
+    assert (np.abs(gk - rkc) <= 2.0 ** -7 * np.abs(rkc) + 1e-30).all()
+
+
 def test_paged_mixed_batch_reduced(ortmi, oracle):
     """Mixed prefill + decode: 2 sequences prefill 40-token chunks, 6 decode one token,
     block 16, 32/8 heads, hd 128 (a reduced form of the mixed-batch config)."""
