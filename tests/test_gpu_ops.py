@@ -504,6 +504,41 @@ def test_gqa_prefill_decoder_shape(ortmi, oracle):
              seed=9, base=1e6)
 
 
+@pytest.mark.parametrize("dt", ["bf16"])
+@pytest.mark.parametrize("past", [250, 4])
+def test_gqa_decode_dtypes(ortmi, oracle, dt, past):
+    """One-token GQA with bf16 tensors (the decode kernel's FMA score path, its
+    RoPE on bf16 table entries): within bf16 rounding of the fp32 oracle run on
+    the same values. (The op takes fp16 and bf16.)"""
+    import torch
+
+    rng = np.random.default_rng(90 + past + len(dt))
+    B, H, KV, hd, cap = 2, 8, 2, 128, 300
+    tdt = torch.float32 if dt == "f32" else torch.bfloat16
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(tdt)  # noqa: E731
+    q = t(rng.standard_normal((B, 1, H * hd)))
+    k = t(rng.standard_normal((B, 1, KV * hd)))
+    v = t(rng.standard_normal((B, 1, KV * hd)))
+    pk = t(rng.standard_normal((B, KV, cap, hd)))
+    pv = t(rng.standard_normal((B, KV, cap, hd)))
+    c, s_ = refs.rotary_caches(1024, hd, 10000.0)
+    cos, sin = t(c), t(s_)
+    total = past + 1
+    out, prk, prv = ortmi.group_query_attention(
+        q.cuda(), k.cuda(), v.cuda(), pk.cuda(), pv.cuda(),
+        dev(np.full(B, total - 1, np.int32)), total, cos.cuda(), sin.cuda(), num_heads=H,
+        kv_num_heads=KV, do_rotary=1)
+    f = lambda x: x.float().numpy()  # noqa: E731
+    ro, rk, rv, _ = oracle.gqa(f(q), f(k), f(v), f(pk), f(pv), total, H, KV, cos=f(cos),
+                               sin=f(sin))
+    got = out.float().cpu().numpy()
+    rel = 2.0 ** -22 if dt == "f32" else 2.0 ** -6
+    tol = (6e-5 if dt == "f32" else 4e-3) + rel * np.abs(ro)
+    assert (np.abs(got - ro) <= tol).all(), f"gqa {dt}: max diff {np.abs(got - ro).max():.3e}"
+    gv = prv.float().cpu().numpy()
+    np.testing.assert_array_equal(gv[:, :, :total], rv[:, :, :total])
+
+
 def test_gqa_no_rotary(ortmi, oracle):
     _run_gqa(ortmi, oracle, B=1, S=1, H=8, KV=8, hd=64, cap=40, past=40, rope=False, seed=12)
 
