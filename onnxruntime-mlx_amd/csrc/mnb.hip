@@ -30,6 +30,14 @@ namespace ortmi {
 // Dot product of 32 activations with the 32 4-bit codes of one 16-byte chunk.
 // Code i of the chunk is nibble (i & 1) of byte i/2, i.e. bits [4i, 4i+4) of the
 // little-endian 128-bit word.
+//
+// The codes are converted two at a time by the fp8 (e4m3) pack convert: a byte
+// 0000qqqq read as e4m3 is q * 2^-9 exactly (a subnormal m * 2^-9 for q < 8,
+// (8 + m) * 2^-9 with exponent field 1 for q >= 8), so the sum comes out scaled
+// by the exact power of two code_unit() and the caller scales it back. Scaling
+// by a power of two commutes with every rounding here, so the result equals the
+// unscaled sum bit for bit. One instruction per two codes, against a bit-field
+// extract plus a byte convert per code.
 __device__ __forceinline__ float dot32_codes(const float* a, uint4 w) {
     const uint32_t words[4] = {w.x, w.y, w.z, w.w};
     float d0 = 0.f, d1 = 0.f;
@@ -38,16 +46,24 @@ __device__ __forceinline__ float dot32_codes(const float* a, uint4 w) {
         const uint32_t lo = words[i] & 0x0F0F0F0Fu;         // codes 8i+0,2,4,6
         const uint32_t hi = (words[i] >> 4) & 0x0F0F0F0Fu;  // codes 8i+1,3,5,7
         const float* ai = a + 8 * i;
-        d0 = fmaf(ai[0], (float)(lo & 0xffu), d0);
-        d1 = fmaf(ai[1], (float)(hi & 0xffu), d1);
-        d0 = fmaf(ai[2], (float)((lo >> 8) & 0xffu), d0);
-        d1 = fmaf(ai[3], (float)((hi >> 8) & 0xffu), d1);
-        d0 = fmaf(ai[4], (float)((lo >> 16) & 0xffu), d0);
-        d1 = fmaf(ai[5], (float)((hi >> 16) & 0xffu), d1);
-        d0 = fmaf(ai[6], (float)(lo >> 24), d0);
-        d1 = fmaf(ai[7], (float)(hi >> 24), d1);
+        const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);
+        const auto l23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+        const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false);
+        const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);
+        d0 = fmaf(ai[0], l01[0], d0);
+        d1 = fmaf(ai[1], h01[0], d1);
+        d0 = fmaf(ai[2], l01[1], d0);
+        d1 = fmaf(ai[3], h01[1], d1);
+        d0 = fmaf(ai[4], l23[0], d0);
+        d1 = fmaf(ai[5], h23[0], d1);
+        d0 = fmaf(ai[6], l23[1], d0);
+        d1 = fmaf(ai[7], h23[1], d1);
     }
     return d0 + d1;
+}
+// The value dot32_codes gives code 1 (2^-9 for e4m3), read from the hardware.
+__device__ __forceinline__ float code_unit() {
+    return __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
 }
 
 // Reorder 8 activations [a0..a7] to the pair order [a0,a4,a1,a5,a2,a6,a3,a7] used by
@@ -464,9 +480,11 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                 a[j][4 * i + 3] = v.w;
                 s += (v.x + v.y) + (v.z + v.w);
             }
-            asum[j] = s;
+            asum[j] = s * code_unit();  // in dot32_codes' scaled units (exact)
         }
     }
+    // Back from dot32_codes' units: an exact power of two.
+    const float code_scale = H2 ? 1.f : 1.0f / code_unit();
 
     auto reduce_store = [&](const Group& gr, int gi) {
         float acc[R];
@@ -491,7 +509,7 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                     total = fmaf(to_f32(gr.s[r][j]), d32 - (float)zq * asum[j], total);
                 }
             }
-            acc[r] = total;
+            acc[r] = total * code_scale;
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r] = group_sum<LR>(acc[r]);
@@ -540,8 +558,8 @@ static int launch_gemv4_inst(const T* A, const uint8_t* B, const T* S, const uin
 // weights streamed from HBM (the decoder's N x K = 2048 x 1536, 1536 x 1536,
 // 17920 x 1536 in pairs, 1536 x 8960 and 151936 x 1536 in fp16, and 11008 x 4096
 // in fp32). Groups per wave: 1 while the groups fit about 10 waves per CU, 2 for
-// K > 4096 fp16 (activations fill the VGPRs), about 2.7 (4 workgroups per CU) for
-// fp32 K = 4096, 3 up to about 80 groups per CU, 16 beyond. A ring of 2, of 1 when
+// K > 4096 fp16 (activations fill the VGPRs), about 3.6 (3 workgroups per CU) for
+// K = 4096, 3 up to about 80 groups per CU, 16 beyond. A ring of 2, of 1 when
 // the activations fill the VGPRs, of 4 for the long walks. Weights non-temporal
 // except for those two cases, which measured faster with cached loads.
 template <typename T, int BS, int CPL, bool PRO, bool PAIR, bool MRG>
@@ -560,7 +578,10 @@ static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint
     // workgroups, 5.13 -> 4.87 us).
     else if (MRG && groups <= 10 * cus) grid = (groups + 5) / 6;
     else if (groups <= 10 * cus) grid = (groups + 3) / 4;
-    else if (CPL >= 2) grid = std::min((groups + 3) / 4, 4 * cus);
+    // Three workgroups per CU: K = 4096, N = 11008 measured 8.1 us against 8.6 us at
+    // four (fp32 and fp16 alike); grids that are not a multiple of the CU count
+    // (2.5 or 3.5 per CU) measured slowest.
+    else if (CPL >= 2) grid = std::min((groups + 3) / 4, 3 * cus);
     else grid = (groups + 11) / 12;
     bool sv = false;
     if constexpr (BS == 32 && CPL % 2 == 0)  // scale pairs as one load when every lane's pair is aligned
