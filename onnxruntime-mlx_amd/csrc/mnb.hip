@@ -680,7 +680,14 @@ struct GemmStage {
 // own LDS buffers, common barriers: both halves run the same number of steps),
 // whose accumulators are summed through LDS at the end: 2 waves per SIMD to hide
 // the load latency when the grid has only about one tile per CU.
-template <int BM, int BN, int BS, int KS = 1, bool SWI = false>
+//
+// BR (weights in registers, BN = 128): the 4 waves sit side by side, each with
+// all BM rows and 32 columns. Lane l of a wave loads chunk 2s + (l >> 5) of
+// column (l & 31) of k-step s and dequantises it straight into its MFMA B
+// operands (word kk of the chunk for sub-step kk). Only the activation tile goes
+// through LDS, read at column 32 (l >> 5) + 8 kk so that both operands take the
+// same codes in each k slot.
+template <int BM, int BN, int BS, int KS = 1, bool SWI = false, bool BR = false>
 __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __restrict__ A,
                                                              const uint8_t* __restrict__ B,
                                                              const half_t* __restrict__ S,
@@ -692,15 +699,16 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
     // (BN = 128) or half a chunk per thread (BN = 64).
     static_assert(BN == 128 || BN == 64, "weight tile rows");
     static_assert(KS == 1 || KS == 2, "k split");
-    constexpr int WM = BM / 2, WN = BN / 2;
+    static_assert(!BR || BN == 128, "weights in registers: 4 waves x 32 columns");
+    constexpr int WM = BR ? BM : BM / 2, WN = BR ? 32 : BN / 2;
     constexpr int TM = WM / 32, TN = WN / 32;
     using Stage = GemmStage<BM, BN, BS>;
     constexpr int A_VEC = Stage::A_VEC;
     __shared__ half_t sAall[KS][2][BM * kLdsRow];
-    __shared__ half_t sBall[KS][2][BN * kLdsRow];
+    __shared__ half_t sBall[KS][2][BR ? 8 : BN * kLdsRow];
     const int half_id = KS == 2 ? (int)(threadIdx.x >> 8) : 0;
     half_t (&sA)[2][BM * kLdsRow] = sAall[half_id];
-    half_t (&sB)[2][BN * kLdsRow] = sBall[half_id];
+    auto& sB = sBall[half_id];
 
     // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs; give each
     // XCD a contiguous range of tiles (m fastest) so tiles sharing weight columns
@@ -712,7 +720,7 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
-    const int wm = (wave & 1) * WM, wn = (wave >> 1) * WN;
+    const int wm = BR ? 0 : (wave & 1) * WM, wn = BR ? wave * 32 : (wave >> 1) * WN;
     const int Kp = nb * BS;
     const int ksteps_all = (Kp + kBK - 1) / kBK;
     // This half's k-steps: [kbase, kbase + ksteps); steps past the end read zeros.
@@ -756,8 +764,9 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
             st.a[p] = make_uint4(v.x, v.y, v.z, v.w);
         }
         constexpr int TPR = 256 / BN;  // threads per weight row: 2 (one chunk) or 4 (half)
-        const int r = tid / TPR;
-        const int chunk = 2 * ks + (tid % TPR) * 2 / TPR;
+        // BR: column (lane & 31) of this wave's 32, chunk (lane >> 5) of the step.
+        const int r = BR ? wn + (lane & 31) : tid / TPR;
+        const int chunk = 2 * ks + (BR ? (lane >> 5) : (tid % TPR) * 2 / TPR);
         const int n = n0 + r;
         const bool ok = live && n < N && chunk < chunks;
         const int blk = (chunk * 32) / BS;
@@ -786,22 +795,24 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
             const int r = idx >> 3, c = (idx & 7) * 8;
             *reinterpret_cast<uint4*>(&sA[buf][r * kLdsRow + c]) = permute_act8(st.a[p]);
         }
-        const float zf = Z ? (float)nibble(st.z, st.zhi) : 8.f;
-        const half_t sh = __builtin_bit_cast(half_t, st.s);
-        const half2_t zoff = {(half_t)(1024.f + zf), (half_t)(1024.f + zf)};
-        const half2_t s2 = {sh, sh};
-        if constexpr (BN == 128) {
-            const int r = tid >> 1, h = tid & 1;
-            uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32]);
-            dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
-            dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
-            dst[2] = dequant_word_pairs(st.b.z, zoff, s2);
-            dst[3] = dequant_word_pairs(st.b.w, zoff, s2);
-        } else {
-            const int r = tid >> 2, h = (tid >> 1) & 1, q = tid & 1;
-            uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32 + q * 16]);
-            dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
-            dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
+        if constexpr (!BR) {
+            const float zf = Z ? (float)nibble(st.z, st.zhi) : 8.f;
+            const half_t sh = __builtin_bit_cast(half_t, st.s);
+            const half2_t zoff = {(half_t)(1024.f + zf), (half_t)(1024.f + zf)};
+            const half2_t s2 = {sh, sh};
+            if constexpr (BN == 128) {
+                const int r = tid >> 1, h = tid & 1;
+                uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32]);
+                dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
+                dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
+                dst[2] = dequant_word_pairs(st.b.z, zoff, s2);
+                dst[3] = dequant_word_pairs(st.b.w, zoff, s2);
+            } else {
+                const int r = tid >> 2, h = (tid >> 1) & 1, q = tid & 1;
+                uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32 + q * 16]);
+                dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
+                dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
+            }
         }
     };
 
@@ -814,18 +825,37 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
     const int lrow = lane & 31, lk = (lane >> 5) * 8;
+    // BR: the B operands of the current step, dequantised from its stage.
+    uint4 bq[BR ? 4 : 1];
+    auto dequant_b = [&](const Stage& st) {
+        const float zf = Z ? (float)nibble(st.z, st.zhi) : 8.f;
+        const half_t sh = __builtin_bit_cast(half_t, st.s);
+        const half2_t zoff = {(half_t)(1024.f + zf), (half_t)(1024.f + zf)};
+        const half2_t s2 = {sh, sh};
+        bq[0] = dequant_word_pairs(st.b.x, zoff, s2);
+        if constexpr (BR) {
+            bq[1] = dequant_word_pairs(st.b.y, zoff, s2);
+            bq[2] = dequant_word_pairs(st.b.z, zoff, s2);
+            bq[3] = dequant_word_pairs(st.b.w, zoff, s2);
+        }
+    };
     auto compute = [&](int buf) {
 #pragma unroll
         for (int kk = 0; kk < kBK / 16; ++kk) {
             half8_t af[TM], bf[TN];
+            const int acol = BR ? 4 * lk + kk * 8 : kk * 16 + lk;
 #pragma unroll
             for (int i = 0; i < TM; ++i)
                 af[i] = *reinterpret_cast<const half8_t*>(
-                    &sA[buf][(wm + i * 32 + lrow) * kLdsRow + kk * 16 + lk]);
+                    &sA[buf][(wm + i * 32 + lrow) * kLdsRow + acol]);
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
-                bf[j] = *reinterpret_cast<const half8_t*>(
-                    &sB[buf][(wn + j * 32 + lrow) * kLdsRow + kk * 16 + lk]);
+            for (int j = 0; j < TN; ++j) {
+                if constexpr (BR)
+                    bf[j] = __builtin_bit_cast(half8_t, bq[kk]);
+                else
+                    bf[j] = *reinterpret_cast<const half8_t*>(
+                        &sB[buf][(wn + j * 32 + lrow) * kLdsRow + kk * 16 + lk]);
+            }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -848,12 +878,15 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
     __syncthreads();
     const int ksteps2 = (ksteps + 1) & ~1;
     for (int ks = 0; ks < ksteps2; ks += 2) {
-        // even step ks: LDS buf 0 holds it; r1 holds step ks+1.
+        // even step ks: LDS buf 0 holds it; r1 holds step ks+1. (BR: r0's weights
+        // become the B operands before r0 is reloaded.)
+        if constexpr (BR) dequant_b(r0);
         gload(r0, ks + 2);
         compute(0);
         sstore(r1, 1);
         __syncthreads();
         // odd step ks+1: LDS buf 1; r0 holds step ks+2.
+        if constexpr (BR) dequant_b(r1);
         gload(r1, ks + 3);
         compute(1);
         sstore(r0, 0);
@@ -863,8 +896,10 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
     if constexpr (KS == 2) {
         // Half 1 hands its accumulators to half 0 through LDS (the loop ended on a
         // barrier, so the tile buffers are free).
-        float* xch = reinterpret_cast<float*>(&sBall[0][0][0]);
-        static_assert(4 * TM * TN * 16 * 64 * sizeof(float) <= sizeof(sBall), "exchange space");
+        float* xch = BR ? reinterpret_cast<float*>(&sAall[0][0][0])
+                        : reinterpret_cast<float*>(&sBall[0][0][0]);
+        static_assert(4 * TM * TN * 16 * 64 * sizeof(float) <= (BR ? sizeof(sAall) : sizeof(sBall)),
+                      "exchange space");
         if (half_id == 1) {
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -923,11 +958,11 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
         }
 }
 
-template <int BM, int BN, int BS, int KS = 1, bool SWI = false>
+template <int BM, int BN, int BS, int KS = 1, bool SWI = false, bool BR = false>
 static int launch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, const uint8_t* Z,
                         half_t* Y, int M, int N, int K, int nb, hipStream_t st) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    hipLaunchKernelGGL((mnb_gemm4_kernel<BM, BN, BS, KS, SWI>), dim3(tiles_m * tiles_n),
+    hipLaunchKernelGGL((mnb_gemm4_kernel<BM, BN, BS, KS, SWI, BR>), dim3(tiles_m * tiles_n),
                        dim3(256 * KS), 0, st, A, B, S, Z, Y, M, N, K, nb, tiles_m, tiles_n);
     return check_launch("mnb_gemm4");
 }
@@ -942,7 +977,10 @@ static int dispatch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, co
     // with 64x64).
     const int cus = device_cu_count();
     const long big = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (big >= 2L * cus) return launch_gemm4<128, 128, BS, 1, SWI>(A, B, S, Z, Y, M, N, K, nb, st);
+    // 128x128 tiles take their weights in registers (gate/up 512x17920x1536:
+    // 52-54 -> 46-47 us); at 64x128 the LDS form measured equal or faster.
+    if (big >= 2L * cus)
+        return launch_gemm4<128, 128, BS, 1, SWI, true>(A, B, S, Z, Y, M, N, K, nb, st);
     const long mid = (long)((M + 63) / 64) * ((N + 127) / 128);
     if (mid >= cus) return launch_gemm4<64, 128, BS, 2, SWI>(A, B, S, Z, Y, M, N, K, nb, st);
     return launch_gemm4<64, 64, BS, 2, SWI>(A, B, S, Z, Y, M, N, K, nb, st);

@@ -198,6 +198,20 @@ def test_mnb_gemm_config2_shape(ortmi, oracle):
     assert_f16_close(got[rows], ref, extra=bound, what="gemm config2")
 
 
+@pytest.mark.parametrize("M,N,K,block", [(1030, 8200, 1000, 64), (1024, 8192, 1536, 32)])
+def test_mnb_gemm_large_tiles(ortmi, oracle, M, N, K, block):
+    """Shapes that fill the CUs twice with 128x128 tiles (the weights-in-registers
+    tile): ragged M, N and K edges, and the aligned case, on a sample of rows."""
+    rng = np.random.default_rng(M + N + K)
+    A, B, s, zp = _mnb_inputs(rng, M, N, K, block, dtype=np.float16)
+    got = host(ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N, block_size=block))
+    rows = np.r_[np.arange(0, M, 41), M - 1]
+    ref = oracle.mnb_matmul(A[rows], B, s, zp, N, K, 4, block)
+    W = refs.dequant_ref(B, s, zp, N, K, 4, block)
+    bound = 2.0 ** -11 * (np.abs(A[rows].astype(np.float64)) @ np.abs(W).T)
+    assert_f16_close(got[rows], ref, extra=bound, what="gemm large tiles")
+
+
 @pytest.mark.parametrize("M,N,K,block", [(37, 400, 1536, 32), (512, 2048, 1536, 32),
                                          (512, 17920, 1536, 32), (64, 256, 1000, 64)])
 def test_mnb_gemm_swiglu_pairs(ortmi, oracle, M, N, K, block):
