@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X execution provider's hot path on one GPU.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|gemv|gemm|gqa|paged|copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload all|gemv|gemm|gqa|paged|decoder|copy]
 
 Primary line: int4 MatMulNBits decode GEMV (K=4096, N=11008, block 32, fp32
 activations) as achieved HBM GB/s. A step is one MatMulNBits call; consecutive
@@ -10,9 +11,13 @@ weights from HBM, not from the 256 MB Infinity Cache. Launches are captured in a
 HIP graph and replayed, and the per-launch duration is taken from HIP events
 recorded on the stream the kernels run on.
 
-Secondary measurements (same JSON line, "secondary"): the MFMA prefill GEMM
-(M=512, K=N=4096, fp16), the GQA decode step (B=8, H=32/8, hd=128, 4K context,
-growing KV contract) and the PagedAttention mixed batch.
+Secondary measurements (same JSON line, "secondary"):
+- the same GEMV at one GPU's share of an 8-way N split (N = 1376);
+- the MFMA prefill GEMM (M=512, K=N=4096, fp16);
+- the GQA decode step (B=8, H=32/8, hd=128, 4K context), with the growing and
+  with the shared KV contract;
+- the PagedAttention mixed batch;
+- the int4 decoder (decode tokens/s and the prompt prefill).
 
 cpu_baseline: the oracle's C restatement of MatMulNBits (OpenMP over the host
 cores) timed on a bounded sample of the same GEMV on this machine's CPU.
@@ -100,7 +105,9 @@ def timed_eager(torch, launch_one, steps, warmup):
 
 # ------------------------------------------------------------------- workloads --
 
-def bench_gemv(torch, ortmi, steps, warmup):
+def bench_gemv(torch, ortmi, steps, warmup, shard=1):
+    """The cfg1 GEMV; shard > 1 runs one GPU's share of an N-sharded layer (the
+    first N / shard rows), the shape each GPU would run under tensor parallelism."""
     import ctypes
 
     from ortmi import workloads  # noqa: F401  (loaded as a submodule)
@@ -108,6 +115,10 @@ def bench_gemv(torch, ortmi, steps, warmup):
     wl = sys.modules["ortmi.workloads"]
     K, N = 4096, 11008
     A, B, s, zp = wl.mnb_gemv_config()
+    if shard > 1:
+        rows = N // shard
+        B, s, zp = (x.reshape(N, -1)[:rows].copy() for x in (B, s, zp))
+        N = rows
     bytes_per_call = B.nbytes + s.nbytes + zp.nbytes + A.nbytes + N * 4
     copies = max(2, -(-(2 * MALL_BYTES) // bytes_per_call))
     dA = torch.from_numpy(A).cuda()
@@ -386,6 +397,15 @@ def main():
     if wl in ("all", "gemv"):
         gemv = bench_gemv(torch, ortmi, args.steps, args.warmup)
         log(f"gemv: {gemv['gbs']:.1f} GB/s ({gemv['gpu_ms'] * 1e3:.2f} us/call)")
+        r = bench_gemv(torch, ortmi, args.steps, args.warmup, shard=8)
+        secondary["gemv_shard_of_8"] = {
+            "config": "one GPU's share of the same GEMV sharded 8 ways along N: M=1 K=4096 "
+                      "N=1376, fp32",
+            "gbs": round(r["gbs"], 1), "us_per_call": round(r["gpu_ms"] * 1e3, 2),
+            "bytes_per_call": r["bytes_per_call"],
+            "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}}
+        log(f"gemv shard 1/8: {r['gbs']:.1f} GB/s ({r['gpu_ms'] * 1e3:.2f} us/call)")
     if wl in ("all", "gemm"):
         r = bench_gemm(torch, ortmi, args.steps, args.warmup)
         secondary["mnb_gemm_prefill"] = {
