@@ -250,6 +250,29 @@ def test_mnb_gemm_swiglu_pairs(ortmi, oracle, M, N, K, block):
     assert_f16_close(host(y)[rows], ref, extra=extra, what="gemm swiglu pairs")
 
 
+@pytest.mark.parametrize("M", [1, 5])
+@pytest.mark.parametrize("K,N,block,asym", [(1536, 300, 32, True), (4096, 257, 64, False),
+                                            (1000, 130, 128, True), (8960, 64, 32, False)])
+def test_mnb_bf16(ortmi, oracle, M, K, N, block, asym):
+    """bf16 activations and scales (M = 1: the decode GEMV and its fp8-convert dot
+    product; M > 1: the generic kernel) against the oracle run on the same bf16
+    values: within the output's bf16 rounding plus fp32 accumulation."""
+    import torch
+
+    rng = np.random.default_rng(M * 7 + K + N + block)
+    A, B, s, zp = _mnb_inputs(rng, M, N, K, block, asym=asym)
+    tA = torch.from_numpy(A).to(torch.bfloat16)
+    ts = torch.from_numpy(s).to(torch.bfloat16)
+    A_r, s_r = tA.float().numpy(), ts.float().numpy()
+    got = host(ortmi.matmul_nbits(tA.cuda(), dev(B), ts.cuda(), dev(zp) if asym else None,
+                                  K=K, N=N, block_size=block))
+    ref = oracle.mnb_matmul(A_r, B, s_r, zp if asym else None, N, K, 4, block)
+    W = refs.dequant_ref(B, s_r, zp if asym else None, N, K, 4, block)
+    accum = 2.0 ** -18 * (np.abs(A_r.astype(np.float64)) @ np.abs(W).T)
+    bound = 2.0 ** -8 * np.abs(ref) + accum
+    assert (np.abs(got - ref) <= bound).all(), np.abs(got - ref).max()
+
+
 @pytest.mark.parametrize("M,bits,block", [(1, 8, 32), (3, 8, 64), (1, 4, 16), (5, 4, 16)])
 def test_mnb_generic_forms_fp32(ortmi, oracle, M, bits, block):
     rng = np.random.default_rng(M + bits + block)
