@@ -91,7 +91,7 @@ def test_mnb_decode_fused(ortmi, oracle, K, N, block, skip, pair):
     a16 = oracle.round_f16(y)
     exact = oracle.mnb_matmul(a16, B, s, zp, N, K, 4, block)
     lib = ortmi.load_kernels()
-    dx, dB, ds = dev(x), dev(B), dev(s)
+    dx, dB, ds, dg = dev(x), dev(B), dev(s), dev(gamma)
     dz = dev(zp) if zp is not None else None
     dsk = dev(sk) if skip else None
     res = torch.empty(K, dtype=torch.float16, device="cuda") if skip else None
@@ -100,7 +100,7 @@ def test_mnb_decode_fused(ortmi, oracle, K, N, block, skip, pair):
     flags = 1 | (2 if pair else 0)
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     ortmi.check(lib.ortmi_matmul_nbits_decode_fused(
-        p(dx), p(dsk), p(dev(gamma)), 1e-6, p(res), p(dB), p(ds), p(dz), p(out), N, K, block,
+        p(dx), p(dsk), p(dg), 1e-6, p(res), p(dB), p(ds), p(dz), p(out), N, K, block,
         flags, 10, st))
     got = host(out)
     if skip:
@@ -120,6 +120,64 @@ def test_mnb_decode_fused(ortmi, oracle, K, N, block, skip, pair):
     dsilu = np.abs(sig * (1 + g * (1 - sig)))
     bound = eg * dsilu * np.abs(u) + eu * np.abs(g * sig) + eg * eu * 1.2 + 2 * ulp16(ref)
     assert (np.abs(got - ref) <= 1e-3 + bound).all(), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("K,N,block,skip,pair", [
+    (1536, 2048, 32, False, False), (1536, 17920, 32, True, True), (4096, 512, 128, True, True),
+    (8960, 1536, 32, True, False)])
+def test_mnb_decode_fused_bf16(ortmi, oracle, K, N, block, skip, pair):
+    """The fused decode GEMV with bf16 tensors (norm prologue in fp32 rounded to
+    bf16, the fp8-convert dot product, SwiGLU op by op in bf16) against the
+    oracle's unfused ops on the same bf16 inputs."""
+    import ctypes
+
+    import torch
+
+    def rb(a):  # round to bf16 (RNE) and widen back
+        return torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+
+    def tb(a):
+        return torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16).cuda()
+
+    rng = np.random.default_rng(K + N + block + 1)
+    A, B, s, zp = _mnb_inputs(rng, 1, N, K, block, asym=N % 3 == 0)
+    x, s_r = rb(A[0]), rb(s)
+    sk = rb(rng.standard_normal(K)) if skip else None
+    gamma = rb(1 + 0.2 * rng.standard_normal(K))
+    y, r = oracle.rms_norm(x, gamma, 1e-6, skip=sk)
+    a_b = rb(y)
+    exact = oracle.mnb_matmul(a_b[None], B, s_r, zp, N, K, 4, block)[0]
+    lib = ortmi.load_kernels()
+    # Every device tensor is held by a name until the kernel has run (a temporary
+    # would go back to the allocator and its block could be handed out again).
+    dx, dg, ds, dB = tb(x), tb(gamma), tb(s_r), dev(B)
+    dz = dev(zp) if zp is not None else None
+    dsk = tb(sk) if skip else None
+    res = torch.empty(K, dtype=torch.bfloat16, device="cuda") if skip else None
+    out = torch.empty(N // 2 if pair else N, dtype=torch.bfloat16, device="cuda")
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ortmi.check(lib.ortmi_matmul_nbits_decode_fused(
+        p(dx), p(dsk), p(dg), 1e-6, p(res), p(dB), p(ds), p(dz), p(out), N, K,
+        block, 1 | (2 if pair else 0), 16, st))  # 16: bf16
+    got = host(out)
+    if skip:
+        np.testing.assert_array_equal(host(res), rb(r))
+    W = oracle.mnb_dequant(B, s_r, zp, N, K, 4, block)
+    # The normalised activations may differ by one bf16 rounding; fp32 accumulation.
+    extra = np.abs(W) @ (np.abs(a_b) * 2.0 ** -7) + 2.0 ** -18 * (np.abs(W) @ np.abs(a_b))
+    if not pair:
+        assert (np.abs(got - exact) <= 2.0 ** -8 * np.abs(exact) + extra).all(), \
+            np.abs(got - exact).max()
+        return
+    g, u = rb(exact[0::2]), rb(exact[1::2])
+    sig = rb(1.0 / (1.0 + np.exp(-g.astype(np.float64))))
+    ref = rb(rb(g * sig) * u)
+    eg = 2.0 ** -8 * np.abs(g) + extra[0::2]
+    eu = 2.0 ** -8 * np.abs(u) + extra[1::2]
+    dsilu = np.abs(sig * (1 + g * (1 - sig)))
+    bound = eg * dsilu * np.abs(u) + eu * np.abs(g * sig) + eg * eu * 1.2 + 2.0 ** -7 * np.abs(ref)
+    assert (np.abs(got - ref) <= 1e-6 + bound).all(), np.abs(got - ref).max()
 
 
 @pytest.mark.parametrize("K,block", [(256, 32), (1176, 32), (256, 64), (512, 128), (8960, 32),
