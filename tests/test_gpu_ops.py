@@ -509,27 +509,42 @@ def test_gqa_decode_capturable(ortmi, oracle, H, KV, hd):
         assert torch.equal(kg, ke) and torch.equal(vg, ve)
 
 
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("H,KV,hd,past", [(12, 2, 128, 140), (8, 8, 64, 5), (16, 4, 128, 299)])
-def test_gqa_partials_merge_gemv(ortmi, oracle, H, KV, hd, past):
+def test_gqa_partials_merge_gemv(ortmi, oracle, H, KV, hd, past, dt):
     """One-token attention left as split partials and merged in the o_proj GEMV's
     prologue equals the capturable attention followed by the plain GEMV (same KV
-    append, bit for bit; outputs within the GEMV tolerance plus one fp16 rounding
-    of each activation)."""
+    append, bit for bit; outputs within the GEMV tolerance plus one rounding of
+    each activation to the dtype). bf16 runs the merge GEMV's fp8-convert dot
+    product."""
     import ctypes
 
     import torch
 
+    bf = dt == "bf16"
+    code = 16 if bf else 10
+    tdt = torch.bfloat16 if bf else torch.float16
+
+    def rnd(a):  # round to the dtype and widen back
+        return torch.from_numpy(np.asarray(a, np.float32)).to(tdt).float().numpy()
+
+    def td(a):
+        return torch.from_numpy(np.asarray(a, np.float32)).to(tdt).cuda()
+
     rng = np.random.default_rng(H * 3 + hd + past)
     B, cap = 1, 300
     q, k, v, pk, pv, cos, sin = _gqa_inputs(rng, B, 1, H, KV, hd, cap, True, 1e6)
-    dq, dk, dv, dcos, dsin = dev(q), dev(k), dev(v), dev(cos), dev(sin)
+    if bf:
+        q, k, v, pk, pv, cos, sin = (rnd(x) for x in (q, k, v, pk, pv, cos, sin))
+    dq, dk, dv, dcos, dsin = (td(x) for x in (q, k, v, cos, sin))
     tot = torch.tensor([past + 1], dtype=torch.int32, device="cuda")
-    ka, va, kb, vb = dev(pk), dev(pv), dev(pk), dev(pv)
+    ka, va, kb, vb = td(pk), td(pv), td(pk), td(pv)
     ref = ortmi.group_query_attention_decode_capturable(
         dq, dk, dv, ka, va, tot, dcos, dsin, num_heads=H, kv_num_heads=KV)
     K, N, block = H * hd, 1536, 32
-    _, W, s_, zp = _mnb_inputs(rng, 1, N, K, block, asym=True, dtype=np.float16)
-    dW, ds, dz = dev(W), dev(s_), dev(zp)
+    _, W, s_, zp = _mnb_inputs(rng, 1, N, K, block, asym=True)
+    s_ = rnd(s_)
+    dW, ds, dz = dev(W), td(s_), dev(zp)
     y_ref = ortmi.matmul_nbits(ref.reshape(1, K), dW, ds, dz, K=K, N=N, bits=4, block_size=block)
     lib = ortmi.load_kernels()
     ns = lib.ortmi_group_query_attention_decode_splits(B, H, KV, hd, cap)
@@ -539,18 +554,26 @@ def test_gqa_partials_merge_gemv(ortmi, oracle, H, KV, hd, past):
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     ortmi.check(lib.ortmi_group_query_attention_decode_partials(
         p(dq), p(dk), p(dv), p(kb), p(vb), cap, p(tot), p(dcos), p(dsin), cos.shape[1],
-        cos.shape[0], p(part), B, H, KV, hd, 0.0, 0, 10, st))
-    y = torch.empty(N, dtype=torch.float16, device="cuda")
+        cos.shape[0], p(part), B, H, KV, hd, 0.0, 0, code, st))
+    y = torch.empty(N, dtype=tdt, device="cuda")
     ortmi.check(lib.ortmi_matmul_nbits_decode_merge(
-        p(part), ns, hd, p(dW), p(ds), p(dz), p(y), N, K, block, 10, st))
+        p(part), ns, hd, p(dW), p(ds), p(dz), p(y), N, K, block, code, st))
     torch.cuda.synchronize()
     assert torch.equal(ka, kb) and torch.equal(va, vb)
     a = host(ref).reshape(K)
     Wd = oracle.mnb_dequant(W, s_, zp, N, K, 4, block)
-    exact = oracle.mnb_matmul(oracle.round_f16(a), W, s_, zp, N, K, 4, block)
-    extra = np.abs(Wd) @ (np.abs(a) * 2.0 ** -10)
-    assert_f16_close(host(y), exact, extra=extra, what="merged o_proj GEMV")
-    assert_f16_close(host(y_ref).reshape(N), exact, extra=extra, what="unfused o_proj GEMV")
+    exact = oracle.mnb_matmul(rnd(a)[None], W, s_, zp, N, K, 4, block)[0]
+    if not bf:
+        extra = np.abs(Wd) @ (np.abs(a) * 2.0 ** -10)
+        assert_f16_close(host(y), exact, extra=extra, what="merged o_proj GEMV")
+        assert_f16_close(host(y_ref).reshape(N), exact, extra=extra, what="unfused o_proj GEMV")
+        return
+    # bf16: output rounding (2^-8 relative), one bf16 rounding of each merged
+    # activation, fp32 accumulation.
+    extra = np.abs(Wd) @ (np.abs(a) * 2.0 ** -7) + 2.0 ** -18 * (np.abs(Wd) @ np.abs(a))
+    for got, what in ((host(y), "merged"), (host(y_ref).reshape(N), "unfused")):
+        assert (np.abs(got - exact) <= 2.0 ** -8 * np.abs(exact) + extra).all(), \
+            (what, np.abs(got - exact).max())
 
 
 @pytest.mark.parametrize("S,past,cap", [(1, 40, 64), (9, 10, 64)])
