@@ -153,6 +153,29 @@ int ortmi_group_query_attention(const void* query, const void* key, const void* 
                                 size_t workspace_bytes, void* stream);
 
 /*
+ * ortmi_group_query_attention without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). It has no counterpart in the
+ * reference. Arguments and results are those of ortmi_group_query_attention;
+ * the workspace is a fixed scratch array inside this library, one per GPU
+ * (ortmi_group_query_attention_noalloc_max_workspace() bytes, 32 MiB), held
+ * until the process ends. A call whose
+ * ortmi_group_query_attention_workspace_size(batch, seq_len, num_heads,
+ * head_size, valid_past + seq_len) exceeds it returns ORTMI_E_WORKSPACE before
+ * any launch. The call allocates nothing. Every call on one GPU shares that
+ * GPU's scratch, so calls that overlap on one GPU (concurrent streams or
+ * threads) race; calls ordered on one stream do not.
+ */
+size_t ortmi_group_query_attention_noalloc_max_workspace(void);
+int ortmi_group_query_attention_noalloc(
+    const void* query, const void* key, const void* value, const void* past_key,
+    const void* past_value, int64_t past_cap, int32_t total_sequence_length,
+    const void* cos_cache, const void* sin_cache, int64_t rotary_half, int64_t max_pos,
+    void* output, void* present_key, void* present_value, int64_t batch, int64_t seq_len,
+    int64_t num_heads, int64_t kv_num_heads, int64_t head_size, float scale,
+    int32_t rotary_interleaved, int32_t dtype, void* stream);
+
+/*
  * One-token GroupQueryAttention decode step over a fixed-capacity shared KV
  * buffer, in a form that can be captured into a HIP graph and replayed across
  * steps: total_sequence_length is read from device memory by the kernels, and

@@ -11,12 +11,15 @@
 //    contiguous rows per load), and in the growing contract writes the same rows
 //    to `present` from the registers it already holds, so the past->present copy
 //    costs no extra read. Partial softmax states are merged by attn_merge.
-//  * attn_tile - VALU flash-attention tile for everything else (GQA prefill and
-//    PagedAttention): Q rows of one sequence and one kv-head group against
-//    64-key tiles staged in LDS, online softmax in fp32. Paged keys are fetched
-//    through the block table on the device; no control tensor is read back to
-//    the host.
-//  * attn_merge - log-sum-exp merge of split-K partials.
+//  * gqa_tile / paged_tile - matrix-core flash-attention tiles for everything
+//    with more than one query token (GQA prefill, PagedAttention prefill
+//    chunks): S^T = K.Q^T and O^T += V^T.P^T on v_mfma_f32_32x32x16_f16, Q^T
+//    and K staged in LDS, V transposed in LDS, online softmax in fp32 with one
+//    query per lane. Paged keys are fetched through the block table on the
+//    device; no control tensor is read back to the host.
+//  * paged_decode - one-token PagedAttention rows on the vector units, split-K.
+//  * attn_merge / paged_merge - log-sum-exp merge of split-K partials.
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -2115,6 +2118,72 @@ extern "C" int ortmi_group_query_attention_decode_partials(
                                        rotary_half, max_pos, nullptr, partials, batch, num_heads,
                                        kv_num_heads, head_size, scale, rotary_interleaved, dtype,
                                        nullptr, 0, stream);
+}
+
+// ------------------------------------- GQA without caller-owned workspace --
+
+// Workspace of ortmi_group_query_attention_noalloc: device memory of this
+// library, one copy per GPU, held until the process ends. Host code never passes
+// `scratch` itself to a kernel (in host code the name is a host-side stand-in,
+// not a device address); it uses the per-device address from
+// hipGetSymbolAddress kept in g_scratch_addr.
+constexpr size_t kGqaScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kGqaScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[kMaxScratchDevices];
+
+// Device address of the current device's `scratch`, looked up once per device
+// (with that device current) on the first call.
+static int scratch_address(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return check_launch("hipGetDevice");
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return fail(ORTMI_E_INVALID, "GroupQueryAttention: device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return fail(ORTMI_E_HIP, std::string("GroupQueryAttention: hipGetSymbolAddress: ") +
+                                         hipGetErrorString(e));
+        }
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return ORTMI_OK;
+}
+
+extern "C" size_t ortmi_group_query_attention_noalloc_max_workspace(void) {
+    return kGqaScratchBytes;
+}
+
+extern "C" int ortmi_group_query_attention_noalloc(
+    const void* query, const void* key, const void* value, const void* past_key,
+    const void* past_value, int64_t past_cap, int32_t total_sequence_length, const void* cos_cache,
+    const void* sin_cache, int64_t rotary_half, int64_t max_pos, void* output, void* present_key,
+    void* present_value, int64_t batch, int64_t seq_len, int64_t num_heads, int64_t kv_num_heads,
+    int64_t head_size, float scale, int32_t rotary_interleaved, int32_t dtype, void* stream) {
+    ORTMI_REQUIRE(batch > 0 && seq_len > 0 && num_heads > 0 && head_size > 0 && past_cap >= 0,
+                  "GroupQueryAttention: bad shape");
+    int64_t vp = (int64_t)total_sequence_length - seq_len;
+    if (vp < 0 || vp > past_cap) vp = past_cap;
+    const size_t need =
+        ortmi_group_query_attention_workspace_size(batch, seq_len, num_heads, head_size, vp + seq_len);
+    if (need > kGqaScratchBytes)
+        return fail(ORTMI_E_WORKSPACE,
+                    "GroupQueryAttention (no-alloc): needs " + std::to_string(need) +
+                        " bytes of workspace, above the library's fixed " +
+                        std::to_string(kGqaScratchBytes) + "-byte scratch");
+    void* ws = nullptr;
+    if (int rc = scratch_address(&ws)) return rc;
+    return ortmi_group_query_attention(query, key, value, past_key, past_value, past_cap,
+                                       total_sequence_length, cos_cache, sin_cache, rotary_half,
+                                       max_pos, output, present_key, present_value, batch, seq_len,
+                                       num_heads, kv_num_heads, head_size, scale,
+                                       rotary_interleaved, dtype, ws, kGqaScratchBytes, stream);
 }
 
 // ------------------------------------------------------- PagedAttention API --
