@@ -119,6 +119,18 @@ typedef enum OrtHardwareDeviceType {
     OrtHardwareDeviceType_NPU = 2,
 } OrtHardwareDeviceType;
 
+typedef enum OrtAllocatorType {
+    OrtInvalidAllocator = -1,
+    OrtDeviceAllocator = 0,
+    OrtArenaAllocator = 1,
+} OrtAllocatorType;
+
+typedef enum OrtMemType {
+    OrtMemTypeCPUInput = -2,
+    OrtMemTypeCPUOutput = -1,
+    OrtMemTypeDefault = 0,
+} OrtMemType;
+
 typedef enum OrtDeviceMemoryType {
     OrtDeviceMemoryType_DEFAULT = 0,
     OrtDeviceMemoryType_HOST_ACCESSIBLE = 5,
@@ -190,7 +202,10 @@ typedef struct OrtEp {
                                             const OrtMemoryDevice* memory_device,
                                             OrtSyncStreamImpl** stream);
     const char* (*GetCompiledModelCompatibilityInfo)(struct OrtEp* this_ptr, const OrtGraph* graph);
-    const OrtMemoryDevice* (*GetDefaultMemoryDevice)(const struct OrtEp* this_ptr);
+    /* Memory device the EP's inputs and outputs should live on; *device = NULL
+     * means CPU memory (rust/src/ep.rs:104-113 binds this exact type). */
+    OrtStatus* (*GetDefaultMemoryDevice)(const struct OrtEp* this_ptr,
+                                         const OrtMemoryDevice** device);
 } OrtEp;
 
 typedef struct OrtEpFactory {
@@ -247,6 +262,11 @@ typedef struct OrtEpFactory {
       (const OrtTensorTypeAndShapeInfo* info, size_t* out))                                      \
     X(65, GetTensorTypeAndShape, OrtStatus*, (const OrtValue* value,                             \
                                               OrtTensorTypeAndShapeInfo** out))                  \
+    X(68, CreateMemoryInfo, OrtStatus*,                                                          \
+      (const char* name, OrtAllocatorType type, int id, OrtMemType mem_type,                    \
+       OrtMemoryInfo** out))                                                                    \
+    X(71, MemoryInfoGetName, OrtStatus*, (const OrtMemoryInfo* info, const char** out))          \
+    X(72, MemoryInfoGetId, OrtStatus*, (const OrtMemoryInfo* info, int* out))                    \
     X(88, KernelContext_GetInputCount, OrtStatus*, (const OrtKernelContext* ctx, size_t* out))   \
     X(89, KernelContext_GetOutputCount, OrtStatus*, (const OrtKernelContext* ctx, size_t* out))  \
     X(90, KernelContext_GetInput, OrtStatus*,                                                    \
@@ -255,6 +275,7 @@ typedef struct OrtEpFactory {
       (OrtKernelContext * ctx, size_t index, const int64_t* dims, size_t dim_count,              \
        OrtValue** out))                                                                          \
     X(93, ReleaseStatus, void, (OrtStatus * status))                                             \
+    X(94, ReleaseMemoryInfo, void, (OrtMemoryInfo * info))                                       \
     X(99, ReleaseTensorTypeAndShapeInfo, void, (OrtTensorTypeAndShapeInfo * info))               \
     X(285, GetEpApi, const OrtEpApi*, (void))                                                    \
     X(286, HardwareDevice_Type, OrtHardwareDeviceType, (const OrtHardwareDevice* device))        \

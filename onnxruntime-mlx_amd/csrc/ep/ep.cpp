@@ -45,24 +45,47 @@ bool env_flag(const char* name) {
 }
 
 // ------------------------------------------------------------- allocator --
+// Name of the memory info whose allocator this EP hands out: HBM of the GPU
+// given by the memory info's id. Any other memory info gets no allocator (a null
+// OrtAllocator and a null status, the reference's answer for every memory info,
+// rust/src/factory.rs:221-235), so ORT keeps using its own.
+constexpr const char* kHbmMemoryInfoName = "MI355X_HBM";
+
 struct DeviceAllocator {
     OrtAllocator base;  // first member: an OrtAllocator* is a DeviceAllocator*
     const OrtMemoryInfo* info;
     int device;
 };
 
+// Runs `body` with `device` current and restores the caller's current device.
+template <typename F>
+bool on_device(int device, F&& body) {
+    int prev = -1;
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != device && hipSetDevice(device) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    const bool ok = body();
+    if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
+    return ok;
+}
+
 void* alloc_fn(OrtAllocator* self, size_t size) {
     auto* d = reinterpret_cast<DeviceAllocator*>(self);
     void* p = nullptr;
-    if (hipSetDevice(d->device) != hipSuccess) return nullptr;
-    if (hipMalloc(&p, size ? size : 1) != hipSuccess) {
+    on_device(d->device, [&] {
+        if (hipMalloc(&p, size ? size : 1) == hipSuccess) return true;
         (void)hipGetLastError();
-        return nullptr;
-    }
+        p = nullptr;
+        return false;
+    });
     return p;
 }
-void free_fn(OrtAllocator*, void* p) {
-    if (p) (void)hipFree(p);
+void free_fn(OrtAllocator* self, void* p) {
+    if (!p) return;
+    auto* d = reinterpret_cast<DeviceAllocator*>(self);
+    on_device(d->device, [&] { return hipFree(p) == hipSuccess; });
 }
 const OrtMemoryInfo* info_fn(const OrtAllocator* self) {
     return reinterpret_cast<const DeviceAllocator*>(self)->info;
@@ -221,9 +244,13 @@ void ep_release_infos(OrtEp*, OrtNodeComputeInfo** infos, size_t n) {
     for (size_t i = 0; i < n; ++i) delete reinterpret_cast<ComputeInfo*>(infos[i]);
 }
 
-const OrtMemoryDevice* ep_default_memory_device(const OrtEp*) {
-    return nullptr;  // CPU memory, as the reference (rust/src/ep.rs:104-113); inputs
-                     // already in HBM are used in place, host ones are staged.
+// CPU memory, as the reference (rust/src/ep.rs:104-113): ORT hands Compute host
+// buffers unless the caller binds device ones. Inputs already in HBM are used in
+// place; host inputs are staged, and host KV caches shared between past and
+// present get only their new rows written back (the plan's delta copy-out).
+OrtStatus* ep_default_memory_device(const OrtEp*, const OrtMemoryDevice** device) {
+    if (device) *device = nullptr;
+    return nullptr;
 }
 
 // ---------------------------------------------------------------- factory --
@@ -291,9 +318,28 @@ void f_release_ep(OrtEpFactory*, OrtEp* ep) { delete reinterpret_cast<Ep*>(ep); 
 OrtStatus* f_create_allocator(OrtEpFactory* p, const OrtMemoryInfo* info, const OrtKeyValuePairs*,
                               OrtAllocator** out) {
     Factory* f = F(p);
+    if (out) *out = nullptr;
     return guard(f->api, "CreateAllocator", [&] {
+        if (!out) fail("null allocator output", ORT_INVALID_ARGUMENT);
+        if (!info) return;
+        const char* name = nullptr;
+        check_ort(f->api, api::MemoryInfoGetName(f->api)(info, &name), "MemoryInfoGetName");
+        if (!name || std::strcmp(name, kHbmMemoryInfoName) != 0) return;  // not this EP's memory
+        int id = 0;
+        check_ort(f->api, api::MemoryInfoGetId(f->api)(info, &id), "MemoryInfoGetId");
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess) {
+            (void)hipGetLastError();
+            count = 0;
+        }
+        if (id < 0 || id >= count)
+            fail("memory info names GPU " + std::to_string(id) + ", but " +
+                     std::to_string(count) + " are visible",
+                 ORT_INVALID_ARGUMENT);
         auto* a = new DeviceAllocator();
         std::memset(&a->base, 0, sizeof(a->base));
+        // GetStats stays null: ORT's allocator wrapper calls it only when set, and
+        // this allocator keeps no statistics of its own.
         a->base.version = ORT_API_VERSION;
         a->base.Alloc = alloc_fn;
         a->base.Free = free_fn;
@@ -301,7 +347,7 @@ OrtStatus* f_create_allocator(OrtEpFactory* p, const OrtMemoryInfo* info, const 
         a->base.Reserve = reserve_fn;
         a->base.AllocOnStream = alloc_on_stream_fn;
         a->info = info;
-        a->device = 0;
+        a->device = id;
         *out = &a->base;
     });
 }

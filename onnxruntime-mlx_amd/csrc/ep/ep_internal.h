@@ -132,6 +132,11 @@ class Plan {
         // split partials [heads][splits][head + 2] (see the attention-merge rewrite).
         int64_t splits = 0;
         int64_t head = 0;
+        // Host-memory input: `ptr` is its device staging buffer and `host` the
+        // caller's buffer. lazy: the staging copy is left to the consumer (GQA
+        // past KV uploads only its valid rows).
+        const void* host = nullptr;
+        bool lazy = false;
         int64_t numel() const {
             int64_t n = 1;
             for (auto d : dims) n *= d;
@@ -163,6 +168,14 @@ class Plan {
     void* workspace(size_t bytes);
     Tensor& out_tensor(const std::string& name, int dtype, const std::vector<int64_t>& dims,
                        const OrtApi* api, OrtKernelContext* ctx);
+    // The caller's buffer of fused-node output `name` (host or device memory), or
+    // null when `name` is not a fused-node output.
+    void* output_buffer(const std::string& name, const std::vector<int64_t>& dims,
+                        const OrtApi* api, OrtKernelContext* ctx);
+    // Queue a device -> host copy of `rows` rows of `row_bytes` from each of
+    // `slabs` slabs (pitch `pitch` bytes on both sides) after the run's kernels.
+    void copy_out_rows(void* host, const void* dev, size_t pitch, size_t row_bytes, size_t rows,
+                       size_t slabs);
     void run_node(const NodeDesc& n, const OrtApi* api, OrtKernelContext* ctx);
     int32_t host_i32(const std::string& name);
     bool guards_hold(const std::vector<Guard>& guards) const;
@@ -184,6 +197,7 @@ class Plan {
     std::unique_ptr<DeviceBuffer> workspace_;
     std::vector<std::unique_ptr<DeviceBuffer>> stage_;   // per input: host-input staging
     std::vector<std::pair<const void*, bool>> devptr_;   // per input: last pointer, is device
+    std::vector<bool> lazy_input_;                      // per input: GQA past KV (staged lazily)
     std::mutex mu_;  // one Compute at a time per fused node (rust/src/ep.rs:1884-1889)
 
     // HIP-graph replay of a whole Compute. A run whose every launch is graph-safe

@@ -52,6 +52,21 @@ Plan::Plan(GraphIR sub, std::vector<std::string> inputs, std::vector<std::string
     check_hip(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
     for (size_t i = 0; i < outputs_.size(); ++i)
         if (!outputs_[i].empty()) output_index_[outputs_[i]] = (int)i;
+    // Past-KV inputs that only GroupQueryAttention reads are staged by its executor
+    // when they arrive in host memory: with present bound to the same host buffer,
+    // only the valid past rows go up and only the new rows come back.
+    lazy_input_.assign(inputs_.size(), false);
+    for (size_t i = 0; i < inputs_.size(); ++i) {
+        if (inputs_[i].empty()) continue;
+        int gqa_past = 0, other = 0;
+        for (const NodeDesc& n : sub_.nodes)
+            for (size_t k = 0; k < n.inputs.size(); ++k) {
+                if (n.inputs[k] != inputs_[i]) continue;
+                if (n.op == "GroupQueryAttention" && (k == 3 || k == 4)) ++gqa_past;
+                else ++other;
+            }
+        lazy_input_[i] = gqa_past == 1 && other == 0;
+    }
     // Constant initializers are copied to HBM once (the reference keeps a plan-owned
     // constant cache, rust/src/engine.rs:409-411).
     for (auto& kv : sub_.values) {
@@ -124,13 +139,36 @@ int32_t Plan::host_i32(const std::string& name) {
 }
 
 namespace {
+// A device -> host copy queued for the end of a run: `height` rows of `width`
+// bytes, `pitch` bytes apart on both sides (one row for a whole tensor).
 struct Staged {
     void* host;
-    void* dev;
-    size_t bytes;
+    const void* dev;
+    size_t pitch, width, height;
 };
 thread_local std::vector<Staged>* g_out_staging = nullptr;
 }  // namespace
+
+void* Plan::output_buffer(const std::string& name, const std::vector<int64_t>& dims,
+                          const OrtApi* a, OrtKernelContext* ctx) {
+    auto oi = output_index_.find(name);
+    if (oi == output_index_.end()) return nullptr;
+    OrtValue* ov = nullptr;
+    check_ort(a, api::KernelContext_GetOutput(a)(ctx, (size_t)oi->second, dims.data(), dims.size(),
+                                                 &ov),
+              "KernelContext_GetOutput");
+    void* p = nullptr;
+    check_ort(a, api::GetTensorMutableData(a)(ov, &p), "GetTensorMutableData");
+    outs_.push_back({(size_t)oi->second, dims, p});
+    return p;
+}
+
+void Plan::copy_out_rows(void* host, const void* dev, size_t pitch, size_t row_bytes,
+                         size_t rows, size_t slabs) {
+    if (capturing_) fail("host-memory output during graph capture");
+    capturable_ = false;
+    if (row_bytes && rows && slabs) g_out_staging->push_back({host, dev, pitch, row_bytes * rows, slabs});
+}
 
 Plan::Tensor& Plan::out_tensor(const std::string& name, int dtype,
                                const std::vector<int64_t>& dims, const OrtApi* a,
@@ -139,20 +177,12 @@ Plan::Tensor& Plan::out_tensor(const std::string& name, int dtype,
     t.dtype = dtype;
     t.dims = dims;
     const size_t bytes = (size_t)std::max<int64_t>(t.numel(), 0) * dtype_size(dtype);
-    auto oi = output_index_.find(name);
-    if (oi != output_index_.end()) {
-        OrtValue* ov = nullptr;
-        check_ort(a, api::KernelContext_GetOutput(a)(ctx, (size_t)oi->second, dims.data(),
-                                                     dims.size(), &ov),
-                  "KernelContext_GetOutput");
-        void* p = nullptr;
-        check_ort(a, api::GetTensorMutableData(a)(ov, &p), "GetTensorMutableData");
-        outs_.push_back({(size_t)oi->second, dims, p});
+    if (output_index_.count(name)) {
+        void* p = output_buffer(name, dims, a, ctx);
         if (bytes && !is_device_ptr(p)) {
-            if (capturing_) fail("host-memory output during graph capture");
-            capturable_ = false;
+            // Host-memory output: computed into the arena, copied out at the end.
             void* d = arena_alloc(bytes);
-            g_out_staging->push_back({p, d, bytes});
+            copy_out_rows(p, d, bytes, bytes, 1, 1);
             p = d;
         }
         t.ptr = p;
@@ -235,6 +265,7 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
     g_out_staging = &out_staging;
     if (stage_.size() < inputs_.size()) stage_.resize(inputs_.size());
     if (devptr_.size() < inputs_.size()) devptr_.resize(inputs_.size(), {nullptr, false});
+    if (lazy_input_.size() < inputs_.size()) lazy_input_.resize(inputs_.size(), false);
     std::vector<InputSig> sig(inputs_.size());
     for (size_t i = 0; i < inputs_.size(); ++i) {
         if (inputs_[i].empty()) continue;
@@ -270,9 +301,12 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
                 buf = device_alloc(std::max<size_t>(bytes, 256));
                 ++mem_epoch_;
             }
-            check_hip(hipMemcpyAsync(buf->ptr, p, bytes, hipMemcpyHostToDevice, stream_),
-                      "stage input");
             t.ptr = buf->ptr;
+            t.host = p;
+            t.lazy = lazy_input_[i];
+            if (!t.lazy)
+                check_hip(hipMemcpyAsync(buf->ptr, p, bytes, hipMemcpyHostToDevice, stream_),
+                          "stage input");
             // keep the host copy for scalar reads without a device round trip
             if (bytes == 4 && (et == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT32)) {
                 int32_t hv;
@@ -314,7 +348,8 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
     outs_.clear();
     for (const NodeDesc& n : sub_.nodes) run_node(n, a, ctx);
     for (const Staged& s : out_staging)
-        check_hip(hipMemcpyAsync(s.host, s.dev, s.bytes, hipMemcpyDeviceToHost, stream_),
+        check_hip(hipMemcpy2DAsync(s.host, s.pitch, s.dev, s.pitch, s.width, s.height,
+                                   hipMemcpyDeviceToHost, stream_),
                   "stage output");
     check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
     g_out_staging = nullptr;
@@ -458,11 +493,60 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         const int64_t half = cs ? cs->dims[1] : 0, max_pos = cs ? cs->dims[0] : 0;
         Tensor& O = out_tensor(outname(0), q.dtype, {B, S, H * hd}, a, ctx);
         void* optr = O.ptr;
-        void *prk, *prv;
-        if (!outname(1).empty()) prk = out_tensor(outname(1), q.dtype, {B, KV, pcap, hd}, a, ctx).ptr;
-        else prk = arena_alloc((size_t)(B * KV * pcap * hd) * dtype_size(q.dtype));
-        if (!outname(2).empty()) prv = out_tensor(outname(2), q.dtype, {B, KV, pcap, hd}, a, ctx).ptr;
-        else prv = arena_alloc((size_t)(B * KV * pcap * hd) * dtype_size(q.dtype));
+        void *prk = nullptr, *prv = nullptr;
+        const size_t es = dtype_size(q.dtype);
+        const std::vector<int64_t> pdims = {B, KV, pcap, hd};
+        // Host KV shared between past and present (present bound to the past's host
+        // buffer): the staging buffer is updated in place; only rows [0, valid_past)
+        // go up and only the S new rows of each (batch, kv head) slab come back, as
+        // the reference's delta write-back (rust/src/engine.rs:78-94, 1997-2093).
+        if (shared && pk && pv && pk->host && pv->host && !outname(1).empty() &&
+            !outname(2).empty()) {
+            void* hk = output_buffer(outname(1), pdims, a, ctx);
+            void* hv = output_buffer(outname(2), pdims, a, ctx);
+            if (hk == pk->host && hv == pv->host) {
+                const size_t pitch = (size_t)cap * hd * es;
+                for (Tensor* t : {pk, pv}) {
+                    if (t->lazy && vpast > 0)
+                        check_hip(hipMemcpy2DAsync(t->ptr, pitch, t->host, pitch,
+                                                   (size_t)vpast * hd * es, (size_t)(B * KV),
+                                                   hipMemcpyHostToDevice, stream_),
+                                  "stage past rows");
+                    t->lazy = false;
+                    copy_out_rows(static_cast<char*>(const_cast<void*>(t->host)) + vpast * hd * es,
+                                  static_cast<char*>(t->ptr) + vpast * hd * es, pitch, hd * es,
+                                  (size_t)S, (size_t)(B * KV));
+                }
+                prk = pk->ptr;
+                prv = pv->ptr;
+                pkp = prk;
+                pvp = prv;
+                for (int j = 1; j <= 2; ++j) {
+                    Tensor t;
+                    t.ptr = j == 1 ? prk : prv;
+                    t.dtype = q.dtype;
+                    t.dims = pdims;
+                    env_[outname(j)] = t;
+                }
+            } else {
+                // Not aliased: drop the two records; out_tensor below fetches the
+                // outputs again and stages them whole.
+                outs_.resize(outs_.size() - 2);
+            }
+        }
+        for (Tensor* t : {pk, pv})
+            if (t && t->lazy) {  // any other host past: the whole buffer goes up
+                check_hip(hipMemcpyAsync(t->ptr, t->host, (size_t)t->numel() * es,
+                                         hipMemcpyHostToDevice, stream_),
+                          "stage past");
+                t->lazy = false;
+            }
+        if (!prk) {
+            if (!outname(1).empty()) prk = out_tensor(outname(1), q.dtype, pdims, a, ctx).ptr;
+            else prk = arena_alloc((size_t)(B * KV * pcap * hd) * es);
+            if (!outname(2).empty()) prv = out_tensor(outname(2), q.dtype, pdims, a, ctx).ptr;
+            else prv = arena_alloc((size_t)(B * KV * pcap * hd) * es);
+        }
         const float scale = n.attr_float("scale", 0.f);
         const int32_t inter = (int32_t)n.attr_int("rotary_interleaved", 0);
         // One-token decode into a shared buffer written in place: the capturable
@@ -549,9 +633,19 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
                          n.attr_float("scale", 0.f), kdt(q.dtype), workspace_->ptr,
                          workspace_->bytes, st),
                      "PagedAttention");
-        // Updated caches: written in place (rust/src/engine.rs:823-847); outputs 1/2,
-        // when requested, receive the same contents.
+        // Updated caches: written in place (rust/src/engine.rs:823-847,
+        // rust/src/ops/attention.rs:2728-2742). A cache that arrived in host memory
+        // was updated in its device staging copy, which goes back to the caller's
+        // buffer after the run. Outputs 1/2, when requested, receive the same
+        // contents.
         const Tensor* caches[2] = {&kc, vc};
+        for (int i = 0; i < 2; ++i) {
+            if (caches[i] && caches[i]->host) {
+                const size_t bytes = (size_t)caches[i]->numel() * dtype_size(caches[i]->dtype);
+                copy_out_rows(const_cast<void*>(caches[i]->host), caches[i]->ptr, bytes, bytes,
+                              1, 1);
+            }
+        }
         for (int i = 0; i < 2; ++i) {
             if (outname(1 + i).empty() || !caches[i]) continue;
             Tensor& oc = out_tensor(outname(1 + i), caches[i]->dtype, caches[i]->dims, a, ctx);

@@ -8,7 +8,9 @@
 // does (the reference's call sequence: rust/src/lib.rs:90-155,
 // rust/src/factory.rs:116-213, rust/src/ep.rs:119-357, 928-1211, 1931-2134).
 // Graphs must be claimed completely: there is no CPU execution provider here.
-// Every tensor the harness hands to Compute lives in HBM (hipMalloc).
+// Tensors handed to Compute are whatever the caller binds: device memory (the
+// IOBinding case) or host memory (what ORT hands an EP whose default memory
+// device is the CPU); outputs the caller does not bind are hipMalloc'd.
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
@@ -86,6 +88,12 @@ struct OrtKernelContext {
 struct OrtNodeComputeContext {
     std::string name;
 };
+struct OrtMemoryInfo {
+    std::string name;
+    OrtAllocatorType type = OrtDeviceAllocator;
+    int id = 0;
+    OrtMemType mem_type = OrtMemTypeDefault;
+};
 
 namespace {
 
@@ -137,6 +145,21 @@ OrtStatus* h_GetTensorTypeAndShape(const OrtValue* v, OrtTensorTypeAndShapeInfo*
     return nullptr;
 }
 void h_ReleaseTensorTypeAndShapeInfo(OrtTensorTypeAndShapeInfo* t) { delete t; }
+OrtStatus* h_CreateMemoryInfo(const char* name, OrtAllocatorType type, int id, OrtMemType mem_type,
+                              OrtMemoryInfo** out) {
+    if (!name || !out) return mk(ORT_INVALID_ARGUMENT, "CreateMemoryInfo: null argument");
+    *out = new OrtMemoryInfo{name, type, id, mem_type};
+    return nullptr;
+}
+OrtStatus* h_MemoryInfoGetName(const OrtMemoryInfo* m, const char** out) {
+    *out = m->name.c_str();
+    return nullptr;
+}
+OrtStatus* h_MemoryInfoGetId(const OrtMemoryInfo* m, int* out) {
+    *out = m->id;
+    return nullptr;
+}
+void h_ReleaseMemoryInfo(OrtMemoryInfo* m) { delete m; }
 OrtStatus* h_KernelContext_GetInputCount(const OrtKernelContext* c, size_t* out) {
     *out = c->inputs.size();
     return nullptr;
@@ -319,6 +342,12 @@ OrtApiBase g_api_base{get_api, get_version_string};
 
 ORTMI_ORT_API_SLOTS(CHECK_SIG)
 ORTMI_ORT_EP_API_SLOTS(CHECK_EP_SIG)
+
+// The OrtEp slot the reference binds as
+// fn(*const OrtEp, *mut *const OrtMemoryDevice) -> *mut OrtStatus (rust/src/ep.rs:104-113).
+static_assert(std::is_same<decltype(OrtEp::GetDefaultMemoryDevice),
+                           OrtStatus* (*)(const OrtEp*, const OrtMemoryDevice**)>::value,
+              "OrtEp::GetDefaultMemoryDevice must return a status and take an out-parameter");
 
 // ------------------------------------------------------------------ graph --
 struct HxGraph {
@@ -694,6 +723,94 @@ int hx_session_run(Session* s) {
             return 1;
         }
     return 0;
+}
+
+// OrtEp::GetDefaultMemoryDevice: 0 on success with *is_cpu = 1 when the EP
+// reports CPU memory (a null OrtMemoryDevice).
+int hx_session_default_memory_device(Session* s, int* is_cpu) {
+    const OrtMemoryDevice* dev = reinterpret_cast<const OrtMemoryDevice*>(&g_err);  // poison
+    if (!s->ep->GetDefaultMemoryDevice) {
+        g_err = "GetDefaultMemoryDevice is not set";
+        return 1;
+    }
+    if (!take(s->ep->GetDefaultMemoryDevice(s->ep, &dev), "GetDefaultMemoryDevice")) return 1;
+    *is_cpu = dev == nullptr ? 1 : 0;
+    return 0;
+}
+
+// OrtEpFactory::CreateAllocator for a memory info (name, id), as ORT calls it for
+// the memory infos an EP device registers. Returns -1 on error, 0 when the EP
+// hands out no allocator, 1 when it does: then the allocator is exercised (Info,
+// Alloc of `bytes` device bytes checked by a fill and copy-back, Reserve, Free)
+// and released through ReleaseAllocator.
+int hx_factory_allocator_check(Session* s, const char* mem_name, int id, size_t bytes) {
+    OrtMemoryInfo* info = nullptr;
+    if (!take(h_CreateMemoryInfo(mem_name, OrtDeviceAllocator, id, OrtMemTypeDefault, &info),
+              "CreateMemoryInfo"))
+        return -1;
+    std::unique_ptr<OrtMemoryInfo> hold(info);
+    OrtAllocator* a = reinterpret_cast<OrtAllocator*>(&g_err);  // poison: the EP must write it
+    if (!take(s->factory->CreateAllocator(s->factory, info, nullptr, &a), "CreateAllocator"))
+        return -1;
+    if (!a) return 0;
+    auto fail_with = [&](const std::string& m) {
+        g_err = m;
+        s->factory->ReleaseAllocator(s->factory, a);
+        return -1;
+    };
+    if (a->version < 18 || !a->Alloc || !a->Free || !a->Info)
+        return fail_with("allocator lacks Alloc/Free/Info or reports version < 18");
+    if (a->Info(a) != info) return fail_with("allocator Info() is not the memory info it was made for");
+    void* p = a->Alloc(a, bytes);
+    if (!p) return fail_with("Alloc returned null");
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess || attr.type != hipMemoryTypeDevice ||
+        attr.device != id) {
+        (void)hipGetLastError();
+        a->Free(a, p);
+        return fail_with("Alloc did not return device memory of GPU " + std::to_string(id));
+    }
+    std::vector<uint8_t> back(bytes, 0);
+    bool ok = hipMemset(p, 0x5A, bytes) == hipSuccess &&
+              hipMemcpy(back.data(), p, bytes, hipMemcpyDeviceToHost) == hipSuccess;
+    for (size_t i = 0; ok && i < bytes; ++i) ok = back[i] == 0x5A;
+    a->Free(a, p);
+    if (!ok) return fail_with("allocated memory did not hold a fill pattern");
+    if (a->Reserve) {
+        void* r = a->Reserve(a, bytes);
+        if (!r) return fail_with("Reserve returned null");
+        a->Free(a, r);
+    }
+    s->factory->ReleaseAllocator(s->factory, a);
+    return 1;
+}
+
+// OrtEpFactory::CreateDataTransfer + CanCopy + CopyTensors of one tensor
+// (src and dst host or device pointers of the same dtype and shape), then Release.
+int hx_factory_data_transfer_copy(Session* s, void* src, void* dst, int dtype, int rank,
+                                  const int64_t* dims) {
+    OrtDataTransferImpl* dt = nullptr;
+    if (!take(s->factory->CreateDataTransfer(s->factory, &dt), "CreateDataTransfer")) return 1;
+    if (!dt || !dt->CopyTensors || !dt->Release || !dt->CanCopy) {
+        g_err = "CreateDataTransfer returned an incomplete OrtDataTransferImpl";
+        return 1;
+    }
+    if (!dt->CanCopy(dt, nullptr, nullptr)) {
+        dt->Release(dt);
+        g_err = "CanCopy refused a CPU <-> CPU copy";
+        return 1;
+    }
+    OrtValue a, b;
+    a.data = src;
+    b.data = dst;
+    a.info.dtype = b.info.dtype = dtype;
+    a.info.dims.assign(dims, dims + rank);
+    b.info.dims = a.info.dims;
+    const OrtValue* srcs[1] = {&a};
+    OrtValue* dsts[1] = {&b};
+    const bool ok = take(dt->CopyTensors(dt, srcs, dsts, nullptr, 1), "CopyTensors");
+    dt->Release(dt);
+    return ok ? 0 : 1;
 }
 
 int hx_session_get_output(Session* s, const char* name, void** ptr, int* rank, int64_t* dims) {

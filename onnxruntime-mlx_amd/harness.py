@@ -2,8 +2,10 @@
 
 The harness stands in for ONNX Runtime's plugin loader: it builds a graph, loads
 the EP library through CreateEpFactories and drives GetCapability / Compile /
-Compute over the plugin C ABI. Tensors handed to Compute live in HBM (torch
-device tensors or harness-allocated buffers).
+Compute over the plugin C ABI. Tensors handed to Compute are the caller's torch
+tensors, on the device (the IOBinding case) or in host memory (what ONNX Runtime
+hands an EP whose default memory device is the CPU); unbound outputs are
+harness-allocated device buffers.
 """
 
 from __future__ import annotations
@@ -56,6 +58,10 @@ def lib() -> ctypes.CDLL:
             "hx_session_run": (ctypes.c_int, [vp]),
             "hx_session_get_output": (ctypes.c_int, [vp, cp, ctypes.POINTER(vp),
                                                      ctypes.POINTER(ctypes.c_int), i64p]),
+            "hx_session_default_memory_device": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_int)]),
+            "hx_factory_allocator_check": (ctypes.c_int, [vp, cp, ctypes.c_int, ctypes.c_size_t]),
+            "hx_factory_data_transfer_copy": (ctypes.c_int, [vp, vp, vp, ctypes.c_int,
+                                                             ctypes.c_int, i64p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -163,6 +169,29 @@ class Session:
         for name, (t, dt) in feeds.items():
             self.set_input(name, t, dt)
         if lib().hx_session_run(self.h):
+            raise RuntimeError(_err())
+
+    def default_memory_device_is_cpu(self) -> bool:
+        """OrtEp::GetDefaultMemoryDevice: True when the EP reports CPU memory."""
+        flag = ctypes.c_int(-1)
+        if lib().hx_session_default_memory_device(self.h, ctypes.byref(flag)):
+            raise RuntimeError(_err())
+        return bool(flag.value)
+
+    def allocator_check(self, memory_info_name: str, device_id: int = 0, nbytes: int = 1 << 20):
+        """OrtEpFactory::CreateAllocator for (name, id): None when the EP gives no
+        allocator, True when it gave one that allocated, filled and freed HBM."""
+        rc = lib().hx_factory_allocator_check(self.h, memory_info_name.encode(), device_id, nbytes)
+        if rc < 0:
+            raise RuntimeError(_err())
+        return True if rc == 1 else None
+
+    def data_transfer_copy(self, src, dst, dtype):
+        """OrtEpFactory::CreateDataTransfer + CopyTensors of one tensor (torch tensors,
+        host or device, same shape)."""
+        if lib().hx_factory_data_transfer_copy(self.h, ctypes.c_void_p(src.data_ptr()),
+                                               ctypes.c_void_p(dst.data_ptr()), dtype, src.dim(),
+                                               _dims(src.shape)):
             raise RuntimeError(_err())
 
     def output(self, name):

@@ -289,3 +289,32 @@ def test_decoder_graph_fully_claimed_as_one_fused_node():
     assert len(parts[0]) == g.n_nodes
     # the ops of one layer: 2 norms, 7 MatMulNBits, GQA, Sigmoid + 2 Mul
     assert g.n_nodes == 1 + cfg.layers * 13 + 2
+
+
+def test_default_memory_device_slot_matches_reference_binding():
+    """OrtEp::GetDefaultMemoryDevice is bound by the reference as
+    fn(*const OrtEp, *mut *const OrtMemoryDevice) -> *mut OrtStatus
+    (rust/src/ep.rs:104-113): a status return and an out-parameter."""
+    import os
+    import re
+
+    text = open(os.path.join(os.path.dirname(pkg.EP_LIB), "..", "..", "include",
+                             "ort_plugin_ep_abi.h")).read()
+    m = re.search(r"(\w+\s*\*)\s*\(\*GetDefaultMemoryDevice\)\(([^)]*)\)", text)
+    assert m, "GetDefaultMemoryDevice slot missing from the OrtEp declaration"
+    ret, params = m.group(1).replace(" ", ""), " ".join(m.group(2).split())
+    assert ret == "OrtStatus*"
+    assert params == "const struct OrtEp* this_ptr, const OrtMemoryDevice** device"
+
+
+def test_default_memory_device_is_cpu_and_foreign_allocators_declined():
+    """The EP reports CPU memory as its default device (the reference's answer) and
+    hands out no allocator for a memory info that is not its own."""
+    g = hx.Graph()
+    mnb_node(g, "x", "y", 64, 64, "l")
+    g.value("x", F16, [1, -1, 64])
+    g.io(["x"], ["y"])
+    s = session(g)
+    assert s.default_memory_device_is_cpu()
+    assert s.allocator_check("Cpu", 0) is None
+    assert s.allocator_check("Cuda", 0) is None

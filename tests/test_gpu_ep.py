@@ -327,3 +327,185 @@ def test_ep_decoder_fusions_match_unfused(ortmi, dec, monkeypatch):
     for a, b in zip(fl, ul):
         assert np.abs(a - b).max() <= 0.02 * max(1.0, np.abs(b).max())
     assert ft == ut
+
+
+# ------------------------------------------------------------- boundary slots --
+
+def _one_node_mnb_graph(hx, rng, N=256, K=512):
+    A, B, s, zp = _mnb_inputs(rng, 1, N, K, 32, dtype=np.float16)
+    g = hx.Graph()
+    g.value("x", hx.FLOAT16, [1, 1, K])
+    g.value("y", hx.FLOAT16, [1, 1, N])
+    g.initializer("B", B)
+    g.initializer("s", s)
+    g.initializer("zp", zp)
+    g.node("MatMulNBits", ["x", "B", "s", "zp"], ["y"], domain="com.microsoft", K=K, N=N, bits=4,
+           block_size=32)
+    g.io(["x"], ["y"])
+    return g, (A, B, s, zp, N, K)
+
+
+def test_ep_memory_device_allocator_and_data_transfer(ortmi, hx):
+    """GetDefaultMemoryDevice reports CPU memory; CreateAllocator hands out an HBM
+    allocator only for the EP's own memory info (MI355X_HBM, a visible GPU id), whose
+    Alloc/Reserve/Free/Info work; CreateDataTransfer copies host<->device and
+    device<->device bit for bit."""
+    import torch
+
+    g, _ = _one_node_mnb_graph(hx, np.random.default_rng(1))
+    sess = hx.Session(g)
+    assert sess.default_memory_device_is_cpu()
+    assert sess.allocator_check("MI355X_HBM", 0, 3 << 20) is True
+    assert sess.allocator_check("Cpu", 0) is None
+    with pytest.raises(RuntimeError, match="GPU 4096"):
+        sess.allocator_check("MI355X_HBM", 4096)
+    src = torch.arange(3 * 5 * 7, dtype=torch.float32).reshape(3, 5, 7) * 0.25 - 9
+    d1 = torch.empty_like(src, device="cuda")
+    d2 = torch.empty_like(d1)
+    back = torch.empty_like(src)
+    sess.data_transfer_copy(src, d1, hx.FLOAT)    # host -> device
+    sess.data_transfer_copy(d1, d2, hx.FLOAT)     # device -> device
+    sess.data_transfer_copy(d2, back, hx.FLOAT)   # device -> host
+    torch.cuda.synchronize()
+    assert torch.equal(back, src)
+
+
+def test_ep_host_memory_input_and_output(ortmi, oracle, hx):
+    """Host-memory input and output buffers (what ORT hands an EP whose default
+    memory device is the CPU): the input is staged to HBM, the result copied back
+    into the caller's host buffer, identical to the device-bound run."""
+    import torch
+
+    g, (A, B, s, zp, N, K) = _one_node_mnb_graph(hx, np.random.default_rng(2))
+    sess = hx.Session(g)
+    x_host = torch.from_numpy(A.reshape(1, 1, K).copy())
+    y_host = torch.full((1, 1, N), float("nan"), dtype=torch.float16)
+    sess.bind_output("y", y_host)
+    sess.run({"x": (x_host, hx.FLOAT16)})
+    y_dev = torch.empty((1, 1, N), dtype=torch.float16, device="cuda")
+    sess.bind_output("y", y_dev)
+    sess.run({"x": (x_host.cuda(), hx.FLOAT16)})
+    torch.cuda.synchronize()
+    assert torch.equal(y_host, y_dev.cpu())
+    assert_f16_close(y_host.float().numpy().reshape(1, N), oracle.mnb_matmul(A, B, s, zp, N, K),
+                     what="host-memory MatMulNBits")
+
+
+def _gqa_graph(hx, H, KV, hd, cap, cos, sin):
+    g = hx.Graph()
+    g.value("q", hx.FLOAT16, [1, -1, H * hd])
+    g.value("k", hx.FLOAT16, [1, -1, KV * hd])
+    g.value("v", hx.FLOAT16, [1, -1, KV * hd])
+    for n in ("pk", "pv", "ok", "ov"):
+        g.value(n, hx.FLOAT16, [1, KV, cap, hd])
+    g.value("sl", hx.INT32, [1])
+    g.value("tot", hx.INT32, [1])
+    g.value("o", hx.FLOAT16, [1, -1, H * hd])
+    g.initializer("cos", cos)
+    g.initializer("sin", sin)
+    g.node("GroupQueryAttention", ["q", "k", "v", "pk", "pv", "sl", "tot", "cos", "sin"],
+           ["o", "ok", "ov"], domain="com.microsoft", num_heads=H, kv_num_heads=KV, do_rotary=1)
+    g.io(["q", "k", "v", "pk", "pv", "sl", "tot"], ["o", "ok", "ov"])
+    return g
+
+
+def test_ep_gqa_host_kv_delta_write_back(ortmi, hx):
+    """A KV cache in host memory shared by past and present (the reference's
+    shared-buffer contract with a CPU-memory EP): a 5-token prompt then 6 decode
+    steps give outputs and cache contents identical to the same steps over device
+    buffers, and the rows past the live length keep the caller's sentinel (only
+    the new rows are written back)."""
+    import refs
+    import torch
+
+    H, KV, hd, cap = 12, 2, 128, 48
+    c, s_ = refs.rotary_caches(256, hd, 1e6)
+    cos, sin = c.astype(np.float16), s_.astype(np.float16)
+    rng = np.random.default_rng(12)
+    steps = [5] + [1] * 6
+    feeds = [tuple(rng.standard_normal((1, S, n * hd)).astype(np.float16) for n in (H, KV, KV))
+             for S in steps]
+    sentinel = np.float16(-7.5)
+
+    def run(on_device):
+        sess = hx.Session(_gqa_graph(hx, H, KV, hd, cap, cos, sin))
+        kc = torch.full((1, KV, cap, hd), float(sentinel), dtype=torch.float16)
+        vc = torch.full_like(kc, float(sentinel))
+        if on_device:
+            kc, vc = kc.cuda(), vc.cuda()
+        sess.bind_output("ok", kc)
+        sess.bind_output("ov", vc)
+        outs, total = [], 0
+        for (q, k, v), S in zip(feeds, steps):
+            total += S
+            o = torch.empty((1, S, H * hd), dtype=torch.float16,
+                            device="cuda" if on_device else "cpu")
+            sess.bind_output("o", o)
+            t = (lambda a: torch.from_numpy(a).cuda()) if on_device else torch.from_numpy
+            sess.run({"q": (t(q), hx.FLOAT16), "k": (t(k), hx.FLOAT16),
+                      "v": (t(v), hx.FLOAT16), "pk": (kc, hx.FLOAT16), "pv": (vc, hx.FLOAT16),
+                      "sl": (torch.tensor([total - 1], dtype=torch.int32), hx.INT32),
+                      "tot": (torch.tensor([total], dtype=torch.int32), hx.INT32)})
+            torch.cuda.synchronize()
+            outs.append(o.cpu().clone())
+        sess.close()
+        return outs, kc.cpu(), vc.cpu(), total
+
+    dev_outs, dk, dv, total = run(True)
+    host_outs, hk, hv, _ = run(False)
+    for a, b in zip(host_outs, dev_outs):
+        assert torch.equal(a, b)
+    assert torch.equal(hk, dk) and torch.equal(hv, dv)
+    assert (hk[:, :, total:] == float(sentinel)).all() and (hv[:, :, total:] == float(sentinel)).all()
+    assert not (hk[:, :, :total] == float(sentinel)).all()
+
+
+def test_ep_paged_attention_host_caches_written_back(ortmi, oracle, hx):
+    """PagedAttention through the EP with its caches in host memory: the new K/V
+    rows land in the caller's cache buffers (in place, as the reference writes
+    them back, rust/src/ops/attention.rs:2728-2742), and output and caches equal
+    the oracle's over two consecutive calls."""
+    import torch
+
+    rng = np.random.default_rng(90)
+    H, KV, d, blk, batch = 8, 2, 64, 4, 3
+    maxb = 6
+    nb = maxb * batch
+    g = hx.Graph()
+    g.value("q", hx.FLOAT16, [-1, H * d])
+    g.value("k", hx.FLOAT16, [-1, KV * d])
+    g.value("v", hx.FLOAT16, [-1, KV * d])
+    g.value("kc", hx.FLOAT16, [nb, blk, KV, d])
+    g.value("vc", hx.FLOAT16, [nb, blk, KV, d])
+    g.value("cum", hx.INT32, [batch + 1])
+    g.value("past", hx.INT32, [batch])
+    g.value("bt", hx.INT32, [batch, maxb])
+    g.value("o", hx.FLOAT16, [-1, H * d])
+    g.node("PagedAttention", ["q", "k", "v", "kc", "vc", "cum", "past", "bt"], ["o"],
+           domain="com.microsoft", num_heads=H, kv_num_heads=KV)
+    g.io(["q", "k", "v", "kc", "vc", "cum", "past", "bt"], ["o"])
+    sess = hx.Session(g)
+    assert sess.partitions() == [[0]]
+    kc = torch.from_numpy(rng.standard_normal((nb, blk, KV, d)).astype(np.float16))
+    vc = torch.from_numpy(rng.standard_normal((nb, blk, KV, d)).astype(np.float16))
+    bt = rng.permutation(nb).astype(np.int32).reshape(batch, maxb)
+    ref_k, ref_v = kc.float().numpy(), vc.float().numpy()
+    past = np.array([3, 0, 10], np.int32)
+    for call, new in enumerate(([4, 5, 1], [1, 1, 1])):
+        new = np.array(new, np.int32)
+        cum = np.concatenate([[0], np.cumsum(new)]).astype(np.int32)
+        nt = int(cum[-1])
+        q, k, v = (rng.standard_normal((nt, n * d)).astype(np.float16) for n in (H, KV, KV))
+        o = torch.empty((nt, H * d), dtype=torch.float16)
+        sess.bind_output("o", o)
+        tt = torch.from_numpy
+        sess.run({"q": (tt(q), hx.FLOAT16), "k": (tt(k), hx.FLOAT16), "v": (tt(v), hx.FLOAT16),
+                  "kc": (kc, hx.FLOAT16), "vc": (vc, hx.FLOAT16), "cum": (tt(cum), hx.INT32),
+                  "past": (tt(past), hx.INT32), "bt": (tt(bt), hx.INT32)})
+        torch.cuda.synchronize()
+        ro, ref_k, ref_v = oracle.paged_attention(q, k, v, ref_k, ref_v, cum, past, bt, H, KV)
+        ref_k, ref_v = oracle.round_f16(ref_k), oracle.round_f16(ref_v)
+        assert_f16_close(o.float().numpy(), ro, what=f"host-cache PagedAttention call {call}")
+        np.testing.assert_array_equal(kc.float().numpy(), ref_k)
+        np.testing.assert_array_equal(vc.float().numpy(), ref_v)
+        past = past + new
