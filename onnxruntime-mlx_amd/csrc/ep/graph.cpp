@@ -291,6 +291,21 @@ std::string claim_gqa(const NodeDesc& n, const GraphIR& g) {
     const bool packed = !n.has_input(1) && !n.has_input(2);
     REQUIRE(packed || (n.has_input(1) && n.has_input(2)), "key and value must both be given");
     REQUIRE(n.has_input(3) == n.has_input(4), "past_key and past_value must both be given");
+    // Head size from the query width (attention.rs:1667-1683 for the packed form):
+    // the kernels take 64 or 128, so anything else is declined here rather than
+    // failing at Compute with no CPU fallback.
+    REQUIRE(q->dims[2] > 0, "query hidden size must be known");
+    const int64_t qheads = packed ? H + 2 * KV : H;
+    REQUIRE(q->dims[2] % qheads == 0,
+            packed ? "packed QKV hidden size must be divisible by total heads"
+                   : "query hidden size must be divisible by num_heads");
+    const int64_t qhd = q->dims[2] / qheads;
+    REQUIRE(qhd == 64 || qhd == 128, "head_size must be 64 or 128");
+    if (!packed) {
+        auto* k = val(g, n, 1);
+        REQUIRE(k && k->has_shape && k->dims.size() == 3 && k->dims[2] == KV * qhd,
+                "key hidden size must be kv_num_heads * head_size");
+    }
     auto* seq = val(g, n, 5);
     auto* tot = val(g, n, 6);
     REQUIRE(seq && seq->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT32, "seqlens_k must be int32");
@@ -299,9 +314,11 @@ std::string claim_gqa(const NodeDesc& n, const GraphIR& g) {
     if (n.has_input(3)) {
         auto* pk = val(g, n, 3);
         REQUIRE(pk && pk->has_shape && pk->dims.size() == 4, "past_key must be rank 4");
-        const int64_t hd = pk->dims[3];
-        REQUIRE(hd == 64 || hd == 128, "head_size must be 64 or 128");
+        REQUIRE(pk->dims[3] == qhd && pk->dims[1] == KV,
+                "past_key must be [batch, kv_num_heads, capacity, head_size]");
     }
+    // do_rotary defaults to 0 as in ORT's contrib-op schema and CPU kernel (the
+    // parity target); the reference defaults it to 1 (attention.rs:1547).
     const bool rotary = n.attr_int("do_rotary", 0) != 0;
     REQUIRE(!rotary || (n.has_input(7) && n.has_input(8)), "do_rotary needs cos/sin caches");
     REQUIRE(!n.has_input(9), "custom position_ids are not supported");

@@ -318,3 +318,32 @@ def test_default_memory_device_is_cpu_and_foreign_allocators_declined():
     assert s.default_memory_device_is_cpu()
     assert s.allocator_check("Cpu", 0) is None
     assert s.allocator_check("Cuda", 0) is None
+
+
+@pytest.mark.parametrize("qwidth,packed,claimed", [
+    (4 * 128, False, True),
+    (4 * 128 + 8, False, False),        # query width not a multiple of num_heads
+    (4 * 96, False, False),             # head size 96 has no kernel
+    ((4 + 2 * 2) * 64, True, True),     # packed QKV, head size 64
+    ((4 + 2 * 2) * 64 + 2, True, False),
+])
+def test_gqa_claim_checks_head_size_without_past(qwidth, packed, claimed):
+    """Without past inputs the head size comes from the query width and the head
+    counts (rust/src/ops/attention.rs:1667-1683): a width that does not divide, or
+    a head size the kernels lack, is declined at claim time instead of failing in
+    Compute."""
+    H, KV = 4, 2
+    g = hx.Graph()
+    g.value("q", F16, [1, 7, qwidth])
+    hd = qwidth // (H + 2 * KV) if packed else qwidth // H
+    if not packed:
+        g.value("k", F16, [1, 7, KV * hd])
+        g.value("v", F16, [1, 7, KV * hd])
+    g.value("sl", I32, [1])
+    g.value("tot", I32, [1])
+    g.value("o", F16, [1, 7, H * hd])
+    ins = ["q", "", "", "", "", "sl", "tot"] if packed else ["q", "k", "v", "", "", "sl", "tot"]
+    g.node("GroupQueryAttention", ins, ["o"], domain="com.microsoft", num_heads=H,
+           kv_num_heads=KV, do_rotary=0)
+    g.io([n for n in ins if n], ["o"])
+    assert session(g).claimed(0) is claimed
