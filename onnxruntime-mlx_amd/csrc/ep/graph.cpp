@@ -367,6 +367,17 @@ std::string claim_paged(const NodeDesc& n, const GraphIR& g) {
         REQUIRE(sm && sm->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT32, "slot_mapping must be int32");
     }
     REQUIRE(n.has_input(12) == n.has_input(13), "q/k norm weights must both be given");
+    if (n.attr_int("do_rotary", 0) != 0) {
+        // attention.rs:2898-2918
+        auto *c = val(g, n, 8), *s = val(g, n, 9);
+        REQUIRE(c && s && c->dtype == q->dtype && s->dtype == q->dtype,
+                "do_rotary=1 requires cos_cache and sin_cache in the output dtype");
+        REQUIRE(c->has_shape && c->dims.size() == 2 && c->dims[1] > 0,
+                "cos_cache must be [max_position, rotary_dim / 2]");
+        const int64_t off = n.attr_int("rotary_offset", 0);
+        REQUIRE(off + 2 * c->dims[1] <= hd, "rotary_offset + rotary_dim must not exceed head_size");
+        REQUIRE(off % 8 == 0, "rotary_offset must be a multiple of 8");
+    }
     return "";
 }
 

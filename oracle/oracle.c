@@ -98,6 +98,7 @@ int orc_mnb_dequant(const uint8_t* B, const float* scales, const uint8_t* zp, in
     if (bits != 4 && bits != 8) return -1;
     if (block <= 0 || (block * bits) % 8) return -1;
     int64_t nb = (K + block - 1) / block;
+#pragma omp parallel for schedule(static)
     for (int64_t n = 0; n < N; ++n)
         for (int64_t k = 0; k < K; ++k) {
             int64_t b = k / block;
@@ -211,11 +212,18 @@ static void attend_row(const float* qv, int hd, const float* const* krows,
         denom += scores[j];
     }
     if (sink) denom += exp((double)*sink - mx);
-    for (int d = 0; d < vhd; ++d) {
-        double acc = 0.0;
-        for (int j = 0; j < nk; ++j) acc += scores[j] * (double)vrows[j][d];
-        out[d] = (float)(acc / denom);
+    /* Each out[d] sums scores[j] * v[j][d] over j in ascending order (keys past
+     * `last` carry weight 0 and are skipped); j runs in the outer loop so the V
+     * rows are read contiguously. */
+    double acc[512];
+    for (int d = 0; d < vhd; ++d) acc[d] = 0.0;
+    const int nj = last + 1 < nk ? last + 1 : nk;
+    for (int j = 0; j < nj; ++j) {
+        const double w = scores[j];
+        const float* vr = vrows[j];
+        for (int d = 0; d < vhd; ++d) acc[d] += w * (double)vr[d];
     }
+    for (int d = 0; d < vhd; ++d) out[d] = (float)(acc[d] / denom);
 }
 
 /* ---------------------------------------------------------------- GQA --- */
@@ -239,7 +247,7 @@ int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
             const float* past_v, int64_t cap, int total_seq_len, const float* cos_c,
             const float* sin_c, int half, int interleaved, int B, int S, int H, int KV, int hd,
             float scale, int round16, float* out, float* present_k, float* present_v) {
-    if (H <= 0 || KV <= 0 || H % KV || hd <= 0 || S <= 0) return -1;
+    if (H <= 0 || KV <= 0 || H % KV || hd <= 0 || hd > 512 || S <= 0) return -1;
     if (cos_c && 2 * half > hd) return -1;
     int vp;
     int64_t pcap;
@@ -255,9 +263,6 @@ int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
 
     float* qr = (float*)malloc(sizeof(float) * (size_t)hd);
     float* kr = (float*)malloc(sizeof(float) * (size_t)hd);
-    double* scores = (double*)malloc(sizeof(double) * (size_t)(pcap + 1));
-    const float** kp = (const float**)malloc(sizeof(float*) * (size_t)(pcap + 1));
-    const float** vptr = (const float**)malloc(sizeof(float*) * (size_t)(pcap + 1));
 
     /* present = past (growing: rows [0,cap); shared: the whole buffer). */
     for (int b = 0; b < B; ++b)
@@ -290,32 +295,45 @@ int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
                 memcpy(dv, vrow_p + (int64_t)h * hd, sizeof(float) * (size_t)hd);
             }
         }
-    /* Attention over [0, vp+S) with the query at absolute position vp+s. */
+    /* Attention over [0, vp+S) with the query at absolute position vp+s. Rows
+     * (b, s, h) are independent and run in parallel; each row's arithmetic does
+     * not depend on the thread count. */
     int nk = vp + S;
-    for (int b = 0; b < B; ++b)
-        for (int s = 0; s < S; ++s)
-            for (int h = 0; h < H; ++h) {
-                const float* qin = q + ((int64_t)b * S + s) * qrow + (int64_t)h * hd;
-                if (cos_c) {
-                    int64_t pos = vp + s;
-                    rope_vec(qin, qr, hd, cos_c + pos * half, sin_c + pos * half, half,
-                             interleaved, 0, round16);
-                } else {
-                    for (int d = 0; d < hd; ++d) qr[d] = qin[d];
-                }
-                int kvh = h / g;
-                for (int j = 0; j < nk; ++j) {
-                    kp[j] = present_k + (((int64_t)b * KV + kvh) * pcap + j) * hd;
-                    vptr[j] = present_v + (((int64_t)b * KV + kvh) * pcap + j) * hd;
-                }
-                float* o = out + ((int64_t)b * S + s) * (int64_t)H * hd + (int64_t)h * hd;
-                attend_row(qr, hd, kp, vptr, nk, hd, vp + s, sc, NULL, scores, o);
+    const int64_t nrows = (int64_t)B * S * H;
+#pragma omp parallel
+    {
+        float* qrt = (float*)malloc(sizeof(float) * (size_t)hd);
+        double* sbuf = (double*)malloc(sizeof(double) * (size_t)(pcap + 1));
+        const float** kpt = (const float**)malloc(sizeof(float*) * (size_t)(pcap + 1));
+        const float** vpt = (const float**)malloc(sizeof(float*) * (size_t)(pcap + 1));
+#pragma omp for schedule(dynamic, 4)
+        for (int64_t row = 0; row < nrows; ++row) {
+            const int h = (int)(row % H);
+            const int s = (int)((row / H) % S);
+            const int b = (int)(row / ((int64_t)H * S));
+            const float* qin = q + ((int64_t)b * S + s) * qrow + (int64_t)h * hd;
+            if (cos_c) {
+                int64_t pos = vp + s;
+                rope_vec(qin, qrt, hd, cos_c + pos * half, sin_c + pos * half, half,
+                         interleaved, 0, round16);
+            } else {
+                for (int d = 0; d < hd; ++d) qrt[d] = qin[d];
             }
+            int kvh = h / g;
+            for (int j = 0; j < nk; ++j) {
+                kpt[j] = present_k + (((int64_t)b * KV + kvh) * pcap + j) * hd;
+                vpt[j] = present_v + (((int64_t)b * KV + kvh) * pcap + j) * hd;
+            }
+            float* o = out + ((int64_t)b * S + s) * (int64_t)H * hd + (int64_t)h * hd;
+            attend_row(qrt, hd, kpt, vpt, nk, hd, vp + s, sc, NULL, sbuf, o);
+        }
+        free(qrt);
+        free(sbuf);
+        free(kpt);
+        free(vpt);
+    }
     free(qr);
     free(kr);
-    free(scores);
-    free(kp);
-    free(vptr);
     (void)shared;
     return shared;
 }
@@ -336,24 +354,16 @@ int orc_paged_attention(const float* q, const float* k, const float* v, float* k
                         int rot_offset, const int32_t* slot_mapping, const float* head_sink,
                         const float* q_norm_w, const float* k_norm_w, float qk_eps, int H,
                         int KV, int hd, int vhd, float scale, int round16, float* out) {
-    if (H <= 0 || KV <= 0 || H % KV || blk <= 0) return -1;
+    if (H <= 0 || KV <= 0 || H % KV || blk <= 0 || hd > 512 || vhd > 512) return -1;
     int latent = (v == NULL);
     if (latent && vhd > hd) return -1;
     int g = H / KV;
     double sc = scale != 0.0f ? (double)scale : 1.0 / sqrt((double)hd);
     int64_t kslot = (int64_t)KV * hd, vslot = (int64_t)KV * vhd;
-    int64_t maxtok = 0;
-    for (int b = 0; b < batch; ++b) {
-        int64_t t = (int64_t)past_lens[b] + (cum[b + 1] - cum[b]);
-        if (t > maxtok) maxtok = t;
-    }
     int64_t T = cum[batch];
     float* qn = (float*)malloc(sizeof(float) * (size_t)(T * H * hd + 1));
     float* kn = (float*)malloc(sizeof(float) * (size_t)(T * KV * hd + 1));
     float* tmp = (float*)malloc(sizeof(float) * (size_t)hd);
-    double* scores = (double*)malloc(sizeof(double) * (size_t)(maxtok + 1));
-    const float** kp = (const float**)malloc(sizeof(float*) * (size_t)(maxtok + 1));
-    const float** vptr = (const float**)malloc(sizeof(float*) * (size_t)(maxtok + 1));
 
     for (int b = 0; b < batch; ++b) {
         int s0 = cum[b], s1 = cum[b + 1], nq = s1 - s0;
@@ -406,36 +416,49 @@ int orc_paged_attention(const float* q, const float* k, const float* v, float* k
                 }
             }
         }
-        /* Attention: keys [0, past) from the cache, [past, past+nq) new. */
+        /* Attention: keys [0, past) from the cache, [past, past+nq) new. Rows
+         * (head, query) are independent, so they run in parallel; each row's
+         * arithmetic does not depend on the thread count. */
         int total = pastb + nq;
-        for (int h = 0; h < H; ++h) {
-            int kvh = h / g;
+        const float** kpa = (const float**)malloc(sizeof(float*) * (size_t)KV * (total + 1));
+        const float** vpa = (const float**)malloc(sizeof(float*) * (size_t)KV * (total + 1));
+        for (int kvh = 0; kvh < KV; ++kvh) {
+            const float** kr = kpa + (int64_t)kvh * total;
+            const float** vr = vpa + (int64_t)kvh * total;
             for (int j = 0; j < total; ++j) {
                 if (j < pastb) {
                     int64_t slot = (int64_t)bt[(int64_t)b * maxb + j / blk] * blk + j % blk;
-                    kp[j] = kcache + slot * kslot + (int64_t)kvh * hd;
-                    vptr[j] = latent ? kp[j] : vcache + slot * vslot + (int64_t)kvh * vhd;
+                    kr[j] = kcache + slot * kslot + (int64_t)kvh * hd;
+                    vr[j] = latent ? kr[j] : vcache + slot * vslot + (int64_t)kvh * vhd;
                 } else {
                     int64_t t = s0 + (j - pastb);
-                    kp[j] = kn + t * kslot + (int64_t)kvh * hd;
-                    vptr[j] = latent ? kp[j] : v + t * vslot + (int64_t)kvh * vhd;
+                    kr[j] = kn + t * kslot + (int64_t)kvh * hd;
+                    vr[j] = latent ? kr[j] : v + t * vslot + (int64_t)kvh * vhd;
                 }
             }
-            for (int i = 0; i < nq; ++i) {
-                int64_t t = s0 + i;
-                const float* qv = qn + t * (int64_t)H * hd + (int64_t)h * hd;
-                float* o = out + t * (int64_t)H * vhd + (int64_t)h * vhd;
-                attend_row(qv, hd, kp, vptr, total, vhd, pastb + i, sc,
-                           head_sink ? head_sink + h : NULL, scores, o);
-            }
         }
+#pragma omp parallel
+        {
+            double* sbuf = (double*)malloc(sizeof(double) * (size_t)(total + 1));
+#pragma omp for collapse(2) schedule(dynamic, 8)
+            for (int h = 0; h < H; ++h)
+                for (int i = 0; i < nq; ++i) {
+                    int kvh = h / g;
+                    int64_t t = s0 + i;
+                    const float* qv = qn + t * (int64_t)H * hd + (int64_t)h * hd;
+                    float* o = out + t * (int64_t)H * vhd + (int64_t)h * vhd;
+                    attend_row(qv, hd, kpa + (int64_t)kvh * total, vpa + (int64_t)kvh * total,
+                               total, vhd, pastb + i, sc, head_sink ? head_sink + h : NULL, sbuf,
+                               o);
+                }
+            free(sbuf);
+        }
+        free(kpa);
+        free(vpa);
     }
     free(qn);
     free(kn);
     free(tmp);
-    free(scores);
-    free(kp);
-    free(vptr);
     return 0;
 }
 

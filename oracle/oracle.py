@@ -271,7 +271,22 @@ def round_f16(x) -> np.ndarray:
 
 
 # ------------------------------------------------------- int4 decoder -------
-def decoder_forward(w, cfg, ids, past_k, past_v, total):
+def dequant_cache(w, cfg):
+    """Every linear layer of a decoder weight dict dequantised once by the C
+    restatement (orc_mnb_dequant: (q - 8) * s, exact in fp32) and widened to fp64,
+    for decoder_forward(..., wcache=...). About 8 bytes per weight."""
+    out = {}
+    for key in list(w):
+        if key.endswith(".B"):
+            name = key[:-2]
+            B = w[key]
+            N = B.shape[0]
+            K = B.shape[1] * cfg.block
+            out[name] = mnb_dequant(B, w[name + ".s"], None, N, K, 4, cfg.block).astype(np.float64)
+    return out
+
+
+def decoder_forward(w, cfg, ids, past_k, past_v, total, wcache=None, logit_rows=None):
     """One forward of the int4 Llama-style decoder graph, op by op in fp16.
 
     The graph is the ONNX Runtime GenAI q4f16 decoder (op histogram in
@@ -286,13 +301,19 @@ def decoder_forward(w, cfg, ids, past_k, past_v, total):
     cfg: an object with layers, hidden, heads, kv_heads, head_dim, inter, vocab,
     eps, block; ids: int array [S]; past_k/past_v: per-layer f32 [1, KV, cap, hd]
     arrays, updated in place; total: total sequence length after this call.
-    Returns fp16-rounded logits [S, vocab] as f32.
+    wcache: optional dequant_cache(w, cfg); the linear layers are then fp64 matrix
+    products with the cached fp64 weights (the same exact products as the per-row
+    C loop, summed in BLAS order). logit_rows: optional row indices of the logits
+    to compute (default all S). Returns fp16-rounded logits [rows, vocab] as f32.
     """
     r16 = round_f16
     S = len(ids)
     D, H, KV, hd = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
 
     def mm(x, key, N, K):
+        if wcache is not None:
+            x2 = np.asarray(x, np.float32).reshape(-1, K).astype(np.float64)
+            return r16((x2 @ wcache[key].T).reshape(tuple(np.shape(x)[:-1]) + (N,)))
         return r16(mnb_matmul(x, w[key + ".B"], w[key + ".s"], None, N, K, 4, cfg.block))
 
     h = w["embed"][np.asarray(ids)].astype(np.float32).reshape(1, S, D)
@@ -322,5 +343,8 @@ def decoder_forward(w, cfg, ids, past_k, past_v, total):
         act = r16(r16(gate * sig) * up)
         down = mm(act, p + ".down", D, cfg.inter)
     xf, _ = rms_norm(down, w["final_ln"], cfg.eps, skip=residual, round16=True)
-    logits = mm(r16(xf), "lm_head", cfg.vocab, D)
-    return logits.reshape(S, cfg.vocab)
+    xf = r16(xf).reshape(S, D)
+    if logit_rows is not None:
+        xf = xf[np.asarray(logit_rows)]
+    logits = mm(xf, "lm_head", cfg.vocab, D)
+    return logits.reshape(-1, cfg.vocab)

@@ -243,17 +243,32 @@ def test_mnb_gemm_fp16(ortmi, oracle, M, K, N, block):
     assert_f16_close(got, ref16, what="gemm fp16 (fp16 weights)")
 
 
-def test_mnb_gemm_config2_shape(ortmi, oracle):
-    """M=512, K=4096, N=4096 fp16, block 32, zero points U{0..15} (the prefill config)."""
-    rng = np.random.default_rng(4096)
-    M, K, N = 512, 4096, 4096
+def _check_gemm_rows(oracle, got_rows, A_rows, B, s, zp, N, K, block, what):
+    """Two checks of MFMA-GEMM output rows. Primary: against fp64 A . W16^T with the
+    dequantised weights rounded to fp16 once (what the kernel feeds the matrix cores),
+    within the plain fp16 bar (1e-3 + 1 ULP). Secondary: against the oracle's exact
+    fp64 dequantisation, within the bar plus the rigorous bound 2^-11 sum |a w| of
+    that one weight rounding."""
+    W = refs.dequant_ref(B, s, zp, N, K, 4, block)
+    W16 = W.astype(np.float16).astype(np.float64)
+    assert_f16_close(got_rows, A_rows.astype(np.float64) @ W16.T, what=what + " (fp16 weights)")
+    ref = oracle.mnb_matmul(A_rows, B, s, zp, N, K, 4, block)
+    bound = 2.0 ** -11 * (np.abs(A_rows.astype(np.float64)) @ np.abs(W).T)
+    assert_f16_close(got_rows, ref, extra=bound, what=what)
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (512, 4096, 4096),   # the prefill GEMM config
+    (512, 1536, 8960),   # the decoder prefill's down_proj (64x64 tiles, k split)
+    (512, 2048, 1536),   # the decoder prefill's merged QKV
+])
+def test_mnb_gemm_config2_shape(ortmi, oracle, M, N, K):
+    """Prefill GEMM shapes at full size, fp16, block 32, zero points U{0..15}."""
+    rng = np.random.default_rng(M + N + K)
     A, B, s, zp = _mnb_inputs(rng, M, N, K, 32, dtype=np.float16)
     got = host(ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N))
-    rows = np.arange(0, M, 37)  # oracle on a sample of rows keeps the CPU side short
-    ref = oracle.mnb_matmul(A[rows], B, s, zp, N, K, 4, 32)
-    W = refs.dequant_ref(B, s, zp, N, K, 4, 32)
-    bound = 2.0 ** -11 * (np.abs(A[rows].astype(np.float64)) @ np.abs(W).T)
-    assert_f16_close(got[rows], ref, extra=bound, what="gemm config2")
+    rows = np.r_[np.arange(0, M, 37), M - 1]  # a sample of rows keeps the CPU side short
+    _check_gemm_rows(oracle, got[rows], A[rows], B, s, zp, N, K, 32, f"gemm {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("M,N,K,block", [(1030, 8200, 1000, 64), (1024, 8192, 1536, 32)])
@@ -264,10 +279,7 @@ def test_mnb_gemm_large_tiles(ortmi, oracle, M, N, K, block):
     A, B, s, zp = _mnb_inputs(rng, M, N, K, block, dtype=np.float16)
     got = host(ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N, block_size=block))
     rows = np.r_[np.arange(0, M, 41), M - 1]
-    ref = oracle.mnb_matmul(A[rows], B, s, zp, N, K, 4, block)
-    W = refs.dequant_ref(B, s, zp, N, K, 4, block)
-    bound = 2.0 ** -11 * (np.abs(A[rows].astype(np.float64)) @ np.abs(W).T)
-    assert_f16_close(got[rows], ref, extra=bound, what="gemm large tiles")
+    _check_gemm_rows(oracle, got[rows], A[rows], B, s, zp, N, K, block, "gemm large tiles")
 
 
 @pytest.mark.parametrize("M,N,K,block", [(37, 400, 1536, 32), (512, 2048, 1536, 32),
@@ -666,7 +678,8 @@ def test_gqa_no_rotary(ortmi, oracle):
 # ------------------------------------------------------------------ PagedAttention --
 
 def _run_paged(ortmi, oracle, H, KV, d, nb, blk, batch, seed, rope=False, interleaved=0,
-               new_max=4, slot_mapping=None, head_sink=None, qk_norm=False):
+               new_max=4, slot_mapping=None, head_sink=None, qk_norm=False, latent=False,
+               v_head_size=0, rotary_offset=0):
     rng = np.random.default_rng(seed)
     maxb = nb // batch
     cap = maxb * blk
@@ -682,28 +695,36 @@ def _run_paged(ortmi, oracle, H, KV, d, nb, blk, batch, seed, rope=False, interl
     bt = rng.permutation(nb).astype(np.int32).reshape(batch, maxb)
     cos = sin = None
     if rope:
-        c, s_ = refs.rotary_caches(cap, d)
+        # With a rotary_offset the rotated dims are [offset, offset + d/2).
+        c, s_ = refs.rotary_caches(cap, d // 2 if rotary_offset else d)
         cos, sin = c.astype(np.float16), s_.astype(np.float16)
+    if latent:
+        v = vc = None
     qw = kw = None
     if qk_norm:
         qw = np.linspace(0.75, 1.25, d).astype(np.float16)
         kw = np.linspace(1.25, 0.75, d).astype(np.float16)
     sm = None if slot_mapping is None else slot_mapping(cum, past, bt, blk)
-    dkc, dvc = dev(kc), dev(vc)
+    dkc = dev(kc)
+    dvc = None if latent else dev(vc)
     out = ortmi.paged_attention(
-        dev(q), dev(k), dev(v), dkc, dvc, dev(cum), dev(past), dev(bt),
+        dev(q), dev(k), None if latent else dev(v), dkc, dvc, dev(cum), dev(past), dev(bt),
         None if cos is None else dev(cos), None if sin is None else dev(sin),
         None if sm is None else dev(sm), None if head_sink is None else dev(head_sink),
         None if qw is None else dev(qw), None if kw is None else dev(kw), num_heads=H,
         kv_num_heads=KV, do_rotary=int(rope), rotary_interleaved=interleaved,
-        qk_norm_epsilon=1e-5)
+        qk_norm_epsilon=1e-5, kv_cache_layout="LATENT" if latent else "SEPARATE",
+        v_head_size=v_head_size, rotary_offset=rotary_offset)
     ro, rkc, rvc = oracle.paged_attention(q, k, v, kc, vc, cum, past, bt, H, KV, cos=cos, sin=sin,
-                                          interleaved=interleaved, slot_mapping=sm,
-                                          head_sink=head_sink, q_norm=qw, k_norm=kw,
-                                          qk_eps=1e-5, round16=True)
+                                          interleaved=interleaved, rotary_offset=rotary_offset,
+                                          slot_mapping=sm, head_sink=head_sink, q_norm=qw,
+                                          k_norm=kw, qk_eps=1e-5, v_head_size=v_head_size,
+                                          round16=True)
+    assert out.shape == (int(cum[-1]), H * (v_head_size or d))
     assert_f16_close(host(out), ro, what="paged output")
-    gk, gv = host(dkc), host(dvc)
-    np.testing.assert_array_equal(gv, rvc)  # slot writes of V are bit-exact copies
+    gk = host(dkc)
+    if not latent:
+        np.testing.assert_array_equal(host(dvc), rvc)  # slot writes of V are bit-exact copies
     # K slots: untouched rows bit-exact, written rows within 1 ULP (rounded RoPE/norm).
     assert (np.abs(gk - rkc) <= ulp16(rkc)).all()
     return out
@@ -725,6 +746,25 @@ def test_paged_multiblock_long(ortmi, oracle, blk):
 def test_paged_rotary(ortmi, oracle, interleaved):
     _run_paged(ortmi, oracle, 4, 2, 64, nb=16, blk=4, batch=2, seed=31 + interleaved, rope=True,
                interleaved=interleaved)
+
+
+@pytest.mark.parametrize("vhd", [64, 128])
+def test_paged_latent_layout(ortmi, oracle, vhd):
+    """LATENT cache layout (rust/src/ops/attention.rs:2500-2505, 2624-2628): no value
+    input or value cache; values are the first v_head_size dims of each cached key
+    (head size 128, v_head_size 64 or 128), with a multi-token chunk and RoPE."""
+    _run_paged(ortmi, oracle, 8, 2, 128, nb=24, blk=4, batch=3, seed=300 + vhd, new_max=6,
+               rope=True, latent=True, v_head_size=vhd)
+
+
+@pytest.mark.parametrize("interleaved", [0, 1])
+@pytest.mark.parametrize("d,offset", [(64, 16), (128, 8)])
+def test_paged_rotary_offset(ortmi, oracle, interleaved, d, offset):
+    """rotary_offset (rust/src/ops/attention.rs:2455-2493, 2620): RoPE rotates head
+    dims [offset, offset + rotary_dim) and passes the dims before and after through;
+    here rotary_dim = head_size / 2."""
+    _run_paged(ortmi, oracle, 4, 2, d, nb=16, blk=4, batch=2, seed=41 + interleaved + d,
+               rope=True, interleaved=interleaved, new_max=5, rotary_offset=offset)
 
 
 def test_paged_optional_inputs(ortmi, oracle):
@@ -809,6 +849,34 @@ def test_paged_mixed_batch_reduced(ortmi, oracle):
     np.testing.assert_array_equal(host(dvc), rvc)
 
 
+def test_paged_mixed_batch_full_size(ortmi, oracle):
+    """The benchmarked mixed batch at full size: 32 sequences with contexts U[256, 8192],
+    4 prefill 256-token chunks and 28 one-token decodes, block 16, 32/8 heads, hd 128
+    (block tables of up to 512 entries, prefill tiles crossing the causal diagonal,
+    8K-context split counts). Every written K/V slot is bit-exact and every output row
+    of all 32 sequences is within the fp16 tolerance."""
+    import importlib
+
+    wl = importlib.import_module(ortmi.__name__ + ".workloads")
+    cfg = wl.paged_mixed_config()
+    print(f"cfg5: ctx {cfg['ctx'].min()}..{cfg['ctx'].max()}, tokens {int(cfg['cum'][-1])}, "
+          f"blocks {cfg['kc'].shape[0]}, max table {cfg['bt'].shape[1]}", flush=True)
+    dkc, dvc = dev(cfg["kc"]), dev(cfg["vc"])
+    out = ortmi.paged_attention(dev(cfg["q"]), dev(cfg["k"]), dev(cfg["v"]), dkc, dvc,
+                                dev(cfg["cum"]), dev(cfg["past"]), dev(cfg["bt"]),
+                                num_heads=cfg["H"], kv_num_heads=cfg["KV"])
+    got, gk, gv = host(out), host(dkc), host(dvc)
+    ro, rkc, rvc = oracle.paged_attention(cfg["q"], cfg["k"], cfg["v"], cfg["kc"], cfg["vc"],
+                                          cfg["cum"], cfg["past"], cfg["bt"], cfg["H"], cfg["KV"],
+                                          round16=True)
+    np.testing.assert_array_equal(gk, rkc)
+    np.testing.assert_array_equal(gv, rvc)
+    cum = cfg["cum"]
+    for b in range(len(cum) - 1):
+        assert_f16_close(got[cum[b]:cum[b + 1]], ro[cum[b]:cum[b + 1]],
+                         what=f"cfg5 sequence {b} (ctx {cfg['ctx'][b]}, new {cfg['new'][b]})")
+
+
 # ---------------------------------------------------------------- RotaryEmbedding --
 
 @pytest.mark.parametrize("form", ["bsnd_ids", "bsnd_offset", "bnsd_ids", "per_token"])
@@ -816,7 +884,8 @@ def test_paged_mixed_batch_reduced(ortmi, oracle):
 def test_rotary_embedding(ortmi, oracle, form, interleaved):
     import torch
 
-    rng = np.random.default_rng(hash(form) % 1000 + interleaved)
+    rng = np.random.default_rng(["bsnd_ids", "bsnd_offset", "bnsd_ids", "per_token"].index(form)
+                                * 10 + interleaved)
     B, S, NH, hd = 2, 7, 4, 64
     c, s_ = refs.rotary_caches(64, hd)
     cos, sin = c.astype(np.float16), s_.astype(np.float16)

@@ -368,3 +368,43 @@ def test_rms_norm_closed_form_and_numpy(oracle):
     y16, r16 = oracle.rms_norm(x, gamma, 1e-6, skip=skip, round16=True)
     np.testing.assert_array_equal(r16, (x + skip).astype(np.float16).astype(np.float32))
     np.testing.assert_allclose(y16, refs.rms_norm_ref(r16, gamma), rtol=1e-5, atol=1e-6)
+
+
+def test_decoder_forward_cached_weights_match_per_row_form(oracle):
+    """The decoder oracle's fast form (weights dequantised once, fp64 products summed
+    by BLAS) equals the per-row C form (fp64 products summed in order) to fp16 output
+    rounding, over a prompt and two decode steps of a small 2-layer decoder; the
+    logit_rows selection returns exactly the selected rows."""
+    from conftest import load_package
+
+    pkg = load_package()
+    from importlib import import_module
+
+    dec = import_module(pkg.__name__ + ".decoder")
+    cfg = dec.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, inter=512,
+                            vocab=1024, max_pos=128)
+    w = dec.make_weights(cfg, seed=3)
+    wc = oracle.dequant_cache(w, cfg)
+    assert set(wc) == {f"l{i}.{n}" for i in range(2) for n, _, _ in cfg.linear_shapes()} | \
+        {"lm_head"}
+    ids = np.random.default_rng(4).integers(0, cfg.vocab, size=9)
+
+    def run(cache):
+        kr = [np.zeros((1, 2, 32, 64), np.float32) for _ in range(2)]
+        vr = [np.zeros_like(k) for k in kr]
+        out = [oracle.decoder_forward(w, cfg, ids, kr, vr, 9, wcache=cache)]
+        for step, tok in enumerate((5, 77)):
+            out.append(oracle.decoder_forward(w, cfg, [tok], kr, vr, 10 + step, wcache=cache))
+        return out, kr
+
+    slow, ks = run(None)
+    fast, kf = run(wc)
+    for a, b in zip(slow, fast):
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(a), 2.0 ** -14))) - 10)
+        assert (np.abs(a - b) <= ulp).all()
+    for a, b in zip(ks, kf):
+        assert np.abs(a - b).max() <= 2.0 ** -9 * max(1.0, np.abs(a).max())
+    kr = [np.zeros((1, 2, 32, 64), np.float32) for _ in range(2)]
+    vr = [np.zeros_like(k) for k in kr]
+    last = oracle.decoder_forward(w, cfg, ids, kr, vr, 9, wcache=wc, logit_rows=[8, 2])
+    np.testing.assert_array_equal(last, fast[0][[8, 2]])
