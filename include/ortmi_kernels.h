@@ -124,6 +124,76 @@ int ortmi_matmul_nbits_decode_merge(const float* partials, int64_t splits, int64
                                     int64_t block_size, int32_t dtype, void* stream);
 
 /*
+ * Int4 decoder decode step as one launch: the whole one-token step of a
+ * Llama-style decoder graph (embedding Gather; per layer
+ * (Skip)SimplifiedLayerNormalization, q/k/v MatMulNBits, GroupQueryAttention over
+ * a shared KV cache with in-op RoPE, o_proj MatMulNBits,
+ * SkipSimplifiedLayerNormalization, gate/up MatMulNBits with SwiGLU
+ * (Sigmoid/Mul/Mul), down MatMulNBits; final SkipSimplifiedLayerNormalization;
+ * lm_head MatMulNBits) plus the greedy argmax of the logits.
+ * Forms: fp16, 4-bit symmetric weights (no zero points), block 32, head size
+ * 128, non-interleaved rotary (or none), at most 8 query heads per KV head,
+ * hidden and num_heads * head_size multiples of 256 up to 2048, intermediate a
+ * multiple of 32 up to 10240. Other forms return ORTMI_E_INVALID before any
+ * launch (the caller runs the graph op by op).
+ * Weights keep the MatMulNBits layout [N, K/32, 16] with fp16 scales [N * K/32];
+ * qkv_weight holds the q rows, then the k rows, then the v rows of one merged
+ * projection; gate_up_weight interleaves gate row i (row 2i) and up row i
+ * (row 2i+1). k_cache / v_cache [1, kv_num_heads, kv_capacity, head_size] are past
+ * and present at once: the step writes the new row at total - 1 in place.
+ * `layers` is a device array of `dims->layers` records. input_id (int64 [1]) and
+ * total_sequence_length (int32 [1]) are device memory read by the kernel, so a
+ * step needs no host round trip; logits [vocab] fp16 and next_id (int64, the
+ * first index of the largest logit, NaN never wins) are written. `status`
+ * (optional; device or host-pinned memory) receives 0 on success, 1 if a grid
+ * barrier timed out (the results are then invalid), 2 if the token id was out of
+ * range (row 0 was used), 3 if total_sequence_length is outside [1, kv_capacity]
+ * or past the rotary table (nothing computed). The workspace
+ * (ortmi_decoder_decode_step_workspace_size bytes, 256-byte aligned) must be
+ * zero-filled before its first use and then passed unchanged to every step;
+ * steps sharing a workspace must run in order on one stream.
+ * Replaces: the compiled decode path of the reference EP, a shapeless
+ * mlx_compile trace of the decode graph evaluated once per token
+ * (rust/src/compiled.rs:503-822, rust/src/engine.rs:417, 1720-1736), over the
+ * op translations of rust/src/ops/quant.rs:570-601, attention.rs:556-952 and
+ * norm.rs:164-248.
+ */
+typedef struct OrtmiDecoderLayer {
+    const uint8_t* qkv_weight;
+    const void* qkv_scales;
+    const void* ln1_gamma;     /* norm before the attention */
+    float ln1_epsilon;
+    int32_t reserved0;
+    const uint8_t* o_weight;
+    const void* o_scales;
+    const void* ln2_gamma;     /* norm before the MLP */
+    float ln2_epsilon;
+    int32_t reserved1;
+    const uint8_t* gate_up_weight;
+    const void* gate_up_scales;
+    const uint8_t* down_weight;
+    const void* down_scales;
+    void* k_cache;
+    void* v_cache;
+} OrtmiDecoderLayer;
+
+typedef struct OrtmiDecoderDims {
+    int32_t layers, hidden, num_heads, kv_num_heads, head_size, intermediate, vocab;
+    int32_t kv_capacity, max_position, rotary_half, rotary_interleaved, block_size, dtype;
+    float scale; /* 0: 1/sqrt(head_size) */
+} OrtmiDecoderDims;
+
+size_t ortmi_decoder_decode_step_workspace_size(const OrtmiDecoderDims* dims);
+int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const OrtmiDecoderDims* dims,
+                              const void* embed, int64_t embed_rows, const int64_t* input_id,
+                              const int32_t* total_sequence_length, const void* cos_cache,
+                              const void* sin_cache, const void* final_gamma,
+                              float final_epsilon, const uint8_t* lm_weight,
+                              const void* lm_scales, void* logits, int64_t* next_id,
+                              int32_t* status, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/*
  * GroupQueryAttention (com.microsoft), decode and prefill, with in-op RoPE.
  * query [B,S,H*hd] (or packed [B,S,(H+2*KV)*hd] when key == value == NULL),
  * key/value [B,S,KV*hd]; past_key/past_value [B,KV,past_cap,hd].

@@ -65,6 +65,10 @@ SIGNATURES = {
         _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp]),
     "ortmi_matmul_nbits_decode_merge": (ctypes.c_int, [
         _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]),
+    "ortmi_decoder_decode_step_workspace_size": (_sz, [_vp]),
+    "ortmi_decoder_decode_step": (ctypes.c_int, [
+        _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+        _vp]),
     "ortmi_group_query_attention_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "ortmi_group_query_attention": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64,

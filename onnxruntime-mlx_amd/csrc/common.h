@@ -146,6 +146,40 @@ __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
 __device__ __forceinline__ int nibble(uint8_t byte, int hi) { return hi ? (byte >> 4) : (byte & 0x0f); }
 
+// ------------------------------------------------ int4 x fp16 dot products --
+// Reorder 8 activations [a0..a7] to the pair order [a0,a4,a1,a5,a2,a6,a3,a7] used by
+// the dequantised weights (an identical permutation of k on both MFMA operands).
+__device__ __forceinline__ uint4 permute_act8(uint4 v) {
+    return make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u),
+                      __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                      __builtin_amdgcn_perm(v.w, v.y, 0x05040100u),
+                      __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+}
+
+// fp16 activations as pairs: sum over the 32 codes of one chunk of a * (q - zp).
+// `av` holds the chunk's activations in pair order (a_j, a_j+4) for each 8-code
+// word, the order dequant_word_pairs gives the codes in; (1024 + q) - (1024 + zp)
+// is exact in fp16, v_dot2_f32_f16 multiplies exactly and accumulates in fp32.
+__device__ __forceinline__ float dot32_pairs(const uint4 (&av)[4], uint4 w, half2_t zoff) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t aw[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t m = ((words[i] >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+            const half2_t q = __builtin_bit_cast(half2_t, m) - zoff;
+            const half2_t a = __builtin_bit_cast(half2_t, aw[j]);
+            if (j & 1) d1 = __builtin_amdgcn_fdot2(a, q, d1, false);
+            else d0 = __builtin_amdgcn_fdot2(a, q, d0, false);
+        }
+    }
+    return d0 + d1;
+}
+
+
+
 // --------------------------------------------------------------- host side --
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);

@@ -1,0 +1,127 @@
+"""The one-launch decode step (ortmi_decoder_decode_step) against the op-by-op EP
+path and the oracle.
+
+Each decode step runs both ways on the same KV cache: the EP graph (one kernel per
+fused op) and the decode program (one cooperative launch). They round at the same
+op boundaries but sum in different orders, so logits are compared within the fp16
+tolerance carried through the layers, the appended K/V rows within one fp16 ULP of
+the rows' scale, and the program's greedy token must be the argmax of its own
+logits. At full size the program's tokens are checked teacher-forced against the
+oracle with the strict rule of the decoder tests (no agreement quota).
+"""
+
+from __future__ import annotations
+
+from importlib import import_module
+
+import numpy as np
+import pytest
+from test_gpu_ep import _assert_greedy_strict
+from test_gpu_ops import host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dec(ortmi):
+    return import_module(ortmi.__name__ + ".decoder")
+
+
+@pytest.fixture(scope="module")
+def dprog(ortmi):
+    return import_module(ortmi.__name__ + ".decode_program")
+
+
+def _step_both(runner, prog, length):
+    """One decode step through the EP and, on the same KV cache, through the program.
+    Returns (ep logits, program logits, ep token, program token, per-layer max |K/V
+    row diff|); the cache ends up holding the program's new rows."""
+    import torch
+
+    tok = runner.next_id.clone().view(1)
+    snap = [(k.clone(), v.clone()) for k, v in runner.kv]
+    runner.decode_step()
+    torch.cuda.synchronize()
+    ep_logits = host(runner.logits[0, 0])
+    ep_tok = int(runner.next_id.item())
+    ep_rows = [(k[:, :, length].float().clone(), v[:, :, length].float().clone())
+               for k, v in runner.kv]
+    for (k, v), (ks, vs) in zip(runner.kv, snap):
+        k.copy_(ks)
+        v.copy_(vs)
+    prog.total.fill_(length + 1)
+    prog.step(token=tok, total=prog.total)
+    torch.cuda.synchronize()
+    assert int(prog.status.item()) == 0, f"decode program status {int(prog.status.item())}"
+    rows = [(k[:, :, length].float(), v[:, :, length].float()) for k, v in runner.kv]
+    kv_diff = max(float(torch.max(torch.abs(a - b)).item())
+                  for (ka, va), (kb, vb) in zip(rows, ep_rows) for a, b in ((ka, kb), (va, vb)))
+    runner.next_id.copy_(prog.next_id.view(1, 1))
+    return ep_logits, host(prog.logits), ep_tok, int(prog.next_id.item()), kv_diff
+
+
+@pytest.mark.parametrize("G", [2, 6])
+def test_decode_program_matches_ep_steps(ortmi, dec, dprog, G):
+    """2-layer decoder (head 128, G query heads per KV head): 10 decode steps after a
+    19-token prompt, the program against the EP path on the same cache."""
+    H = 2 * G
+    cfg = dec.DecoderConfig(layers=2, hidden=H * 128,
+                            heads=H, kv_heads=2, head_dim=128, inter=512, vocab=4096, max_pos=512)
+    w = dec.make_weights(cfg, seed=50 + G)
+    runner = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
+    prog = dprog.DecodeProgram(cfg, w, runner.kv, 64)
+    prompt = np.random.default_rng(G).integers(0, cfg.vocab, size=19)
+    runner.reset()
+    runner.prefill(prompt)
+    length = len(prompt)
+    for step in range(10):
+        el, pl, et, pt, kvd = _step_both(runner, prog, length)
+        runner.length = length + 1
+        length += 1
+        scale = float(np.abs(el).max())
+        err = float(np.abs(el - pl).max())
+        print(f"G={G} step {step}: max |logit diff| {err:.3e} (|logit| up to {scale:.2f}), "
+              f"K/V row diff {kvd:.3e}, tokens ep {et} program {pt}", flush=True)
+        assert np.isfinite(pl).all()
+        assert pt == int(np.argmax(pl)), "program token is not the argmax of its logits"
+        assert err <= 2.0 ** -7 * max(1.0, scale)
+        assert kvd <= 2.0 ** -7 * 4
+
+
+def test_decode_program_full_size_greedy_strict(ortmi, oracle, dec, dprog):
+    """The 28-layer decoder: 512-token prompt through the EP, then 128 greedy steps
+    through the decode program; every token teacher-forced against the oracle."""
+    import time
+
+    import torch
+
+    cfg = dec.DecoderConfig()
+    w = dec.make_weights(cfg, seed=4)
+    P, steps = 512, 128
+    runner = dec.DecoderRunner(cfg, w, cap=P + steps, max_prompt=P)
+    prog = dprog.DecodeProgram(cfg, w, runner.kv, P + steps)
+    prompt = np.random.default_rng(44).integers(0, cfg.vocab, size=P)
+    runner.reset()
+    runner.prefill(prompt)
+    gpu = [host(runner.logits[0, P - 1])]
+    toks = [int(runner.next_id.item())]
+    prog.next_id.copy_(runner.next_id.view(1))
+    for i in range(steps):
+        prog.total.fill_(P + i + 1)
+        prog.step()
+        torch.cuda.synchronize()
+        assert int(prog.status.item()) == 0
+        gpu.append(host(prog.logits))
+        toks.append(int(prog.next_id.item()))
+    print(f"program tokens {toks[:8]} ... ({len(toks)})", flush=True)
+    t0 = time.time()
+    wc = oracle.dequant_cache(w, cfg)
+    kr = [np.zeros((1, cfg.kv_heads, P + steps, cfg.head_dim), np.float32)
+          for _ in range(cfg.layers)]
+    vr = [np.zeros_like(k) for k in kr]
+    r0 = oracle.decoder_forward(w, cfg, prompt, kr, vr, P, wcache=wc, logit_rows=[P - 1])
+    r1 = oracle.decoder_forward(w, cfg, toks[:steps], kr, vr, P + steps, wcache=wc)
+    ref = np.concatenate([r0, r1])
+    del wc
+    print(f"oracle: {time.time() - t0:.1f} s", flush=True)
+    _assert_greedy_strict(list(zip(gpu, ref, toks)), "decode program 512+128")
