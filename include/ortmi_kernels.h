@@ -145,13 +145,14 @@ int ortmi_matmul_nbits_decode_merge(const float* partials, int64_t splits, int64
  * total_sequence_length (int32 [1]) are device memory read by the kernel, so a
  * step needs no host round trip; logits [vocab] fp16 and next_id (int64, the
  * first index of the largest logit, NaN never wins) are written. `status`
- * (optional; device or host-pinned memory) receives 0 on success, 1 if a grid
- * barrier timed out (the results are then invalid), 2 if the token id was out of
- * range (row 0 was used), 3 if total_sequence_length is outside [1, kv_capacity]
- * or past the rotary table (nothing computed). The workspace
- * (ortmi_decoder_decode_step_workspace_size bytes, 256-byte aligned) must be
- * zero-filled before its first use and then passed unchanged to every step;
- * steps sharing a workspace must run in order on one stream.
+ * (optional; device or host-pinned memory) receives 0 on success, 1 if a wait
+ * between the step's workgroups passed its 100 ms deadline (the results are then
+ * invalid), 2 if the token id was out of range (row 0 was used), 3 if
+ * total_sequence_length is outside [1, kv_capacity] or past the rotary table
+ * (nothing computed). The workspace (ortmi_decoder_decode_step_workspace_size
+ * bytes, 256-byte aligned) must be zero-filled before its first use and then
+ * passed unchanged to every step; steps sharing a workspace must run in order on
+ * one stream. embed, the gammas and the cos/sin caches must be 16-byte aligned.
  * Replaces: the compiled decode path of the reference EP, a shapeless
  * mlx_compile trace of the decode graph evaluated once per token
  * (rust/src/compiled.rs:503-822, rust/src/engine.rs:417, 1720-1736), over the

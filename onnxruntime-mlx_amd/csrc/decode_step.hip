@@ -7,61 +7,71 @@
 // down MatMulNBits] -> final SkipSimplifiedLayerNorm -> lm_head MatMulNBits ->
 // greedy argmax. The reference reaches the same one-dispatch-per-token shape with
 // a shapeless mlx_compile trace of the decode graph (rust/src/compiled.rs:1-28,
-// 503-822); here the step is a fixed program of phases separated by grid-wide
-// barriers.
+// 503-822).
 //
 // Why one kernel: at batch 1 every MatMulNBits of this decoder moves 1.3-16 MB,
 // which the GPU streams in 1-3 us, while a dependent kernel boundary costs about
-// 1.5 us and each small kernel spends another 1-2 us filling and draining. Here
-// the weights of the next phase do not depend on the activations, so every wave
-// issues the loads of its share of the next phase's weights into registers
-// before it waits at the barrier: the HBM latency hides behind the
-// synchronisation.
+// 1.5 us and each small kernel spends another 1-2 us filling and draining. The
+// weights of the next phase do not depend on the activations, so every wave
+// issues the loads of its share of the next phase's weights (straight into LDS)
+// before it waits for that phase's input: the HBM latency hides behind the wait.
 //
-// Grid: one 512-thread workgroup per CU (co-resident by the cooperative launch).
-// Wave 0 of each workgroup synchronises the grid; waves 1..7 do the row work, so
-// their outstanding weight loads never stall the barrier's polling loads (loads
-// and stores share one in-order counter per wave on this architecture).
+// Dataflow, no grid barrier. Every phase output (qkv, attention output, o_proj
+// output, SwiGLU activations, down output) is a vector of tagged words in a
+// buffer of its own per layer: fp16 value in the low half, the launch tag in the
+// high half, written with one device-coherent (sc1) 32-bit store. A consumer
+// thread reads the units (8 words) it needs with sc1 loads and reads again only
+// those whose tags are not yet this launch's, so a phase waits for exactly the
+// data it uses, one memory round trip after the last producer's store, with no
+// store acknowledgement, counter or flag in between. Words are single-copy
+// atomic, so no ordering between stores is needed. The tag comes from a launch
+// counter every workgroup bumps once at entry (launches on one workspace run in
+// stream order, so a launch's workgroups all read the same count / nwg), and
+// every buffer word is rewritten by every launch, so a stale word always carries
+// the previous launch's tag.
 //
-// Cross-workgroup data: phase outputs are written with device-coherent (sc1)
-// stores and read with sc1 loads; a barrier is entered after the wave's stores
-// completed. Barrier: per-XCD arrival counters (workgroup i is on XCD i % 8),
-// the last arrival of an XCD bumps a top counter that every workgroup polls.
-// Every spin is bounded (50 ms of the 100 MHz realtime clock): a workgroup that
-// times out raises the abort word, every other workgroup leaves at its next poll,
-// and the launch reports status 1. Counters come in two sets used by alternate
-// launches: a launch zeroes the other set after its first barrier, so the next
-// launch starts from zero without any host work.
+// Grid: one 512-thread workgroup per CU (co-resident by the cooperative launch),
+// 8 waves, all computing. Attention runs on the last H workgroups, one query
+// head each over all keys (no split merge); they skip o_proj, which the other
+// workgroups run. Every wait is bounded (100 ms of the 100 MHz realtime clock from
+// the workgroup's start): a workgroup past the deadline writes its launch tag to
+// the abort word and status 1, and every other waiting thread leaves when it sees
+// its own tag there. No thread waits on anything its own workgroup produces later,
+// so the waits form a chain along the layer order and always end.
 //
 // Rounding follows the unfused ops of the fp16 graph: residual sums and
 // normalised activations, MatMulNBits outputs, the RoPE'd query/key and the
 // attention output are rounded to fp16 where the graph stores them; sums and
 // softmax state are fp32.
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "common.h"
 
 namespace ortmi {
 namespace dprog {
 
 constexpr int kThreads = 512;
-constexpr int kComputeWaves = 7;      // waves 1..7
-constexpr int kSC1 = 16;              // buffer cache policy: device-coherent (sc1)
-constexpr int kGMax = 8;              // query heads per KV head
-constexpr int kNSMax = 8;             // key splits per KV head
-constexpr int kKeySlots = kComputeWaves * 4;  // key rows per attention step
-constexpr int kPrefSteps = 4;         // attention steps whose K/V rows are prefetched
-constexpr int kIChunksPerLane = 5;    // down_proj: K = I <= 5 * 64 * 32 = 10240
-constexpr unsigned long long kSpinTicks = 5000000ull;  // 50 ms
+constexpr int kWaves = kThreads / 64;
+constexpr int kSC1 = 16;               // buffer cache policy: device-coherent (sc1)
+constexpr int kGMax = 8;               // query heads per KV head
+constexpr int kKeySlots = kWaves * 4;  // key rows per attention step (4 lane groups per wave)
+constexpr int kKvRing = 4;             // attention steps in flight in registers
+constexpr int kIChunksPerLane = 5;     // down_proj: K = I <= 5 * 64 * 32 = 10240
+constexpr int kMaxLayers = 64;
+constexpr int kMaxUnits = 3;           // tagged vectors up to 3 * 512 units of 8 values
+constexpr unsigned long long kDeadlineTicks = 10000000ull;  // 100 ms
 
-// Control block (uint32 words, one 128-byte line per counter).
-constexpr int kCtlParity = 0;
-constexpr int kCtlAbort = 32;
-__host__ __device__ constexpr int ctl_top(int set) { return 32 * (2 + 9 * set); }
-__host__ __device__ constexpr int ctl_xcd(int set, int x) { return 32 * (3 + 9 * set + x); }
-constexpr size_t kCtlBytes = 4096;
+// Control block (uint32 words, one 128-byte line each).
+constexpr int kCtlStart = 0;   // workgroups started, summed over launches
+constexpr int kCtlAbort = 32;  // tag of a launch that gave up
+constexpr size_t kCtlBytes = 256;
 
 struct Params {
     const OrtmiDecoderLayer* layers;
-    int L, D, H, KV, I, V, cap, max_pos, half, nwg;
+    int L, D, H, KV, G, I, V, cap, max_pos, half, nwg;
+    int gq, go, ggu, gd;  // QKV / o_proj / gate-up groups and down rows per workgroup
     float scale, final_eps;
     const half_t* embed;
     int64_t embed_rows;
@@ -76,12 +86,9 @@ struct Params {
     int64_t* next_id;
     int32_t* status;
     uint32_t* ctl;
-    half_t* qkv;
-    float* part;
-    half_t* y;
-    half_t* act;
-    half_t* dout;
-    float4* argp;
+    uint32_t* flow;          // per layer: qkv [NQ], att [H*hd], y [D], act [I], dout [D]
+    uint32_t flow_stride;    // words per layer
+    uint64_t* argp;          // per workgroup: index | fp16 value << 32 | tag << 48
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
@@ -91,11 +98,6 @@ template <int POL>
 __device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL);
     return make_uint4(v.x, v.y, v.z, v.w);
-}
-template <int POL>
-__device__ __forceinline__ void st128(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
-    u32x4_t t = {v.x, v.y, v.z, v.w};
-    __builtin_amdgcn_raw_buffer_store_b128(t, r, off, 0, POL);
 }
 __device__ __forceinline__ unsigned atomic_add_dev(uint32_t* p, unsigned v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -116,54 +118,191 @@ __device__ __forceinline__ uint32_t f2h(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (half_t)x);
 }
 __device__ __forceinline__ float r16(float x) { return (float)(half_t)x; }
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima).
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// Grid barrier, called by every thread of every workgroup; wave 0 lane 0 arrives
-// and polls once every wave's stores of the phase have completed.
-struct Barrier {
+// ------------------------------------------------------------ tagged data
+struct Flow {
     uint32_t* ctl;
-    int set;
-    unsigned round;
+    int32_t* status;
+    uint32_t tag;                 // 1..65535
+    unsigned long long deadline;  // realtime clock
 };
-__device__ __forceinline__ bool grid_sync(Barrier& b, int nwg, int* s_flag, int32_t* status) {
-    // Compute waves have waited for their stores before issuing the next phase's
-    // prefetch (which must stay in flight across the barrier); the sync wave has
-    // nothing in flight but its own staging stores.
-    if (threadIdx.x < 64) __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    ++b.round;
-    if (threadIdx.x == 0) {
-        const int x = blockIdx.x % kXcds;
-        const unsigned per = (unsigned)(nwg / kXcds);
-        const unsigned prev = atomic_add_dev(b.ctl + ctl_xcd(b.set, x), 1u);
-        if (prev + 1 == b.round * per) atomic_add_dev(b.ctl + ctl_top(b.set), 1u);
-        const unsigned target = b.round * (unsigned)kXcds;
-        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-        int ok = 1;
-        for (unsigned it = 0;; ++it) {
-            if ((int)(load_dev(b.ctl + ctl_top(b.set)) - target) >= 0) break;
-            if ((it & 15) == 15 && load_dev(b.ctl + kCtlAbort) != 0) {
-                ok = 0;
-                break;
-            }
-            if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
-                store_dev(b.ctl + kCtlAbort, 1u);
-                ok = 0;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        if (!ok) store_status(status, 1);
-        *s_flag = ok;
+
+// One round of a bounded wait: false when this launch stops (another workgroup
+// gave up, or the deadline passed and this one gives up).
+__device__ __forceinline__ bool keep_waiting(const Flow& f, unsigned it) {
+    if ((it & 7) == 7 && load_dev(f.ctl + kCtlAbort) == f.tag) return false;
+    if (__builtin_amdgcn_s_memrealtime() > f.deadline) {
+        store_dev(f.ctl + kCtlAbort, f.tag);
+        store_status(f.status, 1);
+        return false;
     }
+    __builtin_amdgcn_s_sleep(1);
+    return true;
+}
+
+__device__ __forceinline__ bool tags_ok(const uint4& a, const uint4& b, uint32_t tag) {
+    return ((a.x >> 16) == tag) & ((a.y >> 16) == tag) & ((a.z >> 16) == tag) &
+           ((a.w >> 16) == tag) & ((b.x >> 16) == tag) & ((b.y >> 16) == tag) &
+           ((b.z >> 16) == tag) & ((b.w >> 16) == tag);
+}
+// The fp16 halves of 8 tagged words, in order.
+__device__ __forceinline__ uint4 untag(const uint4& a, const uint4& b) {
+    return make_uint4(__builtin_amdgcn_perm(a.y, a.x, 0x05040100u),
+                      __builtin_amdgcn_perm(a.w, a.z, 0x05040100u),
+                      __builtin_amdgcn_perm(b.y, b.x, 0x05040100u),
+                      __builtin_amdgcn_perm(b.w, b.z, 0x05040100u));
+}
+
+// Waits until the 8-word units at byte offsets off[k] (those with bit k of
+// `pend`) carry this launch's tag and returns their fp16 values. Offsets of units
+// not wanted lie past the buffer (they read zeros and touch no memory). False:
+// the launch stops.
+template <int N>
+__device__ __forceinline__ bool poll_units(__amdgpu_buffer_rsrc_t r, const uint32_t (&off)[N],
+                                           unsigned pend, const Flow& f, uint4 (&out)[N]) {
+    uint4 lo[N], hi[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        lo[k] = ld128<kSC1>(r, off[k]);
+        hi[k] = ld128<kSC1>(r, off[k] + 16u);
+    }
+    for (unsigned it = 0;; ++it) {
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if (((pend >> k) & 1u) && tags_ok(lo[k], hi[k], f.tag)) {
+                out[k] = untag(lo[k], hi[k]);
+                pend &= ~(1u << k);
+            }
+        if (!pend) return true;
+        if (!keep_waiting(f, it)) return false;
+#pragma unroll
+        for (int k = 0; k < N; ++k)
+            if ((pend >> k) & 1u) {
+                lo[k] = ld128<kSC1>(r, off[k]);
+                hi[k] = ld128<kSC1>(r, off[k] + 16u);
+            }
+    }
+}
+
+// Tagged store of one fp16 value.
+__device__ __forceinline__ void put(__amdgpu_buffer_rsrc_t r, int idx, float v, uint32_t tag) {
+    __builtin_amdgcn_raw_buffer_store_b32(f2h(v) | (tag << 16), r, (uint32_t)idx * 4u, 0, kSC1);
+}
+
+// Every thread of the workgroup calls this after its own waits: true when no
+// thread of the workgroup gave up.
+__device__ __forceinline__ bool all_ok(bool ok, int* s_fail) {
+    if (!ok) *s_fail = 1;
     __syncthreads();
-    return *s_flag != 0;
+    return *s_fail == 0;
+}
+
+// Sum of the 8 fp16 values of a unit, and (on the first lane of each 4 lanes) the
+// sum over the 32-value chunk those 4 consecutive lanes hold, into sSum[chunk].
+__device__ __forceinline__ void chunk_sum(uint4 v, bool valid, int unit, float* sSum) {
+    const half_t* h = reinterpret_cast<const half_t*>(&v);
+    float t = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t += (float)h[e];
+    t = group_sum<4>(valid ? t : 0.f);
+    if (valid && (unit & 3) == 0) sSum[unit >> 2] = t;
+}
+
+// Stage a tagged fp16 vector of n values (n % 32 == 0, n <= kMaxUnits * 4096) into
+// LDS in pair order, with its 32-value chunk sums in sSum. The caller has passed a
+// workgroup barrier since sA and sSum were last read.
+__device__ __forceinline__ bool stage_poll(const uint32_t* src, int n, uint4* sA, float* sSum,
+                                           const Flow& f, int* s_fail) {
+    const int units = n / 8;
+    const uint32_t bytes = (uint32_t)n * 4u;
+    uint32_t off[kMaxUnits];
+    unsigned pend = 0;
+#pragma unroll
+    for (int k = 0; k < kMaxUnits; ++k) {
+        const int u = threadIdx.x + k * kThreads;
+        off[k] = u < units ? (uint32_t)u * 32u : bytes;
+        if (u < units) pend |= 1u << k;
+    }
+    uint4 v[kMaxUnits];
+    const bool ok = poll_units<kMaxUnits>(rsrc(src, bytes), off, pend, f, v);
+#pragma unroll
+    for (int k = 0; k < kMaxUnits; ++k) {
+        const int u = threadIdx.x + k * kThreads;
+        if (ok && u < units) sA[u] = permute_act8(v[k]);
+        chunk_sum(v[k], ok && u < units, u, sSum);
+    }
+    return all_ok(ok, s_fail);
+}
+
+// Residual add + RMS norm of one D-vector (D <= 4096) into LDS: r = fp16(in +
+// r_prev) (r = in when r_prev is not added), a = fp16(r * rsqrt(mean(r^2) + eps)
+// * gamma); r kept in sR, a staged in pair order in sA. `in` is a tagged vector
+// (src) or a constant fp16 row.
+__device__ __forceinline__ bool norm_poll(const uint32_t* src, const half_t* row, bool add_prev,
+                                          const half_t* gamma, float eps, int D, uint4* sR,
+                                          uint4* sA, float* sSum, float* sRed, const Flow& f,
+                                          int* s_fail) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int units = D / 8;
+    const bool mine = tid < units;
+    const uint4 gv = mine ? reinterpret_cast<const uint4*>(gamma)[tid] : make_uint4(0, 0, 0, 0);
+    uint4 v = make_uint4(0, 0, 0, 0);
+    bool ok = true;
+    if (src) {
+        const uint32_t bytes = (uint32_t)D * 4u;
+        const uint32_t off[1] = {mine ? (uint32_t)tid * 32u : bytes};
+        uint4 out[1];
+        ok = poll_units<1>(rsrc(src, bytes), off, mine ? 1u : 0u, f, out);
+        v = out[0];
+    } else if (mine) {
+        v = reinterpret_cast<const uint4*>(row)[tid];
+    }
+    float ss = 0.f;
+    if (mine && ok) {
+        if (add_prev) {
+            const uint4 pv = sR[tid];
+            const half_t* a = reinterpret_cast<const half_t*>(&v);
+            const half_t* b = reinterpret_cast<const half_t*>(&pv);
+            half_t t[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) t[e] = (half_t)((float)a[e] + (float)b[e]);
+            v = *reinterpret_cast<const uint4*>(t);
+        }
+        sR[tid] = v;
+        const half_t* t = reinterpret_cast<const half_t*>(&v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += (float)t[e] * (float)t[e];
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) sRed[wave] = ss;
+    if (!all_ok(ok, s_fail)) return false;
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += sRed[w];
+    const float scale = 1.0f / sqrtf(tot / (float)D + eps);
+    uint4 ov = make_uint4(0, 0, 0, 0);
+    if (mine) {
+        const half_t* t = reinterpret_cast<const half_t*>(&v);
+        const half_t* g = reinterpret_cast<const half_t*>(&gv);
+        half_t o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (half_t)((float)t[e] * scale * (float)g[e]);
+        ov = *reinterpret_cast<const uint4*>(o);
+        sA[tid] = permute_act8(ov);
+    }
+    chunk_sum(ov, mine, tid, sSum);
+    __syncthreads();
+    return true;
 }
 
 // 16 lanes (dims 8*li .. 8*li+7 of one head) rotate their 8 values, non-interleaved
-// pairs (i, i + half) over dims [0, 2*half); the partner lane is li ^ (half / 8)
-// inside the same 16-lane group (half is a multiple of 8 and at most 64).
-__device__ __forceinline__ void rope8(float (&x)[8], int li, int half, const half_t* cs,
-                                      const half_t* sn) {
+// pairs (i, i + half) over dims [0, 2*half), with the cos/sin row cs/sn [half]; the
+// partner lane is li ^ (half / 8) inside the same 16-lane group (half is
+// a multiple of 8 and at most 64).
+__device__ __forceinline__ void rope8(float (&x)[8], int li, int half, const float* cs,
+                                      const float* sn) {
     if (half == 0) return;
     const int off = half / 8;
     const int lane = threadIdx.x & 63;
@@ -174,22 +313,26 @@ __device__ __forceinline__ void rope8(float (&x)[8], int li, int half, const hal
     const int d0 = li * 8;
     if (d0 >= 2 * half) return;
     const bool low = d0 < half;
+    const int b = low ? d0 : d0 - half;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int p = (low ? d0 : d0 - half) + i;
-        const float c = (float)cs[p], s = (float)sn[p];
-        x[i] = low ? x[i] * c - px[i] * s : x[i] * c + px[i] * s;
-    }
+    for (int i = 0; i < 8; ++i)
+        x[i] = low ? x[i] * cs[b + i] - px[i] * sn[b + i] : x[i] * cs[b + i] + px[i] * sn[b + i];
+}
+
+// An opaque copy of a per-lane value: what is computed from it inside a loop is
+// recomputed there instead of being hoisted and held (or spilled) across the loop.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
 }
 
 // ------------------------------------------------------------ weight rows
 // Row chunks of one phase are fetched straight into LDS (buffer_load_dwordx4
 // ... lds: lane i's 16 bytes land at the slot base + 16 * i), so the weights a
-// wave prefetches across a barrier hold no registers. A compute wave owns
-// kRegionSlots slots of 64 x 16 bytes; the per-chunk fp16 scales stay in VGPRs.
-// Chunk c = li + j * LPR of row n goes to slot `slot0 + j`; rows past N and
-// chunks past C read zeros (offsets past the buffer ranges), so the loads are
-// unconditional.
+// wave prefetches across a wait hold no registers. A wave owns kRegion slots of
+// 64 x 16 bytes; the per-chunk fp16 scales stay in VGPRs. Chunk c = li + j * LPR
+// of row n goes to slot `slot0 + j`; rows past N and chunks past C read zeros
+// (offsets past the buffer ranges), so the loads are unconditional.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint4* slot) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         r, (__attribute__((address_space(3))) void*)slot, 16, voff, 0, 0, kCachePolicyNT);
@@ -224,14 +367,38 @@ __device__ __forceinline__ void fetch_rows(const WeightRef& wr, int n, int li, u
     }
 }
 
+// sum(a * q) over one 32-code chunk. The codes are never converted: a 16-bit half
+// whose bits are 0000 0000 qqqq 0000 or 0000 0000 0000 qqqq is the fp16 subnormal
+// q * 2^-20 or q * 2^-24, so one AND per pair of codes, (w & 0x000F000F) for
+// nibbles (j, j+4) and (w & 0x00F000F0) for (j+1, j+5), gives both operands of
+// v_dot2_f32_f16 exactly (products exact, fp32 accumulation), and two exact
+// power-of-two multiplies undo the scaling. The activations are in pair order
+// (a_j, a_j+4), as permute_act8 stages them.
+__device__ __forceinline__ float dot32_codes(const uint4 (&av)[4], uint4 w) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t aw[4] = {av[i].x, av[i].y, av[i].z, av[i].w};
+        const uint32_t x = words[i], y = words[i] >> 8;
+        const uint32_t q[4] = {x & 0x000F000Fu, x & 0x00F000F0u, y & 0x000F000Fu, y & 0x00F000F0u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const half2_t a = __builtin_bit_cast(half2_t, aw[j]);
+            const half2_t b = __builtin_bit_cast(half2_t, q[j]);
+            if (j & 1) d1 = __builtin_amdgcn_fdot2(a, b, d1, false);
+            else d0 = __builtin_amdgcn_fdot2(a, b, d0, false);
+        }
+    }
+    return d0 * 16777216.0f + d1 * 1048576.0f;
+}
+
 // Dot product of a lane's chunks (in LDS slots) with the staged activations (pair
-// order, 4 uint4 per 32-code chunk), symmetric int4 (zero point 8):
-// sum_j s_j * sum(a * (q - 8)).
+// order, 4 uint4 per 32-code chunk; sSum the chunk sums), symmetric int4 (zero
+// point 8): sum_j s_j * (sum(a * q) - 8 * sum(a)).
 template <int LPR, int CPL>
 __device__ __forceinline__ float row_dot(const uint4* slot0, const uint32_t (&sc)[CPL],
-                                         const uint4* sA, int C, int li) {
-    const half_t zo = (half_t)1032.0f;
-    const half2_t zoff = {zo, zo};
+                                         const uint4* sA, const float* sSum, int C, int li) {
     const int lane = threadIdx.x & 63;
     float acc = 0.f;
 #pragma unroll
@@ -239,14 +406,14 @@ __device__ __forceinline__ float row_dot(const uint4* slot0, const uint32_t (&sc
         const int c = li + j * LPR;
         if (c < C) {
             const uint4 av[4] = {sA[4 * c], sA[4 * c + 1], sA[4 * c + 2], sA[4 * c + 3]};
-            acc = fmaf(h2f(sc[j]), dot32_pairs(av, slot0[j * 64 + lane], zoff), acc);
+            acc = fmaf(h2f(sc[j]), fmaf(-8.f, sSum[c], dot32_codes(av, slot0[j * 64 + lane])), acc);
         }
     }
     return acc;
 }
 
-// Register form for the lm_head stream (after the layer loop, where registers
-// are free): the chunks themselves in VGPRs.
+// Register form for the lm_head stream and the gate/up groups beyond the
+// prefetched ones: the chunks themselves in VGPRs.
 template <int CPL>
 struct Rows {
     uint4 w[CPL];
@@ -265,609 +432,480 @@ __device__ __forceinline__ void load_rows(Rows<CPL>& r, const WeightRef& wr, int
     }
 }
 template <int LPR, int CPL>
-__device__ __forceinline__ float rows_dot(const Rows<CPL>& r, const uint4* sA, int C, int li) {
-    const half_t zo = (half_t)1032.0f;
-    const half2_t zoff = {zo, zo};
+__device__ __forceinline__ float rows_dot(const Rows<CPL>& r, const uint4* sA, const float* sSum,
+                                          int C, int li) {
     float acc = 0.f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int c = li + j * LPR;
         if (c < C) {
             const uint4 av[4] = {sA[4 * c], sA[4 * c + 1], sA[4 * c + 2], sA[4 * c + 3]};
-            acc = fmaf(h2f(r.s[j]), dot32_pairs(av, r.w[j], zoff), acc);
+            acc = fmaf(h2f(r.s[j]), fmaf(-8.f, sSum[c], dot32_codes(av, r.w[j])), acc);
         }
     }
     return acc;
 }
 
-// Residual add + RMS norm of one D-vector into LDS: r = fp16(in + r_prev) (or
-// r = in when r_prev is not added), a = fp16(r * rsqrt(mean(r^2) + eps) * gamma),
-// r kept in sR, a staged in pair order in sA. `in` comes from `src` through sc1
-// loads (or plain loads for a constant table).
-template <int POL>
-__device__ __forceinline__ void norm_stage(const half_t* src, bool add_prev,
-                                           const half_t* gamma, float eps, int D, uint4* sR,
-                                           uint4* sA, float* sRed) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int units = D / 8;
-    const __amdgpu_buffer_rsrc_t rs = rsrc(src, (uint32_t)D * 2);
-    float ss = 0.f;
-    for (int u = tid; u < units; u += kThreads) {
-        uint4 v = ld128<POL>(rs, (uint32_t)u * 16);
-        if (add_prev) {
-            const uint4 pv = sR[u];
-            const half_t* a = reinterpret_cast<const half_t*>(&v);
-            const half_t* b = reinterpret_cast<const half_t*>(&pv);
-            half_t t[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) t[e] = (half_t)((float)a[e] + (float)b[e]);
-            v = *reinterpret_cast<const uint4*>(t);
-        }
-        sR[u] = v;
-        const half_t* t = reinterpret_cast<const half_t*>(&v);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += (float)t[e] * (float)t[e];
+// (value, index) argmax step: lowest index wins ties, a record without an index
+// never wins, NaN never wins (comparisons with it are false).
+__device__ __forceinline__ void arg_take(float& best, int& bi, float ov, int oi) {
+    if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
+        best = ov;
+        bi = oi;
     }
-    ss = wave_sum(ss);
-    if (lane == 0) sRed[wave] = ss;
-    __syncthreads();
-    float tot = 0.f;
+}
+__device__ __forceinline__ void arg_wave(float& best, int& bi) {
 #pragma unroll
-    for (int w = 0; w < kThreads / 64; ++w) tot += sRed[w];
-    const float scale = 1.0f / sqrtf(tot / (float)D + eps);
-    for (int u = tid; u < units; u += kThreads) {
-        const uint4 v = sR[u];
-        const uint4 gv = reinterpret_cast<const uint4*>(gamma)[u];
-        const half_t* t = reinterpret_cast<const half_t*>(&v);
-        const half_t* g = reinterpret_cast<const half_t*>(&gv);
-        half_t o[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = (half_t)((float)t[e] * scale * (float)g[e]);
-        sA[u] = permute_act8(*reinterpret_cast<const uint4*>(o));
-    }
-    __syncthreads();
+    for (int sh = 32; sh >= 1; sh >>= 1) arg_take(best, bi, __shfl_xor(best, sh, 64), __shfl_xor(bi, sh, 64));
 }
-
-// Copy n fp16 values written by other workgroups (sc1) into LDS in pair order.
-__device__ __forceinline__ void stage_vec(const half_t* src, int n, uint4* sA) {
-    const __amdgpu_buffer_rsrc_t rs = rsrc(src, (uint32_t)n * 2);
-    for (int u = threadIdx.x; u < n / 8; u += kThreads)
-        sA[u] = permute_act8(ld128<kSC1>(rs, (uint32_t)u * 16));
-    __syncthreads();
-}
-
-__device__ __forceinline__ void st_half_sc1(half_t* base, uint32_t bytes, int idx, float v) {
-    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)f2h(v), rsrc(base, bytes), (uint32_t)idx * 2u,
-                                          0, kSC1);
-}
-
-// Online-softmax state of a lane (8 dims) for N query heads.
-template <int N>
-struct AttnState {
-    float m[N], l[N], o[N][8];
-};
 
 constexpr int gu_groups(int cpld) { return cpld == 3 ? 3 : 2; }
-// Slot plan of a compute wave's LDS region (chunks of 64 x 16 bytes):
-//   QKV [0, CPLD)              prefetched at the end of phase E (or at start)
-//   attention K [0, P), V [P, 2P), P = kPrefSteps   end of phase A
-//   o_proj [GU, GU + CPLD)      end of phase A      (GU = gate/up slots)
-//   gate/up [0, GU)             end of phase B
-//   down [GU, GU + 5)           end of phase C
-// Every range is written only after the data it overlaps was consumed.
+// Slot plan of a wave's LDS region (chunks of 64 x 16 bytes):
+//   QKV [0, CPLD)                  end of phase E (or at the start)
+//   o_proj [kLo, kLo + CPLD)       end of phase A (o_proj workgroups)
+//   attention K [0, P), V [P, 2P)  end of phase A (attention workgroups)
+//   gate/up [0, kGu * CPLD)        end of phase C / B
+//   down [kLo, kLo + 5)            end of phase D
+// Every range is written only after the wave consumed what it overlaps.
+constexpr int region_lo(int cpld) { return gu_groups(cpld) * cpld; }
 constexpr int region_slots(int cpld) {
-    const int gu = gu_groups(cpld) * cpld;
-    const int att = 2 * kPrefSteps;
-    const int lo = gu > att ? gu : att;
-    return lo + (cpld > kIChunksPerLane ? cpld : kIChunksPerLane);
+    return region_lo(cpld) + (cpld > kIChunksPerLane ? cpld : kIChunksPerLane);
 }
+constexpr int kv_pref_steps(int cpld) { return region_slots(cpld) / 2; }
 
-template <int HD, int CPLD, int G>
+template <int HD, int CPLD>
 __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
     extern __shared__ uint4 smem[];
-    __shared__ float sRed[16];
-    __shared__ int s_flag;
-    __shared__ float s_am[kComputeWaves][kGMax], s_al[kComputeWaves][kGMax];
-    __shared__ float s_arg_v[8];
-    __shared__ int s_arg_i[8];
+    __shared__ OrtmiDecoderLayer s_layers[kMaxLayers];
+    __shared__ float sRed[kWaves];
+    __shared__ int s_fail;
+    __shared__ uint32_t s_tag;
+    __shared__ float s_am[kWaves], s_al[kWaves];
+    __shared__ float s_arg_v[kWaves];
+    __shared__ int s_arg_i[kWaves];
+    __shared__ float s_cos[64], s_sin[64];
+    __shared__ float s_out[64];  // a phase's outputs of this workgroup, stored as one block
     constexpr int kGu = gu_groups(CPLD);
-    constexpr int kGuSlots = kGu * CPLD;
-    constexpr int kSlotsLo = kGuSlots > 2 * kPrefSteps ? kGuSlots : 2 * kPrefSteps;
+    constexpr int kLo = region_lo(CPLD);
     constexpr int kRegion = region_slots(CPLD);
-    static_assert(kSlotsLo + CPLD <= kRegion && kSlotsLo + kIChunksPerLane <= kRegion, "slots");
+    constexpr int kPref = kv_pref_steps(CPLD);
+    static_assert(kLo + CPLD <= kRegion && 2 * kPref <= kRegion, "slots");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wg = blockIdx.x, nwg = p.nwg;
-    const int cw = wave - 1;  // compute wave index, -1 for the sync wave
-    const int TW = kComputeWaves * nwg;
-    const int gw = cw * nwg + wg;  // global compute-wave index (spreads work over CUs)
+    const int TW = kWaves * nwg;
+    const int gw = wave * nwg + wg;  // global wave index (spreads work over CUs)
     const int D = p.D, H = p.H, KV = p.KV, I = p.I;
-    const int NQ = (H + 2 * KV) * HD;
-    const int CD = D / 32, CO = H * HD / 32, CI = I / 32;
+    const int NQ = (H + 2 * KV) * HD, HO = H * HD;
+    const int CD = D / 32, CO = HO / 32, CI = I / 32;
     const int li16 = lane & 15, grp = lane >> 4;
+    const int NC = nwg - H;  // workgroups [0, NC) run o_proj, [NC, nwg) attention
+    const bool attn_wg = wg >= NC;
+    const int a_head = wg - NC;
 
-    // LDS: weight regions (7 waves), activations / attention merge area, residual.
-    uint4* sW = smem;
-    uint4* wreg = sW + (size_t)(cw < 0 ? 0 : cw) * kRegion * 64;
-    uint4* sA = sW + (size_t)kComputeWaves * kRegion * 64;
-    float* sO = reinterpret_cast<float*>(sA);  // [7][kGMax][HD], phase B only
-    const int a_units = (I > D ? I : D) / 8;
-    const int o_units = kComputeWaves * kGMax * HD / 4;
-    uint4* sR = sA + (a_units > o_units ? a_units : o_units);
+    // LDS: weight regions, activations (norm outputs; staged vectors), residual,
+    // attention merge.
+    uint4* wreg = smem + (size_t)wave * kRegion * 64;
+    uint4* sA0 = smem + (size_t)kWaves * kRegion * 64;
+    uint4* sA1 = sA0 + D / 8;
+    uint4* sR = sA1 + (HO > I ? HO : I) / 8;
+    float* sO = reinterpret_cast<float*>(sR + D / 8);  // [kWaves][HD]
+    float* sSum0 = sO + kWaves * HD;                     // chunk sums of sA0 [D / 32]
+    float* sSum1 = sSum0 + D / 32;                       // chunk sums of sA1
 
-    // Total length, context, splits: the same on every workgroup.
+    if (tid == 0) s_fail = 0;
+    {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(p.layers);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(s_layers);
+        const int words = p.L * (int)(sizeof(OrtmiDecoderLayer) / 4);
+        for (int i = tid; i < words; i += kThreads) dst[i] = src[i];
+    }
     const int total = *p.total;
     if (total < 1 || total > p.cap || (p.half > 0 && total > p.max_pos)) {
         if (wg == 0 && tid == 0) store_status(p.status, 3);
         return;
     }
+    if (tid == 0) {
+        const unsigned started = atomic_add_dev(p.ctl + kCtlStart, 1u);
+        s_tag = (started / (unsigned)nwg) % 65535u + 1u;
+    }
+    __syncthreads();
+    const Flow f{p.ctl, p.status, s_tag, __builtin_amdgcn_s_memrealtime() + kDeadlineTicks};
+    const uint32_t tag = f.tag;
     const int ctx = total - 1;  // cached keys; the new key sits at index ctx
-    int NS = (total + kKeySlots * kPrefSteps - 1) / (kKeySlots * kPrefSteps);
-    NS = NS < 1 ? 1 : (NS > kNSMax ? kNSMax : NS);
-    const int split_keys = (total + NS - 1) / NS;
 
-    Barrier bar{p.ctl, 0, 0};
-    bar.set = (int)load_dev(p.ctl + kCtlParity) & 1;
-
-    // Token id and embedding row (negative ids count from the end).
-    int64_t id = *p.input_id;
+    int64_t id = *p.input_id;  // negative ids count from the end
     if (id < 0) id += p.embed_rows;
     const bool bad_id = id < 0 || id >= p.embed_rows;
     if (bad_id) id = 0;
 
-    // Attention work of this workgroup: KV head a_kvh, keys [k0, k1).
-    const bool attn_wg = wg < KV * NS;
-    const int a_kvh = wg / NS, a_split = wg % NS;
-    const int k0 = a_split * split_keys;
-    const int k1 = min(k0 + split_keys, total);
-    const int slot = (cw < 0 ? 0 : cw) * 4 + grp;
-
+    // Attention workgroup: query head a_head of KV head a_kvh; the rotary row at
+    // position ctx goes to LDS.
+    const int a_kvh = attn_wg ? a_head / p.G : 0;
+    if (attn_wg && tid < p.half) {
+        s_cos[tid] = (float)p.cos[(size_t)ctx * p.half + tid];
+        s_sin[tid] = (float)p.sin[(size_t)ctx * p.half + tid];
+    }
+    const int a_steps = (total + kKeySlots - 1) / kKeySlots;
+    const uint32_t kv_bytes = (uint32_t)KV * p.cap * HD * 2;
+    // Rows are dealt to workgroups in contiguous ranges (a phase's outputs of one
+    // workgroup are then one block of the vector, written by one store instruction:
+    // lines written piecewise by many CUs cost several microseconds to settle), and
+    // within a workgroup to its waves.
+    const int ng_q = (NQ + 3) / 4, ng_o = (D + 3) / 4, ng_gu = (2 * I + 3) / 4;
+    const int gq = p.gq, go = p.go, ggu = p.ggu, gd = p.gd;
+    const int q_g = wave < gq ? wg * gq + wave : ng_q;                  // QKV group
+    const int o_g = !attn_wg && wave < go ? wg * go + wave : ng_o;      // o_proj group
+    const int d_row = wave < gd ? wg * gd + wave : D;                   // down row
     uint32_t sq[CPLD], so[CPLD], sg[kGu][CPLD], sd[kIChunksPerLane];
-
-    auto qkv_fetch = [&](const OrtmiDecoderLayer& ly) {
-        const WeightRef wr = weight_ref(ly.qkv_weight, ly.qkv_scales, NQ, CD);
-        const int ng = (NQ + 3) / 4;
-        fetch_rows<16, CPLD>(wr, gw < ng ? 4 * gw + grp : NQ, li16, wreg, sq);
-    };
-    auto kv_fetch = [&](const OrtmiDecoderLayer& ly) {
-        const uint32_t bytes = (uint32_t)KV * p.cap * HD * 2;
-        const __amdgpu_buffer_rsrc_t rk = rsrc(ly.k_cache, bytes), rv = rsrc(ly.v_cache, bytes);
-#pragma unroll
-        for (int t = 0; t < kPrefSteps; ++t) {
-            const int key = k0 + t * kKeySlots + slot;
-            const bool ok = attn_wg && key < k1 && key < ctx;
-            const uint32_t off = ok ? ((uint32_t)(a_kvh * p.cap + key) * HD + li16 * 8) * 2u : bytes;
-            dma16(rk, off, wreg + t * 64);
-            dma16(rv, off, wreg + (kPrefSteps + t) * 64);
-        }
-    };
-    auto o_fetch = [&](const OrtmiDecoderLayer& ly) {
-        const WeightRef wr = weight_ref(ly.o_weight, ly.o_scales, D, CO);
-        const int ng = (D + 3) / 4;
-        fetch_rows<16, CPLD>(wr, gw < ng ? 4 * gw + grp : D, li16, wreg + kSlotsLo * 64, so);
-    };
-    auto gu_fetch = [&](const OrtmiDecoderLayer& ly) {
-        const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
-        const int ng = (2 * I + 3) / 4;
-#pragma unroll
-        for (int k = 0; k < kGu; ++k) {
-            const int g = gw + k * TW;
-            fetch_rows<16, CPLD>(wr, g < ng ? 4 * g + grp : 2 * I, li16, wreg + k * CPLD * 64,
-                                 sg[k]);
-        }
-    };
-    auto down_fetch = [&](const OrtmiDecoderLayer& ly) {
-        const WeightRef wr = weight_ref(ly.down_weight, ly.down_scales, D, CI);
-        fetch_rows<64, kIChunksPerLane>(wr, gw < D ? gw : D, lane, wreg + kSlotsLo * 64, sd);
-    };
-
-    if (cw >= 0) qkv_fetch(p.layers[0]);
+    {
+        const WeightRef wr = weight_ref(s_layers[0].qkv_weight, s_layers[0].qkv_scales, NQ, CD);
+        fetch_rows<16, CPLD>(wr, q_g < ng_q ? 4 * q_g + grp : NQ, li16, wreg, sq);
+    }
+    const uint32_t* prev_dout = nullptr;
 
     // ------------------------------------------------------------------- layers
     for (int l = 0; l < p.L; ++l) {
-        const OrtmiDecoderLayer& ly = p.layers[l];
+        const OrtmiDecoderLayer& ly = s_layers[l];
+        // Lane-derived indices, recomputed per layer rather than held across it.
+        const int lane = opaque(threadIdx.x & 63);
+        const int li16 = lane & 15, grp = lane >> 4;
+        const int slot = wave * 4 + grp;  // attention key slot of this lane group
+        auto kv_off = [&](int t) -> uint32_t {
+            const int key = slot + t * kKeySlots;
+            return key < ctx ? ((uint32_t)(a_kvh * p.cap + key) * HD + li16 * 8) * 2u : kv_bytes;
+        };
+        auto qkv_fetch = [&](const OrtmiDecoderLayer& lz) {
+            const WeightRef wr = weight_ref(lz.qkv_weight, lz.qkv_scales, NQ, CD);
+            fetch_rows<16, CPLD>(wr, q_g < ng_q ? 4 * q_g + grp : NQ, li16, wreg, sq);
+        };
+        auto kv_fetch = [&]() {
+            const __amdgpu_buffer_rsrc_t rk = rsrc(ly.k_cache, kv_bytes), rv = rsrc(ly.v_cache, kv_bytes);
+#pragma unroll
+            for (int t = 0; t < kPref; ++t) {
+                const uint32_t off = kv_off(t);
+                dma16(rk, off, wreg + t * 64);
+                dma16(rv, off, wreg + (kPref + t) * 64);
+            }
+        };
+        auto o_fetch = [&]() {
+            const WeightRef wr = weight_ref(ly.o_weight, ly.o_scales, D, CO);
+            fetch_rows<16, CPLD>(wr, o_g < ng_o ? 4 * o_g + grp : D, li16, wreg + kLo * 64, so);
+        };
+        auto gu_fetch = [&]() {
+            const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
+#pragma unroll
+            for (int k = 0; k < kGu; ++k) {
+                const int lg = wave + k * kWaves;
+                const int g = lg < ggu ? wg * ggu + lg : ng_gu;
+                fetch_rows<16, CPLD>(wr, g < ng_gu ? 4 * g + grp : 2 * I, li16,
+                                     wreg + k * CPLD * 64, sg[k]);
+            }
+        };
+        auto down_fetch = [&]() {
+            const WeightRef wr = weight_ref(ly.down_weight, ly.down_scales, D, CI);
+            fetch_rows<64, kIChunksPerLane>(wr, d_row, lane, wreg + kLo * 64, sd);
+        };
+        uint32_t* f_qkv = p.flow + (size_t)l * p.flow_stride;
+        uint32_t* f_att = f_qkv + NQ;
+        uint32_t* f_y = f_att + HO;
+        uint32_t* f_act = f_y + D;
+        uint32_t* f_dout = f_act + I;
+
         // Phase A: input norm (+ residual), merged QKV GEMV.
-        if (l == 0) {
-            norm_stage<0>(p.embed + id * D, false, static_cast<const half_t*>(ly.ln1_gamma),
-                          ly.ln1_epsilon, D, sR, sA, sRed);
-        } else {
-            norm_stage<kSC1>(p.dout, true, static_cast<const half_t*>(ly.ln1_gamma),
-                             ly.ln1_epsilon, D, sR, sA, sRed);
-        }
-        if (cw >= 0) {
-            const int ng = (NQ + 3) / 4;
+        if (!norm_poll(prev_dout, p.embed + id * D, l > 0, static_cast<const half_t*>(ly.ln1_gamma),
+                       ly.ln1_epsilon, D, sR, sA0, sSum0, sRed, f, &s_fail))
+            return;
+        {
             __builtin_amdgcn_s_waitcnt(0);
-            float v = group_sum<16>(row_dot<16, CPLD>(wreg, sq, sA, CD, li16));
-            if (gw < ng && li16 == 0 && 4 * gw + grp < NQ)
-                st_half_sc1(p.qkv, (uint32_t)NQ * 2, 4 * gw + grp, v);
-            __builtin_amdgcn_s_waitcnt(0);
-            kv_fetch(ly);
-            o_fetch(ly);
-        }
-        if (!grid_sync(bar, nwg, &s_flag, p.status)) return;
-        if (bar.round == 1 && wg == 0 && tid == 0) {
-            // Every workgroup read the parity before arriving here: reset the other
-            // counter set for the next launch and flip the parity.
-            const int other = bar.set ^ 1;
-            store_dev(p.ctl + ctl_top(other), 0u);
-            for (int x = 0; x < kXcds; ++x) store_dev(p.ctl + ctl_xcd(other, x), 0u);
-            store_dev(p.ctl + kCtlParity, (unsigned)other);
+            const float v = group_sum<16>(row_dot<16, CPLD>(wreg, sq, sA0, sSum0, CD, li16));
+            if (li16 == 0 && wave < gq) s_out[wave * 4 + grp] = v;
+            __syncthreads();
+            if (tid < 4 * gq && 4 * wg * gq + tid < NQ)
+                put(rsrc(f_qkv, (uint32_t)NQ * 4), 4 * wg * gq + tid, s_out[tid], tag);
+            wait_lds();
+            if (attn_wg) kv_fetch();
+            else o_fetch();
         }
 
-        // Phase B: attention (KV * NS workgroups), split partials. The query heads
-        // of the KV group are taken HP at a time over the same K/V rows in LDS,
-        // which bounds the per-lane softmax state.
         if (attn_wg) {
-            constexpr int HP = G < 2 ? G : 2;
-            const __amdgpu_buffer_rsrc_t rq = rsrc(p.qkv, (uint32_t)NQ * 2);
-            const half_t* cs = p.half ? p.cos + (size_t)ctx * p.half : nullptr;
-            const half_t* sn = p.half ? p.sin + (size_t)ctx * p.half : nullptr;
-            if (cw >= 0) {
-                __builtin_amdgcn_s_waitcnt(0);
-                float kn[8], vn[8];
-                uint32_t knw[4];
-                const uint4 kraw = ld128<kSC1>(rq, (uint32_t)((H + a_kvh) * HD + li16 * 8) * 2u);
-                const uint4 vraw =
-                    ld128<kSC1>(rq, (uint32_t)((H + KV + a_kvh) * HD + li16 * 8) * 2u);
-                const half_t* kh = reinterpret_cast<const half_t*>(&kraw);
-                const half_t* vh = reinterpret_cast<const half_t*>(&vraw);
+            // Phase B: attention for query head a_head over keys [0, total).
+            const __amdgpu_buffer_rsrc_t rk = rsrc(ly.k_cache, kv_bytes), rv = rsrc(ly.v_cache, kv_bytes);
+            uint4 ringk[kKvRing], ringv[kKvRing];
+#pragma unroll
+            for (int r = 0; r < kKvRing; ++r) {
+                const uint32_t off = kv_off(kPref + r);
+                ringk[r] = ld128<kCachePolicyNT>(rk, off);
+                ringv[r] = ld128<kCachePolicyNT>(rv, off);
+            }
+            const uint32_t qbytes = (uint32_t)NQ * 4u;
+            const uint32_t off[3] = {(uint32_t)(a_head * HD + li16 * 8) * 4u,
+                                     (uint32_t)((H + a_kvh) * HD + li16 * 8) * 4u,
+                                     (uint32_t)((H + KV + a_kvh) * HD + li16 * 8) * 4u};
+            uint4 qkv3[3];
+            const bool ok = poll_units<3>(rsrc(f_qkv, qbytes), off, 7u, f, qkv3);
+            float q[8], kn[8], vn[8];
+            {
+                const half_t* qh = reinterpret_cast<const half_t*>(&qkv3[0]);
+                const half_t* kh = reinterpret_cast<const half_t*>(&qkv3[1]);
+                const half_t* vh = reinterpret_cast<const half_t*>(&qkv3[2]);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
+                    q[e] = (float)qh[e];
                     kn[e] = (float)kh[e];
                     vn[e] = (float)vh[e];
                 }
-                rope8(kn, li16, p.half, cs, sn);
-                half_t k8[8];
+            }
+            rope8(q, li16, p.half, s_cos, s_sin);
+            rope8(kn, li16, p.half, s_cos, s_sin);
+            uint32_t qw[4], kw_new[4];
+            {
+                half_t q8[8], k8[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) k8[e] = (half_t)kn[e];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) knw[e] = reinterpret_cast<const uint32_t*>(k8)[e];
-                // The split holding the new key appends it to the cache (shared
-                // buffer, written in place at row ctx).
-                if (cw == 0 && grp == 0 && ctx >= k0 && ctx < k1) {
-                    const size_t off = ((size_t)(a_kvh * p.cap + ctx) * HD + li16 * 8);
-                    *reinterpret_cast<uint4*>(static_cast<half_t*>(ly.k_cache) + off) =
-                        *reinterpret_cast<const uint4*>(k8);
-                    *reinterpret_cast<uint4*>(static_cast<half_t*>(ly.v_cache) + off) = vraw;
+                for (int e = 0; e < 8; ++e) {
+                    q8[e] = (half_t)q[e];
+                    k8[e] = (half_t)kn[e];
+                    kn[e] = (float)k8[e];
                 }
-                const float qscale = p.scale * 1.4426950408889634f;  // scores in log2 units
-                const int steps = (k1 - k0 + kKeySlots - 1) / kKeySlots;
-                const uint32_t bytes = (uint32_t)KV * p.cap * HD * 2;
-                const __amdgpu_buffer_rsrc_t rk = rsrc(ly.k_cache, bytes),
-                                             rv = rsrc(ly.v_cache, bytes);
-                for (int g0 = 0; g0 < G; g0 += HP) {
-                    AttnState<HP> st;
-                    uint32_t qh[HP][4];
 #pragma unroll
-                    for (int g = 0; g < HP; ++g) {
-                        st.m[g] = -INFINITY;
-                        st.l[g] = 0.f;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) st.o[g][e] = 0.f;
-                        const int head = a_kvh * G + g0 + g;
-                        const uint4 raw = ld128<kSC1>(rq, (uint32_t)(head * HD + li16 * 8) * 2u);
-                        const half_t* rh = reinterpret_cast<const half_t*>(&raw);
-                        float x[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) x[e] = (float)rh[e];
-                        rope8(x, li16, p.half, cs, sn);
-                        half_t q8[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) q8[e] = (half_t)x[e];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            qh[g][e] = reinterpret_cast<const uint32_t*>(q8)[e];
-                    }
-                    auto attend = [&](const uint4& kr, const uint4& vr, int key) {
-                        if (key >= k1) return;
-                        const bool fresh = key == ctx;
-                        const uint32_t kw[4] = {fresh ? knw[0] : kr.x, fresh ? knw[1] : kr.y,
-                                                fresh ? knw[2] : kr.z, fresh ? knw[3] : kr.w};
-                        float vv[8];
-                        const half_t* vb = reinterpret_cast<const half_t*>(&vr);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) vv[e] = fresh ? vn[e] : (float)vb[e];
-#pragma unroll
-                        for (int g = 0; g < HP; ++g) {
-                            float d = 0.f;
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, qh[g][e]),
-                                                           __builtin_bit_cast(half2_t, kw[e]), d,
-                                                           false);
-                            const float sc = group_sum<16>(d) * qscale;
-                            const float mn = fmaxf(st.m[g], sc);
-                            const float f = st.m[g] == -INFINITY ? 0.f : exp2f(st.m[g] - mn);
-                            const float pe = exp2f(sc - mn);
-                            st.l[g] = st.l[g] * f + pe;
-#pragma unroll
-                            for (int e = 0; e < 8; ++e)
-                                st.o[g][e] = fmaf(pe, vv[e], st.o[g][e] * f);
-                            st.m[g] = mn;
-                        }
-                    };
-#pragma unroll
-                    for (int t = 0; t < kPrefSteps; ++t)
-                        if (t < steps)
-                            attend(wreg[t * 64 + lane], wreg[(kPrefSteps + t) * 64 + lane],
-                                   k0 + t * kKeySlots + slot);
-                    for (int t = kPrefSteps; t < steps; ++t) {
-                        const int key = k0 + t * kKeySlots + slot;
-                        const bool ok = key < k1 && key < ctx;
-                        const uint32_t off =
-                            ok ? ((uint32_t)(a_kvh * p.cap + key) * HD + li16 * 8) * 2u : bytes;
-                        attend(ld128<0>(rk, off), ld128<0>(rv, off), key);
-                    }
-                    // Merge the 4 lane groups of the wave (same dims, other keys).
-#pragma unroll
-                    for (int g = 0; g < HP; ++g) {
-#pragma unroll
-                        for (int sh = 16; sh <= 32; sh <<= 1) {
-                            const float om = __shfl_xor(st.m[g], sh, 64);
-                            const float ol = __shfl_xor(st.l[g], sh, 64);
-                            const float mn = fmaxf(st.m[g], om);
-                            const float fa = st.m[g] == -INFINITY ? 0.f : exp2f(st.m[g] - mn);
-                            const float fb = om == -INFINITY ? 0.f : exp2f(om - mn);
-                            st.l[g] = st.l[g] * fa + ol * fb;
-#pragma unroll
-                            for (int e = 0; e < 8; ++e) {
-                                const float oo = __shfl_xor(st.o[g][e], sh, 64);
-                                st.o[g][e] = st.o[g][e] * fa + oo * fb;
-                            }
-                            st.m[g] = mn;
-                        }
-                        if (lane == 0) {
-                            s_am[cw][g0 + g] = st.m[g];
-                            s_al[cw][g0 + g] = st.l[g];
-                        }
-                        if (grp == 0) {
-#pragma unroll
-                            for (int e = 0; e < 8; ++e)
-                                sO[(cw * kGMax + g0 + g) * HD + li16 * 8 + e] = st.o[g][e];
-                        }
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    qw[e] = reinterpret_cast<const uint32_t*>(q8)[e];
+                    kw_new[e] = reinterpret_cast<const uint32_t*>(k8)[e];
                 }
             }
-            __syncthreads();
-            // Merge the 7 waves, write the split's partial per head: o[HD], m, l
-            // (records of HD + 4 floats keep every record 16-byte aligned).
-            const int stride = HD + 4;
-            for (int idx = tid; idx < G * HD; idx += kThreads) {
-                const int g = idx / HD, d = idx % HD;
+            // The first query head of the KV group appends the new key/value row
+            // to the cache (shared buffer, written in place at row ctx).
+            if (ok && a_head % p.G == 0 && wave == 0 && grp == 0) {
+                const size_t o = ((size_t)(a_kvh * p.cap + ctx) * HD + li16 * 8);
+                *reinterpret_cast<uint4*>(static_cast<half_t*>(ly.k_cache) + o) =
+                    make_uint4(kw_new[0], kw_new[1], kw_new[2], kw_new[3]);
+                *reinterpret_cast<uint4*>(static_cast<half_t*>(ly.v_cache) + o) = qkv3[2];
+            }
+            const float qscale = p.scale * 1.4426950408889634f;  // scores in log2 units
+            float m = -INFINITY, lsum = 0.f, o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = 0.f;
+            auto attend = [&](const uint4& kr, const uint4& vr, int key) {
+                if (key > ctx) return;  // a whole 16-lane group shares the key
+                const bool fresh = key == ctx;
+                const uint32_t kw[4] = {fresh ? kw_new[0] : kr.x, fresh ? kw_new[1] : kr.y,
+                                        fresh ? kw_new[2] : kr.z, fresh ? kw_new[3] : kr.w};
+                float d = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, qw[e]),
+                                               __builtin_bit_cast(half2_t, kw[e]), d, false);
+                const float sc = group_sum<16>(d) * qscale;
+                const float mn = fmaxf(m, sc);
+                const float fo = m == -INFINITY ? 0.f : exp2f(m - mn);
+                const float pe = exp2f(sc - mn);
+                lsum = lsum * fo + pe;
+                const half_t* vb = reinterpret_cast<const half_t*>(&vr);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = fmaf(pe, fresh ? vn[e] : (float)vb[e], o[e] * fo);
+                m = mn;
+            };
+            __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+            for (int t = 0; t < kPref; ++t)
+                if (t < a_steps)
+                    attend(wreg[t * 64 + lane], wreg[(kPref + t) * 64 + lane], slot + t * kKeySlots);
+            for (int t0 = kPref; t0 < a_steps; t0 += kKvRing) {
+#pragma unroll
+                for (int r = 0; r < kKvRing; ++r) {
+                    const int t = t0 + r;
+                    if (t < a_steps) attend(ringk[r], ringv[r], slot + t * kKeySlots);
+                    const uint32_t off2 = kv_off(t + kKvRing);
+                    ringk[r] = ld128<kCachePolicyNT>(rk, off2);
+                    ringv[r] = ld128<kCachePolicyNT>(rv, off2);
+                }
+            }
+            // Merge the 4 lane groups of the wave (same dims, other keys), then the
+            // waves through LDS.
+#pragma unroll
+            for (int sh = 16; sh <= 32; sh <<= 1) {
+                const float om = __shfl_xor(m, sh, 64);
+                const float ol = __shfl_xor(lsum, sh, 64);
+                const float mn = fmaxf(m, om);
+                const float fa = m == -INFINITY ? 0.f : exp2f(m - mn);
+                const float fb = om == -INFINITY ? 0.f : exp2f(om - mn);
+                lsum = lsum * fa + ol * fb;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = o[e] * fa + __shfl_xor(o[e], sh, 64) * fb;
+                m = mn;
+            }
+            if (lane == 0) {
+                s_am[wave] = m;
+                s_al[wave] = lsum;
+            }
+            if (grp == 0) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sO[wave * HD + li16 * 8 + e] = o[e];
+            }
+            if (!all_ok(ok, &s_fail)) return;
+            if (tid < HD) {
                 float M = -INFINITY;
 #pragma unroll
-                for (int w = 0; w < kComputeWaves; ++w) M = fmaxf(M, s_am[w][g]);
-                float Lsum = 0.f, acc = 0.f;
+                for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_am[w]);
+                float L = 0.f, acc = 0.f;
 #pragma unroll
-                for (int w = 0; w < kComputeWaves; ++w) {
-                    const float mw = s_am[w][g];
-                    const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
-                    Lsum += s_al[w][g] * f;
-                    acc += sO[(w * kGMax + g) * HD + d] * f;
+                for (int w = 0; w < kWaves; ++w) {
+                    const float fw = s_am[w] == -INFINITY ? 0.f : exp2f(s_am[w] - M);
+                    L += s_al[w] * fw;
+                    acc += sO[w * HD + tid] * fw;
                 }
-                float* dst = p.part + ((size_t)(a_kvh * G + g) * kNSMax + a_split) * stride;
-                __hip_atomic_store(dst + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (d == 0) {
-                    __hip_atomic_store(dst + HD, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(dst + HD + 1, Lsum, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                }
+                put(rsrc(f_att, (uint32_t)HO * 4), a_head * HD + tid, L > 0.f ? acc / L : 0.f, tag);
             }
-            __syncthreads();  // sO aliases sA, which the next phase restages
-        }
-        if (cw >= 0) {
+            wait_lds();
+            gu_fetch();
+        } else {
+            // Phase C: o_proj GEMV over the attention output.
+            if (!stage_poll(f_att, HO, sA1, sSum1, f, &s_fail)) return;
             __builtin_amdgcn_s_waitcnt(0);
-            gu_fetch(ly);
-        }
-        if (!grid_sync(bar, nwg, &s_flag, p.status)) return;
-
-        // Phase C: merge the splits into the attention output (fp16), o_proj GEMV.
-        {
-            const int stride = HD + 4;
-            const uint32_t pbytes = (uint32_t)H * kNSMax * stride * 4;
-            const __amdgpu_buffer_rsrc_t rp = rsrc(p.part, pbytes);
-            for (int t = tid; t < H * HD / 8; t += kThreads) {
-                const int h = (t * 8) / HD, d0 = (t * 8) % HD;
-                float ms[kNSMax], ls[kNSMax];
-                float M = -INFINITY;
-#pragma unroll
-                for (int sidx = 0; sidx < kNSMax; ++sidx) {
-                    const uint32_t rec = ((uint32_t)(h * kNSMax + sidx) * stride) * 4u;
-                    const bool live = sidx < NS;
-                    const uint4 ml = ld128<kSC1>(rp, live ? rec + (uint32_t)HD * 4u : pbytes);
-                    ms[sidx] = live ? __uint_as_float(ml.x) : -INFINITY;
-                    ls[sidx] = live ? __uint_as_float(ml.y) : 0.f;
-                    M = fmaxf(M, ms[sidx]);
-                }
-                float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                float Lsum = 0.f;
-#pragma unroll
-                for (int sidx = 0; sidx < kNSMax; ++sidx) {
-                    if (sidx >= NS) break;
-                    const uint32_t rec = ((uint32_t)(h * kNSMax + sidx) * stride) * 4u;
-                    const uint4 o0 = ld128<kSC1>(rp, rec + (uint32_t)d0 * 4u);
-                    const uint4 o1 = ld128<kSC1>(rp, rec + (uint32_t)(d0 + 4) * 4u);
-                    const float w = ms[sidx] == -INFINITY ? 0.f : exp2f(ms[sidx] - M);
-                    Lsum += w * ls[sidx];
-                    const float ov[8] = {__uint_as_float(o0.x), __uint_as_float(o0.y),
-                                         __uint_as_float(o0.z), __uint_as_float(o0.w),
-                                         __uint_as_float(o1.x), __uint_as_float(o1.y),
-                                         __uint_as_float(o1.z), __uint_as_float(o1.w)};
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[e] = fmaf(ov[e], w, acc[e]);
-                }
-                const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
-                half_t o8[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o8[e] = (half_t)(acc[e] * inv);
-                sA[t] = permute_act8(*reinterpret_cast<const uint4*>(o8));
-            }
+            const float v = group_sum<16>(row_dot<16, CPLD>(wreg + kLo * 64, so, sA1, sSum1, CO, li16));
+            if (li16 == 0 && wave < go) s_out[wave * 4 + grp] = v;
             __syncthreads();
+            if (tid < 4 * go && 4 * wg * go + tid < D)
+                put(rsrc(f_y, (uint32_t)D * 4), 4 * wg * go + tid, s_out[tid], tag);
+            wait_lds();
+            gu_fetch();
         }
-        if (cw >= 0) {
-            const int ng = (D + 3) / 4;
-            __builtin_amdgcn_s_waitcnt(0);
-            float v = group_sum<16>(row_dot<16, CPLD>(wreg + kSlotsLo * 64, so, sA, CO, li16));
-            if (gw < ng && li16 == 0 && 4 * gw + grp < D)
-                st_half_sc1(p.y, (uint32_t)D * 2, 4 * gw + grp, v);
-            __builtin_amdgcn_s_waitcnt(0);
-            down_fetch(ly);
-        }
-        if (!grid_sync(bar, nwg, &s_flag, p.status)) return;
 
         // Phase D: residual + post-attention norm, gate/up GEMV with SwiGLU.
-        norm_stage<kSC1>(p.y, true, static_cast<const half_t*>(ly.ln2_gamma), ly.ln2_epsilon,
-                         D, sR, sA, sRed);
-        if (cw >= 0) {
-            const int N = 2 * I, ng = (N + 3) / 4;
-            auto gu_out = [&](float v, int g) {
+        if (!norm_poll(f_y, nullptr, true, static_cast<const half_t*>(ly.ln2_gamma), ly.ln2_epsilon,
+                       D, sR, sA0, sSum0, sRed, f, &s_fail))
+            return;
+        {
+            const __amdgpu_buffer_rsrc_t ra = rsrc(f_act, (uint32_t)I * 4);
+            // Local group lg of this workgroup: rows 4g .. 4g+3 (gate, up, gate, up),
+            // g = wg * ggu + lg, giving pairs 2g and 2g + 1 (local 2lg, 2lg + 1).
+            auto gu_out = [&](float v, int lg) {
                 v = group_sum<16>(v);
                 const float other = __shfl_xor(v, 16, 64);  // gate (even group) <-> up (odd)
-                if (g < ng && li16 == 0 && (grp & 1) == 0) {
-                    const int pair = 2 * g + (grp >> 1);
-                    if (pair < I) {
-                        const float gv = r16(v), up = r16(other);
-                        const float sig = r16(1.0f / (1.0f + __expf(-gv)));
-                        st_half_sc1(p.act, (uint32_t)I * 2, pair, r16(r16(gv * sig) * up));
-                    }
+                const int g = wg * ggu + lg;
+                if (lg < ggu && g < ng_gu && li16 == 0 && (grp & 1) == 0) {
+                    const float gv = r16(v), up = r16(other);
+                    const float sig = r16(1.0f / (1.0f + __expf(-gv)));
+                    s_out[2 * lg + (grp >> 1)] = r16(r16(gv * sig) * up);
                 }
             };
             __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
             for (int k = 0; k < kGu; ++k)
-                gu_out(row_dot<16, CPLD>(wreg + k * CPLD * 64, sg[k], sA, CD, li16), gw + k * TW);
-            const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, N, CD);
-            for (int g = gw + kGu * TW; g < ng; g += TW) {
+                gu_out(row_dot<16, CPLD>(wreg + k * CPLD * 64, sg[k], sA0, sSum0, CD, li16), wave + k * kWaves);
+            const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
+            for (int lg = wave + kGu * kWaves; lg < ggu; lg += kWaves) {
+                const int g = wg * ggu + lg;
                 Rows<CPLD> r;
-                load_rows<16, CPLD>(r, wr, 4 * g + grp, li16);
-                gu_out(rows_dot<16, CPLD>(r, sA, CD, li16), g);
+                load_rows<16, CPLD>(r, wr, g < ng_gu ? 4 * g + grp : 2 * I, li16);
+                gu_out(rows_dot<16, CPLD>(r, sA0, sSum0, CD, li16), lg);
             }
-            __builtin_amdgcn_s_waitcnt(0);
-            if (l + 1 < p.L) qkv_fetch(p.layers[l + 1]);
+            __syncthreads();
+            if (tid < 2 * ggu && 2 * wg * ggu + tid < I)
+                put(ra, 2 * wg * ggu + tid, s_out[tid], tag);
+            wait_lds();
+            down_fetch();
         }
-        if (!grid_sync(bar, nwg, &s_flag, p.status)) return;
 
         // Phase E: down GEMV (K = I).
-        stage_vec(p.act, I, sA);
-        if (cw >= 0) {
+        if (!stage_poll(f_act, I, sA1, sSum1, f, &s_fail)) return;
+        {
             __builtin_amdgcn_s_waitcnt(0);
-            const float v = wave_sum(row_dot<64, kIChunksPerLane>(wreg + kSlotsLo * 64, sd, sA, CI, lane));
-            if (gw < D && lane == 0) st_half_sc1(p.dout, (uint32_t)D * 2, gw, v);
+            const float v =
+                wave_sum(row_dot<64, kIChunksPerLane>(wreg + kLo * 64, sd, sA1, sSum1, CI, lane));
+            if (lane == 0 && wave < gd) s_out[wave] = v;
+            __syncthreads();
+            if (tid < gd && wg * gd + tid < D)
+                put(rsrc(f_dout, (uint32_t)D * 4), wg * gd + tid, s_out[tid], tag);
+            wait_lds();
+            if (l + 1 < p.L) qkv_fetch(s_layers[l + 1]);
         }
-        if (!grid_sync(bar, nwg, &s_flag, p.status)) return;
+        prev_dout = f_dout;
     }
 
-    // Phase F: final norm, lm_head GEMV (logits), per-workgroup argmax.
-    norm_stage<kSC1>(p.dout, true, p.final_gamma, p.final_eps, D, sR, sA, sRed);
+    // Phase F: final norm, lm_head GEMV (logits), argmax. The first lm_head rows are
+    // requested before the wait for the last down output.
+    constexpr int kRing = 4;
+    const int lm_ng = (p.V + 3) / 4;
+    const WeightRef lw = weight_ref(p.lm_w, p.lm_s, p.V, CD);
+    Rows<CPLD> ring[kRing];
+#pragma unroll
+    for (int r = 0; r < kRing; ++r) {
+        const int g = gw + r * TW;
+        load_rows<16, CPLD>(ring[r], lw, g < lm_ng ? 4 * g + grp : p.V, li16);
+    }
+    if (!norm_poll(prev_dout, nullptr, true, p.final_gamma, p.final_eps, D, sR, sA0, sSum0, sRed,
+                   f, &s_fail))
+        return;
     float best = -INFINITY;
     int bi = -1;
-    if (cw >= 0) {
-        constexpr int kRing = 4;
-        const int lm_ng = (p.V + 3) / 4;
-        const WeightRef wr = weight_ref(p.lm_w, p.lm_s, p.V, CD);
-        Rows<CPLD> ring[kRing];
+    for (int k = 0;; k += kRing) {
+        bool done = false;
 #pragma unroll
         for (int r = 0; r < kRing; ++r) {
-            const int g = gw + r * TW;
-            load_rows<16, CPLD>(ring[r], wr, g < lm_ng ? 4 * g + grp : p.V, li16);
-        }
-        for (int k = 0;; k += kRing) {
-            bool done = false;
-#pragma unroll
-            for (int r = 0; r < kRing; ++r) {
-                const int g = gw + (k + r) * TW;
-                if (g >= lm_ng) {
-                    done = true;
-                    break;
-                }
-                const float v = group_sum<16>(rows_dot<16, CPLD>(ring[r], sA, CD, li16));
-                const int gn = g + kRing * TW;
-                load_rows<16, CPLD>(ring[r], wr, gn < lm_ng ? 4 * gn + grp : p.V, li16);
-                const int n = 4 * g + grp;
-                if (n < p.V) {
-                    const half_t hv = (half_t)v;
-                    if (li16 == 0) p.logits[n] = hv;
-                    const float fv = (float)hv;
-                    if (fv > best || (bi < 0 && fv == best)) {
-                        best = fv;
-                        bi = n;
-                    }
+            const int g = gw + (k + r) * TW;
+            if (g >= lm_ng) {
+                done = true;
+                break;
+            }
+            const float v = group_sum<16>(rows_dot<16, CPLD>(ring[r], sA0, sSum0, CD, li16));
+            const int gn = g + kRing * TW;
+            load_rows<16, CPLD>(ring[r], lw, gn < lm_ng ? 4 * gn + grp : p.V, li16);
+            const int n = 4 * g + grp;
+            if (n < p.V) {
+                const half_t hv = (half_t)v;
+                if (li16 == 0) p.logits[n] = hv;
+                const float fv = (float)hv;
+                if (fv > best || (bi < 0 && fv == best)) {
+                    best = fv;
+                    bi = n;
                 }
             }
-            if (done) break;
         }
+        if (done) break;
     }
-    // Reduce (value, index) over the workgroup: lowest index wins ties, NaN never wins.
-    {
-#pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) {
-            const float ov = __shfl_xor(best, sh, 64);
-            const int oi = __shfl_xor(bi, sh, 64);
-            if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
-                best = ov;
-                bi = oi;
-            }
-        }
-        if (lane == 0) {
-            s_arg_v[wave] = best;
-            s_arg_i[wave] = bi;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            for (int w = 0; w < kThreads / 64; ++w) {
-                const float ov = s_arg_v[w];
-                const int oi = s_arg_i[w];
-                if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
-                    best = ov;
-                    bi = oi;
-                }
-            }
-            float4 rec = make_float4(best, __int_as_float(bi), 0.f, 0.f);
-            st128<kSC1>(rsrc(p.argp, (uint32_t)nwg * 16), (uint32_t)wg * 16,
-                        *reinterpret_cast<const uint4*>(&rec));
-        }
+    // Reduce (value, index) over the workgroup, publish one tagged record.
+    arg_wave(best, bi);
+    if (lane == 0) {
+        s_arg_v[wave] = best;
+        s_arg_i[wave] = bi;
     }
-    if (!grid_sync(bar, nwg, &s_flag, p.status)) return;
-    if (wg == 0) {
-        best = -INFINITY;
-        bi = -1;
-        const __amdgpu_buffer_rsrc_t ra = rsrc(p.argp, (uint32_t)nwg * 16);
-        for (int w = tid; w < nwg; w += kThreads) {
-            const uint4 raw = ld128<kSC1>(ra, (uint32_t)w * 16);
-            const float ov = __uint_as_float(raw.x);
-            const int oi = (int)raw.y;
-            if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
-                best = ov;
-                bi = oi;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 0; w < kWaves; ++w) arg_take(best, bi, s_arg_v[w], s_arg_i[w]);
+        const uint64_t rec = (uint64_t)(uint32_t)bi | ((uint64_t)f2h(best) << 32) |
+                             ((uint64_t)tag << 48);
+        __hip_atomic_store(p.argp + wg, rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (wg != 0) return;
+    best = -INFINITY;
+    bi = -1;
+    bool ok = true;
+    for (int w0 = 0; w0 < nwg; w0 += kThreads) {
+        const int w = w0 + tid;
+        if (w >= nwg) continue;
+        uint64_t rec = 0;
+        for (unsigned it = 0;; ++it) {
+            rec = __hip_atomic_load(p.argp + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((uint32_t)(rec >> 48) == tag) break;
+            if (!keep_waiting(f, it)) {
+                ok = false;
+                break;
             }
         }
-#pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) {
-            const float ov = __shfl_xor(best, sh, 64);
-            const int oi = __shfl_xor(bi, sh, 64);
-            if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
-                best = ov;
-                bi = oi;
-            }
-        }
-        __syncthreads();
-        if (lane == 0) {
-            s_arg_v[wave] = best;
-            s_arg_i[wave] = bi;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            for (int w = 0; w < kThreads / 64; ++w) {
-                const float ov = s_arg_v[w];
-                const int oi = s_arg_i[w];
-                if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
-                    best = ov;
-                    bi = oi;
-                }
-            }
-            *p.next_id = bi < 0 ? 0 : bi;
-            store_status(p.status, bad_id ? 2 : 0);
-        }
+        if (!ok) break;
+        arg_take(best, bi, h2f((uint32_t)(rec >> 32) & 0xFFFFu), (int)(uint32_t)rec);
+    }
+    arg_wave(best, bi);
+    if (lane == 0) {
+        s_arg_v[wave] = best;
+        s_arg_i[wave] = bi;
+    }
+    if (!all_ok(ok, &s_fail)) return;
+    if (tid == 0) {
+        for (int w = 0; w < kWaves; ++w) arg_take(best, bi, s_arg_v[w], s_arg_i[w]);
+        *p.next_id = bi < 0 ? 0 : bi;
+        store_status(p.status, bad_id ? 2 : 0);
     }
 }
 
@@ -879,27 +917,24 @@ using namespace ortmi;
 namespace {
 
 struct StepShape {
-    size_t ctl, qkv, part, y, act, dout, argp, total;
+    size_t ctl, flow, argp, total;
+    uint32_t flow_stride;
 };
 
 StepShape step_layout(const OrtmiDecoderDims* d, int nwg) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     StepShape s{};
+    const size_t words = (size_t)(d->num_heads + 2 * d->kv_num_heads) * d->head_size +
+                         (size_t)d->num_heads * d->head_size + 2 * (size_t)d->hidden +
+                         (size_t)d->intermediate;
+    s.flow_stride = (uint32_t)((words + 63) & ~(size_t)63);
     size_t off = 0;
     s.ctl = off;
     off += dprog::kCtlBytes;
-    s.qkv = off;
-    off += al((size_t)(d->num_heads + 2 * d->kv_num_heads) * d->head_size * 2);
-    s.part = off;
-    off += al((size_t)d->num_heads * dprog::kNSMax * (d->head_size + 4) * 4);
-    s.y = off;
-    off += al((size_t)d->hidden * 2);
-    s.act = off;
-    off += al((size_t)d->intermediate * 2);
-    s.dout = off;
-    off += al((size_t)d->hidden * 2);
+    s.flow = off;
+    off += al((size_t)std::max(d->layers, 0) * s.flow_stride * 4);
     s.argp = off;
-    off += al((size_t)nwg * 16);
+    off += al((size_t)nwg * 8);
     s.total = off;
     return s;
 }
@@ -931,7 +966,7 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     const OrtmiDecoderDims& d = *dims;
     ORTMI_REQUIRE(d.dtype == ORTMI_F16, "decoder step: fp16 only");
     ORTMI_REQUIRE(d.block_size == 32, "decoder step: block size 32 only");
-    ORTMI_REQUIRE(d.layers >= 1, "decoder step: no layers");
+    ORTMI_REQUIRE(d.layers >= 1 && d.layers <= dprog::kMaxLayers, "decoder step: 1 to 64 layers");
     ORTMI_REQUIRE(d.head_size == 128, "decoder step: head size 128 only");
     ORTMI_REQUIRE(d.num_heads > 0 && d.kv_num_heads > 0 && d.num_heads % d.kv_num_heads == 0 &&
                       d.num_heads / d.kv_num_heads <= dprog::kGMax,
@@ -947,12 +982,14 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
                   "decoder step: rotary half must be a multiple of 8, at most head_size / 2");
     ORTMI_REQUIRE(d.rotary_interleaved == 0, "decoder step: interleaved rotary is not supported");
     const int nwg = program_grid();
-    ORTMI_REQUIRE(nwg >= kXcds, "decoder step: too few compute units");
+    ORTMI_REQUIRE(nwg >= 4 * d.num_heads && nwg >= kXcds,
+                  "decoder step: needs at least 4 compute units per query head");
     const int nq = (d.num_heads + 2 * d.kv_num_heads) * d.head_size;
-    ORTMI_REQUIRE((nq + 3) / 4 <= dprog::kComputeWaves * nwg && (d.hidden + 3) / 4 <= dprog::kComputeWaves * nwg &&
-                      d.hidden <= dprog::kComputeWaves * nwg,
-                  "decoder step: projection rows exceed one group per wave");
-    ORTMI_REQUIRE(d.kv_num_heads * dprog::kNSMax <= nwg, "decoder step: too many KV heads");
+    const int nc = nwg - d.num_heads;
+    const int gq = ((nq + 3) / 4 + nwg - 1) / nwg, go = ((d.hidden + 3) / 4 + nc - 1) / nc;
+    const int ggu = ((2 * d.intermediate + 3) / 4 + nwg - 1) / nwg, gd = (d.hidden + nwg - 1) / nwg;
+    ORTMI_REQUIRE(gq <= dprog::kWaves && go <= dprog::kWaves && gd <= dprog::kWaves && 2 * ggu <= 64,
+                  "decoder step: projection rows exceed the per-workgroup share");
     ORTMI_REQUIRE((int64_t)d.kv_num_heads * d.kv_capacity * d.head_size * 2 < (int64_t)INT32_MAX &&
                       (int64_t)d.vocab * d.hidden / 2 < (int64_t)INT32_MAX,
                   "decoder step: a cache or the lm_head exceeds 2 GiB");
@@ -961,8 +998,11 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
         return fail(ORTMI_E_WORKSPACE, "decoder step: workspace too small");
     ORTMI_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0 &&
                       (reinterpret_cast<uintptr_t>(embed) & 15) == 0 &&
-                      (reinterpret_cast<uintptr_t>(final_gamma) & 15) == 0,
-                  "decoder step: workspace, embedding and gamma must be 16-byte aligned");
+                      (reinterpret_cast<uintptr_t>(final_gamma) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(cos_cache) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(sin_cache) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(layers) & 3) == 0,
+                  "decoder step: workspace, embedding, gamma and cos/sin must be 16-byte aligned");
 
     char* ws = static_cast<char*>(workspace);
     dprog::Params p{};
@@ -971,12 +1011,17 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     p.D = d.hidden;
     p.H = d.num_heads;
     p.KV = d.kv_num_heads;
+    p.G = d.num_heads / d.kv_num_heads;
     p.I = d.intermediate;
     p.V = d.vocab;
     p.cap = d.kv_capacity;
     p.max_pos = d.max_position;
     p.half = d.rotary_half;
     p.nwg = nwg;
+    p.gq = gq;
+    p.go = go;
+    p.ggu = ggu;
+    p.gd = gd;
     p.scale = d.scale != 0.f ? d.scale : 1.0f / sqrtf((float)d.head_size);
     p.final_eps = final_epsilon;
     p.embed = static_cast<const half_t*>(embed);
@@ -992,32 +1037,38 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     p.next_id = next_id;
     p.status = status;
     p.ctl = reinterpret_cast<uint32_t*>(ws + s.ctl);
-    p.qkv = reinterpret_cast<half_t*>(ws + s.qkv);
-    p.part = reinterpret_cast<float*>(ws + s.part);
-    p.y = reinterpret_cast<half_t*>(ws + s.y);
-    p.act = reinterpret_cast<half_t*>(ws + s.act);
-    p.dout = reinterpret_cast<half_t*>(ws + s.dout);
-    p.argp = reinterpret_cast<float4*>(ws + s.argp);
+    p.flow = reinterpret_cast<uint32_t*>(ws + s.flow);
+    p.flow_stride = s.flow_stride;
+    p.argp = reinterpret_cast<uint64_t*>(ws + s.argp);
 
     const int cpld = d.hidden <= 1536 && d.num_heads * d.head_size <= 1536 ? 3 : 4;
-    const int G = d.num_heads / d.kv_num_heads;
-    const void* fn = nullptr;
-#define ORTMI_DP(C, GG)                                                                 \
-    if (cpld == C && G == GG) fn = (const void*)dprog::decode_program_kernel<128, C, GG>;
-    ORTMI_DP(3, 1) ORTMI_DP(3, 2) ORTMI_DP(3, 4) ORTMI_DP(3, 6) ORTMI_DP(3, 8)
-    ORTMI_DP(4, 1) ORTMI_DP(4, 2) ORTMI_DP(4, 4) ORTMI_DP(4, 6) ORTMI_DP(4, 8)
-#undef ORTMI_DP
-    ORTMI_REQUIRE(fn, "decoder step: query heads per KV head must be 1, 2, 4, 6 or 8");
-    const int a_units = std::max(d.hidden, d.intermediate) / 8;
-    const int o_units = dprog::kComputeWaves * dprog::kGMax * d.head_size / 4;
-    const size_t lds = ((size_t)dprog::kComputeWaves * dprog::region_slots(cpld) * 64 +
-                        (size_t)std::max(a_units, o_units) + d.hidden / 8) * 16;
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, dprog::kThreads, lds) != hipSuccess ||
-        per_cu < 1) {
-        (void)hipGetLastError();
-        return fail(ORTMI_E_INVALID, "decoder step: the program does not fit one workgroup per CU");
+    const void* fn = cpld == 3 ? (const void*)dprog::decode_program_kernel<128, 3>
+                               : (const void*)dprog::decode_program_kernel<128, 4>;
+    const int ho = d.num_heads * d.head_size;
+    const size_t lds = ((size_t)dprog::kWaves * dprog::region_slots(cpld) * 64 + d.hidden / 8 +
+                        std::max(ho, d.intermediate) / 8 + d.hidden / 8) * 16 +
+                       ((size_t)dprog::kWaves * d.head_size + d.hidden / 32 +
+                        std::max(ho, d.intermediate) / 32) * 4;
+    // The fit check is made once per (device, kernel, LDS size).
+    static std::mutex fit_mu;
+    static std::map<std::tuple<int, const void*, size_t>, bool> fits;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    bool fit;
+    {
+        std::lock_guard<std::mutex> lock(fit_mu);
+        auto it = fits.find({dev, fn, lds});
+        if (it == fits.end()) {
+            int per_cu = 0;
+            fit = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, dprog::kThreads, lds) ==
+                      hipSuccess && per_cu >= 1;
+            (void)hipGetLastError();
+            fits[{dev, fn, lds}] = fit;
+        } else {
+            fit = it->second;
+        }
     }
+    if (!fit) return fail(ORTMI_E_INVALID, "decoder step: the program does not fit one workgroup per CU");
     void* args[] = {&p};
     const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(dprog::kThreads), args,
                                                     (unsigned)lds, as_stream(stream));

@@ -181,6 +181,14 @@ class Plan {
     bool guards_hold(const std::vector<Guard>& guards) const;
     bool replay(const OrtApi* api, OrtKernelContext* ctx);
     bool capture(const OrtApi* api, OrtKernelContext* ctx, const std::vector<InputSig>& sig);
+    // One-launch decode step (ortmi_decoder_decode_step) for a fused node that is a
+    // whole int4 decoder, at one-token steps on a device-resident shared KV cache.
+    struct DecodeProgram;
+    void match_decode_program();
+    bool run_decode_program(const OrtApi* api, OrtKernelContext* ctx);
+    std::unique_ptr<DecodeProgram> dprog_;
+    bool dprog_required_ = false;  // ORTMI_EP_PROGRAM=require: fail when it does not apply
+    std::string dprog_reject_ = "no decoder structure", dprog_ids_;  // why not; the ids input
 
     GraphIR sub_;
     std::vector<std::string> inputs_, outputs_;

@@ -1,5 +1,6 @@
 // Per-fused-node plan of the MI355X EP: constants in HBM, one HIP stream, shape
 // inference and kernel launches at Compute.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -41,6 +42,36 @@ static bool is_device_ptr(const void* p) {
     return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
 
+// A fused node that is a whole int4 decoder after the decode rewrites:
+//   Gather(embed, ids) -> L x [MatMulNBits q/k/v (norm prologue), GroupQueryAttention
+//   (packed, in-op RoPE), MatMulNBits o_proj, MatMulNBitsSwiGLU gate/up (norm
+//   prologue), MatMulNBits down] -> MatMulNBits lm_head (norm prologue) -> logits.
+// Its one-token steps on a device-resident KV cache shared by past and present run
+// as one launch of ortmi_decoder_decode_step, the counterpart of the reference's
+// one compiled-closure evaluation per token (rust/src/compiled.rs:503-822).
+struct Plan::DecodeProgram {
+    struct Layer {
+        std::string qkv_B, qkv_S, g1, o_B, o_S, g2, gu_B, gu_S, d_B, d_S;
+        float e1 = 1e-6f, e2 = 1e-6f;
+        std::string past_k, past_v, present_k, present_v;
+    };
+    std::string ids, total, logits, embed, cos, sin, gf, lm_B, lm_S;
+    float ef = 1e-6f;
+    std::vector<Layer> layers;
+    OrtmiDecoderDims dims{};
+    std::vector<OrtmiDecoderLayer> proto;       // constant pointers resolved at Compile
+    std::vector<OrtmiDecoderLayer> host_table;  // last table sent to the device
+    const void *embed_p = nullptr, *cos_p = nullptr, *sin_p = nullptr, *gf_p = nullptr,
+               *lm_B_p = nullptr, *lm_S_p = nullptr;
+    int64_t embed_rows = 0;
+    std::unique_ptr<DeviceBuffer> table, ws, next_id;
+    size_t ws_bytes = 0;
+    int32_t* status = nullptr;  // host-pinned: the kernel writes it, the host reads it after the run
+    ~DecodeProgram() {
+        if (status) (void)hipHostFree(status);
+    }
+};
+
 Plan::Plan(GraphIR sub, std::vector<std::string> inputs, std::vector<std::string> outputs,
            int device)
     : sub_(std::move(sub)), inputs_(std::move(inputs)), outputs_(std::move(outputs)),
@@ -79,6 +110,276 @@ Plan::Plan(GraphIR sub, std::vector<std::string> inputs, std::vector<std::string
         constants_[kv.first] = std::move(buf);
         std::vector<uint8_t>().swap(v.data);
     }
+    match_decode_program();
+}
+
+void Plan::match_decode_program() {
+    const char* env = std::getenv("ORTMI_EP_PROGRAM");
+    dprog_required_ = env && std::strcmp(env, "require") == 0;
+    if (env && std::strcmp(env, "0") == 0) {
+        dprog_reject_ = "turned off";
+        return;
+    }
+    const auto& nodes = sub_.nodes;
+    std::map<std::string, std::vector<size_t>> readers;  // value -> nodes reading it as input 0
+    for (size_t i = 0; i < nodes.size(); ++i)
+        if (!nodes[i].inputs.empty() && !nodes[i].inputs[0].empty()) readers[nodes[i].inputs[0]].push_back(i);
+    auto in_list = [](const std::vector<std::string>& l, const std::string& v) {
+        return !v.empty() && std::find(l.begin(), l.end(), v) != l.end();
+    };
+    auto cst = [&](const std::string& v) -> const ValueDesc* {
+        auto it = sub_.values.find(v);
+        return it != sub_.values.end() && it->second.is_initializer && constants_.count(v) ? &it->second
+                                                                                          : nullptr;
+    };
+    auto reader = [&](const std::string& v, const char* op, bool norm) -> const NodeDesc* {
+        auto it = readers.find(v);
+        if (it == readers.end()) return nullptr;
+        const NodeDesc* r = nullptr;
+        for (size_t i : it->second) {
+            const NodeDesc& n = nodes[i];
+            if (n.op != op || (n.attr_int("__norm", 0) != 0) != norm) continue;
+            if (r) return nullptr;
+            r = &n;
+        }
+        return r;
+    };
+    // A 4-bit block-32 MatMulNBits with fp16 scales, no zero points, g_idx or bias.
+    auto mnb = [&](const NodeDesc* n, int64_t K, int64_t N) {
+        if (!n || n->attr_int("bits", 4) != 4 || n->attr_int("block_size", 32) != 32) return false;
+        if (n->attr_int("K", 0) != K || (N >= 0 && n->attr_int("N", 0) != N)) return false;
+        for (size_t i = 3; i < 6; ++i)
+            if (n->has_input(i)) return false;
+        const ValueDesc* B = cst(n->inputs[1]);
+        const ValueDesc* S = cst(n->inputs[2]);
+        return B && S && B->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_UINT8 &&
+               S->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16;
+    };
+    const NodeDesc* gat = nullptr;
+    for (const auto& n : nodes)
+        if (n.op == "Gather" && n.domain.empty()) {
+            if (gat) { dprog_reject_ = "more than one Gather"; return; }
+            gat = &n;
+        }
+    if (!gat || gat->inputs.size() < 2 || gat->attr_int("axis", 0) != 0 || gat->outputs.empty()) { dprog_reject_ = "no embedding Gather"; return; }
+    const ValueDesc* emb = cst(gat->inputs[0]);
+    if (!emb || emb->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16 || emb->dims.size() != 2 ||
+        !in_list(inputs_, gat->inputs[1]))
+        { dprog_reject_ = "embedding is not an fp16 [V, D] constant gathered by a node input"; return; }
+    const int64_t D = emb->dims[1];
+    auto dp = std::make_unique<DecodeProgram>();
+    dp->ids = gat->inputs[1];
+    dp->embed = gat->inputs[0];
+    dprog_ids_ = dp->ids;
+    std::string x = gat->outputs[0], res = x;
+    int64_t H = 0, KV = 0, hd = 0, I = 0, max_pos = 0, half = 0;
+    float scale = 0.f;
+    for (int l = 0;; ++l) {
+        const NodeDesc* q = reader(x, "MatMulNBits", true);
+        if (!q || q->inputs.size() < 8 || q->outputs.empty()) { dprog_reject_ = "no norm prologue MatMulNBits reads the layer input"; return; }
+        if (l == 0 ? q->has_input(6) : q->inputs[6] != res) { dprog_reject_ = "the norm's skip input is not the residual stream"; return; }
+        const NodeDesc* g = reader(q->outputs[0], "GroupQueryAttention", false);
+        if (!g) {  // the lm_head: its output is the fused node's logits
+            if (l == 0 || !in_list(outputs_, q->outputs[0]) || !mnb(q, D, -1)) { dprog_reject_ = "lm_head form"; return; }
+            dp->logits = q->outputs[0];
+            dp->lm_B = q->inputs[1];
+            dp->lm_S = q->inputs[2];
+            dp->gf = q->inputs[7];
+            dp->ef = q->attr_float("__norm_eps", 1e-6f);
+            dp->dims.vocab = (int32_t)q->attr_int("N", 0);
+            break;
+        }
+        // After layer 0 the norm before the attention adds its skip input and
+        // leaves the sum (the next residual) as its output 1.
+        if (l > 0) {
+            if (q->outputs.size() < 2 || q->outputs[1].empty()) {
+                dprog_reject_ = "the norm before the attention has no residual output";
+                return;
+            }
+            res = q->outputs[1];
+        }
+        if (g->inputs.size() < 9 || g->has_input(1) || g->has_input(2) || g->outputs.size() < 3) { dprog_reject_ = "GroupQueryAttention is not packed with 9 inputs"; return; }
+        if (g->attr_int("do_rotary", 0) != 1 || g->attr_int("rotary_interleaved", 0) != 0) { dprog_reject_ = "GroupQueryAttention rotary form"; return; }
+        if (!in_list(inputs_, g->inputs[3]) || !in_list(inputs_, g->inputs[4]) ||
+            !in_list(outputs_, g->outputs[1]) || !in_list(outputs_, g->outputs[2]))
+            { dprog_reject_ = "KV caches are not node inputs and outputs"; return; }
+        const ValueDesc* cs = cst(g->inputs[7]);
+        const ValueDesc* sn = cst(g->inputs[8]);
+        if (!cs || !sn || cs->dims.size() != 2 || sn->dims != cs->dims ||
+            cs->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16)
+            { dprog_reject_ = "cos/sin caches"; return; }
+        if (l == 0) {
+            H = g->attr_int("num_heads", 0);
+            KV = g->attr_int("kv_num_heads", 0);
+            scale = g->attr_float("scale", 0.f);
+            dp->total = g->inputs[6];
+            dp->cos = g->inputs[7];
+            dp->sin = g->inputs[8];
+            max_pos = cs->dims[0];
+            half = cs->dims[1];
+            if (H <= 0 || KV <= 0 || q->attr_int("N", 0) % (H + 2 * KV)) { dprog_reject_ = "head counts"; return; }
+            hd = q->attr_int("N", 0) / (H + 2 * KV);
+        } else if (g->attr_int("num_heads", 0) != H || g->attr_int("kv_num_heads", 0) != KV ||
+                   g->attr_float("scale", 0.f) != scale || g->inputs[6] != dp->total ||
+                   g->inputs[7] != dp->cos || g->inputs[8] != dp->sin) {
+            dprog_reject_ = "layers differ in attention attributes";
+            return;
+        }
+        if (!mnb(q, D, (H + 2 * KV) * hd)) { dprog_reject_ = "QKV projection form"; return; }
+        const NodeDesc* o = reader(g->outputs[0], "MatMulNBits", false);
+        if (!mnb(o, H * hd, D) || o->outputs.empty()) { dprog_reject_ = "o_proj form"; return; }
+        const NodeDesc* gu = reader(o->outputs[0], "MatMulNBitsSwiGLU", true);
+        if (!gu || gu->inputs.size() < 8 || gu->inputs[6] != res || gu->outputs.size() < 2 ||
+            gu->outputs[1].empty() || !mnb(gu, D, -1))
+            { dprog_reject_ = "gate/up form"; return; }
+        const int64_t Il = gu->attr_int("N", 0) / 2;
+        if (l == 0) I = Il;
+        if (Il != I) { dprog_reject_ = "intermediate sizes differ"; return; }
+        const NodeDesc* dn = reader(gu->outputs[0], "MatMulNBits", false);
+        if (!mnb(dn, I, D) || dn->outputs.empty()) { dprog_reject_ = "down form"; return; }
+        DecodeProgram::Layer L;
+        L.qkv_B = q->inputs[1];
+        L.qkv_S = q->inputs[2];
+        L.g1 = q->inputs[7];
+        L.e1 = q->attr_float("__norm_eps", 1e-6f);
+        L.o_B = o->inputs[1];
+        L.o_S = o->inputs[2];
+        L.gu_B = gu->inputs[1];
+        L.gu_S = gu->inputs[2];
+        L.g2 = gu->inputs[7];
+        L.e2 = gu->attr_float("__norm_eps", 1e-6f);
+        L.d_B = dn->inputs[1];
+        L.d_S = dn->inputs[2];
+        L.past_k = g->inputs[3];
+        L.past_v = g->inputs[4];
+        L.present_k = g->outputs[1];
+        L.present_v = g->outputs[2];
+        for (const std::string* gm : {&L.g1, &L.g2}) {
+            const ValueDesc* gv = cst(*gm);
+            if (!gv || gv->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16) { dprog_reject_ = "gamma dtype"; return; }
+        }
+        dp->layers.push_back(L);
+        x = dn->outputs[0];
+        res = gu->outputs[1];
+    }
+    // Every node of the fused node is part of the program, and it has no other outputs.
+    if (nodes.size() != 2 + 5 * dp->layers.size()) { dprog_reject_ = "extra nodes in the fused node"; return; }
+    if (outputs_.size() != 1 + 2 * dp->layers.size()) { dprog_reject_ = "extra outputs of the fused node"; return; }
+    const ValueDesc* gf = cst(dp->gf);
+    if (!gf || gf->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16) { dprog_reject_ = "final gamma dtype"; return; }
+    OrtmiDecoderDims& d = dp->dims;
+    d.layers = (int32_t)dp->layers.size();
+    d.hidden = (int32_t)D;
+    d.num_heads = (int32_t)H;
+    d.kv_num_heads = (int32_t)KV;
+    d.head_size = (int32_t)hd;
+    d.intermediate = (int32_t)I;
+    d.max_position = (int32_t)max_pos;
+    d.rotary_half = (int32_t)half;
+    d.rotary_interleaved = 0;
+    d.block_size = 32;
+    d.dtype = ORTMI_F16;
+    d.scale = scale;
+    auto dev = [&](const std::string& n) { return constants_.at(n)->ptr; };
+    for (const DecodeProgram::Layer& L : dp->layers) {
+        OrtmiDecoderLayer t{};
+        t.qkv_weight = static_cast<const uint8_t*>(dev(L.qkv_B));
+        t.qkv_scales = dev(L.qkv_S);
+        t.ln1_gamma = dev(L.g1);
+        t.ln1_epsilon = L.e1;
+        t.o_weight = static_cast<const uint8_t*>(dev(L.o_B));
+        t.o_scales = dev(L.o_S);
+        t.ln2_gamma = dev(L.g2);
+        t.ln2_epsilon = L.e2;
+        t.gate_up_weight = static_cast<const uint8_t*>(dev(L.gu_B));
+        t.gate_up_scales = dev(L.gu_S);
+        t.down_weight = static_cast<const uint8_t*>(dev(L.d_B));
+        t.down_scales = dev(L.d_S);
+        dp->proto.push_back(t);
+    }
+    dp->embed_p = dev(dp->embed);
+    dp->embed_rows = emb->dims[0];
+    dp->cos_p = dev(dp->cos);
+    dp->sin_p = dev(dp->sin);
+    dp->gf_p = dev(dp->gf);
+    dp->lm_B_p = dev(dp->lm_B);
+    dp->lm_S_p = dev(dp->lm_S);
+    check_hip(hipHostMalloc((void**)&dp->status, sizeof(int32_t), hipHostMallocDefault),
+              "hipHostMalloc");
+    dp->next_id = device_alloc(sizeof(int64_t));
+    dprog_ = std::move(dp);
+    dprog_reject_.clear();
+}
+
+bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
+    DecodeProgram& dp = *dprog_;
+    auto skip = [&](const std::string& why) {
+        if (dprog_required_) fail("decode program does not apply: " + why);
+        return false;
+    };
+    auto ids = env_.find(dp.ids);
+    if (ids == env_.end() || ids->second.numel() != 1) return false;  // a prompt step
+    if (ids->second.dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64) return skip("input ids not int64");
+    if (!env_.count(dp.total)) return skip("no total_sequence_length");
+    OrtmiDecoderDims d = dp.dims;
+    std::vector<OrtmiDecoderLayer> table = dp.proto;
+    int64_t cap = -1;
+    for (size_t l = 0; l < dp.layers.size(); ++l) {
+        const DecodeProgram::Layer& L = dp.layers[l];
+        const Tensor& pk = env_.at(L.past_k);
+        const Tensor& pv = env_.at(L.past_v);
+        if (pk.host || pv.host || pk.dims.size() != 4 || pk.dims != pv.dims)
+            return skip("the KV cache is not in device memory");
+        if (pk.dims[0] != 1 || pk.dims[1] != d.kv_num_heads || pk.dims[3] != d.head_size ||
+            (cap >= 0 && pk.dims[2] != cap))
+            return skip("KV cache shape");
+        cap = pk.dims[2];
+        table[l].k_cache = pk.ptr;
+        table[l].v_cache = pv.ptr;
+    }
+    d.kv_capacity = (int32_t)cap;
+    const int32_t total = host_i32(dp.total);
+    if (total < 1 || total > cap || total > d.max_position) return skip("total_sequence_length out of range");
+    // Present outputs must be the past buffers (KV written in place) and logits a device buffer.
+    const std::vector<int64_t> pdims = {1, d.kv_num_heads, cap, d.head_size};
+    for (size_t l = 0; l < dp.layers.size(); ++l) {
+        if (output_buffer(dp.layers[l].present_k, pdims, a, ctx) != table[l].k_cache ||
+            output_buffer(dp.layers[l].present_v, pdims, a, ctx) != table[l].v_cache)
+            return skip("present is not bound to past");
+    }
+    void* logits = output_buffer(dp.logits, {1, 1, d.vocab}, a, ctx);
+    if (!is_device_ptr(logits)) return skip("logits in host memory");
+    const size_t tb = table.size() * sizeof(OrtmiDecoderLayer);
+    if (!dp.table || dp.host_table.size() != table.size() ||
+        std::memcmp(dp.host_table.data(), table.data(), tb) != 0) {
+        if (!dp.table) dp.table = device_alloc(tb);
+        check_hip(hipMemcpyAsync(dp.table->ptr, table.data(), tb, hipMemcpyHostToDevice, stream_),
+                  "decode program table");
+        check_hip(hipStreamSynchronize(stream_), "decode program table");
+        dp.host_table = table;
+    }
+    const size_t wsb = ortmi_decoder_decode_step_workspace_size(&d);
+    if (!dp.ws || dp.ws_bytes < wsb) {
+        dp.ws = device_alloc(wsb);
+        dp.ws_bytes = wsb;
+        check_hip(hipMemsetAsync(dp.ws->ptr, 0, wsb, stream_), "decode program workspace");
+    }
+    *dp.status = -1;
+    const int rc = ortmi_decoder_decode_step(
+        static_cast<const OrtmiDecoderLayer*>(dp.table->ptr), &d, dp.embed_p, dp.embed_rows,
+        static_cast<const int64_t*>(ids->second.ptr),
+        static_cast<const int32_t*>(env_.at(dp.total).ptr), dp.cos_p, dp.sin_p, dp.gf_p, dp.ef,
+        static_cast<const uint8_t*>(dp.lm_B_p), dp.lm_S_p, logits,
+        static_cast<int64_t*>(dp.next_id->ptr), dp.status, dp.ws->ptr, dp.ws_bytes, stream_);
+    if (rc == ORTMI_E_INVALID) {
+        const std::string why = ortmi_last_error();
+        if (dprog_required_) fail("decode program rejected the decoder: " + why);
+        dprog_.reset();  // this decoder's form is outside the program: op by op from now on
+        dprog_reject_ = why;
+        return false;
+    }
+    check_kernel(rc, "decode program");
+    return true;
 }
 
 Plan::~Plan() {
@@ -318,6 +619,22 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
             sig[i].ptr = p;
         }
         env_[inputs_[i]] = t;
+    }
+    if (!dprog_ && dprog_required_) {
+        auto ids = dprog_ids_.empty() ? env_.end() : env_.find(dprog_ids_);
+        if (ids == env_.end() || ids->second.numel() == 1)
+            fail("decode program does not apply: " + dprog_reject_);
+    }
+    if (dprog_) {
+        outs_.clear();
+        if (run_decode_program(a, ctx)) {
+            check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+            g_out_staging = nullptr;
+            const int32_t st = *dprog_->status;
+            if (st == 2) fail("decode program: input id out of range", ORT_INVALID_ARGUMENT);
+            if (st != 0) fail("decode program failed (status " + std::to_string(st) + ")");
+            return;
+        }
     }
     for (auto& kv : constants_) {
         const ValueDesc& v = sub_.values.at(kv.first);

@@ -211,9 +211,13 @@ class DecoderRunner:
         self.session.bind_output("logits", self.logits)
         self.ids = torch.zeros((1, max_prompt), dtype=torch.int64, device=dev)
         self.next_id = torch.zeros((1, 1), dtype=torch.int64, device=dev)
-        self.seqlens = torch.zeros(1, dtype=torch.int32, device=dev)
-        # total_sequence_length lives in (pinned) host memory, as ONNX Runtime keeps it.
+        # seqlens_k and total_sequence_length live in (pinned) host memory, as ONNX
+        # Runtime keeps them.
+        self.seqlens = torch.zeros(1, dtype=torch.int32, pin_memory=True)
         self.total = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self._host = np.frombuffer(
+            (ctypes.c_int32 * 1).from_address(self.seqlens.data_ptr()), np.int32), np.frombuffer(
+            (ctypes.c_int32 * 1).from_address(self.total.data_ptr()), np.int32)
         self.length = 0
         self.lib = load_kernels()
         self.argmax_ws = torch.empty(
@@ -233,10 +237,10 @@ class DecoderRunner:
         """Forward S new tokens (device int64 [1, S]); logits land in self.logits[:, :S]."""
         if self.length + S > self.cap:
             raise ValueError(f"KV capacity {self.cap} exceeded")
-        self.seqlens.fill_(self.length + S - 1)
         # The EP is not stream aware: like ONNX Runtime, hand it inputs that are ready.
         self.torch.cuda.current_stream().synchronize()
-        self.total[0] = self.length + S
+        self._host[0][0] = self.length + S - 1
+        self._host[1][0] = self.length + S
         self.session.run({"input_ids": (ids, hx.INT64)})
         self.length += S
 

@@ -564,3 +564,38 @@ def test_ep_decoder_config4_greedy_tokens_strict(ortmi, oracle, dec):
     print(f"oracle: {time.time() - t0:.1f} s", flush=True)
     assert ref.shape == (steps + 1, cfg.vocab)
     _assert_greedy_strict(list(zip(gpu, ref, toks)), "cfg4 512+128")
+
+
+def test_ep_decode_program_matches_op_path(ortmi, oracle, dec, monkeypatch):
+    """One-token steps of a fused decoder run as one launch of the decode program
+    (ORTMI_EP_PROGRAM=require makes any other path an error) against the same steps
+    op by op (ORTMI_EP_PROGRAM=0): logits within the fp16 tolerance carried through
+    the layers, identical greedy tokens; and the program's steps teacher-forced
+    against the oracle with the strict token rule."""
+    cfg = _small_cfg(dec, 128)
+    w = dec.make_weights(cfg, seed=41)
+    prompt = np.random.default_rng(42).integers(0, cfg.vocab, size=17)
+
+    def run(mode):
+        monkeypatch.setenv("ORTMI_EP_PROGRAM", mode)
+        r = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
+        r.prefill(prompt)
+        logits, toks = [], [int(r.next_id.item())]
+        for _ in range(10):
+            r.decode_step()
+            logits.append(host(r.logits[0, :1])[0])
+            toks.append(int(r.next_id.item()))
+        return logits, toks
+
+    pl, pt = run("require")
+    ol, ot = run("0")
+    for i, (a, b) in enumerate(zip(pl, ol)):
+        err = float(np.abs(a - b).max())
+        print(f"step {i}: program vs op path max |logit diff| {err:.3e}", flush=True)
+        assert err <= 2.0 ** -7 * max(1.0, float(np.abs(b).max()))
+    assert pt == ot
+
+    monkeypatch.setenv("ORTMI_EP_PROGRAM", "require")
+    runner = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
+    rows = _teacher_forced_check(oracle, runner, cfg, w, prompt.tolist(), steps=10)
+    _assert_greedy_strict(rows, "decode program through the EP")
