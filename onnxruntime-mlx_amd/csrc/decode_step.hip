@@ -61,6 +61,8 @@ constexpr int kKvRing = 4;             // attention steps in flight in registers
 constexpr int kIChunksPerLane = 5;     // down_proj: K = I <= 5 * 64 * 32 = 10240
 constexpr int kMaxLayers = 64;
 constexpr int kMaxUnits = 3;           // tagged vectors up to 3 * 512 units of 8 values
+constexpr int kNSMax = 8;              // key splits per attention head
+constexpr int kPartWords = 130;        // a split's partial: o[128], running max, sum
 constexpr unsigned long long kDeadlineTicks = 10000000ull;  // 100 ms
 
 // Control block (uint32 words, one 128-byte line each).
@@ -72,6 +74,7 @@ struct Params {
     const OrtmiDecoderLayer* layers;
     int L, D, H, KV, G, I, V, cap, max_pos, half, nwg;
     int gq, go, ggu, gd;  // QKV / o_proj / gate-up groups and down rows per workgroup
+    int nc, ns;           // projection workgroups; key splits per attention head
     float scale, final_eps;
     const half_t* embed;
     int64_t embed_rows;
@@ -88,11 +91,22 @@ struct Params {
     uint32_t* ctl;
     uint32_t* flow;          // per layer: qkv [NQ], att [H*hd], y [D], act [I], dout [D]
     uint32_t flow_stride;    // words per layer
+    uint64_t* part;          // per layer: attention split partials [H][NS][kPartWords]
     uint64_t* argp;          // per workgroup: index | fp16 value << 32 | tag << 48
 };
 
+// A pointer every lane of the wave holds, made provably uniform (scalar registers):
+// pointers read from the layer table in LDS arrive in vector registers, and a
+// buffer resource built from those would make every load a per-lane loop.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, kBufferWord3);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform_ptr(p)), 0,
+                                             (int)__builtin_amdgcn_readfirstlane(bytes), kBufferWord3);
 }
 template <int POL>
 __device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -305,11 +319,17 @@ __device__ __forceinline__ void rope8(float (&x)[8], int li, int half, const flo
                                       const float* sn) {
     if (half == 0) return;
     const int off = half / 8;
-    const int lane = threadIdx.x & 63;
-    const int partner = (lane & ~15) | ((li < off || (li >= 2 * off)) ? li + off : li - off);
     float px[8];
+    if (off == 8) {
+        // Partner li ^ 8 inside the 16-lane row: a DPP row rotation by 8.
 #pragma unroll
-    for (int i = 0; i < 8; ++i) px[i] = __shfl(x[i], partner & 63, 64);
+        for (int i = 0; i < 8; ++i) px[i] = dpp_mov<0x128>(x[i]);
+    } else {
+        const int lane = threadIdx.x & 63;
+        const int partner = (lane & ~15) | ((li < off || (li >= 2 * off)) ? li + off : li - off);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) px[i] = __shfl(x[i], partner & 63, 64);
+    }
     const int d0 = li * 8;
     if (d0 >= 2 * half) return;
     const bool low = d0 < half;
@@ -460,13 +480,15 @@ __device__ __forceinline__ void arg_wave(float& best, int& bi) {
 }
 
 constexpr int gu_groups(int cpld) { return cpld == 3 ? 3 : 2; }
-// Slot plan of a wave's LDS region (chunks of 64 x 16 bytes):
-//   QKV [0, CPLD)                  end of phase E (or at the start)
-//   o_proj [kLo, kLo + CPLD)       end of phase A (o_proj workgroups)
-//   attention K [0, P), V [P, 2P)  end of phase A (attention workgroups)
-//   gate/up [0, kGu * CPLD)        end of phase C / B
-//   down [kLo, kLo + 5)            end of phase D
-// Every range is written only after the wave consumed what it overlaps.
+// Slot plan of a wave's LDS region (chunks of 64 x 16 bytes), projection
+// workgroups, with the phase whose end requests each range:
+//   gate/up [0, kGu * CPLD)        end of A      read in D
+//   down [kLo, kLo + 5)            end of C      read in E
+//   QKV [0, CPLD)                  end of D      read in A of the next layer
+//   o_proj [kLo, kLo + CPLD)       end of E      read in C of the next layer
+// Every range is written only after the wave consumed what it overlaps. Attention
+// workgroups hold K [0, P) and V [P, 2P) of their key split, requested at the end
+// of the previous layer's attention.
 constexpr int region_lo(int cpld) { return gu_groups(cpld) * cpld; }
 constexpr int region_slots(int cpld) {
     return region_lo(cpld) + (cpld > kIChunksPerLane ? cpld : kIChunksPerLane);
@@ -485,26 +507,27 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
     __shared__ int s_arg_i[kWaves];
     __shared__ float s_cos[64], s_sin[64];
     __shared__ float s_out[64];  // a phase's outputs of this workgroup, stored as one block
+    __shared__ float s_pm[kNSMax], s_pl[kNSMax];  // sibling splits' running max and sum
     constexpr int kGu = gu_groups(CPLD);
     constexpr int kLo = region_lo(CPLD);
     constexpr int kRegion = region_slots(CPLD);
     constexpr int kPref = kv_pref_steps(CPLD);
     static_assert(kLo + CPLD <= kRegion && 2 * kPref <= kRegion, "slots");
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
     const int wg = blockIdx.x, nwg = p.nwg;
     const int TW = kWaves * nwg;
-    const int gw = wave * nwg + wg;  // global wave index (spreads work over CUs)
+    const int gw = wave * nwg + wg;  // global wave index (spreads the lm_head over CUs)
     const int D = p.D, H = p.H, KV = p.KV, I = p.I;
     const int NQ = (H + 2 * KV) * HD, HO = H * HD;
     const int CD = D / 32, CO = HO / 32, CI = I / 32;
     const int li16 = lane & 15, grp = lane >> 4;
-    const int NC = nwg - H;  // workgroups [0, NC) run o_proj, [NC, nwg) attention
+    const int NC = p.nc;  // workgroups [0, NC) run the projections, [NC, nwg) attention
     const bool attn_wg = wg >= NC;
-    const int a_head = wg - NC;
 
-    // LDS: weight regions, activations (norm outputs; staged vectors), residual,
-    // attention merge.
+    // LDS: weight (or K/V) regions, activations (norm outputs; staged vectors),
+    // residual, attention merge.
     uint4* wreg = smem + (size_t)wave * kRegion * 64;
     uint4* sA0 = smem + (size_t)kWaves * kRegion * 64;
     uint4* sA1 = sA0 + D / 8;
@@ -529,57 +552,41 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         const unsigned started = atomic_add_dev(p.ctl + kCtlStart, 1u);
         s_tag = (started / (unsigned)nwg) % 65535u + 1u;
     }
+    const int ctx = total - 1;  // cached keys; the new key sits at index ctx
+    if (attn_wg && tid < p.half) {
+        s_cos[tid] = (float)p.cos[(size_t)ctx * p.half + tid];
+        s_sin[tid] = (float)p.sin[(size_t)ctx * p.half + tid];
+    }
     __syncthreads();
     const Flow f{p.ctl, p.status, s_tag, __builtin_amdgcn_s_memrealtime() + kDeadlineTicks};
     const uint32_t tag = f.tag;
-    const int ctx = total - 1;  // cached keys; the new key sits at index ctx
 
     int64_t id = *p.input_id;  // negative ids count from the end
     if (id < 0) id += p.embed_rows;
     const bool bad_id = id < 0 || id >= p.embed_rows;
     if (bad_id) id = 0;
+    uint32_t* const f_res = p.flow + (size_t)p.L * p.flow_stride;  // last post-attention residual
+    const uint32_t* prev_dout = p.flow + (size_t)(p.L - 1) * p.flow_stride + NQ + HO + 2 * D + I - D;
 
-    // Attention workgroup: query head a_head of KV head a_kvh; the rotary row at
-    // position ctx goes to LDS.
-    const int a_kvh = attn_wg ? a_head / p.G : 0;
-    if (attn_wg && tid < p.half) {
-        s_cos[tid] = (float)p.cos[(size_t)ctx * p.half + tid];
-        s_sin[tid] = (float)p.sin[(size_t)ctx * p.half + tid];
-    }
-    const int a_steps = (total + kKeySlots - 1) / kKeySlots;
-    const uint32_t kv_bytes = (uint32_t)KV * p.cap * HD * 2;
-    // Rows are dealt to workgroups in contiguous ranges (a phase's outputs of one
-    // workgroup are then one block of the vector, written by one store instruction:
-    // lines written piecewise by many CUs cost several microseconds to settle), and
-    // within a workgroup to its waves.
-    const int ng_q = (NQ + 3) / 4, ng_o = (D + 3) / 4, ng_gu = (2 * I + 3) / 4;
-    const int gq = p.gq, go = p.go, ggu = p.ggu, gd = p.gd;
-    const int q_g = wave < gq ? wg * gq + wave : ng_q;                  // QKV group
-    const int o_g = !attn_wg && wave < go ? wg * go + wave : ng_o;      // o_proj group
-    const int d_row = wave < gd ? wg * gd + wave : D;                   // down row
-    uint32_t sq[CPLD], so[CPLD], sg[kGu][CPLD], sd[kIChunksPerLane];
-    {
-        const WeightRef wr = weight_ref(s_layers[0].qkv_weight, s_layers[0].qkv_scales, NQ, CD);
-        fetch_rows<16, CPLD>(wr, q_g < ng_q ? 4 * q_g + grp : NQ, li16, wreg, sq);
-    }
-    const uint32_t* prev_dout = nullptr;
-
-    // ------------------------------------------------------------------- layers
-    for (int l = 0; l < p.L; ++l) {
-        const OrtmiDecoderLayer& ly = s_layers[l];
-        // Lane-derived indices, recomputed per layer rather than held across it.
-        const int lane = opaque(threadIdx.x & 63);
-        const int li16 = lane & 15, grp = lane >> 4;
-        const int slot = wave * 4 + grp;  // attention key slot of this lane group
+    if (attn_wg) {
+        // ---------------------------------------------------- attention workgroups
+        // Workgroup a = wg - NC owns keys [k0, k1) of query head h = a / NS. Its K/V
+        // rows sit in LDS, requested right after the previous layer's attention, so
+        // the wait for q/k/v never queues behind them. Split 0 of each head merges
+        // the others' partials (tagged 64-bit words: value, tag) into the output.
+        const int NS = p.ns, a = wg - NC;
+        const int h = a / NS, s = a % NS, kvh = h / p.G;
+        const int ks = (total + NS - 1) / NS;
+        const int k0 = s * ks, k1 = min(k0 + ks, total);
+        const int steps = k1 > k0 ? (k1 - k0 + kKeySlots - 1) / kKeySlots : 0;
+        const uint32_t kv_bytes = (uint32_t)KV * p.cap * HD * 2;
+        const int slot = wave * 4 + grp;  // key slot of this lane group
         auto kv_off = [&](int t) -> uint32_t {
-            const int key = slot + t * kKeySlots;
-            return key < ctx ? ((uint32_t)(a_kvh * p.cap + key) * HD + li16 * 8) * 2u : kv_bytes;
+            const int key = k0 + slot + t * kKeySlots;
+            return key < k1 && key < ctx ? ((uint32_t)(kvh * p.cap + key) * HD + li16 * 8) * 2u
+                                         : kv_bytes;
         };
-        auto qkv_fetch = [&](const OrtmiDecoderLayer& lz) {
-            const WeightRef wr = weight_ref(lz.qkv_weight, lz.qkv_scales, NQ, CD);
-            fetch_rows<16, CPLD>(wr, q_g < ng_q ? 4 * q_g + grp : NQ, li16, wreg, sq);
-        };
-        auto kv_fetch = [&]() {
+        auto kv_fetch = [&](const OrtmiDecoderLayer& ly) {
             const __amdgpu_buffer_rsrc_t rk = rsrc(ly.k_cache, kv_bytes), rv = rsrc(ly.v_cache, kv_bytes);
 #pragma unroll
             for (int t = 0; t < kPref; ++t) {
@@ -588,62 +595,29 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 dma16(rv, off, wreg + (kPref + t) * 64);
             }
         };
-        auto o_fetch = [&]() {
-            const WeightRef wr = weight_ref(ly.o_weight, ly.o_scales, D, CO);
-            fetch_rows<16, CPLD>(wr, o_g < ng_o ? 4 * o_g + grp : D, li16, wreg + kLo * 64, so);
-        };
-        auto gu_fetch = [&]() {
-            const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
-#pragma unroll
-            for (int k = 0; k < kGu; ++k) {
-                const int lg = wave + k * kWaves;
-                const int g = lg < ggu ? wg * ggu + lg : ng_gu;
-                fetch_rows<16, CPLD>(wr, g < ng_gu ? 4 * g + grp : 2 * I, li16,
-                                     wreg + k * CPLD * 64, sg[k]);
-            }
-        };
-        auto down_fetch = [&]() {
-            const WeightRef wr = weight_ref(ly.down_weight, ly.down_scales, D, CI);
-            fetch_rows<64, kIChunksPerLane>(wr, d_row, lane, wreg + kLo * 64, sd);
-        };
-        uint32_t* f_qkv = p.flow + (size_t)l * p.flow_stride;
-        uint32_t* f_att = f_qkv + NQ;
-        uint32_t* f_y = f_att + HO;
-        uint32_t* f_act = f_y + D;
-        uint32_t* f_dout = f_act + I;
-
-        // Phase A: input norm (+ residual), merged QKV GEMV.
-        if (!norm_poll(prev_dout, p.embed + id * D, l > 0, static_cast<const half_t*>(ly.ln1_gamma),
-                       ly.ln1_epsilon, D, sR, sA0, sSum0, sRed, f, &s_fail))
-            return;
-        {
-            __builtin_amdgcn_s_waitcnt(0);
-            const float v = group_sum<16>(row_dot<16, CPLD>(wreg, sq, sA0, sSum0, CD, li16));
-            if (li16 == 0 && wave < gq) s_out[wave * 4 + grp] = v;
-            __syncthreads();
-            if (tid < 4 * gq && 4 * wg * gq + tid < NQ)
-                put(rsrc(f_qkv, (uint32_t)NQ * 4), 4 * wg * gq + tid, s_out[tid], tag);
-            wait_lds();
-            if (attn_wg) kv_fetch();
-            else o_fetch();
-        }
-
-        if (attn_wg) {
-            // Phase B: attention for query head a_head over keys [0, total).
+        const float qscale = p.scale * 1.4426950408889634f;  // scores in log2 units
+        kv_fetch(s_layers[0]);
+        for (int l = 0; l < p.L; ++l) {
+            const OrtmiDecoderLayer& ly = s_layers[l];
+            uint32_t* f_qkv = p.flow + (size_t)l * p.flow_stride;
+            uint32_t* f_att = f_qkv + NQ;
+            uint64_t* f_part = p.part + (size_t)l * H * NS * kPartWords;
             const __amdgpu_buffer_rsrc_t rk = rsrc(ly.k_cache, kv_bytes), rv = rsrc(ly.v_cache, kv_bytes);
+            // Steps past the LDS-resident ones (long contexts) go through a register ring.
             uint4 ringk[kKvRing], ringv[kKvRing];
+            if (steps > kPref) {
 #pragma unroll
-            for (int r = 0; r < kKvRing; ++r) {
-                const uint32_t off = kv_off(kPref + r);
-                ringk[r] = ld128<kCachePolicyNT>(rk, off);
-                ringv[r] = ld128<kCachePolicyNT>(rv, off);
+                for (int r = 0; r < kKvRing; ++r) {
+                    const uint32_t off = kv_off(kPref + r);
+                    ringk[r] = ld128<kCachePolicyNT>(rk, off);
+                    ringv[r] = ld128<kCachePolicyNT>(rv, off);
+                }
             }
-            const uint32_t qbytes = (uint32_t)NQ * 4u;
-            const uint32_t off[3] = {(uint32_t)(a_head * HD + li16 * 8) * 4u,
-                                     (uint32_t)((H + a_kvh) * HD + li16 * 8) * 4u,
-                                     (uint32_t)((H + KV + a_kvh) * HD + li16 * 8) * 4u};
+            const uint32_t off[3] = {(uint32_t)(h * HD + li16 * 8) * 4u,
+                                     (uint32_t)((H + kvh) * HD + li16 * 8) * 4u,
+                                     (uint32_t)((H + KV + kvh) * HD + li16 * 8) * 4u};
             uint4 qkv3[3];
-            const bool ok = poll_units<3>(rsrc(f_qkv, qbytes), off, 7u, f, qkv3);
+            const bool ok = poll_units<3>(rsrc(f_qkv, (uint32_t)NQ * 4u), off, 7u, f, qkv3);
             float q[8], kn[8], vn[8];
             {
                 const half_t* qh = reinterpret_cast<const half_t*>(&qkv3[0]);
@@ -665,7 +639,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 for (int e = 0; e < 8; ++e) {
                     q8[e] = (half_t)q[e];
                     k8[e] = (half_t)kn[e];
-                    kn[e] = (float)k8[e];
                 }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -673,20 +646,19 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                     kw_new[e] = reinterpret_cast<const uint32_t*>(k8)[e];
                 }
             }
-            // The first query head of the KV group appends the new key/value row
-            // to the cache (shared buffer, written in place at row ctx).
-            if (ok && a_head % p.G == 0 && wave == 0 && grp == 0) {
-                const size_t o = ((size_t)(a_kvh * p.cap + ctx) * HD + li16 * 8);
+            // The split holding key ctx of the first query head of the KV group
+            // appends the new key/value row to the cache (written in place at ctx).
+            if (ok && h % p.G == 0 && ctx >= k0 && ctx < k1 && wave == 0 && grp == 0) {
+                const size_t o = ((size_t)(kvh * p.cap + ctx) * HD + li16 * 8);
                 *reinterpret_cast<uint4*>(static_cast<half_t*>(ly.k_cache) + o) =
                     make_uint4(kw_new[0], kw_new[1], kw_new[2], kw_new[3]);
                 *reinterpret_cast<uint4*>(static_cast<half_t*>(ly.v_cache) + o) = qkv3[2];
             }
-            const float qscale = p.scale * 1.4426950408889634f;  // scores in log2 units
             float m = -INFINITY, lsum = 0.f, o[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = 0.f;
             auto attend = [&](const uint4& kr, const uint4& vr, int key) {
-                if (key > ctx) return;  // a whole 16-lane group shares the key
+                if (key >= k1) return;  // a whole 16-lane group shares the key
                 const bool fresh = key == ctx;
                 const uint32_t kw[4] = {fresh ? kw_new[0] : kr.x, fresh ? kw_new[1] : kr.y,
                                         fresh ? kw_new[2] : kr.z, fresh ? kw_new[3] : kr.w};
@@ -705,16 +677,21 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 for (int e = 0; e < 8; ++e) o[e] = fmaf(pe, fresh ? vn[e] : (float)vb[e], o[e] * fo);
                 m = mn;
             };
-            __builtin_amdgcn_s_waitcnt(0);
+            // The LDS K/V rows were requested before the q/k/v words, and a wave's
+            // vector memory requests complete in order: reading them through an
+            // index that depends on the polled words orders the reads after both
+            // (without also waiting for the cache-append stores above).
+            int kv_lane = lane;
+            asm volatile("" : "+v"(kv_lane) : "v"(qkv3[0].x), "v"(qkv3[2].w));
 #pragma unroll
             for (int t = 0; t < kPref; ++t)
-                if (t < a_steps)
-                    attend(wreg[t * 64 + lane], wreg[(kPref + t) * 64 + lane], slot + t * kKeySlots);
-            for (int t0 = kPref; t0 < a_steps; t0 += kKvRing) {
+                if (t < steps)
+                    attend(wreg[t * 64 + kv_lane], wreg[(kPref + t) * 64 + kv_lane], k0 + slot + t * kKeySlots);
+            for (int t0 = kPref; t0 < steps; t0 += kKvRing) {
 #pragma unroll
                 for (int r = 0; r < kKvRing; ++r) {
                     const int t = t0 + r;
-                    if (t < a_steps) attend(ringk[r], ringv[r], slot + t * kKeySlots);
+                    if (t < steps) attend(ringk[r], ringv[r], k0 + slot + t * kKeySlots);
                     const uint32_t off2 = kv_off(t + kKvRing);
                     ringk[r] = ld128<kCachePolicyNT>(rk, off2);
                     ringv[r] = ld128<kCachePolicyNT>(rv, off2);
@@ -724,14 +701,19 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             // waves through LDS.
 #pragma unroll
             for (int sh = 16; sh <= 32; sh <<= 1) {
-                const float om = __shfl_xor(m, sh, 64);
-                const float ol = __shfl_xor(lsum, sh, 64);
-                const float mn = fmaxf(m, om);
-                const float fa = m == -INFINITY ? 0.f : exp2f(m - mn);
-                const float fb = om == -INFINITY ? 0.f : exp2f(om - mn);
-                lsum = lsum * fa + ol * fb;
+                // The two states of lanes l and l ^ sh, by v_permlane16/32_swap; the
+                // merge is symmetric in them.
+                auto sw = [&](float v) { return sh == 16 ? swap16(v) : swap32(v); };
+                const LanePair pm = sw(m), pl = sw(lsum);
+                const float mn = fmaxf(pm.a, pm.b);
+                const float fa = pm.a == -INFINITY ? 0.f : exp2f(pm.a - mn);
+                const float fb = pm.b == -INFINITY ? 0.f : exp2f(pm.b - mn);
+                lsum = pl.a * fa + pl.b * fb;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = o[e] * fa + __shfl_xor(o[e], sh, 64) * fb;
+                for (int e = 0; e < 8; ++e) {
+                    const LanePair po = sw(o[e]);
+                    o[e] = po.a * fa + po.b * fb;
+                }
                 m = mn;
             }
             if (lane == 0) {
@@ -743,84 +725,253 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 for (int e = 0; e < 8; ++e) sO[wave * HD + li16 * 8 + e] = o[e];
             }
             if (!all_ok(ok, &s_fail)) return;
-            if (tid < HD) {
-                float M = -INFINITY;
+            // The split's state over its 8 waves: o_d (d = tid), M, L.
+            float M = -INFINITY, L = 0.f, acc = 0.f;
+            if (tid < HD + 2) {
 #pragma unroll
                 for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_am[w]);
-                float L = 0.f, acc = 0.f;
 #pragma unroll
                 for (int w = 0; w < kWaves; ++w) {
                     const float fw = s_am[w] == -INFINITY ? 0.f : exp2f(s_am[w] - M);
                     L += s_al[w] * fw;
-                    acc += sO[w * HD + tid] * fw;
+                    if (tid < HD) acc += sO[w * HD + tid] * fw;
                 }
-                put(rsrc(f_att, (uint32_t)HO * 4), a_head * HD + tid, L > 0.f ? acc / L : 0.f, tag);
             }
+            bool mok = true;
+            if (NS > 1 && s > 0) {
+                if (tid < HD + 2) {
+                    const float v = tid < HD ? acc : (tid == HD ? M : L);
+                    const uint64_t w = (uint64_t)__float_as_uint(v) | ((uint64_t)tag << 32);
+                    __hip_atomic_store(f_part + (size_t)(h * NS + s) * kPartWords + tid, w,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            } else if (NS > 1) {
+                // Split 0 folds in splits 1 .. NS-1: thread d < HD waits for word d of
+                // every sibling, thread j - 1 (j < NS) also for sibling j's max and sum,
+                // which it passes on through LDS. Every word is requested at once; only
+                // those not yet carrying this launch's tag are requested again.
+                uint64_t wo[kNSMax];
+                uint64_t wm = 0, wl = 0;
+                const int mj = tid + 1;  // sibling whose max / sum this thread fetches
+                const bool ml = mj < NS;
+                auto rec = [&](int j) { return f_part + (size_t)(h * NS + j) * kPartWords; };
+                unsigned pend = 0;
+                if (tid < HD) {
+#pragma unroll
+                    for (int j = 1; j < kNSMax; ++j)
+                        if (j < NS) {
+                            wo[j] = __hip_atomic_load(rec(j) + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            pend |= 1u << j;
+                        }
+                    if (ml) {
+                        wm = __hip_atomic_load(rec(mj) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        wl = __hip_atomic_load(rec(mj) + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        pend |= 1u;
+                    }
+                }
+                for (unsigned it = 0; pend; ++it) {
+#pragma unroll
+                    for (int j = 1; j < kNSMax; ++j)
+                        if (((pend >> j) & 1u) && (uint32_t)(wo[j] >> 32) == tag) pend &= ~(1u << j);
+                    if ((pend & 1u) && (uint32_t)(wm >> 32) == tag && (uint32_t)(wl >> 32) == tag) {
+                        s_pm[mj] = __uint_as_float((uint32_t)wm);
+                        s_pl[mj] = __uint_as_float((uint32_t)wl);
+                        pend &= ~1u;
+                    }
+                    if (!pend) break;
+                    if (!keep_waiting(f, it)) {
+                        mok = false;
+                        break;
+                    }
+#pragma unroll
+                    for (int j = 1; j < kNSMax; ++j)
+                        if ((pend >> j) & 1u)
+                            wo[j] = __hip_atomic_load(rec(j) + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (pend & 1u) {
+                        wm = __hip_atomic_load(rec(mj) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        wl = __hip_atomic_load(rec(mj) + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+                if (!all_ok(mok, &s_fail)) return;
+                if (tid < HD) {
+                    float Mt = M;
+                    for (int j = 1; j < NS; ++j) Mt = fmaxf(Mt, s_pm[j]);
+                    const float f0 = M == -INFINITY ? 0.f : exp2f(M - Mt);
+                    float num = acc * f0, den = L * f0;
+#pragma unroll
+                    for (int j = 1; j < kNSMax; ++j)
+                        if (j < NS) {
+                            const float fw = s_pm[j] == -INFINITY ? 0.f : exp2f(s_pm[j] - Mt);
+                            num += __uint_as_float((uint32_t)wo[j]) * fw;
+                            den += s_pl[j] * fw;
+                        }
+                    put(rsrc(f_att, (uint32_t)HO * 4), h * HD + tid, den > 0.f ? num / den : 0.f, tag);
+                }
+            } else if (tid < HD) {
+                put(rsrc(f_att, (uint32_t)HO * 4), h * HD + tid, L > 0.f ? acc / L : 0.f, tag);
+            }
+            // This split's K/V rows are consumed: the next layer's go to LDS now.
             wait_lds();
-            gu_fetch();
-        } else {
-            // Phase C: o_proj GEMV over the attention output.
-            if (!stage_poll(f_att, HO, sA1, sSum1, f, &s_fail)) return;
-            __builtin_amdgcn_s_waitcnt(0);
-            const float v = group_sum<16>(row_dot<16, CPLD>(wreg + kLo * 64, so, sA1, sSum1, CO, li16));
-            if (li16 == 0 && wave < go) s_out[wave * 4 + grp] = v;
-            __syncthreads();
-            if (tid < 4 * go && 4 * wg * go + tid < D)
-                put(rsrc(f_y, (uint32_t)D * 4), 4 * wg * go + tid, s_out[tid], tag);
-            wait_lds();
-            gu_fetch();
+            if (l + 1 < p.L) kv_fetch(s_layers[l + 1]);
+            if (!all_ok(mok, &s_fail)) return;
         }
-
-        // Phase D: residual + post-attention norm, gate/up GEMV with SwiGLU.
-        if (!norm_poll(f_y, nullptr, true, static_cast<const half_t*>(ly.ln2_gamma), ly.ln2_epsilon,
-                       D, sR, sA0, sSum0, sRed, f, &s_fail))
-            return;
+        // The final norm's residual: the last layer's post-attention residual,
+        // published by workgroup 0.
         {
-            const __amdgpu_buffer_rsrc_t ra = rsrc(f_act, (uint32_t)I * 4);
-            // Local group lg of this workgroup: rows 4g .. 4g+3 (gate, up, gate, up),
-            // g = wg * ggu + lg, giving pairs 2g and 2g + 1 (local 2lg, 2lg + 1).
-            auto gu_out = [&](float v, int lg) {
-                v = group_sum<16>(v);
-                const float other = __shfl_xor(v, 16, 64);  // gate (even group) <-> up (odd)
-                const int g = wg * ggu + lg;
-                if (lg < ggu && g < ng_gu && li16 == 0 && (grp & 1) == 0) {
-                    const float gv = r16(v), up = r16(other);
-                    const float sig = r16(1.0f / (1.0f + __expf(-gv)));
-                    s_out[2 * lg + (grp >> 1)] = r16(r16(gv * sig) * up);
+            const int units = D / 8;
+            const uint32_t bytes = (uint32_t)D * 4u;
+            const uint32_t offr[1] = {tid < units ? (uint32_t)tid * 32u : bytes};
+            uint4 rv[1];
+            const bool rok = poll_units<1>(rsrc(f_res, bytes), offr, tid < units ? 1u : 0u, f, rv);
+            if (rok && tid < units) sR[tid] = rv[0];
+            if (!all_ok(rok, &s_fail)) return;
+        }
+    } else {
+        // --------------------------------------------------- projection workgroups
+        // Rows are dealt to workgroups [0, NC) in contiguous ranges (a phase's outputs
+        // of one workgroup are then one block of the vector, written by one store
+        // instruction: lines written piecewise by many CUs cost several microseconds
+        // to settle), and within a workgroup to its waves.
+        const int ng_q = (NQ + 3) / 4, ng_o = (D + 3) / 4, ng_gu = (2 * I + 3) / 4;
+        const int gq = p.gq, go = p.go, ggu = p.ggu, gd = p.gd;
+        const int q_g = wave < gq ? wg * gq + wave : ng_q;  // QKV group
+        const int o_g = wave < go ? wg * go + wave : ng_o;  // o_proj group
+        const int d_row = wave < gd ? wg * gd + wave : D;   // down row
+        uint32_t sq[CPLD], so[CPLD], sg[kGu][CPLD], sd[kIChunksPerLane];
+        // Weights are requested two phases ahead of their use, into slot ranges no
+        // phase in between reads: end of A -> gate/up, end of C -> down, end of D ->
+        // next QKV, end of E -> next o_proj (region_lo).
+        {
+            const WeightRef wr = weight_ref(s_layers[0].qkv_weight, s_layers[0].qkv_scales, NQ, CD);
+            fetch_rows<16, CPLD>(wr, q_g < ng_q ? 4 * q_g + grp : NQ, li16, wreg, sq);
+            const WeightRef wo = weight_ref(s_layers[0].o_weight, s_layers[0].o_scales, D, CO);
+            fetch_rows<16, CPLD>(wo, o_g < ng_o ? 4 * o_g + grp : D, li16, wreg + kLo * 64, so);
+        }
+        const uint32_t* in_dout = nullptr;
+        for (int l = 0; l < p.L; ++l) {
+            const OrtmiDecoderLayer& ly = s_layers[l];
+            // Lane-derived indices, recomputed per layer rather than held across it.
+            const int lane = opaque(threadIdx.x & 63);
+            const int li16 = lane & 15, grp = lane >> 4;
+            auto qkv_fetch = [&](const OrtmiDecoderLayer& lz) {
+                const WeightRef wr = weight_ref(lz.qkv_weight, lz.qkv_scales, NQ, CD);
+                fetch_rows<16, CPLD>(wr, q_g < ng_q ? 4 * q_g + grp : NQ, li16, wreg, sq);
+            };
+            auto o_fetch = [&](const OrtmiDecoderLayer& lz) {
+                const WeightRef wr = weight_ref(lz.o_weight, lz.o_scales, D, CO);
+                fetch_rows<16, CPLD>(wr, o_g < ng_o ? 4 * o_g + grp : D, li16, wreg + kLo * 64, so);
+            };
+            auto gu_fetch = [&]() {
+                const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
+#pragma unroll
+                for (int k = 0; k < kGu; ++k) {
+                    const int lg = wave + k * kWaves;
+                    const int g = lg < ggu ? wg * ggu + lg : ng_gu;
+                    fetch_rows<16, CPLD>(wr, g < ng_gu ? 4 * g + grp : 2 * I, li16,
+                                         wreg + k * CPLD * 64, sg[k]);
                 }
             };
-            __builtin_amdgcn_s_waitcnt(0);
-#pragma unroll
-            for (int k = 0; k < kGu; ++k)
-                gu_out(row_dot<16, CPLD>(wreg + k * CPLD * 64, sg[k], sA0, sSum0, CD, li16), wave + k * kWaves);
-            const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
-            for (int lg = wave + kGu * kWaves; lg < ggu; lg += kWaves) {
-                const int g = wg * ggu + lg;
-                Rows<CPLD> r;
-                load_rows<16, CPLD>(r, wr, g < ng_gu ? 4 * g + grp : 2 * I, li16);
-                gu_out(rows_dot<16, CPLD>(r, sA0, sSum0, CD, li16), lg);
-            }
-            __syncthreads();
-            if (tid < 2 * ggu && 2 * wg * ggu + tid < I)
-                put(ra, 2 * wg * ggu + tid, s_out[tid], tag);
-            wait_lds();
-            down_fetch();
-        }
+            auto down_fetch = [&]() {
+                const WeightRef wr = weight_ref(ly.down_weight, ly.down_scales, D, CI);
+                fetch_rows<64, kIChunksPerLane>(wr, d_row, lane, wreg + kLo * 64, sd);
+            };
+            uint32_t* f_qkv = p.flow + (size_t)l * p.flow_stride;
+            uint32_t* f_att = f_qkv + NQ;
+            uint32_t* f_y = f_att + HO;
+            uint32_t* f_act = f_y + D;
+            uint32_t* f_dout = f_act + I;
 
-        // Phase E: down GEMV (K = I).
-        if (!stage_poll(f_act, I, sA1, sSum1, f, &s_fail)) return;
-        {
-            __builtin_amdgcn_s_waitcnt(0);
-            const float v =
-                wave_sum(row_dot<64, kIChunksPerLane>(wreg + kLo * 64, sd, sA1, sSum1, CI, lane));
-            if (lane == 0 && wave < gd) s_out[wave] = v;
-            __syncthreads();
-            if (tid < gd && wg * gd + tid < D)
-                put(rsrc(f_dout, (uint32_t)D * 4), wg * gd + tid, s_out[tid], tag);
-            wait_lds();
-            if (l + 1 < p.L) qkv_fetch(s_layers[l + 1]);
+            // Phase A: input norm (+ residual), merged QKV GEMV.
+            if (!norm_poll(in_dout, p.embed + id * D, l > 0, static_cast<const half_t*>(ly.ln1_gamma),
+                           ly.ln1_epsilon, D, sR, sA0, sSum0, sRed, f, &s_fail))
+                return;
+            {
+                __builtin_amdgcn_s_waitcnt(0);
+                const float v = group_sum<16>(row_dot<16, CPLD>(wreg, sq, sA0, sSum0, CD, li16));
+                if (li16 == 0 && wave < gq) s_out[wave * 4 + grp] = v;
+                __syncthreads();
+                if (tid < 4 * gq && 4 * wg * gq + tid < NQ)
+                    put(rsrc(f_qkv, (uint32_t)NQ * 4), 4 * wg * gq + tid, s_out[tid], tag);
+                wait_lds();
+                gu_fetch();
+            }
+
+            // Phase C: o_proj GEMV over the attention output.
+            if (!stage_poll(f_att, HO, sA1, sSum1, f, &s_fail)) return;
+            {
+                __builtin_amdgcn_s_waitcnt(0);
+                const float v = group_sum<16>(row_dot<16, CPLD>(wreg + kLo * 64, so, sA1, sSum1, CO, li16));
+                if (li16 == 0 && wave < go) s_out[wave * 4 + grp] = v;
+                __syncthreads();
+                if (tid < 4 * go && 4 * wg * go + tid < D)
+                    put(rsrc(f_y, (uint32_t)D * 4), 4 * wg * go + tid, s_out[tid], tag);
+                wait_lds();
+                down_fetch();
+            }
+
+            // Phase D: residual + post-attention norm, gate/up GEMV with SwiGLU.
+            if (!norm_poll(f_y, nullptr, true, static_cast<const half_t*>(ly.ln2_gamma), ly.ln2_epsilon,
+                           D, sR, sA0, sSum0, sRed, f, &s_fail))
+                return;
+            if (l + 1 == p.L && wg == 0) {
+                // The final norm's residual, for the attention workgroups.
+                for (int u = tid; u < D / 8; u += kThreads) {
+                    const uint4 r = sR[u];
+                    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+                    const __amdgpu_buffer_rsrc_t rr = rsrc(f_res, (uint32_t)D * 4);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        __builtin_amdgcn_raw_buffer_store_b32(((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) | (tag << 16),
+                                                              rr, (uint32_t)(u * 8 + e) * 4u, 0, kSC1);
+                }
+            }
+            {
+                const __amdgpu_buffer_rsrc_t ra = rsrc(f_act, (uint32_t)I * 4);
+                // Local group lg of this workgroup: rows 4g .. 4g+3 (gate, up, gate, up),
+                // g = wg * ggu + lg, giving pairs 2g and 2g + 1 (local 2lg, 2lg + 1).
+                auto gu_out = [&](float v, int lg) {
+                    v = group_sum<16>(v);
+                    const float other = __shfl_xor(v, 16, 64);  // gate (even group) <-> up (odd)
+                    const int g = wg * ggu + lg;
+                    if (lg < ggu && g < ng_gu && li16 == 0 && (grp & 1) == 0) {
+                        const float gv = r16(v), up = r16(other);
+                        const float sig = r16(1.0f / (1.0f + __expf(-gv)));
+                        s_out[2 * lg + (grp >> 1)] = r16(r16(gv * sig) * up);
+                    }
+                };
+                __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+                for (int k = 0; k < kGu; ++k)
+                    gu_out(row_dot<16, CPLD>(wreg + k * CPLD * 64, sg[k], sA0, sSum0, CD, li16), wave + k * kWaves);
+                const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
+                for (int lg = wave + kGu * kWaves; lg < ggu; lg += kWaves) {
+                    const int g = wg * ggu + lg;
+                    Rows<CPLD> r;
+                    load_rows<16, CPLD>(r, wr, g < ng_gu ? 4 * g + grp : 2 * I, li16);
+                    gu_out(rows_dot<16, CPLD>(r, sA0, sSum0, CD, li16), lg);
+                }
+                __syncthreads();
+                if (tid < 2 * ggu && 2 * wg * ggu + tid < I)
+                    put(ra, 2 * wg * ggu + tid, s_out[tid], tag);
+                wait_lds();
+                if (l + 1 < p.L) qkv_fetch(s_layers[l + 1]);
+            }
+
+            // Phase E: down GEMV (K = I).
+            if (!stage_poll(f_act, I, sA1, sSum1, f, &s_fail)) return;
+            {
+                __builtin_amdgcn_s_waitcnt(0);
+                const float v =
+                    wave_sum(row_dot<64, kIChunksPerLane>(wreg + kLo * 64, sd, sA1, sSum1, CI, lane));
+                if (lane == 0 && wave < gd) s_out[wave] = v;
+                __syncthreads();
+                if (tid < gd && wg * gd + tid < D)
+                    put(rsrc(f_dout, (uint32_t)D * 4), wg * gd + tid, s_out[tid], tag);
+                wait_lds();
+                if (l + 1 < p.L) o_fetch(s_layers[l + 1]);
+            }
+            in_dout = f_dout;
         }
-        prev_dout = f_dout;
     }
 
     // Phase F: final norm, lm_head GEMV (logits), argmax. The first lm_head rows are
@@ -917,9 +1068,18 @@ using namespace ortmi;
 namespace {
 
 struct StepShape {
-    size_t ctl, flow, argp, total;
+    size_t ctl, flow, part, argp, total;
     uint32_t flow_stride;
 };
+
+// Key splits per attention head: about 160 keys each (their K/V rows fit one
+// workgroup's LDS), while at least half the workgroups stay on the projections.
+int step_splits(const OrtmiDecoderDims* d, int nwg) {
+    int ns = (d->kv_capacity + 159) / 160;
+    ns = ns < 1 ? 1 : (ns > dprog::kNSMax ? dprog::kNSMax : ns);
+    while (ns > 1 && nwg - d->num_heads * ns < nwg / 2) --ns;
+    return ns;
+}
 
 StepShape step_layout(const OrtmiDecoderDims* d, int nwg) {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
@@ -931,8 +1091,11 @@ StepShape step_layout(const OrtmiDecoderDims* d, int nwg) {
     size_t off = 0;
     s.ctl = off;
     off += dprog::kCtlBytes;
-    s.flow = off;
-    off += al((size_t)std::max(d->layers, 0) * s.flow_stride * 4);
+    s.flow = off;  // per layer, then the final norm's residual [hidden]
+    off += al(((size_t)std::max(d->layers, 0) * s.flow_stride + (size_t)d->hidden) * 4);
+    s.part = off;
+    off += al((size_t)std::max(d->layers, 0) * d->num_heads * step_splits(d, nwg) *
+              dprog::kPartWords * 8);
     s.argp = off;
     off += al((size_t)nwg * 8);
     s.total = off;
@@ -985,9 +1148,10 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     ORTMI_REQUIRE(nwg >= 4 * d.num_heads && nwg >= kXcds,
                   "decoder step: needs at least 4 compute units per query head");
     const int nq = (d.num_heads + 2 * d.kv_num_heads) * d.head_size;
-    const int nc = nwg - d.num_heads;
-    const int gq = ((nq + 3) / 4 + nwg - 1) / nwg, go = ((d.hidden + 3) / 4 + nc - 1) / nc;
-    const int ggu = ((2 * d.intermediate + 3) / 4 + nwg - 1) / nwg, gd = (d.hidden + nwg - 1) / nwg;
+    const int ns = step_splits(dims, nwg);
+    const int nc = nwg - d.num_heads * ns;
+    const int gq = ((nq + 3) / 4 + nc - 1) / nc, go = ((d.hidden + 3) / 4 + nc - 1) / nc;
+    const int ggu = ((2 * d.intermediate + 3) / 4 + nc - 1) / nc, gd = (d.hidden + nc - 1) / nc;
     ORTMI_REQUIRE(gq <= dprog::kWaves && go <= dprog::kWaves && gd <= dprog::kWaves && 2 * ggu <= 64,
                   "decoder step: projection rows exceed the per-workgroup share");
     ORTMI_REQUIRE((int64_t)d.kv_num_heads * d.kv_capacity * d.head_size * 2 < (int64_t)INT32_MAX &&
@@ -1022,6 +1186,8 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     p.go = go;
     p.ggu = ggu;
     p.gd = gd;
+    p.nc = nc;
+    p.ns = ns;
     p.scale = d.scale != 0.f ? d.scale : 1.0f / sqrtf((float)d.head_size);
     p.final_eps = final_epsilon;
     p.embed = static_cast<const half_t*>(embed);
@@ -1039,6 +1205,7 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     p.ctl = reinterpret_cast<uint32_t*>(ws + s.ctl);
     p.flow = reinterpret_cast<uint32_t*>(ws + s.flow);
     p.flow_stride = s.flow_stride;
+    p.part = reinterpret_cast<uint64_t*>(ws + s.part);
     p.argp = reinterpret_cast<uint64_t*>(ws + s.argp);
 
     const int cpld = d.hidden <= 1536 && d.num_heads * d.head_size <= 1536 ? 3 : 4;
