@@ -224,6 +224,36 @@ int ortmi_group_query_attention(const void* query, const void* key, const void* 
                                 size_t workspace_bytes, void* stream);
 
 /*
+ * GroupQueryAttention with the optional inputs of the 11- and 16-input forms,
+ * for fp32, fp16 and bf16, head_size a multiple of 16 up to 256. Arguments and
+ * KV contract as ortmi_group_query_attention, plus:
+ *  - q_norm_weight / k_norm_weight [head_size] (inputs 14/15, both or neither,
+ *    in dtype): q and the new k are RMS-normalised per head with qk_norm_epsilon
+ *    before RoPE (rust/src/ops/attention.rs:663-670, claim 1698-1720);
+ *  - attention_bias (input 10, NULL when absent, in dtype), contiguous
+ *    [bias_batch, bias_heads, bias_rows, bias_cols] with bias_batch in {1, batch},
+ *    bias_heads in {1, num_heads}, bias_rows >= seq_len and bias_cols >=
+ *    valid_past + seq_len: entry [b, h, s, j] is added to scale * q.k of key j
+ *    and the causal mask still applies (attention.rs:256-285, claim 1637-1657).
+ * The workspace holds ortmi_group_query_attention_ex_workspace_size bytes.
+ * Replaces: the same reference op as ortmi_group_query_attention, for the forms
+ * whose rms_norm / array-mask SDPA calls (attention.rs:663-670, 264-285) the fused
+ * kernels do not cover.
+ */
+size_t ortmi_group_query_attention_ex_workspace_size(int64_t batch, int64_t seq_len,
+                                                     int64_t num_heads, int64_t head_size);
+int ortmi_group_query_attention_ex(
+    const void* query, const void* key, const void* value, const void* past_key,
+    const void* past_value, int64_t past_cap, int32_t total_sequence_length,
+    const void* cos_cache, const void* sin_cache, int64_t rotary_half, int64_t max_pos,
+    const void* q_norm_weight, const void* k_norm_weight, float qk_norm_epsilon,
+    const void* attention_bias, int64_t bias_batch, int64_t bias_heads, int64_t bias_rows,
+    int64_t bias_cols, void* output, void* present_key, void* present_value, int64_t batch,
+    int64_t seq_len, int64_t num_heads, int64_t kv_num_heads, int64_t head_size, float scale,
+    int32_t rotary_interleaved, int32_t dtype, void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/*
  * ortmi_group_query_attention without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). It has no counterpart in the

@@ -73,6 +73,11 @@ SIGNATURES = {
     "ortmi_group_query_attention": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
         _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
+    "ortmi_group_query_attention_ex_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "ortmi_group_query_attention_ex": (ctypes.c_int, [
+        _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _i64,
+        _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _vp,
+        _sz, _vp]),
     "ortmi_group_query_attention_noalloc_max_workspace": (_sz, []),
     "ortmi_group_query_attention_noalloc": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64,

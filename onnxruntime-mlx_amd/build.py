@@ -22,7 +22,8 @@ INCLUDE = os.path.normpath(os.path.join(HERE, "..", "include"))
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
-KERNEL_SOURCES = ["runtime.hip", "mnb.hip", "attention.hip", "norm.hip", "decode_step.hip"]
+KERNEL_SOURCES = ["runtime.hip", "mnb.hip", "attention.hip", "norm.hip", "decode_step.hip",
+                  "gqa_ext.hip"]
 EP_SOURCES = ["ep/ep.cpp", "ep/graph.cpp", "ep/fuse.cpp", "ep/plan.cpp"]
 
 HIP_FLAGS = [

@@ -283,24 +283,26 @@ std::string claim_matmulnbits(const NodeDesc& n, const GraphIR& g) {
 // rust/src/ops/attention.rs:1527-1738, restricted to what the gfx950 kernels run.
 std::string claim_gqa(const NodeDesc& n, const GraphIR& g) {
     REQUIRE(n.inputs.size() >= 7 && n.inputs.size() <= 16, "GroupQueryAttention needs 7-16 inputs");
+    REQUIRE(!n.outputs.empty() && !n.outputs[0].empty(), "GroupQueryAttention needs an output");
     const int64_t H = n.attr_int("num_heads", 0), KV = n.attr_int("kv_num_heads", 0);
     REQUIRE(H > 0 && KV > 0 && H % KV == 0, "num_heads must be a multiple of kv_num_heads");
     auto* q = val(g, n, 0);
     REQUIRE(q && q->has_shape && q->dims.size() == 3, "query must be rank 3");
-    REQUIRE(is_half(q->dtype), "fp16/bf16 GroupQueryAttention only");
+    REQUIRE(is_float(q->dtype), "GroupQueryAttention must be fp32, fp16 or bf16");
     const bool packed = !n.has_input(1) && !n.has_input(2);
     REQUIRE(packed || (n.has_input(1) && n.has_input(2)), "key and value must both be given");
     REQUIRE(n.has_input(3) == n.has_input(4), "past_key and past_value must both be given");
     // Head size from the query width (attention.rs:1667-1683 for the packed form):
-    // the kernels take 64 or 128, so anything else is declined here rather than
-    // failing at Compute with no CPU fallback.
+    // the fused kernels take 64 or 128 and the generic ones multiples of 16 up to
+    // 256, so anything else is declined here rather than failing at Compute with no
+    // CPU fallback.
     REQUIRE(q->dims[2] > 0, "query hidden size must be known");
     const int64_t qheads = packed ? H + 2 * KV : H;
     REQUIRE(q->dims[2] % qheads == 0,
             packed ? "packed QKV hidden size must be divisible by total heads"
                    : "query hidden size must be divisible by num_heads");
     const int64_t qhd = q->dims[2] / qheads;
-    REQUIRE(qhd == 64 || qhd == 128, "head_size must be 64 or 128");
+    REQUIRE(qhd % 16 == 0 && qhd <= 256, "head_size must be a multiple of 16 up to 256");
     if (!packed) {
         auto* k = val(g, n, 1);
         REQUIRE(k && k->has_shape && k->dims.size() == 3 && k->dims[2] == KV * qhd,
@@ -321,16 +323,47 @@ std::string claim_gqa(const NodeDesc& n, const GraphIR& g) {
     // parity target); the reference defaults it to 1 (attention.rs:1547).
     const bool rotary = n.attr_int("do_rotary", 0) != 0;
     REQUIRE(!rotary || (n.has_input(7) && n.has_input(8)), "do_rotary needs cos/sin caches");
-    REQUIRE(!n.has_input(9), "custom position_ids are not supported");
-    REQUIRE(!n.has_input(10), "attention_bias is not supported");
+    // Every float input shares the output dtype (attention.rs:1583-1615).
+    std::vector<size_t> floats = {0, 1, 2, 3, 4};
+    if (rotary) floats.insert(floats.end(), {7, 8});
+    floats.insert(floats.end(), {10, 14, 15});
+    for (size_t i : floats) {
+        if (!n.has_input(i)) continue;
+        auto* t = val(g, n, (int)i);
+        REQUIRE(t && t->dtype == q->dtype, "GroupQueryAttention float inputs must share one dtype");
+    }
+    // position_ids only feed the in-op rotary, which is off when do_rotary = 0
+    // (attention.rs:1700-1703).
+    REQUIRE(!n.has_input(9) || !rotary, "custom position_ids with in-op rotary are not supported");
+    if (n.has_input(10)) {  // attention_bias: additive [B or 1, H or 1, S, total] mask
+        auto* b = val(g, n, 10);
+        REQUIRE(b && b->has_shape && b->dims.size() == 4, "attention_bias must have rank 4");
+        REQUIRE(b->dims[1] <= 0 || b->dims[1] == 1 || b->dims[1] == H,
+                "attention_bias heads must be 1 or num_heads");
+    }
     REQUIRE(!n.has_input(11), "head_sink is not supported");
-    for (size_t i = 12; i < n.inputs.size(); ++i)
-        REQUIRE(!n.has_input(i), "GroupQueryAttention extension inputs are not supported");
-    REQUIRE(n.attr_int("local_window_size", -1) == -1, "sliding window is not supported");
+    REQUIRE(!n.has_input(12) && !n.has_input(13), "quantized KV cache scales are not supported");
+    REQUIRE(n.attr_str("k_quant_type", "NONE") == "NONE" &&
+                n.attr_str("v_quant_type", "NONE") == "NONE",
+            "quantized KV cache is not supported");
+    REQUIRE(n.has_input(14) == n.has_input(15),
+            "q_norm_weight and k_norm_weight must be provided together");
+    for (size_t i : {14, 15})
+        if (n.has_input(i)) {
+            auto* w = val(g, n, (int)i);
+            REQUIRE(w && w->has_shape && w->dims.size() == 1 && w->dims[0] == qhd,
+                    "Q/K norm weights must have shape [head_size]");
+        }
+    // The ring-buffer sliding-window cache (attention.rs:725-880) is not built. A
+    // local_window_size without it is carried by attention_bias in the reference's
+    // Gemma3n form (attention.rs:256-262); without a bias the reference ignores the
+    // window while ORT applies it, so that form is declined.
+    REQUIRE(n.attr_int("sliding_window_cache", 0) == 0, "sliding_window_cache is not supported");
+    REQUIRE(n.attr_int("local_window_size", -1) == -1 || n.has_input(10),
+            "local_window_size without attention_bias is not supported");
     REQUIRE(n.attr_float("softcap", 0.f) == 0.f, "softcap is not supported");
     REQUIRE(n.attr_int("smooth_softmax", 0) == 0, "smooth_softmax is not supported");
     REQUIRE(n.attr_int("qk_output", 0) == 0, "qk_output is not supported");
-    for (size_t i = 1; i < n.outputs.size() && i < 3; ++i) (void)i;
     REQUIRE(n.outputs.size() <= 3 || n.outputs[3].empty(), "qk output is not supported");
     return "";
 }

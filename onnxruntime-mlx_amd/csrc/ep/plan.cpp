@@ -114,6 +114,7 @@ Plan::Plan(GraphIR sub, std::vector<std::string> inputs, std::vector<std::string
 }
 
 void Plan::match_decode_program() {
+    const auto reject = [this](const char* why) { dprog_reject_ = why; };
     const char* env = std::getenv("ORTMI_EP_PROGRAM");
     dprog_required_ = env && std::strcmp(env, "require") == 0;
     if (env && std::strcmp(env, "0") == 0) {
@@ -158,14 +159,15 @@ void Plan::match_decode_program() {
     const NodeDesc* gat = nullptr;
     for (const auto& n : nodes)
         if (n.op == "Gather" && n.domain.empty()) {
-            if (gat) { dprog_reject_ = "more than one Gather"; return; }
+            if (gat) return reject("more than one Gather");
             gat = &n;
         }
-    if (!gat || gat->inputs.size() < 2 || gat->attr_int("axis", 0) != 0 || gat->outputs.empty()) { dprog_reject_ = "no embedding Gather"; return; }
+    if (!gat || gat->inputs.size() < 2 || gat->attr_int("axis", 0) != 0 || gat->outputs.empty())
+        return reject("no embedding Gather");
     const ValueDesc* emb = cst(gat->inputs[0]);
     if (!emb || emb->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16 || emb->dims.size() != 2 ||
         !in_list(inputs_, gat->inputs[1]))
-        { dprog_reject_ = "embedding is not an fp16 [V, D] constant gathered by a node input"; return; }
+        return reject("embedding is not an fp16 [V, D] constant gathered by a node input");
     const int64_t D = emb->dims[1];
     auto dp = std::make_unique<DecodeProgram>();
     dp->ids = gat->inputs[1];
@@ -176,11 +178,14 @@ void Plan::match_decode_program() {
     float scale = 0.f;
     for (int l = 0;; ++l) {
         const NodeDesc* q = reader(x, "MatMulNBits", true);
-        if (!q || q->inputs.size() < 8 || q->outputs.empty()) { dprog_reject_ = "no norm prologue MatMulNBits reads the layer input"; return; }
-        if (l == 0 ? q->has_input(6) : q->inputs[6] != res) { dprog_reject_ = "the norm's skip input is not the residual stream"; return; }
+        if (!q || q->inputs.size() < 8 || q->outputs.empty())
+            return reject("no norm prologue MatMulNBits reads the layer input");
+        if (l == 0 ? q->has_input(6) : q->inputs[6] != res)
+            return reject("the norm's skip input is not the residual stream");
         const NodeDesc* g = reader(q->outputs[0], "GroupQueryAttention", false);
         if (!g) {  // the lm_head: its output is the fused node's logits
-            if (l == 0 || !in_list(outputs_, q->outputs[0]) || !mnb(q, D, -1)) { dprog_reject_ = "lm_head form"; return; }
+            if (l == 0 || !in_list(outputs_, q->outputs[0]) || !mnb(q, D, -1))
+                return reject("lm_head form");
             dp->logits = q->outputs[0];
             dp->lm_B = q->inputs[1];
             dp->lm_S = q->inputs[2];
@@ -198,16 +203,25 @@ void Plan::match_decode_program() {
             }
             res = q->outputs[1];
         }
-        if (g->inputs.size() < 9 || g->has_input(1) || g->has_input(2) || g->outputs.size() < 3) { dprog_reject_ = "GroupQueryAttention is not packed with 9 inputs"; return; }
-        if (g->attr_int("do_rotary", 0) != 1 || g->attr_int("rotary_interleaved", 0) != 0) { dprog_reject_ = "GroupQueryAttention rotary form"; return; }
+        bool extra = false;  // position_ids, attention_bias, QK-norm, ...
+        for (size_t i = 9; i < g->inputs.size(); ++i) extra = extra || g->has_input(i);
+        if (g->inputs.size() < 9 || g->has_input(1) || g->has_input(2) ||
+            g->outputs.size() < 3 || extra) {
+            dprog_reject_ = "GroupQueryAttention is not the packed 9-input form";
+            return;
+        }
+        if (g->attr_int("do_rotary", 0) != 1 || g->attr_int("rotary_interleaved", 0) != 0) {
+            dprog_reject_ = "GroupQueryAttention rotary form";
+            return;
+        }
         if (!in_list(inputs_, g->inputs[3]) || !in_list(inputs_, g->inputs[4]) ||
             !in_list(outputs_, g->outputs[1]) || !in_list(outputs_, g->outputs[2]))
-            { dprog_reject_ = "KV caches are not node inputs and outputs"; return; }
+            return reject("KV caches are not node inputs and outputs");
         const ValueDesc* cs = cst(g->inputs[7]);
         const ValueDesc* sn = cst(g->inputs[8]);
         if (!cs || !sn || cs->dims.size() != 2 || sn->dims != cs->dims ||
             cs->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16)
-            { dprog_reject_ = "cos/sin caches"; return; }
+            return reject("cos/sin caches");
         if (l == 0) {
             H = g->attr_int("num_heads", 0);
             KV = g->attr_int("kv_num_heads", 0);
@@ -217,7 +231,8 @@ void Plan::match_decode_program() {
             dp->sin = g->inputs[8];
             max_pos = cs->dims[0];
             half = cs->dims[1];
-            if (H <= 0 || KV <= 0 || q->attr_int("N", 0) % (H + 2 * KV)) { dprog_reject_ = "head counts"; return; }
+            if (H <= 0 || KV <= 0 || q->attr_int("N", 0) % (H + 2 * KV))
+                return reject("head counts");
             hd = q->attr_int("N", 0) / (H + 2 * KV);
         } else if (g->attr_int("num_heads", 0) != H || g->attr_int("kv_num_heads", 0) != KV ||
                    g->attr_float("scale", 0.f) != scale || g->inputs[6] != dp->total ||
@@ -225,18 +240,18 @@ void Plan::match_decode_program() {
             dprog_reject_ = "layers differ in attention attributes";
             return;
         }
-        if (!mnb(q, D, (H + 2 * KV) * hd)) { dprog_reject_ = "QKV projection form"; return; }
+        if (!mnb(q, D, (H + 2 * KV) * hd)) return reject("QKV projection form");
         const NodeDesc* o = reader(g->outputs[0], "MatMulNBits", false);
-        if (!mnb(o, H * hd, D) || o->outputs.empty()) { dprog_reject_ = "o_proj form"; return; }
+        if (!mnb(o, H * hd, D) || o->outputs.empty()) return reject("o_proj form");
         const NodeDesc* gu = reader(o->outputs[0], "MatMulNBitsSwiGLU", true);
         if (!gu || gu->inputs.size() < 8 || gu->inputs[6] != res || gu->outputs.size() < 2 ||
             gu->outputs[1].empty() || !mnb(gu, D, -1))
-            { dprog_reject_ = "gate/up form"; return; }
+            return reject("gate/up form");
         const int64_t Il = gu->attr_int("N", 0) / 2;
         if (l == 0) I = Il;
-        if (Il != I) { dprog_reject_ = "intermediate sizes differ"; return; }
+        if (Il != I) return reject("intermediate sizes differ");
         const NodeDesc* dn = reader(gu->outputs[0], "MatMulNBits", false);
-        if (!mnb(dn, I, D) || dn->outputs.empty()) { dprog_reject_ = "down form"; return; }
+        if (!mnb(dn, I, D) || dn->outputs.empty()) return reject("down form");
         DecodeProgram::Layer L;
         L.qkv_B = q->inputs[1];
         L.qkv_S = q->inputs[2];
@@ -256,17 +271,20 @@ void Plan::match_decode_program() {
         L.present_v = g->outputs[2];
         for (const std::string* gm : {&L.g1, &L.g2}) {
             const ValueDesc* gv = cst(*gm);
-            if (!gv || gv->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16) { dprog_reject_ = "gamma dtype"; return; }
+            if (!gv || gv->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16)
+                return reject("gamma dtype");
         }
         dp->layers.push_back(L);
         x = dn->outputs[0];
         res = gu->outputs[1];
     }
     // Every node of the fused node is part of the program, and it has no other outputs.
-    if (nodes.size() != 2 + 5 * dp->layers.size()) { dprog_reject_ = "extra nodes in the fused node"; return; }
-    if (outputs_.size() != 1 + 2 * dp->layers.size()) { dprog_reject_ = "extra outputs of the fused node"; return; }
+    if (nodes.size() != 2 + 5 * dp->layers.size()) return reject("extra nodes in the fused node");
+    if (outputs_.size() != 1 + 2 * dp->layers.size())
+        return reject("extra outputs of the fused node");
     const ValueDesc* gf = cst(dp->gf);
-    if (!gf || gf->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16) { dprog_reject_ = "final gamma dtype"; return; }
+    if (!gf || gf->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16)
+        return reject("final gamma dtype");
     OrtmiDecoderDims& d = dp->dims;
     d.layers = (int32_t)dp->layers.size();
     d.hidden = (int32_t)D;
@@ -866,6 +884,32 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         }
         const float scale = n.attr_float("scale", 0.f);
         const int32_t inter = (int32_t)n.attr_int("rotary_interleaved", 0);
+        // fp32, attention_bias, QK-norm and head sizes other than 64/128 run the
+        // generic kernels (one prep launch, one attention launch).
+        Tensor* bias = in(10);
+        Tensor* qnw = in(14);
+        Tensor* knw = in(15);
+        if (q.dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT || bias || qnw || knw ||
+            (hd != 64 && hd != 128)) {
+            if (capturing_) fail("GroupQueryAttention form is not capturable");
+            capturable_ = false;
+            int64_t bd[4] = {0, 0, 0, 0};
+            if (bias) {
+                if (bias->dims.size() != 4)
+                    fail("GroupQueryAttention: attention_bias must be rank 4");
+                for (int i = 0; i < 4; ++i) bd[i] = bias->dims[i];
+            }
+            const size_t wsb = ortmi_group_query_attention_ex_workspace_size(B, S, H, hd);
+            void* ws = workspace(wsb);
+            check_kernel(ortmi_group_query_attention_ex(
+                             q.ptr, kptr, vptr, pkp, pvp, cap, total, csp, snp, half, max_pos,
+                             qnw ? qnw->ptr : nullptr, knw ? knw->ptr : nullptr,
+                             n.attr_float("qk_norm_epsilon", 1e-6f), bias ? bias->ptr : nullptr,
+                             bd[0], bd[1], bd[2], bd[3], optr, prk, prv, B, S, H, KV, hd, scale,
+                             inter, kdt(q.dtype), ws, wsb, st),
+                         "GroupQueryAttention");
+            return;
+        }
         // One-token decode into a shared buffer written in place: the capturable
         // kernels read total_sequence_length from device memory, so the step can
         // be replayed from a graph. Eager runs take the same kernels, so replayed

@@ -121,7 +121,9 @@ def gqa_contract(total_sequence_length: int, seq_len: int, past_cap: int):
 def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
                           total_sequence_length, cos_cache=None, sin_cache=None, *, num_heads,
                           kv_num_heads, scale=0.0, do_rotary=0, rotary_interleaved=0,
-                          present_key=None, present_value=None, stream=None):
+                          present_key=None, present_value=None, attention_bias=None,
+                          q_norm_weight=None, k_norm_weight=None, qk_norm_epsilon=1e-6,
+                          stream=None):
     """com.microsoft GroupQueryAttention (decode and prefill, in-op RoPE).
 
     Follows group_query_attention_op (rust/src/ops/attention.rs:556-952): one
@@ -129,7 +131,11 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
     consulted, attention.rs:642-651); shared-buffer contract when the past buffer
     is longer than valid_past, growing contract otherwise. Pass
     present_key=past_key / present_value=past_value to update a shared buffer in
-    place. Returns (output, present_key, present_value).
+    place. attention_bias (input 10, rank 4 [B or 1, H or 1, >= S, >= total]) is
+    added to the scaled scores; q_norm_weight / k_norm_weight (inputs 14/15, [head])
+    RMS-normalise q and k per head before RoPE (attention.rs:663-670). fp32 tensors,
+    those inputs and head sizes other than 64/128 run the generic kernels
+    (ortmi_group_query_attention_ex). Returns (output, present_key, present_value).
     """
     del seqlens_k  # not consulted outside sliding-window mode, as in the reference
     total = int(total_sequence_length)
@@ -151,14 +157,34 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
         raise ValueError("GroupQueryAttention: present_key has the wrong shape for the contract")
     out = torch.empty((B, S, num_heads * hd), dtype=query.dtype, device=query.device)
     lib = load_kernels()
-    ws_bytes = lib.ortmi_group_query_attention_workspace_size(B, S, num_heads, hd, vp + S)
-    ws = _workspace(ws_bytes, query.device)
     use_rope = bool(do_rotary) and cos_cache is not None
     half = cos_cache.shape[1] if use_rope else 0
     max_pos = cos_cache.shape[0] if use_rope else 0
+    rope = (_p(cos_cache) if use_rope else None, _p(sin_cache) if use_rope else None, half,
+            max_pos)
+    generic = (query.dtype == torch.float32 or attention_bias is not None
+               or q_norm_weight is not None or k_norm_weight is not None or hd not in (64, 128))
+    if generic:
+        ws = _workspace(lib.ortmi_group_query_attention_ex_workspace_size(B, S, num_heads, hd),
+                        query.device)
+        bdims = (0, 0, 0, 0)
+        if attention_bias is not None:
+            if attention_bias.dim() != 4 or attention_bias.dtype != query.dtype:
+                raise ValueError("GroupQueryAttention: attention_bias must be rank 4 in the "
+                                 "output dtype")
+            attention_bias = attention_bias.contiguous()
+            bdims = tuple(attention_bias.shape)
+        check(lib.ortmi_group_query_attention_ex(
+            _p(query), _p(key), _p(value), _p(past_key), _p(past_value), cap, total, *rope,
+            _p(q_norm_weight), _p(k_norm_weight), float(qk_norm_epsilon), _p(attention_bias),
+            *bdims, _p(out), _p(present_key), _p(present_value), B, S, num_heads, kv_num_heads,
+            hd, float(scale), int(rotary_interleaved), _dt(query), _p(ws), ws.numel(),
+            _stream(stream)))
+        return out, present_key, present_value
+    ws_bytes = lib.ortmi_group_query_attention_workspace_size(B, S, num_heads, hd, vp + S)
+    ws = _workspace(ws_bytes, query.device)
     check(lib.ortmi_group_query_attention(
-        _p(query), _p(key), _p(value), _p(past_key), _p(past_value), cap, total,
-        _p(cos_cache) if use_rope else None, _p(sin_cache) if use_rope else None, half, max_pos,
+        _p(query), _p(key), _p(value), _p(past_key), _p(past_value), cap, total, *rope,
         _p(out), _p(present_key), _p(present_value), B, S, num_heads, kv_num_heads, hd,
         float(scale), int(rotary_interleaved), _dt(query), _p(ws), ws.numel(), _stream(stream)))
     return out, present_key, present_value

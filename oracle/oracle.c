@@ -63,7 +63,20 @@ void orc_f32_to_f16_n(const float* src, uint16_t* dst, int64_t n) {
     for (int64_t i = 0; i < n; ++i) dst[i] = orc_f32_to_f16(src[i]);
 }
 
+/* Round-to-nearest-even to bfloat16 (the top 16 bits of the binary32 pattern). */
+static inline float rbf16(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    if ((u & 0x7F800000u) == 0x7F800000u) return v;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    u &= 0xFFFF0000u;
+    memcpy(&v, &u, 4);
+    return v;
+}
+
+/* round16: 0 keeps fp32, 1 rounds to fp16, 2 rounds to bf16. */
 static inline float r16(float v, int round16) {
+    if (round16 == 2) return rbf16(v);
     return round16 ? orc_f16_to_f32(orc_f32_to_f16(v)) : v;
 }
 
@@ -193,7 +206,7 @@ void orc_rotary(const float* x, float* y, int B, int S, int NH, int hd, int64_t 
  * denominator (attention.rs:2423-2452; test_paged_attention.py:130-134). */
 static void attend_row(const float* qv, int hd, const float* const* krows,
                        const float* const* vrows, int nk, int vhd, int last, double scale,
-                       const float* sink, double* scores, float* out) {
+                       const float* sink, const float* bias, double* scores, float* out) {
     double mx = -INFINITY;
     for (int j = 0; j < nk; ++j) {
         if (j > last) {
@@ -202,13 +215,13 @@ static void attend_row(const float* qv, int hd, const float* const* krows,
         }
         double acc = 0.0;
         for (int d = 0; d < hd; ++d) acc += (double)qv[d] * (double)krows[j][d];
-        scores[j] = acc * scale;
+        scores[j] = acc * scale + (bias ? (double)bias[j] : 0.0);
         if (scores[j] > mx) mx = scores[j];
     }
     if (sink && (double)*sink > mx) mx = *sink;
     double denom = 0.0;
     for (int j = 0; j < nk; ++j) {
-        scores[j] = (j > last) ? 0.0 : exp(scores[j] - mx);
+        scores[j] = (j > last || scores[j] == -INFINITY) ? 0.0 : exp(scores[j] - mx);
         denom += scores[j];
     }
     if (sink) denom += exp((double)*sink - mx);
@@ -228,6 +241,15 @@ static void attend_row(const float* qv, int hd, const float* const* krows,
 
 /* ---------------------------------------------------------------- GQA --- */
 
+/* RMS-normalise one head vector with per-dimension weights (QK-norm). */
+static void rms_vec(const float* x, float* y, int d, const float* w, float eps, int round16) {
+    double ss = 0.0;
+    for (int i = 0; i < d; ++i) ss += (double)x[i] * (double)x[i];
+    double inv = 1.0 / sqrt(ss / d + (double)eps);
+    for (int i = 0; i < d; ++i) y[i] = r16((float)((double)x[i] * inv * (double)w[i]), round16);
+}
+
+
 int orc_gqa_contract(int total_seq_len, int S, int64_t cap, int* valid_past, int64_t* pcap) {
     /* attention.rs:636-651 */
     int vp = total_seq_len - S;
@@ -243,10 +265,12 @@ int orc_gqa_contract(int total_seq_len, int S, int64_t cap, int* valid_past, int
     return shared;
 }
 
-int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
-            const float* past_v, int64_t cap, int total_seq_len, const float* cos_c,
-            const float* sin_c, int half, int interleaved, int B, int S, int H, int KV, int hd,
-            float scale, int round16, float* out, float* present_k, float* present_v) {
+int orc_gqa_ex(const float* q, const float* k, const float* v, const float* past_k,
+               const float* past_v, int64_t cap, int total_seq_len, const float* cos_c,
+               const float* sin_c, int half, int interleaved, int B, int S, int H, int KV, int hd,
+               float scale, int round16, const float* q_norm_w, const float* k_norm_w,
+               float qk_eps, const float* bias, int64_t bias_sb, int64_t bias_sh,
+               int64_t bias_ss, float* out, float* present_k, float* present_v) {
     if (H <= 0 || KV <= 0 || H % KV || hd <= 0 || hd > 512 || S <= 0) return -1;
     if (cos_c && 2 * half > hd) return -1;
     int vp;
@@ -282,6 +306,11 @@ int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
             const float* vrow_p = vbase + ((int64_t)b * S + s) * krow;
             for (int h = 0; h < KV; ++h) {
                 const float* kin = krow_p + (int64_t)h * hd;
+                /* QK-norm, then RoPE (attention.rs:663-708). */
+                if (k_norm_w) {
+                    rms_vec(kin, qr, hd, k_norm_w, qk_eps, round16);
+                    kin = qr;
+                }
                 if (cos_c) {
                     int64_t pos = vp + s;
                     rope_vec(kin, kr, hd, cos_c + pos * half, sin_c + pos * half, half,
@@ -303,6 +332,7 @@ int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
 #pragma omp parallel
     {
         float* qrt = (float*)malloc(sizeof(float) * (size_t)hd);
+        float* qnt = (float*)malloc(sizeof(float) * (size_t)hd);
         double* sbuf = (double*)malloc(sizeof(double) * (size_t)(pcap + 1));
         const float** kpt = (const float**)malloc(sizeof(float*) * (size_t)(pcap + 1));
         const float** vpt = (const float**)malloc(sizeof(float*) * (size_t)(pcap + 1));
@@ -312,6 +342,10 @@ int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
             const int s = (int)((row / H) % S);
             const int b = (int)(row / ((int64_t)H * S));
             const float* qin = q + ((int64_t)b * S + s) * qrow + (int64_t)h * hd;
+            if (q_norm_w) {
+                rms_vec(qin, qnt, hd, q_norm_w, qk_eps, round16);
+                qin = qnt;
+            }
             if (cos_c) {
                 int64_t pos = vp + s;
                 rope_vec(qin, qrt, hd, cos_c + pos * half, sin_c + pos * half, half,
@@ -325,9 +359,13 @@ int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
                 vpt[j] = present_v + (((int64_t)b * KV + kvh) * pcap + j) * hd;
             }
             float* o = out + ((int64_t)b * S + s) * (int64_t)H * hd + (int64_t)h * hd;
-            attend_row(qrt, hd, kpt, vpt, nk, hd, vp + s, sc, NULL, sbuf, o);
+            /* attention_bias (input 10): an additive mask row over the key
+             * positions (attention.rs:1593-1640), broadcast over batch/heads. */
+            const float* brow = bias ? bias + b * bias_sb + h * bias_sh + s * bias_ss : NULL;
+            attend_row(qrt, hd, kpt, vpt, nk, hd, vp + s, sc, NULL, brow, sbuf, o);
         }
         free(qrt);
+        free(qnt);
         free(sbuf);
         free(kpt);
         free(vpt);
@@ -338,14 +376,17 @@ int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
     return shared;
 }
 
+int orc_gqa(const float* q, const float* k, const float* v, const float* past_k,
+            const float* past_v, int64_t cap, int total_seq_len, const float* cos_c,
+            const float* sin_c, int half, int interleaved, int B, int S, int H, int KV, int hd,
+            float scale, int round16, float* out, float* present_k, float* present_v) {
+    return orc_gqa_ex(q, k, v, past_k, past_v, cap, total_seq_len, cos_c, sin_c, half,
+                      interleaved, B, S, H, KV, hd, scale, round16, NULL, NULL, 0.f, NULL, 0, 0, 0,
+                      out, present_k, present_v);
+}
+
 /* ------------------------------------------------------ PagedAttention --- */
 
-static void rms_vec(const float* x, float* y, int d, const float* w, float eps, int round16) {
-    double ss = 0.0;
-    for (int i = 0; i < d; ++i) ss += (double)x[i] * (double)x[i];
-    double inv = 1.0 / sqrt(ss / d + (double)eps);
-    for (int i = 0; i < d; ++i) y[i] = r16((float)((double)x[i] * inv * (double)w[i]), round16);
-}
 
 int orc_paged_attention(const float* q, const float* k, const float* v, float* kcache,
                         float* vcache, int64_t nblk, int blk, const int32_t* cum,
@@ -448,8 +489,8 @@ int orc_paged_attention(const float* q, const float* k, const float* v, float* k
                     const float* qv = qn + t * (int64_t)H * hd + (int64_t)h * hd;
                     float* o = out + t * (int64_t)H * vhd + (int64_t)h * vhd;
                     attend_row(qv, hd, kpa + (int64_t)kvh * total, vpa + (int64_t)kvh * total,
-                               total, vhd, pastb + i, sc, head_sink ? head_sink + h : NULL, sbuf,
-                               o);
+                               total, vhd, pastb + i, sc, head_sink ? head_sink + h : NULL, NULL,
+                               sbuf, o);
                 }
             free(sbuf);
         }

@@ -80,6 +80,23 @@ int orc_gqa(const float* q, const float* k, const float* v,
             const float* cos_c, const float* sin_c, int half, int interleaved,
             int B, int S, int H, int KV, int hd, float scale, int round16,
             float* out, float* present_k, float* present_v);
+/*
+ * orc_gqa plus the optional GroupQueryAttention inputs the reference accepts
+ * (rust/src/ops/attention.rs:1520-1720):
+ *  - q_norm_w/k_norm_w [hd] (inputs 14/15): per-head RMS norm with qk_eps applied to
+ *    q and to the new k before RoPE (attention.rs:663-670);
+ *  - bias (input 10): additive scores mask; the row for (batch b, head h, query s)
+ *    starts at bias + b*bias_sb + h*bias_sh + s*bias_ss and is indexed by key
+ *    position; it is added to scale*q.k and the causal mask still applies
+ *    (attention.rs:256-285). Broadcast dimensions carry stride 0.
+ * round16 = 2 rounds to bf16 where 1 rounds to fp16.
+ */
+int orc_gqa_ex(const float* q, const float* k, const float* v, const float* past_k,
+               const float* past_v, int64_t cap, int total_seq_len, const float* cos_c,
+               const float* sin_c, int half, int interleaved, int B, int S, int H, int KV, int hd,
+               float scale, int round16, const float* q_norm_w, const float* k_norm_w,
+               float qk_eps, const float* bias, int64_t bias_sb, int64_t bias_sh,
+               int64_t bias_ss, float* out, float* present_k, float* present_v);
 
 /*
  * PagedAttention per rust/src/ops/attention.rs:2495-2744, with RoPE read straight

@@ -61,6 +61,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_gqa_contract.argtypes = [_int, _int, _i64, _i32p, _i64p]
     L.orc_gqa.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _int, _f32p, _f32p, _int,
                           _int, _int, _int, _int, _int, _int, _flt, _int, _f32p, _f32p, _f32p]
+    L.orc_gqa_ex.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _int, _f32p, _f32p,
+                             _int, _int, _int, _int, _int, _int, _int, _flt, _int, _f32p, _f32p,
+                             _flt, _f32p, _i64, _i64, _i64, _f32p, _f32p, _f32p]
     L.orc_paged_attention.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _int, _i32p,
                                       _i32p, _i32p, _int, _int, _f32p, _f32p, _int, _int, _int,
                                       _i32p, _f32p, _f32p, _f32p, _flt, _int, _int, _int, _int,
@@ -197,8 +200,13 @@ def gqa_contract(total_seq_len: int, S: int, cap: int):
 
 
 def gqa(q, k, v, past_k, past_v, total_seq_len, num_heads, kv_heads, cos=None, sin=None,
-        interleaved=False, scale=0.0, round16=False):
-    """GroupQueryAttention; returns (out [B,S,H*hd] f32, present_k, present_v, shared)."""
+        interleaved=False, scale=0.0, round16=False, q_norm=None, k_norm=None, qk_eps=1e-6,
+        bias=None):
+    """GroupQueryAttention; returns (out [B,S,H*hd] f32, present_k, present_v, shared).
+
+    q_norm/k_norm: [hd] QK-norm weights; bias: additive mask of rank 4
+    [B or 1, H or 1, >= S, >= total] indexed by key position. round16: False/1 = fp16
+    rounding when true, 2 = bf16 rounding."""
     q = _f32(q)
     B, S, _ = q.shape
     past_k, past_v = _f32(past_k), _f32(past_v)
@@ -210,10 +218,22 @@ def gqa(q, k, v, past_k, past_v, total_seq_len, num_heads, kv_heads, cos=None, s
     pv = np.zeros((B, KV, pcap, hd), np.float32)
     cos, sin = _f32(cos), _f32(sin)
     half = 0 if cos is None else cos.shape[-1]
-    rc = lib().orc_gqa(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p), _p(past_k, _f32p),
-                       _p(past_v, _f32p), cap, total_seq_len, _p(cos, _f32p), _p(sin, _f32p),
-                       half, int(interleaved), B, S, num_heads, KV, hd, scale, int(round16),
-                       _p(out, _f32p), _p(pk, _f32p), _p(pv, _f32p))
+    sb = sh = ss = 0
+    if bias is not None:
+        bias = _f32(bias)
+        if bias.ndim != 4 or bias.shape[0] not in (1, B) or bias.shape[1] not in (1, num_heads) \
+                or bias.shape[2] < S or bias.shape[3] < vp + S:
+            raise ValueError(f"oracle: attention_bias shape {bias.shape} does not cover "
+                             f"[{B}, {num_heads}, {S}, {vp + S}]")
+        sb = bias.strides[0] // 4 if bias.shape[0] > 1 else 0
+        sh = bias.strides[1] // 4 if bias.shape[1] > 1 else 0
+        ss = bias.strides[2] // 4
+    rc = lib().orc_gqa_ex(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p), _p(past_k, _f32p),
+                          _p(past_v, _f32p), cap, total_seq_len, _p(cos, _f32p), _p(sin, _f32p),
+                          half, int(interleaved), B, S, num_heads, KV, hd, scale, int(round16),
+                          _p(_f32(q_norm), _f32p), _p(_f32(k_norm), _f32p), qk_eps,
+                          _p(bias, _f32p), sb, sh, ss, _p(out, _f32p), _p(pk, _f32p),
+                          _p(pv, _f32p))
     if rc < 0:
         raise ValueError("oracle: bad GroupQueryAttention arguments")
     return out, pk, pv, shared

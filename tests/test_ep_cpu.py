@@ -166,42 +166,79 @@ def test_gather_block_quantized_claim_predicate(kw, claimed):
     assert session(gbq_graph(**kw)).claimed(0) is claimed
 
 
-def gqa_graph(hd=64, extra=None, inputs_extra=()):
+def gqa_graph(hd=64, extra=None, inputs_extra=(), dtype=F16, at=None):
+    """One GroupQueryAttention node (decode, in-op RoPE). inputs_extra are appended
+    after sin (from input 9); `at` maps an input index >= 9 to (name, dtype, dims)."""
     g = hx.Graph()
     H, KV, cap = 4, 2, 32
-    g.value("q", F16, [1, 1, H * hd])
-    g.value("k", F16, [1, 1, KV * hd])
-    g.value("v", F16, [1, 1, KV * hd])
-    g.value("pk", F16, [1, KV, cap, hd])
-    g.value("pv", F16, [1, KV, cap, hd])
+    npdt = np.float16 if dtype == F16 else np.float32
+    g.value("q", dtype, [1, 1, H * hd])
+    g.value("k", dtype, [1, 1, KV * hd])
+    g.value("v", dtype, [1, 1, KV * hd])
+    g.value("pk", dtype, [1, KV, cap, hd])
+    g.value("pv", dtype, [1, KV, cap, hd])
     g.value("sl", I32, [1])
     g.value("tot", I32, [1])
-    g.initializer("cos", np.ones((64, hd // 2), np.float16))
-    g.initializer("sin", np.zeros((64, hd // 2), np.float16))
+    g.initializer("cos", np.ones((64, hd // 2), npdt))
+    g.initializer("sin", np.zeros((64, hd // 2), npdt))
     for name, dt, dims in inputs_extra:
         g.value(name, dt, dims)
-    g.value("o", F16, [1, 1, H * hd])
-    g.value("ok", F16, [1, KV, cap, hd])
-    g.value("ov", F16, [1, KV, cap, hd])
+    g.value("o", dtype, [1, 1, H * hd])
+    g.value("ok", dtype, [1, KV, cap, hd])
+    g.value("ov", dtype, [1, KV, cap, hd])
     ins = ["q", "k", "v", "pk", "pv", "sl", "tot", "cos", "sin"] + [n for n, _, _ in inputs_extra]
+    for i, (name, dt, dims) in sorted((at or {}).items()):
+        g.value(name, dt, dims)
+        ins += [""] * (i - len(ins)) + [name]
     attrs = dict(num_heads=H, kv_num_heads=KV, do_rotary=1)
     attrs.update(extra or {})
     g.node("GroupQueryAttention", ins, ["o", "ok", "ov"], domain="com.microsoft", **attrs)
-    g.io([n for n in ins if n not in ("cos", "sin")], ["o", "ok", "ov"])
+    g.io([n for n in ins if n and n not in ("cos", "sin")], ["o", "ok", "ov"])
     return g
 
 
 @pytest.mark.parametrize("hd,extra,ins,claimed", [
     (128, None, (), True),
     (64, None, (), True),
-    (96, None, (), False),                                  # head size without a kernel
+    (96, None, (), True),                                   # generic kernels: multiples of 16
+    (72, None, (), False),                                  # head size without a kernel
     (128, dict(softcap=30.0), (), False),
-    (128, dict(local_window_size=128), (), False),
+    (128, dict(local_window_size=128), (), False),          # window with no bias to carry it
+    (128, dict(sliding_window_cache=1, local_window_size=16), (), False),
+    (128, dict(smooth_softmax=1), (), False),
     (128, dict(kv_num_heads=3), (), False),                 # 4 % 3 != 0
-    (128, None, (("pos", I64, [1, 1]),), False),            # position_ids
+    (128, None, (("pos", I64, [1, 1]),), False),            # position_ids with in-op rotary
+    (128, dict(do_rotary=0), (("pos", I64, [1, 1]),), True),  # ignored without it
 ])
 def test_gqa_claim_predicate(hd, extra, ins, claimed):
     assert session(gqa_graph(hd, extra, ins)).claimed(0) is claimed
+
+
+HD = 64
+
+
+@pytest.mark.parametrize("dtype,extra,at,claimed", [
+    (F32, None, {}, True),                                                     # fp32 tensors
+    (F16, None, {10: ("bias", F16, [1, 1, 1, 32])}, True),                     # attention_bias
+    (F16, None, {10: ("bias", F16, [1, 4, 1, 32])}, True),                     # per-head bias
+    (F16, None, {10: ("bias", F16, [1, 3, 1, 32])}, False),                    # 3 heads of 4
+    (F16, None, {10: ("bias", F16, [1, 32])}, False),                          # rank 2
+    (F16, None, {10: ("bias", F32, [1, 1, 1, 32])}, False),                    # dtype mismatch
+    (F16, dict(local_window_size=8), {10: ("bias", F16, [1, 1, 1, 32])}, True),  # bias carries it
+    (F16, None, {14: ("qn", F16, [HD]), 15: ("kn", F16, [HD])}, True),         # QK-norm
+    (F32, None, {14: ("qn", F32, [HD]), 15: ("kn", F32, [HD])}, True),
+    (F16, None, {14: ("qn", F16, [HD])}, False),                               # q without k
+    (F16, None, {14: ("qn", F16, [HD // 2]), 15: ("kn", F16, [HD // 2])}, False),
+    (F16, None, {11: ("sink", F16, [4])}, False),                              # head_sink
+    (F16, None, {12: ("ks", F32, [1]), 13: ("vs", F32, [1])}, False),          # quantized KV
+    (F16, dict(k_quant_type="PER_TENSOR"), {}, False),
+])
+def test_gqa_claim_optional_inputs(dtype, extra, at, claimed):
+    """The optional GroupQueryAttention inputs the reference claims
+    (rust/src/ops/attention.rs:1520-1745): attention_bias (input 10, rank 4, output
+    dtype), QK-norm weights (inputs 14/15, together, shape [head_size]), fp32; and
+    the ones it declines (head_sink, quantized KV, ...)."""
+    assert session(gqa_graph(HD, extra, (), dtype, at)).claimed(0) is claimed
 
 
 def test_unsupported_node_splits_partitions():
@@ -323,7 +360,7 @@ def test_default_memory_device_is_cpu_and_foreign_allocators_declined():
 @pytest.mark.parametrize("qwidth,packed,claimed", [
     (4 * 128, False, True),
     (4 * 128 + 8, False, False),        # query width not a multiple of num_heads
-    (4 * 96, False, False),             # head size 96 has no kernel
+    (4 * 72, False, False),             # head size 72 has no kernel
     ((4 + 2 * 2) * 64, True, True),     # packed QKV, head size 64
     ((4 + 2 * 2) * 64 + 2, True, False),
 ])

@@ -242,6 +242,114 @@ def test_gqa_head_mapping_sensitivity(oracle):
     assert not np.allclose(other, out)
 
 
+def _gqa_case(rng, B=2, S=3, H=4, KV=2, hd=16, cap=6):
+    q = rng.standard_normal((B, S, H * hd)).astype(np.float32)
+    k = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    v = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    pk = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    pv = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    return q, k, v, pk, pv
+
+
+def test_gqa_qk_norm_is_rms_norm_before_rope(oracle):
+    """QK-norm (inputs 14/15) equals normalising q and k per head with numpy first;
+    normalising after RoPE instead (weights are not rotation invariant) differs."""
+    rng = np.random.default_rng(21)
+    B, S, H, KV, hd, cap = 2, 3, 4, 2, 16, 6
+    q, k, v, pk, pv = _gqa_case(rng, B, S, H, KV, hd, cap)
+    qw = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    kw = rng.uniform(0.5, 1.5, hd).astype(np.float32)
+    cos, sin = refs.rotary_caches(32, hd)
+    out, prk, prv, _ = oracle.gqa(q, k, v, pk, pv, cap + S, H, KV, cos=cos, sin=sin,
+                                  q_norm=qw, k_norm=kw, qk_eps=1e-5)
+    qn = refs.rms_norm_ref(q.reshape(B, S, H, hd), qw, 1e-5).reshape(q.shape)
+    kn = refs.rms_norm_ref(k.reshape(B, S, KV, hd), kw, 1e-5).reshape(k.shape)
+    want, wk, wv, _ = oracle.gqa(qn, kn, v, pk, pv, cap + S, H, KV, cos=cos, sin=sin)
+    np.testing.assert_allclose(out, want, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(prk, wk, rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(prv, wv)
+    ro, rk, _ = refs.gqa_ref(qn, kn, v, pk, pv, cap + S, H, KV, cos=cos, sin=sin)
+    np.testing.assert_allclose(out, ro, rtol=1e-5, atol=1e-6)
+    # Norm after RoPE: a different result, so the order is pinned.
+    pos = np.arange(cap, cap + S)
+    qr = np.stack([refs.apply_rope(q.reshape(B, S, H, hd)[b], cos, sin, pos, False)
+                   for b in range(B)])
+    qrn = refs.rms_norm_ref(qr, qw, 1e-5)
+    qh = qn.reshape(B, S, H, hd)
+    qrot = np.stack([refs.apply_rope(qh[b], cos, sin, pos, False) for b in range(B)])
+    assert not np.allclose(qrn, qrot, atol=1e-3)
+
+
+def test_gqa_bias_zero_and_constant_rows_change_nothing(oracle):
+    rng = np.random.default_rng(22)
+    B, S, H, KV, hd, cap = 2, 3, 4, 2, 16, 6
+    q, k, v, pk, pv = _gqa_case(rng, B, S, H, KV, hd, cap)
+    total = cap + S
+    base, *_ = oracle.gqa(q, k, v, pk, pv, total, H, KV)
+    zero = np.zeros((1, 1, S, total), np.float32)
+    got, *_ = oracle.gqa(q, k, v, pk, pv, total, H, KV, bias=zero)
+    np.testing.assert_array_equal(got, base)
+    # A per-row constant shifts every score of the row alike: softmax is unchanged.
+    const = np.broadcast_to(rng.uniform(-3, 3, (B, H, S, 1)), (B, H, S, total + 2))
+    got, *_ = oracle.gqa(q, k, v, pk, pv, total, H, KV, bias=np.ascontiguousarray(const))
+    np.testing.assert_allclose(got, base, rtol=1e-5, atol=1e-6)
+
+
+def test_gqa_bias_one_hot_selects_a_value_row(oracle):
+    """A bias of -inf everywhere but key j[b,h,s] makes the softmax one-hot: the
+    output row is that key's value row (indexing by batch, head, query and key)."""
+    rng = np.random.default_rng(23)
+    B, S, H, KV, hd, cap = 2, 3, 4, 2, 16, 6
+    q, k, v, pk, pv = _gqa_case(rng, B, S, H, KV, hd, cap)
+    total = cap + S
+    bias = np.full((B, H, S, total), -np.inf, np.float32)
+    pick = np.zeros((B, H, S), np.int64)
+    for b in range(B):
+        for h in range(H):
+            for s in range(S):
+                pick[b, h, s] = rng.integers(0, cap + s + 1)  # causal: keys <= cap + s
+                bias[b, h, s, pick[b, h, s]] = 0.0
+    out, _, prv, _ = oracle.gqa(q, k, v, pk, pv, total, H, KV, bias=bias)
+    out = out.reshape(B, S, H, hd)
+    g = H // KV
+    for b in range(B):
+        for h in range(H):
+            for s in range(S):
+                want = prv[b, h // g, pick[b, h, s]]
+                np.testing.assert_allclose(out[b, s, h], want, rtol=1e-6, atol=1e-7)
+
+
+def test_gqa_bias_broadcast_equals_tiled(oracle):
+    rng = np.random.default_rng(24)
+    B, S, H, KV, hd, cap = 2, 2, 4, 2, 8, 5
+    q, k, v, pk, pv = _gqa_case(rng, B, S, H, KV, hd, cap)
+    total = cap + S
+    small = rng.standard_normal((1, 1, S, total)).astype(np.float32)
+    a, *_ = oracle.gqa(q, k, v, pk, pv, total, H, KV, bias=small)
+    b, *_ = oracle.gqa(q, k, v, pk, pv, total, H, KV,
+                       bias=np.ascontiguousarray(np.broadcast_to(small, (B, H, S, total))))
+    np.testing.assert_array_equal(a, b)
+    # A bias does change the result (it is not silently dropped).
+    base, *_ = oracle.gqa(q, k, v, pk, pv, total, H, KV)
+    assert not np.allclose(a, base, atol=1e-3)
+
+
+def test_gqa_bf16_rounding_matches_torch(oracle):
+    """round16=2 rounds the roped K rows to bfloat16 exactly as torch does (an identity
+    rotation, cos = 1 and sin = 0, leaves only the rounding)."""
+    import torch
+
+    rng = np.random.default_rng(25)
+    B, S, H, KV, hd, cap = 1, 4, 2, 1, 16, 0
+    q, k, v, pk, pv = _gqa_case(rng, B, S, H, KV, hd, cap)
+    k = k * np.float32(1 + 2.0 ** -9)  # push values off the bf16 grid, including ties
+    cos = np.ones((8, hd // 2), np.float32)
+    sin = np.zeros((8, hd // 2), np.float32)
+    _, prk, _, _ = oracle.gqa(q, k, v, pk, pv, S, H, KV, cos=cos, sin=sin, round16=2)
+    want = torch.from_numpy(k).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(prk[0].transpose(1, 0, 2).reshape(S, KV * hd), want[0])
+
+
 # ------------------------------------------------------------ PagedAttention ---
 
 
