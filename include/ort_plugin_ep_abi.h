@@ -267,6 +267,7 @@ typedef struct OrtEpFactory {
        OrtMemoryInfo** out))                                                                    \
     X(71, MemoryInfoGetName, OrtStatus*, (const OrtMemoryInfo* info, const char** out))          \
     X(72, MemoryInfoGetId, OrtStatus*, (const OrtMemoryInfo* info, int* out))                    \
+    X(78, GetAllocatorWithDefaultOptions, OrtStatus*, (OrtAllocator * *out))                     \
     X(88, KernelContext_GetInputCount, OrtStatus*, (const OrtKernelContext* ctx, size_t* out))   \
     X(89, KernelContext_GetOutputCount, OrtStatus*, (const OrtKernelContext* ctx, size_t* out))  \
     X(90, KernelContext_GetInput, OrtStatus*,                                                    \
@@ -277,6 +278,10 @@ typedef struct OrtEpFactory {
     X(93, ReleaseStatus, void, (OrtStatus * status))                                             \
     X(94, ReleaseMemoryInfo, void, (OrtMemoryInfo * info))                                       \
     X(99, ReleaseTensorTypeAndShapeInfo, void, (OrtTensorTypeAndShapeInfo * info))               \
+    X(116, ModelMetadataLookupCustomMetadataMap, OrtStatus*,                                     \
+      (const OrtModelMetadata* model_metadata, OrtAllocator* allocator, const char* key,         \
+       char** value))                                                                            \
+    X(118, ReleaseModelMetadata, void, (OrtModelMetadata * model_metadata))                      \
     X(285, GetEpApi, const OrtEpApi*, (void))                                                    \
     X(286, HardwareDevice_Type, OrtHardwareDeviceType, (const OrtHardwareDevice* device))        \
     X(301, GetTensorData, OrtStatus*, (const OrtValue* value, const void** out))                 \
@@ -301,6 +306,9 @@ typedef struct OrtEpFactory {
     X(341, Graph_GetNumNodes, OrtStatus*, (const OrtGraph* graph, size_t* out))                  \
     X(342, Graph_GetNodes, OrtStatus*, (const OrtGraph* graph, const OrtNode** nodes,            \
                                         size_t num))                                             \
+    X(343, Graph_GetParentNode, OrtStatus*, (const OrtGraph* graph, const OrtNode** node))       \
+    X(345, Graph_GetModelMetadata, OrtStatus*,                                                   \
+      (const OrtGraph* graph, OrtModelMetadata** out))                                           \
     X(348, Node_GetId, OrtStatus*, (const OrtNode* node, size_t* id))                            \
     X(349, Node_GetName, OrtStatus*, (const OrtNode* node, const char** name))                   \
     X(350, Node_GetOperatorType, OrtStatus*, (const OrtNode* node, const char** op_type))        \

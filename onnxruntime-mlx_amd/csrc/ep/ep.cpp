@@ -169,6 +169,22 @@ struct Factory {
 
 const char* ep_get_name(const OrtEp* self) { return reinterpret_cast<const Ep*>(self)->name.c_str(); }
 
+// Value of one entry of the model's custom metadata map; false when absent.
+bool read_metadata(const OrtApi* a, const OrtGraph* graph, const char* key, std::string* value) {
+    OrtModelMetadata* md = nullptr;
+    check_ort(a, api::Graph_GetModelMetadata(a)(graph, &md), "Graph_GetModelMetadata");
+    OrtAllocator* alloc = nullptr;
+    char* v = nullptr;
+    OrtStatus* st = api::GetAllocatorWithDefaultOptions(a)(&alloc);
+    if (!st) st = api::ModelMetadataLookupCustomMetadataMap(a)(md, alloc, key, &v);
+    api::ReleaseModelMetadata(a)(md);
+    check_ort(a, st, "ModelMetadataLookupCustomMetadataMap");
+    if (!v) return false;
+    *value = v;
+    alloc->Free(alloc, v);
+    return true;
+}
+
 OrtStatus* ep_get_capability(OrtEp* self, const OrtGraph* graph, OrtEpGraphSupportInfo* support) {
     Ep* ep = reinterpret_cast<Ep*>(self);
     return guard(ep->api, "GetCapability", [&] {
@@ -182,7 +198,31 @@ OrtStatus* ep_get_capability(OrtEp* self, const OrtGraph* graph, OrtEpGraphSuppo
                 std::fprintf(stderr, "[mi355x-ep] decline %s (%s): %s\n", g.nodes[i].name.c_str(),
                              g.nodes[i].op.c_str(), why.c_str());
         }
-        for (const auto& cl : build_clusters(g, claimed)) {
+        auto clusters = build_clusters(g, claimed);
+        // Layer groups of large decoders (rust/src/ep.rs:296-332): boundaries from
+        // the model metadata, else inferred; none inside a control-flow body.
+        const OrtNode* parent = nullptr;
+        check_ort(ep->api, api::Graph_GetParentNode(ep->api)(graph, &parent), "Graph_GetParentNode");
+        const char* env = std::getenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS");
+        const size_t span = parent ? 0 : select_layer_span(env);
+        if (span) {
+            std::set<std::string> bounds;
+            std::string md;
+            if (read_metadata(ep->api, graph, kLayerBoundaryKey, &md)) {
+                std::vector<std::string> names;
+                if (parse_json_string_array(md, &names)) {
+                    for (auto& n : names)
+                        if (!n.empty()) bounds.insert(n);
+                } else {
+                    std::fprintf(stderr, "[mi355x-ep] ignoring invalid %s metadata\n",
+                                 kLayerBoundaryKey);
+                }
+            } else {
+                bounds = infer_layer_boundaries(g);
+            }
+            clusters = split_layer_clusters(g, std::move(clusters), bounds, span);
+        }
+        for (const auto& cl : clusters) {
             std::vector<const OrtNode*> nodes;
             for (size_t i : cl) nodes.push_back(g.nodes[i].handle);
             OrtNodeFusionOptions opts{ORT_API_VERSION, true};

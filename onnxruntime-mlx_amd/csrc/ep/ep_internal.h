@@ -17,6 +17,7 @@
 #include <map>
 #include <memory>
 #include <mutex>
+#include <set>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -100,6 +101,31 @@ std::string claim_reason(const NodeDesc& n, const GraphIR& g);  // "" = claimed
 // fused node). Returns node indices (into g.nodes) per cluster, topologically
 // ordered inside each cluster.
 std::vector<std::vector<size_t>> build_clusters(const GraphIR& g, const std::vector<bool>& claimed);
+
+// ------------------------------------------- layer groups of large decoders --
+// (rust/src/ep.rs:296-516, README.md "Large-decoder partition metadata")
+// Model metadata key whose value is a JSON array of residual output names, one
+// per transformer layer; it takes precedence over inference.
+constexpr const char* kLayerBoundaryKey = "onnxruntime_ep_mlx.layer_boundary_outputs";
+// Parse a JSON array of strings (the metadata value); false if it is anything else.
+bool parse_json_string_array(const std::string& text, std::vector<std::string>* out);
+// Residual outputs that end each layer, inferred from data flow: between two
+// consecutive decoder-attention nodes (PagedAttention, or GroupQueryAttention /
+// MultiHeadAttention / Attention with present key and value outputs) the last
+// Add that the first reaches and that reaches the second. Empty when any pair
+// has no such Add or there are fewer than two attention nodes.
+std::set<std::string> infer_layer_boundaries(const GraphIR& g);
+// Layers per partition from the ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS value; 0 keeps
+// every cluster whole. Unset, empty or "auto" keeps decoders whole on MI355X (the
+// one-launch decode step needs the whole decoder in one fused node); "0", "off",
+// "false" disable; a positive integer is the span; anything else disables.
+size_t select_layer_span(const char* value);
+// Cut each cluster (in its topological order) after every `span`-th node that
+// produces a boundary output.
+std::vector<std::vector<size_t>> split_layer_clusters(const GraphIR& g,
+                                                      std::vector<std::vector<size_t>> clusters,
+                                                      const std::set<std::string>& boundaries,
+                                                      size_t span);
 
 // Compile-time rewrites of a fused node's subgraph (SwiGLU, and with
 // decode_fusions the QKV / gate-up merges and norm prologues).

@@ -700,4 +700,234 @@ std::vector<std::vector<size_t>> build_clusters(const GraphIR& g,
     return out;
 }
 
+// ------------------------------------------- layer groups of large decoders --
+
+namespace {
+void put_utf8(uint32_t cp, std::string* out) {
+    if (cp < 0x80) {
+        out->push_back((char)cp);
+    } else if (cp < 0x800) {
+        out->push_back((char)(0xC0 | (cp >> 6)));
+        out->push_back((char)(0x80 | (cp & 0x3F)));
+    } else if (cp < 0x10000) {
+        out->push_back((char)(0xE0 | (cp >> 12)));
+        out->push_back((char)(0x80 | ((cp >> 6) & 0x3F)));
+        out->push_back((char)(0x80 | (cp & 0x3F)));
+    } else {
+        out->push_back((char)(0xF0 | (cp >> 18)));
+        out->push_back((char)(0x80 | ((cp >> 12) & 0x3F)));
+        out->push_back((char)(0x80 | ((cp >> 6) & 0x3F)));
+        out->push_back((char)(0x80 | (cp & 0x3F)));
+    }
+}
+
+// Recursive-descent reader over the JSON grammar's array-of-strings subset.
+struct JsonStrings {
+    const std::string& t;
+    size_t i = 0;
+    void ws() {
+        while (i < t.size() && (t[i] == ' ' || t[i] == '\t' || t[i] == '\n' || t[i] == '\r')) ++i;
+    }
+    bool hex4(uint32_t* v) {
+        if (i + 4 > t.size()) return false;
+        *v = 0;
+        for (int k = 0; k < 4; ++k) {
+            const char c = t[i++];
+            *v <<= 4;
+            if (c >= '0' && c <= '9') *v |= (uint32_t)(c - '0');
+            else if (c >= 'a' && c <= 'f') *v |= (uint32_t)(c - 'a' + 10);
+            else if (c >= 'A' && c <= 'F') *v |= (uint32_t)(c - 'A' + 10);
+            else return false;
+        }
+        return true;
+    }
+    bool str(std::string* out) {
+        if (i >= t.size() || t[i] != '"') return false;
+        ++i;
+        while (i < t.size()) {
+            const unsigned char c = (unsigned char)t[i++];
+            if (c == '"') return true;
+            if (c < 0x20) return false;  // control characters must be escaped
+            if (c != '\\') {
+                out->push_back((char)c);
+                continue;
+            }
+            if (i >= t.size()) return false;
+            const char e = t[i++];
+            switch (e) {
+                case '"': out->push_back('"'); break;
+                case '\\': out->push_back('\\'); break;
+                case '/': out->push_back('/'); break;
+                case 'b': out->push_back('\b'); break;
+                case 'f': out->push_back('\f'); break;
+                case 'n': out->push_back('\n'); break;
+                case 'r': out->push_back('\r'); break;
+                case 't': out->push_back('\t'); break;
+                case 'u': {
+                    uint32_t cp;
+                    if (!hex4(&cp)) return false;
+                    if (cp >= 0xD800 && cp < 0xDC00) {  // high surrogate: a low one follows
+                        uint32_t lo;
+                        if (i + 2 > t.size() || t[i] != '\\' || t[i + 1] != 'u') return false;
+                        i += 2;
+                        if (!hex4(&lo) || lo < 0xDC00 || lo >= 0xE000) return false;
+                        cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
+                    } else if (cp >= 0xDC00 && cp < 0xE000) {
+                        return false;
+                    }
+                    put_utf8(cp, out);
+                    break;
+                }
+                default: return false;
+            }
+        }
+        return false;  // unterminated
+    }
+};
+}  // namespace
+
+bool parse_json_string_array(const std::string& text, std::vector<std::string>* out) {
+    JsonStrings p{text};
+    std::vector<std::string> items;
+    p.ws();
+    if (p.i >= text.size() || text[p.i] != '[') return false;
+    ++p.i;
+    p.ws();
+    if (p.i < text.size() && text[p.i] == ']') {
+        ++p.i;
+    } else {
+        for (;;) {
+            p.ws();
+            std::string s;
+            if (!p.str(&s)) return false;
+            items.push_back(std::move(s));
+            p.ws();
+            if (p.i >= text.size()) return false;
+            if (text[p.i] == ',') {
+                ++p.i;
+                continue;
+            }
+            if (text[p.i] != ']') return false;
+            ++p.i;
+            break;
+        }
+    }
+    p.ws();
+    if (p.i != text.size()) return false;
+    *out = std::move(items);
+    return true;
+}
+
+namespace {
+bool is_attention_anchor(const NodeDesc& n) {
+    if (n.domain == "com.microsoft" && n.op == "PagedAttention") return true;
+    const bool presents = n.outputs.size() >= 3 && !n.outputs[1].empty() && !n.outputs[2].empty();
+    if (!presents) return false;
+    if (n.domain == "com.microsoft") return n.op == "GroupQueryAttention" || n.op == "MultiHeadAttention";
+    return (n.domain.empty() || n.domain == "ai.onnx") && n.op == "Attention";
+}
+}  // namespace
+
+std::set<std::string> infer_layer_boundaries(const GraphIR& g) {
+    const size_t N = g.nodes.size();
+    std::map<std::string, size_t> producer;
+    std::vector<size_t> anchors;
+    for (size_t i = 0; i < N; ++i) {
+        if (is_attention_anchor(g.nodes[i])) anchors.push_back(i);
+        for (const auto& o : g.nodes[i].outputs)
+            if (!o.empty()) producer.emplace(o, i);  // first producer wins
+    }
+    if (anchors.size() < 2) return {};
+    std::vector<std::vector<size_t>> succs(N), preds(N);
+    for (size_t i = 0; i < N; ++i) {
+        std::set<size_t> seen;
+        for (const auto& in : g.nodes[i].inputs) {
+            auto it = in.empty() ? producer.end() : producer.find(in);
+            if (it == producer.end() || it->second == i || !seen.insert(it->second).second) continue;
+            succs[it->second].push_back(i);
+            preds[i].push_back(it->second);
+        }
+    }
+    std::set<std::string> out;
+    std::vector<char> down(N), up(N);
+    for (size_t a = 0; a + 1 < anchors.size(); ++a) {
+        const size_t cur = anchors[a], next = anchors[a + 1];
+        // Nodes in graph order up to `next` reached from `cur`, and nodes from `cur`
+        // on that reach `next`.
+        std::fill(down.begin(), down.end(), 0);
+        std::fill(up.begin(), up.end(), 0);
+        std::vector<size_t> stack{cur};
+        while (!stack.empty()) {
+            const size_t v = stack.back();
+            stack.pop_back();
+            for (size_t s : succs[v])
+                if (s <= next && !down[s]) {
+                    down[s] = 1;
+                    stack.push_back(s);
+                }
+        }
+        stack.assign(1, next);
+        while (!stack.empty()) {
+            const size_t v = stack.back();
+            stack.pop_back();
+            for (size_t p : preds[v])
+                if (p >= cur && !up[p]) {
+                    up[p] = 1;
+                    stack.push_back(p);
+                }
+        }
+        size_t hit = 0;
+        for (size_t k = next; k-- > cur + 1;)
+            if (g.nodes[k].op == "Add" && down[k] && up[k]) {
+                hit = k;
+                break;
+            }
+        if (!hit) return {};  // one layer without a residual Add: no boundaries at all
+        if (!g.nodes[hit].outputs.empty() && !g.nodes[hit].outputs[0].empty())
+            out.insert(g.nodes[hit].outputs[0]);
+    }
+    return out;
+}
+
+size_t select_layer_span(const char* value) {
+    if (!value) return 0;  // auto: whole at any depth
+    std::string v(value);
+    const auto b = v.find_first_not_of(" \t\n\r");
+    if (b == std::string::npos) return 0;
+    v = v.substr(b, v.find_last_not_of(" \t\n\r") - b + 1);
+    if (v == "auto" || v == "0" || v == "off" || v == "false") return 0;
+    size_t i = v[0] == '+' ? 1 : 0;
+    if (i == v.size() || v.size() - i > 18) return 0;
+    size_t span = 0;
+    for (; i < v.size(); ++i) {
+        if (v[i] < '0' || v[i] > '9') return 0;
+        span = span * 10 + (size_t)(v[i] - '0');
+    }
+    return span;
+}
+
+std::vector<std::vector<size_t>> split_layer_clusters(const GraphIR& g,
+                                                      std::vector<std::vector<size_t>> clusters,
+                                                      const std::set<std::string>& boundaries,
+                                                      size_t span) {
+    if (!span || boundaries.empty()) return clusters;
+    std::vector<std::vector<size_t>> out;
+    for (auto& cl : clusters) {
+        std::vector<size_t> part;
+        size_t layers = 0;
+        for (size_t v : cl) {
+            part.push_back(v);
+            bool ends = false;
+            for (const auto& o : g.nodes[v].outputs) ends = ends || (!o.empty() && boundaries.count(o));
+            if (ends && ++layers == span) {
+                out.push_back(std::move(part));
+                part.clear();
+                layers = 0;
+            }
+        }
+        if (!part.empty()) out.push_back(std::move(part));
+    }
+    return out;
+}
+
 }  // namespace ortmi_ep

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -75,6 +76,11 @@ struct OrtNode {
 struct OrtGraph {
     std::vector<OrtNode*> nodes;
     std::vector<OrtValueInfo*> inputs, outputs, initializers;
+    std::map<std::string, std::string> metadata;  // the model's custom metadata map
+    const OrtNode* parent = nullptr;              // set for a control-flow body
+};
+struct OrtModelMetadata {
+    std::map<std::string, std::string> custom;
 };
 struct OrtEpGraphSupportInfo {
     std::vector<std::vector<const OrtNode*>> groups;
@@ -212,6 +218,39 @@ LIST_FNS(Outputs, outputs, OrtValueInfo)
 LIST_FNS(Initializers, initializers, OrtValueInfo)
 LIST_FNS(Nodes, nodes, OrtNode)
 #undef LIST_FNS
+OrtStatus* h_Graph_GetParentNode(const OrtGraph* g, const OrtNode** node) {
+    *node = g->parent;
+    return nullptr;
+}
+OrtStatus* h_Graph_GetModelMetadata(const OrtGraph* g, OrtModelMetadata** out) {
+    *out = new OrtModelMetadata{g->metadata};
+    return nullptr;
+}
+OrtStatus* h_ModelMetadataLookupCustomMetadataMap(const OrtModelMetadata* md, OrtAllocator* alloc,
+                                                  const char* key, char** value) {
+    *value = nullptr;
+    auto it = md->custom.find(key);
+    if (it == md->custom.end()) return nullptr;
+    char* p = static_cast<char*>(alloc->Alloc(alloc, it->second.size() + 1));
+    if (!p) return mk(ORT_FAIL, "allocation failed");
+    std::memcpy(p, it->second.c_str(), it->second.size() + 1);
+    *value = p;
+    return nullptr;
+}
+void h_ReleaseModelMetadata(OrtModelMetadata* md) { delete md; }
+void* default_alloc(OrtAllocator*, size_t n) { return std::malloc(n); }
+void default_free(OrtAllocator*, void* p) { std::free(p); }
+OrtStatus* h_GetAllocatorWithDefaultOptions(OrtAllocator** out) {
+    static OrtAllocator cpu = [] {
+        OrtAllocator a{};
+        a.version = ORT_API_VERSION;
+        a.Alloc = default_alloc;
+        a.Free = default_free;
+        return a;
+    }();
+    *out = &cpu;
+    return nullptr;
+}
 OrtStatus* h_Node_GetId(const OrtNode* n, size_t* id) {
     *id = n->id;
     return nullptr;
@@ -533,6 +572,11 @@ int hx_node_attr_string(HxGraph* g, int node, const char* name, const char* v) {
 }
 int hx_node_attr_ints(HxGraph* g, int node, const char* name, int n, const int64_t* v) {
     new_attr(g, node, name, ORT_OP_ATTR_INTS)->ints.assign(v, v + n);
+    return 0;
+}
+
+int hx_graph_set_metadata(HxGraph* g, const char* key, const char* value) {
+    g->g.metadata[key] = value;
     return 0;
 }
 

@@ -18,6 +18,7 @@ input id, so a decode step reads nothing back to the host but total_sequence_len
 from __future__ import annotations
 
 import ctypes
+import json
 import time
 from dataclasses import dataclass
 
@@ -99,8 +100,13 @@ def make_weights(cfg: DecoderConfig, seed: int = 4):
     return w
 
 
-def build_graph(cfg: DecoderConfig, w, cap: int) -> hx.Graph:
-    """Decoder graph with symbolic sequence length S and KV capacity `cap`."""
+def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False) -> hx.Graph:
+    """Decoder graph with symbolic sequence length S and KV capacity `cap`.
+
+    layer_metadata: also record the residual stream after each layer (the last one's
+    is the final norm's residual output) under the model metadata key
+    onnxruntime_ep_mlx.layer_boundary_outputs, as the reference's exporters do
+    (README.md "Large-decoder partition metadata")."""
     g = hx.Graph()
     F16, I32, I64 = hx.FLOAT16, hx.INT32, hx.INT64
     D, H, KV, hd = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
@@ -179,6 +185,9 @@ def build_graph(cfg: DecoderConfig, w, cap: int) -> hx.Graph:
     g.initializer("lm_head.s", w["lm_head.s"])
     g.node("MatMulNBits", ["xf", "lm_head.B", "lm_head.s"], ["logits"], domain="com.microsoft",
            name="lm_head", K=D, N=cfg.vocab, bits=4, block_size=cfg.block)
+    if layer_metadata:
+        names = [f"l{layer}.res1" for layer in range(1, cfg.layers)] + ["resf"]
+        g.metadata("onnxruntime_ep_mlx.layer_boundary_outputs", json.dumps(names))
     g.io(inputs, outputs)
     return g
 
@@ -190,13 +199,14 @@ class DecoderRunner:
     ONNX Runtime keeps it in CPU memory); ids, logits, KV and the argmax stay in HBM.
     """
 
-    def __init__(self, cfg: DecoderConfig, weights, cap: int, max_prompt: int):
+    def __init__(self, cfg: DecoderConfig, weights, cap: int, max_prompt: int,
+                 layer_metadata: bool = False):
         import torch
 
         self.torch = torch
         self.cfg = cfg
         self.cap = cap
-        self.graph = build_graph(cfg, weights, cap)
+        self.graph = build_graph(cfg, weights, cap, layer_metadata)
         self.session = hx.Session(self.graph)
         dev = "cuda"
         self.kv = []

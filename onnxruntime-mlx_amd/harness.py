@@ -47,6 +47,7 @@ def lib() -> ctypes.CDLL:
             "hx_node_attr_string": (ctypes.c_int, [vp, ctypes.c_int, cp, cp]),
             "hx_node_attr_ints": (ctypes.c_int, [vp, ctypes.c_int, cp, ctypes.c_int, i64p]),
             "hx_graph_set_io": (ctypes.c_int, [vp, ctypes.c_int, cpp, ctypes.c_int, cpp]),
+            "hx_graph_set_metadata": (ctypes.c_int, [vp, cp, cp]),
             "hx_session_new": (vp, [vp, cp, cp, ctypes.c_int, ctypes.c_int]),
             "hx_session_free": (None, [vp]),
             "hx_session_num_partitions": (ctypes.c_int, [vp]),
@@ -122,6 +123,10 @@ class Graph:
                 vals = [int(x) for x in v]
                 lib().hx_node_attr_ints(self.h, idx, k.encode(), len(vals), _dims(vals))
         return idx
+
+    def metadata(self, key, value):
+        """Set one entry of the model's custom metadata map."""
+        lib().hx_graph_set_metadata(self.h, key.encode(), value.encode())
 
     def io(self, inputs, outputs):
         lib().hx_graph_set_io(self.h, len(inputs), _strs(inputs), len(outputs), _strs(outputs))

@@ -328,6 +328,23 @@ def test_decoder_graph_fully_claimed_as_one_fused_node():
     assert g.n_nodes == 1 + cfg.layers * 13 + 2
 
 
+def test_decoder_graph_with_layer_metadata_splits_by_span(monkeypatch):
+    """The decoder's residual outputs named in metadata (one per layer, the last
+    being the final norm's): span 2 over 5 layers cuts after layers 2 and 4."""
+    cfg = dec.DecoderConfig(layers=5, hidden=256, heads=4, kv_heads=2, head_dim=64, inter=512,
+                            vocab=1000, max_pos=256)
+    w = dec.make_weights(cfg, seed=0)
+    g = dec.build_graph(cfg, w, cap=64, layer_metadata=True)
+    monkeypatch.delenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", raising=False)
+    assert [len(p) for p in session(g).partitions()] == [g.n_nodes]
+    monkeypatch.setenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", "2")
+    parts = session(g).partitions()
+    # gather + 13 nodes per layer; layer l's residual comes out of layer l+1's first
+    # norm, so a cut after two layers holds 1 + 2*13 + 1 nodes.
+    assert [len(p) for p in parts] == [28, 26, 14]
+    assert sum(len(p) for p in parts) == g.n_nodes
+
+
 def test_default_memory_device_slot_matches_reference_binding():
     """OrtEp::GetDefaultMemoryDevice is bound by the reference as
     fn(*const OrtEp, *mut *const OrtMemoryDevice) -> *mut OrtStatus
@@ -384,3 +401,139 @@ def test_gqa_claim_checks_head_size_without_past(qwidth, packed, claimed):
            kv_num_heads=KV, do_rotary=0)
     g.io([n for n in ins if n], ["o"])
     assert session(g).claimed(0) is claimed
+
+
+# ------------------------------------------------- layer groups of large decoders ---
+
+def layered_graph(layers, residual="add", metadata=None):
+    """A decoder-shaped graph, per layer: q/k/v MatMulNBits -> GroupQueryAttention
+    (present key/value outputs) -> o_proj MatMulNBits -> Add (residual) ->
+    MatMulNBits -> Add (residual, the layer's output x{l+1}). residual="skipnorm"
+    puts a SkipSimplifiedLayerNormalization in place of the first Add;
+    residual="none" replaces both Adds by such norms (no Add in the layer)."""
+    g = hx.Graph()
+    H, KV, hd, cap = 2, 1, 64, 16
+    D = H * hd
+    g.value("x0", F16, [1, 1, D])
+    g.value("sl", I32, [1])
+    g.value("tot", I32, [1])
+    g.value("gamma", F16, [D])
+    g.initializer("gamma", np.ones(D, np.float16))
+    inputs = ["x0", "sl", "tot"]
+    outputs = []
+    for l in range(layers):
+        x = f"x{l}"
+        mnb_node(g, x, f"q{l}", D, D, f"L{l}.q")
+        mnb_node(g, x, f"k{l}", KV * hd, D, f"L{l}.k")
+        mnb_node(g, x, f"v{l}", KV * hd, D, f"L{l}.v")
+        for n in (f"pk{l}", f"pv{l}", f"ok{l}", f"ov{l}"):
+            g.value(n, F16, [1, KV, cap, hd])
+        g.value(f"a{l}", F16, [1, 1, D])
+        g.node("GroupQueryAttention", [f"q{l}", f"k{l}", f"v{l}", f"pk{l}", f"pv{l}", "sl", "tot"],
+               [f"a{l}", f"ok{l}", f"ov{l}"], domain="com.microsoft", num_heads=H,
+               kv_num_heads=KV, name=f"L{l}.attn")
+        mnb_node(g, f"a{l}", f"o{l}", D, D, f"L{l}.o")
+        g.value(f"h{l}", F16, [1, 1, D])
+        if residual == "add":
+            g.node("Add", [x, f"o{l}"], [f"h{l}"], name=f"L{l}.add1")
+        else:
+            g.value(f"n{l}", F16, [1, 1, D])
+            g.node("SkipSimplifiedLayerNormalization", [f"o{l}", x, "gamma"],
+                   [f"n{l}", "", "", f"h{l}"], domain="com.microsoft", name=f"L{l}.norm")
+        mnb_node(g, f"h{l}", f"m{l}", D, D, f"L{l}.mlp")
+        g.value(f"x{l + 1}", F16, [1, 1, D])
+        if residual == "none":
+            g.node("SkipSimplifiedLayerNormalization", [f"m{l}", f"h{l}", "gamma"],
+                   [f"y{l}", "", "", f"x{l + 1}"], domain="com.microsoft", name=f"L{l}.norm2")
+            g.value(f"y{l}", F16, [1, 1, D])
+            outputs.append(f"y{l}")
+        else:
+            g.node("Add", [f"h{l}", f"m{l}"], [f"x{l + 1}"], name=f"L{l}.add2")
+        inputs += [f"pk{l}", f"pv{l}"]
+        outputs += [f"ok{l}", f"ov{l}"]
+    outputs.append(f"x{layers}")
+    if metadata is not None:
+        g.metadata("onnxruntime_ep_mlx.layer_boundary_outputs", metadata)
+    g.io(inputs, outputs)
+    return g
+
+
+NODES_PER_LAYER = 8
+
+
+def _sizes(g):
+    return [len(p) for p in session(g).partitions()]
+
+
+def test_layer_partitions_auto_keeps_decoder_whole(monkeypatch):
+    """Unset / "auto": one fused node at any depth (the reference splits decoders
+    of 23+ layers, rust/src/ep.rs:365-374; on MI355X the whole-step decode program
+    needs the whole decoder in one fused node)."""
+    monkeypatch.delenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", raising=False)
+    assert _sizes(layered_graph(24)) == [24 * NODES_PER_LAYER]
+    monkeypatch.setenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", "auto")
+    assert _sizes(layered_graph(24)) == [24 * NODES_PER_LAYER]
+
+
+@pytest.mark.parametrize("value,sizes", [
+    ("5", [40, 40, 40, 40, 32]),   # 23 inferred boundaries (between 24 attention nodes)
+    (" 8 ", [64, 64, 64]),
+    ("+12", [96, 96]),
+    ("1", [8] * 23 + [8]),
+    ("0", [192]), ("off", [192]), ("false", [192]), ("invalid", [192]), ("-3", [192]),
+])
+def test_layer_partitions_inferred_boundaries_span(monkeypatch, value, sizes):
+    """Inferred boundaries are each layer's last residual Add (the reference's
+    structural test, rust/src/ep.rs:539-569); the span override follows
+    select_layer_span's grammar (rust/src/ep.rs:360-375, tests 522-537)."""
+    monkeypatch.setenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", value)
+    assert _sizes(layered_graph(24)) == sizes
+
+
+def test_layer_partitions_split_after_the_last_residual_add(monkeypatch):
+    monkeypatch.setenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", "2")
+    g = layered_graph(4)
+    parts = session(g).partitions()
+    # Node order of the graph: 8 per layer, add2 last; the cut follows L1.add2 and
+    # the last layer (no attention after it) stays with the remainder.
+    assert [len(p) for p in parts] == [16, 16]
+    assert parts[0] == list(range(16)) and parts[1] == list(range(16, 32))
+
+
+def test_layer_partitions_metadata_takes_precedence(monkeypatch):
+    """Metadata names the boundaries (here the first residual Add of every layer,
+    which inference would not pick) and is used instead of inference."""
+    import json
+
+    monkeypatch.setenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", "3")
+    names = [f"h{layer}" for layer in range(9)]
+    parts = session(layered_graph(9, metadata=json.dumps(names))).partitions()
+    assert [len(p) for p in parts] == [22, 24, 24, 2]
+    # Each cut follows an add1 node (index 5 of its layer).
+    assert [p[-1] % NODES_PER_LAYER for p in parts[:-1]] == [5, 5, 5]
+
+
+@pytest.mark.parametrize("metadata,sizes", [
+    ('["x1", "x3"]', [8, 16, 8]),                       # span 1: cut after each named output
+    ('[]', [32]),                                       # empty list: no boundaries, no inference
+    ('not json', [32]),                                 # invalid: ignored, no inference
+    ('["x1", 3]', [32]),                                # not all strings
+    ('["x\\u0031", "x\\u00333"]', [8, 24]),            # \u escapes decode ("x1", "x33" absent)
+    (' [ "x2" , "" ] ', [16, 16]),                      # whitespace; empty names dropped
+])
+def test_layer_partitions_metadata_parsing(monkeypatch, metadata, sizes):
+    monkeypatch.setenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", "1")
+    assert _sizes(layered_graph(4, metadata=metadata)) == sizes
+
+
+@pytest.mark.parametrize("residual", ["skipnorm", "none"])
+def test_layer_partitions_inference_needs_a_residual_add_in_every_layer(monkeypatch, residual):
+    """With SkipSimplifiedLayerNormalization carrying the residual the second Add
+    is still found ("skipnorm"); with no Add between two attention nodes
+    ("none") inference yields no boundaries and the graph stays whole."""
+    monkeypatch.setenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", "2")
+    sizes = _sizes(layered_graph(6, residual=residual))
+    if residual == "skipnorm":
+        assert sizes == [16, 16, 16]
+    else:
+        assert sizes == [48]

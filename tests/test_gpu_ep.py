@@ -347,6 +347,37 @@ def test_ep_decoder_fusions_match_unfused(ortmi, dec, monkeypatch):
     assert ft == ut
 
 
+def test_ep_decoder_layer_partitions_match_whole(ortmi, oracle, dec, monkeypatch):
+    """A 4-layer decoder whose metadata names its layer boundaries, split two layers
+    per fused node (ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS=2): three fused nodes, and
+    the same logits (within the fp16 tolerance of the fusions that cannot cross a
+    cut) and greedy tokens as the whole graph; tokens teacher-forced against the
+    oracle."""
+    cfg = dec.DecoderConfig(layers=4, hidden=256, heads=4, kv_heads=2, head_dim=64, inter=512,
+                            vocab=2048, max_pos=512)
+    w = dec.make_weights(cfg, seed=41)
+    prompt = np.random.default_rng(42).integers(0, cfg.vocab, size=14)
+    monkeypatch.setenv("ORTMI_EP_PROGRAM", "0")
+
+    def run(span):
+        if span:
+            monkeypatch.setenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", str(span))
+        else:
+            monkeypatch.delenv("ONNXRUNTIME_EP_MLX_LAYER_PARTITIONS", raising=False)
+        r = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32, layer_metadata=True)
+        nparts = len(r.session.partitions())
+        rows = _teacher_forced_check(oracle, r, cfg, w, prompt.tolist(), steps=6)
+        return nparts, rows
+
+    n_whole, whole = run(0)
+    n_split, split = run(2)
+    assert (n_whole, n_split) == (1, 3)
+    for (a, _, ta), (b, _, tb) in zip(split, whole):
+        assert np.abs(a - b).max() <= 0.02 * max(1.0, np.abs(b).max())
+        assert ta == tb
+    _assert_greedy_strict(split, "decoder split in layer groups")
+
+
 # ------------------------------------------------------------- boundary slots --
 
 def _one_node_mnb_graph(hx, rng, N=256, K=512):
