@@ -20,6 +20,7 @@
 #include <set>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../../include/ort_plugin_ep_abi.h"
@@ -195,9 +196,10 @@ class Plan {
     Tensor& out_tensor(const std::string& name, int dtype, const std::vector<int64_t>& dims,
                        const OrtApi* api, OrtKernelContext* ctx);
     // The caller's buffer of fused-node output `name` (host or device memory), or
-    // null when `name` is not a fused-node output.
+    // null when `name` is not a fused-node output. `record` keeps the output for
+    // the graph-replay bookkeeping (the decode program does not need it).
     void* output_buffer(const std::string& name, const std::vector<int64_t>& dims,
-                        const OrtApi* api, OrtKernelContext* ctx);
+                        const OrtApi* api, OrtKernelContext* ctx, bool record = true);
     // Queue a device -> host copy of `rows` rows of `row_bytes` from each of
     // `slabs` slabs (pitch `pitch` bytes on both sides) after the run's kernels.
     void copy_out_rows(void* host, const void* dev, size_t pitch, size_t row_bytes, size_t rows,
@@ -218,10 +220,10 @@ class Plan {
 
     GraphIR sub_;
     std::vector<std::string> inputs_, outputs_;
-    std::map<std::string, int> output_index_;
+    std::unordered_map<std::string, int> output_index_;
     std::map<std::string, std::unique_ptr<DeviceBuffer>> constants_;  // initializers in HBM
-    std::map<std::string, Tensor> env_;                               // values of this run
-    std::map<std::string, int32_t> host_scalars_;
+    std::unordered_map<std::string, Tensor> env_;                     // values of this run
+    std::unordered_map<std::string, int32_t> host_scalars_;
     int device_ = 0;
     hipStream_t stream_ = nullptr;
     // Bump arena for intermediates, reset per Compute and grown on demand.

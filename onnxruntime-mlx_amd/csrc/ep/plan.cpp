@@ -66,6 +66,8 @@ struct Plan::DecodeProgram {
     int64_t embed_rows = 0;
     std::unique_ptr<DeviceBuffer> table, ws, next_id;
     size_t ws_bytes = 0;
+    void* logits_ptr = nullptr;  // the last logits buffer and whether it is device memory
+    bool logits_dev = false;
     int32_t* status = nullptr;  // host-pinned: the kernel writes it, the host reads it after the run
     ~DecodeProgram() {
         if (status) (void)hipHostFree(status);
@@ -361,12 +363,16 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
     // Present outputs must be the past buffers (KV written in place) and logits a device buffer.
     const std::vector<int64_t> pdims = {1, d.kv_num_heads, cap, d.head_size};
     for (size_t l = 0; l < dp.layers.size(); ++l) {
-        if (output_buffer(dp.layers[l].present_k, pdims, a, ctx) != table[l].k_cache ||
-            output_buffer(dp.layers[l].present_v, pdims, a, ctx) != table[l].v_cache)
+        if (output_buffer(dp.layers[l].present_k, pdims, a, ctx, false) != table[l].k_cache ||
+            output_buffer(dp.layers[l].present_v, pdims, a, ctx, false) != table[l].v_cache)
             return skip("present is not bound to past");
     }
-    void* logits = output_buffer(dp.logits, {1, 1, d.vocab}, a, ctx);
-    if (!is_device_ptr(logits)) return skip("logits in host memory");
+    void* logits = output_buffer(dp.logits, {1, 1, d.vocab}, a, ctx, false);
+    if (logits != dp.logits_ptr) {  // the pointer query costs microseconds: once per buffer
+        dp.logits_dev = is_device_ptr(logits);
+        dp.logits_ptr = logits;
+    }
+    if (!dp.logits_dev) return skip("logits in host memory");
     const size_t tb = table.size() * sizeof(OrtmiDecoderLayer);
     if (!dp.table || dp.host_table.size() != table.size() ||
         std::memcmp(dp.host_table.data(), table.data(), tb) != 0) {
@@ -469,7 +475,7 @@ thread_local std::vector<Staged>* g_out_staging = nullptr;
 }  // namespace
 
 void* Plan::output_buffer(const std::string& name, const std::vector<int64_t>& dims,
-                          const OrtApi* a, OrtKernelContext* ctx) {
+                          const OrtApi* a, OrtKernelContext* ctx, bool record) {
     auto oi = output_index_.find(name);
     if (oi == output_index_.end()) return nullptr;
     OrtValue* ov = nullptr;
@@ -478,7 +484,7 @@ void* Plan::output_buffer(const std::string& name, const std::vector<int64_t>& d
               "KernelContext_GetOutput");
     void* p = nullptr;
     check_ort(a, api::GetTensorMutableData(a)(ov, &p), "GetTensorMutableData");
-    outs_.push_back({(size_t)oi->second, dims, p});
+    if (record) outs_.push_back({(size_t)oi->second, dims, p});
     return p;
 }
 
@@ -578,6 +584,8 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
     std::lock_guard<std::mutex> lock(mu_);
     check_hip(hipSetDevice(device_), "hipSetDevice");
     env_.clear();
+    if (env_.bucket_count() < 2 * (inputs_.size() + sub_.values.size()))
+        env_.reserve(inputs_.size() + sub_.values.size());
     host_scalars_.clear();
     arena_off_ = 0;
     std::vector<Staged> out_staging;

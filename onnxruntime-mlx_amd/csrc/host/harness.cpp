@@ -22,6 +22,7 @@
 #include <set>
 #include <string>
 #include <type_traits>
+#include <unordered_map>
 #include <vector>
 
 #include "../../../include/ort_plugin_ep_abi.h"
@@ -87,9 +88,8 @@ struct OrtEpGraphSupportInfo {
 };
 struct OrtKernelContext {
     std::vector<OrtValue*> inputs;
-    std::vector<std::string> output_names;
+    std::vector<const OrtValueInfo*> outputs;  // the fused node's outputs (name, type)
     struct Session* session;
-    std::vector<OrtValue*> outputs;
 };
 struct OrtNodeComputeContext {
     std::string name;
@@ -171,7 +171,7 @@ OrtStatus* h_KernelContext_GetInputCount(const OrtKernelContext* c, size_t* out)
     return nullptr;
 }
 OrtStatus* h_KernelContext_GetOutputCount(const OrtKernelContext* c, size_t* out) {
-    *out = c->output_names.size();
+    *out = c->outputs.size();
     return nullptr;
 }
 OrtStatus* h_KernelContext_GetInput(const OrtKernelContext* c, size_t i, const OrtValue** out) {
@@ -428,9 +428,17 @@ struct Session {
     std::vector<std::unique_ptr<Partition>> parts;
     std::vector<std::unique_ptr<OrtValueInfo>> extra_vis;
     std::set<const OrtNode*> claimed;
-    std::map<std::string, std::unique_ptr<OrtValue>> env;      // values of the current run
-    std::map<std::string, DevBuf> owned;                        // harness-allocated outputs
-    std::map<std::string, void*> bound;                         // caller-bound output buffers
+    // Values of the current run (not owning), one persistent OrtValue per name
+    // (owning: its fields are rewritten when the value is set again).
+    std::unordered_map<std::string, OrtValue*> env;
+    std::unordered_map<std::string, std::unique_ptr<OrtValue>> store;
+    std::unordered_map<std::string, DevBuf> owned;              // harness-allocated outputs
+    std::unordered_map<std::string, void*> bound;               // caller-bound output buffers
+    OrtValue* value(const std::string& name) {
+        auto& v = store[name];
+        if (!v) v = std::make_unique<OrtValue>();
+        return v.get();
+    }
     std::vector<std::unique_ptr<OrtNodeComputeContext>> ctxs;
     ~Session();
 };
@@ -447,13 +455,12 @@ static size_t esize(int dt) {
 namespace {
 OrtStatus* h_KernelContext_GetOutput(OrtKernelContext* c, size_t i, const int64_t* dims, size_t n,
                                      OrtValue** out) {
-    if (i >= c->output_names.size()) return mk(ORT_INVALID_ARGUMENT, "output index out of range");
+    if (i >= c->outputs.size()) return mk(ORT_INVALID_ARGUMENT, "output index out of range");
     Session* s = c->session;
-    const std::string& name = c->output_names[i];
-    auto v = std::make_unique<OrtValue>();
+    const std::string& name = c->outputs[i]->name;
+    OrtValue* v = s->value(name);
     v->info.dims.assign(dims, dims + n);
-    auto vi = s->graph->values.find(name);
-    v->info.dtype = vi != s->graph->values.end() ? vi->second->type.dtype : 0;
+    v->info.dtype = c->outputs[i]->type.dtype;
     size_t bytes = esize(v->info.dtype);
     for (size_t k = 0; k < n; ++k) bytes *= (size_t)(dims[k] < 0 ? 0 : dims[k]);
     auto b = s->bound.find(name);
@@ -470,8 +477,8 @@ OrtStatus* h_KernelContext_GetOutput(OrtKernelContext* c, size_t i, const int64_
         }
         v->data = buf.ptr;
     }
-    *out = v.get();
-    s->env[name] = std::move(v);
+    *out = v;
+    s->env[name] = v;
     return nullptr;
 }
 }  // namespace
@@ -727,11 +734,11 @@ int hx_session_bind_output(Session* s, const char* name, void* ptr) {
 
 int hx_session_set_input(Session* s, const char* name, void* ptr, int dtype, int rank,
                          const int64_t* dims) {
-    auto v = std::make_unique<OrtValue>();
+    OrtValue* v = s->value(name);
     v->data = ptr;
     v->info.dtype = dtype;
     v->info.dims.assign(dims, dims + rank);
-    s->env[name] = std::move(v);
+    s->env[name] = v;
     return 0;
 }
 
@@ -754,8 +761,9 @@ int hx_session_run(Session* s) {
             if (!ready) continue;
             OrtKernelContext ctx;
             ctx.session = s;
-            for (auto* v : p->fused.inputs) ctx.inputs.push_back(s->env[v->name].get());
-            for (auto* v : p->fused.outputs) ctx.output_names.push_back(v->name);
+            ctx.inputs.reserve(p->fused.inputs.size());
+            for (auto* v : p->fused.inputs) ctx.inputs.push_back(s->env[v->name]);
+            ctx.outputs.assign(p->fused.outputs.begin(), p->fused.outputs.end());
             if (!take(p->info->Compute(p->info, p->state, &ctx), "Compute")) return 1;
             done[pi] = progressed = true;
         }

@@ -244,6 +244,51 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const T* __restrict
     if (threadIdx.x == 0) part[row * parts + p] = ArgPartial{best, 0, bi};
 }
 
+// The same partials from 16-byte loads: each thread issues its kArgVec vectors of
+// the 2048-column slice at once (one memory round trip per workgroup instead of a
+// dependent load per element). Elements past the slice or the row read as zeros
+// without a memory access and are skipped by index.
+constexpr int kArgSlice = 2048;
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_partial_vec_kernel(const T* __restrict__ x,
+                                                                 ArgPartial* __restrict__ part,
+                                                                 int64_t cols, int parts) {
+    constexpr int E = 16 / (int)sizeof(T);     // elements per vector
+    constexpr int NV = kArgSlice / (256 * E);  // vectors per thread
+    __shared__ float sv[256];
+    __shared__ int64_t si[256];
+    const int64_t row = blockIdx.y;
+    const int p = blockIdx.x;
+    const int64_t c0 = (int64_t)p * kArgSlice;
+    const uint32_t row_bytes = (uint32_t)(cols * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(x + row * cols, row_bytes);
+    uint4 v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int64_t c = c0 + (int64_t)(j * 256 + (int)threadIdx.x) * E;
+        const uint32_t off = c < cols ? (uint32_t)(c * (int64_t)sizeof(T)) : row_bytes;
+        const auto w = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        v[j] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    float best = -INFINITY;
+    int64_t bi = -1;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const T* e = reinterpret_cast<const T*>(&v[j]);
+        const int64_t cb = c0 + (int64_t)(j * 256 + (int)threadIdx.x) * E;
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            const float val = to_f32(e[k]);
+            if (cb + k < cols && (val > best || (bi < 0 && val == best))) {
+                best = val;
+                bi = cb + k;
+            }
+        }
+    }
+    argmax_block(best, bi, sv, si);
+    if (threadIdx.x == 0) part[row * parts + p] = ArgPartial{best, 0, bi};
+}
+
 __global__ __launch_bounds__(256) void argmax_final_kernel(const ArgPartial* __restrict__ part,
                                                            int64_t* __restrict__ out,
                                                            int parts) {
@@ -263,9 +308,11 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const ArgPartial* __r
     if (threadIdx.x == 0) out[row] = bi < 0 ? 0 : bi;
 }
 
+static int64_t dtype_bytes(int32_t dtype) { return dtype == ORTMI_F32 ? 4 : 2; }
+
 static int argmax_parts(int64_t cols) {
-    // About 2048 columns per workgroup, at most 256 partials per row.
-    int64_t p = (cols + 2047) / 2048;
+    // 2048 columns per workgroup, at most 256 partials per row.
+    int64_t p = (cols + kArgSlice - 1) / kArgSlice;
     return (int)std::min<int64_t>(std::max<int64_t>(p, 1), 256);
 }
 
@@ -411,7 +458,20 @@ extern "C" int ortmi_argmax_rows(const void* x, int64_t* out, int64_t rows, int6
     const bool split = parts > 1 && workspace &&
                        workspace_bytes >= ortmi_argmax_rows_workspace_size(rows, cols);
     const int64_t slice = (cols + parts - 1) / parts;
+    // 16-byte loads need aligned rows and a slice that fits the 256 partials.
+    const bool vec = split && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                     (cols * dtype_bytes(dtype)) % 16 == 0 &&
+                     cols <= (int64_t)kArgSlice * 256 && cols * dtype_bytes(dtype) < (1LL << 31);
 #define ORTMI_ARGMAX(T)                                                                         \
+    if (vec) {                                                                                  \
+        hipLaunchKernelGGL((argmax_partial_vec_kernel<T>), dim3((unsigned)parts, (unsigned)rows), \
+                           dim3(256), 0, st, static_cast<const T*>(x),                          \
+                           static_cast<ArgPartial*>(workspace), cols, parts);                   \
+        if (int rc = check_launch("argmax_partial")) return rc;                                 \
+        hipLaunchKernelGGL(argmax_final_kernel, dim3((unsigned)rows), dim3(256), 0, st,         \
+                           static_cast<const ArgPartial*>(workspace), out, parts);              \
+        return check_launch("argmax_final");                                                    \
+    }                                                                                           \
     if (split) {                                                                                \
         hipLaunchKernelGGL((argmax_partial_kernel<T>), dim3((unsigned)parts, (unsigned)rows),   \
                            dim3(256), 0, st, static_cast<const T*>(x),                          \

@@ -973,8 +973,11 @@ def test_glue_kernels(ortmi):
                                           ctypes.c_void_p(idx.data_ptr()), 3, 151936, 10, w, wb,
                                           st))
         np.testing.assert_array_equal(host(idx), np.argmax(x.astype(np.float32), axis=1))
-    # the same rows in fp32, and fp16 rows of 200000 columns with NaNs that never win
-    for xs, dt in ((x.astype(np.float32), 1), (None, 10)):
+    # the same rows in fp32, fp16 rows of 200000 columns with NaNs that never win, and
+    # rows of 4099 columns (not whole 16-byte vectors: the element-wise partial pass)
+    odd = rng.standard_normal((2, 4099)).astype(np.float16)
+    odd[0, 4098] = odd[1, 2048] = 30.0
+    for xs, dt in ((x.astype(np.float32), 1), (None, 10), (odd, 10)):
         if xs is None:
             xs = rng.standard_normal((2, 200000)).astype(np.float16)
             xs[0, 199999] = 50.0
