@@ -261,7 +261,9 @@ __device__ __forceinline__ bool norm_poll(const uint32_t* src, const half_t* row
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int units = D / 8;
     const bool mine = tid < units;
-    const uint4 gv = mine ? reinterpret_cast<const uint4*>(gamma)[tid] : make_uint4(0, 0, 0, 0);
+    // A buffer load (the pointer comes from LDS, so a plain load would be a flat one,
+    // which also counts against the LDS counter).
+    const uint4 gv = ld128<0>(rsrc(gamma, (uint32_t)D * 2u), mine ? (uint32_t)tid * 16u : (uint32_t)D * 2u);
     uint4 v = make_uint4(0, 0, 0, 0);
     bool ok = true;
     if (src) {
@@ -648,11 +650,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             }
             // The split holding key ctx of the first query head of the KV group
             // appends the new key/value row to the cache (written in place at ctx).
-            if (ok && h % p.G == 0 && ctx >= k0 && ctx < k1 && wave == 0 && grp == 0) {
-                const size_t o = ((size_t)(kvh * p.cap + ctx) * HD + li16 * 8);
-                *reinterpret_cast<uint4*>(static_cast<half_t*>(ly.k_cache) + o) =
-                    make_uint4(kw_new[0], kw_new[1], kw_new[2], kw_new[3]);
-                *reinterpret_cast<uint4*>(static_cast<half_t*>(ly.v_cache) + o) = qkv3[2];
+            // Buffer stores (an offset past the caches when this lane does not append):
+            // a flat store would also count against the LDS counter, and the LDS
+            // reads below would wait for it to complete.
+            {
+                const bool app = ok && h % p.G == 0 && ctx >= k0 && ctx < k1 && wave == 0 && grp == 0;
+                const uint32_t ao =
+                    app ? (uint32_t)(((size_t)(kvh * p.cap + ctx) * HD + li16 * 8) * 2) : kv_bytes;
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    u32x4_t{kw_new[0], kw_new[1], kw_new[2], kw_new[3]}, rk, ao, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    u32x4_t{qkv3[2].x, qkv3[2].y, qkv3[2].z, qkv3[2].w}, rv, ao, 0, 0);
             }
             float m = -INFINITY, lsum = 0.f, o[8];
 #pragma unroll
@@ -683,10 +691,48 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             // (without also waiting for the cache-append stores above).
             int kv_lane = lane;
             asm volatile("" : "+v"(kv_lane) : "v"(qkv3[0].x), "v"(qkv3[2].w));
+            // The LDS-resident keys as one block: every score first (independent
+            // dot products and reductions), then one maximum and the weighted sum,
+            // instead of a rescale chain through the keys one at a time.
+            {
+                float sc[kPref];
+                float bmax = -INFINITY;
 #pragma unroll
-            for (int t = 0; t < kPref; ++t)
-                if (t < steps)
-                    attend(wreg[t * 64 + kv_lane], wreg[(kPref + t) * 64 + kv_lane], k0 + slot + t * kKeySlots);
+                for (int t = 0; t < kPref; ++t) {
+                    sc[t] = -INFINITY;
+                    if (t < steps) {
+                        const int key = k0 + slot + t * kKeySlots;
+                        const uint4 kr = wreg[t * 64 + kv_lane];
+                        const bool fresh = key == ctx;
+                        const uint32_t kw[4] = {fresh ? kw_new[0] : kr.x, fresh ? kw_new[1] : kr.y,
+                                                fresh ? kw_new[2] : kr.z, fresh ? kw_new[3] : kr.w};
+                        float d = 0.f;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, qw[e]),
+                                                       __builtin_bit_cast(half2_t, kw[e]), d, false);
+                        const float sv = group_sum<16>(d) * qscale;
+                        sc[t] = key < k1 ? sv : -INFINITY;
+                        bmax = fmaxf(bmax, sc[t]);
+                    }
+                }
+                if (bmax != -INFINITY) {  // m is still -inf: no rescale
+#pragma unroll
+                    for (int t = 0; t < kPref; ++t) {
+                        if (t < steps) {
+                            const int key = k0 + slot + t * kKeySlots;
+                            const float pe = sc[t] == -INFINITY ? 0.f : exp2f(sc[t] - bmax);
+                            lsum += pe;
+                            const uint4 vr = wreg[(kPref + t) * 64 + kv_lane];
+                            const half_t* vb = reinterpret_cast<const half_t*>(&vr);
+                            const bool fresh = key == ctx;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) o[e] = fmaf(pe, fresh ? vn[e] : (float)vb[e], o[e]);
+                        }
+                    }
+                    m = bmax;
+                }
+            }
             for (int t0 = kPref; t0 < steps; t0 += kKvRing) {
 #pragma unroll
                 for (int r = 0; r < kKvRing; ++r) {
@@ -810,8 +856,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             } else if (tid < HD) {
                 put(rsrc(f_att, (uint32_t)HO * 4), h * HD + tid, L > 0.f ? acc / L : 0.f, tag);
             }
-            // This split's K/V rows are consumed: the next layer's go to LDS now.
-            wait_lds();
+            // This split's K/V rows are consumed: the next layer's go to LDS now, once
+            // this wave's output stores have completed (requests queued behind a
+            // prefetch of the K/V rows would reach the consumers later).
+            __builtin_amdgcn_s_waitcnt(0);
             if (l + 1 < p.L) kv_fetch(s_layers[l + 1]);
             if (!all_ok(mok, &s_fail)) return;
         }
