@@ -177,14 +177,19 @@ def bench_gemv(torch, ortmi, steps, warmup, shard=1):
                 launches=n, gbs=gbs, inputs=(A, B, s, zp))
 
 
-def bench_gemm(torch, ortmi, steps, warmup):
+def bench_gemm(torch, ortmi, steps, warmup, bf16=False):
+    """The prefill GEMM config (fp16), or the same shape in bf16 (activations and
+    scales rounded to bf16, the bf16 matrix-core path)."""
     import ctypes
 
     wl = sys.modules["ortmi.workloads"]
     M, K, N = 512, 4096, 4096
     A, B, s, zp = wl.mnb_gemm_config()
-    dA, dB, ds, dz = (torch.from_numpy(x).cuda() for x in (A, B, s, zp))
-    Y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    tdt = torch.bfloat16 if bf16 else torch.float16
+    dA, ds = (torch.from_numpy(x).to(tdt).cuda() for x in (A, s))
+    dB, dz = (torch.from_numpy(x).cuda() for x in (B, zp))
+    Y = torch.empty((M, N), dtype=tdt, device="cuda")
+    code = 16 if bf16 else 10
     lib = ortmi.load_kernels()
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     a = (ptr(dA), ptr(dB), ptr(ds), ptr(dz), ptr(Y))
@@ -192,7 +197,7 @@ def bench_gemm(torch, ortmi, steps, warmup):
     def launch_batch():
         st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         for _ in range(10):
-            rc = lib.ortmi_matmul_nbits(*a, M, N, K, 4, 32, 10, st)
+            rc = lib.ortmi_matmul_nbits(*a, M, N, K, 4, 32, code, st)
             if rc:
                 raise RuntimeError(lib.ortmi_last_error().decode())
 
@@ -518,6 +523,14 @@ def main():
                          "peak": FP16_DENSE_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(r["mfma_frac"], 4)}}
         log(f"gemm: {r['tflops']:.1f} TFLOP/s ({r['gpu_ms'] * 1e3:.2f} us/call)")
+        r = bench_gemm(torch, ortmi, args.steps, args.warmup, bf16=True)
+        secondary["mnb_gemm_prefill_bf16"] = {
+            "config": "the same GEMM in bf16 (activations and scales rounded to bf16)",
+            "tflops": round(r["tflops"], 2), "us_per_call": round(r["gpu_ms"] * 1e3, 2),
+            "roofline": {"bound": "mfma", "achieved": round(r["tflops"], 2),
+                         "peak": FP16_DENSE_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(r["mfma_frac"], 4)}}
+        log(f"gemm bf16: {r['tflops']:.1f} TFLOP/s ({r['gpu_ms'] * 1e3:.2f} us/call)")
     if wl in ("all", "gqa"):
         r = bench_gqa(torch, ortmi, args.steps, args.warmup)
         secondary["gqa_decode"] = {

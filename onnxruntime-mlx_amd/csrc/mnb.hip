@@ -15,12 +15,12 @@
 //    s*(sum(a*q) - zp*sum(a)), one byte-convert and one FMA per code. fp16
 //    activations: codes become exact fp16 (q - zp) pairs and v_dot2_f32_f16
 //    takes two codes per instruction.
-//  * mnb_gemm4  - prefill (M > 1, fp16), bits 4, bs in {32, 64, 128}. MFMA
-//    v_mfma_f32_32x32x16_f16: the weight tile is dequantised to fp16 in LDS
-//    (fp16((q - zp) * s), one rounding) and the activation tile is staged in LDS;
-//    fp32 accumulation, one rounding of Y.
-//  * mnb_generic - every other form (bits 8, bs 16, fp32/bf16 prefill): fp32
-//    dequant to LDS and a VALU tile product.
+//  * mnb_gemm4  - prefill (M > 1, fp16 or bf16), bits 4, bs in {32, 64, 128}.
+//    MFMA v_mfma_f32_32x32x16_f16 / _bf16: the weight tile is dequantised to the
+//    activation dtype (fp16((q - zp) * s) or bf16((q - zp) * s), one rounding)
+//    and the activation tile is staged in LDS; fp32 accumulation, one rounding of Y.
+//  * mnb_generic - every other form (bits 8, bs 16, fp32 prefill): fp32 dequant
+//    to LDS and a VALU tile product.
 #include "common.h"
 
 namespace ortmi {
@@ -633,6 +633,60 @@ __device__ __forceinline__ uint4 dequant_word_pairs(uint32_t w, half2_t zoff, ha
 }
 
 
+// bf16 weights: (q - zp) is formed exactly in fp16 as above, widened and scaled
+// in fp32, and rounded once to bf16 (bf16((q - zp) * s)).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint4 dequant_word_pairs_bf16(uint32_t w, half2_t zoff, float s) {
+    uint32_t r[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t m = ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+        const half2_t h = __builtin_bit_cast(half2_t, m) - zoff;
+        const bf16x2_t v = {(__bf16)((float)h.x * s), (__bf16)((float)h.y * s)};
+        r[j] = __builtin_bit_cast(uint32_t, v);
+    }
+    return make_uint4(r[0], r[1], r[2], r[3]);
+}
+
+// Per-element-type pieces of the MFMA GEMM: T = half_t (fp16) or uint16_t (bf16
+// bits). A block's dequantisation parameters, one word of codes to four operand
+// pairs, and the 32x32x16 matrix-core step.
+template <typename T>
+struct GemmDq {
+    half2_t zoff;
+    half2_t s2;  // fp16: the scale as a pair
+    float s;     // bf16: the scale in fp32
+};
+template <typename T>
+__device__ __forceinline__ GemmDq<T> gemm_dq(float zf, uint16_t sbits) {
+    GemmDq<T> d;
+    d.zoff = half2_t{(half_t)(1024.f + zf), (half_t)(1024.f + zf)};
+    if constexpr (std::is_same<T, half_t>::value) {
+        const half_t sh = __builtin_bit_cast(half_t, sbits);
+        d.s2 = half2_t{sh, sh};
+        d.s = 0.f;
+    } else {
+        d.s2 = half2_t{(half_t)0.f, (half_t)0.f};
+        d.s = to_f32(sbits);
+    }
+    return d;
+}
+template <typename T>
+__device__ __forceinline__ uint4 gemm_dequant(uint32_t w, const GemmDq<T>& d) {
+    if constexpr (std::is_same<T, half_t>::value) return dequant_word_pairs(w, d.zoff, d.s2);
+    else return dequant_word_pairs_bf16(w, d.zoff, d.s);
+}
+template <typename T>
+__device__ __forceinline__ float16_t gemm_mfma(half8_t a, half8_t b, float16_t c) {
+    if constexpr (std::is_same<T, half_t>::value)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0,
+                                                       0);
+}
+
 // One k-step's loads, kept raw until they are stored to LDS (a conversion at load
 // time would make the compiler wait for this load, and so for every earlier one).
 template <int BM, int BN, int BS>
@@ -656,14 +710,15 @@ struct GemmStage {
 // operands (word kk of the chunk for sub-step kk). Only the activation tile goes
 // through LDS, read at column 32 (l >> 5) + 8 kk so that both operands take the
 // same codes in each k slot.
-template <int BM, int BN, int BS, int KS = 1, bool SWI = false, bool BR = false>
-__global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __restrict__ A,
+template <typename T, int BM, int BN, int BS, int KS = 1, bool SWI = false, bool BR = false>
+__global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const T* __restrict__ A,
                                                              const uint8_t* __restrict__ B,
-                                                             const half_t* __restrict__ S,
+                                                             const T* __restrict__ S,
                                                              const uint8_t* __restrict__ Z,
-                                                             half_t* __restrict__ Y, int M,
+                                                             T* __restrict__ Y, int M,
                                                              int N, int K, int nb, int tiles_m,
                                                              int tiles_n) {
+    static_assert(sizeof(T) == 2, "fp16 or bf16 (16-bit storage)");
     // Each k-step stages BN weight rows x 2 chunks of 32 codes: one chunk per thread
     // (BN = 128) or half a chunk per thread (BN = 64).
     static_assert(BN == 128 || BN == 64, "weight tile rows");
@@ -707,11 +762,11 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
     const uint32_t s_end = (uint32_t)((size_t)N * nb * sizeof(half_t));
     const uint32_t z_end = Z ? (uint32_t)((size_t)N * zp_cols) : 0u;
     const __amdgpu_buffer_rsrc_t ra =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(A), 0, (int)a_end, kBufferWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(A), 0, (int)a_end, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rb =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(B), 0, (int)b_end, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(S), 0, (int)s_end, kBufferWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(S), 0, (int)s_end, kBufferWord3);
     const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(Z ? Z : B), 0, (int)z_end, kBufferWord3);
 
@@ -766,21 +821,19 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
         }
         if constexpr (!BR) {
             const float zf = Z ? (float)nibble(st.z, st.zhi) : 8.f;
-            const half_t sh = __builtin_bit_cast(half_t, st.s);
-            const half2_t zoff = {(half_t)(1024.f + zf), (half_t)(1024.f + zf)};
-            const half2_t s2 = {sh, sh};
+            const GemmDq<T> dq = gemm_dq<T>(zf, st.s);
             if constexpr (BN == 128) {
                 const int r = tid >> 1, h = tid & 1;
                 uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32]);
-                dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
-                dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
-                dst[2] = dequant_word_pairs(st.b.z, zoff, s2);
-                dst[3] = dequant_word_pairs(st.b.w, zoff, s2);
+                dst[0] = gemm_dequant<T>(st.b.x, dq);
+                dst[1] = gemm_dequant<T>(st.b.y, dq);
+                dst[2] = gemm_dequant<T>(st.b.z, dq);
+                dst[3] = gemm_dequant<T>(st.b.w, dq);
             } else {
                 const int r = tid >> 2, h = (tid >> 1) & 1, q = tid & 1;
                 uint4* dst = reinterpret_cast<uint4*>(&sB[buf][r * kLdsRow + h * 32 + q * 16]);
-                dst[0] = dequant_word_pairs(st.b.x, zoff, s2);
-                dst[1] = dequant_word_pairs(st.b.y, zoff, s2);
+                dst[0] = gemm_dequant<T>(st.b.x, dq);
+                dst[1] = gemm_dequant<T>(st.b.y, dq);
             }
         }
     };
@@ -798,14 +851,12 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
     uint4 bq[BR ? 4 : 1];
     auto dequant_b = [&](const Stage& st) {
         const float zf = Z ? (float)nibble(st.z, st.zhi) : 8.f;
-        const half_t sh = __builtin_bit_cast(half_t, st.s);
-        const half2_t zoff = {(half_t)(1024.f + zf), (half_t)(1024.f + zf)};
-        const half2_t s2 = {sh, sh};
-        bq[0] = dequant_word_pairs(st.b.x, zoff, s2);
+        const GemmDq<T> dq = gemm_dq<T>(zf, st.s);
+        bq[0] = gemm_dequant<T>(st.b.x, dq);
         if constexpr (BR) {
-            bq[1] = dequant_word_pairs(st.b.y, zoff, s2);
-            bq[2] = dequant_word_pairs(st.b.z, zoff, s2);
-            bq[3] = dequant_word_pairs(st.b.w, zoff, s2);
+            bq[1] = gemm_dequant<T>(st.b.y, dq);
+            bq[2] = gemm_dequant<T>(st.b.z, dq);
+            bq[3] = gemm_dequant<T>(st.b.w, dq);
         }
     };
     auto compute = [&](int buf) {
@@ -829,8 +880,7 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0,
-                                                                       0, 0);
+                    acc[i][j] = gemm_mfma<T>(af[i], bf[j], acc[i][j]);
         }
     };
 
@@ -902,13 +952,12 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
                 const int n = n0 + wn + j * 32 + (lane & 31);
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const float y = (float)(half_t)acc[i][j][e];
+                    const float y = round_to<T>(acc[i][j][e]);
                     const float partner = dpp_mov<0xB1>(y);  // quad_perm [1,0,3,2]
                     const int m = m0 + wm + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
                     if ((lane & 1) == 0 && m < M && n < N) {
-                        const float sig = (float)(half_t)(1.0f / (1.0f + __expf(-y)));
-                        Y[(size_t)m * Nh + n / 2] =
-                            (half_t)((float)(half_t)(y * sig) * partner);
+                        const float sig = round_to<T>(1.0f / (1.0f + __expf(-y)));
+                        Y[(size_t)m * Nh + n / 2] = from_f32<T>(round_to<T>(y * sig) * partner);
                     }
                 }
             }
@@ -922,23 +971,23 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const half_t* __res
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int m = m0 + wm + i * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-                if (m < M && n < N) Y[(size_t)m * N + n] = (half_t)acc[i][j][e];
+                if (m < M && n < N) Y[(size_t)m * N + n] = from_f32<T>(acc[i][j][e]);
             }
         }
 }
 
-template <int BM, int BN, int BS, int KS = 1, bool SWI = false, bool BR = false>
-static int launch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, const uint8_t* Z,
-                        half_t* Y, int M, int N, int K, int nb, hipStream_t st) {
+template <typename T, int BM, int BN, int BS, int KS = 1, bool SWI = false, bool BR = false>
+static int launch_gemm4(const T* A, const uint8_t* B, const T* S, const uint8_t* Z,
+                        T* Y, int M, int N, int K, int nb, hipStream_t st) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    hipLaunchKernelGGL((mnb_gemm4_kernel<BM, BN, BS, KS, SWI, BR>), dim3(tiles_m * tiles_n),
+    hipLaunchKernelGGL((mnb_gemm4_kernel<T, BM, BN, BS, KS, SWI, BR>), dim3(tiles_m * tiles_n),
                        dim3(256 * KS), 0, st, A, B, S, Z, Y, M, N, K, nb, tiles_m, tiles_n);
     return check_launch("mnb_gemm4");
 }
 
-template <int BS, bool SWI = false>
-static int dispatch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, const uint8_t* Z,
-                          half_t* Y, int M, int N, int K, int nb, hipStream_t st) {
+template <typename T, int BS, bool SWI = false>
+static int dispatch_gemm4(const T* A, const uint8_t* B, const T* S, const uint8_t* Z,
+                          T* Y, int M, int N, int K, int nb, hipStream_t st) {
     // 128x128 tiles once they fill the CUs twice over; below that, the k-steps are
     // split over two wave groups, with 64x128 tiles while those still give every
     // CU a tile and 64x64 tiles under that (M=512 on MI355X: K=N=4096 41.6 us
@@ -949,10 +998,10 @@ static int dispatch_gemm4(const half_t* A, const uint8_t* B, const half_t* S, co
     // 128x128 tiles take their weights in registers (gate/up 512x17920x1536:
     // 52-54 -> 46-47 us); at 64x128 the LDS form measured equal or faster.
     if (big >= 2L * cus)
-        return launch_gemm4<128, 128, BS, 1, SWI, true>(A, B, S, Z, Y, M, N, K, nb, st);
+        return launch_gemm4<T, 128, 128, BS, 1, SWI, true>(A, B, S, Z, Y, M, N, K, nb, st);
     const long mid = (long)((M + 63) / 64) * ((N + 127) / 128);
-    if (mid >= cus) return launch_gemm4<64, 128, BS, 2, SWI>(A, B, S, Z, Y, M, N, K, nb, st);
-    return launch_gemm4<64, 64, BS, 2, SWI>(A, B, S, Z, Y, M, N, K, nb, st);
+    if (mid >= cus) return launch_gemm4<T, 64, 128, BS, 2, SWI>(A, B, S, Z, Y, M, N, K, nb, st);
+    return launch_gemm4<T, 64, 64, BS, 2, SWI>(A, B, S, Z, Y, M, N, K, nb, st);
 }
 
 // ----------------------------------------------------------------- generic --
@@ -1046,14 +1095,14 @@ static int run_mnb(const void* A, const uint8_t* B, const void* S, const uint8_t
         if (bs == 128) rc = launch_gemv4<T, 128>(a, B, s, Z, y, N, K, nb, st);
         if (rc >= 0) return rc;
     }
-    if constexpr (sizeof(T) == 2 && !std::is_same<T, uint16_t>::value) {
+    if constexpr (sizeof(T) == 2) {  // fp16 and bf16 prefill on the matrix cores
         const bool a_aligned = (reinterpret_cast<uintptr_t>(A) % 16) == 0 && K % 8 == 0;
         const bool fits32 = (size_t)M * K * 2 <= 0xFFFFFF00ull &&
                             (size_t)N * nb * bs / 2 <= 0xFFFFFF00ull;  // 32-bit buffer offsets
         if (fast_form && M > 1 && a_aligned && fits32) {
-            if (bs == 32) return dispatch_gemm4<32>(a, B, s, Z, y, M, N, K, nb, st);
-            if (bs == 64) return dispatch_gemm4<64>(a, B, s, Z, y, M, N, K, nb, st);
-            if (bs == 128) return dispatch_gemm4<128>(a, B, s, Z, y, M, N, K, nb, st);
+            if (bs == 32) return dispatch_gemm4<T, 32>(a, B, s, Z, y, M, N, K, nb, st);
+            if (bs == 64) return dispatch_gemm4<T, 64>(a, B, s, Z, y, M, N, K, nb, st);
+            if (bs == 128) return dispatch_gemm4<T, 128>(a, B, s, Z, y, M, N, K, nb, st);
         }
     }
     return launch_generic<T>(a, B, s, Z, y, M, N, K, nb, bits, bs, st);
@@ -1213,9 +1262,11 @@ extern "C" int ortmi_matmul_nbits_swiglu_pairs(const void* A, const uint8_t* B,
     half_t* y = static_cast<half_t*>(Y);
     hipStream_t st = as_stream(stream);
     const int m = (int)M, n = (int)N, k = (int)K;
-    if (block_size == 32) return dispatch_gemm4<32, true>(a, B, s, zero_points, y, m, n, k, nb, st);
-    if (block_size == 64) return dispatch_gemm4<64, true>(a, B, s, zero_points, y, m, n, k, nb, st);
-    return dispatch_gemm4<128, true>(a, B, s, zero_points, y, m, n, k, nb, st);
+    if (block_size == 32)
+        return dispatch_gemm4<half_t, 32, true>(a, B, s, zero_points, y, m, n, k, nb, st);
+    if (block_size == 64)
+        return dispatch_gemm4<half_t, 64, true>(a, B, s, zero_points, y, m, n, k, nb, st);
+    return dispatch_gemm4<half_t, 128, true>(a, B, s, zero_points, y, m, n, k, nb, st);
 }
 
 extern "C" int ortmi_matmul_nbits(const void* A, const uint8_t* B, const void* scales,

@@ -325,8 +325,10 @@ def test_mnb_gemm_swiglu_pairs(ortmi, oracle, M, N, K, block):
                                             (1000, 130, 128, True), (8960, 64, 32, False)])
 def test_mnb_bf16(ortmi, oracle, M, K, N, block, asym):
     """bf16 activations and scales (M = 1: the decode GEMV and its fp8-convert dot
-    product; M > 1: the generic kernel) against the oracle run on the same bf16
-    values: within the output's bf16 rounding plus fp32 accumulation."""
+    product; M > 1: the matrix-core GEMM, which rounds each dequantised weight to
+    bf16 once) against the oracle run on the same bf16 values: within the output's
+    bf16 rounding plus fp32 accumulation, plus 2^-9 sum |a w| for that weight
+    rounding when M > 1."""
     import torch
 
     rng = np.random.default_rng(M * 7 + K + N + block)
@@ -339,8 +341,41 @@ def test_mnb_bf16(ortmi, oracle, M, K, N, block, asym):
     ref = oracle.mnb_matmul(A_r, B, s_r, zp if asym else None, N, K, 4, block)
     W = refs.dequant_ref(B, s_r, zp if asym else None, N, K, 4, block)
     accum = 2.0 ** -18 * (np.abs(A_r.astype(np.float64)) @ np.abs(W).T)
-    bound = 2.0 ** -8 * np.abs(ref) + accum
+    wround = 2.0 ** -9 * (np.abs(A_r.astype(np.float64)) @ np.abs(W).T) if M > 1 else 0.0
+    bound = 2.0 ** -8 * np.abs(ref) + accum + wround
     assert (np.abs(got - ref) <= bound).all(), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("M,K,N,block", [(64, 512, 256, 32), (130, 1176, 64, 32),
+                                         (40, 1024, 384, 64), (96, 768, 200, 128),
+                                         (512, 4096, 4096, 32)])
+def test_mnb_gemm_bf16(ortmi, oracle, M, K, N, block):
+    """bf16 prefill on the matrix cores (v_mfma_f32_32x32x16_bf16), zero points
+    U{0..15}. Primary check: against fp64 A . Wbf16^T with the dequantised weights
+    rounded to bf16 once, as the kernel feeds them, within the output's bf16
+    rounding plus fp32 accumulation. Secondary: against the oracle's exact
+    dequantisation, plus the rigorous bound 2^-9 sum |a w| of that rounding."""
+    import torch
+
+    rng = np.random.default_rng(M + K + N + block)
+    A, B, s, zp = _mnb_inputs(rng, M, N, K, block)
+    tA = torch.from_numpy(A).to(torch.bfloat16)
+    ts = torch.from_numpy(s).to(torch.bfloat16)
+    A_r, s_r = tA.float().numpy(), ts.float().numpy()
+    got = host(ortmi.matmul_nbits(tA.cuda(), dev(B), ts.cuda(), dev(zp), K=K, N=N,
+                                  block_size=block))
+    rows = np.r_[np.arange(0, M, max(1, M // 24)), M - 1]
+    W = refs.dequant_ref(B, s_r, zp, N, K, 4, block)
+    Wb = torch.from_numpy(W.astype(np.float32)).to(torch.bfloat16).double().numpy()
+    Ar = A_r[rows].astype(np.float64)
+    accum = 2.0 ** -18 * (np.abs(Ar) @ np.abs(W).T)
+    want = Ar @ Wb.T
+    bound = 2.0 ** -8 * np.abs(want) + accum + 1e-30
+    bad = np.abs(got[rows] - want) > bound
+    assert not bad.any(), f"bf16 gemm (bf16 weights): max diff {np.abs(got[rows] - want).max():.3e}"
+    ref = oracle.mnb_matmul(A_r[rows], B, s_r, zp, N, K, 4, block)
+    bound2 = 2.0 ** -8 * np.abs(ref) + accum + 2.0 ** -9 * (np.abs(Ar) @ np.abs(W).T)
+    assert (np.abs(got[rows] - ref) <= bound2).all(), np.abs(got[rows] - ref).max()
 
 
 @pytest.mark.parametrize("M,bits,block", [(1, 8, 32), (3, 8, 64), (1, 4, 16), (5, 4, 16)])
