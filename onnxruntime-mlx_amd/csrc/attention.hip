@@ -869,9 +869,13 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
     // Earliest position among the wave's queries: keys up to it are causally
     // visible to every query of the wave.
     const int qpos_wave = t.qpos0 + (wave * 32) / G;
-    // Scores are kept in the log2 domain (exp2 is the hardware exponential).
+    // Scores are kept in the log2 domain (exp2 is the hardware exponential). The
+    // scale is applied inside the exponent, after the block maximum of the raw
+    // scores, which needs it positive: a negative scale flips the sign of Q as it
+    // is staged (exact in fp16) and scales by its magnitude.
     constexpr float kLog2e = 1.4426950408889634f;
-    const float sc2 = scale * kLog2e;
+    const float sc2 = fabsf(scale) * kLog2e;
+    const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
     // Q^T operand: the tile's query rows are staged in LDS once (zeros past the
     // last row) and each k-step reads its 8 head dims from there, which keeps
     // HD / 2 VGPRs free for the whole key walk.
@@ -880,11 +884,11 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
         constexpr int CPR = HD / 8;  // 16-byte chunks per row
         for (int i = tid; i < kRows * CPR; i += NT) {
             const int r = i / CPR, c = i % CPR;
-            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            u32x4_t v = {0u, 0u, 0u, 0u};
             if (r < rows)
-                v = *reinterpret_cast<const uint4*>(
+                v = *reinterpret_cast<const u32x4_t*>(
                     qrot + ((int64_t)(t.tok0 + r / G) * H + kvh * G + r % G) * HD + c * 8);
-            *reinterpret_cast<uint4*>(&sQ[r * KP + c * 8]) = v;
+            *reinterpret_cast<u32x4_t*>(&sQ[r * KP + c * 8]) = v ^ qsign;
         }
     }
     float m = -INFINITY;
@@ -893,226 +897,299 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
     for (int d = 0; d < DT; ++d)
 #pragma unroll
         for (int e = 0; e < 16; ++e) oT[d][e] = 0.f;
-    // Running softmax sums: every element of lT holds this lane's query's sum.
-    float16_t lT;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) lT[e] = 0.f;
-    half8_t ones;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ones[i] = (half_t)1.f;
+    // Running softmax sum over this lane's keys (its 32 of each 64-key block); the
+    // two lanes of a query add theirs at the end.
+    float lsum = 0.f;
 
     constexpr int KPT = kKeyTile * (HD / 8) / NT, VPT = kKeyTile * (VHD / 8) / NT;
     static_assert(KPT >= 1 && VPT >= 1, "block staging");
-    uint4 kreg[KPT], vreg[VPT];
+    // Native vectors, not uint4: a struct-typed copy keeps these arrays in memory
+    // (the compiler moved them to LDS or scratch, and waited on every prefetch to
+    // store it there); as vectors they stay in registers.
+    u32x4_t kreg[KPT], vreg[VPT];
     int kok = 0, vok = 0;
     // Paged rows: the block-table entries of keys [k0, min(k1, past)) are staged in
-    // LDS once (power-of-two block sizes), so a row costs an LDS read and a shift.
+    // LDS once, as the cache row index of row 0 of (block, kv head), phys * blk * KV
+    // + kvh, or ~0u for an entry out of range; a row then costs an LDS read, a
+    // shift (a division for block sizes that are not powers of two) and 32-bit
+    // integer work. A range of more than kBtLds blocks, or a cache of 2^32 rows
+    // or more, reads the table from global memory instead (the second form of the
+    // walk below).
     constexpr int kBtLds = 512;
-    __shared__ int s_bt[PAGED ? kBtLds : 1];
+    __shared__ uint32_t s_bt[PAGED ? kBtLds : 1];
     int lb0 = 0;
-    bool bt_lds = false;
+    bool bt_lds = true;
     if constexpr (PAGED) {
         const int cend = min(k1, t.past);
-        if (cend > k0 && pk.blk_shift >= 0) {
-            lb0 = k0 >> pk.blk_shift;
-            const int n = ((cend - 1) >> pk.blk_shift) - lb0 + 1;
-            if (n <= kBtLds) {
-                bt_lds = true;
+        if (cend > k0) {
+            lb0 = k0 / pk.blk;
+            const int n = (cend - 1) / pk.blk - lb0 + 1;
+            bt_lds = n <= kBtLds && pk.nblk * pk.blk * pk.KV < (int64_t)0xffffffff;
+            if (bt_lds)
                 for (int i = tid; i < n; i += NT) {
                     const int lb = lb0 + i;
-                    s_bt[i] = lb < pk.maxb ? pk.bt[(int64_t)t.seq * pk.maxb + lb] : -1;
+                    const int phys = lb < pk.maxb ? pk.bt[(int64_t)t.seq * pk.maxb + lb] : -1;
+                    s_bt[i] = phys >= 0 && phys < pk.nblk
+                                  ? ((uint32_t)phys * (uint32_t)pk.blk) * (uint32_t)pk.KV + kvh
+                                  : ~0u;
                 }
-            }
         }
         __syncthreads();
     }
+    // Byte address of new row 0 of the sequence's (virtual) new-row range, such
+    // that key j >= past is at nrow0 + j * nstride (modular arithmetic).
+    // Cache and new rows, keys and values alike, are HD dims apart: with a value
+    // cache VHD equals HD (the entry point checks it), and without one the values
+    // are the leading VHD dims of the key rows.
+    constexpr uint32_t kRowBytes = HD * 2;
+    // (Pointer arithmetic, not integers, so the loads stay global loads: a flat
+    // load would also count against every LDS wait.)
+    const uint32_t nstride = (uint32_t)pk.KV * HD * 2;
+    const int64_t nrow0 = ((int64_t)(t.tok_seq0 - t.past) * pk.KV + kvh) * HD * 2;
+    const char* nrow_k = static_cast<const char*>(pk.knew) + nrow0;
+    const char* nrow_v = static_cast<const char*>(pk.vnew ? pk.vnew : pk.knew) + nrow0;
     // Source row of key j (k0 <= j < k1): always a valid address; `ok` is false
-    // for a row whose block-table entry is out of range (block 0 stands in).
-    auto row_src = [&](int j, bool value, bool& ok) -> const half_t* {
+    // for a row whose block-table entry is out of range (block 0 stands in). Both
+    // candidates (the sequence's new row, the cache row) are formed and one is
+    // selected, with no branch. With the table in LDS (`lds` true) forming an
+    // address issues no global load: a global load between two K/V loads would
+    // make the wait for its table entry wait for the K/V loads issued before it
+    // (loads retire in order), and the block's loads would run one at a time.
+    auto row_src = [&](int j, bool value, bool& ok, auto lds) -> const half_t* {
         if constexpr (!PAGED) {
             ok = true;
             const half_t* base = static_cast<const half_t*>(value ? dk.v : dk.k);
             return base + (((int64_t)t.seq * dk.KV + kvh) * dk.cap + j) * (value ? VHD : HD);
         } else {
-            if (j >= t.past) {
-                ok = true;
-                const int tok = t.tok_seq0 + (j - t.past);
-                if (value && pk.vnew)
-                    return static_cast<const half_t*>(pk.vnew) + ((int64_t)tok * pk.KV + kvh) * VHD;
-                return static_cast<const half_t*>(pk.knew) + ((int64_t)tok * pk.KV + kvh) * HD;
-            }
-            int phys, within;
-            if (bt_lds) {
-                phys = s_bt[(j >> pk.blk_shift) - lb0];
-                within = j & ((1 << pk.blk_shift) - 1);
+            const bool fresh = j >= t.past;
+            const int jc = fresh ? k0 : j;  // a cache row stands in for a new one
+            int lb, within;
+            if (pk.blk_shift >= 0) {
+                lb = jc >> pk.blk_shift;
+                within = jc & ((1 << pk.blk_shift) - 1);
             } else {
-                const int lb = j / pk.blk;
-                phys = lb < pk.maxb ? pk.bt[(int64_t)t.seq * pk.maxb + lb] : -1;
-                within = j - lb * pk.blk;
+                lb = jc / pk.blk;
+                within = jc - lb * pk.blk;
             }
-            ok = phys >= 0 && phys < pk.nblk;
-            const int64_t slot = (int64_t)(ok ? phys : 0) * pk.blk + within;
-            if (value && pk.vcache)
-                return static_cast<const half_t*>(pk.vcache) + (slot * pk.KV + kvh) * VHD;
-            return static_cast<const half_t*>(pk.kcache) + (slot * pk.KV + kvh) * HD;
+            const char* ac;
+            bool cok;
+            if constexpr (decltype(lds)::value) {
+                const uint32_t e = s_bt[min((unsigned)(lb - lb0), (unsigned)(kBtLds - 1))];
+                cok = e != ~0u;
+                const uint32_t r = (cok ? e : 0u) + __umul24((uint32_t)within, (uint32_t)pk.KV);
+                const char* cb = static_cast<const char*>((value && pk.vcache) ? pk.vcache : pk.kcache);
+                ac = cb + (uint64_t)r * kRowBytes;
+            } else {
+                // maxb >= 1 (the entry point checks it), so the clamped index is in range.
+                const int e = pk.bt[(int64_t)t.seq * pk.maxb + min(lb, pk.maxb - 1)];
+                const int phys = lb < pk.maxb ? e : -1;
+                cok = phys >= 0 && phys < pk.nblk;
+                const int64_t slot = (int64_t)(cok ? phys : 0) * pk.blk + within;
+                const char* cb = static_cast<const char*>((value && pk.vcache) ? pk.vcache : pk.kcache);
+                ac = cb + (uint64_t)(slot * pk.KV + kvh) * kRowBytes;
+            }
+            const char* an = (value ? nrow_v : nrow_k) + (uint64_t)(uint32_t)j * (uint64_t)nstride;
+            ok = fresh || cok;
+            return reinterpret_cast<const half_t*>(fresh ? an : ac);
         }
     };
-    // Loads are never conditional (a branch around a load makes the compiler drain
-    // every prefetch at the join): rows past the block end load its last row again,
-    // and the validity bits mask keys (sOk) and zero values at commit.
-    auto fetch = [&](int kb) {
+    // A 64-key block into registers, keys and values separately: the row addresses
+    // first, then the loads back to back. Loads are never conditional (a branch
+    // around a load makes the compiler drain every prefetch at the join): rows past
+    // the block end load its last row again, and the validity bits mask keys (sOk)
+    // and zero values at commit. A thread stages one key row (NT is a multiple of
+    // the block) and VPT consecutive value rows of one 8-dim chunk, so the
+    // transposed store writes VPT keys of a head dim at once.
+    static_assert(NT % kKeyTile == 0, "one key row per thread");
+    auto fetch_k = [&](int kb, auto lds) {
         const int nk = min(kKeyTile, k1 - kb);
-        kok = 0;
+        const int rk = tid % kKeyTile;
+        bool okk;
+        const half_t* pkr = row_src(kb + min(rk, nk - 1), false, okk, lds);
 #pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-            const int idx = tid + NT * i, r = idx % kKeyTile, c = (idx / kKeyTile) * 8;
-            bool ok;
-            const half_t* p = row_src(kb + min(r, nk - 1), false, ok);
-            kreg[i] = *reinterpret_cast<const uint4*>(p + c);
-            kok |= (int)(ok && r < nk) << i;
-        }
-        // V: a thread takes VPT consecutive keys of one 8-dim chunk, so the
-        // transposed store writes VPT keys of a head dim at once.
+        for (int i = 0; i < KPT; ++i)
+            kreg[i] = *reinterpret_cast<const u32x4_t*>(pkr + ((tid + NT * i) / kKeyTile) * 8);
+        kok = okk && rk < nk;
+    };
+    auto fetch_v = [&](int kb, auto lds) {
+        const int nk = min(kKeyTile, k1 - kb);
+        const int rv = VPT * (tid % (kKeyTile / VPT)), cv = (tid / (kKeyTile / VPT)) * 8;
+        bool okv[VPT];
+        const half_t* pvr[VPT];
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) pvr[i] = row_src(kb + min(rv + i, nk - 1), true, okv[i], lds);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) vreg[i] = *reinterpret_cast<const u32x4_t*>(pvr[i] + cv);
         vok = 0;
 #pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int r = VPT * (tid % (kKeyTile / VPT)) + i, c = (tid / (kKeyTile / VPT)) * 8;
-            bool ok;
-            const half_t* p = row_src(kb + min(r, nk - 1), true, ok);
-            vreg[i] = *reinterpret_cast<const uint4*>(p + c);
-            vok |= (int)(ok && r < nk) << i;
-        }
+        for (int i = 0; i < VPT; ++i) vok |= (int)(okv[i] && rv + i < nk) << i;
     };
-    auto commit = [&]() {
+    auto commit_k = [&]() {
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int idx = tid + NT * i, r = idx % kKeyTile, c = (idx / kKeyTile) * 8;
-            *reinterpret_cast<uint4*>(&sK[r * KP + c]) = kreg[i];
+            *reinterpret_cast<u32x4_t*>(&sK[r * KP + c]) = kreg[i];
         }
         // Threads 0..63 hold the first vector (c = 0) of keys 0..63: one ballot.
         const unsigned long long ok = __ballot(kok & 1);
         if (tid == 0) sOk = ok;
-        {
-            const int r0 = VPT * (tid % (kKeyTile / VPT)), c = (tid / (kKeyTile / VPT)) * 8;
+    };
+    auto commit_v = [&]() {
+        const int r0 = VPT * (tid % (kKeyTile / VPT)), c = (tid / (kKeyTile / VPT)) * 8;
 #pragma unroll
-            for (int i = 0; i < VPT; ++i)
-                if (!((vok >> i) & 1)) vreg[i] = make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < VPT; ++i)
+            if (!((vok >> i) & 1)) vreg[i] = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                half_t col[VPT];
+        for (int e = 0; e < 8; ++e) {
+            half_t col[VPT];
 #pragma unroll
-                for (int i = 0; i < VPT; ++i) col[i] = reinterpret_cast<const half_t*>(&vreg[i])[e];
-                if constexpr (VPT == 4)
-                    *reinterpret_cast<uint2*>(&sVt[(c + e) * VP + r0]) =
-                        *reinterpret_cast<const uint2*>(col);
-                else if constexpr (VPT == 2)
-                    *reinterpret_cast<uint32_t*>(&sVt[(c + e) * VP + r0]) =
-                        *reinterpret_cast<const uint32_t*>(col);
-                else
+            for (int i = 0; i < VPT; ++i) col[i] = __builtin_bit_cast(half8_t, vreg[i])[e];
+            if constexpr (VPT == 4)
+                *reinterpret_cast<uint2*>(&sVt[(c + e) * VP + r0]) =
+                    *reinterpret_cast<const uint2*>(col);
+            else if constexpr (VPT == 2)
+                *reinterpret_cast<uint32_t*>(&sVt[(c + e) * VP + r0]) =
+                    *reinterpret_cast<const uint32_t*>(col);
+            else
 #pragma unroll
-                    for (int i = 0; i < VPT; ++i) sVt[(c + e) * VP + r0 + i] = col[i];
-            }
+                for (int i = 0; i < VPT; ++i) sVt[(c + e) * VP + r0 + i] = col[i];
         }
     };
-    if (k0 < k1) fetch(k0);
-    for (int kb = k0; kb < k1; kb += kKeyTile) {
-        commit();
-        __syncthreads();
-        if (kb + kKeyTile < k1) fetch(kb + kKeyTile);
-        const unsigned long long okm = sOk;
-        // S^T for the two 32-key tiles.
-        float16_t st[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) st[kt][e] = 0.f;
-#pragma unroll
-            for (int s2 = 0; s2 < HD / 16; ++s2) {
-                const half8_t a =
-                    *reinterpret_cast<const half8_t*>(&sK[(kt * 32 + lrow) * KP + s2 * 16 + lk]);
-                const half8_t b =
-                    *reinterpret_cast<const half8_t*>(&sQ[q * KP + s2 * 16 + lk]);
-                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, st[kt], 0, 0, 0);
-            }
-        }
-        // Mask (only blocks that are not fully visible), scale, block max.
-        const bool full = kb + kKeyTile <= k1 && okm == ~0ull && kb + kKeyTile - 1 <= qpos_wave;
-        float bmax = -INFINITY;
-        if (full) {
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    st[kt][e] *= sc2;
-                    bmax = fmaxf(bmax, st[kt][e]);
-                }
-        } else {
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int kk = kt * 32 + 8 * (e / 4) + 4 * hh + (e & 3);
-                    const int j = kb + kk;
-                    const bool ok = j < k1 && j <= qpos && ((okm >> kk) & 1ull);
-                    const float x = ok ? st[kt][e] * sc2 : -INFINITY;
-                    st[kt][e] = x;
-                    bmax = fmaxf(bmax, x);
-                }
-        }
-        {
-            const LanePair pr = swap32(bmax);
-            bmax = fmaxf(pr.a, pr.b);
-        }
-        const float m_new = fmaxf(m, bmax);
-        // v_exp_f32 directly: results below 2^-126 flush to zero, which the
-        // softmax weights can afford.
-        const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
-        half8_t pb[4];  // P^T operands: k-step kk uses e in [8 (kk % 2), 8 (kk % 2) + 8) of tile kk / 2
-        const float mref = m_new == -INFINITY ? 0.f : m_new;  // exp2(-inf - 0) = 0
+    // S^T of the staged keys against this wave's queries (two 32-key tiles).
+    auto scores = [&](float16_t (&st)[2]) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                pb[kt * 2 + e / 8][e % 8] = (half_t)__builtin_amdgcn_exp2f(st[kt][e] - mref);
-        m = m_new;
-        // Rescale O (and the running sums) only when some query's running max moved.
-        if (__any(alpha != 1.f)) {
+            for (int e = 0; e < 16; ++e) st[kt][e] = 0.f;
 #pragma unroll
-            for (int d = 0; d < DT; ++d)
+        for (int s2 = 0; s2 < HD / 16; ++s2)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) oT[d][e] *= alpha;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) lT[e] *= alpha;
-        }
-        // Row sums on the matrix cores: a row of ones times P^T sums the same fp16
-        // probabilities that weight V, for every query at once.
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-            lT = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pb[kk], lT, 0, 0, 0);
-        // O^T += V^T P^T over the 4 k-steps of 16 keys.
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const int kbase = (kk / 2) * 32 + (kk % 2) * 16 + 4 * hh;
-#pragma unroll
-            for (int d = 0; d < DT; ++d) {
-                const half_t* vr = &sVt[(d * 32 + lrow) * VP + kbase];
-                const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-                const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
-                half8_t a;
-                const half_t* lo_h = reinterpret_cast<const half_t*>(&lo);
-                const half_t* hi_h = reinterpret_cast<const half_t*>(&hi);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    a[i] = lo_h[i];
-                    a[4 + i] = hi_h[i];
-                }
-                oT[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kk], oT[d], 0, 0, 0);
+            for (int kt = 0; kt < 2; ++kt) {
+                const half8_t a =
+                    *reinterpret_cast<const half8_t*>(&sK[(kt * 32 + lrow) * KP + s2 * 16 + lk]);
+                const half8_t b = *reinterpret_cast<const half8_t*>(&sQ[q * KP + s2 * 16 + lk]);
+                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, st[kt], 0, 0, 0);
             }
+    };
+    // The key walk, software-pipelined across blocks: while the matrix cores score
+    // block b + 1, the vector units run the softmax of block b, whose scores came
+    // from the previous step. Keys are therefore staged one block ahead of values:
+    // a step commits V(b) and K(b + 1), both into slots whose last readers finished
+    // before the previous barrier. Per-block work is unchanged; only its order is.
+    auto walk = [&](auto lds) {
+        if (k0 >= k1) return;
+        fetch_k(k0, lds);
+        fetch_v(k0, lds);
+        commit_k();
+        __syncthreads();
+        unsigned long long okm = sOk;
+        if (k0 + kKeyTile < k1) fetch_k(k0 + kKeyTile, lds);
+        float16_t stA[2], stB[2];
+        scores(stA);
+        __syncthreads();  // sK is restaged by the first step
+        auto step = [&](int kb, float16_t (&cur)[2], float16_t (&nxt)[2]) {
+            const bool more = kb + kKeyTile < k1;
+            commit_v();
+            if (more) commit_k();
+            __syncthreads();
+            const unsigned long long okm_next = sOk;
+            if (more) {
+                fetch_v(kb + kKeyTile, lds);
+                if (kb + 2 * kKeyTile < k1) fetch_k(kb + 2 * kKeyTile, lds);
+            }
+            // Keys of block kb that are out of range, causally hidden or behind an
+            // invalid block-table entry (only blocks that are not fully visible).
+            const bool full = kb + kKeyTile <= k1 && okm == ~0ull && kb + kKeyTile - 1 <= qpos_wave;
+            if (!full) {
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int kk = kt * 32 + 8 * (e / 4) + 4 * hh + (e & 3);
+                        const int j = kb + kk;
+                        const bool ok = j < k1 && j <= qpos && ((okm >> kk) & 1ull);
+                        cur[kt][e] = ok ? cur[kt][e] : -INFINITY;
+                    }
+            }
+            if (more) scores(nxt);
+            // Block max of the raw scores. Scaling by sc2 > 0 keeps the maximum (and
+            // rounds it alike), so the scale joins the exponent's argument in one fma.
+            float bmax = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) bmax = fmaxf(bmax, cur[kt][e]);
+            {
+                const LanePair pr = swap32(bmax);
+                bmax = fmaxf(pr.a, pr.b);
+            }
+            const float m_new = fmaxf(m, bmax * sc2);
+            // v_exp_f32 directly: results below 2^-126 flush to zero, which the
+            // softmax weights can afford.
+            const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
+            // P^T operands: k-step kk uses e in [8 (kk % 2), 8 (kk % 2) + 8) of tile kk / 2.
+            half8_t pb[4];
+            const float mref = m_new == -INFINITY ? 0.f : m_new;  // exp2(-inf - 0) = 0
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    pb[kt * 2 + e / 8][e % 8] =
+                        (half_t)__builtin_amdgcn_exp2f(fmaf(cur[kt][e], sc2, -mref));
+            m = m_new;
+            // Rescale O (and the running sums) only when some query's running max moved.
+            if (__any(alpha != 1.f)) {
+#pragma unroll
+                for (int d = 0; d < DT; ++d)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) oT[d][e] *= alpha;
+            }
+            // Row sums of the same fp16 probabilities that weight V, accumulated in
+            // fp32 (v_dot2_f32_f16 against ones, four independent chains).
+            {
+                const half2_t one2 = {(half_t)1.f, (half_t)1.f};
+                float ls[4];
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    ls[kk] = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        ls[kk] = __builtin_amdgcn_fdot2(
+                            half2_t{pb[kk][2 * i], pb[kk][2 * i + 1]}, one2, ls[kk], false);
+                }
+                lsum = fmaf(lsum, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
+            }
+            // O^T += V^T P^T over the 4 k-steps of 16 keys.
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int kbase = (kk / 2) * 32 + (kk % 2) * 16 + 4 * hh;
+#pragma unroll
+                for (int d = 0; d < DT; ++d) {
+                    const half_t* vr = &sVt[(d * 32 + lrow) * VP + kbase];
+                    const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
+                    const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 8);
+                    const half8_t a = __builtin_bit_cast(half8_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+                    oT[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kk], oT[d], 0, 0, 0);
+                }
+            }
+            okm = okm_next;
+            __syncthreads();  // the next step restages sK, sVt and sOk
+        };
+        for (int kb = k0; kb < k1; kb += 2 * kKeyTile) {
+            step(kb, stA, stB);
+            if (kb + kKeyTile < k1) step(kb + kKeyTile, stB, stA);
         }
-        __syncthreads();  // the next block overwrites sK, sVt and sOk
+    };
+    if (bt_lds)
+        walk(std::true_type{});
+    else
+        walk(std::false_type{});
+    {
+        const LanePair pr = swap32(lsum);
+        lsum = pr.a + pr.b;
     }
     if (!qlive) return;
-    float l = lT[0];
+    float l = lsum;
     m = m == -INFINITY ? m : m / kLog2e;  // back to the natural-log domain of the merge
     const int tok = t.tok0 + q / G, h = kvh * G + q % G;
     if (part) {
