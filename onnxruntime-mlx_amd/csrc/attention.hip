@@ -1123,7 +1123,13 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
                 const LanePair pr = swap32(bmax);
                 bmax = fmaxf(pr.a, pr.b);
             }
-            const float m_new = fmaxf(m, bmax * sc2);
+            // The reference point m moves only when the block max passes it by more
+            // than kLazy (log2 units), so P = exp2(s - m) stays below 2^kLazy (exact
+            // in fp16's range) and O is rarely rescaled; the final O / l, and the
+            // merge of (m, l, O) partials, do not depend on where m sits.
+            constexpr float kLazy = 8.f;
+            const float bm = bmax * sc2;
+            const float m_new = bm > m + kLazy ? bm : m;
             // v_exp_f32 directly: results below 2^-126 flush to zero, which the
             // softmax weights can afford.
             const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
