@@ -2303,43 +2303,6 @@ extern "C" size_t ortmi_paged_attention_workspace_size(int64_t num_tokens, int64
     return sz;
 }
 
-// A second stream (default priority) with a fork and a join event, one set per
-// host thread and device, created on first use and kept for the process.
-struct SideStream {
-    hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-};
-// The side stream of the calling thread for the device `st` runs on, or nullptr
-// when there is none to use: `st` is being captured, belongs to another device
-// than the current one, or the stream or events cannot be created.
-static SideStream* side_stream_for(hipStream_t st) {
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
-        return nullptr;
-    int cur = 0;
-    hipDevice_t sdev = 0;
-    if (hipGetDevice(&cur) != hipSuccess || hipStreamGetDevice(st, &sdev) != hipSuccess ||
-        sdev != cur || cur < 0 || cur >= 64)
-        return nullptr;
-    thread_local SideStream per_dev[64];
-    SideStream& ss = per_dev[cur];
-    if (!ss.s) {
-        hipStream_t s = nullptr;
-        hipEvent_t f = nullptr, j = nullptr;
-        if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
-        if (hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
-            hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
-            if (f) (void)hipEventDestroy(f);
-            (void)hipStreamDestroy(s);
-            return nullptr;
-        }
-        ss.s = s;
-        ss.fork = f;
-        ss.join = j;
-    }
-    return &ss;
-}
-
 template <typename T, int HD, int VHD>
 static int run_paged(const void* query, const void* key, const void* value, void* kcache,
                      void* vcache, int64_t nblk, int blk, const int32_t* cum, const int32_t* past,
@@ -2402,24 +2365,16 @@ static int run_paged(const void* query, const void* key, const void* value, void
     PagedKV pk{kcache, vcache, knew, value, bt, nblk, blk, maxb, KV, pow2 ? blk_shift : -1};
     if (!vcache) pk.vnew = nullptr;
     // Single-token tiles go to the vector-unit decode kernel when the block size is a
-    // power of two and values have the key's head size.
+    // power of two and values have the key's head size. It writes rows no
+    // multi-token tile owns (output, partials, split counts) and runs before the
+    // tile kernel on the same stream: beside it, on a second stream, its
+    // workgroups took the CUs the tile workgroups (a whole CU each) were waiting
+    // for, and the pair finished no sooner than in sequence.
     bool dec = false;
-    // The single-token kernel writes rows no multi-token tile owns (output,
-    // partials, split counts), so it runs on a second stream beside the tile
-    // kernel: forked after the tile map, joined before the merge.
-    hipStream_t dst = st;
-    SideStream* side = nullptr;
     if constexpr (VHD == HD) {
         dec = vcache && value && pow2 && (G == 1 || G == 2 || G == 4 || G == 8);
-        if (dec && (side = side_stream_for(st)) != nullptr) {
-            if (hipEventRecord(side->fork, st) == hipSuccess &&
-                hipStreamWaitEvent(side->s, side->fork, 0) == hipSuccess)
-                dst = side->s;
-            else
-                side = nullptr;
-        }
         auto launch = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, dim3(mt, KV, ns), dim3(256), 0, dst, tiles, count, cum,
+            hipLaunchKernelGGL(kernel, dim3(mt, KV, ns), dim3(256), 0, st, tiles, count, cum,
                                past, pk, blk_shift, qrot, H, sc, sink ? sink32 : nullptr, chunk,
                                ns, static_cast<T*>(output), part, nsplit_row);
         };
@@ -2441,11 +2396,6 @@ static int run_paged(const void* query, const void* key, const void* value, void
                        count, cum, past, pk, qrot, G, H, sc, sink ? sink32 : nullptr, chunk, ns,
                        static_cast<T*>(output), part, nsplit_row, dec ? 1 : 0, mt);
     if (int rc = check_launch("paged_tile")) return rc;
-    if (side) {
-        if (hipEventRecord(side->join, dst) != hipSuccess ||
-            hipStreamWaitEvent(st, side->join, 0) != hipSuccess)
-            return fail(ORTMI_E_HIP, "PagedAttention: joining the single-token stream failed");
-    }
     if (ns > 1) {
         hipLaunchKernelGGL((paged_merge_kernel<T>), dim3((unsigned)T_, (unsigned)H), dim3(128), 0, st, part,
                            static_cast<T*>(output), ns, nsplit_row, VHD, H,
