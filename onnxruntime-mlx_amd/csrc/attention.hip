@@ -4,7 +4,8 @@
 //  * gqa_prep / paged_prep - per new token: optional QK RMS-norm, RoPE on Q and K
 //    (fp32 math, one rounding to the op dtype), new K/V written to their cache
 //    rows (dense present buffer or paged slot); rotated Q (and, paged, rotated K)
-//    staged in the workspace.
+//    staged in the workspace. paged_prep also builds the tile map on the device
+//    and clears the per-row split counts.
 //  * gqa_decode - S == 1 over a dense [B,KV,T,hd] cache. One workgroup per
 //    (batch, kv head, key split); it reads each K/V row once for all H/KV query
 //    heads of the group (16 lanes x 16 bytes per 128-dim row, a wave covers 4
@@ -1306,21 +1307,37 @@ __global__ __launch_bounds__(256, 2) void gqa_tile_kernel(const T* __restrict__ 
 
 // ------------------------------------------------------- PagedAttention --
 
-// Tile map built on the device: for each sequence, ceil(nq/QT) tiles of QT
-// tokens. tiles[i] = {seq, first token, ntok}; tiles[max_tiles] = count.
-__global__ void paged_tilemap_kernel(const int32_t* __restrict__ cum, int batch, int QT,
-                                     int max_tiles, int4* __restrict__ tiles,
-                                     int* __restrict__ count) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    int n = 0;
-    for (int b = 0; b < batch; ++b) {
-        const int s0 = cum[b], s1 = cum[b + 1];
-        for (int t = s0; t < s1 && n < max_tiles; t += QT) {
-            tiles[n] = make_int4(b, t, min(QT, s1 - t), 0);
-            ++n;
+// Tile map built on the device by one 64-lane wave (no host read of the control
+// tensors): ceil(n_b / QT) tiles of QT tokens for each sequence b, in sequence
+// order, tiles[i] = {seq, first token, ntok}, and the count. Token ranges are
+// clamped to [0, T), so a malformed cum_seqlens yields fewer tiles, never a tile
+// outside the batch; at most max_tiles are written.
+__device__ void build_tile_map(const int32_t* __restrict__ cum, int batch, int T, int QT,
+                               int max_tiles, int4* __restrict__ tiles, int* __restrict__ count) {
+    const int lane = threadIdx.x;
+    int base = 0;
+    for (int b0 = 0; b0 < batch; b0 += 64) {
+        const int b = b0 + lane;
+        int s0 = 0, s1 = 0;
+        if (b < batch) {
+            s0 = min(max(cum[b], 0), T);
+            s1 = min(max(cum[b + 1], s0), T);
         }
+        const int nt = (s1 - s0 + QT - 1) / QT;
+        int incl = nt;  // inclusive prefix sum of the tile counts over the wave
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += v;
+        }
+        const int first = base + incl - nt;
+        for (int i = 0; i < nt && first + i < max_tiles; ++i) {
+            const int t = s0 + i * QT;
+            tiles[first + i] = make_int4(b, t, min(QT, s1 - t), 0);
+        }
+        base += __shfl(incl, 63, 64);
     }
-    *count = n;
+    if (lane == 0) *count = min(base, max_tiles);
 }
 
 // One workgroup (64 threads) per (token, head slot); slots 0..H-1 are query
@@ -1335,10 +1352,17 @@ __global__ __launch_bounds__(64) void paged_prep_kernel(
     const T* __restrict__ sin_c, int half, int interleaved, int rot_off,
     const int32_t* __restrict__ slot_mapping, const T* __restrict__ qw,
     const T* __restrict__ kw, float eps, int H, int KV, int hd, int vhd,
-    T* __restrict__ qrot, T* __restrict__ knew, int64_t max_pos) {
+    T* __restrict__ qrot, T* __restrict__ knew, int64_t max_pos, int QT, int max_tiles,
+    int4* __restrict__ tiles, int* __restrict__ tile_count, int* __restrict__ nsplit_row) {
     extern __shared__ float sv[];
     __shared__ float red[4];
     const int tok = blockIdx.x, head = blockIdx.y;
+    // Two jobs for the attention kernels that follow, folded in to save launches:
+    // block (0, 0) builds the tile map, and each query row's split count starts
+    // at 0 (a row no tile owns, under a malformed cum_seqlens, keeps it).
+    if (tok == 0 && head == 0)
+        build_tile_map(cum, batch, (int)gridDim.x, QT, max_tiles, tiles, tile_count);
+    if (head < H && threadIdx.x == 0) nsplit_row[(int64_t)tok * H + head] = 0;
     const bool is_q = head < H;
     const T* src = is_q ? q + ((int64_t)tok * H + head) * hd
                         : k + ((int64_t)tok * KV + (head - H)) * hd;
@@ -1745,10 +1769,6 @@ __global__ __launch_bounds__(128) void paged_merge_kernel(const float* __restric
     }
 }
 
-__global__ void fill_i32_kernel(int* __restrict__ p, int v, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = v;
-}
 
 __global__ void sink_to_f32_kernel(const void* src, int dtype, float* dst, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -2345,20 +2365,15 @@ static int run_paged(const void* query, const void* key, const void* value, void
                            bt, batch, maxb, static_cast<const T*>(cos_c),
                            static_cast<const T*>(sin_c), half, interleaved, rot_off, slot_mapping,
                            static_cast<const T*>(qw), static_cast<const T*>(kw), eps, H, KV, HD,
-                           VHD, qrot, knew, max_pos);
+                           VHD, qrot, knew, max_pos, QT, mt, tiles, count, nsplit_row);
         if (int rc = check_launch("paged_prep")) return rc;
     }
-    hipLaunchKernelGGL(paged_tilemap_kernel, dim3(1), dim3(64), 0, st, cum, batch, QT, mt, tiles,
-                       count);
+    if (T_ == 0) return ORTMI_OK;
     if (sink) {
         hipLaunchKernelGGL(sink_to_f32_kernel, dim3((H + 63) / 64), dim3(64), 0, st, sink,
                            sink_dtype, sink32, H);
+        if (int rc = check_launch("paged_sink")) return rc;
     }
-    if (int rc = check_launch("paged_tilemap")) return rc;
-    if (T_ == 0) return ORTMI_OK;
-    // Rows that no tile owns (a malformed cum) keep a split count of 0.
-    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((prow + 255) / 256)), dim3(256), 0, st,
-                       nsplit_row, 0, prow);
     int blk_shift = 0;
     while ((1 << blk_shift) < blk && blk_shift < 30) ++blk_shift;
     const bool pow2 = (1 << blk_shift) == blk && blk_shift <= 12;
