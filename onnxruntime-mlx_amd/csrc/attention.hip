@@ -1264,9 +1264,14 @@ __device__ __forceinline__ void attn_tile(const TileDesc& t, int kvh, int G, int
                                           out_tok_stride, part, nsplit, split);
 }
 
-// GQA prefill / S > 1: grid (B * tiles_per_seq, KV). Keys from `present`.
+// GQA prefill / S > 1: grid (B * tiles_per_seq, KV). Keys from `present`. The
+// matrix-core tile takes 8 waves (256 query rows, one workgroup per CU), as the
+// paged tile does: the per-thread K/V prefetch halves, which keeps the body
+// within 256 VGPRs.
+constexpr int kGqaTileWaves = 8;
 template <typename T, int HD>
-__global__ __launch_bounds__(256, 2) void gqa_tile_kernel(const T* __restrict__ qrot, DenseKV dk,
+__global__ __launch_bounds__((tile_threads<T, HD, kGqaTileWaves>()),
+                             (mfma_tile<T, HD>() ? 1 : 2)) void gqa_tile_kernel(const T* __restrict__ qrot, DenseKV dk,
                                                        int S, int QT, int tiles_per_seq, int G,
                                                        int H, int vp, float scale,
                                                        T* __restrict__ out, int chunk, int nsplit,
@@ -1295,14 +1300,14 @@ __global__ __launch_bounds__(256, 2) void gqa_tile_kernel(const T* __restrict__ 
     }
     if (split >= ns) return;
     if (ns == 1) {
-        attn_tile<T, HD, HD, false>(t, kvh, G, H, qrot, dk, none, scale, nullptr, 0, k1, out,
-                                    (int64_t)H * HD, nullptr, 1, 0);
+        attn_tile<T, HD, HD, false, kGqaTileWaves>(t, kvh, G, H, qrot, dk, none, scale, nullptr,
+                                                   0, k1, out, (int64_t)H * HD, nullptr, 1, 0);
         return;
     }
     const int k0 = split * chunk;
     const int ks1 = split == ns - 1 ? k1 : min(k1, k0 + chunk);
-    attn_tile<T, HD, HD, false>(t, kvh, G, H, qrot, dk, none, scale, nullptr, k0, ks1, out,
-                                (int64_t)H * HD, part, nsplit, split);
+    attn_tile<T, HD, HD, false, kGqaTileWaves>(t, kvh, G, H, qrot, dk, none, scale, nullptr, k0,
+                                               ks1, out, (int64_t)H * HD, part, nsplit, split);
 }
 
 // ------------------------------------------------------- PagedAttention --
@@ -2001,7 +2006,7 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
                        interleaved, qrot, static_cast<T*>(pk), static_cast<T*>(pv), B, S, H, KV,
                        hd, pcap, vp, q_stride, kv_stride);
     if (int rc = check_launch("gqa_prep")) return rc;
-    const int QT = std::max(1, tile_rows_for<T>(HD) / G);
+    const int QT = std::max(1, tile_rows_for<T>(HD, kGqaTileWaves) / G);
     const int tiles = (S + QT - 1) / QT;
     DenseKV dk{pk, pv, pcap, KV};
     // Key splits when the tiles alone leave CUs idle (a 512-token decoder prefill
@@ -2025,7 +2030,8 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
         prow = reinterpret_cast<int*>(base + align_up((size_t)B * S * H * kPrefillSplits *
                                                       (hd + 2) * 4));
     }
-    hipLaunchKernelGGL((gqa_tile_kernel<T, HD>), dim3(B * tiles, KV, ns), dim3(256), 0, st, qrot,
+    hipLaunchKernelGGL((gqa_tile_kernel<T, HD>), dim3(B * tiles, KV, ns),
+                       dim3(tile_threads<T, HD, kGqaTileWaves>()), 0, st, qrot,
                        dk, S, QT, tiles, G, H, vp, sc, static_cast<T*>(output), chunk, ns, ppart,
                        prow);
     if (int rc = check_launch("gqa_tile")) return rc;
