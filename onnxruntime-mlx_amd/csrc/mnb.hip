@@ -694,9 +694,14 @@ struct GemmStage {
     static constexpr int A_VEC = BM * kBK / 8 / 256;  // 16-byte activation vectors per thread
     uint4 a[A_VEC];
     uint4 b;         // 32 codes (one 32-code chunk of one weight row)
-    uint16_t s;      // fp16 bits of that chunk's block scale
-    uint8_t z;       // zero-point byte of the block pair
-    uint8_t zhi;     // 1: the block's zero point is the byte's high nibble
+    // Whole registers for the small fields: packed as 16 + 8 + 8 bits, the stage
+    // was carried across the loop as byte pieces, and splitting a freshly loaded
+    // scale into them waited on that load (loads complete in order, so on all of
+    // the stage's loads, issued only one step before) at the end of every odd
+    // step, which left one step of prefetch instead of two.
+    uint32_t s;      // fp16 bits of that chunk's block scale
+    uint32_t z;      // zero-point byte of the block pair
+    uint32_t zhi;    // 1: the block's zero point is the byte's high nibble
 };
 
 // KS = 2 splits the k-steps of a tile between two groups of 4 waves (512 threads,
@@ -810,7 +815,7 @@ __global__ __launch_bounds__(256 * KS) void mnb_gemm4_kernel(const T* __restrict
         st.s = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, soff, 0, 0);  // 0 out of range
         const uint32_t zoff = ok ? (uint32_t)((size_t)n * zp_cols + blk / 2) : z_end;
         st.z = (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(rz, zoff, 0, 0);
-        st.zhi = (uint8_t)(blk & 1);
+        st.zhi = (uint32_t)(blk & 1);
     };
     auto sstore = [&](const Stage& st, int buf) {
 #pragma unroll
