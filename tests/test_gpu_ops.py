@@ -671,6 +671,64 @@ def test_gqa_prefill_decoder_shape(ortmi, oracle):
              seed=9, base=1e6)
 
 
+@pytest.mark.parametrize("scale,amp", [(-0.06, 1.0), (0.35, 1.0), (0.09, 3.0)])
+def test_gqa_prefill_scale_and_score_range(ortmi, oracle, scale, amp):
+    """Prefill tiles with an explicit scale attribute: a negative one (the tile stages Q
+    with its sign flipped and scales by the magnitude), and wide score ranges whose
+    running maxima grow along the key walk (cached keys scaled up with their position,
+    up to 3x): the block maxima then pass the tile's lazy-rescale threshold of 8 log2
+    units several times per query. Output within the fp16 tolerance of the oracle at
+    the same scale."""
+    rng = np.random.default_rng(int(1000 * abs(scale)) + int(amp))
+    B, S, H, KV, hd, cap, past = 2, 200, 8, 2, 128, 400, 150
+    q, k, v, pk, pv, cos, sin = _gqa_inputs(rng, B, S, H, KV, hd, cap, True, 1e6)
+    q = (q.astype(np.float32) * amp).astype(np.float16)
+    ramp = (1.0 + 2.0 * np.arange(cap) / cap).astype(np.float32)[None, None, :, None]
+    pk = (pk.astype(np.float32) * ramp).astype(np.float16)
+    total = past + S
+    dpk, dpv = dev(pk), dev(pv)
+    out, _, _ = ortmi.group_query_attention(
+        dev(q), dev(k), dev(v), dpk, dpv, dev(np.full(B, total - 1, np.int32)), total, dev(cos),
+        dev(sin), num_heads=H, kv_num_heads=KV, scale=scale, do_rotary=1, present_key=dpk,
+        present_value=dpv)
+    ro, _, _, shared = oracle.gqa(q, k, v, pk, pv, total, H, KV, cos=cos, sin=sin, scale=scale,
+                                  round16=True)
+    assert shared
+    assert_f16_close(host(out), ro, what=f"gqa prefill scale {scale} x{amp}")
+
+
+@pytest.mark.parametrize("scale,amp", [(-0.08, 1.0), (0.1, 3.0)])
+def test_paged_prefill_scale_and_score_range(ortmi, oracle, scale, amp):
+    """The paged tile body with an explicit scale: negative, and a wide score range
+    that moves the lazy reference point several times per walk (as for GQA above).
+    Long prefill chunks, so every sequence takes the matrix-core tiles over several
+    key blocks."""
+    rng = np.random.default_rng(77 + int(amp))
+    H, KV, d, blk, batch, maxb = 8, 2, 128, 16, 3, 40
+    nb = maxb * batch
+    new = np.array([150, 97, 64], np.int32)
+    past = np.array([300, 0, 511], np.int32)
+    cum = np.concatenate([[0], np.cumsum(new)]).astype(np.int32)
+    nt = int(cum[-1])
+    q = (rng.standard_normal((nt, H * d)) * amp).astype(np.float16)
+    k = rng.standard_normal((nt, KV * d)).astype(np.float16)
+    v = rng.standard_normal((nt, KV * d)).astype(np.float16)
+    kc = rng.standard_normal((nb, blk, KV, d)).astype(np.float16)
+    vc = rng.standard_normal((nb, blk, KV, d)).astype(np.float16)
+    bt = rng.permutation(nb).astype(np.int32).reshape(batch, maxb)
+    # Cached keys grow with their position in the sequence (up to 3x), so the walk's
+    # block maxima keep passing the lazy-rescale threshold.
+    for b in range(batch):
+        for lb in range(maxb):
+            kc[bt[b, lb]] = (kc[bt[b, lb]].astype(np.float32) * (1 + 2 * lb / maxb)).astype(
+                np.float16)
+    out = ortmi.paged_attention(dev(q), dev(k), dev(v), dev(kc), dev(vc), dev(cum), dev(past),
+                                dev(bt), num_heads=H, kv_num_heads=KV, scale=scale)
+    ro, _, _ = oracle.paged_attention(q, k, v, kc, vc, cum, past, bt, H, KV, scale=scale,
+                                      round16=True)
+    assert_f16_close(host(out), ro, what=f"paged prefill scale {scale} x{amp}")
+
+
 @pytest.mark.parametrize("dt", ["bf16"])
 @pytest.mark.parametrize("past", [250, 4])
 def test_gqa_decode_dtypes(ortmi, oracle, dt, past):
