@@ -1665,14 +1665,17 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
         };
         // The next block is always requested (rows past w1 repeat row w1 - 1): a
         // load behind a branch would make the compiler wait for every load in
-        // flight where the paths join.
+        // flight where the paths join. The loop takes blocks in pairs with no exit
+        // inside its body (an odd count ends with one fully masked block): with a
+        // mid-body exit the compiler copied the register sets between iterations,
+        // and a copy of a register still being loaded waited for every load in
+        // flight, the prefetched block included.
+        uint4 kn2[U], vn2[U];
+        unsigned okn = 0;
         load_block(kr, vr, okr, w0);
         for (int base = w0; base < w1; base += 2 * BLK) {
-            uint4 kn2[U], vn2[U];
-            unsigned okn = 0;
             load_block(kn2, vn2, okn, base + BLK);
             process(kr, vr, okr, base);
-            if (base + BLK >= w1) break;
             load_block(kr, vr, okr, base + 2 * BLK);
             process(kn2, vn2, okn, base + BLK);
         }
