@@ -44,11 +44,12 @@ __device__ __forceinline__ void rope_pair_index(int i, int half, int interleaved
     }
 }
 
-// Block-cooperative: thread t handles pair t (and t + blockDim.x ...).
+// One wave per head vector: lane l handles pairs l, l + 64, ... The wave's own LDS
+// accesses stay in program order, so no barrier is needed between its steps.
 template <typename T>
 __device__ void rope_head_lds(float* v, const T* cos_row, const T* sin_row, int half,
                               int interleaved, int off) {
-    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+    for (int i = threadIdx.x & 63; i < half; i += 64) {
         int ia, ib;
         rope_pair_index<T>(i, half, interleaved, ia, ib);
         const float c = to_f32(cos_row[i]), s = to_f32(sin_row[i]);
@@ -58,63 +59,96 @@ __device__ void rope_head_lds(float* v, const T* cos_row, const T* sin_row, int 
     }
 }
 
-// RMS-normalise a head vector in LDS (block reduction), scale by w.
+// RMS-normalise a head vector in LDS (one wave per vector), scale by w.
 template <typename T>
-__device__ void rms_head_lds(float* v, int hd, const T* w, float eps, float* red) {
+__device__ void rms_head_lds(float* v, int hd, const T* w, float eps) {
+    const int lane = threadIdx.x & 63;
     float ss = 0.f;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) ss += v[d] * v[d];
-    ss = wave_sum(ss);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float tot = 0.f;
-    for (int i = 0; i < (int)(blockDim.x + 63) / 64; ++i) tot += red[i];
-    const float inv = 1.0f / sqrtf(tot / hd + eps);
-    __syncthreads();
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) v[d] = round_to<T>(v[d] * inv * to_f32(w[d]));
-    __syncthreads();
+    for (int d = lane; d < hd; d += 64) ss += v[d] * v[d];
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / hd + eps);
+    for (int d = lane; d < hd; d += 64) v[d] = round_to<T>(v[d] * inv * to_f32(w[d]));
+}
+
+// Heads per prep workgroup, one wave each (fewer, fuller workgroups).
+constexpr int kPrepHeads = 4;
+
+// Row traffic of the prep kernels in element pairs, one 32-bit access each (a
+// 128-dim row is one load instruction per wave instead of two 16-bit ones per
+// lane); a row start that is not 4-byte aligned takes single elements.
+template <typename T>
+__device__ __forceinline__ bool pair_aligned(const T* p) {
+    return (reinterpret_cast<uintptr_t>(p) & 3) == 0;
+}
+template <typename T>
+__device__ __forceinline__ void row_to_lds(float* sv, const T* src, int hd, int lane) {
+    static_assert(sizeof(T) == 2, "16-bit rows");
+    if (pair_aligned(src)) {
+        for (int d2 = lane; d2 < hd / 2; d2 += 64) {
+            const uint32_t w = reinterpret_cast<const uint32_t*>(src)[d2];
+            sv[2 * d2] = to_f32(__builtin_bit_cast(T, (uint16_t)(w & 0xffffu)));
+            sv[2 * d2 + 1] = to_f32(__builtin_bit_cast(T, (uint16_t)(w >> 16)));
+        }
+    } else {
+        for (int d = lane; d < hd; d += 64) sv[d] = to_f32(src[d]);
+    }
+}
+template <typename T>
+__device__ __forceinline__ void lds_to_row(T* dst, const float* sv, int hd, int lane) {
+    if (pair_aligned(dst)) {
+        for (int d2 = lane; d2 < hd / 2; d2 += 64) {
+            const uint32_t lo = __builtin_bit_cast(uint16_t, from_f32<T>(sv[2 * d2]));
+            const uint32_t hi = __builtin_bit_cast(uint16_t, from_f32<T>(sv[2 * d2 + 1]));
+            reinterpret_cast<uint32_t*>(dst)[d2] = lo | (hi << 16);
+        }
+    } else {
+        for (int d = lane; d < hd; d += 64) dst[d] = from_f32<T>(sv[d]);
+    }
+}
+template <typename T>
+__device__ __forceinline__ void copy_row(T* dst, const T* src, int n, int lane) {
+    if (pair_aligned(dst) && pair_aligned(src)) {
+        for (int d2 = lane; d2 < n / 2; d2 += 64)
+            reinterpret_cast<uint32_t*>(dst)[d2] = reinterpret_cast<const uint32_t*>(src)[d2];
+    } else {
+        for (int d = lane; d < n; d += 64) dst[d] = src[d];
+    }
 }
 
 // -------------------------------------------------------------- GQA prep --
 
-// One workgroup (64 threads) per (token, head) with heads 0..H-1 = query,
-// H..H+KV-1 = key. Rotated Q goes to qrot [B*S, H, hd]; rotated K and raw V go
-// to present rows valid_past + s.
+// One wave per (token, head), kPrepHeads heads per workgroup, with heads
+// 0..H-1 = query, H..H+KV-1 = key. Rotated Q goes to qrot [B*S, H, hd]; rotated K
+// and raw V go to present rows valid_past + s.
 template <typename T>
-__global__ __launch_bounds__(64) void gqa_prep_kernel(
+__global__ __launch_bounds__(64 * kPrepHeads) void gqa_prep_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ cos_c, const T* __restrict__ sin_c, int half, int interleaved,
     T* __restrict__ qrot, T* __restrict__ pk, T* __restrict__ pv, int B, int S, int H, int KV,
     int hd, int64_t pcap, int vp, int64_t q_stride, int64_t kv_stride) {
-    extern __shared__ float sv[];
+    extern __shared__ float sv_all[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int tok = blockIdx.x;  // b*S + s
-    const int head = blockIdx.y;
+    const int head = blockIdx.y * kPrepHeads + wave;
+    if (head >= H + KV) return;
+    float* sv = sv_all + wave * hd;
     const int b = tok / S, s = tok % S;
     const int pos = vp + s;
     const bool is_q = head < H;
     const T* src = is_q ? q + (int64_t)tok * q_stride + (int64_t)head * hd
                         : k + (int64_t)tok * kv_stride + (int64_t)(head - H) * hd;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) sv[d] = to_f32(src[d]);
-    __syncthreads();
+    row_to_lds<T>(sv, src, hd, lane);
     if (cos_c) rope_head_lds<T>(sv, cos_c + (int64_t)pos * half, sin_c + (int64_t)pos * half, half,
                                 interleaved, 0);
-    __syncthreads();
     if (is_q) {
-        T* dst = qrot + ((int64_t)tok * H + head) * hd;
-        for (int d = threadIdx.x; d < hd; d += blockDim.x) dst[d] = from_f32<T>(sv[d]);
+        lds_to_row<T>(qrot + ((int64_t)tok * H + head) * hd, sv, hd, lane);
     } else {
         const int kvh = head - H;
         const int64_t row = (((int64_t)b * KV + kvh) * pcap + pos) * hd;
-        const T* vs = v + (int64_t)tok * kv_stride + (int64_t)kvh * hd;
-        for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-            pk[row + d] = from_f32<T>(sv[d]);
-            pv[row + d] = vs[d];
-        }
+        lds_to_row<T>(pk + row, sv, hd, lane);
+        copy_row<T>(pv + row, v + (int64_t)tok * kv_stride + (int64_t)kvh * hd, hd, lane);
     }
 }
 
-// Plain copy of `rows` rows of hd elements from [B,KV,src_cap,hd] to
-// [B,KV,dst_cap,hd] (rows < copy_rows), 16-byte vectors.
 __global__ __launch_bounds__(256) void kv_copy_kernel(const uint4* __restrict__ src,
                                                       uint4* __restrict__ dst, int64_t src_cap,
                                                       int64_t dst_cap, int64_t copy_rows,
@@ -1349,7 +1383,7 @@ __device__ void build_tile_map(const int32_t* __restrict__ cum, int batch, int T
 // heads, H..H+KV-1 key heads. Q/K: optional RMS norm, RoPE; rotated Q ->
 // qrot, rotated K -> knew, K/V -> cache slot.
 template <typename T>
-__global__ __launch_bounds__(64) void paged_prep_kernel(
+__global__ __launch_bounds__(64 * kPrepHeads) void paged_prep_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     T* __restrict__ kcache, T* __restrict__ vcache, int64_t nblk, int blk,
     const int32_t* __restrict__ cum, const int32_t* __restrict__ past,
@@ -1359,15 +1393,18 @@ __global__ __launch_bounds__(64) void paged_prep_kernel(
     const T* __restrict__ kw, float eps, int H, int KV, int hd, int vhd,
     T* __restrict__ qrot, T* __restrict__ knew, int64_t max_pos, int QT, int max_tiles,
     int4* __restrict__ tiles, int* __restrict__ tile_count, int* __restrict__ nsplit_row) {
-    extern __shared__ float sv[];
-    __shared__ float red[4];
-    const int tok = blockIdx.x, head = blockIdx.y;
+    extern __shared__ float sv_all[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // One wave per (token, head), kPrepHeads heads per workgroup.
+    const int tok = blockIdx.x, head = blockIdx.y * kPrepHeads + wave;
+    if (head >= H + KV) return;
+    float* sv = sv_all + wave * hd;
     // Two jobs for the attention kernels that follow, folded in to save launches:
     // block (0, 0) builds the tile map, and each query row's split count starts
     // at 0 (a row no tile owns, under a malformed cum_seqlens, keeps it).
     if (tok == 0 && head == 0)
         build_tile_map(cum, batch, (int)gridDim.x, QT, max_tiles, tiles, tile_count);
-    if (head < H && threadIdx.x == 0) nsplit_row[(int64_t)tok * H + head] = 0;
+    if (head < H && lane == 0) nsplit_row[(int64_t)tok * H + head] = 0;
     const bool is_q = head < H;
     const T* src = is_q ? q + ((int64_t)tok * H + head) * hd
                         : k + ((int64_t)tok * KV + (head - H)) * hd;
@@ -1375,12 +1412,11 @@ __global__ __launch_bounds__(64) void paged_prep_kernel(
     // lane l holds cum[l] and past[l] (one batch of loads, together with the
     // head row) and a ballot counts the cum[l] <= tok for l >= 1; beyond that, a
     // binary search.
-    const int lane = threadIdx.x;
     int b, cb, pb;
     if (batch <= 64) {
         const int l = min(lane, batch - 1);
         const int cl = cum[l], pl = past[l];
-        for (int d = lane; d < hd; d += blockDim.x) sv[d] = to_f32(src[d]);
+        row_to_lds<T>(sv, src, hd, lane);
         b = (int)__popcll(__ballot(lane >= 1 && lane < batch && cl <= tok));
         cb = __shfl(cl, b, 64);
         pb = __shfl(pl, b, 64);
@@ -1394,29 +1430,24 @@ __global__ __launch_bounds__(64) void paged_prep_kernel(
         b = lo;
         cb = cum[b];
         pb = past[b];
-        for (int d = lane; d < hd; d += blockDim.x) sv[d] = to_f32(src[d]);
+        row_to_lds<T>(sv, src, hd, lane);
     }
     const int pos = pb + (tok - cb);
-    __syncthreads();
     const T* nw = is_q ? qw : kw;
-    if (nw) rms_head_lds<T>(sv, hd, nw, eps, red);
+    if (nw) rms_head_lds<T>(sv, hd, nw, eps);
     if (cos_c) {
         // A position outside the cache violates the op contract; clamp the row so
         // the read stays inside the cos/sin tensors.
         const int64_t prow = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
         rope_head_lds<T>(sv, cos_c + prow * half, sin_c + prow * half, half, interleaved, rot_off);
-        __syncthreads();
-        for (int d = threadIdx.x; d < hd; d += blockDim.x) sv[d] = round_to<T>(sv[d]);
+        for (int d = lane; d < hd; d += 64) sv[d] = round_to<T>(sv[d]);
     }
-    __syncthreads();
     if (is_q) {
-        T* dst = qrot + ((int64_t)tok * H + head) * hd;
-        for (int d = threadIdx.x; d < hd; d += blockDim.x) dst[d] = from_f32<T>(sv[d]);
+        lds_to_row<T>(qrot + ((int64_t)tok * H + head) * hd, sv, hd, lane);
         return;
     }
     const int kvh = head - H;
-    T* kn = knew + ((int64_t)tok * KV + kvh) * hd;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) kn[d] = from_f32<T>(sv[d]);
+    lds_to_row<T>(knew + ((int64_t)tok * KV + kvh) * hd, sv, hd, lane);
     int64_t slot;
     if (slot_mapping) {
         slot = slot_mapping[tok];
@@ -1426,12 +1457,10 @@ __global__ __launch_bounds__(64) void paged_prep_kernel(
         slot = phys < 0 ? -1 : (int64_t)phys * blk + pos % blk;
     }
     if (slot < 0 || slot >= nblk * blk) return;
-    T* kc = kcache + (slot * KV + kvh) * hd;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) kc[d] = from_f32<T>(sv[d]);
+    lds_to_row<T>(kcache + (slot * KV + kvh) * hd, sv, hd, lane);
     if (vcache) {
-        const T* vs = v + ((int64_t)tok * KV + kvh) * vhd;
-        T* vc = vcache + (slot * KV + kvh) * vhd;
-        for (int d = threadIdx.x; d < vhd; d += blockDim.x) vc[d] = vs[d];
+        copy_row<T>(vcache + (slot * KV + kvh) * vhd, v + ((int64_t)tok * KV + kvh) * vhd, vhd,
+                    lane);
     }
 }
 
@@ -2004,7 +2033,8 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
                            (int64_t)H * hd, (const int*)nullptr);
         return check_launch("gqa_merge");
     }
-    hipLaunchKernelGGL((gqa_prep_kernel<T>), dim3(B * S, H + KV), dim3(64), hd * sizeof(float), st,
+    hipLaunchKernelGGL((gqa_prep_kernel<T>), dim3(B * S, (H + KV + kPrepHeads - 1) / kPrepHeads),
+                       dim3(64 * kPrepHeads), kPrepHeads * hd * sizeof(float), st,
                        q, k, v, static_cast<const T*>(cos_c), static_cast<const T*>(sin_c), half,
                        interleaved, qrot, static_cast<T*>(pk), static_cast<T*>(pv), B, S, H, KV,
                        hd, pcap, vp, q_stride, kv_stride);
@@ -2367,8 +2397,10 @@ static int run_paged(const void* query, const void* key, const void* value, void
     const float sc = scale != 0.f ? scale : 1.0f / sqrtf((float)HD);
 
     if (T_ > 0) {
-        hipLaunchKernelGGL((paged_prep_kernel<T>), dim3((unsigned)T_, H + KV), dim3(64),
-                           HD * sizeof(float), st, static_cast<const T*>(query),
+        hipLaunchKernelGGL((paged_prep_kernel<T>),
+                           dim3((unsigned)T_, (H + KV + kPrepHeads - 1) / kPrepHeads),
+                           dim3(64 * kPrepHeads), kPrepHeads * HD * sizeof(float), st,
+                           static_cast<const T*>(query),
                            static_cast<const T*>(key), static_cast<const T*>(value),
                            static_cast<T*>(kcache), static_cast<T*>(vcache), nblk, blk, cum, past,
                            bt, batch, maxb, static_cast<const T*>(cos_c),
