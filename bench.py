@@ -376,6 +376,9 @@ def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
     w = dec.make_weights(cfg, seed=4)
     cap = prompt_len + gen
     runner = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=prompt_len)
+    # The same decoder ending in an ArgMax node: the EP's decode program writes the
+    # greedy id to the graph output, so a step is the EP run alone.
+    runner_am = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=prompt_len, argmax_node=True)
     del w
     prompt = np.random.default_rng(44).integers(0, cfg.vocab, size=prompt_len)
     runner.generate(prompt[:16], steps=4)  # warm-up: allocations and first launches
@@ -394,6 +397,9 @@ def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
         torch.cuda.synchronize()
         run_times.append(time.perf_counter() - t1)
     runner.length = length + 1
+    runner_am.generate(prompt[:16], steps=4)
+    tokens_am, _, times_am = runner_am.generate(prompt, steps=gen)
+    del runner_am
     tok_s = len(times) / dec_s
     wbytes = cfg.weight_bytes()
     # KV read per token at the mean decode context, K and V, all layers.
@@ -404,7 +410,9 @@ def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
                 prefill_tok_s=prompt_len / ttft, bytes_per_token=int(per_tok),
                 gbs=per_tok * tok_s / 1e9, tokens=tokens[:8], n_decode=len(times),
                 p50_ms=float(np.median(times)) * 1e3,
-                run_p50_ms=float(np.median(run_times)) * 1e3)
+                run_p50_ms=float(np.median(run_times)) * 1e3,
+                am_tok_s=len(times_am) / float(np.sum(times_am)),
+                am_p50_ms=float(np.median(times_am)) * 1e3, am_same_tokens=tokens_am == tokens)
 
 
 def measured_traffic(profile: str):
@@ -584,6 +592,10 @@ def main():
             # without the greedy argmax and its synchronisation.
             "run_only_p50_ms": round(r["run_p50_ms"], 3),
             "run_only_tok_s": round(1e3 / r["run_p50_ms"], 1),
+            # The graph with a trailing ArgMax: the greedy id comes out of the EP run.
+            "argmax_node_tok_s": round(r["am_tok_s"], 1),
+            "argmax_node_p50_ms": round(r["am_p50_ms"], 3),
+            "argmax_node_same_tokens": r["am_same_tokens"],
             "prefill_tok_s": round(r["prefill_tok_s"], 1),
             "bytes_per_token": r["bytes_per_token"],
             "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
@@ -591,7 +603,8 @@ def main():
             "first_tokens": r["tokens"]}
         log(f"decoder: {r['tok_s']:.1f} tok/s ({r['ms_per_token']:.3f} ms/token, p50 "
             f"{r['p50_ms']:.3f}), prefill {r['ttft_ms']:.1f} ms; EP run alone p50 "
-            f"{r['run_p50_ms']:.3f} ms")
+            f"{r['run_p50_ms']:.3f} ms; with the ArgMax node {r['am_tok_s']:.1f} tok/s (p50 "
+            f"{r['am_p50_ms']:.3f} ms, same tokens: {r['am_same_tokens']})")
         if not args.no_cpu_baseline:
             cpu_dec = cpu_baseline_decoder()
             secondary["int4_decoder"]["cpu_baseline"] = cpu_dec

@@ -482,6 +482,31 @@ std::string claim_gather(const NodeDesc& n, const GraphIR& g) {
     return "";
 }
 
+// rust/src/ops/reduction.rs:582-630 (registered at :962). The reference claims any
+// numeric dtype, axis and select_last_index; the kernel here reduces contiguous
+// float rows with the lowest index winning ties, so other forms are declined.
+std::string claim_argmax(const NodeDesc& n, const GraphIR& g) {
+    REQUIRE(n.inputs.size() == 1 && n.outputs.size() == 1 && !n.outputs[0].empty(),
+            "requires 1 input and 1 output");
+    auto* x = val(g, n, 0);
+    REQUIRE(x && is_float(x->dtype), "float input required");
+    REQUIRE(x->has_shape && !x->dims.empty(), "input rank must be known and at least 1");
+    const int64_t r = (int64_t)x->dims.size();
+    int64_t axis = n.attr_int("axis", 0);
+    if (axis < 0) axis += r;
+    REQUIRE(axis >= 0 && axis < r, "axis out of range");
+    REQUIRE(axis == r - 1, "only the last axis is reduced");
+    const int64_t kd = n.attr_int("keepdims", 1);
+    REQUIRE(kd == 0 || kd == 1, "keepdims must be 0 or 1");
+    const int64_t last = n.attr_int("select_last_index", 0);
+    REQUIRE(last == 0 || last == 1, "select_last_index must be 0 or 1");
+    REQUIRE(last == 0, "select_last_index=1 is not supported");
+    REQUIRE(x->dims.back() != 0, "the reduced axis is empty");
+    auto* out = out_val(g, n, 0);
+    REQUIRE(!out || out->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64, "output must be int64");
+    return "";
+}
+
 // rust/src/ops/quant.rs:1713-1749
 std::string claim_gbq(const NodeDesc& n, const GraphIR& g) {
     REQUIRE(!n.outputs.empty() && !n.outputs[0].empty(), "requires at least one output");
@@ -532,6 +557,7 @@ const Entry kRegistry[] = {
     {"", "Sigmoid", claim_unary},
     {"", "Cast", claim_cast},
     {"", "Gather", claim_gather},
+    {"", "ArgMax", claim_argmax},
 };
 
 }  // namespace

@@ -45,7 +45,8 @@ static bool is_device_ptr(const void* p) {
 // A fused node that is a whole int4 decoder after the decode rewrites:
 //   Gather(embed, ids) -> L x [MatMulNBits q/k/v (norm prologue), GroupQueryAttention
 //   (packed, in-op RoPE), MatMulNBits o_proj, MatMulNBitsSwiGLU gate/up (norm
-//   prologue), MatMulNBits down] -> MatMulNBits lm_head (norm prologue) -> logits.
+//   prologue), MatMulNBits down] -> MatMulNBits lm_head (norm prologue) -> logits
+//   [-> ArgMax over the vocabulary -> next token id].
 // Its one-token steps on a device-resident KV cache shared by past and present run
 // as one launch of ortmi_decoder_decode_step, the counterpart of the reference's
 // one compiled-closure evaluation per token (rust/src/compiled.rs:503-822).
@@ -56,6 +57,9 @@ struct Plan::DecodeProgram {
         std::string past_k, past_v, present_k, present_v;
     };
     std::string ids, total, logits, embed, cos, sin, gf, lm_B, lm_S;
+    std::string argmax;       // the ArgMax output, or empty when the graph has none
+    bool argmax_keep = false;  // its keepdims
+    bool logits_out = true;    // logits are a node output (else only the ArgMax reads them)
     float ef = 1e-6f;
     std::vector<Layer> layers;
     OrtmiDecoderDims dims{};
@@ -64,10 +68,12 @@ struct Plan::DecodeProgram {
     const void *embed_p = nullptr, *cos_p = nullptr, *sin_p = nullptr, *gf_p = nullptr,
                *lm_B_p = nullptr, *lm_S_p = nullptr;
     int64_t embed_rows = 0;
-    std::unique_ptr<DeviceBuffer> table, ws, next_id;
+    std::unique_ptr<DeviceBuffer> table, ws, next_id, logits_buf;
     size_t ws_bytes = 0;
     void* logits_ptr = nullptr;  // the last logits buffer and whether it is device memory
     bool logits_dev = false;
+    void* argmax_ptr = nullptr;  // the same for the ArgMax output
+    bool argmax_dev = false;
     int32_t* status = nullptr;  // host-pinned: the kernel writes it, the host reads it after the run
     ~DecodeProgram() {
         if (status) (void)hipHostFree(status);
@@ -185,9 +191,20 @@ void Plan::match_decode_program() {
         if (l == 0 ? q->has_input(6) : q->inputs[6] != res)
             return reject("the norm's skip input is not the residual stream");
         const NodeDesc* g = reader(q->outputs[0], "GroupQueryAttention", false);
-        if (!g) {  // the lm_head: its output is the fused node's logits
-            if (l == 0 || !in_list(outputs_, q->outputs[0]) || !mnb(q, D, -1))
-                return reject("lm_head form");
+        if (!g) {  // the lm_head: its logits are a fused-node output, an ArgMax input or both
+            const NodeDesc* am = reader(q->outputs[0], "ArgMax", false);
+            dp->logits_out = in_list(outputs_, q->outputs[0]);
+            if (l == 0 || !(dp->logits_out || am) || !mnb(q, D, -1)) return reject("lm_head form");
+            if (am) {
+                auto lv = sub_.values.find(q->outputs[0]);
+                const int64_t r = lv == sub_.values.end() ? 0 : (int64_t)lv->second.dims.size();
+                const int64_t ax = am->attr_int("axis", 0);
+                if (r != 3 || (ax != -1 && ax != 2) || am->attr_int("select_last_index", 0) != 0 ||
+                    am->outputs.size() != 1 || !in_list(outputs_, am->outputs[0]))
+                    return reject("ArgMax form");
+                dp->argmax = am->outputs[0];
+                dp->argmax_keep = am->attr_int("keepdims", 1) != 0;
+            }
             dp->logits = q->outputs[0];
             dp->lm_B = q->inputs[1];
             dp->lm_S = q->inputs[2];
@@ -281,8 +298,9 @@ void Plan::match_decode_program() {
         res = gu->outputs[1];
     }
     // Every node of the fused node is part of the program, and it has no other outputs.
-    if (nodes.size() != 2 + 5 * dp->layers.size()) return reject("extra nodes in the fused node");
-    if (outputs_.size() != 1 + 2 * dp->layers.size())
+    const size_t am = dp->argmax.empty() ? 0 : 1;
+    if (nodes.size() != 2 + am + 5 * dp->layers.size()) return reject("extra nodes in the fused node");
+    if (outputs_.size() != (dp->logits_out ? 1 : 0) + am + 2 * dp->layers.size())
         return reject("extra outputs of the fused node");
     const ValueDesc* gf = cst(dp->gf);
     if (!gf || gf->dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16)
@@ -367,12 +385,33 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
             output_buffer(dp.layers[l].present_v, pdims, a, ctx, false) != table[l].v_cache)
             return skip("present is not bound to past");
     }
-    void* logits = output_buffer(dp.logits, {1, 1, d.vocab}, a, ctx, false);
-    if (logits != dp.logits_ptr) {  // the pointer query costs microseconds: once per buffer
-        dp.logits_dev = is_device_ptr(logits);
-        dp.logits_ptr = logits;
+    void* logits = nullptr;
+    if (dp.logits_out) {
+        logits = output_buffer(dp.logits, {1, 1, d.vocab}, a, ctx, false);
+        if (logits != dp.logits_ptr) {  // the pointer query costs microseconds: once per buffer
+            dp.logits_dev = is_device_ptr(logits);
+            dp.logits_ptr = logits;
+        }
+        if (!dp.logits_dev) return skip("logits in host memory");
+    } else {  // only the ArgMax reads them: a buffer of the program's own
+        if (!dp.logits_buf) dp.logits_buf = device_alloc((size_t)d.vocab * 2);
+        logits = dp.logits_buf->ptr;
     }
-    if (!dp.logits_dev) return skip("logits in host memory");
+    // The program's greedy argmax (lowest index on ties) is the ArgMax output: written
+    // in place when that is device memory, else copied out after the launch.
+    int64_t* next_id = static_cast<int64_t*>(dp.next_id->ptr);
+    void* argmax_host = nullptr;
+    if (!dp.argmax.empty()) {
+        const std::vector<int64_t> od = dp.argmax_keep ? std::vector<int64_t>{1, 1, 1}
+                                                       : std::vector<int64_t>{1, 1};
+        void* o = output_buffer(dp.argmax, od, a, ctx, false);
+        if (o != dp.argmax_ptr) {
+            dp.argmax_dev = is_device_ptr(o);
+            dp.argmax_ptr = o;
+        }
+        if (dp.argmax_dev) next_id = static_cast<int64_t*>(o);
+        else argmax_host = o;
+    }
     const size_t tb = table.size() * sizeof(OrtmiDecoderLayer);
     if (!dp.table || dp.host_table.size() != table.size() ||
         std::memcmp(dp.host_table.data(), table.data(), tb) != 0) {
@@ -393,8 +432,8 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
         static_cast<const OrtmiDecoderLayer*>(dp.table->ptr), &d, dp.embed_p, dp.embed_rows,
         static_cast<const int64_t*>(ids->second.ptr),
         static_cast<const int32_t*>(env_.at(dp.total).ptr), dp.cos_p, dp.sin_p, dp.gf_p, dp.ef,
-        static_cast<const uint8_t*>(dp.lm_B_p), dp.lm_S_p, logits,
-        static_cast<int64_t*>(dp.next_id->ptr), dp.status, dp.ws->ptr, dp.ws_bytes, stream_);
+        static_cast<const uint8_t*>(dp.lm_B_p), dp.lm_S_p, logits, next_id, dp.status, dp.ws->ptr,
+        dp.ws_bytes, stream_);
     if (rc == ORTMI_E_INVALID) {
         const std::string why = ortmi_last_error();
         if (dprog_required_) fail("decode program rejected the decoder: " + why);
@@ -403,6 +442,10 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
         return false;
     }
     check_kernel(rc, "decode program");
+    if (argmax_host)
+        check_hip(hipMemcpyAsync(argmax_host, next_id, sizeof(int64_t), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "ArgMax output");
     return true;
 }
 
@@ -1116,6 +1159,23 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         check_kernel(ortmi_gather_rows(tab.ptr, (const int64_t*)ids.ptr, O.ptr, ids.numel(),
                                        tab.dims[0], tab.dims[1], kdt(tab.dtype), st),
                      "Gather");
+        return;
+    }
+    if (op == "ArgMax") {  // last axis, lowest index on ties (claim_argmax)
+        Tensor x = need(0);
+        if (x.dims.empty()) fail("ArgMax: scalar input", ORT_INVALID_ARGUMENT);
+        const int64_t cols = x.dims.back();
+        if (cols <= 0) fail("ArgMax: the reduced axis is empty", ORT_INVALID_ARGUMENT);
+        const int64_t rows = x.numel() / cols;
+        std::vector<int64_t> od(x.dims.begin(), x.dims.end() - 1);
+        if (n.attr_int("keepdims", 1)) od.push_back(1);
+        Tensor& O = out_tensor(outname(0), ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64, od, a, ctx);
+        if (rows == 0) return;
+        const size_t wsb = ortmi_argmax_rows_workspace_size(rows, cols);
+        void* ws = wsb ? workspace(wsb) : nullptr;
+        check_kernel(ortmi_argmax_rows(x.ptr, (int64_t*)O.ptr, rows, cols, kdt(x.dtype), ws, wsb,
+                                       st),
+                     "ArgMax");
         return;
     }
     if (op == "GatherBlockQuantized") {

@@ -100,8 +100,12 @@ def make_weights(cfg: DecoderConfig, seed: int = 4):
     return w
 
 
-def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False) -> hx.Graph:
+def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False,
+                argmax: bool = False) -> hx.Graph:
     """Decoder graph with symbolic sequence length S and KV capacity `cap`.
+
+    argmax: end the graph with ArgMax(logits, axis=-1, keepdims=0) -> next_tokens
+    (int64 [1, S]), so greedy decoding takes its next id from the graph itself.
 
     layer_metadata: also record the residual stream after each layer (the last one's
     is the final norm's residual output) under the model metadata key
@@ -185,6 +189,10 @@ def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False) -
     g.initializer("lm_head.s", w["lm_head.s"])
     g.node("MatMulNBits", ["xf", "lm_head.B", "lm_head.s"], ["logits"], domain="com.microsoft",
            name="lm_head", K=D, N=cfg.vocab, bits=4, block_size=cfg.block)
+    if argmax:
+        g.value("next_tokens", I64, [1, S])
+        g.node("ArgMax", ["logits"], ["next_tokens"], name="greedy", axis=-1, keepdims=0)
+        outputs.append("next_tokens")
     if layer_metadata:
         names = [f"l{layer}.res1" for layer in range(1, cfg.layers)] + ["resf"]
         g.metadata("onnxruntime_ep_mlx.layer_boundary_outputs", json.dumps(names))
@@ -197,16 +205,21 @@ class DecoderRunner:
 
     Per call the host sends only total_sequence_length (a 4-byte host input, as
     ONNX Runtime keeps it in CPU memory); ids, logits, KV and the argmax stay in HBM.
+
+    argmax_node: build the graph with its ArgMax (build_graph's argmax) and feed its
+    output back as the next input id; otherwise the runner takes the argmax of the
+    last logits row with ortmi_argmax_rows after each run.
     """
 
     def __init__(self, cfg: DecoderConfig, weights, cap: int, max_prompt: int,
-                 layer_metadata: bool = False):
+                 layer_metadata: bool = False, argmax_node: bool = False):
         import torch
 
         self.torch = torch
         self.cfg = cfg
         self.cap = cap
-        self.graph = build_graph(cfg, weights, cap, layer_metadata)
+        self.argmax_node = argmax_node
+        self.graph = build_graph(cfg, weights, cap, layer_metadata, argmax=argmax_node)
         self.session = hx.Session(self.graph)
         dev = "cuda"
         self.kv = []
@@ -221,6 +234,12 @@ class DecoderRunner:
         self.session.bind_output("logits", self.logits)
         self.ids = torch.zeros((1, max_prompt), dtype=torch.int64, device=dev)
         self.next_id = torch.zeros((1, 1), dtype=torch.int64, device=dev)
+        # ArgMax outputs alternate between two buffers, so a step's input id (the
+        # previous step's output) is never the buffer it writes.
+        self.tokens = [torch.zeros((1, max_prompt), dtype=torch.int64, device=dev)
+                       for _ in range(2)]
+        self._first = [t[:, :1] for t in self.tokens]
+        self._flip = 0
         # seqlens_k and total_sequence_length live in (pinned) host memory, as ONNX
         # Runtime keeps them.
         self.seqlens = torch.zeros(1, dtype=torch.int32, pin_memory=True)
@@ -251,10 +270,18 @@ class DecoderRunner:
         self.torch.cuda.current_stream().synchronize()
         self._host[0][0] = self.length + S - 1
         self._host[1][0] = self.length + S
+        if self.argmax_node:
+            out = self.tokens[self._flip]
+            self.session.bind_output("next_tokens", out)
         self.session.run({"input_ids": (ids, hx.INT64)})
         self.length += S
+        if self.argmax_node:
+            self.next_id = self._first[self._flip] if S == 1 else out[:, S - 1:S]
+            self._flip ^= 1
 
     def argmax_last(self, S: int):
+        if self.argmax_node:
+            return  # the graph's ArgMax already wrote next_id
         st = ctypes.c_void_p(self.torch.cuda.current_stream().cuda_stream)
         last = self.logits[0, S - 1]
         check(self.lib.ortmi_argmax_rows(ctypes.c_void_p(last.data_ptr()),

@@ -315,6 +315,37 @@ def test_norm_claims():
     assert s.claimed(0) and s.claimed(1) and not s.claimed(2)
 
 
+@pytest.mark.parametrize("dtype,attrs,out_dtype,claimed", [
+    (F16, dict(axis=-1, keepdims=0), I64, True),
+    (F16, dict(axis=2, keepdims=1), I64, True),
+    (F32, dict(axis=-1), I64, True),          # keepdims defaults to 1
+    (hx.BFLOAT16, dict(axis=2, keepdims=0, select_last_index=0), I64, True),
+    (F16, dict(axis=1), I64, False),          # only the last axis
+    (F16, dict(axis=0), I64, False),          # the default axis is 0
+    (F16, dict(axis=3), I64, False),          # out of range (reduction.rs:610-617)
+    (F16, dict(axis=-1, keepdims=2), I64, False),
+    (F16, dict(axis=-1, select_last_index=1), I64, False),
+    (I32, dict(axis=-1), I64, False),         # float inputs only
+])
+def test_argmax_claim_predicate(dtype, attrs, out_dtype, claimed):
+    g = hx.Graph()
+    g.value("x", dtype, [1, -1, 1000])
+    g.value("y", out_dtype, [1, -1] if attrs.get("keepdims", 1) == 0 else [1, -1, 1])
+    g.node("ArgMax", ["x"], ["y"], **attrs)
+    g.io(["x"], ["y"])
+    assert session(g).claimed(0) is claimed
+
+
+def test_decoder_graph_with_argmax_fully_claimed():
+    cfg = dec.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, inter=512,
+                            vocab=1000, max_pos=256)
+    w = dec.make_weights(cfg, seed=0)
+    g = dec.build_graph(cfg, w, cap=64, argmax=True)
+    parts = session(g).partitions()
+    assert len(parts) == 1 and len(parts[0]) == g.n_nodes
+    assert g.n_nodes == 1 + cfg.layers * 13 + 3
+
+
 def test_decoder_graph_fully_claimed_as_one_fused_node():
     cfg = dec.DecoderConfig(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, inter=512,
                             vocab=1000, max_pos=256)

@@ -192,6 +192,82 @@ def test_ep_gqa_decode_steps_shared_kv(ortmi, oracle, hx):
 TIE_ULPS = 16
 
 
+@pytest.mark.parametrize("dtype,V,keepdims", [
+    (np.float16, 151936, 0),
+    (np.float32, 1000, 1),
+    (np.float16, 77, 1),
+])
+def test_ep_argmax_node(ortmi, hx, dtype, V, keepdims):
+    """ArgMax over the last axis through the EP against numpy's argmax (the lowest
+    index wins ties, as ONNX ArgMax with select_last_index=0 defines it; a NaN never
+    wins). Rows carry planted ties, a NaN and a maximum in the last column; the
+    keepdims=1 cases write into a host-memory output."""
+    import torch
+
+    rng = np.random.default_rng(V + keepdims)
+    x = rng.standard_normal((2, 3, V)).astype(dtype)
+    x[0, 0, 5] = x[0, 0, 7] = 9.0
+    x[0, 1, 0] = np.nan
+    x[0, 1, V - 1] = 9.0
+    x[0, 2, V - 2] = x[0, 2, V - 1] = 9.0
+    x[1, 0, :] = 1.0
+    onnx_dt = hx.FLOAT16 if dtype == np.float16 else hx.FLOAT
+    g = hx.Graph()
+    g.value("x", onnx_dt, [-1, -1, V])
+    g.value("y", hx.INT64, [-1, -1, 1] if keepdims else [-1, -1])
+    g.node("ArgMax", ["x"], ["y"], axis=-1, keepdims=keepdims)
+    g.io(["x"], ["y"])
+    sess = hx.Session(g)
+    assert sess.partitions() == [[0]]
+    shape = (2, 3, 1) if keepdims else (2, 3)
+    if keepdims:
+        y = torch.full(shape, -1, dtype=torch.int64)
+    else:
+        y = torch.full(shape, -1, dtype=torch.int64, device="cuda")
+    sess.bind_output("y", y)
+    sess.run({"x": (dev(x), onnx_dt)})
+    torch.cuda.synchronize()
+    want = np.argmax(np.where(np.isnan(x), -np.inf, x), axis=-1).reshape(shape)
+    assert want[0, 0].item() == 5 and want[0, 1].item() == V - 1 and want[0, 2].item() == V - 2
+    assert want[1, 0].item() == 0
+    np.testing.assert_array_equal(y.cpu().numpy(), want)
+
+
+def test_ep_decode_program_argmax_node(ortmi, dec, monkeypatch):
+    """A decoder graph that ends in ArgMax: its one-token steps run as the decode
+    program with the program's argmax written to the ArgMax output (ORTMI_EP_PROGRAM
+    =require), giving the tokens and logits of the graph without ArgMax (the runner
+    taking the argmax itself) and of the op-by-op path; one step writes the ArgMax
+    output into host memory."""
+    import torch
+
+    cfg = _small_cfg(dec, 128)
+    w = dec.make_weights(cfg, seed=43)
+    prompt = np.random.default_rng(44).integers(0, cfg.vocab, size=13)
+
+    def run(mode, argmax_node, host_last=False):
+        monkeypatch.setenv("ORTMI_EP_PROGRAM", mode)
+        r = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32, argmax_node=argmax_node)
+        r.prefill(prompt)
+        toks, logits = [int(r.next_id.item())], []
+        for i in range(8):
+            if host_last and i == 7:
+                buf = torch.full((1, 32), -1, dtype=torch.int64)
+                r.tokens[r._flip], r._first[r._flip] = buf, buf[:, :1]
+            r.decode_step()
+            logits.append(host(r.logits[0, :1])[0])
+            toks.append(int(r.next_id.item()))
+        return toks, logits
+
+    base_t, base_l = run("require", False)
+    prog_t, prog_l = run("require", True, host_last=True)
+    op_t, _ = run("0", True)
+    print(f"tokens {base_t}", flush=True)
+    assert prog_t == base_t and op_t == base_t
+    for a, b in zip(prog_l, base_l):
+        np.testing.assert_array_equal(a, b)
+
+
 def _fp16_ulp(x):
     return 2.0 ** (np.floor(np.log2(max(abs(float(x)), 2.0 ** -14))) - 10)
 
