@@ -254,6 +254,38 @@ int ortmi_group_query_attention_ex(
     void* stream);
 
 /*
+ * GroupQueryAttention with sliding_window_cache = 1: past_key / past_value
+ * [batch, kv_num_heads, past_cap, head_size] are a compacting cache. Per sequence
+ * b, p = max(seqlens_k[b] + 1 - seq_len, 0) tokens precede the new ones and the
+ * cache holds the last cache_end(p) of them in rows [0, cache_end(p)), where
+ * cache_end(n) = n for n <= past_cap, else n - gap * ceil((n - past_cap) / gap)
+ * with gap = past_cap - local_window_size + 1 (the cache drops its oldest gap rows
+ * whenever it is full). Query s of sequence b, at position p + s (its RoPE
+ * position too), attends the positions (p + s - local_window_size, p + s].
+ * present_key / present_value [batch, kv_num_heads, past_cap, head_size] receive
+ * the last cache_end(p + seq_len) rows (new K rows RoPE'd), zeros after; they may
+ * be the past buffers themselves. seqlens_k is device int32 [batch]; RoPE
+ * positions past the cos/sin rows read the last row. q_norm_weight /
+ * k_norm_weight, dtypes and head sizes as ortmi_group_query_attention_ex; no
+ * attention_bias (the reference declines the pair). The workspace holds
+ * ortmi_group_query_attention_sliding_workspace_size bytes.
+ * Replaces: the sliding-cache branch of group_query_attention_op
+ * (rust/src/ops/attention.rs:725-880) and its causal_window_mask (191-219).
+ */
+size_t ortmi_group_query_attention_sliding_workspace_size(int64_t batch, int64_t seq_len,
+                                                          int64_t num_heads,
+                                                          int64_t kv_num_heads,
+                                                          int64_t head_size, int64_t past_cap);
+int ortmi_group_query_attention_sliding(
+    const void* query, const void* key, const void* value, const void* past_key,
+    const void* past_value, int64_t past_cap, const int32_t* seqlens_k, const void* cos_cache,
+    const void* sin_cache, int64_t rotary_half, int64_t max_pos, const void* q_norm_weight,
+    const void* k_norm_weight, float qk_norm_epsilon, int64_t local_window_size, void* output,
+    void* present_key, void* present_value, int64_t batch, int64_t seq_len, int64_t num_heads,
+    int64_t kv_num_heads, int64_t head_size, float scale, int32_t rotary_interleaved,
+    int32_t dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * ortmi_group_query_attention without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). It has no counterpart in the

@@ -78,6 +78,10 @@ SIGNATURES = {
         _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _i64,
         _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _vp,
         _sz, _vp]),
+    "ortmi_group_query_attention_sliding_workspace_size": (_sz, [_i64] * 6),
+    "ortmi_group_query_attention_sliding": (ctypes.c_int, [
+        _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _f32, _i64, _vp, _vp,
+        _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
     "ortmi_group_query_attention_noalloc_max_workspace": (_sz, []),
     "ortmi_group_query_attention_noalloc": (ctypes.c_int, [
         _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64,
@@ -128,6 +132,7 @@ from .ops import (  # noqa: E402,F401
     gather_block_quantized,
     group_query_attention,
     group_query_attention_decode_capturable,
+    group_query_attention_sliding,
     matmul_nbits,
     paged_attention,
     rotary_embedding,

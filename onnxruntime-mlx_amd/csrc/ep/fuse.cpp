@@ -330,6 +330,7 @@ void mark_attention_merge(GraphIR& g, const std::vector<std::string>& outputs) {
     auto uses = count_uses(g, outputs);
     for (auto& n : g.nodes) {
         if (n.op != "GroupQueryAttention" || n.outputs.empty() || n.outputs[0].empty()) continue;
+        if (n.attr_int("sliding_window_cache", 0)) continue;  // its output is always whole
         const std::string& y = n.outputs[0];
         if (uses[y] != 1) continue;
         const int64_t H = n.attr_int("num_heads", 0);

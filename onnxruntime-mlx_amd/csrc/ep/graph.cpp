@@ -354,13 +354,28 @@ std::string claim_gqa(const NodeDesc& n, const GraphIR& g) {
             REQUIRE(w && w->has_shape && w->dims.size() == 1 && w->dims[0] == qhd,
                     "Q/K norm weights must have shape [head_size]");
         }
-    // The ring-buffer sliding-window cache (attention.rs:725-880) is not built. A
-    // local_window_size without it is carried by attention_bias in the reference's
-    // Gemma3n form (attention.rs:256-262); without a bias the reference ignores the
-    // window while ORT applies it, so that form is declined.
-    REQUIRE(n.attr_int("sliding_window_cache", 0) == 0, "sliding_window_cache is not supported");
-    REQUIRE(n.attr_int("local_window_size", -1) == -1 || n.has_input(10),
-            "local_window_size without attention_bias is not supported");
+    // The sliding-window cache (attention.rs:725-880, claim 1552-1575). Otherwise a
+    // local_window_size is carried by attention_bias in the reference's Gemma3n
+    // form (attention.rs:256-262); without a bias the reference ignores the window
+    // while ORT applies it, so that form is declined.
+    if (n.attr_int("sliding_window_cache", 0) != 0) {
+        const int64_t window = n.attr_int("local_window_size", -1);
+        REQUIRE(window > 0, "sliding_window_cache=1 requires local_window_size > 0");
+        REQUIRE(!n.has_input(10), "sliding_window_cache is incompatible with attention_bias");
+        REQUIRE(n.has_input(3) && n.outputs.size() >= 3 && !n.outputs[1].empty() &&
+                    !n.outputs[2].empty(),
+                "sliding_window_cache requires past and present key/value");
+        auto* pk = val(g, n, 3);
+        auto* pv = val(g, n, 4);
+        REQUIRE(pk->dims[2] < 0 || pk->dims[2] >= window,
+                "sliding-window key cache capacity must be at least local_window_size");
+        REQUIRE(!pv || !pv->has_shape || pv->dims.size() != 4 || pv->dims[2] < 0 ||
+                    pv->dims[2] >= window,
+                "sliding-window value cache capacity must be at least local_window_size");
+    } else {
+        REQUIRE(n.attr_int("local_window_size", -1) == -1 || n.has_input(10),
+                "local_window_size without attention_bias is not supported");
+    }
     REQUIRE(n.attr_float("softcap", 0.f) == 0.f, "softcap is not supported");
     REQUIRE(n.attr_int("smooth_softmax", 0) == 0, "smooth_softmax is not supported");
     REQUIRE(n.attr_int("qk_output", 0) == 0, "qk_output is not supported");

@@ -233,6 +233,7 @@ void Plan::match_decode_program() {
             dprog_reject_ = "GroupQueryAttention rotary form";
             return;
         }
+        if (g->attr_int("sliding_window_cache", 0)) return reject("sliding-window KV cache");
         if (!in_list(inputs_, g->inputs[3]) || !in_list(inputs_, g->inputs[4]) ||
             !in_list(outputs_, g->outputs[1]) || !in_list(outputs_, g->outputs[2]))
             return reject("KV caches are not node inputs and outputs");
@@ -852,6 +853,57 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         Tensor* vp = in(2);
         Tensor* pk = in(3);
         Tensor* pv = in(4);
+        if (n.attr_int("sliding_window_cache", 0)) {  // claim_gqa: past and present given
+            const int64_t H = n.attr_int("num_heads", 0), KV = n.attr_int("kv_num_heads", 0);
+            const int64_t B = q.dims[0], S = q.dims[1];
+            const bool packed = kp == nullptr;
+            const int64_t hd = packed ? q.dims[2] / (H + 2 * KV) : q.dims[2] / H;
+            if (!pk || !pv || pk->dims.size() != 4 || pv->dims != pk->dims)
+                fail("GroupQueryAttention: sliding cache needs past key/value of one shape",
+                     ORT_INVALID_ARGUMENT);
+            const int64_t cap = pk->dims[2];
+            Tensor& seq = need(5);
+            if (seq.numel() != B)
+                fail("GroupQueryAttention: seqlens_k must have one value per batch",
+                     ORT_INVALID_ARGUMENT);
+            const bool rotary = n.attr_int("do_rotary", 0) != 0;
+            Tensor* cs = rotary ? in(7) : nullptr;
+            Tensor* sn = rotary ? in(8) : nullptr;
+            if (cs && seq.host) {  // host lengths: positions checked against the cos/sin rows
+                const int32_t* sl = static_cast<const int32_t*>(seq.host);
+                for (int64_t b = 0; b < B; ++b)
+                    if (std::max<int64_t>((int64_t)sl[b] + 1 - S, 0) + S > cs->dims[0])
+                        fail("GroupQueryAttention: position exceeds the cos/sin cache",
+                             ORT_INVALID_ARGUMENT);
+            }
+            for (Tensor* t : {pk, pv})
+                if (t->lazy) {
+                    check_hip(hipMemcpyAsync(t->ptr, t->host, (size_t)t->numel() * dtype_size(t->dtype),
+                                             hipMemcpyHostToDevice, stream_),
+                              "stage past");
+                    t->lazy = false;
+                }
+            Tensor& O = out_tensor(outname(0), q.dtype, {B, S, H * hd}, a, ctx);
+            void* optr = O.ptr;
+            void* prk = out_tensor(outname(1), q.dtype, pk->dims, a, ctx).ptr;
+            void* prv = out_tensor(outname(2), q.dtype, pk->dims, a, ctx).ptr;
+            Tensor* qnw = in(14);
+            Tensor* knw = in(15);
+            const size_t wsb =
+                ortmi_group_query_attention_sliding_workspace_size(B, S, H, KV, hd, cap);
+            void* ws = workspace(wsb);
+            check_kernel(ortmi_group_query_attention_sliding(
+                             q.ptr, kp ? kp->ptr : nullptr, vp ? vp->ptr : nullptr, pk->ptr,
+                             pv->ptr, cap, static_cast<const int32_t*>(seq.ptr),
+                             cs ? cs->ptr : nullptr, sn ? sn->ptr : nullptr, cs ? cs->dims[1] : 0,
+                             cs ? cs->dims[0] : 0, qnw ? qnw->ptr : nullptr,
+                             knw ? knw->ptr : nullptr, n.attr_float("qk_norm_epsilon", 1e-6f),
+                             n.attr_int("local_window_size", -1), optr, prk, prv, B, S, H, KV, hd,
+                             n.attr_float("scale", 0.f), (int32_t)n.attr_int("rotary_interleaved", 0),
+                             kdt(q.dtype), ws, wsb, st),
+                         "GroupQueryAttention");
+            return;
+        }
         const int32_t total = host_i32(n.inputs[6]);
         const int64_t H = n.attr_int("num_heads", 0), KV = n.attr_int("kv_num_heads", 0);
         const int64_t B = q.dims[0], S = q.dims[1];

@@ -14,6 +14,13 @@
 //    merged through LDS. Causal: query s attends keys [0, valid_past + s].
 // The KV contract (shared buffer vs growing, attention.rs:636-651) is that of
 // ortmi_group_query_attention.
+//
+// The sliding-window cache (sliding_window_cache = 1, attention.rs:725-880) adds
+// two: gqa_sw_attn_kernel (the same teams, keys read from the cached rows and the
+// new rows of the query's window) and gqa_sw_present_kernel (the compacted
+// present: the last cache_end(length) rows, zeros after). The prep kernel then
+// takes per-sequence positions from seqlens_k and writes the new K/V rows to a
+// workspace instead of present.
 
 #include <algorithm>
 #include <cmath>
@@ -54,17 +61,25 @@ __global__ __launch_bounds__(64) void gqa_ex_prep_kernel(
     int64_t kv_stride, const T* __restrict__ cos_c, const T* __restrict__ sin_c, int half,
     int interleaved, const T* __restrict__ qw, const T* __restrict__ kw, float eps,
     float* __restrict__ qf, T* __restrict__ pk, T* __restrict__ pv, int S, int H, int KV, int hd,
-    int64_t pcap, int vp) {
+    int64_t pcap, int vp, const int* __restrict__ seqlens, int max_pos) {
     __shared__ float sx[kMaxHead];
     const int bs = blockIdx.x;
     const int b = bs / S, s = bs % S;
     const int head = blockIdx.y;
     const int lane = threadIdx.x;
-    const int64_t pos = vp + s;
+    // Rotary position and destination row: valid_past + s for the dense contracts;
+    // with seqlens (the sliding-window cache) the sequence's own past length
+    // max(seqlens_k + 1 - S, 0) + s, clamped to the cos/sin rows, and row s of the
+    // [B, KV, S, hd] new-row workspace.
+    int64_t pos = vp + s, row = vp + s;
+    if (seqlens) {
+        pos = min(max((int64_t)seqlens[b] + 1 - S, (int64_t)0) + s, (int64_t)max(max_pos - 1, 0));
+        row = s;
+    }
     if (head >= H + KV) {  // V head: copied as is
         const int kh = head - H - KV;
         const T* src = v + (int64_t)bs * kv_stride + (int64_t)kh * hd;
-        T* dst = pv + (((int64_t)b * KV + kh) * pcap + pos) * hd;
+        T* dst = pv + (((int64_t)b * KV + kh) * pcap + row) * hd;
         for (int d = lane; d < hd; d += 64) dst[d] = src[d];
         return;
     }
@@ -123,12 +138,134 @@ __global__ __launch_bounds__(64) void gqa_ex_prep_kernel(
             if (d < hd) dst[d] = x[e];
         }
     } else {
-        T* dst = pk + (((int64_t)b * KV + kh) * pcap + pos) * hd;
+        T* dst = pk + (((int64_t)b * KV + kh) * pcap + row) * hd;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int d = lane + 64 * e;
             if (d < hd) dst[d] = from_f32<T>(x[e]);
         }
+    }
+}
+
+// Rows a sliding-window cache of capacity cap holds after `length` tokens: once
+// full it drops its oldest gap = cap - window + 1 rows at a time
+// (attention.rs:736-745).
+__device__ __forceinline__ int64_t sw_cache_end(int64_t length, int64_t cap, int64_t gap) {
+    if (length <= cap) return length;
+    return length - gap * ((length - cap + gap - 1) / gap);
+}
+
+// Sliding-window attention, grid (B*S*H), block 256 (the teams of
+// gqa_ex_attn_kernel). The sequence's p = max(seqlens_k + 1 - S, 0) earlier
+// tokens sit in cache rows [0, before), the last `before` of them; query s (position
+// t = p + s) attends positions (t - window, t]: cached rows first, then the new
+// rows (the workspace written by the prep kernel). Equal to the reference's
+// working buffer with its causal window mask (attention.rs:786-839).
+template <typename T>
+__global__ __launch_bounds__(256) void gqa_sw_attn_kernel(
+    const float* __restrict__ qf, const T* __restrict__ past_k, const T* __restrict__ past_v,
+    const T* __restrict__ knew, const T* __restrict__ vnew, const int* __restrict__ seqlens,
+    T* __restrict__ out, int S, int H, int KV, int hd, int cap, int window, float scale) {
+    __shared__ float s_m[kTeams], s_l[kTeams];
+    __shared__ float s_acc[kTeams][kMaxHead];
+    const int row = blockIdx.x;  // (b*S + s)*H + h
+    const int h = row % H;
+    const int bs = row / H;
+    const int b = bs / S, s = bs % S;
+    const int kh = h / (H / KV);
+    const int team = threadIdx.x / kTeamLanes;
+    const int lt = threadIdx.x % kTeamLanes;
+    const int E = hd / kTeamLanes;
+    const int64_t p = max((int64_t)seqlens[b] + 1 - S, (int64_t)0);
+    const int64_t before = sw_cache_end(p, cap, cap - window + 1);
+    const int64_t t = p + s;
+    const int64_t lo = max(t - window + 1, (int64_t)0);
+    const int npast = (int)max(p - lo, (int64_t)0);      // cached keys, rows [before - npast, before)
+    const int first_new = (int)max(lo - p, (int64_t)0);  // new keys [first_new, s]
+    const int nk = npast + s - first_new + 1;
+    const int64_t slab = (int64_t)b * KV + kh;
+    const T* kc = past_k + (slab * cap + (before - npast)) * hd;
+    const T* vc = past_v + (slab * cap + (before - npast)) * hd;
+    const T* kn = knew + (slab * S + first_new) * hd;
+    const T* vn = vnew + (slab * S + first_new) * hd;
+    const float* qrow = qf + (int64_t)row * hd;
+
+    float qv[kMaxPerLane], acc[kMaxPerLane];
+#pragma unroll
+    for (int e = 0; e < kMaxPerLane; ++e) {
+        qv[e] = e < E ? qrow[lt + kTeamLanes * e] : 0.f;
+        acc[e] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    for (int base = 0; base < nk; base += kTeams) {
+        const int j = base + team;
+        if (j >= nk) continue;  // uniform over the team's 16 lanes
+        const bool cached = j < npast;
+        const T* kr = cached ? kc + (int64_t)j * hd : kn + (int64_t)(j - npast) * hd;
+        const T* vr = cached ? vc + (int64_t)j * hd : vn + (int64_t)(j - npast) * hd;
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < kMaxPerLane; ++e)
+            if (e < E) dot += qv[e] * to_f32(kr[lt + kTeamLanes * e]);
+        const float sc = group_sum<kTeamLanes>(dot) * scale;
+        const float mn = fmaxf(m, sc);
+        const float corr = __expf(m - mn);  // m = -inf -> 0
+        const float pe = __expf(sc - mn);
+        l = l * corr + pe;
+#pragma unroll
+        for (int e = 0; e < kMaxPerLane; ++e)
+            if (e < E) acc[e] = acc[e] * corr + pe * to_f32(vr[lt + kTeamLanes * e]);
+        m = mn;
+    }
+    if (lt == 0) {
+        s_m[team] = m;
+        s_l[team] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < kMaxPerLane; ++e)
+        if (e < E) s_acc[team][lt + kTeamLanes * e] = acc[e];
+    __syncthreads();
+    float M = -INFINITY;
+    for (int tm = 0; tm < kTeams; ++tm) M = fmaxf(M, s_m[tm]);
+    T* orow = out + (int64_t)row * hd;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float num = 0.f, den = 0.f;
+        for (int tm = 0; tm < kTeams; ++tm) {
+            if (s_m[tm] == -INFINITY) continue;
+            const float wt = __expf(s_m[tm] - M);
+            num += wt * s_acc[tm][d];
+            den += wt * s_l[tm];
+        }
+        orow[d] = from_f32<T>(num / den);
+    }
+}
+
+// The compacted present of a sliding-window cache, 32-bit words over
+// [B, KV, cap, hd]: row r < after = cache_end(p + S) holds position
+// p + S - after + r (a cached row of src when before p, else a new row), rows from
+// `after` on are zero (attention.rs:840-862). src is the past cache, or a copy of
+// it when present is the same buffer (rows move towards the front).
+__global__ __launch_bounds__(256) void gqa_sw_present_kernel(
+    const uint32_t* __restrict__ src, const uint32_t* __restrict__ knew, uint32_t* __restrict__ dst,
+    const int* __restrict__ seqlens, int S, int KV, int cap, int window, int row_words,
+    int64_t total) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int w = (int)(i % row_words);
+        const int64_t rr = i / row_words;
+        const int r = (int)(rr % cap);
+        const int64_t slab = rr / cap;
+        const int b = (int)(slab / KV);
+        const int64_t p = max((int64_t)seqlens[b] + 1 - S, (int64_t)0);
+        const int gap = cap - window + 1;
+        const int64_t after = sw_cache_end(p + S, cap, gap);
+        uint32_t x = 0u;
+        if (r < after) {
+            const int64_t a = p + S - after + r;
+            x = a < p ? src[(slab * cap + (a - p + sw_cache_end(p, cap, gap))) * row_words + w]
+                      : knew[(slab * S + (a - p)) * row_words + w];
+        }
+        dst[i] = x;
     }
 }
 
@@ -250,13 +387,72 @@ int run_gqa_ex(const void* query, const void* key, const void* value, const void
                        q_stride, kv_stride, static_cast<const T*>(cos_c),
                        static_cast<const T*>(sin_c), half, interleaved, static_cast<const T*>(qw),
                        static_cast<const T*>(kw), eps, qf, static_cast<T*>(pk),
-                       static_cast<T*>(pv), S, H, KV, hd, pcap, vp);
+                       static_cast<T*>(pv), S, H, KV, hd, pcap, vp, nullptr, 0);
     if (int rc = check_launch("gqa_ex_prep")) return rc;
     hipLaunchKernelGGL((gqa_ex_attn_kernel<T>), dim3(B * S * H), dim3(256), 0, st, qf,
                        static_cast<const T*>(pk), static_cast<const T*>(pv),
                        static_cast<const T*>(bias), sb, sh, ss, static_cast<T*>(output), S, H, KV,
                        hd, pcap, vp, sc);
     return check_launch("gqa_ex_attn");
+}
+
+
+// Sliding-window cache (attention.rs:725-880): prep (positions from seqlens_k, new
+// rows to the workspace), attention over each query's window, then the compacted
+// present. When present is the past buffer its rows move towards the front, so
+// the past is copied aside first.
+template <typename T>
+int run_gqa_sliding(const void* query, const void* key, const void* value, const void* past_key,
+                    const void* past_value, int cap, const int* seqlens, const void* cos_c,
+                    const void* sin_c, int half, int max_pos, int interleaved, const void* qw,
+                    const void* kw, float eps, int window, void* output, void* pk, void* pv,
+                    int B, int S, int H, int KV, int hd, float scale, void* ws, hipStream_t st) {
+    const bool packed = key == nullptr;
+    const int64_t q_stride = packed ? (int64_t)(H + 2 * KV) * hd : (int64_t)H * hd;
+    const int64_t kv_stride = packed ? q_stride : (int64_t)KV * hd;
+    const T* q = static_cast<const T*>(query);
+    const T* k = packed ? q + (int64_t)H * hd : static_cast<const T*>(key);
+    const T* v = packed ? q + (int64_t)(H + KV) * hd : static_cast<const T*>(value);
+    const float sc = scale != 0.f ? scale : 1.0f / sqrtf((float)hd);
+    char* w = static_cast<char*>(ws);
+    float* qf = reinterpret_cast<float*>(w);
+    w += align256((size_t)B * S * H * hd * 4);
+    const size_t new_bytes = align256((size_t)B * KV * S * hd * sizeof(T));
+    T* knew = reinterpret_cast<T*>(w);
+    T* vnew = reinterpret_cast<T*>(w + new_bytes);
+    w += 2 * new_bytes;
+    hipLaunchKernelGGL((gqa_ex_prep_kernel<T>), dim3(B * S, H + 2 * KV), dim3(64), 0, st, q, k, v,
+                       q_stride, kv_stride, static_cast<const T*>(cos_c),
+                       static_cast<const T*>(sin_c), half, interleaved, static_cast<const T*>(qw),
+                       static_cast<const T*>(kw), eps, qf, knew, vnew, S, H, KV, hd, (int64_t)S, 0,
+                       seqlens, max_pos);
+    if (int rc = check_launch("gqa_sliding_prep")) return rc;
+    hipLaunchKernelGGL((gqa_sw_attn_kernel<T>), dim3(B * S * H), dim3(256), 0, st, qf,
+                       static_cast<const T*>(past_key), static_cast<const T*>(past_value), knew,
+                       vnew, seqlens, static_cast<T*>(output), S, H, KV, hd, cap, window, sc);
+    if (int rc = check_launch("gqa_sliding_attn")) return rc;
+    const int row_words = hd * (int)sizeof(T) / 4;
+    const int64_t total_w = (int64_t)B * KV * cap * row_words;
+    if (total_w == 0) return ORTMI_OK;
+    const int grid = (int)std::min<int64_t>((total_w + 255) / 256, 65536);
+    const void* srcs[2] = {past_key, past_value};
+    const T* news[2] = {knew, vnew};
+    void* dsts[2] = {pk, pv};
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t* src = static_cast<const uint32_t*>(srcs[i]);
+        if (srcs[i] == dsts[i]) {  // in place: read the old rows from a copy
+            uint32_t* copy = reinterpret_cast<uint32_t*>(w);
+            hipLaunchKernelGGL(kv_rows_copy_kernel, dim3(grid), dim3(256), 0, st, src, copy,
+                               (int64_t)cap, (int64_t)cap, (int64_t)cap, row_words, total_w);
+            src = copy;
+        }
+        hipLaunchKernelGGL(gqa_sw_present_kernel, dim3(grid), dim3(256), 0, st, src,
+                           reinterpret_cast<const uint32_t*>(news[i]),
+                           static_cast<uint32_t*>(dsts[i]), seqlens, S, KV, cap, window,
+                           row_words, total_w);
+        if (int rc = check_launch("gqa_sliding_present")) return rc;
+    }
+    return ORTMI_OK;
 }
 
 }  // namespace
@@ -344,5 +540,72 @@ extern "C" int ortmi_group_query_attention_ex(
     if (dtype == ORTMI_F16) ORTMI_GQA_EX(half_t);
     if (dtype == ORTMI_BF16) ORTMI_GQA_EX(uint16_t);
 #undef ORTMI_GQA_EX
+    return fail(ORTMI_E_INVALID, "GroupQueryAttention: dtype must be fp32, fp16 or bf16");
+}
+
+extern "C" size_t ortmi_group_query_attention_sliding_workspace_size(int64_t batch,
+                                                                     int64_t seq_len,
+                                                                     int64_t num_heads,
+                                                                     int64_t kv_num_heads,
+                                                                     int64_t head_size,
+                                                                     int64_t past_cap) {
+    if (batch <= 0 || seq_len <= 0 || num_heads <= 0 || kv_num_heads <= 0 || head_size <= 0 ||
+        past_cap < 0)
+        return 0;
+    // fp32 queries, new K/V rows and one past copy, sized for 4-byte elements.
+    return align256((size_t)batch * seq_len * num_heads * head_size * 4) +
+           2 * align256((size_t)batch * kv_num_heads * seq_len * head_size * 4) +
+           align256((size_t)batch * kv_num_heads * past_cap * head_size * 4);
+}
+
+extern "C" int ortmi_group_query_attention_sliding(
+    const void* query, const void* key, const void* value, const void* past_key,
+    const void* past_value, int64_t past_cap, const int32_t* seqlens_k, const void* cos_cache,
+    const void* sin_cache, int64_t rotary_half, int64_t max_pos, const void* q_norm_weight,
+    const void* k_norm_weight, float qk_norm_epsilon, int64_t local_window_size, void* output,
+    void* present_key, void* present_value, int64_t batch, int64_t seq_len, int64_t num_heads,
+    int64_t kv_num_heads, int64_t head_size, float scale, int32_t rotary_interleaved,
+    int32_t dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    // attention.rs:725-735 and the claim at 1552-1575.
+    ORTMI_REQUIRE(num_heads > 0 && kv_num_heads > 0 && num_heads % kv_num_heads == 0,
+                  "GroupQueryAttention: num_heads must be a positive multiple of kv_num_heads");
+    ORTMI_REQUIRE(head_size > 0 && head_size % 16 == 0 && head_size <= 256,
+                  "GroupQueryAttention: head_size must be a multiple of 16 up to 256");
+    ORTMI_REQUIRE(batch > 0 && seq_len > 0 && num_heads <= 65535 && past_cap <= 0x7fffffffLL &&
+                      batch * seq_len * num_heads <= 0x7fffffffLL,
+                  "GroupQueryAttention: bad shape");
+    ORTMI_REQUIRE(local_window_size > 0 && local_window_size <= past_cap,
+                  "GroupQueryAttention: sliding cache requires 0 < local_window_size <= capacity");
+    ORTMI_REQUIRE(query && output && present_key && present_value && past_key && past_value &&
+                      seqlens_k,
+                  "GroupQueryAttention: null tensor");
+    ORTMI_REQUIRE((key == nullptr) == (value == nullptr),
+                  "GroupQueryAttention: key and value must both be given or both be packed");
+    ORTMI_REQUIRE((q_norm_weight == nullptr) == (k_norm_weight == nullptr),
+                  "GroupQueryAttention: q_norm_weight and k_norm_weight must be provided together");
+    const bool rotary = cos_cache != nullptr;
+    ORTMI_REQUIRE(rotary == (sin_cache != nullptr),
+                  "GroupQueryAttention: cos_cache and sin_cache must both be given");
+    if (rotary)
+        ORTMI_REQUIRE(rotary_half > 0 && 2 * rotary_half <= head_size && max_pos > 0,
+                      "GroupQueryAttention: rotary dim exceeds head_size");
+    if ((past_key == present_key) != (past_value == present_value))
+        return fail(ORTMI_E_INVALID, "GroupQueryAttention: present_key/value alias mismatch");
+    const size_t need = ortmi_group_query_attention_sliding_workspace_size(
+        batch, seq_len, num_heads, kv_num_heads, head_size, past_cap);
+    if (!workspace || workspace_bytes < need)
+        return fail(ORTMI_E_WORKSPACE, "GroupQueryAttention: workspace too small");
+    hipStream_t st = as_stream(stream);
+#define ORTMI_GQA_SW(T)                                                                          \
+    return run_gqa_sliding<T>(query, key, value, past_key, past_value, (int)past_cap, seqlens_k,  \
+                              cos_cache, sin_cache, (int)rotary_half, (int)max_pos,              \
+                              rotary_interleaved, q_norm_weight, k_norm_weight, qk_norm_epsilon, \
+                              (int)local_window_size, output, present_key, present_value,        \
+                              (int)batch, (int)seq_len, (int)num_heads, (int)kv_num_heads,       \
+                              (int)head_size, scale, workspace, st)
+    if (dtype == ORTMI_F32) ORTMI_GQA_SW(float);
+    if (dtype == ORTMI_F16) ORTMI_GQA_SW(half_t);
+    if (dtype == ORTMI_BF16) ORTMI_GQA_SW(uint16_t);
+#undef ORTMI_GQA_SW
     return fail(ORTMI_E_INVALID, "GroupQueryAttention: dtype must be fp32, fp16 or bf16");
 }

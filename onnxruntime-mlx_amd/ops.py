@@ -190,6 +190,41 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
     return out, present_key, present_value
 
 
+def group_query_attention_sliding(query, key, value, past_key, past_value, seqlens_k,
+                                  cos_cache=None, sin_cache=None, *, num_heads, kv_num_heads,
+                                  local_window_size, scale=0.0, do_rotary=0,
+                                  rotary_interleaved=0, present_key=None, present_value=None,
+                                  q_norm_weight=None, k_norm_weight=None, qk_norm_epsilon=1e-6,
+                                  stream=None):
+    """GroupQueryAttention with sliding_window_cache = 1 (rust/src/ops/attention.rs:725-880):
+    past_key/past_value [B, KV, cap, hd] are a compacting cache, seqlens_k (device
+    int32 [B]) gives each sequence's length minus one. Pass present_key=past_key /
+    present_value=past_value to compact in place. Returns (output, present_key,
+    present_value), present at capacity cap with zero rows after the kept ones."""
+    B, S, hidden = query.shape
+    packed = key is None
+    hd = hidden // (num_heads + 2 * kv_num_heads) if packed else hidden // num_heads
+    cap = past_key.shape[2]
+    if present_key is None:
+        present_key = torch.empty_like(past_key)
+    if present_value is None:
+        present_value = torch.empty_like(past_value)
+    out = torch.empty((B, S, num_heads * hd), dtype=query.dtype, device=query.device)
+    lib = load_kernels()
+    use_rope = bool(do_rotary) and cos_cache is not None
+    half = cos_cache.shape[1] if use_rope else 0
+    max_pos = cos_cache.shape[0] if use_rope else 0
+    ws = _workspace(lib.ortmi_group_query_attention_sliding_workspace_size(
+        B, S, num_heads, kv_num_heads, hd, cap), query.device)
+    check(lib.ortmi_group_query_attention_sliding(
+        _p(query), _p(key), _p(value), _p(past_key), _p(past_value), cap, _p(seqlens_k),
+        _p(cos_cache) if use_rope else None, _p(sin_cache) if use_rope else None, half, max_pos,
+        _p(q_norm_weight), _p(k_norm_weight), float(qk_norm_epsilon), int(local_window_size),
+        _p(out), _p(present_key), _p(present_value), B, S, num_heads, kv_num_heads, hd,
+        float(scale), int(rotary_interleaved), _dt(query), _p(ws), ws.numel(), _stream(stream)))
+    return out, present_key, present_value
+
+
 def group_query_attention_decode_capturable(query, key, value, kv_key, kv_value,
                                             total_sequence_length_device, cos_cache=None,
                                             sin_cache=None, *, num_heads, kv_num_heads,

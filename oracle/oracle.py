@@ -239,6 +239,112 @@ def gqa(q, k, v, past_k, past_v, total_seq_len, num_heads, kv_heads, cos=None, s
     return out, pk, pv, shared
 
 
+def _round_mode(x, mode):
+    """Rounds fp32 values to fp16 (mode 1) or bf16 (mode 2, nearest even); mode 0
+    keeps them."""
+    x = np.ascontiguousarray(x, np.float32)
+    if mode == 1:
+        return x.astype(np.float16).astype(np.float32)
+    if mode == 2:
+        b = x.view(np.uint32).astype(np.uint64)
+        b = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
+        return b.astype(np.uint32).view(np.float32)
+    return x
+
+
+def sliding_cache_end(length: int, cap: int, window: int) -> int:
+    """Rows a sliding-window cache of capacity `cap` holds after `length` tokens: once
+    full it drops its oldest cap - window + 1 rows at a time
+    (rust/src/ops/attention.rs:736-745)."""
+    gap = cap - window + 1
+    if length <= cap:
+        return length
+    return length - gap * ((length - cap + gap - 1) // gap)
+
+
+def gqa_sliding(q, k, v, past_k, past_v, seqlens_k, num_heads, kv_heads, window, cos=None,
+                sin=None, interleaved=False, scale=0.0, round16=0, q_norm=None, k_norm=None,
+                qk_eps=1e-6):
+    """GroupQueryAttention with sliding_window_cache = 1, restated from
+    rust/src/ops/attention.rs:725-880 (numpy, fp64 products).
+
+    Per batch b: p = max(seqlens_k[b] + 1 - S, 0) tokens precede the new ones, of
+    which the cache holds the last before = sliding_cache_end(p) in rows [0, before).
+    The working keys are the seed rows past[seed_start:before] followed by the S new
+    (RoPE'd at positions p..p+S-1) rows, seed_start = before - kept unless some batch
+    keeps fewer rows than its window needs (then 0, the staging form); query i
+    attends working key j when seed_rows + i - window < j <= seed_rows + i
+    (causal_window_mask, attention.rs:191-219). present = working rows from
+    write_start (the staging form drops the seed rows the cache does not keep),
+    zero rows after. Returns (out [B,S,H*hd] f32, present_k, present_v) with present
+    [B, KV, cap, hd]. round16: 0 fp32, 1 fp16, 2 bf16 rounding of the RoPE/QK-norm
+    outputs, as the op materialises them."""
+    q = _f32(q)
+    B, S, _ = q.shape
+    past_k, past_v = _f32(past_k), _f32(past_v)
+    _, KV, cap, hd = past_k.shape
+    H = num_heads
+    G = H // KV
+    k = _f32(k).reshape(B, S, KV, hd)
+    v = _f32(v).reshape(B, S, KV, hd)
+    qh = q.reshape(B, S, H, hd)
+    if not 0 < window <= cap:
+        raise ValueError("oracle: sliding cache requires 0 < local_window_size <= capacity")
+    sc = scale if scale != 0.0 else 1.0 / np.sqrt(hd)
+    seq = np.asarray(seqlens_k, np.int64).reshape(-1)
+
+    def qk_norm(x, w):
+        if w is None:
+            return x
+        x64 = x.astype(np.float64)
+        inv = 1.0 / np.sqrt((x64 * x64).mean(axis=-1, keepdims=True) + qk_eps)
+        return _round_mode((x64 * inv * _f32(w)).astype(np.float32), round16)
+
+    qh = qk_norm(qh, q_norm)
+    k = qk_norm(k, k_norm)
+    geo = []
+    staging = False
+    for b in range(B):
+        p = max(int(seq[b]) + 1 - S, 0)
+        before = sliding_cache_end(p, cap, window)
+        after = sliding_cache_end(p + S, cap, window)
+        kept = after - S
+        staging |= kept < min(p, window - 1)
+        geo.append((p, before, after, before - kept))
+    out = np.zeros((B, S, H, hd), np.float32)
+    pk = np.zeros((B, KV, cap, hd), np.float32)
+    pv = np.zeros((B, KV, cap, hd), np.float32)
+    for b, (p, before, after, seed_off) in enumerate(geo):
+        rows = np.arange(p, p + S)[None, :]
+        qb, kb = qh[b:b + 1].reshape(1, S, H * hd), k[b:b + 1].reshape(1, S, KV * hd)
+        if cos is not None:
+            qb = rotary(qb, rows, cos, sin, interleaved, round16=round16, num_heads=H)
+            kb = rotary(kb, rows, cos, sin, interleaved, round16=round16, num_heads=KV)
+        qb = qb.reshape(S, H, hd).astype(np.float64)
+        kb = kb.reshape(S, KV, hd)
+        seed_start = 0 if staging else seed_off
+        work_k = np.concatenate([past_k[b, :, seed_start:before], kb.transpose(1, 0, 2)], axis=1)
+        work_v = np.concatenate([past_v[b, :, seed_start:before],
+                                 v[b].transpose(1, 0, 2)], axis=1)
+        seed_rows = before - seed_start
+        k_len = seed_rows + S
+        j = np.arange(k_len)[None, :]
+        qpos = seed_rows + np.arange(S)[:, None]
+        allow = (j <= qpos) & (j >= qpos - window + 1)
+        for h in range(H):
+            kv = h // G
+            sco = (qb[:, h] @ work_k[kv].astype(np.float64).T) * sc
+            sco = np.where(allow, sco, -np.inf)
+            m = sco.max(axis=1, keepdims=True)
+            e = np.exp(sco - m)
+            out[b, :, h] = (e @ work_v[kv].astype(np.float64)) / e.sum(axis=1, keepdims=True)
+        write_start = seed_off if staging else 0
+        n = k_len - write_start
+        pk[b, :, :n] = work_k[:, write_start:]
+        pv[b, :, :n] = work_v[:, write_start:]
+    return out.reshape(B, S, H * hd), pk, pv
+
+
 # -------------------------------------------------------- PagedAttention ----
 def paged_attention(q, k, v, kcache, vcache, cum, past, block_table, num_heads, kv_heads,
                     cos=None, sin=None, interleaved=False, rotary_offset=0, slot_mapping=None,

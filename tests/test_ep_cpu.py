@@ -204,7 +204,9 @@ def gqa_graph(hd=64, extra=None, inputs_extra=(), dtype=F16, at=None):
     (72, None, (), False),                                  # head size without a kernel
     (128, dict(softcap=30.0), (), False),
     (128, dict(local_window_size=128), (), False),          # window with no bias to carry it
-    (128, dict(sliding_window_cache=1, local_window_size=16), (), False),
+    (128, dict(sliding_window_cache=1, local_window_size=16), (), True),   # cap 32 >= 16
+    (128, dict(sliding_window_cache=1, local_window_size=64), (), False),  # window > capacity
+    (128, dict(sliding_window_cache=1), (), False),         # no window
     (128, dict(smooth_softmax=1), (), False),
     (128, dict(kv_num_heads=3), (), False),                 # 4 % 3 != 0
     (128, None, (("pos", I64, [1, 1]),), False),            # position_ids with in-op rotary
@@ -232,6 +234,9 @@ HD = 64
     (F16, None, {11: ("sink", F16, [4])}, False),                              # head_sink
     (F16, None, {12: ("ks", F32, [1]), 13: ("vs", F32, [1])}, False),          # quantized KV
     (F16, dict(k_quant_type="PER_TENSOR"), {}, False),
+    (F32, dict(sliding_window_cache=1, local_window_size=8), {}, True),        # fp32 sliding
+    (F16, dict(sliding_window_cache=1, local_window_size=8),                   # with a bias
+     {10: ("bias", F16, [1, 1, 1, 32])}, False),
 ])
 def test_gqa_claim_optional_inputs(dtype, extra, at, claimed):
     """The optional GroupQueryAttention inputs the reference claims

@@ -19,7 +19,7 @@ from importlib import import_module
 
 import numpy as np
 import pytest
-from test_gpu_ops import _mnb_inputs, assert_f16_close, dev, host
+from test_gpu_ops import _mnb_inputs, assert_f16_close, dev, host, ulp16
 
 pytestmark = pytest.mark.gpu
 
@@ -706,3 +706,77 @@ def test_ep_decode_program_matches_op_path(ortmi, oracle, dec, monkeypatch):
     runner = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
     rows = _teacher_forced_check(oracle, runner, cfg, w, prompt.tolist(), steps=10)
     _assert_greedy_strict(rows, "decode program through the EP")
+
+
+def test_ep_gqa_sliding_window_cache(ortmi, oracle, hx):
+    """GroupQueryAttention with sliding_window_cache = 1 through the EP: a 5-token
+    prompt, a 3-token chunk and single tokens into a capacity-6, window-4 cache
+    that present compacts in place, each step against oracle.gqa_sliding on the
+    cache the step read; the same steps with the cache in host memory give
+    identical outputs and caches."""
+    import refs
+    import torch
+
+    H, KV, hd, cap, window = 4, 2, 64, 6, 4
+    c, s_ = refs.rotary_caches(64, hd, 1e4)
+    cos, sin = c.astype(np.float16), s_.astype(np.float16)
+    rng = np.random.default_rng(13)
+    steps = [5, 3, 1, 1, 2, 1, 1]
+    feeds = [tuple(rng.standard_normal((1, S, n * hd)).astype(np.float16) for n in (H, KV, KV))
+             for S in steps]
+
+    def run(on_device, check):
+        g = hx.Graph()
+        g.value("q", hx.FLOAT16, [1, -1, H * hd])
+        g.value("k", hx.FLOAT16, [1, -1, KV * hd])
+        g.value("v", hx.FLOAT16, [1, -1, KV * hd])
+        for n in ("pk", "pv", "ok", "ov"):
+            g.value(n, hx.FLOAT16, [1, KV, cap, hd])
+        g.value("sl", hx.INT32, [1])
+        g.value("tot", hx.INT32, [1])
+        g.value("o", hx.FLOAT16, [1, -1, H * hd])
+        g.initializer("cos", cos)
+        g.initializer("sin", sin)
+        g.node("GroupQueryAttention", ["q", "k", "v", "pk", "pv", "sl", "tot", "cos", "sin"],
+               ["o", "ok", "ov"], domain="com.microsoft", num_heads=H, kv_num_heads=KV,
+               do_rotary=1, sliding_window_cache=1, local_window_size=window)
+        g.io(["q", "k", "v", "pk", "pv", "sl", "tot"], ["o", "ok", "ov"])
+        sess = hx.Session(g)
+        assert sess.partitions() == [[0]]
+        kc = torch.zeros((1, KV, cap, hd), dtype=torch.float16)
+        vc = torch.zeros_like(kc)
+        if on_device:
+            kc, vc = kc.cuda(), vc.cuda()
+        sess.bind_output("ok", kc)
+        sess.bind_output("ov", vc)
+        outs, total = [], 0
+        for (q, k, v), S in zip(feeds, steps):
+            past_k, past_v = kc.float().cpu().numpy(), vc.float().cpu().numpy()
+            total += S
+            o = torch.empty((1, S, H * hd), dtype=torch.float16,
+                            device="cuda" if on_device else "cpu")
+            sess.bind_output("o", o)
+            t = (lambda a: torch.from_numpy(a).cuda()) if on_device else torch.from_numpy
+            sess.run({"q": (t(q), hx.FLOAT16), "k": (t(k), hx.FLOAT16),
+                      "v": (t(v), hx.FLOAT16), "pk": (kc, hx.FLOAT16), "pv": (vc, hx.FLOAT16),
+                      "sl": (torch.tensor([total - 1], dtype=torch.int32), hx.INT32),
+                      "tot": (torch.tensor([total], dtype=torch.int32), hx.INT32)})
+            torch.cuda.synchronize()
+            outs.append(o.cpu().clone())
+            if check:
+                ro, rk, rv = oracle.gqa_sliding(q, k, v, past_k, past_v, [total - 1], H, KV,
+                                                window, cos=cos, sin=sin, round16=1)
+                assert_f16_close(outs[-1].float().numpy().reshape(S, -1), ro.reshape(S, -1),
+                                 extra=ulp16(ro.reshape(S, -1)),
+                                 what=f"sliding step S={S} total={total}")
+                gk, gv = kc.float().cpu().numpy(), vc.float().cpu().numpy()
+                np.testing.assert_array_equal(gv, rv)
+                assert (np.abs(gk - rk) <= ulp16(rk)).all()
+        sess.close()
+        return outs, kc.cpu(), vc.cpu()
+
+    dev_outs, dk, dv = run(True, True)
+    host_outs, hk, hv = run(False, False)
+    for a, b in zip(host_outs, dev_outs):
+        assert torch.equal(a, b)
+    assert torch.equal(hk, dk) and torch.equal(hv, dv)

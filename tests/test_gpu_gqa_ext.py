@@ -283,3 +283,111 @@ def test_ep_gqa_node_bias_and_qk_norm(ortmi, oracle, dt):
         tol_k = 1e-6 + 1e-6 * np.abs(rk) if dt == "f32" else 2 * _ulp(rk, dt)
         assert (np.abs(gk - rk) <= tol_k).all()
         npk, npv = gk, rv
+
+
+# ------------------------------------------------------- sliding-window cache ---
+
+
+def _run_sliding(ortmi, oracle, dt, B, S, H, KV, hd, cap, window, seqlens, *, rope=True,
+                 interleaved=False, qk_norm=False, packed=False, inplace=False, seed=0,
+                 past=None):
+    """One sliding-cache step through ortmi.group_query_attention_sliding against
+    oracle.gqa_sliding on the same rounded inputs; returns the device present
+    (key, value) for the next step. past: (key, value) device tensors, or None for
+    random ones."""
+    import torch
+
+    rng = np.random.default_rng(seed)
+    q, nq = _cast(rng.standard_normal((B, S, H * hd)), dt)
+    k, nk = _cast(rng.standard_normal((B, S, KV * hd)), dt)
+    v, nv = _cast(rng.standard_normal((B, S, KV * hd)), dt)
+    if past is None:
+        pk, npk = _cast(rng.standard_normal((B, KV, cap, hd)), dt)
+        pv, npv = _cast(rng.standard_normal((B, KV, cap, hd)), dt)
+    else:
+        pk, pv = past
+        npk, npv = pk.float().cpu().numpy(), pv.float().cpu().numpy()
+    cos = sin = ncos = nsin = None
+    if rope:
+        c, s_ = refs.rotary_caches(max(seqlens) + S + 8, hd, 10000.0)
+        cos, ncos = _cast(c, dt)
+        sin, nsin = _cast(s_, dt)
+    qn = kn = nqn = nkn = None
+    if qk_norm:
+        qn, nqn = _cast(rng.uniform(0.5, 1.5, hd), dt)
+        kn, nkn = _cast(rng.uniform(0.5, 1.5, hd), dt)
+    if packed:
+        qin, kin, vin = torch.cat([q, k, v], dim=-1).contiguous(), None, None
+    else:
+        qin, kin, vin = q, k, v
+    kw = dict(present_key=pk, present_value=pv) if inplace else {}
+    sl = torch.tensor(seqlens, dtype=torch.int32, device="cuda")
+    out, prk, prv = ortmi.group_query_attention_sliding(
+        qin, kin, vin, pk, pv, sl, cos, sin, num_heads=H, kv_num_heads=KV,
+        local_window_size=window, do_rotary=int(rope), rotary_interleaved=int(interleaved),
+        q_norm_weight=qn, k_norm_weight=kn, qk_norm_epsilon=1e-5, **kw)
+    torch.cuda.synchronize()
+    ro, rk, rv = oracle.gqa_sliding(nq, nk, nv, npk, npv, seqlens, H, KV, window, cos=ncos,
+                                    sin=nsin, interleaved=interleaved, round16=_ROUND[dt],
+                                    q_norm=nqn, k_norm=nkn, qk_eps=1e-5)
+    got = out.float().cpu().numpy()
+    if dt == "f32":
+        tol = 1e-5 + 1e-5 * np.abs(ro)
+    elif dt == "f16":
+        tol = 1e-3 + 2 * ulp16(ro)
+    else:
+        tol = 4e-3 + 2.0 ** -6 * np.abs(ro)
+    bad = ~(np.abs(got - ro) <= tol)
+    assert not bad.any(), (f"{dt} sliding output: {bad.sum()} of {bad.size} beyond tolerance, "
+                           f"max diff {np.nanmax(np.abs(got - ro)):.3e}")
+    gk, gv = prk.float().cpu().numpy(), prv.float().cpu().numpy()
+    np.testing.assert_array_equal(gv, rv)
+    ulps = 2 if qk_norm else 1
+    for b in range(B):
+        p = max(seqlens[b] + 1 - S, 0)
+        after = oracle.sliding_cache_end(p + S, cap, window)
+        first_new = max(after - S, 0)  # rows [first_new, after) are this step's keys
+        np.testing.assert_array_equal(gk[b, :, :first_new], rk[b, :, :first_new])
+        np.testing.assert_array_equal(gk[b, :, after:], 0)
+        new_k, want_k = gk[b, :, first_new:after], rk[b, :, first_new:after]
+        tol_k = 1e-6 + 1e-6 * np.abs(want_k) if dt == "f32" else ulps * _ulp(want_k, dt)
+        assert (np.abs(new_k - want_k) <= tol_k).all(), \
+            f"new K rows: max diff {np.abs(new_k - want_k).max():.3e}"
+    return prk, prv
+
+
+# The reference's sliding_window_cache cases (tests/ops/test_mlx_ops.py:245-300).
+_SLIDING_REF = [
+    ("sliding-decode", dict(B=1, H=4, KV=2, hd=16, S=1, past=8, cap=5, rope=False, window=3)),
+    ("sliding-chunk-staging", dict(B=1, H=4, KV=2, hd=16, S=3, past=5, cap=5, rope=False,
+                                   window=4)),
+    ("sliding-batched-rope", dict(B=2, H=4, KV=2, hd=16, S=1, past=7, cap=6, rope=True,
+                                  window=4)),
+]
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+@pytest.mark.parametrize("name,g", _SLIDING_REF, ids=[c[0] for c in _SLIDING_REF])
+def test_gqa_sliding_reference_cases(ortmi, oracle, name, g, inplace):
+    seqlens = [g["past"] + g["S"] - 1] * g["B"]
+    _run_sliding(ortmi, oracle, "f32", g["B"], g["S"], g["H"], g["KV"], g["hd"], g["cap"],
+                 g["window"], seqlens, rope=g["rope"], inplace=inplace, seed=11)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_gqa_sliding_steps_in_place(ortmi, oracle, dt):
+    """Chunks and single tokens fed one after the other into one cache compacted in
+    place (present bound to past), through several reclaims: head 128, RoPE."""
+    past = None
+    length = 0
+    for i, S in enumerate([9, 3, 1, 1, 4, 1, 1, 1, 7, 1]):
+        past = _run_sliding(ortmi, oracle, dt, 1, S, 8, 2, 128, 12, 8, [length + S - 1],
+                            interleaved=True, inplace=True, seed=20 + i, past=past)
+        length += S
+
+
+def test_gqa_sliding_batches_qk_norm_packed(ortmi, oracle):
+    """Two sequences at different lengths (one needing the staging form, one not
+    yet full), packed QKV, QK-norm, head 64, fp16, separate present."""
+    _run_sliding(ortmi, oracle, "f16", 2, 3, 6, 3, 64, 5, 4, [5 + 3 - 1, 1 + 3 - 1],
+                 qk_norm=True, packed=True, seed=30)

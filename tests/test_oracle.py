@@ -350,6 +350,136 @@ def test_gqa_bf16_rounding_matches_torch(oracle):
     np.testing.assert_array_equal(prk[0].transpose(1, 0, 2).reshape(S, KV * hd), want[0])
 
 
+# ---------------------------------------------------- GQA sliding window cache ---
+
+
+def _sliding_history(rng, N, H, KV, hd, max_pos, interleaved):
+    """Queries, keys and values for N absolute positions, and the cos/sin cache."""
+    q = (rng.standard_normal((N, H * hd)) * 0.5).astype(np.float32)
+    k = (rng.standard_normal((N, KV * hd)) * 0.5).astype(np.float32)
+    v = rng.standard_normal((N, KV * hd)).astype(np.float32)
+    c, s_ = refs.rotary_caches(max_pos, hd)
+    return q, k, v, c.astype(np.float32), s_.astype(np.float32)
+
+
+def _windowed_attention(oracle, q, k, v, cos, sin, H, KV, hd, t, window, interleaved):
+    """Query at absolute position t over the keys at positions (t - window, t], each
+    key RoPE'd at its own position: the window read off the whole history, with no
+    cache in between."""
+    lo = max(0, t - window + 1)
+    pos = np.arange(lo, t + 1)
+    kr = oracle.rotary(k[None, lo:t + 1], pos[None], cos, sin, interleaved,
+                       num_heads=KV)[0].reshape(-1, KV, hd).astype(np.float64)
+    qr = oracle.rotary(q[None, t:t + 1], np.array([[t]]), cos, sin, interleaved,
+                       num_heads=H)[0].reshape(H, hd).astype(np.float64)
+    vv = v[lo:t + 1].reshape(-1, KV, hd).astype(np.float64)
+    out = np.zeros((H, hd))
+    for h in range(H):
+        kv = h // (H // KV)
+        sc = kr[:, kv] @ qr[h] / np.sqrt(hd)
+        e = np.exp(sc - sc.max())
+        out[h] = e @ vv[:, kv] / e.sum()
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("cap,window,chunks,interleaved", [
+    (5, 3, [1] * 12, 0),            # the reference's sliding-decode (past 8, cap 5, window 3)
+    (5, 4, [5, 3, 1, 2, 1, 4], 1),  # sliding-chunk-staging: 3 new rows on a full cache
+    (6, 4, [7, 1, 1, 3, 1], 0),     # sliding-batched-rope: past 7 on capacity 6
+    (8, 8, [2, 3, 3, 1, 1], 0),     # window = capacity: one row reclaimed at a time
+    (4, 1, [3, 2, 1], 1),           # window 1: each query sees only itself
+])
+def test_gqa_sliding_matches_windowed_history(oracle, cap, window, chunks, interleaved):
+    """Chunks fed one after the other, present back into past: every output row equals
+    attention over the window of the full history, and present holds the last
+    sliding_cache_end(length) keys (RoPE'd at their positions) and values in order,
+    zeros after. This pins the cache bookkeeping (the reclaim arithmetic, which rows
+    survive, the staging form) and the window bound independently of the reference's
+    working-buffer construction that the oracle restates."""
+    H, KV, hd = 4, 2, 16
+    N = sum(chunks)
+    rng = np.random.default_rng(cap * 100 + window * 10 + len(chunks))
+    q, k, v, cos, sin = _sliding_history(rng, N, H, KV, hd, N + 4, interleaved)
+    pk = rng.standard_normal((1, KV, cap, hd)).astype(np.float32)  # garbage past the valid rows
+    pv = rng.standard_normal((1, KV, cap, hd)).astype(np.float32)
+    length = 0
+    for S in chunks:
+        sl = slice(length, length + S)
+        out, pk, pv = oracle.gqa_sliding(q[None, sl], k[None, sl], v[None, sl], pk, pv,
+                                         [length + S - 1], H, KV, window, cos=cos, sin=sin,
+                                         interleaved=bool(interleaved))
+        for i in range(S):
+            want = _windowed_attention(oracle, q, k, v, cos, sin, H, KV, hd, length + i, window,
+                                       interleaved)
+            np.testing.assert_allclose(out[0, i], want, rtol=1e-5, atol=1e-6)
+        length += S
+        end = oracle.sliding_cache_end(length, cap, window)
+        first = length - end
+        krot = oracle.rotary(k[None, first:length], np.arange(first, length)[None], cos, sin,
+                             bool(interleaved), num_heads=KV)[0]
+        np.testing.assert_allclose(pk[0, :, :end].transpose(1, 0, 2).reshape(end, -1), krot,
+                                   rtol=1e-6, atol=1e-6)
+        np.testing.assert_array_equal(pv[0, :, :end].transpose(1, 0, 2).reshape(end, -1),
+                                      v[first:length])
+        assert not pk[0, :, end:].any() and not pv[0, :, end:].any()
+
+
+def test_gqa_sliding_cache_end_closed_form(oracle):
+    """Reclaim arithmetic against a step-by-step simulation: append one row at a time
+    and drop the oldest cap - window + 1 rows whenever a row would not fit."""
+    for cap in range(1, 9):
+        for window in range(1, cap + 1):
+            rows = 0
+            for length in range(1, 40):
+                if rows == cap:
+                    rows -= cap - window + 1
+                rows += 1
+                assert oracle.sliding_cache_end(length, cap, window) == rows
+
+
+def test_gqa_sliding_without_eviction_is_plain_gqa(oracle):
+    """No row reclaimed and a window covering every key: the shared-buffer GQA of
+    oracle.gqa, present included (its rows past the valid ones are old past rows
+    there and zeros here)."""
+    rng = np.random.default_rng(31)
+    B, S, H, KV, hd, cap, past = 2, 3, 6, 2, 32, 16, 7
+    q = rng.standard_normal((B, S, H * hd)).astype(np.float32)
+    k = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    v = rng.standard_normal((B, S, KV * hd)).astype(np.float32)
+    pk = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    pv = rng.standard_normal((B, KV, cap, hd)).astype(np.float32)
+    cos, sin = refs.rotary_caches(32, hd)
+    total = past + S
+    out, prk, prv = oracle.gqa_sliding(q, k, v, pk, pv, [total - 1] * B, H, KV, cap, cos=cos,
+                                       sin=sin)
+    ro, rk, rv, shared = oracle.gqa(q, k, v, pk, pv, total, H, KV, cos=cos, sin=sin)
+    assert shared
+    np.testing.assert_allclose(out, ro, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(prk[:, :, :total], rk[:, :, :total], rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(prv[:, :, :total], rv[:, :, :total])
+    assert not prk[:, :, total:].any()
+
+
+def test_gqa_sliding_batches_keep_their_own_geometry(oracle):
+    """Two sequences at different lengths in one call equal the two run alone, also
+    when only one of them needs the staging form (a global switch in the reference)."""
+    rng = np.random.default_rng(32)
+    H, KV, hd, cap, window, S = 4, 2, 16, 5, 4, 3
+    q = rng.standard_normal((2, S, H * hd)).astype(np.float32)
+    k = rng.standard_normal((2, S, KV * hd)).astype(np.float32)
+    v = rng.standard_normal((2, S, KV * hd)).astype(np.float32)
+    pk = rng.standard_normal((2, KV, cap, hd)).astype(np.float32)
+    pv = rng.standard_normal((2, KV, cap, hd)).astype(np.float32)
+    cos, sin = refs.rotary_caches(32, hd)
+    seqlens = [5 + S - 1, 1 + S - 1]  # past 5 (staging) and past 1 (no eviction)
+    both = oracle.gqa_sliding(q, k, v, pk, pv, seqlens, H, KV, window, cos=cos, sin=sin)
+    for b in range(2):
+        one = oracle.gqa_sliding(q[b:b + 1], k[b:b + 1], v[b:b + 1], pk[b:b + 1], pv[b:b + 1],
+                                 [seqlens[b]], H, KV, window, cos=cos, sin=sin)
+        for x, y in zip(both, one):
+            np.testing.assert_allclose(x[b], y[0], rtol=1e-6, atol=1e-7)
+
+
 # ------------------------------------------------------------ PagedAttention ---
 
 
