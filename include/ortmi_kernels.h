@@ -365,7 +365,10 @@ int ortmi_group_query_attention_decode_partials(
  * (optional, slot < 0 skips the write) are int32 device tensors: nothing is read
  * back to the host. max_context is a host upper bound on past + new tokens of
  * every sequence (max_blocks * block_size always is one); keys beyond it are not
- * attended. cos/sin caches are [rotary_max_pos, rotary_half]. head_sink [H],
+ * attended. dtype fp32, fp16 or bf16; head_size a multiple of 16 up to 256
+ * (fp16/bf16 with head 64/128 run the matrix-core tiles and the decode kernel,
+ * every other form one VALU workgroup per (token, head) row). cos/sin caches are
+ * [rotary_max_pos, rotary_half]. head_sink [H],
  * q_norm_weight/k_norm_weight [hd] optional. output [T,H*vhd]. Malformed control
  * tensors (block ids or positions out of range) never cause out-of-bounds
  * accesses: such keys are masked and such writes skipped.

@@ -72,21 +72,32 @@ __device__ void rms_head_lds(float* v, int hd, const T* w, float eps) {
 // Heads per prep workgroup, one wave each (fewer, fuller workgroups).
 constexpr int kPrepHeads = 4;
 
+// 16-bit element <-> its storage bits (fp32 rows never take the pair path).
+template <typename T>
+__device__ __forceinline__ T bits16_to(uint16_t b) {
+    if constexpr (sizeof(T) == 2) return __builtin_bit_cast(T, b);
+    else return T(0);
+}
+template <typename T>
+__device__ __forceinline__ uint32_t to_bits16(T x) {
+    if constexpr (sizeof(T) == 2) return __builtin_bit_cast(uint16_t, x);
+    else return 0u;
+}
 // Row traffic of the prep kernels in element pairs, one 32-bit access each (a
 // 128-dim row is one load instruction per wave instead of two 16-bit ones per
-// lane); a row start that is not 4-byte aligned takes single elements.
+// lane); a row start that is not 4-byte aligned, or a 32-bit row, takes single
+// elements.
 template <typename T>
 __device__ __forceinline__ bool pair_aligned(const T* p) {
     return (reinterpret_cast<uintptr_t>(p) & 3) == 0;
 }
 template <typename T>
 __device__ __forceinline__ void row_to_lds(float* sv, const T* src, int hd, int lane) {
-    static_assert(sizeof(T) == 2, "16-bit rows");
-    if (pair_aligned(src)) {
+    if (sizeof(T) == 2 && pair_aligned(src)) {
         for (int d2 = lane; d2 < hd / 2; d2 += 64) {
             const uint32_t w = reinterpret_cast<const uint32_t*>(src)[d2];
-            sv[2 * d2] = to_f32(__builtin_bit_cast(T, (uint16_t)(w & 0xffffu)));
-            sv[2 * d2 + 1] = to_f32(__builtin_bit_cast(T, (uint16_t)(w >> 16)));
+            sv[2 * d2] = to_f32(bits16_to<T>((uint16_t)(w & 0xffffu)));
+            sv[2 * d2 + 1] = to_f32(bits16_to<T>((uint16_t)(w >> 16)));
         }
     } else {
         for (int d = lane; d < hd; d += 64) sv[d] = to_f32(src[d]);
@@ -94,10 +105,10 @@ __device__ __forceinline__ void row_to_lds(float* sv, const T* src, int hd, int 
 }
 template <typename T>
 __device__ __forceinline__ void lds_to_row(T* dst, const float* sv, int hd, int lane) {
-    if (pair_aligned(dst)) {
+    if (sizeof(T) == 2 && pair_aligned(dst)) {
         for (int d2 = lane; d2 < hd / 2; d2 += 64) {
-            const uint32_t lo = __builtin_bit_cast(uint16_t, from_f32<T>(sv[2 * d2]));
-            const uint32_t hi = __builtin_bit_cast(uint16_t, from_f32<T>(sv[2 * d2 + 1]));
+            const uint32_t lo = to_bits16(from_f32<T>(sv[2 * d2]));
+            const uint32_t hi = to_bits16(from_f32<T>(sv[2 * d2 + 1]));
             reinterpret_cast<uint32_t*>(dst)[d2] = lo | (hi << 16);
         }
     } else {
@@ -106,7 +117,7 @@ __device__ __forceinline__ void lds_to_row(T* dst, const float* sv, int hd, int 
 }
 template <typename T>
 __device__ __forceinline__ void copy_row(T* dst, const T* src, int n, int lane) {
-    if (pair_aligned(dst) && pair_aligned(src)) {
+    if (sizeof(T) == 2 && pair_aligned(dst) && pair_aligned(src)) {
         for (int d2 = lane; d2 < n / 2; d2 += 64)
             reinterpret_cast<uint32_t*>(dst)[d2] = reinterpret_cast<const uint32_t*>(src)[d2];
     } else {
@@ -2362,6 +2373,156 @@ extern "C" size_t ortmi_paged_attention_workspace_size(int64_t num_tokens, int64
     return sz;
 }
 
+// PagedAttention for the forms the tile and decode kernels do not take: fp32, and
+// head sizes (and LATENT value sizes) that are multiples of 16 up to 256 other
+// than 64/128. The prep kernel writes RoPE'd/normalised queries and new keys to
+// the workspace and the new rows to their cache slots; paged_generic_attn_kernel
+// then gives each (token, head) row one workgroup of 16 teams x 16 lanes (the
+// layout of the generic GroupQueryAttention kernel): keys [0, past) come from the
+// cache through the block table, keys from past on from the new rows themselves
+// (as attention.rs:2640-2700 concatenates them), causal, with the head_sink logit
+// joining the softmax normaliser (attention.rs:2420-2450).
+constexpr int kGenTeams = 16, kGenLanes = 16, kGenMaxPerLane = 16;
+template <typename T>
+__global__ __launch_bounds__(256) void paged_generic_attn_kernel(
+    const T* __restrict__ qrot, const T* __restrict__ knew, const T* __restrict__ vnew,
+    const T* __restrict__ kcache, const T* __restrict__ vcache, int64_t nslots, int blk,
+    const int32_t* __restrict__ cum, const int32_t* __restrict__ past,
+    const int32_t* __restrict__ bt, int batch, int maxb, const float* __restrict__ sink,
+    T* __restrict__ out, int H, int KV, int hd, int vhd, float scale) {
+    __shared__ float s_m[kGenTeams], s_l[kGenTeams];
+    __shared__ float s_acc[kGenTeams][kGenLanes * kGenMaxPerLane];
+    const int row = blockIdx.x;  // tok * H + h
+    const int h = row % H, tok = row / H;
+    const int kvh = h / (H / KV);
+    const int team = threadIdx.x / kGenLanes, lt = threadIdx.x % kGenLanes;
+    const int E = hd / kGenLanes, EV = vhd / kGenLanes;
+    int lo = 0, hi = batch;  // the sequence: last b with cum[b] <= tok
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (cum[mid] <= tok) lo = mid;
+        else hi = mid;
+    }
+    const int b = lo, s0 = cum[b], pb = max(past[b], 0);
+    const int nk = pb + (tok - s0) + 1;  // causal: keys [0, past + i]
+    // LATENT (vcache == nullptr): values are the first vhd dims of the key rows.
+    const int64_t kslot = (int64_t)KV * hd, vslot = (int64_t)KV * vhd;
+    const T* qrow = qrot + (int64_t)row * hd;
+    float qv[kGenMaxPerLane], acc[kGenMaxPerLane];
+#pragma unroll
+    for (int e = 0; e < kGenMaxPerLane; ++e) {
+        qv[e] = e < E ? to_f32(qrow[lt + kGenLanes * e]) : 0.f;
+        acc[e] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    for (int base = 0; base < nk; base += kGenTeams) {
+        const int j = base + team;
+        if (j >= nk) continue;  // uniform over the team's 16 lanes
+        const T *kr, *vr;
+        if (j < pb) {
+            const int lb = j / blk;
+            const int phys = lb < maxb ? bt[(int64_t)b * maxb + lb] : -1;
+            const int64_t slot = phys < 0 ? -1 : (int64_t)phys * blk + j % blk;
+            if (slot < 0 || slot >= nslots) continue;  // outside the cache: no key
+            kr = kcache + slot * kslot + (int64_t)kvh * hd;
+            vr = vcache ? vcache + slot * vslot + (int64_t)kvh * vhd : kr;
+        } else {
+            const int64_t t = s0 + (j - pb);
+            kr = knew + t * kslot + (int64_t)kvh * hd;
+            vr = vcache ? vnew + t * vslot + (int64_t)kvh * vhd : kr;
+        }
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < kGenMaxPerLane; ++e)
+            if (e < E) dot += qv[e] * to_f32(kr[lt + kGenLanes * e]);
+        const float sc = group_sum<kGenLanes>(dot) * scale;
+        const float mn = fmaxf(m, sc);
+        const float corr = __expf(m - mn);  // m = -inf -> 0
+        const float pe = __expf(sc - mn);
+        l = l * corr + pe;
+#pragma unroll
+        for (int e = 0; e < kGenMaxPerLane; ++e)
+            if (e < EV) acc[e] = acc[e] * corr + pe * to_f32(vr[lt + kGenLanes * e]);
+        m = mn;
+    }
+    if (lt == 0) {
+        s_m[team] = m;
+        s_l[team] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < kGenMaxPerLane; ++e)
+        if (e < EV) s_acc[team][lt + kGenLanes * e] = acc[e];
+    __syncthreads();
+    float M = -INFINITY;
+    for (int tm = 0; tm < kGenTeams; ++tm) M = fmaxf(M, s_m[tm]);
+    const float sk = sink ? sink[h] : -INFINITY;
+    M = fmaxf(M, sk);
+    T* orow = out + (int64_t)row * vhd;
+    for (int d = threadIdx.x; d < vhd; d += blockDim.x) {
+        float num = 0.f, den = sink ? __expf(sk - M) : 0.f;
+        for (int tm = 0; tm < kGenTeams; ++tm) {
+            if (s_m[tm] == -INFINITY) continue;
+            const float wt = __expf(s_m[tm] - M);
+            num += wt * s_acc[tm][d];
+            den += wt * s_l[tm];
+        }
+        orow[d] = from_f32<T>(num / den);
+    }
+}
+
+template <typename T>
+static int run_paged_generic(const void* query, const void* key, const void* value,
+                             void* kcache, void* vcache, int64_t nblk, int blk,
+                             const int32_t* cum, const int32_t* past, const int32_t* bt, int batch,
+                             int maxb, int64_t T_, const void* cos_c, const void* sin_c, int half,
+                             int64_t max_pos, int interleaved, int rot_off,
+                             const int32_t* slot_mapping, const void* sink, int sink_dtype,
+                             const void* qw, const void* kw, float eps, void* output, int H,
+                             int KV, int hd, int vhd, float scale, void* ws, hipStream_t st) {
+    // The workspace layout of run_paged (qrot, knew, tile map, split counts, ...):
+    // the prep kernel also builds the tile map, which nothing here reads.
+    const int G = H / KV;
+    const int QT = paged_qt(G);
+    const int mt = paged_max_tiles(T_, batch, QT);
+    char* p = static_cast<char*>(ws);
+    T* qrot = reinterpret_cast<T*>(p);
+    p += align_up((size_t)T_ * H * hd * 4);
+    T* knew = reinterpret_cast<T*>(p);
+    p += align_up((size_t)T_ * KV * hd * 4);
+    int4* tiles = reinterpret_cast<int4*>(p);
+    int* count = reinterpret_cast<int*>(tiles + mt);
+    p += align_up((size_t)(mt + 1) * 16);
+    int* nsplit_row = reinterpret_cast<int*>(p);
+    p += align_up((size_t)T_ * H * 4);
+    int chunk;
+    const int ns = paged_nsplit(1, chunk);
+    p += align_up((size_t)T_ * H * ns * (vhd + 2) * 4);
+    float* sink32 = reinterpret_cast<float*>(p);
+    const float sc = scale != 0.f ? scale : 1.0f / sqrtf((float)hd);
+    if (T_ == 0) return ORTMI_OK;
+    hipLaunchKernelGGL((paged_prep_kernel<T>),
+                       dim3((unsigned)T_, (H + KV + kPrepHeads - 1) / kPrepHeads),
+                       dim3(64 * kPrepHeads), kPrepHeads * hd * sizeof(float), st,
+                       static_cast<const T*>(query), static_cast<const T*>(key),
+                       static_cast<const T*>(value), static_cast<T*>(kcache),
+                       static_cast<T*>(vcache), nblk, blk, cum, past, bt, batch, maxb,
+                       static_cast<const T*>(cos_c), static_cast<const T*>(sin_c), half,
+                       interleaved, rot_off, slot_mapping, static_cast<const T*>(qw),
+                       static_cast<const T*>(kw), eps, H, KV, hd, vhd, qrot, knew, max_pos, QT,
+                       mt, tiles, count, nsplit_row);
+    if (int rc = check_launch("paged_prep")) return rc;
+    if (sink) {
+        hipLaunchKernelGGL(sink_to_f32_kernel, dim3((H + 63) / 64), dim3(64), 0, st, sink,
+                           sink_dtype, sink32, H);
+        if (int rc = check_launch("paged_sink")) return rc;
+    }
+    hipLaunchKernelGGL((paged_generic_attn_kernel<T>), dim3((unsigned)(T_ * H)), dim3(256), 0, st,
+                       qrot, knew, static_cast<const T*>(value), static_cast<const T*>(kcache),
+                       static_cast<const T*>(vcache), nblk * blk, blk, cum, past, bt, batch, maxb,
+                       sink ? sink32 : nullptr, static_cast<T*>(output), H, KV, hd, vhd, sc);
+    return check_launch("paged_generic_attn");
+}
+
 template <typename T, int HD, int VHD>
 static int run_paged(const void* query, const void* key, const void* value, void* kcache,
                      void* vcache, int64_t nblk, int blk, const int32_t* cum, const int32_t* past,
@@ -2479,8 +2640,9 @@ extern "C" int ortmi_paged_attention(
     const bool latent = value_cache == nullptr;
     ORTMI_REQUIRE(latent == (value == nullptr),
                   "PagedAttention: value and value_cache must both be given (or both absent for LATENT)");
-    ORTMI_REQUIRE(head_size == 64 || head_size == 128, "PagedAttention: head_size must be 64 or 128");
-    ORTMI_REQUIRE(vhd == head_size || (latent && (vhd == 64 || vhd == 128) && vhd <= head_size),
+    ORTMI_REQUIRE(head_size > 0 && head_size % 16 == 0 && head_size <= 256,
+                  "PagedAttention: head_size must be a multiple of 16 up to 256");
+    ORTMI_REQUIRE(vhd == head_size || (latent && vhd % 16 == 0 && vhd <= head_size),
                   "PagedAttention: unsupported v_head_size");
     ORTMI_REQUIRE(batch > 0 && block_size > 0 && num_blocks > 0 && max_blocks > 0,
                   "PagedAttention: bad cache or batch shape");
@@ -2509,6 +2671,29 @@ extern "C" int ortmi_paged_attention(
                                  q_norm_weight, k_norm_weight, qk_norm_eps, output,              \
                                  (int)num_heads, (int)kv_num_heads, scale, workspace,            \
                                  workspace_bytes, st)
+    // fp32 and the head sizes the tile/decode kernels do not take run the generic kernels.
+    const bool fused = dtype != ORTMI_F32 && (head_size == 64 || head_size == 128) &&
+                       (vhd == head_size || vhd == 64) && rotary_offset % 8 == 0;
+    if (!fused) {
+        const size_t need = ortmi_paged_attention_workspace_size(
+            num_tokens, batch, num_heads, kv_num_heads, head_size, v_head_size, max_context);
+        if (!workspace || workspace_bytes < need)
+            return fail(ORTMI_E_WORKSPACE, "PagedAttention: workspace too small");
+#define ORTMI_PAG(T)                                                                              \
+    return run_paged_generic<T>(query, key, value, key_cache, value_cache, num_blocks,            \
+                                (int)block_size, cum_seqlens, past_seqlens, block_table,          \
+                                (int)batch, (int)max_blocks, num_tokens, cos_cache, sin_cache,    \
+                                (int)rotary_half, rotary_max_pos, rotary_interleaved,             \
+                                (int)rotary_offset, slot_mapping, head_sink, dtype,               \
+                                q_norm_weight, k_norm_weight, qk_norm_eps, output,                \
+                                (int)num_heads, (int)kv_num_heads, (int)head_size, (int)vhd,      \
+                                scale, workspace, st)
+        if (dtype == ORTMI_F32) ORTMI_PAG(float);
+        if (dtype == ORTMI_F16) ORTMI_PAG(half_t);
+        if (dtype == ORTMI_BF16) ORTMI_PAG(uint16_t);
+#undef ORTMI_PAG
+        return fail(ORTMI_E_INVALID, "PagedAttention: dtype must be fp32, fp16 or bf16");
+    }
     if (dtype == ORTMI_F16) {
         if (head_size == 64) ORTMI_PA(half_t, 64, 64);
         if (vhd == 64) ORTMI_PA(half_t, 128, 64);
@@ -2520,7 +2705,7 @@ extern "C" int ortmi_paged_attention(
         ORTMI_PA(uint16_t, 128, 128);
     }
 #undef ORTMI_PA
-    return fail(ORTMI_E_INVALID, "PagedAttention: dtype must be fp16 or bf16");
+    return fail(ORTMI_E_INVALID, "PagedAttention: dtype must be fp32, fp16 or bf16");
 }
 
 // ------------------------------------------------------- RotaryEmbedding --

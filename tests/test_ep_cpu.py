@@ -573,3 +573,32 @@ def test_layer_partitions_inference_needs_a_residual_add_in_every_layer(monkeypa
         assert sizes == [16, 16, 16]
     else:
         assert sizes == [48]
+
+
+@pytest.mark.parametrize("dtype,d,attrs,claimed", [
+    (F16, 128, {}, True),
+    (F32, 128, {}, True),                                  # fp32: the generic kernels
+    (F16, 96, {}, True),                                   # head sizes 16k <= 256
+    (F16, 72, {}, False),
+    (F16, 512, {}, False),
+    (F16, 128, dict(local_window_size=64), False),         # declined by the reference too
+    (F16, 128, dict(softcap=30.0), False),
+])
+def test_paged_attention_claim_forms(dtype, d, attrs, claimed):
+    """PagedAttention claim (rust/src/ops/attention.rs:2746-2977): any float dtype and
+    the head sizes the kernels take."""
+    g = hx.Graph()
+    H, KV, nb, blk, batch, maxb = 4, 2, 8, 4, 2, 4
+    g.value("q", dtype, [-1, H * d])
+    g.value("k", dtype, [-1, KV * d])
+    g.value("v", dtype, [-1, KV * d])
+    g.value("kc", dtype, [nb, blk, KV, d])
+    g.value("vc", dtype, [nb, blk, KV, d])
+    g.value("cum", I32, [batch + 1])
+    g.value("past", I32, [batch])
+    g.value("bt", I32, [batch, maxb])
+    g.value("o", dtype, [-1, H * d])
+    g.node("PagedAttention", ["q", "k", "v", "kc", "vc", "cum", "past", "bt"], ["o"],
+           domain="com.microsoft", num_heads=H, kv_num_heads=KV, **attrs)
+    g.io(["q", "k", "v", "kc", "vc", "cum", "past", "bt"], ["o"])
+    assert session(g).claimed(0) is claimed

@@ -1094,3 +1094,99 @@ def test_glue_kernels(ortmi):
     ortmi.check(lib.ortmi_gather_rows(ctypes.c_void_p(dt_.data_ptr()), ctypes.c_void_p(di.data_ptr()),
                                       ctypes.c_void_p(o.data_ptr()), 3, 100, 64, 10, st))
     np.testing.assert_array_equal(host(o), table[[3, 99, 50]].astype(np.float32))
+
+
+# ------------------------------------------------------ PagedAttention, generic ---
+
+
+def _run_paged_generic(ortmi, oracle, dt, H, KV, d, nb, blk, batch, seed, rope=False,
+                       interleaved=0, new_max=4, latent=False, v_head_size=0, rotary_offset=0,
+                       head_sink=False, qk_norm=False):
+    """The forms the generic kernels serve (fp32, head sizes other than 64/128, LATENT
+    value sizes other than 64/128, odd rotary offsets) against the oracle on the same
+    rounded inputs. Tolerances: fp32 1e-5 + 1e-5 |exact|, fp16 1e-3 + 2 ULP, bf16
+    4e-3 + 2^-6 |exact|; V slots exact, K slots within one rounding of the oracle."""
+    import torch
+
+    tdt = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[dt]
+
+    def cast(a):
+        t = torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(tdt)
+        return t.cuda(), t.float().numpy()
+
+    rng = np.random.default_rng(seed)
+    maxb = nb // batch
+    cap = maxb * blk
+    new_lens = rng.integers(1, min(new_max, cap) + 1, size=batch).astype(np.int32)
+    past = np.array([rng.integers(0, cap - nl + 1) for nl in new_lens], np.int32)
+    cum = np.concatenate([[0], np.cumsum(new_lens)]).astype(np.int32)
+    nt = int(cum[-1])
+    vd = v_head_size or d
+    q, nq = cast(rng.standard_normal((nt, H * d)) * 0.3)
+    k, nk = cast(rng.standard_normal((nt, KV * d)) * 0.3)
+    v, nv = cast(rng.standard_normal((nt, KV * d)) * 0.3)
+    kc, nkc = cast(rng.standard_normal((nb, blk, KV, d)) * 0.3)
+    vc, nvc = cast(rng.standard_normal((nb, blk, KV, d)) * 0.3)
+    bt = rng.permutation(nb).astype(np.int32).reshape(batch, maxb)
+    cos = sin = ncos = nsin = None
+    if rope:
+        c, s_ = refs.rotary_caches(cap, d // 2 if rotary_offset else d)
+        cos, ncos = cast(c)
+        sin, nsin = cast(s_)
+    if latent:
+        v = vc = nv = nvc = None
+    sink = nsink = qw = nqw = kw = nkw = None
+    if head_sink:
+        sink, nsink = cast(rng.uniform(-1, 1, H))
+    if qk_norm:
+        qw, nqw = cast(np.linspace(0.75, 1.25, d))
+        kw, nkw = cast(np.linspace(1.25, 0.75, d))
+    out = ortmi.paged_attention(
+        q, k, v, kc, vc, dev(cum), dev(past), dev(bt), cos, sin, None, sink, qw, kw,
+        num_heads=H, kv_num_heads=KV, do_rotary=int(rope), rotary_interleaved=interleaved,
+        qk_norm_epsilon=1e-5, kv_cache_layout="LATENT" if latent else "SEPARATE",
+        v_head_size=v_head_size, rotary_offset=rotary_offset)
+    torch.cuda.synchronize()
+    r16 = {"f32": 0, "f16": 1, "bf16": 2}[dt]
+    ro, rkc, rvc = oracle.paged_attention(nq, nk, nv, nkc, nvc, cum, past, bt, H, KV, cos=ncos,
+                                          sin=nsin, interleaved=interleaved,
+                                          rotary_offset=rotary_offset, head_sink=nsink,
+                                          q_norm=nqw, k_norm=nkw, qk_eps=1e-5,
+                                          v_head_size=v_head_size, round16=r16)
+    got = out.float().cpu().numpy()
+    assert got.shape == (nt, H * vd) and out.dtype == tdt
+    if dt == "f32":
+        tol = 1e-5 + 1e-5 * np.abs(ro)
+    elif dt == "f16":
+        tol = 1e-3 + 2 * ulp16(ro)
+    else:
+        tol = 4e-3 + 2.0 ** -6 * np.abs(ro)
+    bad = ~(np.abs(got - ro) <= tol)
+    assert not bad.any(), (f"{dt} paged output: {bad.sum()} of {bad.size} beyond tolerance, "
+                           f"max diff {np.nanmax(np.abs(got - ro)):.3e}")
+    if not latent:
+        np.testing.assert_array_equal(vc.float().cpu().numpy(), rvc)
+    gk = kc.float().cpu().numpy()
+    mant = {"f32": 23, "f16": 10, "bf16": 7}[dt]
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(rkc), 2.0 ** -24))) - mant)
+    assert (np.abs(gk - rkc) <= (2 if qk_norm else 1) * ulp + (1e-6 if dt == "f32" else 0)).all()
+
+
+@pytest.mark.parametrize("rope,interleaved", [(False, 0), (True, 0), (True, 1)])
+def test_paged_generic_fp32(ortmi, oracle, rope, interleaved):
+    _run_paged_generic(ortmi, oracle, "f32", 8, 2, 128, nb=24, blk=4, batch=3, seed=500 + rope,
+                       rope=rope, interleaved=interleaved, new_max=6)
+
+
+@pytest.mark.parametrize("dt,d", [("f16", 96), ("bf16", 256), ("f16", 32)])
+def test_paged_generic_head_sizes(ortmi, oracle, dt, d):
+    _run_paged_generic(ortmi, oracle, dt, 4, 2, d, nb=16, blk=4, batch=2, seed=510 + d,
+                       rope=True, new_max=5, head_sink=True, qk_norm=True)
+
+
+def test_paged_generic_latent_and_offset(ortmi, oracle):
+    """LATENT with v_head_size 96 of head 128, and a rotary_offset of 4 (fp16)."""
+    _run_paged_generic(ortmi, oracle, "f16", 8, 1, 128, nb=24, blk=4, batch=3, seed=520,
+                       rope=True, new_max=6, latent=True, v_head_size=96)
+    _run_paged_generic(ortmi, oracle, "f16", 4, 2, 64, nb=16, blk=4, batch=2, seed=521,
+                       rope=True, interleaved=1, new_max=5, rotary_offset=4)
