@@ -136,6 +136,13 @@ typedef enum OrtDeviceMemoryType {
     OrtDeviceMemoryType_HOST_ACCESSIBLE = 5,
 } OrtDeviceMemoryType;
 
+typedef enum OrtMemoryInfoDeviceType {
+    OrtMemoryInfoDeviceType_CPU = 0,
+    OrtMemoryInfoDeviceType_GPU = 1,
+    OrtMemoryInfoDeviceType_FPGA = 2,
+    OrtMemoryInfoDeviceType_NPU = 3,
+} OrtMemoryInfoDeviceType;
+
 /* ----------------------------------------------------------- plain structs */
 typedef struct OrtApiBase {
     const OrtApi* (*GetApi)(uint32_t version);
@@ -285,6 +292,10 @@ typedef struct OrtEpFactory {
     X(285, GetEpApi, const OrtEpApi*, (void))                                                    \
     X(286, HardwareDevice_Type, OrtHardwareDeviceType, (const OrtHardwareDevice* device))        \
     X(301, GetTensorData, OrtStatus*, (const OrtValue* value, const void** out))                 \
+    X(317, CreateMemoryInfo_V2, OrtStatus*,                                                      \
+      (const char* name, OrtMemoryInfoDeviceType device_type, uint32_t vendor_id,                \
+       int32_t device_id, OrtDeviceMemoryType mem_type, size_t alignment,                        \
+       OrtAllocatorType allocator_type, OrtMemoryInfo** out))                                   \
     X(310, GetValueInfoName, OrtStatus*, (const OrtValueInfo* value_info, const char** name))    \
     X(311, GetValueInfoTypeInfo, OrtStatus*,                                                     \
       (const OrtValueInfo* value_info, const OrtTypeInfo** type_info))                           \
@@ -341,7 +352,13 @@ typedef struct OrtEpFactory {
        const OrtNodeFusionOptions* options))                                                     \
     X(3, EpGraphSupportInfo_AddSingleNode, OrtStatus*,                                           \
       (OrtEpGraphSupportInfo * info, const OrtNode* node))                                       \
-    X(4, NodeComputeContext_NodeName, const char*, (const OrtNodeComputeContext* context))
+    X(4, NodeComputeContext_NodeName, const char*, (const OrtNodeComputeContext* context))       \
+    X(5, EpDevice_AddAllocatorInfo, OrtStatus*,                                                  \
+      (OrtEpDevice * ep_device, const OrtMemoryInfo* allocator_memory_info))                     \
+    X(6, MemoryInfo_GetMemoryDevice, const OrtMemoryDevice*, (const OrtMemoryInfo* memory_info)) \
+    X(9, MemoryDevice_GetDeviceType, OrtMemoryInfoDeviceType, (const OrtMemoryDevice* device))   \
+    X(11, MemoryDevice_GetVendorId, uint32_t, (const OrtMemoryDevice* device))                   \
+    X(12, MemoryDevice_GetDeviceId, uint32_t, (const OrtMemoryDevice* device))
 
 /* Upper bounds of the slot numbers above (sizes of a table that holds them). */
 #define ORTMI_ORT_API_TABLE_SIZE 400

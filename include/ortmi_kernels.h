@@ -146,13 +146,22 @@ int ortmi_matmul_nbits_decode_merge(const float* partials, int64_t splits, int64
  * step needs no host round trip; logits [vocab] fp16 and next_id (int64, the
  * first index of the largest logit, NaN never wins) are written. `status`
  * (optional; device or host-pinned memory) receives 0 on success, 1 if a wait
- * between the step's workgroups passed its 100 ms deadline (the results are then
+ * between the step's workgroups saw no data for 100 ms (the results are then
  * invalid), 2 if the token id was out of range (row 0 was used), 3 if
  * total_sequence_length is outside [1, kv_capacity] or past the rotary table
- * (nothing computed). The workspace (ortmi_decoder_decode_step_workspace_size
- * bytes, 256-byte aligned) must be zero-filled before its first use and then
- * passed unchanged to every step; steps sharing a workspace must run in order on
- * one stream. embed, the gammas and the cos/sin caches must be 16-byte aligned.
+ * (nothing computed); it is left unwritten by a launch the host aborted before
+ * it started (below), so a caller that sets it to -1 before each step sees every
+ * step that did not complete. The workspace
+ * (ortmi_decoder_decode_step_workspace_size bytes, 256-byte aligned) must be
+ * zero-filled before its first use and then passed unchanged to every step;
+ * steps sharing a workspace must run in order on one stream. Its first 8 bytes
+ * count started workgroups (a 64-bit integer; launch index = count / grid, the
+ * grid being the device's CU count rounded down to a multiple of 8), and the
+ * 32-bit word at byte 128 aborts the launch whose index + 1 it holds: that
+ * launch reads and writes nothing. A step that is not completed leaves the KV
+ * row at total - 1 possibly written; running the step again (by this call or op
+ * by op) rewrites it with the same values. embed, the gammas and the cos/sin
+ * caches must be 16-byte aligned.
  * Replaces: the compiled decode path of the reference EP, a shapeless
  * mlx_compile trace of the decode graph evaluated once per token
  * (rust/src/compiled.rs:503-822, rust/src/engine.rs:417, 1720-1736), over the
@@ -364,10 +373,13 @@ int ortmi_group_query_attention_decode_partials(
  * past_seqlens [batch], block_table [batch, max_blocks] and slot_mapping [T]
  * (optional, slot < 0 skips the write) are int32 device tensors: nothing is read
  * back to the host. max_context is a host upper bound on past + new tokens of
- * every sequence (max_blocks * block_size always is one); keys beyond it are not
- * attended. dtype fp32, fp16 or bf16; head_size a multiple of 16 up to 256
- * (fp16/bf16 with head 64/128 run the matrix-core tiles and the decode kernel,
- * every other form one VALU workgroup per (token, head) row). cos/sin caches are
+ * every sequence (max_blocks * block_size always is one); keys at positions
+ * max_context and beyond are not attended, and past_seqlens is read clamped to
+ * [0, max_context]. dtype fp32, fp16 or bf16; head_size a multiple of 16 up to
+ * 256 (fp16/bf16 with head 64/128 run the multi-token tiles and the single-token
+ * decode kernel, the tiles on the matrix cores for fp16 and on the vector units
+ * for bf16; every other form one VALU workgroup per (token, head) row). A token's
+ * sequence range is cum_seqlens clamped to [0, num_tokens). cos/sin caches are
  * [rotary_max_pos, rotary_half]. head_sink [H],
  * q_norm_weight/k_norm_weight [hd] optional. output [T,H*vhd]. Malformed control
  * tensors (block ids or positions out of range) never cause out-of-bounds

@@ -693,6 +693,7 @@ struct PagedKV {
     int64_t nblk;
     int blk, maxb, KV;
     int blk_shift;  // log2(blk) when blk is a power of two, else -1
+    int max_ctx;    // keys at positions >= max_ctx are not attended
 };
 
 struct TileDesc {
@@ -1359,9 +1360,11 @@ __global__ __launch_bounds__((tile_threads<T, HD, kGqaTileWaves>()),
 
 // Tile map built on the device by one 64-lane wave (no host read of the control
 // tensors): ceil(n_b / QT) tiles of QT tokens for each sequence b, in sequence
-// order, tiles[i] = {seq, first token, ntok}, and the count. Token ranges are
-// clamped to [0, T), so a malformed cum_seqlens yields fewer tiles, never a tile
-// outside the batch; at most max_tiles are written.
+// order, tiles[i] = {seq, first token, ntok, first token of the sequence}, and
+// the count. Token ranges are clamped to [0, T), so a malformed cum_seqlens
+// yields fewer tiles, never a tile outside the batch, and the attention kernels
+// take the sequence start from the tile (clamped) rather than from cum_seqlens:
+// a new key row is then always a token of [0, T). At most max_tiles are written.
 __device__ void build_tile_map(const int32_t* __restrict__ cum, int batch, int T, int QT,
                                int max_tiles, int4* __restrict__ tiles, int* __restrict__ count) {
     const int lane = threadIdx.x;
@@ -1383,7 +1386,7 @@ __device__ void build_tile_map(const int32_t* __restrict__ cum, int batch, int T
         const int first = base + incl - nt;
         for (int i = 0; i < nt && first + i < max_tiles; ++i) {
             const int t = s0 + i * QT;
-            tiles[first + i] = make_int4(b, t, min(QT, s1 - t), 0);
+            tiles[first + i] = make_int4(b, t, min(QT, s1 - t), s0);
         }
         base += __shfl(incl, 63, 64);
     }
@@ -1443,7 +1446,12 @@ __global__ __launch_bounds__(64 * kPrepHeads) void paged_prep_kernel(
         pb = past[b];
         row_to_lds<T>(sv, src, hd, lane);
     }
-    const int pos = pb + (tok - cb);
+    // The sequence start clamped to [0, T), as the tile map and the attention
+    // kernels take it, so positions agree across the kernels of one call.
+    // past is clamped below at 0 as there, and the position is formed in 64 bits
+    // (a past near 2^31 then gives a position past the block table, not a wrap).
+    cb = min(max(cb, 0), (int)gridDim.x);
+    const int pos = (int)min((int64_t)max(pb, 0) + (tok - cb), (int64_t)INT32_MAX);
     const T* nw = is_q ? qw : kw;
     if (nw) rms_head_lds<T>(sv, hd, nw, eps);
     if (cos_c) {
@@ -1507,11 +1515,14 @@ __global__ __launch_bounds__((tile_threads<T, VHD, kPagedTileWaves>()),
     t.seq = td.x;
     t.tok0 = td.y;
     t.ntok = td.z;
-    t.tok_seq0 = cum[t.seq];
-    t.past = past_lens[t.seq];
+    // Sequence start from the tile map (clamped to the batch); past clamped to
+    // [0, max_ctx], so every new key row is a token of the tile's sequence range
+    // and the walk is bounded whatever past_seqlens holds.
+    t.tok_seq0 = td.w;
+    t.past = min(max(past_lens[t.seq], 0), pk.max_ctx);
     t.qpos0 = t.past + (t.tok0 - t.tok_seq0);
-    t.nkeys = t.past + (cum[t.seq + 1] - t.tok_seq0);
-    const int kend = min(t.nkeys, t.qpos0 + t.ntok);
+    t.nkeys = t.qpos0 + t.ntok;
+    const int kend = min(t.nkeys, pk.max_ctx);  // causal bound of the tile
     DenseKV none{};
     const int ns = min(nsplit, max(1, (kend + chunk - 1) / chunk));
     if (split == 0) {
@@ -1562,9 +1573,10 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
     const int4 td = tiles[ti];
     if (td.z != 1) return;
     const int seq = td.x, tok = td.y;
-    const int tok_seq0 = cum[seq];
-    const int past = past_lens[seq];
-    const int kend = past + (tok - tok_seq0) + 1;  // causal: keys up to the token itself
+    const int tok_seq0 = td.w;  // clamped sequence start (tile map)
+    const int past = min(max(past_lens[seq], 0), pk.max_ctx);
+    // causal: keys up to the token itself, none at positions >= max_ctx
+    const int kend = min(past + (tok - tok_seq0) + 1, pk.max_ctx);
     const int ns = min(nsplit, max(1, (kend + chunk - 1) / chunk));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = lane / LPR;
@@ -2389,7 +2401,7 @@ __global__ __launch_bounds__(256) void paged_generic_attn_kernel(
     const T* __restrict__ kcache, const T* __restrict__ vcache, int64_t nslots, int blk,
     const int32_t* __restrict__ cum, const int32_t* __restrict__ past,
     const int32_t* __restrict__ bt, int batch, int maxb, const float* __restrict__ sink,
-    T* __restrict__ out, int H, int KV, int hd, int vhd, float scale) {
+    T* __restrict__ out, int H, int KV, int hd, int vhd, float scale, int max_ctx) {
     __shared__ float s_m[kGenTeams], s_l[kGenTeams];
     __shared__ float s_acc[kGenTeams][kGenLanes * kGenMaxPerLane];
     const int row = blockIdx.x;  // tok * H + h
@@ -2403,8 +2415,20 @@ __global__ __launch_bounds__(256) void paged_generic_attn_kernel(
         if (cum[mid] <= tok) lo = mid;
         else hi = mid;
     }
-    const int b = lo, s0 = cum[b], pb = max(past[b], 0);
-    const int nk = pb + (tok - s0) + 1;  // causal: keys [0, past + i]
+    // The sequence's token range clamped to [0, T), as the tile map clamps it, and
+    // past to [0, max_ctx]: new key rows stay tokens of [0, T) and the walk stays
+    // bounded whatever the control tensors hold. A token outside its sequence's
+    // clamped range (a malformed cum_seqlens) belongs to no sequence: zero row.
+    const int T_ = (int)(gridDim.x / H);
+    const int b = lo;
+    const int s0 = min(max(cum[b], 0), T_), s1 = min(max(cum[b + 1], s0), T_);
+    const int pb = min(max(past[b], 0), max_ctx);
+    T* orow = out + (int64_t)row * vhd;
+    if (tok < s0 || tok >= s1) {
+        for (int d = threadIdx.x; d < vhd; d += blockDim.x) orow[d] = from_f32<T>(0.f);
+        return;
+    }
+    const int nk = min(pb + (tok - s0) + 1, max_ctx);  // causal: keys [0, past + i]
     // LATENT (vcache == nullptr): values are the first vhd dims of the key rows.
     const int64_t kslot = (int64_t)KV * hd, vslot = (int64_t)KV * vhd;
     const T* qrow = qrot + (int64_t)row * hd;
@@ -2457,7 +2481,6 @@ __global__ __launch_bounds__(256) void paged_generic_attn_kernel(
     for (int tm = 0; tm < kGenTeams; ++tm) M = fmaxf(M, s_m[tm]);
     const float sk = sink ? sink[h] : -INFINITY;
     M = fmaxf(M, sk);
-    T* orow = out + (int64_t)row * vhd;
     for (int d = threadIdx.x; d < vhd; d += blockDim.x) {
         float num = 0.f, den = sink ? __expf(sk - M) : 0.f;
         for (int tm = 0; tm < kGenTeams; ++tm) {
@@ -2478,7 +2501,8 @@ static int run_paged_generic(const void* query, const void* key, const void* val
                              int64_t max_pos, int interleaved, int rot_off,
                              const int32_t* slot_mapping, const void* sink, int sink_dtype,
                              const void* qw, const void* kw, float eps, void* output, int H,
-                             int KV, int hd, int vhd, float scale, void* ws, hipStream_t st) {
+                             int KV, int hd, int vhd, float scale, int64_t max_context, void* ws,
+                             hipStream_t st) {
     // The workspace layout of run_paged (qrot, knew, tile map, split counts, ...):
     // the prep kernel also builds the tile map, which nothing here reads.
     const int G = H / KV;
@@ -2519,7 +2543,8 @@ static int run_paged_generic(const void* query, const void* key, const void* val
     hipLaunchKernelGGL((paged_generic_attn_kernel<T>), dim3((unsigned)(T_ * H)), dim3(256), 0, st,
                        qrot, knew, static_cast<const T*>(value), static_cast<const T*>(kcache),
                        static_cast<const T*>(vcache), nblk * blk, blk, cum, past, bt, batch, maxb,
-                       sink ? sink32 : nullptr, static_cast<T*>(output), H, KV, hd, vhd, sc);
+                       sink ? sink32 : nullptr, static_cast<T*>(output), H, KV, hd, vhd, sc,
+                       (int)std::min<int64_t>(max_context, INT32_MAX));
     return check_launch("paged_generic_attn");
 }
 
@@ -2579,7 +2604,8 @@ static int run_paged(const void* query, const void* key, const void* value, void
     int blk_shift = 0;
     while ((1 << blk_shift) < blk && blk_shift < 30) ++blk_shift;
     const bool pow2 = (1 << blk_shift) == blk && blk_shift <= 12;
-    PagedKV pk{kcache, vcache, knew, value, bt, nblk, blk, maxb, KV, pow2 ? blk_shift : -1};
+    PagedKV pk{kcache, vcache, knew, value, bt, nblk, blk, maxb, KV, pow2 ? blk_shift : -1,
+               (int)std::min<int64_t>(max_context, INT32_MAX)};
     if (!vcache) pk.vnew = nullptr;
     // Single-token tiles go to the vector-unit decode kernel when the block size is a
     // power of two and values have the key's head size. It writes rows no
@@ -2687,7 +2713,7 @@ extern "C" int ortmi_paged_attention(
                                 (int)rotary_offset, slot_mapping, head_sink, dtype,               \
                                 q_norm_weight, k_norm_weight, qk_norm_eps, output,                \
                                 (int)num_heads, (int)kv_num_heads, (int)head_size, (int)vhd,      \
-                                scale, workspace, st)
+                                scale, max_context, workspace, st)
         if (dtype == ORTMI_F32) ORTMI_PAG(float);
         if (dtype == ORTMI_F16) ORTMI_PAG(half_t);
         if (dtype == ORTMI_BF16) ORTMI_PAG(uint16_t);

@@ -31,13 +31,14 @@
 // the previous launch's tag.
 //
 // Grid: one 512-thread workgroup per CU (co-resident by the cooperative launch),
-// 8 waves, all computing. Attention runs on the last H workgroups, one query
-// head each over all keys (no split merge); they skip o_proj, which the other
-// workgroups run. Every wait is bounded (100 ms of the 100 MHz realtime clock from
-// the workgroup's start): a workgroup past the deadline writes its launch tag to
-// the abort word and status 1, and every other waiting thread leaves when it sees
-// its own tag there. No thread waits on anything its own workgroup produces later,
-// so the waits form a chain along the layer order and always end.
+// 8 waves, all computing. Attention runs on the last H * NS workgroups, one
+// (query head, key split) each; the projections run on the others. Every wait is
+// bounded: a wait that sees no new data for 100 ms of the 100 MHz realtime clock
+// writes its launch index to the abort word and status 1, and every other waiting
+// thread leaves when it sees its own launch index there. A workgroup that finds
+// its launch index in the abort word at entry leaves at once (the host can abort
+// a launch before it starts). No thread waits on anything its own workgroup
+// produces later, so the waits form a chain along the layer order and always end.
 //
 // Rounding follows the unfused ops of the fp16 graph: residual sums and
 // normalised activations, MatMulNBits outputs, the RoPE'd query/key and the
@@ -66,8 +67,8 @@ constexpr int kPartWords = 130;        // a split's partial: o[128], running max
 constexpr unsigned long long kDeadlineTicks = 10000000ull;  // 100 ms
 
 // Control block (uint32 words, one 128-byte line each).
-constexpr int kCtlStart = 0;   // workgroups started, summed over launches
-constexpr int kCtlAbort = 32;  // tag of a launch that gave up
+constexpr int kCtlStart = 0;   // workgroups started, summed over launches (64-bit)
+constexpr int kCtlAbort = 32;  // launch index + 1 of a launch that gave up
 constexpr size_t kCtlBytes = 256;
 
 struct Params {
@@ -113,7 +114,8 @@ __device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL);
     return make_uint4(v.x, v.y, v.z, v.w);
 }
-__device__ __forceinline__ unsigned atomic_add_dev(uint32_t* p, unsigned v) {
+__device__ __forceinline__ unsigned long long atomic_add_dev64(unsigned long long* p,
+                                                               unsigned long long v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ unsigned load_dev(const uint32_t* p) {
@@ -139,16 +141,20 @@ __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F);
 struct Flow {
     uint32_t* ctl;
     int32_t* status;
-    uint32_t tag;                 // 1..65535
-    unsigned long long deadline;  // realtime clock
+    uint32_t tag;     // 1..65535, in the high half of every data word
+    uint32_t launch;  // launch index + 1 (32 bits), what the abort word holds
 };
 
 // One round of a bounded wait: false when this launch stops (another workgroup
-// gave up, or the deadline passed and this one gives up).
-__device__ __forceinline__ bool keep_waiting(const Flow& f, unsigned it) {
-    if ((it & 7) == 7 && load_dev(f.ctl + kCtlAbort) == f.tag) return false;
-    if (__builtin_amdgcn_s_memrealtime() > f.deadline) {
-        store_dev(f.ctl + kCtlAbort, f.tag);
+// gave up, or this wait saw no data for 100 ms and gives up). `t0` is the wait's
+// start on the realtime clock, taken at its first round, so the bound is per wait
+// and a long step that keeps making progress is never cut short.
+__device__ __forceinline__ bool keep_waiting(const Flow& f, unsigned it, unsigned long long& t0) {
+    const unsigned long long now = __builtin_amdgcn_s_memrealtime();
+    if (it == 0) t0 = now;
+    if ((it & 7) == 7 && load_dev(f.ctl + kCtlAbort) == f.launch) return false;
+    if (now - t0 > kDeadlineTicks) {
+        store_dev(f.ctl + kCtlAbort, f.launch);
         store_status(f.status, 1);
         return false;
     }
@@ -182,6 +188,7 @@ __device__ __forceinline__ bool poll_units(__amdgpu_buffer_rsrc_t r, const uint3
         lo[k] = ld128<kSC1>(r, off[k]);
         hi[k] = ld128<kSC1>(r, off[k] + 16u);
     }
+    unsigned long long t0 = 0;
     for (unsigned it = 0;; ++it) {
 #pragma unroll
         for (int k = 0; k < N; ++k)
@@ -190,7 +197,7 @@ __device__ __forceinline__ bool poll_units(__amdgpu_buffer_rsrc_t r, const uint3
                 pend &= ~(1u << k);
             }
         if (!pend) return true;
-        if (!keep_waiting(f, it)) return false;
+        if (!keep_waiting(f, it, t0)) return false;
 #pragma unroll
         for (int k = 0; k < N; ++k)
             if ((pend >> k) & 1u) {
@@ -503,7 +510,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
     __shared__ OrtmiDecoderLayer s_layers[kMaxLayers];
     __shared__ float sRed[kWaves];
     __shared__ int s_fail;
-    __shared__ uint32_t s_tag;
+    __shared__ uint32_t s_tag, s_launch;
+    __shared__ int s_aborted;
     __shared__ float s_am[kWaves], s_al[kWaves];
     __shared__ float s_arg_v[kWaves];
     __shared__ int s_arg_i[kWaves];
@@ -551,8 +559,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         return;
     }
     if (tid == 0) {
-        const unsigned started = atomic_add_dev(p.ctl + kCtlStart, 1u);
-        s_tag = (started / (unsigned)nwg) % 65535u + 1u;
+        // A 64-bit count: the launch index stays the same for every workgroup of a
+        // launch (a 32-bit count would wrap inside a launch unless nwg divides 2^32).
+        const unsigned long long started =
+            atomic_add_dev64(reinterpret_cast<unsigned long long*>(p.ctl + kCtlStart), 1ull);
+        const unsigned long long li = started / (unsigned long long)nwg;
+        s_tag = (uint32_t)(li % 65535ull) + 1u;
+        s_launch = (uint32_t)li + 1u;
+        s_aborted = load_dev(p.ctl + kCtlAbort) == s_launch;
     }
     const int ctx = total - 1;  // cached keys; the new key sits at index ctx
     if (attn_wg && tid < p.half) {
@@ -560,7 +574,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         s_sin[tid] = (float)p.sin[(size_t)ctx * p.half + tid];
     }
     __syncthreads();
-    const Flow f{p.ctl, p.status, s_tag, __builtin_amdgcn_s_memrealtime() + kDeadlineTicks};
+    if (s_aborted) return;  // aborted before it started: nothing is read or written
+    const Flow f{p.ctl, p.status, s_tag, s_launch};
     const uint32_t tag = f.tag;
 
     int64_t id = *p.input_id;  // negative ids count from the end
@@ -815,6 +830,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                         pend |= 1u;
                     }
                 }
+                unsigned long long t0 = 0;
                 for (unsigned it = 0; pend; ++it) {
 #pragma unroll
                     for (int j = 1; j < kNSMax; ++j)
@@ -825,7 +841,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                         pend &= ~1u;
                     }
                     if (!pend) break;
-                    if (!keep_waiting(f, it)) {
+                    if (!keep_waiting(f, it, t0)) {
                         mok = false;
                         break;
                     }
@@ -1084,10 +1100,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         const int w = w0 + tid;
         if (w >= nwg) continue;
         uint64_t rec = 0;
+        unsigned long long t0 = 0;
         for (unsigned it = 0;; ++it) {
             rec = __hip_atomic_load(p.argp + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if ((uint32_t)(rec >> 48) == tag) break;
-            if (!keep_waiting(f, it)) {
+            if (!keep_waiting(f, it, t0)) {
                 ok = false;
                 break;
             }

@@ -99,16 +99,36 @@ void* alloc_on_stream_fn(OrtAllocator* self, size_t size, OrtSyncStreamImpl*) {
 struct DataTransfer {
     OrtDataTransferImpl base;
     const OrtApi* api;
+    const OrtEpApi* ep_api;
+    hipStream_t stream = nullptr;  // copies of one CopyTensors call, then one synchronisation
 };
 
-void dt_release(OrtDataTransferImpl* self) { delete reinterpret_cast<DataTransfer*>(self); }
-bool dt_can_copy(const OrtDataTransferImpl*, const OrtMemoryDevice*, const OrtMemoryDevice*) {
-    return true;  // unified addressing: hipMemcpyDefault handles every direction
+void dt_release(OrtDataTransferImpl* self) {
+    auto* t = reinterpret_cast<DataTransfer*>(self);
+    if (t->stream) (void)hipStreamDestroy(t->stream);
+    delete t;
+}
+// Host memory, or memory of an AMD GPU: hipMemcpyDefault copies between any two
+// of them (unified addressing). A null memory device is host memory.
+bool dt_side_ok(const DataTransfer* t, const OrtMemoryDevice* d) {
+    if (!d) return true;
+    const OrtMemoryInfoDeviceType ty = ep_api::MemoryDevice_GetDeviceType(t->ep_api)(d);
+    if (ty == OrtMemoryInfoDeviceType_CPU) return true;
+    return ty == OrtMemoryInfoDeviceType_GPU &&
+           ep_api::MemoryDevice_GetVendorId(t->ep_api)(d) == kVendorIdAmd;
+}
+bool dt_can_copy(const OrtDataTransferImpl* self, const OrtMemoryDevice* src,
+                 const OrtMemoryDevice* dst) {
+    const auto* t = reinterpret_cast<const DataTransfer*>(self);
+    return dt_side_ok(t, src) && dt_side_ok(t, dst);
 }
 OrtStatus* dt_copy(OrtDataTransferImpl* self, const OrtValue** src, OrtValue** dst,
                    OrtSyncStreamImpl**, size_t n) {
-    const OrtApi* a = reinterpret_cast<DataTransfer*>(self)->api;
+    auto* t = reinterpret_cast<DataTransfer*>(self);
+    const OrtApi* a = t->api;
     return guard(a, "CopyTensors", [&] {
+        if (!t->stream)
+            check_hip(hipStreamCreateWithFlags(&t->stream, hipStreamNonBlocking), "hipStreamCreate");
         for (size_t i = 0; i < n; ++i) {
             OrtTensorTypeAndShapeInfo* info = nullptr;
             check_ort(a, api::GetTensorTypeAndShape(a)(src[i], &info), "GetTensorTypeAndShape");
@@ -124,8 +144,10 @@ OrtStatus* dt_copy(OrtDataTransferImpl* self, const OrtValue** src, OrtValue** d
             check_ort(a, api::GetTensorData(a)(src[i], &s), "GetTensorData");
             check_ort(a, api::GetTensorMutableData(a)(dst[i], &d), "GetTensorMutableData");
             const size_t bytes = count * dtype_size(et);
-            if (bytes) check_hip(hipMemcpy(d, s, bytes, hipMemcpyDefault), "hipMemcpy");
+            if (bytes)
+                check_hip(hipMemcpyAsync(d, s, bytes, hipMemcpyDefault, t->stream), "hipMemcpyAsync");
         }
+        check_hip(hipStreamSynchronize(t->stream), "hipStreamSynchronize");
     });
 }
 
@@ -158,6 +180,7 @@ struct Ep {
     const OrtEpApi* ep_api;
     std::string name;
     int device = 0;
+    const OrtMemoryDevice* memory_device = nullptr;  // null: CPU memory
 };
 
 struct Factory {
@@ -165,6 +188,13 @@ struct Factory {
     const OrtApi* api;
     const OrtEpApi* ep_api;
     std::string name, vendor, version;
+    // HBM of GPU 0, registered on the EP device as its allocator's memory info:
+    // ORT allocates the fused nodes' inputs and outputs there and copies host
+    // values in and out through CreateDataTransfer. Owned by the factory.
+    OrtMemoryInfo* hbm_info = nullptr;
+    ~Factory() {
+        if (hbm_info) api::ReleaseMemoryInfo(api)(hbm_info);
+    }
 };
 
 const char* ep_get_name(const OrtEp* self) { return reinterpret_cast<const Ep*>(self)->name.c_str(); }
@@ -284,12 +314,15 @@ void ep_release_infos(OrtEp*, OrtNodeComputeInfo** infos, size_t n) {
     for (size_t i = 0; i < n; ++i) delete reinterpret_cast<ComputeInfo*>(infos[i]);
 }
 
-// CPU memory, as the reference (rust/src/ep.rs:104-113): ORT hands Compute host
-// buffers unless the caller binds device ones. Inputs already in HBM are used in
-// place; host inputs are staged, and host KV caches shared between past and
-// present get only their new rows written back (the plan's delta copy-out).
-OrtStatus* ep_default_memory_device(const OrtEp*, const OrtMemoryDevice** device) {
-    if (device) *device = nullptr;
+// The HBM memory device registered on the EP device (f_supported_devices): ORT
+// then places the fused nodes' inputs and outputs in HBM, copying host feeds in
+// and host-bound outputs out through this EP's data transfer, and a KV cache bound
+// to device buffers never crosses PCIe. ORTMI_EP_MEMORY=cpu reports CPU memory
+// instead, the reference's answer on unified memory (rust/src/ep.rs:104-113): ORT
+// then hands Compute host buffers, which the plan stages itself (host KV caches
+// shared between past and present get only their new rows written back).
+OrtStatus* ep_default_memory_device(const OrtEp* self, const OrtMemoryDevice** device) {
+    if (device) *device = reinterpret_cast<const Ep*>(self)->memory_device;
     return nullptr;
 }
 
@@ -323,6 +356,17 @@ OrtStatus* f_supported_devices(OrtEpFactory* p, const OrtHardwareDevice* const* 
         OrtEpDevice* d = nullptr;
         check_ort(f->api, ep_api::CreateEpDevice(f->ep_api)(p, gpu, nullptr, nullptr, &d),
                   "CreateEpDevice");
+        // The device's memory: HBM of GPU 0 (AMD vendor id), device allocator.
+        if (!f->hbm_info) {
+            OrtStatus* st = api::CreateMemoryInfo_V2(f->api)(
+                kHbmMemoryInfoName, OrtMemoryInfoDeviceType_GPU, kVendorIdAmd, 0,
+                OrtDeviceMemoryType_DEFAULT, 256, OrtDeviceAllocator, &f->hbm_info);
+            if (st) ep_api::ReleaseEpDevice(f->ep_api)(d);
+            check_ort(f->api, st, "CreateMemoryInfo_V2");
+        }
+        OrtStatus* st = ep_api::EpDevice_AddAllocatorInfo(f->ep_api)(d, f->hbm_info);
+        if (st) ep_api::ReleaseEpDevice(f->ep_api)(d);
+        check_ort(f->api, st, "EpDevice_AddAllocatorInfo");
         ep_devices[0] = d;
         *num_ep_devices = 1;
     });
@@ -349,6 +393,10 @@ OrtStatus* f_create_ep(OrtEpFactory* p, const OrtHardwareDevice* const*,
         ep->ep_api = f->ep_api;
         ep->name = f->name;
         ep->device = 0;
+        const char* mem = std::getenv("ORTMI_EP_MEMORY");
+        const bool cpu = mem && std::strcmp(mem, "cpu") == 0;
+        if (!cpu && f->hbm_info)
+            ep->memory_device = ep_api::MemoryInfo_GetMemoryDevice(f->ep_api)(f->hbm_info);
         *out = &ep->base;
     });
 }
@@ -403,6 +451,7 @@ OrtStatus* f_create_data_transfer(OrtEpFactory* p, OrtDataTransferImpl** out) {
         t->base.CanCopy = dt_can_copy;
         t->base.CopyTensors = dt_copy;
         t->api = f->api;
+        t->ep_api = f->ep_api;
         *out = &t->base;
     });
 }

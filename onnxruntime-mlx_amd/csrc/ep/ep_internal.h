@@ -206,6 +206,9 @@ class Plan {
                        size_t slabs);
     void run_node(const NodeDesc& n, const OrtApi* api, OrtKernelContext* ctx);
     int32_t host_i32(const std::string& name);
+    void read_device_scalars();
+    int32_t* scalar_host_ = nullptr;  // pinned landing slots of read_device_scalars
+    size_t scalar_host_n_ = 0;
     bool guards_hold(const std::vector<Guard>& guards) const;
     bool replay(const OrtApi* api, OrtKernelContext* ctx);
     bool capture(const OrtApi* api, OrtKernelContext* ctx, const std::vector<InputSig>& sig);
@@ -216,6 +219,7 @@ class Plan {
     bool run_decode_program(const OrtApi* api, OrtKernelContext* ctx);
     std::unique_ptr<DecodeProgram> dprog_;
     bool dprog_required_ = false;  // ORTMI_EP_PROGRAM=require: fail when it does not apply
+    int64_t dprog_fallbacks_ = 0;  // one-token steps the program did not complete (run op by op)
     std::string dprog_reject_ = "no decoder structure", dprog_ids_;  // why not; the ids input
 
     GraphIR sub_;

@@ -428,18 +428,53 @@ std::string claim_paged(const NodeDesc& n, const GraphIR& g) {
     return "";
 }
 
-// rust/src/ops/attention.rs:2158-2264
+// rust/src/ops/attention.rs:2158-2264. The rotated width is the cos/sin cache's last
+// dim (half), as the reference's rope_apply takes it; dims past 2 * half keep their
+// values (partial rotary).
 std::string claim_rotary(const NodeDesc& n, const GraphIR& g) {
+    REQUIRE(!n.outputs.empty() && !n.outputs[0].empty(), "requires an output");
+    const bool ms = n.domain == "com.microsoft";
+    const int ci = ms ? 2 : 1, si = ms ? 3 : 2, pi = ms ? 1 : 3;
+    REQUIRE(n.inputs.size() >= (size_t)(ms ? 4 : 3), "too few inputs");
     auto* x = val(g, n, 0);
     REQUIRE(x && x->has_shape && (x->dims.size() == 3 || x->dims.size() == 4),
             "input must be rank 3 or 4");
     REQUIRE(is_float(x->dtype), "float input required");
-    const bool ms = n.domain == "com.microsoft";
-    const int ci = ms ? 2 : 1, si = ms ? 3 : 2;
     auto *c = val(g, n, ci), *s = val(g, n, si);
-    REQUIRE(c && s && c->dtype == x->dtype && s->dtype == x->dtype,
+    REQUIRE(c && s && c->dtype == x->dtype && s->dtype == x->dtype && c->has_shape &&
+                !c->dims.empty(),
             "cos/sin caches must share the input dtype");
+    auto* o = g.values.count(n.outputs[0]) ? &g.values.at(n.outputs[0]) : nullptr;
+    REQUIRE(!o || o->dtype == 0 || o->dtype == x->dtype, "output must share the input dtype");
     REQUIRE(n.attr_int("is_packed_batching", 0) == 0, "packed batching is not supported");
+    const int64_t half = c->dims.back();
+    REQUIRE(half > 0, "empty cos cache");
+    if (x->dims.size() == 3) {
+        const int64_t nh = n.attr_int("num_heads", 0), hidden = x->dims[2];
+        if (nh > 0) {
+            REQUIRE(hidden > 0 && hidden % nh == 0, "hidden must divide by num_heads");
+            REQUIRE(2 * half <= hidden / nh, "rotary width exceeds the head size");
+        } else {
+            REQUIRE(n.attr_int("rotary_embedding_dim", 0) == 0,
+                    "num_heads = 0 needs rotary_embedding_dim = 0 to infer the head size");
+            REQUIRE(hidden > 0 && hidden % (2 * half) == 0,
+                    "hidden must divide by the inferred head size (2 x cos width)");
+        }
+    } else if (x->dims[3] > 0) {
+        REQUIRE(2 * half <= x->dims[3], "rotary width exceeds the head size");
+    }
+    const bool has_pos = n.has_input(pi);
+    REQUIRE(!ms || has_pos, "com.microsoft RotaryEmbedding requires position_ids");
+    if (has_pos) {
+        auto* p = val(g, n, pi);
+        // The ONNX schemas (ai.onnx opset 23, com.microsoft) type position_ids int64.
+        REQUIRE(p && p->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64, "position_ids must be int64");
+        REQUIRE(p->has_shape && (p->dims.size() == 2 || (ms && p->dims.size() == 1 && p->dims[0] == 1)),
+                "position_ids must be [B,S] or, for com.microsoft, [1]");
+        REQUIRE(c->dims.size() == 2, "a gathered cos cache must have rank 2");
+    } else {
+        REQUIRE(c->dims.size() == 3, "without position_ids the cos cache must be [B,S,half]");
+    }
     return "";
 }
 
@@ -457,8 +492,18 @@ std::string claim_rms(const NodeDesc& n, const GraphIR& g) {
     if (n.op == "SkipSimplifiedLayerNormalization") {
         auto* sk = val(g, n, 1);
         REQUIRE(sk && sk->dtype == x->dtype, "skip must share the input dtype");
-        REQUIRE(n.outputs.size() < 2 || n.outputs[1].empty(), "mean output is not produced");
-        REQUIRE(n.outputs.size() < 3 || n.outputs[2].empty(), "inv_std_var output is not produced");
+        // mean (output 1) and inv_std_var (output 2) are not produced. Declared but
+        // unused, as transformers.js / Mobius exports leave them, the node is claimed
+        // (rust/src/ops/norm.rs:586-594); read by any node or a graph output, it is
+        // declined, so ORT's own kernel produces them.
+        for (size_t i = 1; i <= 2 && i < n.outputs.size(); ++i) {
+            const std::string& o = n.outputs[i];
+            if (o.empty()) continue;
+            bool read = std::find(g.outputs.begin(), g.outputs.end(), o) != g.outputs.end();
+            for (const NodeDesc& m : g.nodes)
+                for (const std::string& in : m.inputs) read = read || in == o;
+            REQUIRE(!read, i == 1 ? "mean output is read" : "inv_std_var output is read");
+        }
     } else {
         REQUIRE(n.outputs.size() < 2 || n.outputs[1].empty(), "inv_std_var output is not produced");
     }

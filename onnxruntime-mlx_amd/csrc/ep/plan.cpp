@@ -75,6 +75,8 @@ struct Plan::DecodeProgram {
     void* argmax_ptr = nullptr;  // the same for the ArgMax output
     bool argmax_dev = false;
     int32_t* status = nullptr;  // host-pinned: the kernel writes it, the host reads it after the run
+    int64_t steps = 0;          // program launches so far
+    int64_t abort_step = 0;     // ORTMI_EP_PROGRAM_ABORT: launch to abort before it starts (1-based)
     ~DecodeProgram() {
         if (status) (void)hipHostFree(status);
     }
@@ -343,6 +345,7 @@ void Plan::match_decode_program() {
     dp->gf_p = dev(dp->gf);
     dp->lm_B_p = dev(dp->lm_B);
     dp->lm_S_p = dev(dp->lm_S);
+    if (const char* ab = std::getenv("ORTMI_EP_PROGRAM_ABORT")) dp->abort_step = std::atoll(ab);
     check_hip(hipHostMalloc((void**)&dp->status, sizeof(int32_t), hipHostMallocDefault),
               "hipHostMalloc");
     dp->next_id = device_alloc(sizeof(int64_t));
@@ -377,8 +380,13 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
         table[l].v_cache = pv.ptr;
     }
     d.kv_capacity = (int32_t)cap;
-    const int32_t total = host_i32(dp.total);
-    if (total < 1 || total > cap || total > d.max_position) return skip("total_sequence_length out of range");
+    // A host total is checked here; one in device memory (an EP whose memory device
+    // is HBM gets its inputs there) is checked by the kernel itself (status 3), which
+    // saves the step a device -> host round trip.
+    auto hs = host_scalars_.find(dp.total);
+    if (hs != host_scalars_.end() &&
+        (hs->second < 1 || hs->second > cap || hs->second > d.max_position))
+        return skip("total_sequence_length out of range");
     // Present outputs must be the past buffers (KV written in place) and logits a device buffer.
     const std::vector<int64_t> pdims = {1, d.kv_num_heads, cap, d.head_size};
     for (size_t l = 0; l < dp.layers.size(); ++l) {
@@ -429,6 +437,25 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
         check_hip(hipMemsetAsync(dp.ws->ptr, 0, wsb, stream_), "decode program workspace");
     }
     *dp.status = -1;
+    if (++dp.steps == dp.abort_step) {
+        // Diagnostic (ORTMI_EP_PROGRAM_ABORT=n): abort the n-th launch before it
+        // starts, through the workspace's abort word, so the op-path fallback for a
+        // step the program did not complete can be exercised. Launch index = started
+        // workgroups / grid (the CU count rounded down to a multiple of 8).
+        int cus = 0;
+        check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device_),
+                  "CU count");
+        const uint64_t grid = (uint64_t)(cus - cus % 8);
+        uint64_t started = 0;
+        check_hip(hipMemcpyAsync(&started, dp.ws->ptr, 8, hipMemcpyDeviceToHost, stream_),
+                  "abort word");
+        check_hip(hipStreamSynchronize(stream_), "abort word");
+        const uint32_t word = (uint32_t)(started / (grid ? grid : 1)) + 1u;
+        check_hip(hipMemcpyAsync(static_cast<char*>(dp.ws->ptr) + 128, &word, 4,
+                                 hipMemcpyHostToDevice, stream_),
+                  "abort word");
+        check_hip(hipStreamSynchronize(stream_), "abort word");
+    }
     const int rc = ortmi_decoder_decode_step(
         static_cast<const OrtmiDecoderLayer*>(dp.table->ptr), &d, dp.embed_p, dp.embed_rows,
         static_cast<const int64_t*>(ids->second.ptr),
@@ -442,6 +469,12 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
         dprog_reject_ = why;
         return false;
     }
+    if (rc == ORTMI_E_HIP && !dprog_required_) {
+        // The cooperative launch itself failed (e.g. the CUs are not all free for a
+        // grid that must be co-resident): this step runs op by op.
+        ++dprog_fallbacks_;
+        return false;
+    }
     check_kernel(rc, "decode program");
     if (argmax_host)
         check_hip(hipMemcpyAsync(argmax_host, next_id, sizeof(int64_t), hipMemcpyDeviceToHost,
@@ -451,6 +484,7 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
 }
 
 Plan::~Plan() {
+    if (scalar_host_) (void)hipHostFree(scalar_host_);
     if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
     if (stream_) (void)hipStreamDestroy(stream_);
 }
@@ -487,6 +521,37 @@ void* Plan::arena_alloc(size_t bytes) {
     ++mem_epoch_;
     arena_off_ = base + bytes;
     return arena_.back()->ptr;
+}
+
+// One-element int32 inputs in device memory (total_sequence_length, seqlens_k when
+// the EP's memory device is HBM) are read back once per op-path run, in one batch:
+// shapes and the graph-replay guards need their values on the host. The captured
+// kernels read them from the same device buffers, so replay stays valid.
+void Plan::read_device_scalars() {
+    std::vector<size_t> idx;
+    for (size_t i = 0; i < inputs_.size(); ++i) {
+        if (inputs_[i].empty() || !devptr_[i].second || host_scalars_.count(inputs_[i])) continue;
+        auto it = env_.find(inputs_[i]);
+        if (it == env_.end() || it->second.dtype != ONNX_TENSOR_ELEMENT_DATA_TYPE_INT32 ||
+            it->second.numel() != 1)
+            continue;
+        idx.push_back(i);
+    }
+    if (idx.empty()) return;
+    if (scalar_host_n_ < idx.size()) {
+        if (scalar_host_) (void)hipHostFree(scalar_host_);
+        scalar_host_ = nullptr;
+        check_hip(hipHostMalloc((void**)&scalar_host_, idx.size() * sizeof(int32_t),
+                                hipHostMallocDefault),
+                  "pinned scalars");
+        scalar_host_n_ = idx.size();
+    }
+    for (size_t k = 0; k < idx.size(); ++k)
+        check_hip(hipMemcpyAsync(scalar_host_ + k, env_.at(inputs_[idx[k]]).ptr, 4,
+                                 hipMemcpyDeviceToHost, stream_),
+                  "read scalar");
+    check_hip(hipStreamSynchronize(stream_), "read scalar");
+    for (size_t k = 0; k < idx.size(); ++k) host_scalars_[inputs_[idx[k]]] = scalar_host_[k];
 }
 
 int32_t Plan::host_i32(const std::string& name) {
@@ -702,10 +767,17 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
             g_out_staging = nullptr;
             const int32_t st = *dprog_->status;
             if (st == 2) fail("decode program: input id out of range", ORT_INVALID_ARGUMENT);
-            if (st != 0) fail("decode program failed (status " + std::to_string(st) + ")");
-            return;
+            if (st == 0) return;
+            // Not completed (1: a wait saw no data for 100 ms; -1: the launch stopped
+            // before writing a status). The step runs again op by op: the K/V row it
+            // may have written at total - 1 is rewritten with the same values.
+            if (dprog_required_)
+                fail("decode program failed (status " + std::to_string(st) + ")");
+            ++dprog_fallbacks_;
+            outs_.clear();
         }
     }
+    read_device_scalars();
     for (auto& kv : constants_) {
         const ValueDesc& v = sub_.values.at(kv.first);
         Tensor t;
@@ -940,6 +1012,7 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         // the reference's delta write-back (rust/src/engine.rs:78-94, 1997-2093).
         if (shared && pk && pv && pk->host && pv->host && !outname(1).empty() &&
             !outname(2).empty()) {
+            const size_t nrec = outs_.size();  // output_buffer records only fused-node outputs
             void* hk = output_buffer(outname(1), pdims, a, ctx);
             void* hv = output_buffer(outname(2), pdims, a, ctx);
             if (hk == pk->host && hv == pv->host) {
@@ -967,9 +1040,9 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
                     env_[outname(j)] = t;
                 }
             } else {
-                // Not aliased: drop the two records; out_tensor below fetches the
-                // outputs again and stages them whole.
-                outs_.resize(outs_.size() - 2);
+                // Not aliased: drop the records just made; out_tensor below fetches
+                // the outputs again and stages them whole.
+                outs_.resize(nrec);
             }
         }
         for (Tensor* t : {pk, pv})
@@ -1140,9 +1213,9 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
             hd = nh_attr > 0 ? x.dims[2] / nh_attr : 2 * cs.dims.back();
             NH = x.dims[2] / hd;
         }
-        int64_t half = cs.dims.back();
-        const int64_t rdim = n.attr_int("rotary_embedding_dim", 0);
-        if (rdim > 0 && rdim / 2 != half) fail("RotaryEmbedding: partial rotary cache layout", ORT_NOT_IMPLEMENTED);
+        // The cache's last dim is the rotated half width (rust/src/ops/attention.rs:
+        // 1234-1282): dims from 2 * half on keep their values.
+        const int64_t half = cs.dims.back();
         const int64_t rows = cs.numel() / half;
         Tensor& Y = out_tensor(outname(0), x.dtype, x.dims, a, ctx);
         check_kernel(ortmi_rotary_embedding(x.ptr, pos ? (const int64_t*)pos->ptr : nullptr,
@@ -1167,8 +1240,10 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         Tensor& Y = out_tensor(outname(0), x.dtype, x.dims, a, ctx);
         void* yp = Y.ptr;
         void* rp = nullptr;
-        if (skip && n.outputs.size() >= 2 && !n.outputs.back().empty())
-            rp = out_tensor(n.outputs.back(), x.dtype, x.dims, a, ctx).ptr;
+        // input_skip_bias_sum is output 3 (outputs 1 and 2, mean and inv_std_var,
+        // are declared-but-unread when the node is claimed).
+        if (skip && n.outputs.size() >= 4 && !n.outputs[3].empty())
+            rp = out_tensor(n.outputs[3], x.dtype, x.dims, a, ctx).ptr;
         check_kernel(ortmi_rms_norm(x.ptr, skp, bp, gp, yp, rp, x.numel() / D, D, eps,
                                     kdt(x.dtype), st),
                      op.c_str());

@@ -8,9 +8,15 @@
 // does (the reference's call sequence: rust/src/lib.rs:90-155,
 // rust/src/factory.rs:116-213, rust/src/ep.rs:119-357, 928-1211, 1931-2134).
 // Graphs must be claimed completely: there is no CPU execution provider here.
-// Tensors handed to Compute are whatever the caller binds: device memory (the
-// IOBinding case) or host memory (what ORT hands an EP whose default memory
-// device is the CPU); outputs the caller does not bind are hipMalloc'd.
+// Placement follows ORT's rule for a fused node: its inputs and outputs live on
+// the EP's default memory device (OrtEp::GetDefaultMemoryDevice; null = CPU
+// memory). A feed on the other side (host vs device) is copied there through the
+// EP factory's data transfer before Compute, into a buffer from the allocator the
+// factory hands out for the memory info the EP device registered; an output bound
+// to memory on the other side is produced in such a buffer and copied back after
+// Compute; an output nobody binds is allocated on the EP's side. A feed or binding
+// already on the EP's side (device buffers with an HBM EP: the IOBinding case) is
+// used in place.
 #include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
@@ -38,6 +44,14 @@ struct OrtHardwareDevice {
 struct OrtEpDevice {
     OrtEpFactory* factory;
     const OrtHardwareDevice* device;
+    std::vector<const OrtMemoryInfo*> allocator_infos;  // EpDevice_AddAllocatorInfo (not owned)
+};
+// Where memory lives (ORT's OrtDevice): type, vendor id, device id, memory type.
+struct OrtMemoryDevice {
+    OrtMemoryInfoDeviceType type = OrtMemoryInfoDeviceType_CPU;
+    uint32_t vendor = 0;
+    int32_t id = 0;
+    OrtDeviceMemoryType mem = OrtDeviceMemoryType_DEFAULT;
 };
 // Type/shape info; the same object serves as OrtTypeInfo and as the tensor info.
 struct OrtTensorTypeAndShapeInfo {
@@ -49,6 +63,7 @@ struct OrtValue {
     OrtTensorTypeAndShapeInfo info;
     void* data = nullptr;       // device pointer (or host for initializers)
     std::vector<uint8_t> host;  // initializer storage
+    bool on_device = false;     // where `data` lives (GPU memory or host memory)
 };
 struct OrtValueInfo {
     std::string name;
@@ -99,6 +114,8 @@ struct OrtMemoryInfo {
     OrtAllocatorType type = OrtDeviceAllocator;
     int id = 0;
     OrtMemType mem_type = OrtMemTypeDefault;
+    OrtMemoryDevice device;
+    size_t alignment = 0;
 };
 
 namespace {
@@ -154,7 +171,30 @@ void h_ReleaseTensorTypeAndShapeInfo(OrtTensorTypeAndShapeInfo* t) { delete t; }
 OrtStatus* h_CreateMemoryInfo(const char* name, OrtAllocatorType type, int id, OrtMemType mem_type,
                               OrtMemoryInfo** out) {
     if (!name || !out) return mk(ORT_INVALID_ARGUMENT, "CreateMemoryInfo: null argument");
-    *out = new OrtMemoryInfo{name, type, id, mem_type};
+    auto* m = new OrtMemoryInfo();
+    m->name = name;
+    m->type = type;
+    m->id = id;
+    m->mem_type = mem_type;
+    // ORT's names: "Cpu" is host memory; this harness reads any other as GPU memory.
+    if (std::strcmp(name, "Cpu") != 0) m->device = {OrtMemoryInfoDeviceType_GPU, 0x1002, id, {}};
+    *out = m;
+    return nullptr;
+}
+OrtStatus* h_CreateMemoryInfo_V2(const char* name, OrtMemoryInfoDeviceType device_type,
+                                 uint32_t vendor_id, int32_t device_id, OrtDeviceMemoryType mem_type,
+                                 size_t alignment, OrtAllocatorType allocator_type,
+                                 OrtMemoryInfo** out) {
+    if (!name || !out) return mk(ORT_INVALID_ARGUMENT, "CreateMemoryInfo_V2: null argument");
+    if (device_type != OrtMemoryInfoDeviceType_CPU && device_type != OrtMemoryInfoDeviceType_GPU)
+        return mk(ORT_INVALID_ARGUMENT, "CreateMemoryInfo_V2: device type not supported here");
+    auto* m = new OrtMemoryInfo();
+    m->name = name;
+    m->type = allocator_type;
+    m->id = device_id;
+    m->device = {device_type, vendor_id, device_id, mem_type};
+    m->alignment = alignment;
+    *out = m;
     return nullptr;
 }
 OrtStatus* h_MemoryInfoGetName(const OrtMemoryInfo* m, const char** out) {
@@ -333,7 +373,7 @@ OrtStatus* h_ReadOpAttr(const OrtOpAttr* a, OrtOpAttrType t, void* data, size_t 
 // ---------------------------------------------------------- OrtEpApi impl --
 OrtStatus* h_CreateEpDevice(OrtEpFactory* f, const OrtHardwareDevice* d, const OrtKeyValuePairs*,
                             const OrtKeyValuePairs*, OrtEpDevice** out) {
-    *out = new OrtEpDevice{f, d};
+    *out = new OrtEpDevice{f, d, {}};
     return nullptr;
 }
 void h_ReleaseEpDevice(OrtEpDevice* d) { delete d; }
@@ -349,6 +389,15 @@ OrtStatus* h_EpGraphSupportInfo_AddSingleNode(OrtEpGraphSupportInfo* info, const
     return nullptr;
 }
 const char* h_NodeComputeContext_NodeName(const OrtNodeComputeContext* c) { return c->name.c_str(); }
+OrtStatus* h_EpDevice_AddAllocatorInfo(OrtEpDevice* d, const OrtMemoryInfo* info) {
+    if (!d || !info) return mk(ORT_INVALID_ARGUMENT, "EpDevice_AddAllocatorInfo: null argument");
+    d->allocator_infos.push_back(info);
+    return nullptr;
+}
+const OrtMemoryDevice* h_MemoryInfo_GetMemoryDevice(const OrtMemoryInfo* m) { return &m->device; }
+OrtMemoryInfoDeviceType h_MemoryDevice_GetDeviceType(const OrtMemoryDevice* d) { return d->type; }
+uint32_t h_MemoryDevice_GetVendorId(const OrtMemoryDevice* d) { return d->vendor; }
+uint32_t h_MemoryDevice_GetDeviceId(const OrtMemoryDevice* d) { return (uint32_t)d->id; }
 
 // Function tables built from the shared slot lists.
 void* g_api[ORTMI_ORT_API_TABLE_SIZE];
@@ -417,6 +466,13 @@ struct DevBuf {
     size_t bytes = 0;
 };
 
+// A value's copy on the EP's side of the placement rule (a fixed buffer per name,
+// regrown only when a larger value comes).
+struct Placed {
+    OrtValue value;
+    size_t bytes = 0;
+};
+
 struct Session {
     HxGraph* graph = nullptr;
     void* lib = nullptr;
@@ -433,7 +489,26 @@ struct Session {
     std::unordered_map<std::string, OrtValue*> env;
     std::unordered_map<std::string, std::unique_ptr<OrtValue>> store;
     std::unordered_map<std::string, DevBuf> owned;              // harness-allocated outputs
-    std::unordered_map<std::string, void*> bound;               // caller-bound output buffers
+    std::unordered_map<std::string, std::pair<void*, bool>> bound;  // caller-bound outputs (ptr, on device)
+    // Placement rule state: the EP's default memory device (null: CPU memory), the
+    // allocator the factory handed out for it, the EP's data transfer, the copies
+    // of feeds and the staged outputs bound on the other side.
+    const OrtMemoryDevice* ep_mem = nullptr;
+    bool ep_dev = false;  // the EP's memory is GPU memory
+    OrtAllocator* ep_alloc = nullptr;
+    OrtDataTransferImpl* dt = nullptr;
+    std::unordered_map<std::string, Placed> feeds, staged_outs;
+    std::vector<std::pair<OrtValue*, std::string>> copy_back;  // staged output -> its binding
+    int64_t copies = 0;                                        // data-transfer calls made by runs
+    void* side_alloc(size_t bytes) {
+        if (!ep_dev) return std::malloc(bytes ? bytes : 1);
+        return ep_alloc ? ep_alloc->Alloc(ep_alloc, bytes ? bytes : 1) : nullptr;
+    }
+    void side_free(void* p) {
+        if (!p) return;
+        if (!ep_dev) std::free(p);
+        else if (ep_alloc) ep_alloc->Free(ep_alloc, p);
+    }
     OrtValue* value(const std::string& name) {
         auto& v = store[name];
         if (!v) v = std::make_unique<OrtValue>();
@@ -464,18 +539,38 @@ OrtStatus* h_KernelContext_GetOutput(OrtKernelContext* c, size_t i, const int64_
     size_t bytes = esize(v->info.dtype);
     for (size_t k = 0; k < n; ++k) bytes *= (size_t)(dims[k] < 0 ? 0 : dims[k]);
     auto b = s->bound.find(name);
-    if (b != s->bound.end()) {
-        v->data = b->second;
+    if (b != s->bound.end() && b->second.second == s->ep_dev) {
+        v->data = b->second.first;  // bound on the EP's side: written in place
+        v->on_device = s->ep_dev;
+    } else if (b != s->bound.end()) {
+        // Bound on the other side: produced in a buffer on the EP's side and copied
+        // to the binding after Compute.
+        Placed& st = s->staged_outs[name];
+        if (st.bytes < bytes) {
+            s->side_free(st.value.data);
+            st.value.data = s->side_alloc(bytes);
+            st.bytes = st.value.data ? bytes : 0;
+            if (!st.value.data) return mk(ORT_FAIL, "harness: allocation failed for output " + name);
+        }
+        st.value.info = v->info;
+        st.value.on_device = s->ep_dev;
+        v->data = b->second.first;
+        v->on_device = b->second.second;
+        s->copy_back.push_back({&st.value, name});
+        *out = &st.value;
+        s->env[name] = v;
+        return nullptr;
     } else {
+        // Nobody binds it: allocated on the EP's side.
         DevBuf& buf = s->owned[name];
         if (buf.bytes < bytes) {
-            if (buf.ptr) (void)hipFree(buf.ptr);
-            buf.ptr = nullptr;
-            if (hipMalloc(&buf.ptr, bytes ? bytes : 1) != hipSuccess)
-                return mk(ORT_FAIL, "harness: hipMalloc failed for output " + name);
-            buf.bytes = bytes;
+            s->side_free(buf.ptr);
+            buf.ptr = s->side_alloc(bytes);
+            buf.bytes = buf.ptr ? bytes : 0;
+            if (!buf.ptr) return mk(ORT_FAIL, "harness: allocation failed for output " + name);
         }
         v->data = buf.ptr;
+        v->on_device = s->ep_dev;
     }
     *out = v;
     s->env[name] = v;
@@ -491,11 +586,14 @@ Session::~Session() {
         for (auto& p : parts) infos.push_back(p->info);
         ep->ReleaseNodeComputeInfos(ep, infos.data(), infos.size());
     }
+    for (auto& kv : owned) side_free(kv.second.ptr);
+    for (auto* m : {&feeds, &staged_outs})
+        for (auto& kv : *m) side_free(kv.second.value.data);
+    if (ep_alloc) factory->ReleaseAllocator(factory, ep_alloc);
+    if (dt) dt->Release(dt);
     if (ep) factory->ReleaseEp(factory, ep);
     if (ep_device) h_ReleaseEpDevice(ep_device);
     if (factory && release_factory) release_factory(factory);
-    for (auto& kv : owned)
-        if (kv.second.ptr) (void)hipFree(kv.second.ptr);
     if (lib) dlclose(lib);
 }
 
@@ -697,6 +795,39 @@ Session* hx_session_new(HxGraph* g, const char* ep_path, const char* registratio
         graphs.push_back(&p->sub);
         fused.push_back(&p->fused);
     }
+    // Placement: the EP's default memory device, and for a GPU one the allocator the
+    // factory hands out for the matching memory info the EP device registered (as
+    // ORT creates the device allocators of a session); the EP's data transfer.
+    if (!s->ep->GetDefaultMemoryDevice) {
+        g_err = "OrtEp::GetDefaultMemoryDevice is not set";
+        return nullptr;
+    }
+    if (!take(s->ep->GetDefaultMemoryDevice(s->ep, &s->ep_mem), "GetDefaultMemoryDevice"))
+        return nullptr;
+    s->ep_dev = s->ep_mem && s->ep_mem->type != OrtMemoryInfoDeviceType_CPU;
+    if (s->ep_dev) {
+        const OrtMemoryInfo* info = nullptr;
+        if (s->ep_device)
+            for (const OrtMemoryInfo* m : s->ep_device->allocator_infos)
+                if (&m->device == s->ep_mem) info = m;
+        if (!info) {
+            g_err = "the EP's default memory device is not one its EP device registered";
+            return nullptr;
+        }
+        if (!take(s->factory->CreateAllocator(s->factory, info, nullptr, &s->ep_alloc),
+                  "CreateAllocator"))
+            return nullptr;
+        if (!s->ep_alloc) {
+            g_err = "the EP factory gave no allocator for its own memory info";
+            return nullptr;
+        }
+    }
+    if (!take(s->factory->CreateDataTransfer(s->factory, &s->dt), "CreateDataTransfer"))
+        return nullptr;
+    if (!s->dt || !s->dt->CopyTensors || !s->dt->CanCopy || !s->dt->Release) {
+        g_err = "CreateDataTransfer returned an incomplete OrtDataTransferImpl";
+        return nullptr;
+    }
     std::vector<OrtNodeComputeInfo*> infos(s->parts.size(), nullptr);
     std::vector<OrtNode*> ctx_nodes(s->parts.size(), nullptr);
     if (!take(s->ep->Compile(s->ep, graphs.data(), fused.data(), graphs.size(), infos.data(),
@@ -726,8 +857,17 @@ int hx_session_node_claimed(Session* s, int node) {
 // Bind a caller-owned device buffer as the storage of a graph value produced by
 // the EP (an IOBinding analogue; binding a present-KV output to the past-KV input
 // buffer gives the shared-buffer contract).
+static bool is_device_memory(const void* p) {
+    hipPointerAttribute_t attr;
+    if (!p || hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
 int hx_session_bind_output(Session* s, const char* name, void* ptr) {
-    if (ptr) s->bound[name] = ptr;
+    if (ptr) s->bound[name] = {ptr, is_device_memory(ptr)};
     else s->bound.erase(name);
     return 0;
 }
@@ -735,6 +875,7 @@ int hx_session_bind_output(Session* s, const char* name, void* ptr) {
 int hx_session_set_input(Session* s, const char* name, void* ptr, int dtype, int rank,
                          const int64_t* dims) {
     OrtValue* v = s->value(name);
+    if (v->data != ptr || !ptr) v->on_device = is_device_memory(ptr);  // classified once per buffer
     v->data = ptr;
     v->info.dtype = dtype;
     v->info.dims.assign(dims, dims + rank);
@@ -762,9 +903,65 @@ int hx_session_run(Session* s) {
             OrtKernelContext ctx;
             ctx.session = s;
             ctx.inputs.reserve(p->fused.inputs.size());
-            for (auto* v : p->fused.inputs) ctx.inputs.push_back(s->env[v->name]);
+            // Feeds on the other side of the EP's memory are copied over first, in one
+            // data-transfer call.
+            std::vector<const OrtValue*> srcs;
+            std::vector<OrtValue*> dsts;
+            for (auto* vi : p->fused.inputs) {
+                OrtValue* v = s->env[vi->name];
+                if (v->on_device != s->ep_dev) {
+                    Placed& st = s->feeds[vi->name];
+                    size_t bytes = esize(v->info.dtype);
+                    for (int64_t d : v->info.dims) bytes *= (size_t)(d < 0 ? 0 : d);
+                    if (st.bytes < bytes) {
+                        s->side_free(st.value.data);
+                        st.value.data = s->side_alloc(bytes);
+                        st.bytes = st.value.data ? bytes : 0;
+                        if (!st.value.data) {
+                            g_err = "harness: allocation failed for feed " + vi->name;
+                            return 1;
+                        }
+                    }
+                    st.value.info = v->info;
+                    st.value.on_device = s->ep_dev;
+                    srcs.push_back(v);
+                    dsts.push_back(&st.value);
+                    v = &st.value;
+                }
+                ctx.inputs.push_back(v);
+            }
+            if (!srcs.empty()) {
+                // Host memory is a null device; device memory the EP did not declare
+                // is GPU 0 of AMD's vendor id.
+                static const OrtMemoryDevice gpu0{OrtMemoryInfoDeviceType_GPU, 0x1002, 0, {}};
+                const OrtMemoryDevice* src_dev = s->ep_dev ? nullptr : &gpu0;
+                const OrtMemoryDevice* dst_dev = s->ep_dev ? s->ep_mem : nullptr;
+                if (!s->dt->CanCopy(s->dt, src_dev, dst_dev)) {
+                    g_err = "the EP's data transfer cannot copy feeds to its memory device";
+                    return 1;
+                }
+                ++s->copies;
+                if (!take(s->dt->CopyTensors(s->dt, srcs.data(), dsts.data(), nullptr, srcs.size()),
+                          "CopyTensors (feeds)"))
+                    return 1;
+            }
             ctx.outputs.assign(p->fused.outputs.begin(), p->fused.outputs.end());
+            s->copy_back.clear();
             if (!take(p->info->Compute(p->info, p->state, &ctx), "Compute")) return 1;
+            // Outputs bound on the other side: staged on the EP's side, copied back.
+            if (!s->copy_back.empty()) {
+                std::vector<const OrtValue*> from;
+                std::vector<OrtValue*> to;
+                for (auto& cb : s->copy_back) {
+                    from.push_back(cb.first);
+                    to.push_back(s->env[cb.second]);
+                }
+                ++s->copies;
+                if (!take(s->dt->CopyTensors(s->dt, from.data(), to.data(), nullptr, from.size()),
+                          "CopyTensors (outputs)"))
+                    return 1;
+                s->copy_back.clear();
+            }
             done[pi] = progressed = true;
         }
         if (!progressed) break;
@@ -777,6 +974,18 @@ int hx_session_run(Session* s) {
     return 0;
 }
 
+// Data-transfer calls the placement rule made so far (feeds in, outputs back).
+int64_t hx_session_copies(Session* s) { return s->copies; }
+
+// The EP's default memory device as the session placed values: type
+// (OrtMemoryInfoDeviceType; CPU when the EP reports null), vendor id, device id.
+int hx_session_memory_device(Session* s, int* type, uint32_t* vendor, int* id) {
+    *type = s->ep_mem ? (int)s->ep_mem->type : (int)OrtMemoryInfoDeviceType_CPU;
+    *vendor = s->ep_mem ? s->ep_mem->vendor : 0;
+    *id = s->ep_mem ? s->ep_mem->id : 0;
+    return 0;
+}
+
 // OrtEp::GetDefaultMemoryDevice: 0 on success with *is_cpu = 1 when the EP
 // reports CPU memory (a null OrtMemoryDevice).
 int hx_session_default_memory_device(Session* s, int* is_cpu) {
@@ -786,7 +995,7 @@ int hx_session_default_memory_device(Session* s, int* is_cpu) {
         return 1;
     }
     if (!take(s->ep->GetDefaultMemoryDevice(s->ep, &dev), "GetDefaultMemoryDevice")) return 1;
-    *is_cpu = dev == nullptr ? 1 : 0;
+    *is_cpu = (dev == nullptr || dev->type == OrtMemoryInfoDeviceType_CPU) ? 1 : 0;
     return 0;
 }
 

@@ -102,12 +102,28 @@ class DecodeProgram:
         self.total = torch.zeros(1, dtype=torch.int32, device=dev)
         self.status = torch.full((1,), -1, dtype=torch.int32, device=dev)
 
+    def abort_next(self):
+        """Abort the next step before it starts, through the workspace's abort word
+        (byte 128: launch index + 1; launch index = the 64-bit started-workgroup
+        count at byte 0 / the grid, the CU count rounded down to a multiple of 8).
+        The aborted step reads and writes nothing and leaves status at -1."""
+        torch = self.torch
+        torch.cuda.synchronize()
+        base = self.ws[self.ws_off:self.ws_off + 256]
+        started = int(base[0:8].view(torch.int64).item())
+        cus = torch.cuda.get_device_properties(self.ws.device).multi_processor_count
+        word = (started // (cus - cus % 8) + 1) & 0xFFFFFFFF
+        base[128:132].view(torch.int32).fill_(word - (1 << 32) if word >= 1 << 31 else word)
+
     def step(self, token=None, total=None, stream=None):
         """One decode step: token (device int64 [1], default the last next_id) at
         position total - 1 (device int32 [1]); logits and next_id are written."""
         torch = self.torch
         tok = self.next_id if token is None else token
         tot = self.total if total is None else total
+        # Every step starts from "not completed": a launch that stops early (or is
+        # aborted before it starts) leaves -1, not the previous step's 0.
+        self.status.fill_(-1)
         st = ctypes.c_void_p(stream if stream is not None else
                              torch.cuda.current_stream().cuda_stream)
         check(self.lib.ortmi_decoder_decode_step(

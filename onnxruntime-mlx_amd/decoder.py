@@ -101,11 +101,14 @@ def make_weights(cfg: DecoderConfig, seed: int = 4):
 
 
 def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False,
-                argmax: bool = False) -> hx.Graph:
+                argmax: bool = False, norm_stats: bool = False) -> hx.Graph:
     """Decoder graph with symbolic sequence length S and KV capacity `cap`.
 
     argmax: end the graph with ArgMax(logits, axis=-1, keepdims=0) -> next_tokens
     (int64 [1, S]), so greedy decoding takes its next id from the graph itself.
+
+    norm_stats: every SkipSimplifiedLayerNormalization also declares its mean and
+    inv_std_var outputs (read by nothing), as transformers.js / Mobius exports do.
 
     layer_metadata: also record the residual stream after each layer (the last one's
     is the final norm's residual output) under the model metadata key
@@ -135,6 +138,16 @@ def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False,
     g.value("h0", F16, [1, S, D])
     g.node("Gather", ["embed", "input_ids"], ["h0"], name="embed_gather", axis=0)
     prev_out, residual = None, "h0"
+
+    def skip_norm(x, skip, gamma, y, res, name):
+        stats = ["", ""]
+        if norm_stats:
+            stats = [f"{name}.mean", f"{name}.inv_std"]
+            for v in stats:
+                g.value(v, hx.FLOAT, [1, S, 1])
+        g.node("SkipSimplifiedLayerNormalization", [x, skip, gamma], [y] + stats + [res],
+               domain="com.microsoft", name=name, epsilon=cfg.eps)
+
     for layer in range(cfg.layers):
         p = f"l{layer}"
         g.initializer(f"{p}.ln1", w[f"{p}.ln1"])
@@ -145,9 +158,7 @@ def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False,
                    name=f"{p}.ln1", epsilon=cfg.eps, axis=-1)
         else:
             g.value(f"{p}.res1", F16, [1, S, D])
-            g.node("SkipSimplifiedLayerNormalization", [prev_out, residual, f"{p}.ln1"],
-                   [f"{p}.x", "", "", f"{p}.res1"], domain="com.microsoft", name=f"{p}.ln1",
-                   epsilon=cfg.eps)
+            skip_norm(prev_out, residual, f"{p}.ln1", f"{p}.x", f"{p}.res1", f"{p}.ln1")
             residual = f"{p}.res1"
         for name, N, K in cfg.linear_shapes()[:3]:
             linear(f"{p}.x", f"{p}.{name}_proj", f"{p}.{name}", N, K, f"{p}.{name}")
@@ -167,9 +178,7 @@ def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False,
         linear(f"{p}.attn", f"{p}.o_proj", f"{p}.o", D, H * hd, f"{p}.o")
         g.value(f"{p}.x2", F16, [1, S, D])
         g.value(f"{p}.res2", F16, [1, S, D])
-        g.node("SkipSimplifiedLayerNormalization", [f"{p}.o", residual, f"{p}.ln2"],
-               [f"{p}.x2", "", "", f"{p}.res2"], domain="com.microsoft", name=f"{p}.ln2",
-               epsilon=cfg.eps)
+        skip_norm(f"{p}.o", residual, f"{p}.ln2", f"{p}.x2", f"{p}.res2", f"{p}.ln2")
         residual = f"{p}.res2"
         linear(f"{p}.x2", f"{p}.gate_proj", f"{p}.gate", cfg.inter, D, f"{p}.gate")
         linear(f"{p}.x2", f"{p}.up_proj", f"{p}.up", cfg.inter, D, f"{p}.up")
@@ -183,8 +192,7 @@ def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False,
     g.initializer("final_ln", w["final_ln"])
     g.value("xf", F16, [1, S, D])
     g.value("resf", F16, [1, S, D])
-    g.node("SkipSimplifiedLayerNormalization", [prev_out, residual, "final_ln"],
-           ["xf", "", "", "resf"], domain="com.microsoft", name="final_ln", epsilon=cfg.eps)
+    skip_norm(prev_out, residual, "final_ln", "xf", "resf", "final_ln")
     g.initializer("lm_head.B", w["lm_head.B"])
     g.initializer("lm_head.s", w["lm_head.s"])
     g.node("MatMulNBits", ["xf", "lm_head.B", "lm_head.s"], ["logits"], domain="com.microsoft",
@@ -203,23 +211,33 @@ def build_graph(cfg: DecoderConfig, w, cap: int, layer_metadata: bool = False,
 class DecoderRunner:
     """Greedy generation through the EP with a device-resident KV cache.
 
-    Per call the host sends only total_sequence_length (a 4-byte host input, as
-    ONNX Runtime keeps it in CPU memory); ids, logits, KV and the argmax stay in HBM.
+    seqlens_k and total_sequence_length are host inputs (pinned), as ONNX Runtime
+    keeps them; logits and KV are bound to device buffers (IOBinding).
 
     argmax_node: build the graph with its ArgMax (build_graph's argmax) and feed its
     output back as the next input id; otherwise the runner takes the argmax of the
     last logits row with ortmi_argmax_rows after each run.
+
+    host_feeds: the input ids are a host tensor too, as an application without
+    IOBinding feeds them (ONNX Runtime GenAI's loop): each step reads the greedy id
+    back to the host and feeds it, and the harness copies every host feed to the
+    EP's memory device (HBM) through the EP's data transfer before Compute.
+    Otherwise the ids stay in HBM and the argmax output is fed back in place.
     """
 
     def __init__(self, cfg: DecoderConfig, weights, cap: int, max_prompt: int,
-                 layer_metadata: bool = False, argmax_node: bool = False):
+                 layer_metadata: bool = False, argmax_node: bool = False,
+                 host_feeds: bool = False, norm_stats: bool = False):
         import torch
 
         self.torch = torch
         self.cfg = cfg
         self.cap = cap
         self.argmax_node = argmax_node
-        self.graph = build_graph(cfg, weights, cap, layer_metadata, argmax=argmax_node)
+        self.host_feeds = host_feeds
+        self.ids_host = torch.zeros((1, max_prompt), dtype=torch.int64, pin_memory=True)
+        self.graph = build_graph(cfg, weights, cap, layer_metadata, argmax=argmax_node,
+                                 norm_stats=norm_stats)
         self.session = hx.Session(self.graph)
         dev = "cuda"
         self.kv = []
@@ -292,12 +310,23 @@ class DecoderRunner:
 
     def prefill(self, prompt: np.ndarray):
         S = int(prompt.shape[-1])
-        self.ids[0, :S].copy_(self.torch.from_numpy(np.asarray(prompt, np.int64).reshape(-1)))
-        self.run(self.ids[:, :S], S)
+        ids = self.torch.from_numpy(np.asarray(prompt, np.int64).reshape(-1))
+        if self.host_feeds:
+            self.ids_host[0, :S].copy_(ids)
+            self.run(self.ids_host[:, :S], S)
+        else:
+            self.ids[0, :S].copy_(ids)
+            self.run(self.ids[:, :S], S)
         self.argmax_last(S)
 
     def decode_step(self):
-        self.run(self.next_id, 1)
+        if self.host_feeds:
+            # The greedy id back to the host (the stream is synchronised by the copy),
+            # then fed as a host input.
+            self.ids_host[0, 0] = int(self.next_id.reshape(-1)[0].item())
+            self.run(self.ids_host[:, :1], 1)
+        else:
+            self.run(self.next_id, 1)
         self.argmax_last(1)
 
     def generate(self, prompt: np.ndarray, steps: int):

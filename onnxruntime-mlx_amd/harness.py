@@ -2,10 +2,13 @@
 
 The harness stands in for ONNX Runtime's plugin loader: it builds a graph, loads
 the EP library through CreateEpFactories and drives GetCapability / Compile /
-Compute over the plugin C ABI. Tensors handed to Compute are the caller's torch
-tensors, on the device (the IOBinding case) or in host memory (what ONNX Runtime
-hands an EP whose default memory device is the CPU); unbound outputs are
-harness-allocated device buffers.
+Compute over the plugin C ABI. Values are placed as ONNX Runtime places them for
+a fused node: on the EP's default memory device (HBM for this EP; CPU memory with
+ORTMI_EP_MEMORY=cpu). Feeds and bound outputs on that side (device tensors with
+the HBM EP: the IOBinding case) are used in place; feeds on the other side are
+copied over through the EP's data transfer before Compute, outputs bound on the
+other side are produced there and copied back after it, and outputs nobody binds
+are allocated on the EP's side.
 """
 
 from __future__ import annotations
@@ -60,6 +63,10 @@ def lib() -> ctypes.CDLL:
             "hx_session_get_output": (ctypes.c_int, [vp, cp, ctypes.POINTER(vp),
                                                      ctypes.POINTER(ctypes.c_int), i64p]),
             "hx_session_default_memory_device": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_int)]),
+            "hx_session_memory_device": (ctypes.c_int, [vp, ctypes.POINTER(ctypes.c_int),
+                                                        ctypes.POINTER(ctypes.c_uint32),
+                                                        ctypes.POINTER(ctypes.c_int)]),
+            "hx_session_copies": (ctypes.c_int64, [vp]),
             "hx_factory_allocator_check": (ctypes.c_int, [vp, cp, ctypes.c_int, ctypes.c_size_t]),
             "hx_factory_data_transfer_copy": (ctypes.c_int, [vp, vp, vp, ctypes.c_int,
                                                              ctypes.c_int, i64p]),
@@ -182,6 +189,18 @@ class Session:
         if lib().hx_session_default_memory_device(self.h, ctypes.byref(flag)):
             raise RuntimeError(_err())
         return bool(flag.value)
+
+    def memory_device(self):
+        """(OrtMemoryInfoDeviceType, vendor id, device id) of the EP's default memory
+        device as the session places values: (0, 0, 0) for CPU memory, (1, 0x1002, 0)
+        for HBM of GPU 0."""
+        t, v, i = ctypes.c_int(), ctypes.c_uint32(), ctypes.c_int()
+        lib().hx_session_memory_device(self.h, ctypes.byref(t), ctypes.byref(v), ctypes.byref(i))
+        return t.value, v.value, i.value
+
+    def copies(self) -> int:
+        """Data-transfer calls the placement rule made in this session's runs."""
+        return int(lib().hx_session_copies(self.h))
 
     def allocator_check(self, memory_info_name: str, device_id: int = 0, nbytes: int = 1 << 20):
         """OrtEpFactory::CreateAllocator for (name, id): None when the EP gives no

@@ -315,9 +315,20 @@ def test_norm_claims():
            domain="com.microsoft", epsilon=1e-6)
     g.node("SkipSimplifiedLayerNormalization", ["x", "r", "w"], ["y2", "mean"],
            domain="com.microsoft", epsilon=1e-6)
-    g.io(["x", "r"], ["y0", "y1", "res", "y2", "mean"])
+    # mean / inv_std_var declared but read by nobody (a transformers.js / Mobius
+    # export): claimed, as rust/src/ops/norm.rs:586-594 claims it.
+    for v in ("y3", "mean3", "istd3", "res3", "y4", "istd4", "res4", "z4"):
+        g.value(v, F16, [1, -1, 1536])
+    g.node("SkipSimplifiedLayerNormalization", ["x", "r", "w"], ["y3", "mean3", "istd3", "res3"],
+           domain="com.microsoft", epsilon=1e-6)
+    # inv_std_var read by another node: declined (it is not produced).
+    g.node("SkipSimplifiedLayerNormalization", ["x", "r", "w"], ["y4", "", "istd4", "res4"],
+           domain="com.microsoft", epsilon=1e-6)
+    g.node("Add", ["y4", "istd4"], ["z4"])
+    g.io(["x", "r"], ["y0", "y1", "res", "y2", "mean", "y3", "res3", "z4", "res4"])
     s = session(g)
     assert s.claimed(0) and s.claimed(1) and not s.claimed(2)
+    assert s.claimed(3) and not s.claimed(4)
 
 
 @pytest.mark.parametrize("dtype,attrs,out_dtype,claimed", [
@@ -349,6 +360,17 @@ def test_decoder_graph_with_argmax_fully_claimed():
     parts = session(g).partitions()
     assert len(parts) == 1 and len(parts[0]) == g.n_nodes
     assert g.n_nodes == 1 + cfg.layers * 13 + 3
+
+
+def test_decoder_graph_with_declared_norm_stats_fully_claimed():
+    """Declared-but-unread mean / inv_std_var outputs of every SkipSimplifiedLayerNorm
+    keep the decoder one fused node (rust/src/ops/norm.rs:586-594)."""
+    cfg = dec.DecoderConfig(layers=3, hidden=256, heads=4, kv_heads=2, head_dim=64, inter=512,
+                            vocab=1000, max_pos=256)
+    w = dec.make_weights(cfg, seed=0)
+    g = dec.build_graph(cfg, w, cap=64, norm_stats=True)
+    parts = session(g).partitions()
+    assert len(parts) == 1 and len(parts[0]) == g.n_nodes
 
 
 def test_decoder_graph_fully_claimed_as_one_fused_node():
@@ -601,4 +623,44 @@ def test_paged_attention_claim_forms(dtype, d, attrs, claimed):
     g.node("PagedAttention", ["q", "k", "v", "kc", "vc", "cum", "past", "bt"], ["o"],
            domain="com.microsoft", num_heads=H, kv_num_heads=KV, **attrs)
     g.io(["q", "k", "v", "kc", "vc", "cum", "past", "bt"], ["o"])
+    assert session(g).claimed(0) is claimed
+
+
+@pytest.mark.parametrize("domain,xshape,pos,cos_shape,attrs,claimed", [
+    ("com.microsoft", [2, 7, 256], ("pos", I64, [2, 7]), [64, 32], dict(num_heads=4), True),
+    # partial rotary: a cache narrower than head_size / 2, the tail keeps its values
+    ("com.microsoft", [2, 7, 256], ("pos", I64, [2, 7]), [64, 16], dict(num_heads=4), True),
+    ("com.microsoft", [2, 7, 256], ("pos", I64, [1]), [64, 16], dict(num_heads=4), True),
+    ("", [2, 4, 7, 64], ("pos", I64, [2, 7]), [64, 8], {}, True),
+    ("", [2, 7, 256], None, [2, 7, 32], dict(num_heads=4), True),   # per-token cache
+    ("", [2, 7, 256], ("pos", I64, [1]), [64, 32], dict(num_heads=4), False),  # [1]: ms only
+    ("com.microsoft", [2, 7, 256], None, [2, 7, 32], dict(num_heads=4), False),  # ms needs ids
+    ("com.microsoft", [2, 7, 256], ("pos", I32, [2, 7]), [64, 32], dict(num_heads=4), False),
+    ("com.microsoft", [2, 7, 256], ("pos", I64, [2, 7]), [64, 64], dict(num_heads=4), False),
+    ("com.microsoft", [2, 7, 256], ("pos", I64, [2, 7]), [64, 16],
+     dict(num_heads=0, rotary_embedding_dim=32), False),  # head size not inferable
+    ("com.microsoft", [2, 7, 256], ("pos", I64, [2, 7]), [64, 32], dict(num_heads=0), True),
+])
+def test_rotary_claim_predicate(domain, xshape, pos, cos_shape, attrs, claimed):
+    """The RotaryEmbedding claim contract of rust/src/ops/attention.rs:2158-2264: the
+    two input orders, position_ids [B,S] (or [1] in com.microsoft) or absent with a
+    per-token cache, the head size inferred from the cache when num_heads = 0, and a
+    cache narrower than head_size / 2 (partial rotary). position_ids must be int64,
+    the type both ONNX schemas give it."""
+    g = hx.Graph()
+    g.value("x", F16, xshape)
+    g.value("y", F16, xshape)
+    g.value("cos", F16, cos_shape)
+    g.value("sin", F16, cos_shape)
+    ins = ["x", "", "cos", "sin"] if domain else ["x", "cos", "sin"]
+    io_in = ["x", "cos", "sin"]
+    if pos is not None:
+        g.value(*pos)
+        io_in.append(pos[0])
+        if domain:
+            ins[1] = pos[0]
+        else:
+            ins.append(pos[0])
+    g.node("RotaryEmbedding", ins, ["y"], domain=domain, **attrs)
+    g.io(io_in, ["y"])
     assert session(g).claimed(0) is claimed

@@ -125,3 +125,49 @@ def test_decode_program_full_size_greedy_strict(ortmi, oracle, dec, dprog):
     del wc
     print(f"oracle: {time.time() - t0:.1f} s", flush=True)
     _assert_greedy_strict(list(zip(gpu, ref, toks)), "decode program 512+128")
+
+
+def test_decode_program_abort_word(ortmi, dec, dprog):
+    """A launch aborted before it starts (its launch index + 1 written to the
+    workspace's abort word by the host) reads and writes nothing: status stays -1,
+    the KV caches, logits and next id are bit-identical to before, and every
+    workgroup exits normally. The next launch is not affected: it completes with
+    status 0 and gives the bit-identical results of the same step run again from the
+    same cache."""
+    import torch
+
+    cfg = dec.DecoderConfig(layers=2, hidden=768, heads=6, kv_heads=2, head_dim=128, inter=512,
+                            vocab=4096, max_pos=512)
+    w = dec.make_weights(cfg, seed=61)
+    runner = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
+    prog = dprog.DecodeProgram(cfg, w, runner.kv, 64)
+    prompt = np.random.default_rng(62).integers(0, cfg.vocab, size=17)
+    runner.reset()
+    runner.prefill(prompt)
+    tok = runner.next_id.clone().view(1)
+    prog.total.fill_(len(prompt) + 1)
+    prog.logits.fill_(float("nan"))
+    prog.next_id.fill_(-5)
+    torch.cuda.synchronize()
+    snap = [(k.clone(), v.clone()) for k, v in runner.kv]
+    prog.abort_next()
+    prog.step(token=tok, total=prog.total)
+    torch.cuda.synchronize()
+    assert int(prog.status.item()) == -1
+    assert torch.isnan(prog.logits).all() and int(prog.next_id.item()) == -5
+    for (k, v), (ks, vs) in zip(runner.kv, snap):
+        assert torch.equal(k, ks) and torch.equal(v, vs)
+    results = []
+    for _ in range(2):
+        for (k, v), (ks, vs) in zip(runner.kv, snap):
+            k.copy_(ks)
+            v.copy_(vs)
+        prog.step(token=tok, total=prog.total)
+        torch.cuda.synchronize()
+        assert int(prog.status.item()) == 0
+        results.append((prog.logits.clone(), int(prog.next_id.item()),
+                        [(k.clone(), v.clone()) for k, v in runner.kv]))
+    (l0, t0, kv0), (l1, t1, kv1) = results
+    assert torch.equal(l0, l1) and t0 == t1 == int(torch.argmax(l0.float()).item())
+    for (a, b), (c, d) in zip(kv0, kv1):
+        assert torch.equal(a, c) and torch.equal(b, d)

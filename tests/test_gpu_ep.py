@@ -292,7 +292,8 @@ def _assert_greedy_strict(rows, what):
                                               f" margin {margin:.4g} > {TIE_ULPS} ULPs")
             ties.append(i)
     print(f"{what}: {len(rows) - len(ties)} of {len(rows)} tokens equal the oracle's argmax; "
-          f"max |logit diff| {worst:.1f} fp16 ULPs of the row max", flush=True)
+          f"near ties {len(ties)} (steps {ties}); max |logit diff| {worst:.1f} fp16 ULPs of "
+          f"the row max", flush=True)
     assert worst <= TIE_ULPS, f"{what}: logits differ by {worst:.1f} ULPs of the row max"
     return ties, worst
 
@@ -470,16 +471,24 @@ def _one_node_mnb_graph(hx, rng, N=256, K=512):
     return g, (A, B, s, zp, N, K)
 
 
-def test_ep_memory_device_allocator_and_data_transfer(ortmi, hx):
-    """GetDefaultMemoryDevice reports CPU memory; CreateAllocator hands out an HBM
-    allocator only for the EP's own memory info (MI355X_HBM, a visible GPU id), whose
-    Alloc/Reserve/Free/Info work; CreateDataTransfer copies host<->device and
-    device<->device bit for bit."""
+def test_ep_memory_device_allocator_and_data_transfer(ortmi, hx, monkeypatch):
+    """GetDefaultMemoryDevice reports the HBM memory device the EP device registered
+    (GPU, AMD's vendor id, GPU 0), or CPU memory with ORTMI_EP_MEMORY=cpu;
+    CreateAllocator hands out an HBM allocator only for the EP's own memory info
+    (MI355X_HBM, a visible GPU id), whose Alloc/Reserve/Free/Info work;
+    CreateDataTransfer copies host<->device and device<->device bit for bit."""
     import torch
 
     g, _ = _one_node_mnb_graph(hx, np.random.default_rng(1))
+    monkeypatch.setenv("ORTMI_EP_MEMORY", "cpu")
+    cpu_sess = hx.Session(g)
+    assert cpu_sess.default_memory_device_is_cpu()
+    assert cpu_sess.memory_device() == (0, 0, 0)
+    cpu_sess.close()
+    monkeypatch.delenv("ORTMI_EP_MEMORY")
     sess = hx.Session(g)
-    assert sess.default_memory_device_is_cpu()
+    assert not sess.default_memory_device_is_cpu()
+    assert sess.memory_device() == (1, 0x1002, 0)
     assert sess.allocator_check("MI355X_HBM", 0, 3 << 20) is True
     assert sess.allocator_check("Cpu", 0) is None
     with pytest.raises(RuntimeError, match="GPU 4096"):
@@ -495,18 +504,25 @@ def test_ep_memory_device_allocator_and_data_transfer(ortmi, hx):
     assert torch.equal(back, src)
 
 
-def test_ep_host_memory_input_and_output(ortmi, oracle, hx):
-    """Host-memory input and output buffers (what ORT hands an EP whose default
-    memory device is the CPU): the input is staged to HBM, the result copied back
-    into the caller's host buffer, identical to the device-bound run."""
+@pytest.mark.parametrize("memory", ["hbm", "cpu"])
+def test_ep_host_memory_input_and_output(ortmi, oracle, hx, monkeypatch, memory):
+    """Host-memory input and output buffers. With the HBM memory device the harness
+    applies ORT's placement rule (the feed copied to HBM and the output produced
+    there and copied back, through the EP's data transfer); with CPU memory
+    (ORTMI_EP_MEMORY=cpu, what ORT hands an EP whose default memory device is the
+    CPU) the EP gets the host buffers and stages them itself. Either way the caller's
+    host buffer receives the result, identical to the device-bound run."""
     import torch
 
     g, (A, B, s, zp, N, K) = _one_node_mnb_graph(hx, np.random.default_rng(2))
+    monkeypatch.setenv("ORTMI_EP_MEMORY", memory)
     sess = hx.Session(g)
     x_host = torch.from_numpy(A.reshape(1, 1, K).copy())
     y_host = torch.full((1, 1, N), float("nan"), dtype=torch.float16)
     sess.bind_output("y", y_host)
     sess.run({"x": (x_host, hx.FLOAT16)})
+    # HBM: one copy in (the feed), one out (the output); CPU: the EP's own staging.
+    assert sess.copies() == (2 if memory == "hbm" else 0)
     y_dev = torch.empty((1, 1, N), dtype=torch.float16, device="cuda")
     sess.bind_output("y", y_dev)
     sess.run({"x": (x_host.cuda(), hx.FLOAT16)})
@@ -534,7 +550,7 @@ def _gqa_graph(hx, H, KV, hd, cap, cos, sin):
     return g
 
 
-def test_ep_gqa_host_kv_delta_write_back(ortmi, hx):
+def test_ep_gqa_host_kv_delta_write_back(ortmi, hx, monkeypatch):
     """A KV cache in host memory shared by past and present (the reference's
     shared-buffer contract with a CPU-memory EP): a 5-token prompt then 6 decode
     steps give outputs and cache contents identical to the same steps over device
@@ -553,6 +569,9 @@ def test_ep_gqa_host_kv_delta_write_back(ortmi, hx):
     sentinel = np.float16(-7.5)
 
     def run(on_device):
+        # Device buffers with the HBM EP; host buffers with an EP that reports CPU
+        # memory, which ORT hands the host buffers themselves.
+        monkeypatch.setenv("ORTMI_EP_MEMORY", "hbm" if on_device else "cpu")
         sess = hx.Session(_gqa_graph(hx, H, KV, hd, cap, cos, sin))
         kc = torch.full((1, KV, cap, hd), float(sentinel), dtype=torch.float16)
         vc = torch.full_like(kc, float(sentinel))
@@ -585,13 +604,15 @@ def test_ep_gqa_host_kv_delta_write_back(ortmi, hx):
     assert not (hk[:, :, :total] == float(sentinel)).all()
 
 
-def test_ep_paged_attention_host_caches_written_back(ortmi, oracle, hx):
-    """PagedAttention through the EP with its caches in host memory: the new K/V
-    rows land in the caller's cache buffers (in place, as the reference writes
-    them back, rust/src/ops/attention.rs:2728-2742), and output and caches equal
-    the oracle's over two consecutive calls."""
+def test_ep_paged_attention_host_caches_written_back(ortmi, oracle, hx, monkeypatch):
+    """PagedAttention through an EP that reports CPU memory (ORTMI_EP_MEMORY=cpu),
+    with its caches in host memory: the new K/V rows land in the caller's cache
+    buffers (in place, as the reference writes them back,
+    rust/src/ops/attention.rs:2728-2742), and output and caches equal the oracle's
+    over two consecutive calls."""
     import torch
 
+    monkeypatch.setenv("ORTMI_EP_MEMORY", "cpu")
     rng = np.random.default_rng(90)
     H, KV, d, blk, batch = 8, 2, 64, 4, 3
     maxb = 6
@@ -636,28 +657,38 @@ def test_ep_paged_attention_host_caches_written_back(ortmi, oracle, hx):
         past = past + new
 
 
-def test_ep_decoder_config4_greedy_tokens_strict(ortmi, oracle, dec):
+def test_ep_decoder_config4_greedy_tokens_strict(ortmi, oracle, dec, monkeypatch):
     """The benchmarked int4 decoder end to end: 28 layers, vocab 151936, a 512-token
     prompt then 128 greedy decode steps (129 tokens), every token checked against
     the oracle teacher-forced: the oracle runs the prompt, then the GPU's 128 fed-back
     tokens in one causal pass, and each GPU token must be the oracle's argmax, or the
     oracle's margin over it must be within TIE_ULPS fp16 ULPs of the row's max |logit|
-    (each such step is printed). No agreement quota."""
+    (each such step is printed, and their count). No agreement quota.
+    Fed the way a stock ONNX Runtime feeds an EP whose memory device is HBM: input
+    ids, seqlens_k and total_sequence_length are host tensors that the harness copies
+    to HBM through the EP's data transfer each step (the KV cache and logits bound to
+    device buffers), and every one-token step must run as the decode program
+    (ORTMI_EP_PROGRAM=require)."""
     import time
 
+    monkeypatch.setenv("ORTMI_EP_PROGRAM", "require")
     cfg = dec.DecoderConfig()
     w = dec.make_weights(cfg, seed=4)
     P, steps = 512, 128
-    runner = dec.DecoderRunner(cfg, w, cap=P + steps, max_prompt=P)
+    runner = dec.DecoderRunner(cfg, w, cap=P + steps, max_prompt=P, host_feeds=True)
+    assert runner.session.memory_device() == (1, 0x1002, 0)
     prompt = np.random.default_rng(44).integers(0, cfg.vocab, size=P)
     runner.reset()
     runner.prefill(prompt)
     gpu = [host(runner.logits[0, P - 1])]
     toks = [int(runner.next_id.item())]
+    copies0 = runner.session.copies()
     for _ in range(steps):
         runner.decode_step()
         gpu.append(host(runner.logits[0, 0]))
         toks.append(int(runner.next_id.item()))
+    # One data-transfer call per step: the host feeds (ids, seqlens_k, total) to HBM.
+    assert runner.session.copies() - copies0 == steps
     print(f"GPU tokens {toks[:8]} ... ({len(toks)})", flush=True)
     t0 = time.time()
     wc = oracle.dequant_cache(w, cfg)
@@ -708,7 +739,7 @@ def test_ep_decode_program_matches_op_path(ortmi, oracle, dec, monkeypatch):
     _assert_greedy_strict(rows, "decode program through the EP")
 
 
-def test_ep_gqa_sliding_window_cache(ortmi, oracle, hx):
+def test_ep_gqa_sliding_window_cache(ortmi, oracle, hx, monkeypatch):
     """GroupQueryAttention with sliding_window_cache = 1 through the EP: a 5-token
     prompt, a 3-token chunk and single tokens into a capacity-6, window-4 cache
     that present compacts in place, each step against oracle.gqa_sliding on the
@@ -726,6 +757,7 @@ def test_ep_gqa_sliding_window_cache(ortmi, oracle, hx):
              for S in steps]
 
     def run(on_device, check):
+        monkeypatch.setenv("ORTMI_EP_MEMORY", "hbm" if on_device else "cpu")
         g = hx.Graph()
         g.value("q", hx.FLOAT16, [1, -1, H * hd])
         g.value("k", hx.FLOAT16, [1, -1, KV * hd])
@@ -780,3 +812,59 @@ def test_ep_gqa_sliding_window_cache(ortmi, oracle, hx):
     for a, b in zip(host_outs, dev_outs):
         assert torch.equal(a, b)
     assert torch.equal(hk, dk) and torch.equal(hv, dv)
+
+
+def test_ep_decode_program_abort_falls_back_to_op_path(ortmi, dec, monkeypatch):
+    """A one-token step the decode program does not complete runs op by op: the
+    program's third launch is aborted before it starts (ORTMI_EP_PROGRAM_ABORT=3,
+    through the workspace's abort word), and the run still returns that step's
+    tokens, equal to an unaborted run's. With ORTMI_EP_PROGRAM=require the same
+    abort is an error naming the status."""
+    cfg = _small_cfg(dec, 128)
+    w = dec.make_weights(cfg, seed=71)
+    prompt = np.random.default_rng(72).integers(0, cfg.vocab, size=11)
+
+    def run(abort, mode):
+        monkeypatch.setenv("ORTMI_EP_PROGRAM", mode)
+        if abort:
+            monkeypatch.setenv("ORTMI_EP_PROGRAM_ABORT", str(abort))
+        else:
+            monkeypatch.delenv("ORTMI_EP_PROGRAM_ABORT", raising=False)
+        r = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
+        r.prefill(prompt)
+        toks, logits = [int(r.next_id.item())], []
+        for _ in range(6):
+            r.decode_step()
+            logits.append(host(r.logits[0, :1])[0])
+            toks.append(int(r.next_id.item()))
+        r.session.close()
+        return toks, logits
+
+    base_toks, base_logits = run(0, "1")
+    toks, logits = run(3, "1")
+    assert toks == base_toks
+    for i, (a, b) in enumerate(zip(logits, base_logits)):
+        err = float(np.abs(a - b).max())
+        if i < 2:  # before the abort: the same program launches, bit for bit
+            assert err == 0.0, f"step {i}: {err}"
+        else:      # the op path's step (and its K/V row) from then on: fp16 tolerance
+            assert err <= 2.0 ** -7 * max(1.0, float(np.abs(b).max())), f"step {i}: {err}"
+    with pytest.raises(RuntimeError, match="decode program failed"):
+        run(3, "require")
+
+
+def test_ep_decoder_with_declared_norm_stats(ortmi, oracle, dec, monkeypatch):
+    """A decoder whose SkipSimplifiedLayerNormalization nodes declare their mean and
+    inv_std_var outputs, read by nothing (the transformers.js / Mobius export form,
+    claimed as rust/src/ops/norm.rs:586-594 claims it): the graph stays one fused node,
+    its one-token steps run as the decode program (ORTMI_EP_PROGRAM=require), and the
+    greedy tokens pass the strict teacher-forced check against the oracle."""
+    monkeypatch.setenv("ORTMI_EP_PROGRAM", "require")
+    cfg = _small_cfg(dec, 128)
+    w = dec.make_weights(cfg, seed=81)
+    runner = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32, norm_stats=True)
+    assert len(runner.session.partitions()) == 1
+    assert all(runner.session.claimed(i) for i in range(runner.graph.n_nodes))
+    prompt = np.random.default_rng(82).integers(0, cfg.vocab, size=15).tolist()
+    rows = _teacher_forced_check(oracle, runner, cfg, w, prompt, steps=8)
+    _assert_greedy_strict(rows, "decoder with declared norm stats")

@@ -139,3 +139,41 @@ def test_ep_rotary_embedding_node(ortmi, oracle, hx, domain, layout, interleaved
     got = host(y)
     assert (np.abs(got - want) <= ulp16(want)).all(), \
         f"max diff {np.abs(got - want).max():.3e}"
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("domain", ["com.microsoft", ""])
+def test_ep_rotary_embedding_node_partial_dtypes(ortmi, oracle, hx, dt, domain):
+    """A RotaryEmbedding node in both domains with partial rotary (a cos/sin cache of
+    width 16 for head size 64: dims [0, 32) rotate, the tail passes through bit for
+    bit) in fp16, bf16 and fp32, on device tensors, against the oracle on the same
+    rounded inputs."""
+    import torch
+    from test_gpu_ops import rotary_case
+
+    rng = np.random.default_rng(300 + 7 * ("f16", "bf16", "f32").index(dt) + len(domain))
+    B, S, NH, hd, half, max_pos = 2, 5, 4, 64, 16, 64
+    shape = [B, S, NH * hd]
+    (dx, dc, ds), (x, c, s_), mode, tol = rotary_case(dt, rng, tuple(shape), max_pos, hd, half)
+    et = {"f16": hx.FLOAT16, "bf16": hx.BFLOAT16, "f32": hx.FLOAT}[dt]
+    pos = rng.integers(0, max_pos, size=(B, S)).astype(np.int64)
+    g = hx.Graph()
+    g.value("x", et, shape)
+    g.value("pos", hx.INT64, [B, S])
+    g.value("cos", et, [max_pos, half])
+    g.value("sin", et, [max_pos, half])
+    g.value("y", et, shape)
+    ins = ["x", "pos", "cos", "sin"] if domain else ["x", "cos", "sin", "pos"]
+    g.node("RotaryEmbedding", ins, ["y"], domain=domain, num_heads=NH, interleaved=0)
+    g.io(["x", "pos", "cos", "sin"], ["y"])
+    sess = hx.Session(g)
+    assert sess.partitions() == [[0]]
+    y = torch.empty(shape, dtype=dx.dtype, device="cuda")
+    sess.bind_output("y", y)
+    sess.run({"x": (dx, et), "pos": (dev(pos), hx.INT64), "cos": (dc, et), "sin": (ds, et)})
+    torch.cuda.synchronize()
+    want = oracle.rotary(x, pos, c, s_, round16=mode, num_heads=NH)
+    got = host(y)
+    assert (np.abs(got - want) <= tol(want)).all(), f"max diff {np.abs(got - want).max():.3e}"
+    np.testing.assert_array_equal(got.reshape(B, S, NH, hd)[..., 2 * half:],
+                                  x.reshape(B, S, NH, hd)[..., 2 * half:])

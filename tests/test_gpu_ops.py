@@ -263,11 +263,13 @@ def _check_gemm_rows(oracle, got_rows, A_rows, B, s, zp, N, K, block, what):
     (512, 2048, 1536),   # the decoder prefill's merged QKV
 ])
 def test_mnb_gemm_config2_shape(ortmi, oracle, M, N, K):
-    """Prefill GEMM shapes at full size, fp16, block 32, zero points U{0..15}."""
+    """Prefill GEMM shapes at full size, fp16, block 32, zero points U{0..15}. The
+    prefill GEMM config (512 x 4096 x 4096) is checked on all 512 rows; the two
+    decoder shapes on a sample of rows, which keeps the CPU side short."""
     rng = np.random.default_rng(M + N + K)
     A, B, s, zp = _mnb_inputs(rng, M, N, K, 32, dtype=np.float16)
     got = host(ortmi.matmul_nbits(dev(A), dev(B), dev(s), dev(zp), K=K, N=N))
-    rows = np.r_[np.arange(0, M, 37), M - 1]  # a sample of rows keeps the CPU side short
+    rows = np.arange(M) if (N, K) == (4096, 4096) else np.r_[np.arange(0, M, 37), M - 1]
     _check_gemm_rows(oracle, got[rows], A[rows], B, s, zp, N, K, 32, f"gemm {M}x{N}x{K}")
 
 
@@ -1008,6 +1010,56 @@ def test_rotary_embedding(ortmi, oracle, form, interleaved):
     assert y.dtype == torch.float16
 
 
+def _ulp_bf16(x):
+    x = np.abs(np.asarray(x, np.float64))
+    return 2.0 ** (np.floor(np.log2(np.maximum(x, 2.0 ** -126))) - 7)
+
+
+def rotary_case(dt, rng, shape, max_pos, hd, half):
+    """Inputs of one RotaryEmbedding case in dtype `dt` ("f16", "bf16", "f32"): the
+    device tensors (x, cos, sin), their float32 values (what the oracle rotates),
+    the oracle's rounding mode and a tolerance function of the exact result."""
+    import torch
+
+    tdt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[dt]
+    c, s_ = refs.rotary_caches(max_pos, 2 * half, 10000.0)
+    xs = torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(tdt)
+    cs, sn = torch.from_numpy(c.astype(np.float32)).to(tdt), torch.from_numpy(s_.astype(np.float32)).to(tdt)
+    vals = [t.float().numpy() for t in (xs, cs, sn)]
+    mode = {"f16": 1, "bf16": 2, "f32": 0}[dt]
+    tol = {"f16": lambda r: ulp16(r), "bf16": _ulp_bf16,
+           "f32": lambda r: 1e-6 + 1e-6 * np.abs(r)}[dt]
+    return [t.cuda() for t in (xs, cs, sn)], vals, mode, tol
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("half,interleaved,layout", [
+    (16, 0, "bsnd"), (16, 1, "bsnd"), (24, 0, "bnsd"), (32, 1, "bnsd"), (32, 0, "bsnd")])
+def test_rotary_embedding_dtypes_partial(ortmi, oracle, dt, half, interleaved, layout):
+    """Standalone RotaryEmbedding in fp16, bf16 and fp32, with partial rotary (a
+    cos/sin cache narrower than head_size / 2: only dims [0, 2 * half) rotate, the
+    tail keeps its values bit for bit, rust/src/ops/attention.rs:1234-1282) and
+    full rotary, both pair layouts and both tensor layouts, against the oracle on
+    the same rounded inputs (one rounding of the rotated value to the dtype)."""
+    rng = np.random.default_rng(half * 10 + interleaved + 3 * ("f16", "bf16", "f32").index(dt))
+    B, S, NH, hd, max_pos = 2, 9, 4, 64, 96
+    shape = (B, S, NH * hd) if layout == "bsnd" else (B, NH, S, hd)
+    (dx, dc, ds), (x, c, s_), mode, tol = rotary_case(dt, rng, shape, max_pos, hd, half)
+    pos = rng.integers(0, max_pos, size=(B, S)).astype(np.int64)
+    y = ortmi.rotary_embedding(dx, dev(pos), dc, ds, interleaved=interleaved,
+                               num_heads=NH if layout == "bsnd" else 0)
+    ref = oracle.rotary(x, pos, c, s_, interleaved=bool(interleaved), round16=mode,
+                        layout=layout, num_heads=NH if layout == "bsnd" else None)
+    got = host(y)
+    assert y.dtype == dx.dtype
+    assert (np.abs(got - ref) <= tol(ref)).all(), f"max diff {np.abs(got - ref).max():.3e}"
+    if layout == "bsnd":
+        g4, x4 = got.reshape(B, S, NH, hd), x.reshape(B, S, NH, hd)
+    else:
+        g4, x4 = got, x
+    np.testing.assert_array_equal(g4[..., 2 * half:], x4[..., 2 * half:])
+
+
 # ------------------------------------------------------------ (Skip)SimplifiedLN --
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float16])
@@ -1029,6 +1081,33 @@ def test_rms_norm(ortmi, oracle, dtype, skip):
         assert_f16_close(host(y), ry, what="rms fp16")
     else:
         assert np.abs(host(y) - ry).max() <= 6e-5
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_skip_rms_norm_bias(ortmi, oracle, dtype):
+    """SkipSimplifiedLayerNormalization with its optional bias input ([D], the same for
+    every row): the residual output is x + skip + bias rounded once to the dtype
+    (bit-exact against the oracle), the normalised output within the dtype's bar; and
+    a zero bias gives exactly the bias-free results."""
+    rng = np.random.default_rng(31 + (dtype == np.float16))
+    rows, D = 7, 1536
+    x = rng.standard_normal((rows, D)).astype(dtype)
+    sk = rng.standard_normal((rows, D)).astype(dtype)
+    b = rng.standard_normal(D).astype(dtype)
+    g = rng.standard_normal(D).astype(dtype)
+    r16 = dtype == np.float16
+    y, r = ortmi.skip_simplified_layer_norm(dev(x), dev(sk), dev(g), dev(b), epsilon=1e-6)
+    ry, rr = oracle.rms_norm(x, g, 1e-6, skip=sk, bias=b, round16=r16)
+    np.testing.assert_array_equal(host(r), rr)
+    if r16:
+        assert_f16_close(host(y), ry, what="skip rms + bias fp16")
+    else:
+        assert np.abs(host(y) - ry).max() <= 6e-5
+    y0, r0 = ortmi.skip_simplified_layer_norm(dev(x), dev(sk), dev(g), dev(np.zeros_like(b)),
+                                              epsilon=1e-6)
+    y1, r1 = ortmi.skip_simplified_layer_norm(dev(x), dev(sk), dev(g), epsilon=1e-6)
+    np.testing.assert_array_equal(host(r0), host(r1))
+    np.testing.assert_array_equal(host(y0), host(y1))
 
 
 # ------------------------------------------------------------------------- glue --
@@ -1190,3 +1269,58 @@ def test_paged_generic_latent_and_offset(ortmi, oracle):
                        rope=True, new_max=6, latent=True, v_head_size=96)
     _run_paged_generic(ortmi, oracle, "f16", 4, 2, 64, nb=16, blk=4, batch=2, seed=521,
                        rope=True, interleaved=1, new_max=5, rotary_offset=4)
+
+
+@pytest.mark.parametrize("path", ["fused", "generic"])
+def test_paged_attention_malformed_control_tensors(ortmi, oracle, path):
+    """Malformed control tensors stay in bounds and read as clamped: a negative first
+    cum_seqlens entry is the sequence start 0 (outputs and caches bit-identical to
+    cum_seqlens[0] = 0); a past length of 2^31 - 1 reads as max_context (identical to
+    past = max_context: every key from the cache, none beyond max_context); unsorted
+    cum_seqlens with negative and huge past lengths and out-of-range block ids
+    complete, and a well-formed call on the same buffers afterwards equals the
+    oracle. path: fp16 head 128 (the tile and single-token kernels) or fp32 head 64
+    (the generic kernel)."""
+    import torch
+
+    dtype, d = (np.float16, 128) if path == "fused" else (np.float32, 64)
+    rng = np.random.default_rng(5 if path == "fused" else 6)
+    H, KV, blk, batch, maxb = 4, 2, 16, 3, 4
+    nb = batch * maxb
+    max_ctx = maxb * blk
+    T = 6
+    kc0 = rng.standard_normal((nb, blk, KV, d)).astype(dtype)
+    vc0 = rng.standard_normal((nb, blk, KV, d)).astype(dtype)
+    bt = rng.permutation(nb).astype(np.int32).reshape(batch, maxb)
+    q, k, v = (rng.standard_normal((T, n * d)).astype(dtype) for n in (H, KV, KV))
+    i32 = lambda a: dev(np.asarray(a, np.int32))  # noqa: E731
+
+    def call(cum, past, table=bt):
+        kc, vc = dev(kc0), dev(vc0)
+        o = ortmi.paged_attention(dev(q), dev(k), dev(v), kc, vc, i32(cum), i32(past), i32(table),
+                                  num_heads=H, kv_num_heads=KV)
+        torch.cuda.synchronize()
+        return host(o), host(kc), host(vc)
+
+    def same(a, b):
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(x, y)
+
+    ok = call([0, 3, 4, 6], [5, 20, 0])
+    same(call([-6, 3, 4, 6], [5, 20, 0]), ok)
+    same(call([0, 3, 4, 6], [5, 2 ** 31 - 1, 0]), call([0, 3, 4, 6], [5, max_ctx, 0]))
+    bad_bt = bt.copy()
+    bad_bt[0, 1], bad_bt[2, 0] = -1, nb + 5
+    call([0, 5, 2, 6], [-3, 5, 99999], bad_bt)
+    call([3, -2 ** 31, 2 ** 31 - 1, 1], [2 ** 31 - 1, -1, 7], bad_bt)
+    got = call([0, 3, 4, 6], [5, 20, 0])
+    same(got, ok)
+    ro, rk, rv = oracle.paged_attention(q, k, v, kc0.astype(np.float32), vc0.astype(np.float32),
+                                        np.array([0, 3, 4, 6], np.int32),
+                                        np.array([5, 20, 0], np.int32), bt, H, KV)
+    if dtype == np.float16:
+        assert_f16_close(got[0], ro, what="paged after malformed calls")
+        np.testing.assert_array_equal(got[1], oracle.round_f16(rk))
+    else:
+        assert np.abs(got[0] - ro).max() <= 6e-5
+        np.testing.assert_array_equal(got[1], rk)
