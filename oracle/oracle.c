@@ -512,10 +512,13 @@ void orc_rms_norm(const float* x, const float* skip, const float* bias, const fl
         const float* xi = x + i * D;
         double ss = 0.0;
         for (int64_t d = 0; d < D; ++d) {
-            double t = (double)xi[d];
-            if (skip) t += (double)skip[i * D + d];
-            if (bias) t += (double)bias[d];
-            r[d] = r16((float)t, round16 && (skip || bias));
+            /* The residual sum in fp32, left to right (input + skip, then + bias), as
+             * ORT's CPU SkipLayerNorm kernels form input_skip_bias_sum; the sum of
+             * two values is one correctly rounded fp32 add either way. */
+            float t = xi[d];
+            if (skip) t = (float)((double)t + (double)skip[i * D + d]);
+            if (bias) t = (float)((double)t + (double)bias[d]);
+            r[d] = r16(t, round16 && (skip || bias));
             ss += (double)r[d] * (double)r[d];
         }
         double inv = 1.0 / sqrt(ss / (double)D + (double)eps);

@@ -607,8 +607,7 @@ def test_rms_norm_closed_form_and_numpy(oracle):
     np.testing.assert_array_equal(r16, (x + skip).astype(np.float16).astype(np.float32))
     np.testing.assert_allclose(y16, refs.rms_norm_ref(r16, gamma), rtol=1e-5, atol=1e-6)
     # The skip variant's optional bias [D] joins every row's residual sum (ORT's
-    # input_skip_bias_sum); a zero bias changes nothing, a bias equal to -skip of row 0
-    # leaves that row's residual equal to x exactly.
+    # input_skip_bias_sum) and a zero bias changes nothing.
     bias = rng.standard_normal(D).astype(np.float32)
     yb, rb = oracle.rms_norm(x, gamma, 1e-6, skip=skip, bias=bias)
     np.testing.assert_allclose(rb, x + skip + bias[None, :], rtol=1e-6, atol=1e-6)
@@ -616,8 +615,13 @@ def test_rms_norm_closed_form_and_numpy(oracle):
     y0, r0 = oracle.rms_norm(x, gamma, 1e-6, skip=skip, bias=np.zeros(D, np.float32))
     np.testing.assert_array_equal(r0, r)
     np.testing.assert_array_equal(y0, y)
-    _, rn = oracle.rms_norm(x, gamma, 1e-6, skip=skip, bias=-skip[0])
-    np.testing.assert_array_equal(rn[0], x[0])
+    # The sum is formed in fp32 left to right, as ORT's CPU kernel forms it: 1 + 2^-24
+    # rounds (to even) to 1, and 1 + 2^-24 again stays 1, where a single rounding of
+    # the exact sum 1 + 2^-23 would keep it.
+    one = np.ones((1, D), np.float32)
+    tiny = np.full((1, D), 2.0 ** -24, np.float32)
+    _, rt = oracle.rms_norm(one, gamma, 1e-6, skip=tiny, bias=tiny[0])
+    np.testing.assert_array_equal(rt, one)
 
 
 def test_decoder_forward_cached_weights_match_per_row_form(oracle):
