@@ -2,6 +2,7 @@
 
     python onnxruntime-mlx_amd/build.py            # everything
     python onnxruntime-mlx_amd/build.py kernels    # libortmi_kernels.so only
+    python onnxruntime-mlx_amd/build.py stamps     # the decode program with phase stamps
 
 Outputs go to onnxruntime-mlx_amd/lib/. hipcc cross-compiles for gfx950 without a
 GPU, so this runs on any host with ROCm installed.
@@ -92,12 +93,30 @@ def build_harness() -> str:
     return out
 
 
+def build_stamps() -> str:
+    """The decode program with per-phase timestamps compiled in (-DORTMI_DPROG_STAMPS),
+    as a library of its own for dprog_stamps.py; the product libraries never have them."""
+    os.makedirs(OBJ, exist_ok=True)
+    objs = []
+    for src in ("runtime.hip", "decode_step.hip"):
+        obj = os.path.join(OBJ, "stamps_" + src + ".o")
+        _run([HIPCC, *HIP_FLAGS, "-DORTMI_DPROG_STAMPS", "-c", os.path.join(CSRC, src), "-o", obj])
+        objs.append(obj)
+    out = os.path.join(LIB, "libortmi_dprog_stamps.so")
+    tmp = out + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs,
+          "-Wl,-soname,libortmi_dprog_stamps.so"])
+    os.replace(tmp, out)
+    return out
+
+
 def build_all(jobs: int = 4) -> list[str]:
     outs = [build_kernels(jobs)]
     ep = build_ep(jobs)
     if ep:
         outs.append(ep)
     outs.append(build_harness())
+    outs.append(build_stamps())
     return outs
 
 
@@ -105,6 +124,8 @@ if __name__ == "__main__":
     what = sys.argv[1] if len(sys.argv) > 1 else "all"
     if what == "kernels":
         print(build_kernels())
+    elif what == "stamps":
+        print(build_stamps())
     else:
         for p in build_all():
             print(p)

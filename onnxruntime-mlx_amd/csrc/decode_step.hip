@@ -53,6 +53,29 @@
 namespace ortmi {
 namespace dprog {
 
+// Per-phase timestamps for profiling, compiled in only with -DORTMI_DPROG_STAMPS
+// (onnxruntime-mlx_amd/dprog_stamps.py builds that variant): thread 0 of each
+// workgroup writes the 100 MHz realtime clock to slot k of its row, read back with
+// ortmi_decoder_decode_step_stamps. Slots: 0 start; per layer l at 1 + 8 l:
+// projection workgroups +0 A input ready, +1 A output stored, +2 C input ready,
+// +3 C stored, +4 D input ready, +5 D stored, +6 E input ready, +7 E stored;
+// attention workgroups +2 q/k/v ready, +4 keys attended, +5 merged in the
+// workgroup, +6 partials in hand, +3 output stored; 1 + 8 L lm_head input ready,
+// 2 + 8 L lm_head done.
+constexpr int kStampSlots = 256;
+#ifdef ORTMI_DPROG_STAMPS
+__device__ unsigned long long g_stamps[1024 * kStampSlots];
+#define DPROG_STAMP(k)                                                                \
+    do {                                                                              \
+        if (threadIdx.x == 0 && (k) < kStampSlots)                                    \
+            g_stamps[blockIdx.x * kStampSlots + (k)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define DPROG_STAMP(k) \
+    do {               \
+    } while (0)
+#endif
+
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kSC1 = 16;               // buffer cache policy: device-coherent (sc1)
@@ -577,6 +600,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
     if (s_aborted) return;  // aborted before it started: nothing is read or written
     const Flow f{p.ctl, p.status, s_tag, s_launch};
     const uint32_t tag = f.tag;
+    DPROG_STAMP(0);
 
     int64_t id = *p.input_id;  // negative ids count from the end
     if (id < 0) id += p.embed_rows;
@@ -635,6 +659,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                                      (uint32_t)((H + KV + kvh) * HD + li16 * 8) * 4u};
             uint4 qkv3[3];
             const bool ok = poll_units<3>(rsrc(f_qkv, (uint32_t)NQ * 4u), off, 7u, f, qkv3);
+            DPROG_STAMP(1 + l * 8 + 2);
             float q[8], kn[8], vn[8];
             {
                 const half_t* qh = reinterpret_cast<const half_t*>(&qkv3[0]);
@@ -758,6 +783,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                     ringv[r] = ld128<kCachePolicyNT>(rv, off2);
                 }
             }
+            DPROG_STAMP(1 + l * 8 + 4);
             // Merge the 4 lane groups of the wave (same dims, other keys), then the
             // waves through LDS.
 #pragma unroll
@@ -786,6 +812,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 for (int e = 0; e < 8; ++e) sO[wave * HD + li16 * 8 + e] = o[e];
             }
             if (!all_ok(ok, &s_fail)) return;
+            DPROG_STAMP(1 + l * 8 + 5);
             // The split's state over its 8 waves: o_d (d = tid), M, L.
             float M = -INFINITY, L = 0.f, acc = 0.f;
             if (tid < HD + 2) {
@@ -855,6 +882,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                     }
                 }
                 if (!all_ok(mok, &s_fail)) return;
+                DPROG_STAMP(1 + l * 8 + 6);
                 if (tid < HD) {
                     float Mt = M;
                     for (int j = 1; j < NS; ++j) Mt = fmaxf(Mt, s_pm[j]);
@@ -876,6 +904,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             // this wave's output stores have completed (requests queued behind a
             // prefetch of the K/V rows would reach the consumers later).
             __builtin_amdgcn_s_waitcnt(0);
+            DPROG_STAMP(1 + l * 8 + 3);
             if (l + 1 < p.L) kv_fetch(s_layers[l + 1]);
             if (!all_ok(mok, &s_fail)) return;
         }
@@ -949,6 +978,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             if (!norm_poll(in_dout, p.embed + id * D, l > 0, static_cast<const half_t*>(ly.ln1_gamma),
                            ly.ln1_epsilon, D, sR, sA0, sSum0, sRed, f, &s_fail))
                 return;
+            DPROG_STAMP(1 + l * 8);
             {
                 __builtin_amdgcn_s_waitcnt(0);
                 const float v = group_sum<16>(row_dot<16, CPLD>(wreg, sq, sA0, sSum0, CD, li16));
@@ -956,12 +986,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 __syncthreads();
                 if (tid < 4 * gq && 4 * wg * gq + tid < NQ)
                     put(rsrc(f_qkv, (uint32_t)NQ * 4), 4 * wg * gq + tid, s_out[tid], tag);
+                DPROG_STAMP(1 + l * 8 + 1);
                 wait_lds();
                 gu_fetch();
             }
 
             // Phase C: o_proj GEMV over the attention output.
             if (!stage_poll(f_att, HO, sA1, sSum1, f, &s_fail)) return;
+            DPROG_STAMP(1 + l * 8 + 2);
             {
                 __builtin_amdgcn_s_waitcnt(0);
                 const float v = group_sum<16>(row_dot<16, CPLD>(wreg + kLo * 64, so, sA1, sSum1, CO, li16));
@@ -969,6 +1001,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 __syncthreads();
                 if (tid < 4 * go && 4 * wg * go + tid < D)
                     put(rsrc(f_y, (uint32_t)D * 4), 4 * wg * go + tid, s_out[tid], tag);
+                DPROG_STAMP(1 + l * 8 + 3);
                 wait_lds();
                 down_fetch();
             }
@@ -977,6 +1010,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             if (!norm_poll(f_y, nullptr, true, static_cast<const half_t*>(ly.ln2_gamma), ly.ln2_epsilon,
                            D, sR, sA0, sSum0, sRed, f, &s_fail))
                 return;
+            DPROG_STAMP(1 + l * 8 + 4);
             if (l + 1 == p.L && wg == 0) {
                 // The final norm's residual, for the attention workgroups.
                 for (int u = tid; u < D / 8; u += kThreads) {
@@ -1017,12 +1051,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 __syncthreads();
                 if (tid < 2 * ggu && 2 * wg * ggu + tid < I)
                     put(ra, 2 * wg * ggu + tid, s_out[tid], tag);
+                DPROG_STAMP(1 + l * 8 + 5);
                 wait_lds();
                 if (l + 1 < p.L) qkv_fetch(s_layers[l + 1]);
             }
 
             // Phase E: down GEMV (K = I).
             if (!stage_poll(f_act, I, sA1, sSum1, f, &s_fail)) return;
+            DPROG_STAMP(1 + l * 8 + 6);
             {
                 __builtin_amdgcn_s_waitcnt(0);
                 const float v =
@@ -1031,6 +1067,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 __syncthreads();
                 if (tid < gd && wg * gd + tid < D)
                     put(rsrc(f_dout, (uint32_t)D * 4), wg * gd + tid, s_out[tid], tag);
+                DPROG_STAMP(1 + l * 8 + 7);
                 wait_lds();
                 if (l + 1 < p.L) o_fetch(s_layers[l + 1]);
             }
@@ -1052,6 +1089,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
     if (!norm_poll(prev_dout, nullptr, true, p.final_gamma, p.final_eps, D, sR, sA0, sSum0, sRed,
                    f, &s_fail))
         return;
+    DPROG_STAMP(1 + p.L * 8);
     float best = -INFINITY;
     int bi = -1;
     for (int k = 0;; k += kRing) {
@@ -1079,6 +1117,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         }
         if (done) break;
     }
+    DPROG_STAMP(2 + p.L * 8);
     // Reduce (value, index) over the workgroup, publish one tagged record.
     arg_wave(best, bi);
     if (lane == 0) {
@@ -1173,6 +1212,18 @@ int program_grid() {
 }
 
 }  // namespace
+
+#ifdef ORTMI_DPROG_STAMPS
+// The stamps of the last launch: `rows` workgroup rows of kStampSlots 64-bit clock
+// values (100 MHz), copied to host memory after the device has finished.
+extern "C" int ortmi_decoder_decode_step_stamps(unsigned long long* host, int rows) {
+    if (!host || rows < 1 || rows > 1024) return fail(ORTMI_E_INVALID, "stamps: bad rows");
+    const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(dprog::g_stamps),
+                                             (size_t)rows * dprog::kStampSlots * 8, 0,
+                                             hipMemcpyDeviceToHost);
+    return e == hipSuccess ? ORTMI_OK : fail(ORTMI_E_HIP, hipGetErrorString(e));
+}
+#endif
 
 extern "C" size_t ortmi_decoder_decode_step_workspace_size(const OrtmiDecoderDims* dims) {
     if (!dims) return 0;
