@@ -61,7 +61,8 @@ namespace dprog {
 // +3 C stored, +4 D input ready, +5 D stored, +6 E input ready, +7 E stored;
 // attention workgroups +2 q/k/v ready, +4 keys attended, +5 merged in the
 // workgroup, +6 partials in hand, +3 output stored; 1 + 8 L lm_head input ready,
-// 2 + 8 L lm_head done.
+// 2 + 8 L lm_head done; the last slot kernel entry, the one before it the greedy
+// id written (workgroup 0).
 constexpr int kStampSlots = 256;
 #ifdef ORTMI_DPROG_STAMPS
 __device__ unsigned long long g_stamps[1024 * kStampSlots];
@@ -547,6 +548,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
     constexpr int kPref = kv_pref_steps(CPLD);
     static_assert(kLo + CPLD <= kRegion && 2 * kPref <= kRegion, "slots");
 
+    DPROG_STAMP(kStampSlots - 1);  // kernel entry
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
     const int wg = blockIdx.x, nwg = p.nwg;
@@ -1161,6 +1163,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         for (int w = 0; w < kWaves; ++w) arg_take(best, bi, s_arg_v[w], s_arg_i[w]);
         *p.next_id = bi < 0 ? 0 : bi;
         store_status(p.status, bad_id ? 2 : 0);
+        DPROG_STAMP(kStampSlots - 2);  // greedy id written (workgroup 0)
     }
 }
 
@@ -1352,13 +1355,21 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
         }
     }
     if (!fit) return fail(ORTMI_E_INVALID, "decoder step: the program does not fit one workgroup per CU");
+    // One workgroup per CU, at most one fits per CU: with the device otherwise idle a
+    // plain launch makes every workgroup resident at once, and costs about 30 us less
+    // per step than a cooperative launch, which guarantees it. Either way every wait
+    // inside is bounded, so a workgroup that cannot start (another kernel holds its
+    // CU) makes the launch stop with status 1 rather than hang; the caller then runs
+    // the step op by op and can ask for cooperative launches from then on.
     void* args[] = {&p};
-    const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(dprog::kThreads), args,
-                                                    (unsigned)lds, as_stream(stream));
+    const hipError_t e =
+        d.cooperative ? hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(dprog::kThreads), args,
+                                                   (unsigned)lds, as_stream(stream))
+                      : hipLaunchKernel(fn, dim3(nwg), dim3(dprog::kThreads), args, (size_t)lds,
+                                        as_stream(stream));
     if (e != hipSuccess) {
         (void)hipGetLastError();
-        return fail(ORTMI_E_HIP, std::string("decoder step: cooperative launch: ") +
-                                     hipGetErrorString(e));
+        return fail(ORTMI_E_HIP, std::string("decoder step: launch: ") + hipGetErrorString(e));
     }
     return ORTMI_OK;
 }

@@ -77,6 +77,10 @@ struct Plan::DecodeProgram {
     int32_t* status = nullptr;  // host-pinned: the kernel writes it, the host reads it after the run
     int64_t steps = 0;          // program launches so far
     int64_t abort_step = 0;     // ORTMI_EP_PROGRAM_ABORT: launch to abort before it starts (1-based)
+    // Plain launches until one ends with status 1 (a workgroup could not start while
+    // the others waited for it); cooperative launches from then on, or always with
+    // ORTMI_EP_PROGRAM_COOPERATIVE=1.
+    int32_t cooperative = 0;
     ~DecodeProgram() {
         if (status) (void)hipHostFree(status);
     }
@@ -346,6 +350,8 @@ void Plan::match_decode_program() {
     dp->lm_B_p = dev(dp->lm_B);
     dp->lm_S_p = dev(dp->lm_S);
     if (const char* ab = std::getenv("ORTMI_EP_PROGRAM_ABORT")) dp->abort_step = std::atoll(ab);
+    if (const char* co = std::getenv("ORTMI_EP_PROGRAM_COOPERATIVE"))
+        dp->cooperative = std::strcmp(co, "0") != 0;
     check_hip(hipHostMalloc((void**)&dp->status, sizeof(int32_t), hipHostMallocDefault),
               "hipHostMalloc");
     dp->next_id = device_alloc(sizeof(int64_t));
@@ -380,6 +386,7 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
         table[l].v_cache = pv.ptr;
     }
     d.kv_capacity = (int32_t)cap;
+    d.cooperative = dp.cooperative;
     // A host total is checked here; one in device memory (an EP whose memory device
     // is HBM gets its inputs there) is checked by the kernel itself (status 3), which
     // saves the step a device -> host round trip.
@@ -773,6 +780,7 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
             // may have written at total - 1 is rewritten with the same values.
             if (dprog_required_)
                 fail("decode program failed (status " + std::to_string(st) + ")");
+            if (st == 1) dprog_->cooperative = 1;
             ++dprog_fallbacks_;
             outs_.clear();
         }

@@ -33,7 +33,7 @@ class Dims(ctypes.Structure):
     _fields_ = [(n, _i32) for n in ("layers", "hidden", "num_heads", "kv_num_heads", "head_size",
                                     "intermediate", "vocab", "kv_capacity", "max_position",
                                     "rotary_half", "rotary_interleaved", "block_size",
-                                    "dtype")] + [("scale", _f32)]
+                                    "dtype")] + [("scale", _f32), ("cooperative", _i32)]
 
 
 def merge_qkv(w, prefix):
@@ -89,7 +89,7 @@ class DecodeProgram:
         self.lmB, self.lms = t(w["lm_head.B"]), t(w["lm_head.s"])
         self.dims = Dims(cfg.layers, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim,
                          cfg.inter, cfg.vocab, cap, cfg.max_pos, cfg.head_dim // 2, 0,
-                         cfg.block, ORTMI_F16, 0.0)
+                         cfg.block, ORTMI_F16, 0.0, 1)
         lib = load_kernels()
         self.lib = lib
         nbytes = lib.ortmi_decoder_decode_step_workspace_size(ctypes.byref(self.dims))

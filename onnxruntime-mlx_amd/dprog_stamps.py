@@ -43,6 +43,8 @@ def main():
     ap.add_argument("--total", type=int, default=576, help="total_sequence_length of the step")
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--cooperative", type=int, default=0,
+                    help="1: cooperative launch; 0: plain launch of the same grid")
     args = ap.parse_args()
     import torch
 
@@ -68,6 +70,7 @@ def main():
     prog = dp.DecodeProgram(cfg, w, kv, cap)
     del w
     prog.lib = lab
+    prog.dims.cooperative = args.cooperative
     prog.total.fill_(args.total)
     for _ in range(args.reps):
         prog.step()
@@ -83,13 +86,15 @@ def main():
     ts = np.zeros((nwg, SLOTS), np.uint64)
     if lab.ortmi_decoder_decode_step_stamps(ts.ctypes.data, nwg):
         raise RuntimeError("stamps read failed")
-    T = (ts.astype(np.int64) - int(ts[:, 0].min())) * 10  # ns
+    base = int(ts[:, SLOTS - 1].min())  # the first workgroup's entry
+    T = (ts.astype(np.int64) - base) * 10  # ns
     L, H = cfg.layers, cfg.heads
-    attn = np.where(T[:, 1] == -int(ts[:, 0].min()) * 10)[0]  # no A stamp: attention workgroup
+    attn = np.where(ts[:, 1] == 0)[0]  # no A stamp: attention workgroup
     proj = np.setdiff1d(np.arange(nwg), attn)
     NS = max(1, len(attn) // H)
     split0 = attn[::NS]
-    print(f"decode program, {L} layers, total {args.total}: status {status}, launch "
+    print(f"decode program, {L} layers, total {args.total}, "
+          f"{'cooperative' if args.cooperative else 'plain'} launch: status {status}, launch "
           f"{e0.elapsed_time(e1) * 1e3:.1f} us (HIP events); {len(proj)} projection and "
           f"{len(attn)} attention workgroups ({NS} key splits per head)")
     med = np.median
@@ -130,6 +135,12 @@ def main():
     print(f"| lm_head phase | {lm:.2f} |")
     print(f"| whole launch (first start to last lm_head stamp) | "
           f"{(T[:, 2 + 8 * L].max() - T[:, 0].min()) / 1e3:.1f} |")
+    entry = T[:, SLOTS - 1]
+    print(f"| workgroup entries spread (first to last entry) | {(entry.max() - entry.min()) / 1e3:.2f} |")
+    print(f"| entry to start (layer table, launch index) | {med(T[:, 0] - entry) / 1e3:.2f} |")
+    print(f"| last lm_head stamp to greedy id written | "
+          f"{(T[0, SLOTS - 2] - T[:, 2 + 8 * L].max()) / 1e3:.2f} |")
+    print(f"| first entry to greedy id written | {(T[0, SLOTS - 2] - entry.min()) / 1e3:.1f} |")
 
 
 if __name__ == "__main__":

@@ -38,7 +38,7 @@ def test_python_signatures_cover_header():
 
 
 def test_abi_version(lib):
-    assert lib.ortmi_abi_version() == 1
+    assert lib.ortmi_abi_version() == 2
 
 
 def _err(lib):
