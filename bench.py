@@ -2,7 +2,7 @@
 """Benchmark of the MI355X execution provider's hot path on one GPU.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload all|gemv|gemm|gqa|paged|decoder|copy]
+                    [--workload all|gemv|gemm|gqa|gqa_growing|gqa_shared|paged|decoder|copy]
 
 Primary line: int4 MatMulNBits decode GEMV (K=4096, N=11008, block 32, fp32
 activations) as achieved HBM GB/s. A step is one MatMulNBits call; consecutive
@@ -364,9 +364,15 @@ def bench_copy(torch, steps, warmup):
 def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
     """Int4 decoder through the EP: prompt prefill, then greedy decode steps.
 
-    A decode step is one EP Compute over the whole graph for one token (host
-    total_sequence_length in, argmax on the device), timed on the wall clock with
-    the device synchronised at both ends, as a serving loop sees it."""
+    The feeds are placed as a stock ONNX Runtime places them for an EP whose memory
+    device is HBM: input ids, seqlens_k and total_sequence_length are host tensors
+    that the harness copies to HBM through the EP's data transfer each run; the KV
+    cache and the logits are bound to device buffers (IOBinding). The graph ends in
+    ArgMax(logits), so a greedy step is one EP run over the whole graph for one
+    token plus the read-back of the id the application feeds next, timed on the
+    wall clock with the device synchronised at both ends, as a serving loop sees
+    it. Also reported: the graph without the ArgMax node (the application takes
+    the argmax of the logits on the device), and the ids bound in HBM as well."""
     import importlib
 
     import numpy as np
@@ -375,10 +381,14 @@ def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
     cfg = dec.DecoderConfig()
     w = dec.make_weights(cfg, seed=4)
     cap = prompt_len + gen
-    runner = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=prompt_len)
-    # The same decoder ending in an ArgMax node: the EP's decode program writes the
-    # greedy id to the graph output, so a step is the EP run alone.
-    runner_am = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=prompt_len, argmax_node=True)
+    # The decoder ending in an ArgMax node: the EP's decode program writes the greedy
+    # id to the graph output.
+    runner = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=prompt_len, argmax_node=True,
+                               host_feeds=True)
+    # The same decoder without it: the application's argmax over the logits.
+    runner_app = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=prompt_len, host_feeds=True)
+    # The ids bound in HBM too (the argmax output fed back in place).
+    runner_dev = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=prompt_len)
     del w
     prompt = np.random.default_rng(44).integers(0, cfg.vocab, size=prompt_len)
     runner.generate(prompt[:16], steps=4)  # warm-up: allocations and first launches
@@ -389,17 +399,21 @@ def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
     # repeated at the final context (each run rewrites the same KV row), the device
     # synchronised around it, without the greedy argmax that feeds the next token.
     length = runner.length - 1
+    runner.ids_host[0, 0] = int(runner.next_id.reshape(-1)[0].item())
     run_times = []
     for _ in range(max(20, gen // 2)):
         runner.length = length
         t1 = time.perf_counter()
-        runner.run(runner.next_id, 1)
+        runner.run(runner.ids_host[:, :1], 1)
         torch.cuda.synchronize()
         run_times.append(time.perf_counter() - t1)
     runner.length = length + 1
-    runner_am.generate(prompt[:16], steps=4)
-    tokens_am, _, times_am = runner_am.generate(prompt, steps=gen)
-    del runner_am
+    runner_app.generate(prompt[:16], steps=4)
+    tokens_app, _, times_app = runner_app.generate(prompt, steps=gen)
+    del runner_app
+    runner_dev.generate(prompt[:16], steps=4)
+    tokens_dev, _, times_dev = runner_dev.generate(prompt, steps=gen)
+    del runner_dev
     tok_s = len(times) / dec_s
     wbytes = cfg.weight_bytes()
     # KV read per token at the mean decode context, K and V, all layers.
@@ -411,8 +425,11 @@ def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
                 gbs=per_tok * tok_s / 1e9, tokens=tokens[:8], n_decode=len(times),
                 p50_ms=float(np.median(times)) * 1e3,
                 run_p50_ms=float(np.median(run_times)) * 1e3,
-                am_tok_s=len(times_am) / float(np.sum(times_am)),
-                am_p50_ms=float(np.median(times_am)) * 1e3, am_same_tokens=tokens_am == tokens)
+                app_tok_s=len(times_app) / float(np.sum(times_app)),
+                app_p50_ms=float(np.median(times_app)) * 1e3,
+                app_same_tokens=tokens_app == tokens,
+                dev_tok_s=len(times_dev) / float(np.sum(times_dev)),
+                dev_p50_ms=float(np.median(times_dev)) * 1e3, dev_same_tokens=tokens_dev == tokens)
 
 
 def measured_traffic(profile: str):
@@ -497,7 +514,8 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "gemv", "gemm", "gqa", "paged", "decoder", "copy"])
+                    choices=["all", "gemv", "gemm", "gqa", "gqa_growing", "gqa_shared", "paged",
+                             "decoder", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -553,7 +571,7 @@ def main():
                          "peak": FP16_DENSE_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(r["mfma_frac"], 4)}}
         log(f"gemm bf16: {r['tflops']:.1f} TFLOP/s ({r['gpu_ms'] * 1e3:.2f} us/call)")
-    if wl in ("all", "gqa"):
+    if wl in ("all", "gqa", "gqa_growing"):
         r = bench_gqa(torch, ortmi, args.steps, args.warmup)
         secondary["gqa_decode"] = {
             "config": "B=8 H=32 KV=8 hd=128 past=4096 fp16 rotary, growing contract",
@@ -562,6 +580,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(r["gbs"] / HBM_PEAK_GBS, 4)}}
         log(f"gqa: {r['gbs']:.1f} GB/s ({r['gpu_ms'] * 1e3:.2f} us/call)")
+    if wl in ("all", "gqa", "gqa_shared"):
         r = bench_gqa_shared(torch, ortmi, args.steps, args.warmup)
         secondary["gqa_decode_shared"] = {
             "config": "B=8 H=32 KV=8 hd=128 past=4096 fp16 rotary, shared (in-place) contract",
@@ -589,13 +608,22 @@ def main():
             "decode_tok_s": round(r["tok_s"], 1), "ms_per_token": round(r["ms_per_token"], 3),
             "p50_ms_per_token": round(r["p50_ms"], 3), "prefill_ms": round(r["ttft_ms"], 2),
             # The EP run alone, as the reference's bench times session.run (median),
-            # without the greedy argmax and its synchronisation.
+            # without reading the id back.
             "run_only_p50_ms": round(r["run_p50_ms"], 3),
             "run_only_tok_s": round(1e3 / r["run_p50_ms"], 1),
-            # The graph with a trailing ArgMax: the greedy id comes out of the EP run.
-            "argmax_node_tok_s": round(r["am_tok_s"], 1),
-            "argmax_node_p50_ms": round(r["am_p50_ms"], 3),
-            "argmax_node_same_tokens": r["am_same_tokens"],
+            # The graph without the trailing ArgMax: the application's argmax on the
+            # device over the logits output.
+            "app_argmax_tok_s": round(r["app_tok_s"], 1),
+            "app_argmax_p50_ms": round(r["app_p50_ms"], 3),
+            "app_argmax_same_tokens": r["app_same_tokens"],
+            # Input ids bound in HBM as well (IOBinding of every feed but the two
+            # int32 scalars), the argmax output fed back in place.
+            "device_ids_tok_s": round(r["dev_tok_s"], 1),
+            "device_ids_p50_ms": round(r["dev_p50_ms"], 3),
+            "device_ids_same_tokens": r["dev_same_tokens"],
+            "feeds": "input ids, seqlens_k, total_sequence_length in host memory, copied to "
+                     "HBM by the EP's data transfer (ORT's placement rule); KV cache and "
+                     "logits bound in HBM",
             "prefill_tok_s": round(r["prefill_tok_s"], 1),
             "bytes_per_token": r["bytes_per_token"],
             "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
@@ -603,8 +631,9 @@ def main():
             "first_tokens": r["tokens"]}
         log(f"decoder: {r['tok_s']:.1f} tok/s ({r['ms_per_token']:.3f} ms/token, p50 "
             f"{r['p50_ms']:.3f}), prefill {r['ttft_ms']:.1f} ms; EP run alone p50 "
-            f"{r['run_p50_ms']:.3f} ms; with the ArgMax node {r['am_tok_s']:.1f} tok/s (p50 "
-            f"{r['am_p50_ms']:.3f} ms, same tokens: {r['am_same_tokens']})")
+            f"{r['run_p50_ms']:.3f} ms; application argmax {r['app_tok_s']:.1f} tok/s (p50 "
+            f"{r['app_p50_ms']:.3f} ms, same tokens: {r['app_same_tokens']}); ids in HBM "
+            f"{r['dev_tok_s']:.1f} tok/s (same tokens: {r['dev_same_tokens']})")
         if not args.no_cpu_baseline:
             cpu_dec = cpu_baseline_decoder()
             secondary["int4_decoder"]["cpu_baseline"] = cpu_dec
