@@ -519,8 +519,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (the sharding "
-              "design is described in DESIGN.md); run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path (the kernels are "
+              "measured at one GPU's share); run with --gpus 1.", file=sys.stderr)
         return 2
 
     import torch

@@ -1,6 +1,6 @@
 // Int4 decoder decode step as one persistent kernel ("decode program") for gfx950.
 //
-// One cooperative launch runs a whole one-token step of a Llama-style int4
+// One launch runs a whole one-token step of a Llama-style int4
 // decoder: embedding row -> per layer [(Skip)SimplifiedLayerNorm, merged QKV
 // MatMulNBits, GroupQueryAttention over the shared KV cache with in-op RoPE,
 // o_proj MatMulNBits, SkipSimplifiedLayerNorm, gate/up MatMulNBits with SwiGLU,
@@ -30,15 +30,17 @@
 // every buffer word is rewritten by every launch, so a stale word always carries
 // the previous launch's tag.
 //
-// Grid: one 512-thread workgroup per CU (co-resident by the cooperative launch),
-// 8 waves, all computing. Attention runs on the last H * NS workgroups, one
-// (query head, key split) each; the projections run on the others. Every wait is
-// bounded: a wait that sees no new data for 100 ms of the 100 MHz realtime clock
-// writes its launch index to the abort word and status 1, and every other waiting
-// thread leaves when it sees its own launch index there. A workgroup that finds
-// its launch index in the abort word at entry leaves at once (the host can abort
-// a launch before it starts). No thread waits on anything its own workgroup
-// produces later, so the waits form a chain along the layer order and always end.
+// Grid: one 512-thread workgroup per CU (at most one fits per CU, so on an
+// otherwise idle device a plain launch makes them all resident at once; a
+// cooperative launch guarantees it), 8 waves, all computing. Attention runs on
+// the last H * NS workgroups, one (query head, key split) each; the projections
+// run on the others. Every wait is bounded: a wait that sees no new data for
+// 100 ms of the 100 MHz realtime clock writes its launch index to the abort word
+// and status 1, and every other waiting thread leaves when it sees its own
+// launch index there. A workgroup that finds its launch index in the abort word
+// at entry leaves at once (the host can abort a launch before it starts). No
+// thread waits on anything its own workgroup produces later, so the waits form a
+// chain along the layer order and always end.
 //
 // Rounding follows the unfused ops of the fp16 graph: residual sums and
 // normalised activations, MatMulNBits outputs, the RoPE'd query/key and the

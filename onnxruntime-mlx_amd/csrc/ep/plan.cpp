@@ -477,8 +477,8 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
         return false;
     }
     if (rc == ORTMI_E_HIP && !dprog_required_) {
-        // The cooperative launch itself failed (e.g. the CUs are not all free for a
-        // grid that must be co-resident): this step runs op by op.
+        // The launch itself failed (e.g. a cooperative launch while the CUs are not
+        // all free for a grid that must be co-resident): this step runs op by op.
         ++dprog_fallbacks_;
         return false;
     }

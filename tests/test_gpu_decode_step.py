@@ -2,7 +2,7 @@
 path and the oracle.
 
 Each decode step runs both ways on the same KV cache: the EP graph (one kernel per
-fused op) and the decode program (one cooperative launch). They round at the same
+fused op) and the decode program (one launch). They round at the same
 op boundaries but sum in different orders, so logits are compared within the fp16
 tolerance carried through the layers, the appended K/V rows within one fp16 ULP of
 the rows' scale, and the program's greedy token must be the argmax of its own

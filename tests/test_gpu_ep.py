@@ -2,10 +2,9 @@
 (CreateEpFactories -> GetCapability -> Compile -> Compute) against the oracle.
 
 Per-op tolerances are those of the kernel tests (fp16: 1e-3 + 1 ULP of the exact
-value). The decoder is checked end to end the way the north-star bar states it:
-identical greedy tokens. Logits of a many-layer fp16 graph differ from the
-fp64-accumulating oracle by accumulated fp16 rounding of intermediates, so the
-token check is made teacher-forced: at every step the oracle runs on the same
+value). The decoder is checked end to end on identical greedy tokens. Logits of
+a many-layer fp16 graph differ from the fp64-accumulating oracle by accumulated
+fp16 rounding of intermediates, so the token check is made teacher-forced: at every step the oracle runs on the same
 tokens as the GPU, and the GPU's greedy token must equal the oracle's argmax
 unless the oracle's own top-1 margin over the GPU token is within TIE_ULPS fp16
 ULPs of the row's largest |logit| (a near tie, which the test prints). There is

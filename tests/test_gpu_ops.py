@@ -1,6 +1,6 @@
 """GPU parity: every hot-path kernel, called through the C ABI, against the oracle.
 
-Tolerances (stated per test, from the north-star bar):
+Tolerances (stated per test):
   * int4/int8 unpack, block and zero-point indexing, KV-cache row copies and
     paged slot writes: bit-exact.
   * fp32 outputs: max abs diff <= 6e-5 (plus the fp32-accumulation term for long
