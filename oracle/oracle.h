@@ -48,6 +48,16 @@ int orc_mnb_matmul(const float* A, const uint8_t* B, const float* scales, const 
                    int nthreads);
 
 /*
+ * fast.c: the CPU baseline's form of the same product for 4-bit weights, fp32
+ * accumulation with AVX2/FMA (scales fp32, or fp16 bits when scale_f16; blocks of
+ * 32, 64, 96 or 128 codes, K a multiple of the block). -1 when the form or the CPU is outside
+ * it. Pinned against orc_mnb_matmul by tests/test_oracle.py.
+ */
+int orc_mnb_matmul_fast(const float* A, int64_t M, const uint8_t* B, const void* scales,
+                        int scale_f16, const uint8_t* zp, int64_t N, int64_t K, int block,
+                        float* Y, int nthreads);
+
+/*
  * Rotary embedding over a strided tensor: element (b, s, n, d) lives at
  * x[b*sb + s*ss + n*sn + d]. Token (b, s) uses cache row rows[b*S + s].
  * Rotates dims [offset, offset + 2*half) of each head; other dims pass through.

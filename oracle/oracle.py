@@ -71,6 +71,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_rms_norm.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _flt, _int, _f32p,
                                _f32p]
     L.orc_rms_norm.restype = None
+    L.orc_mnb_matmul_fast.argtypes = [_f32p, _i64, _u8p, ctypes.c_void_p, _int, _u8p, _i64, _i64,
+                                      _int, _f32p, _int]
 
 
 def _p(a, t):
@@ -141,6 +143,25 @@ def mnb_matmul(A, B, scales, zp, N, K, bits=4, block=32, nthreads=0) -> np.ndarr
                               A2.shape[0], N, K, bits, block, _p(Y, _f64p), nthreads)
     if rc:
         raise ValueError("oracle: unsupported MatMulNBits form")
+    return Y.reshape(tuple(np.shape(A)[:-1]) + (N,))
+
+
+def mnb_matmul_fast(A, B, scales, zp, N, K, block=32, nthreads=0) -> np.ndarray:
+    """The CPU baseline's int4 MatMulNBits (fast.c): fp32 accumulation with
+    AVX2/FMA, scales fp32 or fp16 (used as stored). A [..., K]; returns float32
+    [..., N]. Timing baseline only: the parity reference is mnb_matmul."""
+    A2 = _f32(A).reshape(-1, K)
+    B = np.ascontiguousarray(B, dtype=np.uint8)
+    s = np.ascontiguousarray(scales)
+    if s.dtype not in (np.float32, np.float16):
+        s = s.astype(np.float32)
+    z = None if zp is None else np.ascontiguousarray(zp, dtype=np.uint8)
+    Y = np.empty((A2.shape[0], N), np.float32)
+    rc = lib().orc_mnb_matmul_fast(_p(A2, _f32p), A2.shape[0], _p(B, _u8p),
+                                   s.ctypes.data_as(ctypes.c_void_p), int(s.dtype == np.float16),
+                                   _p(z, _u8p), N, K, block, _p(Y, _f32p), nthreads)
+    if rc:
+        raise ValueError("oracle: form outside the fast MatMulNBits (4-bit, block 32-128, AVX2)")
     return Y.reshape(tuple(np.shape(A)[:-1]) + (N,))
 
 
@@ -412,7 +433,32 @@ def dequant_cache(w, cfg):
     return out
 
 
-def decoder_forward(w, cfg, ids, past_k, past_v, total, wcache=None, logit_rows=None):
+def _gqa_step_fast(q, k, v, past_k, past_v, total, H, KV, cos, sin):
+    """One-token GroupQueryAttention on the shared KV buffer in fp32 numpy (the CPU
+    baseline's form of gqa() at S = 1 with non-interleaved rotary over the whole
+    head): RoPE of q and the new key at position total - 1, the new K/V row written
+    in place, then per KV head softmax(q K^T * scale) V over the total keys."""
+    hd = past_k.shape[-1]
+    half, pos, G = hd // 2, total - 1, H // KV
+    c, s = cos[pos].astype(np.float32), sin[pos].astype(np.float32)
+
+    def rope(x):
+        x1, x2 = x[:, :half], x[:, half:]
+        return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], axis=1)
+
+    qh = round_f16(rope(np.asarray(q, np.float32).reshape(H, hd)))
+    past_k[0, :, pos] = round_f16(rope(np.asarray(k, np.float32).reshape(KV, hd)))
+    past_v[0, :, pos] = np.asarray(v, np.float32).reshape(KV, hd)
+    out = np.empty((H, hd), np.float32)
+    for g in range(KV):
+        sc = (qh[g * G:(g + 1) * G] @ past_k[0, g, :total].T) * np.float32(1.0 / np.sqrt(hd))
+        sc = np.exp(sc - sc.max(axis=1, keepdims=True))
+        out[g * G:(g + 1) * G] = (sc @ past_v[0, g, :total]) / sc.sum(axis=1, keepdims=True)
+    return round_f16(out).reshape(1, 1, H * hd)
+
+
+def decoder_forward(w, cfg, ids, past_k, past_v, total, wcache=None, logit_rows=None,
+                    fast=False):
     """One forward of the int4 Llama-style decoder graph, op by op in fp16.
 
     The graph is the ONNX Runtime GenAI q4f16 decoder (op histogram in
@@ -430,13 +476,19 @@ def decoder_forward(w, cfg, ids, past_k, past_v, total, wcache=None, logit_rows=
     wcache: optional dequant_cache(w, cfg); the linear layers are then fp64 matrix
     products with the cached fp64 weights (the same exact products as the per-row
     C loop, summed in BLAS order). logit_rows: optional row indices of the logits
-    to compute (default all S). Returns fp16-rounded logits [rows, vocab] as f32.
+    to compute (default all S). fast: the linear layers go through the CPU
+    baseline's fp32 AVX2 MatMulNBits (fast.c) and one-token attention through
+    _gqa_step_fast instead, for timing a CPU decoder; its logits are not a parity
+    reference. Returns fp16-rounded logits [rows, vocab] as
+    f32.
     """
     r16 = round_f16
     S = len(ids)
     D, H, KV, hd = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
 
     def mm(x, key, N, K):
+        if fast:
+            return r16(mnb_matmul_fast(x, w[key + ".B"], w[key + ".s"], None, N, K, cfg.block))
         if wcache is not None:
             x2 = np.asarray(x, np.float32).reshape(-1, K).astype(np.float64)
             return r16((x2 @ wcache[key].T).reshape(tuple(np.shape(x)[:-1]) + (N,)))
@@ -455,11 +507,14 @@ def decoder_forward(w, cfg, ids, past_k, past_v, total, wcache=None, logit_rows=
         q = mm(x, p + ".q", H * hd, D)
         k = mm(x, p + ".k", KV * hd, D)
         v = mm(x, p + ".v", KV * hd, D)
-        out, pk, pv, shared = gqa(q, k, v, past_k[layer], past_v[layer], total, H, KV, cos, sin,
-                                  round16=True)
-        assert shared, "the decoder runs the shared-buffer KV contract"
-        past_k[layer][...] = pk
-        past_v[layer][...] = pv
+        if fast and S == 1:
+            out = _gqa_step_fast(q, k, v, past_k[layer], past_v[layer], total, H, KV, cos, sin)
+        else:
+            out, pk, pv, shared = gqa(q, k, v, past_k[layer], past_v[layer], total, H, KV, cos,
+                                      sin, round16=True)
+            assert shared, "the decoder runs the shared-buffer KV contract"
+            past_k[layer][...] = pk
+            past_v[layer][...] = pv
         o = mm(r16(out), p + ".o", D, H * hd)
         x2, residual = rms_norm(o, w[p + ".ln2"], cfg.eps, skip=residual, round16=True)
         x2 = r16(x2)

@@ -132,6 +132,44 @@ def test_mnb_matmul_matches_fp64_gemm(oracle, M, K, block):
     np.testing.assert_allclose(Y, ref, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("K,block,asym,f16", [(4096, 32, True, False), (1536, 32, False, True),
+                                              (8960, 32, True, True), (1024, 64, True, False),
+                                              (2048, 128, False, False)])
+def test_mnb_matmul_fast_matches_fp64(oracle, K, block, asym, f16):
+    """The CPU baseline's fp32 AVX2 GEMV against the fp64 restatement, within an
+    fp32 accumulation bound: the kernel sums a*q and a*z per block before subtracting,
+    so its error is bounded by 2^-20 * sum_k |a_k| (q_k + z) s < 2^-15 * sum_k |a_k| s
+    per row (sums of <= 8960 terms), for fp32 and fp16 scales, with and without zero
+    points. A swapped nibble order fails by orders of magnitude more."""
+    try:
+        probe = oracle.mnb_matmul_fast(np.zeros(32, np.float32), np.zeros((1, 1, 16), np.uint8),
+                                       np.ones(1, np.float32), None, 1, 32, 32)
+    except ValueError:
+        pytest.skip("no AVX2/FMA on this CPU")
+    assert probe[0] == 0
+    rng = np.random.default_rng(K + block)
+    N, nb = 97, K // block
+    B = oracle.pack_nibbles(rng.integers(0, 16, size=(N, nb, block), dtype=np.uint8))
+    s = (np.abs(rng.standard_normal(N * nb)) * 0.02 + 1e-3).astype(np.float16 if f16 else np.float32)
+    zp = (oracle.pack_zero_points(rng.integers(0, 16, size=(N, nb), dtype=np.uint8), 4)
+          if asym else None)
+    a = rng.standard_normal(K).astype(np.float32)
+    y = oracle.mnb_matmul_fast(a, B, s, zp, N, K, block)
+    s32 = s.astype(np.float32)
+    ref = oracle.mnb_matmul(a[None], B, s32, zp, N, K, 4, block)[0]
+    abs_blocks = np.abs(a.astype(np.float64)).reshape(nb, block).sum(axis=1)
+    bound = 2.0 ** -15 * (s32.astype(np.float64).reshape(N, nb) @ abs_blocks)
+    assert (np.abs(y - ref) <= bound).all(), float(np.max(np.abs(y - ref) / bound))
+    # The bound is far below the error of a swapped nibble order.
+    swapped = oracle.mnb_matmul(a[None], (B >> 4) | ((B & 15) << 4), s32, zp, N, K, 4, block)[0]
+    assert (np.abs(swapped - ref) > 100 * bound).mean() > 0.9
+    # Several activation rows at once (the prefill form) give each row's GEMV.
+    A = rng.standard_normal((3, K)).astype(np.float32)
+    Y = oracle.mnb_matmul_fast(A, B, s, zp, N, K, block)
+    for m in range(3):
+        np.testing.assert_array_equal(Y[m], oracle.mnb_matmul_fast(A[m], B, s, zp, N, K, block))
+
+
 # ---------------------------------------------------------------------- RoPE ---
 
 
@@ -211,6 +249,28 @@ def test_gqa_packed_equals_separate(oracle):
     packed = np.concatenate([q, k, v], axis=-1)
     b = oracle.gqa(packed, None, None, pk, pv, cap + S, H, KV)
     np.testing.assert_array_equal(a[0], b[0])
+
+
+@pytest.mark.parametrize("total", [1, 33, 600])
+def test_gqa_step_fast_matches_gqa(oracle, total):
+    """The CPU baseline's one-token attention (fp32 numpy) against the oracle's GQA
+    on the shared buffer: the new K/V rows identical, the output within one fp16
+    ULP (fp32 against fp64 softmax sums, both rounded to fp16). A rotation applied to the wrong
+    half of the head, or the new row written at total instead of total - 1, fails."""
+    rng = np.random.default_rng(total)
+    H, KV, hd, cap = 12, 2, 128, 640
+    f16 = lambda *s: rng.standard_normal(s).astype(np.float16).astype(np.float32)  # noqa: E731
+    ang = np.arange(1024)[:, None] / (10000.0 ** (np.arange(hd // 2) / (hd // 2)))
+    cos, sin = np.cos(ang).astype(np.float16), np.sin(ang).astype(np.float16)
+    pk, pv = f16(1, KV, cap, hd), f16(1, KV, cap, hd)
+    q, k, v = f16(1, 1, H * hd), f16(1, 1, KV * hd), f16(1, 1, KV * hd)
+    ref, rk, rv, shared = oracle.gqa(q, k, v, pk, pv, total, H, KV, cos, sin, round16=True)
+    assert shared
+    fk, fv = pk.copy(), pv.copy()
+    got = oracle._gqa_step_fast(q, k, v, fk, fv, total, H, KV, cos, sin)
+    np.testing.assert_array_equal(fk[0, :, :total], rk[0, :, :total])
+    np.testing.assert_array_equal(fv[0, :, :total], rv[0, :, :total])
+    assert refs.max_ulp_f16(got, ref) <= 1.0
 
 
 def test_gqa_single_key_returns_value(oracle):
