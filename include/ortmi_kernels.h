@@ -384,9 +384,9 @@ int ortmi_group_query_attention_decode_partials(
  * every sequence (max_blocks * block_size always is one); keys at positions
  * max_context and beyond are not attended, and past_seqlens is read clamped to
  * [0, max_context]. dtype fp32, fp16 or bf16; head_size a multiple of 16 up to
- * 256 (fp16/bf16 with head 64/128 run the multi-token tiles and the single-token
- * decode kernel, the tiles on the matrix cores for fp16 and on the vector units
- * for bf16; every other form one VALU workgroup per (token, head) row). A token's
+ * 256 (fp16/bf16 with head 64/128 run the multi-token tiles on the matrix cores
+ * and the single-token decode kernel; every other form one VALU workgroup per
+ * (token, head) row). A token's
  * sequence range is cum_seqlens clamped to [0, num_tokens). cos/sin caches are
  * [rotary_max_pos, rotary_half]. head_sink [H],
  * q_norm_weight/k_norm_weight [hd] optional. output [T,H*vhd]. Malformed control
@@ -480,6 +480,12 @@ int ortmi_rms_norm(const void* x, const void* skip, const void* bias, const void
  *    long rows are reduced by many workgroups in two passes; with workspace =
  *    NULL one workgroup scans each row. Greedy decoding takes it over the last
  *    logits row (the reference's callers do this on the host after Compute).
+ *  - ortmi_argmax_axis: ArgMax over any axis, x viewed as [outer, dim, inner],
+ *    out [outer, inner] int64; select_last_index = 1 gives the last index on
+ *    ties (0 the first); NaN never wins, an all-NaN slice gives 0. Replaces
+ *    argminmax / argmax_op (rust/src/ops/reduction.rs:239-278; claim
+ *    reduction.rs:582-630) for the axes and tie rule ortmi_argmax_rows does not
+ *    cover.
  *  - ortmi_cast: f32 <-> f16 <-> bf16.
  */
 int ortmi_gather_rows(const void* table, const int64_t* ids, void* out, int64_t num_ids,
@@ -494,6 +500,8 @@ int ortmi_sigmoid(const void* x, void* out, int64_t n, int32_t dtype, void* stre
 size_t ortmi_argmax_rows_workspace_size(int64_t rows, int64_t cols);
 int ortmi_argmax_rows(const void* x, int64_t* out, int64_t rows, int64_t cols, int32_t dtype,
                       void* workspace, size_t workspace_bytes, void* stream);
+int ortmi_argmax_axis(const void* x, int64_t* out, int64_t outer, int64_t dim, int64_t inner,
+                      int32_t select_last_index, int32_t dtype, void* stream);
 int ortmi_cast(const void* x, int32_t src_dtype, void* y, int32_t dst_dtype, int64_t n,
                void* stream);
 

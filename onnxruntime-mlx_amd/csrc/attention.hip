@@ -891,20 +891,57 @@ __device__ void attn_tile_body(const TileDesc& t, int kvh, int G, int H, const T
 // Wave w owns queries 32w..32w+31 of the tile. Key blocks of 64 go global ->
 // registers -> LDS, the next block's loads in flight while the current one is used.
 
-template <int HD, int VHD, bool PAGED, int NW = 4>
+// 16-bit element pieces of the matrix-core tile: T = half_t (fp16) or uint16_t
+// (bf16 bits). Operands travel as 16-bit bit patterns; only the matrix-core step,
+// the rounding of P and of the output, and the P row sums depend on the type.
+typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+template <typename T>
+__device__ __forceinline__ float16_t tile_mfma(u16x8_t a, u16x8_t b, float16_t c) {
+    if constexpr (std::is_same<T, half_t>::value)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a),
+                                                      __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+// A float rounded to T (round to nearest even), as bits.
+template <typename T>
+__device__ __forceinline__ uint16_t tile_round(float x) {
+    if constexpr (std::is_same<T, half_t>::value)
+        return __builtin_bit_cast(uint16_t, (half_t)x);
+    else
+        return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+// Sum of two T values (bits lo, hi of w) added to acc in fp32, exactly widened.
+template <typename T>
+__device__ __forceinline__ float tile_pair_sum(uint32_t w, float acc) {
+    if constexpr (std::is_same<T, half_t>::value) {
+        const half2_t one2 = {(half_t)1.f, (half_t)1.f};
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w), one2, acc, false);
+    } else {
+        const bf16x2_t one2 = {(__bf16)1.f, (__bf16)1.f};
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), one2, acc, false);
+    }
+}
+
+template <typename T, int HD, int VHD, bool PAGED, int NW = 4>
 __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
-                               const half_t* __restrict__ qrot, const DenseKV& dk,
+                               const T* __restrict__ qrot, const DenseKV& dk,
                                const PagedKV& pk, float scale, const float* __restrict__ sink,
-                               int k0, int k1, half_t* __restrict__ out, int64_t out_tok_stride,
+                               int k0, int k1, T* __restrict__ out, int64_t out_tok_stride,
                                float* __restrict__ part, int nsplit, int split) {
+    static_assert(std::is_same<T, half_t>::value || std::is_same<T, uint16_t>::value,
+                  "fp16 or bf16 (16-bit storage)");
     static_assert(kKeyTile == 64 && HD % 16 == 0 && VHD % 32 == 0, "tile shape");
     static_assert(NW == 4 || NW == 8, "waves per tile");
     constexpr int NT = 64 * NW;       // threads
     constexpr int kRows = 32 * NW;    // query rows of the tile (32 per wave)
     constexpr int KP = HD + 8, VP = kKeyTile + 8;
     constexpr int DT = VHD / 32;          // head-dim tiles of O^T
-    __shared__ half_t sK[kKeyTile * KP];
-    __shared__ half_t sVt[VHD * VP];
+    __shared__ uint16_t sK[kKeyTile * KP];
+    __shared__ uint16_t sVt[VHD * VP];
     __shared__ unsigned long long sOk;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -919,14 +956,14 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
     // Scores are kept in the log2 domain (exp2 is the hardware exponential). The
     // scale is applied inside the exponent, after the block maximum of the raw
     // scores, which needs it positive: a negative scale flips the sign of Q as it
-    // is staged (exact in fp16) and scales by its magnitude.
+    // is staged (the sign bit, exact in fp16 and bf16) and scales by its magnitude.
     constexpr float kLog2e = 1.4426950408889634f;
     const float sc2 = fabsf(scale) * kLog2e;
     const uint32_t qsign = scale < 0.f ? 0x80008000u : 0u;
     // Q^T operand: the tile's query rows are staged in LDS once (zeros past the
     // last row) and each k-step reads its 8 head dims from there, which keeps
     // HD / 2 VGPRs free for the whole key walk.
-    __shared__ half_t sQ[kRows * KP];
+    __shared__ uint16_t sQ[kRows * KP];
     {
         constexpr int CPR = HD / 8;  // 16-byte chunks per row
         for (int i = tid; i < kRows * CPR; i += NT) {
@@ -1088,9 +1125,9 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
             if (!((vok >> i) & 1)) vreg[i] = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            half_t col[VPT];
+            uint16_t col[VPT];
 #pragma unroll
-            for (int i = 0; i < VPT; ++i) col[i] = __builtin_bit_cast(half8_t, vreg[i])[e];
+            for (int i = 0; i < VPT; ++i) col[i] = __builtin_bit_cast(u16x8_t, vreg[i])[e];
             if constexpr (VPT == 4)
                 *reinterpret_cast<uint2*>(&sVt[(c + e) * VP + r0]) =
                     *reinterpret_cast<const uint2*>(col);
@@ -1112,10 +1149,10 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
         for (int s2 = 0; s2 < HD / 16; ++s2)
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
-                const half8_t a =
-                    *reinterpret_cast<const half8_t*>(&sK[(kt * 32 + lrow) * KP + s2 * 16 + lk]);
-                const half8_t b = *reinterpret_cast<const half8_t*>(&sQ[q * KP + s2 * 16 + lk]);
-                st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, st[kt], 0, 0, 0);
+                const u16x8_t a =
+                    *reinterpret_cast<const u16x8_t*>(&sK[(kt * 32 + lrow) * KP + s2 * 16 + lk]);
+                const u16x8_t b = *reinterpret_cast<const u16x8_t*>(&sQ[q * KP + s2 * 16 + lk]);
+                st[kt] = tile_mfma<T>(a, b, st[kt]);
             }
     };
     // The key walk, software-pipelined across blocks: while the matrix cores score
@@ -1181,14 +1218,14 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
             // softmax weights can afford.
             const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
             // P^T operands: k-step kk uses e in [8 (kk % 2), 8 (kk % 2) + 8) of tile kk / 2.
-            half8_t pb[4];
+            u16x8_t pb[4];
             const float mref = m_new == -INFINITY ? 0.f : m_new;  // exp2(-inf - 0) = 0
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
                     pb[kt * 2 + e / 8][e % 8] =
-                        (half_t)__builtin_amdgcn_exp2f(fmaf(cur[kt][e], sc2, -mref));
+                        tile_round<T>(__builtin_amdgcn_exp2f(fmaf(cur[kt][e], sc2, -mref)));
             m = m_new;
             // Rescale O (and the running sums) only when some query's running max moved.
             if (__any(alpha != 1.f)) {
@@ -1197,18 +1234,16 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
 #pragma unroll
                     for (int e = 0; e < 16; ++e) oT[d][e] *= alpha;
             }
-            // Row sums of the same fp16 probabilities that weight V, accumulated in
-            // fp32 (v_dot2_f32_f16 against ones, four independent chains).
+            // Row sums of the same rounded probabilities that weight V, accumulated in
+            // fp32 (v_dot2 against ones, four independent chains).
             {
-                const half2_t one2 = {(half_t)1.f, (half_t)1.f};
                 float ls[4];
 #pragma unroll
                 for (int kk = 0; kk < 4; ++kk) {
                     ls[kk] = 0.f;
+                    const u32x4_t pw = __builtin_bit_cast(u32x4_t, pb[kk]);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        ls[kk] = __builtin_amdgcn_fdot2(
-                            half2_t{pb[kk][2 * i], pb[kk][2 * i + 1]}, one2, ls[kk], false);
+                    for (int i = 0; i < 4; ++i) ls[kk] = tile_pair_sum<T>(pw[i], ls[kk]);
                 }
                 lsum = fmaf(lsum, alpha, (ls[0] + ls[1]) + (ls[2] + ls[3]));
             }
@@ -1218,11 +1253,11 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
                 const int kbase = (kk / 2) * 32 + (kk % 2) * 16 + 4 * hh;
 #pragma unroll
                 for (int d = 0; d < DT; ++d) {
-                    const half_t* vr = &sVt[(d * 32 + lrow) * VP + kbase];
+                    const uint16_t* vr = &sVt[(d * 32 + lrow) * VP + kbase];
                     const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
                     const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 8);
-                    const half8_t a = __builtin_bit_cast(half8_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
-                    oT[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[kk], oT[d], 0, 0, 0);
+                    const u16x8_t a = __builtin_bit_cast(u16x8_t, u32x4_t{lo[0], lo[1], hi[0], hi[1]});
+                    oT[d] = tile_mfma<T>(a, pb[kk], oT[d]);
                 }
             }
             okm = okm_next;
@@ -1265,29 +1300,31 @@ __device__ void attn_mfma_body(const TileDesc& t, int kvh, int G, int H,
         l = l * a + __expf(sv2 - mm);
     }
     const float inv = l > 0.f ? a / l : 0.f;
-    half_t* dst = out + (int64_t)tok * out_tok_stride + (int64_t)h * VHD;
+    T* dst = out + (int64_t)tok * out_tok_stride + (int64_t)h * VHD;
 #pragma unroll
     for (int d = 0; d < DT; ++d)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
-            half_t v4[4];
+            uint16_t v4[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v4[i] = (half_t)(oT[d][4 * e4 + i] * inv);
+            for (int i = 0; i < 4; ++i) v4[i] = tile_round<T>(oT[d][4 * e4 + i] * inv);
             *reinterpret_cast<uint2*>(dst + d * 32 + 8 * e4 + 4 * hh) =
                 *reinterpret_cast<const uint2*>(v4);
         }
 }
 
-// Tile body for a dtype: the matrix-core tile for fp16 (NW waves of 32 query
-// rows), the VALU tile (kTileRows rows, 256 threads) otherwise.
+// Tile body for a dtype: the matrix-core tile for fp16 and bf16 (NW waves of 32
+// query rows), the VALU tile (kTileRows rows, 256 threads) otherwise.
 template <typename T, int VHD>
 constexpr bool mfma_tile() {
-    return std::is_same<T, half_t>::value && VHD % 32 == 0;
+    return (std::is_same<T, half_t>::value || std::is_same<T, uint16_t>::value) && VHD % 32 == 0;
 }
 // Query rows per workgroup of the tile body used for dtype T.
 template <typename T>
 static int tile_rows_for(int vhd, int nw = 4) {
-    return std::is_same<T, half_t>::value && vhd % 32 == 0 ? 32 * nw : kTileRows;
+    return (std::is_same<T, half_t>::value || std::is_same<T, uint16_t>::value) && vhd % 32 == 0
+               ? 32 * nw
+               : kTileRows;
 }
 // Threads of a tile workgroup.
 template <typename T, int VHD, int NW>
@@ -1303,7 +1340,7 @@ __device__ __forceinline__ void attn_tile(const TileDesc& t, int kvh, int G, int
                                           T* __restrict__ out, int64_t out_tok_stride,
                                           float* __restrict__ part, int nsplit, int split) {
     if constexpr (mfma_tile<T, VHD>())
-        attn_mfma_body<HD, VHD, PAGED, NW>(t, kvh, G, H, qrot, dk, pk, scale, sink, k0, k1, out,
+        attn_mfma_body<T, HD, VHD, PAGED, NW>(t, kvh, G, H, qrot, dk, pk, scale, sink, k0, k1, out,
                                             out_tok_stride, part, nsplit, split);
     else
         attn_tile_body<T, HD, VHD, PAGED>(t, kvh, G, H, qrot, dk, pk, scale, sink, k0, k1, out,

@@ -911,6 +911,85 @@ def test_paged_bf16(ortmi, oracle, new_max, nbs):
     assert (np.abs(gk - rkc) <= 2.0 ** -7 * np.abs(rkc) + 1e-30).all()
 
 
+def _bf16_tile_tol(ro, vmax):
+    """bf16 matrix-core tile bound: the output's bf16 rounding (2^-8 relative, with
+    margin 2^-7), fp32 accumulation (2e-3), and P rounded to bf16 once before the
+    P V product: each weight moves by at most 2^-9 relative, which moves a weighted
+    average of values within [-vmax, vmax] by at most 2^-8 * 2 vmax."""
+    return 2e-3 + 2.0 ** -7 * np.abs(ro) + 2.0 ** -7 * vmax
+
+
+@pytest.mark.parametrize("B,S,H,KV,past,cap,inplace", [
+    (1, 512, 12, 2, 0, 640, True),     # the decoder's 512-token prompt
+    (2, 300, 32, 8, 200, 600, True),   # a chunk after cached rows, shared buffer
+    (1, 96, 8, 2, 40, 40, False),      # growing contract
+])
+def test_gqa_prefill_bf16_matrix_cores(ortmi, oracle, B, S, H, KV, past, cap, inplace):
+    """bf16 GQA prefill on the matrix cores (S^T = K Q^T and O^T += V^T P^T with
+    v_mfma_f32_32x32x16_bf16) at the decoder's size, RoPE in the op, against the
+    oracle run in fp32 on the same bf16 values with bf16 rounding of the RoPE'd
+    rows: outputs within _bf16_tile_tol, cached and new V rows bit-exact, new K rows
+    within one bf16 ulp."""
+    import torch
+
+    rng = np.random.default_rng(500 + S + past)
+    hd = 128
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16)  # noqa: E731
+    q, k, v = (bf(0.5 * rng.standard_normal((B, S, n * hd))) for n in (H, KV, KV))
+    pk, pv = (bf(0.5 * rng.standard_normal((B, KV, cap, hd))) for _ in range(2))
+    c, s_ = refs.rotary_caches(4096, hd, 1e6)
+    cos, sin = bf(c), bf(s_)
+    total = past + S
+    dpk, dpv = pk.cuda(), pv.cuda()
+    kw = dict(present_key=dpk, present_value=dpv) if inplace else {}
+    out, prk, prv = ortmi.group_query_attention(
+        q.cuda(), k.cuda(), v.cuda(), dpk, dpv, dev(np.full(B, total - 1, np.int32)), total,
+        cos.cuda(), sin.cuda(), num_heads=H, kv_num_heads=KV, do_rotary=1, **kw)
+    f = lambda x: x.float().numpy()  # noqa: E731
+    ro, rk, rv, _ = oracle.gqa(f(q), f(k), f(v), f(pk), f(pv), total, H, KV, cos=f(cos),
+                               sin=f(sin), round16=2)
+    assert out.dtype == torch.bfloat16
+    got = out.float().cpu().numpy()
+    tol = _bf16_tile_tol(ro, max(np.abs(f(v)).max(), np.abs(f(pv)).max()))
+    assert (np.abs(got - ro) <= tol).all(), f"gqa bf16 prefill: max diff {np.abs(got - ro).max():.3e}"
+    gv, gk = prv.float().cpu().numpy(), prk.float().cpu().numpy()
+    np.testing.assert_array_equal(gv[:, :, :total], rv[:, :, :total])
+    assert (np.abs(gk[:, :, :total] - rk[:, :, :total]) <= _ulp_bf16(rk[:, :, :total])).all()
+
+
+def test_paged_prefill_bf16_matrix_cores(ortmi, oracle):
+    """bf16 PagedAttention at the mixed-batch shape's head layout (H 32, KV 8, head
+    128, block 16): four sequences prefill 256-token chunks on the matrix-core tiles
+    and eight decode one token, against the oracle in fp32 on the same bf16 values:
+    outputs within _bf16_tile_tol, the written cache slots bit-exact."""
+    import torch
+
+    rng = np.random.default_rng(77)
+    H, KV, d, blk = 32, 8, 128, 16
+    new_lens = np.array([256] * 4 + [1] * 8, np.int32)
+    batch = len(new_lens)
+    past = rng.integers(0, 700, size=batch).astype(np.int32)
+    maxb = int((past + new_lens).max() + blk - 1) // blk
+    nb = batch * maxb
+    cum = np.concatenate([[0], np.cumsum(new_lens)]).astype(np.int32)
+    nt = int(cum[-1])
+    bf = lambda a: torch.from_numpy((a * 0.5).astype(np.float32)).to(torch.bfloat16)  # noqa: E731
+    q, k, v = (bf(rng.standard_normal((nt, n * d))) for n in (H, KV, KV))
+    kc, vc = (bf(rng.standard_normal((nb, blk, KV, d))) for _ in range(2))
+    bt = rng.permutation(nb).astype(np.int32).reshape(batch, maxb)
+    dkc, dvc = kc.cuda(), vc.cuda()
+    out = ortmi.paged_attention(q.cuda(), k.cuda(), v.cuda(), dkc, dvc, dev(cum), dev(past),
+                                dev(bt), num_heads=H, kv_num_heads=KV)
+    f = lambda t: t.float().numpy()  # noqa: E731
+    ro, rkc, rvc = oracle.paged_attention(f(q), f(k), f(v), f(kc), f(vc), cum, past, bt, H, KV)
+    got = out.float().cpu().numpy()
+    assert out.dtype == torch.bfloat16
+    tol = _bf16_tile_tol(ro, max(np.abs(f(v)).max(), np.abs(f(vc)).max()))
+    assert (np.abs(got - ro) <= tol).all(), f"paged bf16: max diff {np.abs(got - ro).max():.3e}"
+    np.testing.assert_array_equal(dvc.float().cpu().numpy(), rvc)
+    np.testing.assert_array_equal(dkc.float().cpu().numpy(), rkc)
+
+
 def test_paged_mixed_batch_reduced(ortmi, oracle):
     """Mixed prefill + decode: 2 sequences prefill 40-token chunks, 6 decode one token,
     block 16, 32/8 heads, hd 128 (a reduced form of the mixed-batch config)."""
