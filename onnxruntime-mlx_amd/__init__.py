@@ -110,6 +110,7 @@ SIGNATURES = {
     "ortmi_sigmoid": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp]),
     "ortmi_argmax_rows_workspace_size": (_sz, [_i64, _i64]),
     "ortmi_argmax_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp, _sz, _vp]),
+    "ortmi_argmax_axis": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
     "ortmi_cast": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i64, _vp]),
 }
 

@@ -247,6 +247,7 @@ bool is_half(int dt) {
     return dt == ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT16 || dt == ONNX_TENSOR_ELEMENT_DATA_TYPE_BFLOAT16;
 }
 std::string fmt(const char* s) { return s; }
+std::string fmt(const std::string& s) { return s; }
 
 #define REQUIRE(cond, msg) \
     do {                   \
@@ -408,8 +409,26 @@ std::string claim_paged(const NodeDesc& n, const GraphIR& g) {
     const int64_t vhd = n.attr_int("v_head_size", 0) ? n.attr_int("v_head_size", 0) : hd;
     REQUIRE(vhd == hd || (latent && vhd % 16 == 0 && vhd <= hd),
             "unsupported v_head_size");
-    for (const char* k : {"k_cache_dtype", "v_cache_dtype"})
-        REQUIRE(n.attr_str(k, "").empty(), "quantized KV caches are not supported");
+    // Query, key and key cache (and value and value cache unless LATENT) share the
+    // output's float dtype (attention.rs:2800-2815).
+    auto* o = out_val(g, n, 0);
+    REQUIRE(!o || o->dtype == q->dtype, "the output must share the query dtype");
+    for (int i : {1, 3}) {
+        auto* t = val(g, n, i);
+        REQUIRE(t && t->dtype == q->dtype, "key and key_cache must share the query dtype");
+    }
+    if (!latent)
+        for (int i : {2, 4}) {
+            auto* t = val(g, n, i);
+            REQUIRE(t && t->dtype == q->dtype, "value and value_cache must share the query dtype");
+        }
+    // A cache dtype attribute names the caches' storage; the caches themselves must be
+    // the activation dtype (checked above), so only sub-byte packings are declined
+    // outright, as the reference does (attention.rs:2759-2765).
+    for (const char* k : {"k_cache_dtype", "v_cache_dtype"}) {
+        const std::string cd = n.attr_str(k, "");
+        REQUIRE(cd != "int4" && cd != "float4e2m1", std::string(k) + " sub-byte packing is unsupported");
+    }
     if (n.has_input(10)) {
         auto* sm = val(g, n, 10);
         REQUIRE(sm && sm->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT32, "slot_mapping must be int32");
@@ -554,13 +573,11 @@ std::string claim_argmax(const NodeDesc& n, const GraphIR& g) {
     int64_t axis = n.attr_int("axis", 0);
     if (axis < 0) axis += r;
     REQUIRE(axis >= 0 && axis < r, "axis out of range");
-    REQUIRE(axis == r - 1, "only the last axis is reduced");
     const int64_t kd = n.attr_int("keepdims", 1);
     REQUIRE(kd == 0 || kd == 1, "keepdims must be 0 or 1");
     const int64_t last = n.attr_int("select_last_index", 0);
     REQUIRE(last == 0 || last == 1, "select_last_index must be 0 or 1");
-    REQUIRE(last == 0, "select_last_index=1 is not supported");
-    REQUIRE(x->dims.back() != 0, "the reduced axis is empty");
+    REQUIRE(x->dims[axis] != 0, "the reduced axis is empty");
     auto* out = out_val(g, n, 0);
     REQUIRE(!out || out->dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64, "output must be int64");
     return "";

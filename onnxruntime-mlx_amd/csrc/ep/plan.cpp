@@ -1296,21 +1296,36 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
                      "Gather");
         return;
     }
-    if (op == "ArgMax") {  // last axis, lowest index on ties (claim_argmax)
+    if (op == "ArgMax") {  // any axis, either tie rule (claim_argmax)
         Tensor x = need(0);
-        if (x.dims.empty()) fail("ArgMax: scalar input", ORT_INVALID_ARGUMENT);
-        const int64_t cols = x.dims.back();
-        if (cols <= 0) fail("ArgMax: the reduced axis is empty", ORT_INVALID_ARGUMENT);
-        const int64_t rows = x.numel() / cols;
-        std::vector<int64_t> od(x.dims.begin(), x.dims.end() - 1);
-        if (n.attr_int("keepdims", 1)) od.push_back(1);
+        const int64_t r = (int64_t)x.dims.size();
+        if (r == 0) fail("ArgMax: scalar input", ORT_INVALID_ARGUMENT);
+        int64_t axis = n.attr_int("axis", 0);
+        if (axis < 0) axis += r;
+        if (axis < 0 || axis >= r) fail("ArgMax: axis out of range", ORT_INVALID_ARGUMENT);
+        const int64_t dim = x.dims[axis];
+        if (dim <= 0) fail("ArgMax: the reduced axis is empty", ORT_INVALID_ARGUMENT);
+        int64_t outer = 1, inner = 1;
+        for (int64_t i = 0; i < axis; ++i) outer *= x.dims[i];
+        for (int64_t i = axis + 1; i < r; ++i) inner *= x.dims[i];
+        const bool last = n.attr_int("select_last_index", 0) != 0;
+        std::vector<int64_t> od;
+        for (int64_t i = 0; i < r; ++i)
+            if (i != axis) od.push_back(x.dims[i]);
+            else if (n.attr_int("keepdims", 1)) od.push_back(1);
         Tensor& O = out_tensor(outname(0), ONNX_TENSOR_ELEMENT_DATA_TYPE_INT64, od, a, ctx);
-        if (rows == 0) return;
-        const size_t wsb = ortmi_argmax_rows_workspace_size(rows, cols);
-        void* ws = wsb ? workspace(wsb) : nullptr;
-        check_kernel(ortmi_argmax_rows(x.ptr, (int64_t*)O.ptr, rows, cols, kdt(x.dtype), ws, wsb,
-                                       st),
-                     "ArgMax");
+        if (outer * inner == 0) return;
+        if (inner == 1 && !last && outer <= 65535) {  // greedy decoding: two passes per row
+            const size_t wsb = ortmi_argmax_rows_workspace_size(outer, dim);
+            void* ws = wsb ? workspace(wsb) : nullptr;
+            check_kernel(ortmi_argmax_rows(x.ptr, (int64_t*)O.ptr, outer, dim, kdt(x.dtype), ws,
+                                           wsb, st),
+                         "ArgMax");
+        } else {
+            check_kernel(ortmi_argmax_axis(x.ptr, (int64_t*)O.ptr, outer, dim, inner, last ? 1 : 0,
+                                           kdt(x.dtype), st),
+                         "ArgMax");
+        }
         return;
     }
     if (op == "GatherBlockQuantized") {

@@ -149,8 +149,9 @@ __global__ void sigmoid_kernel(const T* __restrict__ x, T* __restrict__ o, int64
     o[i] = from_f32<T>(1.0f / (1.0f + __expf(-to_f32(x[i]))));
 }
 
-// First index of the maximum of each row; NaNs are skipped.
-template <typename T>
+// Index of the maximum of each row, the first on ties (the last with LAST, ONNX
+// select_last_index = 1); NaNs are skipped, an all-NaN row gives 0.
+template <typename T, bool LAST = false>
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ x,
                                                           int64_t* __restrict__ out,
                                                           int64_t cols) {
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ 
     int64_t bi = -1;
     for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
         const float v = to_f32(xr[c]);
-        if (v > best || (bi < 0 && v == best)) {
+        if (v > best || (v == best && (LAST || bi < 0))) {
             best = v;
             bi = c;
         }
@@ -176,7 +177,8 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ 
             const int64_t oi = si[threadIdx.x + s];
             const float mv = sv[threadIdx.x];
             const int64_t mi = si[threadIdx.x];
-            const bool take = oi >= 0 && (mi < 0 || ov > mv || (ov == mv && oi < mi));
+            const bool take =
+                oi >= 0 && (mi < 0 || ov > mv || (ov == mv && (LAST ? oi > mi : oi < mi)));
             if (take) {
                 sv[threadIdx.x] = ov;
                 si[threadIdx.x] = oi;
@@ -185,6 +187,30 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ 
         __syncthreads();
     }
     if (threadIdx.x == 0) out[row] = si[0] < 0 ? 0 : si[0];
+}
+
+// Arg max along the middle axis of x viewed as [outer, dim, inner] (inner > 1):
+// one thread per (outer, inner) column walks the axis, consecutive threads reading
+// consecutive inner elements. Ties and NaNs as argmax_rows_kernel.
+template <typename T, bool LAST>
+__global__ __launch_bounds__(256) void argmax_axis_kernel(const T* __restrict__ x,
+                                                          int64_t* __restrict__ out,
+                                                          int64_t cols_total, int64_t dim,
+                                                          int64_t inner) {
+    const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (col >= cols_total) return;
+    const int64_t o = col / inner, i = col - o * inner;
+    const T* p = x + o * dim * inner + i;
+    float best = -INFINITY;
+    int64_t bi = -1;
+    for (int64_t d = 0; d < dim; ++d) {
+        const float v = to_f32(p[d * inner]);
+        if (v > best || (v == best && (LAST || bi < 0))) {
+            best = v;
+            bi = d;
+        }
+    }
+    out[col] = bi < 0 ? 0 : bi;
 }
 
 // Block-wide argmax of (value, index) pairs held one per thread; the lowest index
@@ -486,6 +512,24 @@ extern "C" int ortmi_argmax_rows(const void* x, int64_t* out, int64_t rows, int6
     return check_launch("argmax_rows")
     ORTMI_DISPATCH_FLOAT(dtype, ORTMI_ARGMAX)
 #undef ORTMI_ARGMAX
+}
+
+extern "C" int ortmi_argmax_axis(const void* x, int64_t* out, int64_t outer, int64_t dim,
+                                 int64_t inner, int32_t select_last_index, int32_t dtype,
+                                 void* stream) {
+    ORTMI_REQUIRE(outer >= 0 && inner >= 0 && dim > 0, "ArgMax: bad shape");
+    ORTMI_REQUIRE(select_last_index == 0 || select_last_index == 1,
+                  "ArgMax: select_last_index must be 0 or 1");
+    if (outer == 0 || inner == 0) return ORTMI_OK;
+    ORTMI_REQUIRE(x && out, "ArgMax: null tensor");
+    ORTMI_REQUIRE(outer <= INT32_MAX && outer * dim <= (INT64_MAX / 4) / (inner > 0 ? inner : 1),
+                  "ArgMax: tensor too large");
+    hipStream_t st = as_stream(stream);
+    const bool last = select_last_index != 0;
+    const int64_t cols = outer * inner;
+#define ORTMI_ARGMAX_AXIS(T)                                                                        if (inner == 1) {                                                                                   if (last)                                                                                           hipLaunchKernelGGL((argmax_rows_kernel<T, true>), dim3((unsigned)outer), dim3(256),                                0, st, static_cast<const T*>(x), out, dim);                              else                                                                                                hipLaunchKernelGGL((argmax_rows_kernel<T, false>), dim3((unsigned)outer),                                          dim3(256), 0, st, static_cast<const T*>(x), out, dim);               } else {                                                                                            const unsigned blocks = (unsigned)((cols + 255) / 256);                                         if (last)                                                                                           hipLaunchKernelGGL((argmax_axis_kernel<T, true>), dim3(blocks), dim3(256), 0, st,                                  static_cast<const T*>(x), out, cols, dim, inner);                        else                                                                                                hipLaunchKernelGGL((argmax_axis_kernel<T, false>), dim3(blocks), dim3(256), 0, st,                                 static_cast<const T*>(x), out, cols, dim, inner);                    }                                                                                               return check_launch("argmax_axis")
+    ORTMI_DISPATCH_FLOAT(dtype, ORTMI_ARGMAX_AXIS)
+#undef ORTMI_ARGMAX_AXIS
 }
 
 extern "C" int ortmi_cast(const void* x, int32_t src_dtype, void* y, int32_t dst_dtype, int64_t n,

@@ -336,11 +336,12 @@ def test_norm_claims():
     (F16, dict(axis=2, keepdims=1), I64, True),
     (F32, dict(axis=-1), I64, True),          # keepdims defaults to 1
     (hx.BFLOAT16, dict(axis=2, keepdims=0, select_last_index=0), I64, True),
-    (F16, dict(axis=1), I64, False),          # only the last axis
-    (F16, dict(axis=0), I64, False),          # the default axis is 0
+    (F16, dict(axis=1), I64, True),           # any axis (reduction.rs:582-630)
+    (F16, dict(axis=0), I64, True),           # the default axis is 0
     (F16, dict(axis=3), I64, False),          # out of range (reduction.rs:610-617)
     (F16, dict(axis=-1, keepdims=2), I64, False),
-    (F16, dict(axis=-1, select_last_index=1), I64, False),
+    (F16, dict(axis=-1, select_last_index=1), I64, True),
+    (F16, dict(axis=-1, select_last_index=2), I64, False),
     (I32, dict(axis=-1), I64, False),         # float inputs only
 ])
 def test_argmax_claim_predicate(dtype, attrs, out_dtype, claimed):
@@ -605,17 +606,26 @@ def test_layer_partitions_inference_needs_a_residual_add_in_every_layer(monkeypa
     (F16, 512, {}, False),
     (F16, 128, dict(local_window_size=64), False),         # declined by the reference too
     (F16, 128, dict(softcap=30.0), False),
+    # cache dtype names: the caches are the activation dtype, only sub-byte packings
+    # are declined (attention.rs:2759-2765)
+    (F16, 128, dict(k_cache_dtype="int8", v_cache_dtype="float8e4m3fn"), True),
+    (F16, 128, dict(k_cache_dtype="int4"), False),
+    (F16, 128, dict(v_cache_dtype="float4e2m1"), False),
+    (F16, 128, dict(cache_tensor=hx.INT8), False),         # caches must share the dtype
+    (F16, 128, dict(cache_tensor=hx.BFLOAT16), False),
 ])
 def test_paged_attention_claim_forms(dtype, d, attrs, claimed):
-    """PagedAttention claim (rust/src/ops/attention.rs:2746-2977): any float dtype and
-    the head sizes the kernels take."""
+    """PagedAttention claim (rust/src/ops/attention.rs:2746-2977): any float dtype, the
+    head sizes the kernels take, caches in the activation dtype."""
     g = hx.Graph()
     H, KV, nb, blk, batch, maxb = 4, 2, 8, 4, 2, 4
+    attrs = dict(attrs)
+    cdt = attrs.pop("cache_tensor", dtype)
     g.value("q", dtype, [-1, H * d])
     g.value("k", dtype, [-1, KV * d])
     g.value("v", dtype, [-1, KV * d])
-    g.value("kc", dtype, [nb, blk, KV, d])
-    g.value("vc", dtype, [nb, blk, KV, d])
+    g.value("kc", cdt, [nb, blk, KV, d])
+    g.value("vc", cdt, [nb, blk, KV, d])
     g.value("cum", I32, [batch + 1])
     g.value("past", I32, [batch])
     g.value("bt", I32, [batch, maxb])

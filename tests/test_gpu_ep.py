@@ -232,6 +232,51 @@ def test_ep_argmax_node(ortmi, hx, dtype, V, keepdims):
     np.testing.assert_array_equal(y.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("dtype,axis,keepdims,last", [
+    (np.float16, 0, 1, 0),
+    (np.float32, 1, 0, 1),
+    (np.float16, -1, 1, 1),
+    ("bf16", 1, 1, 0),
+    (np.float32, -1, 0, 1),
+])
+def test_ep_argmax_node_any_axis_and_tie_rule(ortmi, hx, dtype, axis, keepdims, last):
+    """ArgMax over a leading, middle or last axis, with select_last_index 0 (the
+    first maximum) and 1 (the last), through the EP against numpy: argmax of the
+    values with NaN read as -inf, on the reversed axis for the last index. Values
+    are drawn from 7 levels so that most slices tie; a NaN is planted."""
+    import torch
+
+    rng = np.random.default_rng(31 + axis + 3 * last)
+    shape = (6, 50, 37)
+    x = rng.integers(0, 7, size=shape).astype(np.float32)
+    x[1, 2, 3] = np.nan
+    if dtype == "bf16":
+        onnx_dt, xt = hx.BFLOAT16, torch.from_numpy(x).to(torch.bfloat16).cuda()
+    else:
+        onnx_dt = hx.FLOAT16 if dtype == np.float16 else hx.FLOAT
+        xt = torch.from_numpy(x.astype(dtype)).cuda()
+    ax = axis % 3
+    oshape = tuple(1 if i == ax else d for i, d in enumerate(shape)) if keepdims else \
+        tuple(d for i, d in enumerate(shape) if i != ax)
+    g = hx.Graph()
+    g.value("x", onnx_dt, list(shape))
+    g.value("y", hx.INT64, list(oshape))
+    g.node("ArgMax", ["x"], ["y"], axis=axis, keepdims=keepdims, select_last_index=last)
+    g.io(["x"], ["y"])
+    sess = hx.Session(g)
+    assert sess.partitions() == [[0]]
+    y = torch.full(oshape, -1, dtype=torch.int64, device="cuda")
+    sess.bind_output("y", y)
+    sess.run({"x": (xt, onnx_dt)})
+    torch.cuda.synchronize()
+    xv = np.where(np.isnan(x), -np.inf, x)
+    if last:
+        want = shape[ax] - 1 - np.argmax(np.flip(xv, axis=ax), axis=ax)
+    else:
+        want = np.argmax(xv, axis=ax)
+    np.testing.assert_array_equal(y.cpu().numpy(), want.reshape(oshape))
+
+
 def test_ep_decode_program_argmax_node(ortmi, dec, monkeypatch):
     """A decoder graph that ends in ArgMax: its one-token steps run as the decode
     program with the program's argmax written to the ArgMax output (ORTMI_EP_PROGRAM
