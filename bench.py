@@ -2,7 +2,8 @@
 """Benchmark of the MI355X execution provider's hot path on one GPU.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload all|gemv|gemm|gqa|gqa_growing|gqa_shared|paged|decoder|copy]
+                    [--workload all|gemv|gemm|gqa|gqa_growing|gqa_shared|paged|decoder|
+                                decoder_qwen05|copy]
 
 Primary line: int4 MatMulNBits decode GEMV (K=4096, N=11008, block 32, fp32
 activations) as achieved HBM GB/s. A step is one MatMulNBits call; consecutive
@@ -18,6 +19,8 @@ Secondary measurements (same JSON line, "secondary"):
   with the shared KV contract;
 - the PagedAttention mixed batch;
 - the int4 decoder (decode tokens/s and the prompt prefill).
+On request (--workload decoder_qwen05, not part of "all"): the Qwen2.5-0.5B decoder
+layout, decode program against the op-by-op path.
 
 cpu_baseline: the same GEMV (and, for the decoder, its decode steps) on this
 machine's host cores through the oracle's fp32 AVX2 MatMulNBits (oracle/fast.c,
@@ -447,6 +450,46 @@ def measured_traffic(profile: str):
     return int(m.group(1)) if m else None
 
 
+def bench_decoder_qwen05(torch, prompt_len=512, gen=128):
+    """The Qwen2.5-0.5B decoder layout (24 layers, hidden 896, 14/2 heads of 64,
+    SwiGLU 4864, vocab 151936, random int4 weights) through the EP, fed as in
+    bench_decoder (host ids, ArgMax node): greedy decode on the decode program
+    (ORTMI_EP_PROGRAM=require) and op by op (ORTMI_EP_PROGRAM=0)."""
+    import numpy as np
+
+    dec = importlib.import_module("ortmi.decoder")
+    cfg = dec.DecoderConfig(layers=24, hidden=896, heads=14, kv_heads=2, head_dim=64,
+                            inter=4864, vocab=151936, max_pos=4096)
+    w = dec.make_weights(cfg, seed=4)
+    prompt = np.random.default_rng(44).integers(0, cfg.vocab, size=prompt_len)
+    out, toks = {}, {}
+    prev = os.environ.get("ORTMI_EP_PROGRAM")
+    try:
+        for mode, key in (("require", "program"), ("0", "op_path")):
+            os.environ["ORTMI_EP_PROGRAM"] = mode
+            r = dec.DecoderRunner(cfg, w, cap=prompt_len + gen, max_prompt=prompt_len,
+                                  argmax_node=True, host_feeds=True)
+            r.generate(prompt[:16], steps=4)
+            tokens, ttft, times = r.generate(prompt, steps=gen)
+            toks[key] = tokens
+            out[key] = dict(decode_tok_s=round(len(times) / float(np.sum(times)), 1),
+                            p50_ms_per_token=round(float(np.median(times)) * 1e3, 3),
+                            prefill_ms=round(ttft * 1e3, 2))
+            del r
+            torch.cuda.empty_cache()
+    finally:
+        if prev is None:
+            os.environ.pop("ORTMI_EP_PROGRAM", None)
+        else:
+            os.environ["ORTMI_EP_PROGRAM"] = prev
+    out["config"] = ("Qwen2.5-0.5B layout: 24 layers, hidden 896, 14/2 heads, hd 64, SwiGLU 4864, "
+                     "vocab 151936, int4 block 32 random weights; 512-token prompt then "
+                     f"{gen} greedy tokens, batch 1, host-fed ids, ArgMax node")
+    out["same_tokens"] = toks["program"] == toks["op_path"]
+    out["first_tokens"] = toks["program"][:8]
+    return out
+
+
 def cpu_baseline_decoder(budget_s=15.0, prompt_len=512):
     """The same int4 decoder's greedy decode steps on the host cores, the way a CPU
     runs them: every MatMulNBits through the oracle's fp32 AVX2 kernel (fast.c,
@@ -527,7 +570,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="all",
                     choices=["all", "gemv", "gemm", "gqa", "gqa_growing", "gqa_shared", "paged",
-                             "decoder", "copy"])
+                             "decoder", "decoder_qwen05", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -650,6 +693,11 @@ def main():
             cpu_dec = cpu_baseline_decoder()
             secondary["int4_decoder"]["cpu_baseline"] = cpu_dec
             log(f"decoder cpu baseline: {cpu_dec['value']} tok/s on {cpu_dec['cores']} threads")
+
+    if wl == "decoder_qwen05":  # not part of "all": a second decoder layout on request
+        secondary["int4_decoder_qwen05_layout"] = r = bench_decoder_qwen05(torch)
+        log(f"qwen0.5b layout: program {r['program']['decode_tok_s']} tok/s, op path "
+            f"{r['op_path']['decode_tok_s']} tok/s, same tokens {r['same_tokens']}")
 
     if gemv is None:
         print(json.dumps({"workload": wl, "secondary": secondary}))

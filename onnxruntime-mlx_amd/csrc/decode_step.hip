@@ -83,7 +83,6 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kSC1 = 16;               // buffer cache policy: device-coherent (sc1)
 constexpr int kGMax = 8;               // query heads per KV head
-constexpr int kKeySlots = kWaves * 4;  // key rows per attention step (4 lane groups per wave)
 constexpr int kKvRing = 4;             // attention steps in flight in registers
 constexpr int kIChunksPerLane = 5;     // down_proj: K = I <= 5 * 64 * 32 = 10240
 constexpr int kMaxLayers = 64;
@@ -346,22 +345,24 @@ __device__ __forceinline__ bool norm_poll(const uint32_t* src, const half_t* row
     return true;
 }
 
-// 16 lanes (dims 8*li .. 8*li+7 of one head) rotate their 8 values, non-interleaved
-// pairs (i, i + half) over dims [0, 2*half), with the cos/sin row cs/sn [half]; the
-// partner lane is li ^ (half / 8) inside the same 16-lane group (half is
-// a multiple of 8 and at most 64).
+// LPR lanes (dims 8*li .. 8*li+7 of one head of LPR * 8 dims) rotate their 8
+// values, non-interleaved pairs (i, i + half) over dims [0, 2*half), with the
+// cos/sin row cs/sn [half]; the partner lane is li +- half / 8 inside the same
+// LPR-lane group (half is a multiple of 8 and at most 4 * LPR).
+template <int LPR>
 __device__ __forceinline__ void rope8(float (&x)[8], int li, int half, const float* cs,
                                       const float* sn) {
     if (half == 0) return;
     const int off = half / 8;
     float px[8];
-    if (off == 8) {
+    if (LPR == 16 && off == 8) {
         // Partner li ^ 8 inside the 16-lane row: a DPP row rotation by 8.
 #pragma unroll
         for (int i = 0; i < 8; ++i) px[i] = dpp_mov<0x128>(x[i]);
     } else {
         const int lane = threadIdx.x & 63;
-        const int partner = (lane & ~15) | ((li < off || (li >= 2 * off)) ? li + off : li - off);
+        const int partner = (lane & ~(LPR - 1)) |
+                            (((li < off || (li >= 2 * off)) ? li + off : li - off) & (LPR - 1));
 #pragma unroll
         for (int i = 0; i < 8; ++i) px[i] = __shfl(x[i], partner & 63, 64);
     }
@@ -619,16 +620,20 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         // rows sit in LDS, requested right after the previous layer's attention, so
         // the wait for q/k/v never queues behind them. Split 0 of each head merges
         // the others' partials (tagged 64-bit words: value, tag) into the output.
+        // A key row is LPR lanes of 8 dims (16 lanes for head 128, 8 for head 64);
+        // a wave holds GPW keys per step.
+        constexpr int LPR = HD / 8, GPW = 64 / LPR, KEYS = kWaves * GPW;
+        const int lr = lane % LPR, ag = lane / LPR;
         const int NS = p.ns, a = wg - NC;
         const int h = a / NS, s = a % NS, kvh = h / p.G;
         const int ks = (total + NS - 1) / NS;
         const int k0 = s * ks, k1 = min(k0 + ks, total);
-        const int steps = k1 > k0 ? (k1 - k0 + kKeySlots - 1) / kKeySlots : 0;
+        const int steps = k1 > k0 ? (k1 - k0 + KEYS - 1) / KEYS : 0;
         const uint32_t kv_bytes = (uint32_t)KV * p.cap * HD * 2;
-        const int slot = wave * 4 + grp;  // key slot of this lane group
+        const int slot = wave * GPW + ag;  // key slot of this lane group
         auto kv_off = [&](int t) -> uint32_t {
-            const int key = k0 + slot + t * kKeySlots;
-            return key < k1 && key < ctx ? ((uint32_t)(kvh * p.cap + key) * HD + li16 * 8) * 2u
+            const int key = k0 + slot + t * KEYS;
+            return key < k1 && key < ctx ? ((uint32_t)(kvh * p.cap + key) * HD + lr * 8) * 2u
                                          : kv_bytes;
         };
         auto kv_fetch = [&](const OrtmiDecoderLayer& ly) {
@@ -658,9 +663,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                     ringv[r] = ld128<kCachePolicyNT>(rv, off);
                 }
             }
-            const uint32_t off[3] = {(uint32_t)(h * HD + li16 * 8) * 4u,
-                                     (uint32_t)((H + kvh) * HD + li16 * 8) * 4u,
-                                     (uint32_t)((H + KV + kvh) * HD + li16 * 8) * 4u};
+            const uint32_t off[3] = {(uint32_t)(h * HD + lr * 8) * 4u,
+                                     (uint32_t)((H + kvh) * HD + lr * 8) * 4u,
+                                     (uint32_t)((H + KV + kvh) * HD + lr * 8) * 4u};
             uint4 qkv3[3];
             const bool ok = poll_units<3>(rsrc(f_qkv, (uint32_t)NQ * 4u), off, 7u, f, qkv3);
             DPROG_STAMP(1 + l * 8 + 2);
@@ -676,8 +681,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                     vn[e] = (float)vh[e];
                 }
             }
-            rope8(q, li16, p.half, s_cos, s_sin);
-            rope8(kn, li16, p.half, s_cos, s_sin);
+            rope8<LPR>(q, lr, p.half, s_cos, s_sin);
+            rope8<LPR>(kn, lr, p.half, s_cos, s_sin);
             uint32_t qw[4], kw_new[4];
             {
                 half_t q8[8], k8[8];
@@ -698,9 +703,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             // a flat store would also count against the LDS counter, and the LDS
             // reads below would wait for it to complete.
             {
-                const bool app = ok && h % p.G == 0 && ctx >= k0 && ctx < k1 && wave == 0 && grp == 0;
+                const bool app = ok && h % p.G == 0 && ctx >= k0 && ctx < k1 && wave == 0 && ag == 0;
                 const uint32_t ao =
-                    app ? (uint32_t)(((size_t)(kvh * p.cap + ctx) * HD + li16 * 8) * 2) : kv_bytes;
+                    app ? (uint32_t)(((size_t)(kvh * p.cap + ctx) * HD + lr * 8) * 2) : kv_bytes;
                 __builtin_amdgcn_raw_buffer_store_b128(
                     u32x4_t{kw_new[0], kw_new[1], kw_new[2], kw_new[3]}, rk, ao, 0, 0);
                 __builtin_amdgcn_raw_buffer_store_b128(
@@ -710,7 +715,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = 0.f;
             auto attend = [&](const uint4& kr, const uint4& vr, int key) {
-                if (key >= k1) return;  // a whole 16-lane group shares the key
+                if (key >= k1) return;  // a whole LPR-lane group shares the key
                 const bool fresh = key == ctx;
                 const uint32_t kw[4] = {fresh ? kw_new[0] : kr.x, fresh ? kw_new[1] : kr.y,
                                         fresh ? kw_new[2] : kr.z, fresh ? kw_new[3] : kr.w};
@@ -719,7 +724,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 for (int e = 0; e < 4; ++e)
                     d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, qw[e]),
                                                __builtin_bit_cast(half2_t, kw[e]), d, false);
-                const float sc = group_sum<16>(d) * qscale;
+                const float sc = group_sum<LPR>(d) * qscale;
                 const float mn = fmaxf(m, sc);
                 const float fo = m == -INFINITY ? 0.f : exp2f(m - mn);
                 const float pe = exp2f(sc - mn);
@@ -745,7 +750,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 for (int t = 0; t < kPref; ++t) {
                     sc[t] = -INFINITY;
                     if (t < steps) {
-                        const int key = k0 + slot + t * kKeySlots;
+                        const int key = k0 + slot + t * KEYS;
                         const uint4 kr = wreg[t * 64 + kv_lane];
                         const bool fresh = key == ctx;
                         const uint32_t kw[4] = {fresh ? kw_new[0] : kr.x, fresh ? kw_new[1] : kr.y,
@@ -755,7 +760,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                         for (int e = 0; e < 4; ++e)
                             d = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, qw[e]),
                                                        __builtin_bit_cast(half2_t, kw[e]), d, false);
-                        const float sv = group_sum<16>(d) * qscale;
+                        const float sv = group_sum<LPR>(d) * qscale;
                         sc[t] = key < k1 ? sv : -INFINITY;
                         bmax = fmaxf(bmax, sc[t]);
                     }
@@ -764,7 +769,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
 #pragma unroll
                     for (int t = 0; t < kPref; ++t) {
                         if (t < steps) {
-                            const int key = k0 + slot + t * kKeySlots;
+                            const int key = k0 + slot + t * KEYS;
                             const float pe = sc[t] == -INFINITY ? 0.f : exp2f(sc[t] - bmax);
                             lsum += pe;
                             const uint4 vr = wreg[(kPref + t) * 64 + kv_lane];
@@ -781,20 +786,22 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
 #pragma unroll
                 for (int r = 0; r < kKvRing; ++r) {
                     const int t = t0 + r;
-                    if (t < steps) attend(ringk[r], ringv[r], k0 + slot + t * kKeySlots);
+                    if (t < steps) attend(ringk[r], ringv[r], k0 + slot + t * KEYS);
                     const uint32_t off2 = kv_off(t + kKvRing);
                     ringk[r] = ld128<kCachePolicyNT>(rk, off2);
                     ringv[r] = ld128<kCachePolicyNT>(rv, off2);
                 }
             }
             DPROG_STAMP(1 + l * 8 + 4);
-            // Merge the 4 lane groups of the wave (same dims, other keys), then the
+            // Merge the GPW lane groups of the wave (same dims, other keys), then the
             // waves through LDS.
 #pragma unroll
-            for (int sh = 16; sh <= 32; sh <<= 1) {
-                // The two states of lanes l and l ^ sh, by v_permlane16/32_swap; the
-                // merge is symmetric in them.
-                auto sw = [&](float v) { return sh == 16 ? swap16(v) : swap32(v); };
+            for (int sh = LPR; sh <= 32; sh <<= 1) {
+                // The two states of lanes l and l ^ sh (a DPP row rotation by 8, or
+                // v_permlane16/32_swap); the merge is symmetric in them.
+                auto sw = [&](float v) {
+                    return sh == 8 ? LanePair{v, dpp_mov<0x128>(v)} : sh == 16 ? swap16(v) : swap32(v);
+                };
                 const LanePair pm = sw(m), pl = sw(lsum);
                 const float mn = fmaxf(pm.a, pm.b);
                 const float fa = pm.a == -INFINITY ? 0.f : exp2f(pm.a - mn);
@@ -811,9 +818,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 s_am[wave] = m;
                 s_al[wave] = lsum;
             }
-            if (grp == 0) {
+            if (ag == 0) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) sO[wave * HD + li16 * 8 + e] = o[e];
+                for (int e = 0; e < 8; ++e) sO[wave * HD + lr * 8 + e] = o[e];
             }
             if (!all_ok(ok, &s_fail)) return;
             DPROG_STAMP(1 + l * 8 + 5);
@@ -1251,13 +1258,13 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     ORTMI_REQUIRE(d.dtype == ORTMI_F16, "decoder step: fp16 only");
     ORTMI_REQUIRE(d.block_size == 32, "decoder step: block size 32 only");
     ORTMI_REQUIRE(d.layers >= 1 && d.layers <= dprog::kMaxLayers, "decoder step: 1 to 64 layers");
-    ORTMI_REQUIRE(d.head_size == 128, "decoder step: head size 128 only");
+    ORTMI_REQUIRE(d.head_size == 128 || d.head_size == 64, "decoder step: head size 64 or 128");
     ORTMI_REQUIRE(d.num_heads > 0 && d.kv_num_heads > 0 && d.num_heads % d.kv_num_heads == 0 &&
                       d.num_heads / d.kv_num_heads <= dprog::kGMax,
                   "decoder step: at most 8 query heads per KV head");
-    ORTMI_REQUIRE(d.hidden % 256 == 0 && d.hidden <= 2048, "decoder step: hidden % 256 == 0, <= 2048");
-    ORTMI_REQUIRE((d.num_heads * d.head_size) % 256 == 0 && d.num_heads * d.head_size <= 2048,
-                  "decoder step: num_heads * head_size % 256 == 0, <= 2048");
+    ORTMI_REQUIRE(d.hidden % 32 == 0 && d.hidden <= 2048, "decoder step: hidden % 32 == 0, <= 2048");
+    ORTMI_REQUIRE((d.num_heads * d.head_size) % 32 == 0 && d.num_heads * d.head_size <= 2048,
+                  "decoder step: num_heads * head_size % 32 == 0, <= 2048");
     ORTMI_REQUIRE(d.intermediate % 32 == 0 && d.intermediate <= 64 * 32 * dprog::kIChunksPerLane,
                   "decoder step: intermediate % 32 == 0, <= 10240");
     ORTMI_REQUIRE(d.vocab > 0 && embed_rows > 0 && d.kv_capacity > 0, "decoder step: bad sizes");
@@ -1330,8 +1337,11 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     p.argp = reinterpret_cast<uint64_t*>(ws + s.argp);
 
     const int cpld = d.hidden <= 1536 && d.num_heads * d.head_size <= 1536 ? 3 : 4;
-    const void* fn = cpld == 3 ? (const void*)dprog::decode_program_kernel<128, 3>
-                               : (const void*)dprog::decode_program_kernel<128, 4>;
+    const void* fn = d.head_size == 128
+                         ? (cpld == 3 ? (const void*)dprog::decode_program_kernel<128, 3>
+                                      : (const void*)dprog::decode_program_kernel<128, 4>)
+                         : (cpld == 3 ? (const void*)dprog::decode_program_kernel<64, 3>
+                                      : (const void*)dprog::decode_program_kernel<64, 4>);
     const int ho = d.num_heads * d.head_size;
     const size_t lds = ((size_t)dprog::kWaves * dprog::region_slots(cpld) * 64 + d.hidden / 8 +
                         std::max(ho, d.intermediate) / 8 + d.hidden / 8) * 16 +

@@ -60,14 +60,27 @@ def _step_both(runner, prog, length):
     return ep_logits, host(prog.logits), ep_tok, int(prog.next_id.item()), kv_diff
 
 
-@pytest.mark.parametrize("G", [2, 6])
-def test_decode_program_matches_ep_steps(ortmi, dec, dprog, G):
-    """2-layer decoder (head 128, G query heads per KV head): 10 decode steps after a
-    19-token prompt, the program against the EP path on the same cache."""
-    H = 2 * G
-    cfg = dec.DecoderConfig(layers=2, hidden=H * 128,
-                            heads=H, kv_heads=2, head_dim=128, inter=512, vocab=4096, max_pos=512)
-    w = dec.make_weights(cfg, seed=50 + G)
+@pytest.mark.parametrize("shape", [
+    dict(G=2),
+    dict(G=6),
+    # head 64 (16 query heads over 4 KV heads, hidden 1024)
+    dict(G=4, heads=16, kv_heads=4, head_dim=64, hidden=1024, inter=2816),
+    # the Qwen2.5-0.5B layout: hidden 896 (not a multiple of 256), head 64, 14/2 heads
+    dict(G=7, heads=14, kv_heads=2, head_dim=64, hidden=896, inter=4864),
+])
+def test_decode_program_matches_ep_steps(ortmi, dec, dprog, monkeypatch, shape):
+    """2-layer decoders (head 128 with G query heads per KV head; head 64 at hidden
+    1024 and at the Qwen2.5-0.5B layout, hidden 896): 10 decode steps after a 19-token
+    prompt, the program against the EP's op-by-op path (ORTMI_EP_PROGRAM=0) on the
+    same cache."""
+    monkeypatch.setenv("ORTMI_EP_PROGRAM", "0")
+    G = shape["G"]
+    H = shape.get("heads", 2 * G)
+    hd = shape.get("head_dim", 128)
+    cfg = dec.DecoderConfig(layers=2, hidden=shape.get("hidden", H * 128), heads=H,
+                            kv_heads=shape.get("kv_heads", 2), head_dim=hd,
+                            inter=shape.get("inter", 512), vocab=4096, max_pos=512)
+    w = dec.make_weights(cfg, seed=50 + G + hd)
     runner = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
     prog = dprog.DecodeProgram(cfg, w, runner.kv, 64)
     prompt = np.random.default_rng(G).integers(0, cfg.vocab, size=19)
@@ -80,7 +93,7 @@ def test_decode_program_matches_ep_steps(ortmi, dec, dprog, G):
         length += 1
         scale = float(np.abs(el).max())
         err = float(np.abs(el - pl).max())
-        print(f"G={G} step {step}: max |logit diff| {err:.3e} (|logit| up to {scale:.2f}), "
+        print(f"G={G} hd={hd} step {step}: max |logit diff| {err:.3e} (|logit| up to {scale:.2f}), "
               f"K/V row diff {kvd:.3e}, tokens ep {et} program {pt}", flush=True)
         assert np.isfinite(pl).all()
         assert pt == int(np.argmax(pl)), "program token is not the argmax of its logits"
