@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
                     [--workload all|gemv|gemm|gqa|gqa_growing|gqa_shared|paged|decoder|
-                                decoder_qwen05|copy]
+                                decoder_layouts|copy]
 
 Primary line: int4 MatMulNBits decode GEMV (K=4096, N=11008, block 32, fp32
 activations) as achieved HBM GB/s. A step is one MatMulNBits call; consecutive
@@ -19,8 +19,8 @@ Secondary measurements (same JSON line, "secondary"):
   with the shared KV contract;
 - the PagedAttention mixed batch;
 - the int4 decoder (decode tokens/s and the prompt prefill).
-On request (--workload decoder_qwen05, not part of "all"): the Qwen2.5-0.5B decoder
-layout, decode program against the op-by-op path.
+On request (--workload decoder_layouts, not part of "all"): the Qwen2.5-0.5B and
+Llama-3.2-1B decoder layouts, decode program against the op-by-op path.
 
 cpu_baseline: the same GEMV (and, for the decoder, its decode steps) on this
 machine's host cores through the oracle's fp32 AVX2 MatMulNBits (oracle/fast.c,
@@ -450,16 +450,29 @@ def measured_traffic(profile: str):
     return int(m.group(1)) if m else None
 
 
-def bench_decoder_qwen05(torch, prompt_len=512, gen=128):
-    """The Qwen2.5-0.5B decoder layout (24 layers, hidden 896, 14/2 heads of 64,
-    SwiGLU 4864, vocab 151936, random int4 weights) through the EP, fed as in
-    bench_decoder (host ids, ArgMax node): greedy decode on the decode program
+# Decoder layouts of the reference's documented models besides the headline one:
+# name -> (DecoderConfig fields, description).
+DECODER_LAYOUTS = {
+    "qwen2.5_0.5b": (dict(layers=24, hidden=896, heads=14, kv_heads=2, head_dim=64, inter=4864,
+                          vocab=151936, max_pos=4096),
+                     "Qwen2.5-0.5B layout: 24 layers, hidden 896, 14/2 heads, hd 64, SwiGLU 4864, "
+                     "vocab 151936"),
+    "llama3.2_1b": (dict(layers=16, hidden=2048, heads=32, kv_heads=8, head_dim=64, inter=8192,
+                         vocab=128256, max_pos=4096, rope_base=5e5),
+                    "Llama-3.2-1B layout: 16 layers, hidden 2048, 32/8 heads, hd 64, SwiGLU 8192, "
+                    "vocab 128256"),
+}
+
+
+def bench_decoder_layout(torch, name, prompt_len=512, gen=128):
+    """A decoder layout of DECODER_LAYOUTS (random int4 weights) through the EP, fed
+    as in bench_decoder (host ids, ArgMax node): greedy decode on the decode program
     (ORTMI_EP_PROGRAM=require) and op by op (ORTMI_EP_PROGRAM=0)."""
     import numpy as np
 
     dec = importlib.import_module("ortmi.decoder")
-    cfg = dec.DecoderConfig(layers=24, hidden=896, heads=14, kv_heads=2, head_dim=64,
-                            inter=4864, vocab=151936, max_pos=4096)
+    fields, desc = DECODER_LAYOUTS[name]
+    cfg = dec.DecoderConfig(**fields)
     w = dec.make_weights(cfg, seed=4)
     prompt = np.random.default_rng(44).integers(0, cfg.vocab, size=prompt_len)
     out, toks = {}, {}
@@ -482,8 +495,7 @@ def bench_decoder_qwen05(torch, prompt_len=512, gen=128):
             os.environ.pop("ORTMI_EP_PROGRAM", None)
         else:
             os.environ["ORTMI_EP_PROGRAM"] = prev
-    out["config"] = ("Qwen2.5-0.5B layout: 24 layers, hidden 896, 14/2 heads, hd 64, SwiGLU 4864, "
-                     "vocab 151936, int4 block 32 random weights; 512-token prompt then "
+    out["config"] = (f"{desc}, int4 block 32 random weights; {prompt_len}-token prompt then "
                      f"{gen} greedy tokens, batch 1, host-fed ids, ArgMax node")
     out["same_tokens"] = toks["program"] == toks["op_path"]
     out["first_tokens"] = toks["program"][:8]
@@ -570,7 +582,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="all",
                     choices=["all", "gemv", "gemm", "gqa", "gqa_growing", "gqa_shared", "paged",
-                             "decoder", "decoder_qwen05", "copy"])
+                             "decoder", "decoder_layouts", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -694,10 +706,11 @@ def main():
             secondary["int4_decoder"]["cpu_baseline"] = cpu_dec
             log(f"decoder cpu baseline: {cpu_dec['value']} tok/s on {cpu_dec['cores']} threads")
 
-    if wl == "decoder_qwen05":  # not part of "all": a second decoder layout on request
-        secondary["int4_decoder_qwen05_layout"] = r = bench_decoder_qwen05(torch)
-        log(f"qwen0.5b layout: program {r['program']['decode_tok_s']} tok/s, op path "
-            f"{r['op_path']['decode_tok_s']} tok/s, same tokens {r['same_tokens']}")
+    if wl == "decoder_layouts":  # not part of "all": further decoder layouts on request
+        for name in DECODER_LAYOUTS:
+            secondary[f"int4_decoder_{name}"] = r = bench_decoder_layout(torch, name)
+            log(f"{name}: program {r['program']['decode_tok_s']} tok/s, op path "
+                f"{r['op_path']['decode_tok_s']} tok/s, same tokens {r['same_tokens']}")
 
     if gemv is None:
         print(json.dumps({"workload": wl, "secondary": secondary}))

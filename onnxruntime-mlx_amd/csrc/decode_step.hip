@@ -941,7 +941,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         const int q_g = wave < gq ? wg * gq + wave : ng_q;  // QKV group
         const int o_g = wave < go ? wg * go + wave : ng_o;  // o_proj group
         const int d_row = wave < gd ? wg * gd + wave : D;   // down row
+        // A second down row per wave when the share exceeds one row per wave: read
+        // into registers at the end of D (its wait overlaps the D -> E hop).
+        const int d_row2 = wave + kWaves < gd ? wg * gd + wave + kWaves : D;
         uint32_t sq[CPLD], so[CPLD], sg[kGu][CPLD], sd[kIChunksPerLane];
+        Rows<kIChunksPerLane> dr2;
         // Weights are requested two phases ahead of their use, into slot ranges no
         // phase in between reads: end of A -> gate/up, end of C -> down, end of D ->
         // next QKV, end of E -> next o_proj (region_lo).
@@ -1065,6 +1069,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 DPROG_STAMP(1 + l * 8 + 5);
                 wait_lds();
                 if (l + 1 < p.L) qkv_fetch(s_layers[l + 1]);
+                if (gd > kWaves)
+                    load_rows<64, kIChunksPerLane>(
+                        dr2, weight_ref(ly.down_weight, ly.down_scales, D, CI), d_row2, lane);
             }
 
             // Phase E: down GEMV (K = I).
@@ -1075,6 +1082,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 const float v =
                     wave_sum(row_dot<64, kIChunksPerLane>(wreg + kLo * 64, sd, sA1, sSum1, CI, lane));
                 if (lane == 0 && wave < gd) s_out[wave] = v;
+                if (gd > kWaves) {
+                    const float v2 = wave_sum(rows_dot<64, kIChunksPerLane>(dr2, sA1, sSum1, CI, lane));
+                    if (lane == 0 && wave + kWaves < gd) s_out[wave + kWaves] = v2;
+                }
                 __syncthreads();
                 if (tid < gd && wg * gd + tid < D)
                     put(rsrc(f_dout, (uint32_t)D * 4), wg * gd + tid, s_out[tid], tag);
@@ -1280,7 +1291,8 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     const int nc = nwg - d.num_heads * ns;
     const int gq = ((nq + 3) / 4 + nc - 1) / nc, go = ((d.hidden + 3) / 4 + nc - 1) / nc;
     const int ggu = ((2 * d.intermediate + 3) / 4 + nc - 1) / nc, gd = (d.hidden + nc - 1) / nc;
-    ORTMI_REQUIRE(gq <= dprog::kWaves && go <= dprog::kWaves && gd <= dprog::kWaves && 2 * ggu <= 64,
+    ORTMI_REQUIRE(gq <= dprog::kWaves && go <= dprog::kWaves && gd <= 2 * dprog::kWaves &&
+                      2 * ggu <= 64,
                   "decoder step: projection rows exceed the per-workgroup share");
     ORTMI_REQUIRE((int64_t)d.kv_num_heads * d.kv_capacity * d.head_size * 2 < (int64_t)INT32_MAX &&
                       (int64_t)d.vocab * d.hidden / 2 < (int64_t)INT32_MAX,

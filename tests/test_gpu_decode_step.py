@@ -67,12 +67,15 @@ def _step_both(runner, prog, length):
     dict(G=4, heads=16, kv_heads=4, head_dim=64, hidden=1024, inter=2816),
     # the Qwen2.5-0.5B layout: hidden 896 (not a multiple of 256), head 64, 14/2 heads
     dict(G=7, heads=14, kv_heads=2, head_dim=64, hidden=896, inter=4864),
+    # the Llama-3.2-1B layout: hidden 2048, 32/8 heads of 64, SwiGLU 8192 (two down
+    # rows per wave, gate/up rows beyond the prefetched ones read in the phase)
+    dict(G=4, heads=32, kv_heads=8, head_dim=64, hidden=2048, inter=8192),
 ])
 def test_decode_program_matches_ep_steps(ortmi, dec, dprog, monkeypatch, shape):
     """2-layer decoders (head 128 with G query heads per KV head; head 64 at hidden
-    1024 and at the Qwen2.5-0.5B layout, hidden 896): 10 decode steps after a 19-token
-    prompt, the program against the EP's op-by-op path (ORTMI_EP_PROGRAM=0) on the
-    same cache."""
+    1024 and at the Qwen2.5-0.5B and Llama-3.2-1B layouts): 10 decode steps after a
+    19-token prompt, the program against the EP's op-by-op path (ORTMI_EP_PROGRAM=0)
+    on the same cache."""
     monkeypatch.setenv("ORTMI_EP_PROGRAM", "0")
     G = shape["G"]
     H = shape.get("heads", 2 * G)
