@@ -62,12 +62,15 @@ def load_pkg():
 
 
 MIN_REPLAYS = 100
+MIN_WARM_S = 0.2  # warm-up replays continue until this much wall time has passed
 
 
 def timed_graph(torch, launch_batch, batch_len, steps, warmup):
     """Capture `launch_batch()` (batch_len launches) in a HIP graph and replay it:
-    warm-up replays covering `warmup` launches, then max(100, steps / batch_len)
-    timed replays, each bracketed by HIP events on the replay stream. Returns
+    warm-up replays covering `warmup` launches and at least MIN_WARM_S seconds (the
+    first tenths of a second of a fresh process measured up to 5% slower), then
+    max(100, steps / batch_len) timed replays, each bracketed by HIP events on the
+    replay stream. Returns
     (median gpu ms per launch, wall ms per launch, launches timed)."""
     import numpy as np
 
@@ -82,9 +85,14 @@ def timed_graph(torch, launch_batch, batch_len, steps, warmup):
         launch_batch()
     reps_w = max(1, -(-warmup // batch_len))
     reps = max(MIN_REPLAYS, -(-steps // batch_len))
+    tw = time.perf_counter()
     for _ in range(reps_w):
         g.replay()
     torch.cuda.synchronize()
+    while time.perf_counter() - tw < MIN_WARM_S:
+        for _ in range(reps_w):
+            g.replay()
+        torch.cuda.synchronize()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
     t0 = time.perf_counter()
     ev[0].record()

@@ -404,8 +404,10 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 
     // 2. Past length, the rotary table entries, the second block.
     if (total_dev) vp = min(max(tv - 1, 0), vp_max);
+    // The last split runs to the end: splits are sized over the cached rows, and
+    // the new row (and any rows past nsplit * chunk) fall to it.
     const int nkeys = vp + 1;
-    const int j1 = min(nkeys, j0 + chunk);
+    const int j1 = split == nsplit - 1 ? nkeys : min(nkeys, j0 + chunk);
     const bool rot = cos_c != nullptr;
     const RopeLane rl = rope_fetch<T>(rot ? cos_c + (int64_t)vp * half : q,
                                       rot ? sin_c + (int64_t)vp * half : q, rot ? half : 0, dl,
@@ -1922,12 +1924,14 @@ __global__ __launch_bounds__(256) void rotary_kernel(const T* __restrict__ x,
 
 static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static int gqa_nsplit(int64_t BKV, int64_t nkeys, int& chunk) {
+static int gqa_nsplit(int64_t BKV, int64_t nkeys, int& chunk, int per_cu = 2) {
     // One round of two workgroups per CU (the decode kernel's occupancy): longer
     // splits amortise the epilogue and the merge, and a second round would run
     // with a partial tail (B=8 KV=8 ctx 4097 on MI355X: 512 workgroups 66.5 us,
-    // 1408 workgroups 73 us). Chunks are multiples of 64 keys.
-    const int64_t want = std::max<int64_t>(1, 2L * device_cu_count() / BKV);
+    // 1408 workgroups 73 us). Chunks are multiples of 64 keys. The copying
+    // (growing) form takes two rounds (per_cu = 4): its stores and loads overlap
+    // better over more, shorter splits (B=8 KV=8, 4096 past rows: 61.4 -> 59.2 us).
+    const int64_t want = std::max<int64_t>(1, (int64_t)per_cu * device_cu_count() / BKV);
     int64_t c = (nkeys + want - 1) / want;
     c = ((c + 63) / 64) * 64;
     if (c < 64) c = 64;
@@ -2079,8 +2083,11 @@ static int run_gqa(const void* query, const void* key, const void* value, const 
         if (int rc = check_launch("gqa kv copy")) return rc;
     }
     if (decode_fast) {
+        // Splits over the cached rows; the new row falls to the last split (B=8 KV=8
+        // with 4096 past rows: 8 splits of 512 instead of 7 of 576 and one of 65,
+        // shared contract 35.0-36.0 -> 33.8-34.0 us).
         int chunk = 0;
-        const int ns = gqa_nsplit((int64_t)B * KV, nkeys, chunk);
+        const int ns = gqa_nsplit((int64_t)B * KV, std::max(vp, 1), chunk, fused_copy ? 4 : 2);
         if (int rc = launch_gqa_decode<T, HD>(
                 G, B, KV, ns, chunk, q, k, v, q_stride, kv_stride, static_cast<const T*>(cos_c),
                 static_cast<const T*>(sin_c), half, interleaved, static_cast<const T*>(past_key),
