@@ -379,11 +379,11 @@ def bench_decoder(torch, ortmi, prompt_len=512, gen=128):
     The feeds are placed as a stock ONNX Runtime places them for an EP whose memory
     device is HBM: input ids, seqlens_k and total_sequence_length are host tensors
     that the harness copies to HBM through the EP's data transfer each run; the KV
-    cache and the logits are bound to device buffers (IOBinding). The graph ends in
-    ArgMax(logits), so a greedy step is one EP run over the whole graph for one
-    token plus the read-back of the id the application feeds next, timed on the
-    wall clock with the device synchronised at both ends, as a serving loop sees
-    it. Also reported: the graph without the ArgMax node (the application takes
+    cache and the logits are bound to device buffers and the ArgMax output to host
+    memory (IOBinding). The graph ends in ArgMax(logits), so a greedy step is one
+    EP run over the whole graph for one token, its id landing in host memory for
+    the application to feed next, timed on the wall clock with the device
+    synchronised at both ends, as a serving loop sees it. Also reported: the graph without the ArgMax node (the application takes
     the argmax of the logits on the device), and the ids bound in HBM as well."""
     import importlib
 

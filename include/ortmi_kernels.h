@@ -51,6 +51,22 @@ int ortmi_abi_version(void);
 const char* ortmi_last_error(void);
 
 /*
+ * Host-to-device copies of up to ORTMI_SMALL_COPIES small host buffers (at most
+ * ORTMI_SMALL_COPY_BYTES bytes in all) in one kernel launch on `stream`: the
+ * bytes travel in the launch's arguments, so the host buffers may be pageable and
+ * may be reused as soon as the call returns; dst[i] are device pointers that
+ * receive bytes[i] bytes each, in stream order. Used by the execution provider's
+ * OrtDataTransferImpl::CopyTensors for the per-run feeds of a decode step (input
+ * ids and the two length scalars), which as separate DMA copies cost about 6 us
+ * each. No counterpart in the reference, whose factory creates no data transfer
+ * (rust/src/factory.rs:238-242: MLX memory is unified with the host).
+ */
+#define ORTMI_SMALL_COPIES 16
+#define ORTMI_SMALL_COPY_BYTES 1024
+int ortmi_copy_small_h2d(int n, void* const* dst, const void* const* src, const size_t* bytes,
+                         void* stream);
+
+/*
  * MatMulNBits (com.microsoft): Y[M,N] = A[M,K] . dequant(B)^T with
  * dequant(B)[n,k] = (q[n,k] - zp[n,k/bs]) * scales[n,k/bs].
  * B: uint8 [N, ceil(K/bs), bs*bits/8] (ORT layout, low nibble first);
@@ -146,7 +162,8 @@ int ortmi_matmul_nbits_decode_merge(const float* partials, int64_t splits, int64
  * `layers` is a device array of `dims->layers` records. input_id (int64 [1]) and
  * total_sequence_length (int32 [1]) are device memory read by the kernel, so a
  * step needs no host round trip; logits [vocab] fp16 and next_id (int64, the
- * first index of the largest logit, NaN never wins) are written. `status`
+ * first index of the largest logit, NaN never wins; device or host-pinned
+ * memory, written once at the end of the step) are written. `status`
  * (optional; device or host-pinned memory) receives 0 on success, 1 if a wait
  * between the step's workgroups saw no data for 100 ms (the results are then
  * invalid), 2 if the token id was out of range (row 0 was used), 3 if

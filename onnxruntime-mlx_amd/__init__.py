@@ -57,6 +57,8 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "ortmi_abi_version": (ctypes.c_int, []),
     "ortmi_last_error": (ctypes.c_char_p, []),
+    "ortmi_copy_small_h2d": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_void_p]),
     "ortmi_matmul_nbits": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                           _i32, _vp]),
     "ortmi_matmul_nbits_decode_fused": (ctypes.c_int, [

@@ -122,6 +122,17 @@ bool dt_can_copy(const OrtDataTransferImpl* self, const OrtMemoryDevice* src,
     const auto* t = reinterpret_cast<const DataTransfer*>(self);
     return dt_side_ok(t, src) && dt_side_ok(t, dst);
 }
+// Where a pointer lives: 0 host memory the runtime does not know (pageable), 1
+// pinned host memory, 2 device memory (a query of about 0.5 us).
+int mem_kind(const void* p) {
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();  // the query's error must not reach the next launch check
+        return 0;
+    }
+    if (attr.type == hipMemoryTypeDevice) return 2;
+    return attr.type == hipMemoryTypeHost ? 1 : -1;
+}
 OrtStatus* dt_copy(OrtDataTransferImpl* self, const OrtValue** src, OrtValue** dst,
                    OrtSyncStreamImpl**, size_t n) {
     auto* t = reinterpret_cast<DataTransfer*>(self);
@@ -129,6 +140,45 @@ OrtStatus* dt_copy(OrtDataTransferImpl* self, const OrtValue** src, OrtValue** d
     return guard(a, "CopyTensors", [&] {
         if (!t->stream)
             check_hip(hipStreamCreateWithFlags(&t->stream, hipStreamNonBlocking), "hipStreamCreate");
+        // A few small host-to-device copies (a decode step's input ids and length
+        // scalars) go in one launch that carries the bytes (ortmi_copy_small_h2d):
+        // 12.7 against 21.5 us for three 8-byte DMA copies and their synchronisation.
+        std::vector<void*> sd;
+        std::vector<const void*> ss;
+        std::vector<size_t> sb;
+        bool small = n <= (size_t)ORTMI_SMALL_COPIES;
+        size_t small_bytes = 0;
+        for (size_t i = 0; i < n && small; ++i) {
+            OrtTensorTypeAndShapeInfo* info = nullptr;
+            check_ort(a, api::GetTensorTypeAndShape(a)(src[i], &info), "GetTensorTypeAndShape");
+            size_t count = 0;
+            ONNXTensorElementDataType et = ONNX_TENSOR_ELEMENT_DATA_TYPE_UNDEFINED;
+            OrtStatus* s1 = api::GetTensorShapeElementCount(a)(info, &count);
+            OrtStatus* s2 = s1 ? nullptr : api::GetTensorElementType(a)(info, &et);
+            api::ReleaseTensorTypeAndShapeInfo(a)(info);
+            check_ort(a, s1, "GetTensorShapeElementCount");
+            check_ort(a, s2, "GetTensorElementType");
+            const void* s = nullptr;
+            void* d = nullptr;
+            check_ort(a, api::GetTensorData(a)(src[i], &s), "GetTensorData");
+            check_ort(a, api::GetTensorMutableData(a)(dst[i], &d), "GetTensorMutableData");
+            const size_t bytes = count * dtype_size(et);
+            small_bytes += bytes;
+            if (small_bytes > (size_t)ORTMI_SMALL_COPY_BYTES) small = false;
+            if (small && bytes) {  // host source (pageable or pinned), device destination
+                const int ks = mem_kind(s);
+                small = (ks == 0 || ks == 1) && mem_kind(d) == 2;
+            }
+            sd.push_back(d);
+            ss.push_back(s);
+            sb.push_back(bytes);
+        }
+        if (small && n > 0) {
+            check_kernel(ortmi_copy_small_h2d((int)n, sd.data(), ss.data(), sb.data(), t->stream),
+                         "small copy");
+            check_hip(hipStreamSynchronize(t->stream), "hipStreamSynchronize");
+            return;
+        }
         for (size_t i = 0; i < n; ++i) {
             OrtTensorTypeAndShapeInfo* info = nullptr;
             check_ort(a, api::GetTensorTypeAndShape(a)(src[i], &info), "GetTensorTypeAndShape");

@@ -75,6 +75,11 @@ struct Plan::DecodeProgram {
     void* argmax_ptr = nullptr;  // the same for the ArgMax output
     bool argmax_dev = false;
     int32_t* status = nullptr;  // host-pinned: the kernel writes it, the host reads it after the run
+    // Host-pinned greedy id for an ArgMax output in host memory: the kernel writes it
+    // there directly (a device-to-host copy of 8 bytes costs about 20 us per step),
+    // and the host copies it to the output after the run.
+    int64_t* next_host = nullptr;
+    void* pending_host = nullptr;  // the host ArgMax output of the launch in flight
     int64_t steps = 0;          // program launches so far
     int64_t abort_step = 0;     // ORTMI_EP_PROGRAM_ABORT: launch to abort before it starts (1-based)
     // Plain launches until one ends with status 1 (a workgroup could not start while
@@ -83,6 +88,7 @@ struct Plan::DecodeProgram {
     int32_t cooperative = 0;
     ~DecodeProgram() {
         if (status) (void)hipHostFree(status);
+        if (next_host) (void)hipHostFree(next_host);
     }
 };
 
@@ -354,6 +360,8 @@ void Plan::match_decode_program() {
         dp->cooperative = std::strcmp(co, "0") != 0;
     check_hip(hipHostMalloc((void**)&dp->status, sizeof(int32_t), hipHostMallocDefault),
               "hipHostMalloc");
+    check_hip(hipHostMalloc((void**)&dp->next_host, sizeof(int64_t), hipHostMallocDefault),
+              "hipHostMalloc");
     dp->next_id = device_alloc(sizeof(int64_t));
     dprog_ = std::move(dp);
     dprog_reject_.clear();
@@ -416,7 +424,7 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
     // The program's greedy argmax (lowest index on ties) is the ArgMax output: written
     // in place when that is device memory, else copied out after the launch.
     int64_t* next_id = static_cast<int64_t*>(dp.next_id->ptr);
-    void* argmax_host = nullptr;
+    dp.pending_host = nullptr;
     if (!dp.argmax.empty()) {
         const std::vector<int64_t> od = dp.argmax_keep ? std::vector<int64_t>{1, 1, 1}
                                                        : std::vector<int64_t>{1, 1};
@@ -425,8 +433,12 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
             dp.argmax_dev = is_device_ptr(o);
             dp.argmax_ptr = o;
         }
-        if (dp.argmax_dev) next_id = static_cast<int64_t*>(o);
-        else argmax_host = o;
+        if (dp.argmax_dev) {
+            next_id = static_cast<int64_t*>(o);
+        } else {  // written by the kernel to pinned memory, copied out after the run
+            next_id = dp.next_host;
+            dp.pending_host = o;
+        }
     }
     const size_t tb = table.size() * sizeof(OrtmiDecoderLayer);
     if (!dp.table || dp.host_table.size() != table.size() ||
@@ -483,10 +495,6 @@ bool Plan::run_decode_program(const OrtApi* a, OrtKernelContext* ctx) {
         return false;
     }
     check_kernel(rc, "decode program");
-    if (argmax_host)
-        check_hip(hipMemcpyAsync(argmax_host, next_id, sizeof(int64_t), hipMemcpyDeviceToHost,
-                                 stream_),
-                  "ArgMax output");
     return true;
 }
 
@@ -774,7 +782,11 @@ void Plan::compute(const OrtApi* a, OrtKernelContext* ctx) {
             g_out_staging = nullptr;
             const int32_t st = *dprog_->status;
             if (st == 2) fail("decode program: input id out of range", ORT_INVALID_ARGUMENT);
-            if (st == 0) return;
+            if (st == 0) {
+                if (dprog_->pending_host)
+                    std::memcpy(dprog_->pending_host, dprog_->next_host, sizeof(int64_t));
+                return;
+            }
             // Not completed (1: a wait saw no data for 100 ms; -1: the launch stopped
             // before writing a status). The step runs again op by op: the K/V row it
             // may have written at total - 1 is rewritten with the same values.

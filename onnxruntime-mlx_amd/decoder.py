@@ -221,8 +221,10 @@ class DecoderRunner:
     host_feeds: the input ids are a host tensor too, as an application without
     IOBinding feeds them (ONNX Runtime GenAI's loop): each step reads the greedy id
     back to the host and feeds it, and the harness copies every host feed to the
-    EP's memory device (HBM) through the EP's data transfer before Compute.
-    Otherwise the ids stay in HBM and the argmax output is fed back in place.
+    EP's memory device (HBM) through the EP's data transfer before Compute. With
+    argmax_node the ArgMax output is bound to host memory, where a serving loop
+    reads the token. Otherwise the ids stay in HBM and the argmax output is fed
+    back in place.
     """
 
     def __init__(self, cfg: DecoderConfig, weights, cap: int, max_prompt: int,
@@ -254,7 +256,8 @@ class DecoderRunner:
         self.next_id = torch.zeros((1, 1), dtype=torch.int64, device=dev)
         # ArgMax outputs alternate between two buffers, so a step's input id (the
         # previous step's output) is never the buffer it writes.
-        self.tokens = [torch.zeros((1, max_prompt), dtype=torch.int64, device=dev)
+        tok_dev = "cpu" if (host_feeds and argmax_node) else dev
+        self.tokens = [torch.zeros((1, max_prompt), dtype=torch.int64, device=tok_dev)
                        for _ in range(2)]
         self._first = [t[:, :1] for t in self.tokens]
         self._flip = 0

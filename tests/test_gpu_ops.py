@@ -1403,3 +1403,46 @@ def test_paged_attention_malformed_control_tensors(ortmi, oracle, path):
     else:
         assert np.abs(got[0] - ro).max() <= 6e-5
         np.testing.assert_array_equal(got[1], rk)
+
+
+def test_copy_small_h2d(ortmi):
+    """ortmi_copy_small_h2d (the data transfer's one-launch path for a run's small
+    feeds): every byte of up to 16 host buffers (pageable numpy memory, 1024 bytes in
+    all) lands at its device destination, at any offset and alignment, bit-exact;
+    zero-length copies and bytes around the destinations are left alone; more than 16
+    copies or 1024 bytes are rejected before anything is launched."""
+    import ctypes
+
+    import torch
+
+    lib = ortmi.load_kernels()
+    rng = np.random.default_rng(91)
+    sizes = [8, 4, 4, 0, 37, 1, 200, 3, 16, 90, 64, 2, 5, 8, 7, 574]
+    assert sum(sizes) == 1023
+    srcs = [rng.integers(0, 256, size=n, dtype=np.uint8) for n in sizes]
+    buf = torch.full((4096,), 0xA5, dtype=torch.uint8, device="cuda")
+    offs, o = [], 3
+    for n in sizes:
+        offs.append(o)
+        o += n + 5  # a gap of untouched bytes after each destination
+    base = buf.data_ptr()
+    n = len(sizes)
+    dst = (ctypes.c_void_p * n)(*[base + x for x in offs])
+    src = (ctypes.c_void_p * n)(*[s.ctypes.data if len(s) else None for s in srcs])
+    nb = (ctypes.c_size_t * n)(*sizes)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.ortmi_copy_small_h2d(n, dst, src, nb, st) == 0
+    got = host(buf)
+    want = np.full(4096, 0xA5, np.uint8)
+    for x, s in zip(offs, srcs):
+        want[x:x + len(s)] = s
+    np.testing.assert_array_equal(got, want)
+    assert lib.ortmi_copy_small_h2d(0, None, None, None, st) == 0
+    big = (ctypes.c_size_t * n)(*(sizes[:-1] + [sizes[-1] + 2]))  # 1025 bytes
+    assert lib.ortmi_copy_small_h2d(n, dst, src, big, st) == 1
+    assert b"1024" in lib.ortmi_last_error()
+    d17 = (ctypes.c_void_p * 17)(*([base] * 17))
+    s17 = (ctypes.c_void_p * 17)(*([srcs[0].ctypes.data] * 17))
+    n17 = (ctypes.c_size_t * 17)(*([1] * 17))
+    assert lib.ortmi_copy_small_h2d(17, d17, s17, n17, st) == 1
+    np.testing.assert_array_equal(host(buf), want)
