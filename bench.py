@@ -698,7 +698,8 @@ def main():
             "device_ids_same_tokens": r["dev_same_tokens"],
             "feeds": "input ids, seqlens_k, total_sequence_length in host memory, copied to "
                      "HBM by the EP's data transfer (ORT's placement rule); KV cache and "
-                     "logits bound in HBM",
+                     "logits bound in HBM; the ArgMax output (the greedy id) bound to host "
+                     "memory",
             "prefill_tok_s": round(r["prefill_tok_s"], 1),
             "bytes_per_token": r["bytes_per_token"],
             "roofline": {"bound": "hbm", "achieved": round(r["gbs"], 1), "peak": HBM_PEAK_GBS,
