@@ -520,7 +520,10 @@ def test_ep_memory_device_allocator_and_data_transfer(ortmi, hx, monkeypatch):
     (GPU, AMD's vendor id, GPU 0), or CPU memory with ORTMI_EP_MEMORY=cpu;
     CreateAllocator hands out an HBM allocator only for the EP's own memory info
     (MI355X_HBM, a visible GPU id), whose Alloc/Reserve/Free/Info work;
-    CreateDataTransfer copies host<->device and device<->device bit for bit."""
+    CreateDataTransfer copies host<->device and device<->device bit for bit, on each
+    of its paths: small host-to-device copies in one launch, device-to-pageable-host
+    copies through its pinned staging buffer, and plain asynchronous copies for
+    larger tensors and pinned destinations."""
     import torch
 
     g, _ = _one_node_mnb_graph(hx, np.random.default_rng(1))
@@ -546,6 +549,17 @@ def test_ep_memory_device_allocator_and_data_transfer(ortmi, hx, monkeypatch):
     sess.data_transfer_copy(d2, back, hx.FLOAT)   # device -> host
     torch.cuda.synchronize()
     assert torch.equal(back, src)
+    # Larger than the one-launch (1 KiB) and staging (1 MiB) bounds, and a pinned
+    # destination.
+    big = torch.randn(3, 1000, 100, dtype=torch.float32)  # 1.2 MB
+    db = torch.empty_like(big, device="cuda")
+    sess.data_transfer_copy(big, db, hx.FLOAT)
+    big_back = torch.empty_like(big)
+    sess.data_transfer_copy(db, big_back, hx.FLOAT)
+    pinned = torch.empty_like(src).pin_memory()
+    sess.data_transfer_copy(d2, pinned, hx.FLOAT)
+    torch.cuda.synchronize()
+    assert torch.equal(big_back, big) and torch.equal(pinned, src)
 
 
 @pytest.mark.parametrize("memory", ["hbm", "cpu"])
