@@ -83,8 +83,9 @@ int ortmi_matmul_nbits(const void* A, const uint8_t* B, const void* scales,
                        int64_t bits, int64_t block_size, int32_t dtype, void* stream);
 
 /*
- * MatMulNBits decode step (M = 1, 4-bit, block 32/64/128, fp16/bf16) with its
- * graph neighbours fused in; flags select what is fused:
+ * MatMulNBits decode step (M = 1, 4-bit, block 32/64/128, fp16/bf16; K up to
+ * 16384 in fp16, 10240 in bf16) with its graph neighbours fused in; flags select
+ * what is fused:
  *  - ORTMI_FUSE_RMS_NORM: the activation row is first normalised,
  *    a = (x [+ skip]) / sqrt(mean((x [+ skip])^2) + epsilon) * gamma, each
  *    result rounded to dtype as the unfused ops store it; skip is optional, and
@@ -239,7 +240,8 @@ int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const OrtmiDecode
  * [B,KV,past_cap,hd] (they may alias past_*, then only the S new rows are
  * written); otherwise the growing contract: present_* are [B,KV,past_cap+S,hd].
  * cos_cache/sin_cache [max_pos, rotary_half] (NULL when do_rotary = 0), in dtype.
- * output [B,S,H*hd]. scale = 0 means 1/sqrt(hd).
+ * output [B,S,H*hd]. scale = 0 means 1/sqrt(hd). hd is 64, 96 or 128 (other head
+ * sizes, fp32, attention_bias and QK-norm: ortmi_group_query_attention_ex).
  * Replaces: group_query_attention_op (rust/src/ops/attention.rs:556-952): the
  * two mlx_fast_rope calls (attention.rs:671-708), the KV concat /
  * slice_update (attention.rs:881-908) and mlx_fast_scaled_dot_product_attention

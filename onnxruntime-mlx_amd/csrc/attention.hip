@@ -319,7 +319,9 @@ __device__ __forceinline__ void decode_merge(float (&m)[G], float (&l)[G], float
 
 // Each lane group of LPR lanes owns one row per step; scores use a blocked
 // online softmax. In the growing contract rows below vp are copied from past to
-// present out of the registers already loaded.
+// present out of the registers already loaded. Head 96 runs on 16-lane groups
+// like head 128: its last 4 lanes of each group are padding that loads and
+// stores nothing and adds zeros.
 template <typename T, int HD, int G>
 __global__ __launch_bounds__(256) void gqa_decode_kernel(
     const T* __restrict__ q, const T* __restrict__ knew, const T* __restrict__ vnew,
@@ -328,13 +330,15 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     T* __restrict__ kpres, T* __restrict__ vpres, int64_t past_cap, int64_t pres_cap,
     int copy_past, int vp, int chunk, int nsplit, int KV, float scale, float* __restrict__ part,
     T* __restrict__ out, const int* __restrict__ total_dev, int vp_max, int gsplit) {
-    constexpr int LPR = HD / 8;          // lanes per row (16 bytes each)
+    static_assert(HD == 64 || HD == 96 || HD == 128, "head size");
+    constexpr int LPR = HD <= 64 ? 8 : 16;  // lanes per row (16 bytes each; head 96 padded)
+    constexpr int HDP = 8 * LPR;            // head dims the lane groups span
     constexpr int RPW = 64 / LPR;        // rows per wave per step
     constexpr int NW = 4;                // waves
     constexpr int RPS = NW * RPW;        // rows per workgroup step
     constexpr int U = G <= 4 ? 4 : 2;    // steps per online-softmax block (registers)
     constexpr int BLK = RPS * U;         // rows per block
-    __shared__ float s_o[NW][G][HD];
+    __shared__ float s_o[NW][G][HDP];
     __shared__ float s_m[NW][G], s_l[NW][G];
 
     // blockIdx.x = (b*KV + kvh) * gsplit + head group: the G*gsplit query heads of
@@ -350,6 +354,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = lane / LPR;
     const int dl = (lane % LPR) * 8;
+    const bool padl = dl >= HD;  // a padding lane of head 96
     T* kw = kpres + (int64_t)bk * pres_cap * HD;
     T* vw = vpres + (int64_t)bk * pres_cap * HD;
     const T* kbase = copy_past ? kpast + (int64_t)bk * past_cap * HD : kw;
@@ -374,15 +379,22 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     // (A scalar load: its wait does not count vector memory operations.)
     int tv = 0;
     if (total_dev) tv = total_dev[0];
+    // Padding lanes read the head's first 8 dims (in bounds) and zero them.
+    const int dlr = padl ? 0 : dl;
+    const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
     uint4 qraw[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-        qraw[g] = *reinterpret_cast<const uint4*>(q + (int64_t)b * q_stride +
-                                                  (int64_t)(h0 + g) * HD + dl);
-    const uint4 kraw = *reinterpret_cast<const uint4*>(knew + (int64_t)b * kv_stride +
-                                                       (int64_t)kvh * HD + dl);
-    const uint4 vraw = *reinterpret_cast<const uint4*>(vnew + (int64_t)b * kv_stride +
-                                                       (int64_t)kvh * HD + dl);
+    for (int g = 0; g < G; ++g) {
+        const uint4 v = *reinterpret_cast<const uint4*>(q + (int64_t)b * q_stride +
+                                                        (int64_t)(h0 + g) * HD + dlr);
+        qraw[g] = padl ? zero4 : v;
+    }
+    const uint4 kraw0 = *reinterpret_cast<const uint4*>(knew + (int64_t)b * kv_stride +
+                                                        (int64_t)kvh * HD + dlr);
+    const uint4 vraw0 = *reinterpret_cast<const uint4*>(vnew + (int64_t)b * kv_stride +
+                                                        (int64_t)kvh * HD + dlr);
+    const uint4 kraw = padl ? zero4 : kraw0;
+    const uint4 vraw = padl ? zero4 : vraw0;
     // Rows [base, base + BLK) below `lim`; rows at or past src_rows fall outside
     // the slice and read zeros. Rows are streamed once per step: loads and the
     // copy stores are non-temporal (measured 5% faster on the 4096-row copy).
@@ -391,7 +403,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
         for (int u = 0; u < U; ++u) {
             const int j = base + u * RPS + wave * RPW + sub;
             const uint32_t off =
-                j < lim && j < src_rows ? (uint32_t)j * row_bytes + lane_off : src_end;
+                j < lim && j < src_rows && !padl ? (uint32_t)j * row_bytes + lane_off : src_end;
             kk[u] = __builtin_amdgcn_raw_buffer_load_b128(rsk, off, 0, kCachePolicyNT);
             vv[u] = __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, kCachePolicyNT);
         }
@@ -525,7 +537,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
             const int j = base + u * RPS + wave * RPW + sub;
             // Past rows below vp are copied into the present buffer.
             const uint32_t coff =
-                copier && j < jw ? (uint32_t)j * row_bytes + lane_off : pres_end;
+                copier && j < jw && !padl ? (uint32_t)j * row_bytes + lane_off : pres_end;
             __builtin_amdgcn_raw_buffer_store_b128(kk[u], rdk, coff, 0, kCachePolicyNT);
             __builtin_amdgcn_raw_buffer_store_b128(vv[u], rdv, coff, 0, kCachePolicyNT);
 #pragma unroll
@@ -566,7 +578,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     // The new row (RoPE'd key, value) goes to row vp of the present buffer, from
     // the split that owns it; it is written last so no reload waits on it.
     {
-        const uint32_t noff = own_new && hgrp == 0 && wave == 0 && sub == 0
+        const uint32_t noff = own_new && hgrp == 0 && wave == 0 && sub == 0 && !padl
                                   ? (uint32_t)vp * row_bytes + lane_off
                                   : pres_end;
         __builtin_amdgcn_raw_buffer_store_b128(knb, rdk, noff, 0, 0);
@@ -574,7 +586,8 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
                                                noff, 0, 0);
     }
     // out == null: split partials only (even for one split), merged by the consumer.
-    decode_merge<HD, G, LPR, NW>(m, l, o, s_m, s_l, s_o, [&](int g, int d, float M, float L, float acc) {
+    decode_merge<HDP, G, LPR, NW>(m, l, o, s_m, s_l, s_o, [&](int g, int d, float M, float L, float acc) {
+        if (d >= HD) return;  // padding dims of head 96
         const int64_t row = (int64_t)b * H + h0 + g;
         if (nsplit == 1 && out) {
             out[row * HD + d] = from_f32<T>(L > 0.f ? acc / L : 0.f);
@@ -1979,6 +1992,10 @@ extern "C" size_t ortmi_group_query_attention_workspace_size(int64_t batch, int6
         part = std::max(part, align_up(rows * kPrefillSplits * (head_size + 2) * 4) +
                                   align_up(rows * 4));
     }
+    // Head 96 takes the generic kernels for everything but the one-token decode.
+    if (head_size == 96)
+        return std::max(q + part, ortmi_group_query_attention_ex_workspace_size(
+                                      batch, seq_len, num_heads, head_size));
     return q + part;
 }
 
@@ -2151,8 +2168,8 @@ extern "C" int ortmi_group_query_attention(
     // Claim/op contract of rust/src/ops/attention.rs:1527-1738 and 556-952.
     ORTMI_REQUIRE(num_heads > 0 && kv_num_heads > 0 && num_heads % kv_num_heads == 0,
                   "GroupQueryAttention: num_heads must be a positive multiple of kv_num_heads");
-    ORTMI_REQUIRE(head_size == 64 || head_size == 128,
-                  "GroupQueryAttention: head_size must be 64 or 128");
+    ORTMI_REQUIRE(head_size == 64 || head_size == 96 || head_size == 128,
+                  "GroupQueryAttention: head_size must be 64, 96 or 128");
     ORTMI_REQUIRE(batch > 0 && seq_len > 0 && past_cap >= 0, "GroupQueryAttention: bad shape");
     ORTMI_REQUIRE(query && output && present_key && present_value,
                   "GroupQueryAttention: null tensor");
@@ -2183,6 +2200,27 @@ extern "C" int ortmi_group_query_attention(
     if (shared_c)
         ORTMI_REQUIRE(total_sequence_length <= past_cap,
                       "GroupQueryAttention: total_sequence_length exceeds the KV buffer capacity");
+    // Head 96 runs the one-token decode on the fast kernel (16-lane groups with 4
+    // padding lanes); prompts, and decode steps the fast kernel does not take
+    // (unaligned tensors, more than 8 query heads per KV head, a rotary half that is
+    // not a multiple of 8), go to the generic kernels.
+    if (head_size == 96) {
+        const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+        const bool packed = key == nullptr;
+        const void* kk = packed ? static_cast<const char*>(query) + num_heads * 96 * 2 : key;
+        const void* vv = packed ? static_cast<const char*>(query) + (num_heads + kv_num_heads) * 96 * 2
+                                : value;
+        const bool fast = seq_len == 1 && num_heads / kv_num_heads <= 8 && dtype != ORTMI_F32 &&
+                          (!rotary || rotary_interleaved || rotary_half % 8 == 0) && a16(query) &&
+                          a16(kk) && a16(vv) && a16(present_key) && a16(present_value) &&
+                          (past_cap == 0 || (a16(past_key) && a16(past_value)));
+        if (!fast)
+            return ortmi_group_query_attention_ex(
+                query, key, value, past_key, past_value, past_cap, total_sequence_length,
+                cos_cache, sin_cache, rotary_half, max_pos, nullptr, nullptr, 1e-6f, nullptr, 0, 0,
+                0, 0, output, present_key, present_value, batch, seq_len, num_heads, kv_num_heads,
+                head_size, scale, rotary_interleaved, dtype, workspace, workspace_bytes, stream);
+    }
     hipStream_t st = as_stream(stream);
     const int B = (int)batch, S = (int)seq_len, H = (int)num_heads, KV = (int)kv_num_heads;
     const int half = (int)rotary_half;
@@ -2193,10 +2231,12 @@ extern "C" int ortmi_group_query_attention(
                           workspace_bytes, st)
     if (dtype == ORTMI_F16) {
         if (head_size == 64) ORTMI_GQA(half_t, 64);
+        if (head_size == 96) ORTMI_GQA(half_t, 96);
         ORTMI_GQA(half_t, 128);
     }
     if (dtype == ORTMI_BF16) {
         if (head_size == 64) ORTMI_GQA(uint16_t, 64);
+        if (head_size == 96) ORTMI_GQA(uint16_t, 96);
         ORTMI_GQA(uint16_t, 128);
     }
 #undef ORTMI_GQA
@@ -2259,8 +2299,8 @@ static int gqa_decode_capturable_entry(
     void* stream) {
     ORTMI_REQUIRE(num_heads > 0 && kv_num_heads > 0 && num_heads % kv_num_heads == 0,
                   "GroupQueryAttention: num_heads must be a positive multiple of kv_num_heads");
-    ORTMI_REQUIRE(head_size == 64 || head_size == 128,
-                  "GroupQueryAttention: head_size must be 64 or 128");
+    ORTMI_REQUIRE(head_size == 64 || head_size == 96 || head_size == 128,
+                  "GroupQueryAttention: head_size must be 64, 96 or 128");
     ORTMI_REQUIRE(batch > 0 && kv_cap > 0, "GroupQueryAttention: bad shape");
     ORTMI_REQUIRE(query && (output || partials) && kv_key && kv_value && total_dev,
                   "GroupQueryAttention: null tensor");
@@ -2281,10 +2321,12 @@ static int gqa_decode_capturable_entry(
                                             workspace, workspace_bytes, partials, st)
     if (dtype == ORTMI_F16) {
         if (head_size == 64) ORTMI_GQA_CAP(half_t, 64);
+        if (head_size == 96) ORTMI_GQA_CAP(half_t, 96);
         ORTMI_GQA_CAP(half_t, 128);
     }
     if (dtype == ORTMI_BF16) {
         if (head_size == 64) ORTMI_GQA_CAP(uint16_t, 64);
+        if (head_size == 96) ORTMI_GQA_CAP(uint16_t, 96);
         ORTMI_GQA_CAP(uint16_t, 128);
     }
 #undef ORTMI_GQA_CAP

@@ -1080,13 +1080,13 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         }
         const float scale = n.attr_float("scale", 0.f);
         const int32_t inter = (int32_t)n.attr_int("rotary_interleaved", 0);
-        // fp32, attention_bias, QK-norm and head sizes other than 64/128 run the
+        // fp32, attention_bias, QK-norm and head sizes other than 64/96/128 run the
         // generic kernels (one prep launch, one attention launch).
         Tensor* bias = in(10);
         Tensor* qnw = in(14);
         Tensor* knw = in(15);
         if (q.dtype == ONNX_TENSOR_ELEMENT_DATA_TYPE_FLOAT || bias || qnw || knw ||
-            (hd != 64 && hd != 128)) {
+            (hd != 64 && hd != 96 && hd != 128)) {
             if (capturing_) fail("GroupQueryAttention form is not capturable");
             capturable_ = false;
             int64_t bd[4] = {0, 0, 0, 0};

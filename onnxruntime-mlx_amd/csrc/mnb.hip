@@ -605,8 +605,20 @@ static int launch_gemv4(const T* A, const uint8_t* B, const T* S, const uint8_t*
         case 3: return launch_gemv4_cpl<T, BS, 3, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
         case 4: return launch_gemv4_cpl<T, BS, 4, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
         case 5: return launch_gemv4_cpl<T, BS, 5, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
-        default: return -1;  // K > 10240: the caller falls back
+        default: break;
     }
+    // fp16 activations held as pairs (16 VGPRs per chunk) also take K up to 16384
+    // (the down_proj of 7B-class decoders, K = 11008 or 14336); fp32 and bf16 hold
+    // 32 VGPRs per chunk and stop at 10240.
+    if constexpr (std::is_same<T, half_t>::value) {
+        switch (cpl) {
+            case 6: return launch_gemv4_cpl<T, BS, 6, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
+            case 7: return launch_gemv4_cpl<T, BS, 7, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
+            case 8: return launch_gemv4_cpl<T, BS, 8, PRO, PAIR, MRG>(A, B, S, Z, Y, N, K, nb, pro, st);
+            default: break;
+        }
+    }
+    return -1;  // the caller falls back
 }
 
 // ------------------------------------------------------------- GEMM (MFMA) --
@@ -1093,7 +1105,8 @@ static int run_mnb(const void* A, const uint8_t* B, const void* S, const uint8_t
     T* y = static_cast<T*>(Y);
     const bool aligned = (reinterpret_cast<uintptr_t>(B) % 16) == 0;
     const bool fast_form = bits == 4 && (bs == 32 || bs == 64 || bs == 128) && aligned;
-    if (fast_form && M == 1 && (size_t)nb * bs <= 10240) {
+    const size_t kmax = std::is_same<T, half_t>::value ? 16384 : 10240;
+    if (fast_form && M == 1 && (size_t)nb * bs <= kmax) {
         int rc = -1;
         if (bs == 32) rc = launch_gemv4<T, 32>(a, B, s, Z, y, N, K, nb, st);
         if (bs == 64) rc = launch_gemv4<T, 64>(a, B, s, Z, y, N, K, nb, st);
@@ -1168,7 +1181,7 @@ extern "C" int ortmi_matmul_nbits_decode_fused(const void* x, const void* skip, 
                   "MatMulNBits fused: B must be 16-byte aligned");
     const int64_t nb = (K + block_size - 1) / block_size;
     const int64_t limit = 2048LL * (dtype == ORTMI_F32 ? 4 : 8);
-    ORTMI_REQUIRE(nb * block_size <= std::min<int64_t>(limit, 10240),
+    ORTMI_REQUIRE(nb * block_size <= std::min<int64_t>(limit, dtype == ORTMI_F16 ? 16384 : 10240),
                   "MatMulNBits fused: K too large for the decode kernel");
     hipStream_t st = as_stream(stream);
     int rc;

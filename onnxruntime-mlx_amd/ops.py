@@ -134,7 +134,7 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
     place. attention_bias (input 10, rank 4 [B or 1, H or 1, >= S, >= total]) is
     added to the scaled scores; q_norm_weight / k_norm_weight (inputs 14/15, [head])
     RMS-normalise q and k per head before RoPE (attention.rs:663-670). fp32 tensors,
-    those inputs and head sizes other than 64/128 run the generic kernels
+    those inputs and head sizes other than 64/96/128 run the generic kernels
     (ortmi_group_query_attention_ex). Returns (output, present_key, present_value).
     """
     del seqlens_k  # not consulted outside sliding-window mode, as in the reference
@@ -163,7 +163,8 @@ def group_query_attention(query, key, value, past_key, past_value, seqlens_k,
     rope = (_p(cos_cache) if use_rope else None, _p(sin_cache) if use_rope else None, half,
             max_pos)
     generic = (query.dtype == torch.float32 or attention_bias is not None
-               or q_norm_weight is not None or k_norm_weight is not None or hd not in (64, 128))
+               or q_norm_weight is not None or k_norm_weight is not None
+               or hd not in (64, 96, 128))
     if generic:
         ws = _workspace(lib.ortmi_group_query_attention_ex_workspace_size(B, S, num_heads, hd),
                         query.device)

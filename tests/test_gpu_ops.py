@@ -74,7 +74,8 @@ def _mnb_inputs(rng, M, N, K, block, bits=4, asym=True, zp_all8=False, dtype=np.
 @pytest.mark.parametrize("K,N,block,skip,pair", [
     (1536, 2048, 32, False, False), (1536, 1536, 32, True, False), (1536, 17920, 32, True, True),
     (8960, 1536, 32, True, False), (4096, 512, 128, True, True), (1000, 64, 64, False, True),
-    (1536, 24576, 32, True, False), (1536, 45056, 32, False, True)])
+    (1536, 24576, 32, True, False), (1536, 45056, 32, False, True),
+    (14336, 512, 32, True, False)])
 def test_mnb_decode_fused(ortmi, oracle, K, N, block, skip, pair):
     """Norm prologue and SwiGLU-pair epilogue of the decode GEMV against the unfused
     ops of the oracle (norm rounded to fp16, matmul in fp64, SwiGLU op by op)."""
@@ -212,10 +213,14 @@ def test_mnb_gemv_config1_shape(ortmi, oracle):
 
 
 @pytest.mark.parametrize("K,block,N", [(1536, 32, 300), (8960, 32, 300), (4096, 64, 300),
-                                       (1536, 32, 20700), (520, 32, 21001), (1000, 64, 20481)])
+                                       (1536, 32, 20700), (520, 32, 21001), (1000, 64, 20481),
+                                       (11008, 32, 300), (14336, 32, 300), (12000, 64, 257),
+                                       (16384, 128, 200)])
 def test_mnb_gemv_fp16(ortmi, oracle, K, block, N):
     """Includes long walks over short rows (N beyond 80 rows per CU, K <= 1536),
-    which take four rows per wave, with an odd N and a partial final block."""
+    which take four rows per wave, with an odd N and a partial final block, and the
+    long rows of 7B-class down projections (K = 11008, 14336, up to 16384: six to
+    eight 32-code chunks per lane)."""
     import torch
 
     rng = np.random.default_rng(K * 3 + block + N)
@@ -508,7 +513,7 @@ def test_gqa_decode_group_sizes(ortmi, oracle, H, KV, hd):
                     seed=H * 10 + KV, base=1e6)
 
 
-@pytest.mark.parametrize("H,KV,hd", [(12, 2, 128), (32, 8, 128), (8, 8, 64)])
+@pytest.mark.parametrize("H,KV,hd", [(12, 2, 128), (32, 8, 128), (8, 8, 64), (32, 32, 96)])
 def test_gqa_decode_capturable(ortmi, oracle, H, KV, hd):
     """Device-resident total_sequence_length: equal to the oracle, and a HIP graph
     captured at one length and replayed at others equals eager calls bit for bit."""
@@ -645,6 +650,22 @@ def test_gqa_packed_qkv(ortmi, oracle, S, past, cap):
 
 def test_gqa_decode_shared_separate_present(ortmi, oracle):
     assert _run_gqa(ortmi, oracle, B=3, S=1, H=4, KV=4, hd=64, cap=100, past=37, seed=3)
+
+
+@pytest.mark.parametrize("B,S,H,KV,cap,past,inplace", [
+    (2, 1, 32, 32, 700, 650, True),    # Phi-3.5-mini's heads: one query head per KV head
+    (2, 1, 12, 4, 300, 300, False),    # growing contract (past rows copied by the kernel)
+    (3, 1, 16, 2, 8192, 8000, True),   # long context: many key splits
+    (2, 40, 12, 4, 100, 30, True),     # prefill chunk after cached rows (matrix-core tiles)
+    (1, 300, 32, 32, 300, 0, True),    # a prompt into an empty buffer
+])
+def test_gqa_head96(ortmi, oracle, B, S, H, KV, cap, past, inplace):
+    """Head size 96 (Phi-3.5-mini) on the fast kernels: one-token decode on 16-lane
+    groups whose last 4 lanes are padding, prefill on the matrix-core tiles; the
+    output within the fp16 tolerance, every cached row bit-exact, the new K rows
+    within one fp16 ulp (full rotary over the 96 dims, half 48)."""
+    _run_gqa(ortmi, oracle, B=B, S=S, H=H, KV=KV, hd=96, cap=cap, past=past, inplace=inplace,
+             seed=96 + S + past, base=1e4)
 
 
 def test_gqa_decode_config3_shape(ortmi, oracle):
