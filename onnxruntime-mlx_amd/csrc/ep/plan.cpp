@@ -1113,10 +1113,15 @@ void Plan::run_node(const NodeDesc& n, const OrtApi* a, OrtKernelContext* ctx) {
         if (S == 1 && shared && pk && pv && prk == pkp && prv == pvp &&
             host_scalars_.count(n.inputs[6]) && (!cs || total <= max_pos)) {
             const int32_t* tdev = (const int32_t*)env_.at(n.inputs[6]).ptr;
-            if (B == 1 && n.attr_int("__partials", 0) &&
-                ortmi_group_query_attention_decode_splits(B, H, KV, hd, cap) > 0) {
+            // Partials for the o_proj GEMV to merge, unless their bound (the GEMV
+            // stages all heads' partials) leaves too few key splits: with 32 heads of
+            // 128 one split walks the whole context in one workgroup per KV head
+            // (Mistral-7B's layout at 640 keys: 11.8 us per layer against 4 us split).
+            const int64_t nsp = ortmi_group_query_attention_decode_splits(B, H, KV, hd, cap);
+            if (B == 1 && n.attr_int("__partials", 0) && nsp > 0 &&
+                nsp >= std::min<int64_t>(4, (cap + 255) / 256)) {
                 // Output left as split partials for the o_proj GEMV to merge.
-                const int64_t ns = ortmi_group_query_attention_decode_splits(B, H, KV, hd, cap);
+                const int64_t ns = nsp;
                 float* part = (float*)arena_alloc((size_t)(B * H * ns * (hd + 2)) * sizeof(float));
                 const int rc = ortmi_group_query_attention_decode_partials(
                     q.ptr, kptr, vptr, prk, prv, cap, tdev, csp, snp, half, max_pos, part, B, H,
