@@ -535,7 +535,13 @@ def bench_decoder_layout(torch, name, prompt_len=512, gen=128):
     out["config"] = (f"{desc}, int4 block 32 random weights; {prompt_len}-token prompt then "
                      f"{gen} greedy tokens, batch 1, host-fed ids, ArgMax node")
     if toks["program"] is not None:
-        out["same_tokens"] = toks["program"] == toks["op_path"]
+        a, b = toks["program"], toks["op_path"]
+        out["same_tokens"] = a == b
+        if a != b:
+            # Free-running greedy decodes part at the first near-tie of the logits and
+            # then follow different prompts; the teacher-forced comparison is in the tests.
+            out["first_divergence"] = next(i for i in range(min(len(a), len(b)) + 1)
+                                           if i == min(len(a), len(b)) or a[i] != b[i])
     out["first_tokens"] = (toks["program"] or toks["op_path"])[:8]
     return out
 
@@ -622,6 +628,8 @@ def main():
                     choices=["all", "gemv", "gemm", "gqa", "gqa_growing", "gqa_shared", "paged",
                              "decoder", "decoder_layouts", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layouts", default="",
+                    help="decoder_layouts: comma-separated names (default: every layout)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: there is no multi-GPU path (the kernels are "
@@ -746,7 +754,8 @@ def main():
             log(f"decoder cpu baseline: {cpu_dec['value']} tok/s on {cpu_dec['cores']} threads")
 
     if wl == "decoder_layouts":  # not part of "all": further decoder layouts on request
-        for name in DECODER_LAYOUTS:
+        names = [n for n in args.layouts.split(",") if n] or list(DECODER_LAYOUTS)
+        for name in names:
             secondary[f"int4_decoder_{name}"] = r = bench_decoder_layout(torch, name)
             prog = (f"program {r['program']['decode_tok_s']} tok/s" if "decode_tok_s" in r["program"]
                     else "program does not apply")

@@ -515,7 +515,7 @@ __device__ __forceinline__ void arg_wave(float& best, int& bi) {
     for (int sh = 32; sh >= 1; sh >>= 1) arg_take(best, bi, __shfl_xor(best, sh, 64), __shfl_xor(bi, sh, 64));
 }
 
-constexpr int gu_groups(int cpld) { return cpld == 3 ? 3 : 2; }
+constexpr int gu_groups(int cpld) { return cpld == 3 ? 3 : cpld == 4 ? 2 : 1; }
 // Slot plan of a wave's LDS region (chunks of 64 x 16 bytes), projection
 // workgroups, with the phase whose end requests each range:
 //   gate/up [0, kGu * CPLD)        end of A      read in D
@@ -946,6 +946,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         const int d_row2 = wave + kWaves < gd ? wg * gd + wave + kWaves : D;
         uint32_t sq[CPLD], so[CPLD], sg[kGu][CPLD], sd[kIChunksPerLane];
         Rows<kIChunksPerLane> dr2;
+        // With one gate/up group per wave in LDS (wide rows), the wave's next two
+        // groups and its second down row are read into registers at the end of A,
+        // their wait overlapping the attention phase instead of sitting inside D or
+        // before E (requested at the end of C or D, loads delayed the next poll,
+        // which completes in order behind them).
+        constexpr bool kGuReg = kGu == 1;
+        Rows<CPLD> gx, gx2;
         // Weights are requested two phases ahead of their use, into slot ranges no
         // phase in between reads: end of A -> gate/up, end of C -> down, end of D ->
         // next QKV, end of E -> next o_proj (region_lo).
@@ -1004,6 +1011,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 DPROG_STAMP(1 + l * 8 + 1);
                 wait_lds();
                 gu_fetch();
+                if constexpr (kGuReg) {
+                    const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
+                    const int lg = wave + kWaves, lg2 = lg + kWaves;
+                    const int g = lg < ggu ? wg * ggu + lg : ng_gu;
+                    const int g2 = lg2 < ggu ? wg * ggu + lg2 : ng_gu;
+                    load_rows<16, CPLD>(gx, wr, g < ng_gu ? 4 * g + grp : 2 * I, li16);
+                    load_rows<16, CPLD>(gx2, wr, g2 < ng_gu ? 4 * g2 + grp : 2 * I, li16);
+                    if (gd > kWaves)
+                        load_rows<64, kIChunksPerLane>(
+                            dr2, weight_ref(ly.down_weight, ly.down_scales, D, CI), d_row2, lane);
+                }
             }
 
             // Phase C: o_proj GEMV over the attention output.
@@ -1056,8 +1074,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
 #pragma unroll
                 for (int k = 0; k < kGu; ++k)
                     gu_out(row_dot<16, CPLD>(wreg + k * CPLD * 64, sg[k], sA0, sSum0, CD, li16), wave + k * kWaves);
+                int lg0 = wave + kGu * kWaves;
+                if constexpr (kGuReg) {
+                    gu_out(rows_dot<16, CPLD>(gx, sA0, sSum0, CD, li16), lg0);
+                    gu_out(rows_dot<16, CPLD>(gx2, sA0, sSum0, CD, li16), lg0 + kWaves);
+                    lg0 += 2 * kWaves;
+                }
                 const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
-                for (int lg = wave + kGu * kWaves; lg < ggu; lg += kWaves) {
+                for (int lg = lg0; lg < ggu; lg += kWaves) {
                     const int g = wg * ggu + lg;
                     Rows<CPLD> r;
                     load_rows<16, CPLD>(r, wr, g < ng_gu ? 4 * g + grp : 2 * I, li16);
@@ -1069,7 +1093,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 DPROG_STAMP(1 + l * 8 + 5);
                 wait_lds();
                 if (l + 1 < p.L) qkv_fetch(s_layers[l + 1]);
-                if (gd > kWaves)
+                if (!kGuReg && gd > kWaves)
                     load_rows<64, kIChunksPerLane>(
                         dr2, weight_ref(ly.down_weight, ly.down_scales, D, CI), d_row2, lane);
             }
@@ -1099,7 +1123,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
 
     // Phase F: final norm, lm_head GEMV (logits), argmax. The first lm_head rows are
     // requested before the wait for the last down output.
-    constexpr int kRing = 4;
+    constexpr int kRing = CPLD <= 4 ? 4 : 2;
     const int lm_ng = (p.V + 3) / 4;
     const WeightRef lw = weight_ref(p.lm_w, p.lm_s, p.V, CD);
     Rows<CPLD> ring[kRing];
@@ -1199,12 +1223,33 @@ struct StepShape {
     uint32_t flow_stride;
 };
 
+// Rows of each projection phase per projection workgroup (groups of 4 rows for
+// QKV, o_proj and gate/up; single rows for down) with `nc` projection workgroups.
+struct Shares {
+    int gq, go, ggu, gd;
+    bool fit() const {
+        return gq <= dprog::kWaves && go <= dprog::kWaves && gd <= 2 * dprog::kWaves && 2 * ggu <= 64;
+    }
+};
+Shares step_shares(const OrtmiDecoderDims* d, int nc) {
+    const int nq = (d->num_heads + 2 * d->kv_num_heads) * d->head_size;
+    Shares s;
+    s.gq = ((nq + 3) / 4 + nc - 1) / nc;
+    s.go = ((d->hidden + 3) / 4 + nc - 1) / nc;
+    s.ggu = ((2 * d->intermediate + 3) / 4 + nc - 1) / nc;
+    s.gd = (d->hidden + nc - 1) / nc;
+    return s;
+}
+
 // Key splits per attention head: about 160 keys each (their K/V rows fit one
-// workgroup's LDS), while at least half the workgroups stay on the projections.
+// workgroup's LDS), while at least half the workgroups stay on the projections
+// and each projection workgroup's share of rows fits its waves.
 int step_splits(const OrtmiDecoderDims* d, int nwg) {
     int ns = (d->kv_capacity + 159) / 160;
     ns = ns < 1 ? 1 : (ns > dprog::kNSMax ? dprog::kNSMax : ns);
-    while (ns > 1 && nwg - d->num_heads * ns < nwg / 2) --ns;
+    while (ns > 1 && (nwg - d->num_heads * ns < nwg / 2 ||
+                      !step_shares(d, nwg - d->num_heads * ns).fit()))
+        --ns;
     return ns;
 }
 
@@ -1273,9 +1318,9 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     ORTMI_REQUIRE(d.num_heads > 0 && d.kv_num_heads > 0 && d.num_heads % d.kv_num_heads == 0 &&
                       d.num_heads / d.kv_num_heads <= dprog::kGMax,
                   "decoder step: at most 8 query heads per KV head");
-    ORTMI_REQUIRE(d.hidden % 32 == 0 && d.hidden <= 2048, "decoder step: hidden % 32 == 0, <= 2048");
-    ORTMI_REQUIRE((d.num_heads * d.head_size) % 32 == 0 && d.num_heads * d.head_size <= 2048,
-                  "decoder step: num_heads * head_size % 32 == 0, <= 2048");
+    ORTMI_REQUIRE(d.hidden % 32 == 0 && d.hidden <= 3072, "decoder step: hidden % 32 == 0, <= 3072");
+    ORTMI_REQUIRE((d.num_heads * d.head_size) % 32 == 0 && d.num_heads * d.head_size <= 3072,
+                  "decoder step: num_heads * head_size % 32 == 0, <= 3072");
     ORTMI_REQUIRE(d.intermediate % 32 == 0 && d.intermediate <= 64 * 32 * dprog::kIChunksPerLane,
                   "decoder step: intermediate % 32 == 0, <= 10240");
     ORTMI_REQUIRE(d.vocab > 0 && embed_rows > 0 && d.kv_capacity > 0, "decoder step: bad sizes");
@@ -1286,14 +1331,11 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     const int nwg = program_grid();
     ORTMI_REQUIRE(nwg >= 4 * d.num_heads && nwg >= kXcds,
                   "decoder step: needs at least 4 compute units per query head");
-    const int nq = (d.num_heads + 2 * d.kv_num_heads) * d.head_size;
     const int ns = step_splits(dims, nwg);
     const int nc = nwg - d.num_heads * ns;
-    const int gq = ((nq + 3) / 4 + nc - 1) / nc, go = ((d.hidden + 3) / 4 + nc - 1) / nc;
-    const int ggu = ((2 * d.intermediate + 3) / 4 + nc - 1) / nc, gd = (d.hidden + nc - 1) / nc;
-    ORTMI_REQUIRE(gq <= dprog::kWaves && go <= dprog::kWaves && gd <= 2 * dprog::kWaves &&
-                      2 * ggu <= 64,
-                  "decoder step: projection rows exceed the per-workgroup share");
+    const Shares sh = step_shares(dims, nc);
+    const int gq = sh.gq, go = sh.go, ggu = sh.ggu, gd = sh.gd;
+    ORTMI_REQUIRE(sh.fit(), "decoder step: projection rows exceed the per-workgroup share");
     ORTMI_REQUIRE((int64_t)d.kv_num_heads * d.kv_capacity * d.head_size * 2 < (int64_t)INT32_MAX &&
                       (int64_t)d.vocab * d.hidden / 2 < (int64_t)INT32_MAX,
                   "decoder step: a cache or the lm_head exceeds 2 GiB");
@@ -1348,12 +1390,18 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     p.part = reinterpret_cast<uint64_t*>(ws + s.part);
     p.argp = reinterpret_cast<uint64_t*>(ws + s.argp);
 
-    const int cpld = d.hidden <= 1536 && d.num_heads * d.head_size <= 1536 ? 3 : 4;
-    const void* fn = d.head_size == 128
-                         ? (cpld == 3 ? (const void*)dprog::decode_program_kernel<128, 3>
-                                      : (const void*)dprog::decode_program_kernel<128, 4>)
-                         : (cpld == 3 ? (const void*)dprog::decode_program_kernel<64, 3>
-                                      : (const void*)dprog::decode_program_kernel<64, 4>);
+    // Chunks of 32 codes per lane for the K = hidden and K = H * head rows (16 lanes
+    // per row): 3, 4 or 6.
+    const int kmax = std::max(d.hidden, d.num_heads * d.head_size);
+    const int cpld = kmax <= 1536 ? 3 : kmax <= 2048 ? 4 : 6;
+    const void* fn =
+        d.head_size == 128
+            ? (cpld == 3   ? (const void*)dprog::decode_program_kernel<128, 3>
+               : cpld == 4 ? (const void*)dprog::decode_program_kernel<128, 4>
+                           : (const void*)dprog::decode_program_kernel<128, 6>)
+            : (cpld == 3   ? (const void*)dprog::decode_program_kernel<64, 3>
+               : cpld == 4 ? (const void*)dprog::decode_program_kernel<64, 4>
+                           : (const void*)dprog::decode_program_kernel<64, 6>);
     const int ho = d.num_heads * d.head_size;
     const size_t lds = ((size_t)dprog::kWaves * dprog::region_slots(cpld) * 64 + d.hidden / 8 +
                         std::max(ho, d.intermediate) / 8 + d.hidden / 8) * 16 +

@@ -4,7 +4,8 @@ variant of the program (libortmi_dprog_stamps.so, `build.py stamps`).
     python onnxruntime-mlx_amd/dprog_stamps.py [--total 576] [--layers 28]
 
 Runs the benchmark decoder's shape (hidden 1536, 12/2 heads, head 128, SwiGLU
-8960, vocab 151936; random weights) as the decode program at a given context and
+8960, vocab 151936; or the shape --hidden/--heads/... give; random weights) as the
+decode program at a given context and
 prints, as medians over layers 1..L-1, the time each phase of the dataflow takes:
 per projection phase from its input being ready to its output stored, per
 producer -> consumer hop from the last producer's store to the consumer's input
@@ -41,7 +42,14 @@ def _package():
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--total", type=int, default=576, help="total_sequence_length of the step")
-    ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--layers", type=int, default=28,
+                    help="at most 31: each layer takes 8 of the 256 stamp slots per workgroup")
+    ap.add_argument("--hidden", type=int)
+    ap.add_argument("--heads", type=int)
+    ap.add_argument("--kv-heads", type=int)
+    ap.add_argument("--head-dim", type=int)
+    ap.add_argument("--inter", type=int)
+    ap.add_argument("--vocab", type=int)
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--cooperative", type=int, default=0,
                     help="1: cooperative launch; 0: plain launch of the same grid")
@@ -61,7 +69,12 @@ def main():
     lab.ortmi_decoder_decode_step_stamps.argtypes = [ctypes.c_void_p, ctypes.c_int]
     lab.ortmi_decoder_decode_step_stamps.restype = ctypes.c_int
 
-    cfg = dec.DecoderConfig(layers=args.layers)
+    if not 1 <= args.layers <= 31:
+        raise SystemExit("--layers must be 1..31 (8 stamp slots per layer, 256 per workgroup)")
+    shape = {k: v for k, v in (("hidden", args.hidden), ("heads", args.heads),
+                               ("kv_heads", args.kv_heads), ("head_dim", args.head_dim),
+                               ("inter", args.inter), ("vocab", args.vocab)) if v is not None}
+    cfg = dec.DecoderConfig(layers=args.layers, **shape)
     w = dec.make_weights(cfg, seed=4)
     cap = max(640, args.total)
     kv = [(torch.randn((1, cfg.kv_heads, cap, cfg.head_dim), dtype=torch.float16, device="cuda"),

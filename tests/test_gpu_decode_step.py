@@ -70,12 +70,18 @@ def _step_both(runner, prog, length):
     # the Llama-3.2-1B layout: hidden 2048, 32/8 heads of 64, SwiGLU 8192 (two down
     # rows per wave, gate/up rows beyond the prefetched ones read in the phase)
     dict(G=4, heads=32, kv_heads=8, head_dim=64, hidden=2048, inter=8192),
+    # the Phi-4-mini layout: hidden 3072, 24/8 heads of 128, SwiGLU 8192 (6 chunks per
+    # lane, one prefetched gate/up group); a 400-row cache asks for 3 key splits and
+    # gets 2, the most that leave each projection workgroup at most 16 down rows
+    dict(G=3, heads=24, kv_heads=8, head_dim=128, hidden=3072, inter=8192, cap=400),
+    # the same layout with one key split (a 64-row cache)
+    dict(G=3, heads=24, kv_heads=8, head_dim=128, hidden=3072, inter=8192),
 ])
 def test_decode_program_matches_ep_steps(ortmi, dec, dprog, monkeypatch, shape):
     """2-layer decoders (head 128 with G query heads per KV head; head 64 at hidden
-    1024 and at the Qwen2.5-0.5B and Llama-3.2-1B layouts): 10 decode steps after a
-    19-token prompt, the program against the EP's op-by-op path (ORTMI_EP_PROGRAM=0)
-    on the same cache."""
+    1024 and at the Qwen2.5-0.5B and Llama-3.2-1B layouts; the Phi-4-mini layout at
+    hidden 3072): 10 decode steps after a 19-token prompt, the program against the
+    EP's op-by-op path (ORTMI_EP_PROGRAM=0) on the same cache."""
     monkeypatch.setenv("ORTMI_EP_PROGRAM", "0")
     G = shape["G"]
     H = shape.get("heads", 2 * G)
@@ -84,8 +90,9 @@ def test_decode_program_matches_ep_steps(ortmi, dec, dprog, monkeypatch, shape):
                             kv_heads=shape.get("kv_heads", 2), head_dim=hd,
                             inter=shape.get("inter", 512), vocab=4096, max_pos=512)
     w = dec.make_weights(cfg, seed=50 + G + hd)
-    runner = dec.DecoderRunner(cfg, w, cap=64, max_prompt=32)
-    prog = dprog.DecodeProgram(cfg, w, runner.kv, 64)
+    cap = shape.get("cap", 64)
+    runner = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=32)
+    prog = dprog.DecodeProgram(cfg, w, runner.kv, cap)
     prompt = np.random.default_rng(G).integers(0, cfg.vocab, size=19)
     runner.reset()
     runner.prefill(prompt)
@@ -102,6 +109,42 @@ def test_decode_program_matches_ep_steps(ortmi, dec, dprog, monkeypatch, shape):
         assert pt == int(np.argmax(pl)), "program token is not the argmax of its logits"
         assert err <= 2.0 ** -7 * max(1.0, scale)
         assert kvd <= 2.0 ** -7 * 4
+
+
+def test_decode_program_wide_layout_long_context(ortmi, dec, dprog, monkeypatch):
+    """The Phi-4-mini layout (hidden 3072, 24/8 heads of 128, SwiGLU 8192, vocab
+    200064) with 4 layers: a 512-token prompt, then 8 decode steps teacher-forced
+    against the op path on the same cache. Two key splits of about 260 keys take the
+    register ring past the LDS-resident keys, and each wave streams about 25 lm_head
+    row groups through its two-entry ring. A token may differ only where the op path's top two logits lie
+    within the logit tolerance."""
+    monkeypatch.setenv("ORTMI_EP_PROGRAM", "0")
+    cfg = dec.DecoderConfig(layers=4, hidden=3072, heads=24, kv_heads=8, head_dim=128, inter=8192,
+                            vocab=200064, max_pos=1024)
+    w = dec.make_weights(cfg, seed=8)
+    cap = 640
+    runner = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=512)
+    prog = dprog.DecodeProgram(cfg, w, runner.kv, cap)
+    prompt = np.random.default_rng(9).integers(0, cfg.vocab, size=512)
+    runner.reset()
+    runner.prefill(prompt)
+    length = len(prompt)
+    for step in range(8):
+        el, pl, et, pt, kvd = _step_both(runner, prog, length)
+        runner.length = length + 1
+        length += 1
+        scale = float(np.abs(el).max())
+        err = float(np.abs(el - pl).max())
+        tol = 2.0 ** -7 * max(1.0, scale)
+        top2 = np.sort(el.astype(np.float32))[-2:]
+        margin = float(top2[1] - top2[0])
+        print(f"step {step}: max |logit diff| {err:.3e} (|logit| up to {scale:.2f}), K/V row diff "
+              f"{kvd:.3e}, tokens ep {et} program {pt}, op-path top-2 margin {margin:.4f}", flush=True)
+        assert np.isfinite(pl).all()
+        assert pt == int(np.argmax(pl)), "program token is not the argmax of its logits"
+        assert err <= tol
+        assert kvd <= 2.0 ** -7 * 4
+        assert pt == et or margin <= 2 * tol
 
 
 def test_decode_program_full_size_greedy_strict(ortmi, oracle, dec, dprog, capsys):
