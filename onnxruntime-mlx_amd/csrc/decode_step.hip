@@ -951,7 +951,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         // their wait overlapping the attention phase instead of sitting inside D or
         // before E (requested at the end of C or D, loads delayed the next poll,
         // which completes in order behind them).
-        constexpr bool kGuReg = kGu == 1;
+        constexpr bool kGuReg = kGu <= 2;
         Rows<CPLD> gx, gx2;
         // Weights are requested two phases ahead of their use, into slot ranges no
         // phase in between reads: end of A -> gate/up, end of C -> down, end of D ->
@@ -1013,7 +1013,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 gu_fetch();
                 if constexpr (kGuReg) {
                     const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
-                    const int lg = wave + kWaves, lg2 = lg + kWaves;
+                    const int lg = wave + kGu * kWaves, lg2 = lg + kWaves;
                     const int g = lg < ggu ? wg * ggu + lg : ng_gu;
                     const int g2 = lg2 < ggu ? wg * ggu + lg2 : ng_gu;
                     load_rows<16, CPLD>(gx, wr, g < ng_gu ? 4 * g + grp : 2 * I, li16);
