@@ -99,7 +99,9 @@ struct GemvGroup {
 
 // Lane l owns the CPL consecutive 32-code chunks [l*CPL, (l+1)*CPL) of every row,
 // so a row costs one 16*CPL-byte weight run, CPL adjacent scales and one or two
-// zero-point bytes per lane. The activation loads are issued first, then the
+// zero-point bytes per lane; or (IL, fp16 rows of whole 64-chunk runs at block 32)
+// chunks l, l + 64, ..., so each of the row's CPL weight loads reads 1 KB
+// contiguous, each scale load 128 bytes, with one zero-point byte per chunk. The activation loads are issued first, then the
 // weight loads of the wave's first D row groups; the activations go through LDS
 // (one copy per workgroup) into VGPRs while the weights are in flight. Row groups
 // of R rows are dealt to waves round-robin; a ring of D groups keeps the next
@@ -167,7 +169,7 @@ static inline size_t gemv_merge_bytes(int K, int hd, int splits) {
 
 template <typename T, int BS, int CPL, int R, int D, bool PRO = false, bool PAIR = false,
           bool SV = false, bool H2 = std::is_same<T, half_t>::value, bool NT = true,
-          bool MRG = false, int RW = 1>
+          bool MRG = false, int RW = 1, bool IL = false>
 __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
                                                         const uint8_t* __restrict__ B,
                                                         const T* __restrict__ S,
@@ -177,9 +179,10 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     static_assert(!PAIR || R == 2, "SwiGLU pairs take two rows per group");
     static_assert(!H2 || std::is_same<T, half_t>::value, "fp16 pairs need fp16 activations");
     static_assert(D >= 1, "ring depth");
+    static_assert(!IL || (H2 && !SV && BS == 32), "interleaved chunks: fp16 pairs, block 32");
     extern __shared__ float4 sA[];
     __shared__ float s_red[4];
-    constexpr int ZB = zp_window(BS, CPL);
+    constexpr int ZB = IL ? CPL : zp_window(BS, CPL);
     using Group = GemvGroup<T, R, CPL, ZB>;
     const int Kp = nb * BS;
     const int C = Kp / 32;  // 32-code chunks per row
@@ -196,6 +199,9 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     const size_t row_bytes = (size_t)Kp / 2;
     const int zp_cols = (nb + 1) / 2;
     const int c0 = li * CPL;
+    // Chunk j of this lane: CPL consecutive chunks, or (IL) chunks li + j * LR, so
+    // that each load instruction of a unit reads one contiguous run.
+    auto chunk = [&](int j) { return IL ? li + j * LR : c0 + j; };
 
     // 1. activation loads (16 bytes each), all in flight before anything else.
     constexpr int EPL = 16 / sizeof(T);
@@ -271,13 +277,14 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
 #pragma unroll
             for (int t = 0; t < ZB; ++t) {
                 // Loaded either way (no records without Z): no load behind a branch.
+                const int zcol = IL ? min(chunk(t), C - 1) / 2 : blk0 / 2 + t;
                 const uint8_t zb = (uint8_t)__builtin_amdgcn_raw_buffer_load_b8(
-                    rz, zoff + (uint32_t)min(blk0 / 2 + t, zp_cols - 1), 0, 0);
+                    rz, zoff + (uint32_t)min(zcol, zp_cols - 1), 0, 0);
                 g.z[r][t] = Z ? zb : (uint8_t)0x88;
             }
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
-                const int c = c0 + j;
+                const int c = chunk(j);
                 const bool ok = live && c < C;
                 const uint32_t boff = ok ? (uint32_t)((size_t)n * row_bytes) + 16u * c : b_end;
                 // Streamed once: optionally non-temporal (cache policy nt).
@@ -431,7 +438,7 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
     uint4 ah[H2 ? CPL : 1][4];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int c = c0 + j;
+        const int c = chunk(j);
         if constexpr (H2) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -462,12 +469,16 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
             float total = 0.f;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
-                const int blk = (32 * min(c0 + j, C - 1)) / BS;
+                const int blk = (32 * min(chunk(j), C - 1)) / BS;
                 const int d = blk / 2 - blk0 / 2;
                 uint8_t zbyte = gr.z[r][0];
+                if constexpr (IL) {
+                    zbyte = gr.z[r][j];
+                } else {
 #pragma unroll
-                for (int t = 1; t < ZB; ++t)
-                    if (d == t) zbyte = gr.z[r][t];
+                    for (int t = 1; t < ZB; ++t)
+                        if (d == t) zbyte = gr.z[r][t];
+                }
                 const int zq = nibble(zbyte, blk & 1);
                 if constexpr (H2) {
                     const half_t zo = (half_t)(1024 + zq);
@@ -512,13 +523,13 @@ __global__ __launch_bounds__(256) void mnb_gemv4_kernel(const T* __restrict__ A,
 
 // Launch of one kernel instance: `grid` workgroups of 4 waves.
 template <typename T, int BS, int CPL, int R, int D, bool PRO, bool PAIR, bool SV, bool H2,
-          bool NT = true, bool MRG = false, int RW = 1>
+          bool NT = true, bool MRG = false, int RW = 1, bool IL = false>
 static int launch_gemv4_inst(const T* A, const uint8_t* B, const T* S, const uint8_t* Z, T* Y,
                              int N, int K, int nb, const GemvPrologue<T>& pro, long grid,
                              hipStream_t st) {
     size_t lds = gemv_stage_bytes<T, H2>(nb * BS);
     if constexpr (MRG) lds += gemv_merge_bytes(K, pro.hd, pro.splits);
-    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, D, PRO, PAIR, SV, H2, NT, MRG, RW>),
+    hipLaunchKernelGGL((mnb_gemv4_kernel<T, BS, CPL, R, D, PRO, PAIR, SV, H2, NT, MRG, RW, IL>),
                        dim3((unsigned)grid), dim3(256), lds, st, A, B, S, Z, Y, N, K, nb, pro);
     return check_launch("mnb_gemv4");
 }
@@ -559,16 +570,31 @@ static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint
 #define ORTMI_GEMV_INST(DV, SVV, NTV)                                                              \
     return launch_gemv4_inst<T, BS, CPL, R, DV, PRO, PAIR, SVV, H2, NTV, MRG>(A, B, S, Z, Y, N, K, \
                                                                              nb, pro, grid, st)
+    // Interleaved chunks (lane l owns chunks l, l + 64, ...: every weight load of a
+    // row one contiguous 1 KB run) for fp16 rows of a whole number of 64-chunk runs,
+    // with non-temporal loads. Measured on MI355X in graph replay against the
+    // consecutive chunks: 4096 x 14336 13.4 -> 11.8 us, 3072 x 8192 9.1 -> 6.8 us,
+    // 8192 x 8192 (zero points) 14.8 -> 13.3 us, 4096 x 4096 4.9 -> 4.6 us; equal at
+    // 6144 and 11008 x 4096 (kept consecutive above 16 row groups per CU at two
+    // chunks per lane); 1536 x 8960 (280 chunks) 5.8 -> 6.2 us, so rows with a
+    // partial run keep consecutive chunks.
+    const bool il = H2 && BS == 32 && nb % 64 == 0 && (CPL >= 3 || groups <= 16 * cus);
+#define ORTMI_GEMV_IL(DV)                                                                         \
+    return launch_gemv4_inst<T, BS, CPL, R, DV, PRO, PAIR, false, H2, true, MRG, 1, H2 && BS == 32>( \
+        A, B, S, Z, Y, N, K, nb, pro, grid, st)
     if constexpr (CPL >= 6 && H2) {
         // fp16 rows of K > 10240 (6-8 chunks per lane): two rows in flight per wave
         // (Mistral-7B's down_proj 4096 x 14336: 14.3 -> 13.1 us; 16 rows per
         // workgroup instead of 8 measured 14.7 us).
+        if (il) ORTMI_GEMV_IL(2);
         if (sv) ORTMI_GEMV_INST(2, kSV, false);
         ORTMI_GEMV_INST(2, false, false);
     } else if constexpr (CPL >= 3) {
+        if (il) ORTMI_GEMV_IL(1);
         if (sv) ORTMI_GEMV_INST(1, kSV, false);
         ORTMI_GEMV_INST(1, false, false);
     } else {
+        if (il && !longwalk) ORTMI_GEMV_IL(2);
         if (longwalk) {
             if (sv) ORTMI_GEMV_INST(4, kSV, false);
             ORTMI_GEMV_INST(4, false, false);
@@ -577,6 +603,7 @@ static int launch_gemv4_cpl(const T* A, const uint8_t* B, const T* S, const uint
         ORTMI_GEMV_INST(2, false, true);
     }
 #undef ORTMI_GEMV_INST
+#undef ORTMI_GEMV_IL
 }
 
 template <typename T, int BS, bool PRO = false, bool PAIR = false, bool MRG = false>

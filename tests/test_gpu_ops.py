@@ -75,7 +75,7 @@ def _mnb_inputs(rng, M, N, K, block, bits=4, asym=True, zp_all8=False, dtype=np.
     (1536, 2048, 32, False, False), (1536, 1536, 32, True, False), (1536, 17920, 32, True, True),
     (8960, 1536, 32, True, False), (4096, 512, 128, True, True), (1000, 64, 64, False, True),
     (1536, 24576, 32, True, False), (1536, 45056, 32, False, True),
-    (14336, 512, 32, True, False)])
+    (14336, 512, 32, True, False), (4096, 1024, 32, True, True), (8192, 768, 32, True, False)])
 def test_mnb_decode_fused(ortmi, oracle, K, N, block, skip, pair):
     """Norm prologue and SwiGLU-pair epilogue of the decode GEMV against the unfused
     ops of the oracle (norm rounded to fp16, matmul in fp64, SwiGLU op by op)."""
@@ -215,12 +215,14 @@ def test_mnb_gemv_config1_shape(ortmi, oracle):
 @pytest.mark.parametrize("K,block,N", [(1536, 32, 300), (8960, 32, 300), (4096, 64, 300),
                                        (1536, 32, 20700), (520, 32, 21001), (1000, 64, 20481),
                                        (11008, 32, 300), (14336, 32, 300), (12000, 64, 257),
-                                       (16384, 128, 200)])
+                                       (16384, 128, 200), (2048, 32, 999), (4096, 32, 4096),
+                                       (8192, 32, 3072), (16384, 32, 515)])
 def test_mnb_gemv_fp16(ortmi, oracle, K, block, N):
     """Includes long walks over short rows (N beyond 80 rows per CU, K <= 1536),
-    which take four rows per wave, with an odd N and a partial final block, and the
+    which take four rows per wave, with an odd N and a partial final block, the
     long rows of 7B-class down projections (K = 11008, 14336, up to 16384: six to
-    eight 32-code chunks per lane)."""
+    eight 32-code chunks per lane), and rows of whole 64-chunk runs at block 32,
+    which take interleaved chunks (K = 2048 to 16384, one to eight per lane)."""
     import torch
 
     rng = np.random.default_rng(K * 3 + block + N)
@@ -229,6 +231,18 @@ def test_mnb_gemv_fp16(ortmi, oracle, K, block, N):
     assert Y.dtype == torch.float16
     ref = oracle.mnb_matmul(A, B, s, zp, N, K, 4, block)
     assert_f16_close(host(Y), ref, what="gemv fp16")
+
+
+@pytest.mark.parametrize("K,N", [(4096, 1000), (8192, 700), (14336, 257), (2048, 64)])
+def test_mnb_gemv_fp16_interleaved_symmetric(ortmi, oracle, K, N):
+    """Interleaved chunks (block 32, rows of whole 64-chunk runs) without zero
+    points, the decoder's symmetric form: every code is offset by 8."""
+    rng = np.random.default_rng(K + N + 7)
+    A, B, s, zp = _mnb_inputs(rng, 1, N, K, 32, asym=False, dtype=np.float16)
+    assert zp is None
+    Y = ortmi.matmul_nbits(dev(A), dev(B), dev(s), None, K=K, N=N, block_size=32)
+    ref = oracle.mnb_matmul(A, B, s, None, N, K, 4, 32)
+    assert_f16_close(host(Y), ref, what="gemv fp16 symmetric")
 
 
 @pytest.mark.parametrize("M", [2, 8, 64, 130])
