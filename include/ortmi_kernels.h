@@ -149,12 +149,13 @@ int ortmi_matmul_nbits_decode_merge(const float* partials, int64_t splits, int64
  * (Sigmoid/Mul/Mul), down MatMulNBits; final SkipSimplifiedLayerNormalization;
  * lm_head MatMulNBits) plus the greedy argmax of the logits.
  * Forms: fp16, 4-bit symmetric weights (no zero points), block 32, head size
- * 64 or 128, non-interleaved rotary (or none), at most 8 query heads per KV
+ * 64, 96 or 128, non-interleaved rotary (or none), at most 8 query heads per KV
  * head, hidden and num_heads * head_size multiples of 32 up to 3072,
  * intermediate a multiple of 32 up to 10240, and projection rows that fit the
- * per-workgroup share (down_proj: at most two rows per wave of the projection
- * workgroups; the key splits per head shrink until the rows fit). Other forms return ORTMI_E_INVALID before any launch (the caller
- * runs the graph op by op).
+ * per-workgroup share (QKV: at most two groups of 4 rows per wave, down_proj: at
+ * most two rows per wave of the projection workgroups; the key splits per head
+ * shrink until the rows fit). Other forms return ORTMI_E_INVALID before any
+ * launch (the caller runs the graph op by op).
  * Weights keep the MatMulNBits layout [N, K/32, 16] with fp16 scales [N * K/32];
  * qkv_weight holds the q rows, then the k rows, then the v rows of one merged
  * projection; gate_up_weight interleaves gate row i (row 2i) and up row i

@@ -620,10 +620,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         // rows sit in LDS, requested right after the previous layer's attention, so
         // the wait for q/k/v never queues behind them. Split 0 of each head merges
         // the others' partials (tagged 64-bit words: value, tag) into the output.
-        // A key row is LPR lanes of 8 dims (16 lanes for head 128, 8 for head 64);
-        // a wave holds GPW keys per step.
-        constexpr int LPR = HD / 8, GPW = 64 / LPR, KEYS = kWaves * GPW;
+        // A key row is LPR lanes of 8 dims (16 lanes for head 128, 8 for head 64;
+        // head 96 takes 16-lane rows whose last 4 lanes hold no dims: their loads
+        // read zeros and they store nothing); a wave holds GPW keys per step.
+        constexpr int LPR = HD <= 64 ? 8 : 16, GPW = 64 / LPR, KEYS = kWaves * GPW;
         const int lr = lane % LPR, ag = lane / LPR;
+        const bool padl = lr * 8 >= HD;
         const int NS = p.ns, a = wg - NC;
         const int h = a / NS, s = a % NS, kvh = h / p.G;
         const int ks = (total + NS - 1) / NS;
@@ -633,8 +635,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         const int slot = wave * GPW + ag;  // key slot of this lane group
         auto kv_off = [&](int t) -> uint32_t {
             const int key = k0 + slot + t * KEYS;
-            return key < k1 && key < ctx ? ((uint32_t)(kvh * p.cap + key) * HD + lr * 8) * 2u
-                                         : kv_bytes;
+            return key < k1 && key < ctx && !padl
+                       ? ((uint32_t)(kvh * p.cap + key) * HD + lr * 8) * 2u
+                       : kv_bytes;
         };
         auto kv_fetch = [&](const OrtmiDecoderLayer& ly) {
             const __amdgpu_buffer_rsrc_t rk = rsrc(ly.k_cache, kv_bytes), rv = rsrc(ly.v_cache, kv_bytes);
@@ -666,8 +669,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             const uint32_t off[3] = {(uint32_t)(h * HD + lr * 8) * 4u,
                                      (uint32_t)((H + kvh) * HD + lr * 8) * 4u,
                                      (uint32_t)((H + KV + kvh) * HD + lr * 8) * 4u};
-            uint4 qkv3[3];
-            const bool ok = poll_units<3>(rsrc(f_qkv, (uint32_t)NQ * 4u), off, 7u, f, qkv3);
+            uint4 qkv3[3] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+            const uint32_t none = (uint32_t)NQ * 4u;
+            const uint32_t offp[3] = {padl ? none : off[0], padl ? none : off[1], padl ? none : off[2]};
+            const bool ok = poll_units<3>(rsrc(f_qkv, (uint32_t)NQ * 4u), offp, padl ? 0u : 7u, f, qkv3);
             DPROG_STAMP(1 + l * 8 + 2);
             float q[8], kn[8], vn[8];
             {
@@ -703,7 +708,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             // a flat store would also count against the LDS counter, and the LDS
             // reads below would wait for it to complete.
             {
-                const bool app = ok && h % p.G == 0 && ctx >= k0 && ctx < k1 && wave == 0 && ag == 0;
+                const bool app =
+                    ok && h % p.G == 0 && ctx >= k0 && ctx < k1 && wave == 0 && ag == 0 && !padl;
                 const uint32_t ao =
                     app ? (uint32_t)(((size_t)(kvh * p.cap + ctx) * HD + lr * 8) * 2) : kv_bytes;
                 __builtin_amdgcn_raw_buffer_store_b128(
@@ -818,7 +824,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 s_am[wave] = m;
                 s_al[wave] = lsum;
             }
-            if (ag == 0) {
+            if (ag == 0 && !padl) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) sO[wave * HD + lr * 8 + e] = o[e];
             }
@@ -939,6 +945,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         const int ng_q = (NQ + 3) / 4, ng_o = (D + 3) / 4, ng_gu = (2 * I + 3) / 4;
         const int gq = p.gq, go = p.go, ggu = p.ggu, gd = p.gd;
         const int q_g = wave < gq ? wg * gq + wave : ng_q;  // QKV group
+        // A second QKV group per wave when the share exceeds one group per wave: read
+        // into registers at the end of the previous layer's A (or before the first).
+        const int q_g2 = wave + kWaves < gq ? wg * gq + wave + kWaves : ng_q;
         const int o_g = wave < go ? wg * go + wave : ng_o;  // o_proj group
         const int d_row = wave < gd ? wg * gd + wave : D;   // down row
         // A second down row per wave when the share exceeds one row per wave: read
@@ -952,7 +961,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         // before E (requested at the end of C or D, loads delayed the next poll,
         // which completes in order behind them).
         constexpr bool kGuReg = kGu <= 2;
-        Rows<CPLD> gx, gx2;
+        Rows<CPLD> gx, gx2, qx;
+        auto qkv2_load = [&](const OrtmiDecoderLayer& lz) {
+            const int li = opaque(threadIdx.x & 63) & 15, gp = (threadIdx.x & 63) >> 4;
+            load_rows<16, CPLD>(qx, weight_ref(lz.qkv_weight, lz.qkv_scales, NQ, CD),
+                                q_g2 < ng_q ? 4 * q_g2 + gp : NQ, li);
+        };
         // Weights are requested two phases ahead of their use, into slot ranges no
         // phase in between reads: end of A -> gate/up, end of C -> down, end of D ->
         // next QKV, end of E -> next o_proj (region_lo).
@@ -961,6 +975,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             fetch_rows<16, CPLD>(wr, q_g < ng_q ? 4 * q_g + grp : NQ, li16, wreg, sq);
             const WeightRef wo = weight_ref(s_layers[0].o_weight, s_layers[0].o_scales, D, CO);
             fetch_rows<16, CPLD>(wo, o_g < ng_o ? 4 * o_g + grp : D, li16, wreg + kLo * 64, so);
+            if (gq > kWaves) qkv2_load(s_layers[0]);
         }
         const uint32_t* in_dout = nullptr;
         for (int l = 0; l < p.L; ++l) {
@@ -1005,12 +1020,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                 __builtin_amdgcn_s_waitcnt(0);
                 const float v = group_sum<16>(row_dot<16, CPLD>(wreg, sq, sA0, sSum0, CD, li16));
                 if (li16 == 0 && wave < gq) s_out[wave * 4 + grp] = v;
+                if (gq > kWaves) {
+                    const float v2 = group_sum<16>(rows_dot<16, CPLD>(qx, sA0, sSum0, CD, li16));
+                    if (li16 == 0 && wave + kWaves < gq) s_out[(wave + kWaves) * 4 + grp] = v2;
+                }
                 __syncthreads();
                 if (tid < 4 * gq && 4 * wg * gq + tid < NQ)
                     put(rsrc(f_qkv, (uint32_t)NQ * 4), 4 * wg * gq + tid, s_out[tid], tag);
                 DPROG_STAMP(1 + l * 8 + 1);
                 wait_lds();
                 gu_fetch();
+                if (gq > kWaves && l + 1 < p.L) qkv2_load(s_layers[l + 1]);
                 if constexpr (kGuReg) {
                     const WeightRef wr = weight_ref(ly.gate_up_weight, ly.gate_up_scales, 2 * I, CD);
                     const int lg = wave + kGu * kWaves, lg2 = lg + kWaves;
@@ -1228,7 +1248,8 @@ struct StepShape {
 struct Shares {
     int gq, go, ggu, gd;
     bool fit() const {
-        return gq <= dprog::kWaves && go <= dprog::kWaves && gd <= 2 * dprog::kWaves && 2 * ggu <= 64;
+        return gq <= 2 * dprog::kWaves && go <= dprog::kWaves && gd <= 2 * dprog::kWaves &&
+               2 * ggu <= 64;
     }
 };
 Shares step_shares(const OrtmiDecoderDims* d, int nc) {
@@ -1314,7 +1335,8 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
     ORTMI_REQUIRE(d.dtype == ORTMI_F16, "decoder step: fp16 only");
     ORTMI_REQUIRE(d.block_size == 32, "decoder step: block size 32 only");
     ORTMI_REQUIRE(d.layers >= 1 && d.layers <= dprog::kMaxLayers, "decoder step: 1 to 64 layers");
-    ORTMI_REQUIRE(d.head_size == 128 || d.head_size == 64, "decoder step: head size 64 or 128");
+    ORTMI_REQUIRE(d.head_size == 128 || d.head_size == 96 || d.head_size == 64,
+                  "decoder step: head size 64, 96 or 128");
     ORTMI_REQUIRE(d.num_heads > 0 && d.kv_num_heads > 0 && d.num_heads % d.kv_num_heads == 0 &&
                       d.num_heads / d.kv_num_heads <= dprog::kGMax,
                   "decoder step: at most 8 query heads per KV head");
@@ -1399,6 +1421,10 @@ extern "C" int ortmi_decoder_decode_step(const OrtmiDecoderLayer* layers, const 
             ? (cpld == 3   ? (const void*)dprog::decode_program_kernel<128, 3>
                : cpld == 4 ? (const void*)dprog::decode_program_kernel<128, 4>
                            : (const void*)dprog::decode_program_kernel<128, 6>)
+        : d.head_size == 96
+            ? (cpld == 3   ? (const void*)dprog::decode_program_kernel<96, 3>
+               : cpld == 4 ? (const void*)dprog::decode_program_kernel<96, 4>
+                           : (const void*)dprog::decode_program_kernel<96, 6>)
             : (cpld == 3   ? (const void*)dprog::decode_program_kernel<64, 3>
                : cpld == 4 ? (const void*)dprog::decode_program_kernel<64, 4>
                            : (const void*)dprog::decode_program_kernel<64, 6>);

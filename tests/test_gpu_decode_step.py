@@ -76,6 +76,13 @@ def _step_both(runner, prog, length):
     dict(G=3, heads=24, kv_heads=8, head_dim=128, hidden=3072, inter=8192, cap=400),
     # the same layout with one key split (a 64-row cache)
     dict(G=3, heads=24, kv_heads=8, head_dim=128, hidden=3072, inter=8192),
+    # the Phi-3.5-mini layout: 32/32 heads of 96 (16-lane key rows, 4 lanes idle),
+    # 9216 QKV rows (a second QKV group per wave in registers), one key split
+    dict(G=1, heads=32, kv_heads=32, head_dim=96, hidden=3072, inter=8192),
+    # the same with two key splits (a 400-row cache)
+    dict(G=1, heads=32, kv_heads=32, head_dim=96, hidden=3072, inter=8192, cap=400),
+    # head 96 with 4 query heads per KV head at hidden 1536
+    dict(G=4, heads=16, kv_heads=4, head_dim=96, hidden=1536, inter=4096),
 ])
 def test_decode_program_matches_ep_steps(ortmi, dec, dprog, monkeypatch, shape):
     """2-layer decoders (head 128 with G query heads per KV head; head 64 at hidden
@@ -111,16 +118,20 @@ def test_decode_program_matches_ep_steps(ortmi, dec, dprog, monkeypatch, shape):
         assert kvd <= 2.0 ** -7 * 4
 
 
-def test_decode_program_wide_layout_long_context(ortmi, dec, dprog, monkeypatch):
+@pytest.mark.parametrize("layout", [
+    dict(heads=24, kv_heads=8, head_dim=128, vocab=200064),  # Phi-4-mini
+    dict(heads=32, kv_heads=32, head_dim=96, vocab=32064),  # Phi-3.5-mini
+])
+def test_decode_program_wide_layout_long_context(ortmi, dec, dprog, monkeypatch, layout):
     """The Phi-4-mini layout (hidden 3072, 24/8 heads of 128, SwiGLU 8192, vocab
-    200064) with 4 layers: a 512-token prompt, then 8 decode steps teacher-forced
-    against the op path on the same cache. Two key splits of about 260 keys take the
-    register ring past the LDS-resident keys, and each wave streams about 25 lm_head
-    row groups through its two-entry ring. A token may differ only where the op path's top two logits lie
-    within the logit tolerance."""
+    200064) and the Phi-3.5-mini layout (32/32 heads of 96, vocab 32064) with 4
+    layers: a 512-token prompt, then 8 decode steps teacher-forced against the op
+    path on the same cache. Two key splits of about 260 keys take the register ring
+    past the LDS-resident keys, and at Phi-4-mini's vocabulary each wave streams
+    about 25 lm_head row groups through its two-entry ring. A token may differ only
+    where the op path's top two logits lie within the logit tolerance."""
     monkeypatch.setenv("ORTMI_EP_PROGRAM", "0")
-    cfg = dec.DecoderConfig(layers=4, hidden=3072, heads=24, kv_heads=8, head_dim=128, inter=8192,
-                            vocab=200064, max_pos=1024)
+    cfg = dec.DecoderConfig(layers=4, hidden=3072, inter=8192, max_pos=1024, **layout)
     w = dec.make_weights(cfg, seed=8)
     cap = 640
     runner = dec.DecoderRunner(cfg, w, cap=cap, max_prompt=512)
