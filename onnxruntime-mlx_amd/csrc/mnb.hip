@@ -101,8 +101,9 @@ struct GemvGroup {
 // so a row costs one 16*CPL-byte weight run, CPL adjacent scales and one or two
 // zero-point bytes per lane; or (IL, fp16 rows of whole 64-chunk runs at block 32)
 // chunks l, l + 64, ..., so each of the row's CPL weight loads reads 1 KB
-// contiguous, each scale load 128 bytes, with one zero-point byte per chunk. The activation loads are issued first, then the
-// weight loads of the wave's first D row groups; the activations go through LDS
+// contiguous, each scale load 128 bytes, with one zero-point byte per chunk. The
+// activation loads are issued first, then the weight loads of the wave's first D
+// row groups; the activations go through LDS
 // (one copy per workgroup) into VGPRs while the weights are in flight. Row groups
 // of R rows are dealt to waves round-robin; a ring of D groups keeps the next
 // D - 1 groups' loads in flight while one group is reduced.
