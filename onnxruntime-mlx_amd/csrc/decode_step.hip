@@ -135,6 +135,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t b
                                              (int)__builtin_amdgcn_readfirstlane(bytes), kBufferWord3);
 }
 template <int POL>
+__device__ __forceinline__ uint2 ld64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POL));
+}
+template <int POL>
 __device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL);
     return make_uint4(v.x, v.y, v.z, v.w);
@@ -853,35 +857,45 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             } else if (NS > 1) {
                 // Split 0 folds in splits 1 .. NS-1: thread d < HD waits for word d of
                 // every sibling, thread j - 1 (j < NS) also for sibling j's max and sum,
-                // which it passes on through LDS. Every word is requested at once; only
-                // those not yet carrying this launch's tag are requested again.
-                uint64_t wo[kNSMax];
-                uint64_t wm = 0, wl = 0;
+                // which it passes on through LDS. Each round requests every word still
+                // missing at once, with buffer loads that never branch (a word already
+                // held, or not wanted, takes an offset past the buffer and touches no
+                // memory), so a round costs one round trip. Reloads behind per-word
+                // branches were each followed by a wait for that load, one round trip
+                // per sibling per round.
                 const int mj = tid + 1;  // sibling whose max / sum this thread fetches
-                const bool ml = mj < NS;
-                auto rec = [&](int j) { return f_part + (size_t)(h * NS + j) * kPartWords; };
+                const uint32_t pbytes = (uint32_t)(NS * kPartWords * 8);
+                const __amdgpu_buffer_rsrc_t rp = rsrc(f_part + (size_t)h * NS * kPartWords, pbytes);
+                float vo[kNSMax];
                 unsigned pend = 0;
-                if (tid < HD) {
+#pragma unroll
+                for (int j = 1; j < kNSMax; ++j) {
+                    vo[j] = 0.f;
+                    if (tid < HD && j < NS) pend |= 1u << j;
+                }
+                if (tid < HD && mj < NS) pend |= 1u;
+                const uint32_t off_m = (uint32_t)((mj * kPartWords + HD) * 8);
+                uint2 wv[kNSMax], wm, wl;
+                auto request = [&]() {
 #pragma unroll
                     for (int j = 1; j < kNSMax; ++j)
-                        if (j < NS) {
-                            wo[j] = __hip_atomic_load(rec(j) + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            pend |= 1u << j;
-                        }
-                    if (ml) {
-                        wm = __hip_atomic_load(rec(mj) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        wl = __hip_atomic_load(rec(mj) + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        pend |= 1u;
-                    }
-                }
+                        wv[j] = ld64<kSC1>(rp, ((pend >> j) & 1u) ? (uint32_t)((j * kPartWords + tid) * 8)
+                                                                  : pbytes);
+                    wm = ld64<kSC1>(rp, (pend & 1u) ? off_m : pbytes);
+                    wl = ld64<kSC1>(rp, (pend & 1u) ? off_m + 8u : pbytes);
+                };
+                request();
                 unsigned long long t0 = 0;
                 for (unsigned it = 0; pend; ++it) {
 #pragma unroll
                     for (int j = 1; j < kNSMax; ++j)
-                        if (((pend >> j) & 1u) && (uint32_t)(wo[j] >> 32) == tag) pend &= ~(1u << j);
-                    if ((pend & 1u) && (uint32_t)(wm >> 32) == tag && (uint32_t)(wl >> 32) == tag) {
-                        s_pm[mj] = __uint_as_float((uint32_t)wm);
-                        s_pl[mj] = __uint_as_float((uint32_t)wl);
+                        if (((pend >> j) & 1u) && wv[j].y == tag) {
+                            vo[j] = __uint_as_float(wv[j].x);
+                            pend &= ~(1u << j);
+                        }
+                    if ((pend & 1u) && wm.y == tag && wl.y == tag) {
+                        s_pm[mj] = __uint_as_float(wm.x);
+                        s_pl[mj] = __uint_as_float(wl.x);
                         pend &= ~1u;
                     }
                     if (!pend) break;
@@ -889,14 +903,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                         mok = false;
                         break;
                     }
-#pragma unroll
-                    for (int j = 1; j < kNSMax; ++j)
-                        if ((pend >> j) & 1u)
-                            wo[j] = __hip_atomic_load(rec(j) + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (pend & 1u) {
-                        wm = __hip_atomic_load(rec(mj) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        wl = __hip_atomic_load(rec(mj) + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
+                    request();
                 }
                 if (!all_ok(mok, &s_fail)) return;
                 DPROG_STAMP(1 + l * 8 + 6);
@@ -909,7 +916,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
                     for (int j = 1; j < kNSMax; ++j)
                         if (j < NS) {
                             const float fw = s_pm[j] == -INFINITY ? 0.f : exp2f(s_pm[j] - Mt);
-                            num += __uint_as_float((uint32_t)wo[j]) * fw;
+                            num += vo[j] * fw;
                             den += s_pl[j] * fw;
                         }
                     put(rsrc(f_att, (uint32_t)HO * 4), h * HD + tid, den > 0.f ? num / den : 0.f, tag);
