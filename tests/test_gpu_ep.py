@@ -343,7 +343,8 @@ def _assert_greedy_strict(rows, what):
 
 
 def _small_cfg(dec, hd=64):
-    return dec.DecoderConfig(layers=2, hidden=256, heads=4 if hd == 64 else 12, kv_heads=2,
+    heads = {64: 4, 96: 8}.get(hd, 12)
+    return dec.DecoderConfig(layers=2, hidden=256, heads=heads, kv_heads=2,
                              head_dim=hd, inter=512, vocab=2048, max_pos=512)
 
 
@@ -370,7 +371,7 @@ def _teacher_forced_check(oracle, runner, cfg, w, prompt, steps):
     return rows
 
 
-@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("hd", [64, 96, 128])
 def test_ep_decoder_small_greedy_matches_oracle(ortmi, oracle, dec, hd):
     cfg = _small_cfg(dec, hd)
     w = dec.make_weights(cfg, seed=hd)
