@@ -578,7 +578,8 @@ def test_gqa_decode_capturable(ortmi, oracle, H, KV, hd):
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
-@pytest.mark.parametrize("H,KV,hd,past", [(12, 2, 128, 140), (8, 8, 64, 5), (16, 4, 128, 299)])
+@pytest.mark.parametrize("H,KV,hd,past", [(12, 2, 128, 140), (8, 8, 64, 5), (16, 4, 128, 299),
+                                         (32, 8, 128, 290)])
 def test_gqa_partials_merge_gemv(ortmi, oracle, H, KV, hd, past, dt):
     """One-token attention left as split partials and merged in the o_proj GEMV's
     prologue equals the capturable attention followed by the plain GEMV (same KV
