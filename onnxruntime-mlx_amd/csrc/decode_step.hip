@@ -999,7 +999,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
         // A second down row per wave when the share exceeds one row per wave: read
         // into registers at the end of D (its wait overlaps the D -> E hop).
         const int d_row2 = wave + kWaves < gd ? wg * gd + wave + kWaves : D;
-        uint32_t sq[1][CPLD], so[CPLD], sg[kGu][CPLD], sd[kIChunksPerLane];
+        uint32_t sq[1][CPLD], so[CPLD], sg[kGu][CPLD], sd[1][kIChunksPerLane];
         Rows<kIChunksPerLane> dr2;
         // With one gate/up group per wave in LDS (wide rows), the wave's next two
         // groups and its second down row are read into registers at the end of A,
@@ -1049,7 +1049,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             };
             auto down_fetch = [&]() {
                 const WeightRef wr = weight_ref(ly.down_weight, ly.down_scales, D, CI);
-                fetch_rows<64, kIChunksPerLane>(wr, d_row, lane, wreg + kLo * 64, sd);
+                fetch_rows<64, kIChunksPerLane>(wr, d_row, lane, wreg + kLo * 64, sd[0]);
             };
             uint32_t* f_qkv = p.flow + (size_t)l * p.flow_stride;
             uint32_t* f_att = f_qkv + NQ;
@@ -1185,12 +1185,18 @@ __global__ __launch_bounds__(kThreads, 1) void decode_program_kernel(Params p) {
             DPROG_STAMP(1 + l * 8 + 6);
             {
                 __builtin_amdgcn_s_waitcnt(0);
-                const float v =
-                    wave_sum(row_dot<64, kIChunksPerLane>(wreg + kLo * 64, sd, sA1, sSum1, CI, lane));
-                if (lane == 0 && wave < gd) s_out[wave] = v;
                 if (gd > kWaves) {
-                    const float v2 = wave_sum(rows_dot<64, kIChunksPerLane>(dr2, sA1, sSum1, CI, lane));
+                    // Both down rows of the wave in one pass over the activations.
+                    float da[2];
+                    const Rows<kIChunksPerLane>* const rg[1] = {&dr2};
+                    rows_dot_multi<64, kIChunksPerLane, 1, 1>(wreg + kLo * 64, sd, rg, sA1, sSum1, CI, lane, da);
+                    const float v = wave_sum(da[0]), v2 = wave_sum(da[1]);
+                    if (lane == 0 && wave < gd) s_out[wave] = v;
                     if (lane == 0 && wave + kWaves < gd) s_out[wave + kWaves] = v2;
+                } else {
+                    const float v =
+                        wave_sum(row_dot<64, kIChunksPerLane>(wreg + kLo * 64, sd[0], sA1, sSum1, CI, lane));
+                    if (lane == 0 && wave < gd) s_out[wave] = v;
                 }
                 __syncthreads();
                 if (tid < gd && wg * gd + tid < D)
